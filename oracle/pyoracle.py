@@ -1,0 +1,419 @@
+"""ctypes view of the CPU oracle (liboracle.so) and of the reference checker
+library (_ref/libftref.so).
+
+TEST INFRASTRUCTURE ONLY: imported by tests/, __graft_entry__.smoke() and the
+cpu_baseline leg of bench.py.  The product (xwfes_amd/) never imports it.
+"""
+import ctypes as C
+import os
+import subprocess
+
+import numpy as np
+
+HERE = os.path.dirname(os.path.abspath(__file__))
+LIB_PATH = os.path.join(HERE, "liboracle.so")
+REF_PATH = os.path.join(HERE, "_ref", "libftref.so")
+
+F32, F16, Q4_0, Q4_1, Q8_0, Q4_K, Q6_K, BF16 = 0, 1, 2, 3, 8, 12, 14, 30
+BLOCK = {F32: (1, 4), F16: (1, 2), BF16: (1, 2), Q4_0: (32, 18), Q4_1: (32, 20),
+         Q8_0: (32, 34), Q4_K: (256, 144), Q6_K: (256, 210)}
+ACCEPT_GREEDY, ACCEPT_RATIO, ACCEPT_RESIDUAL = 0, 1, 2
+KV_F32, KV_F16 = 0, 1
+LAYER_TENSORS = ("attn_norm", "q", "k", "v", "o", "ffn_norm", "gate", "up", "down")
+
+_fp = C.POINTER(C.c_float)
+_u8p = C.POINTER(C.c_uint8)
+_i32p = C.POINTER(C.c_int32)
+_u64p = C.POINTER(C.c_uint64)
+_dp = C.POINTER(C.c_double)
+
+
+def build():
+    subprocess.check_call(["make", "-s", "-C", HERE, "liboracle.so"])
+
+
+def build_ref(ref_root="/root/reference/ft-igpu-src"):
+    """Compile the reference checker where the reference tree exists."""
+    if not os.path.isdir(ref_root):
+        return False
+    subprocess.check_call(["make", "-s", "-C", HERE, "-f", "Makefile.ref",
+                           "REF_ROOT=" + ref_root])
+    return True
+
+
+def row_bytes(dtype, n):
+    be, bb = BLOCK[dtype]
+    return (n + be - 1) // be * bb
+
+
+def _ptr(a, t):
+    return a.ctypes.data_as(t)
+
+
+class _TensorC(C.Structure):
+    _fields_ = [("data", C.c_void_p), ("dtype", C.c_int32), ("pad_", C.c_int32),
+                ("ne0", C.c_int64), ("ne1", C.c_int64)]
+
+
+class _ModelC(C.Structure):
+    _fields_ = [("n_layer", C.c_int64), ("n_embd", C.c_int64), ("n_head", C.c_int64),
+                ("n_head_kv", C.c_int64), ("head_dim", C.c_int64), ("n_ff", C.c_int64),
+                ("vocab", C.c_int64), ("rms_eps", C.c_float), ("rope_neox", C.c_int32),
+                ("rope_theta", C.c_double), ("tok_embd", _TensorC), ("out_norm", _TensorC),
+                ("output", _TensorC), ("layers", C.POINTER(_TensorC))]
+
+
+class Oracle:
+    def __init__(self, path=LIB_PATH):
+        if not os.path.exists(path):
+            build()
+        L = self.lib = C.CDLL(path)
+        L.orc_half_to_float.restype = C.c_float
+        L.orc_half_to_float.argtypes = [C.c_uint16]
+        L.orc_float_to_half.restype = C.c_uint16
+        L.orc_float_to_half.argtypes = [C.c_float]
+        L.orc_bf16_to_float.restype = C.c_float
+        L.orc_bf16_to_float.argtypes = [C.c_uint16]
+        L.orc_dequant_row.argtypes = [_fp, C.c_void_p, C.c_int, C.c_int64]
+        L.orc_dot_row_f32.restype = C.c_float
+        L.orc_dot_row_f32.argtypes = [_fp, C.c_void_p, C.c_int, C.c_int64]
+        L.orc_quantize_row.argtypes = [C.c_void_p, _fp, C.c_int, C.c_int64]
+        L.orc_set_threads.argtypes = [C.c_int]
+        L.orc_matmul.argtypes = [_fp, C.c_int64, C.c_int64, C.c_void_p, C.c_int, C.c_int64, _fp]
+        L.orc_down_axpy.argtypes = [_fp, C.c_int64, C.c_int64, C.c_void_p, C.c_int, C.c_int64, _fp]
+        L.orc_rms_norm.argtypes = [_fp, _fp, _fp, C.c_int64, C.c_float]
+        L.orc_rope_vec.argtypes = [_fp, C.c_int64, C.c_int64, C.c_double, C.c_int]
+        L.orc_softmax_inplace.argtypes = [_fp, C.c_int64]
+        L.orc_forward.argtypes = [C.POINTER(_ModelC), C.c_void_p, C.c_void_p, C.c_int, C.c_int64,
+                                  C.c_int64, _i32p, C.c_int64, _i32p, C.c_int, _fp]
+        L.orc_rng_next.restype = C.c_uint64
+        L.orc_rng_next.argtypes = [_u64p]
+        L.orc_rng_float.restype = C.c_float
+        L.orc_rng_float.argtypes = [_u64p]
+        L.orc_argmax.restype = C.c_int32
+        L.orc_argmax.argtypes = [_fp, C.c_int64]
+        L.orc_softmax_prob.restype = C.c_float
+        L.orc_softmax_prob.argtypes = [_fp, C.c_int64, C.c_int32, C.c_float]
+        L.orc_accept_chain_greedy.argtypes = [_fp, _fp, C.c_int64, _i32p, C.c_int64]
+        L.orc_accept_chain_sampling.argtypes = [_fp, _fp, _fp, C.c_int64, _i32p, C.c_int64,
+                                                C.c_float, _u64p]
+        L.orc_sample_weights.restype = C.c_int32
+        L.orc_sample_weights.argtypes = [_dp, C.c_int64, C.c_float]
+        L.orc_verify_accept.argtypes = [_fp, _fp, C.c_int64, C.c_int64, _i32p, _i32p, _fp, _fp,
+                                        C.c_int, C.c_float, _u64p, _i32p, _i32p, _i32p, _fp]
+
+    # ---- formats ----
+    def half_to_float(self, h):
+        return self.lib.orc_half_to_float(int(h))
+
+    def float_to_half(self, f):
+        return self.lib.orc_float_to_half(float(f))
+
+    def bf16_to_float(self, b):
+        return self.lib.orc_bf16_to_float(int(b))
+
+    def dequant(self, raw, dtype, n, rows=1):
+        raw = np.ascontiguousarray(raw, dtype=np.uint8)
+        rb = row_bytes(dtype, n)
+        assert raw.size >= rb * rows
+        out = np.empty((rows, n), np.float32)
+        for r in range(rows):
+            rc = self.lib.orc_dequant_row(_ptr(out[r], _fp), raw.ctypes.data + r * rb, dtype, n)
+            assert rc == 0, "unsupported dtype %d" % dtype
+        return out if rows > 1 else out[0]
+
+    def quantize(self, x, dtype):
+        x = np.ascontiguousarray(x, dtype=np.float32)
+        if x.ndim == 1:
+            x = x[None, :]
+        rows, n = x.shape
+        rb = row_bytes(dtype, n)
+        out = np.zeros(rows * rb, np.uint8)
+        for r in range(rows):
+            rc = self.lib.orc_quantize_row(out.ctypes.data + r * rb, _ptr(x[r], _fp), dtype, n)
+            assert rc == 0
+        return out
+
+    def dot(self, x, raw, dtype, n):
+        x = np.ascontiguousarray(x, dtype=np.float32)
+        raw = np.ascontiguousarray(raw, dtype=np.uint8)
+        return self.lib.orc_dot_row_f32(_ptr(x, _fp), raw.ctypes.data, dtype, n)
+
+    # ---- ops ----
+    def set_threads(self, n):
+        self.lib.orc_set_threads(int(n))
+
+    def matmul(self, x, raw, dtype, N):
+        x = np.ascontiguousarray(x, dtype=np.float32)
+        M, K = x.shape
+        y = np.empty((M, N), np.float32)
+        self.lib.orc_matmul(_ptr(x, _fp), M, K, raw.ctypes.data, dtype, N, _ptr(y, _fp))
+        return y
+
+    def down_axpy(self, x, raw, dtype, N, y=None):
+        x = np.ascontiguousarray(x, dtype=np.float32)
+        M, n_in = x.shape
+        y = np.zeros((M, N), np.float32) if y is None else np.ascontiguousarray(y, np.float32).copy()
+        self.lib.orc_down_axpy(_ptr(x, _fp), M, n_in, raw.ctypes.data, dtype, N, _ptr(y, _fp))
+        return y
+
+    def rms_norm(self, x, w, eps=1e-5):
+        x = np.ascontiguousarray(x, np.float32)
+        out = np.empty_like(x)
+        wp = _ptr(np.ascontiguousarray(w, np.float32), _fp) if w is not None else None
+        self.lib.orc_rms_norm(_ptr(out, _fp), _ptr(x, _fp), wp, x.size, eps)
+        return out
+
+    def rope(self, v, pos, theta, neox):
+        v = np.ascontiguousarray(v, np.float32).copy()
+        self.lib.orc_rope_vec(_ptr(v, _fp), v.size, pos, theta, int(neox))
+        return v
+
+    def softmax(self, p):
+        p = np.ascontiguousarray(p, np.float32).copy()
+        self.lib.orc_softmax_inplace(_ptr(p, _fp), p.size)
+        return p
+
+    def forward(self, model, kcache, vcache, npast, toks, parents=None, layer_limit=0):
+        """model: dict from make_model(); kcache/vcache: numpy [L][cap][dk]
+        (float32 or float16, modified in place).  Returns logits [M][V]."""
+        cfg = model["cfg"]
+        keep = []
+
+        def tc(name):
+            t = model[name]
+            keep.append(t["raw"])
+            return _TensorC(t["raw"].ctypes.data, t["dtype"], 0, t["ne0"], t["ne1"])
+
+        lay = (_TensorC * (cfg["n_layer"] * 9))()
+        for l in range(cfg["n_layer"]):
+            for i, nm in enumerate(LAYER_TENSORS):
+                lay[l * 9 + i] = tc("blk.%d.%s" % (l, nm))
+        out_t = tc("output") if "output" in model else _TensorC(None, 0, 0, 0, 0)
+        md = _ModelC(cfg["n_layer"], cfg["n_embd"], cfg["n_head"], cfg["n_head_kv"],
+                     cfg["head_dim"], cfg["n_ff"], cfg["vocab"], cfg.get("rms_eps", 1e-5),
+                     int(cfg.get("rope_neox", 0)), cfg.get("rope_theta", 10000.0),
+                     tc("tok_embd"), tc("out_norm"), out_t, lay)
+        toks = np.ascontiguousarray(toks, np.int32)
+        M = toks.size
+        par = None if parents is None else np.ascontiguousarray(parents, np.int32)
+        kv_dt = KV_F16 if kcache.dtype == np.float16 else KV_F32
+        assert kcache.flags.c_contiguous and vcache.flags.c_contiguous
+        cap = kcache.shape[1]
+        logits = np.empty((M, cfg["vocab"]), np.float32)
+        rc = self.lib.orc_forward(C.byref(md), kcache.ctypes.data, vcache.ctypes.data, kv_dt, cap,
+                                  npast, _ptr(toks, _i32p), M,
+                                  None if par is None else _ptr(par, _i32p), layer_limit,
+                                  _ptr(logits, _fp))
+        assert rc == 0, "orc_forward failed"
+        return logits
+
+    # ---- acceptance ----
+    def rng_next(self, state):
+        s = C.c_uint64(state)
+        v = self.lib.orc_rng_next(C.byref(s))
+        return v, s.value
+
+    def rng_floats(self, seed, n):
+        s = C.c_uint64(seed)
+        return np.array([self.lib.orc_rng_float(C.byref(s)) for _ in range(n)], np.float32)
+
+    def argmax(self, row):
+        row = np.ascontiguousarray(row, np.float32)
+        return self.lib.orc_argmax(_ptr(row, _fp), row.size)
+
+    def softmax_prob(self, row, t, temp=1.0):
+        row = np.ascontiguousarray(row, np.float32)
+        return self.lib.orc_softmax_prob(_ptr(row, _fp), row.size, int(t), temp)
+
+    def accept_chain_greedy(self, base, rows, props):
+        base = np.ascontiguousarray(base, np.float32)
+        rows = np.ascontiguousarray(rows, np.float32)
+        props = np.ascontiguousarray(props, np.int32)
+        return self.lib.orc_accept_chain_greedy(_ptr(base, _fp), _ptr(rows, _fp), base.size,
+                                                _ptr(props, _i32p), props.size)
+
+    def accept_chain_sampling(self, base, rows, pd, props, temp, seed):
+        base = np.ascontiguousarray(base, np.float32)
+        rows = np.ascontiguousarray(rows, np.float32)
+        pd = np.ascontiguousarray(pd, np.float32)
+        props = np.ascontiguousarray(props, np.int32)
+        s = C.c_uint64(seed)
+        a = self.lib.orc_accept_chain_sampling(_ptr(base, _fp), _ptr(rows, _fp), _ptr(pd, _fp),
+                                               base.size, _ptr(props, _i32p), props.size, temp,
+                                               C.byref(s))
+        return a, s.value
+
+    def sample_weights(self, w, u):
+        w = np.ascontiguousarray(w, np.float64)
+        return self.lib.orc_sample_weights(_ptr(w, _dp), w.size, float(u))
+
+    def verify_accept(self, base, rows, props, mode, temp=1.0, seed=0, parents=None, pd=None,
+                      q=None):
+        base = np.ascontiguousarray(base, np.float32)
+        rows = np.ascontiguousarray(rows, np.float32)
+        props = np.ascontiguousarray(props, np.int32)
+        M, V = props.size, base.size
+        par = None if parents is None else np.ascontiguousarray(parents, np.int32)
+        pdv = None if pd is None else np.ascontiguousarray(pd, np.float32)
+        qv = None if q is None else np.ascontiguousarray(q, np.float32)
+        acc = np.zeros(max(M, 1), np.int32)
+        na = C.c_int32(0)
+        bonus = C.c_int32(0)
+        mg = C.c_float(0)
+        s = C.c_uint64(seed)
+        rc = self.lib.orc_verify_accept(
+            _ptr(base, _fp), _ptr(rows, _fp), M, V, _ptr(props, _i32p),
+            None if par is None else _ptr(par, _i32p),
+            None if pdv is None else _ptr(pdv, _fp),
+            None if qv is None else _ptr(qv, _fp), mode, temp, C.byref(s),
+            _ptr(acc, _i32p), C.byref(na), C.byref(bonus), C.byref(mg))
+        assert rc == 0, "orc_verify_accept failed"
+        return dict(accepted=acc[:na.value].tolist(), bonus=bonus.value, rng=s.value,
+                    margin=mg.value)
+
+
+class Ref:
+    """The reference's own functions (compiled from its sources by
+    Makefile.ref).  Available only where the reference tree was present when
+    the checker was built."""
+
+    def __init__(self, path=REF_PATH):
+        L = self.lib = C.CDLL(path)
+        L.ref_half_to_float.restype = C.c_float
+        L.ref_half_to_float.argtypes = [C.c_uint16]
+        L.ref_float_to_half.restype = C.c_uint16
+        L.ref_float_to_half.argtypes = [C.c_float]
+        L.ref_bf16_to_float.restype = C.c_float
+        L.ref_bf16_to_float.argtypes = [C.c_uint16]
+        L.ref_dequant_row.argtypes = [_fp, C.c_void_p, C.c_int, C.c_int64]
+        L.ref_dot_row_f32.restype = C.c_float
+        L.ref_dot_row_f32.argtypes = [_fp, C.c_void_p, C.c_int, C.c_int64]
+        L.ref_cpu_matmul.argtypes = [_fp, C.c_int64, C.c_int64, C.c_void_p, C.c_int, C.c_int64,
+                                     _fp, C.c_int]
+        L.ref_down_axpy.argtypes = [_fp, C.c_int64, C.c_int64, C.c_void_p, C.c_int, C.c_int64, _fp]
+        L.ref_argmax.argtypes = [_fp, C.c_int64]
+        L.ref_softmax_prob.restype = C.c_float
+        L.ref_softmax_prob.argtypes = [_fp, C.c_int64, C.c_int32]
+        L.ref_accept_chain_greedy.argtypes = [_fp, _fp, C.c_int64, _i32p, C.c_int64]
+        L.ref_accept_chain_sampling.argtypes = [_fp, _fp, _fp, C.c_int64, _i32p, C.c_int64,
+                                                C.c_float, _u64p]
+        L.ref_engine_load.restype = C.c_void_p
+        L.ref_engine_load.argtypes = [C.c_char_p, C.c_int, C.c_int64]
+        L.ref_engine_free.argtypes = [C.c_void_p]
+        L.ref_engine_vocab.restype = C.c_int64
+        L.ref_engine_vocab.argtypes = [C.c_void_p]
+        L.ref_engine_step.argtypes = [C.c_void_p, C.c_int32, _fp]
+
+    @staticmethod
+    def available():
+        return os.path.exists(REF_PATH)
+
+    def dequant(self, raw, dtype, n):
+        raw = np.ascontiguousarray(raw, np.uint8)
+        out = np.empty(n, np.float32)
+        self.lib.ref_dequant_row(_ptr(out, _fp), raw.ctypes.data, dtype, n)
+        return out
+
+    def dot(self, x, raw, dtype, n):
+        x = np.ascontiguousarray(x, np.float32)
+        raw = np.ascontiguousarray(raw, np.uint8)
+        return self.lib.ref_dot_row_f32(_ptr(x, _fp), raw.ctypes.data, dtype, n)
+
+    def cpu_matmul(self, x, raw, dtype, N, threads=1):
+        x = np.ascontiguousarray(x, np.float32)
+        M, K = x.shape
+        y = np.zeros(N, np.float32)
+        self.lib.ref_cpu_matmul(_ptr(x, _fp), M, K, raw.ctypes.data, dtype, N, _ptr(y, _fp),
+                                threads)
+        return y
+
+    def down_axpy(self, x, raw, dtype, N):
+        x = np.ascontiguousarray(x, np.float32)
+        M, n_in = x.shape
+        y = np.zeros((M, N), np.float32)
+        self.lib.ref_down_axpy(_ptr(x, _fp), M, n_in, raw.ctypes.data, dtype, N, _ptr(y, _fp))
+        return y
+
+    def softmax_prob(self, row, t):
+        row = np.ascontiguousarray(row, np.float32)
+        return self.lib.ref_softmax_prob(_ptr(row, _fp), row.size, int(t))
+
+    def argmax(self, row):
+        row = np.ascontiguousarray(row, np.float32)
+        return self.lib.ref_argmax(_ptr(row, _fp), row.size)
+
+    def accept_chain_greedy(self, base, rows, props):
+        base = np.ascontiguousarray(base, np.float32)
+        rows = np.ascontiguousarray(rows, np.float32)
+        props = np.ascontiguousarray(props, np.int32)
+        return self.lib.ref_accept_chain_greedy(_ptr(base, _fp), _ptr(rows, _fp), base.size,
+                                                _ptr(props, _i32p), props.size)
+
+    def accept_chain_sampling(self, base, rows, pd, props, temp, seed):
+        base = np.ascontiguousarray(base, np.float32)
+        rows = np.ascontiguousarray(rows, np.float32)
+        pd = np.ascontiguousarray(pd, np.float32)
+        props = np.ascontiguousarray(props, np.int32)
+        s = C.c_uint64(seed)
+        a = self.lib.ref_accept_chain_sampling(_ptr(base, _fp), _ptr(rows, _fp), _ptr(pd, _fp),
+                                               base.size, _ptr(props, _i32p), props.size, temp,
+                                               C.byref(s))
+        return a, s.value
+
+    def engine_load(self, path, threads=1, ctx_len=0):
+        h = self.lib.ref_engine_load(path.encode(), threads, ctx_len)
+        assert h, "reference Engine failed to load " + path
+        return h
+
+    def engine_step(self, h, tok):
+        V = self.lib.ref_engine_vocab(h)
+        out = np.empty(V, np.float32)
+        assert self.lib.ref_engine_step(h, tok, _ptr(out, _fp)) == 0
+        return out
+
+    def engine_free(self, h):
+        self.lib.ref_engine_free(h)
+
+
+# ---------------- synthetic models (test data) ----------------
+
+def model_cfg(n_layer, n_embd, n_head, n_head_kv, head_dim, n_ff, vocab, rope_theta=10000.0,
+              rope_neox=0, rms_eps=1e-5):
+    return dict(n_layer=n_layer, n_embd=n_embd, n_head=n_head, n_head_kv=n_head_kv,
+                head_dim=head_dim, n_ff=n_ff, vocab=vocab, rope_theta=rope_theta,
+                rope_neox=rope_neox, rms_eps=rms_eps)
+
+
+def tensor_shapes(cfg):
+    """(name, ne0 cols, ne1 rows) of every tensor; down uses the reference
+    orientation (n_ff rows of n_embd cols)."""
+    d, hd = cfg["n_embd"], cfg["head_dim"]
+    qd, kd = cfg["n_head"] * hd, cfg["n_head_kv"] * hd
+    out = [("tok_embd", d, cfg["vocab"]), ("out_norm", d, 1), ("output", d, cfg["vocab"])]
+    for l in range(cfg["n_layer"]):
+        p = "blk.%d." % l
+        out += [(p + "attn_norm", d, 1), (p + "q", d, qd), (p + "k", d, kd), (p + "v", d, kd),
+                (p + "o", qd, d), (p + "ffn_norm", d, 1), (p + "gate", d, cfg["n_ff"]),
+                (p + "up", d, cfg["n_ff"]), (p + "down", d, cfg["n_ff"])]
+    return out
+
+
+def make_model(orc, cfg, dtypes, seed=1, std=0.02, tied=False):
+    """Random-init model: weights N(0, std) quantised to dtypes[name-suffix]
+    (keys: 'tok_embd', 'output', 'q', 'k', 'v', 'o', 'gate', 'up', 'down';
+    norms are F32 ones)."""
+    rng = np.random.default_rng(seed)
+    model = {"cfg": dict(cfg)}
+    for name, ne0, ne1 in tensor_shapes(cfg):
+        if name == "output" and tied:
+            continue
+        key = name.split(".")[-1]
+        if key in ("attn_norm", "ffn_norm", "out_norm"):
+            w = np.ones(ne0, np.float32)
+            model[name] = dict(raw=w.view(np.uint8).copy(), dtype=F32, ne0=ne0, ne1=1)
+            continue
+        dt = dtypes[key]
+        w = (rng.standard_normal((ne1, ne0)) * std).astype(np.float32)
+        model[name] = dict(raw=orc.quantize(w, dt), dtype=dt, ne0=ne0, ne1=ne1)
+    return model
