@@ -25,3 +25,13 @@ def ref():
     if not pyoracle.Ref.available():
         pytest.skip("reference checker library oracle/_ref not built here")
     return pyoracle.Ref()
+
+
+@pytest.fixture(scope="session")
+def gctx():
+    """ftx context on device 0.  The GPU tests must run the HIP library: a
+    missing library or device is an error, not a skip."""
+    from xwfes_amd import ftx
+    ctx = ftx.Context(0)
+    yield ctx
+    ctx.close()

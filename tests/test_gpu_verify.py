@@ -1,0 +1,301 @@
+"""GPU parity of the verify step (ftx_verify_step) and of the acceptance
+sampler (ftx_accept) against the CPU oracle, through the C ABI.
+
+Logits: per row max|gpu - oracle| / max|oracle| <= 1e-3 (LOGIT_TOL), fp32
+accumulation on both sides in different orders.
+Acceptance: given identical logits and the same SplitMix64 state, accepted
+node lists, bonus tokens and the advanced rng state are identical.
+"""
+import numpy as np
+import pytest
+
+import pyoracle as P
+from xwfes_amd import ftx
+
+pytestmark = pytest.mark.gpu
+
+LOGIT_TOL = 1e-3
+
+
+def rel_err_rows(a, b):
+    a = np.atleast_2d(a).astype(np.float64)
+    b = np.atleast_2d(b).astype(np.float64)
+    return (np.abs(a - b).max(axis=1) / np.maximum(np.abs(b).max(axis=1), 1e-30)).max()
+
+
+def upload_model(gctx, model):
+    cfg = model["cfg"]
+    tensors = {}
+    for name, t in model.items():
+        if name == "cfg":
+            continue
+        tensors[name] = gctx.upload(t["raw"], t["dtype"], (t["ne0"], t["ne1"]))
+    return tensors
+
+
+def free_all(tensors):
+    for t in tensors.values():
+        t.free()
+
+
+def kv_context(cfg, cap, npast, seed):
+    rng = np.random.default_rng(seed)
+    shape = (cfg["n_layer"], cap, cfg["n_head_kv"] * cfg["head_dim"])
+    k = np.zeros(shape, np.float16)
+    v = np.zeros(shape, np.float16)
+    k[:, :npast] = rng.standard_normal((shape[0], npast, shape[2]))
+    v[:, :npast] = rng.standard_normal((shape[0], npast, shape[2]))
+    return k, v
+
+
+def run_both(gctx, orc, model, toks, npast, cap, parents=None, seed=5):
+    cfg = model["cfg"]
+    tensors = upload_model(gctx, model)
+    gm = gctx.model(cfg, tensors, max_tokens=max(8, len(toks)))
+    kv = gm.kv(cap)
+    k0, v0 = kv_context(cfg, cap, npast, seed)
+    kv.write(k0, v0)
+    kv.truncate(npast)
+    M, V = len(toks), cfg["vocab"]
+    buf = gctx.buffer(M * V * 4)
+    gm.verify(kv, toks, buf.ptr, parents=parents)
+    gctx.sync()
+    got = buf.read(np.float32, M * V).reshape(M, V)
+    kg, vg = kv.read()
+    kc, vc = k0.copy(), v0.copy()
+    want = orc.forward(model, kc, vc, npast, toks, parents=parents)
+    buf.free()
+    kv.free()
+    gm.free()
+    free_all(tensors)
+    return got, want, (kg, vg), (kc, vc)
+
+
+TINY = P.model_cfg(2, 64, 4, 2, 16, 96, 50, rope_theta=10000.0)
+TINY_DT = dict(tok_embd=P.F32, output=P.Q8_0, q=P.Q4_0, k=P.Q8_0, v=P.Q4_0, o=P.Q8_0,
+               gate=P.Q4_0, up=P.Q4_0, down=P.Q8_0)
+
+
+def test_verify_chain_tiny(gctx, orc):
+    model = P.make_model(orc, TINY, TINY_DT, seed=3)
+    got, want, (kg, vg), (kc, vc) = run_both(gctx, orc, model, [3, 17, 42, 0, 9], 7, 32)
+    assert rel_err_rows(got, want) < LOGIT_TOL
+    # the draft rows written to the cache agree to fp16 rounding
+    assert np.abs(kg.astype(np.float32) - kc.astype(np.float32)).max() < 2e-2
+    assert np.abs(vg.astype(np.float32) - vc.astype(np.float32)).max() < 2e-2
+    assert np.array_equal(kg[:, :7], kc[:, :7])
+
+
+def test_verify_tree_tiny(gctx, orc):
+    model = P.make_model(orc, TINY, TINY_DT, seed=4)
+    parents = [-1, -1, 0, 0, 3, 1, 5]
+    got, want, _, _ = run_both(gctx, orc, model, [5, 6, 7, 8, 9, 10, 11], 6, 32, parents=parents)
+    assert rel_err_rows(got, want) < LOGIT_TOL
+
+
+def test_verify_tree_equals_paths_on_gpu(gctx, orc):
+    """Tree invariant on the device: node i's logits equal the chain forward
+    of its root-to-i path."""
+    model = P.make_model(orc, TINY, TINY_DT, seed=8)
+    cfg = model["cfg"]
+    tensors = upload_model(gctx, model)
+    gm = gctx.model(cfg, tensors, max_tokens=8)
+    kv = gm.kv(32)
+    k0, v0 = kv_context(cfg, 32, 6, 9)
+    parents = [-1, -1, 0, 0, 3]
+    toks = [5, 6, 7, 8, 9]
+    V = cfg["vocab"]
+    buf = gctx.buffer(8 * V * 4)
+    kv.write(k0, v0)
+    kv.truncate(6)
+    gm.verify(kv, toks, buf.ptr, parents=parents)
+    gctx.sync()
+    tree = buf.read(np.float32, 5 * V).reshape(5, V)
+    paths = {0: [0], 1: [1], 2: [0, 2], 3: [0, 3], 4: [0, 3, 4]}
+    for node, path in paths.items():
+        kv.write(k0, v0)
+        kv.truncate(6)
+        gm.verify(kv, [toks[i] for i in path], buf.ptr)
+        gctx.sync()
+        chain = buf.read(np.float32, len(path) * V).reshape(len(path), V)
+        assert rel_err_rows(chain[-1], tree[node]) < 1e-5, node
+    buf.free()
+    kv.free()
+    gm.free()
+    free_all(tensors)
+
+
+CFG1 = P.model_cfg(2, 512, 8, 8, 64, 1408, 32000, rope_theta=10000.0)
+CFG1_DT = dict(tok_embd=P.F32, output=P.Q4_0, q=P.Q4_0, k=P.Q4_0, v=P.Q4_0, o=P.Q4_0,
+               gate=P.Q4_0, up=P.Q4_0, down=P.Q4_0)
+
+
+def test_verify_tiny_llama_shape(gctx, orc):
+    """The tiny-Llama workload's layer shape (d 512, 8 heads x 64, FFN 1408,
+    V 32000, Q4_0 in the reference nibble order, F32 embedding), 2 layers,
+    K=4 draft after a 128-token context."""
+    orc.set_threads(8)
+    model = P.make_model(orc, CFG1, CFG1_DT, seed=1)
+    rng = np.random.default_rng(3)
+    toks = rng.integers(0, 32000, 4).tolist()
+    got, want, _, _ = run_both(gctx, orc, model, toks, 128, 160)
+    assert rel_err_rows(got, want) < LOGIT_TOL
+
+
+def q4k_m_dtypes(layer, n_layer):
+    """Q4_K_M mix: Q6_K for attn_v and ffn_down on the 'more bits' layers."""
+    more = layer < n_layer // 8 or layer >= 7 * n_layer // 8 or (layer - n_layer // 8) % 3 == 2
+    dv = P.Q6_K if more else P.Q4_K
+    return dict(q=P.Q4_K, k=P.Q4_K, v=dv, o=P.Q4_K, gate=P.Q4_K, up=P.Q4_K, down=dv)
+
+
+def test_verify_8b_shape_two_layers(gctx, orc):
+    """8B layer shape (d 4096, 32/8 heads x 128, FFN 14336, V 128256), Q4_K
+    with Q6_K attn_v / ffn_down on one layer and a Q6_K head, 2 layers, an
+    8-token chain at context 64, theta 500000."""
+    orc.set_threads(16)
+    cfg = P.model_cfg(2, 4096, 32, 8, 128, 14336, 128256, rope_theta=500000.0)
+    model = {"cfg": dict(cfg)}
+    rng = np.random.default_rng(21)
+
+    def q(rows, cols, dt):
+        # at most 2048 distinct random rows, tiled (keeps host quantisation short)
+        u = min(rows, 2048)
+        w = (rng.standard_normal((u, cols)) * 0.02).astype(np.float32)
+        raw = np.tile(orc.quantize(w, dt), -(-rows // u))[: rows * P.row_bytes(dt, cols)]
+        return dict(raw=np.ascontiguousarray(raw), dtype=dt, ne0=cols, ne1=rows)
+
+    ones = np.ones(4096, np.float32).view(np.uint8).copy()
+    model["tok_embd"] = q(128256, 4096, P.Q4_K)
+    model["output"] = q(128256, 4096, P.Q6_K)
+    model["out_norm"] = dict(raw=ones, dtype=P.F32, ne0=4096, ne1=1)
+    for l in range(2):
+        dts = q4k_m_dtypes(l if l == 0 else 5, 32)
+        p = "blk.%d." % l
+        model[p + "attn_norm"] = dict(raw=ones, dtype=P.F32, ne0=4096, ne1=1)
+        model[p + "ffn_norm"] = dict(raw=ones, dtype=P.F32, ne0=4096, ne1=1)
+        model[p + "q"] = q(4096, 4096, dts["q"])
+        model[p + "k"] = q(1024, 4096, dts["k"])
+        model[p + "v"] = q(1024, 4096, dts["v"])
+        model[p + "o"] = q(4096, 4096, dts["o"])
+        model[p + "gate"] = q(14336, 4096, dts["gate"])
+        model[p + "up"] = q(14336, 4096, dts["up"])
+        model[p + "down"] = q(14336, 4096, dts["down"])
+    toks = rng.integers(0, 128256, 8).tolist()
+    got, want, _, _ = run_both(gctx, orc, model, toks, 64, 96)
+    assert rel_err_rows(got, want) < LOGIT_TOL
+
+
+def test_verify_errors(gctx, orc):
+    model = P.make_model(orc, TINY, TINY_DT, seed=3)
+    tensors = upload_model(gctx, model)
+    gm = gctx.model(TINY, tensors, max_tokens=8)
+    kv = gm.kv(16)
+    buf = gctx.buffer(8 * 50 * 4)
+    with pytest.raises(ftx.FtxError) as e:
+        gm.verify(kv, [1, 50], buf.ptr)
+    assert e.value.code == -5
+    with pytest.raises(ftx.FtxError) as e:
+        gm.verify(kv, [1, 2], buf.ptr, parents=[-1, 1])
+    assert e.value.code == -1
+    kv.truncate(12)
+    with pytest.raises(ftx.FtxError) as e:
+        gm.verify(kv, [1, 2, 3, 4, 5], buf.ptr)
+    assert e.value.code == -5
+    buf.free()
+    kv.free()
+    gm.free()
+    free_all(tensors)
+
+
+# ---------------------------------------------------------------- acceptance
+
+def accept_both(gctx, orc, base, rows, props, mode, temp, seed, parents=None, pd=None, q=None):
+    M, V = rows.shape
+    b = gctx.buffer((M + 1) * V * 4)
+    b.write(np.ascontiguousarray(base, np.float32))
+    b.write(np.ascontiguousarray(rows, np.float32), V * 4)
+    qb = None
+    if q is not None:
+        qb = gctx.buffer(M * V * 4)
+        qb.write(np.ascontiguousarray(q, np.float32))
+    g = gctx.accept(b.ptr, b.ptr + V * 4, M, V, props, mode, temp=temp, rng=seed,
+                    parents=parents, pd=pd, q_ptr=qb.ptr if qb else None)
+    b.free()
+    if qb:
+        qb.free()
+    o = orc.verify_accept(base, rows, props, mode, temp=temp, seed=seed, parents=parents, pd=pd,
+                          q=q)
+    return g, o
+
+
+def case(rng, k, V, spread=2.0, hit=0.7):
+    base = (rng.standard_normal(V) * spread).astype(np.float32)
+    rows = (rng.standard_normal((k, V)) * spread).astype(np.float32)
+    props = rng.integers(0, V, k).astype(np.int32)
+    for a in range(k):
+        if rng.random() < hit:
+            props[a] = int(np.argmax(base if a == 0 else rows[a - 1]))
+    return base, rows, props
+
+
+def test_accept_reference_kat(gctx, orc):
+    """src/tests/test_core.cpp:348-356: props {0,1,2} -> 3, {0,3,2} -> 1."""
+    base = np.array([9, 1, 1, 1], np.float32)
+    rows = np.array([[1, 9, 1, 1], [1, 1, 9, 1], [1, 1, 1, 9]], np.float32)
+    for props, n in (([0, 1, 2], 3), ([0, 3, 2], 1)):
+        g, o = accept_both(gctx, orc, base, rows, props, ftx.ACCEPT_GREEDY, 1.0, 0)
+        assert len(g["accepted"]) == n == len(o["accepted"])
+        assert g == o or (g["accepted"], g["bonus"]) == (o["accepted"], o["bonus"])
+
+
+@pytest.mark.parametrize("V", [64, 32000])
+def test_accept_greedy_chain_and_tree(gctx, orc, V):
+    rng = np.random.default_rng(V)
+    for trial in range(20):
+        base, rows, props = case(rng, 8, V)
+        g, o = accept_both(gctx, orc, base, rows, props, ftx.ACCEPT_GREEDY, 1.0, 0)
+        assert (g["accepted"], g["bonus"]) == (o["accepted"], o["bonus"])
+        parents = [-1, -1, 0, 0, 1, 2, 2, 4]
+        g, o = accept_both(gctx, orc, base, rows, props, ftx.ACCEPT_GREEDY, 1.0, 0,
+                           parents=parents)
+        assert (g["accepted"], g["bonus"]) == (o["accepted"], o["bonus"])
+
+
+@pytest.mark.parametrize("V,temp", [(64, 1.0), (32000, 0.8), (128256, 0.8)])
+def test_accept_ratio_chain(gctx, orc, V, temp):
+    rng = np.random.default_rng(V + 1)
+    for trial in range(12 if V > 1000 else 60):
+        base, rows, props = case(rng, 8, V, spread=1.0)
+        pd = (rng.random(8) * 0.05).astype(np.float32)
+        pd[rng.random(8) < 0.1] = 0.0
+        seed = int(rng.integers(1, 2**63))
+        g, o = accept_both(gctx, orc, base, rows, props, ftx.ACCEPT_RATIO, temp, seed, pd=pd)
+        assert (g["accepted"], g["bonus"], g["rng"]) == (o["accepted"], o["bonus"], o["rng"])
+
+
+@pytest.mark.parametrize("V", [24, 32000])
+def test_accept_residual_chain_and_tree(gctx, orc, V):
+    rng = np.random.default_rng(V + 2)
+    for trial in range(10 if V > 1000 else 50):
+        parents = [-1, -1, -1, 0, 0, 1, 3, 3] if trial % 2 else list(range(-1, 7))
+        base, rows, props = case(rng, 8, V, spread=1.0, hit=0.5)
+        q = rng.dirichlet(np.ones(V), size=8).astype(np.float32)
+        for c in range(8):
+            if rng.random() < 0.5:
+                props[c] = int(np.argmax(q[c]))
+        seed = int(rng.integers(1, 2**63))
+        g, o = accept_both(gctx, orc, base, rows, props, ftx.ACCEPT_RESIDUAL, 0.8, seed,
+                           parents=parents, q=q)
+        assert (g["accepted"], g["bonus"], g["rng"]) == (o["accepted"], o["bonus"], o["rng"])
+
+
+def test_accept_empty_draft(gctx, orc):
+    """M = 0: only the bonus token is drawn."""
+    rng = np.random.default_rng(4)
+    base = rng.standard_normal(1000).astype(np.float32)
+    b = gctx.buffer(1000 * 4)
+    b.write(base)
+    g = gctx.accept(b.ptr, None, 0, 1000, [], ftx.ACCEPT_GREEDY)
+    b.free()
+    assert g["accepted"] == [] and g["bonus"] == int(np.argmax(base))

@@ -1,0 +1,153 @@
+// ftx_internal.h -- shared declarations of the HIP library behind ftx.h.
+#pragma once
+
+#include <hip/hip_runtime.h>
+
+#include <cstdint>
+#include <cstring>
+#include <string>
+#include <vector>
+
+#include "../../include/ftx.h"
+
+// ---------------------------------------------------------------- host side
+
+struct ftx_ctx {
+    int device = 0;
+    hipStream_t own_stream = nullptr;
+    hipStream_t stream = nullptr;
+    std::string err;
+    int cu_count = 0;
+    // grow-only device workspace for staging host buffers and split sums
+    void* ws = nullptr;
+    size_t ws_bytes = 0;
+    // small pinned host buffer for step arguments
+    void* pinned = nullptr;
+    size_t pinned_bytes = 0;
+};
+
+struct ftx_tensor {
+    ftx_ctx* ctx = nullptr;
+    int dtype = 0;
+    int64_t ne[4] = {1, 1, 1, 1};
+    int64_t row_bytes = 0;
+    int64_t nrows = 0;  // ne1 * ne2 * ne3
+    uint8_t* data = nullptr;
+    bool owned = true;
+};
+
+int64_t ftx_block_elems(int dt);
+int64_t ftx_block_bytes(int dt);
+bool ftx_dtype_ok(int dt);
+
+int ftx_fail(ftx_ctx* ctx, int code, const std::string& msg);
+#define FTX_HIP(ctx, call)                                                           \
+    do {                                                                             \
+        hipError_t e_ = (call);                                                      \
+        if (e_ != hipSuccess)                                                        \
+            return ftx_fail((ctx), FTX_E_DEVICE,                                     \
+                            std::string(#call) + ": " + hipGetErrorString(e_));      \
+    } while (0)
+
+// device workspace of at least `bytes`, 256-B aligned
+int ftx_workspace(ftx_ctx* ctx, size_t bytes, void** out);
+// pinned host staging of at least `bytes`
+int ftx_pinned(ftx_ctx* ctx, size_t bytes, void** out);
+bool ftx_is_device_ptr(const void* p);
+
+// ---------------------------------------------------------------- launchers
+// All enqueue on `st` and return hipError_t of the launch.
+
+// dequantise `nrows` rows of `ncols` elements (bit-exact export)
+hipError_t launch_dequant(hipStream_t st, const uint8_t* W, int dt, int64_t row_bytes,
+                          int64_t ncols, int64_t nrows, float* out);
+
+// row-dot GEMV/GEMM segment: y[m*ldy + n] (=|+=) sum_k x[m*ldx + k] W[n,k]
+struct GemvSeg {
+    const uint8_t* W;
+    int dt;
+    int64_t row_bytes;
+    int64_t N;
+    float* y;
+    int64_t ldy;
+};
+enum { EPI_STORE = 0, EPI_ACCUM = 1 };
+hipError_t launch_gemv(hipStream_t st, const GemvSeg* segs, int nseg, const float* x,
+                       int64_t ldx, int64_t K, int64_t M, int epi);
+// gate/up pair with SwiGLU epilogue: h[m*ldh + n] = silu(x.g_n) * (x.u_n)
+hipError_t launch_gemv_swiglu(hipStream_t st, const uint8_t* Wg, const uint8_t* Wu, int dt,
+                              int64_t row_bytes, int64_t N, const float* x, int64_t ldx,
+                              int64_t K, int64_t M, float* h, int64_t ldh);
+// y[m*ldy + j] += sum_i h[m*ldh + i] W[i, j] (W n_in rows x N cols)
+// uses `part` scratch of down_scratch_floats(...) floats
+size_t down_scratch_floats(int64_t M, int64_t n_in, int64_t N);
+hipError_t launch_down(hipStream_t st, const uint8_t* W, int dt, int64_t row_bytes,
+                       int64_t n_in, int64_t N, const float* h, int64_t ldh, int64_t M,
+                       float* y, int64_t ldy, float* part);
+
+// quantise rows (synthetic model builder)
+hipError_t launch_quantize(hipStream_t st, const float* src, int dt, int64_t ncols,
+                           int64_t nrows, int64_t row_bytes, uint8_t* dst);
+
+hipError_t launch_fill_normal(hipStream_t st, void* dst, int f16, int64_t n, uint64_t seed,
+                              float std);
+
+// layer ops
+hipError_t launch_embed(hipStream_t st, const uint8_t* E, int dt, int64_t row_bytes,
+                        int64_t d, const int32_t* toks, int64_t M, float* x);
+hipError_t launch_rmsnorm(hipStream_t st, const float* x, const float* w, int64_t d,
+                          int64_t M, float eps, float* out);
+struct RopeArgs {
+    float* qkv;        // [M][ldq]: q at 0, k at qdim, v at qdim + kdim
+    int64_t ldq;
+    int64_t n_head, n_kv, hd;
+    const int32_t* depth;   // [M]
+    const int64_t* npast;   // device scalar
+    double theta;
+    int neox;
+    void* kc;          // layer base of K cache [cap][kdim]
+    void* vc;
+    int kv_f16;
+};
+hipError_t launch_rope_kv(hipStream_t st, const RopeArgs& a, int64_t M);
+struct AttnArgs {
+    const float* qkv;   // q rows, ldq stride
+    int64_t ldq;
+    const void* kc;     // layer base [cap][kdim]
+    const void* vc;
+    int kv_f16;
+    const int64_t* npast;      // device scalar
+    const uint32_t* anc;       // [M][anc_words] ancestor bitmask (self included)
+    int anc_words;
+    int64_t n_head, n_kv, hd;
+    int64_t max_ctx;           // upper bound of npast + M for LDS sizing
+    float* out;                // [M][n_head*hd]
+};
+hipError_t launch_attention(hipStream_t st, const AttnArgs& a, int64_t M);
+
+// acceptance
+struct RowStats {
+    float mx;
+    int32_t amax;
+    double sum;  // sum_i exp((l_i - mx)/T) in double
+};
+hipError_t launch_row_stats(hipStream_t st, const float* rows, int64_t nrows, int64_t V,
+                            float temp, RowStats* out);
+struct AcceptDev {
+    const float* base_row;
+    const float* rows;
+    const float* q;
+    const RowStats* stats;   // [M+1]: stats[0] = base row, stats[1+i] = row i
+    int64_t M, V;
+    const int32_t* props;    // device [M]
+    const int32_t* parents;  // device [M] (chain given explicitly)
+    const float* pd;         // device [M] or null
+    int mode;
+    float temp;
+    uint64_t* rng;           // device state
+    double* p;               // scratch [V]
+    double* part;            // scratch [1024]
+    int32_t* out;            // device: [0]=n_acc, [1]=bonus, [2..2+M) accepted
+    float* margin;           // device scalar
+};
+hipError_t launch_accept(hipStream_t st, const AcceptDev& a);

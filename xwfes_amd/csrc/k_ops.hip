@@ -1,0 +1,221 @@
+// k_ops.hip -- per-layer host ops of Engine::forward moved to the device:
+// embedding lookup, RMSNorm, RoPE + KV append, and tree-masked GQA attention.
+#include "ftx_internal.h"
+#include "quant_dev.h"
+
+// ---------------------------------------------------------------- embedding
+// x[m, :] = dequant(E row toks[m]): a row lookup (the reference indexes a
+// plane with HostTensor::slice(t), src/engine.cpp:494-495, which is only
+// right for t == 0; the row is what forward() means).
+__global__ void __launch_bounds__(256) k_embed(const uint8_t* __restrict__ E, int dt,
+                                               int64_t row_bytes, int64_t d,
+                                               const int32_t* __restrict__ toks,
+                                               float* __restrict__ x) {
+    const int64_t m = blockIdx.y;
+    const int64_t g = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
+    if (g * 8 >= d) return;
+    float v[8];
+    dq8(E + (int64_t)toks[m] * row_bytes, dt, g * 8, d, v);
+    float* o = x + m * d + g * 8;
+#pragma unroll
+    for (int i = 0; i < 8; ++i)
+        if (g * 8 + i < d) o[i] = v[i];
+}
+
+hipError_t launch_embed(hipStream_t st, const uint8_t* E, int dt, int64_t row_bytes, int64_t d,
+                        const int32_t* toks, int64_t M, float* x) {
+    if (M == 0) return hipSuccess;
+    const int64_t groups = (d + 7) / 8;
+    hipLaunchKernelGGL(k_embed, dim3((unsigned)((groups + 255) / 256), (unsigned)M), dim3(256), 0,
+                       st, E, dt, row_bytes, d, toks, x);
+    return hipGetLastError();
+}
+
+// ---------------------------------------------------------------- RMSNorm
+// src/engine.cpp:23-41: ss = sum x^2; inv = 1/sqrt(ss/n + eps); (x*inv)*w
+__global__ void __launch_bounds__(256) k_rmsnorm(const float* __restrict__ x,
+                                                 const float* __restrict__ w, int64_t d,
+                                                 float eps, float* __restrict__ out) {
+#pragma clang fp contract(off)
+    const int64_t m = blockIdx.x;
+    const float* xr = x + m * d;
+    float ss = 0.f;
+    for (int64_t i = threadIdx.x; i < d; i += 256) ss += xr[i] * xr[i];
+    __shared__ float red[256];
+    red[threadIdx.x] = ss;
+    __syncthreads();
+    for (int o = 128; o > 0; o >>= 1) {
+        if (threadIdx.x < o) red[threadIdx.x] += red[threadIdx.x + o];
+        __syncthreads();
+    }
+    const float inv = 1.f / sqrtf(red[0] / (float)d + eps);
+    float* orow = out + m * d;
+    for (int64_t i = threadIdx.x; i < d; i += 256) orow[i] = xr[i] * inv * w[i];
+}
+
+hipError_t launch_rmsnorm(hipStream_t st, const float* x, const float* w, int64_t d, int64_t M,
+                          float eps, float* out) {
+    if (M == 0) return hipSuccess;
+    hipLaunchKernelGGL(k_rmsnorm, dim3((unsigned)M), dim3(256), 0, st, x, w, d, eps, out);
+    return hipGetLastError();
+}
+
+// ---------------------------------------------------------------- RoPE + KV
+// src/engine.cpp:43-60 (frequencies and angles in double, cos/sin rounded
+// to float; neox pairs (i, i+hd/2), else interleaved (2i, 2i+1)) applied to
+// q and k at position npast + depth[m]; k and v are then written to KV slot
+// npast + m (src/engine.cpp:555-561).
+__global__ void k_rope_kv(RopeArgs a) {
+#pragma clang fp contract(off)
+    const int64_t m = blockIdx.x;
+    const int64_t h = blockIdx.y;  // 0..n_head-1: q heads; then kv heads
+    const int64_t half = a.hd / 2;
+    const int64_t npast = *a.npast;
+    const int64_t pos = npast + a.depth[m];
+    const int64_t qdim = a.n_head * a.hd, kdim = a.n_kv * a.hd;
+    float* row = a.qkv + m * a.ldq;
+    float* v;
+    if (h < a.n_head) v = row + h * a.hd;
+    else v = row + qdim + (h - a.n_head) * a.hd;
+    for (int64_t i = threadIdx.x; i < half; i += blockDim.x) {
+        const double f = pow(a.theta, -2.0 * (double)i / (double)a.hd);
+        const double ang = (double)pos * f;
+        const float c = (float)cos(ang), s = (float)sin(ang);
+        const int64_t ia = a.neox ? i : 2 * i, ib = a.neox ? i + half : 2 * i + 1;
+        const float x0 = v[ia], x1 = v[ib];
+        v[ia] = x0 * c - x1 * s;
+        v[ib] = x0 * s + x1 * c;
+    }
+    if (h < a.n_head) return;
+    __syncthreads();
+    const int64_t kh = h - a.n_head;
+    const int64_t slot = npast + m;
+    const float* kr = row + qdim + kh * a.hd;
+    const float* vr = row + qdim + kdim + kh * a.hd;
+    for (int64_t t = threadIdx.x; t < a.hd; t += blockDim.x) {
+        const int64_t idx = slot * kdim + kh * a.hd + t;
+        if (a.kv_f16) {
+            ((_Float16*)a.kc)[idx] = (_Float16)kr[t];
+            ((_Float16*)a.vc)[idx] = (_Float16)vr[t];
+        } else {
+            ((float*)a.kc)[idx] = kr[t];
+            ((float*)a.vc)[idx] = vr[t];
+        }
+    }
+}
+
+hipError_t launch_rope_kv(hipStream_t st, const RopeArgs& a, int64_t M) {
+    if (M == 0) return hipSuccess;
+    hipLaunchKernelGGL(k_rope_kv, dim3((unsigned)M, (unsigned)(a.n_head + a.n_kv)), dim3(64), 0,
+                       st, a);
+    return hipGetLastError();
+}
+
+// ---------------------------------------------------------------- attention
+// Impl::attn (src/engine.cpp:137-177) with an ancestor mask: query row m of
+// head h attends to cache positions [0, npast) and to the tree slots
+// npast + j of its ancestors j (itself included).  kv head = h / (n_head /
+// n_kv); scores are float dots scaled by 1/sqrt(hd); softmax as
+// softmax_inplace (float max, float exp, double sum, float scale).
+__device__ __forceinline__ float kv_load(const void* base, int f16, int64_t idx) {
+    return f16 ? (float)((const _Float16*)base)[idx] : ((const float*)base)[idx];
+}
+
+__global__ void __launch_bounds__(256) k_attention(AttnArgs a) {
+#pragma clang fp contract(off)
+    extern __shared__ float lds[];
+    const int64_t m = blockIdx.x, h = blockIdx.y;
+    const int64_t hd = a.hd, kdim = a.n_kv * hd;
+    const int64_t kvh = h / (a.n_head / a.n_kv);
+    const int64_t npast = *a.npast;
+    float* qv = lds;                  // hd
+    float* sc = lds + hd;             // slots
+    __shared__ int32_t tslot[256];    // tree slots of this row
+    __shared__ int ntree;
+    __shared__ float red[256];
+    __shared__ double redd[256];
+    const int tid = threadIdx.x;
+    for (int64_t t = tid; t < hd; t += 256) qv[t] = a.qkv[m * a.ldq + h * hd + t];
+    if (tid == 0) {
+        int c = 0;
+        const uint32_t* an = a.anc + m * a.anc_words;
+        for (int w = 0; w < a.anc_words; ++w) {
+            uint32_t bits = an[w];
+            while (bits) {
+                const int b = __builtin_ctz(bits);
+                bits &= bits - 1;
+                tslot[c++] = w * 32 + b;
+            }
+        }
+        ntree = c;
+    }
+    __syncthreads();
+    const int64_t n = npast + ntree;
+    const float scale = 1.f / sqrtf((float)hd);
+    const int64_t koff = kvh * hd;
+    for (int64_t s = tid; s < n; s += 256) {
+        const int64_t slot = s < npast ? s : npast + tslot[s - npast];
+        const int64_t base = slot * kdim + koff;
+        float d = 0.f;
+        for (int64_t t = 0; t < hd; ++t) d += qv[t] * kv_load(a.kc, a.kv_f16, base + t);
+        sc[s] = d * scale;
+    }
+    __syncthreads();
+    float mx = -INFINITY;
+    for (int64_t s = tid; s < n; s += 256) mx = fmaxf(mx, sc[s]);
+    red[tid] = mx;
+    __syncthreads();
+    for (int o = 128; o > 0; o >>= 1) {
+        if (tid < o) red[tid] = fmaxf(red[tid], red[tid + o]);
+        __syncthreads();
+    }
+    mx = red[0];
+    double sum = 0.0;
+    for (int64_t s = tid; s < n; s += 256) {
+        const float e = expf(sc[s] - mx);
+        sc[s] = e;
+        sum += (double)e;
+    }
+    redd[tid] = sum;
+    __syncthreads();
+    for (int o = 128; o > 0; o >>= 1) {
+        if (tid < o) redd[tid] += redd[tid + o];
+        __syncthreads();
+    }
+    const float inv = (float)(1.0 / redd[0]);
+    // output: two threads per dimension, each over half the slots
+    const int64_t dim = tid % 128, part = tid / 128;
+    float* ored = red;  // reuse: [128] partials of part 1
+    float acc = 0.f;
+    if (dim < hd) {
+        for (int64_t s = part; s < n; s += 2) {
+            const float w = sc[s] * inv;
+            if (w == 0.f) continue;
+            const int64_t slot = s < npast ? s : npast + tslot[s - npast];
+            acc += w * kv_load(a.vc, a.kv_f16, slot * kdim + koff + dim);
+        }
+    }
+    __syncthreads();
+    if (part == 1 && dim < hd) ored[dim] = acc;
+    __syncthreads();
+    if (part == 0 && dim < hd) a.out[m * a.n_head * hd + h * hd + dim] = acc + ored[dim];
+    // head_dim above 128 is handled by the loop below
+    for (int64_t t = 128 + tid; t < hd; t += 256) {
+        float o = 0.f;
+        for (int64_t s = 0; s < n; ++s) {
+            const float w = sc[s] * inv;
+            if (w == 0.f) continue;
+            const int64_t slot = s < npast ? s : npast + tslot[s - npast];
+            o += w * kv_load(a.vc, a.kv_f16, slot * kdim + koff + t);
+        }
+        a.out[m * a.n_head * hd + h * hd + t] = o;
+    }
+}
+
+hipError_t launch_attention(hipStream_t st, const AttnArgs& a, int64_t M) {
+    if (M == 0) return hipSuccess;
+    const size_t lds = (size_t)(a.hd + a.max_ctx) * sizeof(float);
+    if (lds > 160 * 1024 - 8 * 1024) return hipErrorInvalidValue;
+    hipLaunchKernelGGL(k_attention, dim3((unsigned)M, (unsigned)a.n_head), dim3(256), lds, st, a);
+    return hipGetLastError();
+}

@@ -1,0 +1,165 @@
+// quant_dev.h -- device-side GGUF block formats.
+//
+// dq8() returns 8 consecutive dequantised elements of a row, bit-exact with
+// dequant_row (include/ft/quant.h:10-84) for the reference types and with the
+// ggml Q4_K / Q6_K layouts under a fixed operation order:
+//   Q4_K: y = (d*sc)*q - (dmin*m)      Q6_K: y = (d*sc)*(q6 - 32)
+// Contraction is switched off inside these functions so that the rounding
+// steps are the ones written.
+#pragma once
+
+#include <hip/hip_runtime.h>
+#include <stdint.h>
+
+#include "../../include/ftx.h"
+
+__device__ __forceinline__ float h2f(uint16_t h) {
+    return (float)__builtin_bit_cast(_Float16, h);
+}
+
+__device__ __forceinline__ float bf2f(uint16_t b) {
+    return __uint_as_float((uint32_t)b << 16);
+}
+
+__device__ __forceinline__ uint16_t ld16(const uint8_t* p) {
+    return (uint16_t)(p[0] | ((uint16_t)p[1] << 8));
+}
+
+// Q4_K 6-bit (scale, min) of sub-block j (ggml get_scale_min_k4 layout)
+__device__ __forceinline__ void q4k_sc_m(int j, const uint8_t* s, int& sc, int& m) {
+    if (j < 4) {
+        sc = s[j] & 63;
+        m = s[j + 4] & 63;
+    } else {
+        sc = (s[j + 4] & 0xF) | ((s[j - 4] >> 6) << 4);
+        m = (s[j + 4] >> 4) | ((s[j] >> 6) << 4);
+    }
+}
+
+__host__ __device__ constexpr int64_t blk_elems(int dt) {
+    return (dt == FTX_Q4_0 || dt == FTX_Q4_1 || dt == FTX_Q8_0) ? 32
+           : (dt == FTX_Q4_K || dt == FTX_Q6_K)                 ? 256
+                                                                : 1;
+}
+
+__host__ __device__ constexpr int64_t blk_bytes(int dt) {
+    return dt == FTX_F32    ? 4
+           : dt == FTX_F16  ? 2
+           : dt == FTX_BF16 ? 2
+           : dt == FTX_Q4_0 ? 18
+           : dt == FTX_Q4_1 ? 20
+           : dt == FTX_Q8_0 ? 34
+           : dt == FTX_Q4_K ? 144
+           : dt == FTX_Q6_K ? 210
+                            : 0;
+}
+
+// Elements e0 .. e0+7 of `row` (e0 % 8 == 0); elements at or past n are 0.
+__device__ inline void dq8(const uint8_t* __restrict__ row, int dt, int64_t e0, int64_t n,
+                           float* __restrict__ o) {
+#pragma clang fp contract(off)
+    switch (dt) {
+        case FTX_F32: {
+            const float* r = (const float*)row;
+#pragma unroll
+            for (int i = 0; i < 8; ++i) {
+                o[i] = 0.f;
+                if (e0 + i < n) o[i] = r[e0 + i];
+            }
+            return;
+        }
+        case FTX_F16: {
+            const uint16_t* r = (const uint16_t*)row;
+#pragma unroll
+            for (int i = 0; i < 8; ++i) {
+                o[i] = 0.f;
+                if (e0 + i < n) o[i] = h2f(r[e0 + i]);
+            }
+            return;
+        }
+        case FTX_BF16: {
+            const uint16_t* r = (const uint16_t*)row;
+#pragma unroll
+            for (int i = 0; i < 8; ++i) {
+                o[i] = 0.f;
+                if (e0 + i < n) o[i] = bf2f(r[e0 + i]);
+            }
+            return;
+        }
+        case FTX_Q8_0: {
+            const uint8_t* p = row + (e0 >> 5) * 34;
+            const float d = h2f(ld16(p));
+            const int j0 = (int)(e0 & 31);
+#pragma unroll
+            for (int i = 0; i < 8; ++i)
+                o[i] = e0 + i < n ? d * (float)(int8_t)p[2 + j0 + i] : 0.f;
+            return;
+        }
+        case FTX_Q4_0: {
+            const uint8_t* p = row + (e0 >> 5) * 18;
+            const float d = h2f(ld16(p));
+            const int j0 = (int)(e0 & 31);
+#pragma unroll
+            for (int i = 0; i < 8; ++i) {
+                const int j = j0 + i;
+                const uint8_t b = p[2 + (j >> 1)];
+                const int nib = (j & 1) ? (b >> 4) : (b & 0xF);
+                o[i] = e0 + i < n ? d * (float)(nib - 8) : 0.f;
+            }
+            return;
+        }
+        case FTX_Q4_1: {
+            const uint8_t* p = row + (e0 >> 5) * 20;
+            const float first = h2f(ld16(p));
+            const float second = h2f(ld16(p + 2));
+            const int j0 = (int)(e0 & 31);
+#pragma unroll
+            for (int i = 0; i < 8; ++i) {
+                const int j = j0 + i;
+                const uint8_t b = p[4 + (j >> 1)];
+                const int nib = (j & 1) ? (b >> 4) : (b & 0xF);
+                o[i] = e0 + i < n ? first + second * (float)nib : 0.f;
+            }
+            return;
+        }
+        case FTX_Q4_K: {
+            const uint8_t* p = row + (e0 >> 8) * 144;
+            const float d = h2f(ld16(p));
+            const float dmin = h2f(ld16(p + 2));
+            const int r = (int)(e0 & 255);
+            const int j = r >> 5, l0 = r & 31, g = j >> 1;
+            int sc, m;
+            q4k_sc_m(j, p + 4, sc, m);
+            const float ds = d * (float)sc;
+            const float dm = dmin * (float)m;
+            const uint8_t* qs = p + 16 + 32 * g + l0;
+#pragma unroll
+            for (int i = 0; i < 8; ++i) {
+                const int q = (j & 1) ? (qs[i] >> 4) : (qs[i] & 0xF);
+                const float t = ds * (float)q;
+                o[i] = e0 + i < n ? t - dm : 0.f;
+            }
+            return;
+        }
+        case FTX_Q6_K: {
+            const uint8_t* p = row + (e0 >> 8) * 210;
+            const int r = (int)(e0 & 255);
+            const int c = r >> 7, rr = r & 127, k = rr >> 5, l0 = rr & 31;
+            const float d = h2f(ld16(p + 208));
+            const float ds = d * (float)(int8_t)p[192 + (r >> 4)];
+            const uint8_t* ql = p + 64 * c + 32 * (k & 1) + l0;
+            const uint8_t* qh = p + 128 + 32 * c + l0;
+#pragma unroll
+            for (int i = 0; i < 8; ++i) {
+                const int lo = (k >> 1) ? (ql[i] >> 4) : (ql[i] & 0xF);
+                const int hi = (qh[i] >> (2 * k)) & 3;
+                o[i] = e0 + i < n ? ds * (float)((lo | (hi << 4)) - 32) : 0.f;
+            }
+            return;
+        }
+        default:
+#pragma unroll
+            for (int i = 0; i < 8; ++i) o[i] = 0.f;
+            return;
+    }
+}

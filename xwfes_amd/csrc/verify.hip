@@ -1,0 +1,362 @@
+// verify.hip -- the device-resident verify step: Engine::forward for M
+// draft tokens (src/engine.cpp:461-596, extend_verify 669-674) with every op
+// on the GPU, plus the acceptance sampler entry point.
+#include <algorithm>
+#include <new>
+
+#include "ftx_internal.h"
+#include "quant_dev.h"
+
+struct ftx_model {
+    ftx_ctx* ctx = nullptr;
+    ftx_model_desc d{};
+    std::vector<const ftx_tensor*> layers;
+    int64_t qdim = 0, kdim = 0, ldq = 0, Mmax = 0;
+    // F32 copies of the norm vectors
+    float* norms = nullptr;  // [n_layer*2 + 1][n_embd]
+    // activations
+    float *x = nullptr, *xn = nullptr, *qkv = nullptr, *att = nullptr, *h = nullptr;
+    float* part = nullptr;
+    size_t part_floats = 0;
+    int32_t* toks = nullptr;
+    int32_t* depth = nullptr;
+    uint32_t* anc = nullptr;
+    int64_t* npast = nullptr;
+};
+
+struct ftx_kv {
+    ftx_ctx* ctx = nullptr;
+    int64_t n_layer = 0, cap = 0, kdim = 0;
+    int kv_f16 = 1;
+    void* k = nullptr;
+    void* v = nullptr;
+    int64_t npast = 0;
+};
+
+static void model_release(ftx_model* m) {
+    if (!m) return;
+    void* bufs[] = {m->norms, m->x, m->xn, m->qkv, m->att, m->h, m->part,
+                    m->toks,  m->depth, m->anc, m->npast};
+    for (void* b : bufs)
+        if (b) (void)hipFree(b);
+    delete m;
+}
+
+template <typename T>
+static bool dalloc(T** p, size_t n) {
+    if (hipMalloc((void**)p, n * sizeof(T) + 256) != hipSuccess) {
+        (void)hipGetLastError();
+        *p = nullptr;
+        return false;
+    }
+    return true;
+}
+
+extern "C" {
+
+int ftx_model_create(ftx_ctx* ctx, const ftx_model_desc* d, ftx_model** out) {
+    if (!ctx || !d || !out || !d->layers || !d->tok_embd || !d->out_norm)
+        return ftx_fail(ctx, FTX_E_INVALID, "null argument");
+    *out = nullptr;
+    if (d->n_layer < 1 || d->n_embd < 1 || d->n_head < 1 || d->n_head_kv < 1 ||
+        d->n_head % d->n_head_kv || d->head_dim < 2 || d->head_dim % 2 || d->n_ff < 1 ||
+        d->vocab < 1)
+        return ftx_fail(ctx, FTX_E_INVALID, "bad model hyper-parameters");
+    const int64_t Mmax = d->max_tokens > 0 ? d->max_tokens : 64;
+    if (Mmax > 256) return ftx_fail(ctx, FTX_E_INVALID, "max_tokens above 256");
+    const int64_t D = d->n_embd, qdim = d->n_head * d->head_dim, kdim = d->n_head_kv * d->head_dim;
+    auto need = [&](const ftx_tensor* t, int64_t cols, int64_t rows, const char* nm) -> int {
+        if (!t) return ftx_fail(ctx, FTX_E_INVALID, std::string("missing tensor ") + nm);
+        if (t->ne[0] != cols || t->nrows != rows)
+            return ftx_fail(ctx, FTX_E_INVALID, std::string("bad shape of tensor ") + nm);
+        return FTX_OK;
+    };
+    int rc;
+    if ((rc = need(d->tok_embd, D, d->vocab, "tok_embd"))) return rc;
+    if ((rc = need(d->out_norm, D, 1, "out_norm"))) return rc;
+    if (d->output && (rc = need(d->output, D, d->vocab, "output"))) return rc;
+    for (int64_t l = 0; l < d->n_layer; ++l) {
+        const ftx_tensor* const* T = d->layers + l * FTX_LAYER_TENSORS;
+        if ((rc = need(T[FTX_T_ATTN_NORM], D, 1, "attn_norm")) ||
+            (rc = need(T[FTX_T_Q], D, qdim, "attn_q")) ||
+            (rc = need(T[FTX_T_K], D, kdim, "attn_k")) ||
+            (rc = need(T[FTX_T_V], D, kdim, "attn_v")) ||
+            (rc = need(T[FTX_T_O], qdim, D, "attn_output")) ||
+            (rc = need(T[FTX_T_FFN_NORM], D, 1, "ffn_norm")) ||
+            (rc = need(T[FTX_T_GATE], D, d->n_ff, "ffn_gate")) ||
+            (rc = need(T[FTX_T_UP], D, d->n_ff, "ffn_up")) ||
+            (rc = need(T[FTX_T_DOWN], D, d->n_ff, "ffn_down")))
+            return rc;
+        if (T[FTX_T_GATE]->dtype != T[FTX_T_UP]->dtype)
+            return ftx_fail(ctx, FTX_E_UNSUPPORTED, "ffn_gate and ffn_up must share a dtype");
+    }
+    ftx_model* m = new (std::nothrow) ftx_model;
+    if (!m) return ftx_fail(ctx, FTX_E_NOMEM, "host allocation failed");
+    m->ctx = ctx;
+    m->d = *d;
+    m->layers.assign(d->layers, d->layers + d->n_layer * FTX_LAYER_TENSORS);
+    m->d.layers = nullptr;
+    m->qdim = qdim;
+    m->kdim = kdim;
+    m->ldq = qdim + 2 * kdim;
+    m->Mmax = Mmax;
+    m->part_floats = down_scratch_floats(Mmax, d->n_ff, D);
+    const size_t nn = (size_t)(d->n_layer * 2 + 1);
+    bool ok = dalloc(&m->norms, nn * D) && dalloc(&m->x, Mmax * D) && dalloc(&m->xn, Mmax * D) &&
+              dalloc(&m->qkv, Mmax * m->ldq) && dalloc(&m->att, Mmax * qdim) &&
+              dalloc(&m->h, Mmax * d->n_ff) && dalloc(&m->part, m->part_floats) &&
+              dalloc(&m->toks, Mmax) && dalloc(&m->depth, Mmax) && dalloc(&m->anc, Mmax * 8) &&
+              dalloc(&m->npast, 1);
+    if (!ok) {
+        model_release(m);
+        return ftx_fail(ctx, FTX_E_NOMEM, "activation allocation failed");
+    }
+    // norm vectors as F32 (any stored dtype is dequantised once)
+    for (int64_t l = 0; l <= d->n_layer; ++l) {
+        for (int k = 0; k < 2; ++k) {
+            if (l == d->n_layer && k == 1) break;
+            const ftx_tensor* t =
+                l == d->n_layer ? d->out_norm
+                                : d->layers[l * FTX_LAYER_TENSORS + (k ? FTX_T_FFN_NORM : FTX_T_ATTN_NORM)];
+            hipError_t e = launch_dequant(ctx->stream, t->data, t->dtype, t->row_bytes, D, 1,
+                                          m->norms + (l * 2 + k) * D);
+            if (e != hipSuccess) {
+                model_release(m);
+                return ftx_fail(ctx, FTX_E_DEVICE, "norm dequant failed");
+            }
+        }
+    }
+    if (hipStreamSynchronize(ctx->stream) != hipSuccess) {
+        model_release(m);
+        return ftx_fail(ctx, FTX_E_DEVICE, "norm dequant failed");
+    }
+    *out = m;
+    return FTX_OK;
+}
+
+int ftx_model_free(ftx_model* m) {
+    if (m && m->ctx) (void)hipStreamSynchronize(m->ctx->stream);
+    model_release(m);
+    return FTX_OK;
+}
+
+int ftx_kv_create(ftx_ctx* ctx, const ftx_model* m, int64_t cap, int kv_dtype, ftx_kv** out) {
+    if (!ctx || !m || !out) return ftx_fail(ctx, FTX_E_INVALID, "null argument");
+    if (cap < 1) return ftx_fail(ctx, FTX_E_INVALID, "cap must be >= 1");
+    if (kv_dtype != FTX_KV_F16 && kv_dtype != FTX_KV_F32)
+        return ftx_fail(ctx, FTX_E_UNSUPPORTED, "kv dtype");
+    ftx_kv* kv = new (std::nothrow) ftx_kv;
+    if (!kv) return ftx_fail(ctx, FTX_E_NOMEM, "host allocation failed");
+    kv->ctx = ctx;
+    kv->n_layer = m->d.n_layer;
+    kv->cap = cap;
+    kv->kdim = m->kdim;
+    kv->kv_f16 = kv_dtype == FTX_KV_F16;
+    const size_t bytes = (size_t)(kv->n_layer * cap * kv->kdim) * (kv->kv_f16 ? 2 : 4);
+    if (hipMalloc(&kv->k, bytes) != hipSuccess || hipMalloc(&kv->v, bytes) != hipSuccess) {
+        (void)hipGetLastError();
+        if (kv->k) (void)hipFree(kv->k);
+        delete kv;
+        return ftx_fail(ctx, FTX_E_NOMEM, "kv allocation failed");
+    }
+    (void)hipMemset(kv->k, 0, bytes);
+    (void)hipMemset(kv->v, 0, bytes);
+    *out = kv;
+    return FTX_OK;
+}
+
+int ftx_kv_free(ftx_kv* kv) {
+    if (!kv) return FTX_OK;
+    if (kv->ctx) (void)hipStreamSynchronize(kv->ctx->stream);
+    if (kv->k) (void)hipFree(kv->k);
+    if (kv->v) (void)hipFree(kv->v);
+    delete kv;
+    return FTX_OK;
+}
+
+int ftx_kv_pointers(ftx_kv* kv, void** k, void** v, int64_t* npast) {
+    if (!kv) return FTX_E_INVALID;
+    if (k) *k = kv->k;
+    if (v) *v = kv->v;
+    if (npast) *npast = kv->npast;
+    return FTX_OK;
+}
+
+int ftx_kv_truncate(ftx_kv* kv, int64_t npast) {
+    if (!kv) return FTX_E_INVALID;
+    if (npast < 0 || npast > kv->cap) return ftx_fail(kv->ctx, FTX_E_RANGE, "npast out of range");
+    kv->npast = npast;
+    return FTX_OK;
+}
+
+int ftx_verify_step(ftx_ctx* ctx, ftx_model* m, ftx_kv* kv, const ftx_verify_args* a) {
+    if (!ctx || !m || !kv || !a || !a->tokens || !a->logits)
+        return ftx_fail(ctx, FTX_E_INVALID, "null argument");
+    const ftx_model_desc& d = m->d;
+    const int64_t M = a->M;
+    if (M < 1 || M > m->Mmax) return ftx_fail(ctx, FTX_E_INVALID, "M out of range");
+    if (kv->n_layer != d.n_layer || kv->kdim != m->kdim)
+        return ftx_fail(ctx, FTX_E_INVALID, "kv cache does not match the model");
+    const int64_t npast = kv->npast;
+    if (npast + M > kv->cap) return ftx_fail(ctx, FTX_E_RANGE, "kv capacity exceeded");
+    // host-side argument prep: tokens, depth, ancestor masks, npast
+    const int aw = (int)((M + 31) / 32);
+    const size_t pin_bytes = (size_t)M * 4 * 2 + (size_t)M * aw * 4 + 64;
+    uint8_t* pin;
+    int rc = ftx_pinned(ctx, pin_bytes, (void**)&pin);
+    if (rc) return rc;
+    FTX_HIP(ctx, hipStreamSynchronize(ctx->stream));  // pinned buffer reuse
+    int32_t* toks = (int32_t*)pin;
+    int32_t* depth = toks + M;
+    uint32_t* anc = (uint32_t*)(depth + M);
+    int64_t* np = (int64_t*)(((uintptr_t)(anc + M * aw) + 7) & ~(uintptr_t)7);
+    for (int64_t i = 0; i < M; ++i) {
+        const int32_t t = a->tokens[i];
+        if (t < 0 || t >= d.vocab) return ftx_fail(ctx, FTX_E_RANGE, "token id out of range");
+        const int32_t p = a->parents ? a->parents[i] : (int32_t)i - 1;
+        if (p < -1 || p >= i) return ftx_fail(ctx, FTX_E_INVALID, "parents[i] must be in [-1, i)");
+        toks[i] = t;
+        depth[i] = p < 0 ? 0 : depth[p] + 1;
+        uint32_t* row = anc + i * aw;
+        if (p >= 0)
+            for (int w = 0; w < aw; ++w) row[w] = anc[p * aw + w];
+        else
+            for (int w = 0; w < aw; ++w) row[w] = 0;
+        row[i / 32] |= 1u << (i % 32);
+    }
+    *np = npast;
+    hipStream_t st = ctx->stream;
+    FTX_HIP(ctx, hipMemcpyAsync(m->toks, toks, M * 4, hipMemcpyHostToDevice, st));
+    FTX_HIP(ctx, hipMemcpyAsync(m->depth, depth, M * 4, hipMemcpyHostToDevice, st));
+    FTX_HIP(ctx, hipMemcpyAsync(m->anc, anc, (size_t)M * aw * 4, hipMemcpyHostToDevice, st));
+    FTX_HIP(ctx, hipMemcpyAsync(m->npast, np, 8, hipMemcpyHostToDevice, st));
+
+    const int64_t D = d.n_embd, F = d.n_ff, V = d.vocab;
+    const float eps = d.rms_eps;
+    FTX_HIP(ctx, launch_embed(st, d.tok_embd->data, d.tok_embd->dtype, d.tok_embd->row_bytes, D,
+                              m->toks, M, m->x));
+    const size_t kvel = kv->kv_f16 ? 2 : 4;
+    for (int64_t l = 0; l < d.n_layer; ++l) {
+        const ftx_tensor* const* T = m->layers.data() + l * FTX_LAYER_TENSORS;
+        FTX_HIP(ctx, launch_rmsnorm(st, m->x, m->norms + (l * 2) * D, D, M, eps, m->xn));
+        GemvSeg qkv[3] = {
+            {T[FTX_T_Q]->data, T[FTX_T_Q]->dtype, T[FTX_T_Q]->row_bytes, m->qdim, m->qkv, m->ldq},
+            {T[FTX_T_K]->data, T[FTX_T_K]->dtype, T[FTX_T_K]->row_bytes, m->kdim, m->qkv + m->qdim,
+             m->ldq},
+            {T[FTX_T_V]->data, T[FTX_T_V]->dtype, T[FTX_T_V]->row_bytes, m->kdim,
+             m->qkv + m->qdim + m->kdim, m->ldq}};
+        FTX_HIP(ctx, launch_gemv(st, qkv, 3, m->xn, D, D, M, EPI_STORE));
+        uint8_t* kl = (uint8_t*)kv->k + (size_t)(l * kv->cap * kv->kdim) * kvel;
+        uint8_t* vl = (uint8_t*)kv->v + (size_t)(l * kv->cap * kv->kdim) * kvel;
+        RopeArgs ra{m->qkv, m->ldq, d.n_head, d.n_head_kv, d.head_dim, m->depth, m->npast,
+                    d.rope_theta, d.rope_neox, kl, vl, kv->kv_f16};
+        FTX_HIP(ctx, launch_rope_kv(st, ra, M));
+        AttnArgs aa{m->qkv,  m->ldq, kl,           vl,         kv->kv_f16, m->npast,
+                    m->anc,  aw,     d.n_head,     d.n_head_kv, d.head_dim, npast + M,
+                    m->att};
+        FTX_HIP(ctx, launch_attention(st, aa, M));
+        GemvSeg o{T[FTX_T_O]->data, T[FTX_T_O]->dtype, T[FTX_T_O]->row_bytes, D, m->x, D};
+        FTX_HIP(ctx, launch_gemv(st, &o, 1, m->att, m->qdim, m->qdim, M, EPI_ACCUM));
+        FTX_HIP(ctx, launch_rmsnorm(st, m->x, m->norms + (l * 2 + 1) * D, D, M, eps, m->xn));
+        FTX_HIP(ctx, launch_gemv_swiglu(st, T[FTX_T_GATE]->data, T[FTX_T_UP]->data,
+                                        T[FTX_T_GATE]->dtype, T[FTX_T_GATE]->row_bytes, F, m->xn,
+                                        D, D, M, m->h, F));
+        FTX_HIP(ctx, launch_down(st, T[FTX_T_DOWN]->data, T[FTX_T_DOWN]->dtype,
+                                 T[FTX_T_DOWN]->row_bytes, F, D, m->h, F, M, m->x, D, m->part));
+    }
+    FTX_HIP(ctx, launch_rmsnorm(st, m->x, m->norms + (d.n_layer * 2) * D, D, M, eps, m->xn));
+    const ftx_tensor* lm = d.output ? d.output : d.tok_embd;
+    GemvSeg hs{lm->data, lm->dtype, lm->row_bytes, V, a->logits, V};
+    FTX_HIP(ctx, launch_gemv(st, &hs, 1, m->xn, D, D, M, EPI_STORE));
+    if (a->advance) kv->npast = npast + M;
+    return FTX_OK;
+}
+
+int ftx_accept(ftx_ctx* ctx, const ftx_accept_args* a) {
+    if (!ctx || !a || !a->base_row || !a->props || !a->rng || !a->accepted || !a->n_acc ||
+        !a->bonus)
+        return ftx_fail(ctx, FTX_E_INVALID, "null argument");
+    const int64_t M = a->M, V = a->V;
+    if (M < 0 || V < 1 || (M > 0 && !a->rows)) return ftx_fail(ctx, FTX_E_INVALID, "bad M or V");
+    if (a->mode != FTX_ACCEPT_GREEDY && a->mode != FTX_ACCEPT_RATIO &&
+        a->mode != FTX_ACCEPT_RESIDUAL)
+        return ftx_fail(ctx, FTX_E_UNSUPPORTED, "unknown acceptance mode");
+    if (a->mode == FTX_ACCEPT_RATIO && (!a->pd && M > 0))
+        return ftx_fail(ctx, FTX_E_INVALID, "ratio mode needs pd");
+    if (a->mode == FTX_ACCEPT_RESIDUAL && (!a->q && M > 0))
+        return ftx_fail(ctx, FTX_E_INVALID, "residual mode needs q");
+    if (!(a->temp > 0.f)) return ftx_fail(ctx, FTX_E_INVALID, "temperature must be > 0");
+    for (int64_t i = 0; i < M; ++i) {
+        const int32_t p = a->parents ? a->parents[i] : (int32_t)i - 1;
+        if (p < -1 || p >= i) return ftx_fail(ctx, FTX_E_INVALID, "parents[i] must be in [-1, i)");
+        if (a->props[i] < 0 || a->props[i] >= V)
+            return ftx_fail(ctx, FTX_E_RANGE, "draft token out of range");
+        if (a->mode == FTX_ACCEPT_RATIO && p != i - 1)
+            return ftx_fail(ctx, FTX_E_INVALID, "ratio mode is chain only");
+    }
+    // workspace: stats [M+1], p [V] doubles, out ints, rng, margin, props,
+    // parents, pd
+    const size_t stats_b = (size_t)(M + 1) * sizeof(RowStats);
+    const size_t off_p = (stats_b + 255) & ~(size_t)255;
+    const size_t off_out = off_p + (((size_t)V * 8 + 255) & ~(size_t)255);
+    const size_t off_small = off_out + (((size_t)(M + 2) * 4 + 255) & ~(size_t)255);
+    const size_t small_b = 8 + 8 + (size_t)M * 12 + 64;
+    uint8_t* ws;
+    int rc = ftx_workspace(ctx, off_small + small_b, (void**)&ws);
+    if (rc) return rc;
+    uint8_t* pin;
+    rc = ftx_pinned(ctx, small_b + (size_t)(M + 2) * 4 + 64, (void**)&pin);
+    if (rc) return rc;
+    hipStream_t st = ctx->stream;
+    FTX_HIP(ctx, hipStreamSynchronize(st));
+    // small host block: rng | margin | props | parents | pd
+    uint64_t* h_rng = (uint64_t*)pin;
+    float* h_margin = (float*)(pin + 8);
+    int32_t* h_props = (int32_t*)(pin + 16);
+    int32_t* h_par = h_props + M;
+    float* h_pd = (float*)(h_par + M);
+    int32_t* h_out = (int32_t*)(pin + small_b);
+    *h_rng = *a->rng;
+    *h_margin = INFINITY;
+    for (int64_t i = 0; i < M; ++i) {
+        h_props[i] = a->props[i];
+        h_par[i] = a->parents ? a->parents[i] : (int32_t)i - 1;
+        h_pd[i] = a->pd ? a->pd[i] : 0.f;
+    }
+    uint8_t* d_small = ws + off_small;
+    FTX_HIP(ctx, hipMemcpyAsync(d_small, pin, small_b, hipMemcpyHostToDevice, st));
+    RowStats* stats = (RowStats*)ws;
+    FTX_HIP(ctx, launch_row_stats(st, a->base_row, 1, V, a->temp, stats));
+    if (M > 0) FTX_HIP(ctx, launch_row_stats(st, a->rows, M, V, a->temp, stats + 1));
+    AcceptDev ad{};
+    ad.base_row = a->base_row;
+    ad.rows = a->rows;
+    ad.q = a->q;
+    ad.stats = stats;
+    ad.M = M;
+    ad.V = V;
+    ad.props = (const int32_t*)(d_small + 16);
+    ad.parents = ad.props + M;
+    ad.pd = (const float*)(ad.parents + M);
+    ad.mode = a->mode;
+    ad.temp = a->temp;
+    ad.rng = (uint64_t*)d_small;
+    ad.p = (double*)(ws + off_p);
+    ad.part = nullptr;
+    ad.out = (int32_t*)(ws + off_out);
+    ad.margin = (float*)(d_small + 8);
+    FTX_HIP(ctx, launch_accept(st, ad));
+    FTX_HIP(ctx, hipMemcpyAsync(h_out, ad.out, (size_t)(M + 2) * 4, hipMemcpyDeviceToHost, st));
+    FTX_HIP(ctx, hipMemcpyAsync(pin, d_small, 16, hipMemcpyDeviceToHost, st));
+    FTX_HIP(ctx, hipStreamSynchronize(st));
+    const int32_t na = h_out[0];
+    if (na < 0 || na > M) return ftx_fail(ctx, FTX_E_DEVICE, "acceptance returned a bad count");
+    *a->n_acc = na;
+    *a->bonus = h_out[1];
+    for (int32_t i = 0; i < na; ++i) a->accepted[i] = h_out[2 + i];
+    *a->rng = *h_rng;
+    if (a->margin) *a->margin = *h_margin;
+    return FTX_OK;
+}
+
+}  // extern "C"
