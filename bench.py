@@ -1,0 +1,231 @@
+#!/usr/bin/env python3
+"""Verify-step benchmark on one MI355X.
+
+A step is one speculative-decoding verification of an 8-token linear draft
+against a Llama-3-8B-shaped random-init Q4_K_M model at context 2048: the
+device-resident forward of the 8 draft tokens (ftx_verify_step) followed by
+stochastic acceptance at T = 0.8 with the reference's ratio test and seeded
+SplitMix64 uniforms plus the bonus token (ftx_accept).  Inputs (weights, KV
+context, draft) are resident in HBM before the timed region.
+
+Prints one JSON line.  `value` = verified tokens per second (M / t_step).
+"""
+import argparse
+import json
+import os
+import statistics
+import sys
+import time
+
+import numpy as np
+
+ROOT = os.path.dirname(os.path.abspath(__file__))
+sys.path.insert(0, ROOT)
+
+HBM_PEAK_GBS = 8000.0
+WORKLOADS = {
+    # name: (model cfg, mix, context, draft length, acceptance temperature)
+    "llama3-8b-q4km-k8-ctx2048": dict(
+        cfg=dict(n_layer=32, n_embd=4096, n_head=32, n_head_kv=8, head_dim=128, n_ff=14336,
+                 vocab=128256, rope_theta=500000.0, rope_neox=0, rms_eps=1e-5),
+        mix="q4_k_m", ctx=2048, M=8, temp=0.8),
+}
+
+
+def log(msg):
+    print("[bench] " + msg, file=sys.stderr, flush=True)
+
+
+def draft(V, M, seed):
+    """q_a ~ Dirichlet(1) over the vocab (normalised -log u); props[a] drawn
+    from q_a by inverse CDF; pd[a] = q_a(props[a])."""
+    rng = np.random.default_rng(seed)
+    props = np.zeros(M, np.int32)
+    pd = np.zeros(M, np.float32)
+    for a in range(M):
+        e = -np.log(rng.random(V))
+        q = e / e.sum()
+        props[a] = min(int(np.searchsorted(np.cumsum(q), rng.random())), V - 1)
+        pd[a] = np.float32(q[props[a]])
+    return props, pd
+
+
+def step_bytes(tensors, cfg, ctx_len, M):
+    """Algorithmic HBM bytes of one verify step: every weight tensor at its
+    stored size (the LM head counted once), the KV read 2*L*(ctx+M)*kvdim*2 B,
+    M embedding rows and the M*V*4 B logits write."""
+    L, d, V = cfg["n_layer"], cfg["n_embd"], cfg["vocab"]
+    kdim = cfg["n_head_kv"] * cfg["head_dim"]
+    w = sum(t.nbytes for n, t in tensors.items() if n != "tok_embd")
+    emb = M * tensors["tok_embd"].nbytes // V
+    kv = 2 * L * (ctx_len + M) * kdim * 2
+    logits = M * V * 4
+    return w + emb + kv + logits
+
+
+def cpu_baseline(ctx, tensors, cfg, ctx_len, M, props, threads):
+    """The oracle's reference loop nest (CpuBackend::matmul, matmul_down_axpy,
+    Impl::attn) timed on this host on a bounded sample: 1-layer and 2-layer
+    forwards of the same weights (layer 0, tok_embd, output) at the same M and
+    context, extrapolated linearly to all layers."""
+    sys.path.insert(0, os.path.join(ROOT, "oracle"))
+    import pyoracle as P
+    orc = P.Oracle()
+    orc.set_threads(threads)
+
+    def host(t):
+        raw = np.empty(t.nbytes, np.uint8)
+        ctx.copy(raw.ctypes.data, t.ptr, t.nbytes)
+        return dict(raw=raw, dtype=t.dtype, ne0=t.ne[0], ne1=t.ne[1])
+
+    base = {k: host(tensors[k]) for k in ("tok_embd", "output", "out_norm")}
+    layer0 = {nm: host(tensors["blk.0." + nm]) for nm in P.LAYER_TENSORS}
+    kdim = cfg["n_head_kv"] * cfg["head_dim"]
+    rng = np.random.default_rng(4)
+    times = {}
+    for nl in (1, 2):
+        model = dict(base)
+        model["cfg"] = dict(cfg, n_layer=nl)
+        for l in range(nl):
+            for nm in P.LAYER_TENSORS:
+                model["blk.%d.%s" % (l, nm)] = layer0[nm]
+        cap = ctx_len + M
+        k = rng.standard_normal((nl, cap, kdim)).astype(np.float16)
+        v = rng.standard_normal((nl, cap, kdim)).astype(np.float16)
+        orc.forward(model, k, v, ctx_len, props[:1])  # warm caches and threads
+        t0 = time.perf_counter()
+        orc.forward(model, k, v, ctx_len, props)
+        times[nl] = time.perf_counter() - t0
+    t_layer = max(times[2] - times[1], 0.0)
+    t_step = times[1] + (cfg["n_layer"] - 1) * t_layer
+    return dict(value=M / t_step, unit="verified tokens/s", cores=threads, kind="port",
+                sample="oracle forward of M=%d tokens at ctx %d over 1 and 2 layers of the same "
+                       "weights (%.2f s, %.2f s), extrapolated to %d layers: %.3f s/step"
+                       % (M, ctx_len, times[1], times[2], cfg["n_layer"], t_step))
+
+
+def main():
+    ap = argparse.ArgumentParser()
+    ap.add_argument("--gpus", type=int, default=1)
+    ap.add_argument("--steps", type=int, default=50)
+    ap.add_argument("--warmup", type=int, default=5)
+    ap.add_argument("--workload", default="llama3-8b-q4km-k8-ctx2048", choices=sorted(WORKLOADS))
+    ap.add_argument("--no-cpu-baseline", action="store_true")
+    ap.add_argument("--trace-steps", type=int, default=10)
+    args = ap.parse_args()
+    if args.gpus != 1:
+        print("bench.py measures one GPU: the verify step runs on a single MI355X and this "
+              "build has no multi-GPU path (asked for --gpus %d)" % args.gpus, file=sys.stderr)
+        sys.exit(2)
+
+    from xwfes_amd import ftx, synth
+    W = WORKLOADS[args.workload]
+    cfg, ctx_len, M, temp = W["cfg"], W["ctx"], W["M"], W["temp"]
+    V = cfg["vocab"]
+    ctx = ftx.Context(0)
+    t0 = time.perf_counter()
+    tensors = synth.build(ctx, cfg, synth.q4_k_m_mix(cfg), seed=1)
+    log("model built in %.1f s (%.3f GB of weights)" % (time.perf_counter() - t0,
+                                                        synth.weight_bytes(tensors) / 1e9))
+    model = ctx.model(cfg, tensors, max_tokens=M)
+    kv = model.kv(ctx_len + M + 8)
+    kp, vp, _ = kv.pointers()
+    n_kv = cfg["n_layer"] * kv.cap * cfg["n_head_kv"] * cfg["head_dim"]
+    ctx.fill_normal(kp, n_kv, seed=4, std=1.0, dtype=ftx.F16)
+    ctx.fill_normal(vp, n_kv, seed=5, std=1.0, dtype=ftx.F16)
+    logits = ctx.buffer(M * V * 4)
+    base = ctx.buffer(V * 4)
+    # the base row: logits of the last committed token (position ctx - 1)
+    kv.truncate(ctx_len - 1)
+    model.verify(kv, [int(np.random.default_rng(3).integers(V))], base.ptr, advance=True)
+    ctx.sync()
+    props, pd = draft(V, M, seed=6)
+    rng_state = [5]
+    accepted = []
+
+    def step():
+        kv.truncate(ctx_len)
+        model.verify(kv, props, logits.ptr)
+        r = ctx.accept(base.ptr, logits.ptr, M, V, props, ftx.ACCEPT_RATIO, temp=temp,
+                       rng=rng_state[0], pd=pd)
+        rng_state[0] = r["rng"]
+        accepted.append(len(r["accepted"]))
+
+    for _ in range(args.warmup):
+        step()
+    ctx.sync()
+    accepted.clear()
+    per = []
+    ctx.sync()
+    t_start = time.perf_counter()
+    for _ in range(args.steps):
+        ts = time.perf_counter()
+        step()
+        per.append(time.perf_counter() - ts)
+    ctx.sync()
+    elapsed = time.perf_counter() - t_start
+    ms_step = elapsed / args.steps * 1e3
+    med_ms = statistics.median(per) * 1e3
+    log("timed %d steps: mean %.3f ms, median %.3f ms" % (args.steps, ms_step, med_ms))
+
+    # per-kernel-class device time from HIP events on the launch stream
+    ctx.trace(True)
+    for _ in range(args.trace_steps):
+        step()
+    tr = ctx.trace_read()
+    ctx.trace(False)
+    traced_ms = sum(e["ms"] for e in tr.values()) / max(args.trace_steps, 1)
+    dom_name, dom = max(tr.items(), key=lambda kv_: kv_[1]["ms"])
+    per_launch_b = dom["bytes"] / dom["launches"]
+    per_launch_ms = dom["ms"] / dom["launches"]
+    achieved = per_launch_b / (per_launch_ms * 1e-3) / 1e9
+    for name, e in sorted(tr.items(), key=lambda kv_: -kv_[1]["ms"]):
+        log("  %-12s %5d launches %8.3f ms/step  %7.1f GB/s" % (
+            name, e["launches"] // args.trace_steps, e["ms"] / args.trace_steps,
+            e["bytes"] / (e["ms"] * 1e-3) / 1e9 if e["ms"] > 0 else 0.0))
+
+    sb = step_bytes(tensors, cfg, ctx_len, M)
+    gbs = sb / (ms_step * 1e-3) / 1e9
+    out = {
+        "metric": "verify-step tokens/s + HBM GB/s (% of peak), 8B-shape Q4_K, K=8 draft, 1 GPU",
+        "value": round(M / (ms_step * 1e-3), 2),
+        "unit": "verified tokens/s",
+        "n_gpus": 1, "steps": args.steps, "warmup": args.warmup,
+        "ms_per_step": round(ms_step, 4),
+        "ms_per_step_median": round(med_ms, 4),
+        "higher_is_better": True, "scaling": "weak", "vs_baseline": None,
+        "dtype": "q4_k/q6_k weights, f16 KV, fp32 accumulate",
+        "data": "synthetic: random-init N(0,0.02) weights quantised on device, N(0,1) fp16 KV, "
+                "Dirichlet(1) draft",
+        "config": {"workload": args.workload, "M": M, "ctx": ctx_len, "layers": cfg["n_layer"],
+                   "d_model": cfg["n_embd"], "vocab": V, "mix": W["mix"], "accept": "ratio",
+                   "temperature": temp, "batch": 1},
+        "step_bytes": sb,
+        "hbm_gbs": round(gbs, 1),
+        "hbm_frac": round(gbs / HBM_PEAK_GBS, 4),
+        "committed_tokens_per_s": round((statistics.mean(accepted) + 1) / (ms_step * 1e-3), 2),
+        "mean_accepted": round(statistics.mean(accepted), 3),
+        "traced_device_ms_per_step": round(traced_ms, 4),
+        "roofline": {"bound": "hbm", "kernel": dom_name, "achieved": round(achieved, 1),
+                     "peak": HBM_PEAK_GBS, "unit": "GB/s",
+                     "frac": round(achieved / HBM_PEAK_GBS, 4),
+                     "bytes_per_launch": per_launch_b, "us_per_launch": round(per_launch_ms * 1e3, 2),
+                     "traffic": None},
+        "cpu_baseline": None,
+    }
+    if not args.no_cpu_baseline:
+        threads = min(16, os.cpu_count() or 1)
+        t0 = time.perf_counter()
+        out["cpu_baseline"] = cpu_baseline(ctx, tensors, cfg, ctx_len, M, props, threads)
+        log("cpu baseline in %.1f s" % (time.perf_counter() - t0))
+    print(json.dumps(out), flush=True)
+    logits.free()
+    base.free()
+    kv.free()
+    model.free()
+    synth.free(tensors)
+    ctx.close()
+
+
+if __name__ == "__main__":
+    main()

@@ -231,6 +231,19 @@ typedef struct {
 } ftx_accept_args;
 int ftx_accept(ftx_ctx* ctx, const ftx_accept_args* a);
 
+/* ---- kernel trace (the reference keeps wall-clock RunStats only,
+ * include/ft/engine.h:25-39) ---- */
+typedef struct {
+    char name[24];
+    int64_t launches;
+    double ms;     /* summed device time between HIP events around each launch */
+    double bytes;  /* summed algorithmic bytes (weights at stored size, KV, rows) */
+} ftx_trace_entry;
+/* enable != 0 starts recording (and clears earlier records); 0 stops. */
+int ftx_trace(ftx_ctx* ctx, int enable);
+/* Waits for the stream, then returns one entry per kernel class seen. */
+int ftx_trace_read(ftx_ctx* ctx, ftx_trace_entry* out, int max, int* n);
+
 #ifdef __cplusplus
 }
 #endif

@@ -12,8 +12,38 @@
 
 // ---------------------------------------------------------------- host side
 
+// kernel classes recorded by the trace
+enum TraceKind {
+    TK_EMBED = 0,
+    TK_RMSNORM,
+    TK_GEMV_QKV,
+    TK_ROPE_KV,
+    TK_ATTENTION,
+    TK_GEMV_O,
+    TK_GEMV_SWIGLU,
+    TK_DOWN,
+    TK_HEAD,
+    TK_ROW_STATS,
+    TK_ACCEPT,
+    TK_COUNT
+};
+
+struct TraceRec {
+    int kind;
+    int ev0, ev1;
+    double bytes;
+};
+
 struct ftx_ctx {
     int device = 0;
+    // trace: events around launches, resolved by ftx_trace_read
+    bool trace = false;
+    std::vector<hipEvent_t> events;
+    int next_event = 0;
+    std::vector<TraceRec> pending;
+    int64_t tr_launches[TK_COUNT] = {};
+    double tr_ms[TK_COUNT] = {};
+    double tr_bytes[TK_COUNT] = {};
     hipStream_t own_stream = nullptr;
     hipStream_t stream = nullptr;
     std::string err;
@@ -54,6 +84,11 @@ int ftx_workspace(ftx_ctx* ctx, size_t bytes, void** out);
 // pinned host staging of at least `bytes`
 int ftx_pinned(ftx_ctx* ctx, size_t bytes, void** out);
 bool ftx_is_device_ptr(const void* p);
+
+// trace brackets: tr_begin returns a token (-1 when tracing is off) that
+// tr_end closes after the launch
+int tr_begin(ftx_ctx* ctx);
+void tr_end(ftx_ctx* ctx, int token, int kind, double bytes);
 
 // ---------------------------------------------------------------- launchers
 // All enqueue on `st` and return hipError_t of the launch.

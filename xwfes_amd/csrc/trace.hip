@@ -1,0 +1,100 @@
+// trace.hip -- per-kernel-class device time from HIP events recorded around
+// each launch on the context's stream (ftx_trace / ftx_trace_read).
+#include <cstdio>
+
+#include "ftx_internal.h"
+
+static const char* kTraceNames[TK_COUNT] = {
+    "embed", "rmsnorm", "gemv_qkv", "rope_kv", "attention", "gemv_o",
+    "gemv_swiglu", "down", "head", "row_stats", "accept"};
+
+static void resolve(ftx_ctx* ctx) {
+    if (ctx->pending.empty()) {
+        ctx->next_event = 0;
+        return;
+    }
+    (void)hipStreamSynchronize(ctx->stream);
+    for (const TraceRec& r : ctx->pending) {
+        float ms = 0.f;
+        if (hipEventElapsedTime(&ms, ctx->events[r.ev0], ctx->events[r.ev1]) != hipSuccess) {
+            (void)hipGetLastError();
+            continue;
+        }
+        ctx->tr_launches[r.kind] += 1;
+        ctx->tr_ms[r.kind] += ms;
+        ctx->tr_bytes[r.kind] += r.bytes;
+    }
+    ctx->pending.clear();
+    ctx->next_event = 0;
+}
+
+static int take_event(ftx_ctx* ctx) {
+    if (ctx->next_event >= (int)ctx->events.size()) {
+        hipEvent_t e;
+        if (hipEventCreate(&e) != hipSuccess) {
+            (void)hipGetLastError();
+            return -1;
+        }
+        ctx->events.push_back(e);
+    }
+    return ctx->next_event++;
+}
+
+int tr_begin(ftx_ctx* ctx) {
+    if (!ctx->trace) return -1;
+    if (ctx->next_event > 4096) resolve(ctx);
+    const int e = take_event(ctx);
+    if (e < 0) return -1;
+    if (hipEventRecord(ctx->events[e], ctx->stream) != hipSuccess) {
+        (void)hipGetLastError();
+        return -1;
+    }
+    return e;
+}
+
+void tr_end(ftx_ctx* ctx, int token, int kind, double bytes) {
+    if (token < 0 || !ctx->trace) return;
+    const int e = take_event(ctx);
+    if (e < 0) return;
+    if (hipEventRecord(ctx->events[e], ctx->stream) != hipSuccess) {
+        (void)hipGetLastError();
+        return;
+    }
+    ctx->pending.push_back(TraceRec{kind, token, e, bytes});
+}
+
+extern "C" {
+
+int ftx_trace(ftx_ctx* ctx, int enable) {
+    if (!ctx) return FTX_E_INVALID;
+    resolve(ctx);
+    ctx->trace = enable != 0;
+    if (enable)
+        for (int k = 0; k < TK_COUNT; ++k) {
+            ctx->tr_launches[k] = 0;
+            ctx->tr_ms[k] = 0;
+            ctx->tr_bytes[k] = 0;
+        }
+    return FTX_OK;
+}
+
+int ftx_trace_read(ftx_ctx* ctx, ftx_trace_entry* out, int max, int* n) {
+    if (!ctx || !n || (max > 0 && !out)) return FTX_E_INVALID;
+    resolve(ctx);
+    int c = 0;
+    for (int k = 0; k < TK_COUNT; ++k) {
+        if (!ctx->tr_launches[k]) continue;
+        if (c < max) {
+            memset(&out[c], 0, sizeof(out[c]));
+            snprintf(out[c].name, sizeof(out[c].name), "%s", kTraceNames[k]);
+            out[c].launches = ctx->tr_launches[k];
+            out[c].ms = ctx->tr_ms[k];
+            out[c].bytes = ctx->tr_bytes[k];
+        }
+        ++c;
+    }
+    *n = c < max ? c : max;
+    return FTX_OK;
+}
+
+}  // extern "C"

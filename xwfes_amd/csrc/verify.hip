@@ -233,41 +233,66 @@ int ftx_verify_step(ftx_ctx* ctx, ftx_model* m, ftx_kv* kv, const ftx_verify_arg
 
     const int64_t D = d.n_embd, F = d.n_ff, V = d.vocab;
     const float eps = d.rms_eps;
-    FTX_HIP(ctx, launch_embed(st, d.tok_embd->data, d.tok_embd->dtype, d.tok_embd->row_bytes, D,
-                              m->toks, M, m->x));
+    const double f4 = 4.0, Md = (double)M;
+    auto wbytes = [](const ftx_tensor* t) { return (double)(t->row_bytes * t->nrows); };
+#define TRACED(kind, bytes, call)                 \
+    do {                                          \
+        const int tk_ = tr_begin(ctx);            \
+        FTX_HIP(ctx, call);                       \
+        tr_end(ctx, tk_, (kind), (double)(bytes)); \
+    } while (0)
+    TRACED(TK_EMBED, Md * d.tok_embd->row_bytes + Md * D * f4,
+           launch_embed(st, d.tok_embd->data, d.tok_embd->dtype, d.tok_embd->row_bytes, D,
+                        m->toks, M, m->x));
     const size_t kvel = kv->kv_f16 ? 2 : 4;
+    const double norm_b = 2 * Md * D * f4 + D * f4;
     for (int64_t l = 0; l < d.n_layer; ++l) {
         const ftx_tensor* const* T = m->layers.data() + l * FTX_LAYER_TENSORS;
-        FTX_HIP(ctx, launch_rmsnorm(st, m->x, m->norms + (l * 2) * D, D, M, eps, m->xn));
+        TRACED(TK_RMSNORM, norm_b,
+               launch_rmsnorm(st, m->x, m->norms + (l * 2) * D, D, M, eps, m->xn));
         GemvSeg qkv[3] = {
             {T[FTX_T_Q]->data, T[FTX_T_Q]->dtype, T[FTX_T_Q]->row_bytes, m->qdim, m->qkv, m->ldq},
             {T[FTX_T_K]->data, T[FTX_T_K]->dtype, T[FTX_T_K]->row_bytes, m->kdim, m->qkv + m->qdim,
              m->ldq},
             {T[FTX_T_V]->data, T[FTX_T_V]->dtype, T[FTX_T_V]->row_bytes, m->kdim,
              m->qkv + m->qdim + m->kdim, m->ldq}};
-        FTX_HIP(ctx, launch_gemv(st, qkv, 3, m->xn, D, D, M, EPI_STORE));
+        TRACED(TK_GEMV_QKV,
+               wbytes(T[FTX_T_Q]) + wbytes(T[FTX_T_K]) + wbytes(T[FTX_T_V]) + Md * D * f4 +
+                   Md * m->ldq * f4,
+               launch_gemv(st, qkv, 3, m->xn, D, D, M, EPI_STORE));
         uint8_t* kl = (uint8_t*)kv->k + (size_t)(l * kv->cap * kv->kdim) * kvel;
         uint8_t* vl = (uint8_t*)kv->v + (size_t)(l * kv->cap * kv->kdim) * kvel;
         RopeArgs ra{m->qkv, m->ldq, d.n_head, d.n_head_kv, d.head_dim, m->depth, m->npast,
                     d.rope_theta, d.rope_neox, kl, vl, kv->kv_f16};
-        FTX_HIP(ctx, launch_rope_kv(st, ra, M));
+        TRACED(TK_ROPE_KV, 2 * Md * m->ldq * f4 + 2 * Md * m->kdim * (double)kvel,
+               launch_rope_kv(st, ra, M));
         AttnArgs aa{m->qkv,  m->ldq, kl,           vl,         kv->kv_f16, m->npast,
                     m->anc,  aw,     d.n_head,     d.n_head_kv, d.head_dim, npast + M,
                     m->att};
-        FTX_HIP(ctx, launch_attention(st, aa, M));
+        TRACED(TK_ATTENTION,
+               2.0 * (double)(npast + M) * m->kdim * (double)kvel + 2 * Md * m->qdim * f4,
+               launch_attention(st, aa, M));
         GemvSeg o{T[FTX_T_O]->data, T[FTX_T_O]->dtype, T[FTX_T_O]->row_bytes, D, m->x, D};
-        FTX_HIP(ctx, launch_gemv(st, &o, 1, m->att, m->qdim, m->qdim, M, EPI_ACCUM));
-        FTX_HIP(ctx, launch_rmsnorm(st, m->x, m->norms + (l * 2 + 1) * D, D, M, eps, m->xn));
-        FTX_HIP(ctx, launch_gemv_swiglu(st, T[FTX_T_GATE]->data, T[FTX_T_UP]->data,
-                                        T[FTX_T_GATE]->dtype, T[FTX_T_GATE]->row_bytes, F, m->xn,
-                                        D, D, M, m->h, F));
-        FTX_HIP(ctx, launch_down(st, T[FTX_T_DOWN]->data, T[FTX_T_DOWN]->dtype,
-                                 T[FTX_T_DOWN]->row_bytes, F, D, m->h, F, M, m->x, D, m->part));
+        TRACED(TK_GEMV_O, wbytes(T[FTX_T_O]) + Md * m->qdim * f4 + 2 * Md * D * f4,
+               launch_gemv(st, &o, 1, m->att, m->qdim, m->qdim, M, EPI_ACCUM));
+        TRACED(TK_RMSNORM, norm_b,
+               launch_rmsnorm(st, m->x, m->norms + (l * 2 + 1) * D, D, M, eps, m->xn));
+        TRACED(TK_GEMV_SWIGLU,
+               wbytes(T[FTX_T_GATE]) + wbytes(T[FTX_T_UP]) + Md * D * f4 + Md * F * f4,
+               launch_gemv_swiglu(st, T[FTX_T_GATE]->data, T[FTX_T_UP]->data,
+                                  T[FTX_T_GATE]->dtype, T[FTX_T_GATE]->row_bytes, F, m->xn, D, D,
+                                  M, m->h, F));
+        TRACED(TK_DOWN, wbytes(T[FTX_T_DOWN]) + Md * F * f4 + 2 * Md * D * f4,
+               launch_down(st, T[FTX_T_DOWN]->data, T[FTX_T_DOWN]->dtype,
+                           T[FTX_T_DOWN]->row_bytes, F, D, m->h, F, M, m->x, D, m->part));
     }
-    FTX_HIP(ctx, launch_rmsnorm(st, m->x, m->norms + (d.n_layer * 2) * D, D, M, eps, m->xn));
+    TRACED(TK_RMSNORM, norm_b,
+           launch_rmsnorm(st, m->x, m->norms + (d.n_layer * 2) * D, D, M, eps, m->xn));
     const ftx_tensor* lm = d.output ? d.output : d.tok_embd;
     GemvSeg hs{lm->data, lm->dtype, lm->row_bytes, V, a->logits, V};
-    FTX_HIP(ctx, launch_gemv(st, &hs, 1, m->xn, D, D, M, EPI_STORE));
+    TRACED(TK_HEAD, wbytes(lm) + Md * D * f4 + Md * V * f4,
+           launch_gemv(st, &hs, 1, m->xn, D, D, M, EPI_STORE));
+#undef TRACED
     if (a->advance) kv->npast = npast + M;
     return FTX_OK;
 }
@@ -326,8 +351,10 @@ int ftx_accept(ftx_ctx* ctx, const ftx_accept_args* a) {
     uint8_t* d_small = ws + off_small;
     FTX_HIP(ctx, hipMemcpyAsync(d_small, pin, small_b, hipMemcpyHostToDevice, st));
     RowStats* stats = (RowStats*)ws;
+    int tk = tr_begin(ctx);
     FTX_HIP(ctx, launch_row_stats(st, a->base_row, 1, V, a->temp, stats));
     if (M > 0) FTX_HIP(ctx, launch_row_stats(st, a->rows, M, V, a->temp, stats + 1));
+    tr_end(ctx, tk, TK_ROW_STATS, (double)(M + 1) * V * 4);
     AcceptDev ad{};
     ad.base_row = a->base_row;
     ad.rows = a->rows;
@@ -345,7 +372,9 @@ int ftx_accept(ftx_ctx* ctx, const ftx_accept_args* a) {
     ad.part = nullptr;
     ad.out = (int32_t*)(ws + off_out);
     ad.margin = (float*)(d_small + 8);
+    tk = tr_begin(ctx);
     FTX_HIP(ctx, launch_accept(st, ad));
+    tr_end(ctx, tk, TK_ACCEPT, (double)V * 4);
     FTX_HIP(ctx, hipMemcpyAsync(h_out, ad.out, (size_t)(M + 2) * 4, hipMemcpyDeviceToHost, st));
     FTX_HIP(ctx, hipMemcpyAsync(pin, d_small, 16, hipMemcpyDeviceToHost, st));
     FTX_HIP(ctx, hipStreamSynchronize(st));

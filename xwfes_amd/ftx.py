@@ -65,6 +65,11 @@ class AcceptArgs(C.Structure):
                 ("n_acc", _i32p), ("bonus", _i32p), ("margin", _fp)]
 
 
+class TraceEntry(C.Structure):
+    _fields_ = [("name", C.c_char * 24), ("launches", C.c_int64), ("ms", C.c_double),
+                ("bytes", C.c_double)]
+
+
 def header_functions(path=HEADER):
     """Names of the functions include/ftx.h declares."""
     import re
@@ -107,6 +112,8 @@ def load(path=LIB_PATH):
         "ftx_verify_step": (C.c_int, [_vp, _vp, _vp, C.POINTER(VerifyArgs)]),
         "ftx_accept": (C.c_int, [_vp, C.POINTER(AcceptArgs)]),
         "ftx_fill_normal": (C.c_int, [_vp, _vp, C.c_int, _i64, C.c_uint64, C.c_float]),
+        "ftx_trace": (C.c_int, [_vp, C.c_int]),
+        "ftx_trace_read": (C.c_int, [_vp, C.POINTER(TraceEntry), C.c_int, C.POINTER(C.c_int)]),
     }
     for name, (res, args) in sig.items():
         f = getattr(L, name)
@@ -201,6 +208,17 @@ class Context:
 
     def sync(self):
         self.check(self.lib.ftx_sync(self.h))
+
+    def trace(self, enable):
+        self.check(self.lib.ftx_trace(self.h, int(enable)))
+
+    def trace_read(self):
+        """{kernel class: dict(launches, ms, bytes)} since trace(True)."""
+        buf = (TraceEntry * 32)()
+        n = C.c_int(0)
+        self.check(self.lib.ftx_trace_read(self.h, buf, 32, C.byref(n)))
+        return {buf[i].name.decode(): dict(launches=buf[i].launches, ms=buf[i].ms,
+                                           bytes=buf[i].bytes) for i in range(n.value)}
 
     def copy(self, dst, src, nbytes):
         self.check(self.lib.ftx_stage(self.h, dst, src, nbytes))
