@@ -130,7 +130,7 @@ def main():
     model = ctx.model(cfg, tensors, max_tokens=M)
     kv = model.kv(ctx_len + M + 8)
     kp, vp, _ = kv.pointers()
-    n_kv = cfg["n_layer"] * kv.cap * cfg["n_head_kv"] * cfg["head_dim"]
+    n_kv = cfg["n_layer"] * kv.cap_alloc * cfg["n_head_kv"] * cfg["head_dim"]
     ctx.fill_normal(kp, n_kv, seed=4, std=1.0, dtype=ftx.F16)
     ctx.fill_normal(vp, n_kv, seed=5, std=1.0, dtype=ftx.F16)
     logits = ctx.buffer(M * V * 4)

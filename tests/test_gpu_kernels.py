@@ -106,6 +106,41 @@ def test_matmul_vs_oracle(gctx, orc, dtype, M):
     assert rel_err_rows(got, want) < TOL
 
 
+@pytest.mark.parametrize("M", [1, 2, 5, 8])
+@pytest.mark.parametrize("N", [96, 1000, 4128])
+def test_matmul_mfma_q4k_vs_oracle(gctx, orc, M, N):
+    """K = 4096 Q4_K takes the int8-MFMA row-dot path (split sums over the
+    contraction for small N, ragged last tile for N = 96)."""
+    rng = np.random.default_rng(M * 1000 + N)
+    K = 4096
+    raw = rand_weight(orc, rng, N, K, P.Q4_K)
+    t = gctx.upload(raw, P.Q4_K, (K, N))
+    x = rng.standard_normal((M, K)).astype(np.float32)
+    x[-1, :7] *= 40.0   # outliers in the first 256-element block of the last row
+    got = gctx.matmul(x, t)
+    t.free()
+    want = orc.matmul(x, raw, P.Q4_K, N)
+    assert rel_err_rows(got[:-1], want[:-1]) < TOL if M > 1 else True
+    # the activation limbs are relative to each block's maximum: a block with
+    # 40x outliers carries its other values 40x more coarsely
+    assert rel_err_rows(got[-1:], want[-1:]) < 3 * TOL
+
+
+def test_matmul_mfma_zero_row(gctx, orc):
+    """An all-zero activation row gives zeros (row scale 0)."""
+    rng = np.random.default_rng(3)
+    K, N = 4096, 64
+    raw = rand_weight(orc, rng, N, K, P.Q4_K)
+    t = gctx.upload(raw, P.Q4_K, (K, N))
+    x = rng.standard_normal((3, K)).astype(np.float32)
+    x[1] = 0.0
+    got = gctx.matmul(x, t)
+    t.free()
+    assert np.all(got[1] == 0.0)
+    want = orc.matmul(x, raw, P.Q4_K, N)
+    assert rel_err_rows(got[[0, 2]], want[[0, 2]]) < TOL
+
+
 def test_matmul_rows_are_independent(gctx, orc):
     """An M-row product equals M single-row products (the reference's M-sum
     behaviour, src/cpu_backend.cpp:98-101, is not reproduced)."""

@@ -125,6 +125,27 @@ def test_verify_tree_equals_paths_on_gpu(gctx, orc):
     free_all(tensors)
 
 
+HD128 = P.model_cfg(1, 1024, 8, 2, 128, 1024, 1000, rope_theta=500000.0)
+HD128_DT = dict(tok_embd=P.Q8_0, output=P.Q8_0, q=P.Q8_0, k=P.Q8_0, v=P.Q8_0, o=P.Q8_0,
+                gate=P.Q8_0, up=P.Q8_0, down=P.Q8_0)
+
+
+@pytest.mark.parametrize("npast,parents", [
+    (1000, None),                                   # chain over 16 context chunks
+    (77, [-1, -1, 0, 0, 1, 1, 2, 3, 3, 4, 7, 7]),   # tree, context not chunk aligned
+    (0, [-1, 0, 0, 1, 1, 2]),                        # tree with no context at all
+    (64, [-1] * 9),                                  # 9 siblings: 36 query rows, 2 tiles
+])
+def test_verify_mfma_attention(gctx, orc, npast, parents):
+    """head_dim 128 / fp16 KV takes the chunked MFMA attention; the chain and
+    tree masks, chunk boundaries and query tiles agree with the oracle."""
+    model = P.make_model(orc, HD128, HD128_DT, seed=11)
+    M = 8 if parents is None else len(parents)
+    toks = list(np.random.default_rng(npast).integers(0, 1000, M))
+    got, want, _, _ = run_both(gctx, orc, model, toks, npast, npast + M + 5, parents=parents)
+    assert rel_err_rows(got, want) < LOGIT_TOL
+
+
 CFG1 = P.model_cfg(2, 512, 8, 8, 64, 1408, 32000, rope_theta=10000.0)
 CFG1_DT = dict(tok_embd=P.F32, output=P.Q4_0, q=P.Q4_0, k=P.Q4_0, v=P.Q4_0, o=P.Q4_0,
                gate=P.Q4_0, up=P.Q4_0, down=P.Q4_0)

@@ -297,10 +297,20 @@ int ftx_matmul(ftx_ctx* ctx, const float* x, int64_t M, int64_t K, const ftx_ten
     if (M == 0) return FTX_OK;
     Staged s{};
     float* extra;
-    int rc = stage_xy(ctx, x, (size_t)(M * K), y, (size_t)(M * N), false, 0, s, &extra);
+    const bool mv = mv_supported(W->dtype, K, M);
+    const size_t xqf = (xq_bytes(K) + 255) / 4;
+    const size_t mvf = mv ? xqf + mv_part_floats(N, K, ctx->cu_count) : 0;
+    int rc = stage_xy(ctx, x, (size_t)(M * K), y, (size_t)(M * N), false, mvf, s, &extra);
     if (rc) return rc;
     GemvSeg seg{W->data, W->dtype, W->row_bytes, N, s.y, N};
-    FTX_HIP(ctx, launch_gemv(ctx->stream, &seg, 1, s.x, K, K, M, EPI_STORE));
+    if (mv) {
+        int8_t* xq = (int8_t*)extra;
+        FTX_HIP(ctx, launch_xq_prep(ctx->stream, s.x, K, nullptr, 0.f, K, M, xq));
+        FTX_HIP(ctx, launch_mv(ctx->stream, &seg, 1, xq, K, M, EPI_STORE, extra + xqf,
+                               ctx->cu_count));
+    } else {
+        FTX_HIP(ctx, launch_gemv(ctx->stream, &seg, 1, s.x, K, K, M, EPI_STORE));
+    }
     if (s.y_host)
         FTX_HIP(ctx, hipMemcpyAsync(y, s.y, (size_t)(M * N) * sizeof(float),
                                     hipMemcpyDeviceToHost, ctx->stream));

@@ -25,6 +25,7 @@ enum TraceKind {
     TK_HEAD,
     TK_ROW_STATS,
     TK_ACCEPT,
+    TK_XQ_PREP,
     TK_COUNT
 };
 
@@ -120,6 +121,17 @@ hipError_t launch_down(hipStream_t st, const uint8_t* W, int dt, int64_t row_byt
                        int64_t n_in, int64_t N, const float* h, int64_t ldh, int64_t M,
                        float* y, int64_t ldy, float* part);
 
+// int8-MFMA GEMV (k_mfma.hip): activation operand prep + row-dot product
+size_t xq_bytes(int64_t K);
+hipError_t launch_xq_prep(hipStream_t st, const float* x, int64_t ldx, const float* normw,
+                          float eps, int64_t K, int64_t M, int8_t* xq);
+bool mv_supported(int dt, int64_t K, int64_t M);
+// split-sum scratch a launch_mv over `rows` total rows needs
+size_t mv_part_floats(int64_t rows, int64_t K, int cu_count);
+enum { EPI_SWIGLU = 2 };
+hipError_t launch_mv(hipStream_t st, const GemvSeg* segs, int nseg, const int8_t* xq, int64_t K,
+                     int64_t M, int epi, float* part, int cu_count);
+
 // quantise rows (synthetic model builder)
 hipError_t launch_quantize(hipStream_t st, const float* src, int dt, int64_t ncols,
                            int64_t nrows, int64_t row_bytes, uint8_t* dst);
@@ -132,6 +144,15 @@ hipError_t launch_embed(hipStream_t st, const uint8_t* E, int dt, int64_t row_by
                         int64_t d, const int32_t* toks, int64_t M, float* x);
 hipError_t launch_rmsnorm(hipStream_t st, const float* x, const float* w, int64_t d,
                           int64_t M, float eps, float* out);
+// KV cache layout per layer: K [cap][n_kv*hd] (the reference's
+// [pos][n_kv*hd], include/ft/kv_cache.h:10-47); V transposed as
+// [n_kv][hd][cap] so attention reads P.V operands contiguously.  `cap` here
+// is the allocated slot count, a multiple of 64.
+__host__ __device__ inline int64_t v_index(int64_t slot, int64_t kvh, int64_t dim, int64_t hd,
+                                           int64_t cap) {
+    return (kvh * hd + dim) * cap + slot;
+}
+
 struct RopeArgs {
     float* qkv;        // [M][ldq]: q at 0, k at qdim, v at qdim + kdim
     int64_t ldq;
@@ -141,15 +162,16 @@ struct RopeArgs {
     double theta;
     int neox;
     void* kc;          // layer base of K cache [cap][kdim]
-    void* vc;
+    void* vc;          // layer base of V cache [n_kv][hd][cap]
     int kv_f16;
+    int64_t cap;
 };
 hipError_t launch_rope_kv(hipStream_t st, const RopeArgs& a, int64_t M);
 struct AttnArgs {
     const float* qkv;   // q rows, ldq stride
     int64_t ldq;
     const void* kc;     // layer base [cap][kdim]
-    const void* vc;
+    const void* vc;     // layer base [n_kv][hd][cap]
     int kv_f16;
     const int64_t* npast;      // device scalar
     const uint32_t* anc;       // [M][anc_words] ancestor bitmask (self included)
@@ -157,8 +179,30 @@ struct AttnArgs {
     int64_t n_head, n_kv, hd;
     int64_t max_ctx;           // upper bound of npast + M for LDS sizing
     float* out;                // [M][n_head*hd]
+    int64_t cap;
 };
 hipError_t launch_attention(hipStream_t st, const AttnArgs& a, int64_t M);
+
+// MFMA attention (k_attn.hip): fp16 KV, hd 64 or 128
+struct AttnMArgs {
+    const float* qkv;
+    int64_t ldq;
+    const _Float16* kc;  // layer base [cap][kdim]
+    const _Float16* vt;  // layer base [n_kv][hd][cap]
+    int64_t cap;         // allocated slots, multiple of 64
+    const int64_t* npast;
+    const uint32_t* anc;
+    int anc_words;
+    int M, n_head, n_kv, hd;
+    float* out;          // [M][n_head*hd]
+    float *pmax, *psum, *pout;  // chunk partials
+};
+bool attn_mfma_supported(int64_t hd, int kv_f16, int64_t M, int64_t n_head, int64_t n_kv);
+size_t attn_part_floats(int64_t M, int64_t n_head, int64_t hd, int64_t cap_alloc);
+hipError_t launch_attn_mfma(hipStream_t st, AttnMArgs a, float* part);
+// canonical [slot][kdim] <-> device V layout (per layer, all slots)
+hipError_t launch_v_layout(hipStream_t st, const void* src, void* dst, int64_t n_layer,
+                           int64_t cap, int64_t n_kv, int64_t hd, int elem_bytes, int to_device);
 
 // acceptance
 struct RowStats {

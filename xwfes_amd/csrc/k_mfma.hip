@@ -1,0 +1,345 @@
+// k_mfma.hip -- int8-MFMA quantised GEMV for small M (M <= 8), row-dot form
+// (y = x W^T with the quantisation blocks along the contraction), the
+// layout of every verify-step projection except ffn_down.
+//
+// Math.  Activations are split per row m and 256-element block into two
+// int8 limbs with a block scale s = max|x_block| / 127:  x ~= s*(a + b/256),
+// |a|,|b| <= 127, so x is carried to ~1/65000 of its block maximum.  Weights
+// enter the MFMA as their raw quantised integers, so every MFMA product and
+// sum is exact integer arithmetic; the block scales are applied on the MFMA
+// outputs:
+//   Q4_K  w = d*sc_j*q - dmin*m_j  (q in 0..15, sub-block j of 32)
+//     y = sum_sb s_sb * [ d * sum_j sc_j * (A_j . q_j) - dmin * sum_j m_j * X_j ]
+//   where X_j is the sum of the activation limb over sub-block j, formed by
+//   a second MFMA whose B operand is the eight m_j of the super-block.
+// Shapes.  v_mfma_i32_32x32x32_i8: A rows 0..7 = limb a of m = 0..7, rows
+// 8..15 = limb b, rows 16..31 zero; B columns = 32 weight rows; K = 32 = one
+// Q4_K sub-block.  Lane l holds A[l%32][16*(l/32) + s], B[16*(l/32) + s][l%32]
+// and C[8*(r/4) + 4*(l/32) + r%4][l%32] (checked on gfx950).
+#include "ftx_internal.h"
+#include "quant_dev.h"
+
+namespace {
+
+typedef int v4i __attribute__((ext_vector_type(4)));
+typedef int v16i __attribute__((ext_vector_type(16)));
+
+__device__ __forceinline__ v4i ld16g(const void* p) { return *(const v4i*)p; }
+
+// ---------------------------------------------------------------- prep
+// One block per activation row m < 8 (rows m >= M are written as zeros).
+// Optional RMSNorm (src/engine.cpp:23-41) fused in front.
+__global__ void __launch_bounds__(256) k_xq_prep(const float* __restrict__ x, int64_t ldx,
+                                                 const float* __restrict__ normw, float eps,
+                                                 int64_t K, int M, int8_t* __restrict__ frag,
+                                                 int8_t* __restrict__ xs32,
+                                                 int8_t* __restrict__ xs16,
+                                                 float* __restrict__ scale) {
+#pragma clang fp contract(off)
+    extern __shared__ float xr[];  // K floats
+    __shared__ float red[256];
+    const int m = blockIdx.x, tid = threadIdx.x;
+    const bool live = m < M;
+    float ss = 0.f, mx = 0.f;
+    if (live) {
+        const float* row = x + (int64_t)m * ldx;
+        for (int64_t k = tid; k < K; k += 256) {
+            const float v = row[k];
+            xr[k] = v;
+            ss += v * v;
+        }
+    }
+    if (normw && live) {
+        red[tid] = ss;
+        __syncthreads();
+        for (int o = 128; o > 0; o >>= 1) {
+            if (tid < o) red[tid] += red[tid + o];
+            __syncthreads();
+        }
+        const float inv = 1.f / sqrtf(red[0] / (float)K + eps);
+        __syncthreads();
+        for (int64_t k = tid; k < K; k += 256) xr[k] = xr[k] * inv * normw[k];
+    }
+    __syncthreads();
+    const int64_t ngroups = K / 16;
+    // 256 | ngroups: the 16 groups of a super-block are 16 adjacent lanes
+    for (int64_t G = tid; G < ngroups; G += 256) {
+        mx = 0.f;
+        if (live)
+#pragma unroll
+            for (int t = 0; t < 16; ++t) mx = fmaxf(mx, fabsf(xr[G * 16 + t]));
+#pragma unroll
+        for (int o = 1; o < 16; o <<= 1) mx = fmaxf(mx, __shfl_xor(mx, o, 64));
+        const float q = mx > 0.f ? 127.f / mx : 0.f;
+        if ((G & 15) == 0) scale[(G >> 4) * 8 + m] = mx > 0.f ? mx / 127.f : 0.f;
+        int sa = 0, sb = 0;
+        uint32_t pa[4] = {0, 0, 0, 0}, pb[4] = {0, 0, 0, 0};
+        if (live && mx > 0.f) {
+#pragma unroll
+            for (int t = 0; t < 16; ++t) {
+                const float v = xr[G * 16 + t] * q;
+                const float a = rintf(v);
+                float bf = rintf((v - a) * 256.f);
+                bf = fminf(fmaxf(bf, -127.f), 127.f);
+                const int ai = (int)a, bi = (int)bf;
+                sa += ai;
+                sb += bi;
+                pa[t >> 2] |= (uint32_t)(ai & 0xFF) << (8 * (t & 3));
+                pb[t >> 2] |= (uint32_t)(bi & 0xFF) << (8 * (t & 3));
+            }
+        }
+        const int64_t kb = G >> 1, g = G & 1;  // 32-element block, half
+        v4i va = {(int)pa[0], (int)pa[1], (int)pa[2], (int)pa[3]};
+        v4i vb = {(int)pb[0], (int)pb[1], (int)pb[2], (int)pb[3]};
+        *(v4i*)(frag + ((kb * 2 + g) * 16 + m) * 16) = va;
+        *(v4i*)(frag + ((kb * 2 + g) * 16 + 8 + m) * 16) = vb;
+        // 16-element sums split into 6-bit lo / signed hi
+        const int64_t sbk = G >> 4, s16 = G & 15;
+        xs16[(sbk * 32 + m) * 16 + s16] = (int8_t)(sa & 63);
+        xs16[(sbk * 32 + 16 + m) * 16 + s16] = (int8_t)(sa >> 6);
+        xs16[(sbk * 32 + 8 + m) * 16 + s16] = (int8_t)(sb & 63);
+        xs16[(sbk * 32 + 24 + m) * 16 + s16] = (int8_t)(sb >> 6);
+        // 32-element sums from the partner group
+        const int sa2 = sa + __shfl_xor(sa, 1, 64), sb2 = sb + __shfl_xor(sb, 1, 64);
+        if (!(G & 1)) {
+            const int64_t j = (G >> 1) & 7;
+            xs32[(sbk * 32 + m) * 8 + j] = (int8_t)(sa2 & 63);
+            xs32[(sbk * 32 + 16 + m) * 8 + j] = (int8_t)(sa2 >> 6);
+            xs32[(sbk * 32 + 8 + m) * 8 + j] = (int8_t)(sb2 & 63);
+            xs32[(sbk * 32 + 24 + m) * 8 + j] = (int8_t)(sb2 >> 6);
+        }
+    }
+}
+
+// ---------------------------------------------------------------- Q4_K
+
+struct MvSeg {
+    const uint8_t* W;
+    int64_t row_bytes;
+    int64_t N;
+    int64_t tile0;  // first global tile of the segment
+    int64_t row0;   // first global row of the segment
+};
+
+struct MvArgs {
+    MvSeg seg[3];
+    int nseg;
+    int64_t tiles;
+    int64_t rows;       // global rows (sum of N)
+    int sb_per_split;
+    const int8_t* frag;
+    const int8_t* xs32;
+    const float* scale;
+    float* part;        // [S][8][rows]
+};
+
+__global__ void __launch_bounds__(256) k_mv_q4k(MvArgs a) {
+    const int lane = threadIdx.x & 63;
+    const int64_t T = (int64_t)blockIdx.x * 4 + (threadIdx.x >> 6);
+    if (T >= a.tiles) return;
+    int si = 0;
+    while (si + 1 < a.nseg && T >= a.seg[si + 1].tile0) ++si;
+    const MvSeg sg = a.seg[si];
+    const int col = lane & 31, g = lane >> 5;
+    const int64_t n_raw = (T - sg.tile0) * 32 + col;
+    const int64_t n = n_raw < sg.N ? n_raw : sg.N - 1;
+    const uint8_t* wrow = sg.W + n * sg.row_bytes;
+    const int sp = blockIdx.y;
+    const int sb0 = sp * a.sb_per_split, sb1 = sb0 + a.sb_per_split;
+    const bool arow = col < 16;
+    float acc[8];
+#pragma unroll
+    for (int r = 0; r < 8; ++r) acc[r] = 0.f;
+    const v4i zero4 = {0, 0, 0, 0};
+    const v16i zero16 = {};
+    for (int sb = sb0; sb < sb1; ++sb) {
+        const uint8_t* blk = wrow + (int64_t)sb * 144;
+        const v4i hdr = ld16g(blk);
+        v4i qs[4];
+#pragma unroll
+        for (int gg = 0; gg < 4; ++gg) qs[gg] = ld16g(blk + 16 + 32 * gg + 16 * g);
+        v4i af[8];
+#pragma unroll
+        for (int j = 0; j < 8; ++j)
+            af[j] = arow ? ld16g(a.frag + ((((int64_t)sb * 8 + j) * 2 + g) * 16 + col) * 16)
+                         : zero4;
+        v4i ax = zero4;
+        if (g == 0) {
+            const int2 t = *(const int2*)(a.xs32 + ((int64_t)sb * 32 + col) * 8);
+            ax.x = t.x;
+            ax.y = t.y;
+        }
+        const uint32_t S0 = (uint32_t)hdr.y, S1 = (uint32_t)hdr.z, S2 = (uint32_t)hdr.w;
+        const uint32_t sc_lo = S0 & 0x3F3F3F3Fu;
+        const uint32_t mn_lo = S1 & 0x3F3F3F3Fu;
+        const uint32_t sc_hi = (S2 & 0x0F0F0F0Fu) | ((S0 >> 2) & 0x30303030u);
+        const uint32_t mn_hi = ((S2 >> 4) & 0x0F0F0F0Fu) | ((S1 >> 2) & 0x30303030u);
+        int ai[8];
+#pragma unroll
+        for (int r = 0; r < 8; ++r) ai[r] = 0;
+#pragma unroll
+        for (int j = 0; j < 8; ++j) {
+            const v4i w = qs[j >> 1];
+            v4i b;
+            if (j & 1) {
+                b.x = (int)(((uint32_t)w.x >> 4) & 0x0F0F0F0Fu);
+                b.y = (int)(((uint32_t)w.y >> 4) & 0x0F0F0F0Fu);
+                b.z = (int)(((uint32_t)w.z >> 4) & 0x0F0F0F0Fu);
+                b.w = (int)(((uint32_t)w.w >> 4) & 0x0F0F0F0Fu);
+            } else {
+                b.x = (int)((uint32_t)w.x & 0x0F0F0F0Fu);
+                b.y = (int)((uint32_t)w.y & 0x0F0F0F0Fu);
+                b.z = (int)((uint32_t)w.z & 0x0F0F0F0Fu);
+                b.w = (int)((uint32_t)w.w & 0x0F0F0F0Fu);
+            }
+            const v16i c = __builtin_amdgcn_mfma_i32_32x32x32_i8(af[j], b, zero16, 0, 0, 0);
+            const int sc = (int)(((j < 4 ? sc_lo : sc_hi) >> (8 * (j & 3))) & 0xFF);
+#pragma unroll
+            for (int r = 0; r < 8; ++r) ai[r] += sc * c[r];
+        }
+        v4i bm = zero4;
+        if (g == 0) {
+            bm.x = (int)mn_lo;
+            bm.y = (int)mn_hi;
+        }
+        const v16i dm = __builtin_amdgcn_mfma_i32_32x32x32_i8(ax, bm, zero16, 0, 0, 0);
+        const float d = h2f((uint16_t)((uint32_t)hdr.x & 0xFFFF));
+        const float dmin = h2f((uint16_t)((uint32_t)hdr.x >> 16));
+        // activation scales of this super-block for m = 4g .. 4g+3
+        const float4 s4 = *(const float4*)(a.scale + (int64_t)sb * 8 + 4 * g);
+        const float sm[4] = {s4.x, s4.y, s4.z, s4.w};
+#pragma unroll
+        for (int r = 0; r < 8; ++r) {
+            const int mins = dm[r] + 64 * dm[r + 8];
+            acc[r] += sm[r & 3] * (d * (float)ai[r] - dmin * (float)mins);
+        }
+    }
+    // rows 4g+r (limb a, r < 4) and 8+4g+r (limb b) of activation m = 4g + r
+    float* out = a.part + (int64_t)sp * 8 * a.rows + sg.row0;
+    if (n_raw < sg.N) {
+#pragma unroll
+        for (int r = 0; r < 4; ++r) {
+            const int m = 4 * g + r;
+            out[(int64_t)m * a.rows + n_raw] = acc[r] + acc[r + 4] * (1.f / 256.f);
+        }
+    }
+}
+
+// Sum the S split partials in order and apply the epilogue.
+struct RedSeg {
+    float* y;
+    int64_t ldy;
+    int64_t row0, N;
+};
+struct RedArgs {
+    const float* part;
+    int S;
+    int64_t rows;
+    int M;
+    int epi;  // EPI_STORE, EPI_ACCUM, or 2 = SwiGLU (seg 0 gate, seg 1 up -> seg 0 y)
+    RedSeg seg[3];
+    int nseg;
+};
+
+__global__ void __launch_bounds__(256) k_mv_reduce(RedArgs a) {
+    const int64_t t = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
+    const int m = blockIdx.y;
+    if (m >= a.M) return;
+    if (a.epi == 2) {
+        const int64_t N = a.seg[0].N;
+        if (t >= N) return;
+        float g = 0.f, u = 0.f;
+        for (int s = 0; s < a.S; ++s) {
+            const float* p = a.part + ((int64_t)s * 8 + m) * a.rows;
+            g += p[a.seg[0].row0 + t];
+            u += p[a.seg[1].row0 + t];
+        }
+        // src/engine.cpp:271-273: g / (1 + exp(-g)) * u
+        a.seg[0].y[(int64_t)m * a.seg[0].ldy + t] = g / (1.f + expf(-g)) * u;
+        return;
+    }
+    if (t >= a.rows) return;
+    int si = 0;
+    while (si + 1 < a.nseg && t >= a.seg[si + 1].row0) ++si;
+    float v = 0.f;
+    for (int s = 0; s < a.S; ++s) v += a.part[((int64_t)s * 8 + m) * a.rows + t];
+    float* yp = a.seg[si].y + (int64_t)m * a.seg[si].ldy + (t - a.seg[si].row0);
+    *yp = a.epi == EPI_ACCUM ? *yp + v : v;
+}
+
+}  // namespace
+
+// fragments K*16 | xs32 K | xs16 2K | scales (K/256)*8 floats
+size_t xq_bytes(int64_t K) { return (size_t)(K * 16 + K + K * 2 + K / 8 + 64); }
+
+hipError_t launch_xq_prep(hipStream_t st, const float* x, int64_t ldx, const float* normw,
+                          float eps, int64_t K, int64_t M, int8_t* xq) {
+    if (K % 4096 || K > 16384) return hipErrorInvalidValue;
+    int8_t* frag = xq;
+    int8_t* xs32 = xq + K * 16;
+    int8_t* xs16 = xs32 + K;
+    float* scale = (float*)(xs16 + K * 2);
+    const size_t lds = (size_t)K * sizeof(float);
+    hipLaunchKernelGGL(k_xq_prep, dim3(8), dim3(256), lds, st, x, ldx, normw, eps, K, (int)M, frag,
+                       xs32, xs16, scale);
+    return hipGetLastError();
+}
+
+bool mv_supported(int dt, int64_t K, int64_t M) {
+    return dt == FTX_Q4_K && M >= 1 && M <= 8 && K % 4096 == 0 && K <= 16384;
+}
+
+// contraction splits: double until ~8 waves per CU or one super-block each
+static int mv_splits(int64_t tiles, int nsb, int cu_count) {
+    int S = 1;
+    const int64_t want = (int64_t)(cu_count > 0 ? cu_count : 256) * 8;
+    while (S < nsb && tiles * S < want && nsb % (S * 2) == 0) S *= 2;
+    return S;
+}
+
+size_t mv_part_floats(int64_t rows, int64_t K, int cu_count) {
+    const int64_t tiles = (rows + 31) / 32;
+    return (size_t)mv_splits(tiles, (int)(K / 256), cu_count) * 8 * (size_t)rows;
+}
+
+// segs: up to 3 same-K Q4_K weight segments; epi as in RedArgs
+hipError_t launch_mv(hipStream_t st, const GemvSeg* segs, int nseg, const int8_t* xq, int64_t K,
+                     int64_t M, int epi, float* part, int cu_count) {
+    MvArgs a{};
+    a.nseg = nseg;
+    int64_t tiles = 0, rows = 0;
+    for (int i = 0; i < nseg; ++i) {
+        a.seg[i].W = segs[i].W;
+        a.seg[i].row_bytes = segs[i].row_bytes;
+        a.seg[i].N = segs[i].N;
+        a.seg[i].tile0 = tiles;
+        a.seg[i].row0 = rows;
+        tiles += (segs[i].N + 31) / 32;
+        rows += segs[i].N;
+    }
+    a.tiles = tiles;
+    a.rows = rows;
+    const int nsb = (int)(K / 256);
+    const int S = mv_splits(tiles, nsb, cu_count);
+    a.sb_per_split = nsb / S;
+    a.frag = xq;
+    a.xs32 = xq + K * 16;
+    a.scale = (const float*)(xq + K * 16 + K + K * 2);
+    a.part = part;
+    hipLaunchKernelGGL(k_mv_q4k, dim3((unsigned)((tiles + 3) / 4), (unsigned)S), dim3(256), 0, st,
+                       a);
+    hipError_t e = hipGetLastError();
+    if (e != hipSuccess) return e;
+    RedArgs r{};
+    r.part = part;
+    r.S = S;
+    r.rows = rows;
+    r.M = (int)M;
+    r.epi = epi;
+    r.nseg = nseg;
+    for (int i = 0; i < nseg; ++i) r.seg[i] = RedSeg{segs[i].y, segs[i].ldy, a.seg[i].row0, segs[i].N};
+    const int64_t span = epi == 2 ? segs[0].N : rows;
+    hipLaunchKernelGGL(k_mv_reduce, dim3((unsigned)((span + 255) / 256), (unsigned)M), dim3(256), 0,
+                       st, r);
+    return hipGetLastError();
+}

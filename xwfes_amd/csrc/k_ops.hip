@@ -94,14 +94,43 @@ __global__ void k_rope_kv(RopeArgs a) {
     const float* vr = row + qdim + kdim + kh * a.hd;
     for (int64_t t = threadIdx.x; t < a.hd; t += blockDim.x) {
         const int64_t idx = slot * kdim + kh * a.hd + t;
+        const int64_t vidx = v_index(slot, kh, t, a.hd, a.cap);
         if (a.kv_f16) {
             ((_Float16*)a.kc)[idx] = (_Float16)kr[t];
-            ((_Float16*)a.vc)[idx] = (_Float16)vr[t];
+            ((_Float16*)a.vc)[vidx] = (_Float16)vr[t];
         } else {
             ((float*)a.kc)[idx] = kr[t];
-            ((float*)a.vc)[idx] = vr[t];
+            ((float*)a.vc)[vidx] = vr[t];
         }
     }
+}
+
+// V between the canonical per-layer [slot][n_kv*hd] layout and the device
+// [n_kv][hd][slot] layout; one thread per element.
+__global__ void __launch_bounds__(256) k_v_layout(const uint8_t* __restrict__ src,
+                                                  uint8_t* __restrict__ dst, int64_t cap,
+                                                  int64_t n_kv, int64_t hd, int eb,
+                                                  int to_device, int64_t total) {
+    const int64_t t = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
+    if (t >= total) return;
+    const int64_t per = cap * n_kv * hd;
+    const int64_t l = t / per, r = t % per;
+    const int64_t slot = r / (n_kv * hd), c = r % (n_kv * hd);
+    const int64_t canon = l * per + r;
+    const int64_t dev = l * per + v_index(slot, c / hd, c % hd, hd, cap);
+    const int64_t s = to_device ? canon : dev, d = to_device ? dev : canon;
+    if (eb == 2) ((uint16_t*)dst)[d] = ((const uint16_t*)src)[s];
+    else ((uint32_t*)dst)[d] = ((const uint32_t*)src)[s];
+}
+
+hipError_t launch_v_layout(hipStream_t st, const void* src, void* dst, int64_t n_layer,
+                           int64_t cap, int64_t n_kv, int64_t hd, int elem_bytes, int to_device) {
+    const int64_t total = n_layer * cap * n_kv * hd;
+    if (total == 0) return hipSuccess;
+    hipLaunchKernelGGL(k_v_layout, dim3((unsigned)((total + 255) / 256)), dim3(256), 0, st,
+                       (const uint8_t*)src, (uint8_t*)dst, cap, n_kv, hd, elem_bytes, to_device,
+                       total);
+    return hipGetLastError();
 }
 
 hipError_t launch_rope_kv(hipStream_t st, const RopeArgs& a, int64_t M) {
@@ -192,7 +221,7 @@ __global__ void __launch_bounds__(256) k_attention(AttnArgs a) {
             const float w = sc[s] * inv;
             if (w == 0.f) continue;
             const int64_t slot = s < npast ? s : npast + tslot[s - npast];
-            acc += w * kv_load(a.vc, a.kv_f16, slot * kdim + koff + dim);
+            acc += w * kv_load(a.vc, a.kv_f16, v_index(slot, kvh, dim, hd, a.cap));
         }
     }
     __syncthreads();
@@ -206,7 +235,7 @@ __global__ void __launch_bounds__(256) k_attention(AttnArgs a) {
             const float w = sc[s] * inv;
             if (w == 0.f) continue;
             const int64_t slot = s < npast ? s : npast + tslot[s - npast];
-            o += w * kv_load(a.vc, a.kv_f16, slot * kdim + koff + t);
+            o += w * kv_load(a.vc, a.kv_f16, v_index(slot, kvh, t, hd, a.cap));
         }
         a.out[m * a.n_head * hd + h * hd + t] = o;
     }

@@ -6,7 +6,7 @@
 
 static const char* kTraceNames[TK_COUNT] = {
     "embed", "rmsnorm", "gemv_qkv", "rope_kv", "attention", "gemv_o",
-    "gemv_swiglu", "down", "head", "row_stats", "accept"};
+    "gemv_swiglu", "down", "head", "row_stats", "accept", "xq_prep"};
 
 static void resolve(ftx_ctx* ctx) {
     if (ctx->pending.empty()) {

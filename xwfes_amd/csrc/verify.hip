@@ -22,21 +22,33 @@ struct ftx_model {
     int32_t* depth = nullptr;
     uint32_t* anc = nullptr;
     int64_t* npast = nullptr;
+    // int8-MFMA GEMV operands: activation fragments and split sums
+    int8_t* xq = nullptr;
+    float* mvpart = nullptr;
 };
+
+// the MFMA row-dot path applies to every segment of a projection, or none
+static bool mv_all(const ftx_tensor* const* ts, int n, int64_t K, int64_t M) {
+    for (int i = 0; i < n; ++i)
+        if (!mv_supported(ts[i]->dtype, K, M)) return false;
+    return true;
+}
 
 struct ftx_kv {
     ftx_ctx* ctx = nullptr;
-    int64_t n_layer = 0, cap = 0, kdim = 0;
+    int64_t n_layer = 0, cap = 0, kdim = 0, n_kv = 0, hd = 0;
+    int64_t cap_alloc = 0;  // slots allocated per layer, a multiple of 64
     int kv_f16 = 1;
-    void* k = nullptr;
-    void* v = nullptr;
+    void* k = nullptr;      // [n_layer][cap_alloc][kdim]
+    void* v = nullptr;      // [n_layer][n_kv][hd][cap_alloc]
+    float* attn_part = nullptr;  // chunk partials of the MFMA attention
     int64_t npast = 0;
 };
 
 static void model_release(ftx_model* m) {
     if (!m) return;
-    void* bufs[] = {m->norms, m->x, m->xn, m->qkv, m->att, m->h, m->part,
-                    m->toks,  m->depth, m->anc, m->npast};
+    void* bufs[] = {m->norms, m->x,     m->xn,  m->qkv,   m->att, m->h,     m->part,
+                    m->toks,  m->depth, m->anc, m->npast, m->xq,  m->mvpart};
     for (void* b : bufs)
         if (b) (void)hipFree(b);
     delete m;
@@ -107,6 +119,13 @@ int ftx_model_create(ftx_ctx* ctx, const ftx_model_desc* d, ftx_model** out) {
               dalloc(&m->h, Mmax * d->n_ff) && dalloc(&m->part, m->part_floats) &&
               dalloc(&m->toks, Mmax) && dalloc(&m->depth, Mmax) && dalloc(&m->anc, Mmax * 8) &&
               dalloc(&m->npast, 1);
+    if (ok) {
+        const int64_t Kmax = std::max(D, qdim);
+        size_t pf = 0;
+        for (int64_t rows : {m->ldq, D, 2 * d->n_ff, d->vocab})
+            pf = std::max(pf, mv_part_floats(rows, Kmax, ctx->cu_count));
+        ok = dalloc(&m->xq, xq_bytes(Kmax)) && dalloc(&m->mvpart, pf);
+    }
     if (!ok) {
         model_release(m);
         return ftx_fail(ctx, FTX_E_NOMEM, "activation allocation failed");
@@ -150,15 +169,22 @@ int ftx_kv_create(ftx_ctx* ctx, const ftx_model* m, int64_t cap, int kv_dtype, f
     kv->ctx = ctx;
     kv->n_layer = m->d.n_layer;
     kv->cap = cap;
+    kv->cap_alloc = (cap + 63) / 64 * 64;
     kv->kdim = m->kdim;
+    kv->n_kv = m->d.n_head_kv;
+    kv->hd = m->d.head_dim;
     kv->kv_f16 = kv_dtype == FTX_KV_F16;
-    const size_t bytes = (size_t)(kv->n_layer * cap * kv->kdim) * (kv->kv_f16 ? 2 : 4);
-    if (hipMalloc(&kv->k, bytes) != hipSuccess || hipMalloc(&kv->v, bytes) != hipSuccess) {
+    const size_t bytes = (size_t)(kv->n_layer * kv->cap_alloc * kv->kdim) * (kv->kv_f16 ? 2 : 4);
+    const size_t pf = attn_part_floats(m->Mmax, m->d.n_head, m->d.head_dim, kv->cap_alloc);
+    if (hipMalloc(&kv->k, bytes) != hipSuccess || hipMalloc(&kv->v, bytes) != hipSuccess ||
+        hipMalloc((void**)&kv->attn_part, pf * sizeof(float)) != hipSuccess) {
         (void)hipGetLastError();
         if (kv->k) (void)hipFree(kv->k);
+        if (kv->v) (void)hipFree(kv->v);
         delete kv;
         return ftx_fail(ctx, FTX_E_NOMEM, "kv allocation failed");
     }
+    // finite contents everywhere: masked slots still meet the P.V product
     (void)hipMemset(kv->k, 0, bytes);
     (void)hipMemset(kv->v, 0, bytes);
     *out = kv;
@@ -170,8 +196,56 @@ int ftx_kv_free(ftx_kv* kv) {
     if (kv->ctx) (void)hipStreamSynchronize(kv->ctx->stream);
     if (kv->k) (void)hipFree(kv->k);
     if (kv->v) (void)hipFree(kv->v);
+    if (kv->attn_part) (void)hipFree(kv->attn_part);
     delete kv;
     return FTX_OK;
+}
+
+// host arrays in the canonical [n_layer][cap][n_kv*hd] layout
+static int kv_copy(ftx_kv* kv, void* kh, void* vh, bool to_device) {
+    ftx_ctx* ctx = kv->ctx;
+    const int eb = kv->kv_f16 ? 2 : 4;
+    const size_t row = (size_t)kv->kdim * eb;
+    const size_t canon = (size_t)(kv->n_layer * kv->cap) * row;
+    const size_t dev = (size_t)(kv->n_layer * kv->cap_alloc) * row;
+    void* tmp;
+    int rc = ftx_workspace(ctx, dev, &tmp);
+    if (rc) return rc;
+    hipStream_t st = ctx->stream;
+    const hipMemcpyKind kind = to_device ? hipMemcpyHostToDevice : hipMemcpyDeviceToHost;
+    // K: the same layout with cap_alloc rows per layer
+    if (to_device)
+        FTX_HIP(ctx, hipMemcpy2DAsync(kv->k, (size_t)kv->cap_alloc * row, kh, (size_t)kv->cap * row,
+                                      (size_t)kv->cap * row, (size_t)kv->n_layer, kind, st));
+    else
+        FTX_HIP(ctx, hipMemcpy2DAsync(kh, (size_t)kv->cap * row, kv->k, (size_t)kv->cap_alloc * row,
+                                      (size_t)kv->cap * row, (size_t)kv->n_layer, kind, st));
+    // V: canonical rows staged with cap_alloc rows per layer, then transposed
+    if (to_device) {
+        FTX_HIP(ctx, hipMemsetAsync(tmp, 0, dev, st));
+        FTX_HIP(ctx, hipMemcpy2DAsync(tmp, (size_t)kv->cap_alloc * row, vh, (size_t)kv->cap * row,
+                                      (size_t)kv->cap * row, (size_t)kv->n_layer, kind, st));
+        FTX_HIP(ctx, launch_v_layout(st, tmp, kv->v, kv->n_layer, kv->cap_alloc, kv->n_kv, kv->hd,
+                                     eb, 1));
+    } else {
+        FTX_HIP(ctx, launch_v_layout(st, kv->v, tmp, kv->n_layer, kv->cap_alloc, kv->n_kv, kv->hd,
+                                     eb, 0));
+        FTX_HIP(ctx, hipMemcpy2DAsync(vh, (size_t)kv->cap * row, tmp, (size_t)kv->cap_alloc * row,
+                                      (size_t)kv->cap * row, (size_t)kv->n_layer, kind, st));
+    }
+    FTX_HIP(ctx, hipStreamSynchronize(st));
+    (void)canon;
+    return FTX_OK;
+}
+
+int ftx_kv_write(ftx_kv* kv, const void* k, const void* v) {
+    if (!kv || !k || !v) return FTX_E_INVALID;
+    return kv_copy(kv, (void*)k, (void*)v, true);
+}
+
+int ftx_kv_read(ftx_kv* kv, void* k, void* v) {
+    if (!kv || !k || !v) return FTX_E_INVALID;
+    return kv_copy(kv, k, v, false);
 }
 
 int ftx_kv_pointers(ftx_kv* kv, void** k, void** v, int64_t* npast) {
@@ -246,52 +320,97 @@ int ftx_verify_step(ftx_ctx* ctx, ftx_model* m, ftx_kv* kv, const ftx_verify_arg
                         m->toks, M, m->x));
     const size_t kvel = kv->kv_f16 ? 2 : 4;
     const double norm_b = 2 * Md * D * f4 + D * f4;
+    // One projection: x (row stride ldx) [-> RMSNorm] -> weight segments.  The
+    // int8-MFMA path runs when every segment qualifies (the norm is fused
+    // into its activation prep); the generic kernels run otherwise.
+    auto project = [&](int kind, double bytes, const float* xin, int64_t ldx, const float* normw,
+                       const ftx_tensor* const* ts, GemvSeg* segs, int nseg, int64_t K,
+                       int epi) -> int {
+        if (mv_all(ts, nseg, K, M)) {
+            TRACED(TK_XQ_PREP, Md * K * f4 + 19.0 * K,
+                   launch_xq_prep(st, xin, ldx, normw, eps, K, M, m->xq));
+            TRACED(kind, bytes,
+                   launch_mv(st, segs, nseg, m->xq, K, M, epi, m->mvpart, ctx->cu_count));
+            return FTX_OK;
+        }
+        const float* src = xin;
+        int64_t lds = ldx;
+        if (normw) {
+            TRACED(TK_RMSNORM, norm_b, launch_rmsnorm(st, xin, normw, K, M, eps, m->xn));
+            src = m->xn;
+            lds = K;
+        }
+        if (epi == EPI_SWIGLU)
+            TRACED(kind, bytes,
+                   launch_gemv_swiglu(st, segs[0].W, segs[1].W, segs[0].dt, segs[0].row_bytes,
+                                      segs[0].N, src, lds, K, M, segs[0].y, segs[0].ldy));
+        else
+            TRACED(kind, bytes, launch_gemv(st, segs, nseg, src, lds, K, M, epi));
+        return FTX_OK;
+    };
+    auto seg = [](const ftx_tensor* t, float* y, int64_t ldy) {
+        return GemvSeg{t->data, t->dtype, t->row_bytes, t->nrows, y, ldy};
+    };
     for (int64_t l = 0; l < d.n_layer; ++l) {
         const ftx_tensor* const* T = m->layers.data() + l * FTX_LAYER_TENSORS;
-        TRACED(TK_RMSNORM, norm_b,
-               launch_rmsnorm(st, m->x, m->norms + (l * 2) * D, D, M, eps, m->xn));
-        GemvSeg qkv[3] = {
-            {T[FTX_T_Q]->data, T[FTX_T_Q]->dtype, T[FTX_T_Q]->row_bytes, m->qdim, m->qkv, m->ldq},
-            {T[FTX_T_K]->data, T[FTX_T_K]->dtype, T[FTX_T_K]->row_bytes, m->kdim, m->qkv + m->qdim,
-             m->ldq},
-            {T[FTX_T_V]->data, T[FTX_T_V]->dtype, T[FTX_T_V]->row_bytes, m->kdim,
-             m->qkv + m->qdim + m->kdim, m->ldq}};
-        TRACED(TK_GEMV_QKV,
-               wbytes(T[FTX_T_Q]) + wbytes(T[FTX_T_K]) + wbytes(T[FTX_T_V]) + Md * D * f4 +
-                   Md * m->ldq * f4,
-               launch_gemv(st, qkv, 3, m->xn, D, D, M, EPI_STORE));
-        uint8_t* kl = (uint8_t*)kv->k + (size_t)(l * kv->cap * kv->kdim) * kvel;
-        uint8_t* vl = (uint8_t*)kv->v + (size_t)(l * kv->cap * kv->kdim) * kvel;
-        RopeArgs ra{m->qkv, m->ldq, d.n_head, d.n_head_kv, d.head_dim, m->depth, m->npast,
-                    d.rope_theta, d.rope_neox, kl, vl, kv->kv_f16};
+        const ftx_tensor* tqkv[3] = {T[FTX_T_Q], T[FTX_T_K], T[FTX_T_V]};
+        GemvSeg qkv[3] = {seg(T[FTX_T_Q], m->qkv, m->ldq), seg(T[FTX_T_K], m->qkv + m->qdim, m->ldq),
+                          seg(T[FTX_T_V], m->qkv + m->qdim + m->kdim, m->ldq)};
+        rc = project(TK_GEMV_QKV,
+                     wbytes(T[FTX_T_Q]) + wbytes(T[FTX_T_K]) + wbytes(T[FTX_T_V]) + Md * D * f4 +
+                         Md * m->ldq * f4,
+                     m->x, D, m->norms + (l * 2) * D, tqkv, qkv, 3, D, EPI_STORE);
+        if (rc) return rc;
+        uint8_t* kl = (uint8_t*)kv->k + (size_t)(l * kv->cap_alloc * kv->kdim) * kvel;
+        uint8_t* vl = (uint8_t*)kv->v + (size_t)(l * kv->cap_alloc * kv->kdim) * kvel;
+        RopeArgs ra{m->qkv,       m->ldq,       d.n_head, d.n_head_kv, d.head_dim,   m->depth,
+                    m->npast,     d.rope_theta, d.rope_neox, kl,       vl,           kv->kv_f16,
+                    kv->cap_alloc};
         TRACED(TK_ROPE_KV, 2 * Md * m->ldq * f4 + 2 * Md * m->kdim * (double)kvel,
                launch_rope_kv(st, ra, M));
-        AttnArgs aa{m->qkv,  m->ldq, kl,           vl,         kv->kv_f16, m->npast,
-                    m->anc,  aw,     d.n_head,     d.n_head_kv, d.head_dim, npast + M,
-                    m->att};
-        TRACED(TK_ATTENTION,
-               2.0 * (double)(npast + M) * m->kdim * (double)kvel + 2 * Md * m->qdim * f4,
-               launch_attention(st, aa, M));
-        GemvSeg o{T[FTX_T_O]->data, T[FTX_T_O]->dtype, T[FTX_T_O]->row_bytes, D, m->x, D};
-        TRACED(TK_GEMV_O, wbytes(T[FTX_T_O]) + Md * m->qdim * f4 + 2 * Md * D * f4,
-               launch_gemv(st, &o, 1, m->att, m->qdim, m->qdim, M, EPI_ACCUM));
-        TRACED(TK_RMSNORM, norm_b,
-               launch_rmsnorm(st, m->x, m->norms + (l * 2 + 1) * D, D, M, eps, m->xn));
-        TRACED(TK_GEMV_SWIGLU,
-               wbytes(T[FTX_T_GATE]) + wbytes(T[FTX_T_UP]) + Md * D * f4 + Md * F * f4,
-               launch_gemv_swiglu(st, T[FTX_T_GATE]->data, T[FTX_T_UP]->data,
-                                  T[FTX_T_GATE]->dtype, T[FTX_T_GATE]->row_bytes, F, m->xn, D, D,
-                                  M, m->h, F));
+        const double attn_b =
+            2.0 * (double)(npast + M) * m->kdim * (double)kvel + 2 * Md * m->qdim * f4;
+        if (attn_mfma_supported(d.head_dim, kv->kv_f16, M, d.n_head, d.n_head_kv)) {
+            AttnMArgs am{};
+            am.qkv = m->qkv;
+            am.ldq = m->ldq;
+            am.kc = (const _Float16*)kl;
+            am.vt = (const _Float16*)vl;
+            am.cap = kv->cap_alloc;
+            am.npast = m->npast;
+            am.anc = m->anc;
+            am.anc_words = aw;
+            am.M = (int)M;
+            am.n_head = (int)d.n_head;
+            am.n_kv = (int)d.n_head_kv;
+            am.hd = (int)d.head_dim;
+            am.out = m->att;
+            TRACED(TK_ATTENTION, attn_b, launch_attn_mfma(st, am, kv->attn_part));
+        } else {
+            AttnArgs aa{m->qkv,  m->ldq, kl,       vl,          kv->kv_f16, m->npast,
+                        m->anc,  aw,     d.n_head, d.n_head_kv, d.head_dim, npast + M,
+                        m->att,  kv->cap_alloc};
+            TRACED(TK_ATTENTION, attn_b, launch_attention(st, aa, M));
+        }
+        GemvSeg o = seg(T[FTX_T_O], m->x, D);
+        rc = project(TK_GEMV_O, wbytes(T[FTX_T_O]) + Md * m->qdim * f4 + 2 * Md * D * f4, m->att,
+                     m->qdim, nullptr, &T[FTX_T_O], &o, 1, m->qdim, EPI_ACCUM);
+        if (rc) return rc;
+        const ftx_tensor* tgu[2] = {T[FTX_T_GATE], T[FTX_T_UP]};
+        GemvSeg gu[2] = {seg(T[FTX_T_GATE], m->h, F), seg(T[FTX_T_UP], nullptr, 0)};
+        rc = project(TK_GEMV_SWIGLU,
+                     wbytes(T[FTX_T_GATE]) + wbytes(T[FTX_T_UP]) + Md * D * f4 + Md * F * f4, m->x,
+                     D, m->norms + (l * 2 + 1) * D, tgu, gu, 2, D, EPI_SWIGLU);
+        if (rc) return rc;
         TRACED(TK_DOWN, wbytes(T[FTX_T_DOWN]) + Md * F * f4 + 2 * Md * D * f4,
                launch_down(st, T[FTX_T_DOWN]->data, T[FTX_T_DOWN]->dtype,
                            T[FTX_T_DOWN]->row_bytes, F, D, m->h, F, M, m->x, D, m->part));
     }
-    TRACED(TK_RMSNORM, norm_b,
-           launch_rmsnorm(st, m->x, m->norms + (d.n_layer * 2) * D, D, M, eps, m->xn));
     const ftx_tensor* lm = d.output ? d.output : d.tok_embd;
-    GemvSeg hs{lm->data, lm->dtype, lm->row_bytes, V, a->logits, V};
-    TRACED(TK_HEAD, wbytes(lm) + Md * D * f4 + Md * V * f4,
-           launch_gemv(st, &hs, 1, m->xn, D, D, M, EPI_STORE));
+    GemvSeg hs = seg(lm, a->logits, V);
+    rc = project(TK_HEAD, wbytes(lm) + Md * D * f4 + Md * V * f4, m->x, D,
+                 m->norms + (d.n_layer * 2) * D, &lm, &hs, 1, D, EPI_STORE);
+    if (rc) return rc;
 #undef TRACED
     if (a->advance) kv->npast = npast + M;
     return FTX_OK;

@@ -109,6 +109,8 @@ def load(path=LIB_PATH):
         "ftx_kv_free": (C.c_int, [_vp]),
         "ftx_kv_pointers": (C.c_int, [_vp, C.POINTER(_vp), C.POINTER(_vp), C.POINTER(_i64)]),
         "ftx_kv_truncate": (C.c_int, [_vp, _i64]),
+        "ftx_kv_write": (C.c_int, [_vp, _vp, _vp]),
+        "ftx_kv_read": (C.c_int, [_vp, _vp, _vp]),
         "ftx_verify_step": (C.c_int, [_vp, _vp, _vp, C.POINTER(VerifyArgs)]),
         "ftx_accept": (C.c_int, [_vp, C.POINTER(AcceptArgs)]),
         "ftx_fill_normal": (C.c_int, [_vp, _vp, C.c_int, _i64, C.c_uint64, C.c_float]),
@@ -354,23 +356,24 @@ class KV:
     def truncate(self, npast):
         self.ctx.check(self.ctx.lib.ftx_kv_truncate(self.handle, npast))
 
+    @property
+    def cap_alloc(self):
+        return (self.cap + 63) // 64 * 64
+
     def write(self, k, v):
-        """Copy host arrays shaped like self.shape into the cache."""
-        kp, vp, _ = self.pointers()
+        """Copy host arrays shaped like self.shape (the reference layout)
+        into the cache."""
         dt = np.float16 if self.kv_dtype == KV_F16 else np.float32
         k = np.ascontiguousarray(k, dt)
         v = np.ascontiguousarray(v, dt)
         assert k.shape == self.shape and v.shape == self.shape
-        self.ctx.copy(kp, k.ctypes.data, k.nbytes)
-        self.ctx.copy(vp, v.ctypes.data, v.nbytes)
+        self.ctx.check(self.ctx.lib.ftx_kv_write(self.handle, k.ctypes.data, v.ctypes.data))
 
     def read(self):
-        kp, vp, _ = self.pointers()
         dt = np.float16 if self.kv_dtype == KV_F16 else np.float32
         k = np.empty(self.shape, dt)
         v = np.empty(self.shape, dt)
-        self.ctx.copy(k.ctypes.data, kp, k.nbytes)
-        self.ctx.copy(v.ctypes.data, vp, v.nbytes)
+        self.ctx.check(self.ctx.lib.ftx_kv_read(self.handle, k.ctypes.data, v.ctypes.data))
         return k, v
 
     def free(self):
