@@ -126,6 +126,35 @@ def test_matmul_mfma_q4k_vs_oracle(gctx, orc, M, N):
     assert rel_err_rows(got[-1:], want[-1:]) < 3 * TOL
 
 
+@pytest.mark.parametrize("M", [1, 3, 8])
+@pytest.mark.parametrize("N", [64, 1000])
+def test_matmul_mfma_q6k_vs_oracle(gctx, orc, M, N):
+    """K = 4096 Q6_K: planar device layout, int8-MFMA over 16-element
+    sub-blocks."""
+    rng = np.random.default_rng(M * 77 + N)
+    K = 4096
+    raw = rand_weight(orc, rng, N, K, P.Q6_K)
+    t = gctx.upload(raw, P.Q6_K, (K, N))
+    x = rng.standard_normal((M, K)).astype(np.float32)
+    got = gctx.matmul(x, t)
+    t.free()
+    want = orc.matmul(x, raw, P.Q6_K, N)
+    assert rel_err_rows(got, want) < TOL
+
+
+def test_q6k_device_layout_roundtrip(gctx, orc):
+    """The planar Q6_K layout dequantises bit-exactly, including rows whose
+    super-block count is odd (padded rows)."""
+    rng = np.random.default_rng(12)
+    for cols in (256, 768, 4096):
+        raw = random_blocks(rng, P.Q6_K, 9, cols)
+        t = gctx.upload(raw, P.Q6_K, (cols, 9))
+        got = gctx.dequant(t)
+        t.free()
+        want = orc.dequant(raw, P.Q6_K, cols, rows=9)
+        assert np.array_equal(got.view(np.uint32), want.view(np.uint32)), cols
+
+
 def test_matmul_mfma_zero_row(gctx, orc):
     """An all-zero activation row gives zeros (row scale 0)."""
     rng = np.random.default_rng(3)

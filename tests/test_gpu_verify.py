@@ -146,6 +146,38 @@ def test_verify_mfma_attention(gctx, orc, npast, parents):
     assert rel_err_rows(got, want) < LOGIT_TOL
 
 
+def test_verify_mfma_down(gctx, orc):
+    """ffn_down in Q4_K (layer 0) and Q6_K (layer 1) takes the re-tiled MFMA
+    down kernel (two 256-column super-blocks, 32 row slices)."""
+    cfg = P.model_cfg(2, 512, 4, 1, 128, 1024, 500, rope_theta=10000.0)
+    model = {"cfg": dict(cfg)}
+    rng = np.random.default_rng(31)
+
+    def q(rows, cols, dt):
+        w = (rng.standard_normal((rows, cols)) * 0.02).astype(np.float32)
+        return dict(raw=orc.quantize(w, dt), dtype=dt, ne0=cols, ne1=rows)
+
+    ones = np.ones(512, np.float32).view(np.uint8).copy()
+    model["tok_embd"] = q(500, 512, P.Q8_0)
+    model["output"] = q(500, 512, P.Q8_0)
+    model["out_norm"] = dict(raw=ones, dtype=P.F32, ne0=512, ne1=1)
+    for l, ddt in enumerate((P.Q4_K, P.Q6_K)):
+        p = "blk.%d." % l
+        model[p + "attn_norm"] = dict(raw=ones, dtype=P.F32, ne0=512, ne1=1)
+        model[p + "ffn_norm"] = dict(raw=ones, dtype=P.F32, ne0=512, ne1=1)
+        model[p + "q"] = q(512, 512, P.Q8_0)
+        model[p + "k"] = q(128, 512, P.Q8_0)
+        model[p + "v"] = q(128, 512, P.Q8_0)
+        model[p + "o"] = q(512, 512, P.Q8_0)
+        model[p + "gate"] = q(1024, 512, P.Q8_0)
+        model[p + "up"] = q(1024, 512, P.Q8_0)
+        model[p + "down"] = q(1024, 512, ddt)
+    for M in (1, 5, 8):
+        toks = rng.integers(0, 500, M).tolist()
+        got, want, _, _ = run_both(gctx, orc, model, toks, 40, 64)
+        assert rel_err_rows(got, want) < LOGIT_TOL, M
+
+
 CFG1 = P.model_cfg(2, 512, 8, 8, 64, 1408, 32000, rope_theta=10000.0)
 CFG1_DT = dict(tok_embd=P.F32, output=P.Q4_0, q=P.Q4_0, k=P.Q4_0, v=P.Q4_0, o=P.Q4_0,
                gate=P.Q4_0, up=P.Q4_0, down=P.Q4_0)

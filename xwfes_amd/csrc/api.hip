@@ -6,6 +6,10 @@
 #include "ftx_internal.h"
 #include "quant_dev.h"
 
+int64_t dev_row_bytes(int dt, int64_t ncols) {
+    return dt == FTX_Q6_K ? q6k_dev_row_bytes(ncols) : ftx_row_bytes(dt, ncols);
+}
+
 int64_t ftx_block_elems(int dt) { return blk_elems(dt); }
 int64_t ftx_block_bytes(int dt) { return blk_bytes(dt); }
 
@@ -152,7 +156,7 @@ static int make_tensor(ftx_ctx* ctx, int dtype, const int64_t ne[4], ftx_tensor*
     t->ctx = ctx;
     t->dtype = dtype;
     for (int i = 0; i < 4; ++i) t->ne[i] = ne[i];
-    t->row_bytes = ftx_row_bytes(dtype, ne[0]);
+    t->row_bytes = dev_row_bytes(dtype, ne[0]);
     t->nrows = ne[1] * ne[2] * ne[3];
     const size_t bytes = (size_t)(t->row_bytes * t->nrows);
     if (bytes && hipMalloc(&t->data, bytes) != hipSuccess) {
@@ -174,18 +178,35 @@ int ftx_tensor_upload(ftx_ctx* ctx, int dtype, const int64_t ne[4], int64_t row_
     int rc = make_tensor(ctx, dtype, ne, out);
     if (rc) return rc;
     ftx_tensor* t = *out;
-    const int64_t stride = row_stride > 0 ? row_stride : t->row_bytes;
-    if (stride < t->row_bytes) {
+    const int64_t host_rb = ftx_row_bytes(dtype, ne[0]);  // GGUF row size
+    const int64_t stride = row_stride > 0 ? row_stride : host_rb;
+    if (stride < host_rb) {
         ftx_tensor_free(t);
         *out = nullptr;
         return ftx_fail(ctx, FTX_E_INVALID, "row_stride shorter than a row");
     }
     hipError_t e;
-    if (stride == t->row_bytes)
+    if (dtype == FTX_Q6_K) {
+        // GGUF rows through the workspace, then into the device planes
+        uint8_t* tmp;
+        rc = ftx_workspace(ctx, (size_t)(host_rb * t->nrows), (void**)&tmp);
+        if (rc) {
+            ftx_tensor_free(t);
+            *out = nullptr;
+            return rc;
+        }
+        e = hipMemcpy2D(tmp, (size_t)host_rb, host, (size_t)stride, (size_t)host_rb,
+                        (size_t)t->nrows, hipMemcpyHostToDevice);
+        if (e == hipSuccess)
+            e = launch_q6k_repack(ctx->stream, tmp, host_rb, ne[0], t->nrows, t->row_bytes,
+                                  t->data);
+        if (e == hipSuccess) e = hipStreamSynchronize(ctx->stream);
+    } else if (stride == t->row_bytes) {
         e = hipMemcpy(t->data, host, (size_t)(t->row_bytes * t->nrows), hipMemcpyHostToDevice);
-    else
+    } else {
         e = hipMemcpy2D(t->data, (size_t)t->row_bytes, host, (size_t)stride, (size_t)t->row_bytes,
                         (size_t)t->nrows, hipMemcpyHostToDevice);
+    }
     if (e != hipSuccess) {
         (void)hipGetLastError();
         ftx_tensor_free(t);
@@ -345,7 +366,7 @@ int ftx_expert_chunk(ftx_ctx* ctx, const ftx_expert_job* j) {
     if (!j->x || !j->out || !j->gate || !j->up || !j->down)
         return ftx_fail(ctx, FTX_E_INVALID, "null job pointer");
     if (!ftx_dtype_ok(j->dt)) return ftx_fail(ctx, FTX_E_UNSUPPORTED, "unsupported dtype");
-    const int64_t rb = ftx_row_bytes(j->dt, j->K);
+    const int64_t rb = dev_row_bytes(j->dt, j->K);
     if (j->gate_up_row_stride != rb || j->down_row_stride != rb)
         return ftx_fail(ctx, FTX_E_INVALID, "expert rows must be dense (stride == row bytes)");
     if (!ftx_is_device_ptr(j->gate) || !ftx_is_device_ptr(j->up) || !ftx_is_device_ptr(j->down))

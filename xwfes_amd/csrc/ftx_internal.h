@@ -70,6 +70,10 @@ struct ftx_tensor {
 int64_t ftx_block_elems(int dt);
 int64_t ftx_block_bytes(int dt);
 bool ftx_dtype_ok(int dt);
+// bytes of one resident row: the GGUF row, except Q6_K's planar layout
+int64_t dev_row_bytes(int dt, int64_t ncols);
+hipError_t launch_q6k_repack(hipStream_t st, const uint8_t* src, int64_t src_row_bytes,
+                             int64_t ncols, int64_t nrows, int64_t dst_row_bytes, uint8_t* dst);
 
 int ftx_fail(ftx_ctx* ctx, int code, const std::string& msg);
 #define FTX_HIP(ctx, call)                                                           \
@@ -131,6 +135,19 @@ size_t mv_part_floats(int64_t rows, int64_t K, int cu_count);
 enum { EPI_SWIGLU = 2 };
 hipError_t launch_mv(hipStream_t st, const GemvSeg* segs, int nseg, const int8_t* xq, int64_t K,
                      int64_t M, int epi, float* part, int cu_count);
+
+hipError_t launch_part_reduce(hipStream_t st, const float* part, int S, int64_t N, int64_t M,
+                              float* y, int64_t ldy);
+
+// MFMA ffn_down (k_down.hip) over a re-tiled copy of the weights
+bool down_mfma_supported(int dt, int64_t n_in, int64_t N, int64_t M);
+size_t down_tiled_bytes(int dt, int64_t n_in, int64_t N);
+hipError_t launch_down_tile(hipStream_t st, const uint8_t* src, int64_t src_row_bytes, int dt,
+                            int64_t n_in, int64_t N, uint8_t* dst);
+size_t down_mfma_part_floats(int64_t n_in, int64_t N, int cu_count);
+hipError_t launch_down_mfma(hipStream_t st, int dt, const uint8_t* tiled, int64_t n_in, int64_t N,
+                            const float* h, int64_t ldh, int64_t M, float* y, int64_t ldy,
+                            float* part, int cu_count);
 
 // quantise rows (synthetic model builder)
 hipError_t launch_quantize(hipStream_t st, const float* src, int dt, int64_t ncols,

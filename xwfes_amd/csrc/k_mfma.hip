@@ -119,6 +119,7 @@ struct MvSeg {
     int64_t N;
     int64_t tile0;  // first global tile of the segment
     int64_t row0;   // first global row of the segment
+    int dt;
 };
 
 struct MvArgs {
@@ -127,11 +128,103 @@ struct MvArgs {
     int64_t tiles;
     int64_t rows;       // global rows (sum of N)
     int sb_per_split;
+    int nsb;            // super-blocks per row
     const int8_t* frag;
     const int8_t* xs32;
+    const int8_t* xs16;
     const float* scale;
     float* part;        // [S][8][rows]
 };
+
+// Q6_K  w = d*sc_s*(q - 32)  (q in 0..63, sub-block s of 16)
+//   y = sum_sb s_sb * d * [ sum_s sc_s * (A_s . q_s)  -  32 * sum_s sc_s * X_s ]
+// with v_mfma_i32_32x32x16_i8 per sub-block (lane l holds 8 slots
+// 8*(l/32) + t) and the second sum as one 32x32x32 MFMA whose B operand is
+// the 16 int8 scales.
+__global__ void __launch_bounds__(256) k_mv_q6k(MvArgs a) {
+    const int lane = threadIdx.x & 63;
+    const int64_t T = (int64_t)blockIdx.x * 4 + (threadIdx.x >> 6);
+    if (T >= a.tiles) return;
+    int si = 0;
+    while (si + 1 < a.nseg && T >= a.seg[si + 1].tile0) ++si;
+    const MvSeg sg = a.seg[si];
+    if (sg.dt != FTX_Q6_K) return;
+    const int col = lane & 31, g = lane >> 5;
+    const int64_t n_raw = (T - sg.tile0) * 32 + col;
+    const int64_t n = n_raw < sg.N ? n_raw : sg.N - 1;
+    const uint8_t* wrow = sg.W + n * sg.row_bytes;
+    const int64_t nsb = a.nsb;
+    const int sp = blockIdx.y;
+    const int sb0 = sp * a.sb_per_split, sb1 = sb0 + a.sb_per_split;
+    const bool arow = col < 16;
+    float acc[8];
+#pragma unroll
+    for (int r = 0; r < 8; ++r) acc[r] = 0.f;
+    const v4i zero4 = {0, 0, 0, 0};
+    const v16i zero16 = {};
+    for (int sb = sb0; sb < sb1; ++sb) {
+        v4i ql[4], qh[2];
+#pragma unroll
+        for (int i = 0; i < 4; ++i) ql[i] = ld16g(wrow + (int64_t)sb * 128 + 64 * g + 16 * i);
+#pragma unroll
+        for (int i = 0; i < 2; ++i)
+            qh[i] = ld16g(wrow + nsb * 128 + (int64_t)sb * 64 + 32 * g + 16 * i);
+        const v4i scv = ld16g(wrow + nsb * 192 + (int64_t)sb * 16);
+        const float d = h2f(*(const uint16_t*)(wrow + nsb * 208 + (int64_t)sb * 2));
+        const uint32_t* qlw = (const uint32_t*)ql;  // 16 dwords: [c][a][b][2]
+        const uint32_t* qhw = (const uint32_t*)qh;  // 8 dwords: [c][b][2]
+        const uint32_t* scw = (const uint32_t*)&scv;
+        int ai[8];
+#pragma unroll
+        for (int r = 0; r < 8; ++r) ai[r] = 0;
+#pragma unroll
+        for (int s = 0; s < 16; ++s) {
+            const int c = s >> 3, k = (s & 7) >> 1, b = s & 1;
+            long af = 0;
+            if (arow)
+                af = *(const long*)(a.frag +
+                                    ((((int64_t)sb * 8 + (s >> 1)) * 2 + b) * 16 + col) * 16 +
+                                    8 * g);
+            uint32_t v[2];
+#pragma unroll
+            for (int h = 0; h < 2; ++h) {
+                const uint32_t L = qlw[8 * c + 4 * (k & 1) + 2 * b + h];
+                const uint32_t H = qhw[4 * c + 2 * b + h];
+                const uint32_t lo = (k >> 1) ? (L >> 4) & 0x0F0F0F0Fu : L & 0x0F0F0F0Fu;
+                const uint32_t hi = ((H >> (2 * k)) & 0x03030303u) << 4;
+                v[h] = lo | hi;
+            }
+            const long bf = (long)((uint64_t)v[0] | ((uint64_t)v[1] << 32));
+            const v16i cm = __builtin_amdgcn_mfma_i32_32x32x16_i8(af, bf, zero16, 0, 0, 0);
+            const int sc = (int)(int8_t)((scw[s >> 2] >> (8 * (s & 3))) & 0xFF);
+#pragma unroll
+            for (int r = 0; r < 8; ++r) ai[r] += sc * cm[r];
+            // keep at most two sub-blocks in flight (bounds the accumulators)
+            if (s & 1) __builtin_amdgcn_sched_barrier(0);
+        }
+        v4i ax = zero4, bs = zero4;
+        if (g == 0) {
+            ax = ld16g(a.xs16 + ((int64_t)sb * 32 + col) * 16);
+            bs = scv;
+        }
+        const v16i dm = __builtin_amdgcn_mfma_i32_32x32x32_i8(ax, bs, zero16, 0, 0, 0);
+        const float4 s4 = *(const float4*)(a.scale + (int64_t)sb * 8 + 4 * g);
+        const float sm[4] = {s4.x, s4.y, s4.z, s4.w};
+#pragma unroll
+        for (int r = 0; r < 8; ++r) {
+            const int corr = dm[r] + 64 * dm[r + 8];
+            acc[r] += sm[r & 3] * (d * (float)(ai[r] - 32 * corr));
+        }
+    }
+    float* out = a.part + (int64_t)sp * 8 * a.rows + sg.row0;
+    if (n_raw < sg.N) {
+#pragma unroll
+        for (int r = 0; r < 4; ++r) {
+            const int m = 4 * g + r;
+            out[(int64_t)m * a.rows + n_raw] = acc[r] + acc[r + 4] * (1.f / 256.f);
+        }
+    }
+}
 
 __global__ void __launch_bounds__(256) k_mv_q4k(MvArgs a) {
     const int lane = threadIdx.x & 63;
@@ -140,6 +233,7 @@ __global__ void __launch_bounds__(256) k_mv_q4k(MvArgs a) {
     int si = 0;
     while (si + 1 < a.nseg && T >= a.seg[si + 1].tile0) ++si;
     const MvSeg sg = a.seg[si];
+    if (sg.dt != FTX_Q4_K) return;
     const int col = lane & 31, g = lane >> 5;
     const int64_t n_raw = (T - sg.tile0) * 32 + col;
     const int64_t n = n_raw < sg.N ? n_raw : sg.N - 1;
@@ -286,7 +380,24 @@ hipError_t launch_xq_prep(hipStream_t st, const float* x, int64_t ldx, const flo
 }
 
 bool mv_supported(int dt, int64_t K, int64_t M) {
-    return dt == FTX_Q4_K && M >= 1 && M <= 8 && K % 4096 == 0 && K <= 16384;
+    return (dt == FTX_Q4_K || dt == FTX_Q6_K) && M >= 1 && M <= 8 && K % 4096 == 0 &&
+           K <= 16384;
+}
+
+// y[m*ldy + n] += sum_s part[s][m][n] for n < N, m < M (part rows of 8)
+hipError_t launch_part_reduce(hipStream_t st, const float* part, int S, int64_t N, int64_t M,
+                              float* y, int64_t ldy) {
+    RedArgs r{};
+    r.part = part;
+    r.S = S;
+    r.rows = N;
+    r.M = (int)M;
+    r.epi = EPI_ACCUM;
+    r.nseg = 1;
+    r.seg[0] = RedSeg{y, ldy, 0, N};
+    hipLaunchKernelGGL(k_mv_reduce, dim3((unsigned)((N + 255) / 256), (unsigned)M), dim3(256), 0,
+                       st, r);
+    return hipGetLastError();
 }
 
 // contraction splits: double until ~8 waves per CU or one super-block each
@@ -308,12 +419,16 @@ hipError_t launch_mv(hipStream_t st, const GemvSeg* segs, int nseg, const int8_t
     MvArgs a{};
     a.nseg = nseg;
     int64_t tiles = 0, rows = 0;
+    bool has4 = false, has6 = false;
     for (int i = 0; i < nseg; ++i) {
         a.seg[i].W = segs[i].W;
         a.seg[i].row_bytes = segs[i].row_bytes;
         a.seg[i].N = segs[i].N;
         a.seg[i].tile0 = tiles;
         a.seg[i].row0 = rows;
+        a.seg[i].dt = segs[i].dt;
+        has4 |= segs[i].dt == FTX_Q4_K;
+        has6 |= segs[i].dt == FTX_Q6_K;
         tiles += (segs[i].N + 31) / 32;
         rows += segs[i].N;
     }
@@ -322,13 +437,19 @@ hipError_t launch_mv(hipStream_t st, const GemvSeg* segs, int nseg, const int8_t
     const int nsb = (int)(K / 256);
     const int S = mv_splits(tiles, nsb, cu_count);
     a.sb_per_split = nsb / S;
+    a.nsb = nsb;
     a.frag = xq;
     a.xs32 = xq + K * 16;
+    a.xs16 = xq + K * 16 + K;
     a.scale = (const float*)(xq + K * 16 + K + K * 2);
     a.part = part;
-    hipLaunchKernelGGL(k_mv_q4k, dim3((unsigned)((tiles + 3) / 4), (unsigned)S), dim3(256), 0, st,
-                       a);
+    // each kernel takes the tiles of its dtype; both write disjoint rows
+    const dim3 grid((unsigned)((tiles + 3) / 4), (unsigned)S);
+    if (has4) hipLaunchKernelGGL(k_mv_q4k, grid, dim3(256), 0, st, a);
     hipError_t e = hipGetLastError();
+    if (e != hipSuccess) return e;
+    if (has6) hipLaunchKernelGGL(k_mv_q6k, grid, dim3(256), 0, st, a);
+    e = hipGetLastError();
     if (e != hipSuccess) return e;
     RedArgs r{};
     r.part = part;

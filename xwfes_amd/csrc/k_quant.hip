@@ -182,6 +182,38 @@ __device__ void q_q6_k(uint8_t* o, const float* x) {
     st16(o + 208, dh);
 }
 
+// place one GGUF Q6_K block into the device planes of its row
+__device__ void q6k_scatter(uint8_t* row, int64_t nsb, int64_t sb, const uint8_t* blk) {
+    for (int i = 0; i < 128; ++i) row[sb * 128 + q6k_ql_dev(i)] = blk[i];
+    for (int i = 0; i < 64; ++i) row[nsb * 128 + sb * 64 + q6k_qh_dev(i)] = blk[128 + i];
+    for (int i = 0; i < 16; ++i) row[nsb * 192 + sb * 16 + i] = blk[192 + i];
+    row[nsb * 208 + sb * 2] = blk[208];
+    row[nsb * 208 + sb * 2 + 1] = blk[209];
+}
+
+// GGUF Q6_K rows -> device planar rows, one thread per block
+__global__ void __launch_bounds__(256) k_q6k_repack(const uint8_t* __restrict__ src,
+                                                    int64_t src_row_bytes, int64_t nsb,
+                                                    int64_t total, int64_t dst_row_bytes,
+                                                    uint8_t* __restrict__ dst) {
+    const int64_t t = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
+    if (t >= total) return;
+    const int64_t r = t / nsb, sb = t % nsb;
+    uint8_t blk[210];
+    const uint8_t* s = src + r * src_row_bytes + sb * 210;
+    for (int i = 0; i < 210; ++i) blk[i] = s[i];
+    q6k_scatter(dst + r * dst_row_bytes, nsb, sb, blk);
+}
+
+hipError_t launch_q6k_repack(hipStream_t st, const uint8_t* src, int64_t src_row_bytes,
+                             int64_t ncols, int64_t nrows, int64_t dst_row_bytes, uint8_t* dst) {
+    const int64_t nsb = (ncols + 255) / 256, total = nsb * nrows;
+    if (total == 0) return hipSuccess;
+    hipLaunchKernelGGL(k_q6k_repack, dim3((unsigned)((total + 255) / 256)), dim3(256), 0, st, src,
+                       src_row_bytes, nsb, total, dst_row_bytes, dst);
+    return hipGetLastError();
+}
+
 // one thread per block (per element for the plain types)
 __global__ void __launch_bounds__(256) k_quantize(const float* __restrict__ src, int dt,
                                                   int64_t ncols, int64_t nblk_row,
@@ -207,7 +239,12 @@ __global__ void __launch_bounds__(256) k_quantize(const float* __restrict__ src,
         case FTX_Q4_0: q_q4_0(o, x); break;
         case FTX_Q4_1: q_q4_1(o, x); break;
         case FTX_Q4_K: q_q4_k(o, x); break;
-        case FTX_Q6_K: q_q6_k(o, x); break;
+        case FTX_Q6_K: {
+            uint8_t blk[210];
+            q_q6_k(blk, x);
+            q6k_scatter(dst + r * row_bytes, nblk_row, b, blk);
+            break;
+        }
         default: break;
     }
 }

@@ -54,6 +54,29 @@ __host__ __device__ constexpr int64_t blk_bytes(int dt) {
                             : 0;
 }
 
+// ---- Q6_K device layout ----
+// GGUF Q6_K super-blocks are 210 bytes, so inside a row they sit at 2-byte
+// alignment only.  On the device a Q6_K row is stored as planes, each
+// 16-byte aligned, with the same bytes permuted:
+//   QL plane  [nsb][128]: GGUF ql byte 64c + 32a + 16b + 8g + t  ->  64g + 32c + 16a + 8b + t
+//   QH plane  [nsb][64] : GGUF qh byte 32c + 16b + 8g + t        ->  32g + 16c + 8b + t
+//   SC plane  [nsb][16] : the 16 int8 sub-block scales
+//   D  plane  [nsb][2]  : the fp16 super-block scale
+// and the row padded to a multiple of 16 bytes.  g is the half of a
+// 16-element sub-block an MFMA lane group reads, so each lane group's bytes
+// are contiguous.
+__host__ __device__ constexpr int64_t q6k_dev_row_bytes(int64_t ncols) {
+    return ((ncols + 255) / 256 * 210 + 15) / 16 * 16;
+}
+__host__ __device__ inline int q6k_ql_dev(int i) {  // GGUF ql index -> plane index
+    const int c = i >> 6, a = (i >> 5) & 1, b = (i >> 4) & 1, g = (i >> 3) & 1, t = i & 7;
+    return 64 * g + 32 * c + 16 * a + 8 * b + t;
+}
+__host__ __device__ inline int q6k_qh_dev(int i) {
+    const int c = i >> 5, b = (i >> 4) & 1, g = (i >> 3) & 1, t = i & 7;
+    return 32 * g + 16 * c + 8 * b + t;
+}
+
 // Elements e0 .. e0+7 of `row` (e0 % 8 == 0); elements at or past n are 0.
 __device__ inline void dq8(const uint8_t* __restrict__ row, int dt, int64_t e0, int64_t n,
                            float* __restrict__ o) {
@@ -141,14 +164,15 @@ __device__ inline void dq8(const uint8_t* __restrict__ row, int dt, int64_t e0, 
             }
             return;
         }
-        case FTX_Q6_K: {
-            const uint8_t* p = row + (e0 >> 8) * 210;
+        case FTX_Q6_K: {  // device planar layout (above)
+            const int64_t nsb = (n + 255) / 256, sb = e0 >> 8;
             const int r = (int)(e0 & 255);
             const int c = r >> 7, rr = r & 127, k = rr >> 5, l0 = rr & 31;
-            const float d = h2f(ld16(p + 208));
-            const float ds = d * (float)(int8_t)p[192 + (r >> 4)];
-            const uint8_t* ql = p + 64 * c + 32 * (k & 1) + l0;
-            const uint8_t* qh = p + 128 + 32 * c + l0;
+            const float d = h2f(ld16(row + nsb * 208 + sb * 2));
+            const float ds = d * (float)(int8_t)row[nsb * 192 + sb * 16 + (r >> 4)];
+            // 8 consecutive l share (b, g): contiguous in both planes
+            const uint8_t* ql = row + sb * 128 + q6k_ql_dev(64 * c + 32 * (k & 1) + l0);
+            const uint8_t* qh = row + nsb * 128 + sb * 64 + q6k_qh_dev(32 * c + l0);
 #pragma unroll
             for (int i = 0; i < 8; ++i) {
                 const int lo = (k >> 1) ? (ql[i] >> 4) : (ql[i] & 0xF);

@@ -25,6 +25,9 @@ struct ftx_model {
     // int8-MFMA GEMV operands: activation fragments and split sums
     int8_t* xq = nullptr;
     float* mvpart = nullptr;
+    // per-layer re-tiled ffn_down copies for the MFMA down kernel (or null)
+    std::vector<uint8_t*> down_tiled;
+    float* downpart = nullptr;
 };
 
 // the MFMA row-dot path applies to every segment of a projection, or none
@@ -51,6 +54,9 @@ static void model_release(ftx_model* m) {
                     m->toks,  m->depth, m->anc, m->npast, m->xq,  m->mvpart};
     for (void* b : bufs)
         if (b) (void)hipFree(b);
+    for (uint8_t* b : m->down_tiled)
+        if (b) (void)hipFree(b);
+    if (m->downpart) (void)hipFree(m->downpart);
     delete m;
 }
 
@@ -126,6 +132,24 @@ int ftx_model_create(ftx_ctx* ctx, const ftx_model_desc* d, ftx_model** out) {
             pf = std::max(pf, mv_part_floats(rows, Kmax, ctx->cu_count));
         ok = dalloc(&m->xq, xq_bytes(Kmax)) && dalloc(&m->mvpart, pf);
     }
+    // re-tiled ffn_down copies (same bytes, MFMA-friendly order)
+    m->down_tiled.assign((size_t)d->n_layer, nullptr);
+    bool any_tiled = false;
+    for (int64_t l = 0; ok && l < d->n_layer; ++l) {
+        const ftx_tensor* dn = d->layers[l * FTX_LAYER_TENSORS + FTX_T_DOWN];
+        if (!down_mfma_supported(dn->dtype, d->n_ff, D, 1)) continue;
+        uint8_t* buf = nullptr;
+        if (!dalloc(&buf, down_tiled_bytes(dn->dtype, d->n_ff, D))) {
+            ok = false;
+            break;
+        }
+        m->down_tiled[l] = buf;
+        any_tiled = true;
+        if (launch_down_tile(ctx->stream, dn->data, dn->row_bytes, dn->dtype, d->n_ff, D, buf) !=
+            hipSuccess)
+            ok = false;
+    }
+    if (ok && any_tiled) ok = dalloc(&m->downpart, down_mfma_part_floats(d->n_ff, D, ctx->cu_count));
     if (!ok) {
         model_release(m);
         return ftx_fail(ctx, FTX_E_NOMEM, "activation allocation failed");
@@ -402,9 +426,15 @@ int ftx_verify_step(ftx_ctx* ctx, ftx_model* m, ftx_kv* kv, const ftx_verify_arg
                      wbytes(T[FTX_T_GATE]) + wbytes(T[FTX_T_UP]) + Md * D * f4 + Md * F * f4, m->x,
                      D, m->norms + (l * 2 + 1) * D, tgu, gu, 2, D, EPI_SWIGLU);
         if (rc) return rc;
-        TRACED(TK_DOWN, wbytes(T[FTX_T_DOWN]) + Md * F * f4 + 2 * Md * D * f4,
-               launch_down(st, T[FTX_T_DOWN]->data, T[FTX_T_DOWN]->dtype,
-                           T[FTX_T_DOWN]->row_bytes, F, D, m->h, F, M, m->x, D, m->part));
+        const double down_b = wbytes(T[FTX_T_DOWN]) + Md * F * f4 + 2 * Md * D * f4;
+        if (m->down_tiled[l] && down_mfma_supported(T[FTX_T_DOWN]->dtype, F, D, M))
+            TRACED(TK_DOWN, down_b,
+                   launch_down_mfma(st, T[FTX_T_DOWN]->dtype, m->down_tiled[l], F, D, m->h, F, M,
+                                    m->x, D, m->downpart, ctx->cu_count));
+        else
+            TRACED(TK_DOWN, down_b,
+                   launch_down(st, T[FTX_T_DOWN]->data, T[FTX_T_DOWN]->dtype,
+                               T[FTX_T_DOWN]->row_bytes, F, D, m->h, F, M, m->x, D, m->part));
     }
     const ftx_tensor* lm = d.output ? d.output : d.tok_embd;
     GemvSeg hs = seg(lm, a->logits, V);
