@@ -169,6 +169,7 @@ def main():
     log("timed %d steps: mean %.3f ms, median %.3f ms" % (args.steps, ms_step, med_ms))
 
     # per-kernel-class device time from HIP events on the launch stream
+    args.trace_steps = max(args.trace_steps, 1)
     ctx.trace(True)
     for _ in range(args.trace_steps):
         step()

@@ -227,8 +227,10 @@ struct RowStats {
     int32_t amax;
     double sum;  // sum_i exp((l_i - mx)/T) in double
 };
+size_t row_stats_scratch_bytes(int64_t nrows, int64_t V);
+// with_sum = 0 skips the exp sums (greedy decisions need the argmax only)
 hipError_t launch_row_stats(hipStream_t st, const float* rows, int64_t nrows, int64_t V,
-                            float temp, RowStats* out);
+                            float temp, int with_sum, void* scratch, RowStats* out);
 struct AcceptDev {
     const float* base_row;
     const float* rows;
@@ -245,5 +247,7 @@ struct AcceptDev {
     double* part;            // scratch [1024]
     int32_t* out;            // device: [0]=n_acc, [1]=bonus, [2..2+M) accepted
     float* margin;           // device scalar
+    int32_t* brow;           // device scalar: row of the ratio-mode bonus draw
+    float* bu;               // device scalar: its uniform
 };
 hipError_t launch_accept(hipStream_t st, const AcceptDev& a);

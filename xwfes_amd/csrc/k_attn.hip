@@ -155,22 +155,45 @@ __global__ void __launch_bounds__(64) k_attn_mfma(AttnMArgs a) {
 }
 
 // out[m][h*hd + d] = sum_c e^(max_c - M) O_c[d] / sum_c e^(max_c - M) sum_c
-__global__ void k_attn_combine(AttnMArgs a, int nch) {
+// one block per query row; the chunk weights are formed once in LDS so the
+// output loop is a stream of independent loads
+__global__ void __launch_bounds__(128) k_attn_combine(AttnMArgs a, int nch) {
+    __shared__ float wsh[1024];  // chunk weights (nch <= 1024)
+    __shared__ float red[128];
     const int64_t qi = blockIdx.x;  // m * n_head + h
     const int d = threadIdx.x;
     const int64_t npast = *a.npast;
     const int nvalid = (int)((npast + a.M + CH - 1) / CH);
     float M = -INFINITY;
-    for (int c = 0; c < nvalid; ++c) M = fmaxf(M, a.pmax[qi * nch + c]);
-    float den = 0.f, num = 0.f;
-    for (int c = 0; c < nvalid; ++c) {
-        const float mc = a.pmax[qi * nch + c];
-        if (mc == -INFINITY) continue;
-        const float w = expf(mc - M);
-        den += w * a.psum[qi * nch + c];
-        num += w * a.pout[(qi * nch + c) * a.hd + d];
+    for (int c = d; c < nvalid; c += 128) M = fmaxf(M, a.pmax[qi * nch + c]);
+    red[d] = M;
+    __syncthreads();
+    for (int o = 64; o > 0; o >>= 1) {
+        if (d < o) red[d] = fmaxf(red[d], red[d + o]);
+        __syncthreads();
     }
-    a.out[qi * a.hd + d] = num / den;
+    M = red[0];
+    __syncthreads();
+    float den = 0.f;
+    for (int c = d; c < nvalid; c += 128) {
+        const float mc = a.pmax[qi * nch + c];
+        const float w = mc == -INFINITY ? 0.f : expf(mc - M);
+        wsh[c] = w;
+        den += w * a.psum[qi * nch + c];
+    }
+    red[d] = den;
+    __syncthreads();
+    for (int o = 64; o > 0; o >>= 1) {
+        if (d < o) red[d] += red[d + o];
+        __syncthreads();
+    }
+    den = red[0];
+    if (d < a.hd) {
+        float num = 0.f;
+#pragma unroll 8
+        for (int c = 0; c < nvalid; ++c) num += wsh[c] * a.pout[(qi * nch + c) * a.hd + d];
+        a.out[qi * a.hd + d] = num / den;
+    }
 }
 
 }  // namespace
@@ -186,6 +209,7 @@ size_t attn_part_floats(int64_t M, int64_t n_head, int64_t hd, int64_t cap_alloc
 
 hipError_t launch_attn_mfma(hipStream_t st, AttnMArgs a, float* part) {
     const int nch = (int)(a.cap / CH);
+    if (nch > 1024) return hipErrorInvalidValue;  // combine weights live in LDS
     const int64_t qi = (int64_t)a.M * a.n_head;
     a.pmax = part;
     a.psum = part + qi * nch;
@@ -201,6 +225,6 @@ hipError_t launch_attn_mfma(hipStream_t st, AttnMArgs a, float* part) {
         return hipErrorInvalidValue;
     hipError_t e = hipGetLastError();
     if (e != hipSuccess) return e;
-    hipLaunchKernelGGL(k_attn_combine, dim3((unsigned)qi), dim3((unsigned)a.hd), 0, st, a, nch);
+    hipLaunchKernelGGL(k_attn_combine, dim3((unsigned)qi), dim3(128), 0, st, a, nch);
     return hipGetLastError();
 }

@@ -27,87 +27,94 @@ typedef int v16i __attribute__((ext_vector_type(16)));
 __device__ __forceinline__ v4i ld16g(const void* p) { return *(const v4i*)p; }
 
 // ---------------------------------------------------------------- prep
-// One block per activation row m < 8 (rows m >= M are written as zeros).
-// Optional RMSNorm (src/engine.cpp:23-41) fused in front.
-__global__ void __launch_bounds__(256) k_xq_prep(const float* __restrict__ x, int64_t ldx,
-                                                 const float* __restrict__ normw, float eps,
-                                                 int64_t K, int M, int8_t* __restrict__ frag,
-                                                 int8_t* __restrict__ xs32,
-                                                 int8_t* __restrict__ xs16,
-                                                 float* __restrict__ scale) {
+// One wave per (256-element super-block sb, activation row m < 8); rows
+// m >= M are written as zeros.  Optional RMSNorm (src/engine.cpp:23-41) in
+// front: each wave reduces the sum of squares of its whole row (L2 hits).
+// Lane l quantises elements 4l .. 4l+3 of the super-block.
+__global__ void __launch_bounds__(64) k_xq_prep(const float* __restrict__ x, int64_t ldx,
+                                                const float* __restrict__ normw, float eps,
+                                                int64_t K, int M, int8_t* __restrict__ frag,
+                                                int8_t* __restrict__ xs32,
+                                                int8_t* __restrict__ xs16,
+                                                float* __restrict__ scale) {
 #pragma clang fp contract(off)
-    extern __shared__ float xr[];  // K floats
-    __shared__ float red[256];
-    const int m = blockIdx.x, tid = threadIdx.x;
+    const int64_t sb = blockIdx.x;
+    const int m = blockIdx.y, l = threadIdx.x;
     const bool live = m < M;
-    float ss = 0.f, mx = 0.f;
+    const float* row = x + (int64_t)m * ldx;
+    float v[4] = {0.f, 0.f, 0.f, 0.f};
     if (live) {
-        const float* row = x + (int64_t)m * ldx;
-        for (int64_t k = tid; k < K; k += 256) {
-            const float v = row[k];
-            xr[k] = v;
-            ss += v * v;
-        }
-    }
-    if (normw && live) {
-        red[tid] = ss;
-        __syncthreads();
-        for (int o = 128; o > 0; o >>= 1) {
-            if (tid < o) red[tid] += red[tid + o];
-            __syncthreads();
-        }
-        const float inv = 1.f / sqrtf(red[0] / (float)K + eps);
-        __syncthreads();
-        for (int64_t k = tid; k < K; k += 256) xr[k] = xr[k] * inv * normw[k];
-    }
-    __syncthreads();
-    const int64_t ngroups = K / 16;
-    // 256 | ngroups: the 16 groups of a super-block are 16 adjacent lanes
-    for (int64_t G = tid; G < ngroups; G += 256) {
-        mx = 0.f;
-        if (live)
-#pragma unroll
-            for (int t = 0; t < 16; ++t) mx = fmaxf(mx, fabsf(xr[G * 16 + t]));
-#pragma unroll
-        for (int o = 1; o < 16; o <<= 1) mx = fmaxf(mx, __shfl_xor(mx, o, 64));
-        const float q = mx > 0.f ? 127.f / mx : 0.f;
-        if ((G & 15) == 0) scale[(G >> 4) * 8 + m] = mx > 0.f ? mx / 127.f : 0.f;
-        int sa = 0, sb = 0;
-        uint32_t pa[4] = {0, 0, 0, 0}, pb[4] = {0, 0, 0, 0};
-        if (live && mx > 0.f) {
-#pragma unroll
-            for (int t = 0; t < 16; ++t) {
-                const float v = xr[G * 16 + t] * q;
-                const float a = rintf(v);
-                float bf = rintf((v - a) * 256.f);
-                bf = fminf(fmaxf(bf, -127.f), 127.f);
-                const int ai = (int)a, bi = (int)bf;
-                sa += ai;
-                sb += bi;
-                pa[t >> 2] |= (uint32_t)(ai & 0xFF) << (8 * (t & 3));
-                pb[t >> 2] |= (uint32_t)(bi & 0xFF) << (8 * (t & 3));
+        const float4 t = *(const float4*)(row + sb * 256 + 4 * l);
+        v[0] = t.x;
+        v[1] = t.y;
+        v[2] = t.z;
+        v[3] = t.w;
+        if (normw) {
+            float ss = 0.f;
+            for (int64_t k = 4 * l; k < K; k += 256) {
+                const float4 u = *(const float4*)(row + k);
+                ss += u.x * u.x;
+                ss += u.y * u.y;
+                ss += u.z * u.z;
+                ss += u.w * u.w;
             }
+#pragma unroll
+            for (int o = 32; o > 0; o >>= 1) ss += __shfl_xor(ss, o, 64);
+            const float inv = 1.f / sqrtf(ss / (float)K + eps);
+            const float4 w4 = *(const float4*)(normw + sb * 256 + 4 * l);
+            v[0] = v[0] * inv * w4.x;
+            v[1] = v[1] * inv * w4.y;
+            v[2] = v[2] * inv * w4.z;
+            v[3] = v[3] * inv * w4.w;
         }
-        const int64_t kb = G >> 1, g = G & 1;  // 32-element block, half
-        v4i va = {(int)pa[0], (int)pa[1], (int)pa[2], (int)pa[3]};
-        v4i vb = {(int)pb[0], (int)pb[1], (int)pb[2], (int)pb[3]};
-        *(v4i*)(frag + ((kb * 2 + g) * 16 + m) * 16) = va;
-        *(v4i*)(frag + ((kb * 2 + g) * 16 + 8 + m) * 16) = vb;
-        // 16-element sums split into 6-bit lo / signed hi
-        const int64_t sbk = G >> 4, s16 = G & 15;
-        xs16[(sbk * 32 + m) * 16 + s16] = (int8_t)(sa & 63);
-        xs16[(sbk * 32 + 16 + m) * 16 + s16] = (int8_t)(sa >> 6);
-        xs16[(sbk * 32 + 8 + m) * 16 + s16] = (int8_t)(sb & 63);
-        xs16[(sbk * 32 + 24 + m) * 16 + s16] = (int8_t)(sb >> 6);
-        // 32-element sums from the partner group
-        const int sa2 = sa + __shfl_xor(sa, 1, 64), sb2 = sb + __shfl_xor(sb, 1, 64);
-        if (!(G & 1)) {
-            const int64_t j = (G >> 1) & 7;
-            xs32[(sbk * 32 + m) * 8 + j] = (int8_t)(sa2 & 63);
-            xs32[(sbk * 32 + 16 + m) * 8 + j] = (int8_t)(sa2 >> 6);
-            xs32[(sbk * 32 + 8 + m) * 8 + j] = (int8_t)(sb2 & 63);
-            xs32[(sbk * 32 + 24 + m) * 8 + j] = (int8_t)(sb2 >> 6);
-        }
+    }
+    float mx = fmaxf(fmaxf(fabsf(v[0]), fabsf(v[1])), fmaxf(fabsf(v[2]), fabsf(v[3])));
+#pragma unroll
+    for (int o = 32; o > 0; o >>= 1) mx = fmaxf(mx, __shfl_xor(mx, o, 64));
+    const float q = mx > 0.f ? 127.f / mx : 0.f;
+    if (l == 0) scale[sb * 8 + m] = mx > 0.f ? mx / 127.f : 0.f;
+    int sa = 0, sbb = 0;
+    uint32_t pa = 0, pb = 0;
+#pragma unroll
+    for (int t = 0; t < 4; ++t) {
+        const float y = v[t] * q;
+        const float a = rintf(y);
+        float bf = rintf((y - a) * 256.f);
+        bf = fminf(fmaxf(bf, -127.f), 127.f);
+        const int ai = (int)a, bi = (int)bf;
+        sa += ai;
+        sbb += bi;
+        pa |= (uint32_t)(ai & 0xFF) << (8 * t);
+        pb |= (uint32_t)(bi & 0xFF) << (8 * t);
+    }
+    // fragment bytes: element 4l+t of the super-block sits in 32-block
+    // kb = 8 sb + l/8, half (l%8)/4, byte 4(l%4) + t
+    const int64_t kb = sb * 8 + (l >> 3);
+    const int half = (l & 7) >> 2, byte = 4 * (l & 3);
+    *(uint32_t*)(frag + ((kb * 2 + half) * 16 + m) * 16 + byte) = pa;
+    *(uint32_t*)(frag + ((kb * 2 + half) * 16 + 8 + m) * 16 + byte) = pb;
+    // 16-element sums (4 lanes), split into 6-bit lo / signed hi
+#pragma unroll
+    for (int o = 1; o < 4; o <<= 1) {
+        sa += __shfl_xor(sa, o, 64);
+        sbb += __shfl_xor(sbb, o, 64);
+    }
+    if ((l & 3) == 0) {
+        const int s16 = l >> 2;
+        xs16[(sb * 32 + m) * 16 + s16] = (int8_t)(sa & 63);
+        xs16[(sb * 32 + 16 + m) * 16 + s16] = (int8_t)(sa >> 6);
+        xs16[(sb * 32 + 8 + m) * 16 + s16] = (int8_t)(sbb & 63);
+        xs16[(sb * 32 + 24 + m) * 16 + s16] = (int8_t)(sbb >> 6);
+    }
+    // 32-element sums (8 lanes)
+    sa += __shfl_xor(sa, 4, 64);
+    sbb += __shfl_xor(sbb, 4, 64);
+    if ((l & 7) == 0) {
+        const int j = l >> 3;
+        xs32[(sb * 32 + m) * 8 + j] = (int8_t)(sa & 63);
+        xs32[(sb * 32 + 16 + m) * 8 + j] = (int8_t)(sa >> 6);
+        xs32[(sb * 32 + 8 + m) * 8 + j] = (int8_t)(sbb & 63);
+        xs32[(sb * 32 + 24 + m) * 8 + j] = (int8_t)(sbb >> 6);
     }
 }
 
@@ -373,9 +380,8 @@ hipError_t launch_xq_prep(hipStream_t st, const float* x, int64_t ldx, const flo
     int8_t* xs32 = xq + K * 16;
     int8_t* xs16 = xs32 + K;
     float* scale = (float*)(xs16 + K * 2);
-    const size_t lds = (size_t)K * sizeof(float);
-    hipLaunchKernelGGL(k_xq_prep, dim3(8), dim3(256), lds, st, x, ldx, normw, eps, K, (int)M, frag,
-                       xs32, xs16, scale);
+    hipLaunchKernelGGL(k_xq_prep, dim3((unsigned)(K / 256), 8), dim3(64), 0, st, x, ldx, normw, eps,
+                       K, (int)M, frag, xs32, xs16, scale);
     return hipGetLastError();
 }
 

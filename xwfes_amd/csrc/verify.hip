@@ -475,8 +475,11 @@ int ftx_accept(ftx_ctx* ctx, const ftx_accept_args* a) {
     const size_t off_out = off_p + (((size_t)V * 8 + 255) & ~(size_t)255);
     const size_t off_small = off_out + (((size_t)(M + 2) * 4 + 255) & ~(size_t)255);
     const size_t small_b = 8 + 8 + (size_t)M * 12 + 64;
+    const size_t off_rs = off_small + ((small_b + 255) & ~(size_t)255);  // row-stat chunks
+    const size_t off_b = off_rs + ((row_stats_scratch_bytes(std::max<int64_t>(M, 1), V) + 255) &
+                                   ~(size_t)255);
     uint8_t* ws;
-    int rc = ftx_workspace(ctx, off_small + small_b, (void**)&ws);
+    int rc = ftx_workspace(ctx, off_b + 256, (void**)&ws);
     if (rc) return rc;
     uint8_t* pin;
     rc = ftx_pinned(ctx, small_b + (size_t)(M + 2) * 4 + 64, (void**)&pin);
@@ -501,8 +504,10 @@ int ftx_accept(ftx_ctx* ctx, const ftx_accept_args* a) {
     FTX_HIP(ctx, hipMemcpyAsync(d_small, pin, small_b, hipMemcpyHostToDevice, st));
     RowStats* stats = (RowStats*)ws;
     int tk = tr_begin(ctx);
-    FTX_HIP(ctx, launch_row_stats(st, a->base_row, 1, V, a->temp, stats));
-    if (M > 0) FTX_HIP(ctx, launch_row_stats(st, a->rows, M, V, a->temp, stats + 1));
+    const int with_sum = a->mode != FTX_ACCEPT_GREEDY;
+    FTX_HIP(ctx, launch_row_stats(st, a->base_row, 1, V, a->temp, with_sum, ws + off_rs, stats));
+    if (M > 0)
+        FTX_HIP(ctx, launch_row_stats(st, a->rows, M, V, a->temp, with_sum, ws + off_rs, stats + 1));
     tr_end(ctx, tk, TK_ROW_STATS, (double)(M + 1) * V * 4);
     AcceptDev ad{};
     ad.base_row = a->base_row;
@@ -521,6 +526,8 @@ int ftx_accept(ftx_ctx* ctx, const ftx_accept_args* a) {
     ad.part = nullptr;
     ad.out = (int32_t*)(ws + off_out);
     ad.margin = (float*)(d_small + 8);
+    ad.brow = (int32_t*)(ws + off_b);
+    ad.bu = (float*)(ws + off_b + 16);
     tk = tr_begin(ctx);
     FTX_HIP(ctx, launch_accept(st, ad));
     tr_end(ctx, tk, TK_ACCEPT, (double)V * 4);
