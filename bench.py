@@ -112,6 +112,9 @@ def main():
     ap.add_argument("--workload", default="llama3-8b-q4km-k8-ctx2048", choices=sorted(WORKLOADS))
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--trace-steps", type=int, default=10)
+    ap.add_argument("--copy-calibration", type=int, default=0, metavar="MIB",
+                    help="before the timed steps, copy MIB MiB device-to-device three times "
+                         "(a copy of known size for scaling hardware byte counters)")
     args = ap.parse_args()
     if args.gpus != 1:
         print("bench.py measures one GPU: the verify step runs on a single MI355X and this "
@@ -123,6 +126,15 @@ def main():
     cfg, ctx_len, M, temp = W["cfg"], W["ctx"], W["M"], W["temp"]
     V = cfg["vocab"]
     ctx = ftx.Context(0)
+    if args.copy_calibration > 0:
+        nb = args.copy_calibration << 20
+        src, dst = ctx.buffer(nb), ctx.buffer(nb)
+        ctx.fill_normal(src.ptr, nb // 4, seed=9, std=1.0)
+        for _ in range(3):
+            ctx.copy(dst.ptr, src.ptr, nb)
+        log("copy calibration: 3 device copies of %d bytes" % nb)
+        src.free()
+        dst.free()
     t0 = time.perf_counter()
     tensors = synth.build(ctx, cfg, synth.q4_k_m_mix(cfg), seed=1)
     log("model built in %.1f s (%.3f GB of weights)" % (time.perf_counter() - t0,
