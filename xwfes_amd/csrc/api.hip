@@ -320,15 +320,14 @@ int ftx_matmul(ftx_ctx* ctx, const float* x, int64_t M, int64_t K, const ftx_ten
     float* extra;
     const bool mv = mv_supported(W->dtype, K, M);
     const size_t xqf = (xq_bytes(K) + 255) / 4;
-    const size_t mvf = mv ? xqf + mv_part_floats(N, K, ctx->cu_count) : 0;
+    const size_t mvf = mv ? xqf : 0;
     int rc = stage_xy(ctx, x, (size_t)(M * K), y, (size_t)(M * N), false, mvf, s, &extra);
     if (rc) return rc;
     GemvSeg seg{W->data, W->dtype, W->row_bytes, N, s.y, N};
     if (mv) {
         int8_t* xq = (int8_t*)extra;
         FTX_HIP(ctx, launch_xq_prep(ctx->stream, s.x, K, nullptr, 0.f, K, M, xq));
-        FTX_HIP(ctx, launch_mv(ctx->stream, &seg, 1, xq, K, M, EPI_STORE, extra + xqf,
-                               ctx->cu_count));
+        FTX_HIP(ctx, launch_mv(ctx->stream, &seg, 1, xq, K, M, EPI_STORE, ctx->cu_count));
     } else {
         FTX_HIP(ctx, launch_gemv(ctx->stream, &seg, 1, s.x, K, K, M, EPI_STORE));
     }

@@ -102,7 +102,8 @@ void tr_end(ftx_ctx* ctx, int token, int kind, double bytes);
 hipError_t launch_dequant(hipStream_t st, const uint8_t* W, int dt, int64_t row_bytes,
                           int64_t ncols, int64_t nrows, float* out);
 
-// row-dot GEMV/GEMM segment: y[m*ldy + n] (=|+=) sum_k x[m*ldx + k] W[n,k]
+// row-dot GEMV/GEMM segment: y[m*ldy + n] (=|+=) sum_k x[m*ldx + k] W[n,k];
+// `tiled` marks W as an int8-MFMA tiled copy made with `rpt` rows per tile
 struct GemvSeg {
     const uint8_t* W;
     int dt;
@@ -110,6 +111,8 @@ struct GemvSeg {
     int64_t N;
     float* y;
     int64_t ldy;
+    int tiled = 0;
+    int rpt = 0;
 };
 enum { EPI_STORE = 0, EPI_ACCUM = 1 };
 hipError_t launch_gemv(hipStream_t st, const GemvSeg* segs, int nseg, const float* x,
@@ -130,11 +133,17 @@ size_t xq_bytes(int64_t K);
 hipError_t launch_xq_prep(hipStream_t st, const float* x, int64_t ldx, const float* normw,
                           float eps, int64_t K, int64_t M, int8_t* xq);
 bool mv_supported(int dt, int64_t K, int64_t M);
-// split-sum scratch a launch_mv over `rows` total rows needs
-size_t mv_part_floats(int64_t rows, int64_t K, int cu_count);
+// the SwiGLU epilogue needs the whole contraction in one pass
+bool mv_swiglu_supported(int64_t K);
 enum { EPI_SWIGLU = 2 };
+// tiled copies for the row-dot kernel: rows per tile for an N-row tensor,
+// bytes of the copy, and the re-tiling launch (src in the resident row layout)
+int mv_tile_rows(int64_t N, int cu_count);
+size_t mv_tiled_bytes(int dt, int64_t N, int64_t K, int rpt);
+hipError_t launch_mv_tile(hipStream_t st, const uint8_t* src, int64_t src_row_bytes, int dt,
+                          int64_t N, int64_t K, int rpt, uint8_t* dst);
 hipError_t launch_mv(hipStream_t st, const GemvSeg* segs, int nseg, const int8_t* xq, int64_t K,
-                     int64_t M, int epi, float* part, int cu_count);
+                     int64_t M, int epi, int cu_count);
 
 hipError_t launch_part_reduce(hipStream_t st, const float* part, int S, int64_t N, int64_t M,
                               float* y, int64_t ldy);

@@ -12,10 +12,27 @@
 //     y = sum_sb s_sb * [ d * sum_j sc_j * (A_j . q_j) - dmin * sum_j m_j * X_j ]
 //   where X_j is the sum of the activation limb over sub-block j, formed by
 //   a second MFMA whose B operand is the eight m_j of the super-block.
-// Shapes.  v_mfma_i32_32x32x32_i8: A rows 0..7 = limb a of m = 0..7, rows
-// 8..15 = limb b, rows 16..31 zero; B columns = 32 weight rows; K = 32 = one
-// Q4_K sub-block.  Lane l holds A[l%32][16*(l/32) + s], B[16*(l/32) + s][l%32]
-// and C[8*(r/4) + 4*(l/32) + r%4][l%32] (checked on gfx950).
+//   Q6_K  w = d*sc_s*(q - 32)  (q in 0..63, sub-block s of 16)
+//     y = sum_sb s_sb * d * [ sum_s sc_s * (A_s . q_s)  -  32 * sum_s sc_s * X_s ]
+// Shapes.  v_mfma_i32_32x32x32_i8: lane l holds A[l%32][16*(l/32) + s],
+// B[16*(l/32) + s][l%32] and C[8*(r/4) + 4*(l/32) + r%4][l%32] (checked on
+// gfx950).  B columns = 32 weight rows.  A rows 0..7 = limb a of m = 0..7,
+// rows 8..15 = limb b.
+//   Q4_K: K = 32 = one sub-block; A rows 16..31 only feed C rows 16..31,
+//   which are never read, so those lanes load rows 0..15 again.
+//   Q6_K: K = 32 = two sub-blocks 2p, 2p+1 made block-diagonal: A rows 0..15
+//   carry sub-block 2p on the K slots of 2p and zeros elsewhere, rows 16..31
+//   carry sub-block 2p+1, so C rows 0..15 and 16..31 are the two sub-block
+//   dot products and every output register is used.
+// Work split.  A persistent workgroup of 16 waves per CU walks a strided
+// sequence of output units (a tile of 16 or 32 weight rows; for SwiGLU a gate
+// tile and its up tile) over the whole contraction: wave w takes super-blocks
+// w, w+16, ..., holds its activation operand in registers for the whole
+// launch and streams the weights of the workgroup's tiles through it, the
+// next tile's weights in flight during the current one's arithmetic.  The 16
+// wave partials of a unit are added in wave order in LDS (double-buffered, one
+// barrier per unit), so the result is deterministic, and the epilogue (store,
+// accumulate, or SwiGLU) is applied there.
 #include "ftx_internal.h"
 #include "quant_dev.h"
 
@@ -25,6 +42,14 @@ typedef int v4i __attribute__((ext_vector_type(4)));
 typedef int v16i __attribute__((ext_vector_type(16)));
 
 __device__ __forceinline__ v4i ld16g(const void* p) { return *(const v4i*)p; }
+
+// Materialise eight running sums here: keeps the compiler from re-associating
+// a chain of integer multiply-adds into a tree that holds every MFMA result
+// live at once (which spills).  Emits no instruction.
+__device__ __forceinline__ void reg_fence8(int* v) {
+#pragma unroll
+    for (int r = 0; r < 8; ++r) asm volatile("" : "+v"(v[r]));
+}
 
 // ---------------------------------------------------------------- prep
 // One wave per (256-element super-block sb, activation row m < 8); rows
@@ -118,254 +143,359 @@ __global__ void __launch_bounds__(64) k_xq_prep(const float* __restrict__ x, int
     }
 }
 
-// ---------------------------------------------------------------- Q4_K
+// ---------------------------------------------------------------- row-dot
+
+typedef unsigned v4u __attribute__((ext_vector_type(4)));
 
 struct MvSeg {
     const uint8_t* W;
     int64_t row_bytes;
     int64_t N;
-    int64_t tile0;  // first global tile of the segment
-    int64_t row0;   // first global row of the segment
-    int dt;
+    int64_t tile0;  // first tile of the segment
+    float* y;       // outputs [m][ldy]
+    int64_t ldy;
+    int rpt;        // weight rows per tile: 16 or 32
 };
 
 struct MvArgs {
     MvSeg seg[3];
     int nseg;
-    int64_t tiles;
-    int64_t rows;       // global rows (sum of N)
-    int sb_per_split;
-    int nsb;            // super-blocks per row
+    int64_t tiles;      // all tiles of the launch (SwiGLU: gate tiles then up tiles)
+    int nsb;            // super-blocks per row (a multiple of 16)
+    int M;
+    int epi;            // EPI_STORE, EPI_ACCUM or EPI_SWIGLU (seg 0 gate, seg 1 up -> seg 0 y)
     const int8_t* frag;
     const int8_t* xs32;
     const int8_t* xs16;
     const float* scale;
-    float* part;        // [S][8][rows]
 };
 
-// Q6_K  w = d*sc_s*(q - 32)  (q in 0..63, sub-block s of 16)
-//   y = sum_sb s_sb * d * [ sum_s sc_s * (A_s . q_s)  -  32 * sum_s sc_s * X_s ]
-// with v_mfma_i32_32x32x16_i8 per sub-block (lane l holds 8 slots
-// 8*(l/32) + t) and the second sum as one 32x32x32 MFMA whose B operand is
-// the 16 int8 scales.
-__global__ void __launch_bounds__(256) k_mv_q6k(MvArgs a) {
-    const int lane = threadIdx.x & 63;
-    const int64_t T = (int64_t)blockIdx.x * 4 + (threadIdx.x >> 6);
-    if (T >= a.tiles) return;
+constexpr int MV_WAVES = 16;
+
+
+__device__ __forceinline__ int mv_seg_of(const MvArgs& a, int64_t T) {
     int si = 0;
     while (si + 1 < a.nseg && T >= a.seg[si + 1].tile0) ++si;
-    const MvSeg sg = a.seg[si];
-    if (sg.dt != FTX_Q6_K) return;
-    const int col = lane & 31, g = lane >> 5;
-    const int64_t n_raw = (T - sg.tile0) * 32 + col;
-    const int64_t n = n_raw < sg.N ? n_raw : sg.N - 1;
-    const uint8_t* wrow = sg.W + n * sg.row_bytes;
-    const int64_t nsb = a.nsb;
-    const int sp = blockIdx.y;
-    const int sb0 = sp * a.sb_per_split, sb1 = sb0 + a.sb_per_split;
-    const bool arow = col < 16;
-    float acc[8];
-#pragma unroll
-    for (int r = 0; r < 8; ++r) acc[r] = 0.f;
-    const v4i zero4 = {0, 0, 0, 0};
+    return si;
+}
+
+// one Q4_K super-block for weight row col of a tile: hdr = d, dmin, 12 scale bytes;
+// qs[c] = bytes 32c + 16g .. +15 of the quants (sub-blocks 2c, 2c+1 in the
+// low / high nibbles); af[j] = activation fragment of sub-block j; xv = the
+// eight 32-element limb sums of activation row col (6-bit split rows).
+__device__ __forceinline__ void q4k_block(const v4i hdr, const v4i* qs, const v4i* af, int2 xv,
+                                          float4 s4, int g, float* acc) {
+    const uint32_t S0 = (uint32_t)hdr.y, S1 = (uint32_t)hdr.z, S2 = (uint32_t)hdr.w;
+    const uint32_t sc_lo = S0 & 0x3F3F3F3Fu;
+    const uint32_t mn_lo = S1 & 0x3F3F3F3Fu;
+    const uint32_t sc_hi = (S2 & 0x0F0F0F0Fu) | ((S0 >> 2) & 0x30303030u);
+    const uint32_t mn_hi = ((S2 >> 4) & 0x0F0F0F0Fu) | ((S1 >> 2) & 0x30303030u);
     const v16i zero16 = {};
-    for (int sb = sb0; sb < sb1; ++sb) {
-        v4i ql[4], qh[2];
+    int ai[8];
 #pragma unroll
-        for (int i = 0; i < 4; ++i) ql[i] = ld16g(wrow + (int64_t)sb * 128 + 64 * g + 16 * i);
+    for (int r = 0; r < 8; ++r) ai[r] = 0;
+#pragma unroll
+    for (int j = 0; j < 8; ++j) {
+        const v4u w = __builtin_bit_cast(v4u, qs[j >> 1]);
+        const v4u b = (j & 1) ? (w >> 4) & 0x0F0F0F0Fu : w & 0x0F0F0F0Fu;
+        const v16i c =
+            __builtin_amdgcn_mfma_i32_32x32x32_i8(af[j], __builtin_bit_cast(v4i, b), zero16, 0, 0, 0);
+        const int sc = (int)(((j < 4 ? sc_lo : sc_hi) >> (8 * (j & 3))) & 0xFF);
+#pragma unroll
+        for (int r = 0; r < 8; ++r) ai[r] += __mul24(sc, c[r]);
+        reg_fence8(ai);
+    }
+    const v4i ax = {xv.x, xv.y, 0, 0};
+    const v4i bm = g == 0 ? v4i{(int)mn_lo, (int)mn_hi, 0, 0} : v4i{0, 0, 0, 0};
+    const v16i dm = __builtin_amdgcn_mfma_i32_32x32x32_i8(ax, bm, zero16, 0, 0, 0);
+    const float d = h2f((uint16_t)((uint32_t)hdr.x & 0xFFFF));
+    const float dmin = h2f((uint16_t)((uint32_t)hdr.x >> 16));
+    const float sm[4] = {s4.x, s4.y, s4.z, s4.w};
+#pragma unroll
+    for (int r = 0; r < 8; ++r) {
+        const int mins = dm[r] + 64 * dm[r + 8];
+        acc[r] += sm[r & 3] * (d * (float)ai[r] - dmin * (float)mins);
+    }
+}
+
+
+// Q6_K quant word h (elements 8g + 4h .. +3) of sub-block s from the planar
+// device layout: qlw = this lane's 64 low-nibble bytes [c][a][b][2 words],
+// qhw = its 32 high-bit bytes [c][b][2 words]
+__device__ __forceinline__ uint32_t q6k_word(const uint32_t* qlw, const uint32_t* qhw, int s,
+                                             int h) {
+    const int c = s >> 3, k = (s & 7) >> 1, b = s & 1;
+    const uint32_t L = qlw[8 * c + 4 * (k & 1) + 2 * b + h];
+    const uint32_t H = qhw[4 * c + 2 * b + h];
+    const uint32_t lo = (k >> 1) ? (L >> 4) & 0x0F0F0F0Fu : L & 0x0F0F0F0Fu;
+    const uint32_t hi = ((H >> (2 * k)) & 0x03030303u) << 4;
+    return lo | hi;
+}
+
+// one Q6_K super-block: ql/qh as q6k_word, scv = the 16 int8 scales, x8[p] =
+// 8 activation bytes of sub-block 2p + (col >= 16) (elements 8g .. 8g+7)
+__device__ __forceinline__ void q6k_block(const v4i* ql, const v4i* qh, const v4i scv, float d,
+                                          const long* x8, const v4i ax, float4 s4, int col, int g,
+                                          float* acc) {
+    const uint32_t* qlw = (const uint32_t*)ql;
+    const uint32_t* qhw = (const uint32_t*)qh;
+    const uint32_t* scw = (const uint32_t*)&scv;
+    const v16i zero16 = {};
+    const bool lower = col < 16;
+    int ai[8];
+#pragma unroll
+    for (int r = 0; r < 8; ++r) ai[r] = 0;
+#pragma unroll
+    for (int p = 0; p < 8; ++p) {
+        const int s0 = 2 * p, s1 = 2 * p + 1;
+        const v4i b = {(int)q6k_word(qlw, qhw, s0, 0), (int)q6k_word(qlw, qhw, s0, 1),
+                       (int)q6k_word(qlw, qhw, s1, 0), (int)q6k_word(qlw, qhw, s1, 1)};
+        const int xl = (int)(uint32_t)((uint64_t)x8[p]), xh = (int)(uint32_t)((uint64_t)x8[p] >> 32);
+        const v4i af = lower ? v4i{xl, xh, 0, 0} : v4i{0, 0, xl, xh};
+        const v16i c = __builtin_amdgcn_mfma_i32_32x32x32_i8(af, b, zero16, 0, 0, 0);
+        const int sc0 = (int)(int8_t)((scw[s0 >> 2] >> (8 * (s0 & 3))) & 0xFF);
+        const int sc1 = (int)(int8_t)((scw[s1 >> 2] >> (8 * (s1 & 3))) & 0xFF);
+#pragma unroll
+        for (int r = 0; r < 8; ++r) ai[r] += __mul24(sc0, c[r]) + __mul24(sc1, c[r + 8]);
+        reg_fence8(ai);
+    }
+    const v4i bs = g == 0 ? scv : v4i{0, 0, 0, 0};
+    const v16i dm = __builtin_amdgcn_mfma_i32_32x32x32_i8(ax, bs, zero16, 0, 0, 0);
+    const float sm[4] = {s4.x, s4.y, s4.z, s4.w};
+#pragma unroll
+    for (int r = 0; r < 8; ++r) {
+        const int corr = dm[r] + 64 * dm[r + 8];
+        acc[r] += sm[r & 3] * (d * (float)(ai[r] - 32 * corr));
+    }
+}
+
+
+// bytes per row and super-block
+template <int DT>
+constexpr int mv_bpr() { return DT == FTX_Q4_K ? 144 : 210; }
+
+// weights of one (row, super-block): Q4_K hdr + 4 quant words, Q6_K 4 QL
+// words, 2 QH words, scales and d
+template <int DT>
+struct MvW {
+    v4i w[DT == FTX_Q4_K ? 5 : 7];
+    uint16_t d;
+};
+
+// Byte offsets of a lane's chunks within one (tile, super-block).
+// Row layout (GGUF Q4_K rows; the planar Q6_K device rows): `base` is the
+// lane's weight row.  Tiled layout: `base` is the tile and the R-row block of
+// a super-block is laid out so that every load is one contiguous run over the
+// lanes (li = r + R*g, r = lane row within the tile):
+//   Q4_K  QS [c 4][li 2R][16 B] | HDR [r R][16 B]                  (144 R B)
+//   Q6_K  QL [i 4][li][16 B] | QH [i 2][li][16 B] | SC [r][16 B] | D [r][2 B]
+//                                                                 (210 R B)
+template <int DT, bool TILED>
+__device__ __forceinline__ void mv_load(MvW<DT>& o, const uint8_t* base, int64_t nsb, int sb,
+                                        int g, int r, int li, int R) {
+    if constexpr (TILED) {
+        const uint8_t* blk = base + (int64_t)sb * R * mv_bpr<DT>();
+        if constexpr (DT == FTX_Q4_K) {
+#pragma unroll
+            for (int c = 0; c < 4; ++c) o.w[1 + c] = ld16g(blk + c * R * 32 + li * 16);
+            o.w[0] = ld16g(blk + 4 * R * 32 + r * 16);
+            o.d = 0;
+        } else {
+#pragma unroll
+            for (int i = 0; i < 6; ++i) o.w[i] = ld16g(blk + i * R * 32 + li * 16);
+            o.w[6] = ld16g(blk + 6 * R * 32 + r * 16);
+            o.d = *(const uint16_t*)(blk + 6 * R * 32 + R * 16 + r * 2);
+        }
+    } else if constexpr (DT == FTX_Q4_K) {
+        const uint8_t* blk = base + (int64_t)sb * 144;
+        o.w[0] = ld16g(blk);
+#pragma unroll
+        for (int c = 0; c < 4; ++c) o.w[1 + c] = ld16g(blk + 16 + 32 * c + 16 * g);
+        o.d = 0;
+    } else {
+        // planes: QL 128 B, QH 64 B, SC 16 B, D 2 B per super-block
+#pragma unroll
+        for (int i = 0; i < 4; ++i) o.w[i] = ld16g(base + (int64_t)sb * 128 + 64 * g + 16 * i);
 #pragma unroll
         for (int i = 0; i < 2; ++i)
-            qh[i] = ld16g(wrow + nsb * 128 + (int64_t)sb * 64 + 32 * g + 16 * i);
-        const v4i scv = ld16g(wrow + nsb * 192 + (int64_t)sb * 16);
-        const float d = h2f(*(const uint16_t*)(wrow + nsb * 208 + (int64_t)sb * 2));
-        const uint32_t* qlw = (const uint32_t*)ql;  // 16 dwords: [c][a][b][2]
-        const uint32_t* qhw = (const uint32_t*)qh;  // 8 dwords: [c][b][2]
-        const uint32_t* scw = (const uint32_t*)&scv;
-        int ai[8];
-#pragma unroll
-        for (int r = 0; r < 8; ++r) ai[r] = 0;
-#pragma unroll
-        for (int s = 0; s < 16; ++s) {
-            const int c = s >> 3, k = (s & 7) >> 1, b = s & 1;
-            long af = 0;
-            if (arow)
-                af = *(const long*)(a.frag +
-                                    ((((int64_t)sb * 8 + (s >> 1)) * 2 + b) * 16 + col) * 16 +
-                                    8 * g);
-            uint32_t v[2];
-#pragma unroll
-            for (int h = 0; h < 2; ++h) {
-                const uint32_t L = qlw[8 * c + 4 * (k & 1) + 2 * b + h];
-                const uint32_t H = qhw[4 * c + 2 * b + h];
-                const uint32_t lo = (k >> 1) ? (L >> 4) & 0x0F0F0F0Fu : L & 0x0F0F0F0Fu;
-                const uint32_t hi = ((H >> (2 * k)) & 0x03030303u) << 4;
-                v[h] = lo | hi;
-            }
-            const long bf = (long)((uint64_t)v[0] | ((uint64_t)v[1] << 32));
-            const v16i cm = __builtin_amdgcn_mfma_i32_32x32x16_i8(af, bf, zero16, 0, 0, 0);
-            const int sc = (int)(int8_t)((scw[s >> 2] >> (8 * (s & 3))) & 0xFF);
-#pragma unroll
-            for (int r = 0; r < 8; ++r) ai[r] += sc * cm[r];
-            // keep at most two sub-blocks in flight (bounds the accumulators)
-            if (s & 1) __builtin_amdgcn_sched_barrier(0);
-        }
-        v4i ax = zero4, bs = zero4;
-        if (g == 0) {
-            ax = ld16g(a.xs16 + ((int64_t)sb * 32 + col) * 16);
-            bs = scv;
-        }
-        const v16i dm = __builtin_amdgcn_mfma_i32_32x32x32_i8(ax, bs, zero16, 0, 0, 0);
-        const float4 s4 = *(const float4*)(a.scale + (int64_t)sb * 8 + 4 * g);
-        const float sm[4] = {s4.x, s4.y, s4.z, s4.w};
-#pragma unroll
-        for (int r = 0; r < 8; ++r) {
-            const int corr = dm[r] + 64 * dm[r + 8];
-            acc[r] += sm[r & 3] * (d * (float)(ai[r] - 32 * corr));
-        }
+            o.w[4 + i] = ld16g(base + nsb * 128 + (int64_t)sb * 64 + 32 * g + 16 * i);
+        o.w[6] = ld16g(base + nsb * 192 + (int64_t)sb * 16);
+        o.d = *(const uint16_t*)(base + nsb * 208 + (int64_t)sb * 2);
     }
-    float* out = a.part + (int64_t)sp * 8 * a.rows + sg.row0;
-    if (n_raw < sg.N) {
+}
+
+// Re-tiling copy: thread (tile, super-block, li) moves its lane's chunks from
+// the row layout to the tiled layout (rows past N repeat row N - 1).
+template <int DT>
+__global__ void __launch_bounds__(256) k_mv_tile(const uint8_t* __restrict__ src, int64_t rb,
+                                                 int64_t N, int64_t nsb, int R, int64_t ntiles,
+                                                 uint8_t* __restrict__ dst) {
+    const int64_t t = (int64_t)blockIdx.x * 256 + threadIdx.x;
+    const int64_t per = nsb * 2 * R;
+    if (t >= ntiles * per) return;
+    const int64_t tl = t / per;
+    const int sb = (int)((t % per) / (2 * R));
+    const int li = (int)(t % (2 * R)), r = li % R, g = li / R;
+    int64_t n = tl * R + r;
+    if (n >= N) n = N - 1;
+    MvW<DT> o;
+    mv_load<DT, false>(o, src + n * rb, nsb, sb, g, r, li, R);
+    uint8_t* blk = dst + (tl * nsb + sb) * R * mv_bpr<DT>();
+    if constexpr (DT == FTX_Q4_K) {
 #pragma unroll
-        for (int r = 0; r < 4; ++r) {
-            const int m = 4 * g + r;
-            out[(int64_t)m * a.rows + n_raw] = acc[r] + acc[r + 4] * (1.f / 256.f);
+        for (int c = 0; c < 4; ++c) *(v4i*)(blk + c * R * 32 + li * 16) = o.w[1 + c];
+        if (g == 0) *(v4i*)(blk + 4 * R * 32 + r * 16) = o.w[0];
+    } else {
+#pragma unroll
+        for (int i = 0; i < 6; ++i) *(v4i*)(blk + i * R * 32 + li * 16) = o.w[i];
+        if (g == 0) {
+            *(v4i*)(blk + 6 * R * 32 + r * 16) = o.w[6];
+            *(uint16_t*)(blk + 6 * R * 32 + R * 16 + r * 2) = o.d;
         }
     }
 }
 
-__global__ void __launch_bounds__(256) k_mv_q4k(MvArgs a) {
-    const int lane = threadIdx.x & 63;
-    const int64_t T = (int64_t)blockIdx.x * 4 + (threadIdx.x >> 6);
-    if (T >= a.tiles) return;
-    int si = 0;
-    while (si + 1 < a.nseg && T >= a.seg[si + 1].tile0) ++si;
-    const MvSeg sg = a.seg[si];
-    if (sg.dt != FTX_Q4_K) return;
-    const int col = lane & 31, g = lane >> 5;
-    const int64_t n_raw = (T - sg.tile0) * 32 + col;
-    const int64_t n = n_raw < sg.N ? n_raw : sg.N - 1;
-    const uint8_t* wrow = sg.W + n * sg.row_bytes;
-    const int sp = blockIdx.y;
-    const int sb0 = sp * a.sb_per_split, sb1 = sb0 + a.sb_per_split;
-    const bool arow = col < 16;
-    float acc[8];
+// activation operand of one super-block for lane (col, g)
+template <int DT>
+struct MvX {
+    v4i af[DT == FTX_Q4_K ? 8 : 1];
+    long x8[DT == FTX_Q4_K ? 1 : 8];
+    v4i ax;
+    int2 xv;
+    float4 s4;
+};
+
+template <int DT>
+__device__ __forceinline__ void mv_load_x(MvX<DT>& x, const MvArgs& a, int sb, int col, int g) {
+    if constexpr (DT == FTX_Q4_K) {
+        const int8_t* fp = a.frag + (((int64_t)sb * 16 + g) * 16 + (col & 15)) * 16;
 #pragma unroll
-    for (int r = 0; r < 8; ++r) acc[r] = 0.f;
-    const v4i zero4 = {0, 0, 0, 0};
-    const v16i zero16 = {};
-    for (int sb = sb0; sb < sb1; ++sb) {
-        const uint8_t* blk = wrow + (int64_t)sb * 144;
-        const v4i hdr = ld16g(blk);
-        v4i qs[4];
+        for (int j = 0; j < 8; ++j) x.af[j] = ld16g(fp + 512 * j);
+        x.xv = *(const int2*)(a.xs32 + ((int64_t)sb * 32 + col) * 8);
+    } else {
+        const int8_t* fp = a.frag + (int64_t)sb * 4096 + (col >> 4) * 256 + (col & 15) * 16 + 8 * g;
 #pragma unroll
-        for (int gg = 0; gg < 4; ++gg) qs[gg] = ld16g(blk + 16 + 32 * gg + 16 * g);
-        v4i af[8];
-#pragma unroll
-        for (int j = 0; j < 8; ++j)
-            af[j] = arow ? ld16g(a.frag + ((((int64_t)sb * 8 + j) * 2 + g) * 16 + col) * 16)
-                         : zero4;
-        v4i ax = zero4;
-        if (g == 0) {
-            const int2 t = *(const int2*)(a.xs32 + ((int64_t)sb * 32 + col) * 8);
-            ax.x = t.x;
-            ax.y = t.y;
+        for (int p = 0; p < 8; ++p) x.x8[p] = *(const long*)(fp + 512 * p);
+        x.ax = ld16g(a.xs16 + ((int64_t)sb * 32 + col) * 16);
+    }
+    x.s4 = *(const float4*)(a.scale + (int64_t)sb * 8 + 4 * g);
+}
+
+template <int DT>
+__device__ __forceinline__ void mv_block(const MvW<DT>& w, const MvX<DT>& x, int col, int g,
+                                         float* acc) {
+    if constexpr (DT == FTX_Q4_K)
+        q4k_block(w.w[0], w.w + 1, x.af, x.xv, x.s4, g, acc);
+    else
+        q6k_block(w.w, w.w + 4, w.w[6], h2f(w.d), x.x8, x.ax, x.s4, col, g, acc);
+}
+
+// grid = persistent workgroups (<= units); block = 16 waves;
+// LDS = 2 slots x tiles per unit x 16 waves x 256 floats
+template <int DT, bool TILED>
+__global__ void __launch_bounds__(1024) k_mv(MvArgs a) {
+    __shared__ float part[2][2][MV_WAVES][256];  // [slot][tile of unit][wave][m * 32 + col]
+    const int w = threadIdx.x >> 6, lane = threadIdx.x & 63, col = lane & 31, g = lane >> 5;
+    const bool pair = a.epi == EPI_SWIGLU;
+    const int tpu = pair ? 2 : 1;                     // tiles per unit
+    const int64_t units = pair ? a.tiles / 2 : a.tiles;
+    const int64_t G = gridDim.x;
+    const int64_t my_units = units > blockIdx.x ? (units - blockIdx.x + G - 1) / G : 0;
+    const int64_t nseq = my_units * tpu;              // this workgroup's tile sequence
+    // tile q of the sequence: unit blockIdx.x + (q / tpu) * G, gate or up
+    auto tile_of = [&](int64_t q) -> int64_t {
+        const int64_t u = blockIdx.x + (q / tpu) * G;
+        return (q % tpu) ? units + u : u;
+    };
+    const int64_t nsb = a.nsb;
+    // lane base of tile q: its weight row (row layout) or the tile (tiled)
+    auto load = [&](MvW<DT>& o, int64_t q, int sb) {
+        const int64_t T = tile_of(q);
+        const MvSeg& sg = a.seg[mv_seg_of(a, T)];
+        const int R = sg.rpt, r = col & (R - 1);
+        const uint8_t* base;
+        if constexpr (TILED) {
+            base = sg.W + (T - sg.tile0) * nsb * R * mv_bpr<DT>();
+        } else {
+            int64_t n = (T - sg.tile0) * R + r;
+            if (n >= sg.N) n = sg.N - 1;
+            base = sg.W + n * sg.row_bytes;
         }
-        const uint32_t S0 = (uint32_t)hdr.y, S1 = (uint32_t)hdr.z, S2 = (uint32_t)hdr.w;
-        const uint32_t sc_lo = S0 & 0x3F3F3F3Fu;
-        const uint32_t mn_lo = S1 & 0x3F3F3F3Fu;
-        const uint32_t sc_hi = (S2 & 0x0F0F0F0Fu) | ((S0 >> 2) & 0x30303030u);
-        const uint32_t mn_hi = ((S2 >> 4) & 0x0F0F0F0Fu) | ((S1 >> 2) & 0x30303030u);
-        int ai[8];
-#pragma unroll
-        for (int r = 0; r < 8; ++r) ai[r] = 0;
-#pragma unroll
-        for (int j = 0; j < 8; ++j) {
-            const v4i w = qs[j >> 1];
-            v4i b;
-            if (j & 1) {
-                b.x = (int)(((uint32_t)w.x >> 4) & 0x0F0F0F0Fu);
-                b.y = (int)(((uint32_t)w.y >> 4) & 0x0F0F0F0Fu);
-                b.z = (int)(((uint32_t)w.z >> 4) & 0x0F0F0F0Fu);
-                b.w = (int)(((uint32_t)w.w >> 4) & 0x0F0F0F0Fu);
+        mv_load<DT, TILED>(o, base, nsb, sb, g, r, r + R * g, R);
+    };
+    // waves own super-blocks w + 16 k: rows of more than 16 super-blocks
+    // walk the tile sequence once per round, later rounds adding to the
+    // output (SwiGLU needs its sums whole: one round only)
+    const int rounds = a.nsb / MV_WAVES;
+    for (int rd = 0; rd < rounds; ++rd) {
+        const int sb = w + MV_WAVES * rd;
+        MvX<DT> x;
+        mv_load_x<DT>(x, a, sb, col, g);
+        MvW<DT> cur, nxt;
+        // Q4_K: the next tile's weights in flight during this tile's
+        // arithmetic (the last tile re-reads its own block); Q6_K's larger
+        // blocks do not fit twice in the register budget
+        constexpr bool PF = DT == FTX_Q4_K;
+        if (PF && nseq > 0) load(cur, 0, sb);
+        for (int64_t q = 0; q < nseq; ++q) {
+            if constexpr (PF) {
+                __builtin_amdgcn_sched_barrier(0);
+                load(nxt, q + 1 < nseq ? q + 1 : q, sb);
+                __builtin_amdgcn_sched_barrier(0);
             } else {
-                b.x = (int)((uint32_t)w.x & 0x0F0F0F0Fu);
-                b.y = (int)((uint32_t)w.y & 0x0F0F0F0Fu);
-                b.z = (int)((uint32_t)w.z & 0x0F0F0F0Fu);
-                b.w = (int)((uint32_t)w.w & 0x0F0F0F0Fu);
+                load(cur, q, sb);
             }
-            const v16i c = __builtin_amdgcn_mfma_i32_32x32x32_i8(af[j], b, zero16, 0, 0, 0);
-            const int sc = (int)(((j < 4 ? sc_lo : sc_hi) >> (8 * (j & 3))) & 0xFF);
+            float acc[8];
 #pragma unroll
-            for (int r = 0; r < 8; ++r) ai[r] += sc * c[r];
-        }
-        v4i bm = zero4;
-        if (g == 0) {
-            bm.x = (int)mn_lo;
-            bm.y = (int)mn_hi;
-        }
-        const v16i dm = __builtin_amdgcn_mfma_i32_32x32x32_i8(ax, bm, zero16, 0, 0, 0);
-        const float d = h2f((uint16_t)((uint32_t)hdr.x & 0xFFFF));
-        const float dmin = h2f((uint16_t)((uint32_t)hdr.x >> 16));
-        // activation scales of this super-block for m = 4g .. 4g+3
-        const float4 s4 = *(const float4*)(a.scale + (int64_t)sb * 8 + 4 * g);
-        const float sm[4] = {s4.x, s4.y, s4.z, s4.w};
+            for (int r = 0; r < 8; ++r) acc[r] = 0.f;
+            mv_block<DT>(cur, x, col, g, acc);
+            const int slot = (int)((q / tpu) & 1), ti = (int)(q % tpu);
+            float* pp = &part[slot][ti][w][col];
 #pragma unroll
-        for (int r = 0; r < 8; ++r) {
-            const int mins = dm[r] + 64 * dm[r + 8];
-            acc[r] += sm[r & 3] * (d * (float)ai[r] - dmin * (float)mins);
-        }
-    }
-    // rows 4g+r (limb a, r < 4) and 8+4g+r (limb b) of activation m = 4g + r
-    float* out = a.part + (int64_t)sp * 8 * a.rows + sg.row0;
-    if (n_raw < sg.N) {
+            for (int r = 0; r < 4; ++r) pp[(4 * g + r) * 32] = acc[r] + acc[r + 4] * (1.f / 256.f);
+            if constexpr (PF) cur = nxt;
+            if (ti != tpu - 1) continue;
+            __syncthreads();
+            // unit complete: threads (m, c) add the 16 wave partials in order
+            const int t = threadIdx.x;
+            const int64_t T = tile_of(q - ti);
+            const MvSeg& sg = a.seg[mv_seg_of(a, T)];
+            const int rpt = sg.rpt;
+            if (t < 8 * rpt) {
+                const int m = t / rpt, c = t % rpt;
+                const int64_t n = (T - sg.tile0) * rpt + c;
+                if (m < a.M && n < sg.N) {
+                    float v = 0.f;
 #pragma unroll
-        for (int r = 0; r < 4; ++r) {
-            const int m = 4 * g + r;
-            out[(int64_t)m * a.rows + n_raw] = acc[r] + acc[r + 4] * (1.f / 256.f);
+                    for (int ww = 0; ww < MV_WAVES; ++ww) v += part[slot][0][ww][m * 32 + c];
+                    float* yp = sg.y + (int64_t)m * sg.ldy + n;
+                    if (pair) {
+                        float u = 0.f;
+#pragma unroll
+                        for (int ww = 0; ww < MV_WAVES; ++ww) u += part[slot][1][ww][m * 32 + c];
+                        // src/engine.cpp:271-273: g / (1 + exp(-g)) * u
+                        *yp = v / (1.f + expf(-v)) * u;
+                    } else if (rd > 0 || a.epi == EPI_ACCUM) {
+                        *yp += v;
+                    } else {
+                        *yp = v;
+                    }
+                }
+            }
         }
     }
 }
 
-// Sum the S split partials in order and apply the epilogue.
-struct RedSeg {
-    float* y;
-    int64_t ldy;
-    int64_t row0, N;
-};
-struct RedArgs {
-    const float* part;
-    int S;
-    int64_t rows;
-    int M;
-    int epi;  // EPI_STORE, EPI_ACCUM, or 2 = SwiGLU (seg 0 gate, seg 1 up -> seg 0 y)
-    RedSeg seg[3];
-    int nseg;
-};
-
-__global__ void __launch_bounds__(256) k_mv_reduce(RedArgs a) {
+// y[m*ldy + n] += sum_s part[s][m][n] in split order (ffn_down's splits)
+__global__ void __launch_bounds__(256) k_part_reduce(const float* __restrict__ part, int S,
+                                                     int64_t N, float* __restrict__ y,
+                                                     int64_t ldy) {
     const int64_t t = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
     const int m = blockIdx.y;
-    if (m >= a.M) return;
-    if (a.epi == 2) {
-        const int64_t N = a.seg[0].N;
-        if (t >= N) return;
-        float g = 0.f, u = 0.f;
-        for (int s = 0; s < a.S; ++s) {
-            const float* p = a.part + ((int64_t)s * 8 + m) * a.rows;
-            g += p[a.seg[0].row0 + t];
-            u += p[a.seg[1].row0 + t];
-        }
-        // src/engine.cpp:271-273: g / (1 + exp(-g)) * u
-        a.seg[0].y[(int64_t)m * a.seg[0].ldy + t] = g / (1.f + expf(-g)) * u;
-        return;
-    }
-    if (t >= a.rows) return;
-    int si = 0;
-    while (si + 1 < a.nseg && t >= a.seg[si + 1].row0) ++si;
+    if (t >= N) return;
     float v = 0.f;
-    for (int s = 0; s < a.S; ++s) v += a.part[((int64_t)s * 8 + m) * a.rows + t];
-    float* yp = a.seg[si].y + (int64_t)m * a.seg[si].ldy + (t - a.seg[si].row0);
-    *yp = a.epi == EPI_ACCUM ? *yp + v : v;
+    for (int s = 0; s < S; ++s) v += part[((int64_t)s * 8 + m) * N + t];
+    y[(int64_t)m * ldy + t] += v;
 }
 
 }  // namespace
@@ -385,6 +515,8 @@ hipError_t launch_xq_prep(hipStream_t st, const float* x, int64_t ldx, const flo
     return hipGetLastError();
 }
 
+bool mv_swiglu_supported(int64_t K) { return K == 256 * MV_WAVES; }
+
 bool mv_supported(int dt, int64_t K, int64_t M) {
     return (dt == FTX_Q4_K || dt == FTX_Q6_K) && M >= 1 && M <= 8 && K % 4096 == 0 &&
            K <= 16384;
@@ -393,80 +525,92 @@ bool mv_supported(int dt, int64_t K, int64_t M) {
 // y[m*ldy + n] += sum_s part[s][m][n] for n < N, m < M (part rows of 8)
 hipError_t launch_part_reduce(hipStream_t st, const float* part, int S, int64_t N, int64_t M,
                               float* y, int64_t ldy) {
-    RedArgs r{};
-    r.part = part;
-    r.S = S;
-    r.rows = N;
-    r.M = (int)M;
-    r.epi = EPI_ACCUM;
-    r.nseg = 1;
-    r.seg[0] = RedSeg{y, ldy, 0, N};
-    hipLaunchKernelGGL(k_mv_reduce, dim3((unsigned)((N + 255) / 256), (unsigned)M), dim3(256), 0,
-                       st, r);
+    hipLaunchKernelGGL(k_part_reduce, dim3((unsigned)((N + 255) / 256), (unsigned)M), dim3(256), 0,
+                       st, part, S, N, y, ldy);
     return hipGetLastError();
 }
 
-// contraction splits: double until ~8 waves per CU or one super-block each
-static int mv_splits(int64_t tiles, int nsb, int cu_count) {
-    int S = 1;
-    const int64_t want = (int64_t)(cu_count > 0 ? cu_count : 256) * 8;
-    while (S < nsb && tiles * S < want && nsb % (S * 2) == 0) S *= 2;
-    return S;
+int mv_tile_rows(int64_t N, int cu_count) {
+    return (N + 31) / 32 < (cu_count > 0 ? cu_count : 256) ? 16 : 32;
 }
 
-size_t mv_part_floats(int64_t rows, int64_t K, int cu_count) {
-    const int64_t tiles = (rows + 31) / 32;
-    return (size_t)mv_splits(tiles, (int)(K / 256), cu_count) * 8 * (size_t)rows;
+size_t mv_tiled_bytes(int dt, int64_t N, int64_t K, int rpt) {
+    const int64_t bpr = dt == FTX_Q4_K ? 144 : 210;
+    return (size_t)((N + rpt - 1) / rpt * rpt) * (size_t)(K / 256) * (size_t)bpr;
 }
 
-// segs: up to 3 same-K Q4_K weight segments; epi as in RedArgs
+hipError_t launch_mv_tile(hipStream_t st, const uint8_t* src, int64_t src_row_bytes, int dt,
+                          int64_t N, int64_t K, int rpt, uint8_t* dst) {
+    if ((dt != FTX_Q4_K && dt != FTX_Q6_K) || K % 256 || (rpt != 16 && rpt != 32) || N < 1)
+        return hipErrorInvalidValue;
+    const int64_t nsb = K / 256, ntiles = (N + rpt - 1) / rpt;
+    const int64_t threads = ntiles * nsb * 2 * rpt;
+    const dim3 grid((unsigned)((threads + 255) / 256));
+    if (dt == FTX_Q4_K)
+        hipLaunchKernelGGL(k_mv_tile<FTX_Q4_K>, grid, dim3(256), 0, st, src, src_row_bytes, N, nsb,
+                           rpt, ntiles, dst);
+    else
+        hipLaunchKernelGGL(k_mv_tile<FTX_Q6_K>, grid, dim3(256), 0, st, src, src_row_bytes, N, nsb,
+                           rpt, ntiles, dst);
+    return hipGetLastError();
+}
+
+// segs: up to 3 same-K weight segments (Q4_K and / or Q6_K), all in the row
+// layout or all tiled (GemvSeg::tiled, with the tile rows they were tiled
+// with); one launch per dtype over that dtype's segments
 hipError_t launch_mv(hipStream_t st, const GemvSeg* segs, int nseg, const int8_t* xq, int64_t K,
-                     int64_t M, int epi, float* part, int cu_count) {
-    MvArgs a{};
-    a.nseg = nseg;
-    int64_t tiles = 0, rows = 0;
-    bool has4 = false, has6 = false;
-    for (int i = 0; i < nseg; ++i) {
-        a.seg[i].W = segs[i].W;
-        a.seg[i].row_bytes = segs[i].row_bytes;
-        a.seg[i].N = segs[i].N;
-        a.seg[i].tile0 = tiles;
-        a.seg[i].row0 = rows;
-        a.seg[i].dt = segs[i].dt;
-        has4 |= segs[i].dt == FTX_Q4_K;
-        has6 |= segs[i].dt == FTX_Q6_K;
-        tiles += (segs[i].N + 31) / 32;
-        rows += segs[i].N;
+                     int64_t M, int epi, int cu_count) {
+    if (nseg < 1 || nseg > 3 || M < 1 || M > 8 || K % 4096 || K > 16384)
+        return hipErrorInvalidValue;
+    if (epi == EPI_SWIGLU && (nseg != 2 || segs[0].N != segs[1].N || segs[0].dt != segs[1].dt ||
+                              segs[0].rpt != segs[1].rpt || !mv_swiglu_supported(K)))
+        return hipErrorInvalidValue;
+    const bool tiled = segs[0].tiled != 0;
+    for (int i = 0; i < nseg; ++i)
+        if ((segs[i].tiled != 0) != tiled || (tiled && segs[i].rpt != 16 && segs[i].rpt != 32))
+            return hipErrorInvalidValue;
+    const int cus = cu_count > 0 ? cu_count : 256;
+    for (int dt : {FTX_Q4_K, FTX_Q6_K}) {
+        MvArgs a{};
+        int64_t tiles = 0;
+        for (int i = 0; i < nseg; ++i) {
+            if (segs[i].dt != dt) continue;
+            MvSeg& sg = a.seg[a.nseg++];
+            sg.W = segs[i].W;
+            sg.row_bytes = segs[i].row_bytes;
+            sg.N = segs[i].N;
+            sg.tile0 = tiles;
+            sg.y = segs[i].y;
+            sg.ldy = segs[i].ldy;
+            sg.rpt = tiled ? segs[i].rpt : mv_tile_rows(segs[i].N, cus);
+            tiles += (segs[i].N + sg.rpt - 1) / sg.rpt;
+        }
+        if (!a.nseg) continue;
+        a.tiles = tiles;
+        const bool pair = epi == EPI_SWIGLU;
+        const int64_t units = pair ? tiles / 2 : tiles;
+        a.nsb = (int)(K / 256);
+        a.M = (int)M;
+        a.epi = epi;
+        a.frag = xq;
+        a.xs32 = xq + K * 16;
+        a.xs16 = xq + K * 16 + K;
+        a.scale = (const float*)(xq + K * 16 + K + K * 2);
+        const int64_t grid = units < cus ? units : cus;
+        const dim3 gd((unsigned)grid), bd(64 * MV_WAVES);
+        if (dt == FTX_Q4_K) {
+            if (tiled)
+                hipLaunchKernelGGL((k_mv<FTX_Q4_K, true>), gd, bd, 0, st, a);
+            else
+                hipLaunchKernelGGL((k_mv<FTX_Q4_K, false>), gd, bd, 0, st, a);
+        } else {
+            if (tiled)
+                hipLaunchKernelGGL((k_mv<FTX_Q6_K, true>), gd, bd, 0, st, a);
+            else
+                hipLaunchKernelGGL((k_mv<FTX_Q6_K, false>), gd, bd, 0, st, a);
+        }
+        hipError_t e = hipGetLastError();
+        if (e != hipSuccess) return e;
     }
-    a.tiles = tiles;
-    a.rows = rows;
-    const int nsb = (int)(K / 256);
-    const int S = mv_splits(tiles, nsb, cu_count);
-    a.sb_per_split = nsb / S;
-    a.nsb = nsb;
-    a.frag = xq;
-    a.xs32 = xq + K * 16;
-    a.xs16 = xq + K * 16 + K;
-    a.scale = (const float*)(xq + K * 16 + K + K * 2);
-    a.part = part;
-    // each kernel takes the tiles of its dtype; both write disjoint rows
-    const dim3 grid((unsigned)((tiles + 3) / 4), (unsigned)S);
-    if (has4) hipLaunchKernelGGL(k_mv_q4k, grid, dim3(256), 0, st, a);
-    hipError_t e = hipGetLastError();
-    if (e != hipSuccess) return e;
-    if (has6) hipLaunchKernelGGL(k_mv_q6k, grid, dim3(256), 0, st, a);
-    e = hipGetLastError();
-    if (e != hipSuccess) return e;
-    RedArgs r{};
-    r.part = part;
-    r.S = S;
-    r.rows = rows;
-    r.M = (int)M;
-    r.epi = epi;
-    r.nseg = nseg;
-    for (int i = 0; i < nseg; ++i) r.seg[i] = RedSeg{segs[i].y, segs[i].ldy, a.seg[i].row0, segs[i].N};
-    const int64_t span = epi == 2 ? segs[0].N : rows;
-    hipLaunchKernelGGL(k_mv_reduce, dim3((unsigned)((span + 255) / 256), (unsigned)M), dim3(256), 0,
-                       st, r);
-    return hipGetLastError();
+    return hipSuccess;
 }

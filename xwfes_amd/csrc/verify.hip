@@ -22,11 +22,14 @@ struct ftx_model {
     int32_t* depth = nullptr;
     uint32_t* anc = nullptr;
     int64_t* npast = nullptr;
-    // int8-MFMA GEMV operands: activation fragments and split sums
+    // int8-MFMA GEMV activation operand
     int8_t* xq = nullptr;
-    float* mvpart = nullptr;
     // per-layer re-tiled ffn_down copies for the MFMA down kernel (or null)
     std::vector<uint8_t*> down_tiled;
+    // tiled copies for the int8-MFMA row-dot kernel, [layer * LAYER_TENSORS +
+    // tensor] and the LM head last (null where the kernel does not apply)
+    std::vector<uint8_t*> mvt;
+    std::vector<int> mvt_rpt;
     float* downpart = nullptr;
 };
 
@@ -51,10 +54,12 @@ struct ftx_kv {
 static void model_release(ftx_model* m) {
     if (!m) return;
     void* bufs[] = {m->norms, m->x,     m->xn,  m->qkv,   m->att, m->h,     m->part,
-                    m->toks,  m->depth, m->anc, m->npast, m->xq,  m->mvpart};
+                    m->toks,  m->depth, m->anc, m->npast, m->xq};
     for (void* b : bufs)
         if (b) (void)hipFree(b);
     for (uint8_t* b : m->down_tiled)
+        if (b) (void)hipFree(b);
+    for (uint8_t* b : m->mvt)
         if (b) (void)hipFree(b);
     if (m->downpart) (void)hipFree(m->downpart);
     delete m;
@@ -127,10 +132,7 @@ int ftx_model_create(ftx_ctx* ctx, const ftx_model_desc* d, ftx_model** out) {
               dalloc(&m->npast, 1);
     if (ok) {
         const int64_t Kmax = std::max(D, qdim);
-        size_t pf = 0;
-        for (int64_t rows : {m->ldq, D, 2 * d->n_ff, d->vocab})
-            pf = std::max(pf, mv_part_floats(rows, Kmax, ctx->cu_count));
-        ok = dalloc(&m->xq, xq_bytes(Kmax)) && dalloc(&m->mvpart, pf);
+        ok = dalloc(&m->xq, xq_bytes(Kmax));
     }
     // re-tiled ffn_down copies (same bytes, MFMA-friendly order)
     m->down_tiled.assign((size_t)d->n_layer, nullptr);
@@ -150,6 +152,30 @@ int ftx_model_create(ftx_ctx* ctx, const ftx_model_desc* d, ftx_model** out) {
             ok = false;
     }
     if (ok && any_tiled) ok = dalloc(&m->downpart, down_mfma_part_floats(d->n_ff, D, ctx->cu_count));
+    // row-dot projections and the LM head: tiled copies for the MFMA kernel
+    const size_t nmvt = (size_t)(d->n_layer * FTX_LAYER_TENSORS + 1);
+    m->mvt.assign(nmvt, nullptr);
+    m->mvt_rpt.assign(nmvt, 0);
+    for (size_t i = 0; ok && i < nmvt; ++i) {
+        const int t = (int)(i % FTX_LAYER_TENSORS);
+        const bool head = i + 1 == nmvt;
+        if (!head && t != FTX_T_Q && t != FTX_T_K && t != FTX_T_V && t != FTX_T_O &&
+            t != FTX_T_GATE && t != FTX_T_UP)
+            continue;
+        const ftx_tensor* w = head ? (d->output ? d->output : d->tok_embd) : d->layers[i];
+        if (!mv_supported(w->dtype, w->ne[0], 1)) continue;
+        const int rpt = mv_tile_rows(w->nrows, ctx->cu_count);
+        uint8_t* buf = nullptr;
+        if (!dalloc(&buf, mv_tiled_bytes(w->dtype, w->nrows, w->ne[0], rpt))) {
+            ok = false;
+            break;
+        }
+        m->mvt[i] = buf;
+        m->mvt_rpt[i] = rpt;
+        if (launch_mv_tile(ctx->stream, w->data, w->row_bytes, w->dtype, w->nrows, w->ne[0], rpt,
+                           buf) != hipSuccess)
+            ok = false;
+    }
     if (!ok) {
         model_release(m);
         return ftx_fail(ctx, FTX_E_NOMEM, "activation allocation failed");
@@ -348,13 +374,21 @@ int ftx_verify_step(ftx_ctx* ctx, ftx_model* m, ftx_kv* kv, const ftx_verify_arg
     // int8-MFMA path runs when every segment qualifies (the norm is fused
     // into its activation prep); the generic kernels run otherwise.
     auto project = [&](int kind, double bytes, const float* xin, int64_t ldx, const float* normw,
-                       const ftx_tensor* const* ts, GemvSeg* segs, int nseg, int64_t K,
-                       int epi) -> int {
-        if (mv_all(ts, nseg, K, M)) {
+                       const ftx_tensor* const* ts, GemvSeg* segs, int nseg, int64_t K, int epi,
+                       int64_t tix0, const int* tix) -> int {
+        if (mv_all(ts, nseg, K, M) && (epi != EPI_SWIGLU || mv_swiglu_supported(K))) {
+            // the tiled copies when every segment has one
+            bool all = true;
+            for (int i = 0; i < nseg; ++i) all = all && m->mvt[tix0 + tix[i]];
+            for (int i = 0; all && i < nseg; ++i) {
+                segs[i].W = m->mvt[tix0 + tix[i]];
+                segs[i].tiled = 1;
+                segs[i].rpt = m->mvt_rpt[tix0 + tix[i]];
+            }
             TRACED(TK_XQ_PREP, Md * K * f4 + 19.0 * K,
                    launch_xq_prep(st, xin, ldx, normw, eps, K, M, m->xq));
             TRACED(kind, bytes,
-                   launch_mv(st, segs, nseg, m->xq, K, M, epi, m->mvpart, ctx->cu_count));
+                   launch_mv(st, segs, nseg, m->xq, K, M, epi, ctx->cu_count));
             return FTX_OK;
         }
         const float* src = xin;
@@ -375,15 +409,18 @@ int ftx_verify_step(ftx_ctx* ctx, ftx_model* m, ftx_kv* kv, const ftx_verify_arg
     auto seg = [](const ftx_tensor* t, float* y, int64_t ldy) {
         return GemvSeg{t->data, t->dtype, t->row_bytes, t->nrows, y, ldy};
     };
+    static const int ix_qkv[3] = {FTX_T_Q, FTX_T_K, FTX_T_V}, ix_o[1] = {FTX_T_O},
+                     ix_gu[2] = {FTX_T_GATE, FTX_T_UP}, ix_head[1] = {0};
     for (int64_t l = 0; l < d.n_layer; ++l) {
-        const ftx_tensor* const* T = m->layers.data() + l * FTX_LAYER_TENSORS;
+        const int64_t lt = l * FTX_LAYER_TENSORS;
+        const ftx_tensor* const* T = m->layers.data() + lt;
         const ftx_tensor* tqkv[3] = {T[FTX_T_Q], T[FTX_T_K], T[FTX_T_V]};
         GemvSeg qkv[3] = {seg(T[FTX_T_Q], m->qkv, m->ldq), seg(T[FTX_T_K], m->qkv + m->qdim, m->ldq),
                           seg(T[FTX_T_V], m->qkv + m->qdim + m->kdim, m->ldq)};
         rc = project(TK_GEMV_QKV,
                      wbytes(T[FTX_T_Q]) + wbytes(T[FTX_T_K]) + wbytes(T[FTX_T_V]) + Md * D * f4 +
                          Md * m->ldq * f4,
-                     m->x, D, m->norms + (l * 2) * D, tqkv, qkv, 3, D, EPI_STORE);
+                     m->x, D, m->norms + (l * 2) * D, tqkv, qkv, 3, D, EPI_STORE, lt, ix_qkv);
         if (rc) return rc;
         uint8_t* kl = (uint8_t*)kv->k + (size_t)(l * kv->cap_alloc * kv->kdim) * kvel;
         uint8_t* vl = (uint8_t*)kv->v + (size_t)(l * kv->cap_alloc * kv->kdim) * kvel;
@@ -418,13 +455,13 @@ int ftx_verify_step(ftx_ctx* ctx, ftx_model* m, ftx_kv* kv, const ftx_verify_arg
         }
         GemvSeg o = seg(T[FTX_T_O], m->x, D);
         rc = project(TK_GEMV_O, wbytes(T[FTX_T_O]) + Md * m->qdim * f4 + 2 * Md * D * f4, m->att,
-                     m->qdim, nullptr, &T[FTX_T_O], &o, 1, m->qdim, EPI_ACCUM);
+                     m->qdim, nullptr, &T[FTX_T_O], &o, 1, m->qdim, EPI_ACCUM, lt, ix_o);
         if (rc) return rc;
         const ftx_tensor* tgu[2] = {T[FTX_T_GATE], T[FTX_T_UP]};
         GemvSeg gu[2] = {seg(T[FTX_T_GATE], m->h, F), seg(T[FTX_T_UP], nullptr, 0)};
         rc = project(TK_GEMV_SWIGLU,
                      wbytes(T[FTX_T_GATE]) + wbytes(T[FTX_T_UP]) + Md * D * f4 + Md * F * f4, m->x,
-                     D, m->norms + (l * 2 + 1) * D, tgu, gu, 2, D, EPI_SWIGLU);
+                     D, m->norms + (l * 2 + 1) * D, tgu, gu, 2, D, EPI_SWIGLU, lt, ix_gu);
         if (rc) return rc;
         const double down_b = wbytes(T[FTX_T_DOWN]) + Md * F * f4 + 2 * Md * D * f4;
         if (m->down_tiled[l] && down_mfma_supported(T[FTX_T_DOWN]->dtype, F, D, M))
@@ -439,7 +476,8 @@ int ftx_verify_step(ftx_ctx* ctx, ftx_model* m, ftx_kv* kv, const ftx_verify_arg
     const ftx_tensor* lm = d.output ? d.output : d.tok_embd;
     GemvSeg hs = seg(lm, a->logits, V);
     rc = project(TK_HEAD, wbytes(lm) + Md * D * f4 + Md * V * f4, m->x, D,
-                 m->norms + (d.n_layer * 2) * D, &lm, &hs, 1, D, EPI_STORE);
+                 m->norms + (d.n_layer * 2) * D, &lm, &hs, 1, D, EPI_STORE,
+                 d.n_layer * FTX_LAYER_TENSORS, ix_head);
     if (rc) return rc;
 #undef TRACED
     if (a->advance) kv->npast = npast + M;
