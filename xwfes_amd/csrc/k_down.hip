@@ -60,39 +60,81 @@ __device__ __forceinline__ v8h nib8_to_h(uint32_t w, float bias) {
     return v8h{h0[0], h0[1], h1[0], h1[1], h2[0], h2[1], h3[0], h3[1]};
 }
 
+// One workgroup = one 256-column super-block (wave w: columns 64w..64w+63)
+// over a contiguous range of 32-row slices, processed in batches of NB
+// slices: stage the batch's h and row scales (prefetched into registers one
+// batch ahead), build the scaled fp16 hi/lo activation tables in LDS, then
+// the MFMAs over the batch's weights (also prefetched one batch ahead).
+template <int DT>
+struct DownCfg {
+    static constexpr int NS = DT == FTX_Q4_K ? 8 : 16;  // sub-blocks per super-block
+    static constexpr int NB = 4;                         // slices per batch
+};
+
 template <int DT>
 __global__ void __launch_bounds__(256) k_down_mfma(DownArgs a) {
-    constexpr int NS = DT == FTX_Q4_K ? 8 : 16;  // sub-blocks per super-block
-    __shared__ float hs[8][32];
-    __shared__ float dsc[32][NS];
-    __shared__ float dmn[32][8];
-    __shared__ _Float16 ahi[NS][8][32];
-    __shared__ _Float16 alo[NS][8][32];
+    constexpr int NS = DownCfg<DT>::NS, NB = DownCfg<DT>::NB;
+    __shared__ float hs[8][NB * 32];
+    __shared__ float dsc[NB * 32][NS];
+    __shared__ float dmn[DT == FTX_Q4_K ? NB * 32 : 1][8];
+    __shared__ _Float16 ahi[NB][NS][8][32];
+    __shared__ _Float16 alo[NB][NS][8][32];
     __shared__ float mpart[4][8][8];
     const int tid = threadIdx.x, lane = tid & 63, w = tid >> 6;
     const int64_t sbc = blockIdx.x, split = blockIdx.y;
-    const int64_t nsbc = a.N / 256, nc64 = a.N / 64;
+    const int64_t nc64 = a.N / 64, nsl = a.n_in / 32;
     const int64_t I0 = split * a.slices_per_split;
-    const int64_t I1 = min(I0 + a.slices_per_split, a.n_in / 32);
+    const int64_t I1 = min(I0 + a.slices_per_split, nsl);
     const int col = lane & 15, g = lane >> 4;
     const int64_t c64 = sbc * 4 + w;
     v4f acc[4];
 #pragma unroll
     for (int ct = 0; ct < 4; ++ct) acc[ct] = v4f{0.f, 0.f, 0.f, 0.f};
     float mt = 0.f;  // Q4_K min term of this thread's (s, m)
-    for (int64_t I = I0; I < I1; ++I) {
-        // ---- stage h and the per-row scales of this slice
+    // ---- per-batch register prefetch: h (thread: m = tid / 32, row tid % 32
+    // of each slice), the row header (threads < NB * 32), the weights (lane)
+    float hp[NB];
+    v4i hdp = {0, 0, 0, 0};
+    uint16_t d6p = 0;
+    v4i wq[NB], wqn[NB];
+    int2 wh[NB], whn[NB];
+    auto slice_of = [&](int64_t I) { return I < I1 ? I : I1 - 1; };  // clamped for loads
+    auto load_hs = [&](int64_t Ib) {
+        const int m = tid >> 5, ii = tid & 31;
+#pragma unroll
+        for (int b = 0; b < NB; ++b) {
+            const int64_t I = Ib + b;
+            hp[b] = (m < a.M && I < I1) ? a.h[(int64_t)m * a.ldh + I * 32 + ii] : 0.f;
+        }
+        if (tid < NB * 32) {
+            const int64_t i = slice_of(Ib + tid / 32) * 32 + tid % 32;
+            hdp = *(const v4i*)(a.hdr + (sbc * a.n_in + i) * 16);
+            if (DT == FTX_Q6_K) d6p = *(const uint16_t*)(a.d6 + (sbc * a.n_in + i) * 2);
+        }
+    };
+    auto load_w = [&](int64_t Ib, v4i* q, int2* qh) {
+#pragma unroll
+        for (int b = 0; b < NB; ++b) {
+            const int64_t blk = (slice_of(Ib + b) * nc64 + c64) * 4 + g;
+            q[b] = *(const v4i*)(a.qs + (blk * 16 + col) * 16);
+            if (DT == FTX_Q6_K) qh[b] = *(const int2*)(a.qh + (blk * 16 + col) * 8);
+        }
+    };
+    load_hs(I0);
+    load_w(I0, wq, wh);
+    for (int64_t Ib = I0; Ib < I1; Ib += NB) {
+        __syncthreads();  // the previous batch is done with the LDS tables
+        // ---- stage h and the per-row scales of this batch
         {
             const int m = tid >> 5, ii = tid & 31;
-            hs[m][ii] = m < a.M ? a.h[(int64_t)m * a.ldh + I * 32 + ii] : 0.f;
+#pragma unroll
+            for (int b = 0; b < NB; ++b) hs[m][b * 32 + ii] = hp[b];
         }
-        if (tid < 32) {
-            const int64_t i = I * 32 + tid;
+        if (tid < NB * 32) {
             if (DT == FTX_Q4_K) {
-                const v4i hd = *(const v4i*)(a.hdr + (sbc * a.n_in + i) * 16);
-                const float d = h2f((uint16_t)((uint32_t)hd.x & 0xFFFF));
-                const float dm = h2f((uint16_t)((uint32_t)hd.x >> 16));
-                const uint32_t S0 = hd.y, S1 = hd.z, S2 = hd.w;
+                const float d = h2f((uint16_t)((uint32_t)hdp.x & 0xFFFF));
+                const float dm = h2f((uint16_t)((uint32_t)hdp.x >> 16));
+                const uint32_t S0 = hdp.y, S1 = hdp.z, S2 = hdp.w;
                 const uint32_t sc_lo = S0 & 0x3F3F3F3Fu, mn_lo = S1 & 0x3F3F3F3Fu;
                 const uint32_t sc_hi = (S2 & 0x0F0F0F0Fu) | ((S0 >> 2) & 0x30303030u);
                 const uint32_t mn_hi = ((S2 >> 4) & 0x0F0F0F0Fu) | ((S1 >> 2) & 0x30303030u);
@@ -103,53 +145,55 @@ __global__ void __launch_bounds__(256) k_down_mfma(DownArgs a) {
                     dmn[tid][s] = dm * (float)((mnw >> (8 * (s & 3))) & 0xFF);
                 }
             } else {
-                const v4i sc4 = *(const v4i*)(a.hdr + (sbc * a.n_in + i) * 16);
-                const float d = h2f(*(const uint16_t*)(a.d6 + (sbc * a.n_in + i) * 2));
-                const uint32_t* scw = (const uint32_t*)&sc4;
+                const float d = h2f(d6p);
+                const uint32_t* scw = (const uint32_t*)&hdp;
 #pragma unroll
                 for (int s = 0; s < 16; ++s)
                     dsc[tid][s] = d * (float)(int8_t)((scw[s >> 2] >> (8 * (s & 3))) & 0xFF);
             }
         }
+        // next batch's h and headers in flight from here
+        if (Ib + NB < I1) load_hs(Ib + NB);
         __syncthreads();
-        // ---- A_s[m][i] = h * d * sc as fp16 hi + lo
+        // ---- A_s[m][i] = h * d * sc as fp16 hi + lo, for every slice of the batch
         {
             const int oct = tid >> 6, m = tid & 7, sp = (tid >> 3) & 7;
+#pragma unroll 1
+            for (int b = 0; b < NB; ++b) {
 #pragma unroll
-            for (int rep = 0; rep < NS / 8; ++rep) {
-                const int s = sp * (NS / 8) + rep;
-                _Float16 ph[8], pl[8];
+                for (int rep = 0; rep < NS / 8; ++rep) {
+                    const int s = sp * (NS / 8) + rep;
+                    _Float16 ph[8], pl[8];
 #pragma unroll
-                for (int k = 0; k < 8; ++k) {
-                    const int ii = oct * 8 + k;
-                    const float p = hs[m][ii] * dsc[ii][s];
-                    const _Float16 hi = (_Float16)p;
-                    ph[k] = hi;
-                    pl[k] = (_Float16)(p - (float)hi);
-                    if (DT == FTX_Q4_K) mt += hs[m][ii] * dmn[ii][s];
+                    for (int k = 0; k < 8; ++k) {
+                        const int ii = b * 32 + oct * 8 + k;
+                        const float p = hs[m][ii] * dsc[ii][s];
+                        const _Float16 hi = (_Float16)p;
+                        ph[k] = hi;
+                        pl[k] = (_Float16)(p - (float)hi);
+                        if (DT == FTX_Q4_K) mt += hs[m][ii] * dmn[ii][s];
+                    }
+                    *(v8h*)&ahi[b][s][m][oct * 8] =
+                        v8h{ph[0], ph[1], ph[2], ph[3], ph[4], ph[5], ph[6], ph[7]};
+                    *(v8h*)&alo[b][s][m][oct * 8] =
+                        v8h{pl[0], pl[1], pl[2], pl[3], pl[4], pl[5], pl[6], pl[7]};
                 }
-                *(v8h*)&ahi[s][m][oct * 8] = v8h{ph[0], ph[1], ph[2], ph[3], ph[4], ph[5], ph[6], ph[7]};
-                *(v8h*)&alo[s][m][oct * 8] = v8h{pl[0], pl[1], pl[2], pl[3], pl[4], pl[5], pl[6], pl[7]};
             }
         }
         __syncthreads();
-        // ---- MFMA: this wave's 64 columns (4 tiles of 16) over the 32 rows
-        {
-            const int64_t blk = (I * nc64 + c64) * 4 + g;
-            const v4i qv = *(const v4i*)(a.qs + (blk * 16 + col) * 16);
-            uint32_t qhw[2] = {0, 0};
-            if (DT == FTX_Q6_K) {
-                const int2 t = *(const int2*)(a.qh + (blk * 16 + col) * 8);
-                qhw[0] = (uint32_t)t.x;
-                qhw[1] = (uint32_t)t.y;
-            }
-            const uint32_t* qw = (const uint32_t*)&qv;
-            const int arow = lane & 15;  // A row (token m; rows 8..15 are zero)
+        // next batch's weights in flight during this batch's MFMAs
+        if (Ib + NB < I1) load_w(Ib + NB, wqn, whn);
+        // ---- MFMA: this wave's 64 columns (4 tiles of 16) over the batch's rows
+        const int arow = lane & 15;  // A row (token m; rows 8..15 are zero)
+#pragma unroll
+        for (int b = 0; b < NB; ++b) {
+            const uint32_t* qw = (const uint32_t*)&wq[b];
+            const uint32_t qhw[2] = {(uint32_t)wh[b].x, (uint32_t)wh[b].y};
 #pragma unroll
             for (int ct = 0; ct < 4; ++ct) {
-                v8h b;
+                v8h bv;
                 if (DT == FTX_Q4_K) {
-                    b = nib8_to_h(qw[ct], 0.f);
+                    bv = nib8_to_h(qw[ct], 0.f);
                 } else {
                     const uint32_t X = qhw[ct >> 1];
                     const uint32_t hl = (ct & 1) ? (X << 4) & 0x30303030u : X & 0x30303030u;
@@ -165,19 +209,23 @@ __global__ void __launch_bounds__(256) k_down_mfma(DownArgs a) {
                     const v2h bb = {(_Float16)(-1056.f), (_Float16)(-1056.f)};
                     const v2h h0 = __builtin_bit_cast(v2h, p0) + bb, h1 = __builtin_bit_cast(v2h, p1) + bb;
                     const v2h h2 = __builtin_bit_cast(v2h, p2) + bb, h3 = __builtin_bit_cast(v2h, p3) + bb;
-                    b = v8h{h0[0], h0[1], h1[0], h1[1], h2[0], h2[1], h3[0], h3[1]};
+                    bv = v8h{h0[0], h0[1], h1[0], h1[1], h2[0], h2[1], h3[0], h3[1]};
                 }
                 const int s = DT == FTX_Q4_K ? (w * 64 + ct * 16) / 32 : (w * 64 + ct * 16) / 16;
                 v8h ah = {}, al = {};
                 if (arow < 8) {
-                    ah = *(const v8h*)&ahi[s][arow][g * 8];
-                    al = *(const v8h*)&alo[s][arow][g * 8];
+                    ah = *(const v8h*)&ahi[b][s][arow][g * 8];
+                    al = *(const v8h*)&alo[b][s][arow][g * 8];
                 }
-                acc[ct] = __builtin_amdgcn_mfma_f32_16x16x32_f16(ah, b, acc[ct], 0, 0, 0);
-                acc[ct] = __builtin_amdgcn_mfma_f32_16x16x32_f16(al, b, acc[ct], 0, 0, 0);
+                acc[ct] = __builtin_amdgcn_mfma_f32_16x16x32_f16(ah, bv, acc[ct], 0, 0, 0);
+                acc[ct] = __builtin_amdgcn_mfma_f32_16x16x32_f16(al, bv, acc[ct], 0, 0, 0);
             }
         }
-        __syncthreads();
+#pragma unroll
+        for (int b = 0; b < NB; ++b) {
+            wq[b] = wqn[b];
+            if (DT == FTX_Q6_K) wh[b] = whn[b];
+        }
     }
     // ---- min term per (s, m), summed over the four row octets
     if (DT == FTX_Q4_K) {
@@ -328,13 +376,17 @@ hipError_t launch_down_mfma(hipStream_t st, int dt, const uint8_t* tiled, int64_
     a.n_in = n_in;
     a.N = N;
     const int64_t nslices = n_in / 32, nsb = N / 256;
-    // splits of the contraction: about two workgroups per CU, at most 64
+    // splits of the contraction: about two workgroups per CU, at most 64,
+    // each a whole number of slice batches
+    const int NB = dt == FTX_Q4_K ? DownCfg<FTX_Q4_K>::NB : DownCfg<FTX_Q6_K>::NB;
     int64_t S = (2 * (int64_t)(cu_count > 0 ? cu_count : 256) + nsb - 1) / nsb;
     if (S > 64) S = 64;
     if (S > nslices) S = nslices;
     if (S < 1) S = 1;
-    a.slices_per_split = (int)((nslices + S - 1) / S);
-    S = (nslices + a.slices_per_split - 1) / a.slices_per_split;
+    int64_t spp = (nslices + S - 1) / S;
+    spp = (spp + NB - 1) / NB * NB;
+    a.slices_per_split = (int)spp;
+    S = (nslices + spp - 1) / spp;
     a.part = part;
     const dim3 grid((unsigned)nsb, (unsigned)S);
     if (dt == FTX_Q4_K)

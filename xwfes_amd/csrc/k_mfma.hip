@@ -24,15 +24,14 @@
 //   carry sub-block 2p on the K slots of 2p and zeros elsewhere, rows 16..31
 //   carry sub-block 2p+1, so C rows 0..15 and 16..31 are the two sub-block
 //   dot products and every output register is used.
-// Work split.  A persistent workgroup of 16 waves per CU walks a strided
-// sequence of output units (a tile of 16 or 32 weight rows; for SwiGLU a gate
-// tile and its up tile) over the whole contraction: wave w takes super-blocks
-// w, w+16, ..., holds its activation operand in registers for the whole
-// launch and streams the weights of the workgroup's tiles through it, the
-// next tile's weights in flight during the current one's arithmetic.  The 16
-// wave partials of a unit are added in wave order in LDS (double-buffered, one
-// barrier per unit), so the result is deterministic, and the epilogue (store,
-// accumulate, or SwiGLU) is applied there.
+// Work split.  A workgroup owns one output unit (a tile of 16 or 32 weight
+// rows; for SwiGLU a gate tile and its up tile) over the whole contraction,
+// its W waves splitting the super-blocks into W contiguous ranges (W is
+// chosen so the launch holds up to ~8 waves per CU).  Each wave walks its
+// (super-block, tile) items with the next item's weights in flight during
+// the current one's arithmetic.  With W > 1 the wave partials are added in
+// wave order in LDS, so the result is deterministic; the epilogue (store,
+// accumulate, or SwiGLU) follows.
 #include "ftx_internal.h"
 #include "quant_dev.h"
 
@@ -43,12 +42,14 @@ typedef int v16i __attribute__((ext_vector_type(16)));
 
 __device__ __forceinline__ v4i ld16g(const void* p) { return *(const v4i*)p; }
 
-// Materialise eight running sums here: keeps the compiler from re-associating
-// a chain of integer multiply-adds into a tree that holds every MFMA result
-// live at once (which spills).  Emits no instruction.
+// Materialise eight running sums here and fence the scheduler: keeps the
+// compiler from re-associating a chain of integer multiply-adds into a tree
+// that holds every MFMA result live at once, or from hoisting the operand
+// unpacking of later sub-blocks (both spill).  Emits no instruction.
 __device__ __forceinline__ void reg_fence8(int* v) {
 #pragma unroll
     for (int r = 0; r < 8; ++r) asm volatile("" : "+v"(v[r]));
+    __builtin_amdgcn_sched_barrier(0);
 }
 
 // ---------------------------------------------------------------- prep
@@ -75,7 +76,9 @@ __global__ void __launch_bounds__(64) k_xq_prep(const float* __restrict__ x, int
         v[2] = t.z;
         v[3] = t.w;
         if (normw) {
+            // K / 256 independent loads per lane, issued back to back
             float ss = 0.f;
+#pragma unroll 16
             for (int64_t k = 4 * l; k < K; k += 256) {
                 const float4 u = *(const float4*)(row + k);
                 ss += u.x * u.x;
@@ -170,7 +173,7 @@ struct MvArgs {
     const float* scale;
 };
 
-constexpr int MV_WAVES = 16;
+constexpr int MV_WAVES = 8;  // at most 8 waves per unit (512 threads)
 
 
 __device__ __forceinline__ int mv_seg_of(const MvArgs& a, int64_t T) {
@@ -390,27 +393,23 @@ __device__ __forceinline__ void mv_block(const MvW<DT>& w, const MvX<DT>& x, int
         q6k_block(w.w, w.w + 4, w.w[6], h2f(w.d), x.x8, x.ax, x.s4, col, g, acc);
 }
 
-// grid = persistent workgroups (<= units); block = 16 waves;
-// LDS = 2 slots x tiles per unit x 16 waves x 256 floats
-template <int DT, bool TILED>
-__global__ void __launch_bounds__(1024) k_mv(MvArgs a) {
-    __shared__ float part[2][2][MV_WAVES][256];  // [slot][tile of unit][wave][m * 32 + col]
+// grid = units; block = W waves (W divides the super-block count, W <= 8);
+// at least 3 waves per SIMD fit (<= 168 VGPRs)
+template <int DT, bool TILED, bool PAIR>
+__global__ void __launch_bounds__(64 * MV_WAVES) __attribute__((amdgpu_waves_per_eu(3)))
+k_mv(MvArgs a) {
+    __shared__ float part[PAIR ? 2 : 1][MV_WAVES][256];  // [tile of unit][wave][m * 32 + col]
     const int w = threadIdx.x >> 6, lane = threadIdx.x & 63, col = lane & 31, g = lane >> 5;
-    const bool pair = a.epi == EPI_SWIGLU;
-    const int tpu = pair ? 2 : 1;                     // tiles per unit
+    const int W = blockDim.x >> 6;
+    constexpr bool pair = PAIR;
+    constexpr int tpu = PAIR ? 2 : 1;
     const int64_t units = pair ? a.tiles / 2 : a.tiles;
-    const int64_t G = gridDim.x;
-    const int64_t my_units = units > blockIdx.x ? (units - blockIdx.x + G - 1) / G : 0;
-    const int64_t nseq = my_units * tpu;              // this workgroup's tile sequence
-    // tile q of the sequence: unit blockIdx.x + (q / tpu) * G, gate or up
-    auto tile_of = [&](int64_t q) -> int64_t {
-        const int64_t u = blockIdx.x + (q / tpu) * G;
-        return (q % tpu) ? units + u : u;
-    };
+    const int64_t u = blockIdx.x;
     const int64_t nsb = a.nsb;
-    // lane base of tile q: its weight row (row layout) or the tile (tiled)
-    auto load = [&](MvW<DT>& o, int64_t q, int sb) {
-        const int64_t T = tile_of(q);
+    const int spw = (int)(nsb / W), sb0 = w * spw;
+    auto tile_of = [&](int ti) -> int64_t { return ti ? units + u : u; };
+    auto load = [&](MvW<DT>& o, int ti, int sb) {
+        const int64_t T = tile_of(ti);
         const MvSeg& sg = a.seg[mv_seg_of(a, T)];
         const int R = sg.rpt, r = col & (R - 1);
         const uint8_t* base;
@@ -423,66 +422,74 @@ __global__ void __launch_bounds__(1024) k_mv(MvArgs a) {
         }
         mv_load<DT, TILED>(o, base, nsb, sb, g, r, r + R * g, R);
     };
-    // waves own super-blocks w + 16 k: rows of more than 16 super-blocks
-    // walk the tile sequence once per round, later rounds adding to the
-    // output (SwiGLU needs its sums whole: one round only)
-    const int rounds = a.nsb / MV_WAVES;
-    for (int rd = 0; rd < rounds; ++rd) {
-        const int sb = w + MV_WAVES * rd;
-        MvX<DT> x;
-        mv_load_x<DT>(x, a, sb, col, g);
-        MvW<DT> cur, nxt;
-        // Q4_K: the next tile's weights in flight during this tile's
-        // arithmetic (the last tile re-reads its own block); Q6_K's larger
-        // blocks do not fit twice in the register budget
-        constexpr bool PF = DT == FTX_Q4_K;
-        if (PF && nseq > 0) load(cur, 0, sb);
-        for (int64_t q = 0; q < nseq; ++q) {
-            if constexpr (PF) {
-                __builtin_amdgcn_sched_barrier(0);
-                load(nxt, q + 1 < nseq ? q + 1 : q, sb);
-                __builtin_amdgcn_sched_barrier(0);
-            } else {
-                load(cur, q, sb);
-            }
-            float acc[8];
+    // items i = (super-block sb0 + i / tpu, tile i % tpu)
+    const int nit = spw * tpu;
+    float acc[tpu][8];
 #pragma unroll
-            for (int r = 0; r < 8; ++r) acc[r] = 0.f;
-            mv_block<DT>(cur, x, col, g, acc);
-            const int slot = (int)((q / tpu) & 1), ti = (int)(q % tpu);
-            float* pp = &part[slot][ti][w][col];
+    for (int t = 0; t < tpu; ++t)
 #pragma unroll
-            for (int r = 0; r < 4; ++r) pp[(4 * g + r) * 32] = acc[r] + acc[r + 4] * (1.f / 256.f);
-            if constexpr (PF) cur = nxt;
-            if (ti != tpu - 1) continue;
-            __syncthreads();
-            // unit complete: threads (m, c) add the 16 wave partials in order
-            const int t = threadIdx.x;
-            const int64_t T = tile_of(q - ti);
-            const MvSeg& sg = a.seg[mv_seg_of(a, T)];
-            const int rpt = sg.rpt;
-            if (t < 8 * rpt) {
-                const int m = t / rpt, c = t % rpt;
-                const int64_t n = (T - sg.tile0) * rpt + c;
-                if (m < a.M && n < sg.N) {
-                    float v = 0.f;
-#pragma unroll
-                    for (int ww = 0; ww < MV_WAVES; ++ww) v += part[slot][0][ww][m * 32 + c];
-                    float* yp = sg.y + (int64_t)m * sg.ldy + n;
-                    if (pair) {
-                        float u = 0.f;
-#pragma unroll
-                        for (int ww = 0; ww < MV_WAVES; ++ww) u += part[slot][1][ww][m * 32 + c];
-                        // src/engine.cpp:271-273: g / (1 + exp(-g)) * u
-                        *yp = v / (1.f + expf(-v)) * u;
-                    } else if (rd > 0 || a.epi == EPI_ACCUM) {
-                        *yp += v;
-                    } else {
-                        *yp = v;
-                    }
-                }
-            }
+        for (int r = 0; r < 8; ++r) acc[t][r] = 0.f;
+    // the next item's weights in flight during this item's arithmetic (the
+    // last item re-reads its own block), except for Q6_K SwiGLU pairs whose
+    // larger blocks do not fit twice in the register budget
+    constexpr bool PF = DT == FTX_Q4_K || !PAIR;
+    MvW<DT> cur, nxt;
+    if (PF) load(cur, 0, sb0);
+    MvX<DT> x;
+    for (int i = 0; i < nit; ++i) {
+        const int ti = i % tpu, sb = sb0 + i / tpu;
+        if (ti == 0) mv_load_x<DT>(x, a, sb, col, g);
+        if constexpr (PF) {
+            const int j = i + 1 < nit ? i + 1 : i;
+            __builtin_amdgcn_sched_barrier(0);
+            load(nxt, j % tpu, sb0 + j / tpu);
+            __builtin_amdgcn_sched_barrier(0);
+        } else {
+            load(cur, ti, sb);
         }
+        if (!PAIR || ti == 0)
+            mv_block<DT>(cur, x, col, g, acc[0]);
+        else
+            mv_block<DT>(cur, x, col, g, acc[tpu - 1]);
+        if constexpr (PF) cur = nxt;
+    }
+    // lane (col, g) holds rows m = 4g + r of weight row col of each tile
+    float v[tpu][4];
+#pragma unroll
+    for (int t = 0; t < tpu; ++t)
+#pragma unroll
+        for (int r = 0; r < 4; ++r) v[t][r] = acc[t][r] + acc[t][r + 4] * (1.f / 256.f);
+    const MvSeg& sg = a.seg[mv_seg_of(a, u)];
+    const int rpt = sg.rpt;
+    auto finish = [&](int m, int c, float gv, float uv) {
+        const int64_t n = (u - sg.tile0) * rpt + c;
+        if (m >= a.M || n >= sg.N) return;
+        float* yp = sg.y + (int64_t)m * sg.ldy + n;
+        if (pair)
+            // src/engine.cpp:271-273: g / (1 + exp(-g)) * u
+            *yp = gv / (1.f + expf(-gv)) * uv;
+        else
+            *yp = a.epi == EPI_ACCUM ? *yp + gv : gv;
+    };
+    if (W == 1) {
+        if (col < rpt)
+#pragma unroll
+            for (int r = 0; r < 4; ++r) finish(4 * g + r, col, v[0][r], v[tpu - 1][r]);
+        return;
+    }
+#pragma unroll
+    for (int t = 0; t < tpu; ++t)
+#pragma unroll
+        for (int r = 0; r < 4; ++r) part[t][w][(4 * g + r) * 32 + col] = v[t][r];
+    __syncthreads();
+    const int t = threadIdx.x;
+    if (t < 8 * rpt) {
+        const int m = t / rpt, c = t % rpt;
+        float gv = 0.f, uv = 0.f;
+        for (int ww = 0; ww < W; ++ww) gv += part[0][ww][m * 32 + c];
+        if constexpr (PAIR)
+            for (int ww = 0; ww < W; ++ww) uv += part[tpu - 1][ww][m * 32 + c];
+        finish(m, c, gv, uv);
     }
 }
 
@@ -494,6 +501,7 @@ __global__ void __launch_bounds__(256) k_part_reduce(const float* __restrict__ p
     const int m = blockIdx.y;
     if (t >= N) return;
     float v = 0.f;
+#pragma unroll 8
     for (int s = 0; s < S; ++s) v += part[((int64_t)s * 8 + m) * N + t];
     y[(int64_t)m * ldy + t] += v;
 }
@@ -515,7 +523,7 @@ hipError_t launch_xq_prep(hipStream_t st, const float* x, int64_t ldx, const flo
     return hipGetLastError();
 }
 
-bool mv_swiglu_supported(int64_t K) { return K == 256 * MV_WAVES; }
+bool mv_swiglu_supported(int64_t K) { return K >= 256; }
 
 bool mv_supported(int dt, int64_t K, int64_t M) {
     return (dt == FTX_Q4_K || dt == FTX_Q6_K) && M >= 1 && M <= 8 && K % 4096 == 0 &&
@@ -596,19 +604,19 @@ hipError_t launch_mv(hipStream_t st, const GemvSeg* segs, int nseg, const int8_t
         a.xs32 = xq + K * 16;
         a.xs16 = xq + K * 16 + K;
         a.scale = (const float*)(xq + K * 16 + K + K * 2);
-        const int64_t grid = units < cus ? units : cus;
-        const dim3 gd((unsigned)grid), bd(64 * MV_WAVES);
-        if (dt == FTX_Q4_K) {
-            if (tiled)
-                hipLaunchKernelGGL((k_mv<FTX_Q4_K, true>), gd, bd, 0, st, a);
-            else
-                hipLaunchKernelGGL((k_mv<FTX_Q4_K, false>), gd, bd, 0, st, a);
-        } else {
-            if (tiled)
-                hipLaunchKernelGGL((k_mv<FTX_Q6_K, true>), gd, bd, 0, st, a);
-            else
-                hipLaunchKernelGGL((k_mv<FTX_Q6_K, false>), gd, bd, 0, st, a);
-        }
+        // waves per unit: up to ~8 waves per CU over the launch (measured
+        // best on the 8B shapes: gate/up W = 4, attention projections 8)
+        int W = 1;
+        while (W < MV_WAVES && a.nsb % (2 * W) == 0 && units * W * 2 <= (int64_t)cus * 8) W *= 2;
+        const dim3 gd((unsigned)units), bd(64 * W);
+        // instantiations: {Q4_K, Q6_K} x {row, tiled} x {single, SwiGLU pair}
+        using K_t = void (*)(MvArgs);
+        static const K_t kern[2][2][2] = {
+            {{k_mv<FTX_Q4_K, false, false>, k_mv<FTX_Q4_K, false, true>},
+             {k_mv<FTX_Q4_K, true, false>, k_mv<FTX_Q4_K, true, true>}},
+            {{k_mv<FTX_Q6_K, false, false>, k_mv<FTX_Q6_K, false, true>},
+             {k_mv<FTX_Q6_K, true, false>, k_mv<FTX_Q6_K, true, true>}}};
+        hipLaunchKernelGGL(kern[dt == FTX_Q6_K][tiled][pair], gd, bd, 0, st, a);
         hipError_t e = hipGetLastError();
         if (e != hipSuccess) return e;
     }
