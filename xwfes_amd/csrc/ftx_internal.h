@@ -191,6 +191,9 @@ struct RopeArgs {
     void* vc;          // layer base of V cache [n_kv][hd][cap]
     int kv_f16;
     int64_t cap;
+    // optional: the rotated q also as fp16 hi + lo parts, [m][n_head][hd]
+    _Float16* qh16 = nullptr;
+    _Float16* ql16 = nullptr;
 };
 hipError_t launch_rope_kv(hipStream_t st, const RopeArgs& a, int64_t M);
 struct AttnArgs {
@@ -213,6 +216,8 @@ hipError_t launch_attention(hipStream_t st, const AttnArgs& a, int64_t M);
 struct AttnMArgs {
     const float* qkv;
     int64_t ldq;
+    const _Float16* qh16;  // rotated q split into fp16 hi + lo, [m][n_head][hd]
+    const _Float16* ql16;
     const _Float16* kc;  // layer base [cap][kdim]
     const _Float16* vt;  // layer base [n_kv][hd][cap]
     int64_t cap;         // allocated slots, multiple of 64

@@ -7,25 +7,26 @@
 // slots npast + j of its ancestors j (itself included); kv head =
 // h / (n_head / n_kv); scores are q.k / sqrt(hd); softmax; sum of p * v.
 //
-// One wave handles one kv head, one 64-slot chunk and up to 32 query rows
-// (the GQA group of every draft token: row r -> token r / gqa, head
-// kvh * gqa + r % gqa).  Scores are computed transposed, S^T = K . Q^T, with
-// v_mfma_f32_32x32x16_f16: K is fp16 in the cache (exact operand), Q is
-// split into fp16 hi + lo parts (two MFMAs) so the scores keep fp32
-// accuracy.  In the S^T layout each lane holds 16 slots of one query row,
-// so the row max / sum need one cross-lane step, and the probabilities are
-// already laid out as the A operand of O = P . V (hi + lo again).  V is kept
-// transposed in the cache ([kv head][dim][slot]) so the B operand of P . V
-// is a contiguous load.
+// One workgroup handles one kv head, one 64-slot chunk and one tile of 32
+// query rows of the GQA group (row r -> token r / gqa, head kvh * gqa +
+// r % gqa); its four waves take 16 slots each.  Per wave, with
+// v_mfma_f32_16x16x32_f16: S^T = K . Q^T (K rows are the A operand, exact
+// fp16; Q arrives split into fp16 hi + lo so the scores keep fp32 accuracy); a
+// lane then holds 4 slots of one query row, which is exactly the A operand
+// of O = P . V on v_mfma_f32_16x16x16_f16 (P hi + lo).  V is kept
+// transposed in the cache ([kv head][dim][slot]) so the B operand is one
+// 8-byte load.  The query operand is staged once per workgroup in LDS; the
+// four wave partials (max, sum, O) are merged in LDS into the chunk partial.
 #include "ftx_internal.h"
 
 namespace {
 
 typedef _Float16 v8h __attribute__((ext_vector_type(8)));
 typedef _Float16 v4h __attribute__((ext_vector_type(4)));
-typedef float v16f __attribute__((ext_vector_type(16)));
+typedef float v4f __attribute__((ext_vector_type(4)));
 
-constexpr int CH = 64;  // slots per chunk
+constexpr int CH = 64;   // slots per chunk (workgroup)
+constexpr int WS = 16;   // slots per wave
 
 __device__ __forceinline__ bool slot_visible(const AttnMArgs& a, int64_t npast, int m, int64_t p) {
     if (p < npast) return true;
@@ -35,10 +36,12 @@ __device__ __forceinline__ bool slot_visible(const AttnMArgs& a, int64_t npast, 
 }
 
 template <int HD>
-__global__ void __launch_bounds__(64) k_attn_mfma(AttnMArgs a) {
-    constexpr int NDC = HD / 16;  // 16-dim chunks of the score contraction
-    constexpr int NDT = HD / 32;  // 32-dim tiles of the output
-    const int lane = threadIdx.x, col = lane & 31, g = lane >> 5;
+__global__ void __launch_bounds__(256) k_attn_mfma(AttnMArgs a) {
+    constexpr int NDC = HD / 32;  // 32-dim chunks of the score contraction
+    constexpr int NDT = HD / 16;  // 16-dim tiles of the output
+    __shared__ float obuf[4][32][HD];  // wave partial O [q row][dim]
+    __shared__ float smax[4][32], ssum[4][32];
+    const int tid = threadIdx.x, w = tid >> 6, lane = tid & 63, col = lane & 15, g = lane >> 4;
     const int64_t npast = *a.npast;
     const int64_t total = npast + a.M;
     const int c = blockIdx.x;
@@ -47,110 +50,145 @@ __global__ void __launch_bounds__(64) k_attn_mfma(AttnMArgs a) {
     const int kvh = blockIdx.y;
     const int gqa = a.n_head / a.n_kv;
     const int qrows = a.M * gqa;
-    // this lane's query row (B operand column of S^T)
-    const int rq = blockIdx.z * 32 + col;
-    const bool qvalid = rq < qrows;
-    const int mq = qvalid ? rq / gqa : 0;
-    const int hq = kvh * gqa + (qvalid ? rq % gqa : 0);
-    v8h qh[NDC], ql[NDC];
-    {
-        const float* qv = a.qkv + (int64_t)mq * a.ldq + (int64_t)hq * HD;
-#pragma unroll
-        for (int dc = 0; dc < NDC; ++dc) {
-#pragma unroll
-            for (int s = 0; s < 8; ++s) {
-                const float x = qvalid ? qv[16 * dc + 8 * g + s] : 0.f;
-                const _Float16 h = (_Float16)x;
-                qh[dc][s] = h;
-                ql[dc][s] = (_Float16)(x - (float)h);
-            }
-        }
-    }
+    const int qbase = blockIdx.z * 32;  // first query row of this tile
     const int64_t kdim = (int64_t)a.n_kv * HD;
-    const _Float16* kbase = a.kc + (int64_t)kvh * HD;
-    v16f st[2];
+    const int64_t ws0 = slot0 + w * WS;  // this wave's first slot
+    // ---- every operand load issued up front: K rows (A of S^T), V^T rows
+    // (B of O), the query hi / lo parts (B of S^T)
+    v8h kf[NDC];
+    {
+        const _Float16* krow = a.kc + (ws0 + col) * kdim + (int64_t)kvh * HD + 8 * g;
 #pragma unroll
-    for (int t = 0; t < 2; ++t) {
-        const int64_t p = slot0 + 32 * t + col;  // K row of this lane (< padded cap)
-        const _Float16* krow = kbase + p * kdim;
-        v16f acc = {};
+        for (int dc = 0; dc < NDC; ++dc) kf[dc] = *(const v8h*)(krow + 32 * dc);
+    }
+    v4h vf[NDT];
+    {
+        const _Float16* vbase = a.vt + (int64_t)kvh * HD * a.cap + ws0 + 4 * g;
+#pragma unroll
+        for (int dt = 0; dt < NDT; ++dt) vf[dt] = *(const v4h*)(vbase + (int64_t)(16 * dt + col) * a.cap);
+    }
+    // the query hi / lo parts of this tile's 32 rows, staged once per
+    // workgroup in the (not yet used) merge buffer: [hi|lo][row][dim]
+    _Float16* qs = (_Float16*)&obuf[0][0][0];
+#pragma unroll
+    for (int k = 0; k < 4 * HD / 128; ++k) {
+        const int v = tid + 256 * k;  // 16-byte vector index
+        const int part = v / (32 * HD / 8), r = (v / (HD / 8)) % 32, dv = v % (HD / 8);
+        const int rq = qbase + r;
+        v8h x = {};
+        if (rq < qrows) {
+            const int64_t qo = ((int64_t)(rq / gqa) * a.n_head + kvh * gqa + rq % gqa) * HD + 8 * dv;
+            x = *(const v8h*)((part ? a.ql16 : a.qh16) + qo);
+        }
+        *(v8h*)&qs[(part * 32 + r) * HD + 8 * dv] = x;
+    }
+    __syncthreads();
+    v8h qh[2][NDC], ql[2][NDC];
+#pragma unroll
+    for (int qt = 0; qt < 2; ++qt)
 #pragma unroll
         for (int dc = 0; dc < NDC; ++dc) {
-            const v8h kf = *(const v8h*)(krow + 16 * dc + 8 * g);
-            acc = __builtin_amdgcn_mfma_f32_32x32x16_f16(kf, qh[dc], acc, 0, 0, 0);
-            acc = __builtin_amdgcn_mfma_f32_32x32x16_f16(kf, ql[dc], acc, 0, 0, 0);
+            qh[qt][dc] = *(const v8h*)&qs[(qt * 16 + col) * HD + 32 * dc + 8 * g];
+            ql[qt][dc] = *(const v8h*)&qs[(32 + qt * 16 + col) * HD + 32 * dc + 8 * g];
         }
-        st[t] = acc;
+    // ---- S^T = K . Q^T for the two 16-row query tiles
+    v4f st[2];
+#pragma unroll
+    for (int qt = 0; qt < 2; ++qt) {
+        v4f acc = {0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+        for (int dc = 0; dc < NDC; ++dc) {
+            acc = __builtin_amdgcn_mfma_f32_16x16x32_f16(kf[dc], qh[qt][dc], acc, 0, 0, 0);
+            acc = __builtin_amdgcn_mfma_f32_16x16x32_f16(kf[dc], ql[qt][dc], acc, 0, 0, 0);
+        }
+        st[qt] = acc;
     }
-    // lane (q = col, g) holds S^T[slot 8(r/4) + 4g + r%4][q] of tile t
+    __syncthreads();  // every wave is done with the staged queries
+    // lane (col, g) holds S^T[slot ws0 + 4g + r][query row qt * 16 + col]
     const float scale = 1.f / sqrtf((float)HD);
-    float mx = -INFINITY;
+    float mx[2], sum[2];
 #pragma unroll
-    for (int t = 0; t < 2; ++t)
+    for (int qt = 0; qt < 2; ++qt) {
+        const int rq = qbase + qt * 16 + col;
+        const bool qvalid = rq < qrows;
+        const int mq = qvalid ? rq / gqa : 0;
+        float m_ = -INFINITY;
 #pragma unroll
-        for (int r = 0; r < 16; ++r) {
-            const int64_t ps = slot0 + 32 * t + 8 * (r >> 2) + 4 * g + (r & 3);
-            const bool ok = qvalid && slot_visible(a, npast, mq, ps);
-            const float s = ok ? st[t][r] * scale : -INFINITY;
-            st[t][r] = s;
-            mx = fmaxf(mx, s);
+        for (int r = 0; r < 4; ++r) {
+            const bool ok = qvalid && slot_visible(a, npast, mq, ws0 + 4 * g + r);
+            const float sv = ok ? st[qt][r] * scale : -INFINITY;
+            st[qt][r] = sv;
+            m_ = fmaxf(m_, sv);
         }
-    mx = fmaxf(mx, __shfl_xor(mx, 32, 64));
-    float sum = 0.f;
+        m_ = fmaxf(m_, __shfl_xor(m_, 16, 64));
+        m_ = fmaxf(m_, __shfl_xor(m_, 32, 64));
+        float s_ = 0.f;
 #pragma unroll
-    for (int t = 0; t < 2; ++t)
-#pragma unroll
-        for (int r = 0; r < 16; ++r) {
-            const float e = st[t][r] == -INFINITY ? 0.f : expf(st[t][r] - mx);
-            st[t][r] = e;
-            sum += e;
+        for (int r = 0; r < 4; ++r) {
+            const float e = st[qt][r] == -INFINITY ? 0.f : expf(st[qt][r] - m_);
+            st[qt][r] = e;
+            s_ += e;
         }
-    sum += __shfl_xor(sum, 32, 64);
-    // O = P . V: A = P (rows q, k-slot 8g+s <-> tile slot 16hf + 8(s/4) + 4g + s%4)
-    const _Float16* vbase = a.vt + (int64_t)kvh * HD * a.cap;
-    v16f o[NDT];
-#pragma unroll
-    for (int dt = 0; dt < NDT; ++dt) o[dt] = v16f{};
-#pragma unroll
-    for (int t = 0; t < 2; ++t)
-#pragma unroll
-        for (int hf = 0; hf < 2; ++hf) {
-            v8h ph, pl;
-#pragma unroll
-            for (int s = 0; s < 8; ++s) {
-                const float pv = st[t][8 * hf + s];
-                const _Float16 h = (_Float16)pv;
-                ph[s] = h;
-                pl[s] = (_Float16)(pv - (float)h);
-            }
-            const int64_t sbase = slot0 + 32 * t + 16 * hf + 4 * g;
-#pragma unroll
-            for (int dt = 0; dt < NDT; ++dt) {
-                const _Float16* vrow = vbase + (int64_t)(32 * dt + col) * a.cap + sbase;
-                const v4h v0 = *(const v4h*)vrow;
-                const v4h v1 = *(const v4h*)(vrow + 8);
-                const v8h vf = {v0[0], v0[1], v0[2], v0[3], v1[0], v1[1], v1[2], v1[3]};
-                o[dt] = __builtin_amdgcn_mfma_f32_32x32x16_f16(ph, vf, o[dt], 0, 0, 0);
-                o[dt] = __builtin_amdgcn_mfma_f32_32x32x16_f16(pl, vf, o[dt], 0, 0, 0);
-            }
-        }
-    // partials: per query row max / sum, and O rows
-    const int nch = (int)gridDim.x;
-    if (qvalid && g == 0) {
-        const int64_t qi = (int64_t)mq * a.n_head + hq;
-        a.pmax[qi * nch + c] = mx;
-        a.psum[qi * nch + c] = sum;
+        s_ += __shfl_xor(s_, 16, 64);
+        s_ += __shfl_xor(s_, 32, 64);
+        mx[qt] = m_;
+        sum[qt] = s_;
     }
+    // ---- O = P . V: A = P (query row col, slots 4g .. 4g+3), B = V^T rows
+    v4h ph[2], pl[2];
 #pragma unroll
-    for (int r = 0; r < 16; ++r) {
-        const int q = 8 * (r >> 2) + 4 * g + (r & 3);
-        const int rr = blockIdx.z * 32 + q;
-        if (rr < qrows) {
-            const int64_t qi = (int64_t)(rr / gqa) * a.n_head + kvh * gqa + rr % gqa;
+    for (int qt = 0; qt < 2; ++qt)
 #pragma unroll
-            for (int dt = 0; dt < NDT; ++dt)
-                a.pout[(qi * nch + c) * HD + 32 * dt + col] = o[dt][r];
+        for (int r = 0; r < 4; ++r) {
+            const _Float16 h = (_Float16)st[qt][r];
+            ph[qt][r] = h;
+            pl[qt][r] = (_Float16)(st[qt][r] - (float)h);
         }
+#pragma unroll
+    for (int dt = 0; dt < NDT; ++dt) {
+#pragma unroll
+        for (int qt = 0; qt < 2; ++qt) {
+            v4f o = {0.f, 0.f, 0.f, 0.f};
+            o = __builtin_amdgcn_mfma_f32_16x16x16f16(ph[qt], vf[dt], o, 0, 0, 0);
+            o = __builtin_amdgcn_mfma_f32_16x16x16f16(pl[qt], vf[dt], o, 0, 0, 0);
+            // lane holds O[query row qt * 16 + 4g + r][dim 16 dt + col]
+#pragma unroll
+            for (int r = 0; r < 4; ++r) obuf[w][qt * 16 + 4 * g + r][16 * dt + col] = o[r];
+        }
+    }
+    if (g == 0) {
+#pragma unroll
+        for (int qt = 0; qt < 2; ++qt) {
+            smax[w][qt * 16 + col] = mx[qt];
+            ssum[w][qt * 16 + col] = sum[qt];
+        }
+    }
+    __syncthreads();
+    // ---- merge the four waves: thread -> (query row, 16 dims)
+    const int nch = (int)gridDim.x;
+    const int q = tid >> 3, d0 = (tid & 7) * (HD / 8);
+    if (qbase + q >= qrows) return;
+    float M = -INFINITY;
+#pragma unroll
+    for (int k = 0; k < 4; ++k) M = fmaxf(M, smax[k][q]);
+    float wgt[4], den = 0.f;
+#pragma unroll
+    for (int k = 0; k < 4; ++k) {
+        wgt[k] = smax[k][q] == -INFINITY ? 0.f : expf(smax[k][q] - M);
+        den += wgt[k] * ssum[k][q];
+    }
+    const int64_t qi = (int64_t)((qbase + q) / gqa) * a.n_head + kvh * gqa + (qbase + q) % gqa;
+    if ((tid & 7) == 0) {
+        a.pmax[qi * nch + c] = M;
+        a.psum[qi * nch + c] = den;
+    }
+    float* po = a.pout + (qi * nch + c) * HD + d0;
+#pragma unroll
+    for (int d = 0; d < HD / 8; d += 4) {
+        v4f v = {0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+        for (int k = 0; k < 4; ++k) v += wgt[k] * *(const v4f*)&obuf[k][q][d0 + d];
+        *(v4f*)(po + d) = v;
     }
 }
 
@@ -214,13 +252,13 @@ hipError_t launch_attn_mfma(hipStream_t st, AttnMArgs a, float* part) {
     a.pmax = part;
     a.psum = part + qi * nch;
     a.pout = part + 2 * qi * nch;
-    const int gqa = a.n_head / a.n_kv;
-    const int qtiles = (a.M * gqa + 31) / 32;
-    dim3 grid((unsigned)nch, (unsigned)a.n_kv, (unsigned)qtiles);
+    // one workgroup per (chunk, kv head, tile of 32 query rows)
+    const int qtiles = (int)((a.M * (a.n_head / a.n_kv) + 31) / 32);
+    const dim3 grid((unsigned)nch, (unsigned)a.n_kv, (unsigned)qtiles);
     if (a.hd == 128)
-        hipLaunchKernelGGL(k_attn_mfma<128>, grid, dim3(64), 0, st, a);
+        hipLaunchKernelGGL(k_attn_mfma<128>, grid, dim3(256), 0, st, a);
     else if (a.hd == 64)
-        hipLaunchKernelGGL(k_attn_mfma<64>, grid, dim3(64), 0, st, a);
+        hipLaunchKernelGGL(k_attn_mfma<64>, grid, dim3(256), 0, st, a);
     else
         return hipErrorInvalidValue;
     hipError_t e = hipGetLastError();

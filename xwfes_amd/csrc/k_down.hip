@@ -75,8 +75,8 @@ template <int DT>
 __global__ void __launch_bounds__(256) k_down_mfma(DownArgs a) {
     constexpr int NS = DownCfg<DT>::NS, NB = DownCfg<DT>::NB;
     __shared__ float hs[8][NB * 32];
-    __shared__ float dsc[NB * 32][NS];
-    __shared__ float dmn[DT == FTX_Q4_K ? NB * 32 : 1][8];
+    __shared__ float dsc[NS][NB * 32];  // [sub-block][row of the batch]
+    __shared__ float dmn[DT == FTX_Q4_K ? 8 : 1][NB * 32];
     __shared__ _Float16 ahi[NB][NS][8][32];
     __shared__ _Float16 alo[NB][NS][8][32];
     __shared__ float mpart[4][8][8];
@@ -141,15 +141,15 @@ __global__ void __launch_bounds__(256) k_down_mfma(DownArgs a) {
 #pragma unroll
                 for (int s = 0; s < 8; ++s) {
                     const uint32_t scw = s < 4 ? sc_lo : sc_hi, mnw = s < 4 ? mn_lo : mn_hi;
-                    dsc[tid][s] = d * (float)((scw >> (8 * (s & 3))) & 0xFF);
-                    dmn[tid][s] = dm * (float)((mnw >> (8 * (s & 3))) & 0xFF);
+                    dsc[s][tid] = d * (float)((scw >> (8 * (s & 3))) & 0xFF);
+                    dmn[s][tid] = dm * (float)((mnw >> (8 * (s & 3))) & 0xFF);
                 }
             } else {
                 const float d = h2f(d6p);
                 const uint32_t* scw = (const uint32_t*)&hdp;
 #pragma unroll
                 for (int s = 0; s < 16; ++s)
-                    dsc[tid][s] = d * (float)(int8_t)((scw[s >> 2] >> (8 * (s & 3))) & 0xFF);
+                    dsc[s][tid] = d * (float)(int8_t)((scw[s >> 2] >> (8 * (s & 3))) & 0xFF);
             }
         }
         // next batch's h and headers in flight from here
@@ -163,15 +163,25 @@ __global__ void __launch_bounds__(256) k_down_mfma(DownArgs a) {
 #pragma unroll
                 for (int rep = 0; rep < NS / 8; ++rep) {
                     const int s = sp * (NS / 8) + rep;
+                    const int i0 = b * 32 + oct * 8;
+                    // eight rows at once: two 16-byte LDS reads per table
+                    const v4f h0 = *(const v4f*)&hs[m][i0], h1 = *(const v4f*)&hs[m][i0 + 4];
+                    const v4f f0 = *(const v4f*)&dsc[s][i0], f1 = *(const v4f*)&dsc[s][i0 + 4];
+                    const float hv[8] = {h0[0], h0[1], h0[2], h0[3], h1[0], h1[1], h1[2], h1[3]};
+                    const float fv[8] = {f0[0], f0[1], f0[2], f0[3], f1[0], f1[1], f1[2], f1[3]};
                     _Float16 ph[8], pl[8];
 #pragma unroll
                     for (int k = 0; k < 8; ++k) {
-                        const int ii = b * 32 + oct * 8 + k;
-                        const float p = hs[m][ii] * dsc[ii][s];
+                        const float p = hv[k] * fv[k];
                         const _Float16 hi = (_Float16)p;
                         ph[k] = hi;
                         pl[k] = (_Float16)(p - (float)hi);
-                        if (DT == FTX_Q4_K) mt += hs[m][ii] * dmn[ii][s];
+                    }
+                    if (DT == FTX_Q4_K) {
+                        const v4f n0 = *(const v4f*)&dmn[s][i0], n1 = *(const v4f*)&dmn[s][i0 + 4];
+                        const float nv[8] = {n0[0], n0[1], n0[2], n0[3], n1[0], n1[1], n1[2], n1[3]};
+#pragma unroll
+                        for (int k = 0; k < 8; ++k) mt += hv[k] * nv[k];
                     }
                     *(v8h*)&ahi[b][s][m][oct * 8] =
                         v8h{ph[0], ph[1], ph[2], ph[3], ph[4], ph[5], ph[6], ph[7]};
@@ -376,10 +386,12 @@ hipError_t launch_down_mfma(hipStream_t st, int dt, const uint8_t* tiled, int64_
     a.n_in = n_in;
     a.N = N;
     const int64_t nslices = n_in / 32, nsb = N / 256;
-    // splits of the contraction: about two workgroups per CU, at most 64,
-    // each a whole number of slice batches
+    // splits of the contraction: as many workgroups as fit the CUs at once
+    // (LDS: three Q4_K or two Q6_K workgroups per CU), at most 64, each a
+    // whole number of slice batches
     const int NB = dt == FTX_Q4_K ? DownCfg<FTX_Q4_K>::NB : DownCfg<FTX_Q6_K>::NB;
-    int64_t S = (2 * (int64_t)(cu_count > 0 ? cu_count : 256) + nsb - 1) / nsb;
+    const int64_t per_cu = dt == FTX_Q4_K ? 3 : 2;
+    int64_t S = (per_cu * (int64_t)(cu_count > 0 ? cu_count : 256) + nsb - 1) / nsb;
     if (S > 64) S = 64;
     if (S > nslices) S = nslices;
     if (S < 1) S = 1;

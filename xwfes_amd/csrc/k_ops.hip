@@ -83,8 +83,17 @@ __global__ void k_rope_kv(RopeArgs a) {
         const float c = (float)cos(ang), s = (float)sin(ang);
         const int64_t ia = a.neox ? i : 2 * i, ib = a.neox ? i + half : 2 * i + 1;
         const float x0 = v[ia], x1 = v[ib];
-        v[ia] = x0 * c - x1 * s;
-        v[ib] = x0 * s + x1 * c;
+        const float y0 = x0 * c - x1 * s, y1 = x0 * s + x1 * c;
+        v[ia] = y0;
+        v[ib] = y1;
+        if (h < a.n_head && a.qh16) {
+            const int64_t o = (m * a.n_head + h) * a.hd;
+            const _Float16 h0 = (_Float16)y0, h1 = (_Float16)y1;
+            a.qh16[o + ia] = h0;
+            a.qh16[o + ib] = h1;
+            a.ql16[o + ia] = (_Float16)(y0 - (float)h0);
+            a.ql16[o + ib] = (_Float16)(y1 - (float)h1);
+        }
     }
     if (h < a.n_head) return;
     __syncthreads();

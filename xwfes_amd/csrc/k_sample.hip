@@ -43,6 +43,7 @@ __global__ void __launch_bounds__(256) k_row_max(const float* __restrict__ rows,
     const int64_t b = (int64_t)c * SCH, e = min(V, b + SCH);
     float best = -INFINITY;
     int32_t bi = 0x7FFFFFFF;
+#pragma unroll 8
     for (int64_t i = b + t; i < e; i += 256) {
         const float v = row[i];
         if (bi == 0x7FFFFFFF || better(v, (int32_t)i, best, bi)) {
@@ -78,10 +79,12 @@ __global__ void __launch_bounds__(256) k_row_sum(const float* __restrict__ rows,
     const int64_t r = blockIdx.y;
     const int c = blockIdx.x, t = threadIdx.x;
     float mx = -INFINITY;
+#pragma unroll 8
     for (int k = 0; k < nch; ++k) mx = fmaxf(mx, cmax[r * nch + k]);
     const float* row = rows + r * V;
     const int64_t b = (int64_t)c * SCH, e = min(V, b + SCH);
     double s = 0.0;
+#pragma unroll 8
     for (int64_t i = b + t; i < e; i += 256) s += exp((double)((row[i] - mx) / temp));
     sd[t] = s;
     __syncthreads();
@@ -116,18 +119,31 @@ __global__ void k_row_final(int nch, const float* __restrict__ cmax,
 // ---- inverse-CDF pick over p[0..V) (double weights) by one block: chunk
 // sums, a block scan, then the crossing chunk scanned in order.  Falls back
 // to the last positive weight when rounding leaves no crossing.
-__device__ int32_t block_pick(const double* __restrict__ p, int64_t V, float u) {
+// Inverse-CDF pick over V probabilities: thread t owns the contiguous chunk
+// [t * chunk, (t + 1) * chunk) and sums it in index order.  `tr` selects the
+// chunk-transposed layout p[k * NT + t] = prob(t * chunk + k), whose loads
+// are coalesced across threads; the arithmetic is the same in both layouts.
+__device__ int32_t block_pick(const double* __restrict__ p, int64_t V, float u, bool tr) {
     __shared__ double incl[NT];
     __shared__ int32_t lastpos[NT];
     __shared__ int32_t pick;
     const int t = threadIdx.x;
     const int64_t chunk = (V + NT - 1) / NT;
     const int64_t b = t * chunk, e = min(V, b + chunk);
+    // sums in index order; the loads of eight elements are issued together
     double cs = 0.0;
     int32_t lp = -1;
-    for (int64_t i = b; i < e; ++i) {
-        cs += p[i];
-        if (p[i] > 0) lp = (int32_t)i;
+    auto at = [&](int64_t i) { return tr ? p[(i - b) * NT + t] : p[i]; };
+    for (int64_t i0 = b; i0 < e; i0 += 8) {
+        double v[8];
+#pragma unroll
+        for (int k = 0; k < 8; ++k) v[k] = i0 + k < e ? at(i0 + k) : 0.0;
+#pragma unroll
+        for (int k = 0; k < 8; ++k) {
+            if (i0 + k >= e) break;
+            cs += v[k];
+            if (v[k] > 0) lp = (int32_t)(i0 + k);
+        }
     }
     incl[t] = cs;
     lastpos[t] = lp;
@@ -146,11 +162,19 @@ __device__ int32_t block_pick(const double* __restrict__ p, int64_t V, float u) 
     const double ex = t ? incl[t - 1] : 0.0;
     if (incl[t] > target && ex <= target && b < e) {
         double c = ex;
-        for (int64_t i = b; i < e; ++i) {
-            c += p[i];
-            if (c > target) {
-                pick = (int32_t)i;
-                break;
+        bool found = false;
+        for (int64_t i0 = b; i0 < e && !found; i0 += 8) {
+            double v[8];
+#pragma unroll
+            for (int k = 0; k < 8; ++k) v[k] = i0 + k < e ? at(i0 + k) : 0.0;
+#pragma unroll
+            for (int k = 0; k < 8; ++k) {
+                if (found || i0 + k >= e) break;
+                c += v[k];
+                if (c > target) {
+                    pick = (int32_t)(i0 + k);
+                    found = true;
+                }
             }
         }
     }
@@ -307,7 +331,7 @@ __global__ void __launch_bounds__(NT) k_accept(AcceptDev a) {
                     rng = s;
                 }
                 __syncthreads();
-                const int32_t b = block_pick(a.p, V, ub2);
+                const int32_t b = block_pick(a.p, V, ub2, false);
                 if (t == 0) bonus = b;
                 __syncthreads();
                 break;
@@ -329,7 +353,8 @@ __global__ void __launch_bounds__(NT) k_accept(AcceptDev a) {
     }
 }
 
-// RATIO bonus, step 1: the normalised target of the recorded row, in parallel
+// RATIO bonus, step 1: the normalised target of the recorded row, in
+// parallel, stored chunk-transposed for the pick (see block_pick)
 __global__ void __launch_bounds__(256) k_bonus_dist(AcceptDev a) {
 #pragma clang fp contract(off)
     const int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
@@ -337,12 +362,13 @@ __global__ void __launch_bounds__(256) k_bonus_dist(AcceptDev a) {
     const int32_t c = *a.brow;
     const float* lg = c < 0 ? a.base_row : a.rows + (int64_t)c * a.V;
     const RowStats st = a.stats[c + 1];
-    a.p[i] = exp((double)((lg[i] - st.mx) / a.temp)) / st.sum;
+    const int64_t chunk = (a.V + NT - 1) / NT;
+    a.p[(i % chunk) * NT + i / chunk] = exp((double)((lg[i] - st.mx) / a.temp)) / st.sum;
 }
 
 // RATIO bonus, step 2: the inverse-CDF pick
 __global__ void __launch_bounds__(NT) k_bonus_pick(AcceptDev a) {
-    const int32_t b = block_pick(a.p, a.V, *a.bu);
+    const int32_t b = block_pick(a.p, a.V, *a.bu, true);
     if (threadIdx.x == 0) a.out[1] = b;
 }
 

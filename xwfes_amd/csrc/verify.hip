@@ -24,6 +24,8 @@ struct ftx_model {
     int64_t* npast = nullptr;
     // int8-MFMA GEMV activation operand
     int8_t* xq = nullptr;
+    // rotated q as fp16 hi + lo parts for the MFMA attention, [M][n_head][hd] each
+    _Float16* qhl = nullptr;
     // per-layer re-tiled ffn_down copies for the MFMA down kernel (or null)
     std::vector<uint8_t*> down_tiled;
     // tiled copies for the int8-MFMA row-dot kernel, [layer * LAYER_TENSORS +
@@ -54,7 +56,7 @@ struct ftx_kv {
 static void model_release(ftx_model* m) {
     if (!m) return;
     void* bufs[] = {m->norms, m->x,     m->xn,  m->qkv,   m->att, m->h,     m->part,
-                    m->toks,  m->depth, m->anc, m->npast, m->xq};
+                    m->toks,  m->depth, m->anc, m->npast, m->xq,  m->qhl};
     for (void* b : bufs)
         if (b) (void)hipFree(b);
     for (uint8_t* b : m->down_tiled)
@@ -132,7 +134,7 @@ int ftx_model_create(ftx_ctx* ctx, const ftx_model_desc* d, ftx_model** out) {
               dalloc(&m->npast, 1);
     if (ok) {
         const int64_t Kmax = std::max(D, qdim);
-        ok = dalloc(&m->xq, xq_bytes(Kmax));
+        ok = dalloc(&m->xq, xq_bytes(Kmax)) && dalloc(&m->qhl, (size_t)(2 * Mmax * qdim));
     }
     // re-tiled ffn_down copies (same bytes, MFMA-friendly order)
     m->down_tiled.assign((size_t)d->n_layer, nullptr);
@@ -427,14 +429,21 @@ int ftx_verify_step(ftx_ctx* ctx, ftx_model* m, ftx_kv* kv, const ftx_verify_arg
         RopeArgs ra{m->qkv,       m->ldq,       d.n_head, d.n_head_kv, d.head_dim,   m->depth,
                     m->npast,     d.rope_theta, d.rope_neox, kl,       vl,           kv->kv_f16,
                     kv->cap_alloc};
+        const bool mattn = attn_mfma_supported(d.head_dim, kv->kv_f16, M, d.n_head, d.n_head_kv);
+        if (mattn) {
+            ra.qh16 = m->qhl;
+            ra.ql16 = m->qhl + M * m->qdim;
+        }
         TRACED(TK_ROPE_KV, 2 * Md * m->ldq * f4 + 2 * Md * m->kdim * (double)kvel,
                launch_rope_kv(st, ra, M));
         const double attn_b =
             2.0 * (double)(npast + M) * m->kdim * (double)kvel + 2 * Md * m->qdim * f4;
-        if (attn_mfma_supported(d.head_dim, kv->kv_f16, M, d.n_head, d.n_head_kv)) {
+        if (mattn) {
             AttnMArgs am{};
             am.qkv = m->qkv;
             am.ldq = m->ldq;
+            am.qh16 = ra.qh16;
+            am.ql16 = ra.ql16;
             am.kc = (const _Float16*)kl;
             am.vt = (const _Float16*)vl;
             am.cap = kv->cap_alloc;
@@ -510,7 +519,9 @@ int ftx_accept(ftx_ctx* ctx, const ftx_accept_args* a) {
     // parents, pd
     const size_t stats_b = (size_t)(M + 1) * sizeof(RowStats);
     const size_t off_p = (stats_b + 255) & ~(size_t)255;
-    const size_t off_out = off_p + (((size_t)V * 8 + 255) & ~(size_t)255);
+    // p: V doubles, or the chunk-transposed bonus layout of ceil(V / 1024) * 1024
+    const size_t pn = (size_t)((V + 1023) / 1024 * 1024);
+    const size_t off_out = off_p + ((pn * 8 + 255) & ~(size_t)255);
     const size_t off_small = off_out + (((size_t)(M + 2) * 4 + 255) & ~(size_t)255);
     const size_t small_b = 8 + 8 + (size_t)M * 12 + 64;
     const size_t off_rs = off_small + ((small_b + 255) & ~(size_t)255);  // row-stat chunks
