@@ -1,0 +1,221 @@
+// hip_backend.cpp -- HipBackend / HipVerifier over the C ABI (include/ftx.h).
+#include "hip_backend.hpp"
+
+#include <stdexcept>
+
+namespace ftx_host {
+
+namespace {
+int64_t row_bytes(DType dt, int64_t cols) { return ftx_row_bytes((int)dt, cols); }
+}  // namespace
+
+void HipBackend::check(int rc, const char* what) const {
+    if (rc != FTX_OK) {
+        const char* msg = ctx_ ? ftx_last_error(ctx_) : "no context";
+        throw std::runtime_error(std::string("HipBackend: ") + what + ": " + (msg ? msg : ""));
+    }
+}
+
+HipBackend::HipBackend(int device) {
+    // a failed construction throws, as the reference's accelerator backends
+    // do; Engine::load then keeps the CPU path (src/engine.cpp:293-299)
+    if (ftx_create(device, &ctx_) != FTX_OK) {
+        ctx_ = nullptr;
+        throw std::runtime_error("HipBackend: no usable HIP device");
+    }
+}
+
+HipBackend::~HipBackend() {
+    for (auto& kv : tensors_) ftx_tensor_free(kv.second);
+    for (auto& kv : expert_rows_) ftx_tensor_free(kv.second);
+    if (ctx_) ftx_destroy(ctx_);
+}
+
+std::string HipBackend::name() const { return "hip"; }
+
+DeviceInfo HipBackend::info() const {
+    DeviceInfo d;
+    ftx_device_info_t di{};
+    if (ctx_ && ftx_device_info(ctx_, &di) == FTX_OK) {
+        d.name = di.name;
+        d.mem_bytes = (uint64_t)di.mem_bytes;
+    }
+    return d;  // a discrete GPU: integrated = uma = false
+}
+
+bool HipBackend::ready() const { return ctx_ != nullptr; }
+
+HipBackend::Key HipBackend::key_of(const HostTensor& W) {
+    return {W.data, {(int32_t)W.dtype, {W.ne[0], W.ne[1] * W.ne[2] * W.ne[3]}}};
+}
+
+ftx_tensor* HipBackend::resident(const HostTensor& W) {
+    const Key k = key_of(W);
+    auto it = tensors_.find(k);
+    if (it != tensors_.end()) return it->second;
+    ftx_tensor* t = nullptr;
+    const int64_t rb = row_bytes(W.dtype, W.ne[0]);
+    check(ftx_tensor_upload(ctx_, (int)W.dtype, W.ne, rb, W.data, &t), "upload");
+    tensors_[k] = t;
+    return t;
+}
+
+void HipBackend::evict(const HostTensor& W) {
+    auto it = tensors_.find(key_of(W));
+    if (it == tensors_.end()) return;
+    ftx_tensor_free(it->second);
+    tensors_.erase(it);
+}
+
+void HipBackend::matmul(const float* x, int64_t M, int64_t K, const HostTensor& W, float* y) {
+    if (K != W.cols()) throw std::runtime_error("HipBackend::matmul: K != W.cols()");
+    check(ftx_matmul(ctx_, x, M, K, resident(W), y), "matmul");
+}
+
+const void* HipBackend::resident_rows(const void* host, size_t row_stride, int64_t rows, DType dt,
+                                      int64_t cols, int64_t* dev_stride) {
+    const auto key = std::make_pair(host, row_stride * (size_t)rows);
+    auto it = expert_rows_.find(key);
+    if (it == expert_rows_.end()) {
+        ftx_tensor* t = nullptr;
+        const int64_t ne[4] = {cols, rows, 1, 1};
+        check(ftx_tensor_upload(ctx_, (int)dt, ne, (int64_t)row_stride, host, &t), "upload");
+        it = expert_rows_.emplace(key, t).first;
+    }
+    *dev_stride = ftx_tensor_nbytes(it->second) / rows;
+    return ftx_tensor_data(it->second);
+}
+
+void HipBackend::run_expert_chunk(const ExpertChunkJob& job) {
+    ftx_expert_job j{};
+    j.x = job.x;
+    j.out = job.out;
+    j.dt = (int32_t)job.dt;
+    j.M = job.M;
+    j.K = job.K;
+    j.IC = job.IC;
+    // resident rows are packed at the device row size
+    int64_t s_gu = 0, s_d = 0;
+    j.gate = resident_rows(job.gate, job.gate_up_row_stride, job.IC, job.dt, job.K, &s_gu);
+    j.up = resident_rows(job.up, job.gate_up_row_stride, job.IC, job.dt, job.K, &s_gu);
+    j.down = resident_rows(job.down, job.down_row_stride, job.IC, job.dt, job.K, &s_d);
+    j.gate_up_row_stride = s_gu;
+    j.down_row_stride = s_d;
+    check(ftx_expert_chunk(ctx_, &j), "run_expert_chunk");
+}
+
+void* HipBackend::alloc_staging(size_t bytes) { return ftx_alloc_staging(ctx_, bytes); }
+void HipBackend::free_staging(void* p) { check(ftx_free_staging(ctx_, p), "free_staging"); }
+void HipBackend::stage(void* dst, const void* src, size_t bytes) {
+    check(ftx_stage(ctx_, dst, src, bytes), "stage");
+}
+void HipBackend::sync() { check(ftx_sync(ctx_), "sync"); }
+
+// ------------------------------------------------------------------ verifier
+
+HipVerifier::HipVerifier(HipBackend& be, const ModelConfig& cfg, const ModelWeights& w,
+                         int64_t ctx_cap, int64_t max_tokens, bool kv_f16)
+    : be_(be), cfg_(cfg), max_tokens_(max_tokens) {
+    if ((int64_t)w.layers.size() != cfg.n_layer)
+        throw std::runtime_error("HipVerifier: layer count does not match the config");
+    std::vector<const ftx_tensor*> layers;
+    for (const auto& L : w.layers) {
+        if (L.size() != FTX_LAYER_TENSORS)
+            throw std::runtime_error("HipVerifier: a layer needs 9 tensors");
+        for (const auto& t : L) layers.push_back(be_.resident(t));
+    }
+    ftx_model_desc d{};
+    d.n_layer = cfg.n_layer;
+    d.n_embd = cfg.n_embd;
+    d.n_head = cfg.n_head;
+    d.n_head_kv = cfg.n_head_kv;
+    d.head_dim = cfg.head_dim;
+    d.n_ff = cfg.n_ff;
+    d.vocab = cfg.vocab;
+    d.rms_eps = cfg.rms_eps;
+    d.rope_neox = cfg.rope_neox ? 1 : 0;
+    d.rope_theta = cfg.rope_theta;
+    d.tok_embd = be_.resident(w.tok_embd);
+    d.out_norm = be_.resident(w.out_norm);
+    d.output = w.output.data ? be_.resident(w.output) : nullptr;
+    d.layers = layers.data();
+    d.max_tokens = max_tokens;
+    be_.check(ftx_model_create(be_.ctx(), &d, &model_), "model_create");
+    be_.check(ftx_kv_create(be_.ctx(), model_, ctx_cap, kv_f16 ? FTX_KV_F16 : FTX_KV_F32, &kv_),
+              "kv_create");
+    logits_ = (float*)be_.alloc_staging((size_t)(max_tokens * cfg.vocab) * sizeof(float));
+    if (!logits_) throw std::runtime_error("HipVerifier: logits allocation failed");
+}
+
+HipVerifier::~HipVerifier() {
+    if (logits_) ftx_free_staging(be_.ctx(), logits_);
+    if (kv_) ftx_kv_free(kv_);
+    if (model_) ftx_model_free(model_);
+}
+
+const float* HipVerifier::extend_verify(const std::vector<int32_t>& props,
+                                        const std::vector<int32_t>& parents, bool advance) {
+    const int64_t M = (int64_t)props.size();
+    if (M < 1 || M > max_tokens_) throw std::runtime_error("HipVerifier: bad draft length");
+    if (!parents.empty() && (int64_t)parents.size() != M)
+        throw std::runtime_error("HipVerifier: parents must match the draft");
+    ftx_verify_args a{};
+    a.M = M;
+    a.tokens = props.data();
+    a.parents = parents.empty() ? nullptr : parents.data();
+    a.logits = logits_;
+    a.advance = advance ? 1 : 0;
+    be_.check(ftx_verify_step(be_.ctx(), model_, kv_, &a), "verify_step");
+    return logits_;
+}
+
+void HipVerifier::truncate_to(int64_t npast) { be_.check(ftx_kv_truncate(kv_, npast), "truncate"); }
+
+int64_t HipVerifier::npast() const {
+    void *k = nullptr, *v = nullptr;
+    int64_t n = 0;
+    be_.check(ftx_kv_pointers(kv_, &k, &v, &n), "kv_pointers");
+    return n;
+}
+
+void HipVerifier::write_kv(const void* k, const void* v) { be_.check(ftx_kv_write(kv_, k, v), "kv_write"); }
+void HipVerifier::read_kv(void* k, void* v) { be_.check(ftx_kv_read(kv_, k, v), "kv_read"); }
+
+Accepted accept_on_device(HipBackend& be, int64_t V, const float* base_row, const float* rows,
+                          const std::vector<int32_t>& props, AcceptMode mode, float temp,
+                          uint64_t& rng, const std::vector<float>& pd,
+                          const std::vector<int32_t>& parents, const float* q) {
+    const int64_t M = (int64_t)props.size();
+    Accepted out;
+    out.nodes.assign((size_t)(M > 0 ? M : 1), -1);
+    int32_t n_acc = 0;
+    ftx_accept_args a{};
+    a.base_row = base_row;
+    a.rows = rows;
+    a.q = q;
+    a.M = M;
+    a.V = V;
+    a.props = props.data();
+    a.parents = parents.empty() ? nullptr : parents.data();
+    a.pd = pd.empty() ? nullptr : pd.data();
+    a.mode = (int32_t)mode;
+    a.temp = temp;
+    a.rng = &rng;
+    a.accepted = out.nodes.data();
+    a.n_acc = &n_acc;
+    a.bonus = &out.bonus;
+    a.margin = &out.margin;
+    be.check(ftx_accept(be.ctx(), &a), "accept");
+    out.nodes.resize((size_t)n_acc);
+    return out;
+}
+
+Accepted HipVerifier::accept(const float* base_row, const float* rows,
+                             const std::vector<int32_t>& props, AcceptMode mode, float temp,
+                             uint64_t& rng, const std::vector<float>& pd,
+                             const std::vector<int32_t>& parents, const float* q) {
+    return accept_on_device(be_, cfg_.vocab, base_row, rows, props, mode, temp, rng, pd, parents,
+                            q);
+}
+
+}  // namespace ftx_host

@@ -1,0 +1,188 @@
+// hip_backend.hpp -- C++ host side of the MI355X verify path, above the C ABI
+// of include/ftx.h.
+//
+// HipBackend mirrors the reference engine's backend interface, ft::IBackend
+// (include/ft/backend.h:21-40): the same member names, argument meanings and
+// error behaviour (std::runtime_error), so that a maintainer can derive it
+// from ft::IBackend and construct it where Engine::load builds its
+// accelerator backend (src/engine.cpp:291-300).  The value types below
+// restate the reference's HostTensor, DeviceInfo and ExpertChunkJob fields
+// (include/ft/types.h:119-147, include/ft/backend.h:7-19).
+//
+// HipVerifier is the device-resident verify step: Engine::extend_verify ->
+// Engine::forward(M) over the KV cache (src/engine.cpp:669-674, 461-596),
+// truncate_to (src/engine.cpp:423-428), and the acceptance of
+// accept_chain_greedy / accept_chain_sampling plus the bonus token
+// (src/spec.cpp:203-238, 302-311), with draft-tree and residual extensions.
+#pragma once
+
+#include <cstddef>
+#include <cstdint>
+#include <map>
+#include <memory>
+#include <string>
+#include <utility>
+#include <vector>
+
+#include "../../include/ftx.h"
+
+namespace ftx_host {
+
+// the reference's DType values (include/ft/types.h:20-27) plus GGUF K-quants
+enum class DType : int32_t {
+    F32 = FTX_F32,
+    F16 = FTX_F16,
+    Q4_0 = FTX_Q4_0,
+    Q4_1 = FTX_Q4_1,
+    Q8_0 = FTX_Q8_0,
+    Q4_K = FTX_Q4_K,
+    Q6_K = FTX_Q6_K,
+    BF16 = FTX_BF16,
+};
+
+// a weight tensor as the engine hands it to its backend: ne[0] = cols
+// (contiguous, blocked), ne[1] = rows, data = GGUF bytes in host memory
+struct HostTensor {
+    std::string name;
+    int64_t ne[4] = {1, 1, 1, 1};
+    int32_t n_dims = 0;
+    DType dtype = DType::F32;
+    const uint8_t* data = nullptr;
+    size_t nbytes = 0;
+    int64_t cols() const { return ne[0]; }
+    int64_t rows() const { return ne[1]; }
+};
+
+struct DeviceInfo {
+    std::string name;
+    bool integrated = false;
+    bool uma = false;
+    uint64_t mem_bytes = 0;
+};
+
+// gate / up / down point at IC rows of raw expert weights (host memory)
+struct ExpertChunkJob {
+    const float* x = nullptr;
+    float* out = nullptr;
+    const void* gate = nullptr;
+    const void* up = nullptr;
+    const void* down = nullptr;
+    DType dt = DType::F32;
+    int64_t M = 0;
+    int64_t K = 0;
+    int64_t IC = 0;
+    size_t gate_up_row_stride = 0;
+    size_t down_row_stride = 0;
+};
+
+class HipBackend {
+public:
+    explicit HipBackend(int device = 0);
+    ~HipBackend();
+    HipBackend(const HipBackend&) = delete;
+    HipBackend& operator=(const HipBackend&) = delete;
+
+    std::string name() const;
+    DeviceInfo info() const;
+    bool ready() const;
+
+    // y[m*N + n] = sum_k x[m*K + k] * W[n, k] for m < M, n < W.rows(); x and
+    // y are host or device memory; W is uploaded once and kept resident,
+    // keyed by (W.data, dtype, shape): as in the engine, whose weights live in
+    // the GGUF mapping for the backend's lifetime, the bytes behind a key
+    // must not change while the backend holds them (evict() drops a copy)
+    void matmul(const float* x, int64_t M, int64_t K, const HostTensor& W, float* y);
+
+    // h[m, i] = silu(x_m . gate_i) * (x_m . up_i); out[m, :] += sum_i h[m, i] down_i
+    void run_expert_chunk(const ExpertChunkJob& job);
+
+    void* alloc_staging(size_t bytes);
+    void free_staging(void* p);
+    void stage(void* dst, const void* src, size_t bytes);
+    void sync();
+
+    // the resident copy of W (uploaded on first use)
+    ftx_tensor* resident(const HostTensor& W);
+    void evict(const HostTensor& W);
+    ftx_ctx* ctx() const { return ctx_; }
+    void check(int rc, const char* what) const;
+
+private:
+    const void* resident_rows(const void* host, size_t row_stride, int64_t rows, DType dt,
+                              int64_t cols, int64_t* dev_stride);
+    ftx_ctx* ctx_ = nullptr;
+    using Key = std::pair<const void*, std::pair<int32_t, std::pair<int64_t, int64_t>>>;
+    static Key key_of(const HostTensor& W);
+    std::map<Key, ftx_tensor*> tensors_;
+    std::map<std::pair<const void*, size_t>, ftx_tensor*> expert_rows_;
+};
+
+struct ModelConfig {
+    int64_t n_layer = 0, n_embd = 0, n_head = 0, n_head_kv = 0, head_dim = 0, n_ff = 0, vocab = 0;
+    float rms_eps = 1e-5f;
+    bool rope_neox = false;
+    double rope_theta = 10000.0;
+};
+
+// per-layer tensors in the order attn_norm, q, k, v, o, ffn_norm, gate, up,
+// down (down in the reference orientation: n_ff rows of n_embd columns)
+struct ModelWeights {
+    HostTensor tok_embd, out_norm, output;  // output.data == nullptr: tied
+    std::vector<std::vector<HostTensor>> layers;
+};
+
+enum class AcceptMode : int32_t {
+    Greedy = FTX_ACCEPT_GREEDY,
+    Ratio = FTX_ACCEPT_RATIO,
+    Residual = FTX_ACCEPT_RESIDUAL,
+};
+
+struct Accepted {
+    std::vector<int32_t> nodes;  // accepted node ids, root first
+    int32_t bonus = -1;          // the token that follows them
+    float margin = 0.f;          // min |u - ratio| over the stochastic decisions
+};
+
+// acceptance over device logits (base_row [V], rows [M][V]); rng is the
+// SplitMix64 state (in / out)
+Accepted accept_on_device(HipBackend& be, int64_t V, const float* base_row, const float* rows,
+                          const std::vector<int32_t>& props, AcceptMode mode, float temp,
+                          uint64_t& rng, const std::vector<float>& pd = {},
+                          const std::vector<int32_t>& parents = {}, const float* q = nullptr);
+
+class HipVerifier {
+public:
+    HipVerifier(HipBackend& be, const ModelConfig& cfg, const ModelWeights& w, int64_t ctx_cap,
+                int64_t max_tokens, bool kv_f16 = true);
+    ~HipVerifier();
+    HipVerifier(const HipVerifier&) = delete;
+    HipVerifier& operator=(const HipVerifier&) = delete;
+
+    // forward of the draft tokens against the committed context; parents
+    // empty = linear chain, else parents[i] in {-1, 0..i-1}; returns the
+    // device logits [M][vocab], valid until the next call
+    const float* extend_verify(const std::vector<int32_t>& props,
+                               const std::vector<int32_t>& parents = {}, bool advance = false);
+    void truncate_to(int64_t npast);
+    int64_t npast() const;
+    // whole cache from / to host arrays [n_layer][cap][n_head_kv*head_dim]
+    void write_kv(const void* k, const void* v);
+    void read_kv(void* k, void* v);
+
+    // acceptance over device logits; rng is the SplitMix64 state (in / out)
+    Accepted accept(const float* base_row, const float* rows, const std::vector<int32_t>& props,
+                    AcceptMode mode, float temp, uint64_t& rng, const std::vector<float>& pd = {},
+                    const std::vector<int32_t>& parents = {}, const float* q = nullptr);
+
+    const ModelConfig& config() const { return cfg_; }
+
+private:
+    HipBackend& be_;
+    ModelConfig cfg_;
+    ftx_model* model_ = nullptr;
+    ftx_kv* kv_ = nullptr;
+    float* logits_ = nullptr;
+    int64_t max_tokens_ = 0;
+};
+
+}  // namespace ftx_host
