@@ -326,8 +326,9 @@ int ftx_matmul(ftx_ctx* ctx, const float* x, int64_t M, int64_t K, const ftx_ten
     GemvSeg seg{W->data, W->dtype, W->row_bytes, N, s.y, N};
     if (mv) {
         int8_t* xq = (int8_t*)extra;
-        FTX_HIP(ctx, launch_xq_prep(ctx->stream, s.x, K, nullptr, 0.f, K, M, xq));
-        FTX_HIP(ctx, launch_mv(ctx->stream, &seg, 1, xq, K, M, EPI_STORE, ctx->cu_count));
+        FTX_HIP(ctx, launch_xq_prep(ctx->stream, const_cast<float*>(s.x), K, nullptr, nullptr, 0, 0,
+                                    K, M, xq));
+        FTX_HIP(ctx, launch_mv(ctx->stream, &seg, 1, xq, K, M, EPI_STORE, ctx->cu_count, 0, 0.f));
     } else {
         FTX_HIP(ctx, launch_gemv(ctx->stream, &seg, 1, s.x, K, K, M, EPI_STORE));
     }

@@ -128,10 +128,14 @@ hipError_t launch_down(hipStream_t st, const uint8_t* W, int dt, int64_t row_byt
                        int64_t n_in, int64_t N, const float* h, int64_t ldh, int64_t M,
                        float* y, int64_t ldy, float* part);
 
-// int8-MFMA GEMV (k_mfma.hip): activation operand prep + row-dot product
+// int8-MFMA GEMV (k_mfma.hip): activation operand prep + row-dot product.
+// The prep optionally folds S split partials part[s][m][ldpart] into x
+// (written back) and takes an RMSNorm weight; a normed operand is consumed
+// with launch_mv(..., normed = 1, eps).
 size_t xq_bytes(int64_t K);
-hipError_t launch_xq_prep(hipStream_t st, const float* x, int64_t ldx, const float* normw,
-                          float eps, int64_t K, int64_t M, int8_t* xq);
+hipError_t launch_xq_prep(hipStream_t st, float* x, int64_t ldx, const float* normw,
+                          const float* part, int S, int64_t ldpart, int64_t K, int64_t M,
+                          int8_t* xq);
 bool mv_supported(int dt, int64_t K, int64_t M);
 // the SwiGLU epilogue needs the whole contraction in one pass
 bool mv_swiglu_supported(int64_t K);
@@ -143,7 +147,7 @@ size_t mv_tiled_bytes(int dt, int64_t N, int64_t K, int rpt);
 hipError_t launch_mv_tile(hipStream_t st, const uint8_t* src, int64_t src_row_bytes, int dt,
                           int64_t N, int64_t K, int rpt, uint8_t* dst);
 hipError_t launch_mv(hipStream_t st, const GemvSeg* segs, int nseg, const int8_t* xq, int64_t K,
-                     int64_t M, int epi, int cu_count);
+                     int64_t M, int epi, int cu_count, int normed, float eps);
 
 hipError_t launch_part_reduce(hipStream_t st, const float* part, int S, int64_t N, int64_t M,
                               float* y, int64_t ldy);
@@ -154,9 +158,11 @@ size_t down_tiled_bytes(int dt, int64_t n_in, int64_t N);
 hipError_t launch_down_tile(hipStream_t st, const uint8_t* src, int64_t src_row_bytes, int dt,
                             int64_t n_in, int64_t N, uint8_t* dst);
 size_t down_mfma_part_floats(int64_t n_in, int64_t N, int cu_count);
+// splits == null: the split partials are added into y here; otherwise the
+// partials are left in part[S][8][N] for the caller to fold and *splits = S
 hipError_t launch_down_mfma(hipStream_t st, int dt, const uint8_t* tiled, int64_t n_in, int64_t N,
                             const float* h, int64_t ldh, int64_t M, float* y, int64_t ldy,
-                            float* part, int cu_count);
+                            float* part, int cu_count, int* splits);
 
 // quantise rows (synthetic model builder)
 hipError_t launch_quantize(hipStream_t st, const float* src, int dt, int64_t ncols,

@@ -372,7 +372,7 @@ size_t down_mfma_part_floats(int64_t n_in, int64_t N, int cu_count) {
 
 hipError_t launch_down_mfma(hipStream_t st, int dt, const uint8_t* tiled, int64_t n_in, int64_t N,
                             const float* h, int64_t ldh, int64_t M, float* y, int64_t ldy,
-                            float* part, int cu_count) {
+                            float* part, int cu_count, int* splits) {
     DownArgs a{};
     uint8_t *qs, *qh, *hdr, *d6;
     down_planes(dt, n_in, N, (uint8_t*)tiled, &qs, &qh, &hdr, &d6);
@@ -407,5 +407,9 @@ hipError_t launch_down_mfma(hipStream_t st, int dt, const uint8_t* tiled, int64_
         hipLaunchKernelGGL(k_down_mfma<FTX_Q6_K>, grid, dim3(256), 0, st, a);
     hipError_t e = hipGetLastError();
     if (e != hipSuccess) return e;
+    if (splits) {
+        *splits = (int)S;
+        return hipSuccess;
+    }
     return launch_part_reduce(st, part, (int)S, N, M, y, ldy);
 }

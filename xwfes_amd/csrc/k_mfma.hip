@@ -54,47 +54,69 @@ __device__ __forceinline__ void reg_fence8(int* v) {
 
 // ---------------------------------------------------------------- prep
 // One wave per (256-element super-block sb, activation row m < 8); rows
-// m >= M are written as zeros.  Optional RMSNorm (src/engine.cpp:23-41) in
-// front: each wave reduces the sum of squares of its whole row (L2 hits).
-// Lane l quantises elements 4l .. 4l+3 of the super-block.
-__global__ void __launch_bounds__(64) k_xq_prep(const float* __restrict__ x, int64_t ldx,
-                                                const float* __restrict__ normw, float eps,
-                                                int64_t K, int M, int8_t* __restrict__ frag,
+// m >= M are written as zeros.  Lane l takes elements 4l .. 4l+3.
+//  - fold (part != null): x += sum_s part[s][m][.] over the S split
+//    partials of the previous ffn_down, in split order, written back to x
+//    (the residual add of src/engine.cpp:274-275);
+//  - RMSNorm (src/engine.cpp:23-41) in front when normw is given: the limbs
+//    of x * w are formed with the block scale max|x * w| / 127 -- the limbs
+//    do not depend on the row's 1 / rms factor, which the consuming GEMV
+//    applies to the block scales from the per-block sums of x^2 stored in
+//    ssq[sb][m].
+__global__ void __launch_bounds__(64) k_xq_prep(float* __restrict__ x, int64_t ldx,
+                                                const float* __restrict__ normw,
+                                                const float* __restrict__ part, int S,
+                                                int64_t ldpart, int64_t K, int M,
+                                                int8_t* __restrict__ frag,
                                                 int8_t* __restrict__ xs32,
                                                 int8_t* __restrict__ xs16,
-                                                float* __restrict__ scale) {
+                                                float* __restrict__ scale,
+                                                float* __restrict__ ssq) {
 #pragma clang fp contract(off)
     const int64_t sb = blockIdx.x;
     const int m = blockIdx.y, l = threadIdx.x;
     const bool live = m < M;
-    const float* row = x + (int64_t)m * ldx;
+    float* row = x + (int64_t)m * ldx;
+    const int64_t k0 = sb * 256 + 4 * l;
     float v[4] = {0.f, 0.f, 0.f, 0.f};
     if (live) {
-        const float4 t = *(const float4*)(row + sb * 256 + 4 * l);
+        const float4 t = *(const float4*)(row + k0);
         v[0] = t.x;
         v[1] = t.y;
         v[2] = t.z;
         v[3] = t.w;
-        if (normw) {
-            // K / 256 independent loads per lane, issued back to back
-            float ss = 0.f;
-#pragma unroll 16
-            for (int64_t k = 4 * l; k < K; k += 256) {
-                const float4 u = *(const float4*)(row + k);
-                ss += u.x * u.x;
-                ss += u.y * u.y;
-                ss += u.z * u.z;
-                ss += u.w * u.w;
+        if (part) {
+            float4 acc = {0.f, 0.f, 0.f, 0.f};
+#pragma unroll 8
+            for (int s = 0; s < S; ++s) {
+                const float4 p = *(const float4*)(part + ((int64_t)s * 8 + m) * ldpart + k0);
+                acc.x += p.x;
+                acc.y += p.y;
+                acc.z += p.z;
+                acc.w += p.w;
             }
+            v[0] += acc.x;
+            v[1] += acc.y;
+            v[2] += acc.z;
+            v[3] += acc.w;
+            *(float4*)(row + k0) = make_float4(v[0], v[1], v[2], v[3]);
+        }
+        if (normw) {
+            float ss = v[0] * v[0];
+            ss += v[1] * v[1];
+            ss += v[2] * v[2];
+            ss += v[3] * v[3];
 #pragma unroll
             for (int o = 32; o > 0; o >>= 1) ss += __shfl_xor(ss, o, 64);
-            const float inv = 1.f / sqrtf(ss / (float)K + eps);
-            const float4 w4 = *(const float4*)(normw + sb * 256 + 4 * l);
-            v[0] = v[0] * inv * w4.x;
-            v[1] = v[1] * inv * w4.y;
-            v[2] = v[2] * inv * w4.z;
-            v[3] = v[3] * inv * w4.w;
+            if (l == 0) ssq[sb * 8 + m] = ss;
+            const float4 w4 = *(const float4*)(normw + k0);
+            v[0] = v[0] * w4.x;
+            v[1] = v[1] * w4.y;
+            v[2] = v[2] * w4.z;
+            v[3] = v[3] * w4.w;
         }
+    } else if (normw && l == 0) {
+        ssq[sb * 8 + m] = 0.f;
     }
     float mx = fmaxf(fmaxf(fabsf(v[0]), fabsf(v[1])), fmaxf(fabsf(v[2]), fabsf(v[3])));
 #pragma unroll
@@ -171,6 +193,9 @@ struct MvArgs {
     const int8_t* xs32;
     const int8_t* xs16;
     const float* scale;
+    const float* ssq;   // per-block sums of x^2 [sb][8] when the input is RMS-normed, else null
+    float eps;
+    int64_t K;
 };
 
 constexpr int MV_WAVES = 8;  // at most 8 waves per unit (512 threads)
@@ -369,7 +394,8 @@ struct MvX {
 };
 
 template <int DT>
-__device__ __forceinline__ void mv_load_x(MvX<DT>& x, const MvArgs& a, int sb, int col, int g) {
+__device__ __forceinline__ void mv_load_x(MvX<DT>& x, const MvArgs& a, int sb, int col, int g,
+                                          const float* inv) {
     if constexpr (DT == FTX_Q4_K) {
         const int8_t* fp = a.frag + (((int64_t)sb * 16 + g) * 16 + (col & 15)) * 16;
 #pragma unroll
@@ -381,7 +407,8 @@ __device__ __forceinline__ void mv_load_x(MvX<DT>& x, const MvArgs& a, int sb, i
         for (int p = 0; p < 8; ++p) x.x8[p] = *(const long*)(fp + 512 * p);
         x.ax = ld16g(a.xs16 + ((int64_t)sb * 32 + col) * 16);
     }
-    x.s4 = *(const float4*)(a.scale + (int64_t)sb * 8 + 4 * g);
+    const float4 s4 = *(const float4*)(a.scale + (int64_t)sb * 8 + 4 * g);
+    x.s4 = make_float4(s4.x * inv[0], s4.y * inv[1], s4.z * inv[2], s4.w * inv[3]);
 }
 
 template <int DT>
@@ -393,10 +420,21 @@ __device__ __forceinline__ void mv_block(const MvW<DT>& w, const MvX<DT>& x, int
         q6k_block(w.w, w.w + 4, w.w[6], h2f(w.d), x.x8, x.ax, x.s4, col, g, acc);
 }
 
+// items in flight ahead of the one being computed, within the register
+// budget of each instantiation (Q6_K blocks are 1.5x Q4_K's)
+template <int DT, bool PAIR>
+constexpr int mv_depth() {
+#ifdef MV_DEPTH_Q4
+    if (DT == FTX_Q4_K) return MV_DEPTH_Q4;
+#endif
+    return DT == FTX_Q4_K ? 1 : (PAIR ? 0 : 1);
+}
+
 // grid = units; block = W waves (W divides the super-block count, W <= 8);
-// at least 3 waves per SIMD fit (<= 168 VGPRs)
+// at least 3 waves per SIMD fit (<= 168 VGPRs), 2 for the SwiGLU pairs,
+// whose launches hold fewer waves per CU
 template <int DT, bool TILED, bool PAIR>
-__global__ void __launch_bounds__(64 * MV_WAVES) __attribute__((amdgpu_waves_per_eu(3)))
+__global__ void __launch_bounds__(64 * MV_WAVES) __attribute__((amdgpu_waves_per_eu(PAIR ? 2 : 3)))
 k_mv(MvArgs a) {
     __shared__ float part[PAIR ? 2 : 1][MV_WAVES][256];  // [tile of unit][wave][m * 32 + col]
     const int w = threadIdx.x >> 6, lane = threadIdx.x & 63, col = lane & 31, g = lane >> 5;
@@ -429,29 +467,59 @@ k_mv(MvArgs a) {
     for (int t = 0; t < tpu; ++t)
 #pragma unroll
         for (int r = 0; r < 8; ++r) acc[t][r] = 0.f;
-    // the next item's weights in flight during this item's arithmetic (the
-    // last item re-reads its own block), except for Q6_K SwiGLU pairs whose
-    // larger blocks do not fit twice in the register budget
-    constexpr bool PF = DT == FTX_Q4_K || !PAIR;
-    MvW<DT> cur, nxt;
-    if (PF) load(cur, 0, sb0);
-    MvX<DT> x;
-    for (int i = 0; i < nit; ++i) {
-        const int ti = i % tpu, sb = sb0 + i / tpu;
-        if (ti == 0) mv_load_x<DT>(x, a, sb, col, g);
-        if constexpr (PF) {
-            const int j = i + 1 < nit ? i + 1 : i;
-            __builtin_amdgcn_sched_barrier(0);
-            load(nxt, j % tpu, sb0 + j / tpu);
-            __builtin_amdgcn_sched_barrier(0);
-        } else {
-            load(cur, ti, sb);
+    // the weights of the next D items are in flight during an item's
+    // arithmetic (a ring of D + 1 register buffers; loads past the last item
+    // re-read it)
+    constexpr int D = mv_depth<DT, PAIR>();
+    MvW<DT> buf[D + 1];
+    auto item_load = [&](MvW<DT>& o, int j) {
+        j = j < nit ? j : nit - 1;
+        load(o, j % tpu, sb0 + j / tpu);
+    };
+#pragma unroll
+    for (int d = 0; d < D; ++d) item_load(buf[d], d);
+    // the RMSNorm factor 1 / rms of rows m = 4g .. 4g+3 (src/engine.cpp:23-41)
+    float inv[4] = {1.f, 1.f, 1.f, 1.f};
+    if (a.ssq) {
+        // lanes col and col ^ 16 each sum the super-blocks b = col % 16 + 16 k,
+        // then the 16-lane butterfly gives every lane the row totals of its g
+        float4 ss = {0.f, 0.f, 0.f, 0.f};
+        for (int b = col & 15; b < a.nsb; b += 16) {
+            const float4 t = *(const float4*)(a.ssq + (int64_t)b * 8 + 4 * g);
+            ss.x += t.x;
+            ss.y += t.y;
+            ss.z += t.z;
+            ss.w += t.w;
         }
-        if (!PAIR || ti == 0)
-            mv_block<DT>(cur, x, col, g, acc[0]);
-        else
-            mv_block<DT>(cur, x, col, g, acc[tpu - 1]);
-        if constexpr (PF) cur = nxt;
+#pragma unroll
+        for (int o = 1; o < 16; o <<= 1) {
+            ss.x += __shfl_xor(ss.x, o, 64);
+            ss.y += __shfl_xor(ss.y, o, 64);
+            ss.z += __shfl_xor(ss.z, o, 64);
+            ss.w += __shfl_xor(ss.w, o, 64);
+        }
+        const float kf = (float)a.K;
+        inv[0] = 1.f / sqrtf(ss.x / kf + a.eps);
+        inv[1] = 1.f / sqrtf(ss.y / kf + a.eps);
+        inv[2] = 1.f / sqrtf(ss.z / kf + a.eps);
+        inv[3] = 1.f / sqrtf(ss.w / kf + a.eps);
+    }
+    MvX<DT> x;
+    for (int i0 = 0; i0 < nit; i0 += D + 1) {
+#pragma unroll
+        for (int d = 0; d <= D; ++d) {
+            const int i = i0 + d;
+            if (i >= nit) break;
+            const int ti = i % tpu, sb = sb0 + i / tpu;
+            if (ti == 0) mv_load_x<DT>(x, a, sb, col, g, inv);
+            __builtin_amdgcn_sched_barrier(0);
+            item_load(buf[(d + D) % (D + 1)], i + D);
+            __builtin_amdgcn_sched_barrier(0);
+            if (!PAIR || ti == 0)
+                mv_block<DT>(buf[d], x, col, g, acc[0]);
+            else
+                mv_block<DT>(buf[d], x, col, g, acc[tpu - 1]);
+        }
     }
     // lane (col, g) holds rows m = 4g + r of weight row col of each tile
     float v[tpu][4];
@@ -508,18 +576,22 @@ __global__ void __launch_bounds__(256) k_part_reduce(const float* __restrict__ p
 
 }  // namespace
 
-// fragments K*16 | xs32 K | xs16 2K | scales (K/256)*8 floats
-size_t xq_bytes(int64_t K) { return (size_t)(K * 16 + K + K * 2 + K / 8 + 64); }
+// fragments K*16 | xs32 K | xs16 2K | scales (K/256)*8 floats | ssq (K/256)*8 floats
+size_t xq_bytes(int64_t K) { return (size_t)(K * 16 + K + K * 2 + K / 8 + K / 8 + 64); }
 
-hipError_t launch_xq_prep(hipStream_t st, const float* x, int64_t ldx, const float* normw,
-                          float eps, int64_t K, int64_t M, int8_t* xq) {
+static float* xq_scale(int8_t* xq, int64_t K) { return (float*)(xq + K * 16 + K + K * 2); }
+static float* xq_ssq(int8_t* xq, int64_t K) { return xq_scale(xq, K) + K / 32; }
+
+hipError_t launch_xq_prep(hipStream_t st, float* x, int64_t ldx, const float* normw,
+                          const float* part, int S, int64_t ldpart, int64_t K, int64_t M,
+                          int8_t* xq) {
     if (K % 4096 || K > 16384) return hipErrorInvalidValue;
     int8_t* frag = xq;
     int8_t* xs32 = xq + K * 16;
     int8_t* xs16 = xs32 + K;
-    float* scale = (float*)(xs16 + K * 2);
-    hipLaunchKernelGGL(k_xq_prep, dim3((unsigned)(K / 256), 8), dim3(64), 0, st, x, ldx, normw, eps,
-                       K, (int)M, frag, xs32, xs16, scale);
+    hipLaunchKernelGGL(k_xq_prep, dim3((unsigned)(K / 256), 8), dim3(64), 0, st, x, ldx, normw,
+                       part, S, ldpart, K, (int)M, frag, xs32, xs16, xq_scale(xq, K),
+                       xq_ssq(xq, K));
     return hipGetLastError();
 }
 
@@ -567,7 +639,7 @@ hipError_t launch_mv_tile(hipStream_t st, const uint8_t* src, int64_t src_row_by
 // layout or all tiled (GemvSeg::tiled, with the tile rows they were tiled
 // with); one launch per dtype over that dtype's segments
 hipError_t launch_mv(hipStream_t st, const GemvSeg* segs, int nseg, const int8_t* xq, int64_t K,
-                     int64_t M, int epi, int cu_count) {
+                     int64_t M, int epi, int cu_count, int normed, float eps) {
     if (nseg < 1 || nseg > 3 || M < 1 || M > 8 || K % 4096 || K > 16384)
         return hipErrorInvalidValue;
     if (epi == EPI_SWIGLU && (nseg != 2 || segs[0].N != segs[1].N || segs[0].dt != segs[1].dt ||
@@ -603,7 +675,10 @@ hipError_t launch_mv(hipStream_t st, const GemvSeg* segs, int nseg, const int8_t
         a.frag = xq;
         a.xs32 = xq + K * 16;
         a.xs16 = xq + K * 16 + K;
-        a.scale = (const float*)(xq + K * 16 + K + K * 2);
+        a.scale = xq_scale((int8_t*)xq, K);
+        a.ssq = normed ? xq_ssq((int8_t*)xq, K) : nullptr;
+        a.eps = eps;
+        a.K = K;
         // waves per unit: up to ~8 waves per CU over the launch (measured
         // best on the 8B shapes: gate/up W = 4, attention projections 8)
         int W = 1;

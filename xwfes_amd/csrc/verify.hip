@@ -375,9 +375,13 @@ int ftx_verify_step(ftx_ctx* ctx, ftx_model* m, ftx_kv* kv, const ftx_verify_arg
     // One projection: x (row stride ldx) [-> RMSNorm] -> weight segments.  The
     // int8-MFMA path runs when every segment qualifies (the norm is fused
     // into its activation prep); the generic kernels run otherwise.
-    auto project = [&](int kind, double bytes, const float* xin, int64_t ldx, const float* normw,
+    // split partials of the last ffn_down not yet added into x (folded by the
+    // next projection's activation prep, or added here before a generic one)
+    int fold_S = 0;
+    auto project = [&](int kind, double bytes, float* xin, int64_t ldx, const float* normw,
                        const ftx_tensor* const* ts, GemvSeg* segs, int nseg, int64_t K, int epi,
                        int64_t tix0, const int* tix) -> int {
+        const bool fold = fold_S > 0 && xin == m->x;
         if (mv_all(ts, nseg, K, M) && (epi != EPI_SWIGLU || mv_swiglu_supported(K))) {
             // the tiled copies when every segment has one
             bool all = true;
@@ -387,11 +391,19 @@ int ftx_verify_step(ftx_ctx* ctx, ftx_model* m, ftx_kv* kv, const ftx_verify_arg
                 segs[i].tiled = 1;
                 segs[i].rpt = m->mvt_rpt[tix0 + tix[i]];
             }
-            TRACED(TK_XQ_PREP, Md * K * f4 + 19.0 * K,
-                   launch_xq_prep(st, xin, ldx, normw, eps, K, M, m->xq));
+            TRACED(TK_XQ_PREP, Md * K * f4 * (fold ? 2.0 + fold_S : 1.0) + 19.0 * K,
+                   launch_xq_prep(st, xin, ldx, normw, fold ? m->downpart : nullptr,
+                                  fold ? fold_S : 0, D, K, M, m->xq));
+            if (fold) fold_S = 0;
             TRACED(kind, bytes,
-                   launch_mv(st, segs, nseg, m->xq, K, M, epi, ctx->cu_count));
+                   launch_mv(st, segs, nseg, m->xq, K, M, epi, ctx->cu_count, normw != nullptr,
+                             eps));
             return FTX_OK;
+        }
+        if (fold) {
+            TRACED(TK_DOWN, Md * D * f4 * (2.0 + fold_S),
+                   launch_part_reduce(st, m->downpart, fold_S, D, M, m->x, D));
+            fold_S = 0;
         }
         const float* src = xin;
         int64_t lds = ldx;
@@ -476,7 +488,7 @@ int ftx_verify_step(ftx_ctx* ctx, ftx_model* m, ftx_kv* kv, const ftx_verify_arg
         if (m->down_tiled[l] && down_mfma_supported(T[FTX_T_DOWN]->dtype, F, D, M))
             TRACED(TK_DOWN, down_b,
                    launch_down_mfma(st, T[FTX_T_DOWN]->dtype, m->down_tiled[l], F, D, m->h, F, M,
-                                    m->x, D, m->downpart, ctx->cu_count));
+                                    m->x, D, m->downpart, ctx->cu_count, &fold_S));
         else
             TRACED(TK_DOWN, down_b,
                    launch_down(st, T[FTX_T_DOWN]->data, T[FTX_T_DOWN]->dtype,
