@@ -74,11 +74,15 @@ struct DownCfg {
 template <int DT>
 __global__ void __launch_bounds__(256) k_down_mfma(DownArgs a) {
     constexpr int NS = DownCfg<DT>::NS, NB = DownCfg<DT>::NB;
-    __shared__ float hs[8][NB * 32];
-    __shared__ float dsc[NS][NB * 32];  // [sub-block][row of the batch]
-    __shared__ float dmn[DT == FTX_Q4_K ? 8 : 1][NB * 32];
-    __shared__ _Float16 ahi[NB][NS][8][32];
-    __shared__ _Float16 alo[NB][NS][8][32];
+    // h / scale rows padded so 16-byte reads of different rows fall in
+    // different LDS banks; the activation tables are stored [octet of rows]
+    // [token][8 rows] so that one MFMA operand read covers consecutive bytes
+    constexpr int HP = NB * 32 + 4;
+    __shared__ float hs[8][HP];
+    __shared__ float dsc[NS][HP];  // [sub-block][row of the batch]
+    __shared__ float dmn[DT == FTX_Q4_K ? 8 : 1][HP];
+    __shared__ _Float16 ahi[NB][NS][4][8][8];
+    __shared__ _Float16 alo[NB][NS][4][8][8];
     __shared__ float mpart[4][8][8];
     const int tid = threadIdx.x, lane = tid & 63, w = tid >> 6;
     const int64_t sbc = blockIdx.x, split = blockIdx.y;
@@ -183,9 +187,9 @@ __global__ void __launch_bounds__(256) k_down_mfma(DownArgs a) {
 #pragma unroll
                         for (int k = 0; k < 8; ++k) mt += hv[k] * nv[k];
                     }
-                    *(v8h*)&ahi[b][s][m][oct * 8] =
+                    *(v8h*)&ahi[b][s][oct][m][0] =
                         v8h{ph[0], ph[1], ph[2], ph[3], ph[4], ph[5], ph[6], ph[7]};
-                    *(v8h*)&alo[b][s][m][oct * 8] =
+                    *(v8h*)&alo[b][s][oct][m][0] =
                         v8h{pl[0], pl[1], pl[2], pl[3], pl[4], pl[5], pl[6], pl[7]};
                 }
             }
@@ -224,8 +228,8 @@ __global__ void __launch_bounds__(256) k_down_mfma(DownArgs a) {
                 const int s = DT == FTX_Q4_K ? (w * 64 + ct * 16) / 32 : (w * 64 + ct * 16) / 16;
                 v8h ah = {}, al = {};
                 if (arow < 8) {
-                    ah = *(const v8h*)&ahi[b][s][arow][g * 8];
-                    al = *(const v8h*)&alo[b][s][arow][g * 8];
+                    ah = *(const v8h*)&ahi[b][s][g][arow][0];
+                    al = *(const v8h*)&alo[b][s][g][arow][0];
                 }
                 acc[ct] = __builtin_amdgcn_mfma_f32_16x16x32_f16(ah, bv, acc[ct], 0, 0, 0);
                 acc[ct] = __builtin_amdgcn_mfma_f32_16x16x32_f16(al, bv, acc[ct], 0, 0, 0);
