@@ -180,6 +180,7 @@ struct MvSeg {
     float* y;       // outputs [m][ldy]
     int64_t ldy;
     int rpt;        // weight rows per tile: 16 or 32
+    int dt;
 };
 
 struct MvArgs {
@@ -434,15 +435,13 @@ constexpr int mv_depth() {
 // at least 3 waves per SIMD fit (<= 168 VGPRs), 2 for the SwiGLU pairs,
 // whose launches hold fewer waves per CU
 template <int DT, bool TILED, bool PAIR>
-__global__ void __launch_bounds__(64 * MV_WAVES) __attribute__((amdgpu_waves_per_eu(PAIR ? 2 : 3)))
-k_mv(MvArgs a) {
+__device__ __forceinline__ void mv_unit(const MvArgs& a, int64_t u) {
     __shared__ float part[PAIR ? 2 : 1][MV_WAVES][256];  // [tile of unit][wave][m * 32 + col]
     const int w = threadIdx.x >> 6, lane = threadIdx.x & 63, col = lane & 31, g = lane >> 5;
     const int W = blockDim.x >> 6;
     constexpr bool pair = PAIR;
     constexpr int tpu = PAIR ? 2 : 1;
     const int64_t units = pair ? a.tiles / 2 : a.tiles;
-    const int64_t u = blockIdx.x;
     const int64_t nsb = a.nsb;
     const int spw = (int)(nsb / W), sb0 = w * spw;
     auto tile_of = [&](int ti) -> int64_t { return ti ? units + u : u; };
@@ -561,6 +560,24 @@ k_mv(MvArgs a) {
     }
 }
 
+template <int DT, bool TILED, bool PAIR>
+__global__ void __launch_bounds__(64 * MV_WAVES) __attribute__((amdgpu_waves_per_eu(PAIR ? 2 : 3)))
+k_mv(MvArgs a) {
+    mv_unit<DT, TILED, PAIR>(a, blockIdx.x);
+}
+
+// one launch over segments of both dtypes (q / k Q4_K with a Q6_K v): each
+// workgroup takes the path of its unit's segment
+template <bool TILED>
+__global__ void __launch_bounds__(64 * MV_WAVES) __attribute__((amdgpu_waves_per_eu(3)))
+k_mv_mix(MvArgs a) {
+    const int64_t u = blockIdx.x;
+    if (a.seg[mv_seg_of(a, u)].dt == FTX_Q4_K)
+        mv_unit<FTX_Q4_K, TILED, false>(a, u);
+    else
+        mv_unit<FTX_Q6_K, TILED, false>(a, u);
+}
+
 // y[m*ldy + n] += sum_s part[s][m][n] in split order (ffn_down's splits)
 __global__ void __launch_bounds__(256) k_part_reduce(const float* __restrict__ part, int S,
                                                      int64_t N, float* __restrict__ y,
@@ -650,11 +667,16 @@ hipError_t launch_mv(hipStream_t st, const GemvSeg* segs, int nseg, const int8_t
         if ((segs[i].tiled != 0) != tiled || (tiled && segs[i].rpt != 16 && segs[i].rpt != 32))
             return hipErrorInvalidValue;
     const int cus = cu_count > 0 ? cu_count : 256;
+    // mixed dtypes share one launch unless the units pair up for SwiGLU
+    bool mixed = false;
+    for (int i = 1; i < nseg; ++i) mixed |= segs[i].dt != segs[0].dt;
+    const bool pair = epi == EPI_SWIGLU;
     for (int dt : {FTX_Q4_K, FTX_Q6_K}) {
+        if (mixed && dt == FTX_Q6_K) break;  // the mixed launch took every segment
         MvArgs a{};
         int64_t tiles = 0;
         for (int i = 0; i < nseg; ++i) {
-            if (segs[i].dt != dt) continue;
+            if (!mixed && segs[i].dt != dt) continue;
             MvSeg& sg = a.seg[a.nseg++];
             sg.W = segs[i].W;
             sg.row_bytes = segs[i].row_bytes;
@@ -663,11 +685,11 @@ hipError_t launch_mv(hipStream_t st, const GemvSeg* segs, int nseg, const int8_t
             sg.y = segs[i].y;
             sg.ldy = segs[i].ldy;
             sg.rpt = tiled ? segs[i].rpt : mv_tile_rows(segs[i].N, cus);
+            sg.dt = segs[i].dt;
             tiles += (segs[i].N + sg.rpt - 1) / sg.rpt;
         }
         if (!a.nseg) continue;
         a.tiles = tiles;
-        const bool pair = epi == EPI_SWIGLU;
         const int64_t units = pair ? tiles / 2 : tiles;
         a.nsb = (int)(K / 256);
         a.M = (int)M;
@@ -691,7 +713,9 @@ hipError_t launch_mv(hipStream_t st, const GemvSeg* segs, int nseg, const int8_t
              {k_mv<FTX_Q4_K, true, false>, k_mv<FTX_Q4_K, true, true>}},
             {{k_mv<FTX_Q6_K, false, false>, k_mv<FTX_Q6_K, false, true>},
              {k_mv<FTX_Q6_K, true, false>, k_mv<FTX_Q6_K, true, true>}}};
-        hipLaunchKernelGGL(kern[dt == FTX_Q6_K][tiled][pair], gd, bd, 0, st, a);
+        static const K_t kmix[2] = {k_mv_mix<false>, k_mv_mix<true>};
+        hipLaunchKernelGGL(mixed ? kmix[tiled] : kern[dt == FTX_Q6_K][tiled][pair], gd, bd, 0, st,
+                           a);
         hipError_t e = hipGetLastError();
         if (e != hipSuccess) return e;
     }
