@@ -239,6 +239,53 @@ def test_verify_8b_shape_two_layers(gctx, orc):
     assert rel_err_rows(got, want) < LOGIT_TOL
 
 
+def _wide_model(orc, neox, seed):
+    """one 8B-width layer (d 4096, 32/8 heads x 128) with Q4_K projections and a
+    Q6_K attn_v: the int8-MFMA projections and the MFMA attention both apply"""
+    cfg = P.model_cfg(1, 4096, 32, 8, 128, 4096, 1000, rope_theta=500000.0, rope_neox=neox)
+    model = {"cfg": dict(cfg)}
+    rng = np.random.default_rng(seed)
+
+    def q(rows, cols, dt):
+        u = min(rows, 1024)
+        w = (rng.standard_normal((u, cols)) * 0.02).astype(np.float32)
+        raw = np.tile(orc.quantize(w, dt), -(-rows // u))[: rows * P.row_bytes(dt, cols)]
+        return dict(raw=np.ascontiguousarray(raw), dtype=dt, ne0=cols, ne1=rows)
+
+    ones = np.ones(4096, np.float32).view(np.uint8).copy()
+    model["tok_embd"] = q(1000, 4096, P.Q4_K)
+    model["output"] = q(1000, 4096, P.Q6_K)
+    model["out_norm"] = dict(raw=ones, dtype=P.F32, ne0=4096, ne1=1)
+    model["blk.0.attn_norm"] = dict(raw=ones, dtype=P.F32, ne0=4096, ne1=1)
+    model["blk.0.ffn_norm"] = dict(raw=ones, dtype=P.F32, ne0=4096, ne1=1)
+    for nm, rows, dt in (("q", 4096, P.Q4_K), ("k", 1024, P.Q4_K), ("v", 1024, P.Q6_K),
+                         ("o", 4096, P.Q4_K), ("gate", 4096, P.Q4_K), ("up", 4096, P.Q4_K),
+                         ("down", 4096, P.Q4_K)):
+        model["blk.0." + nm] = q(rows, 4096, dt)
+    return model
+
+
+@pytest.mark.parametrize("neox", [0, 1])
+@pytest.mark.parametrize("parents", [None, [-1, 0, 0, 1, 2, 2, 3]])
+def test_verify_fused_rope_kv(gctx, orc, neox, parents):
+    """Interleaved RoPE and the KV-cache write run in the q/k/v projection's
+    epilogue (neox pairs take the separate RoPE kernel): logits, the written
+    K/V rows and the untouched rest of the cache agree with the oracle, for
+    a chain and a tree at a context that is not chunk aligned."""
+    orc.set_threads(16)
+    model = _wide_model(orc, neox, seed=31 + neox)
+    M = 6 if parents is None else len(parents)
+    toks = list(np.random.default_rng(7).integers(0, 1000, M))
+    npast = 93
+    got, want, (kg, vg), (kc, vc) = run_both(gctx, orc, model, toks, npast, npast + M + 3,
+                                             parents=parents)
+    assert rel_err_rows(got, want) < LOGIT_TOL
+    # the draft rows written to the cache agree to fp16 rounding
+    np.testing.assert_allclose(kg.astype(np.float32), kc.astype(np.float32), rtol=2e-3, atol=2e-3)
+    np.testing.assert_allclose(vg.astype(np.float32), vc.astype(np.float32), rtol=2e-3, atol=2e-3)
+    assert np.array_equal(kg[:, :npast], kc[:, :npast]) and np.array_equal(vg[:, :npast], vc[:, :npast])
+
+
 def test_verify_errors(gctx, orc):
     model = P.make_model(orc, TINY, TINY_DT, seed=3)
     tensors = upload_model(gctx, model)

@@ -139,7 +139,23 @@ hipError_t launch_xq_prep(hipStream_t st, float* x, int64_t ldx, const float* no
 bool mv_supported(int dt, int64_t K, int64_t M);
 // the SwiGLU epilogue needs the whole contraction in one pass
 bool mv_swiglu_supported(int64_t K);
-enum { EPI_SWIGLU = 2 };
+enum { EPI_SWIGLU = 2, EPI_QKV = 3 };
+// EPI_QKV: the q / k / v projection's epilogue does RoPE with interleaved
+// pairs (src/engine.cpp:43-60; cos / sin of position npast + depth per token
+// and pair, computed on the host in double precision as there), writes k and
+// v into the KV cache slot npast + m (K [slot][kdim], V transposed), and q
+// as fp16 hi + lo parts for the MFMA attention
+struct QkvEpi {
+    const float* cs;   // [M][hd / 2][cos, sin]
+    _Float16* qh;      // [M][n_head][hd]
+    _Float16* ql;
+    void* kc;          // layer base of the K cache
+    void* vc;          // layer base of the V cache
+    int64_t slot0;     // npast
+    int64_t cap;
+    int hd, n_head, n_kv, kv_f16;
+};
+
 // tiled copies for the row-dot kernel: rows per tile for an N-row tensor,
 // bytes of the copy, and the re-tiling launch (src in the resident row layout)
 int mv_tile_rows(int64_t N, int cu_count);
@@ -147,7 +163,8 @@ size_t mv_tiled_bytes(int dt, int64_t N, int64_t K, int rpt);
 hipError_t launch_mv_tile(hipStream_t st, const uint8_t* src, int64_t src_row_bytes, int dt,
                           int64_t N, int64_t K, int rpt, uint8_t* dst);
 hipError_t launch_mv(hipStream_t st, const GemvSeg* segs, int nseg, const int8_t* xq, int64_t K,
-                     int64_t M, int epi, int cu_count, int normed, float eps);
+                     int64_t M, int epi, int cu_count, int normed, float eps,
+                     const QkvEpi* qkv = nullptr);
 
 hipError_t launch_part_reduce(hipStream_t st, const float* part, int S, int64_t N, int64_t M,
                               float* y, int64_t ldy);

@@ -183,6 +183,33 @@ struct MvSeg {
     int dt;
 };
 
+__device__ __forceinline__ void qkv_store(const QkvEpi& e, int si, int m, int64_t n, float v,
+                                          float pv, float* yp) {
+#pragma clang fp contract(off)
+    const int64_t d = n % e.hd, h = n / e.hd;
+    if (si < 2) {
+        const float c = e.cs[((int64_t)m * (e.hd / 2) + d / 2) * 2];
+        const float s = e.cs[((int64_t)m * (e.hd / 2) + d / 2) * 2 + 1];
+        // x0' = x0 c - x1 s, x1' = x0 s + x1 c for the pair (x0, x1) = (2i, 2i + 1)
+        v = (d & 1) ? pv * s + v * c : v * c - pv * s;
+    }
+    *yp = v;
+    const int64_t slot = e.slot0 + m, kdim = (int64_t)e.n_kv * e.hd;
+    if (si == 0) {
+        const int64_t o = ((int64_t)m * e.n_head + h) * e.hd + d;
+        const _Float16 hi = (_Float16)v;
+        e.qh[o] = hi;
+        e.ql[o] = (_Float16)(v - (float)hi);
+    } else if (si == 1) {
+        if (e.kv_f16) ((_Float16*)e.kc)[slot * kdim + n] = (_Float16)v;
+        else ((float*)e.kc)[slot * kdim + n] = v;
+    } else {
+        const int64_t vi = v_index(slot, h, d, e.hd, e.cap);
+        if (e.kv_f16) ((_Float16*)e.vc)[vi] = (_Float16)v;
+        else ((float*)e.vc)[vi] = v;
+    }
+}
+
 struct MvArgs {
     MvSeg seg[3];
     int nseg;
@@ -197,6 +224,7 @@ struct MvArgs {
     const float* ssq;   // per-block sums of x^2 [sb][8] when the input is RMS-normed, else null
     float eps;
     int64_t K;
+    QkvEpi qkv;         // EPI_QKV: segments 0, 1, 2 are q, k, v
 };
 
 constexpr int MV_WAVES = 8;  // at most 8 waves per unit (512 threads)
@@ -526,22 +554,29 @@ __device__ __forceinline__ void mv_unit(const MvArgs& a, int64_t u) {
     for (int t = 0; t < tpu; ++t)
 #pragma unroll
         for (int r = 0; r < 4; ++r) v[t][r] = acc[t][r] + acc[t][r + 4] * (1.f / 256.f);
-    const MvSeg& sg = a.seg[mv_seg_of(a, u)];
+    const int si = mv_seg_of(a, u);
+    const MvSeg& sg = a.seg[si];
     const int rpt = sg.rpt;
-    auto finish = [&](int m, int c, float gv, float uv) {
+    // gv: this output; pv: the output of row n ^ 1 (the RoPE partner)
+    auto finish = [&](int m, int c, float gv, float uv, float pv) {
         const int64_t n = (u - sg.tile0) * rpt + c;
         if (m >= a.M || n >= sg.N) return;
         float* yp = sg.y + (int64_t)m * sg.ldy + n;
-        if (pair)
+        if (pair) {
             // src/engine.cpp:271-273: g / (1 + exp(-g)) * u
             *yp = gv / (1.f + expf(-gv)) * uv;
-        else
+        } else if (a.epi == EPI_QKV) {
+            qkv_store(a.qkv, si, m, n, gv, pv, yp);
+        } else {
             *yp = a.epi == EPI_ACCUM ? *yp + gv : gv;
+        }
     };
     if (W == 1) {
-        if (col < rpt)
 #pragma unroll
-            for (int r = 0; r < 4; ++r) finish(4 * g + r, col, v[0][r], v[tpu - 1][r]);
+        for (int r = 0; r < 4; ++r) {
+            const float pv = __shfl_xor(v[0][r], 1, 64);
+            if (col < rpt) finish(4 * g + r, col, v[0][r], v[tpu - 1][r], pv);
+        }
         return;
     }
 #pragma unroll
@@ -556,7 +591,9 @@ __device__ __forceinline__ void mv_unit(const MvArgs& a, int64_t u) {
         for (int ww = 0; ww < W; ++ww) gv += part[0][ww][m * 32 + c];
         if constexpr (PAIR)
             for (int ww = 0; ww < W; ++ww) uv += part[tpu - 1][ww][m * 32 + c];
-        finish(m, c, gv, uv);
+        // threads t and t ^ 1 hold rows c and c ^ 1 (8 * rpt is whole waves)
+        const float pv = __shfl_xor(gv, 1, 64);
+        finish(m, c, gv, uv, pv);
     }
 }
 
@@ -656,7 +693,9 @@ hipError_t launch_mv_tile(hipStream_t st, const uint8_t* src, int64_t src_row_by
 // layout or all tiled (GemvSeg::tiled, with the tile rows they were tiled
 // with); one launch per dtype over that dtype's segments
 hipError_t launch_mv(hipStream_t st, const GemvSeg* segs, int nseg, const int8_t* xq, int64_t K,
-                     int64_t M, int epi, int cu_count, int normed, float eps) {
+                     int64_t M, int epi, int cu_count, int normed, float eps,
+                     const QkvEpi* qkv) {
+    if (epi == EPI_QKV && (!qkv || nseg != 3 || qkv->hd % 2)) return hipErrorInvalidValue;
     if (nseg < 1 || nseg > 3 || M < 1 || M > 8 || K % 4096 || K > 16384)
         return hipErrorInvalidValue;
     if (epi == EPI_SWIGLU && (nseg != 2 || segs[0].N != segs[1].N || segs[0].dt != segs[1].dt ||
@@ -701,6 +740,7 @@ hipError_t launch_mv(hipStream_t st, const GemvSeg* segs, int nseg, const int8_t
         a.ssq = normed ? xq_ssq((int8_t*)xq, K) : nullptr;
         a.eps = eps;
         a.K = K;
+        if (qkv) a.qkv = *qkv;
         // waves per unit: up to ~8 waves per CU over the launch (measured
         // best on the 8B shapes: gate/up W = 4, attention projections 8)
         int W = 1;

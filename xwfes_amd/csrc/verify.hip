@@ -2,6 +2,7 @@
 // draft tokens (src/engine.cpp:461-596, extend_verify 669-674) with every op
 // on the GPU, plus the acceptance sampler entry point.
 #include <algorithm>
+#include <cmath>
 #include <new>
 
 #include "ftx_internal.h"
@@ -26,6 +27,8 @@ struct ftx_model {
     int8_t* xq = nullptr;
     // rotated q as fp16 hi + lo parts for the MFMA attention, [M][n_head][hd] each
     _Float16* qhl = nullptr;
+    // RoPE cos / sin per (token, pair) of the current step, [M][hd / 2][2]
+    float* rcs = nullptr;
     // per-layer re-tiled ffn_down copies for the MFMA down kernel (or null)
     std::vector<uint8_t*> down_tiled;
     // tiled copies for the int8-MFMA row-dot kernel, [layer * LAYER_TENSORS +
@@ -56,7 +59,7 @@ struct ftx_kv {
 static void model_release(ftx_model* m) {
     if (!m) return;
     void* bufs[] = {m->norms, m->x,     m->xn,  m->qkv,   m->att, m->h,     m->part,
-                    m->toks,  m->depth, m->anc, m->npast, m->xq,  m->qhl};
+                    m->toks,  m->depth, m->anc, m->npast, m->xq,  m->qhl,   m->rcs};
     for (void* b : bufs)
         if (b) (void)hipFree(b);
     for (uint8_t* b : m->down_tiled)
@@ -134,7 +137,8 @@ int ftx_model_create(ftx_ctx* ctx, const ftx_model_desc* d, ftx_model** out) {
               dalloc(&m->npast, 1);
     if (ok) {
         const int64_t Kmax = std::max(D, qdim);
-        ok = dalloc(&m->xq, xq_bytes(Kmax)) && dalloc(&m->qhl, (size_t)(2 * Mmax * qdim));
+        ok = dalloc(&m->xq, xq_bytes(Kmax)) && dalloc(&m->qhl, (size_t)(2 * Mmax * qdim)) &&
+             dalloc(&m->rcs, (size_t)(Mmax * d->head_dim));
     }
     // re-tiled ffn_down copies (same bytes, MFMA-friendly order)
     m->down_tiled.assign((size_t)d->n_layer, nullptr);
@@ -327,7 +331,8 @@ int ftx_verify_step(ftx_ctx* ctx, ftx_model* m, ftx_kv* kv, const ftx_verify_arg
     if (npast + M > kv->cap) return ftx_fail(ctx, FTX_E_RANGE, "kv capacity exceeded");
     // host-side argument prep: tokens, depth, ancestor masks, npast
     const int aw = (int)((M + 31) / 32);
-    const size_t pin_bytes = (size_t)M * 4 * 2 + (size_t)M * aw * 4 + 64;
+    const int64_t hd2 = d.head_dim / 2;
+    const size_t pin_bytes = (size_t)M * 4 * 2 + (size_t)M * aw * 4 + 64 + (size_t)(M * hd2 * 2) * 4;
     uint8_t* pin;
     int rc = ftx_pinned(ctx, pin_bytes, (void**)&pin);
     if (rc) return rc;
@@ -336,6 +341,7 @@ int ftx_verify_step(ftx_ctx* ctx, ftx_model* m, ftx_kv* kv, const ftx_verify_arg
     int32_t* depth = toks + M;
     uint32_t* anc = (uint32_t*)(depth + M);
     int64_t* np = (int64_t*)(((uintptr_t)(anc + M * aw) + 7) & ~(uintptr_t)7);
+    float* cs = (float*)(np + 1);
     for (int64_t i = 0; i < M; ++i) {
         const int32_t t = a->tokens[i];
         if (t < 0 || t >= d.vocab) return ftx_fail(ctx, FTX_E_RANGE, "token id out of range");
@@ -351,11 +357,21 @@ int ftx_verify_step(ftx_ctx* ctx, ftx_model* m, ftx_kv* kv, const ftx_verify_arg
         row[i / 32] |= 1u << (i % 32);
     }
     *np = npast;
+    // rope_vec's angles (src/engine.cpp:43-60): f = theta^(-2i/hd) and the
+    // angle in double, cos / sin rounded to float, at position npast + depth
+    for (int64_t i = 0; i < M; ++i)
+        for (int64_t p = 0; p < hd2; ++p) {
+            const double f = std::pow(d.rope_theta, -2.0 * (double)p / (double)d.head_dim);
+            const double ang = (double)(npast + depth[i]) * f;
+            cs[(i * hd2 + p) * 2] = (float)std::cos(ang);
+            cs[(i * hd2 + p) * 2 + 1] = (float)std::sin(ang);
+        }
     hipStream_t st = ctx->stream;
     FTX_HIP(ctx, hipMemcpyAsync(m->toks, toks, M * 4, hipMemcpyHostToDevice, st));
     FTX_HIP(ctx, hipMemcpyAsync(m->depth, depth, M * 4, hipMemcpyHostToDevice, st));
     FTX_HIP(ctx, hipMemcpyAsync(m->anc, anc, (size_t)M * aw * 4, hipMemcpyHostToDevice, st));
     FTX_HIP(ctx, hipMemcpyAsync(m->npast, np, 8, hipMemcpyHostToDevice, st));
+    FTX_HIP(ctx, hipMemcpyAsync(m->rcs, cs, (size_t)(M * hd2 * 2) * 4, hipMemcpyHostToDevice, st));
 
     const int64_t D = d.n_embd, F = d.n_ff, V = d.vocab;
     const float eps = d.rms_eps;
@@ -380,7 +396,7 @@ int ftx_verify_step(ftx_ctx* ctx, ftx_model* m, ftx_kv* kv, const ftx_verify_arg
     int fold_S = 0;
     auto project = [&](int kind, double bytes, float* xin, int64_t ldx, const float* normw,
                        const ftx_tensor* const* ts, GemvSeg* segs, int nseg, int64_t K, int epi,
-                       int64_t tix0, const int* tix) -> int {
+                       int64_t tix0, const int* tix, const QkvEpi* qe = nullptr) -> int {
         const bool fold = fold_S > 0 && xin == m->x;
         if (mv_all(ts, nseg, K, M) && (epi != EPI_SWIGLU || mv_swiglu_supported(K))) {
             // the tiled copies when every segment has one
@@ -397,7 +413,7 @@ int ftx_verify_step(ftx_ctx* ctx, ftx_model* m, ftx_kv* kv, const ftx_verify_arg
             if (fold) fold_S = 0;
             TRACED(kind, bytes,
                    launch_mv(st, segs, nseg, m->xq, K, M, epi, ctx->cu_count, normw != nullptr,
-                             eps));
+                             eps, qe));
             return FTX_OK;
         }
         if (fold) {
@@ -431,23 +447,40 @@ int ftx_verify_step(ftx_ctx* ctx, ftx_model* m, ftx_kv* kv, const ftx_verify_arg
         const ftx_tensor* tqkv[3] = {T[FTX_T_Q], T[FTX_T_K], T[FTX_T_V]};
         GemvSeg qkv[3] = {seg(T[FTX_T_Q], m->qkv, m->ldq), seg(T[FTX_T_K], m->qkv + m->qdim, m->ldq),
                           seg(T[FTX_T_V], m->qkv + m->qdim + m->kdim, m->ldq)};
+        uint8_t* kl = (uint8_t*)kv->k + (size_t)(l * kv->cap_alloc * kv->kdim) * kvel;
+        uint8_t* vl = (uint8_t*)kv->v + (size_t)(l * kv->cap_alloc * kv->kdim) * kvel;
+        const bool mattn = attn_mfma_supported(d.head_dim, kv->kv_f16, M, d.n_head, d.n_head_kv);
+        // RoPE and the KV write ride on the projection's epilogue when the
+        // MFMA kernels take both (interleaved pairs are adjacent outputs)
+        const bool fuse = mattn && !d.rope_neox && mv_all(tqkv, 3, D, M);
+        QkvEpi qe{};
+        qe.cs = m->rcs;
+        qe.qh = m->qhl;
+        qe.ql = m->qhl + M * m->qdim;
+        qe.kc = kl;
+        qe.vc = vl;
+        qe.slot0 = npast;
+        qe.cap = kv->cap_alloc;
+        qe.hd = (int)d.head_dim;
+        qe.n_head = (int)d.n_head;
+        qe.n_kv = (int)d.n_head_kv;
+        qe.kv_f16 = kv->kv_f16;
         rc = project(TK_GEMV_QKV,
                      wbytes(T[FTX_T_Q]) + wbytes(T[FTX_T_K]) + wbytes(T[FTX_T_V]) + Md * D * f4 +
                          Md * m->ldq * f4,
-                     m->x, D, m->norms + (l * 2) * D, tqkv, qkv, 3, D, EPI_STORE, lt, ix_qkv);
+                     m->x, D, m->norms + (l * 2) * D, tqkv, qkv, 3, D,
+                     fuse ? EPI_QKV : EPI_STORE, lt, ix_qkv, fuse ? &qe : nullptr);
         if (rc) return rc;
-        uint8_t* kl = (uint8_t*)kv->k + (size_t)(l * kv->cap_alloc * kv->kdim) * kvel;
-        uint8_t* vl = (uint8_t*)kv->v + (size_t)(l * kv->cap_alloc * kv->kdim) * kvel;
         RopeArgs ra{m->qkv,       m->ldq,       d.n_head, d.n_head_kv, d.head_dim,   m->depth,
                     m->npast,     d.rope_theta, d.rope_neox, kl,       vl,           kv->kv_f16,
                     kv->cap_alloc};
-        const bool mattn = attn_mfma_supported(d.head_dim, kv->kv_f16, M, d.n_head, d.n_head_kv);
         if (mattn) {
-            ra.qh16 = m->qhl;
-            ra.ql16 = m->qhl + M * m->qdim;
+            ra.qh16 = qe.qh;
+            ra.ql16 = qe.ql;
         }
-        TRACED(TK_ROPE_KV, 2 * Md * m->ldq * f4 + 2 * Md * m->kdim * (double)kvel,
-               launch_rope_kv(st, ra, M));
+        if (!fuse)
+            TRACED(TK_ROPE_KV, 2 * Md * m->ldq * f4 + 2 * Md * m->kdim * (double)kvel,
+                   launch_rope_kv(st, ra, M));
         const double attn_b =
             2.0 * (double)(npast + M) * m->kdim * (double)kvel + 2 * Md * m->qdim * f4;
         if (mattn) {
