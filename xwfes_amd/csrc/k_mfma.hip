@@ -183,13 +183,12 @@ struct MvSeg {
     int dt;
 };
 
+// (c, s) = cos / sin of this row's rotation angle (q and k segments)
 __device__ __forceinline__ void qkv_store(const QkvEpi& e, int si, int m, int64_t n, float v,
-                                          float pv, float* yp) {
+                                          float pv, float c, float s, float* yp) {
 #pragma clang fp contract(off)
     const int64_t d = n % e.hd, h = n / e.hd;
     if (si < 2) {
-        const float c = e.cs[((int64_t)m * (e.hd / 2) + d / 2) * 2];
-        const float s = e.cs[((int64_t)m * (e.hd / 2) + d / 2) * 2 + 1];
         // x0' = x0 c - x1 s, x1' = x0 s + x1 c for the pair (x0, x1) = (2i, 2i + 1)
         v = (d & 1) ? pv * s + v * c : v * c - pv * s;
     }
@@ -228,6 +227,9 @@ struct MvArgs {
 };
 
 constexpr int MV_WAVES = 8;  // at most 8 waves per unit (512 threads)
+#ifndef MV_WPE_SINGLE
+#define MV_WPE_SINGLE 2
+#endif
 
 
 __device__ __forceinline__ int mv_seg_of(const MvArgs& a, int64_t T) {
@@ -423,8 +425,7 @@ struct MvX {
 };
 
 template <int DT>
-__device__ __forceinline__ void mv_load_x(MvX<DT>& x, const MvArgs& a, int sb, int col, int g,
-                                          const float* inv) {
+__device__ __forceinline__ void mv_load_x(MvX<DT>& x, const MvArgs& a, int sb, int col, int g) {
     if constexpr (DT == FTX_Q4_K) {
         const int8_t* fp = a.frag + (((int64_t)sb * 16 + g) * 16 + (col & 15)) * 16;
 #pragma unroll
@@ -436,17 +437,33 @@ __device__ __forceinline__ void mv_load_x(MvX<DT>& x, const MvArgs& a, int sb, i
         for (int p = 0; p < 8; ++p) x.x8[p] = *(const long*)(fp + 512 * p);
         x.ax = ld16g(a.xs16 + ((int64_t)sb * 32 + col) * 16);
     }
-    const float4 s4 = *(const float4*)(a.scale + (int64_t)sb * 8 + 4 * g);
-    x.s4 = make_float4(s4.x * inv[0], s4.y * inv[1], s4.z * inv[2], s4.w * inv[3]);
+    x.s4 = *(const float4*)(a.scale + (int64_t)sb * 8 + 4 * g);
 }
 
+// s4 = the block scales of rows 4g .. 4g+3 (times their RMSNorm factors)
 template <int DT>
-__device__ __forceinline__ void mv_block(const MvW<DT>& w, const MvX<DT>& x, int col, int g,
-                                         float* acc) {
+__device__ __forceinline__ void mv_block(const MvW<DT>& w, const MvX<DT>& x, float4 s4, int col,
+                                         int g, float* acc) {
     if constexpr (DT == FTX_Q4_K)
-        q4k_block(w.w[0], w.w + 1, x.af, x.xv, x.s4, g, acc);
+        q4k_block(w.w[0], w.w + 1, x.af, x.xv, s4, g, acc);
     else
-        q6k_block(w.w, w.w + 4, w.w[6], h2f(w.d), x.x8, x.ax, x.s4, col, g, acc);
+        q6k_block(w.w, w.w + 4, w.w[6], h2f(w.d), x.x8, x.ax, s4, col, g, acc);
+}
+
+template <int CTRL>
+__device__ __forceinline__ float dpp_f(float x) {
+    return __builtin_bit_cast(float,
+                              __builtin_amdgcn_mov_dpp(__builtin_bit_cast(int, x), CTRL, 0xF, 0xF, false));
+}
+
+// sum over the 16 lanes of each DPP row; every step adds a lane pair in
+// both orders, so all 16 lanes end with the same bits
+__device__ __forceinline__ float row16_sum(float v) {
+    v += dpp_f<0xB1>(v);   // quad_perm [1, 0, 3, 2]
+    v += dpp_f<0x4E>(v);   // quad_perm [2, 3, 0, 1]
+    v += dpp_f<0x141>(v);  // row_half_mirror: lane i <-> 7 - i
+    v += dpp_f<0x140>(v);  // row_mirror: lane i <-> 15 - i
+    return v;
 }
 
 // items in flight ahead of the one being computed, within the register
@@ -459,9 +476,15 @@ constexpr int mv_depth() {
     return DT == FTX_Q4_K ? 1 : (PAIR ? 0 : 1);
 }
 
-// grid = units; block = W waves (W divides the super-block count, W <= 8);
-// at least 3 waves per SIMD fit (<= 168 VGPRs), 2 for the SwiGLU pairs,
-// whose launches hold fewer waves per CU
+// grid = units; block = W waves (W divides the super-block count, W <= 8, so
+// every wave takes an even number of super-blocks); at least 3 waves per
+// SIMD fit (<= 168 VGPRs), 2 for the SwiGLU pairs, whose launches hold fewer
+// waves per CU.
+// Loads are issued so that no wait covers a later-needed, longer-latency
+// load: the sums of squares first, then the first super-block's activation
+// operand, then the first weights (vector-memory counters retire in issue
+// order); the activation operand of super-block j + 1 is in flight while j
+// computes, and the residual of the accumulate epilogue is read up front.
 template <int DT, bool TILED, bool PAIR>
 __device__ __forceinline__ void mv_unit(const MvArgs& a, int64_t u) {
     __shared__ float part[PAIR ? 2 : 1][MV_WAVES][256];  // [tile of unit][wave][m * 32 + col]
@@ -498,19 +521,16 @@ __device__ __forceinline__ void mv_unit(const MvArgs& a, int64_t u) {
     // arithmetic (a ring of D + 1 register buffers; loads past the last item
     // re-read it)
     constexpr int D = mv_depth<DT, PAIR>();
+    static_assert(D <= 1, "the ring index below assumes D + 1 divides 2 * tpu");
     MvW<DT> buf[D + 1];
     auto item_load = [&](MvW<DT>& o, int j) {
         j = j < nit ? j : nit - 1;
         load(o, j % tpu, sb0 + j / tpu);
     };
-#pragma unroll
-    for (int d = 0; d < D; ++d) item_load(buf[d], d);
-    // the RMSNorm factor 1 / rms of rows m = 4g .. 4g+3 (src/engine.cpp:23-41)
-    float inv[4] = {1.f, 1.f, 1.f, 1.f};
-    if (a.ssq) {
-        // lanes col and col ^ 16 each sum the super-blocks b = col % 16 + 16 k,
-        // then the 16-lane butterfly gives every lane the row totals of its g
-        float4 ss = {0.f, 0.f, 0.f, 0.f};
+    // lanes col and col ^ 16 each sum the super-blocks b = col % 16 + 16 k
+    // of the per-block sums of squares (rows 4g .. 4g+3)
+    float4 ss = {0.f, 0.f, 0.f, 0.f};
+    if (a.ssq)
         for (int b = col & 15; b < a.nsb; b += 16) {
             const float4 t = *(const float4*)(a.ssq + (int64_t)b * 8 + 4 * g);
             ss.x += t.x;
@@ -518,87 +538,121 @@ __device__ __forceinline__ void mv_unit(const MvArgs& a, int64_t u) {
             ss.z += t.z;
             ss.w += t.w;
         }
+    __builtin_amdgcn_sched_barrier(0);
+    MvX<DT> x[2];
+    mv_load_x<DT>(x[0], a, sb0, col, g);
+    __builtin_amdgcn_sched_barrier(0);
 #pragma unroll
-        for (int o = 1; o < 16; o <<= 1) {
-            ss.x += __shfl_xor(ss.x, o, 64);
-            ss.y += __shfl_xor(ss.y, o, 64);
-            ss.z += __shfl_xor(ss.z, o, 64);
-            ss.w += __shfl_xor(ss.w, o, 64);
+    for (int d = 0; d < D; ++d) item_load(buf[d], d);
+    __builtin_amdgcn_sched_barrier(0);
+    const int si = mv_seg_of(a, u);
+    const MvSeg& sg = a.seg[si];
+    const int rpt = sg.rpt;
+    // the epilogue thread t < 8 * rpt owns output (m, c) = (t / rpt, t % rpt)
+    // when W > 1: its residual (accumulate) or rotation (q / k) is read now
+    const int t = threadIdx.x;
+    const int em = t / rpt, ec = t % rpt;
+    const int64_t en = (u - sg.tile0) * rpt + ec;
+    const bool eown = W > 1 && t < 8 * rpt && em < a.M && en < sg.N;
+    float eres = 0.f, ecs = 1.f, esn = 0.f;
+    if (eown) {
+        if (!pair && a.epi == EPI_ACCUM) eres = sg.y[(int64_t)em * sg.ldy + en];
+        if (!pair && a.epi == EPI_QKV && si < 2) {
+            const int64_t d = en % a.qkv.hd;
+            const float2 cs =
+                *(const float2*)(a.qkv.cs + ((int64_t)em * (a.qkv.hd / 2) + d / 2) * 2);
+            ecs = cs.x;
+            esn = cs.y;
         }
-        const float kf = (float)a.K;
-        inv[0] = 1.f / sqrtf(ss.x / kf + a.eps);
-        inv[1] = 1.f / sqrtf(ss.y / kf + a.eps);
-        inv[2] = 1.f / sqrtf(ss.z / kf + a.eps);
-        inv[3] = 1.f / sqrtf(ss.w / kf + a.eps);
     }
-    MvX<DT> x;
-    for (int i0 = 0; i0 < nit; i0 += D + 1) {
+    // the RMSNorm factor 1 / rms of rows m = 4g .. 4g+3 (src/engine.cpp:23-41)
+    float inv[4] = {1.f, 1.f, 1.f, 1.f};
+    if (a.ssq) {
+        const float kf = (float)a.K;
+        inv[0] = 1.f / sqrtf(row16_sum(ss.x) / kf + a.eps);
+        inv[1] = 1.f / sqrtf(row16_sum(ss.y) / kf + a.eps);
+        inv[2] = 1.f / sqrtf(row16_sum(ss.z) / kf + a.eps);
+        inv[3] = 1.f / sqrtf(row16_sum(ss.w) / kf + a.eps);
+    }
+    // two super-blocks per step: x[h] holds super-block sb0 + k + h; the
+    // item index i = (k + h) * tpu + ti keeps i % (D + 1) = (h * tpu + ti) %
+    // (D + 1) because k is even
+    for (int k = 0; k < spw; k += 2) {
 #pragma unroll
-        for (int d = 0; d <= D; ++d) {
-            const int i = i0 + d;
-            if (i >= nit) break;
-            const int ti = i % tpu, sb = sb0 + i / tpu;
-            if (ti == 0) mv_load_x<DT>(x, a, sb, col, g, inv);
-            __builtin_amdgcn_sched_barrier(0);
-            item_load(buf[(d + D) % (D + 1)], i + D);
-            __builtin_amdgcn_sched_barrier(0);
-            if (!PAIR || ti == 0)
-                mv_block<DT>(buf[d], x, col, g, acc[0]);
-            else
-                mv_block<DT>(buf[d], x, col, g, acc[tpu - 1]);
+        for (int h = 0; h < 2; ++h) {
+            if (k + h + 1 < spw) mv_load_x<DT>(x[h ^ 1], a, sb0 + k + h + 1, col, g);
+            const float4 s4 = make_float4(x[h].s4.x * inv[0], x[h].s4.y * inv[1],
+                                          x[h].s4.z * inv[2], x[h].s4.w * inv[3]);
+#pragma unroll
+            for (int ti = 0; ti < tpu; ++ti) {
+                const int il = h * tpu + ti;
+                const int i = k * tpu + il;
+                __builtin_amdgcn_sched_barrier(0);
+                item_load(buf[(il + D) % (D + 1)], i + D);
+                __builtin_amdgcn_sched_barrier(0);
+                mv_block<DT>(buf[il % (D + 1)], x[h], s4, col, g, acc[ti]);
+            }
         }
     }
     // lane (col, g) holds rows m = 4g + r of weight row col of each tile
     float v[tpu][4];
 #pragma unroll
-    for (int t = 0; t < tpu; ++t)
+    for (int q = 0; q < tpu; ++q)
 #pragma unroll
-        for (int r = 0; r < 4; ++r) v[t][r] = acc[t][r] + acc[t][r + 4] * (1.f / 256.f);
-    const int si = mv_seg_of(a, u);
-    const MvSeg& sg = a.seg[si];
-    const int rpt = sg.rpt;
-    // gv: this output; pv: the output of row n ^ 1 (the RoPE partner)
-    auto finish = [&](int m, int c, float gv, float uv, float pv) {
-        const int64_t n = (u - sg.tile0) * rpt + c;
-        if (m >= a.M || n >= sg.N) return;
-        float* yp = sg.y + (int64_t)m * sg.ldy + n;
-        if (pair) {
-            // src/engine.cpp:271-273: g / (1 + exp(-g)) * u
-            *yp = gv / (1.f + expf(-gv)) * uv;
-        } else if (a.epi == EPI_QKV) {
-            qkv_store(a.qkv, si, m, n, gv, pv, yp);
-        } else {
-            *yp = a.epi == EPI_ACCUM ? *yp + gv : gv;
-        }
-    };
+        for (int r = 0; r < 4; ++r) v[q][r] = acc[q][r] + acc[q][r + 4] * (1.f / 256.f);
     if (W == 1) {
+        // gv: this output; pv: the output of row n ^ 1 (the RoPE partner)
 #pragma unroll
         for (int r = 0; r < 4; ++r) {
             const float pv = __shfl_xor(v[0][r], 1, 64);
-            if (col < rpt) finish(4 * g + r, col, v[0][r], v[tpu - 1][r], pv);
+            const int m = 4 * g + r;
+            const int64_t n = (u - sg.tile0) * rpt + col;
+            if (col >= rpt || m >= a.M || n >= sg.N) continue;
+            float* yp = sg.y + (int64_t)m * sg.ldy + n;
+            const float gv = v[0][r];
+            if (pair) {
+                // src/engine.cpp:271-273: g / (1 + exp(-g)) * u
+                *yp = gv / (1.f + expf(-gv)) * v[tpu - 1][r];
+            } else if (a.epi == EPI_QKV) {
+                float c = 1.f, sn = 0.f;
+                if (si < 2) {
+                    const int64_t d = n % a.qkv.hd;
+                    c = a.qkv.cs[((int64_t)m * (a.qkv.hd / 2) + d / 2) * 2];
+                    sn = a.qkv.cs[((int64_t)m * (a.qkv.hd / 2) + d / 2) * 2 + 1];
+                }
+                qkv_store(a.qkv, si, m, n, gv, pv, c, sn, yp);
+            } else {
+                *yp = a.epi == EPI_ACCUM ? *yp + gv : gv;
+            }
         }
         return;
     }
 #pragma unroll
-    for (int t = 0; t < tpu; ++t)
+    for (int q = 0; q < tpu; ++q)
 #pragma unroll
-        for (int r = 0; r < 4; ++r) part[t][w][(4 * g + r) * 32 + col] = v[t][r];
+        for (int r = 0; r < 4; ++r) part[q][w][(4 * g + r) * 32 + col] = v[q][r];
     __syncthreads();
-    const int t = threadIdx.x;
     if (t < 8 * rpt) {
-        const int m = t / rpt, c = t % rpt;
         float gv = 0.f, uv = 0.f;
-        for (int ww = 0; ww < W; ++ww) gv += part[0][ww][m * 32 + c];
+        for (int ww = 0; ww < W; ++ww) gv += part[0][ww][em * 32 + ec];
         if constexpr (PAIR)
-            for (int ww = 0; ww < W; ++ww) uv += part[tpu - 1][ww][m * 32 + c];
+            for (int ww = 0; ww < W; ++ww) uv += part[tpu - 1][ww][em * 32 + ec];
         // threads t and t ^ 1 hold rows c and c ^ 1 (8 * rpt is whole waves)
         const float pv = __shfl_xor(gv, 1, 64);
-        finish(m, c, gv, uv, pv);
+        if (eown) {
+            float* yp = sg.y + (int64_t)em * sg.ldy + en;
+            if (pair)
+                *yp = gv / (1.f + expf(-gv)) * uv;  // src/engine.cpp:271-273
+            else if (a.epi == EPI_QKV)
+                qkv_store(a.qkv, si, em, en, gv, pv, ecs, esn, yp);
+            else
+                *yp = a.epi == EPI_ACCUM ? eres + gv : gv;
+        }
     }
 }
 
 template <int DT, bool TILED, bool PAIR>
-__global__ void __launch_bounds__(64 * MV_WAVES) __attribute__((amdgpu_waves_per_eu(PAIR ? 2 : 3)))
+__global__ void __launch_bounds__(64 * MV_WAVES) __attribute__((amdgpu_waves_per_eu(MV_WPE_SINGLE)))
 k_mv(MvArgs a) {
     mv_unit<DT, TILED, PAIR>(a, blockIdx.x);
 }
@@ -606,7 +660,7 @@ k_mv(MvArgs a) {
 // one launch over segments of both dtypes (q / k Q4_K with a Q6_K v): each
 // workgroup takes the path of its unit's segment
 template <bool TILED>
-__global__ void __launch_bounds__(64 * MV_WAVES) __attribute__((amdgpu_waves_per_eu(3)))
+__global__ void __launch_bounds__(64 * MV_WAVES) __attribute__((amdgpu_waves_per_eu(MV_WPE_SINGLE)))
 k_mv_mix(MvArgs a) {
     const int64_t u = blockIdx.x;
     if (a.seg[mv_seg_of(a, u)].dt == FTX_Q4_K)
