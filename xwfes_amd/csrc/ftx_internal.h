@@ -244,7 +244,7 @@ struct AttnMArgs {
     const _Float16* kc;  // layer base [cap][kdim]
     const _Float16* vt;  // layer base [n_kv][hd][cap]
     int64_t cap;         // allocated slots, multiple of 64
-    const int64_t* npast;
+    int64_t npast;       // committed slots before the draft
     const uint32_t* anc;
     int anc_words;
     int M, n_head, n_kv, hd;
@@ -253,7 +253,10 @@ struct AttnMArgs {
 };
 bool attn_mfma_supported(int64_t hd, int kv_f16, int64_t M, int64_t n_head, int64_t n_kv);
 size_t attn_part_floats(int64_t M, int64_t n_head, int64_t hd, int64_t cap_alloc);
-hipError_t launch_attn_mfma(hipStream_t st, AttnMArgs a, float* part);
+// xq != null: the chunk combine writes the output projection's activation
+// operand (xq_dev.h layout, K = n_head * hd) instead of a.out
+bool attn_combine_xq_supported(int64_t hd, int64_t n_head);
+hipError_t launch_attn_mfma(hipStream_t st, AttnMArgs a, float* part, int8_t* xq = nullptr);
 // canonical [slot][kdim] <-> device V layout (per layer, all slots)
 hipError_t launch_v_layout(hipStream_t st, const void* src, void* dst, int64_t n_layer,
                            int64_t cap, int64_t n_kv, int64_t hd, int elem_bytes, int to_device);

@@ -18,6 +18,7 @@
 // 8-byte load.  The query operand is staged once per workgroup in LDS; the
 // four wave partials (max, sum, O) are merged in LDS into the chunk partial.
 #include "ftx_internal.h"
+#include "xq_dev.h"
 
 namespace {
 
@@ -42,7 +43,7 @@ __global__ void __launch_bounds__(256) k_attn_mfma(AttnMArgs a) {
     __shared__ float obuf[4][32][HD];  // wave partial O [q row][dim]
     __shared__ float smax[4][32], ssum[4][32];
     const int tid = threadIdx.x, w = tid >> 6, lane = tid & 63, col = lane & 15, g = lane >> 4;
-    const int64_t npast = *a.npast;
+    const int64_t npast = a.npast;
     const int64_t total = npast + a.M;
     const int c = blockIdx.x;
     const int64_t slot0 = (int64_t)c * CH;
@@ -200,7 +201,7 @@ __global__ void __launch_bounds__(128) k_attn_combine(AttnMArgs a, int nch) {
     __shared__ float red[128];
     const int64_t qi = blockIdx.x;  // m * n_head + h
     const int d = threadIdx.x;
-    const int64_t npast = *a.npast;
+    const int64_t npast = a.npast;
     const int nvalid = (int)((npast + a.M + CH - 1) / CH);
     float M = -INFINITY;
     for (int c = d; c < nvalid; c += 128) M = fmaxf(M, a.pmax[qi * nch + c]);
@@ -234,7 +235,84 @@ __global__ void __launch_bounds__(128) k_attn_combine(AttnMArgs a, int nch) {
     }
 }
 
+// The combine of k_attn_combine fused with the activation prep of the
+// output projection: workgroup (sb, m) forms elements 256 sb .. 256 sb + 255
+// of attention output row m (the HPB = 256 / HD heads 256 sb / HD ..) and
+// writes them as the GEMV's activation operand (xq_dev.h) instead of fp32.
+// Wave h < HPB forms head h's chunk weights; then wave w adds chunks
+// w, w + 4, ... into per-lane partial numerators (lane l: elements 4l ..
+// 4l+3), which wave 0 sums in wave order and quantises.  Rows m >= M are
+// written as zeros.
+template <int HD>
+__global__ void __launch_bounds__(256) k_attn_combine_xq(AttnMArgs a, int nch, XqPtrs o) {
+    constexpr int HPB = 256 / HD;
+    __shared__ float wsh[HPB][1024];  // chunk weights (nch <= 1024)
+    __shared__ float sden[HPB];
+    __shared__ float4 red[4][64];
+    const int64_t sb = blockIdx.x;
+    const int m = blockIdx.y, tid = threadIdx.x, w = tid >> 6, l = tid & 63;
+    const int nvalid = (int)((a.npast + a.M + CH - 1) / CH);
+    const int hh = (4 * l) / HD, d = (4 * l) % HD;
+    float v[4] = {0.f, 0.f, 0.f, 0.f};
+    if (m < a.M) {
+        if (w < HPB) {
+            const int64_t qi = (int64_t)m * a.n_head + sb * HPB + w;
+            float mx = -INFINITY;
+            for (int c = l; c < nvalid; c += 64) mx = fmaxf(mx, a.pmax[qi * nch + c]);
+#pragma unroll
+            for (int s = 32; s > 0; s >>= 1) mx = fmaxf(mx, __shfl_xor(mx, s, 64));
+            float den = 0.f;
+            for (int c = l; c < nvalid; c += 64) {
+                const float mc = a.pmax[qi * nch + c];
+                const float wc = mc == -INFINITY ? 0.f : expf(mc - mx);
+                wsh[w][c] = wc;
+                den += wc * a.psum[qi * nch + c];
+            }
+#pragma unroll
+            for (int s = 32; s > 0; s >>= 1) den += __shfl_xor(den, s, 64);
+            if (l == 0) sden[w] = den;
+        }
+        __syncthreads();
+        const int64_t qi = (int64_t)m * a.n_head + sb * HPB + hh;
+        const float* po = a.pout + qi * nch * HD + d;
+        float4 num = {0.f, 0.f, 0.f, 0.f};
+#pragma unroll 4
+        for (int c = w; c < nvalid; c += 4) {
+            const float wc = wsh[hh][c];
+            const float4 p = *(const float4*)(po + (int64_t)c * HD);
+            num.x += wc * p.x;
+            num.y += wc * p.y;
+            num.z += wc * p.z;
+            num.w += wc * p.w;
+        }
+        red[w][l] = num;
+        __syncthreads();
+        if (w == 0) {
+            float4 t = red[0][l];
+#pragma unroll
+            for (int k = 1; k < 4; ++k) {
+                const float4 r = red[k][l];
+                t.x += r.x;
+                t.y += r.y;
+                t.z += r.z;
+                t.w += r.w;
+            }
+            const float den = sden[hh];
+            v[0] = t.x / den;
+            v[1] = t.y / den;
+            v[2] = t.z / den;
+            v[3] = t.w / den;
+        }
+    }
+    if (w == 0) xq_emit(v, sb, m, l, o);
+}
+
 }  // namespace
+
+bool attn_combine_xq_supported(int64_t hd, int64_t n_head) {
+    const int64_t K = hd * n_head;
+    return (hd == 64 || hd == 128) && K % 4096 == 0 && K <= 16384;
+}
 
 bool attn_mfma_supported(int64_t hd, int kv_f16, int64_t M, int64_t n_head, int64_t n_kv) {
     return kv_f16 && (hd == 64 || hd == 128) && M >= 1 && (M * (n_head / n_kv)) <= 32 * 16;
@@ -245,7 +323,7 @@ size_t attn_part_floats(int64_t M, int64_t n_head, int64_t hd, int64_t cap_alloc
     return (size_t)(M * n_head * nch) * (size_t)(hd + 2);
 }
 
-hipError_t launch_attn_mfma(hipStream_t st, AttnMArgs a, float* part) {
+hipError_t launch_attn_mfma(hipStream_t st, AttnMArgs a, float* part, int8_t* xq) {
     const int nch = (int)(a.cap / CH);
     if (nch > 1024) return hipErrorInvalidValue;  // combine weights live in LDS
     const int64_t qi = (int64_t)a.M * a.n_head;
@@ -263,6 +341,16 @@ hipError_t launch_attn_mfma(hipStream_t st, AttnMArgs a, float* part) {
         return hipErrorInvalidValue;
     hipError_t e = hipGetLastError();
     if (e != hipSuccess) return e;
-    hipLaunchKernelGGL(k_attn_combine, dim3((unsigned)qi), dim3(128), 0, st, a, nch);
+    if (xq) {
+        if (!attn_combine_xq_supported(a.hd, a.n_head)) return hipErrorInvalidValue;
+        const int64_t K = (int64_t)a.n_head * a.hd;
+        const dim3 cg((unsigned)(K / 256), 8);
+        if (a.hd == 128)
+            hipLaunchKernelGGL(k_attn_combine_xq<128>, cg, dim3(256), 0, st, a, nch, xq_ptrs(xq, K));
+        else
+            hipLaunchKernelGGL(k_attn_combine_xq<64>, cg, dim3(256), 0, st, a, nch, xq_ptrs(xq, K));
+    } else {
+        hipLaunchKernelGGL(k_attn_combine, dim3((unsigned)qi), dim3(128), 0, st, a, nch);
+    }
     return hipGetLastError();
 }

@@ -34,6 +34,7 @@
 // accumulate, or SwiGLU) follows.
 #include "ftx_internal.h"
 #include "quant_dev.h"
+#include "xq_dev.h"
 
 namespace {
 
@@ -118,54 +119,7 @@ __global__ void __launch_bounds__(64) k_xq_prep(float* __restrict__ x, int64_t l
     } else if (normw && l == 0) {
         ssq[sb * 8 + m] = 0.f;
     }
-    float mx = fmaxf(fmaxf(fabsf(v[0]), fabsf(v[1])), fmaxf(fabsf(v[2]), fabsf(v[3])));
-#pragma unroll
-    for (int o = 32; o > 0; o >>= 1) mx = fmaxf(mx, __shfl_xor(mx, o, 64));
-    const float q = mx > 0.f ? 127.f / mx : 0.f;
-    if (l == 0) scale[sb * 8 + m] = mx > 0.f ? mx / 127.f : 0.f;
-    int sa = 0, sbb = 0;
-    uint32_t pa = 0, pb = 0;
-#pragma unroll
-    for (int t = 0; t < 4; ++t) {
-        const float y = v[t] * q;
-        const float a = rintf(y);
-        float bf = rintf((y - a) * 256.f);
-        bf = fminf(fmaxf(bf, -127.f), 127.f);
-        const int ai = (int)a, bi = (int)bf;
-        sa += ai;
-        sbb += bi;
-        pa |= (uint32_t)(ai & 0xFF) << (8 * t);
-        pb |= (uint32_t)(bi & 0xFF) << (8 * t);
-    }
-    // fragment bytes: element 4l+t of the super-block sits in 32-block
-    // kb = 8 sb + l/8, half (l%8)/4, byte 4(l%4) + t
-    const int64_t kb = sb * 8 + (l >> 3);
-    const int half = (l & 7) >> 2, byte = 4 * (l & 3);
-    *(uint32_t*)(frag + ((kb * 2 + half) * 16 + m) * 16 + byte) = pa;
-    *(uint32_t*)(frag + ((kb * 2 + half) * 16 + 8 + m) * 16 + byte) = pb;
-    // 16-element sums (4 lanes), split into 6-bit lo / signed hi
-#pragma unroll
-    for (int o = 1; o < 4; o <<= 1) {
-        sa += __shfl_xor(sa, o, 64);
-        sbb += __shfl_xor(sbb, o, 64);
-    }
-    if ((l & 3) == 0) {
-        const int s16 = l >> 2;
-        xs16[(sb * 32 + m) * 16 + s16] = (int8_t)(sa & 63);
-        xs16[(sb * 32 + 16 + m) * 16 + s16] = (int8_t)(sa >> 6);
-        xs16[(sb * 32 + 8 + m) * 16 + s16] = (int8_t)(sbb & 63);
-        xs16[(sb * 32 + 24 + m) * 16 + s16] = (int8_t)(sbb >> 6);
-    }
-    // 32-element sums (8 lanes)
-    sa += __shfl_xor(sa, 4, 64);
-    sbb += __shfl_xor(sbb, 4, 64);
-    if ((l & 7) == 0) {
-        const int j = l >> 3;
-        xs32[(sb * 32 + m) * 8 + j] = (int8_t)(sa & 63);
-        xs32[(sb * 32 + 16 + m) * 8 + j] = (int8_t)(sa >> 6);
-        xs32[(sb * 32 + 8 + m) * 8 + j] = (int8_t)(sbb & 63);
-        xs32[(sb * 32 + 24 + m) * 8 + j] = (int8_t)(sbb >> 6);
-    }
+    xq_emit(v, sb, m, l, XqPtrs{frag, xs32, xs16, scale, ssq});
 }
 
 // ---------------------------------------------------------------- row-dot
@@ -687,8 +641,8 @@ __global__ void __launch_bounds__(256) k_part_reduce(const float* __restrict__ p
 // fragments K*16 | xs32 K | xs16 2K | scales (K/256)*8 floats | ssq (K/256)*8 floats
 size_t xq_bytes(int64_t K) { return (size_t)(K * 16 + K + K * 2 + K / 8 + K / 8 + 64); }
 
-static float* xq_scale(int8_t* xq, int64_t K) { return (float*)(xq + K * 16 + K + K * 2); }
-static float* xq_ssq(int8_t* xq, int64_t K) { return xq_scale(xq, K) + K / 32; }
+static float* xq_scale(int8_t* xq, int64_t K) { return xq_ptrs(xq, K).scale; }
+static float* xq_ssq(int8_t* xq, int64_t K) { return xq_ptrs(xq, K).ssq; }
 
 hipError_t launch_xq_prep(hipStream_t st, float* x, int64_t ldx, const float* normw,
                           const float* part, int S, int64_t ldpart, int64_t K, int64_t M,

@@ -396,7 +396,8 @@ int ftx_verify_step(ftx_ctx* ctx, ftx_model* m, ftx_kv* kv, const ftx_verify_arg
     int fold_S = 0;
     auto project = [&](int kind, double bytes, float* xin, int64_t ldx, const float* normw,
                        const ftx_tensor* const* ts, GemvSeg* segs, int nseg, int64_t K, int epi,
-                       int64_t tix0, const int* tix, const QkvEpi* qe = nullptr) -> int {
+                       int64_t tix0, const int* tix, const QkvEpi* qe = nullptr,
+                       bool xq_ready = false) -> int {
         const bool fold = fold_S > 0 && xin == m->x;
         if (mv_all(ts, nseg, K, M) && (epi != EPI_SWIGLU || mv_swiglu_supported(K))) {
             // the tiled copies when every segment has one
@@ -407,9 +408,10 @@ int ftx_verify_step(ftx_ctx* ctx, ftx_model* m, ftx_kv* kv, const ftx_verify_arg
                 segs[i].tiled = 1;
                 segs[i].rpt = m->mvt_rpt[tix0 + tix[i]];
             }
-            TRACED(TK_XQ_PREP, Md * K * f4 * (fold ? 2.0 + fold_S : 1.0) + 19.0 * K,
-                   launch_xq_prep(st, xin, ldx, normw, fold ? m->downpart : nullptr,
-                                  fold ? fold_S : 0, D, K, M, m->xq));
+            if (!xq_ready)
+                TRACED(TK_XQ_PREP, Md * K * f4 * (fold ? 2.0 + fold_S : 1.0) + 19.0 * K,
+                       launch_xq_prep(st, xin, ldx, normw, fold ? m->downpart : nullptr,
+                                      fold ? fold_S : 0, D, K, M, m->xq));
             if (fold) fold_S = 0;
             TRACED(kind, bytes,
                    launch_mv(st, segs, nseg, m->xq, K, M, epi, ctx->cu_count, normw != nullptr,
@@ -483,6 +485,10 @@ int ftx_verify_step(ftx_ctx* ctx, ftx_model* m, ftx_kv* kv, const ftx_verify_arg
                    launch_rope_kv(st, ra, M));
         const double attn_b =
             2.0 * (double)(npast + M) * m->kdim * (double)kvel + 2 * Md * m->qdim * f4;
+        // the chunk combine writes the output projection's activation operand
+        // directly when that projection takes the int8-MFMA path
+        const bool o_xq = mattn && attn_combine_xq_supported(d.head_dim, d.n_head) &&
+                          mv_all(&T[FTX_T_O], 1, m->qdim, M);
         if (mattn) {
             AttnMArgs am{};
             am.qkv = m->qkv;
@@ -492,7 +498,7 @@ int ftx_verify_step(ftx_ctx* ctx, ftx_model* m, ftx_kv* kv, const ftx_verify_arg
             am.kc = (const _Float16*)kl;
             am.vt = (const _Float16*)vl;
             am.cap = kv->cap_alloc;
-            am.npast = m->npast;
+            am.npast = npast;
             am.anc = m->anc;
             am.anc_words = aw;
             am.M = (int)M;
@@ -500,7 +506,8 @@ int ftx_verify_step(ftx_ctx* ctx, ftx_model* m, ftx_kv* kv, const ftx_verify_arg
             am.n_kv = (int)d.n_head_kv;
             am.hd = (int)d.head_dim;
             am.out = m->att;
-            TRACED(TK_ATTENTION, attn_b, launch_attn_mfma(st, am, kv->attn_part));
+            TRACED(TK_ATTENTION, attn_b,
+                   launch_attn_mfma(st, am, kv->attn_part, o_xq ? m->xq : nullptr));
         } else {
             AttnArgs aa{m->qkv,  m->ldq, kl,       vl,          kv->kv_f16, m->npast,
                         m->anc,  aw,     d.n_head, d.n_head_kv, d.head_dim, npast + M,
@@ -509,7 +516,8 @@ int ftx_verify_step(ftx_ctx* ctx, ftx_model* m, ftx_kv* kv, const ftx_verify_arg
         }
         GemvSeg o = seg(T[FTX_T_O], m->x, D);
         rc = project(TK_GEMV_O, wbytes(T[FTX_T_O]) + Md * m->qdim * f4 + 2 * Md * D * f4, m->att,
-                     m->qdim, nullptr, &T[FTX_T_O], &o, 1, m->qdim, EPI_ACCUM, lt, ix_o);
+                     m->qdim, nullptr, &T[FTX_T_O], &o, 1, m->qdim, EPI_ACCUM, lt, ix_o, nullptr,
+                     o_xq);
         if (rc) return rc;
         const ftx_tensor* tgu[2] = {T[FTX_T_GATE], T[FTX_T_UP]};
         GemvSeg gu[2] = {seg(T[FTX_T_GATE], m->h, F), seg(T[FTX_T_UP], nullptr, 0)};
