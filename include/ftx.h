@@ -198,7 +198,7 @@ int ftx_kv_create(ftx_ctx* ctx, const ftx_model* m, int64_t cap, int kv_dtype, f
 int ftx_kv_free(ftx_kv* kv);
 /* Raw device buffers: K is [n_layer][cap_alloc][n_head_kv*head_dim], V is
  * stored transposed as [n_layer][n_head_kv][head_dim][cap_alloc], cap_alloc =
- * cap rounded up to a multiple of 64 (for fills that ignore the layout). */
+ * cap rounded up to a multiple of 128 (for fills that ignore the layout). */
 int ftx_kv_pointers(ftx_kv* kv, void** k, void** v, int64_t* npast);
 /* Copy the whole cache from / to host arrays in the reference layout
  * [n_layer][cap][n_head_kv*head_dim] (include/ft/kv_cache.h:10-47). */

@@ -196,7 +196,7 @@ hipError_t launch_rmsnorm(hipStream_t st, const float* x, const float* w, int64_
 // KV cache layout per layer: K [cap][n_kv*hd] (the reference's
 // [pos][n_kv*hd], include/ft/kv_cache.h:10-47); V transposed as
 // [n_kv][hd][cap] so attention reads P.V operands contiguously.  `cap` here
-// is the allocated slot count, a multiple of 64.
+// is the allocated slot count, a multiple of 128.
 __host__ __device__ inline int64_t v_index(int64_t slot, int64_t kvh, int64_t dim, int64_t hd,
                                            int64_t cap) {
     return (kvh * hd + dim) * cap + slot;
@@ -243,7 +243,7 @@ struct AttnMArgs {
     const _Float16* ql16;
     const _Float16* kc;  // layer base [cap][kdim]
     const _Float16* vt;  // layer base [n_kv][hd][cap]
-    int64_t cap;         // allocated slots, multiple of 64
+    int64_t cap;         // allocated slots, multiple of 128
     int64_t npast;       // committed slots before the draft
     const uint32_t* anc;
     int anc_words;

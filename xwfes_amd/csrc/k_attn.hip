@@ -1,22 +1,23 @@
 // k_attn.hip -- tree-masked GQA attention over the fp16 KV cache on MFMA,
-// split over 64-slot chunks of the context (flash-decoding) and combined in
-// a second pass.
+// split over chunks of the context (flash-decoding) and combined in a second
+// pass.
 //
 // Semantics of Impl::attn (src/engine.cpp:137-177) with the draft-tree mask:
 // query row m of head h attends to cache slots [0, npast) and to the tree
 // slots npast + j of its ancestors j (itself included); kv head =
 // h / (n_head / n_kv); scores are q.k / sqrt(hd); softmax; sum of p * v.
 //
-// One workgroup handles one kv head, one 64-slot chunk and one tile of 32
-// query rows of the GQA group (row r -> token r / gqa, head kvh * gqa +
-// r % gqa); its four waves take 16 slots each.  Per wave, with
-// v_mfma_f32_16x16x32_f16: S^T = K . Q^T (K rows are the A operand, exact
-// fp16; Q arrives split into fp16 hi + lo so the scores keep fp32 accuracy); a
-// lane then holds 4 slots of one query row, which is exactly the A operand
-// of O = P . V on v_mfma_f32_16x16x16_f16 (P hi + lo).  V is kept
-// transposed in the cache ([kv head][dim][slot]) so the B operand is one
-// 8-byte load.  The query operand is staged once per workgroup in LDS; the
-// four wave partials (max, sum, O) are merged in LDS into the chunk partial.
+// One workgroup handles one kv head, one chunk of hd slots and one tile of
+// 32 query rows of the GQA group (row r -> token r / gqa, head kvh * gqa +
+// r % gqa) with hd / 16 waves.  Wave w first computes the scores of slots
+// 16w .. 16w+15 with v_mfma_f32_16x16x32_f16: S^T = K . Q^T (K rows are the A
+// operand, exact fp16; Q arrives split into fp16 hi + lo so the scores keep
+// fp32 accuracy).  The chunk's row maxima meet in LDS, each wave writes its
+// p = e^(s - max) as fp16 hi + lo into an LDS tile P[query row][slot], and
+// wave w then forms output dims 16w .. 16w+15 over the whole chunk, O = P . V
+// on v_mfma_f32_16x16x16_f16 with V kept transposed in the cache ([kv head]
+// [dim][slot]) so its B operand is one 8-byte load.  The chunk partial (max,
+// sum, O) goes straight from the MFMA registers to memory.
 #include "ftx_internal.h"
 #include "xq_dev.h"
 
@@ -26,8 +27,8 @@ typedef _Float16 v8h __attribute__((ext_vector_type(8)));
 typedef _Float16 v4h __attribute__((ext_vector_type(4)));
 typedef float v4f __attribute__((ext_vector_type(4)));
 
-constexpr int CH = 64;   // slots per chunk (workgroup)
-constexpr int WS = 16;   // slots per wave
+// slots per chunk (one workgroup of hd / 16 waves) for head size hd
+__host__ __device__ constexpr int chunk_slots(int hd) { return hd; }
 
 __device__ __forceinline__ bool slot_visible(const AttnMArgs& a, int64_t npast, int m, int64_t p) {
     if (p < npast) return true;
@@ -37,43 +38,46 @@ __device__ __forceinline__ bool slot_visible(const AttnMArgs& a, int64_t npast, 
 }
 
 template <int HD>
-__global__ void __launch_bounds__(256) k_attn_mfma(AttnMArgs a) {
+__global__ void __launch_bounds__(64 * (HD / 16)) k_attn_mfma(AttnMArgs a) {
+    constexpr int NW = HD / 16;   // waves: 16 score slots and 16 output dims each
+    constexpr int CHK = 16 * NW;  // slots per chunk (= HD)
     constexpr int NDC = HD / 32;  // 32-dim chunks of the score contraction
-    constexpr int NDT = HD / 16;  // 16-dim tiles of the output
-    __shared__ float obuf[4][32][HD];  // wave partial O [q row][dim]
-    __shared__ float smax[4][32], ssum[4][32];
+    constexpr int QP = HD + 8;    // padded query row (halves)
+    constexpr int PP = CHK + 8;   // padded P row (halves)
+    __shared__ _Float16 qs[2][32][QP];  // query hi / lo [part][row][dim]
+    __shared__ _Float16 ps[2][32][PP];  // P hi / lo [part][query row][slot]
+    __shared__ float smax[NW][32], ssum[NW][32], cmax[32];
     const int tid = threadIdx.x, w = tid >> 6, lane = tid & 63, col = lane & 15, g = lane >> 4;
     const int64_t npast = a.npast;
     const int64_t total = npast + a.M;
     const int c = blockIdx.x;
-    const int64_t slot0 = (int64_t)c * CH;
+    const int64_t slot0 = (int64_t)c * CHK;
     if (slot0 >= total) return;
     const int kvh = blockIdx.y;
     const int gqa = a.n_head / a.n_kv;
     const int qrows = a.M * gqa;
     const int qbase = blockIdx.z * 32;  // first query row of this tile
     const int64_t kdim = (int64_t)a.n_kv * HD;
-    const int64_t ws0 = slot0 + w * WS;  // this wave's first slot
-    // ---- every operand load issued up front: K rows (A of S^T), V^T rows
-    // (B of O), the query hi / lo parts (B of S^T)
+    const int64_t ws0 = slot0 + 16 * w;  // this wave's score slots
+    // ---- operand loads, all issued up front: K rows (A of S^T: slot ws0 +
+    // col, dims 32 dc + 8 g ..), V^T rows (B of O: dim 16 w + col, slots
+    // slot0 + 16 st + 4 g ..), then the query hi / lo parts into LDS
     v8h kf[NDC];
     {
         const _Float16* krow = a.kc + (ws0 + col) * kdim + (int64_t)kvh * HD + 8 * g;
 #pragma unroll
         for (int dc = 0; dc < NDC; ++dc) kf[dc] = *(const v8h*)(krow + 32 * dc);
     }
-    v4h vf[NDT];
+    v4h vf[NW];
     {
-        const _Float16* vbase = a.vt + (int64_t)kvh * HD * a.cap + ws0 + 4 * g;
+        const _Float16* vrow = a.vt + ((int64_t)kvh * HD + 16 * w + col) * a.cap + slot0 + 4 * g;
 #pragma unroll
-        for (int dt = 0; dt < NDT; ++dt) vf[dt] = *(const v4h*)(vbase + (int64_t)(16 * dt + col) * a.cap);
+        for (int st = 0; st < NW; ++st) vf[st] = *(const v4h*)(vrow + 16 * st);
     }
-    // the query hi / lo parts of this tile's 32 rows, staged once per
-    // workgroup in the (not yet used) merge buffer: [hi|lo][row][dim]
-    _Float16* qs = (_Float16*)&obuf[0][0][0];
+    // 16-byte vectors of the staged queries: 2 parts x 32 rows x HD / 8
 #pragma unroll
-    for (int k = 0; k < 4 * HD / 128; ++k) {
-        const int v = tid + 256 * k;  // 16-byte vector index
+    for (int k = 0; k < (2 * 32 * HD / 8) / (64 * NW); ++k) {
+        const int v = tid + 64 * NW * k;
         const int part = v / (32 * HD / 8), r = (v / (HD / 8)) % 32, dv = v % (HD / 8);
         const int rq = qbase + r;
         v8h x = {};
@@ -81,33 +85,26 @@ __global__ void __launch_bounds__(256) k_attn_mfma(AttnMArgs a) {
             const int64_t qo = ((int64_t)(rq / gqa) * a.n_head + kvh * gqa + rq % gqa) * HD + 8 * dv;
             x = *(const v8h*)((part ? a.ql16 : a.qh16) + qo);
         }
-        *(v8h*)&qs[(part * 32 + r) * HD + 8 * dv] = x;
+        *(v8h*)&qs[part][r][8 * dv] = x;
     }
     __syncthreads();
-    v8h qh[2][NDC], ql[2][NDC];
-#pragma unroll
-    for (int qt = 0; qt < 2; ++qt)
-#pragma unroll
-        for (int dc = 0; dc < NDC; ++dc) {
-            qh[qt][dc] = *(const v8h*)&qs[(qt * 16 + col) * HD + 32 * dc + 8 * g];
-            ql[qt][dc] = *(const v8h*)&qs[(32 + qt * 16 + col) * HD + 32 * dc + 8 * g];
-        }
-    // ---- S^T = K . Q^T for the two 16-row query tiles
-    v4f st[2];
+    // ---- S^T = K . Q^T for the two 16-row query tiles; lane (col, g) then
+    // holds S^T[slot ws0 + 4g + r][query row qt * 16 + col]
+    v4f sc[2];
 #pragma unroll
     for (int qt = 0; qt < 2; ++qt) {
         v4f acc = {0.f, 0.f, 0.f, 0.f};
 #pragma unroll
         for (int dc = 0; dc < NDC; ++dc) {
-            acc = __builtin_amdgcn_mfma_f32_16x16x32_f16(kf[dc], qh[qt][dc], acc, 0, 0, 0);
-            acc = __builtin_amdgcn_mfma_f32_16x16x32_f16(kf[dc], ql[qt][dc], acc, 0, 0, 0);
+            const v8h qh = *(const v8h*)&qs[0][qt * 16 + col][32 * dc + 8 * g];
+            const v8h ql = *(const v8h*)&qs[1][qt * 16 + col][32 * dc + 8 * g];
+            acc = __builtin_amdgcn_mfma_f32_16x16x32_f16(kf[dc], qh, acc, 0, 0, 0);
+            acc = __builtin_amdgcn_mfma_f32_16x16x32_f16(kf[dc], ql, acc, 0, 0, 0);
         }
-        st[qt] = acc;
+        sc[qt] = acc;
     }
-    __syncthreads();  // every wave is done with the staged queries
-    // lane (col, g) holds S^T[slot ws0 + 4g + r][query row qt * 16 + col]
+    // masked, scaled scores and this wave's row maxima
     const float scale = 1.f / sqrtf((float)HD);
-    float mx[2], sum[2];
 #pragma unroll
     for (int qt = 0; qt < 2; ++qt) {
         const int rq = qbase + qt * 16 + col;
@@ -117,79 +114,73 @@ __global__ void __launch_bounds__(256) k_attn_mfma(AttnMArgs a) {
 #pragma unroll
         for (int r = 0; r < 4; ++r) {
             const bool ok = qvalid && slot_visible(a, npast, mq, ws0 + 4 * g + r);
-            const float sv = ok ? st[qt][r] * scale : -INFINITY;
-            st[qt][r] = sv;
+            const float sv = ok ? sc[qt][r] * scale : -INFINITY;
+            sc[qt][r] = sv;
             m_ = fmaxf(m_, sv);
         }
         m_ = fmaxf(m_, __shfl_xor(m_, 16, 64));
         m_ = fmaxf(m_, __shfl_xor(m_, 32, 64));
+        if (g == 0) smax[w][qt * 16 + col] = m_;
+    }
+    __syncthreads();
+    // ---- p = e^(s - chunk max); row sums per wave; P hi / lo into LDS
+#pragma unroll
+    for (int qt = 0; qt < 2; ++qt) {
+        const int q = qt * 16 + col;
+        float mx = smax[0][q];
+#pragma unroll
+        for (int k = 1; k < NW; ++k) mx = fmaxf(mx, smax[k][q]);
         float s_ = 0.f;
+        v4h ph, pl;
 #pragma unroll
         for (int r = 0; r < 4; ++r) {
-            const float e = st[qt][r] == -INFINITY ? 0.f : expf(st[qt][r] - m_);
-            st[qt][r] = e;
+            const float e = sc[qt][r] == -INFINITY ? 0.f : expf(sc[qt][r] - mx);
             s_ += e;
+            const _Float16 h = (_Float16)e;
+            ph[r] = h;
+            pl[r] = (_Float16)(e - (float)h);
         }
         s_ += __shfl_xor(s_, 16, 64);
         s_ += __shfl_xor(s_, 32, 64);
-        mx[qt] = m_;
-        sum[qt] = s_;
-    }
-    // ---- O = P . V: A = P (query row col, slots 4g .. 4g+3), B = V^T rows
-    v4h ph[2], pl[2];
-#pragma unroll
-    for (int qt = 0; qt < 2; ++qt)
-#pragma unroll
-        for (int r = 0; r < 4; ++r) {
-            const _Float16 h = (_Float16)st[qt][r];
-            ph[qt][r] = h;
-            pl[qt][r] = (_Float16)(st[qt][r] - (float)h);
+        if (g == 0) {
+            ssum[w][q] = s_;
+            if (w == 0) cmax[q] = mx;
         }
-#pragma unroll
-    for (int dt = 0; dt < NDT; ++dt) {
-#pragma unroll
-        for (int qt = 0; qt < 2; ++qt) {
-            v4f o = {0.f, 0.f, 0.f, 0.f};
-            o = __builtin_amdgcn_mfma_f32_16x16x16f16(ph[qt], vf[dt], o, 0, 0, 0);
-            o = __builtin_amdgcn_mfma_f32_16x16x16f16(pl[qt], vf[dt], o, 0, 0, 0);
-            // lane holds O[query row qt * 16 + 4g + r][dim 16 dt + col]
-#pragma unroll
-            for (int r = 0; r < 4; ++r) obuf[w][qt * 16 + 4 * g + r][16 * dt + col] = o[r];
-        }
-    }
-    if (g == 0) {
-#pragma unroll
-        for (int qt = 0; qt < 2; ++qt) {
-            smax[w][qt * 16 + col] = mx[qt];
-            ssum[w][qt * 16 + col] = sum[qt];
-        }
+        *(v4h*)&ps[0][q][16 * w + 4 * g] = ph;
+        *(v4h*)&ps[1][q][16 * w + 4 * g] = pl;
     }
     __syncthreads();
-    // ---- merge the four waves: thread -> (query row, 16 dims)
+    // ---- O[:, 16 w .. 16 w + 15] = P . V over the chunk: A = P (query row
+    // col, slots 16 st + 4g ..), B = V^T rows; lane then holds O[query row
+    // qt * 16 + 4g + r][dim 16 w + col]
     const int nch = (int)gridDim.x;
-    const int q = tid >> 3, d0 = (tid & 7) * (HD / 8);
-    if (qbase + q >= qrows) return;
-    float M = -INFINITY;
 #pragma unroll
-    for (int k = 0; k < 4; ++k) M = fmaxf(M, smax[k][q]);
-    float wgt[4], den = 0.f;
+    for (int qt = 0; qt < 2; ++qt) {
+        v4f o = {0.f, 0.f, 0.f, 0.f};
 #pragma unroll
-    for (int k = 0; k < 4; ++k) {
-        wgt[k] = smax[k][q] == -INFINITY ? 0.f : expf(smax[k][q] - M);
-        den += wgt[k] * ssum[k][q];
+        for (int st = 0; st < NW; ++st) {
+            const v4h ph = *(const v4h*)&ps[0][qt * 16 + col][16 * st + 4 * g];
+            const v4h pl = *(const v4h*)&ps[1][qt * 16 + col][16 * st + 4 * g];
+            o = __builtin_amdgcn_mfma_f32_16x16x16f16(ph, vf[st], o, 0, 0, 0);
+            o = __builtin_amdgcn_mfma_f32_16x16x16f16(pl, vf[st], o, 0, 0, 0);
+        }
+#pragma unroll
+        for (int r = 0; r < 4; ++r) {
+            const int rq = qbase + qt * 16 + 4 * g + r;
+            if (rq >= qrows) continue;
+            const int64_t qi = (int64_t)(rq / gqa) * a.n_head + kvh * gqa + rq % gqa;
+            a.pout[(qi * nch + c) * HD + 16 * w + col] = o[r];
+        }
     }
-    const int64_t qi = (int64_t)((qbase + q) / gqa) * a.n_head + kvh * gqa + (qbase + q) % gqa;
-    if ((tid & 7) == 0) {
-        a.pmax[qi * nch + c] = M;
+    // chunk statistics of query row lane (wave 0)
+    if (w == 0 && lane < 32 && qbase + lane < qrows) {
+        const int rq = qbase + lane;
+        const int64_t qi = (int64_t)(rq / gqa) * a.n_head + kvh * gqa + rq % gqa;
+        float den = ssum[0][lane];
+#pragma unroll
+        for (int k = 1; k < NW; ++k) den += ssum[k][lane];
+        a.pmax[qi * nch + c] = cmax[lane];
         a.psum[qi * nch + c] = den;
-    }
-    float* po = a.pout + (qi * nch + c) * HD + d0;
-#pragma unroll
-    for (int d = 0; d < HD / 8; d += 4) {
-        v4f v = {0.f, 0.f, 0.f, 0.f};
-#pragma unroll
-        for (int k = 0; k < 4; ++k) v += wgt[k] * *(const v4f*)&obuf[k][q][d0 + d];
-        *(v4f*)(po + d) = v;
     }
 }
 
@@ -202,7 +193,8 @@ __global__ void __launch_bounds__(128) k_attn_combine(AttnMArgs a, int nch) {
     const int64_t qi = blockIdx.x;  // m * n_head + h
     const int d = threadIdx.x;
     const int64_t npast = a.npast;
-    const int nvalid = (int)((npast + a.M + CH - 1) / CH);
+    const int ch = chunk_slots(a.hd);
+    const int nvalid = (int)((npast + a.M + ch - 1) / ch);
     float M = -INFINITY;
     for (int c = d; c < nvalid; c += 128) M = fmaxf(M, a.pmax[qi * nch + c]);
     red[d] = M;
@@ -251,7 +243,8 @@ __global__ void __launch_bounds__(256) k_attn_combine_xq(AttnMArgs a, int nch, X
     __shared__ float4 red[4][64];
     const int64_t sb = blockIdx.x;
     const int m = blockIdx.y, tid = threadIdx.x, w = tid >> 6, l = tid & 63;
-    const int nvalid = (int)((a.npast + a.M + CH - 1) / CH);
+    constexpr int ch = chunk_slots(HD);
+    const int nvalid = (int)((a.npast + a.M + ch - 1) / ch);
     const int hh = (4 * l) / HD, d = (4 * l) % HD;
     float v[4] = {0.f, 0.f, 0.f, 0.f};
     if (m < a.M) {
@@ -319,12 +312,15 @@ bool attn_mfma_supported(int64_t hd, int kv_f16, int64_t M, int64_t n_head, int6
 }
 
 size_t attn_part_floats(int64_t M, int64_t n_head, int64_t hd, int64_t cap_alloc) {
-    const int64_t nch = cap_alloc / CH;
+    const int64_t nch = (cap_alloc + chunk_slots((int)hd) - 1) / chunk_slots((int)hd);
     return (size_t)(M * n_head * nch) * (size_t)(hd + 2);
 }
 
 hipError_t launch_attn_mfma(hipStream_t st, AttnMArgs a, float* part, int8_t* xq) {
-    const int nch = (int)(a.cap / CH);
+    // whole chunks of the allocation: every slot a chunk reads is allocated
+    const int ch = chunk_slots(a.hd);
+    if (a.cap % ch) return hipErrorInvalidValue;
+    const int nch = (int)(a.cap / ch);
     if (nch > 1024) return hipErrorInvalidValue;  // combine weights live in LDS
     const int64_t qi = (int64_t)a.M * a.n_head;
     a.pmax = part;
@@ -334,9 +330,9 @@ hipError_t launch_attn_mfma(hipStream_t st, AttnMArgs a, float* part, int8_t* xq
     const int qtiles = (int)((a.M * (a.n_head / a.n_kv) + 31) / 32);
     const dim3 grid((unsigned)nch, (unsigned)a.n_kv, (unsigned)qtiles);
     if (a.hd == 128)
-        hipLaunchKernelGGL(k_attn_mfma<128>, grid, dim3(256), 0, st, a);
+        hipLaunchKernelGGL(k_attn_mfma<128>, grid, dim3(64 * 8), 0, st, a);
     else if (a.hd == 64)
-        hipLaunchKernelGGL(k_attn_mfma<64>, grid, dim3(256), 0, st, a);
+        hipLaunchKernelGGL(k_attn_mfma<64>, grid, dim3(64 * 4), 0, st, a);
     else
         return hipErrorInvalidValue;
     hipError_t e = hipGetLastError();

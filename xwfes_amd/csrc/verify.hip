@@ -48,7 +48,7 @@ static bool mv_all(const ftx_tensor* const* ts, int n, int64_t K, int64_t M) {
 struct ftx_kv {
     ftx_ctx* ctx = nullptr;
     int64_t n_layer = 0, cap = 0, kdim = 0, n_kv = 0, hd = 0;
-    int64_t cap_alloc = 0;  // slots allocated per layer, a multiple of 64
+    int64_t cap_alloc = 0;  // slots allocated per layer, a multiple of 128
     int kv_f16 = 1;
     void* k = nullptr;      // [n_layer][cap_alloc][kdim]
     void* v = nullptr;      // [n_layer][n_kv][hd][cap_alloc]
@@ -225,7 +225,7 @@ int ftx_kv_create(ftx_ctx* ctx, const ftx_model* m, int64_t cap, int kv_dtype, f
     kv->ctx = ctx;
     kv->n_layer = m->d.n_layer;
     kv->cap = cap;
-    kv->cap_alloc = (cap + 63) / 64 * 64;
+    kv->cap_alloc = (cap + 127) / 128 * 128;  // whole attention chunks
     kv->kdim = m->kdim;
     kv->n_kv = m->d.n_head_kv;
     kv->hd = m->d.head_dim;

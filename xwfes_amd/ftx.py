@@ -358,7 +358,7 @@ class KV:
 
     @property
     def cap_alloc(self):
-        return (self.cap + 63) // 64 * 64
+        return (self.cap + 127) // 128 * 128  # ftx_kv_create's rounding
 
     def write(self, k, v):
         """Copy host arrays shaped like self.shape (the reference layout)
