@@ -30,6 +30,7 @@ namespace {
 
 typedef _Float16 v8h __attribute__((ext_vector_type(8)));
 typedef _Float16 v2h __attribute__((ext_vector_type(2)));
+typedef _Float16 v4h __attribute__((ext_vector_type(4)));
 typedef float v4f __attribute__((ext_vector_type(4)));
 typedef int v4i __attribute__((ext_vector_type(4)));
 
@@ -61,29 +62,59 @@ __device__ __forceinline__ v8h nib8_to_h(uint32_t w, float bias) {
 }
 
 // One workgroup = one 256-column super-block (wave w: columns 64w..64w+63)
-// over a contiguous range of 32-row slices, processed in batches of NB
-// slices: stage the batch's h and row scales (prefetched into registers one
-// batch ahead), build the scaled fp16 hi/lo activation tables in LDS, then
-// the MFMAs over the batch's weights (also prefetched one batch ahead).
+// over a contiguous range of 32-row slices, in batches of NB slices.  The
+// row factors are split from the sub-block scales:
+//   Q4_K  y[m,j] = sum_i (h d)[m,i] * (sc_{i,s} q_{i,j}) - sum_i (h dmin)[m,i] * m_{i,s}
+//   Q6_K  y[m,j] = 16 sum_i (h d)[m,i] * (sh_{i,s} q_{i,j}) + sum_i (h d)[m,i] * (sl_{i,s} q_{i,j})
+//                  - 32 sum_i (h d)[m,i] * sc_{i,s}          (sc = 16 sh + sl, 0 <= sl < 16)
+// so the activation operand (h d, and h dmin) is shared by every sub-block
+// of the super-block and built once per slice per workgroup, as fp16 hi
+// (A rows 0..7, the tokens) + lo (rows 8..15) parts; the weight operand is
+// the integer sc * q (|.| <= 945, exact in fp16); the Q4_K min term and the
+// Q6_K -32 sc term are one more MFMA per slice, with the sub-block scales as
+// the B columns.  Per batch the workgroup builds the next batch's operands
+// into a double-buffered LDS stage (threads 0..127 the activation tables,
+// 128..255 the fp16 scale tables) while the waves run the current batch's
+// MFMAs; one barrier per batch.  The weights of the next two batches are in
+// flight in a three-slot register ring (the loop is unrolled by three so
+// that no ring slot is copied).
 template <int DT>
 struct DownCfg {
     static constexpr int NS = DT == FTX_Q4_K ? 8 : 16;  // sub-blocks per super-block
     static constexpr int NB = 4;                         // slices per batch
+    static constexpr int RP = NB * 32 + 8;               // padded scale-table row (halves)
+};
+// the activation operands are formed as (h d) * 2^10 so that their fp16 lo
+// parts stay clear of the subnormal range (an exact power of two, undone on
+// the outputs); |h d| < 64 keeps the hi parts finite
+constexpr float DOWN_ASCALE = 1024.f;
+
+template <int DT>
+struct DownW {
+    v4i q[DownCfg<DT>::NB];                        // QS / QL words of the lane
+    int2 h[DT == FTX_Q6_K ? DownCfg<DT>::NB : 1];  // Q6_K QH words
+};
+
+// prefetched inputs of one batch's stage: thread t owns rows 4q .. 4q+3 of
+// the batch (q = t / 8) and index e = t % 8 (token for the activation
+// tables, sub-block (and e + 8) for the scale tables); hv = h of token e on
+// those rows, r[k] = the header of row 4q + k, dd = (Q6_K) their d words.
+// Every thread issues the same loads and runs the same straight-line code,
+// so no divergent branch sits between a load and its use (the compiler's
+// vector-memory waits stay exact and the weights in flight are not drained).
+struct DownStageIn {
+    v4i hv;
+    v4i r[4];
+    int2 dd;
 };
 
 template <int DT>
 __global__ void __launch_bounds__(256) k_down_mfma(DownArgs a) {
-    constexpr int NS = DownCfg<DT>::NS, NB = DownCfg<DT>::NB;
-    // h / scale rows padded so 16-byte reads of different rows fall in
-    // different LDS banks; the activation tables are stored [octet of rows]
-    // [token][8 rows] so that one MFMA operand read covers consecutive bytes
-    constexpr int HP = NB * 32 + 4;
-    __shared__ float hs[8][HP];
-    __shared__ float dsc[NS][HP];  // [sub-block][row of the batch]
-    __shared__ float dmn[DT == FTX_Q4_K ? 8 : 1][HP];
-    __shared__ _Float16 ahi[NB][NS][4][8][8];
-    __shared__ _Float16 alo[NB][NS][4][8][8];
-    __shared__ float mpart[4][8][8];
+    constexpr int NS = DownCfg<DT>::NS, NB = DownCfg<DT>::NB, RP = DownCfg<DT>::RP;
+    constexpr int NT = DT == FTX_Q4_K ? 2 : 1;  // activation tables: h d (, h dmin)
+    constexpr int NC = DT == FTX_Q4_K ? 2 : 3;  // scale tables: sc, m | sh, sl, sc
+    __shared__ _Float16 tab[2][NT][NB][4][16][8];  // [buf][table][slice][k octet][A row][8]
+    __shared__ _Float16 sct[2][NC][NS][RP];        // [buf][table][sub-block][row]
     const int tid = threadIdx.x, lane = tid & 63, w = tid >> 6;
     const int64_t sbc = blockIdx.x, split = blockIdx.y;
     const int64_t nc64 = a.N / 64, nsl = a.n_in / 32;
@@ -91,174 +122,193 @@ __global__ void __launch_bounds__(256) k_down_mfma(DownArgs a) {
     const int64_t I1 = min(I0 + a.slices_per_split, nsl);
     const int col = lane & 15, g = lane >> 4;
     const int64_t c64 = sbc * 4 + w;
-    v4f acc[4];
+    v4f acc[4], acc2[DT == FTX_Q6_K ? 4 : 1], accs;
 #pragma unroll
     for (int ct = 0; ct < 4; ++ct) acc[ct] = v4f{0.f, 0.f, 0.f, 0.f};
-    float mt = 0.f;  // Q4_K min term of this thread's (s, m)
-    // ---- per-batch register prefetch: h (thread: m = tid / 32, row tid % 32
-    // of each slice), the row header (threads < NB * 32), the weights (lane)
-    float hp[NB];
-    v4i hdp = {0, 0, 0, 0};
-    uint16_t d6p = 0;
-    v4i wq[NB], wqn[NB];
-    int2 wh[NB], whn[NB];
-    auto slice_of = [&](int64_t I) { return I < I1 ? I : I1 - 1; };  // clamped for loads
-    auto load_hs = [&](int64_t Ib) {
-        const int m = tid >> 5, ii = tid & 31;
 #pragma unroll
-        for (int b = 0; b < NB; ++b) {
-            const int64_t I = Ib + b;
-            hp[b] = (m < a.M && I < I1) ? a.h[(int64_t)m * a.ldh + I * 32 + ii] : 0.f;
+    for (int ct = 0; ct < (DT == FTX_Q6_K ? 4 : 1); ++ct) acc2[ct] = v4f{0.f, 0.f, 0.f, 0.f};
+    accs = v4f{0.f, 0.f, 0.f, 0.f};
+    auto slice_of = [&](int64_t I) { return I < I1 ? I : I1 - 1; };  // clamped for loads
+    const int sq = tid >> 3, se = tid & 7;  // rows 4 sq .. 4 sq + 3 of the batch
+    const int hm = se < a.M ? se : 0;       // token row of h (masked in stage)
+    DownStageIn si;
+    auto load_stage = [&](int64_t Ib) {
+        const int64_t i0 = slice_of(Ib + sq / 8) * 32 + (sq % 8) * 4;
+        si.hv = *(const v4i*)(a.h + (int64_t)hm * a.ldh + i0);
+#pragma unroll
+        for (int k = 0; k < 4; ++k) si.r[k] = *(const v4i*)(a.hdr + (sbc * a.n_in + i0 + k) * 16);
+        if constexpr (DT == FTX_Q6_K) si.dd = *(const int2*)(a.d6 + (sbc * a.n_in + i0) * 2);
+    };
+    auto stage = [&](int64_t Ib, int buf) {
+        const int b = sq / 8, g8 = (sq / 2) % 4, k0 = (sq % 2) * 4;  // slice, k octet, first of 4
+        // activation tables: token se, 4 rows; h of tokens past M or of
+        // slices past the range is zero
+        const bool live = se < a.M && Ib + b < I1;
+        const v4f h4 = live ? __builtin_bit_cast(v4f, si.hv) : v4f{0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+        for (int t = 0; t < NT; ++t) {
+            v4h ph, pl;
+#pragma unroll
+            for (int k = 0; k < 4; ++k) {
+                uint32_t dw;
+                if constexpr (DT == FTX_Q4_K)
+                    dw = (uint32_t)si.r[k].x >> (16 * t);  // d | dmin << 16
+                else
+                    dw = (uint32_t)(k < 2 ? si.dd.x : si.dd.y) >> (16 * (k & 1));
+                const float p = h4[k] * h2f((uint16_t)(dw & 0xFFFF)) * DOWN_ASCALE;
+                const _Float16 hi = (_Float16)p;
+                ph[k] = hi;
+                pl[k] = (_Float16)(p - (float)hi);
+            }
+            *(v4h*)&tab[buf][t][b][g8][se][k0] = ph;
+            *(v4h*)&tab[buf][t][b][g8][8 + se][k0] = pl;
         }
-        if (tid < NB * 32) {
-            const int64_t i = slice_of(Ib + tid / 32) * 32 + tid % 32;
-            hdp = *(const v4i*)(a.hdr + (sbc * a.n_in + i) * 16);
-            if (DT == FTX_Q6_K) d6p = *(const uint16_t*)(a.d6 + (sbc * a.n_in + i) * 2);
+        // scale tables: sub-block se (Q6_K also se + 8), 4 rows
+        const int r0 = sq * 4;
+        if constexpr (DT == FTX_Q4_K) {
+            // 6-bit scale / min of sub-block se (GGUF K-quant packing)
+            const int sh = 8 * (se & 3);
+            v4h sc, mn;
+#pragma unroll
+            for (int k = 0; k < 4; ++k) {
+                const uint32_t S0 = si.r[k].y, S1 = si.r[k].z, S2 = si.r[k].w;
+                const uint32_t sc_lo = (S0 >> sh) & 0x3F, mn_lo = (S1 >> sh) & 0x3F;
+                const uint32_t sc_hi = ((S2 >> sh) & 0x0F) | (((S0 >> sh) >> 2) & 0x30);
+                const uint32_t mn_hi = ((S2 >> sh) >> 4 & 0x0F) | (((S1 >> sh) >> 2) & 0x30);
+                sc[k] = (_Float16)(float)(se < 4 ? sc_lo : sc_hi);
+                mn[k] = (_Float16)(float)(se < 4 ? mn_lo : mn_hi);
+            }
+            *(v4h*)&sct[buf][0][se][r0] = sc;
+            *(v4h*)&sct[buf][1][se][r0] = mn;
+        } else {
+#pragma unroll
+            for (int h2 = 0; h2 < 2; ++h2) {
+                const int sb = se + 8 * h2;
+                v4h vh, vl, vc;
+#pragma unroll
+                for (int k = 0; k < 4; ++k) {
+                    const int sc = (int)(int8_t)(((uint32_t)si.r[k][sb >> 2] >> (8 * (sb & 3))) & 0xFF);
+                    vh[k] = (_Float16)(float)(sc >> 4);  // sc = 16 sh + sl
+                    vl[k] = (_Float16)(float)(sc & 15);
+                    vc[k] = (_Float16)(float)sc;
+                }
+                *(v4h*)&sct[buf][0][sb][r0] = vh;
+                *(v4h*)&sct[buf][1][sb][r0] = vl;
+                *(v4h*)&sct[buf][2][sb][r0] = vc;
+            }
         }
     };
-    auto load_w = [&](int64_t Ib, v4i* q, int2* qh) {
+    auto load_w = [&](int64_t Ib, DownW<DT>& o) {
 #pragma unroll
         for (int b = 0; b < NB; ++b) {
             const int64_t blk = (slice_of(Ib + b) * nc64 + c64) * 4 + g;
-            q[b] = *(const v4i*)(a.qs + (blk * 16 + col) * 16);
-            if (DT == FTX_Q6_K) qh[b] = *(const int2*)(a.qh + (blk * 16 + col) * 8);
+            o.q[b] = *(const v4i*)(a.qs + (blk * 16 + col) * 16);
+            if constexpr (DT == FTX_Q6_K) o.h[b] = *(const int2*)(a.qh + (blk * 16 + col) * 8);
         }
     };
-    load_hs(I0);
-    load_w(I0, wq, wh);
-    for (int64_t Ib = I0; Ib < I1; Ib += NB) {
-        __syncthreads();  // the previous batch is done with the LDS tables
-        // ---- stage h and the per-row scales of this batch
-        {
-            const int m = tid >> 5, ii = tid & 31;
-#pragma unroll
-            for (int b = 0; b < NB; ++b) hs[m][b * 32 + ii] = hp[b];
-        }
-        if (tid < NB * 32) {
-            if (DT == FTX_Q4_K) {
-                const float d = h2f((uint16_t)((uint32_t)hdp.x & 0xFFFF));
-                const float dm = h2f((uint16_t)((uint32_t)hdp.x >> 16));
-                const uint32_t S0 = hdp.y, S1 = hdp.z, S2 = hdp.w;
-                const uint32_t sc_lo = S0 & 0x3F3F3F3Fu, mn_lo = S1 & 0x3F3F3F3Fu;
-                const uint32_t sc_hi = (S2 & 0x0F0F0F0Fu) | ((S0 >> 2) & 0x30303030u);
-                const uint32_t mn_hi = ((S2 >> 4) & 0x0F0F0F0Fu) | ((S1 >> 2) & 0x30303030u);
-#pragma unroll
-                for (int s = 0; s < 8; ++s) {
-                    const uint32_t scw = s < 4 ? sc_lo : sc_hi, mnw = s < 4 ? mn_lo : mn_hi;
-                    dsc[s][tid] = d * (float)((scw >> (8 * (s & 3))) & 0xFF);
-                    dmn[s][tid] = dm * (float)((mnw >> (8 * (s & 3))) & 0xFF);
-                }
-            } else {
-                const float d = h2f(d6p);
-                const uint32_t* scw = (const uint32_t*)&hdp;
-#pragma unroll
-                for (int s = 0; s < 16; ++s)
-                    dsc[s][tid] = d * (float)(int8_t)((scw[s >> 2] >> (8 * (s & 3))) & 0xFF);
-            }
-        }
-        // next batch's h and headers in flight from here
-        if (Ib + NB < I1) load_hs(Ib + NB);
-        __syncthreads();
-        // ---- A_s[m][i] = h * d * sc as fp16 hi + lo, for every slice of the batch
-        {
-            const int oct = tid >> 6, m = tid & 7, sp = (tid >> 3) & 7;
-#pragma unroll 1
-            for (int b = 0; b < NB; ++b) {
-#pragma unroll
-                for (int rep = 0; rep < NS / 8; ++rep) {
-                    const int s = sp * (NS / 8) + rep;
-                    const int i0 = b * 32 + oct * 8;
-                    // eight rows at once: two 16-byte LDS reads per table
-                    const v4f h0 = *(const v4f*)&hs[m][i0], h1 = *(const v4f*)&hs[m][i0 + 4];
-                    const v4f f0 = *(const v4f*)&dsc[s][i0], f1 = *(const v4f*)&dsc[s][i0 + 4];
-                    const float hv[8] = {h0[0], h0[1], h0[2], h0[3], h1[0], h1[1], h1[2], h1[3]};
-                    const float fv[8] = {f0[0], f0[1], f0[2], f0[3], f1[0], f1[1], f1[2], f1[3]};
-                    _Float16 ph[8], pl[8];
-#pragma unroll
-                    for (int k = 0; k < 8; ++k) {
-                        const float p = hv[k] * fv[k];
-                        const _Float16 hi = (_Float16)p;
-                        ph[k] = hi;
-                        pl[k] = (_Float16)(p - (float)hi);
-                    }
-                    if (DT == FTX_Q4_K) {
-                        const v4f n0 = *(const v4f*)&dmn[s][i0], n1 = *(const v4f*)&dmn[s][i0 + 4];
-                        const float nv[8] = {n0[0], n0[1], n0[2], n0[3], n1[0], n1[1], n1[2], n1[3]};
-#pragma unroll
-                        for (int k = 0; k < 8; ++k) mt += hv[k] * nv[k];
-                    }
-                    *(v8h*)&ahi[b][s][oct][m][0] =
-                        v8h{ph[0], ph[1], ph[2], ph[3], ph[4], ph[5], ph[6], ph[7]};
-                    *(v8h*)&alo[b][s][oct][m][0] =
-                        v8h{pl[0], pl[1], pl[2], pl[3], pl[4], pl[5], pl[6], pl[7]};
-                }
-            }
-        }
-        __syncthreads();
-        // next batch's weights in flight during this batch's MFMAs
-        if (Ib + NB < I1) load_w(Ib + NB, wqn, whn);
-        // ---- MFMA: this wave's 64 columns (4 tiles of 16) over the batch's rows
-        const int arow = lane & 15;  // A row (token m; rows 8..15 are zero)
-#pragma unroll
-        for (int b = 0; b < NB; ++b) {
-            const uint32_t* qw = (const uint32_t*)&wq[b];
-            const uint32_t qhw[2] = {(uint32_t)wh[b].x, (uint32_t)wh[b].y};
-#pragma unroll
-            for (int ct = 0; ct < 4; ++ct) {
-                v8h bv;
-                if (DT == FTX_Q4_K) {
-                    bv = nib8_to_h(qw[ct], 0.f);
-                } else {
-                    const uint32_t X = qhw[ct >> 1];
-                    const uint32_t hl = (ct & 1) ? (X << 4) & 0x30303030u : X & 0x30303030u;
-                    const uint32_t hh = (ct & 1) ? (X << 2) & 0x30303030u : (X >> 2) & 0x30303030u;
-                    const uint32_t L = qw[ct];
-                    const uint32_t vlo = (L & 0x0F0F0F0Fu) | hl;
-                    const uint32_t vhi = ((L >> 4) & 0x0F0F0F0Fu) | hh;
-                    // 6-bit values: place as (lo nibble word, hi nibble word)
-                    const uint32_t p0 = __builtin_amdgcn_perm(vlo, 0x64646464u, 0x00050004u);
-                    const uint32_t p1 = __builtin_amdgcn_perm(vlo, 0x64646464u, 0x00070006u);
-                    const uint32_t p2 = __builtin_amdgcn_perm(vhi, 0x64646464u, 0x00050004u);
-                    const uint32_t p3 = __builtin_amdgcn_perm(vhi, 0x64646464u, 0x00070006u);
-                    const v2h bb = {(_Float16)(-1056.f), (_Float16)(-1056.f)};
-                    const v2h h0 = __builtin_bit_cast(v2h, p0) + bb, h1 = __builtin_bit_cast(v2h, p1) + bb;
-                    const v2h h2 = __builtin_bit_cast(v2h, p2) + bb, h3 = __builtin_bit_cast(v2h, p3) + bb;
-                    bv = v8h{h0[0], h0[1], h1[0], h1[1], h2[0], h2[1], h3[0], h3[1]};
-                }
-                const int s = DT == FTX_Q4_K ? (w * 64 + ct * 16) / 32 : (w * 64 + ct * 16) / 16;
-                v8h ah = {}, al = {};
-                if (arow < 8) {
-                    ah = *(const v8h*)&ahi[b][s][g][arow][0];
-                    al = *(const v8h*)&alo[b][s][g][arow][0];
-                }
-                acc[ct] = __builtin_amdgcn_mfma_f32_16x16x32_f16(ah, bv, acc[ct], 0, 0, 0);
-                acc[ct] = __builtin_amdgcn_mfma_f32_16x16x32_f16(al, bv, acc[ct], 0, 0, 0);
-            }
-        }
-#pragma unroll
-        for (int b = 0; b < NB; ++b) {
-            wq[b] = wqn[b];
-            if (DT == FTX_Q6_K) wh[b] = whn[b];
-        }
-    }
-    // ---- min term per (s, m), summed over the four row octets
-    if (DT == FTX_Q4_K) {
-        mpart[tid >> 6][(tid >> 3) & 7][tid & 7] = mt;
-        __syncthreads();
-    }
-    // lane (col, g) holds C[row 4g + r][col]; rows 0..7 are the tokens
-    if (g < 2) {
+    // MFMAs of slice b of the staged batch in buf
+    auto mfma = [&](int buf, const DownW<DT>& wt, int b) {
+        const uint32_t* qw = (const uint32_t*)&wt.q[b];
+        const int r0 = b * 32 + 8 * g;
+        const v8h av = *(const v8h*)&tab[buf][0][b][g][col][0];
 #pragma unroll
         for (int ct = 0; ct < 4; ++ct) {
+            if constexpr (DT == FTX_Q4_K) {
+                const v8h q = nib8_to_h(qw[ct], 0.f);
+                const v8h sc = *(const v8h*)&sct[buf][0][2 * w + (ct >> 1)][r0];
+                acc[ct] = __builtin_amdgcn_mfma_f32_16x16x32_f16(av, q * sc, acc[ct], 0, 0, 0);
+            } else {
+                const uint32_t X = ct < 2 ? (uint32_t)wt.h[b].x : (uint32_t)wt.h[b].y;
+                const uint32_t hl = (ct & 1) ? (X << 4) & 0x30303030u : X & 0x30303030u;
+                const uint32_t hh = (ct & 1) ? (X << 2) & 0x30303030u : (X >> 2) & 0x30303030u;
+                const uint32_t L = qw[ct];
+                const uint32_t vlo = (L & 0x0F0F0F0Fu) | hl;
+                const uint32_t vhi = ((L >> 4) & 0x0F0F0F0Fu) | hh;
+                // 6-bit q as (lo nibble word, hi nibble word) -> fp16 1024 + q
+                const uint32_t p0 = __builtin_amdgcn_perm(vlo, 0x64646464u, 0x00050004u);
+                const uint32_t p1 = __builtin_amdgcn_perm(vlo, 0x64646464u, 0x00070006u);
+                const uint32_t p2 = __builtin_amdgcn_perm(vhi, 0x64646464u, 0x00050004u);
+                const uint32_t p3 = __builtin_amdgcn_perm(vhi, 0x64646464u, 0x00070006u);
+                const v2h bb = {(_Float16)(-1024.f), (_Float16)(-1024.f)};
+                const v2h h0 = __builtin_bit_cast(v2h, p0) + bb, h1 = __builtin_bit_cast(v2h, p1) + bb;
+                const v2h h2 = __builtin_bit_cast(v2h, p2) + bb, h3 = __builtin_bit_cast(v2h, p3) + bb;
+                const v8h q = v8h{h0[0], h0[1], h1[0], h1[1], h2[0], h2[1], h3[0], h3[1]};
+                const int s = 4 * w + ct;
+                const v8h sh = *(const v8h*)&sct[buf][0][s][r0];
+                const v8h sl = *(const v8h*)&sct[buf][1][s][r0];
+                acc[ct] = __builtin_amdgcn_mfma_f32_16x16x32_f16(av, q * sh, acc[ct], 0, 0, 0);
+                acc2[ct] = __builtin_amdgcn_mfma_f32_16x16x32_f16(av, q * sl, acc2[ct], 0, 0, 0);
+            }
+        }
+        // sub-block term: B column col = sub-block (Q4_K: rows of m, with the
+        // h dmin operand; Q6_K: sc, with the h d operand)
+        const v8h as = DT == FTX_Q4_K ? *(const v8h*)&tab[buf][NT - 1][b][g][col][0] : av;
+        v8h bsv = *(const v8h*)&sct[buf][NC - 1][col % NS][r0];
+        if (col >= NS) bsv = v8h{};
+        accs = __builtin_amdgcn_mfma_f32_16x16x32_f16(as, bsv, accs, 0, 0, 0);
+    };
+    // One batch: the next batch's stage into the other buffer, the inputs two
+    // batches ahead (stage inputs before weights), then the MFMAs of the
+    // staged batch.  Vector-memory counters retire in issue order, so each
+    // wait (stage inputs of the next batch, weights of this one) covers only
+    // loads issued before it: the stage inputs of batch b+1 precede the
+    // weights of b+1, the weights of b precede the stage inputs of b+1.
+    // (loads past the range re-read its last slice, so that every batch
+    // issues the same loads)
+    auto batch = [&](int64_t Ib, int buf, DownW<DT>& cur, DownW<DT>& fill) {
+        stage(Ib + NB, buf ^ 1);
+        load_stage(Ib + 2 * NB);
+        load_w(Ib + 2 * NB, fill);
+#pragma unroll
+        for (int b = 0; b < NB; ++b) {
+            if (Ib + b >= I1) break;
+            mfma(buf, cur, b);
+        }
+        __syncthreads();
+    };
+    DownW<DT> w0, w1, w2;
+    load_w(I0, w0);
+    load_stage(I0);
+    stage(I0, 0);
+    load_stage(I0 + NB);
+    load_w(I0 + NB, w1);
+    __syncthreads();
+    int buf = 0;
+    for (int64_t Ib = I0; Ib < I1; Ib += 3 * NB) {
+        batch(Ib, buf, w0, w2);
+        buf ^= 1;
+        if (Ib + NB >= I1) break;
+        batch(Ib + NB, buf, w1, w0);
+        buf ^= 1;
+        if (Ib + 2 * NB >= I1) break;
+        batch(Ib + 2 * NB, buf, w2, w1);
+        buf ^= 1;
+    }
+    // lane (col, g) holds C[4g + r][col]: rows 0..7 the hi parts, 8..15 the
+    // lo parts of tokens 4(g % 2) + r; the sub-block term of (token, s) sits
+    // in lane (s, g) of accs
+#pragma unroll
+    for (int r = 0; r < 4; ++r) accs[r] += __shfl_xor(accs[r], 32, 64);
+#pragma unroll
+    for (int ct = 0; ct < 4; ++ct) {
+        v4f o = acc[ct];
+#pragma unroll
+        for (int r = 0; r < 4; ++r) {
+            o[r] += __shfl_xor(o[r], 32, 64);
+            if constexpr (DT == FTX_Q6_K)
+                o[r] = 16.f * o[r] + (acc2[ct][r] + __shfl_xor(acc2[ct][r], 32, 64));
+        }
+        const int s = DT == FTX_Q4_K ? 2 * w + (ct >> 1) : 4 * w + ct;
+        v4f t;
+#pragma unroll
+        for (int r = 0; r < 4; ++r) t[r] = __shfl(accs[r], s + 16 * g, 64);
+        if (g < 2) {
             const int64_t j = sbc * 256 + w * 64 + ct * 16 + col;
-            const int s = (w * 64 + ct * 16) / 32;
 #pragma unroll
             for (int r = 0; r < 4; ++r) {
                 const int m = 4 * g + r;
-                float v = acc[ct][r];
-                if (DT == FTX_Q4_K)
-                    v -= mpart[0][s][m] + mpart[1][s][m] + mpart[2][s][m] + mpart[3][s][m];
-                a.part[(split * 8 + m) * a.N + j] = v;
+                const float v = DT == FTX_Q4_K ? o[r] - t[r] : o[r] - 32.f * t[r];
+                a.part[(split * 8 + m) * a.N + j] = v * (1.f / DOWN_ASCALE);
             }
         }
     }
@@ -390,11 +440,15 @@ hipError_t launch_down_mfma(hipStream_t st, int dt, const uint8_t* tiled, int64_
     a.n_in = n_in;
     a.N = N;
     const int64_t nslices = n_in / 32, nsb = N / 256;
-    // splits of the contraction: as many workgroups as fit the CUs at once
-    // (LDS: three Q4_K or two Q6_K workgroups per CU), at most 64, each a
-    // whole number of slice batches
+    // splits of the contraction: two workgroups per CU (measured best on the
+    // 8B shapes; more splits add partial traffic and shorten each range), at
+    // most 64, each a whole number of slice batches
     const int NB = dt == FTX_Q4_K ? DownCfg<FTX_Q4_K>::NB : DownCfg<FTX_Q6_K>::NB;
-    const int64_t per_cu = dt == FTX_Q4_K ? 3 : 2;
+#ifdef DOWN_PER_CU
+    const int64_t per_cu = DOWN_PER_CU;
+#else
+    const int64_t per_cu = 2;
+#endif
     int64_t S = (per_cu * (int64_t)(cu_count > 0 ? cu_count : 256) + nsb - 1) / nsb;
     if (S > 64) S = 64;
     if (S > nslices) S = nslices;
