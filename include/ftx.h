@@ -250,6 +250,13 @@ typedef struct {
 int ftx_trace(ftx_ctx* ctx, int enable);
 /* Waits for the stream, then returns one entry per kernel class seen. */
 int ftx_trace_read(ftx_ctx* ctx, ftx_trace_entry* out, int max, int* n);
+/* Measurement hook with no counterpart in the reference: while tracing,
+ * each launch of class `kind` (a trace entry name) whose outputs do not
+ * depend on its own earlier results is issued `times` times back to back
+ * between its events (counted as `times` launches), so that a class's
+ * average launch time is not dominated by the events' own overhead.
+ * times = 1 switches it off. */
+int ftx_trace_replay(ftx_ctx* ctx, const char* kind, int times);
 
 #ifdef __cplusplus
 }

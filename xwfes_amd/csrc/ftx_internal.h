@@ -33,6 +33,7 @@ struct TraceRec {
     int kind;
     int ev0, ev1;
     double bytes;
+    int launches;
 };
 
 struct ftx_ctx {
@@ -45,6 +46,10 @@ struct ftx_ctx {
     int64_t tr_launches[TK_COUNT] = {};
     double tr_ms[TK_COUNT] = {};
     double tr_bytes[TK_COUNT] = {};
+    // ftx_trace_replay: launches of class replay_kind at idempotent call
+    // sites are issued replay_n times between their events
+    int replay_kind = -1;
+    int replay_n = 1;
     hipStream_t own_stream = nullptr;
     hipStream_t stream = nullptr;
     std::string err;
@@ -93,7 +98,9 @@ bool ftx_is_device_ptr(const void* p);
 // trace brackets: tr_begin returns a token (-1 when tracing is off) that
 // tr_end closes after the launch
 int tr_begin(ftx_ctx* ctx);
-void tr_end(ftx_ctx* ctx, int token, int kind, double bytes);
+void tr_end(ftx_ctx* ctx, int token, int kind, double bytes, int launches = 1);
+// issues of one launch at an idempotent call site (1 unless replayed)
+int tr_repeats(const ftx_ctx* ctx, int kind);
 
 // ---------------------------------------------------------------- launchers
 // All enqueue on `st` and return hipError_t of the launch.

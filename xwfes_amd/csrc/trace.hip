@@ -1,6 +1,7 @@
 // trace.hip -- per-kernel-class device time from HIP events recorded around
 // each launch on the context's stream (ftx_trace / ftx_trace_read).
 #include <cstdio>
+#include <cstring>
 
 #include "ftx_internal.h"
 
@@ -20,7 +21,7 @@ static void resolve(ftx_ctx* ctx) {
             (void)hipGetLastError();
             continue;
         }
-        ctx->tr_launches[r.kind] += 1;
+        ctx->tr_launches[r.kind] += r.launches;
         ctx->tr_ms[r.kind] += ms;
         ctx->tr_bytes[r.kind] += r.bytes;
     }
@@ -52,7 +53,7 @@ int tr_begin(ftx_ctx* ctx) {
     return e;
 }
 
-void tr_end(ftx_ctx* ctx, int token, int kind, double bytes) {
+void tr_end(ftx_ctx* ctx, int token, int kind, double bytes, int launches) {
     if (token < 0 || !ctx->trace) return;
     const int e = take_event(ctx);
     if (e < 0) return;
@@ -60,7 +61,11 @@ void tr_end(ftx_ctx* ctx, int token, int kind, double bytes) {
         (void)hipGetLastError();
         return;
     }
-    ctx->pending.push_back(TraceRec{kind, token, e, bytes});
+    ctx->pending.push_back(TraceRec{kind, token, e, bytes, launches});
+}
+
+int tr_repeats(const ftx_ctx* ctx, int kind) {
+    return ctx->trace && kind == ctx->replay_kind ? ctx->replay_n : 1;
 }
 
 extern "C" {
@@ -76,6 +81,18 @@ int ftx_trace(ftx_ctx* ctx, int enable) {
             ctx->tr_bytes[k] = 0;
         }
     return FTX_OK;
+}
+
+int ftx_trace_replay(ftx_ctx* ctx, const char* kind, int times) {
+    if (!ctx) return FTX_E_INVALID;
+    if (!kind || times < 1) return ftx_fail(ctx, FTX_E_INVALID, "trace_replay: bad arguments");
+    for (int k = 0; k < TK_COUNT; ++k)
+        if (!strcmp(kind, kTraceNames[k])) {
+            ctx->replay_kind = times > 1 ? k : -1;
+            ctx->replay_n = times;
+            return FTX_OK;
+        }
+    return ftx_fail(ctx, FTX_E_INVALID, "trace_replay: unknown kernel class");
 }
 
 int ftx_trace_read(ftx_ctx* ctx, ftx_trace_entry* out, int max, int* n) {

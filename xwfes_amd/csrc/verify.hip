@@ -383,6 +383,15 @@ int ftx_verify_step(ftx_ctx* ctx, ftx_model* m, ftx_kv* kv, const ftx_verify_arg
         FTX_HIP(ctx, call);                       \
         tr_end(ctx, tk_, (kind), (double)(bytes)); \
     } while (0)
+    // a launch whose outputs do not depend on its own earlier results
+    // (no accumulate into its inputs): replayable by ftx_trace_replay
+#define TRACED_IDEM(kind, bytes, call)                                  \
+    do {                                                                \
+        const int tk_ = tr_begin(ctx);                                  \
+        const int n_ = tr_repeats(ctx, (kind));                         \
+        for (int r_ = 0; r_ < n_; ++r_) FTX_HIP(ctx, call);              \
+        tr_end(ctx, tk_, (kind), (double)(bytes) * n_, n_);             \
+    } while (0)
     TRACED(TK_EMBED, Md * d.tok_embd->row_bytes + Md * D * f4,
            launch_embed(st, d.tok_embd->data, d.tok_embd->dtype, d.tok_embd->row_bytes, D,
                         m->toks, M, m->x));
@@ -408,14 +417,21 @@ int ftx_verify_step(ftx_ctx* ctx, ftx_model* m, ftx_kv* kv, const ftx_verify_arg
                 segs[i].tiled = 1;
                 segs[i].rpt = m->mvt_rpt[tix0 + tix[i]];
             }
-            if (!xq_ready)
-                TRACED(TK_XQ_PREP, Md * K * f4 * (fold ? 2.0 + fold_S : 1.0) + 19.0 * K,
-                       launch_xq_prep(st, xin, ldx, normw, fold ? m->downpart : nullptr,
-                                      fold ? fold_S : 0, D, K, M, m->xq));
+            if (!xq_ready && fold)  // adds the split partials into x: not replayable
+                TRACED(TK_XQ_PREP, Md * K * f4 * (2.0 + fold_S) + 19.0 * K,
+                       launch_xq_prep(st, xin, ldx, normw, m->downpart, fold_S, D, K, M, m->xq));
+            else if (!xq_ready)
+                TRACED_IDEM(TK_XQ_PREP, Md * K * f4 + 19.0 * K,
+                            launch_xq_prep(st, xin, ldx, normw, nullptr, 0, D, K, M, m->xq));
             if (fold) fold_S = 0;
-            TRACED(kind, bytes,
-                   launch_mv(st, segs, nseg, m->xq, K, M, epi, ctx->cu_count, normw != nullptr,
-                             eps, qe));
+            if (epi == EPI_ACCUM)
+                TRACED(kind, bytes,
+                       launch_mv(st, segs, nseg, m->xq, K, M, epi, ctx->cu_count,
+                                 normw != nullptr, eps, qe));
+            else
+                TRACED_IDEM(kind, bytes,
+                            launch_mv(st, segs, nseg, m->xq, K, M, epi, ctx->cu_count,
+                                      normw != nullptr, eps, qe));
             return FTX_OK;
         }
         if (fold) {
@@ -506,8 +522,8 @@ int ftx_verify_step(ftx_ctx* ctx, ftx_model* m, ftx_kv* kv, const ftx_verify_arg
             am.n_kv = (int)d.n_head_kv;
             am.hd = (int)d.head_dim;
             am.out = m->att;
-            TRACED(TK_ATTENTION, attn_b,
-                   launch_attn_mfma(st, am, kv->attn_part, o_xq ? m->xq : nullptr));
+            TRACED_IDEM(TK_ATTENTION, attn_b,
+                        launch_attn_mfma(st, am, kv->attn_part, o_xq ? m->xq : nullptr));
         } else {
             AttnArgs aa{m->qkv,  m->ldq, kl,       vl,          kv->kv_f16, m->npast,
                         m->anc,  aw,     d.n_head, d.n_head_kv, d.head_dim, npast + M,
@@ -527,9 +543,9 @@ int ftx_verify_step(ftx_ctx* ctx, ftx_model* m, ftx_kv* kv, const ftx_verify_arg
         if (rc) return rc;
         const double down_b = wbytes(T[FTX_T_DOWN]) + Md * F * f4 + 2 * Md * D * f4;
         if (m->down_tiled[l] && down_mfma_supported(T[FTX_T_DOWN]->dtype, F, D, M))
-            TRACED(TK_DOWN, down_b,
-                   launch_down_mfma(st, T[FTX_T_DOWN]->dtype, m->down_tiled[l], F, D, m->h, F, M,
-                                    m->x, D, m->downpart, ctx->cu_count, &fold_S));
+            TRACED_IDEM(TK_DOWN, down_b,
+                        launch_down_mfma(st, T[FTX_T_DOWN]->dtype, m->down_tiled[l], F, D, m->h,
+                                         F, M, m->x, D, m->downpart, ctx->cu_count, &fold_S));
         else
             TRACED(TK_DOWN, down_b,
                    launch_down(st, T[FTX_T_DOWN]->data, T[FTX_T_DOWN]->dtype,

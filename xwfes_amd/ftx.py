@@ -116,6 +116,7 @@ def load(path=LIB_PATH):
         "ftx_fill_normal": (C.c_int, [_vp, _vp, C.c_int, _i64, C.c_uint64, C.c_float]),
         "ftx_trace": (C.c_int, [_vp, C.c_int]),
         "ftx_trace_read": (C.c_int, [_vp, C.POINTER(TraceEntry), C.c_int, C.POINTER(C.c_int)]),
+        "ftx_trace_replay": (C.c_int, [_vp, C.c_char_p, C.c_int]),
     }
     for name, (res, args) in sig.items():
         f = getattr(L, name)
@@ -221,6 +222,11 @@ class Context:
         self.check(self.lib.ftx_trace_read(self.h, buf, 32, C.byref(n)))
         return {buf[i].name.decode(): dict(launches=buf[i].launches, ms=buf[i].ms,
                                            bytes=buf[i].bytes) for i in range(n.value)}
+
+    def trace_replay(self, kind, times):
+        """While tracing, issue each replayable launch of class `kind` `times`
+        times back to back between its events (1 = off)."""
+        self.check(self.lib.ftx_trace_replay(self.h, kind.encode(), int(times)))
 
     def copy(self, dst, src, nbytes):
         self.check(self.lib.ftx_stage(self.h, dst, src, nbytes))
