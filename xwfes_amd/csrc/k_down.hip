@@ -61,11 +61,11 @@ __device__ __forceinline__ v8h nib8_to_h(uint32_t w, float bias) {
     return v8h{h0[0], h0[1], h1[0], h1[1], h2[0], h2[1], h3[0], h3[1]};
 }
 
-// One workgroup = one 256-column super-block (wave w: columns 64w..64w+63)
-// over a contiguous range of 32-row slices, in batches of NB slices.  The
+// One workgroup = one 256-column super-block over a contiguous range of
+// 32-row slices, in batches of NB slices.  The
 // row factors are split from the sub-block scales:
 //   Q4_K  y[m,j] = sum_i (h d)[m,i] * (sc_{i,s} q_{i,j}) - sum_i (h dmin)[m,i] * m_{i,s}
-//   Q6_K  y[m,j] = 16 sum_i (h d)[m,i] * (sh_{i,s} q_{i,j}) + sum_i (h d)[m,i] * (sl_{i,s} q_{i,j})
+//   Q6_K  y[m,j] = sum_i (16 h d)[m,i] * (sh_{i,s} q_{i,j}) + sum_i (h d)[m,i] * (sl_{i,s} q_{i,j})
 //                  - 32 sum_i (h d)[m,i] * sc_{i,s}          (sc = 16 sh + sl, 0 <= sl < 16)
 // so the activation operand (h d, and h dmin) is shared by every sub-block
 // of the super-block and built once per slice per workgroup, as fp16 hi
@@ -75,102 +75,117 @@ __device__ __forceinline__ v8h nib8_to_h(uint32_t w, float bias) {
 // the B columns.  Per batch the workgroup builds the next batch's operands
 // into a double-buffered LDS stage (threads 0..127 the activation tables,
 // 128..255 the fp16 scale tables) while the waves run the current batch's
-// MFMAs; one barrier per batch.  The weights of the next two batches are in
-// flight in a three-slot register ring (the loop is unrolled by three so
-// that no ring slot is copied).
+// MFMAs; one barrier per batch.  The weights of the next batches are in
+// flight in a register ring (the loop is unrolled by the ring size so that
+// no ring slot is copied).
 template <int DT>
 struct DownCfg {
     static constexpr int NS = DT == FTX_Q4_K ? 8 : 16;  // sub-blocks per super-block
     static constexpr int NB = 4;                         // slices per batch
     static constexpr int RP = NB * 32 + 8;               // padded scale-table row (halves)
+    // weight register ring: batches of weights in flight ahead of the one
+    // computed is RING - 1 (Q6_K's larger words take one slot less, which
+    // keeps it within 128 VGPRs, four waves per SIMD)
+    static constexpr int RING = DT == FTX_Q4_K ? 3 : 2;
 };
 // the activation operands are formed as (h d) * 2^10 so that their fp16 lo
 // parts stay clear of the subnormal range (an exact power of two, undone on
-// the outputs); |h d| < 64 keeps the hi parts finite
+// the outputs); |h d| < 64 keeps the hi parts finite, |h d| < 4 for Q6_K,
+// whose sh term takes the operand times 16 (Q6_K d is at most max|w| / 4064)
 constexpr float DOWN_ASCALE = 1024.f;
+
+// 8 waves: wave w takes columns 64 (w % 4) .. + 63 and, of each batch, the
+// slices 2 (w / 4) and 2 (w / 4) + 1; the two slice groups' outputs are added
+// in LDS at the end (wave order)
+constexpr int DOWN_WAVES = 8;
+constexpr int DOWN_SPW = 2;  // slices of a batch per wave
 
 template <int DT>
 struct DownW {
-    v4i q[DownCfg<DT>::NB];                        // QS / QL words of the lane
-    int2 h[DT == FTX_Q6_K ? DownCfg<DT>::NB : 1];  // Q6_K QH words
+    v4i q[DOWN_SPW];                        // QS / QL words of the lane
+    int2 h[DT == FTX_Q6_K ? DOWN_SPW : 1];  // Q6_K QH words
 };
 
-// prefetched inputs of one batch's stage: thread t owns rows 4q .. 4q+3 of
-// the batch (q = t / 8) and index e = t % 8 (token for the activation
-// tables, sub-block (and e + 8) for the scale tables); hv = h of token e on
-// those rows, r[k] = the header of row 4q + k, dd = (Q6_K) their d words.
-// Every thread issues the same loads and runs the same straight-line code,
-// so no divergent branch sits between a load and its use (the compiler's
+// prefetched inputs of one batch's stage: thread t owns rows 2q, 2q+1 of the
+// batch (q = t / 8) and index e = t % 8 (token for the activation tables,
+// sub-block (and e + 8) for the scale tables); hv = h of token e on those
+// rows, r[k] = the header of row 2q + k, dd = (Q6_K) their d words.  Every
+// thread issues the same loads and runs the same straight-line code, so no
+// divergent branch sits between a load and its use (the compiler's
 // vector-memory waits stay exact and the weights in flight are not drained).
 struct DownStageIn {
-    v4i hv;
-    v4i r[4];
-    int2 dd;
+    int2 hv;
+    v4i r[2];
+    uint32_t dd;
 };
 
 template <int DT>
-__global__ void __launch_bounds__(256) k_down_mfma(DownArgs a) {
+__global__ void __launch_bounds__(64 * DOWN_WAVES) __attribute__((amdgpu_waves_per_eu(4)))
+k_down_mfma(DownArgs a) {
     constexpr int NS = DownCfg<DT>::NS, NB = DownCfg<DT>::NB, RP = DownCfg<DT>::RP;
     constexpr int NT = DT == FTX_Q4_K ? 2 : 1;  // activation tables: h d (, h dmin)
     constexpr int NC = DT == FTX_Q4_K ? 2 : 3;  // scale tables: sc, m | sh, sl, sc
     __shared__ _Float16 tab[2][NT][NB][4][16][8];  // [buf][table][slice][k octet][A row][8]
     __shared__ _Float16 sct[2][NC][NS][RP];        // [buf][table][sub-block][row]
-    const int tid = threadIdx.x, lane = tid & 63, w = tid >> 6;
+    __shared__ float red[4][16][64];              // slice group 1's outputs
+    const int tid = threadIdx.x, lane = tid & 63;
+    const int w = __builtin_amdgcn_readfirstlane(tid >> 6);  // wave-uniform: scalar branches
+    const int cw = w & 3, sgp = w >> 2;  // column quarter, slice group
     const int64_t sbc = blockIdx.x, split = blockIdx.y;
     const int64_t nc64 = a.N / 64, nsl = a.n_in / 32;
     const int64_t I0 = split * a.slices_per_split;
     const int64_t I1 = min(I0 + a.slices_per_split, nsl);
     const int col = lane & 15, g = lane >> 4;
-    const int64_t c64 = sbc * 4 + w;
-    v4f acc[4], acc2[DT == FTX_Q6_K ? 4 : 1], accs;
+    const int64_t c64 = sbc * 4 + cw;
+    v4f acc[4], accs;
 #pragma unroll
     for (int ct = 0; ct < 4; ++ct) acc[ct] = v4f{0.f, 0.f, 0.f, 0.f};
-#pragma unroll
-    for (int ct = 0; ct < (DT == FTX_Q6_K ? 4 : 1); ++ct) acc2[ct] = v4f{0.f, 0.f, 0.f, 0.f};
     accs = v4f{0.f, 0.f, 0.f, 0.f};
     auto slice_of = [&](int64_t I) { return I < I1 ? I : I1 - 1; };  // clamped for loads
-    const int sq = tid >> 3, se = tid & 7;  // rows 4 sq .. 4 sq + 3 of the batch
+    const int sq = tid >> 3, se = tid & 7;  // rows 2 sq, 2 sq + 1 of the batch
     const int hm = se < a.M ? se : 0;       // token row of h (masked in stage)
     DownStageIn si;
     auto load_stage = [&](int64_t Ib) {
-        const int64_t i0 = slice_of(Ib + sq / 8) * 32 + (sq % 8) * 4;
-        si.hv = *(const v4i*)(a.h + (int64_t)hm * a.ldh + i0);
+        const int64_t i0 = slice_of(Ib + sq / 16) * 32 + (sq % 16) * 2;
+        si.hv = *(const int2*)(a.h + (int64_t)hm * a.ldh + i0);
 #pragma unroll
-        for (int k = 0; k < 4; ++k) si.r[k] = *(const v4i*)(a.hdr + (sbc * a.n_in + i0 + k) * 16);
-        if constexpr (DT == FTX_Q6_K) si.dd = *(const int2*)(a.d6 + (sbc * a.n_in + i0) * 2);
+        for (int k = 0; k < 2; ++k) si.r[k] = *(const v4i*)(a.hdr + (sbc * a.n_in + i0 + k) * 16);
+        if constexpr (DT == FTX_Q6_K) si.dd = *(const uint32_t*)(a.d6 + (sbc * a.n_in + i0) * 2);
     };
     auto stage = [&](int64_t Ib, int buf) {
-        const int b = sq / 8, g8 = (sq / 2) % 4, k0 = (sq % 2) * 4;  // slice, k octet, first of 4
-        // activation tables: token se, 4 rows; h of tokens past M or of
+        const int b = sq / 16, g8 = (sq / 4) % 4, k0 = (sq % 4) * 2;  // slice, k octet, first of 2
+        // activation tables: token se, 2 rows; h of tokens past M or of
         // slices past the range is zero
-        const bool live = se < a.M && Ib + b < I1;
-        const v4f h4 = live ? __builtin_bit_cast(v4f, si.hv) : v4f{0.f, 0.f, 0.f, 0.f};
+        // (a 0 / 1 factor, not a select: keeps the block free of branches)
+        const float lf = (float)((se < a.M) & (Ib + b < I1));
+        const float2 h2 = __builtin_bit_cast(float2, si.hv);
+        const float hv2[2] = {h2.x * lf, h2.y * lf};
 #pragma unroll
         for (int t = 0; t < NT; ++t) {
-            v4h ph, pl;
+            v2h ph, pl;
 #pragma unroll
-            for (int k = 0; k < 4; ++k) {
+            for (int k = 0; k < 2; ++k) {
                 uint32_t dw;
                 if constexpr (DT == FTX_Q4_K)
                     dw = (uint32_t)si.r[k].x >> (16 * t);  // d | dmin << 16
                 else
-                    dw = (uint32_t)(k < 2 ? si.dd.x : si.dd.y) >> (16 * (k & 1));
-                const float p = h4[k] * h2f((uint16_t)(dw & 0xFFFF)) * DOWN_ASCALE;
+                    dw = si.dd >> (16 * k);
+                const float p = hv2[k] * h2f((uint16_t)(dw & 0xFFFF)) * DOWN_ASCALE;
                 const _Float16 hi = (_Float16)p;
                 ph[k] = hi;
                 pl[k] = (_Float16)(p - (float)hi);
             }
-            *(v4h*)&tab[buf][t][b][g8][se][k0] = ph;
-            *(v4h*)&tab[buf][t][b][g8][8 + se][k0] = pl;
+            *(v2h*)&tab[buf][t][b][g8][se][k0] = ph;
+            *(v2h*)&tab[buf][t][b][g8][8 + se][k0] = pl;
         }
-        // scale tables: sub-block se (Q6_K also se + 8), 4 rows
-        const int r0 = sq * 4;
+        // scale tables: sub-block se (Q6_K also se + 8), 2 rows
+        const int r0 = sq * 2;
         if constexpr (DT == FTX_Q4_K) {
             // 6-bit scale / min of sub-block se (GGUF K-quant packing)
             const int sh = 8 * (se & 3);
-            v4h sc, mn;
+            v2h sc, mn;
 #pragma unroll
-            for (int k = 0; k < 4; ++k) {
+            for (int k = 0; k < 2; ++k) {
                 const uint32_t S0 = si.r[k].y, S1 = si.r[k].z, S2 = si.r[k].w;
                 const uint32_t sc_lo = (S0 >> sh) & 0x3F, mn_lo = (S1 >> sh) & 0x3F;
                 const uint32_t sc_hi = ((S2 >> sh) & 0x0F) | (((S0 >> sh) >> 2) & 0x30);
@@ -178,47 +193,51 @@ __global__ void __launch_bounds__(256) k_down_mfma(DownArgs a) {
                 sc[k] = (_Float16)(float)(se < 4 ? sc_lo : sc_hi);
                 mn[k] = (_Float16)(float)(se < 4 ? mn_lo : mn_hi);
             }
-            *(v4h*)&sct[buf][0][se][r0] = sc;
-            *(v4h*)&sct[buf][1][se][r0] = mn;
+            *(v2h*)&sct[buf][0][se][r0] = sc;
+            *(v2h*)&sct[buf][1][se][r0] = mn;
         } else {
 #pragma unroll
             for (int h2 = 0; h2 < 2; ++h2) {
                 const int sb = se + 8 * h2;
-                v4h vh, vl, vc;
+                v2h vh, vl, vc;
 #pragma unroll
-                for (int k = 0; k < 4; ++k) {
+                for (int k = 0; k < 2; ++k) {
                     const int sc = (int)(int8_t)(((uint32_t)si.r[k][sb >> 2] >> (8 * (sb & 3))) & 0xFF);
                     vh[k] = (_Float16)(float)(sc >> 4);  // sc = 16 sh + sl
                     vl[k] = (_Float16)(float)(sc & 15);
                     vc[k] = (_Float16)(float)sc;
                 }
-                *(v4h*)&sct[buf][0][sb][r0] = vh;
-                *(v4h*)&sct[buf][1][sb][r0] = vl;
-                *(v4h*)&sct[buf][2][sb][r0] = vc;
+                *(v2h*)&sct[buf][0][sb][r0] = vh;
+                *(v2h*)&sct[buf][1][sb][r0] = vl;
+                *(v2h*)&sct[buf][2][sb][r0] = vc;
             }
         }
     };
     auto load_w = [&](int64_t Ib, DownW<DT>& o) {
 #pragma unroll
-        for (int b = 0; b < NB; ++b) {
-            const int64_t blk = (slice_of(Ib + b) * nc64 + c64) * 4 + g;
-            o.q[b] = *(const v4i*)(a.qs + (blk * 16 + col) * 16);
-            if constexpr (DT == FTX_Q6_K) o.h[b] = *(const int2*)(a.qh + (blk * 16 + col) * 8);
+        for (int bb = 0; bb < DOWN_SPW; ++bb) {
+            const int64_t blk = (slice_of(Ib + sgp * DOWN_SPW + bb) * nc64 + c64) * 4 + g;
+            o.q[bb] = *(const v4i*)(a.qs + (blk * 16 + col) * 16);
+            if constexpr (DT == FTX_Q6_K) o.h[bb] = *(const int2*)(a.qh + (blk * 16 + col) * 8);
         }
     };
-    // MFMAs of slice b of the staged batch in buf
-    auto mfma = [&](int buf, const DownW<DT>& wt, int b) {
-        const uint32_t* qw = (const uint32_t*)&wt.q[b];
+    // MFMAs of slice b = 2 sgp + bb of the staged batch in buf
+    auto mfma = [&](int buf, const DownW<DT>& wt, int bb) {
+        const int b = sgp * DOWN_SPW + bb;
+        const uint32_t* qw = (const uint32_t*)&wt.q[bb];
         const int r0 = b * 32 + 8 * g;
         const v8h av = *(const v8h*)&tab[buf][0][b][g][col][0];
+        // Q6_K: sc q = 16 sh q + sl q with both products exact in fp16; the
+        // 16 goes on the activation operand (exact), one accumulator
+        const v8h av16 = av * (_Float16)16.f;
 #pragma unroll
         for (int ct = 0; ct < 4; ++ct) {
             if constexpr (DT == FTX_Q4_K) {
                 const v8h q = nib8_to_h(qw[ct], 0.f);
-                const v8h sc = *(const v8h*)&sct[buf][0][2 * w + (ct >> 1)][r0];
+                const v8h sc = *(const v8h*)&sct[buf][0][2 * cw + (ct >> 1)][r0];
                 acc[ct] = __builtin_amdgcn_mfma_f32_16x16x32_f16(av, q * sc, acc[ct], 0, 0, 0);
             } else {
-                const uint32_t X = ct < 2 ? (uint32_t)wt.h[b].x : (uint32_t)wt.h[b].y;
+                const uint32_t X = ct < 2 ? (uint32_t)wt.h[bb].x : (uint32_t)wt.h[bb].y;
                 const uint32_t hl = (ct & 1) ? (X << 4) & 0x30303030u : X & 0x30303030u;
                 const uint32_t hh = (ct & 1) ? (X << 2) & 0x30303030u : (X >> 2) & 0x30303030u;
                 const uint32_t L = qw[ct];
@@ -233,11 +252,11 @@ __global__ void __launch_bounds__(256) k_down_mfma(DownArgs a) {
                 const v2h h0 = __builtin_bit_cast(v2h, p0) + bb, h1 = __builtin_bit_cast(v2h, p1) + bb;
                 const v2h h2 = __builtin_bit_cast(v2h, p2) + bb, h3 = __builtin_bit_cast(v2h, p3) + bb;
                 const v8h q = v8h{h0[0], h0[1], h1[0], h1[1], h2[0], h2[1], h3[0], h3[1]};
-                const int s = 4 * w + ct;
+                const int s = 4 * cw + ct;
                 const v8h sh = *(const v8h*)&sct[buf][0][s][r0];
                 const v8h sl = *(const v8h*)&sct[buf][1][s][r0];
-                acc[ct] = __builtin_amdgcn_mfma_f32_16x16x32_f16(av, q * sh, acc[ct], 0, 0, 0);
-                acc2[ct] = __builtin_amdgcn_mfma_f32_16x16x32_f16(av, q * sl, acc2[ct], 0, 0, 0);
+                acc[ct] = __builtin_amdgcn_mfma_f32_16x16x32_f16(av16, q * sh, acc[ct], 0, 0, 0);
+                acc[ct] = __builtin_amdgcn_mfma_f32_16x16x32_f16(av, q * sl, acc[ct], 0, 0, 0);
             }
         }
         // sub-block term: B column col = sub-block (Q4_K: rows of m, with the
@@ -247,22 +266,22 @@ __global__ void __launch_bounds__(256) k_down_mfma(DownArgs a) {
         if (col >= NS) bsv = v8h{};
         accs = __builtin_amdgcn_mfma_f32_16x16x32_f16(as, bsv, accs, 0, 0, 0);
     };
-    // One batch: the next batch's stage into the other buffer, the inputs two
-    // batches ahead (stage inputs before weights), then the MFMAs of the
-    // staged batch.  Vector-memory counters retire in issue order, so each
-    // wait (stage inputs of the next batch, weights of this one) covers only
-    // loads issued before it: the stage inputs of batch b+1 precede the
-    // weights of b+1, the weights of b precede the stage inputs of b+1.
-    // (loads past the range re-read its last slice, so that every batch
-    // issues the same loads)
+    // One batch: the next batch's stage into the other buffer, the stage
+    // inputs two batches ahead and the weights RING - 1 ahead (stage inputs
+    // first), then the MFMAs of the staged batch.  Vector-memory counters
+    // retire in issue order, so each wait (stage inputs of the next batch,
+    // weights of this one) covers only loads issued before it.  (Loads past
+    // the range re-read its last slice, so that every batch issues the same
+    // loads.)
+    constexpr int RING = DownCfg<DT>::RING;
     auto batch = [&](int64_t Ib, int buf, DownW<DT>& cur, DownW<DT>& fill) {
         stage(Ib + NB, buf ^ 1);
         load_stage(Ib + 2 * NB);
-        load_w(Ib + 2 * NB, fill);
+        load_w(Ib + (RING - 1) * NB, fill);
 #pragma unroll
-        for (int b = 0; b < NB; ++b) {
-            if (Ib + b >= I1) break;
-            mfma(buf, cur, b);
+        for (int bb = 0; bb < DOWN_SPW; ++bb) {
+            if (Ib + sgp * DOWN_SPW + bb >= I1) break;
+            mfma(buf, cur, bb);
         }
         __syncthreads();
     };
@@ -271,18 +290,27 @@ __global__ void __launch_bounds__(256) k_down_mfma(DownArgs a) {
     load_stage(I0);
     stage(I0, 0);
     load_stage(I0 + NB);
-    load_w(I0 + NB, w1);
+    if constexpr (RING == 3) load_w(I0 + NB, w1);
     __syncthreads();
     int buf = 0;
-    for (int64_t Ib = I0; Ib < I1; Ib += 3 * NB) {
-        batch(Ib, buf, w0, w2);
-        buf ^= 1;
-        if (Ib + NB >= I1) break;
-        batch(Ib + NB, buf, w1, w0);
-        buf ^= 1;
-        if (Ib + 2 * NB >= I1) break;
-        batch(Ib + 2 * NB, buf, w2, w1);
-        buf ^= 1;
+    // unrolled by the ring size so that every slot is a fixed register set
+    for (int64_t Ib = I0; Ib < I1; Ib += RING * NB) {
+        if constexpr (RING == 3) {
+            batch(Ib, buf, w0, w2);
+            buf ^= 1;
+            if (Ib + NB >= I1) break;
+            batch(Ib + NB, buf, w1, w0);
+            buf ^= 1;
+            if (Ib + 2 * NB >= I1) break;
+            batch(Ib + 2 * NB, buf, w2, w1);
+            buf ^= 1;
+        } else {
+            batch(Ib, buf, w0, w1);
+            buf ^= 1;
+            if (Ib + NB >= I1) break;
+            batch(Ib + NB, buf, w1, w0);
+            buf ^= 1;
+        }
     }
     // lane (col, g) holds C[4g + r][col]: rows 0..7 the hi parts, 8..15 the
     // lo parts of tokens 4(g % 2) + r; the sub-block term of (token, s) sits
@@ -293,21 +321,27 @@ __global__ void __launch_bounds__(256) k_down_mfma(DownArgs a) {
     for (int ct = 0; ct < 4; ++ct) {
         v4f o = acc[ct];
 #pragma unroll
-        for (int r = 0; r < 4; ++r) {
-            o[r] += __shfl_xor(o[r], 32, 64);
-            if constexpr (DT == FTX_Q6_K)
-                o[r] = 16.f * o[r] + (acc2[ct][r] + __shfl_xor(acc2[ct][r], 32, 64));
-        }
-        const int s = DT == FTX_Q4_K ? 2 * w + (ct >> 1) : 4 * w + ct;
+        for (int r = 0; r < 4; ++r) o[r] += __shfl_xor(o[r], 32, 64);
+        const int s = DT == FTX_Q4_K ? 2 * cw + (ct >> 1) : 4 * cw + ct;
         v4f t;
 #pragma unroll
         for (int r = 0; r < 4; ++r) t[r] = __shfl(accs[r], s + 16 * g, 64);
-        if (g < 2) {
-            const int64_t j = sbc * 256 + w * 64 + ct * 16 + col;
+#pragma unroll
+        for (int r = 0; r < 4; ++r) {
+            o[r] = DT == FTX_Q4_K ? o[r] - t[r] : o[r] - 32.f * t[r];
+            if (sgp) red[cw][ct * 4 + r][lane] = o[r];
+        }
+        acc[ct] = o;
+    }
+    __syncthreads();
+    if (sgp == 0 && g < 2) {
+#pragma unroll
+        for (int ct = 0; ct < 4; ++ct) {
+            const int64_t j = sbc * 256 + cw * 64 + ct * 16 + col;
 #pragma unroll
             for (int r = 0; r < 4; ++r) {
                 const int m = 4 * g + r;
-                const float v = DT == FTX_Q4_K ? o[r] - t[r] : o[r] - 32.f * t[r];
+                const float v = acc[ct][r] + red[cw][ct * 4 + r][lane];
                 a.part[(split * 8 + m) * a.N + j] = v * (1.f / DOWN_ASCALE);
             }
         }
@@ -460,9 +494,9 @@ hipError_t launch_down_mfma(hipStream_t st, int dt, const uint8_t* tiled, int64_
     a.part = part;
     const dim3 grid((unsigned)nsb, (unsigned)S);
     if (dt == FTX_Q4_K)
-        hipLaunchKernelGGL(k_down_mfma<FTX_Q4_K>, grid, dim3(256), 0, st, a);
+        hipLaunchKernelGGL(k_down_mfma<FTX_Q4_K>, grid, dim3(64 * DOWN_WAVES), 0, st, a);
     else
-        hipLaunchKernelGGL(k_down_mfma<FTX_Q6_K>, grid, dim3(256), 0, st, a);
+        hipLaunchKernelGGL(k_down_mfma<FTX_Q6_K>, grid, dim3(64 * DOWN_WAVES), 0, st, a);
     hipError_t e = hipGetLastError();
     if (e != hipSuccess) return e;
     if (splits) {
