@@ -54,54 +54,62 @@ __device__ __forceinline__ void reg_fence8(int* v) {
 }
 
 // ---------------------------------------------------------------- prep
-// One wave per (256-element super-block sb, activation row m < 8); rows
-// m >= M are written as zeros.  Lane l takes elements 4l .. 4l+3.
+// One workgroup of 256 threads per (256-element super-block sb, activation
+// row m < 8); rows m >= M are written as zeros.  Thread t forms element t:
 //  - fold (part != null): x += sum_s part[s][m][.] over the S split
-//    partials of the previous ffn_down, in split order, written back to x
-//    (the residual add of src/engine.cpp:274-275);
-//  - RMSNorm (src/engine.cpp:23-41) in front when normw is given: the limbs
-//    of x * w are formed with the block scale max|x * w| / 127 -- the limbs
-//    do not depend on the row's 1 / rms factor, which the consuming GEMV
-//    applies to the block scales from the per-block sums of x^2 stored in
-//    ssq[sb][m].
-__global__ void __launch_bounds__(64) k_xq_prep(float* __restrict__ x, int64_t ldx,
-                                                const float* __restrict__ normw,
-                                                const float* __restrict__ part, int S,
-                                                int64_t ldpart, int64_t K, int M,
-                                                int8_t* __restrict__ frag,
-                                                int8_t* __restrict__ xs32,
-                                                int8_t* __restrict__ xs16,
-                                                float* __restrict__ scale,
-                                                float* __restrict__ ssq) {
+//    partials of the previous ffn_down, added in split order (loads issued
+//    16 splits at a time), written back to x (the residual add of
+//    src/engine.cpp:274-275);
+// then wave 0 (lane l: elements 4l .. 4l+3, from LDS) applies
+//  - RMSNorm (src/engine.cpp:23-41) when normw is given: the limbs of x * w
+//    are formed with the block scale max|x * w| / 127 -- the limbs do not
+//    depend on the row's 1 / rms factor, which the consuming GEMV applies
+//    to the block scales from the per-block sums of x^2 stored in ssq[sb][m]
+// and writes the limbs.
+__global__ void __launch_bounds__(256) k_xq_prep(float* __restrict__ x, int64_t ldx,
+                                                 const float* __restrict__ normw,
+                                                 const float* __restrict__ part, int S,
+                                                 int64_t ldpart, int64_t K, int M,
+                                                 int8_t* __restrict__ frag,
+                                                 int8_t* __restrict__ xs32,
+                                                 int8_t* __restrict__ xs16,
+                                                 float* __restrict__ scale,
+                                                 float* __restrict__ ssq) {
 #pragma clang fp contract(off)
+    __shared__ float vs[256];
     const int64_t sb = blockIdx.x;
-    const int m = blockIdx.y, l = threadIdx.x;
-    const bool live = m < M;
+    const int m = blockIdx.y, t = threadIdx.x;
+    const bool live = m < M;  // block-uniform
     float* row = x + (int64_t)m * ldx;
+    if (live) {
+        const int64_t k = sb * 256 + t;
+        float v = row[k];
+        if (part) {
+            float acc = 0.f;
+            for (int s0 = 0; s0 < S; s0 += 16) {
+                float p[16];
+#pragma unroll
+                for (int i = 0; i < 16; ++i)
+                    p[i] = s0 + i < S ? part[((int64_t)(s0 + i) * 8 + m) * ldpart + k] : 0.f;
+#pragma unroll
+                for (int i = 0; i < 16; ++i) acc += p[i];
+            }
+            v += acc;
+            row[k] = v;
+        }
+        vs[t] = v;
+    }
+    __syncthreads();
+    if (t >= 64) return;
+    const int l = t;
     const int64_t k0 = sb * 256 + 4 * l;
     float v[4] = {0.f, 0.f, 0.f, 0.f};
     if (live) {
-        const float4 t = *(const float4*)(row + k0);
-        v[0] = t.x;
-        v[1] = t.y;
-        v[2] = t.z;
-        v[3] = t.w;
-        if (part) {
-            float4 acc = {0.f, 0.f, 0.f, 0.f};
-#pragma unroll 8
-            for (int s = 0; s < S; ++s) {
-                const float4 p = *(const float4*)(part + ((int64_t)s * 8 + m) * ldpart + k0);
-                acc.x += p.x;
-                acc.y += p.y;
-                acc.z += p.z;
-                acc.w += p.w;
-            }
-            v[0] += acc.x;
-            v[1] += acc.y;
-            v[2] += acc.z;
-            v[3] += acc.w;
-            *(float4*)(row + k0) = make_float4(v[0], v[1], v[2], v[3]);
-        }
+        const float4 t4 = *(const float4*)&vs[4 * l];
+        v[0] = t4.x;
+        v[1] = t4.y;
+        v[2] = t4.z;
+        v[3] = t4.w;
         if (normw) {
             float ss = v[0] * v[0];
             ss += v[1] * v[1];
@@ -651,7 +659,7 @@ hipError_t launch_xq_prep(hipStream_t st, float* x, int64_t ldx, const float* no
     int8_t* frag = xq;
     int8_t* xs32 = xq + K * 16;
     int8_t* xs16 = xs32 + K;
-    hipLaunchKernelGGL(k_xq_prep, dim3((unsigned)(K / 256), 8), dim3(64), 0, st, x, ldx, normw,
+    hipLaunchKernelGGL(k_xq_prep, dim3((unsigned)(K / 256), 8), dim3(256), 0, st, x, ldx, normw,
                        part, S, ldpart, K, (int)M, frag, xs32, xs16, xq_scale(xq, K),
                        xq_ssq(xq, K));
     return hipGetLastError();

@@ -10,7 +10,8 @@ import os
 import numpy as np
 
 HERE = os.path.dirname(os.path.abspath(__file__))
-LIB_PATH = os.path.join(HERE, "libftx.so")
+# FTX_LIB selects another build of the library (e.g. to compare two builds)
+LIB_PATH = os.environ.get("FTX_LIB") or os.path.join(HERE, "libftx.so")
 HEADER = os.path.join(os.path.dirname(HERE), "include", "ftx.h")
 
 F32, F16, Q4_0, Q4_1, Q8_0, Q4_K, Q6_K, BF16 = 0, 1, 2, 3, 8, 12, 14, 30
