@@ -105,6 +105,19 @@ def cpu_baseline(ctx, tensors, cfg, ctx_len, M, props, threads):
                        % (M, ctx_len, times[1], times[2], cfg["n_layer"], t_step))
 
 
+def measured_traffic(workload, kernel_class):
+    """HBM bytes per launch of `kernel_class` as measured by the FETCH_SIZE /
+    WRITE_SIZE counter passes recorded in profiles/traffic_<workload>.json
+    (copy-calibrated; the commands are in the file), or None."""
+    path = os.path.join(ROOT, "profiles", "traffic_%s.json" % workload)
+    try:
+        with open(path) as f:
+            t = json.load(f)
+    except (OSError, ValueError):
+        return None
+    return t.get("bytes_per_launch") if t.get("class") == kernel_class else None
+
+
 def main():
     ap = argparse.ArgumentParser()
     ap.add_argument("--gpus", type=int, default=1)
@@ -236,7 +249,7 @@ def main():
                      "frac": round(achieved / HBM_PEAK_GBS, 4),
                      "bytes_per_launch": per_launch_b, "us_per_launch": round(per_launch_ms * 1e3, 2),
                      "replays": REPLAY,
-                     "traffic": None},
+                     "traffic": measured_traffic(args.workload, dom_name)},
         "cpu_baseline": None,
     }
     if not args.no_cpu_baseline:
