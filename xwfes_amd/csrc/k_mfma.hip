@@ -429,12 +429,12 @@ __device__ __forceinline__ float row16_sum(float v) {
 }
 
 // items in flight ahead of the one being computed, within the register
-// budget of each instantiation (Q6_K blocks are 1.5x Q4_K's)
-template <int DT, bool PAIR>
+// budget of each instantiation (Q6_K blocks are 1.5x Q4_K's); DEEP (single
+// tiles, waves of a multiple of 4 super-blocks): three ahead, so that a
+// 4-item wave has all its weights in flight at once
+template <int DT, bool PAIR, bool DEEP>
 constexpr int mv_depth() {
-#ifdef MV_DEPTH_Q4
-    if (DT == FTX_Q4_K) return MV_DEPTH_Q4;
-#endif
+    if (DEEP) return 3;
     return DT == FTX_Q4_K ? 1 : (PAIR ? 0 : 1);
 }
 
@@ -447,7 +447,7 @@ constexpr int mv_depth() {
 // operand, then the first weights (vector-memory counters retire in issue
 // order); the activation operand of super-block j + 1 is in flight while j
 // computes, and the residual of the accumulate epilogue is read up front.
-template <int DT, bool TILED, bool PAIR>
+template <int DT, bool TILED, bool PAIR, bool DEEP>
 __device__ __forceinline__ void mv_unit(const MvArgs& a, int64_t u) {
     __shared__ float part[PAIR ? 2 : 1][MV_WAVES][256];  // [tile of unit][wave][m * 32 + col]
     const int w = threadIdx.x >> 6, lane = threadIdx.x & 63, col = lane & 31, g = lane >> 5;
@@ -482,8 +482,9 @@ __device__ __forceinline__ void mv_unit(const MvArgs& a, int64_t u) {
     // the weights of the next D items are in flight during an item's
     // arithmetic (a ring of D + 1 register buffers; loads past the last item
     // re-read it)
-    constexpr int D = mv_depth<DT, PAIR>();
-    static_assert(D <= 1, "the ring index below assumes D + 1 divides 2 * tpu");
+    constexpr int D = mv_depth<DT, PAIR, DEEP>();
+    static_assert(D <= 1 || (D == 3 && !PAIR), "ring index: D + 1 must divide STEP * tpu");
+    constexpr int STEP = D == 3 ? 4 : 2;  // super-blocks per unrolled step
     MvW<DT> buf[D + 1];
     auto item_load = [&](MvW<DT>& o, int j) {
         j = j < nit ? j : nit - 1;
@@ -501,7 +502,7 @@ __device__ __forceinline__ void mv_unit(const MvArgs& a, int64_t u) {
             ss.w += t.w;
         }
     __builtin_amdgcn_sched_barrier(0);
-    MvX<DT> x[2];
+    MvX<DT> x[DEEP ? 1 : 2];
     mv_load_x<DT>(x[0], a, sb0, col, g);
     __builtin_amdgcn_sched_barrier(0);
 #pragma unroll
@@ -536,15 +537,20 @@ __device__ __forceinline__ void mv_unit(const MvArgs& a, int64_t u) {
         inv[2] = 1.f / sqrtf(row16_sum(ss.z) / kf + a.eps);
         inv[3] = 1.f / sqrtf(row16_sum(ss.w) / kf + a.eps);
     }
-    // two super-blocks per step: x[h] holds super-block sb0 + k + h; the
-    // item index i = (k + h) * tpu + ti keeps i % (D + 1) = (h * tpu + ti) %
-    // (D + 1) because k is even
-    for (int k = 0; k < spw; k += 2) {
+    // STEP super-blocks per unrolled step: x[h % 2] holds super-block
+    // sb0 + k + h; the item index i = (k + h) * tpu + ti keeps i % (D + 1) =
+    // (h * tpu + ti) % (D + 1) because k is a multiple of STEP
+    for (int k = 0; k < spw; k += STEP) {
 #pragma unroll
-        for (int h = 0; h < 2; ++h) {
-            if (k + h + 1 < spw) mv_load_x<DT>(x[h ^ 1], a, sb0 + k + h + 1, col, g);
-            const float4 s4 = make_float4(x[h].s4.x * inv[0], x[h].s4.y * inv[1],
-                                          x[h].s4.z * inv[2], x[h].s4.w * inv[3]);
+        for (int h = 0; h < STEP; ++h) {
+            // (DEEP: one activation buffer, loaded as its super-block starts --
+            // the registers go to the weights, the longer-latency loads)
+            constexpr int XB = DEEP ? 1 : 2;
+            const int xc = h % XB;
+            if (DEEP && k + h > 0) mv_load_x<DT>(x[0], a, sb0 + k + h, col, g);
+            if (!DEEP && k + h + 1 < spw) mv_load_x<DT>(x[(h + 1) % XB], a, sb0 + k + h + 1, col, g);
+            const float4 s4 = make_float4(x[xc].s4.x * inv[0], x[xc].s4.y * inv[1],
+                                          x[xc].s4.z * inv[2], x[xc].s4.w * inv[3]);
 #pragma unroll
             for (int ti = 0; ti < tpu; ++ti) {
                 const int il = h * tpu + ti;
@@ -552,7 +558,7 @@ __device__ __forceinline__ void mv_unit(const MvArgs& a, int64_t u) {
                 __builtin_amdgcn_sched_barrier(0);
                 item_load(buf[(il + D) % (D + 1)], i + D);
                 __builtin_amdgcn_sched_barrier(0);
-                mv_block<DT>(buf[il % (D + 1)], x[h], s4, col, g, acc[ti]);
+                mv_block<DT>(buf[il % (D + 1)], x[xc], s4, col, g, acc[ti]);
             }
         }
     }
@@ -613,22 +619,22 @@ __device__ __forceinline__ void mv_unit(const MvArgs& a, int64_t u) {
     }
 }
 
-template <int DT, bool TILED, bool PAIR>
+template <int DT, bool TILED, bool PAIR, bool DEEP>
 __global__ void __launch_bounds__(64 * MV_WAVES) __attribute__((amdgpu_waves_per_eu(MV_WPE_SINGLE)))
 k_mv(MvArgs a) {
-    mv_unit<DT, TILED, PAIR>(a, blockIdx.x);
+    mv_unit<DT, TILED, PAIR, DEEP>(a, blockIdx.x);
 }
 
 // one launch over segments of both dtypes (q / k Q4_K with a Q6_K v): each
 // workgroup takes the path of its unit's segment
-template <bool TILED>
+template <bool TILED, bool DEEP>
 __global__ void __launch_bounds__(64 * MV_WAVES) __attribute__((amdgpu_waves_per_eu(MV_WPE_SINGLE)))
 k_mv_mix(MvArgs a) {
     const int64_t u = blockIdx.x;
     if (a.seg[mv_seg_of(a, u)].dt == FTX_Q4_K)
-        mv_unit<FTX_Q4_K, TILED, false>(a, u);
+        mv_unit<FTX_Q4_K, TILED, false, DEEP>(a, u);
     else
-        mv_unit<FTX_Q6_K, TILED, false>(a, u);
+        mv_unit<FTX_Q6_K, TILED, false, false>(a, u);  // deep Q6_K does not fit 256 VGPRs
 }
 
 // y[m*ldy + n] += sum_s part[s][m][n] in split order (ffn_down's splits)
@@ -762,16 +768,25 @@ hipError_t launch_mv(hipStream_t st, const GemvSeg* segs, int nseg, const int8_t
         int W = 1;
         while (W < MV_WAVES && a.nsb % (2 * W) == 0 && units * W * 2 <= (int64_t)cus * 8) W *= 2;
         const dim3 gd((unsigned)units), bd(64 * W);
-        // instantiations: {Q4_K, Q6_K} x {row, tiled} x {single, SwiGLU pair}
+        // single Q4_K tiles whose waves take 4 super-blocks: every weight in
+        // flight at once (Q6_K's larger blocks do not fit four deep)
+        const bool deep = !pair && a.nsb / W == 4 && (mixed || dt == FTX_Q4_K);
+        // instantiations: {Q4_K, Q6_K} x {row, tiled} x {single, SwiGLU pair, deep single}
         using K_t = void (*)(MvArgs);
-        static const K_t kern[2][2][2] = {
-            {{k_mv<FTX_Q4_K, false, false>, k_mv<FTX_Q4_K, false, true>},
-             {k_mv<FTX_Q4_K, true, false>, k_mv<FTX_Q4_K, true, true>}},
-            {{k_mv<FTX_Q6_K, false, false>, k_mv<FTX_Q6_K, false, true>},
-             {k_mv<FTX_Q6_K, true, false>, k_mv<FTX_Q6_K, true, true>}}};
-        static const K_t kmix[2] = {k_mv_mix<false>, k_mv_mix<true>};
-        hipLaunchKernelGGL(mixed ? kmix[tiled] : kern[dt == FTX_Q6_K][tiled][pair], gd, bd, 0, st,
-                           a);
+        static const K_t kern[2][2][3] = {
+            {{k_mv<FTX_Q4_K, false, false, false>, k_mv<FTX_Q4_K, false, true, false>,
+              k_mv<FTX_Q4_K, false, false, true>},
+             {k_mv<FTX_Q4_K, true, false, false>, k_mv<FTX_Q4_K, true, true, false>,
+              k_mv<FTX_Q4_K, true, false, true>}},
+            {{k_mv<FTX_Q6_K, false, false, false>, k_mv<FTX_Q6_K, false, true, false>,
+              k_mv<FTX_Q6_K, false, false, false>},
+             {k_mv<FTX_Q6_K, true, false, false>, k_mv<FTX_Q6_K, true, true, false>,
+              k_mv<FTX_Q6_K, true, false, false>}}};
+        static const K_t kmix[2][2] = {{k_mv_mix<false, false>, k_mv_mix<false, true>},
+                                       {k_mv_mix<true, false>, k_mv_mix<true, true>}};
+        hipLaunchKernelGGL(mixed ? kmix[tiled][deep]
+                                 : kern[dt == FTX_Q6_K][tiled][pair ? 1 : (deep ? 2 : 0)],
+                           gd, bd, 0, st, a);
         hipError_t e = hipGetLastError();
         if (e != hipSuccess) return e;
     }
