@@ -28,7 +28,11 @@ typedef _Float16 v4h __attribute__((ext_vector_type(4)));
 typedef float v4f __attribute__((ext_vector_type(4)));
 
 // slots per chunk (one workgroup of hd / 16 waves) for head size hd
+#ifndef ATTN_CHK
 __host__ __device__ constexpr int chunk_slots(int hd) { return hd; }
+#else
+__host__ __device__ constexpr int chunk_slots(int) { return ATTN_CHK; }
+#endif
 
 __device__ __forceinline__ bool slot_visible(const AttnMArgs& a, int64_t npast, int m, int64_t p) {
     if (p < npast) return true;
@@ -37,16 +41,20 @@ __device__ __forceinline__ bool slot_visible(const AttnMArgs& a, int64_t npast, 
     return (a.anc[(int64_t)m * a.anc_words + (j >> 5)] >> (j & 31)) & 1u;
 }
 
-template <int HD>
+template <int HD, int CHK>
 __global__ void __launch_bounds__(64 * (HD / 16)) k_attn_mfma(AttnMArgs a) {
-    constexpr int NW = HD / 16;   // waves: 16 score slots and 16 output dims each
-    constexpr int CHK = 16 * NW;  // slots per chunk (= HD)
+    constexpr int NW = HD / 16;   // waves: 16 output dims each
+    constexpr int NST = CHK / 16; // 16-slot tiles of the chunk
+    // score tiles (slot tile, query tile) per wave: pair p = w PPW + i takes
+    // slot tile p / 2 and query tile p % 2
+    constexpr int PPW = 2 * NST / NW;
+    static_assert(PPW == 1 || PPW == 2, "a wave takes one or two score tiles of one slot tile");
     constexpr int NDC = HD / 32;  // 32-dim chunks of the score contraction
     constexpr int QP = HD + 8;    // padded query row (halves)
     constexpr int PP = CHK + 8;   // padded P row (halves)
     __shared__ _Float16 qs[2][32][QP];  // query hi / lo [part][row][dim]
     __shared__ _Float16 ps[2][32][PP];  // P hi / lo [part][query row][slot]
-    __shared__ float smax[NW][32], ssum[NW][32], cmax[32];
+    __shared__ float smax[NST][32], ssum[NST][32], cmax[32];
     const int tid = threadIdx.x, w = tid >> 6, lane = tid & 63, col = lane & 15, g = lane >> 4;
     const int64_t npast = a.npast;
     const int64_t total = npast + a.M;
@@ -58,7 +66,8 @@ __global__ void __launch_bounds__(64 * (HD / 16)) k_attn_mfma(AttnMArgs a) {
     const int qrows = a.M * gqa;
     const int qbase = blockIdx.z * 32;  // first query row of this tile
     const int64_t kdim = (int64_t)a.n_kv * HD;
-    const int64_t ws0 = slot0 + 16 * w;  // this wave's score slots
+    const int sst = (w * PPW) >> 1;          // this wave's slot tile
+    const int64_t ws0 = slot0 + 16 * sst;    // its score slots
     // ---- operand loads, all issued up front: K rows (A of S^T: slot ws0 +
     // col, dims 32 dc + 8 g ..), V^T rows (B of O: dim 16 w + col, slots
     // slot0 + 16 st + 4 g ..), then the query hi / lo parts into LDS
@@ -68,11 +77,11 @@ __global__ void __launch_bounds__(64 * (HD / 16)) k_attn_mfma(AttnMArgs a) {
 #pragma unroll
         for (int dc = 0; dc < NDC; ++dc) kf[dc] = *(const v8h*)(krow + 32 * dc);
     }
-    v4h vf[NW];
+    v4h vf[NST];
     {
         const _Float16* vrow = a.vt + ((int64_t)kvh * HD + 16 * w + col) * a.cap + slot0 + 4 * g;
 #pragma unroll
-        for (int st = 0; st < NW; ++st) vf[st] = *(const v4h*)(vrow + 16 * st);
+        for (int st = 0; st < NST; ++st) vf[st] = *(const v4h*)(vrow + 16 * st);
     }
     // 16-byte vectors of the staged queries: 2 parts x 32 rows x HD / 8
 #pragma unroll
@@ -88,11 +97,12 @@ __global__ void __launch_bounds__(64 * (HD / 16)) k_attn_mfma(AttnMArgs a) {
         *(v8h*)&qs[part][r][8 * dv] = x;
     }
     __syncthreads();
-    // ---- S^T = K . Q^T for the two 16-row query tiles; lane (col, g) then
+    // ---- S^T = K . Q^T for the wave's query tiles; lane (col, g) then
     // holds S^T[slot ws0 + 4g + r][query row qt * 16 + col]
-    v4f sc[2];
+    v4f sc[PPW];
 #pragma unroll
-    for (int qt = 0; qt < 2; ++qt) {
+    for (int pi = 0; pi < PPW; ++pi) {
+        const int qt = (w * PPW + pi) & 1;
         v4f acc = {0.f, 0.f, 0.f, 0.f};
 #pragma unroll
         for (int dc = 0; dc < NDC; ++dc) {
@@ -101,12 +111,13 @@ __global__ void __launch_bounds__(64 * (HD / 16)) k_attn_mfma(AttnMArgs a) {
             acc = __builtin_amdgcn_mfma_f32_16x16x32_f16(kf[dc], qh, acc, 0, 0, 0);
             acc = __builtin_amdgcn_mfma_f32_16x16x32_f16(kf[dc], ql, acc, 0, 0, 0);
         }
-        sc[qt] = acc;
+        sc[pi] = acc;
     }
     // masked, scaled scores and this wave's row maxima
     const float scale = 1.f / sqrtf((float)HD);
 #pragma unroll
-    for (int qt = 0; qt < 2; ++qt) {
+    for (int pi = 0; pi < PPW; ++pi) {
+        const int qt = (w * PPW + pi) & 1;
         const int rq = qbase + qt * 16 + col;
         const bool qvalid = rq < qrows;
         const int mq = qvalid ? rq / gqa : 0;
@@ -114,27 +125,28 @@ __global__ void __launch_bounds__(64 * (HD / 16)) k_attn_mfma(AttnMArgs a) {
 #pragma unroll
         for (int r = 0; r < 4; ++r) {
             const bool ok = qvalid && slot_visible(a, npast, mq, ws0 + 4 * g + r);
-            const float sv = ok ? sc[qt][r] * scale : -INFINITY;
-            sc[qt][r] = sv;
+            const float sv = ok ? sc[pi][r] * scale : -INFINITY;
+            sc[pi][r] = sv;
             m_ = fmaxf(m_, sv);
         }
         m_ = fmaxf(m_, __shfl_xor(m_, 16, 64));
         m_ = fmaxf(m_, __shfl_xor(m_, 32, 64));
-        if (g == 0) smax[w][qt * 16 + col] = m_;
+        if (g == 0) smax[sst][qt * 16 + col] = m_;
     }
     __syncthreads();
-    // ---- p = e^(s - chunk max); row sums per wave; P hi / lo into LDS
+    // ---- p = e^(s - chunk max); row sums per slot tile; P hi / lo into LDS
 #pragma unroll
-    for (int qt = 0; qt < 2; ++qt) {
+    for (int pi = 0; pi < PPW; ++pi) {
+        const int qt = (w * PPW + pi) & 1;
         const int q = qt * 16 + col;
         float mx = smax[0][q];
 #pragma unroll
-        for (int k = 1; k < NW; ++k) mx = fmaxf(mx, smax[k][q]);
+        for (int k = 1; k < NST; ++k) mx = fmaxf(mx, smax[k][q]);
         float s_ = 0.f;
         v4h ph, pl;
 #pragma unroll
         for (int r = 0; r < 4; ++r) {
-            const float e = sc[qt][r] == -INFINITY ? 0.f : expf(sc[qt][r] - mx);
+            const float e = sc[pi][r] == -INFINITY ? 0.f : expf(sc[pi][r] - mx);
             s_ += e;
             const _Float16 h = (_Float16)e;
             ph[r] = h;
@@ -143,11 +155,11 @@ __global__ void __launch_bounds__(64 * (HD / 16)) k_attn_mfma(AttnMArgs a) {
         s_ += __shfl_xor(s_, 16, 64);
         s_ += __shfl_xor(s_, 32, 64);
         if (g == 0) {
-            ssum[w][q] = s_;
-            if (w == 0) cmax[q] = mx;
+            ssum[sst][q] = s_;
+            if (sst == 0) cmax[q] = mx;
         }
-        *(v4h*)&ps[0][q][16 * w + 4 * g] = ph;
-        *(v4h*)&ps[1][q][16 * w + 4 * g] = pl;
+        *(v4h*)&ps[0][q][16 * sst + 4 * g] = ph;
+        *(v4h*)&ps[1][q][16 * sst + 4 * g] = pl;
     }
     __syncthreads();
     // ---- O[:, 16 w .. 16 w + 15] = P . V over the chunk: A = P (query row
@@ -158,7 +170,7 @@ __global__ void __launch_bounds__(64 * (HD / 16)) k_attn_mfma(AttnMArgs a) {
     for (int qt = 0; qt < 2; ++qt) {
         v4f o = {0.f, 0.f, 0.f, 0.f};
 #pragma unroll
-        for (int st = 0; st < NW; ++st) {
+        for (int st = 0; st < NST; ++st) {
             const v4h ph = *(const v4h*)&ps[0][qt * 16 + col][16 * st + 4 * g];
             const v4h pl = *(const v4h*)&ps[1][qt * 16 + col][16 * st + 4 * g];
             o = __builtin_amdgcn_mfma_f32_16x16x16f16(ph, vf[st], o, 0, 0, 0);
@@ -178,7 +190,7 @@ __global__ void __launch_bounds__(64 * (HD / 16)) k_attn_mfma(AttnMArgs a) {
         const int64_t qi = (int64_t)(rq / gqa) * a.n_head + kvh * gqa + rq % gqa;
         float den = ssum[0][lane];
 #pragma unroll
-        for (int k = 1; k < NW; ++k) den += ssum[k][lane];
+        for (int k = 1; k < NST; ++k) den += ssum[k][lane];
         a.pmax[qi * nch + c] = cmax[lane];
         a.psum[qi * nch + c] = den;
     }
@@ -330,9 +342,9 @@ hipError_t launch_attn_mfma(hipStream_t st, AttnMArgs a, float* part, int8_t* xq
     const int qtiles = (int)((a.M * (a.n_head / a.n_kv) + 31) / 32);
     const dim3 grid((unsigned)nch, (unsigned)a.n_kv, (unsigned)qtiles);
     if (a.hd == 128)
-        hipLaunchKernelGGL(k_attn_mfma<128>, grid, dim3(64 * 8), 0, st, a);
+        hipLaunchKernelGGL((k_attn_mfma<128, chunk_slots(128)>), grid, dim3(64 * 8), 0, st, a);
     else if (a.hd == 64)
-        hipLaunchKernelGGL(k_attn_mfma<64>, grid, dim3(64 * 4), 0, st, a);
+        hipLaunchKernelGGL((k_attn_mfma<64, chunk_slots(64)>), grid, dim3(64 * 4), 0, st, a);
     else
         return hipErrorInvalidValue;
     hipError_t e = hipGetLastError();
