@@ -143,6 +143,7 @@ struct MvSeg {
     int64_t ldy;
     int rpt;        // weight rows per tile: 16 or 32
     int dt;
+    int role;       // index of the caller's segment (EPI_QKV: 0 q, 1 k, 2 v)
 };
 
 // (c, s) = cos / sin of this row's rotation angle (q and k segments)
@@ -520,7 +521,7 @@ __device__ __forceinline__ void mv_unit(const MvArgs& a, int64_t u) {
     float eres = 0.f, ecs = 1.f, esn = 0.f;
     if (eown) {
         if (!pair && a.epi == EPI_ACCUM) eres = sg.y[(int64_t)em * sg.ldy + en];
-        if (!pair && a.epi == EPI_QKV && si < 2) {
+        if (!pair && a.epi == EPI_QKV && sg.role < 2) {
             const int64_t d = en % a.qkv.hd;
             const float2 cs =
                 *(const float2*)(a.qkv.cs + ((int64_t)em * (a.qkv.hd / 2) + d / 2) * 2);
@@ -583,12 +584,12 @@ __device__ __forceinline__ void mv_unit(const MvArgs& a, int64_t u) {
                 *yp = gv / (1.f + expf(-gv)) * v[tpu - 1][r];
             } else if (a.epi == EPI_QKV) {
                 float c = 1.f, sn = 0.f;
-                if (si < 2) {
+                if (sg.role < 2) {
                     const int64_t d = n % a.qkv.hd;
                     c = a.qkv.cs[((int64_t)m * (a.qkv.hd / 2) + d / 2) * 2];
                     sn = a.qkv.cs[((int64_t)m * (a.qkv.hd / 2) + d / 2) * 2 + 1];
                 }
-                qkv_store(a.qkv, si, m, n, gv, pv, c, sn, yp);
+                qkv_store(a.qkv, sg.role, m, n, gv, pv, c, sn, yp);
             } else {
                 *yp = a.epi == EPI_ACCUM ? *yp + gv : gv;
             }
@@ -612,7 +613,7 @@ __device__ __forceinline__ void mv_unit(const MvArgs& a, int64_t u) {
             if (pair)
                 *yp = gv / (1.f + expf(-gv)) * uv;  // src/engine.cpp:271-273
             else if (a.epi == EPI_QKV)
-                qkv_store(a.qkv, si, em, en, gv, pv, ecs, esn, yp);
+                qkv_store(a.qkv, sg.role, em, en, gv, pv, ecs, esn, yp);
             else
                 *yp = a.epi == EPI_ACCUM ? eres + gv : gv;
         }
@@ -736,9 +737,23 @@ hipError_t launch_mv(hipStream_t st, const GemvSeg* segs, int nseg, const int8_t
         if (mixed && dt == FTX_Q6_K) break;  // the mixed launch took every segment
         MvArgs a{};
         int64_t tiles = 0;
-        for (int i = 0; i < nseg; ++i) {
+        // a mixed launch puts the heavier Q6_K segments first, so that their
+        // workgroups are dispatched first instead of finishing last
+        int order[3];
+        int no = 0;
+        if (mixed) {
+            for (int i = 0; i < nseg; ++i)
+                if (segs[i].dt == FTX_Q6_K) order[no++] = i;
+            for (int i = 0; i < nseg; ++i)
+                if (segs[i].dt != FTX_Q6_K) order[no++] = i;
+        } else {
+            for (int i = 0; i < nseg; ++i) order[no++] = i;
+        }
+        for (int oi = 0; oi < no; ++oi) {
+            const int i = order[oi];
             if (!mixed && segs[i].dt != dt) continue;
             MvSeg& sg = a.seg[a.nseg++];
+            sg.role = i;
             sg.W = segs[i].W;
             sg.row_bytes = segs[i].row_bytes;
             sg.N = segs[i].N;
