@@ -19,6 +19,9 @@ struct ftx_model {
     float *x = nullptr, *xn = nullptr, *qkv = nullptr, *att = nullptr, *h = nullptr;
     float* part = nullptr;
     size_t part_floats = 0;
+    // per-step arguments, one device block filled by one copy per step (the
+    // pointers below are views into it, laid out as the pinned host block)
+    uint8_t* args = nullptr;
     int32_t* toks = nullptr;
     int32_t* depth = nullptr;
     uint32_t* anc = nullptr;
@@ -28,7 +31,7 @@ struct ftx_model {
     // rotated q as fp16 hi + lo parts for the MFMA attention, [M][n_head][hd] each
     _Float16* qhl = nullptr;
     // RoPE cos / sin per (token, pair) of the current step, [M][hd / 2][2]
-    float* rcs = nullptr;
+    float* rcs = nullptr;  // (a view into args)
     // per-layer re-tiled ffn_down copies for the MFMA down kernel (or null)
     std::vector<uint8_t*> down_tiled;
     // tiled copies for the int8-MFMA row-dot kernel, [layer * LAYER_TENSORS +
@@ -37,6 +40,24 @@ struct ftx_model {
     std::vector<int> mvt_rpt;
     float* downpart = nullptr;
 };
+
+// Per-step argument block (pinned host copy and device copy share the
+// layout): tokens [M] | depth [M] | ancestor masks [M][aw] | npast (8-byte
+// aligned) | RoPE cos / sin [M][hd / 2][2]
+struct StepArgsLayout {
+    size_t depth, anc, np, cs, bytes;
+};
+static StepArgsLayout step_args_layout(int64_t M, int64_t hd) {
+    const int64_t aw = (M + 31) / 32;
+    StepArgsLayout L;
+    L.depth = (size_t)M * 4;
+    L.anc = L.depth + (size_t)M * 4;
+    L.np = (L.anc + (size_t)(M * aw) * 4 + 7) & ~(size_t)7;
+    L.cs = L.np + 8;
+    L.bytes = L.cs + (size_t)(M * (hd / 2) * 2) * 4;
+    return L;
+}
+static size_t step_args_bytes(int64_t Mmax, int64_t hd) { return step_args_layout(Mmax, hd).bytes; }
 
 // the MFMA row-dot path applies to every segment of a projection, or none
 static bool mv_all(const ftx_tensor* const* ts, int n, int64_t K, int64_t M) {
@@ -58,8 +79,7 @@ struct ftx_kv {
 
 static void model_release(ftx_model* m) {
     if (!m) return;
-    void* bufs[] = {m->norms, m->x,     m->xn,  m->qkv,   m->att, m->h,     m->part,
-                    m->toks,  m->depth, m->anc, m->npast, m->xq,  m->qhl,   m->rcs};
+    void* bufs[] = {m->norms, m->x, m->xn, m->qkv, m->att, m->h, m->part, m->args, m->xq, m->qhl};
     for (void* b : bufs)
         if (b) (void)hipFree(b);
     for (uint8_t* b : m->down_tiled)
@@ -133,12 +153,10 @@ int ftx_model_create(ftx_ctx* ctx, const ftx_model_desc* d, ftx_model** out) {
     bool ok = dalloc(&m->norms, nn * D) && dalloc(&m->x, Mmax * D) && dalloc(&m->xn, Mmax * D) &&
               dalloc(&m->qkv, Mmax * m->ldq) && dalloc(&m->att, Mmax * qdim) &&
               dalloc(&m->h, Mmax * d->n_ff) && dalloc(&m->part, m->part_floats) &&
-              dalloc(&m->toks, Mmax) && dalloc(&m->depth, Mmax) && dalloc(&m->anc, Mmax * 8) &&
-              dalloc(&m->npast, 1);
+              dalloc(&m->args, step_args_bytes(Mmax, d->head_dim));
     if (ok) {
         const int64_t Kmax = std::max(D, qdim);
-        ok = dalloc(&m->xq, xq_bytes(Kmax)) && dalloc(&m->qhl, (size_t)(2 * Mmax * qdim)) &&
-             dalloc(&m->rcs, (size_t)(Mmax * d->head_dim));
+        ok = dalloc(&m->xq, xq_bytes(Kmax)) && dalloc(&m->qhl, (size_t)(2 * Mmax * qdim));
     }
     // re-tiled ffn_down copies (same bytes, MFMA-friendly order)
     m->down_tiled.assign((size_t)d->n_layer, nullptr);
@@ -332,16 +350,16 @@ int ftx_verify_step(ftx_ctx* ctx, ftx_model* m, ftx_kv* kv, const ftx_verify_arg
     // host-side argument prep: tokens, depth, ancestor masks, npast
     const int aw = (int)((M + 31) / 32);
     const int64_t hd2 = d.head_dim / 2;
-    const size_t pin_bytes = (size_t)M * 4 * 2 + (size_t)M * aw * 4 + 64 + (size_t)(M * hd2 * 2) * 4;
+    const StepArgsLayout AL = step_args_layout(M, d.head_dim);
     uint8_t* pin;
-    int rc = ftx_pinned(ctx, pin_bytes, (void**)&pin);
+    int rc = ftx_pinned(ctx, AL.bytes, (void**)&pin);
     if (rc) return rc;
     FTX_HIP(ctx, hipStreamSynchronize(ctx->stream));  // pinned buffer reuse
     int32_t* toks = (int32_t*)pin;
-    int32_t* depth = toks + M;
-    uint32_t* anc = (uint32_t*)(depth + M);
-    int64_t* np = (int64_t*)(((uintptr_t)(anc + M * aw) + 7) & ~(uintptr_t)7);
-    float* cs = (float*)(np + 1);
+    int32_t* depth = (int32_t*)(pin + AL.depth);
+    uint32_t* anc = (uint32_t*)(pin + AL.anc);
+    int64_t* np = (int64_t*)(pin + AL.np);
+    float* cs = (float*)(pin + AL.cs);
     for (int64_t i = 0; i < M; ++i) {
         const int32_t t = a->tokens[i];
         if (t < 0 || t >= d.vocab) return ftx_fail(ctx, FTX_E_RANGE, "token id out of range");
@@ -367,11 +385,12 @@ int ftx_verify_step(ftx_ctx* ctx, ftx_model* m, ftx_kv* kv, const ftx_verify_arg
             cs[(i * hd2 + p) * 2 + 1] = (float)std::sin(ang);
         }
     hipStream_t st = ctx->stream;
-    FTX_HIP(ctx, hipMemcpyAsync(m->toks, toks, M * 4, hipMemcpyHostToDevice, st));
-    FTX_HIP(ctx, hipMemcpyAsync(m->depth, depth, M * 4, hipMemcpyHostToDevice, st));
-    FTX_HIP(ctx, hipMemcpyAsync(m->anc, anc, (size_t)M * aw * 4, hipMemcpyHostToDevice, st));
-    FTX_HIP(ctx, hipMemcpyAsync(m->npast, np, 8, hipMemcpyHostToDevice, st));
-    FTX_HIP(ctx, hipMemcpyAsync(m->rcs, cs, (size_t)(M * hd2 * 2) * 4, hipMemcpyHostToDevice, st));
+    m->toks = (int32_t*)m->args;
+    m->depth = (int32_t*)(m->args + AL.depth);
+    m->anc = (uint32_t*)(m->args + AL.anc);
+    m->npast = (int64_t*)(m->args + AL.np);
+    m->rcs = (float*)(m->args + AL.cs);
+    FTX_HIP(ctx, hipMemcpyAsync(m->args, pin, AL.bytes, hipMemcpyHostToDevice, st));
 
     const int64_t D = d.n_embd, F = d.n_ff, V = d.vocab;
     const float eps = d.rms_eps;
@@ -584,15 +603,16 @@ int ftx_accept(ftx_ctx* ctx, const ftx_accept_args* a) {
         if (a->mode == FTX_ACCEPT_RATIO && p != i - 1)
             return ftx_fail(ctx, FTX_E_INVALID, "ratio mode is chain only");
     }
-    // workspace: stats [M+1], p [V] doubles, out ints, rng, margin, props,
-    // parents, pd
+    // workspace: stats [M+1], p [V] doubles, the small block (rng, margin,
+    // out ints | props, parents, pd: one copy in, one copy of its head out)
     const size_t stats_b = (size_t)(M + 1) * sizeof(RowStats);
     const size_t off_p = (stats_b + 255) & ~(size_t)255;
     // p: V doubles, or the chunk-transposed bonus layout of ceil(V / 1024) * 1024
     const size_t pn = (size_t)((V + 1023) / 1024 * 1024);
-    const size_t off_out = off_p + ((pn * 8 + 255) & ~(size_t)255);
-    const size_t off_small = off_out + (((size_t)(M + 2) * 4 + 255) & ~(size_t)255);
-    const size_t small_b = 8 + 8 + (size_t)M * 12 + 64;
+    const size_t off_small = off_p + ((pn * 8 + 255) & ~(size_t)255);
+    const size_t out_b = ((size_t)(M + 2) * 4 + 7) & ~(size_t)7;
+    const size_t head_b = 16 + out_b;  // rng | margin | pad | out
+    const size_t small_b = head_b + (size_t)M * 12 + 64;
     const size_t off_rs = off_small + ((small_b + 255) & ~(size_t)255);  // row-stat chunks
     const size_t off_b = off_rs + ((row_stats_scratch_bytes(std::max<int64_t>(M, 1), V) + 255) &
                                    ~(size_t)255);
@@ -600,17 +620,17 @@ int ftx_accept(ftx_ctx* ctx, const ftx_accept_args* a) {
     int rc = ftx_workspace(ctx, off_b + 256, (void**)&ws);
     if (rc) return rc;
     uint8_t* pin;
-    rc = ftx_pinned(ctx, small_b + (size_t)(M + 2) * 4 + 64, (void**)&pin);
+    rc = ftx_pinned(ctx, small_b, (void**)&pin);
     if (rc) return rc;
     hipStream_t st = ctx->stream;
     FTX_HIP(ctx, hipStreamSynchronize(st));
-    // small host block: rng | margin | props | parents | pd
+    // small host block: rng | margin | pad | out | props | parents | pd
     uint64_t* h_rng = (uint64_t*)pin;
     float* h_margin = (float*)(pin + 8);
-    int32_t* h_props = (int32_t*)(pin + 16);
+    int32_t* h_out = (int32_t*)(pin + 16);
+    int32_t* h_props = (int32_t*)(pin + head_b);
     int32_t* h_par = h_props + M;
     float* h_pd = (float*)(h_par + M);
-    int32_t* h_out = (int32_t*)(pin + small_b);
     *h_rng = *a->rng;
     *h_margin = INFINITY;
     for (int64_t i = 0; i < M; ++i) {
@@ -634,7 +654,7 @@ int ftx_accept(ftx_ctx* ctx, const ftx_accept_args* a) {
     ad.stats = stats;
     ad.M = M;
     ad.V = V;
-    ad.props = (const int32_t*)(d_small + 16);
+    ad.props = (const int32_t*)(d_small + head_b);
     ad.parents = ad.props + M;
     ad.pd = (const float*)(ad.parents + M);
     ad.mode = a->mode;
@@ -642,15 +662,14 @@ int ftx_accept(ftx_ctx* ctx, const ftx_accept_args* a) {
     ad.rng = (uint64_t*)d_small;
     ad.p = (double*)(ws + off_p);
     ad.part = nullptr;
-    ad.out = (int32_t*)(ws + off_out);
+    ad.out = (int32_t*)(d_small + 16);
     ad.margin = (float*)(d_small + 8);
     ad.brow = (int32_t*)(ws + off_b);
     ad.bu = (float*)(ws + off_b + 16);
     tk = tr_begin(ctx);
     FTX_HIP(ctx, launch_accept(st, ad));
     tr_end(ctx, tk, TK_ACCEPT, (double)V * 4);
-    FTX_HIP(ctx, hipMemcpyAsync(h_out, ad.out, (size_t)(M + 2) * 4, hipMemcpyDeviceToHost, st));
-    FTX_HIP(ctx, hipMemcpyAsync(pin, d_small, 16, hipMemcpyDeviceToHost, st));
+    FTX_HIP(ctx, hipMemcpyAsync(pin, d_small, head_b, hipMemcpyDeviceToHost, st));
     FTX_HIP(ctx, hipStreamSynchronize(st));
     const int32_t na = h_out[0];
     if (na < 0 || na > M) return ftx_fail(ctx, FTX_E_DEVICE, "acceptance returned a bad count");
