@@ -27,6 +27,11 @@ typedef _Float16 v8h __attribute__((ext_vector_type(8)));
 typedef _Float16 v4h __attribute__((ext_vector_type(4)));
 typedef float v4f __attribute__((ext_vector_type(4)));
 
+// waves per workgroup for head size 128 (16: one score tile and one output
+// tile per wave)
+#ifndef ATTN_WAVES_128
+#define ATTN_WAVES_128 8
+#endif
 // slots per chunk (one workgroup of hd / 16 waves) for head size hd
 #ifndef ATTN_CHK
 __host__ __device__ constexpr int chunk_slots(int hd) { return hd; }
@@ -41,14 +46,18 @@ __device__ __forceinline__ bool slot_visible(const AttnMArgs& a, int64_t npast, 
     return (a.anc[(int64_t)m * a.anc_words + (j >> 5)] >> (j & 31)) & 1u;
 }
 
-template <int HD, int CHK>
-__global__ void __launch_bounds__(64 * (HD / 16)) k_attn_mfma(AttnMArgs a) {
-    constexpr int NW = HD / 16;   // waves: 16 output dims each
+template <int HD, int CHK, int NWV>
+__global__ void __launch_bounds__(64 * NWV) k_attn_mfma(AttnMArgs a) {
+    constexpr int NDT = HD / 16;  // 16-dim output tiles
     constexpr int NST = CHK / 16; // 16-slot tiles of the chunk
     // score tiles (slot tile, query tile) per wave: pair p = w PPW + i takes
     // slot tile p / 2 and query tile p % 2
-    constexpr int PPW = 2 * NST / NW;
+    constexpr int PPW = 2 * NST / NWV;
     static_assert(PPW == 1 || PPW == 2, "a wave takes one or two score tiles of one slot tile");
+    // output tiles (dim tile, query tile) per wave: dim tile w % NDT, query
+    // tiles all (QPW = 2) or w / NDT (QPW = 1)
+    constexpr int QPW = 2 * NDT / NWV;
+    static_assert(QPW == 1 || QPW == 2, "a wave takes one or two query tiles of one dim tile");
     constexpr int NDC = HD / 32;  // 32-dim chunks of the score contraction
     constexpr int QP = HD + 8;    // padded query row (halves)
     constexpr int PP = CHK + 8;   // padded P row (halves)
@@ -68,8 +77,9 @@ __global__ void __launch_bounds__(64 * (HD / 16)) k_attn_mfma(AttnMArgs a) {
     const int64_t kdim = (int64_t)a.n_kv * HD;
     const int sst = (w * PPW) >> 1;          // this wave's slot tile
     const int64_t ws0 = slot0 + 16 * sst;    // its score slots
+    const int dt = w % NDT;  // this wave's output dims 16 dt .. 16 dt + 15
     // ---- operand loads, all issued up front: K rows (A of S^T: slot ws0 +
-    // col, dims 32 dc + 8 g ..), V^T rows (B of O: dim 16 w + col, slots
+    // col, dims 32 dc + 8 g ..), V^T rows (B of O: dim 16 dt + col, slots
     // slot0 + 16 st + 4 g ..), then the query hi / lo parts into LDS
     v8h kf[NDC];
     {
@@ -79,14 +89,14 @@ __global__ void __launch_bounds__(64 * (HD / 16)) k_attn_mfma(AttnMArgs a) {
     }
     v4h vf[NST];
     {
-        const _Float16* vrow = a.vt + ((int64_t)kvh * HD + 16 * w + col) * a.cap + slot0 + 4 * g;
+        const _Float16* vrow = a.vt + ((int64_t)kvh * HD + 16 * dt + col) * a.cap + slot0 + 4 * g;
 #pragma unroll
         for (int st = 0; st < NST; ++st) vf[st] = *(const v4h*)(vrow + 16 * st);
     }
     // 16-byte vectors of the staged queries: 2 parts x 32 rows x HD / 8
 #pragma unroll
-    for (int k = 0; k < (2 * 32 * HD / 8) / (64 * NW); ++k) {
-        const int v = tid + 64 * NW * k;
+    for (int k = 0; k < (2 * 32 * HD / 8) / (64 * NWV); ++k) {
+        const int v = tid + 64 * NWV * k;
         const int part = v / (32 * HD / 8), r = (v / (HD / 8)) % 32, dv = v % (HD / 8);
         const int rq = qbase + r;
         v8h x = {};
@@ -162,12 +172,13 @@ __global__ void __launch_bounds__(64 * (HD / 16)) k_attn_mfma(AttnMArgs a) {
         *(v4h*)&ps[1][q][16 * sst + 4 * g] = pl;
     }
     __syncthreads();
-    // ---- O[:, 16 w .. 16 w + 15] = P . V over the chunk: A = P (query row
+    // ---- O[:, 16 dt .. 16 dt + 15] = P . V over the chunk: A = P (query row
     // col, slots 16 st + 4g ..), B = V^T rows; lane then holds O[query row
-    // qt * 16 + 4g + r][dim 16 w + col]
+    // qt * 16 + 4g + r][dim 16 dt + col]
     const int nch = (int)gridDim.x;
 #pragma unroll
-    for (int qt = 0; qt < 2; ++qt) {
+    for (int qi = 0; qi < QPW; ++qi) {
+        const int qt = QPW == 2 ? qi : w / NDT;
         v4f o = {0.f, 0.f, 0.f, 0.f};
 #pragma unroll
         for (int st = 0; st < NST; ++st) {
@@ -180,8 +191,8 @@ __global__ void __launch_bounds__(64 * (HD / 16)) k_attn_mfma(AttnMArgs a) {
         for (int r = 0; r < 4; ++r) {
             const int rq = qbase + qt * 16 + 4 * g + r;
             if (rq >= qrows) continue;
-            const int64_t qi = (int64_t)(rq / gqa) * a.n_head + kvh * gqa + rq % gqa;
-            a.pout[(qi * nch + c) * HD + 16 * w + col] = o[r];
+            const int64_t qrow = (int64_t)(rq / gqa) * a.n_head + kvh * gqa + rq % gqa;
+            a.pout[(qrow * nch + c) * HD + 16 * dt + col] = o[r];
         }
     }
     // chunk statistics of query row lane (wave 0)
@@ -342,9 +353,10 @@ hipError_t launch_attn_mfma(hipStream_t st, AttnMArgs a, float* part, int8_t* xq
     const int qtiles = (int)((a.M * (a.n_head / a.n_kv) + 31) / 32);
     const dim3 grid((unsigned)nch, (unsigned)a.n_kv, (unsigned)qtiles);
     if (a.hd == 128)
-        hipLaunchKernelGGL((k_attn_mfma<128, chunk_slots(128)>), grid, dim3(64 * 8), 0, st, a);
+        hipLaunchKernelGGL((k_attn_mfma<128, chunk_slots(128), ATTN_WAVES_128>), grid,
+                           dim3(64 * ATTN_WAVES_128), 0, st, a);
     else if (a.hd == 64)
-        hipLaunchKernelGGL((k_attn_mfma<64, chunk_slots(64)>), grid, dim3(64 * 4), 0, st, a);
+        hipLaunchKernelGGL((k_attn_mfma<64, chunk_slots(64), 4>), grid, dim3(64 * 4), 0, st, a);
     else
         return hipErrorInvalidValue;
     hipError_t e = hipGetLastError();
