@@ -35,6 +35,8 @@
  *                          causal only, src/engine.cpp:152)
  *   ftx_kv_truncate        Engine::truncate_to / KvCache::set_npast
  *                          (src/engine.cpp:423-428; include/ft/kv_cache.h:31)
+ *   ftx_kv_commit          the same for an accepted draft-tree path (rows of
+ *                          the path's nodes gathered to the committed slots)
  *   ftx_accept             accept_chain_greedy / accept_chain_sampling
  *                          (src/spec.cpp:203-238) plus the bonus token of
  *                          generate() (src/spec.cpp:302-311), and tree and
@@ -206,6 +208,14 @@ int ftx_kv_write(ftx_kv* kv, const void* k, const void* v);
 int ftx_kv_read(ftx_kv* kv, void* k, void* v);
 /* Set the number of committed positions (rollback after acceptance). */
 int ftx_kv_truncate(ftx_kv* kv, int64_t npast);
+/* Commit an accepted draft path after a verify step that did not advance:
+ * the K / V rows of draft nodes nodes[0..n-1] (strictly increasing, nodes[i]
+ * >= i, n <= 256; a root-to-node path of the draft tree) move to slots
+ * npast + i, then npast += n.  A chain (nodes[i] == i) moves nothing and is
+ * Engine::truncate_to(npast + n) (src/engine.cpp:423-428, KvCache::set_npast
+ * include/ft/kv_cache.h:31); trees extend it.  Enqueued on the context's
+ * stream, ordered before later verify steps. */
+int ftx_kv_commit(ftx_kv* kv, const int32_t* nodes, int64_t n);
 
 typedef struct {
     int64_t M;               /* tokens verified in this step */

@@ -174,6 +174,25 @@ class Oracle:
         self.lib.orc_softmax_inplace(_ptr(p, _fp), p.size)
         return p
 
+    @staticmethod
+    def kv_commit(kcache, vcache, npast, nodes):
+        """Keep the accepted draft path `nodes` (node indices of the verify
+        step whose rows were written at npast + j) at slots npast + i; returns
+        the new npast.  A chain (nodes[i] == i) is Engine::truncate_to(npast +
+        n) / KvCache::set_npast (src/engine.cpp:423-428, include/ft/
+        kv_cache.h:31); a tree path gathers its rows.  kcache / vcache are
+        [L][cap][dk] arrays in the reference layout, modified in place."""
+        nodes = [int(j) for j in nodes]
+        for i, j in enumerate(nodes):
+            if j < i or (i and j <= nodes[i - 1]):
+                raise ValueError("nodes must be strictly increasing with nodes[i] >= i")
+            if npast + j >= kcache.shape[1]:
+                raise ValueError("node out of range")
+        for i, j in enumerate(nodes):
+            kcache[:, npast + i] = kcache[:, npast + j]
+            vcache[:, npast + i] = vcache[:, npast + j]
+        return npast + len(nodes)
+
     def forward(self, model, kcache, vcache, npast, toks, parents=None, layer_limit=0):
         """model: dict from make_model(); kcache/vcache: numpy [L][cap][dk]
         (float32 or float16, modified in place).  Returns logits [M][V]."""

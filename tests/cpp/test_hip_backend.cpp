@@ -274,7 +274,26 @@ static void test_verifier(HipBackend& be) {
                           tree ? parents.data() : nullptr, 0, want.data()) == 0,
               "oracle forward");
         CHECK(rel_err(got.data(), want.data(), M, c.vocab) < 1e-3, tree ? "tree logits" : "chain logits");
-        if (tree) continue;
+        if (tree) {
+            // accept the path 0 -> 1 -> 3, commit it, verify one more token:
+            // the logits are the oracle chain forward of the path + that token
+            const std::vector<int32_t> path = {0, 1, 3};
+            ver.commit(path);
+            CHECK(ver.npast() == npast + 3, "commit advances the committed length");
+            const std::vector<int32_t> nxt = {42};
+            const float* d1 = ver.extend_verify(nxt);
+            std::vector<float> g1((size_t)c.vocab), w1((size_t)(4 * c.vocab));
+            be.stage(g1.data(), d1, g1.size() * sizeof(float));
+            std::vector<uint16_t> k4 = kc, v4 = vc;
+            const int32_t chain[4] = {props[0], props[1], props[3], nxt[0]};
+            CHECK(orc_forward(&om, k4.data(), v4.data(), ORC_KV_F16, cap, npast, chain, 4, nullptr,
+                              0, w1.data()) == 0,
+                  "oracle chain of the committed path");
+            CHECK(rel_err(g1.data(), w1.data() + 3 * c.vocab, 1, c.vocab) < 1e-3,
+                  "logits after commit");
+            ver.truncate_to(npast);
+            continue;
+        }
         // acceptance on these logits: base row = oracle logits of position npast - 1
         std::vector<float> base((size_t)c.vocab);
         {

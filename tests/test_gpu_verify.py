@@ -286,6 +286,88 @@ def test_verify_fused_rope_kv(gctx, orc, neox, parents):
     assert np.array_equal(kg[:, :npast], kc[:, :npast]) and np.array_equal(vg[:, :npast], vc[:, :npast])
 
 
+
+@pytest.mark.parametrize("cfg_name,kv_dtype", [("tiny", ftx.KV_F16), ("tiny", ftx.KV_F32),
+                                               ("hd128", ftx.KV_F16)])
+def test_kv_commit_tree_path(gctx, orc, cfg_name, kv_dtype):
+    """Tree verify, commit the accepted path, verify the next token: the
+    committed rows are the path nodes' rows moved bit for bit, the rest of
+    the cache is untouched, and the next step's logits match the oracle's
+    chain forward of the path plus the next token."""
+    if cfg_name == "tiny":
+        model = P.make_model(orc, TINY, TINY_DT, seed=12)
+    else:
+        model = P.make_model(orc, HD128, HD128_DT, seed=12)
+    cfg = model["cfg"]
+    npast, cap = 70, 160
+    parents = [-1, -1, 0, 0, 3, 1, 4, 2]
+    toks = [5, 6, 7, 8, 9, 10, 11, 12]
+    path = [0, 3, 4, 6]
+    nxt = 13
+    tensors = upload_model(gctx, model)
+    gm = gctx.model(cfg, tensors, max_tokens=8)
+    kv = gm.kv(cap, kv_dtype)
+    k0, v0 = kv_context(cfg, cap, npast, 21)
+    kv.write(k0, v0)
+    kv.truncate(npast)
+    V = cfg["vocab"]
+    buf = gctx.buffer(8 * V * 4)
+    gm.verify(kv, toks, buf.ptr, parents=parents)
+    gctx.sync()
+    kt, vt = kv.read()
+    kv.commit(path)
+    gctx.sync()
+    assert kv.pointers()[2] == npast + len(path)
+    kc, vc = kv.read()
+    slots = [npast + j for j in path]
+    assert np.array_equal(kc[:, npast:npast + len(path)], kt[:, slots])
+    assert np.array_equal(vc[:, npast:npast + len(path)], vt[:, slots])
+    assert np.array_equal(kc[:, :npast], kt[:, :npast]) and np.array_equal(vc[:, :npast], vt[:, :npast])
+    gm.verify(kv, [nxt], buf.ptr)
+    gctx.sync()
+    got = buf.read(np.float32, V)
+    dt = np.float16 if kv_dtype == ftx.KV_F16 else np.float32
+    ko, vo = k0.astype(dt), v0.astype(dt)
+    want = orc.forward(model, ko, vo, npast, [toks[j] for j in path] + [nxt])
+    assert rel_err_rows(got, want[-1]) < LOGIT_TOL
+    # a chain commit moves nothing and only advances the committed length
+    kv.truncate(npast)
+    gm.verify(kv, toks[:3], buf.ptr)
+    gctx.sync()
+    kt, vt = kv.read()
+    kv.commit([0, 1, 2])
+    gctx.sync()
+    kc, vc = kv.read()
+    assert kv.pointers()[2] == npast + 3
+    assert np.array_equal(kc, kt) and np.array_equal(vc, vt)
+    buf.free()
+    kv.free()
+    gm.free()
+    free_all(tensors)
+
+
+def test_kv_commit_errors(gctx, orc):
+    model = P.make_model(orc, TINY, TINY_DT, seed=3)
+    tensors = upload_model(gctx, model)
+    gm = gctx.model(TINY, tensors, max_tokens=8)
+    kv = gm.kv(16)
+    kv.truncate(10)
+    for bad, code in (([1, 1], -1), ([2, 1], -1), ([0, 0], -1), ([1], None),
+                      ([0, 6], -5), (list(range(7)), -5)):
+        if code is None:
+            kv.commit(bad)  # node 1 at slot 11 < 16 is in range
+            assert kv.pointers()[2] == 11
+            kv.truncate(10)
+            continue
+        with pytest.raises(ftx.FtxError) as e:
+            kv.commit(bad)
+        assert e.value.code == code, bad
+        assert kv.pointers()[2] == 10
+    kv.free()
+    gm.free()
+    free_all(tensors)
+
+
 def test_verify_errors(gctx, orc):
     model = P.make_model(orc, TINY, TINY_DT, seed=3)
     tensors = upload_model(gctx, model)

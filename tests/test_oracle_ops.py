@@ -163,3 +163,38 @@ def test_forward_tree_equals_paths(orc):
     a = orc.forward(model, kt.copy(), vt.copy(), 6, toks, parents=[-1, 0, 1, 2, 3])
     b = orc.forward(model, kt.copy(), vt.copy(), 6, toks)
     assert np.array_equal(a, b)
+
+
+def test_kv_commit_tree_path_equals_chain(orc):
+    """Committing an accepted tree path leaves the cache exactly as a chain
+    forward of that path would, so the next step's logits are the chain's."""
+    model = P.make_model(orc, TINY, TINY_DT, seed=5)
+    parents = [-1, -1, 0, 0, 3, 1]
+    toks = [5, 6, 7, 8, 9, 10]
+    path = [0, 3, 4]  # root -> node 3 -> node 4
+    kt, vt = kv_for(TINY, 32, npast=6)
+    k1, v1 = kt.copy(), vt.copy()
+    orc.forward(model, k1, v1, 6, toks, parents=parents)
+    npast = P.Oracle.kv_commit(k1, v1, 6, path)
+    assert npast == 9
+    nxt = orc.forward(model, k1, v1, npast, [11])
+    k2, v2 = kt.copy(), vt.copy()
+    chain = orc.forward(model, k2, v2, 6, [toks[i] for i in path] + [11])
+    assert np.array_equal(nxt[0], chain[-1])
+    assert np.array_equal(k1[:, :10], k2[:, :10]) and np.array_equal(v1[:, :10], v2[:, :10])
+
+
+def test_kv_commit_chain_and_errors(orc):
+    k, v = kv_for(TINY, 16, npast=4)
+    k[:, 4:9] = 1.0 + np.arange(5)[None, :, None]
+    v[:, 4:9] = -1.0 - np.arange(5)[None, :, None]
+    k0, v0 = k.copy(), v.copy()
+    # a chain moves nothing
+    assert P.Oracle.kv_commit(k, v, 4, [0, 1, 2]) == 7
+    assert np.array_equal(k, k0) and np.array_equal(v, v0)
+    # a path overlapping its own destinations: nodes 1, 2, 4 -> slots 4, 5, 6
+    assert P.Oracle.kv_commit(k, v, 4, [1, 2, 4]) == 7
+    assert np.array_equal(k[:, 4:7], k0[:, [5, 6, 8]]) and np.array_equal(v[:, 4:7], v0[:, [5, 6, 8]])
+    for bad in ([1, 1], [2, 1], [0, 0], [20]):
+        with pytest.raises(ValueError):
+            P.Oracle.kv_commit(k.copy(), v.copy(), 4, bad)

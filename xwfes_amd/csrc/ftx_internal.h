@@ -264,6 +264,16 @@ size_t attn_part_floats(int64_t M, int64_t n_head, int64_t hd, int64_t cap_alloc
 // operand (xq_dev.h layout, K = n_head * hd) instead of a.out
 bool attn_combine_xq_supported(int64_t hd, int64_t n_head);
 hipError_t launch_attn_mfma(hipStream_t st, AttnMArgs a, float* part, int8_t* xq = nullptr);
+// KV commit of an accepted draft path (nodes by value: at most 256)
+struct KvCommitArgs {
+    int64_t npast;     // committed slots before the draft
+    int64_t cap;       // allocated slots per layer
+    int64_t n_layer;
+    int n_kv, hd;
+    int n;             // path length
+    int32_t nodes[256];
+};
+hipError_t launch_kv_commit(hipStream_t st, const KvCommitArgs& a, void* k, void* v, int kv_f16);
 // canonical [slot][kdim] <-> device V layout (per layer, all slots)
 hipError_t launch_v_layout(hipStream_t st, const void* src, void* dst, int64_t n_layer,
                            int64_t cap, int64_t n_kv, int64_t hd, int elem_bytes, int to_device);

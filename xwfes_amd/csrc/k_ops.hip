@@ -257,3 +257,41 @@ hipError_t launch_attention(hipStream_t st, const AttnArgs& a, int64_t M) {
     hipLaunchKernelGGL(k_attention, dim3((unsigned)M, (unsigned)a.n_head), dim3(256), lds, st, a);
     return hipGetLastError();
 }
+
+// ---------------------------------------------------------------- KV commit
+// After a verify step over draft nodes at slots npast + j, keep the accepted
+// path nodes[0..n-1] at slots npast + i (KvCache::set_npast / Engine::
+// truncate_to, include/ft/kv_cache.h:31, src/engine.cpp:423-428, extended to
+// trees).  Thread = one element of a K row or of a transposed V row of one
+// layer; it walks the path in increasing i.  In place: nodes is strictly
+// increasing with nodes[i] >= i, so a later source nodes[i'] > nodes[i] >= i
+// is never a slot written before it.
+template <typename T>
+__global__ void __launch_bounds__(256) k_kv_commit(KvCommitArgs a, T* __restrict__ k,
+                                                   T* __restrict__ v) {
+    const int64_t e = (int64_t)blockIdx.x * 256 + threadIdx.x;
+    const int64_t l = blockIdx.y;
+    const int64_t kdim = (int64_t)a.n_kv * a.hd;
+    if (e >= kdim) return;
+    T* kl = k + l * a.cap * kdim;
+    // transposed V: [layer][n_kv][hd][cap]; element e = kv head e / hd, dim e % hd
+    T* vr = v + (l * kdim + e) * a.cap;
+    for (int i = 0; i < a.n; ++i) {
+        const int64_t src = a.npast + a.nodes[i], dst = a.npast + i;
+        if (src == dst) continue;
+        kl[dst * kdim + e] = kl[src * kdim + e];
+        vr[dst] = vr[src];
+    }
+}
+
+hipError_t launch_kv_commit(hipStream_t st, const KvCommitArgs& a, void* k, void* v, int kv_f16) {
+    if (a.n <= 0) return hipSuccess;
+    const int64_t kdim = (int64_t)a.n_kv * a.hd;
+    const dim3 grid((unsigned)((kdim + 255) / 256), (unsigned)a.n_layer);
+    if (kv_f16)
+        hipLaunchKernelGGL(k_kv_commit<_Float16>, grid, dim3(256), 0, st, a, (_Float16*)k,
+                           (_Float16*)v);
+    else
+        hipLaunchKernelGGL(k_kv_commit<float>, grid, dim3(256), 0, st, a, (float*)k, (float*)v);
+    return hipGetLastError();
+}

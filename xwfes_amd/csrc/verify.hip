@@ -337,6 +337,33 @@ int ftx_kv_truncate(ftx_kv* kv, int64_t npast) {
     return FTX_OK;
 }
 
+int ftx_kv_commit(ftx_kv* kv, const int32_t* nodes, int64_t n) {
+    if (!kv || (n > 0 && !nodes)) return FTX_E_INVALID;
+    ftx_ctx* ctx = kv->ctx;
+    if (n < 0 || n > 256) return ftx_fail(ctx, FTX_E_INVALID, "kv_commit: path length out of range");
+    if (kv->npast + n > kv->cap) return ftx_fail(ctx, FTX_E_RANGE, "kv_commit: capacity exceeded");
+    KvCommitArgs a{};
+    a.npast = kv->npast;
+    a.cap = kv->cap_alloc;
+    a.n_layer = kv->n_layer;
+    a.n_kv = (int)kv->n_kv;
+    a.hd = (int)kv->hd;
+    a.n = (int)n;
+    bool moves = false;
+    for (int64_t i = 0; i < n; ++i) {
+        const int32_t j = nodes[i];
+        if (j < i || (i > 0 && j <= nodes[i - 1]))
+            return ftx_fail(ctx, FTX_E_INVALID,
+                            "kv_commit: nodes must be strictly increasing with nodes[i] >= i");
+        if (kv->npast + j >= kv->cap) return ftx_fail(ctx, FTX_E_RANGE, "kv_commit: node out of range");
+        a.nodes[i] = j;
+        moves |= j != i;
+    }
+    if (moves) FTX_HIP(ctx, launch_kv_commit(ctx->stream, a, kv->k, kv->v, kv->kv_f16));
+    kv->npast += n;
+    return FTX_OK;
+}
+
 int ftx_verify_step(ftx_ctx* ctx, ftx_model* m, ftx_kv* kv, const ftx_verify_args* a) {
     if (!ctx || !m || !kv || !a || !a->tokens || !a->logits)
         return ftx_fail(ctx, FTX_E_INVALID, "null argument");

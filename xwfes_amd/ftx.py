@@ -110,6 +110,7 @@ def load(path=LIB_PATH):
         "ftx_kv_free": (C.c_int, [_vp]),
         "ftx_kv_pointers": (C.c_int, [_vp, C.POINTER(_vp), C.POINTER(_vp), C.POINTER(_i64)]),
         "ftx_kv_truncate": (C.c_int, [_vp, _i64]),
+        "ftx_kv_commit": (C.c_int, [_vp, C.POINTER(C.c_int32), _i64]),
         "ftx_kv_write": (C.c_int, [_vp, _vp, _vp]),
         "ftx_kv_read": (C.c_int, [_vp, _vp, _vp]),
         "ftx_verify_step": (C.c_int, [_vp, _vp, _vp, C.POINTER(VerifyArgs)]),
@@ -362,6 +363,12 @@ class KV:
 
     def truncate(self, npast):
         self.ctx.check(self.ctx.lib.ftx_kv_truncate(self.handle, npast))
+
+    def commit(self, nodes):
+        """Keep the accepted draft path `nodes` (node indices of the last
+        verify step) at the next committed slots."""
+        arr = (C.c_int32 * max(len(nodes), 1))(*[int(j) for j in nodes])
+        self.ctx.check(self.ctx.lib.ftx_kv_commit(self.handle, arr, len(nodes)))
 
     @property
     def cap_alloc(self):

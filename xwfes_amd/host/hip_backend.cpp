@@ -171,6 +171,10 @@ const float* HipVerifier::extend_verify(const std::vector<int32_t>& props,
 
 void HipVerifier::truncate_to(int64_t npast) { be_.check(ftx_kv_truncate(kv_, npast), "truncate"); }
 
+void HipVerifier::commit(const std::vector<int32_t>& nodes) {
+    be_.check(ftx_kv_commit(kv_, nodes.data(), (int64_t)nodes.size()), "commit");
+}
+
 int64_t HipVerifier::npast() const {
     void *k = nullptr, *v = nullptr;
     int64_t n = 0;

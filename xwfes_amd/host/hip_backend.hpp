@@ -164,6 +164,9 @@ public:
     const float* extend_verify(const std::vector<int32_t>& props,
                                const std::vector<int32_t>& parents = {}, bool advance = false);
     void truncate_to(int64_t npast);
+    // keep the accepted path nodes (node ids of the last extend_verify, root
+    // first) as the next committed positions; a chain is truncate_to
+    void commit(const std::vector<int32_t>& nodes);
     int64_t npast() const;
     // whole cache from / to host arrays [n_layer][cap][n_head_kv*head_dim]
     void write_kv(const void* k, const void* v);
