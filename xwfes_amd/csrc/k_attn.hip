@@ -39,13 +39,6 @@ __host__ __device__ constexpr int chunk_slots(int hd) { return hd; }
 __host__ __device__ constexpr int chunk_slots(int) { return ATTN_CHK; }
 #endif
 
-__device__ __forceinline__ bool slot_visible(const AttnMArgs& a, int64_t npast, int m, int64_t p) {
-    if (p < npast) return true;
-    const int64_t j = p - npast;
-    if (j >= a.M) return false;
-    return (a.anc[(int64_t)m * a.anc_words + (j >> 5)] >> (j & 31)) & 1u;
-}
-
 template <int HD, int CHK, int NWV>
 __global__ void __launch_bounds__(64 * NWV) k_attn_mfma(AttnMArgs a) {
     constexpr int NDT = HD / 16;  // 16-dim output tiles
@@ -61,6 +54,7 @@ __global__ void __launch_bounds__(64 * NWV) k_attn_mfma(AttnMArgs a) {
     constexpr int NDC = HD / 32;  // 32-dim chunks of the score contraction
     constexpr int QP = HD + 8;    // padded query row (halves)
     constexpr int PP = CHK + 8;   // padded P row (halves)
+    constexpr int QV = (2 * 32 * HD / 8) / (64 * NWV);  // staged 16-byte query vectors per thread
     __shared__ _Float16 qs[2][32][QP];  // query hi / lo [part][row][dim]
     __shared__ _Float16 ps[2][32][PP];  // P hi / lo [part][query row][slot]
     __shared__ float smax[NST][32], ssum[NST][32], cmax[32];
@@ -78,9 +72,34 @@ __global__ void __launch_bounds__(64 * NWV) k_attn_mfma(AttnMArgs a) {
     const int sst = (w * PPW) >> 1;          // this wave's slot tile
     const int64_t ws0 = slot0 + 16 * sst;    // its score slots
     const int dt = w % NDT;  // this wave's output dims 16 dt .. 16 dt + 15
-    // ---- operand loads, all issued up front: K rows (A of S^T: slot ws0 +
-    // col, dims 32 dc + 8 g ..), V^T rows (B of O: dim 16 dt + col, slots
-    // slot0 + 16 st + 4 g ..), then the query hi / lo parts into LDS
+    // ---- every operand load issued up front, in the order of use, with
+    // clamped (always valid) addresses and no branch, so that each use waits
+    // only for its own loads: the query vectors this thread stages (2 parts
+    // x 32 rows x HD / 8; rows past qrows repeat the last valid row, whose
+    // scores are masked and never stored), the ancestor-mask words of the
+    // wave's query rows, K rows (A of S^T: slot ws0 + col, dims 32 dc + 8 g
+    // ..), V^T rows (B of O: dim 16 dt + col, slots slot0 + 16 st + 4 g ..)
+    v8h qv[QV];
+#pragma unroll
+    for (int k = 0; k < QV; ++k) {
+        const int v = tid + 64 * NWV * k;
+        const int part = v / (32 * HD / 8), r = (v / (HD / 8)) % 32, dv = v % (HD / 8);
+        const int rq = min(qbase + r, qrows - 1);
+        const int64_t qo = ((int64_t)(rq / gqa) * a.n_head + kvh * gqa + rq % gqa) * HD + 8 * dv;
+        qv[k] = *(const v8h*)((part ? a.ql16 : a.qh16) + qo);
+    }
+    const int64_t j0 = ws0 + 4 * g - npast;  // tree index of this lane's first score slot
+    const int wsel = (int)min(max(j0, (int64_t)0) >> 5, (int64_t)a.anc_words - 1);
+    const int wnext = min(wsel + 1, a.anc_words - 1);
+    uint32_t aw0[PPW], aw1[PPW];
+#pragma unroll
+    for (int pi = 0; pi < PPW; ++pi) {
+        const int qt = (w * PPW + pi) & 1;
+        const int rq = min(qbase + qt * 16 + col, qrows - 1);
+        const uint32_t* an = a.anc + (int64_t)(rq / gqa) * a.anc_words;
+        aw0[pi] = an[wsel];
+        aw1[pi] = an[wnext];
+    }
     v8h kf[NDC];
     {
         const _Float16* krow = a.kc + (ws0 + col) * kdim + (int64_t)kvh * HD + 8 * g;
@@ -93,33 +112,36 @@ __global__ void __launch_bounds__(64 * NWV) k_attn_mfma(AttnMArgs a) {
 #pragma unroll
         for (int st = 0; st < NST; ++st) vf[st] = *(const v4h*)(vrow + 16 * st);
     }
-    // 16-byte vectors of the staged queries: 2 parts x 32 rows x HD / 8
+    __builtin_amdgcn_sched_barrier(0);  // all loads in flight before the first use
 #pragma unroll
-    for (int k = 0; k < (2 * 32 * HD / 8) / (64 * NWV); ++k) {
+    for (int k = 0; k < QV; ++k) {
         const int v = tid + 64 * NWV * k;
         const int part = v / (32 * HD / 8), r = (v / (HD / 8)) % 32, dv = v % (HD / 8);
-        const int rq = qbase + r;
-        v8h x = {};
-        if (rq < qrows) {
-            const int64_t qo = ((int64_t)(rq / gqa) * a.n_head + kvh * gqa + rq % gqa) * HD + 8 * dv;
-            x = *(const v8h*)((part ? a.ql16 : a.qh16) + qo);
-        }
-        *(v8h*)&qs[part][r][8 * dv] = x;
+        *(v8h*)&qs[part][r][8 * dv] = qv[k];
     }
     __syncthreads();
-    // ---- S^T = K . Q^T for the wave's query tiles; lane (col, g) then
-    // holds S^T[slot ws0 + 4g + r][query row qt * 16 + col]
-    v4f sc[PPW];
+    // ---- S^T = K . Q^T for the wave's query tiles (every query fragment
+    // read from LDS first); lane (col, g) then holds S^T[slot ws0 + 4g + r]
+    // [query row qt * 16 + col]
+    v8h qf[PPW][NDC][2];
 #pragma unroll
     for (int pi = 0; pi < PPW; ++pi) {
         const int qt = (w * PPW + pi) & 1;
+#pragma unroll
+        for (int dc = 0; dc < NDC; ++dc) {
+            qf[pi][dc][0] = *(const v8h*)&qs[0][qt * 16 + col][32 * dc + 8 * g];
+            qf[pi][dc][1] = *(const v8h*)&qs[1][qt * 16 + col][32 * dc + 8 * g];
+        }
+    }
+    __builtin_amdgcn_sched_barrier(0);
+    v4f sc[PPW];
+#pragma unroll
+    for (int pi = 0; pi < PPW; ++pi) {
         v4f acc = {0.f, 0.f, 0.f, 0.f};
 #pragma unroll
         for (int dc = 0; dc < NDC; ++dc) {
-            const v8h qh = *(const v8h*)&qs[0][qt * 16 + col][32 * dc + 8 * g];
-            const v8h ql = *(const v8h*)&qs[1][qt * 16 + col][32 * dc + 8 * g];
-            acc = __builtin_amdgcn_mfma_f32_16x16x32_f16(kf[dc], qh, acc, 0, 0, 0);
-            acc = __builtin_amdgcn_mfma_f32_16x16x32_f16(kf[dc], ql, acc, 0, 0, 0);
+            acc = __builtin_amdgcn_mfma_f32_16x16x32_f16(kf[dc], qf[pi][dc][0], acc, 0, 0, 0);
+            acc = __builtin_amdgcn_mfma_f32_16x16x32_f16(kf[dc], qf[pi][dc][1], acc, 0, 0, 0);
         }
         sc[pi] = acc;
     }
@@ -128,13 +150,16 @@ __global__ void __launch_bounds__(64 * NWV) k_attn_mfma(AttnMArgs a) {
 #pragma unroll
     for (int pi = 0; pi < PPW; ++pi) {
         const int qt = (w * PPW + pi) & 1;
-        const int rq = qbase + qt * 16 + col;
-        const bool qvalid = rq < qrows;
-        const int mq = qvalid ? rq / gqa : 0;
+        const bool qvalid = qbase + qt * 16 + col < qrows;
+        const uint64_t win = aw0[pi] | ((uint64_t)aw1[pi] << 32);
         float m_ = -INFINITY;
 #pragma unroll
         for (int r = 0; r < 4; ++r) {
-            const bool ok = qvalid && slot_visible(a, npast, mq, ws0 + 4 * g + r);
+            // committed slot, or tree slot j whose ancestor bit is set (bit
+            // j - 32 wsel of the two-word window)
+            const int64_t j = j0 + r;
+            const bool tree_ok = j >= 0 && j < a.M && ((win >> ((j - 32 * wsel) & 63)) & 1u);
+            const bool ok = qvalid && (j < 0 || tree_ok);
             const float sv = ok ? sc[pi][r] * scale : -INFINITY;
             sc[pi][r] = sv;
             m_ = fmaxf(m_, sv);
@@ -179,13 +204,18 @@ __global__ void __launch_bounds__(64 * NWV) k_attn_mfma(AttnMArgs a) {
 #pragma unroll
     for (int qi = 0; qi < QPW; ++qi) {
         const int qt = QPW == 2 ? qi : w / NDT;
+        v4h ph[NST], pl[NST];
+#pragma unroll
+        for (int st = 0; st < NST; ++st) {
+            ph[st] = *(const v4h*)&ps[0][qt * 16 + col][16 * st + 4 * g];
+            pl[st] = *(const v4h*)&ps[1][qt * 16 + col][16 * st + 4 * g];
+        }
+        __builtin_amdgcn_sched_barrier(0);
         v4f o = {0.f, 0.f, 0.f, 0.f};
 #pragma unroll
         for (int st = 0; st < NST; ++st) {
-            const v4h ph = *(const v4h*)&ps[0][qt * 16 + col][16 * st + 4 * g];
-            const v4h pl = *(const v4h*)&ps[1][qt * 16 + col][16 * st + 4 * g];
-            o = __builtin_amdgcn_mfma_f32_16x16x16f16(ph, vf[st], o, 0, 0, 0);
-            o = __builtin_amdgcn_mfma_f32_16x16x16f16(pl, vf[st], o, 0, 0, 0);
+            o = __builtin_amdgcn_mfma_f32_16x16x16f16(ph[st], vf[st], o, 0, 0, 0);
+            o = __builtin_amdgcn_mfma_f32_16x16x16f16(pl[st], vf[st], o, 0, 0, 0);
         }
 #pragma unroll
         for (int r = 0; r < 4; ++r) {
