@@ -291,6 +291,7 @@ __global__ void __launch_bounds__(128) k_attn_combine(AttnMArgs a, int nch) {
 template <int HD>
 __global__ void __launch_bounds__(256) k_attn_combine_xq(AttnMArgs a, int nch, XqPtrs o) {
     constexpr int HPB = 256 / HD;
+    constexpr int CPF = 8;  // chunk partials per thread held in registers
     __shared__ float wsh[HPB][1024];  // chunk weights (nch <= 1024)
     __shared__ float sden[HPB];
     __shared__ float4 red[4][64];
@@ -301,29 +302,54 @@ __global__ void __launch_bounds__(256) k_attn_combine_xq(AttnMArgs a, int nch, X
     const int hh = (4 * l) / HD, d = (4 * l) % HD;
     float v[4] = {0.f, 0.f, 0.f, 0.f};
     if (m < a.M) {
+        // the common case's loads issued together, branch-free (chunk
+        // indices clamped): chunk statistics of head min(w, HPB - 1), chunk l,
+        // and this thread's partials of chunks w + 4k, k < CPF
+        const int64_t qw = (int64_t)m * a.n_head + sb * HPB + min(w, HPB - 1);
+        const int cl = min(l, nvalid - 1);
+        const float pm = a.pmax[qw * nch + cl], pz = a.psum[qw * nch + cl];
+        const int64_t qi = (int64_t)m * a.n_head + sb * HPB + hh;
+        const float* po = a.pout + qi * nch * HD + d;
+        float4 pf[CPF];
+#pragma unroll
+        for (int k = 0; k < CPF; ++k) pf[k] = *(const float4*)(po + (int64_t)min(w + 4 * k, nvalid - 1) * HD);
+        __builtin_amdgcn_sched_barrier(0);
         if (w < HPB) {
-            const int64_t qi = (int64_t)m * a.n_head + sb * HPB + w;
-            float mx = -INFINITY;
-            for (int c = l; c < nvalid; c += 64) mx = fmaxf(mx, a.pmax[qi * nch + c]);
+            float mx = l < nvalid ? pm : -INFINITY;
+            for (int c = l + 64; c < nvalid; c += 64) mx = fmaxf(mx, a.pmax[qw * nch + c]);
 #pragma unroll
             for (int s = 32; s > 0; s >>= 1) mx = fmaxf(mx, __shfl_xor(mx, s, 64));
             float den = 0.f;
-            for (int c = l; c < nvalid; c += 64) {
-                const float mc = a.pmax[qi * nch + c];
+            if (l < nvalid) {
+                const float wc = pm == -INFINITY ? 0.f : expf(pm - mx);
+                wsh[w][l] = wc;
+                den = wc * pz;
+            }
+            for (int c = l + 64; c < nvalid; c += 64) {
+                const float mc = a.pmax[qw * nch + c];
                 const float wc = mc == -INFINITY ? 0.f : expf(mc - mx);
                 wsh[w][c] = wc;
-                den += wc * a.psum[qi * nch + c];
+                den += wc * a.psum[qw * nch + c];
             }
 #pragma unroll
             for (int s = 32; s > 0; s >>= 1) den += __shfl_xor(den, s, 64);
             if (l == 0) sden[w] = den;
         }
         __syncthreads();
-        const int64_t qi = (int64_t)m * a.n_head + sb * HPB + hh;
-        const float* po = a.pout + qi * nch * HD + d;
+        // chunks in the order w, w + 4, w + 8, ..
         float4 num = {0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+        for (int k = 0; k < CPF; ++k) {
+            if (w + 4 * k < nvalid) {  // wave-uniform
+                const float wc = wsh[hh][w + 4 * k];
+                num.x += wc * pf[k].x;
+                num.y += wc * pf[k].y;
+                num.z += wc * pf[k].z;
+                num.w += wc * pf[k].w;
+            }
+        }
 #pragma unroll 4
-        for (int c = w; c < nvalid; c += 4) {
+        for (int c = w + 4 * CPF; c < nvalid; c += 4) {
             const float wc = wsh[hh][c];
             const float4 p = *(const float4*)(po + (int64_t)c * HD);
             num.x += wc * p.x;
