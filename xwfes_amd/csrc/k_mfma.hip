@@ -81,9 +81,16 @@ __global__ void __launch_bounds__(256) k_xq_prep(float* __restrict__ x, int64_t 
     const int m = blockIdx.y, t = threadIdx.x;
     const bool live = m < M;  // block-uniform
     float* row = x + (int64_t)m * ldx;
+    const int l = t & 63;
+    const int64_t k0 = sb * 256 + 4 * l;
+    // the norm weights of lane l's four elements are loaded first, so that
+    // they arrive with x and the partials (one round trip, not two)
+    float4 w4 = {1.f, 1.f, 1.f, 1.f};
+    if (live && normw) w4 = *(const float4*)(normw + k0);
+    const int64_t k = sb * 256 + t;
+    float xv = 0.f;
     if (live) {
-        const int64_t k = sb * 256 + t;
-        float v = row[k];
+        xv = row[k];
         if (part) {
             float acc = 0.f;
             for (int s0 = 0; s0 < S; s0 += 16) {
@@ -94,16 +101,22 @@ __global__ void __launch_bounds__(256) k_xq_prep(float* __restrict__ x, int64_t 
 #pragma unroll
                 for (int i = 0; i < 16; ++i) acc += p[i];
             }
-            v += acc;
-            row[k] = v;
+            xv += acc;
         }
-        vs[t] = v;
+        vs[t] = xv;
     }
+    // every load has arrived on every path here (vmcnt 0, expcnt and lgkmcnt
+    // untouched), which the compiler then knows at the join below
+    __builtin_amdgcn_s_waitcnt(0x0F70);
     __syncthreads();
-    if (t >= 64) return;
-    const int l = t;
-    const int64_t k0 = sb * 256 + 4 * l;
+    // every store after the barrier (which then waits for none) and after the
+    // last use of a loaded value (so no wait for a load covers a store)
+    if (t >= 64) {
+        if (live && part) row[k] = xv;
+        return;
+    }
     float v[4] = {0.f, 0.f, 0.f, 0.f};
+    float ss = 0.f;
     if (live) {
         const float4 t4 = *(const float4*)&vs[4 * l];
         v[0] = t4.x;
@@ -111,22 +124,20 @@ __global__ void __launch_bounds__(256) k_xq_prep(float* __restrict__ x, int64_t 
         v[2] = t4.z;
         v[3] = t4.w;
         if (normw) {
-            float ss = v[0] * v[0];
+            ss = v[0] * v[0];
             ss += v[1] * v[1];
             ss += v[2] * v[2];
             ss += v[3] * v[3];
 #pragma unroll
             for (int o = 32; o > 0; o >>= 1) ss += __shfl_xor(ss, o, 64);
-            if (l == 0) ssq[sb * 8 + m] = ss;
-            const float4 w4 = *(const float4*)(normw + k0);
             v[0] = v[0] * w4.x;
             v[1] = v[1] * w4.y;
             v[2] = v[2] * w4.z;
             v[3] = v[3] * w4.w;
         }
-    } else if (normw && l == 0) {
-        ssq[sb * 8 + m] = 0.f;
     }
+    if (live && part) row[k] = xv;
+    if (normw && l == 0) ssq[sb * 8 + m] = ss;
     xq_emit(v, sb, m, l, XqPtrs{frag, xs32, xs16, scale, ssq});
 }
 
