@@ -444,7 +444,10 @@ def test_accept_greedy_chain_and_tree(gctx, orc, V):
         assert (g["accepted"], g["bonus"]) == (o["accepted"], o["bonus"])
 
 
-@pytest.mark.parametrize("V,temp", [(64, 1.0), (32000, 0.8), (128256, 0.8)])
+# 1001: rows not 16-byte aligned, a partial last sub-chunk; 262147: several
+# sub-chunks per scanning thread in the bonus pick
+@pytest.mark.parametrize("V,temp", [(64, 1.0), (1001, 0.7), (32000, 0.8), (128256, 0.8),
+                                    (262147, 1.3)])
 def test_accept_ratio_chain(gctx, orc, V, temp):
     rng = np.random.default_rng(V + 1)
     for trial in range(12 if V > 1000 else 60):

@@ -284,15 +284,28 @@ struct RowStats {
     int32_t amax;
     double sum;  // sum_i exp((l_i - mx)/T) in double
 };
+// Full-vocab statistics of M + 1 logits rows (row 0 = base_row, row 1 + i =
+// rows + i V): per 4096-element chunk the first-max argmax and, with
+// with_sum, per 128-element sub-chunk the double sum of exp((l - max)/T)
+// with the row max.  The acceptance kernel combines them.
+struct RowChunks {
+    float* cmax;     // [nrows][nch]
+    int32_t* carg;   // [nrows][nch]
+    double* csub;    // [nrows][nsub]
+    int nch, nsub;
+};
 size_t row_stats_scratch_bytes(int64_t nrows, int64_t V);
-// with_sum = 0 skips the exp sums (greedy decisions need the argmax only)
-hipError_t launch_row_stats(hipStream_t st, const float* rows, int64_t nrows, int64_t V,
-                            float temp, int with_sum, void* scratch, RowStats* out);
+RowChunks row_chunks(void* scratch, int64_t nrows, int64_t V);
+hipError_t launch_row_stats(hipStream_t st, const float* base_row, const float* rows,
+                            int64_t nrows, int64_t V, float temp, int with_sum,
+                            const RowChunks& rc);
 struct AcceptDev {
     const float* base_row;
     const float* rows;
     const float* q;
-    const RowStats* stats;   // [M+1]: stats[0] = base row, stats[1+i] = row i
+    RowChunks rc;            // chunk statistics of the M + 1 rows
+    int with_sum;
+    RowStats* stats;         // [M+1] written by the kernel: stats[0] base row, stats[1+i] row i
     int64_t M, V;
     const int32_t* props;    // device [M]
     const int32_t* parents;  // device [M] (chain given explicitly)
@@ -300,11 +313,8 @@ struct AcceptDev {
     int mode;
     float temp;
     uint64_t* rng;           // device state
-    double* p;               // scratch [V]
-    double* part;            // scratch [1024]
+    double* p;               // scratch [V] (residual mode)
     int32_t* out;            // device: [0]=n_acc, [1]=bonus, [2..2+M) accepted
     float* margin;           // device scalar
-    int32_t* brow;           // device scalar: row of the ratio-mode bonus draw
-    float* bu;               // device scalar: its uniform
 };
 hipError_t launch_accept(hipStream_t st, const AcceptDev& a);

@@ -2,19 +2,24 @@
 //
 // Row statistics: first-max argmax (include/ft/sampler.h:21-28), float max,
 // and sum_i exp((double)((l_i - max) / T)) in double (src/spec.cpp:89-95,
-// 217-223), each computed over 4096-element chunks in parallel and combined
-// in chunk order.  Acceptance: accept_chain_greedy / accept_chain_sampling
+// 217-223).  Two launches cover the base row and every draft row: per
+// 4096-element chunk the first-max argmax, then per 128-element sub-chunk
+// the double sum of the exponentials with the row max.  The acceptance
+// kernel combines them: accept_chain_greedy / accept_chain_sampling
 // (src/spec.cpp:203-238) with the SplitMix64 stream of src/spec.cpp:10-17,
 // the bonus token drawn from the row after the last accepted node, and the
 // tree / residual-resampling extensions (Leviathan et al. 2023 Alg. 1;
 // SpecInfer, Miao et al. 2023).  Inverse-CDF sampling takes the first index
-// whose running double sum of the normalised target exceeds u * total.
+// whose running double sum of the target exceeds u * total; the ratio-mode
+// bonus finds the crossing 128-element sub-chunk by a scan of the sub-chunk
+// sums and sums only that sub-chunk element by element.
 #include "ftx_internal.h"
 
 namespace {
 
-constexpr int NT = 1024;  // threads of the single-block acceptance kernels
+constexpr int NT = 1024;  // threads of the single-block acceptance kernel
 constexpr int SCH = 4096; // elements per statistics chunk
+constexpr int SUB = 128;  // elements per exp-sum sub-chunk (SCH / SUB per chunk)
 
 __device__ __forceinline__ uint64_t splitmix_next(uint64_t& s) {
     uint64_t z = (s += 0x9E3779B97F4A7C15ull);
@@ -31,23 +36,38 @@ __device__ __forceinline__ bool better(float b, int32_t ib, float a, int32_t ia)
     return b > a || (b == a && ib < ia) || (a != a && b == b);
 }
 
-// ---- statistics pass 1: per (row, chunk) first-max argmax
-__global__ void __launch_bounds__(256) k_row_max(const float* __restrict__ rows, int64_t V,
-                                                 int nch, float* __restrict__ cmax,
-                                                 int32_t* __restrict__ carg) {
+__device__ __forceinline__ const float* stat_row(const float* base_row, const float* rows,
+                                                 int64_t r, int64_t V) {
+    return r == 0 ? base_row : rows + (r - 1) * V;
+}
+
+// exp((double)((l - mx) / T)): the one expression every sum and pick uses
+__device__ __forceinline__ double texp(float l, float mx, float temp) {
+#pragma clang fp contract(off)
+    return exp((double)((l - mx) / temp));
+}
+
+// ---- statistics pass 1: per (row, chunk) first-max argmax; the 16 loads
+// of a thread are issued together (clamped index, masked)
+__global__ void __launch_bounds__(256) k_row_max(const float* __restrict__ base_row,
+                                                 const float* __restrict__ rows, int64_t V,
+                                                 RowChunks rc) {
     __shared__ float sv[256];
     __shared__ int32_t si[256];
     const int64_t r = blockIdx.y;
     const int c = blockIdx.x, t = threadIdx.x;
-    const float* row = rows + r * V;
-    const int64_t b = (int64_t)c * SCH, e = min(V, b + SCH);
+    const float* row = stat_row(base_row, rows, r, V);
+    const int64_t b = (int64_t)c * SCH;
+    float v[SCH / 256];
+#pragma unroll
+    for (int k = 0; k < SCH / 256; ++k) v[k] = row[min(b + t + 256 * k, V - 1)];
     float best = -INFINITY;
     int32_t bi = 0x7FFFFFFF;
-#pragma unroll 8
-    for (int64_t i = b + t; i < e; i += 256) {
-        const float v = row[i];
-        if (bi == 0x7FFFFFFF || better(v, (int32_t)i, best, bi)) {
-            best = v;
+#pragma unroll
+    for (int k = 0; k < SCH / 256; ++k) {
+        const int64_t i = b + t + 256 * k;
+        if (i < V && (bi == 0x7FFFFFFF || better(v[k], (int32_t)i, best, bi))) {
+            best = v[k];
             bi = (int32_t)i;
         }
     }
@@ -63,81 +83,70 @@ __global__ void __launch_bounds__(256) k_row_max(const float* __restrict__ rows,
         __syncthreads();
     }
     if (t == 0) {
-        cmax[r * nch + c] = sv[0];
-        carg[r * nch + c] = si[0];
+        rc.cmax[r * rc.nch + c] = sv[0];
+        rc.carg[r * rc.nch + c] = si[0];
     }
 }
 
-// ---- statistics pass 2: per (row, chunk) sum of exp((l - max)/T), the row
-// max being the max of the chunk maxima
-__global__ void __launch_bounds__(256) k_row_sum(const float* __restrict__ rows, int64_t V,
-                                                 int nch, float temp,
-                                                 const float* __restrict__ cmax,
-                                                 double* __restrict__ csum) {
+// ---- statistics pass 2: per (row, 128-element sub-chunk) sum of
+// exp((l - max)/T), the row max being the max of the chunk maxima.  Thread
+// t takes elements 16t .. 16t + 15 of the chunk (vector loads when rows are
+// 16-byte aligned), eight threads one sub-chunk: sums in index order per
+// thread, then over the eight threads in a fixed tree.
+template <bool VEC>
+__global__ void __launch_bounds__(256) k_row_sum(const float* __restrict__ base_row,
+                                                 const float* __restrict__ rows, int64_t V,
+                                                 float temp, RowChunks rc) {
 #pragma clang fp contract(off)
-    __shared__ double sd[256];
     const int64_t r = blockIdx.y;
     const int c = blockIdx.x, t = threadIdx.x;
-    float mx = -INFINITY;
-#pragma unroll 8
-    for (int k = 0; k < nch; ++k) mx = fmaxf(mx, cmax[r * nch + k]);
-    const float* row = rows + r * V;
-    const int64_t b = (int64_t)c * SCH, e = min(V, b + SCH);
-    double s = 0.0;
-#pragma unroll 8
-    for (int64_t i = b + t; i < e; i += 256) s += exp((double)((row[i] - mx) / temp));
-    sd[t] = s;
-    __syncthreads();
-    for (int o = 128; o > 0; o >>= 1) {
-        if (t < o) sd[t] += sd[t + o];
-        __syncthreads();
-    }
-    if (t == 0) csum[r * nch + c] = sd[0];
-}
-
-// ---- statistics pass 3: combine chunks in order
-__global__ void k_row_final(int nch, const float* __restrict__ cmax,
-                            const int32_t* __restrict__ carg, const double* __restrict__ csum,
-                            int with_sum, RowStats* __restrict__ out) {
-    if (threadIdx.x != 0) return;
-    const int64_t r = blockIdx.x;
-    float best = cmax[r * nch];
-    int32_t bi = carg[r * nch];
-    for (int k = 1; k < nch; ++k)
-        if (better(cmax[r * nch + k], carg[r * nch + k], best, bi)) {
-            best = cmax[r * nch + k];
-            bi = carg[r * nch + k];
+    const float* row = stat_row(base_row, rows, r, V);
+    const int64_t i0 = (int64_t)c * SCH + 16 * t;
+    float v[16];
+    if (VEC && i0 + 16 <= V) {
+#pragma unroll
+        for (int k = 0; k < 4; ++k) {
+            const float4 q = *(const float4*)(row + i0 + 4 * k);
+            v[4 * k] = q.x;
+            v[4 * k + 1] = q.y;
+            v[4 * k + 2] = q.z;
+            v[4 * k + 3] = q.w;
         }
+    } else {
+#pragma unroll
+        for (int k = 0; k < 16; ++k) v[k] = row[min(i0 + k, V - 1)];
+    }
+    float mx = -INFINITY;
+    for (int k = 0; k < rc.nch; ++k) mx = fmaxf(mx, rc.cmax[r * rc.nch + k]);
     double s = 0.0;
-    if (with_sum)
-        for (int k = 0; k < nch; ++k) s += csum[r * nch + k];
-    out[r].mx = best;
-    out[r].amax = bi;
-    out[r].sum = s;
+#pragma unroll
+    for (int k = 0; k < 16; ++k)
+        if (i0 + k < V) s += texp(v[k], mx, temp);
+    s += __shfl_xor(s, 4, 64);
+    s += __shfl_xor(s, 2, 64);
+    s += __shfl_xor(s, 1, 64);
+    const int64_t j = (int64_t)c * (SCH / SUB) + t / 8;
+    if ((t & 7) == 0 && j < rc.nsub) rc.csub[r * rc.nsub + j] = s;
 }
 
-// ---- inverse-CDF pick over p[0..V) (double weights) by one block: chunk
-// sums, a block scan, then the crossing chunk scanned in order.  Falls back
-// to the last positive weight when rounding leaves no crossing.
-// Inverse-CDF pick over V probabilities: thread t owns the contiguous chunk
-// [t * chunk, (t + 1) * chunk) and sums it in index order.  `tr` selects the
-// chunk-transposed layout p[k * NT + t] = prob(t * chunk + k), whose loads
-// are coalesced across threads; the arithmetic is the same in both layouts.
-__device__ int32_t block_pick(const double* __restrict__ p, int64_t V, float u, bool tr) {
+// Inverse-CDF pick over p[0..V) (double weights) by one block: thread t sums
+// the contiguous chunk [t * chunk, (t + 1) * chunk) in index order (eight
+// loads issued together), a block scan, then the crossing chunk scanned in
+// order.  Falls back to the last positive weight when rounding leaves no
+// crossing.
+__device__ int32_t block_pick(const double* __restrict__ p, int64_t V, float u) {
     __shared__ double incl[NT];
     __shared__ int32_t lastpos[NT];
     __shared__ int32_t pick;
     const int t = threadIdx.x;
     const int64_t chunk = (V + NT - 1) / NT;
     const int64_t b = t * chunk, e = min(V, b + chunk);
-    // sums in index order; the loads of eight elements are issued together
     double cs = 0.0;
     int32_t lp = -1;
-    auto at = [&](int64_t i) { return tr ? p[(i - b) * NT + t] : p[i]; };
     for (int64_t i0 = b; i0 < e; i0 += 8) {
         double v[8];
 #pragma unroll
-        for (int k = 0; k < 8; ++k) v[k] = i0 + k < e ? at(i0 + k) : 0.0;
+        for (int k = 0; k < 8; ++k) v[k] = i0 + k < e ? p[i0 + k] : 0.0;
 #pragma unroll
         for (int k = 0; k < 8; ++k) {
             if (i0 + k >= e) break;
@@ -166,7 +175,7 @@ __device__ int32_t block_pick(const double* __restrict__ p, int64_t V, float u, 
         for (int64_t i0 = b; i0 < e && !found; i0 += 8) {
             double v[8];
 #pragma unroll
-            for (int k = 0; k < 8; ++k) v[k] = i0 + k < e ? at(i0 + k) : 0.0;
+            for (int k = 0; k < 8; ++k) v[k] = i0 + k < e ? p[i0 + k] : 0.0;
 #pragma unroll
             for (int k = 0; k < 8; ++k) {
                 if (found || i0 + k >= e) break;
@@ -181,6 +190,111 @@ __device__ int32_t block_pick(const double* __restrict__ p, int64_t V, float u, 
     __syncthreads();
     int32_t r = pick;
     if (r < 0) r = lastpos[NT - 1] >= 0 ? lastpos[NT - 1] : 0;
+    __syncthreads();
+    return r;
+}
+
+// Inclusive block scan of one double per thread (wave scans, then the wave
+// totals); returns the thread's inclusive prefix, *tot the block total.
+__device__ double block_scan(double v, double* tot) {
+    __shared__ double wsum[NT / 64];
+    const int t = threadIdx.x, l = t & 63, w = t >> 6;
+#pragma unroll
+    for (int o = 1; o < 64; o <<= 1) {
+        const double n = __shfl_up(v, o, 64);
+        if (l >= o) v += n;
+    }
+    if (l == 63) wsum[w] = v;
+    __syncthreads();
+    if (w == 0) {
+        double x = l < NT / 64 ? wsum[l] : 0.0;
+#pragma unroll
+        for (int o = 1; o < NT / 64; o <<= 1) {
+            const double n = __shfl_up(x, o, 64);
+            if (l >= o) x += n;
+        }
+        if (l < NT / 64) wsum[l] = x;
+    }
+    __syncthreads();
+    const double r = v + (w ? wsum[w - 1] : 0.0);
+    *tot = wsum[NT / 64 - 1];
+    __syncthreads();
+    return r;
+}
+
+// Ratio-mode bonus: inverse CDF over exp((l - mx)/T) of row `lg` from its
+// sub-chunk sums `sub` (nsub of them): thread t owns sub-chunks [t spt, (t +
+// 1) spt); the crossing thread finds the crossing sub-chunk, whose 128
+// exponentials are formed again by one wave and summed in index order by its
+// first lane.  Rounding that leaves no crossing inside the sub-chunk picks
+// its last positive element.
+__device__ int32_t pick_from_subs(const float* __restrict__ lg, int64_t V, float mx, float temp,
+                                  const double* __restrict__ sub, int nsub, float u) {
+#pragma clang fp contract(off)
+    __shared__ int jsel, first;
+    __shared__ double exsel;
+    __shared__ double ev[SUB];
+    __shared__ double incl[NT];
+    __shared__ int32_t pick;
+    const int t = threadIdx.x;
+    const int spt = (nsub + NT - 1) / NT;
+    const int j0 = t * spt, j1 = min(nsub, j0 + spt);
+    double cs = 0.0;
+    for (int j = j0; j < j1; ++j) cs += sub[j];
+    if (t == 0) {
+        jsel = -1;
+        pick = -1;
+        first = NT;
+    }
+    double tot;
+    const double inc = block_scan(cs, &tot);
+    incl[t] = inc;
+    const double target = (double)u * tot;
+    if (inc > target) atomicMin(&first, t);
+    __syncthreads();
+    if (t == first) {
+        // the first thread whose inclusive prefix passes the target: its
+        // sub-chunks in order from the previous thread's prefix
+        double c = t ? incl[t - 1] : 0.0;
+        int js = -1;
+        double es = c;
+        for (int j = j0; j < j1; ++j) {
+            const double nc = c + sub[j];
+            if (sub[j] > 0) {
+                js = j;
+                es = c;
+            }
+            if (nc > target) break;
+            c = nc;
+        }
+        jsel = js;
+        exsel = es;
+    }
+    __syncthreads();
+    const int js = jsel;
+    if (t < 64 && js >= 0) {
+#pragma unroll
+        for (int k = 0; k < SUB / 64; ++k) {
+            const int64_t i = (int64_t)js * SUB + t + 64 * k;
+            ev[t + 64 * k] = i < V ? texp(lg[i], mx, temp) : 0.0;
+        }
+    }
+    __syncthreads();
+    if (t == 0 && js >= 0) {
+        double c = exsel;
+        int32_t last = -1, pk = -1;
+        for (int k = 0; k < SUB; ++k) {
+            if (ev[k] > 0) last = js * SUB + k;
+            c += ev[k];
+            if (c > target) {
+                pk = js * SUB + k;
+                break;
+            }
+        }
+        pick = pk >= 0 ? pk : last;
+    }
+    __syncthreads();
+    const int32_t r = pick >= 0 ? pick : 0;
     __syncthreads();
     return r;
 }
@@ -220,7 +334,7 @@ __global__ void __launch_bounds__(NT) k_accept(AcceptDev a) {
     __shared__ double sd[NT];
     __shared__ uint64_t rng;
     __shared__ int32_t cur, nacc, bonus, next;
-    __shared__ float mg;
+    __shared__ float mg, bu;
     const int t = threadIdx.x;
     const int64_t V = a.V;
     if (t == 0) {
@@ -229,6 +343,41 @@ __global__ void __launch_bounds__(NT) k_accept(AcceptDev a) {
         nacc = 0;
         bonus = 0;
         mg = INFINITY;
+    }
+    // row statistics from the chunk results, one wave per row: first-max
+    // argmax over the chunks, the exp sum over the sub-chunks (lane-strided
+    // sums in index order, then a fixed tree)
+    {
+        const int w = t >> 6, l = t & 63;
+        const RowChunks& rc = a.rc;
+        for (int64_t r = w; r <= a.M; r += NT / 64) {
+            float best = -INFINITY;
+            int32_t bi = 0x7FFFFFFF;
+            for (int c = l; c < rc.nch; c += 64) {
+                const float v = rc.cmax[r * rc.nch + c];
+                const int32_t iv = rc.carg[r * rc.nch + c];
+                if (iv != 0x7FFFFFFF && (bi == 0x7FFFFFFF || better(v, iv, best, bi))) {
+                    best = v;
+                    bi = iv;
+                }
+            }
+#pragma unroll
+            for (int o = 32; o > 0; o >>= 1) {
+                const float ov = __shfl_xor(best, o, 64);
+                const int32_t oi = __shfl_xor(bi, o, 64);
+                if (oi != 0x7FFFFFFF && (bi == 0x7FFFFFFF || better(ov, oi, best, bi))) {
+                    best = ov;
+                    bi = oi;
+                }
+            }
+            double sum = 0.0;
+            if (a.with_sum) {
+                for (int j = l; j < rc.nsub; j += 64) sum += rc.csub[r * rc.nsub + j];
+#pragma unroll
+                for (int o = 32; o > 0; o >>= 1) sum += __shfl_xor(sum, o, 64);
+            }
+            if (l == 0) a.stats[r] = RowStats{best, bi, sum};
+        }
     }
     __syncthreads();
 #define ROW(c) ((c) < 0 ? a.base_row : a.rows + (int64_t)(c) * V)
@@ -276,11 +425,16 @@ __global__ void __launch_bounds__(NT) k_accept(AcceptDev a) {
             for (int32_t i = 0; i < k; ++i) a.out[2 + i] = i;
             nacc = k;
             cur = k - 1;
-            *a.bu = splitmix_float(s);  // the bonus token's uniform
-            *a.brow = k - 1;
+            bu = splitmix_float(s);  // the bonus token's uniform
             rng = s;
             mg = m;
         }
+        __syncthreads();
+        // the bonus from the row after the last accepted node
+        const int32_t c = cur;
+        const int32_t b = pick_from_subs(ROW(c), V, STAT(c).mx, a.temp,
+                                         a.rc.csub + (int64_t)(c + 1) * a.rc.nsub, a.rc.nsub, bu);
+        if (t == 0) bonus = b;
         __syncthreads();
     } else {  // RESIDUAL
         for (;;) {
@@ -331,7 +485,7 @@ __global__ void __launch_bounds__(NT) k_accept(AcceptDev a) {
                     rng = s;
                 }
                 __syncthreads();
-                const int32_t b = block_pick(a.p, V, ub2, false);
+                const int32_t b = block_pick(a.p, V, ub2);
                 if (t == 0) bonus = b;
                 __syncthreads();
                 break;
@@ -353,61 +507,41 @@ __global__ void __launch_bounds__(NT) k_accept(AcceptDev a) {
     }
 }
 
-// RATIO bonus, step 1: the normalised target of the recorded row, in
-// parallel, stored chunk-transposed for the pick (see block_pick)
-__global__ void __launch_bounds__(256) k_bonus_dist(AcceptDev a) {
-#pragma clang fp contract(off)
-    const int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
-    if (i >= a.V) return;
-    const int32_t c = *a.brow;
-    const float* lg = c < 0 ? a.base_row : a.rows + (int64_t)c * a.V;
-    const RowStats st = a.stats[c + 1];
-    const int64_t chunk = (a.V + NT - 1) / NT;
-    a.p[(i % chunk) * NT + i / chunk] = exp((double)((lg[i] - st.mx) / a.temp)) / st.sum;
-}
-
-// RATIO bonus, step 2: the inverse-CDF pick
-__global__ void __launch_bounds__(NT) k_bonus_pick(AcceptDev a) {
-    const int32_t b = block_pick(a.p, a.V, *a.bu, true);
-    if (threadIdx.x == 0) a.out[1] = b;
-}
-
 }  // namespace
 
 size_t row_stats_scratch_bytes(int64_t nrows, int64_t V) {
-    const int64_t nch = (V + SCH - 1) / SCH;
-    return (size_t)(nrows * nch) * (4 + 4 + 8) + 64;
+    const int64_t nch = (V + SCH - 1) / SCH, nsub = (V + SUB - 1) / SUB;
+    return (size_t)(nrows * nsub) * 8 + (size_t)(nrows * nch) * 8 + 64;
 }
 
-hipError_t launch_row_stats(hipStream_t st, const float* rows, int64_t nrows, int64_t V,
-                            float temp, int with_sum, void* scratch, RowStats* out) {
+RowChunks row_chunks(void* scratch, int64_t nrows, int64_t V) {
+    RowChunks rc{};
+    rc.nch = (int)((V + SCH - 1) / SCH);
+    rc.nsub = (int)((V + SUB - 1) / SUB);
+    rc.csub = (double*)scratch;
+    rc.cmax = (float*)(rc.csub + nrows * rc.nsub);
+    rc.carg = (int32_t*)(rc.cmax + nrows * rc.nch);
+    return rc;
+}
+
+hipError_t launch_row_stats(hipStream_t st, const float* base_row, const float* rows,
+                            int64_t nrows, int64_t V, float temp, int with_sum,
+                            const RowChunks& rc) {
     if (nrows == 0) return hipSuccess;
-    const int nch = (int)((V + SCH - 1) / SCH);
-    double* csum = (double*)scratch;
-    float* cmax = (float*)(csum + nrows * nch);
-    int32_t* carg = (int32_t*)(cmax + nrows * nch);
-    hipLaunchKernelGGL(k_row_max, dim3((unsigned)nch, (unsigned)nrows), dim3(256), 0, st, rows, V,
-                       nch, cmax, carg);
+    const dim3 grid((unsigned)rc.nch, (unsigned)nrows);
+    hipLaunchKernelGGL(k_row_max, grid, dim3(256), 0, st, base_row, rows, V, rc);
     hipError_t e = hipGetLastError();
-    if (e != hipSuccess) return e;
-    if (with_sum) {
-        hipLaunchKernelGGL(k_row_sum, dim3((unsigned)nch, (unsigned)nrows), dim3(256), 0, st, rows,
-                           V, nch, temp, cmax, csum);
-        e = hipGetLastError();
-        if (e != hipSuccess) return e;
-    }
-    hipLaunchKernelGGL(k_row_final, dim3((unsigned)nrows), dim3(64), 0, st, nch, cmax, carg, csum,
-                       with_sum, out);
+    if (e != hipSuccess || !with_sum) return e;
+    const bool vec = V % 4 == 0 && ((uintptr_t)base_row % 16) == 0 &&
+                     (nrows == 1 || ((uintptr_t)rows % 16) == 0);
+    if (vec)
+        hipLaunchKernelGGL(k_row_sum<true>, grid, dim3(256), 0, st, base_row, rows, V, temp, rc);
+    else
+        hipLaunchKernelGGL(k_row_sum<false>, grid, dim3(256), 0, st, base_row, rows, V, temp, rc);
     return hipGetLastError();
 }
 
 hipError_t launch_accept(hipStream_t st, const AcceptDev& a) {
     hipLaunchKernelGGL(k_accept, dim3(1), dim3(NT), 0, st, a);
-    hipError_t e = hipGetLastError();
-    if (e != hipSuccess || a.mode != FTX_ACCEPT_RATIO) return e;
-    hipLaunchKernelGGL(k_bonus_dist, dim3((unsigned)((a.V + 255) / 256)), dim3(256), 0, st, a);
-    e = hipGetLastError();
-    if (e != hipSuccess) return e;
-    hipLaunchKernelGGL(k_bonus_pick, dim3(1), dim3(NT), 0, st, a);
     return hipGetLastError();
 }

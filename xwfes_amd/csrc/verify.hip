@@ -630,19 +630,18 @@ int ftx_accept(ftx_ctx* ctx, const ftx_accept_args* a) {
         if (a->mode == FTX_ACCEPT_RATIO && p != i - 1)
             return ftx_fail(ctx, FTX_E_INVALID, "ratio mode is chain only");
     }
-    // workspace: stats [M+1], p [V] doubles, the small block (rng, margin,
-    // out ints | props, parents, pd: one copy in, one copy of its head out)
+    // workspace: stats [M+1], p [V] doubles (residual mode), the small block
+    // (rng, margin, out ints | props, parents, pd: one copy in, one copy of
+    // its head out), the chunk statistics of the M + 1 rows
     const size_t stats_b = (size_t)(M + 1) * sizeof(RowStats);
     const size_t off_p = (stats_b + 255) & ~(size_t)255;
-    // p: V doubles, or the chunk-transposed bonus layout of ceil(V / 1024) * 1024
-    const size_t pn = (size_t)((V + 1023) / 1024 * 1024);
-    const size_t off_small = off_p + ((pn * 8 + 255) & ~(size_t)255);
+    const size_t pb = a->mode == FTX_ACCEPT_RESIDUAL ? (size_t)V * 8 : 0;
+    const size_t off_small = off_p + ((pb + 255) & ~(size_t)255);
     const size_t out_b = ((size_t)(M + 2) * 4 + 7) & ~(size_t)7;
     const size_t head_b = 16 + out_b;  // rng | margin | pad | out
     const size_t small_b = head_b + (size_t)M * 12 + 64;
     const size_t off_rs = off_small + ((small_b + 255) & ~(size_t)255);  // row-stat chunks
-    const size_t off_b = off_rs + ((row_stats_scratch_bytes(std::max<int64_t>(M, 1), V) + 255) &
-                                   ~(size_t)255);
+    const size_t off_b = off_rs + ((row_stats_scratch_bytes(M + 1, V) + 255) & ~(size_t)255);
     uint8_t* ws;
     int rc = ftx_workspace(ctx, off_b + 256, (void**)&ws);
     if (rc) return rc;
@@ -668,16 +667,17 @@ int ftx_accept(ftx_ctx* ctx, const ftx_accept_args* a) {
     uint8_t* d_small = ws + off_small;
     FTX_HIP(ctx, hipMemcpyAsync(d_small, pin, small_b, hipMemcpyHostToDevice, st));
     RowStats* stats = (RowStats*)ws;
+    const RowChunks rch = row_chunks(ws + off_rs, M + 1, V);
     int tk = tr_begin(ctx);
     const int with_sum = a->mode != FTX_ACCEPT_GREEDY;
-    FTX_HIP(ctx, launch_row_stats(st, a->base_row, 1, V, a->temp, with_sum, ws + off_rs, stats));
-    if (M > 0)
-        FTX_HIP(ctx, launch_row_stats(st, a->rows, M, V, a->temp, with_sum, ws + off_rs, stats + 1));
-    tr_end(ctx, tk, TK_ROW_STATS, (double)(M + 1) * V * 4);
+    FTX_HIP(ctx, launch_row_stats(st, a->base_row, a->rows, M + 1, V, a->temp, with_sum, rch));
+    tr_end(ctx, tk, TK_ROW_STATS, (double)(M + 1) * V * 4, with_sum ? 2 : 1);
     AcceptDev ad{};
     ad.base_row = a->base_row;
     ad.rows = a->rows;
     ad.q = a->q;
+    ad.rc = rch;
+    ad.with_sum = with_sum;
     ad.stats = stats;
     ad.M = M;
     ad.V = V;
@@ -688,11 +688,8 @@ int ftx_accept(ftx_ctx* ctx, const ftx_accept_args* a) {
     ad.temp = a->temp;
     ad.rng = (uint64_t*)d_small;
     ad.p = (double*)(ws + off_p);
-    ad.part = nullptr;
     ad.out = (int32_t*)(d_small + 16);
     ad.margin = (float*)(d_small + 8);
-    ad.brow = (int32_t*)(ws + off_b);
-    ad.bu = (float*)(ws + off_b + 16);
     tk = tr_begin(ctx);
     FTX_HIP(ctx, launch_accept(st, ad));
     tr_end(ctx, tk, TK_ACCEPT, (double)V * 4);
