@@ -323,6 +323,8 @@ class Ref:
         L.ref_engine_vocab.restype = C.c_int64
         L.ref_engine_vocab.argtypes = [C.c_void_p]
         L.ref_engine_step.argtypes = [C.c_void_p, C.c_int32, _fp]
+        L.ref_gguf_summary.restype = C.c_int64
+        L.ref_gguf_summary.argtypes = [C.c_char_p, C.c_char_p, C.c_char_p, C.c_int64]
 
     @staticmethod
     def available():
@@ -393,6 +395,15 @@ class Ref:
 
     def engine_free(self, h):
         self.lib.ref_engine_free(h)
+
+    def gguf_summary(self, path, keys):
+        """The reference parser's summary of a GGUF (see ref_harness.cpp),
+        or ("error", message) when it throws."""
+        cap = 1 << 22
+        buf = C.create_string_buffer(cap)
+        n = self.lib.ref_gguf_summary(path.encode(), "\n".join(keys).encode(), buf, cap)
+        text = buf.value.decode("utf-8", "surrogateescape")
+        return ("error", text) if n < 0 else text
 
 
 # ---------------- synthetic models (test data) ----------------

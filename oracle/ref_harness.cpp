@@ -7,9 +7,14 @@
 #include "ft/sampler.h"
 #include "ft/spec.h"
 #include "ft/engine.h"
+#include "ft/gguf.h"
+#include "ft/graph.h"
 
+#include <algorithm>
 #include <cstdint>
+#include <cstdio>
 #include <cstring>
+#include <string>
 #include <vector>
 
 namespace ft {
@@ -104,6 +109,81 @@ int ref_engine_step(void* h, int32_t tok, float* out) {
     } catch (...) {
         return -1;
     }
+}
+
+// The reference parser's view of a GGUF (ft::Gguf, config_from_gguf) in the
+// canonical summary form of xwfes_amd.gguf.summary(offsets=False): the
+// config, the typed accessors of `keys` ('\n'-separated, in order) and every
+// tensor with a hash of its bytes.  Returns the text length, or -1 when the
+// reference throws (the message then fills out).
+int64_t ref_gguf_summary(const char* path, const char* keys, char* out, int64_t cap) {
+    auto hash = [](const uint8_t* b, size_t n) {
+        unsigned long long h = 0;
+        for (size_t i = 0; i < n; ++i)
+            h += (unsigned long long)b[i] * ((i + 1) * 0x9E3779B97F4A7C15ull);
+        return h;
+    };
+    std::string s;
+    char buf[4096];
+    int64_t rc = 0;
+    try {
+        Gguf g(path);
+        try {
+            const ModelConfig c = config_from_gguf(g);
+            std::snprintf(buf, sizeof(buf),
+                          "config arch=%s n_layer=%lld n_embd=%lld n_head=%lld n_head_kv=%lld "
+                          "head_dim=%lld vocab=%lld n_ff=%lld ctx_train=%lld rms_eps=%.9g "
+                          "rope_theta=%.17g rope_neox=%d\n",
+                          c.arch.c_str(), (long long)c.n_layer, (long long)c.n_embd,
+                          (long long)c.n_head, (long long)c.n_head_kv, (long long)c.head_dim,
+                          (long long)c.vocab, (long long)c.n_ff, (long long)c.ctx_train,
+                          (double)c.rms_eps, c.rope_theta, (int)c.rope_neox);
+            s += buf;
+        } catch (...) {
+            s += "config error\n";
+        }
+        std::string ks(keys ? keys : "");
+        size_t p = 0;
+        while (p < ks.size()) {
+            size_t e = ks.find('\n', p);
+            if (e == std::string::npos) e = ks.size();
+            const std::string k = ks.substr(p, e - p);
+            p = e + 1;
+            if (k.empty()) continue;
+            const std::vector<float> f = g.get_f32_arr(k);
+            std::snprintf(buf, sizeof(buf),
+                          "kv %s has=%d i64=%lld f64=%.17g str=%s bool=%d nstr=%zu nf32=%zu "
+                          "hf32=%llu\n",
+                          k.c_str(), (int)g.has(k), (long long)g.get_i64(k, -7),
+                          g.get_f64(k, -7.0), g.get_str(k, "-").c_str(), (int)g.get_bool(k, false),
+                          g.get_str_arr(k).size(), f.size(),
+                          hash((const uint8_t*)f.data(), f.size() * 4));
+            s += buf;
+        }
+        std::vector<std::string> names;
+        for (const auto& kv : g.tensors()) names.push_back(kv.first);
+        std::sort(names.begin(), names.end());
+        for (const std::string& n : names) {
+            const HostTensor& t = *g.tensor(n);
+            std::snprintf(buf, sizeof(buf),
+                          "tensor %s n_dims=%d ne=%lld,%lld,%lld,%lld dtype=%d nbytes=%zu "
+                          "hash=%llu\n",
+                          n.c_str(), t.n_dims, (long long)t.ne[0], (long long)t.ne[1],
+                          (long long)t.ne[2], (long long)t.ne[3], (int)t.dtype, t.nbytes,
+                          hash(t.data, t.nbytes));
+            s += buf;
+        }
+        rc = (int64_t)s.size();
+    } catch (const std::exception& e) {
+        s = e.what();
+        rc = -1;
+    }
+    if (cap > 0) {
+        const size_t n = std::min<size_t>(s.size(), (size_t)cap - 1);
+        std::memcpy(out, s.data(), n);
+        out[n] = 0;
+    }
+    return rc;
 }
 
 }  // extern "C"

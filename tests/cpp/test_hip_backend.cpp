@@ -15,6 +15,7 @@
 #include <vector>
 
 #include "../../oracle/ftx_oracle.h"
+#include "../../xwfes_amd/host/gguf.hpp"
 #include "../../xwfes_amd/host/hip_backend.hpp"
 
 using namespace ftx_host;
@@ -327,8 +328,78 @@ static void test_verifier(HipBackend& be) {
     }
 }
 
-int main() {
+// a GGUF model through the C++ loader: Gguf -> config_from_gguf ->
+// weights_from_gguf -> HipVerifier, a chain verify against the oracle run on
+// the same mapped bytes
+static void test_gguf_verifier(HipBackend& be, const char* path) {
+    Gguf g(path);
+    GgufConfig gc = config_from_gguf(g);
+    ModelConfig& c = gc.cfg;
+    ModelWeights w = weights_from_gguf(g, c);
+    CHECK(c.n_ff == w.layers[0][6].rows(), "n_ff from the gate rows");
+    const int64_t cap = 64, npast = 9, M = 5;
+    const int64_t kdim = c.n_head_kv * c.head_dim;
+    {
+    HipVerifier ver(be, c, w, cap, 8);
+    std::vector<uint16_t> kc((size_t)(c.n_layer * cap * kdim)), vc(kc.size());
+    for (auto& v : kc) v = orc_float_to_half(rnd());
+    for (auto& v : vc) v = orc_float_to_half(rnd());
+    ver.write_kv(kc.data(), vc.data());
+    ver.truncate_to(npast);
+    auto ot = [](const HostTensor& t) {
+        orc_tensor o{};
+        o.data = t.data;
+        o.dtype = (int32_t)t.dtype;
+        o.ne0 = t.ne[0];
+        o.ne1 = t.ne[1];
+        return o;
+    };
+    std::vector<orc_tensor> ol;
+    for (const auto& L : w.layers)
+        for (const auto& t : L) ol.push_back(ot(t));
+    orc_model om{};
+    om.n_layer = c.n_layer;
+    om.n_embd = c.n_embd;
+    om.n_head = c.n_head;
+    om.n_head_kv = c.n_head_kv;
+    om.head_dim = c.head_dim;
+    om.n_ff = c.n_ff;
+    om.vocab = c.vocab;
+    om.rms_eps = c.rms_eps;
+    om.rope_neox = c.rope_neox ? 1 : 0;
+    om.rope_theta = c.rope_theta;
+    om.tok_embd = ot(w.tok_embd);
+    om.out_norm = ot(w.out_norm);
+    om.output = ot(w.output);
+    om.layers = ol.data();
+    const std::vector<int32_t> toks = {1, (int32_t)c.vocab - 1, 7, 0, 3};
+    const float* dev = ver.extend_verify(toks);
+    std::vector<float> got((size_t)(M * c.vocab)), want(got.size());
+    be.stage(got.data(), dev, got.size() * sizeof(float));
+    std::vector<uint16_t> k2 = kc, v2 = vc;
+    CHECK(orc_forward(&om, k2.data(), v2.data(), ORC_KV_F16, cap, npast, toks.data(), M, nullptr,
+                      0, want.data()) == 0,
+          "oracle forward of the GGUF model");
+    CHECK(rel_err(got.data(), want.data(), M, c.vocab) < 1e-3, "GGUF model logits");
+    std::printf("gguf model %s: %lld layers, d %lld, vocab %lld verified\n", path,
+                (long long)c.n_layer, (long long)c.n_embd, (long long)c.vocab);
+    }
+    // the resident copies are keyed by host address: drop them before the
+    // mapping goes away (the verifier, which reads them, is gone already)
+    for (const auto& L : w.layers)
+        for (const auto& t : L) be.evict(t);
+    be.evict(w.tok_embd);
+    be.evict(w.out_norm);
+    be.evict(w.output);
+}
+
+int main(int argc, char** argv) {
     HipBackend be(0);
+    if (argc > 2 && !std::strcmp(argv[1], "--gguf")) {
+        for (int i = 2; i < argc; ++i) test_gguf_verifier(be, argv[i]);
+        std::printf("test_hip_backend: all %d checks passed\n", g_checks);
+        return 0;
+    }
     test_backend_info(be);
     test_matmul(be);
     test_expert_chunk(be);

@@ -328,6 +328,9 @@ class Context:
 class Model:
     def __init__(self, ctx, handle, cfg, tensors):
         self.ctx, self.handle, self.cfg, self.tensors = ctx, handle, cfg, tensors
+        # tensors the model owns (freed with it); the device model reads its
+        # tensors for its whole life, so the caller's stay alive until free()
+        self.owned = []
 
     def kv(self, cap, kv_dtype=KV_F16):
         h = _vp()
@@ -348,6 +351,9 @@ class Model:
         if self.handle:
             self.ctx.lib.ftx_model_free(self.handle)
             self.handle = None
+        for t in self.owned:
+            t.free()
+        self.owned = []
 
 
 class KV:
