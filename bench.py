@@ -24,12 +24,18 @@ sys.path.insert(0, ROOT)
 
 HBM_PEAK_GBS = 8000.0
 REPLAY = 20  # back-to-back issues of each dominant-class launch when timing it
+LLAMA3_8B = dict(n_layer=32, n_embd=4096, n_head=32, n_head_kv=8, head_dim=128, n_ff=14336,
+                vocab=128256, rope_theta=500000.0, rope_neox=0, rms_eps=1e-5)
 WORKLOADS = {
-    # name: (model cfg, mix, context, draft length, acceptance temperature)
-    "llama3-8b-q4km-k8-ctx2048": dict(
-        cfg=dict(n_layer=32, n_embd=4096, n_head=32, n_head_kv=8, head_dim=128, n_ff=14336,
-                 vocab=128256, rope_theta=500000.0, rope_neox=0, rms_eps=1e-5),
-        mix="q4_k_m", ctx=2048, M=8, temp=0.8),
+    # kind verify: one verify step (M draft tokens at context ctx) plus ratio
+    # acceptance; decode: one Engine::step at context ctx; prefill: P prompt
+    # tokens from an empty cache in advancing chains of M
+    "llama3-8b-q4km-k8-ctx2048": dict(kind="verify", cfg=LLAMA3_8B, mix="q4_k_m", ctx=2048, M=8,
+                                      temp=0.8),
+    "llama3-8b-q4km-decode-ctx2048": dict(kind="decode", cfg=LLAMA3_8B, mix="q4_k_m", ctx=2048,
+                                          M=1, temp=0.8),
+    "llama3-8b-q4km-prefill-512": dict(kind="prefill", cfg=LLAMA3_8B, mix="q4_k_m", ctx=0, M=8,
+                                       P=512, temp=0.8),
 }
 
 
@@ -62,6 +68,21 @@ def step_bytes(tensors, cfg, ctx_len, M):
     kv = 2 * L * (ctx_len + M) * kdim * 2
     logits = M * V * 4
     return w + emb + kv + logits
+
+
+def prefill_bytes(tensors, cfg, P, chunk):
+    """Algorithmic HBM bytes of a P-token prefill in chains of `chunk`: each
+    chain a verify step at its context, the LM head and its logits only on
+    the last chain."""
+    head = tensors["output"].nbytes if "output" in tensors else tensors["tok_embd"].nbytes
+    total, n = 0, 0
+    for s0 in range(0, P, chunk):
+        m = min(chunk, P - s0)
+        total += step_bytes(tensors, cfg, s0, m)
+        n += 1
+        if s0 + chunk < P:
+            total -= head + m * cfg["vocab"] * 4
+    return total
 
 
 def cpu_baseline(ctx, tensors, cfg, ctx_len, M, props, threads):
@@ -153,29 +174,40 @@ def main():
     tensors = synth.build(ctx, cfg, synth.q4_k_m_mix(cfg), seed=1)
     log("model built in %.1f s (%.3f GB of weights)" % (time.perf_counter() - t0,
                                                         synth.weight_bytes(tensors) / 1e9))
+    kind = W["kind"]
+    P_tok = W.get("P", 0)
     model = ctx.model(cfg, tensors, max_tokens=M)
-    kv = model.kv(ctx_len + M + 8)
+    kv = model.kv(max(ctx_len, P_tok) + M + 8)
     kp, vp, _ = kv.pointers()
     n_kv = cfg["n_layer"] * kv.cap_alloc * cfg["n_head_kv"] * cfg["head_dim"]
     ctx.fill_normal(kp, n_kv, seed=4, std=1.0, dtype=ftx.F16)
     ctx.fill_normal(vp, n_kv, seed=5, std=1.0, dtype=ftx.F16)
     logits = ctx.buffer(M * V * 4)
     base = ctx.buffer(V * 4)
-    # the base row: logits of the last committed token (position ctx - 1)
-    kv.truncate(ctx_len - 1)
-    model.verify(kv, [int(np.random.default_rng(3).integers(V))], base.ptr, advance=True)
-    ctx.sync()
+    if kind == "verify":
+        # the base row: logits of the last committed token (position ctx - 1)
+        kv.truncate(ctx_len - 1)
+        model.verify(kv, [int(np.random.default_rng(3).integers(V))], base.ptr, advance=True)
+        ctx.sync()
     props, pd = draft(V, M, seed=6)
+    prompt = [int(t) for t in np.random.default_rng(8).integers(0, V, P_tok)]
     rng_state = [5]
     accepted = []
 
     def step():
-        kv.truncate(ctx_len)
-        model.verify(kv, props, logits.ptr)
-        r = ctx.accept(base.ptr, logits.ptr, M, V, props, ftx.ACCEPT_RATIO, temp=temp,
-                       rng=rng_state[0], pd=pd)
-        rng_state[0] = r["rng"]
-        accepted.append(len(r["accepted"]))
+        if kind == "verify":
+            kv.truncate(ctx_len)
+            model.verify(kv, props, logits.ptr)
+            r = ctx.accept(base.ptr, logits.ptr, M, V, props, ftx.ACCEPT_RATIO, temp=temp,
+                           rng=rng_state[0], pd=pd)
+            rng_state[0] = r["rng"]
+            accepted.append(len(r["accepted"]))
+        elif kind == "decode":
+            kv.truncate(ctx_len)
+            model.step(kv, int(props[0]), logits.ptr)
+        else:
+            kv.truncate(0)
+            model.prefill(kv, prompt, logits.ptr, chunk=M)
 
     for _ in range(args.warmup):
         step()
@@ -222,12 +254,24 @@ def main():
             name, e["launches"] // args.trace_steps, e["ms"] / args.trace_steps,
             e["bytes"] / (e["ms"] * 1e-3) / 1e9 if e["ms"] > 0 else 0.0))
 
-    sb = step_bytes(tensors, cfg, ctx_len, M)
+    if kind == "prefill":
+        sb = prefill_bytes(tensors, cfg, P_tok, M)
+        tokens = P_tok
+    else:
+        sb = step_bytes(tensors, cfg, ctx_len, M)
+        tokens = M
     gbs = sb / (ms_step * 1e-3) / 1e9
+    metric = {"verify": "verify-step tokens/s + HBM GB/s (% of peak), 8B-shape Q4_K, K=8 draft, "
+                        "1 GPU",
+              "decode": "decode tokens/s (Engine::step, M=1, ctx 2048), 8B-shape Q4_K, 1 GPU",
+              "prefill": "prefill tokens/s (512-token prompt, chains of 8), 8B-shape Q4_K, "
+                         "1 GPU"}[kind]
+    unit = {"verify": "verified tokens/s", "decode": "decoded tokens/s",
+            "prefill": "prefilled tokens/s"}[kind]
     out = {
-        "metric": "verify-step tokens/s + HBM GB/s (% of peak), 8B-shape Q4_K, K=8 draft, 1 GPU",
-        "value": round(M / (ms_step * 1e-3), 2),
-        "unit": "verified tokens/s",
+        "metric": metric,
+        "value": round(tokens / (ms_step * 1e-3), 2),
+        "unit": unit,
         "n_gpus": 1, "steps": args.steps, "warmup": args.warmup,
         "ms_per_step": round(ms_step, 4),
         "ms_per_step_median": round(med_ms, 4),
@@ -235,14 +279,16 @@ def main():
         "dtype": "q4_k/q6_k weights, f16 KV, fp32 accumulate",
         "data": "synthetic: random-init N(0,0.02) weights quantised on device, N(0,1) fp16 KV, "
                 "Dirichlet(1) draft",
-        "config": {"workload": args.workload, "M": M, "ctx": ctx_len, "layers": cfg["n_layer"],
-                   "d_model": cfg["n_embd"], "vocab": V, "mix": W["mix"], "accept": "ratio",
+        "config": {"workload": args.workload, "kind": kind, "M": M, "ctx": ctx_len,
+                   "prompt": P_tok, "layers": cfg["n_layer"], "d_model": cfg["n_embd"],
+                   "vocab": V, "mix": W["mix"], "accept": "ratio" if kind == "verify" else None,
                    "temperature": temp, "batch": 1},
         "step_bytes": sb,
         "hbm_gbs": round(gbs, 1),
         "hbm_frac": round(gbs / HBM_PEAK_GBS, 4),
-        "committed_tokens_per_s": round((statistics.mean(accepted) + 1) / (ms_step * 1e-3), 2),
-        "mean_accepted": round(statistics.mean(accepted), 3),
+        "committed_tokens_per_s": (round((statistics.mean(accepted) + 1) / (ms_step * 1e-3), 2)
+                                   if accepted else None),
+        "mean_accepted": round(statistics.mean(accepted), 3) if accepted else None,
         "traced_device_ms_per_step": round(traced_ms, 4),
         "roofline": {"bound": "hbm", "kernel": dom_name, "achieved": round(achieved, 1),
                      "peak": HBM_PEAK_GBS, "unit": "GB/s",
@@ -252,7 +298,7 @@ def main():
                      "traffic": measured_traffic(args.workload, dom_name)},
         "cpu_baseline": None,
     }
-    if not args.no_cpu_baseline:
+    if not args.no_cpu_baseline and kind == "verify":
         threads = min(16, os.cpu_count() or 1)
         t0 = time.perf_counter()
         out["cpu_baseline"] = cpu_baseline(ctx, tensors, cfg, ctx_len, M, props, threads)

@@ -221,13 +221,15 @@ typedef struct {
     int64_t M;               /* tokens verified in this step */
     const int32_t* tokens;   /* host [M] */
     const int32_t* parents;  /* host [M], parents[i] in {-1, 0..i-1}; NULL = chain */
-    float* logits;           /* device [M][vocab] */
+    float* logits;           /* device [M][vocab]; NULL skips the LM head (prefill chunks) */
     int32_t advance;         /* 1: npast += M afterwards (chain extend_verify) */
     int32_t pad_;
 } ftx_verify_args;
 /* Forward of M draft tokens against the committed context: node i sits at
  * position npast + depth(i), is written to KV slot npast + i, attends to the
- * context plus its ancestors and itself. */
+ * context plus its ancestors and itself.  Engine::step (src/engine.cpp:650-
+ * 658) is M = 1 with advance = 1; Engine::prefill (598-648, without its
+ * prefix cache) is a sequence of advancing chains, the last with logits. */
 int ftx_verify_step(ftx_ctx* ctx, ftx_model* m, ftx_kv* kv, const ftx_verify_args* a);
 
 typedef struct {

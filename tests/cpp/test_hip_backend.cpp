@@ -381,6 +381,29 @@ static void test_gguf_verifier(HipBackend& be, const char* path) {
                       0, want.data()) == 0,
           "oracle forward of the GGUF model");
     CHECK(rel_err(got.data(), want.data(), M, c.vocab) < 1e-3, "GGUF model logits");
+    // Engine::prefill + Engine::step from an empty cache: 13 prompt tokens in
+    // chains of 8 (+5), then one step, against the forward of all 14
+    {
+        std::vector<int32_t> prompt;
+        for (int i = 0; i < 13; ++i) prompt.push_back((int32_t)((i * 37 + 5) % c.vocab));
+        const int32_t nxt = (int32_t)(c.vocab / 2);
+        ver.truncate_to(0);
+        const float* pl = ver.prefill(prompt, 8);
+        std::vector<float> gp((size_t)(5 * c.vocab)), gs((size_t)c.vocab);
+        be.stage(gp.data(), pl, gp.size() * sizeof(float));
+        const float* sl = ver.step(nxt);
+        be.stage(gs.data(), sl, gs.size() * sizeof(float));
+        CHECK(ver.npast() == 14, "prefill + step advance the cache");
+        std::vector<int32_t> all = prompt;
+        all.push_back(nxt);
+        std::vector<float> w14((size_t)(14 * c.vocab));
+        std::vector<uint16_t> k3(kc.size(), 0), v3(vc.size(), 0);
+        CHECK(orc_forward(&om, k3.data(), v3.data(), ORC_KV_F16, cap, 0, all.data(), 14, nullptr,
+                          0, w14.data()) == 0,
+              "oracle forward of prompt + step");
+        CHECK(rel_err(gp.data(), w14.data() + 8 * c.vocab, 5, c.vocab) < 1e-3, "prefill logits");
+        CHECK(rel_err(gs.data(), w14.data() + 13 * c.vocab, 1, c.vocab) < 1e-3, "step logits");
+    }
     std::printf("gguf model %s: %lld layers, d %lld, vocab %lld verified\n", path,
                 (long long)c.n_layer, (long long)c.n_embd, (long long)c.vocab);
     }

@@ -365,7 +365,7 @@ int ftx_kv_commit(ftx_kv* kv, const int32_t* nodes, int64_t n) {
 }
 
 int ftx_verify_step(ftx_ctx* ctx, ftx_model* m, ftx_kv* kv, const ftx_verify_args* a) {
-    if (!ctx || !m || !kv || !a || !a->tokens || !a->logits)
+    if (!ctx || !m || !kv || !a || !a->tokens)
         return ftx_fail(ctx, FTX_E_INVALID, "null argument");
     const ftx_model_desc& d = m->d;
     const int64_t M = a->M;
@@ -597,12 +597,16 @@ int ftx_verify_step(ftx_ctx* ctx, ftx_model* m, ftx_kv* kv, const ftx_verify_arg
                    launch_down(st, T[FTX_T_DOWN]->data, T[FTX_T_DOWN]->dtype,
                                T[FTX_T_DOWN]->row_bytes, F, D, m->h, F, M, m->x, D, m->part));
     }
-    const ftx_tensor* lm = d.output ? d.output : d.tok_embd;
-    GemvSeg hs = seg(lm, a->logits, V);
-    rc = project(TK_HEAD, wbytes(lm) + Md * D * f4 + Md * V * f4, m->x, D,
-                 m->norms + (d.n_layer * 2) * D, &lm, &hs, 1, D, EPI_STORE,
-                 d.n_layer * FTX_LAYER_TENSORS, ix_head);
-    if (rc) return rc;
+    // the LM head (skipped without a logits buffer: every layer's K / V rows
+    // are written by now, which is all a prefill chunk needs)
+    if (a->logits) {
+        const ftx_tensor* lm = d.output ? d.output : d.tok_embd;
+        GemvSeg hs = seg(lm, a->logits, V);
+        rc = project(TK_HEAD, wbytes(lm) + Md * D * f4 + Md * V * f4, m->x, D,
+                     m->norms + (d.n_layer * 2) * D, &lm, &hs, 1, D, EPI_STORE,
+                     d.n_layer * FTX_LAYER_TENSORS, ix_head);
+        if (rc) return rc;
+    }
 #undef TRACED
     if (a->advance) kv->npast = npast + M;
     return FTX_OK;

@@ -347,6 +347,27 @@ class Model:
         self.ctx.check(self.ctx.lib.ftx_verify_step(self.ctx.h, self.handle, kv.handle,
                                                     C.byref(a)))
 
+    def step(self, kv, token, logits_ptr):
+        """Engine::step (src/engine.cpp:650-658): `token` at the committed
+        position, its logits row (vocab floats) into logits_ptr, the cache
+        one longer."""
+        self.verify(kv, [token], logits_ptr, advance=True)
+
+    def prefill(self, kv, tokens, logits_ptr=None, chunk=8):
+        """Engine::prefill (src/engine.cpp:598-648, without its prefix
+        cache): `tokens` through the model in advancing chains of at most
+        `chunk` (the fast path's width); only the last chain runs the LM
+        head, and logits_ptr (its len * vocab floats; None: no logits)
+        receives its rows.  Returns the number of rows written there."""
+        n = len(tokens)
+        if n == 0:
+            return 0
+        for i in range(0, n, chunk):
+            part = tokens[i:i + chunk]
+            last = i + chunk >= n
+            self.verify(kv, part, logits_ptr if last else None, advance=True)
+        return len(tokens[(n - 1) // chunk * chunk:])
+
     def free(self):
         if self.handle:
             self.ctx.lib.ftx_model_free(self.handle)

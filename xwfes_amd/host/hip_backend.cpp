@@ -1,6 +1,8 @@
 // hip_backend.cpp -- HipBackend / HipVerifier over the C ABI (include/ftx.h).
 #include "hip_backend.hpp"
 
+#include <algorithm>
+
 #include <stdexcept>
 
 namespace ftx_host {
@@ -166,6 +168,26 @@ const float* HipVerifier::extend_verify(const std::vector<int32_t>& props,
     a.logits = logits_;
     a.advance = advance ? 1 : 0;
     be_.check(ftx_verify_step(be_.ctx(), model_, kv_, &a), "verify_step");
+    return logits_;
+}
+
+const float* HipVerifier::step(int32_t token) {
+    return extend_verify({token}, {}, true);
+}
+
+const float* HipVerifier::prefill(const std::vector<int32_t>& tokens, int64_t chunk) {
+    if (tokens.empty()) return nullptr;
+    if (chunk < 1 || chunk > max_tokens_) throw std::runtime_error("HipVerifier: bad prefill chunk");
+    const int64_t n = (int64_t)tokens.size();
+    for (int64_t i = 0; i < n; i += chunk) {
+        const int64_t m = std::min(chunk, n - i);
+        ftx_verify_args a{};
+        a.M = m;
+        a.tokens = tokens.data() + i;
+        a.logits = i + chunk >= n ? logits_ : nullptr;  // the LM head on the last chain only
+        a.advance = 1;
+        be_.check(ftx_verify_step(be_.ctx(), model_, kv_, &a), "prefill");
+    }
     return logits_;
 }
 

@@ -163,6 +163,14 @@ public:
     // device logits [M][vocab], valid until the next call
     const float* extend_verify(const std::vector<int32_t>& props,
                                const std::vector<int32_t>& parents = {}, bool advance = false);
+    // Engine::step (src/engine.cpp:650-658): one token at the committed
+    // position; returns its device logits row, the cache one longer
+    const float* step(int32_t token);
+    // Engine::prefill (src/engine.cpp:598-648, without the prefix cache): the
+    // tokens in advancing chains of at most `chunk`, the LM head only on the
+    // last; returns the device logits of that last chain (rows [0, n % chunk
+    // or chunk)), valid until the next call
+    const float* prefill(const std::vector<int32_t>& tokens, int64_t chunk = 8);
     void truncate_to(int64_t npast);
     // keep the accepted path nodes (node ids of the last extend_verify, root
     // first) as the next committed positions; a chain is truncate_to
