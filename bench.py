@@ -191,7 +191,7 @@ def main():
         ctx.sync()
     props, pd = draft(V, M, seed=6)
     prompt = [int(t) for t in np.random.default_rng(8).integers(0, V, P_tok)]
-    rng_state = [5]
+    rng_state = [5, ftx.SAMPLER_SEED]
     accepted = []
 
     def step():
@@ -199,8 +199,8 @@ def main():
             kv.truncate(ctx_len)
             model.verify(kv, props, logits.ptr)
             r = ctx.accept(base.ptr, logits.ptr, M, V, props, ftx.ACCEPT_RATIO, temp=temp,
-                           rng=rng_state[0], pd=pd)
-            rng_state[0] = r["rng"]
+                           rng=rng_state[0], pd=pd, sampler_state=rng_state[1])
+            rng_state[0], rng_state[1] = r["rng"], r["sampler_state"]
             accepted.append(len(r["accepted"]))
         elif kind == "decode":
             kv.truncate(ctx_len)

@@ -247,7 +247,18 @@ typedef struct {
     int32_t* n_acc;         /* host out */
     int32_t* bonus;         /* host out: next token */
     float* margin;          /* host out: min |u - ratio| over decisions, or NULL */
+    /* RATIO bonus token: Sampler::sample (include/ft/sampler.h:30-94) at
+     * temp with top_k (1..64; <= 0 or >= V: off) and top_p (>= 1: off) from
+     * the sampler's own SplitMix64 state (host, in/out; the reference starts
+     * it at 0x9E3779B97F4A7C15 and carries it over between draws) */
+    uint64_t* sampler_rng;
+    int32_t top_k;
+    float top_p;
 } ftx_accept_args;
+/* Acceptance of a verified draft (GREEDY: argmax tests, chain or tree, bonus
+ * = argmax; RATIO: accept_chain_sampling's test from the rng stream, bonus by
+ * the sampler; RESIDUAL: multi-candidate speculative sampling, bonus from the
+ * residual distribution with one more uniform of the rng stream). */
 int ftx_accept(ftx_ctx* ctx, const ftx_accept_args* a);
 
 /* ---- kernel trace (the reference keeps wall-clock RunStats only,

@@ -92,6 +92,97 @@ int32_t orc_sample_weights(const double* w, int64_t V, float u) {
     return last;
 }
 
+/* Sampler::sample (include/ft/sampler.h:30-94): temp <= 0 -> first-max
+ * argmax; else p_i = expf((l_i - max) / T) in float, their double sum,
+ * p_i = (float)(p_i / sum); top-k (0 < k < n): the k largest p (ties: lower
+ * index first, the reference's partial_sort leaves tie order unspecified),
+ * renormalised by their float sum taken in that order; top-p (p < 1): all p
+ * in descending order (same ties), double cumulative sum cut at the first
+ * cum >= top_p, the rest zeroed and its double sum `tail` divided out of the
+ * kept (when tail > 0); then r = next_float() and the first i in index order
+ * whose running double sum, as float, reaches r; none: argmax.  The state
+ * carries over between calls (the reference re-seeds on every call when its
+ * seed is non-zero, which makes every draw the same; with seed 0 its state
+ * carries over in the same way).  next_float: SplitMix64 step, bits 24..47
+ * of the output as a 24-bit fraction (sampler.h:84-92). */
+static float sampler_next_float(uint64_t* st) {
+    *st += 0x9E3779B97F4A7C15ull;
+    uint64_t z = *st;
+    z = (z ^ (z >> 30)) * 0xBF58476D1CE4E5B9ull;
+    z = (z ^ (z >> 27)) * 0x94D049BB133111EBull;
+    const uint32_t u = (uint32_t)((z ^ (z >> 31)) >> 16);
+    return (float)(u >> 8) * (1.f / 16777216.f);
+}
+
+static const float* g_sort_p;
+static int by_prob_desc(const void* a, const void* b) {
+    const int32_t i = *(const int32_t*)a, j = *(const int32_t*)b;
+    const float pi = g_sort_p[i], pj = g_sort_p[j];
+    if (pi > pj) return -1;
+    if (pi < pj) return 1;
+    return i < j ? -1 : (i > j);
+}
+
+int32_t orc_sampler_sample(const float* lg, int64_t n, float temp, int32_t top_k, float top_p,
+                           uint64_t* state) {
+    if (temp <= 0.f) return orc_argmax(lg, n);
+    float* probs = (float*)malloc((size_t)n * sizeof(float));
+    int32_t* idx = (int32_t*)malloc((size_t)n * sizeof(int32_t));
+    float mx = lg[0];
+    for (int64_t i = 1; i < n; ++i) mx = lg[i] > mx ? lg[i] : mx;
+    double sum = 0;
+    for (int64_t i = 0; i < n; ++i) {
+        probs[i] = expf((lg[i] - mx) / temp);
+        sum += probs[i];
+    }
+    for (int64_t i = 0; i < n; ++i) probs[i] = (float)(probs[i] / sum);
+    if (top_k > 0 && top_k < n) {
+        for (int64_t i = 0; i < n; ++i) idx[i] = (int32_t)i;
+        g_sort_p = probs;
+        qsort(idx, (size_t)n, sizeof(int32_t), by_prob_desc);
+        float keep = 0;
+        for (int32_t i = 0; i < top_k; ++i) keep += probs[idx[i]];
+        float* filt = (float*)calloc((size_t)n, sizeof(float));
+        for (int32_t i = 0; i < top_k; ++i) filt[idx[i]] = probs[idx[i]] / keep;
+        memcpy(probs, filt, (size_t)n * sizeof(float));
+        free(filt);
+    }
+    if (top_p < 1.f) {
+        for (int64_t i = 0; i < n; ++i) idx[i] = (int32_t)i;
+        g_sort_p = probs;
+        qsort(idx, (size_t)n, sizeof(int32_t), by_prob_desc);
+        double cum = 0;
+        int64_t cut = n;
+        for (int64_t i = 0; i < n; ++i) {
+            cum += probs[idx[i]];
+            if (cum >= top_p) {
+                cut = i + 1;
+                break;
+            }
+        }
+        double tail = 0;
+        for (int64_t i = cut; i < n; ++i) {
+            tail += probs[idx[i]];
+            probs[idx[i]] = 0;
+        }
+        if (tail > 0 && cut > 0)
+            for (int64_t i = 0; i < cut; ++i) probs[idx[i]] = (float)(probs[idx[i]] / (1.0 - tail));
+    }
+    const float r = sampler_next_float(state);
+    double c = 0;
+    int32_t pick = -1;
+    for (int64_t i = 0; i < n; ++i) {
+        c += probs[i];
+        if ((float)c >= r) {
+            pick = (int32_t)i;
+            break;
+        }
+    }
+    free(probs);
+    free(idx);
+    return pick >= 0 ? pick : orc_argmax(lg, n);
+}
+
 /* normalised target distribution p_T of a logits row, in double */
 static void target_dist(const float* lg, int64_t V, float temp, double* p) {
     float mx = lg[0];
@@ -125,8 +216,8 @@ static void target_dist(const float* lg, int64_t V, float temp, double* p) {
 int orc_verify_accept(const float* base_row, const float* rows, int64_t M,
                       int64_t V, const int32_t* props, const int32_t* parents,
                       const float* pd, const float* q, int mode, float temp,
-                      uint64_t* rng, int32_t* accepted, int32_t* n_acc,
-                      int32_t* bonus, float* margin) {
+                      uint64_t* rng, uint64_t* sampler_state, int32_t top_k, float top_p,
+                      int32_t* accepted, int32_t* n_acc, int32_t* bonus, float* margin) {
     if (M < 0 || V <= 0) return -1;
     for (int64_t i = 0; i < M; ++i) {
         int32_t pa = parents ? parents[i] : (int32_t)i - 1;
@@ -167,10 +258,9 @@ int orc_verify_accept(const float* base_row, const float* rows, int64_t M,
         }
         for (int i = 0; i < a; ++i) accepted[na++] = i;
         cur = a - 1;
-        double* p = (double*)malloc((size_t)V * sizeof(double));
-        target_dist(ROW(cur), V, temp, p);
-        *bonus = orc_sample_weights(p, V, orc_rng_float(rng));
-        free(p);
+        /* the bonus: Sampler::sample of the row after the last accepted node
+         * (generate, src/spec.cpp:309-311, with the row fixed) */
+        *bonus = orc_sampler_sample(ROW(cur), V, temp, top_k, top_p, sampler_state);
     } else if (mode == ORC_ACCEPT_RESIDUAL) {
         double* p = (double*)malloc((size_t)V * sizeof(double));
         for (;;) {

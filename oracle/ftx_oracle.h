@@ -21,6 +21,8 @@
  *   - generate() samples the bonus token from rows[min(acc,k-1)]
  *     (src/spec.cpp:309-311); orc_verify_accept samples it from the row that
  *     follows the last accepted node.
+ *   - Sampler::sample re-seeds on every call when its seed is non-zero
+ *     (include/ft/sampler.h:31); orc_sampler_sample carries the state over.
  */
 #ifndef FTX_ORACLE_H
 #define FTX_ORACLE_H
@@ -158,8 +160,13 @@ int32_t orc_sample_weights(const double* w, int64_t V, float u);
 int orc_verify_accept(const float* base_row, const float* rows, int64_t M,
                       int64_t V, const int32_t* props, const int32_t* parents,
                       const float* pd, const float* q, int mode, float temp,
-                      uint64_t* rng, int32_t* accepted, int32_t* n_acc,
-                      int32_t* bonus, float* margin);
+                      uint64_t* rng, uint64_t* sampler_state, int32_t top_k, float top_p,
+                      int32_t* accepted, int32_t* n_acc, int32_t* bonus, float* margin);
+
+/* Sampler::sample (include/ft/sampler.h:30-94) with its state carried over
+ * between calls; top_k <= 0 or >= n and top_p >= 1 switch the filters off. */
+int32_t orc_sampler_sample(const float* lg, int64_t n, float temp, int32_t top_k, float top_p,
+                           uint64_t* state);
 
 #ifdef __cplusplus
 }

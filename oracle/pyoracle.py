@@ -15,6 +15,8 @@ LIB_PATH = os.path.join(HERE, "liboracle.so")
 REF_PATH = os.path.join(HERE, "_ref", "libftref.so")
 
 F32, F16, Q4_0, Q4_1, Q8_0, Q4_K, Q6_K, BF16 = 0, 1, 2, 3, 8, 12, 14, 30
+# the Sampler's state for seed 0 (include/ft/sampler.h:19)
+SAMPLER_SEED = 0x9E3779B97F4A7C15
 BLOCK = {F32: (1, 4), F16: (1, 2), BF16: (1, 2), Q4_0: (32, 18), Q4_1: (32, 20),
          Q8_0: (32, 34), Q4_K: (256, 144), Q6_K: (256, 210)}
 ACCEPT_GREEDY, ACCEPT_RATIO, ACCEPT_RESIDUAL = 0, 1, 2
@@ -100,7 +102,12 @@ class Oracle:
         L.orc_sample_weights.restype = C.c_int32
         L.orc_sample_weights.argtypes = [_dp, C.c_int64, C.c_float]
         L.orc_verify_accept.argtypes = [_fp, _fp, C.c_int64, C.c_int64, _i32p, _i32p, _fp, _fp,
-                                        C.c_int, C.c_float, _u64p, _i32p, _i32p, _i32p, _fp]
+                                        C.c_int, C.c_float, C.POINTER(C.c_uint64),
+                                        C.POINTER(C.c_uint64), C.c_int32, C.c_float, _i32p,
+                                        _i32p, _i32p, _fp]
+        L.orc_sampler_sample.restype = C.c_int32
+        L.orc_sampler_sample.argtypes = [_fp, C.c_int64, C.c_float, C.c_int32, C.c_float,
+                                         C.POINTER(C.c_uint64)]
 
     # ---- formats ----
     def half_to_float(self, h):
@@ -267,8 +274,15 @@ class Oracle:
         w = np.ascontiguousarray(w, np.float64)
         return self.lib.orc_sample_weights(_ptr(w, _dp), w.size, float(u))
 
+    def sampler_sample(self, logits, temp=0.7, top_k=40, top_p=0.95, state=SAMPLER_SEED):
+        """Sampler::sample (include/ft/sampler.h:30-94); returns (token, state)."""
+        lg = np.ascontiguousarray(logits, np.float32)
+        s = C.c_uint64(state)
+        t = self.lib.orc_sampler_sample(_ptr(lg, _fp), lg.size, temp, top_k, top_p, C.byref(s))
+        return t, s.value
+
     def verify_accept(self, base, rows, props, mode, temp=1.0, seed=0, parents=None, pd=None,
-                      q=None):
+                      q=None, sampler_state=None, top_k=40, top_p=0.95):
         base = np.ascontiguousarray(base, np.float32)
         rows = np.ascontiguousarray(rows, np.float32)
         props = np.ascontiguousarray(props, np.int32)
@@ -281,15 +295,16 @@ class Oracle:
         bonus = C.c_int32(0)
         mg = C.c_float(0)
         s = C.c_uint64(seed)
+        ss = C.c_uint64(SAMPLER_SEED if sampler_state is None else sampler_state)
         rc = self.lib.orc_verify_accept(
             _ptr(base, _fp), _ptr(rows, _fp), M, V, _ptr(props, _i32p),
             None if par is None else _ptr(par, _i32p),
             None if pdv is None else _ptr(pdv, _fp),
-            None if qv is None else _ptr(qv, _fp), mode, temp, C.byref(s),
-            _ptr(acc, _i32p), C.byref(na), C.byref(bonus), C.byref(mg))
+            None if qv is None else _ptr(qv, _fp), mode, temp, C.byref(s), C.byref(ss), top_k,
+            top_p, _ptr(acc, _i32p), C.byref(na), C.byref(bonus), C.byref(mg))
         assert rc == 0, "orc_verify_accept failed"
         return dict(accepted=acc[:na.value].tolist(), bonus=bonus.value, rng=s.value,
-                    margin=mg.value)
+                    sampler_state=ss.value, margin=mg.value)
 
 
 class Ref:
@@ -323,6 +338,9 @@ class Ref:
         L.ref_engine_vocab.restype = C.c_int64
         L.ref_engine_vocab.argtypes = [C.c_void_p]
         L.ref_engine_step.argtypes = [C.c_void_p, C.c_int32, _fp]
+        L.ref_sampler_sample.restype = C.c_int32
+        L.ref_sampler_sample.argtypes = [_fp, C.c_int64, C.c_float, C.c_int32, C.c_float,
+                                         C.POINTER(C.c_uint64)]
         L.ref_gguf_summary.restype = C.c_int64
         L.ref_gguf_summary.argtypes = [C.c_char_p, C.c_char_p, C.c_char_p, C.c_int64]
 
@@ -395,6 +413,14 @@ class Ref:
 
     def engine_free(self, h):
         self.lib.ref_engine_free(h)
+
+    def sampler_sample(self, logits, temp, top_k, top_p, state):
+        """The reference's Sampler::sample from `state` (seed 0 in the params,
+        so the state is used as it is); returns (token, state after)."""
+        lg = np.ascontiguousarray(logits, np.float32)
+        s = C.c_uint64(state)
+        t = self.lib.ref_sampler_sample(_ptr(lg, _fp), lg.size, temp, top_k, top_p, C.byref(s))
+        return t, s.value
 
     def gguf_summary(self, path, keys):
         """The reference parser's summary of a GGUF (see ref_harness.cpp),

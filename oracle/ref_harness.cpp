@@ -111,6 +111,24 @@ int ref_engine_step(void* h, int32_t tok, float* out) {
     }
 }
 
+// Sampler::sample (include/ft/sampler.h:30-94) from `state`: reset(state)
+// then sample with seed 0, which uses the state as it stands; the state after
+// one draw is state + the SplitMix64 increment (one next_u32), none at temp
+// <= 0 (argmax).
+int32_t ref_sampler_sample(const float* logits, int64_t n, float temp, int32_t top_k,
+                           float top_p, uint64_t* state) {
+    Sampler s;
+    s.reset(*state);
+    SampleParams p;
+    p.temp = temp;
+    p.top_k = top_k;
+    p.top_p = top_p;
+    p.seed = 0;
+    const int32_t t = s.sample(logits, n, p);
+    if (temp > 0.f) *state += 0x9E3779B97F4A7C15ull;
+    return t;
+}
+
 // The reference parser's view of a GGUF (ft::Gguf, config_from_gguf) in the
 // canonical summary form of xwfes_amd.gguf.summary(offsets=False): the
 // config, the typed accessors of `keys` ('\n'-separated, in order) and every

@@ -310,6 +310,7 @@ static void test_verifier(HipBackend& be) {
             const std::vector<float> pd = {0.3f, 0.5f, 0.9f, 0.2f, 0.6f, 0.7f};
             uint64_t s_gpu = 5, s_orc = 5;
             const bool ratio = mode == AcceptMode::Ratio;
+            uint64_t ss_orc = ver.sampler.state;
             Accepted a = ver.accept(dbase, dev, props, mode, 0.8f, s_gpu,
                                     ratio ? pd : std::vector<float>{});
             std::vector<int32_t> acc((size_t)M);
@@ -317,8 +318,10 @@ static void test_verifier(HipBackend& be) {
             float margin = 0.f;
             CHECK(orc_verify_accept(base.data(), got.data(), M, c.vocab, props.data(), nullptr,
                                     ratio ? pd.data() : nullptr, nullptr, (int)mode, 0.8f, &s_orc,
-                                    acc.data(), &n_acc, &bonus, &margin) == 0,
+                                    &ss_orc, ver.sampler.top_k, ver.sampler.top_p, acc.data(),
+                                    &n_acc, &bonus, &margin) == 0,
                   "oracle accept");
+            CHECK(ver.sampler.state == ss_orc, "sampler state matches the oracle");
             CHECK((int32_t)a.nodes.size() == n_acc, "accepted count matches the oracle");
             for (int32_t i = 0; i < n_acc; ++i) CHECK(a.nodes[(size_t)i] == acc[(size_t)i], "accepted ids");
             CHECK(a.bonus == bonus, "bonus token matches the oracle");

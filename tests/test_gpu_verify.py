@@ -392,7 +392,8 @@ def test_verify_errors(gctx, orc):
 
 # ---------------------------------------------------------------- acceptance
 
-def accept_both(gctx, orc, base, rows, props, mode, temp, seed, parents=None, pd=None, q=None):
+def accept_both(gctx, orc, base, rows, props, mode, temp, seed, parents=None, pd=None, q=None,
+                sampler_state=ftx.SAMPLER_SEED, top_k=40, top_p=0.95):
     M, V = rows.shape
     b = gctx.buffer((M + 1) * V * 4)
     b.write(np.ascontiguousarray(base, np.float32))
@@ -402,12 +403,13 @@ def accept_both(gctx, orc, base, rows, props, mode, temp, seed, parents=None, pd
         qb = gctx.buffer(M * V * 4)
         qb.write(np.ascontiguousarray(q, np.float32))
     g = gctx.accept(b.ptr, b.ptr + V * 4, M, V, props, mode, temp=temp, rng=seed,
-                    parents=parents, pd=pd, q_ptr=qb.ptr if qb else None)
+                    parents=parents, pd=pd, q_ptr=qb.ptr if qb else None,
+                    sampler_state=sampler_state, top_k=top_k, top_p=top_p)
     b.free()
     if qb:
         qb.free()
     o = orc.verify_accept(base, rows, props, mode, temp=temp, seed=seed, parents=parents, pd=pd,
-                          q=q)
+                          q=q, sampler_state=sampler_state, top_k=top_k, top_p=top_p)
     return g, o
 
 
@@ -456,7 +458,8 @@ def test_accept_ratio_chain(gctx, orc, V, temp):
         pd[rng.random(8) < 0.1] = 0.0
         seed = int(rng.integers(1, 2**63))
         g, o = accept_both(gctx, orc, base, rows, props, ftx.ACCEPT_RATIO, temp, seed, pd=pd)
-        assert (g["accepted"], g["bonus"], g["rng"]) == (o["accepted"], o["bonus"], o["rng"])
+        assert (g["accepted"], g["bonus"], g["rng"], g["sampler_state"]) == \
+            (o["accepted"], o["bonus"], o["rng"], o["sampler_state"])
 
 
 @pytest.mark.parametrize("V", [24, 32000])
@@ -472,7 +475,8 @@ def test_accept_residual_chain_and_tree(gctx, orc, V):
         seed = int(rng.integers(1, 2**63))
         g, o = accept_both(gctx, orc, base, rows, props, ftx.ACCEPT_RESIDUAL, 0.8, seed,
                            parents=parents, q=q)
-        assert (g["accepted"], g["bonus"], g["rng"]) == (o["accepted"], o["bonus"], o["rng"])
+        assert (g["accepted"], g["bonus"], g["rng"], g["sampler_state"]) == \
+            (o["accepted"], o["bonus"], o["rng"], o["sampler_state"])
 
 
 def test_accept_empty_draft(gctx, orc):
@@ -484,3 +488,47 @@ def test_accept_empty_draft(gctx, orc):
     g = gctx.accept(b.ptr, None, 0, 1000, [], ftx.ACCEPT_GREEDY)
     b.free()
     assert g["accepted"] == [] and g["bonus"] == int(np.argmax(base))
+
+
+# vocab sizes: 33 (no top-k: k >= V), 64, 1001 (a partial last sub-chunk),
+# 128256 (the 8B vocab), 262147 (more than 2048 sub-chunks)
+@pytest.mark.parametrize("V", [33, 64, 1001, 128256, 262147])
+def test_bonus_sampler(gctx, orc, V):
+    """The ratio-mode bonus is Sampler::sample (include/ft/sampler.h:30-94):
+    an empty draft draws it from the base row alone; token and sampler state
+    equal the oracle's over temperatures, top-k and top-p, the state carried
+    from draw to draw.  Rows with near-equal top logits (ties at the top-k
+    boundary after rounding) are part of the mix."""
+    rng = np.random.default_rng(V + 7)
+    state = ftx.SAMPLER_SEED
+    b = gctx.buffer(V * 4)
+    for trial in range(16 if V > 100000 else 40):
+        spread = float(rng.choice([0.5, 2.0, 8.0]))
+        base = (rng.standard_normal(V) * spread).astype(np.float32)
+        if trial % 5 == 4:
+            base[rng.integers(0, V, 6)] = base.max()  # equal maxima
+        temp = float(rng.choice([0.3, 0.7, 1.0, 1.6]))
+        top_k = int(rng.choice([1, 5, 40, 64])) if V > 64 else int(rng.choice([V, V + 5, 0]))
+        top_p = float(rng.choice([0.5, 0.9, 0.95, 1.0]))
+        b.write(base)
+        g = gctx.accept(b.ptr, None, 0, V, [], ftx.ACCEPT_RATIO, temp=temp, rng=3,
+                        sampler_state=state, top_k=top_k, top_p=top_p)
+        o = orc.verify_accept(base, base[None, :0].reshape(0, V), np.zeros(0, np.int32),
+                              P.ACCEPT_RATIO, temp=temp, seed=3, pd=np.zeros(0, np.float32),
+                              sampler_state=state, top_k=top_k, top_p=top_p)
+        assert (g["bonus"], g["sampler_state"]) == (o["bonus"], o["sampler_state"]), \
+            (trial, temp, top_k, top_p)
+        assert g["rng"] == 3 and g["accepted"] == []
+        state = g["sampler_state"]
+    b.free()
+
+
+def test_bonus_sampler_limits(gctx):
+    V = 1000
+    b = gctx.buffer(V * 4)
+    b.write(np.zeros(V, np.float32))
+    for top_k in (65, 0):  # top-k beyond 64, or none over more than 64 tokens
+        with pytest.raises(ftx.FtxError) as e:
+            gctx.accept(b.ptr, None, 0, V, [], ftx.ACCEPT_RATIO, temp=0.7, top_k=top_k)
+        assert e.value.code == -2
+    b.free()

@@ -93,11 +93,16 @@ def test_verify_ratio_equals_chain_sampling(orc):
         pd = (rng.random(6) * 0.3).astype(np.float32)
         seed = int(rng.integers(1, 2**63))
         a, s_after = orc.accept_chain_sampling(base, rows, pd, props, 0.8, seed)
-        r = orc.verify_accept(base, rows, props, P.ACCEPT_RATIO, temp=0.8, seed=seed, pd=pd)
+        ss = int(rng.integers(1, 2**63))
+        r = orc.verify_accept(base, rows, props, P.ACCEPT_RATIO, temp=0.8, seed=seed, pd=pd,
+                              sampler_state=ss)
         assert r["accepted"] == list(range(a))
-        # exactly one more uniform is drawn, for the bonus token
-        _, s_bonus = orc.rng_next(s_after)
-        assert r["rng"] == s_bonus
+        # the acceptance stream stops at the decisions (src/spec.cpp:214-238);
+        # the bonus is Sampler::sample of the row after the last accepted
+        # node, from the sampler's own state
+        assert r["rng"] == s_after
+        after = base if a == 0 else rows[a - 1]
+        assert (r["bonus"], r["sampler_state"]) == orc.sampler_sample(after, 0.8, 40, 0.95, ss)
 
 
 def test_residual_single_child_equals_ratio(orc):
@@ -186,3 +191,47 @@ def test_sample_weights(orc):
     assert orc.sample_weights(w, 0.2499) == 1
     assert orc.sample_weights(w, 0.25) == 3
     assert orc.sample_weights(w, 0.9999999) == 3
+
+
+@pytest.mark.parametrize("V", [7, 64, 1001, 32000])
+def test_sampler_sample_matches_reference(orc, ref, V):
+    """Sampler::sample (include/ft/sampler.h:30-94): the oracle's restatement
+    against the reference's own, on the same rows and states: temperature,
+    top-k, top-p (each on and off), the state carried from draw to draw."""
+    rng = np.random.default_rng(V)
+    state_o = state_r = P.SAMPLER_SEED
+    for trial in range(40):
+        lg = (rng.standard_normal(V) * rng.choice([0.5, 2.0, 6.0])).astype(np.float32)
+        temp = float(rng.choice([0.0, 0.3, 0.7, 1.0, 1.7]))
+        top_k = int(rng.choice([0, 1, 5, 40, V, V + 3]))
+        top_p = float(rng.choice([0.5, 0.9, 0.95, 1.0]))
+        to, state_o = orc.sampler_sample(lg, temp, top_k, top_p, state_o)
+        tr, state_r = ref.sampler_sample(lg, temp, top_k, top_p, state_r)
+        assert (to, state_o) == (tr, state_r), (trial, temp, top_k, top_p)
+
+
+def test_sampler_sample_distribution(orc):
+    """The draws follow the top-k / top-p renormalised softmax (chi-square on a
+    6-token row): p = softmax(l / T) restricted to the 3 largest, then to the
+    smallest prefix whose mass reaches top_p."""
+    lg = np.array([2.0, 0.5, 1.0, -1.0, 1.5, 0.0], np.float32)
+    T, k, p = 0.8, 3, 0.9
+    e = np.exp((lg - lg.max()) / T)
+    q = e / e.sum()
+    order = np.argsort(-q)[:k]
+    kept = np.zeros_like(q)
+    kept[order] = q[order] / q[order].sum()
+    cum = np.cumsum(kept[order])
+    cut = int(np.searchsorted(cum, p) + 1)
+    final = np.zeros_like(q)
+    final[order[:cut]] = kept[order[:cut]] / kept[order[:cut]].sum()
+    n = 20000
+    counts = np.zeros(6)
+    s = P.SAMPLER_SEED
+    for _ in range(n):
+        t, s = orc.sampler_sample(lg, T, k, p, s)
+        counts[t] += 1
+    assert counts[final == 0].sum() == 0
+    nz = final > 0
+    chi2 = ((counts[nz] - n * final[nz]) ** 2 / (n * final[nz])).sum()
+    assert chi2 < 15.0, (counts, final)

@@ -291,7 +291,9 @@ struct RowStats {
 struct RowChunks {
     float* cmax;     // [nrows][nch]
     int32_t* carg;   // [nrows][nch]
-    double* csub;    // [nrows][nsub]
+    double* csub;    // [nrows][nsub] sum of exp((double)((l - max)/T))
+    double* csubf;   // [nrows][nsub] sum of the float expf((l - max)/T) (the sampler's)
+    float* submax;   // [nrows][nsub] sub-chunk maxima
     int nch, nsub;
 };
 size_t row_stats_scratch_bytes(int64_t nrows, int64_t V);
@@ -312,7 +314,10 @@ struct AcceptDev {
     const float* pd;         // device [M] or null
     int mode;
     float temp;
-    uint64_t* rng;           // device state
+    uint64_t* rng;           // device state of the acceptance stream
+    uint64_t* sampler_rng;   // device state of the bonus sampler (ratio mode)
+    int top_k;
+    float top_p;
     double* p;               // scratch [V] (residual mode)
     int32_t* out;            // device: [0]=n_acc, [1]=bonus, [2..2+M) accepted
     float* margin;           // device scalar

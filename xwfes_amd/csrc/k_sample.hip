@@ -41,10 +41,16 @@ __device__ __forceinline__ const float* stat_row(const float* base_row, const fl
     return r == 0 ? base_row : rows + (r - 1) * V;
 }
 
-// exp((double)((l - mx) / T)): the one expression every sum and pick uses
+// exp((double)((l - mx) / T)): the acceptance test's exponential
 __device__ __forceinline__ double texp(float l, float mx, float temp) {
 #pragma clang fp contract(off)
     return exp((double)((l - mx) / temp));
+}
+
+// expf((l - mx) / T) in float: the sampler's exponential (sampler.h:40)
+__device__ __forceinline__ float sexp(float l, float mx, float temp) {
+#pragma clang fp contract(off)
+    return expf((l - mx) / temp);
 }
 
 // ---- statistics pass 1: per (row, chunk) first-max argmax; the 16 loads
@@ -118,15 +124,27 @@ __global__ void __launch_bounds__(256) k_row_sum(const float* __restrict__ base_
     }
     float mx = -INFINITY;
     for (int k = 0; k < rc.nch; ++k) mx = fmaxf(mx, rc.cmax[r * rc.nch + k]);
-    double s = 0.0;
+    double s = 0.0, sf = 0.0;
+    float smx = -INFINITY;
 #pragma unroll
     for (int k = 0; k < 16; ++k)
-        if (i0 + k < V) s += texp(v[k], mx, temp);
-    s += __shfl_xor(s, 4, 64);
-    s += __shfl_xor(s, 2, 64);
-    s += __shfl_xor(s, 1, 64);
+        if (i0 + k < V) {
+            s += texp(v[k], mx, temp);
+            sf += (double)sexp(v[k], mx, temp);
+            smx = fmaxf(smx, v[k]);
+        }
+#pragma unroll
+    for (int o = 4; o > 0; o >>= 1) {
+        s += __shfl_xor(s, o, 64);
+        sf += __shfl_xor(sf, o, 64);
+        smx = fmaxf(smx, __shfl_xor(smx, o, 64));
+    }
     const int64_t j = (int64_t)c * (SCH / SUB) + t / 8;
-    if ((t & 7) == 0 && j < rc.nsub) rc.csub[r * rc.nsub + j] = s;
+    if ((t & 7) == 0 && j < rc.nsub) {
+        rc.csub[r * rc.nsub + j] = s;
+        rc.csubf[r * rc.nsub + j] = sf;
+        rc.submax[r * rc.nsub + j] = smx;
+    }
 }
 
 // Inverse-CDF pick over p[0..V) (double weights) by one block: thread t sums
@@ -194,107 +212,315 @@ __device__ int32_t block_pick(const double* __restrict__ p, int64_t V, float u) 
     return r;
 }
 
-// Inclusive block scan of one double per thread (wave scans, then the wave
-// totals); returns the thread's inclusive prefix, *tot the block total.
-__device__ double block_scan(double v, double* tot) {
-    __shared__ double wsum[NT / 64];
-    const int t = threadIdx.x, l = t & 63, w = t >> 6;
-#pragma unroll
-    for (int o = 1; o < 64; o <<= 1) {
-        const double n = __shfl_up(v, o, 64);
-        if (l >= o) v += n;
-    }
-    if (l == 63) wsum[w] = v;
-    __syncthreads();
-    if (w == 0) {
-        double x = l < NT / 64 ? wsum[l] : 0.0;
-#pragma unroll
-        for (int o = 1; o < NT / 64; o <<= 1) {
-            const double n = __shfl_up(x, o, 64);
-            if (l >= o) x += n;
+constexpr int SMAXK = 64;     // largest top-k of the device sampler
+constexpr int SMAXSUB = 4096; // largest sub-chunk count it takes (V <= 524288)
+constexpr int SMAXEQ = 1024;  // probabilities equal to the k-th kept for the tie break
+
+// The sampler's SplitMix64 draw: bits 24..47 of the output as a 24-bit
+// fraction (include/ft/sampler.h:84-92)
+__device__ __forceinline__ float sampler_next_float(uint64_t& st) {
+    st += 0x9E3779B97F4A7C15ull;
+    uint64_t z = st;
+    z = (z ^ (z >> 30)) * 0xBF58476D1CE4E5B9ull;
+    z = (z ^ (z >> 27)) * 0x94D049BB133111EBull;
+    const uint32_t u = (uint32_t)((z ^ (z >> 31)) >> 16);
+    return (float)(u >> 8) * (1.f / 16777216.f);
+}
+
+// Lanes l < n of one wave: out[rank] = l for the rank of (p[l], i[l]) in the
+// order p descending, index ascending (by_index: index ascending only).
+__device__ __forceinline__ void wave_rank_sort(const float* p, const int32_t* idx, int n,
+                                               bool by_index, int32_t* out, int l) {
+    if (l < n) {
+        const float pl = p[l];
+        const int32_t il = idx[l];
+        int r = 0;
+#pragma unroll 8
+        for (int j = 0; j < n; ++j) {
+            const bool before = by_index ? idx[j] < il : (p[j] > pl || (p[j] == pl && idx[j] < il));
+            r += before;
         }
-        if (l < NT / 64) wsum[l] = x;
+        out[r] = l;
     }
-    __syncthreads();
-    const double r = v + (w ? wsum[w - 1] : 0.0);
-    *tot = wsum[NT / 64 - 1];
+}
+
+// order-preserving unsigned key of a float
+__device__ __forceinline__ uint32_t fkey(float x) {
+    const uint32_t u = __float_as_uint(x);
+    return (u & 0x80000000u) ? ~u : (u | 0x80000000u);
+}
+
+// Block-wide radix select: the `need`-th largest key among n entries (key_of
+// (e, &k) returns false for an entry without a value), 8 bits a pass;
+// returns the key and *take: how many entries equal to it are among the
+// `need` largest.  Wave 0 finds each pass's bin by a suffix scan over the
+// 256 bins (four per lane).
+template <typename KeyOf>
+__device__ uint32_t block_radix_kth(int n, uint32_t need, KeyOf key_of, uint32_t* take) {
+    // one histogram per wave, rows 257 words apart so that the waves' copies
+    // of a bin sit in different banks; summed into row 0 before the scan
+    constexpr int HS = 257;
+    __shared__ uint32_t whist[NT / 64][HS];
+    __shared__ uint32_t s_pre, s_msk, s_need;
+    const int t = threadIdx.x, l = t & 63, w = t >> 6;
+    uint32_t* hist = whist[0];
+    if (t == 0) {
+        s_pre = 0;
+        s_msk = 0;
+        s_need = need;
+    }
+    for (int shift = 24; shift >= 0; shift -= 8) {
+        for (int i = t; i < (NT / 64) * HS; i += NT) (&whist[0][0])[i] = 0;
+        __syncthreads();
+        const uint32_t pre = s_pre, msk = s_msk;
+        for (int e = t; e < n; e += NT) {
+            uint32_t k;
+            if (key_of(e, &k) && (k & msk) == pre) atomicAdd(&whist[w][(k >> shift) & 255u], 1u);
+        }
+        __syncthreads();
+        if (t < 256) {
+            uint32_t v = 0;
+#pragma unroll
+            for (int q = 0; q < NT / 64; ++q) v += whist[q][t];
+            hist[t] = v;  // row 0 is read only by thread t before this write
+        }
+        __syncthreads();
+        if (t < 64) {
+            const uint32_t h0 = hist[4 * l], h1 = hist[4 * l + 1], h2 = hist[4 * l + 2],
+                           h3 = hist[4 * l + 3];
+            const uint32_t loc = h0 + h1 + h2 + h3;
+            uint32_t inc = loc;  // sum over this lane and the lanes above it
+#pragma unroll
+            for (int o = 1; o < 64; o <<= 1) {
+                const uint32_t v = __shfl_down(inc, o, 64);
+                if (l + o < 64) inc += v;
+            }
+            const uint32_t nd = s_need;
+            uint32_t cum = inc - loc;  // entries in higher bins
+            const uint32_t hb[4] = {h0, h1, h2, h3};
+#pragma unroll
+            for (int q = 3; q >= 0; --q) {
+                if (cum < nd && cum + hb[q] >= nd) {
+                    s_pre = pre | ((uint32_t)(4 * l + q) << shift);
+                    s_msk = msk | (255u << shift);
+                    s_need = nd - cum;
+                }
+                cum += hb[q];
+            }
+        }
+        __syncthreads();
+    }
+    const uint32_t r = s_pre;
+    *take = s_need;
     __syncthreads();
     return r;
 }
 
-// Ratio-mode bonus: inverse CDF over exp((l - mx)/T) of row `lg` from its
-// sub-chunk sums `sub` (nsub of them): thread t owns sub-chunks [t spt, (t +
-// 1) spt); the crossing thread finds the crossing sub-chunk, whose 128
-// exponentials are formed again by one wave and summed in index order by its
-// first lane.  Rounding that leaves no crossing inside the sub-chunk picks
-// its last positive element.
-__device__ int32_t pick_from_subs(const float* __restrict__ lg, int64_t V, float mx, float temp,
-                                  const double* __restrict__ sub, int nsub, float u) {
+// Sampler::sample (include/ft/sampler.h:30-94) of row lg (max mx, double sum
+// S of the float exponentials) at temperature T > 0: top-k (1 <= K <= 64, K <
+// V) or, without it, all V <= 64 elements; top-p (< 1) or none; one draw from
+// *state.  The K largest probabilities lie in the K sub-chunks of largest
+// maxima (the probability is monotone in the logit), so those K * 128
+// elements are the candidates; radix selects find the K-th largest sub-chunk
+// maximum and then the K-th largest candidate probability, ties at either
+// going to the lower index (the reference's partial_sort leaves their order
+// unspecified).  The kept values then go through the reference's arithmetic
+// in order.
+__device__ int32_t sampler_pick(const float* __restrict__ lg, int64_t V, float mx, float temp,
+                                int topk, float top_p, const double* __restrict__ csubf,
+                                const float* __restrict__ submax, int nsub, int32_t amax,
+                                uint64_t* state) {
 #pragma clang fp contract(off)
-    __shared__ int jsel, first;
-    __shared__ double exsel;
-    __shared__ double ev[SUB];
-    __shared__ double incl[NT];
+    __shared__ float cp[SMAXK * SUB];  // candidate probabilities (-1: no element)
+    __shared__ float smx[SMAXSUB];
+    __shared__ int32_t sel[SMAXK];
+    __shared__ uint32_t nsel_gt, neq;
+    __shared__ int32_t eqi[SMAXEQ];
+    __shared__ float kp[SMAXK];
+    __shared__ int32_t ki[SMAXK], ord[SMAXK];
+    __shared__ double ssum;
     __shared__ int32_t pick;
-    const int t = threadIdx.x;
-    const int spt = (nsub + NT - 1) / NT;
-    const int j0 = t * spt, j1 = min(nsub, j0 + spt);
-    double cs = 0.0;
-    for (int j = j0; j < j1; ++j) cs += sub[j];
-    if (t == 0) {
-        jsel = -1;
-        pick = -1;
-        first = NT;
-    }
-    double tot;
-    const double inc = block_scan(cs, &tot);
-    incl[t] = inc;
-    const double target = (double)u * tot;
-    if (inc > target) atomicMin(&first, t);
-    __syncthreads();
-    if (t == first) {
-        // the first thread whose inclusive prefix passes the target: its
-        // sub-chunks in order from the previous thread's prefix
-        double c = t ? incl[t - 1] : 0.0;
-        int js = -1;
-        double es = c;
-        for (int j = j0; j < j1; ++j) {
-            const double nc = c + sub[j];
-            if (sub[j] > 0) {
-                js = j;
-                es = c;
-            }
-            if (nc > target) break;
-            c = nc;
-        }
-        jsel = js;
-        exsel = es;
-    }
-    __syncthreads();
-    const int js = jsel;
-    if (t < 64 && js >= 0) {
+    const int t = threadIdx.x, l = t & 63;
+    const bool use_k = topk > 0 && topk < V;
+    const int K = use_k ? topk : (int)V;
+    const int nsel = use_k ? min(K, nsub) : nsub;
+    // the normaliser and the sub-chunk maxima
+    if (t < 64) {
+        double sv = 0.0;
+        for (int j = t; j < nsub; j += 64) sv += csubf[j];
 #pragma unroll
-        for (int k = 0; k < SUB / 64; ++k) {
-            const int64_t i = (int64_t)js * SUB + t + 64 * k;
-            ev[t + 64 * k] = i < V ? texp(lg[i], mx, temp) : 0.0;
+        for (int o = 32; o > 0; o >>= 1) sv += __shfl_xor(sv, o, 64);
+        if (t == 0) {
+            ssum = sv;
+            nsel_gt = 0;
+            neq = 0;
+            pick = -1;
         }
     }
+    for (int j = t; j < nsub; j += NT) smx[j] = submax[j];
     __syncthreads();
-    if (t == 0 && js >= 0) {
-        double c = exsel;
-        int32_t last = -1, pk = -1;
-        for (int k = 0; k < SUB; ++k) {
-            if (ev[k] > 0) last = js * SUB + k;
-            c += ev[k];
-            if (c > target) {
-                pk = js * SUB + k;
-                break;
+    // the nsel sub-chunks of largest maxima (ties: lower index)
+    float thr = -INFINITY;  // the top K all lie at or above the K-th largest maximum
+    if (use_k && nsel < nsub) {
+        uint32_t take;
+        const uint32_t kk = block_radix_kth(nsub, (uint32_t)nsel,
+                                            [&](int e, uint32_t* k) {
+                                                *k = fkey(smx[e]);
+                                                return true;
+                                            },
+                                            &take);
+        for (int j = t; j < nsub; j += NT) {
+            const uint32_t k = fkey(smx[j]);
+            if (k > kk) {
+                sel[atomicAdd(&nsel_gt, 1u)] = j;
+            } else if (k == kk) {
+                const uint32_t s2 = atomicAdd(&neq, 1u);
+                if (s2 < SMAXEQ) eqi[s2] = j;
             }
         }
-        pick = pk >= 0 ? pk : last;
+        __syncthreads();
+        const int ne = (int)min(neq, (uint32_t)SMAXEQ), g = (int)nsel_gt;
+        for (int s2 = t; s2 < ne; s2 += NT) {
+            int r = 0;
+            for (int u = 0; u < ne; ++u) r += eqi[u] < eqi[s2];
+            if (r < (int)take) sel[g + r] = eqi[s2];
+        }
+        __syncthreads();
+        if (t == 0) {
+            nsel_gt = 0;
+            neq = 0;
+        }
+        // the K-th largest maximum: K sub-chunks hold an element at least
+        // this large, so the K-th largest element is too
+        const uint32_t u = (kk & 0x80000000u) ? (kk & 0x7FFFFFFFu) : ~kk;
+        thr = __uint_as_float(u);
+    } else if (t < nsel) {
+        sel[t] = t;
     }
     __syncthreads();
-    const int32_t r = pick >= 0 ? pick : 0;
+    const double S = ssum;
+    const int nc = nsel * SUB;
+    for (int e = t; e < nc; e += NT) {
+        const int64_t i = (int64_t)sel[e / SUB] * SUB + e % SUB;
+        const float x = i < V ? lg[i] : -INFINITY;
+        cp[e] = i < V && x >= thr ? (float)((double)sexp(x, mx, temp) / S) : -1.f;
+    }
+    __syncthreads();
+    // the K-th largest probability (bits of p >= 0 order as p)
+    uint32_t take_eq;
+    const uint32_t kth = block_radix_kth(nc, (uint32_t)K,
+                                         [&](int e, uint32_t* k) {
+                                             const float pv = cp[e];
+                                             *k = __float_as_uint(pv);
+                                             return pv >= 0.f;
+                                         },
+                                         &take_eq);
+    for (int e = t; e < nc; e += NT) {
+        const float pv = cp[e];
+        if (pv < 0.f) continue;
+        const uint32_t key = __float_as_uint(pv);
+        const int32_t i = sel[e / SUB] * SUB + e % SUB;
+        if (key > kth) {
+            const uint32_t s2 = atomicAdd(&nsel_gt, 1u);
+            kp[s2] = pv;
+            ki[s2] = i;
+        } else if (key == kth) {
+            const uint32_t s2 = atomicAdd(&neq, 1u);
+            if (s2 < SMAXEQ) eqi[s2] = i;
+        }
+    }
+    __syncthreads();
+    {
+        const int ne = (int)min(neq, (uint32_t)SMAXEQ), g = (int)nsel_gt;
+        const float kv = __uint_as_float(kth);
+        for (int s2 = t; s2 < ne; s2 += NT) {
+            int r = 0;
+            for (int u = 0; u < ne; ++u) r += eqi[u] < eqi[s2];
+            if (r < (int)take_eq) {
+                kp[g + r] = kv;
+                ki[g + r] = eqi[s2];
+            }
+        }
+    }
+    __syncthreads();
+    // the reference's arithmetic over the K kept values in order p
+    // descending, index ascending (every lane of the one wave reads before
+    // any lane writes: LDS in order within a wave)
+    auto sort_desc = [&]() {
+        if (t < 64) {
+            wave_rank_sort(kp, ki, K, false, ord, l);
+            __builtin_amdgcn_wave_barrier();
+            const float pv = l < K ? kp[ord[l]] : 0.f;
+            const int32_t iv = l < K ? ki[ord[l]] : 0;
+            __builtin_amdgcn_wave_barrier();
+            if (l < K) {
+                kp[l] = pv;
+                ki[l] = iv;
+            }
+        }
+        __syncthreads();
+    };
+    sort_desc();
+    if (t == 0 && use_k) {
+        float keep = 0.f;
+#pragma unroll 8
+        for (int i = 0; i < K; ++i) keep += kp[i];
+#pragma unroll 8
+        for (int i = 0; i < K; ++i) kp[i] = kp[i] / keep;
+    }
+    __syncthreads();
+    if (top_p < 1.f) {
+        sort_desc();  // the filtered values sorted again (division can make new ties)
+        if (t == 0) {
+            double cum = 0.0;
+            int cut = K + 1;  // not reached among the kept: nothing cut
+#pragma unroll 8
+            for (int i = 0; i < K; ++i) {
+                cum += kp[i];
+                if (cum >= (double)top_p) {
+                    cut = i + 1;
+                    break;
+                }
+            }
+            if (cut <= K) {
+                double tail = 0.0;
+#pragma unroll 8
+                for (int i = cut; i < K; ++i) {
+                    tail += kp[i];
+                    kp[i] = 0.f;
+                }
+                if (tail > 0.0)
+#pragma unroll 8
+                    for (int i = 0; i < cut; ++i) kp[i] = (float)(kp[i] / (1.0 - tail));
+            }
+        }
+        __syncthreads();
+    }
+    // the draw: the first index whose running double sum, as float, reaches r
+    if (t < 64) wave_rank_sort(kp, ki, K, true, ord, l);
+    __syncthreads();
+    if (t == 0) {
+        uint64_t st = *state;
+        const float r = sampler_next_float(st);
+        *state = st;
+        int32_t pk = -1;
+        if (r <= 0.f) {
+            pk = 0;  // the reference's loop stops at index 0
+        } else {
+            double c = 0.0;
+#pragma unroll 8
+            for (int i = 0; i < K; ++i) {
+                c += kp[ord[i]];
+                if ((float)c >= r) {
+                    pk = ki[ord[i]];
+                    break;
+                }
+            }
+        }
+        pick = pk >= 0 ? pk : amax;
+    }
+    __syncthreads();
+    const int32_t r = pick;
     __syncthreads();
     return r;
 }
@@ -334,11 +560,13 @@ __global__ void __launch_bounds__(NT) k_accept(AcceptDev a) {
     __shared__ double sd[NT];
     __shared__ uint64_t rng;
     __shared__ int32_t cur, nacc, bonus, next;
-    __shared__ float mg, bu;
+    __shared__ float mg;
+    __shared__ uint64_t srng;
     const int t = threadIdx.x;
     const int64_t V = a.V;
     if (t == 0) {
         rng = *a.rng;
+        srng = a.sampler_rng ? *a.sampler_rng : 0;
         cur = -1;
         nacc = 0;
         bonus = 0;
@@ -425,15 +653,16 @@ __global__ void __launch_bounds__(NT) k_accept(AcceptDev a) {
             for (int32_t i = 0; i < k; ++i) a.out[2 + i] = i;
             nacc = k;
             cur = k - 1;
-            bu = splitmix_float(s);  // the bonus token's uniform
             rng = s;
             mg = m;
         }
         __syncthreads();
-        // the bonus from the row after the last accepted node
+        // the bonus: Sampler::sample of the row after the last accepted node
         const int32_t c = cur;
-        const int32_t b = pick_from_subs(ROW(c), V, STAT(c).mx, a.temp,
-                                         a.rc.csub + (int64_t)(c + 1) * a.rc.nsub, a.rc.nsub, bu);
+        const int64_t ro = (int64_t)(c + 1) * a.rc.nsub;
+        const int32_t b = sampler_pick(ROW(c), V, STAT(c).mx, a.temp, a.top_k, a.top_p,
+                                       a.rc.csubf + ro, a.rc.submax + ro, a.rc.nsub,
+                                       STAT(c).amax, &srng);
         if (t == 0) bonus = b;
         __syncthreads();
     } else {  // RESIDUAL
@@ -503,6 +732,7 @@ __global__ void __launch_bounds__(NT) k_accept(AcceptDev a) {
         a.out[0] = nacc;
         a.out[1] = bonus;
         *a.rng = rng;
+        if (a.sampler_rng) *a.sampler_rng = srng;
         *a.margin = mg;
     }
 }
@@ -511,7 +741,7 @@ __global__ void __launch_bounds__(NT) k_accept(AcceptDev a) {
 
 size_t row_stats_scratch_bytes(int64_t nrows, int64_t V) {
     const int64_t nch = (V + SCH - 1) / SCH, nsub = (V + SUB - 1) / SUB;
-    return (size_t)(nrows * nsub) * 8 + (size_t)(nrows * nch) * 8 + 64;
+    return (size_t)(nrows * nsub) * (8 + 8 + 4) + (size_t)(nrows * nch) * 8 + 64;
 }
 
 RowChunks row_chunks(void* scratch, int64_t nrows, int64_t V) {
@@ -519,8 +749,10 @@ RowChunks row_chunks(void* scratch, int64_t nrows, int64_t V) {
     rc.nch = (int)((V + SCH - 1) / SCH);
     rc.nsub = (int)((V + SUB - 1) / SUB);
     rc.csub = (double*)scratch;
-    rc.cmax = (float*)(rc.csub + nrows * rc.nsub);
+    rc.csubf = rc.csub + nrows * rc.nsub;
+    rc.cmax = (float*)(rc.csubf + nrows * rc.nsub);
     rc.carg = (int32_t*)(rc.cmax + nrows * rc.nch);
+    rc.submax = (float*)(rc.carg + nrows * rc.nch);
     return rc;
 }
 

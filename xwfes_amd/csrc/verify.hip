@@ -626,6 +626,15 @@ int ftx_accept(ftx_ctx* ctx, const ftx_accept_args* a) {
     if (a->mode == FTX_ACCEPT_RESIDUAL && (!a->q && M > 0))
         return ftx_fail(ctx, FTX_E_INVALID, "residual mode needs q");
     if (!(a->temp > 0.f)) return ftx_fail(ctx, FTX_E_INVALID, "temperature must be > 0");
+    if (a->mode == FTX_ACCEPT_RATIO) {
+        // the device sampler: top-k of at most 64, or no top-k over at most
+        // 64 tokens; rows of at most 4096 sub-chunks of 128
+        if (!a->sampler_rng) return ftx_fail(ctx, FTX_E_INVALID, "ratio mode needs sampler_rng");
+        const bool use_k = a->top_k > 0 && a->top_k < V;
+        if ((use_k && a->top_k > 64) || (!use_k && V > 64) || (V + 127) / 128 > 4096)
+            return ftx_fail(ctx, FTX_E_UNSUPPORTED,
+                            "sampler: top_k must be in 1..64 (or V <= 64), V <= 524288");
+    }
     for (int64_t i = 0; i < M; ++i) {
         const int32_t p = a->parents ? a->parents[i] : (int32_t)i - 1;
         if (p < -1 || p >= i) return ftx_fail(ctx, FTX_E_INVALID, "parents[i] must be in [-1, i)");
@@ -642,7 +651,7 @@ int ftx_accept(ftx_ctx* ctx, const ftx_accept_args* a) {
     const size_t pb = a->mode == FTX_ACCEPT_RESIDUAL ? (size_t)V * 8 : 0;
     const size_t off_small = off_p + ((pb + 255) & ~(size_t)255);
     const size_t out_b = ((size_t)(M + 2) * 4 + 7) & ~(size_t)7;
-    const size_t head_b = 16 + out_b;  // rng | margin | pad | out
+    const size_t head_b = 24 + out_b;  // rng | sampler rng | margin | pad | out
     const size_t small_b = head_b + (size_t)M * 12 + 64;
     const size_t off_rs = off_small + ((small_b + 255) & ~(size_t)255);  // row-stat chunks
     const size_t off_b = off_rs + ((row_stats_scratch_bytes(M + 1, V) + 255) & ~(size_t)255);
@@ -654,14 +663,16 @@ int ftx_accept(ftx_ctx* ctx, const ftx_accept_args* a) {
     if (rc) return rc;
     hipStream_t st = ctx->stream;
     FTX_HIP(ctx, hipStreamSynchronize(st));
-    // small host block: rng | margin | pad | out | props | parents | pd
+    // small host block: rng | sampler rng | margin | pad | out | props | parents | pd
     uint64_t* h_rng = (uint64_t*)pin;
-    float* h_margin = (float*)(pin + 8);
-    int32_t* h_out = (int32_t*)(pin + 16);
+    uint64_t* h_srng = (uint64_t*)(pin + 8);
+    float* h_margin = (float*)(pin + 16);
+    int32_t* h_out = (int32_t*)(pin + 24);
     int32_t* h_props = (int32_t*)(pin + head_b);
     int32_t* h_par = h_props + M;
     float* h_pd = (float*)(h_par + M);
     *h_rng = *a->rng;
+    *h_srng = a->sampler_rng ? *a->sampler_rng : 0;
     *h_margin = INFINITY;
     for (int64_t i = 0; i < M; ++i) {
         h_props[i] = a->props[i];
@@ -691,9 +702,12 @@ int ftx_accept(ftx_ctx* ctx, const ftx_accept_args* a) {
     ad.mode = a->mode;
     ad.temp = a->temp;
     ad.rng = (uint64_t*)d_small;
+    ad.sampler_rng = (uint64_t*)(d_small + 8);
+    ad.top_k = a->top_k;
+    ad.top_p = a->top_p;
     ad.p = (double*)(ws + off_p);
-    ad.out = (int32_t*)(d_small + 16);
-    ad.margin = (float*)(d_small + 8);
+    ad.out = (int32_t*)(d_small + 24);
+    ad.margin = (float*)(d_small + 16);
     tk = tr_begin(ctx);
     FTX_HIP(ctx, launch_accept(st, ad));
     tr_end(ctx, tk, TK_ACCEPT, (double)V * 4);
@@ -705,6 +719,7 @@ int ftx_accept(ftx_ctx* ctx, const ftx_accept_args* a) {
     *a->bonus = h_out[1];
     for (int32_t i = 0; i < na; ++i) a->accepted[i] = h_out[2 + i];
     *a->rng = *h_rng;
+    if (a->sampler_rng) *a->sampler_rng = *h_srng;
     if (a->margin) *a->margin = *h_margin;
     return FTX_OK;
 }

@@ -18,6 +18,8 @@ F32, F16, Q4_0, Q4_1, Q8_0, Q4_K, Q6_K, BF16 = 0, 1, 2, 3, 8, 12, 14, 30
 BLOCK = {F32: (1, 4), F16: (1, 2), BF16: (1, 2), Q4_0: (32, 18), Q4_1: (32, 20),
          Q8_0: (32, 34), Q4_K: (256, 144), Q6_K: (256, 210)}
 KV_F32, KV_F16 = 0, 1
+# the sampler state of seed 0 (include/ft/sampler.h:19)
+SAMPLER_SEED = 0x9E3779B97F4A7C15
 ACCEPT_GREEDY, ACCEPT_RATIO, ACCEPT_RESIDUAL = 0, 1, 2
 LAYER_TENSORS = ("attn_norm", "q", "k", "v", "o", "ffn_norm", "gate", "up", "down")
 ERRORS = {-1: "invalid argument", -2: "unsupported", -3: "device error", -4: "out of memory",
@@ -63,7 +65,9 @@ class AcceptArgs(C.Structure):
     _fields_ = [("base_row", _vp), ("rows", _vp), ("q", _vp), ("M", _i64), ("V", _i64),
                 ("props", _i32p), ("parents", _i32p), ("pd", _fp), ("mode", C.c_int32),
                 ("temp", C.c_float), ("rng", C.POINTER(C.c_uint64)), ("accepted", _i32p),
-                ("n_acc", _i32p), ("bonus", _i32p), ("margin", _fp)]
+                ("n_acc", _i32p), ("bonus", _i32p), ("margin", _fp),
+                ("sampler_rng", C.POINTER(C.c_uint64)), ("top_k", C.c_int32),
+                ("top_p", C.c_float)]
 
 
 class TraceEntry(C.Structure):
@@ -308,21 +312,25 @@ class Context:
         return Model(self, h.value, cfg, tensors)
 
     def accept(self, base_ptr, rows_ptr, M, V, props, mode, temp=1.0, rng=0, parents=None,
-               pd=None, q_ptr=None):
+               pd=None, q_ptr=None, sampler_state=SAMPLER_SEED, top_k=40, top_p=0.95):
+        """ftx_accept; returns accepted node ids, bonus token, the advanced
+        acceptance and sampler states and the decision margin.  The sampler
+        defaults are the reference's SampleParams (include/ft/sampler.h:10-15)."""
         props = np.ascontiguousarray(props, np.int32)
         par = None if parents is None else np.ascontiguousarray(parents, np.int32)
         pdv = None if pd is None else np.ascontiguousarray(pd, np.float32)
         acc = np.zeros(max(M, 1), np.int32)
         na, bonus, mg = C.c_int32(0), C.c_int32(0), C.c_float(0)
         s = C.c_uint64(rng)
+        ss = C.c_uint64(sampler_state)
         a = AcceptArgs(base_ptr, rows_ptr, q_ptr, M, V, props.ctypes.data_as(_i32p),
                        None if par is None else par.ctypes.data_as(_i32p),
                        None if pdv is None else pdv.ctypes.data_as(_fp), mode, temp,
                        C.pointer(s), acc.ctypes.data_as(_i32p), C.pointer(na), C.pointer(bonus),
-                       C.pointer(mg))
+                       C.pointer(mg), C.pointer(ss), top_k, top_p)
         self.check(self.lib.ftx_accept(self.h, C.byref(a)))
         return dict(accepted=acc[:na.value].tolist(), bonus=bonus.value, rng=s.value,
-                    margin=mg.value)
+                    sampler_state=ss.value, margin=mg.value)
 
 
 class Model:

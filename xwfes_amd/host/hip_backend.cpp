@@ -210,8 +210,11 @@ void HipVerifier::read_kv(void* k, void* v) { be_.check(ftx_kv_read(kv_, k, v), 
 Accepted accept_on_device(HipBackend& be, int64_t V, const float* base_row, const float* rows,
                           const std::vector<int32_t>& props, AcceptMode mode, float temp,
                           uint64_t& rng, const std::vector<float>& pd,
-                          const std::vector<int32_t>& parents, const float* q) {
+                          const std::vector<int32_t>& parents, const float* q,
+                          BonusSampler* sampler) {
     const int64_t M = (int64_t)props.size();
+    BonusSampler local;
+    BonusSampler& bs = sampler ? *sampler : local;
     Accepted out;
     out.nodes.assign((size_t)(M > 0 ? M : 1), -1);
     int32_t n_acc = 0;
@@ -231,6 +234,9 @@ Accepted accept_on_device(HipBackend& be, int64_t V, const float* base_row, cons
     a.n_acc = &n_acc;
     a.bonus = &out.bonus;
     a.margin = &out.margin;
+    a.sampler_rng = &bs.state;
+    a.top_k = bs.top_k;
+    a.top_p = bs.top_p;
     be.check(ftx_accept(be.ctx(), &a), "accept");
     out.nodes.resize((size_t)n_acc);
     return out;
@@ -241,7 +247,7 @@ Accepted HipVerifier::accept(const float* base_row, const float* rows,
                              uint64_t& rng, const std::vector<float>& pd,
                              const std::vector<int32_t>& parents, const float* q) {
     return accept_on_device(be_, cfg_.vocab, base_row, rows, props, mode, temp, rng, pd, parents,
-                            q);
+                            q, &sampler);
 }
 
 }  // namespace ftx_host

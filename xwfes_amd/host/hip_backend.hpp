@@ -137,6 +137,15 @@ enum class AcceptMode : int32_t {
     Residual = FTX_ACCEPT_RESIDUAL,
 };
 
+// the ratio-mode bonus sampler: Sampler::sample's parameters and state
+// (include/ft/sampler.h:10-19, 30-94); the state carries over between draws
+// as the Sampler object of generate does (src/spec.cpp:248-249)
+struct BonusSampler {
+    uint64_t state = 0x9E3779B97F4A7C15ull;
+    int32_t top_k = 40;
+    float top_p = 0.95f;
+};
+
 struct Accepted {
     std::vector<int32_t> nodes;  // accepted node ids, root first
     int32_t bonus = -1;          // the token that follows them
@@ -148,7 +157,8 @@ struct Accepted {
 Accepted accept_on_device(HipBackend& be, int64_t V, const float* base_row, const float* rows,
                           const std::vector<int32_t>& props, AcceptMode mode, float temp,
                           uint64_t& rng, const std::vector<float>& pd = {},
-                          const std::vector<int32_t>& parents = {}, const float* q = nullptr);
+                          const std::vector<int32_t>& parents = {}, const float* q = nullptr,
+                          BonusSampler* sampler = nullptr);
 
 class HipVerifier {
 public:
@@ -181,6 +191,8 @@ public:
     void read_kv(void* k, void* v);
 
     // acceptance over device logits; rng is the SplitMix64 state (in / out)
+    // the bonus sampler of ratio mode (state carried over between accepts)
+    BonusSampler sampler;
     Accepted accept(const float* base_row, const float* rows, const std::vector<int32_t>& props,
                     AcceptMode mode, float temp, uint64_t& rng, const std::vector<float>& pd = {},
                     const std::vector<int32_t>& parents = {}, const float* q = nullptr);
