@@ -261,6 +261,14 @@ typedef struct {
  * residual distribution with one more uniform of the rng stream). */
 int ftx_accept(ftx_ctx* ctx, const ftx_accept_args* a);
 
+/* Greedy draft pick of one device row [V]: the first maximum
+ * (Sampler::argmax, include/ft/sampler.h:21-28) and its probability under
+ * softmax_prob at T = 1 (src/spec.cpp:89-95) -- what
+ * DraftModelDrafter::draft takes per draft token (src/spec.cpp:100-119).
+ * Synchronous (the host needs the token for the next step); prob may be
+ * NULL. */
+int ftx_argmax_prob(ftx_ctx* ctx, const float* row, int64_t V, int32_t* token, float* prob);
+
 /* ---- kernel trace (the reference keeps wall-clock RunStats only,
  * include/ft/engine.h:25-39) ---- */
 typedef struct {

@@ -181,6 +181,107 @@ class Oracle:
         self.lib.orc_softmax_inplace(_ptr(p, _fp), p.size)
         return p
 
+    def generate(self, target, draft, prompt, max_new, spec_k=8, temp=0.0, top_k=40, top_p=0.95,
+                 seed=0, cap=256, kv_dtype=np.float16, ref_bonus_row=False,
+                 ref_draft_prefill=False):
+        """generate's speculative block (src/spec.cpp:245-333) with a
+        DraftModelDrafter (72-119) over two models of this module's form, on
+        caches of kv_dtype: draft k greedy tokens with their T = 1
+        probabilities (the drafter syncs to the history by prefill and
+        truncates to the accepted prefix, clamped to what it holds, as
+        Engine::truncate_to is, engine.cpp:423-428), cut them (276-285),
+        verify them on the target, accept by the ratio test, draw the bonus
+        from the row after the last accepted token by Sampler::sample (temp
+        <= 0: the argmax, the test at T = 1), truncate, step the target on
+        the bonus.  A round is emitted whole.  ref_bonus_row draws the bonus
+        from rows[min(acc, M - 1)] as the reference does (309-311: the wrong
+        row after a rejection), to compare with it.  ref_draft_prefill makes
+        the drafter's sync forward its whole held history again before the
+        new tokens, as the reference's Engine::prefill does on a non-empty
+        engine without a prefix-cache hit (src/engine.cpp:614-621: the loop
+        starts at the hit length, 0, not at the history length), again only
+        to compare with it.  Returns (tokens, stats)."""
+        def state(model):
+            c = model["cfg"]
+            shape = (c["n_layer"], cap, c["n_head_kv"] * c["head_dim"])
+            return dict(m=model, k=np.zeros(shape, kv_dtype), v=np.zeros(shape, kv_dtype), n=0,
+                        lg=None)
+
+        def fwd(st, toks):
+            rows = self.forward(st["m"], st["k"], st["v"], st["n"], list(toks))
+            return rows
+
+        T, D = state(target), state(draft)
+        D["hist"] = []  # the tokens in the drafter's cache, in order
+        V = target["cfg"]["vocab"]
+        rows = fwd(T, prompt)
+        T["n"] = len(prompt)
+        base = rows[-1]
+        history = list(prompt)
+        out = []
+        rsamp = seed if seed else 88172645463325252
+        sstate = seed if seed else SAMPLER_SEED
+        acc_temp = temp if temp > 0 else 1.0
+        bk, bp = (top_k, top_p) if temp > 0 else (1, 1.0)
+        stats = dict(rounds=0, drafted=0, accepted=0)
+        while len(out) < max_new:
+            # DraftModelDrafter::sync + draft
+            if D["n"] > len(history):
+                D["n"] = 0
+                D["hist"] = []
+            if D["n"] < len(history):
+                tail = history[D["n"]:]
+                toks = (D["hist"] + tail) if ref_draft_prefill else tail
+                r = fwd(D, toks)
+                D["lg"] = r[-1]
+                D["n"] += len(toks)
+                D["hist"] = D["hist"] + toks
+            pending_base = len(history)
+            props, probs = [], []
+            for j in range(spec_k):
+                t = self.argmax(D["lg"])
+                props.append(t)
+                probs.append(self.softmax_prob(D["lg"], t, 1.0))
+                if j + 1 < spec_k:
+                    D["lg"] = fwd(D, [t])[0]
+                    D["n"] += 1
+                    D["hist"] = D["hist"] + [t]
+            # the cut heuristic
+            cut, cum = len(props), 1.0
+            for i, p in enumerate(probs):
+                if 0 <= p < 0.02:
+                    cut = i
+                    break
+                cum *= p if p > 0 else 1.0
+                if cum < 0.05:
+                    cut = i + 1
+                    break
+            props, probs = props[:cut], probs[:cut]
+            M = len(props)
+            rows = fwd(T, props) if M else np.zeros((0, V), np.float32)
+            r = self.verify_accept(base, rows, np.asarray(props, np.int32), ACCEPT_RATIO,
+                                   temp=acc_temp, seed=rsamp, pd=np.asarray(probs, np.float32),
+                                   sampler_state=sstate, top_k=bk, top_p=bp)
+            acc = len(r["accepted"])
+            bonus = r["bonus"]
+            if ref_bonus_row and M:
+                # the same one draw from the same state, from the reference's row
+                bonus, _ = self.sampler_sample(rows[min(acc, M - 1)], temp if temp > 0 else 0.0,
+                                               top_k, top_p, sstate)
+            rsamp, sstate = r["rng"], r["sampler_state"]
+            T["n"] += acc
+            new = props[:acc] + [bonus]
+            out += new
+            history += new
+            base = fwd(T, [bonus])[0]
+            T["n"] += 1
+            D["n"] = min(pending_base + acc, D["n"])
+            D["hist"] = D["hist"][:D["n"]]
+            stats["rounds"] += 1
+            stats["drafted"] += M
+            stats["accepted"] += acc
+        return out, stats
+
     @staticmethod
     def kv_commit(kcache, vcache, npast, nodes):
         """Keep the accepted draft path `nodes` (node indices of the verify
@@ -341,6 +442,10 @@ class Ref:
         L.ref_sampler_sample.restype = C.c_int32
         L.ref_sampler_sample.argtypes = [_fp, C.c_int64, C.c_float, C.c_int32, C.c_float,
                                          C.POINTER(C.c_uint64)]
+        L.ref_generate.restype = C.c_int64
+        L.ref_generate.argtypes = [C.c_char_p, C.c_char_p, _i32p, C.c_int64, C.c_int, C.c_int,
+                                   C.c_float, C.c_int, C.c_float, C.c_uint64, C.c_int64,
+                                   C.c_int64, _i32p, C.c_int64]
         L.ref_gguf_summary.restype = C.c_int64
         L.ref_gguf_summary.argtypes = [C.c_char_p, C.c_char_p, C.c_char_p, C.c_int64]
 
@@ -421,6 +526,18 @@ class Ref:
         s = C.c_uint64(state)
         t = self.lib.ref_sampler_sample(_ptr(lg, _fp), lg.size, temp, top_k, top_p, C.byref(s))
         return t, s.value
+
+    def generate(self, target_path, draft_path, prompt, max_new, spec_k, temp, top_k=40,
+                 top_p=0.95, seed=0, ctx_len=256, prefill_batch=256):
+        """The reference's generate with a DraftModelDrafter (see
+        ref_harness.cpp); returns the emitted tokens."""
+        pr = np.ascontiguousarray(prompt, np.int32)
+        out = np.zeros(max_new + spec_k + 8, np.int32)
+        n = self.lib.ref_generate(target_path.encode(), draft_path.encode(), _ptr(pr, _i32p),
+                                  pr.size, max_new, spec_k, temp, top_k, top_p, seed, ctx_len,
+                                  prefill_batch, _ptr(out, _i32p), out.size)
+        assert n >= 0, "reference generate failed"
+        return out[:n].tolist()
 
     def gguf_summary(self, path, keys):
         """The reference parser's summary of a GGUF (see ref_harness.cpp),

@@ -111,6 +111,44 @@ int ref_engine_step(void* h, int32_t tok, float* out) {
     }
 }
 
+// generate (src/spec.cpp:245-333) with a DraftModelDrafter (72-119): the
+// target loaded from target_path prefills the prompt, the drafter loads
+// draft_path; the emitted tokens go to out (up to cap).  Returns their count
+// or -1.
+int64_t ref_generate(const char* target_path, const char* draft_path, const int32_t* prompt,
+                     int64_t n_prompt, int max_new, int spec_k, float temp, int top_k,
+                     float top_p, uint64_t seed, int64_t ctx_len, int64_t prefill_batch,
+                     int32_t* out, int64_t cap) {
+    try {
+        EngineOptions eo;
+        eo.model_path = target_path;
+        eo.prefill_batch = prefill_batch;
+        eo.threads = 1;
+        eo.igpu = IgpuMode::Off;
+        eo.ctx_len = ctx_len;
+        eo.throttle.enabled = false;
+        Engine eng;
+        eng.load(eo);
+        EngineOptions dopt = eo;
+        dopt.model_path = draft_path;
+        DraftModelDrafter drafter(dopt);
+        eng.prefill(std::vector<token_t>(prompt, prompt + n_prompt));
+        SampleParams sp;
+        sp.temp = temp;
+        sp.top_k = top_k;
+        sp.top_p = top_p;
+        sp.seed = seed;
+        std::vector<token_t> toks;
+        generate(eng, &drafter, sp, max_new, spec_k,
+                 [&](token_t t, const std::string&) { toks.push_back(t); });
+        const int64_t n = std::min<int64_t>((int64_t)toks.size(), cap);
+        for (int64_t i = 0; i < n; ++i) out[i] = toks[(size_t)i];
+        return (int64_t)toks.size();
+    } catch (...) {
+        return -1;
+    }
+}
+
 // Sampler::sample (include/ft/sampler.h:30-94) from `state`: reset(state)
 // then sample with seed 0, which uses the state as it stands; the state after
 // one draw is state + the SplitMix64 increment (one next_u32), none at temp

@@ -323,3 +323,7 @@ struct AcceptDev {
     float* margin;           // device scalar
 };
 hipError_t launch_accept(hipStream_t st, const AcceptDev& a);
+// argmax and its T = 1 softmax probability of one row: out = {token, prob
+// bits} (scratch: row_stats_scratch_bytes(1, V))
+hipError_t launch_argmax_prob(hipStream_t st, const float* row, int64_t V, void* scratch,
+                              int32_t* out);

@@ -737,7 +737,51 @@ __global__ void __launch_bounds__(NT) k_accept(AcceptDev a) {
     }
 }
 
+// Sampler::argmax and softmax_prob of that token (src/spec.cpp:89-95, as
+// DraftModelDrafter::draft uses them, 100-119) from one row's chunk
+// statistics at T = 1: the first maximum and 1 / sum_i exp((double)(l_i -
+// max)) as float.  One wave; out = {token, prob bits}.
+__global__ void __launch_bounds__(64) k_argmax_prob(RowChunks rc, int32_t* out) {
+    const int l = threadIdx.x;
+    float best = -INFINITY;
+    int32_t bi = 0x7FFFFFFF;
+    for (int c = l; c < rc.nch; c += 64) {
+        const float v = rc.cmax[c];
+        const int32_t iv = rc.carg[c];
+        if (iv != 0x7FFFFFFF && (bi == 0x7FFFFFFF || better(v, iv, best, bi))) {
+            best = v;
+            bi = iv;
+        }
+    }
+#pragma unroll
+    for (int o = 32; o > 0; o >>= 1) {
+        const float ov = __shfl_xor(best, o, 64);
+        const int32_t oi = __shfl_xor(bi, o, 64);
+        if (oi != 0x7FFFFFFF && (bi == 0x7FFFFFFF || better(ov, oi, best, bi))) {
+            best = ov;
+            bi = oi;
+        }
+    }
+    double sum = 0.0;
+    for (int j = l; j < rc.nsub; j += 64) sum += rc.csub[j];
+#pragma unroll
+    for (int o = 32; o > 0; o >>= 1) sum += __shfl_xor(sum, o, 64);
+    if (l == 0) {
+        out[0] = bi;
+        out[1] = __float_as_int((float)(exp(0.0) / sum));  // the maximum's exp((double)0)
+    }
+}
+
 }  // namespace
+
+hipError_t launch_argmax_prob(hipStream_t st, const float* row, int64_t V, void* scratch,
+                              int32_t* out) {
+    const RowChunks rc = row_chunks(scratch, 1, V);
+    hipError_t e = launch_row_stats(st, row, nullptr, 1, V, 1.f, 1, rc);
+    if (e != hipSuccess) return e;
+    hipLaunchKernelGGL(k_argmax_prob, dim3(1), dim3(64), 0, st, rc, out);
+    return hipGetLastError();
+}
 
 size_t row_stats_scratch_bytes(int64_t nrows, int64_t V) {
     const int64_t nch = (V + SCH - 1) / SCH, nsub = (V + SUB - 1) / SUB;

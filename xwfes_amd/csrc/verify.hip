@@ -6,6 +6,8 @@
 #include <new>
 
 #include "ftx_internal.h"
+
+#include <cstring>
 #include "quant_dev.h"
 
 struct ftx_model {
@@ -609,6 +611,26 @@ int ftx_verify_step(ftx_ctx* ctx, ftx_model* m, ftx_kv* kv, const ftx_verify_arg
     }
 #undef TRACED
     if (a->advance) kv->npast = npast + M;
+    return FTX_OK;
+}
+
+int ftx_argmax_prob(ftx_ctx* ctx, const float* row, int64_t V, int32_t* token, float* prob) {
+    if (!ctx || !row || !token || V < 1) return ftx_fail(ctx, FTX_E_INVALID, "null argument or V < 1");
+    const size_t rs = (row_stats_scratch_bytes(1, V) + 255) & ~(size_t)255;
+    uint8_t* ws;
+    int rc = ftx_workspace(ctx, rs + 256, (void**)&ws);
+    if (rc) return rc;
+    int32_t* pin;
+    rc = ftx_pinned(ctx, 8, (void**)&pin);
+    if (rc) return rc;
+    hipStream_t st = ctx->stream;
+    int32_t* d_out = (int32_t*)(ws + rs);
+    FTX_HIP(ctx, hipStreamSynchronize(st));  // the pinned buffer is shared
+    FTX_HIP(ctx, launch_argmax_prob(st, row, V, ws, d_out));
+    FTX_HIP(ctx, hipMemcpyAsync(pin, d_out, 8, hipMemcpyDeviceToHost, st));
+    FTX_HIP(ctx, hipStreamSynchronize(st));
+    *token = pin[0];
+    if (prob) std::memcpy(prob, &pin[1], 4);
     return FTX_OK;
 }
 

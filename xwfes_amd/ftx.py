@@ -119,6 +119,7 @@ def load(path=LIB_PATH):
         "ftx_kv_read": (C.c_int, [_vp, _vp, _vp]),
         "ftx_verify_step": (C.c_int, [_vp, _vp, _vp, C.POINTER(VerifyArgs)]),
         "ftx_accept": (C.c_int, [_vp, C.POINTER(AcceptArgs)]),
+        "ftx_argmax_prob": (C.c_int, [_vp, _vp, _i64, _i32p, _fp]),
         "ftx_fill_normal": (C.c_int, [_vp, _vp, C.c_int, _i64, C.c_uint64, C.c_float]),
         "ftx_trace": (C.c_int, [_vp, C.c_int]),
         "ftx_trace_read": (C.c_int, [_vp, C.POINTER(TraceEntry), C.c_int, C.POINTER(C.c_int)]),
@@ -310,6 +311,12 @@ class Context:
         h = _vp()
         self.check(self.lib.ftx_model_create(self.h, C.byref(d), C.byref(h)))
         return Model(self, h.value, cfg, tensors)
+
+    def argmax_prob(self, row_ptr, V):
+        """(first-max token, its T = 1 softmax probability) of a device row."""
+        t, p = C.c_int32(0), C.c_float(0)
+        self.check(self.lib.ftx_argmax_prob(self.h, row_ptr, V, C.byref(t), C.byref(p)))
+        return t.value, p.value
 
     def accept(self, base_ptr, rows_ptr, M, V, props, mode, temp=1.0, rng=0, parents=None,
                pd=None, q_ptr=None, sampler_state=SAMPLER_SEED, top_k=40, top_p=0.95):
