@@ -26,6 +26,8 @@ HBM_PEAK_GBS = 8000.0
 REPLAY = 20  # back-to-back issues of each dominant-class launch when timing it
 LLAMA3_8B = dict(n_layer=32, n_embd=4096, n_head=32, n_head_kv=8, head_dim=128, n_ff=14336,
                 vocab=128256, rope_theta=500000.0, rope_neox=0, rms_eps=1e-5)
+LLAMA32_1B = dict(n_layer=16, n_embd=2048, n_head=32, n_head_kv=8, head_dim=64, n_ff=8192,
+                  vocab=128256, rope_theta=500000.0, rope_neox=0, rms_eps=1e-5)
 WORKLOADS = {
     # kind verify: one verify step (M draft tokens at context ctx) plus ratio
     # acceptance; decode: one Engine::step at context ctx; prefill: P prompt
@@ -36,6 +38,10 @@ WORKLOADS = {
                                           M=1, temp=0.8),
     "llama3-8b-q4km-prefill-512": dict(kind="prefill", cfg=LLAMA3_8B, mix="q4_k_m", ctx=0, M=8,
                                        P=512, temp=0.8),
+    # generate: N tokens after a P-token prompt, a draft model proposing M
+    # tokens a round (greedy); random weights, so the draft is rarely accepted
+    "llama3-8b-q4km+1b-draft-spec4": dict(kind="generate", cfg=LLAMA3_8B, draft_cfg=LLAMA32_1B,
+                                          mix="q4_k_m", ctx=0, M=4, P=8, N=32, temp=0.0),
 }
 
 
@@ -156,7 +162,7 @@ def main():
               "build has no multi-GPU path (asked for --gpus %d)" % args.gpus, file=sys.stderr)
         sys.exit(2)
 
-    from xwfes_amd import ftx, synth
+    from xwfes_amd import ftx, spec, synth
     W = WORKLOADS[args.workload]
     cfg, ctx_len, M, temp = W["cfg"], W["ctx"], W["M"], W["temp"]
     V = cfg["vocab"]
@@ -176,8 +182,17 @@ def main():
                                                         synth.weight_bytes(tensors) / 1e9))
     kind = W["kind"]
     P_tok = W.get("P", 0)
-    model = ctx.model(cfg, tensors, max_tokens=M)
-    kv = model.kv(max(ctx_len, P_tok) + M + 8)
+    model = ctx.model(cfg, tensors, max_tokens=max(M, 8))
+    kv = model.kv(max(ctx_len, P_tok + W.get("N", 0) + 16) + M + 8)
+    drafter = dtensors = dmodel = dkv = None
+    gen_stats = []
+    if kind == "generate":
+        dcfg = W["draft_cfg"]
+        dtensors = synth.build(ctx, dcfg, synth.q4_k_m_mix(dcfg), seed=2)
+        dmodel = ctx.model(dcfg, dtensors, max_tokens=8)
+        dkv = dmodel.kv(P_tok + W["N"] + 32)
+        drafter = spec.DraftModelDrafter(ctx, dmodel, dkv)
+        log("draft model built (%.3f GB of weights)" % (synth.weight_bytes(dtensors) / 1e9))
     kp, vp, _ = kv.pointers()
     n_kv = cfg["n_layer"] * kv.cap_alloc * cfg["n_head_kv"] * cfg["head_dim"]
     ctx.fill_normal(kp, n_kv, seed=4, std=1.0, dtype=ftx.F16)
@@ -205,6 +220,9 @@ def main():
         elif kind == "decode":
             kv.truncate(ctx_len)
             model.step(kv, int(props[0]), logits.ptr)
+        elif kind == "generate":
+            out, st = spec.generate(ctx, model, kv, drafter, prompt, W["N"], spec_k=M, temp=temp)
+            gen_stats.append((len(out), st))
         else:
             kv.truncate(0)
             model.prefill(kv, prompt, logits.ptr, chunk=M)
@@ -213,6 +231,7 @@ def main():
         step()
     ctx.sync()
     accepted.clear()
+    gen_stats.clear()
     per = []
     ctx.sync()
     t_start = time.perf_counter()
@@ -257,6 +276,9 @@ def main():
     if kind == "prefill":
         sb = prefill_bytes(tensors, cfg, P_tok, M)
         tokens = P_tok
+    elif kind == "generate":
+        tokens = statistics.mean(n for n, _ in gen_stats)
+        sb = 0
     else:
         sb = step_bytes(tensors, cfg, ctx_len, M)
         tokens = M
@@ -265,9 +287,11 @@ def main():
                         "1 GPU",
               "decode": "decode tokens/s (Engine::step, M=1, ctx 2048), 8B-shape Q4_K, 1 GPU",
               "prefill": "prefill tokens/s (512-token prompt, chains of 8), 8B-shape Q4_K, "
-                         "1 GPU"}[kind]
+                         "1 GPU",
+              "generate": "generated tokens/s (speculative: 8B-shape Q4_K target, 1B-shape "
+                          "draft, 4 draft tokens a round, greedy), 1 GPU"}[kind]
     unit = {"verify": "verified tokens/s", "decode": "decoded tokens/s",
-            "prefill": "prefilled tokens/s"}[kind]
+            "prefill": "prefilled tokens/s", "generate": "generated tokens/s"}[kind]
     out = {
         "metric": metric,
         "value": round(tokens / (ms_step * 1e-3), 2),
@@ -288,6 +312,11 @@ def main():
         "hbm_frac": round(gbs / HBM_PEAK_GBS, 4),
         "committed_tokens_per_s": (round((statistics.mean(accepted) + 1) / (ms_step * 1e-3), 2)
                                    if accepted else None),
+        "generate_rounds": (statistics.mean(st["rounds"] for _, st in gen_stats)
+                            if gen_stats else None),
+        "draft_acceptance": (round(sum(st["accepted"] for _, st in gen_stats) /
+                                   max(1, sum(st["drafted"] for _, st in gen_stats)), 4)
+                             if gen_stats else None),
         "mean_accepted": round(statistics.mean(accepted), 3) if accepted else None,
         "traced_device_ms_per_step": round(traced_ms, 4),
         "roofline": {"bound": "hbm", "kernel": dom_name, "achieved": round(achieved, 1),
@@ -304,6 +333,11 @@ def main():
         out["cpu_baseline"] = cpu_baseline(ctx, tensors, cfg, ctx_len, M, props, threads)
         log("cpu baseline in %.1f s" % (time.perf_counter() - t0))
     print(json.dumps(out), flush=True)
+    if drafter is not None:
+        drafter.free()
+        dkv.free()
+        dmodel.free()
+        synth.free(dtensors)
     logits.free()
     base.free()
     kv.free()

@@ -239,6 +239,29 @@ def test_verify_8b_shape_two_layers(gctx, orc):
     assert rel_err_rows(got, want) < LOGIT_TOL
 
 
+@pytest.mark.parametrize("d,ff,hd", [(2048, 8192, 64), (3072, 8192, 128), (512, 1024, 64)])
+def test_verify_narrow_widths(gctx, orc, d, ff, hd):
+    """Widths below 4096 on the MFMA row-dot path (Llama-3.2-1B: d 2048, head
+    64; 3B: d 3072, head 128; a 2-super-block 512), Q4_K with Q6_K attn_v /
+    ffn_down, 2 layers: an 8-token chain and a tree at context 70."""
+    orc.set_threads(16)
+    nh = d // hd
+    cfg = P.model_cfg(2, d, nh, max(nh // 4, 1), hd, ff, 3000, rope_theta=500000.0)
+    dts_l = [q4k_m_dtypes(0, 32), q4k_m_dtypes(5, 32)]
+    model = P.make_model(orc, cfg, dict(dts_l[0], tok_embd=P.Q4_K, output=P.Q6_K), seed=d)
+    for name in ("v", "down"):  # the second layer's mix
+        w = (np.random.default_rng(d + 1).standard_normal(
+            (model["blk.1." + name]["ne1"], model["blk.1." + name]["ne0"])) * 0.02).astype(np.float32)
+        model["blk.1." + name] = dict(raw=orc.quantize(w, dts_l[1][name]), dtype=dts_l[1][name],
+                                      ne0=model["blk.1." + name]["ne0"],
+                                      ne1=model["blk.1." + name]["ne1"])
+    rng = np.random.default_rng(d + 2)
+    toks = rng.integers(0, 3000, 8).tolist()
+    for parents in (None, [-1, 0, 0, 1, 2, 2, 4, -1]):
+        got, want, _, _ = run_both(gctx, orc, model, toks, 70, 96, parents=parents)
+        assert rel_err_rows(got, want) < LOGIT_TOL, parents
+
+
 def _wide_model(orc, neox, seed):
     """one 8B-width layer (d 4096, 32/8 heads x 128) with Q4_K projections and a
     Q6_K attn_v: the int8-MFMA projections and the MFMA attention both apply"""

@@ -383,7 +383,7 @@ __global__ void __launch_bounds__(256) k_attn_combine_xq(AttnMArgs a, int nch, X
 
 bool attn_combine_xq_supported(int64_t hd, int64_t n_head) {
     const int64_t K = hd * n_head;
-    return (hd == 64 || hd == 128) && K % 4096 == 0 && K <= 16384;
+    return (hd == 64 || hd == 128) && K % 512 == 0 && K <= 16384;
 }
 
 bool attn_mfma_supported(int64_t hd, int kv_f16, int64_t M, int64_t n_head, int64_t n_kv) {

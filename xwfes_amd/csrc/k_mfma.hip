@@ -673,7 +673,7 @@ static float* xq_ssq(int8_t* xq, int64_t K) { return xq_ptrs(xq, K).ssq; }
 hipError_t launch_xq_prep(hipStream_t st, float* x, int64_t ldx, const float* normw,
                           const float* part, int S, int64_t ldpart, int64_t K, int64_t M,
                           int8_t* xq) {
-    if (K % 4096 || K > 16384) return hipErrorInvalidValue;
+    if (K % 512 || K > 16384) return hipErrorInvalidValue;
     int8_t* frag = xq;
     int8_t* xs32 = xq + K * 16;
     int8_t* xs16 = xs32 + K;
@@ -686,7 +686,7 @@ hipError_t launch_xq_prep(hipStream_t st, float* x, int64_t ldx, const float* no
 bool mv_swiglu_supported(int64_t K) { return K >= 256; }
 
 bool mv_supported(int dt, int64_t K, int64_t M) {
-    return (dt == FTX_Q4_K || dt == FTX_Q6_K) && M >= 1 && M <= 8 && K % 4096 == 0 &&
+    return (dt == FTX_Q4_K || dt == FTX_Q6_K) && M >= 1 && M <= 8 && K % 512 == 0 &&
            K <= 16384;
 }
 
@@ -730,7 +730,7 @@ hipError_t launch_mv(hipStream_t st, const GemvSeg* segs, int nseg, const int8_t
                      int64_t M, int epi, int cu_count, int normed, float eps,
                      const QkvEpi* qkv) {
     if (epi == EPI_QKV && (!qkv || nseg != 3 || qkv->hd % 2)) return hipErrorInvalidValue;
-    if (nseg < 1 || nseg > 3 || M < 1 || M > 8 || K % 4096 || K > 16384)
+    if (nseg < 1 || nseg > 3 || M < 1 || M > 8 || K % 512 || K > 16384)
         return hipErrorInvalidValue;
     if (epi == EPI_SWIGLU && (nseg != 2 || segs[0].N != segs[1].N || segs[0].dt != segs[1].dt ||
                               segs[0].rpt != segs[1].rpt || !mv_swiglu_supported(K)))
@@ -791,8 +791,15 @@ hipError_t launch_mv(hipStream_t st, const GemvSeg* segs, int nseg, const int8_t
         if (qkv) a.qkv = *qkv;
         // waves per unit: up to ~8 waves per CU over the launch (measured
         // best on the 8B shapes: gate/up W = 4, attention projections 8)
+        // (every wave takes a multiple of two super-blocks: the unrolled
+        // loop computes whole steps, so W doubles while 4 W divides nsb)
         int W = 1;
-        while (W < MV_WAVES && a.nsb % (2 * W) == 0 && units * W * 2 <= (int64_t)cus * 8) W *= 2;
+        while (W < MV_WAVES && a.nsb % (4 * W) == 0 && units * W * 2 <= (int64_t)cus * 8) W *= 2;
+        // the W > 1 epilogue gives each of the 8 * rpt outputs of a tile its
+        // own thread; where the block has fewer, one wave computes them all
+        int maxr = 0;
+        for (int i = 0; i < a.nseg; ++i) maxr = a.seg[i].rpt > maxr ? a.seg[i].rpt : maxr;
+        if (W > 1 && 64 * W < 8 * maxr) W = 1;
         const dim3 gd((unsigned)units), bd(64 * W);
         // single Q4_K tiles whose waves take 4 super-blocks: every weight in
         // flight at once (Q6_K's larger blocks do not fit four deep)
