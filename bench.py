@@ -142,7 +142,8 @@ def measured_traffic(workload, kernel_class):
             t = json.load(f)
     except (OSError, ValueError):
         return None
-    return t.get("bytes_per_launch") if t.get("class") == kernel_class else None
+    c = t.get("classes", {}).get(kernel_class)
+    return c.get("bytes_per_launch") if c else None
 
 
 def main():
