@@ -26,6 +26,8 @@ HBM_PEAK_GBS = 8000.0
 REPLAY = 20  # back-to-back issues of each dominant-class launch when timing it
 LLAMA3_8B = dict(n_layer=32, n_embd=4096, n_head=32, n_head_kv=8, head_dim=128, n_ff=14336,
                 vocab=128256, rope_theta=500000.0, rope_neox=0, rms_eps=1e-5)
+TINY_LLAMA = dict(n_layer=4, n_embd=512, n_head=8, n_head_kv=8, head_dim=64, n_ff=1408,
+                  vocab=32000, rope_theta=10000.0, rope_neox=0, rms_eps=1e-5)
 LLAMA32_1B = dict(n_layer=16, n_embd=2048, n_head=32, n_head_kv=8, head_dim=64, n_ff=8192,
                   vocab=128256, rope_theta=500000.0, rope_neox=0, rms_eps=1e-5)
 WORKLOADS = {
@@ -42,7 +44,52 @@ WORKLOADS = {
     # tokens a round (greedy); random weights, so the draft is rarely accepted
     "llama3-8b-q4km+1b-draft-spec4": dict(kind="generate", cfg=LLAMA3_8B, draft_cfg=LLAMA32_1B,
                                           mix="q4_k_m", ctx=0, M=4, P=8, N=32, temp=0.0),
+    # the reference's own CPU-runnable case: a 4-layer Q4_0 target (d 512,
+    # 8 x 64 heads, FFN 1408, vocab 32000, F32 embedding) and a 1-layer draft
+    # of the same shape, a 128-token prompt, 4 draft tokens a round, greedy
+    "tinyllama-q4_0+1l-draft-spec4": dict(kind="generate", cfg=TINY_LLAMA,
+                                          draft_cfg=dict(TINY_LLAMA, n_layer=1), mix="q4_0",
+                                          ctx=0, M=4, P=128, N=32, temp=0.0),
+    # tree: a 52-node draft tree (branching 4, 4, 2 from the root) at context
+    # 4096, ancestor-only attention, residual (SpecInfer) acceptance at T 0.8
+    # with Dirichlet(1) draft distributions; Q8_0 attention projections and a
+    # Q4_K FFN
+    "llama3-8b-q8attn-tree52-ctx4096": dict(kind="tree", cfg=LLAMA3_8B, mix="q8_0_attn", ctx=4096,
+                                            M=52, branching=(4, 4, 2), temp=0.8),
 }
+DTYPES = {"q4_k_m": "q4_k/q6_k weights, f16 KV, fp32 accumulate",
+          "q4_0": "q4_0 weights (f32 embedding), f16 KV, fp32 accumulate",
+          "q8_0_attn": "q8_0 attention / q4_k FFN / q6_k head weights, f16 KV, fp32 accumulate"}
+
+
+def mix_of(name, cfg):
+    from xwfes_amd import synth
+    return {"q4_k_m": lambda: synth.q4_k_m_mix(cfg),
+            "q4_0": lambda: synth.uniform_mix(synth.Q4_0, embd=synth.F32),
+            "q8_0_attn": lambda: synth.q8_attn_mix(cfg)}[name]()
+
+
+def draft_tree(V, branching, seed):
+    """A full draft tree (nodes in breadth-first order, parents[i] < i): each
+    node's children are drawn from one Dirichlet(1) distribution over the
+    vocab, which is every child's q row."""
+    rng = np.random.default_rng(seed)
+    parents, props, q = [], [], []
+    level = [-1]
+    for b in branching:
+        nxt = []
+        for par in level:
+            e = -np.log(rng.random(V))
+            dist = (e / e.sum()).astype(np.float32)
+            cdf = np.cumsum(dist.astype(np.float64))
+            for _ in range(b):
+                parents.append(par)
+                props.append(min(int(np.searchsorted(cdf, rng.random() * cdf[-1])), V - 1))
+                q.append(dist)
+                nxt.append(len(parents) - 1)
+        level = nxt
+    return (np.array(parents, np.int32), np.array(props, np.int32),
+            np.ascontiguousarray(np.stack(q)))
 
 
 def log(msg):
@@ -178,7 +225,7 @@ def main():
         src.free()
         dst.free()
     t0 = time.perf_counter()
-    tensors = synth.build(ctx, cfg, synth.q4_k_m_mix(cfg), seed=1)
+    tensors = synth.build(ctx, cfg, mix_of(W["mix"], cfg), seed=1)
     log("model built in %.1f s (%.3f GB of weights)" % (time.perf_counter() - t0,
                                                         synth.weight_bytes(tensors) / 1e9))
     kind = W["kind"]
@@ -189,7 +236,7 @@ def main():
     gen_stats = []
     if kind == "generate":
         dcfg = W["draft_cfg"]
-        dtensors = synth.build(ctx, dcfg, synth.q4_k_m_mix(dcfg), seed=2)
+        dtensors = synth.build(ctx, dcfg, mix_of(W["mix"], dcfg), seed=2)
         dmodel = ctx.model(dcfg, dtensors, max_tokens=8)
         dkv = dmodel.kv(P_tok + W["N"] + 32)
         drafter = spec.DraftModelDrafter(ctx, dmodel, dkv)
@@ -200,12 +247,19 @@ def main():
     ctx.fill_normal(vp, n_kv, seed=5, std=1.0, dtype=ftx.F16)
     logits = ctx.buffer(M * V * 4)
     base = ctx.buffer(V * 4)
-    if kind == "verify":
+    if kind in ("verify", "tree"):
         # the base row: logits of the last committed token (position ctx - 1)
         kv.truncate(ctx_len - 1)
         model.verify(kv, [int(np.random.default_rng(3).integers(V))], base.ptr, advance=True)
         ctx.sync()
     props, pd = draft(V, M, seed=6)
+    parents = qbuf = None
+    if kind == "tree":
+        parents, props, qrows = draft_tree(V, W["branching"], seed=6)
+        assert len(props) == M
+        qbuf = ctx.buffer(qrows.nbytes)
+        qbuf.write(qrows)
+        del qrows
     prompt = [int(t) for t in np.random.default_rng(8).integers(0, V, P_tok)]
     rng_state = [5, ftx.SAMPLER_SEED]
     accepted = []
@@ -217,6 +271,13 @@ def main():
             r = ctx.accept(base.ptr, logits.ptr, M, V, props, ftx.ACCEPT_RATIO, temp=temp,
                            rng=rng_state[0], pd=pd, sampler_state=rng_state[1])
             rng_state[0], rng_state[1] = r["rng"], r["sampler_state"]
+            accepted.append(len(r["accepted"]))
+        elif kind == "tree":
+            kv.truncate(ctx_len)
+            model.verify(kv, props, logits.ptr, parents=parents)
+            r = ctx.accept(base.ptr, logits.ptr, M, V, props, ftx.ACCEPT_RESIDUAL, temp=temp,
+                           rng=rng_state[0], parents=parents, q_ptr=qbuf.ptr)
+            rng_state[0] = r["rng"]
             accepted.append(len(r["accepted"]))
         elif kind == "decode":
             kv.truncate(ctx_len)
@@ -286,12 +347,18 @@ def main():
     gbs = sb / (ms_step * 1e-3) / 1e9
     metric = {"verify": "verify-step tokens/s + HBM GB/s (% of peak), 8B-shape Q4_K, K=8 draft, "
                         "1 GPU",
+              "tree": "tree verify-step tokens/s + HBM GB/s (% of peak), 8B-shape Q8_0 attention "
+                      "/ Q4_K FFN, 52-node draft tree, ctx 4096, 1 GPU",
               "decode": "decode tokens/s (Engine::step, M=1, ctx 2048), 8B-shape Q4_K, 1 GPU",
               "prefill": "prefill tokens/s (512-token prompt, chains of 8), 8B-shape Q4_K, "
                          "1 GPU",
-              "generate": "generated tokens/s (speculative: 8B-shape Q4_K target, 1B-shape "
-                          "draft, 4 draft tokens a round, greedy), 1 GPU"}[kind]
-    unit = {"verify": "verified tokens/s", "decode": "decoded tokens/s",
+              "generate": "generated tokens/s (speculative: %s target, %s draft, %d draft "
+                          "tokens a round, greedy), 1 GPU" % (
+                              W["mix"] + " %d-layer d%d" % (cfg["n_layer"], cfg["n_embd"]),
+                              "%d-layer d%d" % (W["draft_cfg"]["n_layer"],
+                                                W["draft_cfg"]["n_embd"]) if "draft_cfg" in W
+                              else "", M)}[kind]
+    unit = {"verify": "verified tokens/s", "tree": "verified tokens/s", "decode": "decoded tokens/s",
             "prefill": "prefilled tokens/s", "generate": "generated tokens/s"}[kind]
     out = {
         "metric": metric,
@@ -301,12 +368,12 @@ def main():
         "ms_per_step": round(ms_step, 4),
         "ms_per_step_median": round(med_ms, 4),
         "higher_is_better": True, "scaling": "weak", "vs_baseline": None,
-        "dtype": "q4_k/q6_k weights, f16 KV, fp32 accumulate",
+        "dtype": DTYPES[W["mix"]],
         "data": "synthetic: random-init N(0,0.02) weights quantised on device, N(0,1) fp16 KV, "
                 "Dirichlet(1) draft",
         "config": {"workload": args.workload, "kind": kind, "M": M, "ctx": ctx_len,
                    "prompt": P_tok, "layers": cfg["n_layer"], "d_model": cfg["n_embd"],
-                   "vocab": V, "mix": W["mix"], "accept": "ratio" if kind == "verify" else None,
+                   "vocab": V, "mix": W["mix"], "accept": {"verify": "ratio", "tree": "residual"}.get(kind),
                    "temperature": temp, "batch": 1},
         "step_bytes": sb,
         "hbm_gbs": round(gbs, 1),
@@ -339,6 +406,8 @@ def main():
         dkv.free()
         dmodel.free()
         synth.free(dtensors)
+    if qbuf is not None:
+        qbuf.free()
     logits.free()
     base.free()
     kv.free()

@@ -71,3 +71,34 @@ def test_argmax_prob(gctx, orc, V):
         assert t == orc.argmax(row)
         assert p == np.float32(orc.softmax_prob(row, t, 1.0))
     b.free()
+
+
+def test_generate_tiny_llama_q4_0(gctx, orc):
+    """The reference's own CPU-runnable case on the device: a 4-layer Q4_0
+    target (d 512, 8 x 64 heads, FFN 1408, vocab 32000, F32 embedding) with a
+    1-layer draft of the same shape, a 128-token prompt, 4 draft tokens a
+    round, greedy: the oracle's tokens and statistics exactly."""
+    cfg = P.model_cfg(4, 512, 8, 8, 64, 1408, 32000, rope_theta=10000.0)
+    dts = dict(tok_embd=P.F32, output=P.Q4_0, q=P.Q4_0, k=P.Q4_0, v=P.Q4_0, o=P.Q4_0,
+               gate=P.Q4_0, up=P.Q4_0, down=P.Q4_0)
+    target = P.make_model(orc, cfg, dts, seed=41)
+    target["out_norm"]["raw"] = np.full(512, 30.0, np.float32).view(np.uint8).copy()
+    draft = P.make_model(orc, dict(cfg, n_layer=1), dts, seed=42)
+    # the draft shares the target's embedding and (peaked) head, so its
+    # tokens pass the draft cut and are sometimes accepted
+    for nm in ("tok_embd", "output", "out_norm"):
+        draft[nm] = target[nm]
+    tm, dm = upload(gctx, target), upload(gctx, draft)
+    cap = 256
+    tkv, dkv = tm.kv(cap), dm.kv(cap)
+    drafter = spec.DraftModelDrafter(gctx, dm, dkv)
+    prompt = [int(t) for t in np.random.default_rng(43).integers(0, 32000, 128)]
+    try:
+        got, st = spec.generate(gctx, tm, tkv, drafter, prompt, 24, spec_k=4, temp=0.0)
+    finally:
+        drafter.free()
+    want, sto = orc.generate(target, draft, prompt, 24, spec_k=4, temp=0.0, cap=cap)
+    assert got == want, (st, sto, got, want)
+    assert st == sto and st["drafted"] > 0
+    for x in (tkv, dkv, tm, dm):
+        x.free()

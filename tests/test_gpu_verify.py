@@ -239,6 +239,63 @@ def test_verify_8b_shape_two_layers(gctx, orc):
     assert rel_err_rows(got, want) < LOGIT_TOL
 
 
+def tree_parents(branching):
+    """Parents of a full draft tree in breadth-first order."""
+    parents, level = [], [-1]
+    for b in branching:
+        nxt = []
+        for par in level:
+            for _ in range(b):
+                parents.append(par)
+                nxt.append(len(parents) - 1)
+        level = nxt
+    return parents
+
+
+def test_verify_8b_tree52_q8_attention(gctx, orc):
+    """The tree workload's shape: 8B layers (d 4096, 32/8 heads x 128, FFN
+    14336) with Q8_0 attention projections and a Q4_K FFN, 2 layers, a
+    52-node draft tree (branching 4, 4, 2) at context 4096, then residual
+    acceptance of the device's logits against the oracle's on the same rows.
+    (Vocabulary 32000 and a Q6_K head keep the oracle's head short.)"""
+    orc.set_threads(16)
+    V = 32000
+    cfg = P.model_cfg(2, 4096, 32, 8, 128, 14336, V, rope_theta=500000.0)
+    model = {"cfg": dict(cfg)}
+    rng = np.random.default_rng(52)
+
+    def q(rows, cols, dt):
+        u = min(rows, 2048)
+        w = (rng.standard_normal((u, cols)) * 0.02).astype(np.float32)
+        raw = np.tile(orc.quantize(w, dt), -(-rows // u))[: rows * P.row_bytes(dt, cols)]
+        return dict(raw=np.ascontiguousarray(raw), dtype=dt, ne0=cols, ne1=rows)
+
+    ones = np.ones(4096, np.float32).view(np.uint8).copy()
+    model["tok_embd"] = q(V, 4096, P.Q4_K)
+    model["output"] = q(V, 4096, P.Q6_K)
+    model["out_norm"] = dict(raw=ones, dtype=P.F32, ne0=4096, ne1=1)
+    for l in range(2):
+        p = "blk.%d." % l
+        model[p + "attn_norm"] = dict(raw=ones, dtype=P.F32, ne0=4096, ne1=1)
+        model[p + "ffn_norm"] = dict(raw=ones, dtype=P.F32, ne0=4096, ne1=1)
+        for nm, rows, cols in (("q", 4096, 4096), ("k", 1024, 4096), ("v", 1024, 4096),
+                               ("o", 4096, 4096)):
+            model[p + nm] = q(rows, cols, P.Q8_0)
+        for nm in ("gate", "up", "down"):
+            model[p + nm] = q(14336, 4096, P.Q4_K)
+    parents = tree_parents((4, 4, 2))
+    assert len(parents) == 52
+    toks = rng.integers(0, V, 52).tolist()
+    got, want, _, _ = run_both(gctx, orc, model, toks, 4096, 4096 + 64, parents=parents)
+    assert rel_err_rows(got, want) < LOGIT_TOL
+    base = (rng.standard_normal(V) * 2).astype(np.float32)
+    qd = rng.dirichlet(np.ones(V), size=52).astype(np.float32)
+    props = np.array(toks, np.int32)
+    g, o = accept_both(gctx, orc, base, got, props, ftx.ACCEPT_RESIDUAL, 0.8, 77,
+                       parents=parents, q=qd)
+    assert (g["accepted"], g["bonus"], g["rng"]) == (o["accepted"], o["bonus"], o["rng"])
+
+
 @pytest.mark.parametrize("d,ff,hd", [(2048, 8192, 64), (3072, 8192, 128), (512, 1024, 64)])
 def test_verify_narrow_widths(gctx, orc, d, ff, hd):
     """Widths below 4096 on the MFMA row-dot path (Llama-3.2-1B: d 2048, head

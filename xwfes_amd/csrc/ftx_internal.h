@@ -122,12 +122,15 @@ struct GemvSeg {
     int rpt = 0;
 };
 enum { EPI_STORE = 0, EPI_ACCUM = 1 };
+// fp16_range: the activations and dequantised weights lie within the fp16
+// range, so the MFMA form (fp16 hi + lo operands) may run
 hipError_t launch_gemv(hipStream_t st, const GemvSeg* segs, int nseg, const float* x,
-                       int64_t ldx, int64_t K, int64_t M, int epi);
+                       int64_t ldx, int64_t K, int64_t M, int epi, bool fp16_range = false);
 // gate/up pair with SwiGLU epilogue: h[m*ldh + n] = silu(x.g_n) * (x.u_n)
 hipError_t launch_gemv_swiglu(hipStream_t st, const uint8_t* Wg, const uint8_t* Wu, int dt,
                               int64_t row_bytes, int64_t N, const float* x, int64_t ldx,
-                              int64_t K, int64_t M, float* h, int64_t ldh);
+                              int64_t K, int64_t M, float* h, int64_t ldh,
+                              bool fp16_range = false);
 // y[m*ldy + j] += sum_i h[m*ldh + i] W[i, j] (W n_in rows x N cols)
 // uses `part` scratch of down_scratch_floats(...) floats
 size_t down_scratch_floats(int64_t M, int64_t n_in, int64_t N);

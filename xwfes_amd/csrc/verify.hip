@@ -497,9 +497,9 @@ int ftx_verify_step(ftx_ctx* ctx, ftx_model* m, ftx_kv* kv, const ftx_verify_arg
         if (epi == EPI_SWIGLU)
             TRACED(kind, bytes,
                    launch_gemv_swiglu(st, segs[0].W, segs[1].W, segs[0].dt, segs[0].row_bytes,
-                                      segs[0].N, src, lds, K, M, segs[0].y, segs[0].ldy));
+                                      segs[0].N, src, lds, K, M, segs[0].y, segs[0].ldy, true));
         else
-            TRACED(kind, bytes, launch_gemv(st, segs, nseg, src, lds, K, M, epi));
+            TRACED(kind, bytes, launch_gemv(st, segs, nseg, src, lds, K, M, epi, true));
         return FTX_OK;
     };
     auto seg = [](const ftx_tensor* t, float* y, int64_t ldy) {
@@ -590,14 +590,29 @@ int ftx_verify_step(ftx_ctx* ctx, ftx_model* m, ftx_kv* kv, const ftx_verify_arg
                      D, m->norms + (l * 2 + 1) * D, tgu, gu, 2, D, EPI_SWIGLU, lt, ix_gu);
         if (rc) return rc;
         const double down_b = wbytes(T[FTX_T_DOWN]) + Md * F * f4 + 2 * Md * D * f4;
-        if (m->down_tiled[l] && down_mfma_supported(T[FTX_T_DOWN]->dtype, F, D, M))
+        if (m->down_tiled[l] && down_mfma_supported(T[FTX_T_DOWN]->dtype, F, D, M)) {
             TRACED_IDEM(TK_DOWN, down_b,
                         launch_down_mfma(st, T[FTX_T_DOWN]->dtype, m->down_tiled[l], F, D, m->h,
                                          F, M, m->x, D, m->downpart, ctx->cu_count, &fold_S));
-        else
+        } else if (m->down_tiled[l] && down_mfma_supported(T[FTX_T_DOWN]->dtype, F, D, 8)) {
+            // more than 8 tokens: the MFMA down kernel on 8-row chunks, each
+            // chunk's split partials added into x before the next
+            auto chunks = [&]() -> hipError_t {
+                for (int64_t c0 = 0; c0 < M; c0 += 8) {
+                    const int64_t mc = M - c0 < 8 ? M - c0 : 8;
+                    hipError_t e = launch_down_mfma(st, T[FTX_T_DOWN]->dtype, m->down_tiled[l], F,
+                                                    D, m->h + c0 * F, F, mc, m->x + c0 * D, D,
+                                                    m->downpart, ctx->cu_count, nullptr);
+                    if (e != hipSuccess) return e;
+                }
+                return hipSuccess;
+            };
+            TRACED(TK_DOWN, down_b, chunks());
+        } else {
             TRACED(TK_DOWN, down_b,
                    launch_down(st, T[FTX_T_DOWN]->data, T[FTX_T_DOWN]->dtype,
                                T[FTX_T_DOWN]->row_bytes, F, D, m->h, F, M, m->x, D, m->part));
+        }
     }
     // the LM head (skipped without a logits buffer: every layer's K / V rows
     // are written by now, which is all a prefill chunk needs)

@@ -52,6 +52,16 @@ def q4_k_m_mix(cfg):
     return dtype
 
 
+def q8_attn_mix(cfg):
+    """Q8_0 attention projections (q, k, v, o), Q6_K output, Q4_K FFN."""
+    def dtype(name):
+        key = name.split(".")[-1]
+        if key == "output":
+            return Q6_K
+        return Q8_0 if key in ("q", "k", "v", "o") else Q4_K
+    return dtype
+
+
 def uniform_mix(dt, embd=None):
     def dtype(name):
         if name == "tok_embd" and embd is not None:
