@@ -487,6 +487,36 @@ int ftx_verify_step(ftx_ctx* ctx, ftx_model* m, ftx_kv* kv, const ftx_verify_arg
                    launch_part_reduce(st, m->downpart, fold_S, D, M, m->x, D));
             fold_S = 0;
         }
+        // more than 8 tokens on tiled K-quant weights (not the fused qkv
+        // epilogue): the row-dot MFMA kernel on 8-row chunks, each with its
+        // own activation prep
+        bool tiled_all = epi != EPI_QKV && M > 8 && mv_all(ts, nseg, K, 8) &&
+                         (epi != EPI_SWIGLU || mv_swiglu_supported(K));
+        for (int i = 0; tiled_all && i < nseg; ++i) tiled_all = m->mvt[tix0 + tix[i]] != nullptr;
+        if (tiled_all) {
+            auto chunks = [&]() -> hipError_t {
+                for (int64_t c0 = 0; c0 < M; c0 += 8) {
+                    const int64_t mc = M - c0 < 8 ? M - c0 : 8;
+                    hipError_t e = launch_xq_prep(st, xin + c0 * ldx, ldx, normw, nullptr, 0, D,
+                                                  K, mc, m->xq);
+                    if (e != hipSuccess) return e;
+                    GemvSeg cs[3];
+                    for (int i = 0; i < nseg; ++i) {
+                        cs[i] = segs[i];
+                        cs[i].W = m->mvt[tix0 + tix[i]];
+                        cs[i].tiled = 1;
+                        cs[i].rpt = m->mvt_rpt[tix0 + tix[i]];
+                        if (cs[i].y) cs[i].y += c0 * cs[i].ldy;
+                    }
+                    e = launch_mv(st, cs, nseg, m->xq, K, mc, epi, ctx->cu_count,
+                                  normw != nullptr, eps, nullptr);
+                    if (e != hipSuccess) return e;
+                }
+                return hipSuccess;
+            };
+            TRACED(kind, bytes, chunks());
+            return FTX_OK;
+        }
         const float* src = xin;
         int64_t lds = ldx;
         if (normw) {
