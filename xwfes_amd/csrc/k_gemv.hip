@@ -190,14 +190,14 @@ __global__ void __launch_bounds__(256) k_down_reduce(const float* __restrict__ p
 // 2^-22 of a product).  Inputs must lie within the fp16 range (the
 // normalised activations, attention outputs and weights of the verify step).
 // Workgroup: 16 output rows (and the matching up rows of a SwiGLU pair), all
-// MTI m-tiles; its 4 waves split the contraction into quarters, each reading
+// MTI m-tiles; its 8 waves split the contraction into eighths, each reading
 // its activation fragments straight from global memory (L2-resident), and
-// the quarters are added in LDS in wave order.
+// the slices are added in LDS in wave order.
 
 typedef _Float16 v8h_t __attribute__((ext_vector_type(8)));
 typedef float v4f_t __attribute__((ext_vector_type(4)));
 
-constexpr int GQ = 4;   // contraction quarters (waves)
+constexpr int GQ = 8;   // contraction slices (waves)
 constexpr int GU = 2;   // 32-column steps whose loads are issued together
 constexpr int GK = GQ * GU * 32;  // K must be a multiple of this
 
@@ -212,7 +212,7 @@ __device__ __forceinline__ void split8(const float* w, v8h_t& hi, v8h_t& lo) {
 }
 
 template <int MTI, bool PAIR>
-__global__ void __launch_bounds__(256) k_gemm_rows(Segs segs, const float* __restrict__ x,
+__global__ void __launch_bounds__(64 * GQ) k_gemm_rows(Segs segs, const float* __restrict__ x,
                                                    int64_t ldx, int64_t K, int64_t M, int epi) {
     constexpr int NT = PAIR ? 2 : 1;
     __shared__ v4f_t red[GQ - 1][NT][MTI][64];
@@ -289,7 +289,7 @@ __global__ void __launch_bounds__(256) k_gemm_rows(Segs segs, const float* __res
             }
         }
     }
-    // the quarters added in wave order: waves 1..3 hand theirs to wave 0
+    // the slices added in wave order: waves 1..7 hand theirs to wave 0
     if (w > 0) {
 #pragma unroll
         for (int t = 0; t < NT; ++t)
@@ -358,7 +358,7 @@ int64_t down_splits(int64_t M, int64_t n_in, int64_t N) {
     return S;
 }
 
-// the MFMA form needs K a multiple of 256 (whole steps in every quarter) and
+// the MFMA form needs K a multiple of 512 (whole steps in every slice) and
 // 16-byte aligned activation rows; it runs for more than 8 activation rows,
 // or for at least 16384 output rows (below that the one-wave-per-row kernel
 // fills the device better)
