@@ -122,6 +122,11 @@ struct GemvSeg {
     int rpt = 0;
 };
 enum { EPI_STORE = 0, EPI_ACCUM = 1 };
+// planar Q8_0 / Q4_0 copies (scales, then quants; the generic kernels read
+// them through dq8): the internal dtype for a tensor of ncols columns, or -1
+int planar_dtype(int dt, int64_t ncols);
+hipError_t launch_planar(hipStream_t st, const uint8_t* src, int dt, int64_t nrows, int64_t ncols,
+                         uint8_t* dst);
 // fp16_range: the activations and dequantised weights lie within the fp16
 // range, so the MFMA form (fp16 hi + lo operands) may run
 hipError_t launch_gemv(hipStream_t st, const GemvSeg* segs, int nseg, const float* x,

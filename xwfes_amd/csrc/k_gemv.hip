@@ -367,7 +367,36 @@ bool gemm_rows_ok(const float* x, int64_t ldx, int64_t K, int64_t M, int64_t row
            (M > 8 || rows >= 16384);
 }
 
+// planar copy of Q8_0 / Q4_0 rows: thread per (row, block)
+__global__ void __launch_bounds__(256) k_planar(const uint8_t* __restrict__ src, int64_t nrows,
+                                                int64_t nb, int qb, uint8_t* __restrict__ dst) {
+    const int64_t t = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
+    if (t >= nrows * nb) return;
+    const int64_t r = t / nb, b = t % nb;
+    const int64_t rb = nb * (2 + qb);
+    const uint8_t* s = src + r * rb + b * (2 + qb);
+    uint8_t* d = dst + r * rb;
+    d[2 * b] = s[0];
+    d[2 * b + 1] = s[1];
+    for (int i = 0; i < qb; ++i) d[2 * nb + b * qb + i] = s[2 + i];
+}
+
 }  // namespace
+
+int planar_dtype(int dt, int64_t ncols) {
+    if (ncols % 128) return -1;
+    return dt == FTX_Q8_0 ? FTX_Q8_0_PLANAR : (dt == FTX_Q4_0 ? FTX_Q4_0_PLANAR : -1);
+}
+
+hipError_t launch_planar(hipStream_t st, const uint8_t* src, int dt, int64_t nrows, int64_t ncols,
+                         uint8_t* dst) {
+    if (planar_dtype(dt, ncols) < 0) return hipErrorInvalidValue;
+    const int64_t nb = ncols / 32, total = nrows * nb;
+    const int qb = dt == FTX_Q8_0 ? 32 : 16;
+    hipLaunchKernelGGL(k_planar, dim3((unsigned)((total + 255) / 256)), dim3(256), 0, st, src,
+                       nrows, nb, qb, dst);
+    return hipGetLastError();
+}
 
 hipError_t launch_gemv(hipStream_t st, const GemvSeg* segs, int nseg, const float* x,
                        int64_t ldx, int64_t K, int64_t M, int epi, bool fp16_range) {

@@ -13,6 +13,13 @@
 
 #include "../../include/ftx.h"
 
+// Internal planar layouts of Q8_0 / Q4_0 rows (same bytes as the GGUF row,
+// reordered): the row's fp16 scales first, then its quants, so that 8
+// elements are one aligned 8-byte (Q8_0) or 4-byte (Q4_0) load when the
+// row holds a multiple of 4 blocks.  Never seen outside the library.
+constexpr int FTX_Q8_0_PLANAR = 108;
+constexpr int FTX_Q4_0_PLANAR = 102;
+
 __device__ __forceinline__ float h2f(uint16_t h) {
     return (float)__builtin_bit_cast(_Float16, h);
 }
@@ -127,6 +134,27 @@ __device__ inline void dq8(const uint8_t* __restrict__ row, int dt, int64_t e0, 
                 const int j = j0 + i;
                 const uint8_t b = p[2 + (j >> 1)];
                 const int nib = (j & 1) ? (b >> 4) : (b & 0xF);
+                o[i] = e0 + i < n ? d * (float)(nib - 8) : 0.f;
+            }
+            return;
+        }
+        case FTX_Q8_0_PLANAR: {
+            const float d = h2f(((const uint16_t*)row)[e0 >> 5]);
+            const uint2 q = *(const uint2*)(row + 2 * (n >> 5) + e0);
+#pragma unroll
+            for (int i = 0; i < 8; ++i) {
+                const uint32_t wd = i < 4 ? q.x : q.y;
+                o[i] = e0 + i < n ? d * (float)(int8_t)((wd >> (8 * (i & 3))) & 0xFF) : 0.f;
+            }
+            return;
+        }
+        case FTX_Q4_0_PLANAR: {
+            const float d = h2f(((const uint16_t*)row)[e0 >> 5]);
+            const uint32_t q = *(const uint32_t*)(row + 2 * (n >> 5) + (e0 >> 1));
+#pragma unroll
+            for (int i = 0; i < 8; ++i) {
+                // element j: nibble (j & 1) of byte j / 2 (reference order)
+                const int nib = (int)((q >> (8 * (i >> 1) + 4 * (i & 1))) & 0xF);
                 o[i] = e0 + i < n ? d * (float)(nib - 8) : 0.f;
             }
             return;

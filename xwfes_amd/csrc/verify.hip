@@ -40,6 +40,10 @@ struct ftx_model {
     // tensor] and the LM head last (null where the kernel does not apply)
     std::vector<uint8_t*> mvt;
     std::vector<int> mvt_rpt;
+    // planar copies of Q8_0 / Q4_0 projections for the generic kernels (same
+    // indexing; null where they do not apply) and their internal dtypes
+    std::vector<uint8_t*> pln;
+    std::vector<int> pln_dt;
     float* downpart = nullptr;
 };
 
@@ -87,6 +91,8 @@ static void model_release(ftx_model* m) {
     for (uint8_t* b : m->down_tiled)
         if (b) (void)hipFree(b);
     for (uint8_t* b : m->mvt)
+        if (b) (void)hipFree(b);
+    for (uint8_t* b : m->pln)
         if (b) (void)hipFree(b);
     if (m->downpart) (void)hipFree(m->downpart);
     delete m;
@@ -200,6 +206,27 @@ int ftx_model_create(ftx_ctx* ctx, const ftx_model_desc* d, ftx_model** out) {
         m->mvt_rpt[i] = rpt;
         if (launch_mv_tile(ctx->stream, w->data, w->row_bytes, w->dtype, w->nrows, w->ne[0], rpt,
                            buf) != hipSuccess)
+            ok = false;
+    }
+    m->pln.assign(nmvt, nullptr);
+    m->pln_dt.assign(nmvt, -1);
+    for (size_t i = 0; ok && i < nmvt; ++i) {
+        const int t = (int)(i % FTX_LAYER_TENSORS);
+        const bool head = i + 1 == nmvt;
+        if (!head && t != FTX_T_Q && t != FTX_T_K && t != FTX_T_V && t != FTX_T_O &&
+            t != FTX_T_GATE && t != FTX_T_UP)
+            continue;
+        const ftx_tensor* w = head ? (d->output ? d->output : d->tok_embd) : d->layers[i];
+        const int pdt = planar_dtype(w->dtype, w->ne[0]);
+        if (pdt < 0 || w->row_bytes * 32 != w->ne[0] * (w->dtype == FTX_Q8_0 ? 34 : 18)) continue;
+        uint8_t* buf = nullptr;
+        if (!dalloc(&buf, (size_t)(w->row_bytes * w->nrows))) {
+            ok = false;
+            break;
+        }
+        m->pln[i] = buf;
+        m->pln_dt[i] = pdt;
+        if (launch_planar(ctx->stream, w->data, w->dtype, w->nrows, w->ne[0], buf) != hipSuccess)
             ok = false;
     }
     if (!ok) {
@@ -516,6 +543,13 @@ int ftx_verify_step(ftx_ctx* ctx, ftx_model* m, ftx_kv* kv, const ftx_verify_arg
             };
             TRACED(kind, bytes, chunks());
             return FTX_OK;
+        }
+        // the planar copies where every segment has one
+        bool pl_all = true;
+        for (int i = 0; i < nseg; ++i) pl_all = pl_all && m->pln[tix0 + tix[i]] != nullptr;
+        for (int i = 0; pl_all && i < nseg; ++i) {
+            segs[i].W = m->pln[tix0 + tix[i]];
+            segs[i].dt = m->pln_dt[tix0 + tix[i]];
         }
         const float* src = xin;
         int64_t lds = ldx;
