@@ -137,17 +137,25 @@ __global__ void __launch_bounds__(256) k_down_part(const uint8_t* __restrict__ W
     for (int m = 0; m < MT; ++m)
 #pragma unroll
         for (int k = 0; k < 8; ++k) acc[m][k] = 0.f;
-    for (int64_t i = i0; i < i1; ++i) {
-        float w[8];
-        dq8(W + i * row_bytes, dt, c * 8, N, w);
+    // four rows a pass: every load of the pass is issued before its
+    // arithmetic (rows past the range read the last row with a zero factor)
+    constexpr int RU = 4;
+    for (int64_t ib = i0; ib < i1; ib += RU) {
+        float w[RU][8], hv[RU][MT];
 #pragma unroll
-        for (int m = 0; m < MT; ++m) {
-            if (m < mc) {
-                const float v = h[(m0 + m) * ldh + i];
+        for (int u = 0; u < RU; ++u) {
+            const int64_t i = ib + u < i1 ? ib + u : i1 - 1;
+            dq8(W + i * row_bytes, dt, c * 8, N, w[u]);
 #pragma unroll
-                for (int k = 0; k < 8; ++k) acc[m][k] += v * w[k];
-            }
+            for (int m = 0; m < MT; ++m)
+                hv[u][m] = (m < mc && ib + u < i1) ? h[(m0 + m) * ldh + i] : 0.f;
         }
+#pragma unroll
+        for (int u = 0; u < RU; ++u)
+#pragma unroll
+            for (int m = 0; m < MT; ++m)
+#pragma unroll
+                for (int k = 0; k < 8; ++k) acc[m][k] += hv[u][m] * w[u][k];
     }
     const int64_t S = gridDim.y;
     for (int m = 0; m < mc; ++m) {
@@ -350,10 +358,10 @@ hipError_t launch_gemm_rows(hipStream_t st, const Segs& s, int64_t rows, const f
 int64_t down_splits(int64_t M, int64_t n_in, int64_t N) {
     const int64_t groups = (N + 7) / 8;
     const int64_t mch = (M + MT - 1) / MT;
-    // about 16k threads over the splits, at most 32 partials per output
+    // about 16k threads over the splits, at most 64 partials per output
     int64_t S = (16384 + groups * mch - 1) / (groups * mch);
     if (S > n_in) S = n_in;
-    if (S > 32) S = 32;
+    if (S > 64) S = 64;
     if (S < 1) S = 1;
     return S;
 }
