@@ -176,14 +176,14 @@ __global__ void __launch_bounds__(256) k_down_reduce(const float* __restrict__ p
     const int64_t m = t / N, j = t % N;
     float s = 0.f;
     // split order (the loads issued ahead of the adds)
+    constexpr int RB = 16;
     int64_t k = 0;
-    for (; k + 4 <= S; k += 4) {
-        const float p0 = part[(k * M + m) * N + j], p1 = part[((k + 1) * M + m) * N + j];
-        const float p2 = part[((k + 2) * M + m) * N + j], p3 = part[((k + 3) * M + m) * N + j];
-        s += p0;
-        s += p1;
-        s += p2;
-        s += p3;
+    for (; k + RB <= S; k += RB) {
+        float p[RB];
+#pragma unroll
+        for (int u = 0; u < RB; ++u) p[u] = part[((k + u) * M + m) * N + j];
+#pragma unroll
+        for (int u = 0; u < RB; ++u) s += p[u];
     }
     for (; k < S; ++k) s += part[(k * M + m) * N + j];
     y[m * ldy + j] += s;
