@@ -41,14 +41,14 @@ __global__ void __launch_bounds__(256) k_rmsnorm(const float* __restrict__ x,
     const float* xr = x + m * d;
     float ss = 0.f;
     for (int64_t i = threadIdx.x; i < d; i += 256) ss += xr[i] * xr[i];
-    __shared__ float red[256];
-    red[threadIdx.x] = ss;
+    // wave sums by shuffles, then the four waves' sums in wave order
+#pragma unroll
+    for (int o = 32; o > 0; o >>= 1) ss += __shfl_xor(ss, o, 64);
+    __shared__ float red[4];
+    if ((threadIdx.x & 63) == 0) red[threadIdx.x >> 6] = ss;
     __syncthreads();
-    for (int o = 128; o > 0; o >>= 1) {
-        if (threadIdx.x < o) red[threadIdx.x] += red[threadIdx.x + o];
-        __syncthreads();
-    }
-    const float inv = 1.f / sqrtf(red[0] / (float)d + eps);
+    const float tot = ((red[0] + red[1]) + red[2]) + red[3];
+    const float inv = 1.f / sqrtf(tot / (float)d + eps);
     float* orow = out + m * d;
     for (int64_t i = threadIdx.x; i < d; i += 256) orow[i] = xr[i] * inv * w[i];
 }
