@@ -189,7 +189,8 @@ bool down_mfma_supported(int dt, int64_t n_in, int64_t N, int64_t M);
 size_t down_tiled_bytes(int dt, int64_t n_in, int64_t N);
 hipError_t launch_down_tile(hipStream_t st, const uint8_t* src, int64_t src_row_bytes, int dt,
                             int64_t n_in, int64_t N, uint8_t* dst);
-size_t down_mfma_part_floats(int64_t n_in, int64_t N, int cu_count);
+// split partials of launch_down_mfma for up to Mmax rows in 8-row chunks
+size_t down_mfma_part_floats(int dt, int64_t n_in, int64_t N, int64_t Mmax, int cu_count);
 // splits == null: the split partials are added into y here; otherwise the
 // partials are left in part[S][8][N] for the caller to fold and *splits = S
 hipError_t launch_down_mfma(hipStream_t st, int dt, const uint8_t* tiled, int64_t n_in, int64_t N,

@@ -452,10 +452,30 @@ hipError_t launch_down_tile(hipStream_t st, const uint8_t* src, int64_t src_row_
     return hipGetLastError();
 }
 
-size_t down_mfma_part_floats(int64_t n_in, int64_t N, int cu_count) {
-    (void)cu_count;
-    (void)n_in;
-    return (size_t)64 * 8 * N;
+// split count of launch_down_mfma for a shape (the same for every M) and its
+// slices per split (a whole number of batches)
+static int64_t down_mfma_splits(int dt, int64_t n_in, int64_t N, int cu_count,
+                                int64_t* slices_per_split = nullptr) {
+    const int64_t nslices = n_in / 32, nsb = N / 256;
+    const int NB = dt == FTX_Q4_K ? DownCfg<FTX_Q4_K>::NB : DownCfg<FTX_Q6_K>::NB;
+#ifdef DOWN_PER_CU
+    const int64_t per_cu = DOWN_PER_CU;
+#else
+    const int64_t per_cu = 1;
+#endif
+    int64_t S = (per_cu * (int64_t)(cu_count > 0 ? cu_count : 256) + nsb - 1) / nsb;
+    if (S > 64) S = 64;
+    if (S > nslices) S = nslices;
+    if (S < 1) S = 1;
+    int64_t spp = (nslices + S - 1) / S;
+    spp = (spp + NB - 1) / NB * NB;
+    if (slices_per_split) *slices_per_split = spp;
+    return (nslices + spp - 1) / spp;
+}
+
+size_t down_mfma_part_floats(int dt, int64_t n_in, int64_t N, int64_t Mmax, int cu_count) {
+    const int64_t S = down_mfma_splits(dt, n_in, N, cu_count);
+    return (size_t)(((Mmax + 7) / 8) * S * 8 * N);
 }
 
 hipError_t launch_down_mfma(hipStream_t st, int dt, const uint8_t* tiled, int64_t n_in, int64_t N,
@@ -478,20 +498,9 @@ hipError_t launch_down_mfma(hipStream_t st, int dt, const uint8_t* tiled, int64_
     // on the 8B shapes: more splits add partial traffic for the next prep to
     // fold and shorten each range), at most 64, each a whole number of slice
     // batches
-    const int NB = dt == FTX_Q4_K ? DownCfg<FTX_Q4_K>::NB : DownCfg<FTX_Q6_K>::NB;
-#ifdef DOWN_PER_CU
-    const int64_t per_cu = DOWN_PER_CU;
-#else
-    const int64_t per_cu = 1;
-#endif
-    int64_t S = (per_cu * (int64_t)(cu_count > 0 ? cu_count : 256) + nsb - 1) / nsb;
-    if (S > 64) S = 64;
-    if (S > nslices) S = nslices;
-    if (S < 1) S = 1;
-    int64_t spp = (nslices + S - 1) / S;
-    spp = (spp + NB - 1) / NB * NB;
+    int64_t spp = 0;
+    const int64_t S = down_mfma_splits(dt, n_in, N, cu_count, &spp);
     a.slices_per_split = (int)spp;
-    S = (nslices + spp - 1) / spp;
     a.part = part;
     const dim3 grid((unsigned)nsb, (unsigned)S);
     if (dt == FTX_Q4_K)

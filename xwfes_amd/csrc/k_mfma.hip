@@ -656,9 +656,11 @@ __global__ void __launch_bounds__(256) k_part_reduce(const float* __restrict__ p
     const int64_t t = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
     const int m = blockIdx.y;
     if (t >= N) return;
+    // rows past 8 read the partials of their own 8-row chunk, chunks S * 8 * N apart
+    const float* pc = part + (int64_t)(m >> 3) * S * 8 * N;
     float v = 0.f;
 #pragma unroll 8
-    for (int s = 0; s < S; ++s) v += part[((int64_t)s * 8 + m) * N + t];
+    for (int s = 0; s < S; ++s) v += pc[((int64_t)s * 8 + (m & 7)) * N + t];
     y[(int64_t)m * ldy + t] += v;
 }
 
@@ -690,7 +692,8 @@ bool mv_supported(int dt, int64_t K, int64_t M) {
            K <= 16384;
 }
 
-// y[m*ldy + n] += sum_s part[s][m][n] for n < N, m < M (part rows of 8)
+// y[m*ldy + n] += sum_s part[c][s][m % 8][n] for n < N, m < M, c = m / 8
+// (the split partials of 8-row chunks, one after another)
 hipError_t launch_part_reduce(hipStream_t st, const float* part, int S, int64_t N, int64_t M,
                               float* y, int64_t ldy) {
     hipLaunchKernelGGL(k_part_reduce, dim3((unsigned)((N + 255) / 256), (unsigned)M), dim3(256), 0,

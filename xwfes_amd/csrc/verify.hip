@@ -183,7 +183,12 @@ int ftx_model_create(ftx_ctx* ctx, const ftx_model_desc* d, ftx_model** out) {
             hipSuccess)
             ok = false;
     }
-    if (ok && any_tiled) ok = dalloc(&m->downpart, down_mfma_part_floats(d->n_ff, D, ctx->cu_count));
+    if (ok && any_tiled) {
+        size_t pf = 0;
+        for (int dt : {FTX_Q4_K, FTX_Q6_K})
+            pf = std::max(pf, down_mfma_part_floats(dt, d->n_ff, D, Mmax, ctx->cu_count));
+        ok = dalloc(&m->downpart, pf);
+    }
     // row-dot projections and the LM head: tiled copies for the MFMA kernel
     const size_t nmvt = (size_t)(d->n_layer * FTX_LAYER_TENSORS + 1);
     m->mvt.assign(nmvt, nullptr);
@@ -659,17 +664,21 @@ int ftx_verify_step(ftx_ctx* ctx, ftx_model* m, ftx_kv* kv, const ftx_verify_arg
                         launch_down_mfma(st, T[FTX_T_DOWN]->dtype, m->down_tiled[l], F, D, m->h,
                                          F, M, m->x, D, m->downpart, ctx->cu_count, &fold_S));
         } else if (m->down_tiled[l] && down_mfma_supported(T[FTX_T_DOWN]->dtype, F, D, 8)) {
-            // more than 8 tokens: the MFMA down kernel on 8-row chunks, each
-            // chunk's split partials added into x before the next
+            // more than 8 tokens: the MFMA down kernel on 8-row chunks, every
+            // chunk's split partials added into x by one reduce
             auto chunks = [&]() -> hipError_t {
+                int S = 0;
                 for (int64_t c0 = 0; c0 < M; c0 += 8) {
                     const int64_t mc = M - c0 < 8 ? M - c0 : 8;
+                    // chunk c's partials at downpart + c * S * 8 * D (S is the
+                    // same for every chunk: it depends on the shape only)
+                    float* pc = m->downpart + (S ? (c0 / 8) * (int64_t)S * 8 * D : 0);
                     hipError_t e = launch_down_mfma(st, T[FTX_T_DOWN]->dtype, m->down_tiled[l], F,
-                                                    D, m->h + c0 * F, F, mc, m->x + c0 * D, D,
-                                                    m->downpart, ctx->cu_count, nullptr);
+                                                    D, m->h + c0 * F, F, mc, m->x + c0 * D, D, pc,
+                                                    ctx->cu_count, &S);
                     if (e != hipSuccess) return e;
                 }
-                return hipSuccess;
+                return launch_part_reduce(st, m->downpart, S, D, M, m->x, D);
             };
             TRACED(TK_DOWN, down_b, chunks());
         } else {
