@@ -148,6 +148,8 @@ hipError_t launch_down(hipStream_t st, const uint8_t* W, int dt, int64_t row_byt
 // (written back) and takes an RMSNorm weight; a normed operand is consumed
 // with launch_mv(..., normed = 1, eps).
 size_t xq_bytes(int64_t K);
+// stride of the per-8-row-chunk operands when a prep covers more than 8 rows
+size_t xq_chunk_bytes(int64_t K);
 hipError_t launch_xq_prep(hipStream_t st, float* x, int64_t ldx, const float* normw,
                           const float* part, int S, int64_t ldpart, int64_t K, int64_t M,
                           int8_t* xq);

@@ -74,13 +74,20 @@ __global__ void __launch_bounds__(256) k_xq_prep(float* __restrict__ x, int64_t 
                                                  int8_t* __restrict__ xs32,
                                                  int8_t* __restrict__ xs16,
                                                  float* __restrict__ scale,
-                                                 float* __restrict__ ssq) {
+                                                 float* __restrict__ ssq, int64_t cstride) {
 #pragma clang fp contract(off)
     __shared__ float vs[256];
     const int64_t sb = blockIdx.x;
-    const int m = blockIdx.y, t = threadIdx.x;
-    const bool live = m < M;  // block-uniform
-    float* row = x + (int64_t)m * ldx;
+    // row m of 8-row chunk c: the chunk's operand lies cstride bytes after
+    // the previous one's
+    const int c = blockIdx.y >> 3, m = blockIdx.y & 7, t = threadIdx.x;
+    const bool live = c * 8 + m < M;  // block-uniform
+    float* row = x + (int64_t)(c * 8 + m) * ldx;
+    frag += c * cstride;
+    xs32 += c * cstride;
+    xs16 += c * cstride;
+    scale = (float*)((int8_t*)scale + c * cstride);
+    ssq = (float*)((int8_t*)ssq + c * cstride);
     const int l = t & 63;
     const int64_t k0 = sb * 256 + 4 * l;
     // the norm weights of lane l's four elements are loaded first, so that
@@ -668,6 +675,7 @@ __global__ void __launch_bounds__(256) k_part_reduce(const float* __restrict__ p
 
 // fragments K*16 | xs32 K | xs16 2K | scales (K/256)*8 floats | ssq (K/256)*8 floats
 size_t xq_bytes(int64_t K) { return (size_t)(K * 16 + K + K * 2 + K / 8 + K / 8 + 64); }
+size_t xq_chunk_bytes(int64_t K) { return (xq_bytes(K) + 255) / 256 * 256; }
 
 static float* xq_scale(int8_t* xq, int64_t K) { return xq_ptrs(xq, K).scale; }
 static float* xq_ssq(int8_t* xq, int64_t K) { return xq_ptrs(xq, K).ssq; }
@@ -675,13 +683,15 @@ static float* xq_ssq(int8_t* xq, int64_t K) { return xq_ptrs(xq, K).ssq; }
 hipError_t launch_xq_prep(hipStream_t st, float* x, int64_t ldx, const float* normw,
                           const float* part, int S, int64_t ldpart, int64_t K, int64_t M,
                           int8_t* xq) {
-    if (K % 512 || K > 16384) return hipErrorInvalidValue;
+    if (K % 512 || K > 16384 || M < 1 || (part && M > 8)) return hipErrorInvalidValue;
     int8_t* frag = xq;
     int8_t* xs32 = xq + K * 16;
     int8_t* xs16 = xs32 + K;
-    hipLaunchKernelGGL(k_xq_prep, dim3((unsigned)(K / 256), 8), dim3(256), 0, st, x, ldx, normw,
-                       part, S, ldpart, K, (int)M, frag, xs32, xs16, xq_scale(xq, K),
-                       xq_ssq(xq, K));
+    // one operand per 8-row chunk, xq_chunk_bytes(K) apart
+    const int64_t chunks = (M + 7) / 8;
+    hipLaunchKernelGGL(k_xq_prep, dim3((unsigned)(K / 256), (unsigned)(8 * chunks)), dim3(256), 0,
+                       st, x, ldx, normw, part, S, ldpart, K, (int)M, frag, xs32, xs16,
+                       xq_scale(xq, K), xq_ssq(xq, K), (int64_t)xq_chunk_bytes(K));
     return hipGetLastError();
 }
 

@@ -164,7 +164,8 @@ int ftx_model_create(ftx_ctx* ctx, const ftx_model_desc* d, ftx_model** out) {
               dalloc(&m->args, step_args_bytes(Mmax, d->head_dim));
     if (ok) {
         const int64_t Kmax = std::max(D, qdim);
-        ok = dalloc(&m->xq, xq_bytes(Kmax)) && dalloc(&m->qhl, (size_t)(2 * Mmax * qdim));
+        ok = dalloc(&m->xq, (size_t)((Mmax + 7) / 8) * xq_chunk_bytes(Kmax)) &&
+             dalloc(&m->qhl, (size_t)(2 * Mmax * qdim));
     }
     // re-tiled ffn_down copies (same bytes, MFMA-friendly order)
     m->down_tiled.assign((size_t)d->n_layer, nullptr);
@@ -527,11 +528,11 @@ int ftx_verify_step(ftx_ctx* ctx, ftx_model* m, ftx_kv* kv, const ftx_verify_arg
         for (int i = 0; tiled_all && i < nseg; ++i) tiled_all = m->mvt[tix0 + tix[i]] != nullptr;
         if (tiled_all) {
             auto chunks = [&]() -> hipError_t {
+                // one prep for every chunk's operand, then a launch per chunk
+                hipError_t e = launch_xq_prep(st, xin, ldx, normw, nullptr, 0, D, K, M, m->xq);
+                if (e != hipSuccess) return e;
                 for (int64_t c0 = 0; c0 < M; c0 += 8) {
                     const int64_t mc = M - c0 < 8 ? M - c0 : 8;
-                    hipError_t e = launch_xq_prep(st, xin + c0 * ldx, ldx, normw, nullptr, 0, D,
-                                                  K, mc, m->xq);
-                    if (e != hipSuccess) return e;
                     GemvSeg cs[3];
                     for (int i = 0; i < nseg; ++i) {
                         cs[i] = segs[i];
@@ -540,8 +541,8 @@ int ftx_verify_step(ftx_ctx* ctx, ftx_model* m, ftx_kv* kv, const ftx_verify_arg
                         cs[i].rpt = m->mvt_rpt[tix0 + tix[i]];
                         if (cs[i].y) cs[i].y += c0 * cs[i].ldy;
                     }
-                    e = launch_mv(st, cs, nseg, m->xq, K, mc, epi, ctx->cu_count,
-                                  normw != nullptr, eps, nullptr);
+                    e = launch_mv(st, cs, nseg, m->xq + (c0 / 8) * (int64_t)xq_chunk_bytes(K), K,
+                                  mc, epi, ctx->cu_count, normw != nullptr, eps, nullptr);
                     if (e != hipSuccess) return e;
                 }
                 return hipSuccess;
