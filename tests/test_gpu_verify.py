@@ -239,6 +239,22 @@ def test_verify_8b_shape_two_layers(gctx, orc):
     assert rel_err_rows(got, want) < LOGIT_TOL
 
 
+@pytest.mark.parametrize("parents", [None, [-1, 0, 1, 1, 2, 3, 3, 4, -1, 8, 9, 9]])
+def test_verify_generic_mfma_dtypes(gctx, orc, parents):
+    """More than 8 tokens on non-K-quant weights: the fp16 hi/lo MFMA kernel
+    over every block dtype (F16 q, BF16 k, Q4_1 v, F32 o, Q8_0 gate / up,
+    Q4_0 down, Q4_1 head; d 512, 8 x 64 heads), a 12-token chain and tree at
+    context 40, logits within 1e-3 relative of the oracle's."""
+    cfg = P.model_cfg(2, 512, 8, 4, 64, 1024, 1000, rope_theta=10000.0)
+    dts = dict(tok_embd=P.F32, output=P.Q4_1, q=P.F16, k=P.BF16, v=P.Q4_1, o=P.F32,
+               gate=P.Q8_0, up=P.Q8_0, down=P.Q4_0)
+    model = P.make_model(orc, cfg, dts, seed=12)
+    toks = np.random.default_rng(12).integers(0, 1000, 12).tolist()
+    got, want, (kg, vg), (kc, vc) = run_both(gctx, orc, model, toks, 40, 64, parents=parents)
+    assert rel_err_rows(got, want) < LOGIT_TOL
+    assert np.abs(kg.astype(np.float32) - kc.astype(np.float32)).max() < 2e-2
+
+
 def tree_parents(branching):
     """Parents of a full draft tree in breadth-first order."""
     parents, level = [], [-1]
