@@ -10,7 +10,7 @@ for p in (ROOT, os.path.join(ROOT, "oracle")):
 
 
 def pytest_configure(config):
-    config.addinivalue_line("markers", "gpu: needs an MI355X (runs on the GPU box)")
+    config.addinivalue_line("markers", "gpu: needs an MI355X GPU")
 
 
 @pytest.fixture(scope="session")
