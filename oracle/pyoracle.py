@@ -17,6 +17,10 @@ REF_PATH = os.path.join(HERE, "_ref", "libftref.so")
 F32, F16, Q4_0, Q4_1, Q8_0, Q4_K, Q6_K, BF16 = 0, 1, 2, 3, 8, 12, 14, 30
 # the Sampler's state for seed 0 (include/ft/sampler.h:19)
 SAMPLER_SEED = 0x9E3779B97F4A7C15
+# generate()'s draft cut compares float probabilities with 0.02f and the
+# double running product with 0.05f (src/spec.cpp:279-281)
+CUT_MIN_PROB = float(np.float32(0.02))
+CUT_MIN_CUM = float(np.float32(0.05))
 BLOCK = {F32: (1, 4), F16: (1, 2), BF16: (1, 2), Q4_0: (32, 18), Q4_1: (32, 20),
          Q8_0: (32, 34), Q4_K: (256, 144), Q6_K: (256, 210)}
 ACCEPT_GREEDY, ACCEPT_RATIO, ACCEPT_RESIDUAL = 0, 1, 2
@@ -249,11 +253,11 @@ class Oracle:
             # the cut heuristic
             cut, cum = len(props), 1.0
             for i, p in enumerate(probs):
-                if 0 <= p < 0.02:
+                if 0 <= p < CUT_MIN_PROB:
                     cut = i
                     break
                 cum *= p if p > 0 else 1.0
-                if cum < 0.05:
+                if cum < CUT_MIN_CUM:
                     cut = i + 1
                     break
             props, probs = props[:cut], probs[:cut]

@@ -27,17 +27,12 @@ typedef _Float16 v8h __attribute__((ext_vector_type(8)));
 typedef _Float16 v4h __attribute__((ext_vector_type(4)));
 typedef float v4f __attribute__((ext_vector_type(4)));
 
-// waves per workgroup for head size 128 (16: one score tile and one output
-// tile per wave)
-#ifndef ATTN_WAVES_128
-#define ATTN_WAVES_128 8
-#endif
-// slots per chunk (one workgroup of hd / 16 waves) for head size hd
-#ifndef ATTN_CHK
+// waves per workgroup for head size 128 (16 waves, one score tile and one
+// output tile per wave, measured slower)
+constexpr int ATTN_WAVES_128 = 8;
+// slots per chunk (one workgroup of hd / 16 waves) for head size hd (64-slot
+// chunks measured slower for hd 128)
 __host__ __device__ constexpr int chunk_slots(int hd) { return hd; }
-#else
-__host__ __device__ constexpr int chunk_slots(int) { return ATTN_CHK; }
-#endif
 
 template <int HD, int CHK, int NWV>
 __global__ void __launch_bounds__(64 * NWV) k_attn_mfma(AttnMArgs a) {

@@ -458,12 +458,8 @@ static int64_t down_mfma_splits(int dt, int64_t n_in, int64_t N, int cu_count,
                                 int64_t* slices_per_split = nullptr) {
     const int64_t nslices = n_in / 32, nsb = N / 256;
     const int NB = dt == FTX_Q4_K ? DownCfg<FTX_Q4_K>::NB : DownCfg<FTX_Q6_K>::NB;
-#ifdef DOWN_PER_CU
-    const int64_t per_cu = DOWN_PER_CU;
-#else
-    const int64_t per_cu = 1;
-#endif
-    int64_t S = (per_cu * (int64_t)(cu_count > 0 ? cu_count : 256) + nsb - 1) / nsb;
+    // one 8-wave workgroup per CU
+    int64_t S = ((int64_t)(cu_count > 0 ? cu_count : 256) + nsb - 1) / nsb;
     if (S > 64) S = 64;
     if (S > nslices) S = nslices;
     if (S < 1) S = 1;
@@ -493,7 +489,7 @@ hipError_t launch_down_mfma(hipStream_t st, int dt, const uint8_t* tiled, int64_
     a.M = (int)M;
     a.n_in = n_in;
     a.N = N;
-    const int64_t nslices = n_in / 32, nsb = N / 256;
+    const int64_t nsb = N / 256;
     // splits of the contraction: one 8-wave workgroup per CU (measured best
     // on the 8B shapes: more splits add partial traffic for the next prep to
     // fold and shorten each range), at most 64, each a whole number of slice

@@ -208,9 +208,8 @@ struct MvArgs {
 };
 
 constexpr int MV_WAVES = 8;  // at most 8 waves per unit (512 threads)
-#ifndef MV_WPE_SINGLE
-#define MV_WPE_SINGLE 2
-#endif
+// occupancy hint of the row-dot kernels: at least two waves per SIMD
+constexpr int MV_WPE = 2;
 
 
 __device__ __forceinline__ int mv_seg_of(const MvArgs& a, int64_t T) {
@@ -639,7 +638,7 @@ __device__ __forceinline__ void mv_unit(const MvArgs& a, int64_t u) {
 }
 
 template <int DT, bool TILED, bool PAIR, bool DEEP>
-__global__ void __launch_bounds__(64 * MV_WAVES) __attribute__((amdgpu_waves_per_eu(MV_WPE_SINGLE)))
+__global__ void __launch_bounds__(64 * MV_WAVES) __attribute__((amdgpu_waves_per_eu(MV_WPE)))
 k_mv(MvArgs a) {
     mv_unit<DT, TILED, PAIR, DEEP>(a, blockIdx.x);
 }
@@ -647,7 +646,7 @@ k_mv(MvArgs a) {
 // one launch over segments of both dtypes (q / k Q4_K with a Q6_K v): each
 // workgroup takes the path of its unit's segment
 template <bool TILED, bool DEEP>
-__global__ void __launch_bounds__(64 * MV_WAVES) __attribute__((amdgpu_waves_per_eu(MV_WPE_SINGLE)))
+__global__ void __launch_bounds__(64 * MV_WAVES) __attribute__((amdgpu_waves_per_eu(MV_WPE)))
 k_mv_mix(MvArgs a) {
     const int64_t u = blockIdx.x;
     if (a.seg[mv_seg_of(a, u)].dt == FTX_Q4_K)

@@ -45,6 +45,13 @@ struct ftx_model {
     std::vector<uint8_t*> pln;
     std::vector<int> pln_dt;
     float* downpart = nullptr;
+    // pinned host argument blocks, used in turn; an event recorded after a
+    // block's copy to the device guards its reuse, so the host prepares the
+    // next step while earlier steps still run
+    static constexpr int PIN_RING = 4;
+    uint8_t* pin[PIN_RING] = {};
+    hipEvent_t pin_ev[PIN_RING] = {};
+    int pin_next = 0;
 };
 
 // Per-step argument block (pinned host copy and device copy share the
@@ -75,6 +82,9 @@ static bool mv_all(const ftx_tensor* const* ts, int n, int64_t K, int64_t M) {
 struct ftx_kv {
     ftx_ctx* ctx = nullptr;
     int64_t n_layer = 0, cap = 0, kdim = 0, n_kv = 0, hd = 0;
+    // the creating model's query heads and largest step: attn_part is sized
+    // for them
+    int64_t n_head = 0, mmax = 0;
     int64_t cap_alloc = 0;  // slots allocated per layer, a multiple of 128
     int kv_f16 = 1;
     void* k = nullptr;      // [n_layer][cap_alloc][kdim]
@@ -95,6 +105,10 @@ static void model_release(ftx_model* m) {
     for (uint8_t* b : m->pln)
         if (b) (void)hipFree(b);
     if (m->downpart) (void)hipFree(m->downpart);
+    for (int i = 0; i < ftx_model::PIN_RING; ++i) {
+        if (m->pin[i]) (void)hipHostFree(m->pin[i]);
+        if (m->pin_ev[i]) (void)hipEventDestroy(m->pin_ev[i]);
+    }
     delete m;
 }
 
@@ -162,6 +176,12 @@ int ftx_model_create(ftx_ctx* ctx, const ftx_model_desc* d, ftx_model** out) {
               dalloc(&m->qkv, Mmax * m->ldq) && dalloc(&m->att, Mmax * qdim) &&
               dalloc(&m->h, Mmax * d->n_ff) && dalloc(&m->part, m->part_floats) &&
               dalloc(&m->args, step_args_bytes(Mmax, d->head_dim));
+    for (int i = 0; ok && i < ftx_model::PIN_RING; ++i) {
+        ok = hipHostMalloc((void**)&m->pin[i], step_args_bytes(Mmax, d->head_dim),
+                           hipHostMallocDefault) == hipSuccess &&
+             hipEventCreateWithFlags(&m->pin_ev[i], hipEventDisableTiming) == hipSuccess;
+        if (!ok) (void)hipGetLastError();
+    }
     if (ok) {
         const int64_t Kmax = std::max(D, qdim);
         ok = dalloc(&m->xq, (size_t)((Mmax + 7) / 8) * xq_chunk_bytes(Kmax)) &&
@@ -282,6 +302,8 @@ int ftx_kv_create(ftx_ctx* ctx, const ftx_model* m, int64_t cap, int kv_dtype, f
     kv->kdim = m->kdim;
     kv->n_kv = m->d.n_head_kv;
     kv->hd = m->d.head_dim;
+    kv->n_head = m->d.n_head;
+    kv->mmax = m->Mmax;
     kv->kv_f16 = kv_dtype == FTX_KV_F16;
     const size_t bytes = (size_t)(kv->n_layer * kv->cap_alloc * kv->kdim) * (kv->kv_f16 ? 2 : 4);
     const size_t pf = attn_part_floats(m->Mmax, m->d.n_head, m->d.head_dim, kv->cap_alloc);
@@ -405,18 +427,21 @@ int ftx_verify_step(ftx_ctx* ctx, ftx_model* m, ftx_kv* kv, const ftx_verify_arg
     const ftx_model_desc& d = m->d;
     const int64_t M = a->M;
     if (M < 1 || M > m->Mmax) return ftx_fail(ctx, FTX_E_INVALID, "M out of range");
-    if (kv->n_layer != d.n_layer || kv->kdim != m->kdim)
+    if (kv->n_layer != d.n_layer || kv->kdim != m->kdim || kv->n_kv != d.n_head_kv ||
+        kv->hd != d.head_dim || kv->n_head != d.n_head)
         return ftx_fail(ctx, FTX_E_INVALID, "kv cache does not match the model");
+    if (M > kv->mmax)
+        return ftx_fail(ctx, FTX_E_INVALID, "M above the max_tokens of the kv cache's model");
     const int64_t npast = kv->npast;
     if (npast + M > kv->cap) return ftx_fail(ctx, FTX_E_RANGE, "kv capacity exceeded");
     // host-side argument prep: tokens, depth, ancestor masks, npast
     const int aw = (int)((M + 31) / 32);
     const int64_t hd2 = d.head_dim / 2;
     const StepArgsLayout AL = step_args_layout(M, d.head_dim);
-    uint8_t* pin;
-    int rc = ftx_pinned(ctx, AL.bytes, (void**)&pin);
-    if (rc) return rc;
-    FTX_HIP(ctx, hipStreamSynchronize(ctx->stream));  // pinned buffer reuse
+    const int slot = m->pin_next;
+    uint8_t* pin = m->pin[slot];
+    FTX_HIP(ctx, hipEventSynchronize(m->pin_ev[slot]));  // this block's last copy is done
+    int rc = FTX_OK;
     int32_t* toks = (int32_t*)pin;
     int32_t* depth = (int32_t*)(pin + AL.depth);
     uint32_t* anc = (uint32_t*)(pin + AL.anc);
@@ -453,6 +478,8 @@ int ftx_verify_step(ftx_ctx* ctx, ftx_model* m, ftx_kv* kv, const ftx_verify_arg
     m->npast = (int64_t*)(m->args + AL.np);
     m->rcs = (float*)(m->args + AL.cs);
     FTX_HIP(ctx, hipMemcpyAsync(m->args, pin, AL.bytes, hipMemcpyHostToDevice, st));
+    FTX_HIP(ctx, hipEventRecord(m->pin_ev[slot], st));
+    m->pin_next = (slot + 1) % ftx_model::PIN_RING;
 
     const int64_t D = d.n_embd, F = d.n_ff, V = d.vocab;
     const float eps = d.rms_eps;

@@ -9,274 +9,330 @@
 #include <algorithm>
 #include <cctype>
 #include <climits>
+#include <cstdarg>
+#include <cstdio>
 #include <cstring>
 #include <stdexcept>
 #include <unordered_map>
+#include <variant>
 
 namespace ftx_host {
 
+// The container format as the GGUF specification lays it out (versions 2 and
+// 3): a 24-byte header (magic "GGUF", version, tensor count, metadata
+// count), the metadata entries (key string, type, value), the tensor
+// directory (name, dims, sizes, dtype, offset into the data section), then
+// the data section at the next multiple of general.alignment (32 unless the
+// file says otherwise).  Strings are a u64 length and the bytes; arrays an
+// element type, a u64 count and the elements.
+
 namespace {
 
-constexpr uint32_t kMagic = 0x46554747;  // "GGUF"
-enum : uint32_t {
-    K_U8, K_I8, K_U16, K_I16, K_U32, K_I32, K_F32, K_BOOL, K_STR, K_ARR, K_U64, K_I64, K_F64
+enum MetaType : uint32_t {
+    MT_U8 = 0, MT_I8 = 1, MT_U16 = 2, MT_I16 = 3, MT_U32 = 4, MT_I32 = 5, MT_F32 = 6,
+    MT_BOOL = 7, MT_STRING = 8, MT_ARRAY = 9, MT_U64 = 10, MT_I64 = 11, MT_F64 = 12,
+    MT_END = 13
 };
 
-// one metadata value: integers in i, floats in f, bools in b, strings in s;
-// arrays keep their element kind, count and raw bytes (or strings)
-struct Val {
-    uint32_t kind = 0;
-    int64_t i = 0;
-    double f = 0;
-    bool b = false;
-    std::string s;
-    uint32_t ekind = 0;
+// bytes of a fixed-size metadata type (0: string, array, unknown)
+int fixed_width(uint32_t t) {
+    static const int8_t w[MT_END] = {1, 1, 2, 2, 4, 4, 4, 1, 0, 0, 8, 8, 8};
+    return t < MT_END ? w[t] : 0;
+}
+
+std::string fmt(const char* f, ...) __attribute__((format(printf, 1, 2)));
+std::string fmt(const char* f, ...) {
+    char buf[512];
+    va_list ap;
+    va_start(ap, f);
+    std::vsnprintf(buf, sizeof(buf), f, ap);
+    va_end(ap);
+    return buf;
+}
+
+// The mapped file seen as a byte range with a read position; every read
+// names the part of the file it belongs to, for the error message.
+struct Span {
+    const uint8_t* base;
+    uint64_t size;
+    uint64_t pos = 0;
+
+    const uint8_t* take(uint64_t n, const char* part) {
+        if (n > size - pos)
+            throw std::runtime_error(
+                fmt("gguf: the file ends inside the %s (byte %llu of %llu)", part,
+                    (unsigned long long)pos, (unsigned long long)size));
+        const uint8_t* at = base + pos;
+        pos += n;
+        return at;
+    }
+    template <typename T>
+    T scalar(const char* part) {
+        T v;
+        std::memcpy(&v, take(sizeof(T), part), sizeof(T));
+        return v;
+    }
+    std::string text(const char* part) {
+        const uint64_t n = scalar<uint64_t>(part);
+        const uint8_t* at = take(n, part);
+        return std::string((const char*)at, (size_t)n);
+    }
+};
+
+// A metadata array: its element type and count, the strings of a string
+// array or the packed little-endian elements of a numeric one.
+struct MetaArray {
+    uint32_t elem = 0;
     uint64_t count = 0;
-    std::vector<std::string> strs;
-    std::vector<uint8_t> raw;
+    std::vector<std::string> strings;
+    std::vector<uint8_t> packed;
 };
 
-size_t kind_bytes(uint32_t k) {
-    switch (k) {
-        case K_U8: case K_I8: case K_BOOL: return 1;
-        case K_U16: case K_I16: return 2;
-        case K_U32: case K_I32: case K_F32: return 4;
-        case K_U64: case K_I64: case K_F64: return 8;
+// A decoded metadata value: integers of every width widened to int64, both
+// float widths to double.
+struct Meta {
+    uint32_t type = 0;
+    std::variant<int64_t, double, bool, std::string, MetaArray> v;
+};
+
+int64_t widen_int(const uint8_t* p, uint32_t t) {
+    switch (t) {
+        case MT_U8: return p[0];
+        case MT_I8: return (int8_t)p[0];
+        case MT_U16: { uint16_t x; std::memcpy(&x, p, 2); return x; }
+        case MT_I16: { int16_t x; std::memcpy(&x, p, 2); return x; }
+        case MT_U32: { uint32_t x; std::memcpy(&x, p, 4); return x; }
+        case MT_I32: { int32_t x; std::memcpy(&x, p, 4); return x; }
+        case MT_U64: { uint64_t x; std::memcpy(&x, p, 8); return (int64_t)x; }
+        case MT_I64: { int64_t x; std::memcpy(&x, p, 8); return x; }
         default: return 0;
     }
 }
 
-// (elements, bytes) per block of each accepted tensor dtype
-bool block_of(uint32_t dt, int64_t& eb, int64_t& bb) {
+Meta decode_meta(Span& in, uint32_t type) {
+    Meta m;
+    m.type = type;
+    switch (type) {
+        case MT_F32: m.v = (double)in.scalar<float>("metadata"); break;
+        case MT_F64: m.v = in.scalar<double>("metadata"); break;
+        case MT_BOOL: m.v = in.scalar<uint8_t>("metadata") != 0; break;
+        case MT_STRING: m.v = in.text("metadata"); break;
+        case MT_ARRAY: {
+            MetaArray a;
+            a.elem = in.scalar<uint32_t>("metadata");
+            a.count = in.scalar<uint64_t>("metadata");
+            if (a.elem == MT_STRING) {
+                for (uint64_t i = 0; i < a.count; ++i) a.strings.push_back(in.text("metadata"));
+            } else if (const int w = fixed_width(a.elem)) {
+                if (a.count > (in.size - in.pos) / (uint64_t)w)
+                    throw std::runtime_error("gguf: a metadata array runs past the end of the file");
+                const uint8_t* at = in.take(a.count * (uint64_t)w, "metadata");
+                a.packed.assign(at, at + a.count * (uint64_t)w);
+            } else {
+                throw std::runtime_error(fmt("gguf: arrays of metadata type %u are not supported", a.elem));
+            }
+            m.v = std::move(a);
+            break;
+        }
+        default: {
+            const int w = fixed_width(type);
+            if (!w) throw std::runtime_error(fmt("gguf: metadata type %u is not supported", type));
+            m.v = widen_int(in.take((uint64_t)w, "metadata"), type);
+        }
+    }
+    return m;
+}
+
+// (elements, bytes) of one block of a tensor dtype this library reads
+bool dtype_block(uint32_t dt, int64_t& elems, int64_t& bytes) {
     switch (dt) {
-        case FTX_F32: eb = 1; bb = 4; return true;
-        case FTX_F16: case FTX_BF16: eb = 1; bb = 2; return true;
-        case FTX_Q4_0: eb = 32; bb = 18; return true;
-        case FTX_Q4_1: eb = 32; bb = 20; return true;
-        case FTX_Q8_0: eb = 32; bb = 34; return true;
-        case FTX_Q4_K: eb = 256; bb = 144; return true;
-        case FTX_Q6_K: eb = 256; bb = 210; return true;
+        case FTX_F32: elems = 1; bytes = 4; return true;
+        case FTX_F16: case FTX_BF16: elems = 1; bytes = 2; return true;
+        case FTX_Q4_0: elems = 32; bytes = 18; return true;
+        case FTX_Q4_1: elems = 32; bytes = 20; return true;
+        case FTX_Q8_0: elems = 32; bytes = 34; return true;
+        case FTX_Q4_K: elems = 256; bytes = 144; return true;
+        case FTX_Q6_K: elems = 256; bytes = 210; return true;
         default: return false;
     }
 }
 
-class Cursor {
-public:
-    Cursor(const uint8_t* p, size_t n) : p_(p), n_(n) {}
-    void need(uint64_t k) const {
-        if (k > n_ - off_) throw std::runtime_error("gguf: truncated file");
-    }
-    template <typename T>
-    T get() {
-        need(sizeof(T));
-        T v;
-        std::memcpy(&v, p_ + off_, sizeof(T));
-        off_ += sizeof(T);
-        return v;
-    }
-    std::string str() {
-        const uint64_t n = get<uint64_t>();
-        need(n);
-        std::string s((const char*)p_ + off_, (size_t)n);
-        off_ += (size_t)n;
-        return s;
-    }
-    Val value(uint32_t kind) {
-        Val v;
-        v.kind = kind;
-        switch (kind) {
-            case K_U8: v.i = get<uint8_t>(); break;
-            case K_I8: v.i = get<int8_t>(); break;
-            case K_U16: v.i = get<uint16_t>(); break;
-            case K_I16: v.i = get<int16_t>(); break;
-            case K_U32: v.i = get<uint32_t>(); break;
-            case K_I32: v.i = get<int32_t>(); break;
-            case K_U64: v.i = (int64_t)get<uint64_t>(); break;
-            case K_I64: v.i = get<int64_t>(); break;
-            case K_F32: v.f = get<float>(); break;
-            case K_F64: v.f = get<double>(); break;
-            case K_BOOL: v.b = get<uint8_t>() != 0; break;
-            case K_STR: v.s = str(); break;
-            case K_ARR: {
-                v.ekind = get<uint32_t>();
-                v.count = get<uint64_t>();
-                if (v.ekind == K_STR) {
-                    for (uint64_t i = 0; i < v.count; ++i) v.strs.push_back(str());
-                } else if (kind_bytes(v.ekind)) {
-                    const uint64_t nb = kind_bytes(v.ekind) * v.count;
-                    if (v.count && nb / v.count != kind_bytes(v.ekind))
-                        throw std::runtime_error("gguf: truncated file");
-                    need(nb);
-                    v.raw.assign(p_ + off_, p_ + off_ + nb);
-                    off_ += (size_t)nb;
-                } else {
-                    throw std::runtime_error("gguf: unsupported array element type");
-                }
-                break;
-            }
-            default: throw std::runtime_error("gguf: unsupported kv type");
-        }
-        return v;
-    }
-    size_t offset() const { return off_; }
-
-private:
-    const uint8_t* p_;
-    size_t n_;
-    size_t off_ = 0;
+struct DirEntry {
+    std::string name;
+    int32_t n_dims = 0;
+    int64_t ne[4] = {1, 1, 1, 1};
+    uint32_t dtype = 0;
+    uint64_t offset = 0;
 };
 
 }  // namespace
 
 struct Gguf::Impl {
     int fd = -1;
-    const uint8_t* data = nullptr;
+    const uint8_t* map = nullptr;
     size_t size = 0;
-    std::unordered_map<std::string, Val> kv;
-    std::vector<std::string> order;  // keys in file order
-    uint64_t data_start = 0;
+    std::unordered_map<std::string, Meta> meta;
+    std::vector<std::string> key_order;  // first occurrence of each key, in file order
     uint32_t align = 32;
     ~Impl() {
-        if (data) munmap((void*)data, size);
+        if (map) munmap((void*)map, size);
         if (fd >= 0) ::close(fd);
     }
-    const Val* find(const std::string& k) const {
-        auto it = kv.find(k);
-        return it == kv.end() ? nullptr : &it->second;
+    const Meta* lookup(const std::string& k) const {
+        const auto it = meta.find(k);
+        return it == meta.end() ? nullptr : &it->second;
     }
 };
 
 Gguf::Gguf(const std::string& path) : impl_(new Impl) {
-    Impl& I = *impl_;
-    I.fd = ::open(path.c_str(), O_RDONLY);
-    if (I.fd < 0) throw std::runtime_error("cannot open " + path);
+    Impl& F = *impl_;
+    F.fd = ::open(path.c_str(), O_RDONLY);
+    if (F.fd < 0) throw std::runtime_error("gguf: cannot open '" + path + "'");
     struct stat st {};
-    if (fstat(I.fd, &st) != 0) throw std::runtime_error("cannot stat " + path);
-    I.size = (size_t)st.st_size;
-    if (I.size < 24) throw std::runtime_error("gguf: empty or tiny file");
-    void* m = mmap(nullptr, I.size, PROT_READ, MAP_PRIVATE, I.fd, 0);
-    if (m == MAP_FAILED) throw std::runtime_error("cannot map " + path);
-    I.data = (const uint8_t*)m;
+    if (fstat(F.fd, &st) != 0) throw std::runtime_error("gguf: cannot stat '" + path + "'");
+    F.size = (size_t)st.st_size;
+    if (F.size < 24) throw std::runtime_error("gguf: '" + path + "' is too small for a GGUF header");
+    void* mp = mmap(nullptr, F.size, PROT_READ, MAP_PRIVATE, F.fd, 0);
+    if (mp == MAP_FAILED) throw std::runtime_error("gguf: cannot map '" + path + "'");
+    F.map = (const uint8_t*)mp;
 
-    Cursor c(I.data, I.size);
-    if (c.get<uint32_t>() != kMagic) throw std::runtime_error("not a GGUF file");
-    const uint32_t version = c.get<uint32_t>();
-    if (version != 2 && version != 3)
-        throw std::runtime_error("unsupported GGUF version " + std::to_string(version));
-    const uint64_t n_tensors = c.get<uint64_t>();
-    const uint64_t n_kv = c.get<uint64_t>();
-    for (uint64_t i = 0; i < n_kv; ++i) {
-        std::string key = c.str();
-        const uint32_t kind = c.get<uint32_t>();
-        Val v = c.value(kind);
-        if (I.kv.emplace(key, std::move(v)).second) I.order.push_back(key);
+    Span in{F.map, (uint64_t)F.size};
+    if (std::memcmp(in.take(4, "header"), "GGUF", 4) != 0)
+        throw std::runtime_error("gguf: bad magic, '" + path + "' is not a GGUF file");
+    const uint32_t version = in.scalar<uint32_t>("header");
+    if (version < 2 || version > 3)
+        throw std::runtime_error(fmt("gguf: version %u is not supported (2 or 3 expected)", version));
+    const uint64_t n_tensors = in.scalar<uint64_t>("header");
+    const uint64_t n_meta = in.scalar<uint64_t>("header");
+
+    for (uint64_t i = 0; i < n_meta; ++i) {
+        std::string key = in.text("metadata");
+        const uint32_t type = in.scalar<uint32_t>("metadata");
+        Meta m = decode_meta(in, type);
+        if (F.meta.emplace(key, std::move(m)).second) F.key_order.push_back(std::move(key));
     }
-    if (const Val* a = I.find("general.alignment")) {
-        const int64_t al = (a->kind == K_STR) ? 0 : a->i;
-        I.align = al > 0 && (al & (al - 1)) == 0 && al <= INT32_MAX ? (uint32_t)al : 32;
-    }
-    struct Info {
-        std::string name;
-        int32_t n_dims;
-        int64_t ne[4];
-        uint32_t dt;
-        uint64_t off;
-    };
-    std::vector<Info> infos;
+    // general.alignment is read through its integer slot and cut to 32 bits;
+    // zero or a non-power of two keeps the default
+    if (const Meta* a = F.lookup("general.alignment"))
+        if (const int64_t* iv = std::get_if<int64_t>(&a->v)) {
+            const uint32_t al = (uint32_t)*iv;
+            if (al && !(al & (al - 1))) F.align = al;
+        }
+
+    std::vector<DirEntry> dir;
+    dir.reserve((size_t)std::min<uint64_t>(n_tensors, 1u << 16));
     for (uint64_t i = 0; i < n_tensors; ++i) {
-        Info t{};
-        t.name = c.str();
-        t.n_dims = c.get<int32_t>();
-        if (t.n_dims < 1 || t.n_dims > 4) throw std::runtime_error("gguf: bad dims for " + t.name);
-        for (int d = 0; d < 4; ++d) t.ne[d] = 1;
-        for (int d = 0; d < t.n_dims; ++d) t.ne[d] = (int64_t)c.get<uint64_t>();
-        t.dt = c.get<uint32_t>();
-        int64_t eb, bb;
-        if (!block_of(t.dt, eb, bb))
-            throw std::runtime_error("gguf: unsupported tensor dtype " + std::to_string(t.dt));
-        t.off = c.get<uint64_t>();
-        infos.push_back(std::move(t));
+        DirEntry e;
+        e.name = in.text("tensor directory");
+        e.n_dims = in.scalar<int32_t>("tensor directory");
+        if (e.n_dims < 1 || e.n_dims > 4)
+            throw std::runtime_error(fmt("gguf: tensor '%s' has %d dims (1 to 4 allowed)",
+                                         e.name.c_str(), e.n_dims));
+        for (int d = 0; d < e.n_dims; ++d)
+            e.ne[d] = (int64_t)in.scalar<uint64_t>("tensor directory");
+        e.dtype = in.scalar<uint32_t>("tensor directory");
+        int64_t be, bb;
+        if (!dtype_block(e.dtype, be, bb))
+            throw std::runtime_error(fmt("gguf: tensor '%s' has dtype %u, which is not supported",
+                                         e.name.c_str(), e.dtype));
+        e.offset = in.scalar<uint64_t>("tensor directory");
+        dir.push_back(std::move(e));
     }
-    const uint64_t pos = (c.offset() + I.align - 1) / I.align * I.align;
-    if (pos > I.size) throw std::runtime_error("gguf: data out of bounds");
-    I.data_start = pos;
-    for (const Info& t : infos) {
-        if (tensors_.count(t.name)) continue;  // a repeated name keeps its first info
-        int64_t eb, bb;
-        block_of(t.dt, eb, bb);
-        for (int d = 0; d < 4; ++d)
-            if (t.ne[d] < 0) throw std::runtime_error("gguf: bad dims for " + t.name);
-        const uint64_t row = (uint64_t)((t.ne[0] + eb - 1) / eb * bb);
-        const uint64_t nb = row * (uint64_t)t.ne[1] * (uint64_t)t.ne[2] * (uint64_t)t.ne[3];
-        const uint64_t room = I.size - pos;
-        if (t.off > room || nb > room - t.off)
-            throw std::runtime_error("gguf: tensor out of bounds: " + t.name);
-        HostTensor h;
-        h.name = t.name;
-        for (int d = 0; d < 4; ++d) h.ne[d] = t.ne[d];
-        h.n_dims = t.n_dims;
-        h.dtype = (DType)t.dt;
-        h.data = I.data + pos + t.off;
-        h.nbytes = (size_t)nb;
-        tensors_.emplace(t.name, std::move(h));
+    const uint64_t data0 = (in.pos + F.align - 1) / F.align * F.align;
+    if (data0 > F.size) throw std::runtime_error("gguf: the data section starts past the end of the file");
+    const uint64_t room = F.size - data0;
+
+    for (const DirEntry& e : dir) {
+        if (tensors_.count(e.name)) continue;  // a name listed twice keeps its first entry
+        int64_t be, bb;
+        dtype_block(e.dtype, be, bb);
+        uint64_t nbytes = 0;
+        bool fits = e.offset <= room;
+        for (int d = 0; fits && d < 4; ++d) fits = e.ne[d] >= 0;
+        if (fits) {
+            // bytes = rows * row bytes, each product checked against the room left
+            const uint64_t row = (uint64_t)((e.ne[0] + be - 1) / be) * (uint64_t)bb;
+            nbytes = row;
+            for (int d = 1; fits && d < 4; ++d) {
+                const uint64_t n = (uint64_t)e.ne[d];
+                fits = n == 0 || nbytes <= (room - e.offset) / n;
+                nbytes *= n;
+            }
+            fits = fits && nbytes <= room - e.offset;
+        }
+        if (!fits) throw std::runtime_error("gguf: tensor '" + e.name + "' lies outside the file");
+        HostTensor t;
+        t.name = e.name;
+        std::copy(e.ne, e.ne + 4, t.ne);
+        t.n_dims = e.n_dims;
+        t.dtype = (DType)e.dtype;
+        t.data = F.map + data0 + e.offset;
+        t.nbytes = (size_t)nbytes;
+        tensors_.emplace(e.name, std::move(t));
     }
 }
 
 Gguf::~Gguf() = default;
 
-bool Gguf::has(const std::string& key) const { return impl_->find(key) != nullptr; }
+bool Gguf::has(const std::string& key) const { return impl_->lookup(key) != nullptr; }
 
 std::string Gguf::get_str(const std::string& key, const std::string& def) const {
-    const Val* v = impl_->find(key);
-    return v && v->kind == K_STR ? v->s : def;
+    const Meta* m = impl_->lookup(key);
+    const std::string* s = m ? std::get_if<std::string>(&m->v) : nullptr;
+    return s ? *s : def;
 }
 
-// src/gguf.cpp:258-265: every non-string kind answers with its integer slot,
-// which holds 0 for floats, bools and arrays
+// The typed accessors keep the reference's answers for every stored type
+// (src/gguf.cpp:258-285): an integer read of a float, bool or array key is 0
+// (not the default), a float read of an integer key converts it, and only a
+// missing or string key gives the default.
 int64_t Gguf::get_i64(const std::string& key, int64_t def) const {
-    const Val* v = impl_->find(key);
-    if (!v || v->kind == K_STR) return def;
-    return v->i;
+    const Meta* m = impl_->lookup(key);
+    if (!m || m->type == MT_STRING) return def;
+    const int64_t* iv = std::get_if<int64_t>(&m->v);
+    return iv ? *iv : 0;
 }
 
 double Gguf::get_f64(const std::string& key, double def) const {
-    const Val* v = impl_->find(key);
-    if (!v || v->kind == K_STR) return def;
-    if (v->kind == K_F32 || v->kind == K_F64) return v->f;
-    return (double)v->i;
+    const Meta* m = impl_->lookup(key);
+    if (!m || m->type == MT_STRING) return def;
+    if (const double* dv = std::get_if<double>(&m->v)) return *dv;
+    const int64_t* iv = std::get_if<int64_t>(&m->v);
+    return iv ? (double)*iv : 0.0;
 }
 
 bool Gguf::get_bool(const std::string& key, bool def) const {
-    const Val* v = impl_->find(key);
-    return v && v->kind == K_BOOL ? v->b : def;
+    const Meta* m = impl_->lookup(key);
+    const bool* bv = m ? std::get_if<bool>(&m->v) : nullptr;
+    return bv ? *bv : def;
 }
 
 std::vector<std::string> Gguf::get_str_arr(const std::string& key) const {
-    const Val* v = impl_->find(key);
-    if (!v || v->kind != K_ARR || v->ekind != K_STR) return {};
-    return v->strs;
+    const Meta* m = impl_->lookup(key);
+    const MetaArray* a = m ? std::get_if<MetaArray>(&m->v) : nullptr;
+    return a && a->elem == MT_STRING ? a->strings : std::vector<std::string>{};
 }
 
-// numeric arrays as float; string and bool arrays read as zeros of their
-// length (src/gguf.cpp:288-330)
+// any array as floats, one per element: numbers converted, strings and bools
+// as zeros (src/gguf.cpp:288-330)
 std::vector<float> Gguf::get_f32_arr(const std::string& key) const {
-    const Val* v = impl_->find(key);
-    if (!v || v->kind != K_ARR) return {};
-    std::vector<float> out((size_t)v->count, 0.f);
-    const uint8_t* r = v->raw.data();
-    for (uint64_t i = 0; i < v->count; ++i) {
-        switch (v->ekind) {
-            case K_F32: { float f; std::memcpy(&f, r + i * 4, 4); out[i] = f; break; }
-            case K_F64: { double d; std::memcpy(&d, r + i * 8, 8); out[i] = (float)d; break; }
-            case K_U8: out[i] = (float)r[i]; break;
-            case K_I8: out[i] = (float)(int8_t)r[i]; break;
-            case K_U16: { uint16_t x; std::memcpy(&x, r + i * 2, 2); out[i] = (float)x; break; }
-            case K_I16: { int16_t x; std::memcpy(&x, r + i * 2, 2); out[i] = (float)x; break; }
-            case K_U32: { uint32_t x; std::memcpy(&x, r + i * 4, 4); out[i] = (float)x; break; }
-            case K_I32: { int32_t x; std::memcpy(&x, r + i * 4, 4); out[i] = (float)x; break; }
-            case K_U64: { uint64_t x; std::memcpy(&x, r + i * 8, 8); out[i] = (float)(int64_t)x; break; }
-            case K_I64: { int64_t x; std::memcpy(&x, r + i * 8, 8); out[i] = (float)x; break; }
-            default: break;  // strings, bools
+    const Meta* m = impl_->lookup(key);
+    const MetaArray* a = m ? std::get_if<MetaArray>(&m->v) : nullptr;
+    if (!a) return {};
+    std::vector<float> out((size_t)a->count, 0.f);
+    const int w = a->elem == MT_BOOL ? 0 : fixed_width(a->elem);
+    for (uint64_t i = 0; w && i < a->count; ++i) {
+        const uint8_t* p = a->packed.data() + i * (uint64_t)w;
+        if (a->elem == MT_F32) {
+            float f;
+            std::memcpy(&f, p, 4);
+            out[i] = f;
+        } else if (a->elem == MT_F64) {
+            double f;
+            std::memcpy(&f, p, 8);
+            out[i] = (float)f;
+        } else {
+            out[i] = (float)widen_int(p, a->elem);
         }
     }
     return out;
@@ -284,21 +340,17 @@ std::vector<float> Gguf::get_f32_arr(const std::string& key) const {
 
 std::vector<int32_t> Gguf::get_i32_arr(const std::string& key) const {
     const std::vector<float> f = get_f32_arr(key);
-    std::vector<int32_t> out(f.size());
-    for (size_t i = 0; i < f.size(); ++i) out[i] = (int32_t)f[i];
-    return out;
+    return std::vector<int32_t>(f.begin(), f.end());
 }
 
 const HostTensor* Gguf::tensor(const std::string& name) const {
-    auto it = tensors_.find(name);
+    const auto it = tensors_.find(name);
     return it == tensors_.end() ? nullptr : &it->second;
 }
 
-std::vector<std::string> Gguf::keys() const { return impl_->order; }
+std::vector<std::string> Gguf::keys() const { return impl_->key_order; }
 
-uint64_t Gguf::file_offset(const HostTensor& t) const {
-    return (uint64_t)(t.data - impl_->data);
-}
+uint64_t Gguf::file_offset(const HostTensor& t) const { return (uint64_t)(t.data - impl_->map); }
 
 uint32_t Gguf::alignment() const { return impl_->align; }
 

@@ -22,8 +22,10 @@ import numpy as np
 from . import ftx
 
 # generate's cut heuristic (src/spec.cpp:276-285)
-CUT_MIN_PROB = 0.02
-CUT_MIN_CUM = 0.05
+# the reference compares against the float constants 0.02f and 0.05f
+# (src/spec.cpp:279-281): their exact values as doubles
+CUT_MIN_PROB = float(np.float32(0.02))
+CUT_MIN_CUM = float(np.float32(0.05))
 
 
 class DraftModelDrafter:
