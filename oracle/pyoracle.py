@@ -579,7 +579,7 @@ def tensor_shapes(cfg):
 def make_model(orc, cfg, dtypes, seed=1, std=0.02, tied=False):
     """Random-init model: weights N(0, std) quantised to dtypes[name-suffix]
     (keys: 'tok_embd', 'output', 'q', 'k', 'v', 'o', 'gate', 'up', 'down';
-    norms are F32 ones)."""
+    norms are F32 vectors of 1 + 0.3 N(0, 1), different per layer and role)."""
     rng = np.random.default_rng(seed)
     model = {"cfg": dict(cfg)}
     for name, ne0, ne1 in tensor_shapes(cfg):
@@ -587,7 +587,7 @@ def make_model(orc, cfg, dtypes, seed=1, std=0.02, tied=False):
             continue
         key = name.split(".")[-1]
         if key in ("attn_norm", "ffn_norm", "out_norm"):
-            w = np.ones(ne0, np.float32)
+            w = (1.0 + 0.3 * rng.standard_normal(ne0)).astype(np.float32)
             model[name] = dict(raw=w.view(np.uint8).copy(), dtype=F32, ne0=ne0, ne1=1)
             continue
         dt = dtypes[key]

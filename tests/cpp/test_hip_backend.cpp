@@ -203,23 +203,32 @@ static void test_verifier(HipBackend& be) {
     keep.reserve(64);
     ModelWeights w;
     w.tok_embd = add(DType::F32, c.vocab, c.n_embd, 1.f, "tok_embd");
-    std::vector<float> ones((size_t)c.n_embd, 1.f);
-    HostTensor norm;
-    norm.ne[0] = c.n_embd;
-    norm.dtype = DType::F32;
-    norm.data = (const uint8_t*)ones.data();
-    norm.nbytes = ones.size() * 4;
-    w.out_norm = norm;
+    // RMSNorm weights of 1 + 0.3 N(0, 1), one vector per
+    // layer and role, so that a norm applied with the wrong vector shows
+    std::vector<std::vector<float>> norms((size_t)(2 * c.n_layer + 1));
+    for (auto& v : norms) {
+        v.resize((size_t)c.n_embd);
+        for (auto& x : v) x = 1.f + 0.3f * rnd();
+    }
+    auto norm_of = [&](size_t i) {
+        HostTensor t;
+        t.ne[0] = c.n_embd;
+        t.dtype = DType::F32;
+        t.data = (const uint8_t*)norms[i].data();
+        t.nbytes = norms[i].size() * 4;
+        return t;
+    };
+    w.out_norm = norm_of(2 * (size_t)c.n_layer);
     w.output = add(DType::Q6_K, c.vocab, c.n_embd, 0.05f, "output");
     const int64_t kdim = c.n_head_kv * c.head_dim, qdim = c.n_head * c.head_dim;
     for (int64_t l = 0; l < c.n_layer; ++l) {
         std::vector<HostTensor> L(9);
-        L[0] = norm;
+        L[0] = norm_of(2 * (size_t)l);
         L[1] = add(DType::Q4_K, qdim, c.n_embd, 0.05f, "q");
         L[2] = add(DType::Q4_K, kdim, c.n_embd, 0.05f, "k");
         L[3] = add(DType::Q6_K, kdim, c.n_embd, 0.05f, "v");
         L[4] = add(DType::Q4_K, c.n_embd, qdim, 0.05f, "o");
-        L[5] = norm;
+        L[5] = norm_of(2 * (size_t)l + 1);
         L[6] = add(DType::Q4_K, c.n_ff, c.n_embd, 0.05f, "gate");
         L[7] = add(DType::Q4_K, c.n_ff, c.n_embd, 0.05f, "up");
         L[8] = add(DType::Q4_K, c.n_ff, c.n_embd, 0.05f, "down");  // n_ff rows x n_embd cols

@@ -10,6 +10,7 @@ import numpy as np
 import pytest
 
 import pyoracle as P
+from builders import norm_raw, q_rows
 from xwfes_amd import ftx
 
 pytestmark = pytest.mark.gpu
@@ -157,14 +158,13 @@ def test_verify_mfma_down(gctx, orc):
         w = (rng.standard_normal((rows, cols)) * 0.02).astype(np.float32)
         return dict(raw=orc.quantize(w, dt), dtype=dt, ne0=cols, ne1=rows)
 
-    ones = np.ones(512, np.float32).view(np.uint8).copy()
     model["tok_embd"] = q(500, 512, P.Q8_0)
     model["output"] = q(500, 512, P.Q8_0)
-    model["out_norm"] = dict(raw=ones, dtype=P.F32, ne0=512, ne1=1)
+    model["out_norm"] = norm_raw(rng, 512)
     for l, ddt in enumerate((P.Q4_K, P.Q6_K)):
         p = "blk.%d." % l
-        model[p + "attn_norm"] = dict(raw=ones, dtype=P.F32, ne0=512, ne1=1)
-        model[p + "ffn_norm"] = dict(raw=ones, dtype=P.F32, ne0=512, ne1=1)
+        model[p + "attn_norm"] = norm_raw(rng, 512)
+        model[p + "ffn_norm"] = norm_raw(rng, 512)
         model[p + "q"] = q(512, 512, P.Q8_0)
         model[p + "k"] = q(128, 512, P.Q8_0)
         model[p + "v"] = q(128, 512, P.Q8_0)
@@ -202,31 +202,30 @@ def q4k_m_dtypes(layer, n_layer):
     return dict(q=P.Q4_K, k=P.Q4_K, v=dv, o=P.Q4_K, gate=P.Q4_K, up=P.Q4_K, down=dv)
 
 
-def test_verify_8b_shape_two_layers(gctx, orc):
+@pytest.mark.parametrize("npast", [64, 2040])
+def test_verify_8b_shape_two_layers(gctx, orc, npast):
     """8B layer shape (d 4096, 32/8 heads x 128, FFN 14336, V 128256), Q4_K
     with Q6_K attn_v / ffn_down on one layer and a Q6_K head, 2 layers, an
-    8-token chain at context 64, theta 500000."""
+    8-token chain at context 64 and at the headline workload's context 2048
+    (17 attention chunks through the Q4_K o-projection's fused combine),
+    theta 500000."""
     orc.set_threads(16)
     cfg = P.model_cfg(2, 4096, 32, 8, 128, 14336, 128256, rope_theta=500000.0)
     model = {"cfg": dict(cfg)}
     rng = np.random.default_rng(21)
 
     def q(rows, cols, dt):
-        # at most 2048 distinct random rows, tiled (keeps host quantisation short)
-        u = min(rows, 2048)
-        w = (rng.standard_normal((u, cols)) * 0.02).astype(np.float32)
-        raw = np.tile(orc.quantize(w, dt), -(-rows // u))[: rows * P.row_bytes(dt, cols)]
-        return dict(raw=np.ascontiguousarray(raw), dtype=dt, ne0=cols, ne1=rows)
+        # 2048 random rows repeated with moved scales (host quantisation stays short)
+        return q_rows(orc, rng, rows, cols, dt)
 
-    ones = np.ones(4096, np.float32).view(np.uint8).copy()
     model["tok_embd"] = q(128256, 4096, P.Q4_K)
     model["output"] = q(128256, 4096, P.Q6_K)
-    model["out_norm"] = dict(raw=ones, dtype=P.F32, ne0=4096, ne1=1)
+    model["out_norm"] = norm_raw(rng, 4096)
     for l in range(2):
         dts = q4k_m_dtypes(l if l == 0 else 5, 32)
         p = "blk.%d." % l
-        model[p + "attn_norm"] = dict(raw=ones, dtype=P.F32, ne0=4096, ne1=1)
-        model[p + "ffn_norm"] = dict(raw=ones, dtype=P.F32, ne0=4096, ne1=1)
+        model[p + "attn_norm"] = norm_raw(rng, 4096)
+        model[p + "ffn_norm"] = norm_raw(rng, 4096)
         model[p + "q"] = q(4096, 4096, dts["q"])
         model[p + "k"] = q(1024, 4096, dts["k"])
         model[p + "v"] = q(1024, 4096, dts["v"])
@@ -235,7 +234,7 @@ def test_verify_8b_shape_two_layers(gctx, orc):
         model[p + "up"] = q(14336, 4096, dts["up"])
         model[p + "down"] = q(14336, 4096, dts["down"])
     toks = rng.integers(0, 128256, 8).tolist()
-    got, want, _, _ = run_both(gctx, orc, model, toks, 64, 96)
+    got, want, _, _ = run_both(gctx, orc, model, toks, npast, max(96, npast + 8))
     assert rel_err_rows(got, want) < LOGIT_TOL
 
 
@@ -272,28 +271,24 @@ def test_verify_8b_tree52_q8_attention(gctx, orc):
     """The tree workload's shape: 8B layers (d 4096, 32/8 heads x 128, FFN
     14336) with Q8_0 attention projections and a Q4_K FFN, 2 layers, a
     52-node draft tree (branching 4, 4, 2) at context 4096, then residual
-    acceptance of the device's logits against the oracle's on the same rows.
-    (Vocabulary 32000 and a Q6_K head keep the oracle's head short.)"""
+    acceptance of the device's logits against the oracle's on the same rows,
+    over the full Llama-3 vocabulary (128256) with a Q6_K head."""
     orc.set_threads(16)
-    V = 32000
+    V = 128256
     cfg = P.model_cfg(2, 4096, 32, 8, 128, 14336, V, rope_theta=500000.0)
     model = {"cfg": dict(cfg)}
     rng = np.random.default_rng(52)
 
     def q(rows, cols, dt):
-        u = min(rows, 2048)
-        w = (rng.standard_normal((u, cols)) * 0.02).astype(np.float32)
-        raw = np.tile(orc.quantize(w, dt), -(-rows // u))[: rows * P.row_bytes(dt, cols)]
-        return dict(raw=np.ascontiguousarray(raw), dtype=dt, ne0=cols, ne1=rows)
+        return q_rows(orc, rng, rows, cols, dt)
 
-    ones = np.ones(4096, np.float32).view(np.uint8).copy()
     model["tok_embd"] = q(V, 4096, P.Q4_K)
     model["output"] = q(V, 4096, P.Q6_K)
-    model["out_norm"] = dict(raw=ones, dtype=P.F32, ne0=4096, ne1=1)
+    model["out_norm"] = norm_raw(rng, 4096)
     for l in range(2):
         p = "blk.%d." % l
-        model[p + "attn_norm"] = dict(raw=ones, dtype=P.F32, ne0=4096, ne1=1)
-        model[p + "ffn_norm"] = dict(raw=ones, dtype=P.F32, ne0=4096, ne1=1)
+        model[p + "attn_norm"] = norm_raw(rng, 4096)
+        model[p + "ffn_norm"] = norm_raw(rng, 4096)
         for nm, rows, cols in (("q", 4096, 4096), ("k", 1024, 4096), ("v", 1024, 4096),
                                ("o", 4096, 4096)):
             model[p + nm] = q(rows, cols, P.Q8_0)
@@ -343,17 +338,13 @@ def _wide_model(orc, neox, seed):
     rng = np.random.default_rng(seed)
 
     def q(rows, cols, dt):
-        u = min(rows, 1024)
-        w = (rng.standard_normal((u, cols)) * 0.02).astype(np.float32)
-        raw = np.tile(orc.quantize(w, dt), -(-rows // u))[: rows * P.row_bytes(dt, cols)]
-        return dict(raw=np.ascontiguousarray(raw), dtype=dt, ne0=cols, ne1=rows)
+        return q_rows(orc, rng, rows, cols, dt, unique=1024)
 
-    ones = np.ones(4096, np.float32).view(np.uint8).copy()
     model["tok_embd"] = q(1000, 4096, P.Q4_K)
     model["output"] = q(1000, 4096, P.Q6_K)
-    model["out_norm"] = dict(raw=ones, dtype=P.F32, ne0=4096, ne1=1)
-    model["blk.0.attn_norm"] = dict(raw=ones, dtype=P.F32, ne0=4096, ne1=1)
-    model["blk.0.ffn_norm"] = dict(raw=ones, dtype=P.F32, ne0=4096, ne1=1)
+    model["out_norm"] = norm_raw(rng, 4096)
+    model["blk.0.attn_norm"] = norm_raw(rng, 4096)
+    model["blk.0.ffn_norm"] = norm_raw(rng, 4096)
     for nm, rows, dt in (("q", 4096, P.Q4_K), ("k", 1024, P.Q4_K), ("v", 1024, P.Q6_K),
                          ("o", 4096, P.Q4_K), ("gate", 4096, P.Q4_K), ("up", 4096, P.Q4_K),
                          ("down", 4096, P.Q4_K)):
@@ -380,6 +371,45 @@ def test_verify_fused_rope_kv(gctx, orc, neox, parents):
     np.testing.assert_allclose(kg.astype(np.float32), kc.astype(np.float32), rtol=2e-3, atol=2e-3)
     np.testing.assert_allclose(vg.astype(np.float32), vc.astype(np.float32), rtol=2e-3, atol=2e-3)
     assert np.array_equal(kg[:, :npast], kc[:, :npast]) and np.array_equal(vg[:, :npast], vc[:, :npast])
+
+
+@pytest.mark.parametrize("parents", [None, [-1, 0, 0, 1, 1, 2, 2, 3]])
+def test_verify_long_context_8192(gctx, orc, parents):
+    """Context 8180 (64 whole attention chunks and a partial one: more than
+    the combine's 32-chunk prefetch batch and its 64-chunk loops) on one
+    8B-width layer whose Q4_K o-projection takes the fused combine, an
+    8-token chain and a tree."""
+    orc.set_threads(16)
+    model = _wide_model(orc, 0, seed=81)
+    toks = list(np.random.default_rng(82).integers(0, 1000, 8))
+    npast = 8180
+    got, want, _, _ = run_both(gctx, orc, model, toks, npast, npast + 12, parents=parents)
+    assert rel_err_rows(got, want) < LOGIT_TOL
+
+
+def test_kv_of_another_model_rejected(gctx, orc):
+    """A cache made for one model is refused by a model of the same layer
+    count and K width but more query heads or a larger step (its attention
+    partials were sized for the creating model)."""
+    a = P.model_cfg(1, 256, 4, 2, 64, 256, 100)
+    b = P.model_cfg(1, 512, 8, 2, 64, 256, 100)
+    ma, mb = P.make_model(orc, a, TINY_DT, seed=1), P.make_model(orc, b, TINY_DT, seed=2)
+    ta, tb = upload_model(gctx, ma), upload_model(gctx, mb)
+    ga = gctx.model(a, ta, max_tokens=8)
+    gb = gctx.model(b, tb, max_tokens=8)
+    gc = gctx.model(a, ta, max_tokens=16)
+    kv = ga.kv(64)
+    buf = gctx.buffer(16 * 100 * 4)
+    for gm, M in ((gb, 4), (gc, 12)):
+        with pytest.raises(ftx.FtxError) as e:
+            gm.verify(kv, list(range(M)), buf.ptr)
+        assert e.value.code == -1  # FTX_E_INVALID
+    ga.verify(kv, [1, 2, 3], buf.ptr)  # the creating model still runs
+    gctx.sync()
+    for o in (buf, kv, ga, gb, gc):
+        o.free()
+    free_all(ta)
+    free_all(tb)
 
 
 

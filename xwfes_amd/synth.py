@@ -71,16 +71,19 @@ def uniform_mix(dt, embd=None):
 
 
 def build(ctx, cfg, dtype_of, seed=1, std=0.02, tied=False):
-    """Returns {name: ftx.Tensor}.  Norm weights are F32 ones."""
+    """Returns {name: ftx.Tensor}.  Norm weights are F32 vectors of
+    1 + 0.1 N(0, 1), one per layer and role."""
     shapes = [s for s in tensor_shapes(cfg) if not (tied and s[0] == "output")]
     big = max(ne0 * ne1 for name, ne0, ne1 in shapes)
     scratch = ctx.buffer(big * 4)
     tensors = {}
+    nrng = np.random.default_rng(seed)
     try:
         for i, (name, ne0, ne1) in enumerate(shapes):
             key = name.split(".")[-1]
             if key in ("attn_norm", "ffn_norm", "out_norm"):
-                tensors[name] = ctx.upload(np.ones(ne0, np.float32).view(np.uint8), F32, (ne0, 1))
+                w = (1.0 + 0.1 * nrng.standard_normal(ne0)).astype(np.float32)
+                tensors[name] = ctx.upload(w.view(np.uint8), F32, (ne0, 1))
                 continue
             dt = dtype_of(name)
             t = ctx.alloc(dt, (ne0, ne1))
