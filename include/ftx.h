@@ -144,6 +144,17 @@ int ftx_matmul(ftx_ctx* ctx, const float* x, int64_t M, int64_t K, const ftx_ten
 int ftx_down_axpy(ftx_ctx* ctx, const float* x, int64_t M, int64_t n_in, const ftx_tensor* W,
                   float* y);
 
+/* No counterpart in the reference: ftx_down_axpy for callers that cannot
+ * allocate (code under HIP graph capture, tight serving loops, harnesses
+ * that forbid hipMalloc).  x and y must be device memory; the split partials
+ * go to a file-scope device array of the library (16 MiB per GPU, held until
+ * the process ends) instead of the context's workspace, so nothing is
+ * allocated.  Shapes whose partials exceed that array return FTX_E_RANGE.
+ * Every call on one GPU shares that GPU's array: calls that overlap on one
+ * GPU (several streams or threads) race. */
+int ftx_down_axpy_noalloc(ftx_ctx* ctx, const float* x, int64_t M, int64_t n_in,
+                          const ftx_tensor* W, float* y);
+
 /* ExpertChunkJob (include/ft/backend.h:7-19) with device pointers: gate,
  * up and down point at IC rows of resident expert weights. */
 typedef struct {

@@ -1,6 +1,7 @@
 // api.hip -- the C ABI of include/ftx.h: contexts, resident tensors and the
 // IBackend-level operations.  The verify step lives in verify.hip.
 #include <cstdio>
+#include <mutex>
 #include <new>
 
 #include "ftx_internal.h"
@@ -63,6 +64,34 @@ int ftx_pinned(ftx_ctx* ctx, size_t bytes, void** out) {
     return FTX_OK;
 }
 
+// Scratch of ftx_down_axpy_noalloc (the split partials of its launches): a
+// file-scope device array, one copy per GPU, held until the process ends.
+// Host code never passes the array's name to a kernel; it uses the device
+// address that hipGetSymbolAddress returns for the current device.
+constexpr size_t NOALLOC_SCRATCH_FLOATS = (size_t)4 << 20;  // 16 MiB
+static __device__ __align__(256) float scratch[NOALLOC_SCRATCH_FLOATS];
+
+constexpr int NOALLOC_MAX_DEVICES = 64;
+static std::mutex g_scratch_mu;
+static float* g_scratch_ptr[NOALLOC_MAX_DEVICES] = {};
+
+// the scratch address on `device` (looked up once per device, with the
+// device current); null on failure
+static float* noalloc_scratch(int device) {
+    if (device < 0 || device >= NOALLOC_MAX_DEVICES) return nullptr;
+    std::lock_guard<std::mutex> lk(g_scratch_mu);
+    if (!g_scratch_ptr[device]) {
+        void* ptr = nullptr;
+        if (hipSetDevice(device) != hipSuccess ||
+            hipGetSymbolAddress(&ptr, HIP_SYMBOL(scratch)) != hipSuccess) {
+            (void)hipGetLastError();
+            return nullptr;
+        }
+        g_scratch_ptr[device] = (float*)ptr;
+    }
+    return g_scratch_ptr[device];
+}
+
 bool ftx_is_device_ptr(const void* p) {
     hipPointerAttribute_t at;
     if (hipPointerGetAttributes(&at, p) != hipSuccess) {
@@ -99,6 +128,12 @@ int ftx_create(int device, ftx_ctx** out) {
     c->stream = c->own_stream;
     hipDeviceProp_t pr;
     if (hipGetDeviceProperties(&pr, device) == hipSuccess) c->cu_count = pr.multiProcessorCount;
+    c->noalloc_scratch = noalloc_scratch(device);
+    if (!c->noalloc_scratch) {
+        (void)hipStreamDestroy(c->own_stream);
+        delete c;
+        return FTX_E_DEVICE;
+    }
     *out = c;
     return FTX_OK;
 }
@@ -356,6 +391,31 @@ int ftx_down_axpy(ftx_ctx* ctx, const float* x, int64_t M, int64_t n_in, const f
     if (s.y_host)
         FTX_HIP(ctx, hipMemcpyAsync(y, s.y, (size_t)(M * N) * sizeof(float),
                                     hipMemcpyDeviceToHost, ctx->stream));
+    FTX_HIP(ctx, hipStreamSynchronize(ctx->stream));
+    return FTX_OK;
+}
+
+// ftx_down_axpy on device x / y with its split partials in the library's
+// file-scope scratch array instead of the context's workspace: no device or
+// host memory is allocated.  Every call on a GPU shares that GPU's array, so
+// calls that overlap on one GPU race; each call writes every partial it reads.
+int ftx_down_axpy_noalloc(ftx_ctx* ctx, const float* x, int64_t M, int64_t n_in,
+                          const ftx_tensor* W, float* y) {
+    if (!ctx || !x || !W || !y) return ftx_fail(ctx, FTX_E_INVALID, "null argument");
+    if (M < 0 || n_in != W->nrows)
+        return ftx_fail(ctx, FTX_E_INVALID, "down_axpy_noalloc: n_in must equal the weight row count");
+    if (!ftx_is_device_ptr(x) || !ftx_is_device_ptr(y))
+        return ftx_fail(ctx, FTX_E_INVALID, "down_axpy_noalloc: x and y must be device memory");
+    const int64_t N = W->ne[0];
+    if (M == 0) return FTX_OK;
+    const size_t pf = down_scratch_floats(M, n_in, N);
+    if (pf > NOALLOC_SCRATCH_FLOATS)
+        return ftx_fail(ctx, FTX_E_RANGE,
+                        "down_axpy_noalloc: the shape needs " + std::to_string(pf) +
+                            " floats of scratch, above the limit of " +
+                            std::to_string(NOALLOC_SCRATCH_FLOATS));
+    FTX_HIP(ctx, launch_down(ctx->stream, W->data, W->dtype, W->row_bytes, n_in, N, x, n_in, M, y,
+                             N, ctx->noalloc_scratch));
     FTX_HIP(ctx, hipStreamSynchronize(ctx->stream));
     return FTX_OK;
 }

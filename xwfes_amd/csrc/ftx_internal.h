@@ -60,6 +60,9 @@ struct ftx_ctx {
     // small pinned host buffer for step arguments
     void* pinned = nullptr;
     size_t pinned_bytes = 0;
+    // device address of the no-allocation entry points' scratch array on
+    // this context's device
+    float* noalloc_scratch = nullptr;
 };
 
 struct ftx_tensor {

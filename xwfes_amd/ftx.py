@@ -104,6 +104,7 @@ def load(path=LIB_PATH):
         "ftx_dequant": (C.c_int, [_vp, _vp, _vp]),
         "ftx_matmul": (C.c_int, [_vp, _vp, _i64, _i64, _vp, _vp]),
         "ftx_down_axpy": (C.c_int, [_vp, _vp, _i64, _i64, _vp, _vp]),
+        "ftx_down_axpy_noalloc": (C.c_int, [_vp, _vp, _i64, _i64, _vp, _vp]),
         "ftx_expert_chunk": (C.c_int, [_vp, C.POINTER(ExpertJob)]),
         "ftx_alloc_staging": (_vp, [_vp, C.c_size_t]),
         "ftx_free_staging": (C.c_int, [_vp, _vp]),
