@@ -243,6 +243,25 @@ typedef struct {
  * prefix cache) is a sequence of advancing chains, the last with logits. */
 int ftx_verify_step(ftx_ctx* ctx, ftx_model* m, ftx_kv* kv, const ftx_verify_args* a);
 
+/* Several sequences in one step (no counterpart in the reference, whose
+ * Engine holds one KvCache, include/ft/kv_cache.h:10-47): sequence s
+ * verifies its own draft (a chain or a tree) against its own cache, as
+ * ftx_verify_step would, while every projection streams the weights once
+ * for the tokens of all sequences.  At most FTX_MAX_SEQ sequences and
+ * max_tokens tokens in total; every cache must be made for this model and
+ * distinct; the logits pointers are all NULL (no LM head) or all set. */
+enum { FTX_MAX_SEQ = 16 };
+typedef struct {
+    ftx_kv* kv;
+    int64_t M;               /* tokens of this sequence (>= 1) */
+    const int32_t* tokens;   /* host [M] */
+    const int32_t* parents;  /* host [M], in this sequence's node ids, or NULL */
+    float* logits;           /* device [M][vocab] or NULL */
+    int32_t advance;         /* npast += M afterwards */
+    int32_t pad_;
+} ftx_seq_args;
+int ftx_verify_batch(ftx_ctx* ctx, ftx_model* m, const ftx_seq_args* seqs, int64_t nseq);
+
 typedef struct {
     const float* base_row;  /* device [V]: target logits before the draft */
     const float* rows;      /* device [M][V]: target logits of the M nodes */

@@ -189,7 +189,48 @@ hipError_t launch_mv(hipStream_t st, const GemvSeg* segs, int nseg, const int8_t
 hipError_t launch_part_reduce(hipStream_t st, const float* part, int S, int64_t N, int64_t M,
                               float* y, int64_t ldy);
 
-// MFMA ffn_down (k_down.hip) over a re-tiled copy of the weights
+// Large-M GEMMs (k_gemm.hip): activations as fp16 hi / lo planes [Mp][K] and
+// their 32-element sums [Mp][K / 32] (Mp = tokens padded to 64), weights as
+// the tiled Q4_K copy or the planar Q8_0 / Q4_0 copy.
+struct MmAct {
+    _Float16 *xh, *xl, *sh, *sl;
+    int64_t Mp, K;
+};
+struct MmSeg {
+    const uint8_t* W;
+    int dt;             // FTX_Q4_K (tiled), FTX_Q8_0_PLANAR or FTX_Q4_0_PLANAR
+    int64_t N;          // rows
+    int rpt;            // Q4_K tile rows
+    int64_t row_bytes;  // planar rows
+};
+// output rows of sequence s (row0[s] <= m < row0[s + 1]) go to base[s] +
+// (m - row0[s]) * ld
+struct MmOut {
+    float* base[FTX_MAX_SEQ];
+    int64_t row0[FTX_MAX_SEQ + 1];
+    int nseq;
+    int64_t ld;
+    int accum;
+};
+int64_t mm_pad_tokens(int64_t M);
+size_t mm_act_halves(int64_t Mp, int64_t K);
+MmAct mm_act(void* buf, int64_t Mp, int64_t K);
+hipError_t launch_mm_prep(hipStream_t st, const float* x, int64_t ldx, const float* normw,
+                          float eps, int64_t M, const MmAct& act);
+bool mm_supported(int dt, int64_t K);
+bool mm_down_supported(int dt, int64_t n_in, int64_t N);
+// split-sum scratch of a launch over N output columns (`ntiles` 256-row
+// workgroup columns, `steps` 256-element contraction steps)
+size_t mm_part_floats(int64_t Mp, int64_t N, int64_t steps, int64_t ntiles, int cu_count);
+size_t mm_down_part_floats(int64_t Mp, int64_t n_in, int64_t N, int cu_count);
+// epi: EPI_STORE / EPI_ACCUM (out.accum) or EPI_SWIGLU (segments gate, up)
+hipError_t launch_mm(hipStream_t st, const MmSeg* segs, int nseg, const MmAct& act, int64_t M,
+                     int epi, const MmOut& out, float* part, size_t part_floats, int cu_count);
+hipError_t launch_mm_down(hipStream_t st, const uint8_t* tiled, int64_t n_in, int64_t N,
+                          const float* h, int64_t ldh, int64_t M, const MmOut& out, float* part,
+                          size_t part_floats, int cu_count);
+
+// MFMA ffn_down (k_down.hip) over a re-tiled copy of the weights// MFMA ffn_down (k_down.hip) over a re-tiled copy of the weights
 bool down_mfma_supported(int dt, int64_t n_in, int64_t N, int64_t M);
 size_t down_tiled_bytes(int dt, int64_t n_in, int64_t N);
 hipError_t launch_down_tile(hipStream_t st, const uint8_t* src, int64_t src_row_bytes, int dt,

@@ -1,0 +1,874 @@
+// k_gemm.hip -- the verify step's projections for more than 8 tokens (draft
+// trees, several sequences in one step): quantised GEMMs that stream each
+// weight once per 64-token tile, on v_mfma_f32_16x16x32_f16.
+//
+// Operands.  The activations enter as fp16 hi + lo parts (x = hi + lo to
+// ~22 bits; two MFMAs per product); the weights as exact small integers,
+// with their block scales applied to fp32 accumulators:
+//   Q4_K  w = d*sc_j*q - dmin*m_j   B = sc_j*q (<= 945, exact in fp16),
+//         a super-block's 8 sub-blocks accumulate into a temporary that is
+//         added with the factor d; the min term dmin * sum_j m_j X_j (X_j the
+//         sub-block sums of the activations) is one 16x16x16 MFMA per
+//         super-block on the m_j
+//   Q8_0  w = d*q                   B = q, one temporary per 32-block
+//   Q4_0  w = d*(q - 8)             B = q - 8, the same
+// so every product and sum inside an MFMA is exact and the rounding is that
+// of fp32 accumulation.
+//
+// Row-dot form (y = x W^T, blocks along the contraction; every projection
+// but ffn_down): a workgroup of 4 waves owns 256 weight rows (64 per wave,
+// four 16-column MFMA tiles) and a 64-token tile (four 16-row MFMA tiles);
+// the activation tile is staged in LDS 64 contraction elements at a time
+// (double-buffered, one barrier per stage) and shared by the four waves,
+// which read their weights straight from the tiled (Q4_K) or planar (Q8_0,
+// Q4_0) copies the model keeps.  Split-K across workgroups where the tiles
+// alone do not fill the device; partial sums then go to a buffer that the
+// reduce launch adds in split order with the epilogue (store, accumulate,
+// SwiGLU).
+//
+// Column-axpy form (ffn_down in the reference orientation, n_ff rows of
+// n_embd columns, Q4_K blocks along the output): per 32-row slice the
+// workgroup (one 256-column block) stages h*d and h*dmin of its rows as
+// hi/lo activation operands and the 6-bit scales / mins as fp16 tables; the
+// weights (the re-tiled copy of k_down.hip) enter as sc*q.
+#include "ftx_internal.h"
+#include "quant_dev.h"
+
+namespace {
+
+typedef _Float16 v8h __attribute__((ext_vector_type(8)));
+typedef _Float16 v4h __attribute__((ext_vector_type(4)));
+typedef _Float16 v2h __attribute__((ext_vector_type(2)));
+typedef float v4f __attribute__((ext_vector_type(4)));
+typedef int v4i __attribute__((ext_vector_type(4)));
+typedef int v2i __attribute__((ext_vector_type(2)));
+
+constexpr int MM_TOK = 64;              // tokens per workgroup tile
+constexpr int MM_MS = MM_TOK / 16;      // 16-token MFMA tiles
+constexpr int MM_WAVES = 4;
+constexpr int MM_WROWS = 64;            // weight rows (output columns) per wave
+constexpr int MM_NT = MM_WROWS / 16;    // 16-column MFMA tiles per wave
+constexpr int MM_KC = 64;               // contraction elements per LDS stage
+constexpr int MM_PITCH = MM_KC + 8;     // halves per staged token row
+
+// the activation operands of ffn_down are formed as (h d) * 2^10 so that
+// their fp16 lo parts stay clear of the subnormal range (undone on the
+// outputs)
+constexpr float MMD_ASCALE = 1024.f;
+
+__device__ __forceinline__ v8h ld8h(const _Float16* p) { return *(const v8h*)p; }
+
+// 8 nibbles (slot t: byte t % 4, nibble t / 4) -> fp16 q - bias, exact
+__device__ __forceinline__ v8h nib8(uint32_t w, float bias) {
+    const uint32_t lo = w & 0x0F0F0F0Fu, hi = (w >> 4) & 0x0F0F0F0Fu;
+    // 0x64 in the high byte: fp16 1024 + q
+    const uint32_t p0 = __builtin_amdgcn_perm(lo, 0x64646464u, 0x00050004u);
+    const uint32_t p1 = __builtin_amdgcn_perm(lo, 0x64646464u, 0x00070006u);
+    const uint32_t p2 = __builtin_amdgcn_perm(hi, 0x64646464u, 0x00050004u);
+    const uint32_t p3 = __builtin_amdgcn_perm(hi, 0x64646464u, 0x00070006u);
+    const v2h b = {(_Float16)(-1024.f - bias), (_Float16)(-1024.f - bias)};
+    const v2h h0 = __builtin_bit_cast(v2h, p0) + b, h1 = __builtin_bit_cast(v2h, p1) + b;
+    const v2h h2 = __builtin_bit_cast(v2h, p2) + b, h3 = __builtin_bit_cast(v2h, p3) + b;
+    return v8h{h0[0], h0[1], h1[0], h1[1], h2[0], h2[1], h3[0], h3[1]};
+}
+
+// 8 low (hi = false) or high nibbles of 8 bytes, byte order -> fp16 q, exact
+__device__ __forceinline__ v8h nib8_bytes(v2i w, bool high) {
+    const uint32_t a = high ? ((uint32_t)w.x >> 4) & 0x0F0F0F0Fu : (uint32_t)w.x & 0x0F0F0F0Fu;
+    const uint32_t b = high ? ((uint32_t)w.y >> 4) & 0x0F0F0F0Fu : (uint32_t)w.y & 0x0F0F0F0Fu;
+    const uint32_t p0 = __builtin_amdgcn_perm(a, 0x64646464u, 0x00050004u);
+    const uint32_t p1 = __builtin_amdgcn_perm(a, 0x64646464u, 0x00070006u);
+    const uint32_t p2 = __builtin_amdgcn_perm(b, 0x64646464u, 0x00050004u);
+    const uint32_t p3 = __builtin_amdgcn_perm(b, 0x64646464u, 0x00070006u);
+    const v2h o = {(_Float16)(-1024.f), (_Float16)(-1024.f)};
+    const v2h h0 = __builtin_bit_cast(v2h, p0) + o, h1 = __builtin_bit_cast(v2h, p1) + o;
+    const v2h h2 = __builtin_bit_cast(v2h, p2) + o, h3 = __builtin_bit_cast(v2h, p3) + o;
+    return v8h{h0[0], h0[1], h1[0], h1[1], h2[0], h2[1], h3[0], h3[1]};
+}
+
+// 8 signed bytes -> fp16 q, exact: (q ^ 0x80) = q + 128 as the low byte of
+// fp16 1024 + q + 128, then - 1152
+__device__ __forceinline__ v8h i8x8(v2i w) {
+    const uint32_t a = (uint32_t)w.x ^ 0x80808080u, b = (uint32_t)w.y ^ 0x80808080u;
+    const uint32_t p0 = __builtin_amdgcn_perm(a, 0x64646464u, 0x00050004u);
+    const uint32_t p1 = __builtin_amdgcn_perm(a, 0x64646464u, 0x00070006u);
+    const uint32_t p2 = __builtin_amdgcn_perm(b, 0x64646464u, 0x00050004u);
+    const uint32_t p3 = __builtin_amdgcn_perm(b, 0x64646464u, 0x00070006u);
+    const v2h o = {(_Float16)(-1152.f), (_Float16)(-1152.f)};
+    const v2h h0 = __builtin_bit_cast(v2h, p0) + o, h1 = __builtin_bit_cast(v2h, p1) + o;
+    const v2h h2 = __builtin_bit_cast(v2h, p2) + o, h3 = __builtin_bit_cast(v2h, p3) + o;
+    return v8h{h0[0], h0[1], h1[0], h1[1], h2[0], h2[1], h3[0], h3[1]};
+}
+
+__device__ __forceinline__ void split_hl(float v, _Float16& h, _Float16& l) {
+#pragma clang fp contract(off)
+    h = (_Float16)v;
+    l = (_Float16)(v - (float)h);
+}
+
+// ---------------------------------------------------------------- prep
+// One workgroup (256 threads) per token row m < Mp; rows m >= M are zeros.
+// v = (x * inv) * w with inv = 1 / sqrt(sum x^2 / K + eps) when normw is
+// given (src/engine.cpp:23-41), else v = x; writes v as fp16 hi / lo planes
+// [Mp][K] and the 32-element sums of v as hi / lo planes [Mp][K / 32].
+__global__ void __launch_bounds__(256) k_mm_prep(const float* __restrict__ x, int64_t ldx,
+                                                 const float* __restrict__ normw, float eps,
+                                                 int64_t K, int M, _Float16* __restrict__ xh,
+                                                 _Float16* __restrict__ xl,
+                                                 _Float16* __restrict__ sh,
+                                                 _Float16* __restrict__ sl) {
+#pragma clang fp contract(off)
+    __shared__ float red[4];
+    const int m = blockIdx.x, t = threadIdx.x;
+    const int64_t nsub = K / 32;
+    _Float16* oh = xh + (int64_t)m * K;
+    _Float16* ol = xl + (int64_t)m * K;
+    if (m >= M) {  // block-uniform
+        const v4h z = {};
+        for (int64_t k = 4 * t; k < K; k += 1024) {
+            *(v4h*)(oh + k) = z;
+            *(v4h*)(ol + k) = z;
+        }
+        for (int64_t j = t; j < nsub; j += 256) {
+            sh[m * nsub + j] = (_Float16)0.f;
+            sl[m * nsub + j] = (_Float16)0.f;
+        }
+        return;
+    }
+    const float* row = x + (int64_t)m * ldx;
+    float inv = 1.f;
+    if (normw) {
+        float ss = 0.f;
+        for (int64_t k = 4 * t; k < K; k += 1024) {
+            const float4 v = *(const float4*)(row + k);
+            ss += v.x * v.x;
+            ss += v.y * v.y;
+            ss += v.z * v.z;
+            ss += v.w * v.w;
+        }
+#pragma unroll
+        for (int o = 32; o > 0; o >>= 1) ss += __shfl_xor(ss, o, 64);
+        if ((t & 63) == 0) red[t >> 6] = ss;
+        __syncthreads();
+        ss = (red[0] + red[1]) + (red[2] + red[3]);
+        inv = 1.f / sqrtf(ss / (float)K + eps);
+    }
+    for (int64_t k = 4 * t; k < K; k += 1024) {
+        const float4 v = *(const float4*)(row + k);
+        float o[4] = {v.x, v.y, v.z, v.w};
+        if (normw) {
+            const float4 w = *(const float4*)(normw + k);
+            o[0] = (o[0] * inv) * w.x;
+            o[1] = (o[1] * inv) * w.y;
+            o[2] = (o[2] * inv) * w.z;
+            o[3] = (o[3] * inv) * w.w;
+        }
+        v4h hv, lv;
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
+            _Float16 h, l;
+            split_hl(o[i], h, l);
+            hv[i] = h;
+            lv[i] = l;
+        }
+        *(v4h*)(oh + k) = hv;
+        *(v4h*)(ol + k) = lv;
+        // the 8 threads of a 32-element sub-block
+        float s = (o[0] + o[1]) + (o[2] + o[3]);
+        s += __shfl_xor(s, 1, 64);
+        s += __shfl_xor(s, 2, 64);
+        s += __shfl_xor(s, 4, 64);
+        if ((t & 7) == 0) {
+            _Float16 h, l;
+            split_hl(s, h, l);
+            sh[m * nsub + k / 32] = h;
+            sl[m * nsub + k / 32] = l;
+        }
+    }
+}
+
+// ---------------------------------------------------------------- row-dot
+
+struct MmSegDev {
+    const uint8_t* W;   // tiled (Q4_K) or planar (Q8_0 / Q4_0) copy
+    int64_t N;          // weight rows
+    int64_t unit0;      // first 64-row unit of the segment in the launch
+    int64_t col0;       // first output column of the segment
+    int64_t row_bytes;  // planar rows
+    int rpt;            // Q4_K tile rows (16 or 32)
+};
+
+struct MmOutDev {
+    // row m of the outputs: base[s] + (m - row0[s]) * ld + col for the
+    // sequence s with row0[s] <= m < row0[s + 1]; a split ks adds
+    // ks * split_stride
+    float* base[FTX_MAX_SEQ];
+    int64_t row0[FTX_MAX_SEQ + 1];
+    int nseq;
+    int64_t ld;
+    int64_t split_stride;
+    int accum;          // += instead of =
+};
+
+struct MmArgs {
+    MmSegDev seg[3];
+    int nseg;
+    int64_t units;      // 64-row units over all segments
+    int64_t K;
+    int nsb;            // 256-element steps of the contraction
+    int sb_per_split;
+    const _Float16 *xh, *xl, *sh, *sl;
+    int M;
+    MmOutDev out;
+};
+
+__device__ __forceinline__ int mm_seg_of(const MmArgs& a, int64_t u) {
+    int si = 0;
+    while (si + 1 < a.nseg && u >= a.seg[si + 1].unit0) ++si;
+    return si;
+}
+
+// weights of one 256-element step for the wave's four column tiles
+template <int DT>
+struct MmW;
+template <>
+struct MmW<FTX_Q4_K> {
+    v2i qs[MM_NT][4];  // the lane's 8 quant bytes of each 64-element chunk
+    v4i hdr[MM_NT];    // d | dmin, 12 scale bytes of the lane's row
+};
+template <>
+struct MmW<FTX_Q8_0_PLANAR> {
+    v2i q[MM_NT][8];   // 8 quant bytes of each 32-block
+    v4i d[MM_NT];      // the 8 fp16 block scales
+};
+template <>
+struct MmW<FTX_Q4_0_PLANAR> {
+    uint32_t q[MM_NT][8];  // 4 quant bytes (8 nibbles) of each 32-block
+    v4i d[MM_NT];
+};
+
+// Lane (col = l % 16, kq = l / 16) of MFMA column tile t holds B[8 kq + e][col]
+// of each 32-element K-step.
+template <int DT>
+__device__ __forceinline__ void mm_load_w(MmW<DT>& o, const MmSegDev& sg, int64_t rbase, int sb,
+                                          int nsb, int col, int kq) {
+#pragma unroll
+    for (int t = 0; t < MM_NT; ++t) {
+        int64_t n = rbase + 16 * t + col;  // the lane's weight row in the segment
+        if (n >= sg.N) n = sg.N - 1;
+        if constexpr (DT == FTX_Q4_K) {
+            const int R = sg.rpt;
+            const int64_t T = n / R;
+            const int r = (int)(n % R), li = r + R * (kq >> 1), half = kq & 1;
+            const uint8_t* blk = sg.W + (T * nsb + sb) * (int64_t)R * 144;
+#pragma unroll
+            for (int c = 0; c < 4; ++c)
+                o.qs[t][c] = *(const v2i*)(blk + c * R * 32 + li * 16 + 8 * half);
+            o.hdr[t] = *(const v4i*)(blk + 4 * R * 32 + r * 16);
+        } else if constexpr (DT == FTX_Q8_0_PLANAR) {
+            const uint8_t* row = sg.W + n * sg.row_bytes;
+            const int64_t nb = sg.row_bytes / 34;
+#pragma unroll
+            for (int b = 0; b < 8; ++b)
+                o.q[t][b] = *(const v2i*)(row + 2 * nb + (int64_t)(8 * sb + b) * 32 + 8 * kq);
+            o.d[t] = *(const v4i*)(row + (int64_t)16 * sb);
+        } else {
+            const uint8_t* row = sg.W + n * sg.row_bytes;
+            const int64_t nb = sg.row_bytes / 18;
+#pragma unroll
+            for (int b = 0; b < 8; ++b)
+                o.q[t][b] = *(const uint32_t*)(row + 2 * nb + (int64_t)(8 * sb + b) * 16 + 4 * kq);
+            o.d[t] = *(const v4i*)(row + (int64_t)16 * sb);
+        }
+    }
+}
+
+// fp16 of the d (or dmin: hi = true) word of a Q4_K header, of block b of 8 planar scales
+__device__ __forceinline__ float hdr_half(const v4i& h, bool hi) {
+    return h2f((uint16_t)(hi ? ((uint32_t)h.x >> 16) : ((uint32_t)h.x & 0xFFFF)));
+}
+__device__ __forceinline__ float scale8(const v4i& d, int b) {
+    const uint32_t w = (uint32_t)d[b >> 1];
+    return h2f((uint16_t)((b & 1) ? (w >> 16) : (w & 0xFFFF)));
+}
+
+// Q4_0's nibbles are interleaved (element j = nibble j & 1 of byte j / 2,
+// include/ft/quant.h:45-60): its B slots are [even elements, odd elements]
+// of each octet, so its activation stage stores octets in that order
+template <int DT>
+__device__ __forceinline__ v8h mm_stage_order(v8h v) {
+    if constexpr (DT == FTX_Q4_0_PLANAR)
+        return v8h{v[0], v[2], v[4], v[6], v[1], v[3], v[5], v[7]};
+    return v;
+}
+
+// grid = (ceil(units / 4), Mp / 64, splits); block = 256.  Every wave takes
+// part in the activation staging and its barriers; a wave past the last
+// unit computes nothing.
+template <int DT>
+__global__ void __launch_bounds__(64 * MM_WAVES) __attribute__((amdgpu_waves_per_eu(1, 1)))
+k_mm(MmArgs a) {
+    __shared__ _Float16 st[2][2][MM_TOK][MM_PITCH];  // [buf][hi / lo][token][k]
+    const int tid = threadIdx.x, lane = tid & 63;
+    const int w = __builtin_amdgcn_readfirstlane(tid >> 6);
+    const int col = lane & 15, kq = lane >> 4;
+    const int64_t u = (int64_t)blockIdx.x * MM_WAVES + w;
+    const bool live = u < a.units;  // wave-uniform
+    const int si = mm_seg_of(a, live ? u : a.units - 1);
+    const MmSegDev& sg = a.seg[si];
+    const int64_t rbase = ((live ? u : a.units - 1) - sg.unit0) * MM_WROWS;
+    const int64_t m0 = (int64_t)blockIdx.y * MM_TOK;
+    const int ks = blockIdx.z;
+    const int sb0 = ks * a.sb_per_split;
+    const int sb1 = min(sb0 + a.sb_per_split, a.nsb);
+    const int64_t K = a.K;
+
+    // activation staging: thread t copies token row m0 + t / 4, elements
+    // 16 (t % 4) .. + 15 of the stage, hi and lo
+    const int sm = tid >> 2, sp = tid & 3;
+    const _Float16* gh = a.xh + (m0 + sm) * K + 16 * sp;
+    const _Float16* gl = a.xl + (m0 + sm) * K + 16 * sp;
+    v8h rg[4];
+    auto stage_load = [&](int64_t k0) {
+        rg[0] = ld8h(gh + k0);
+        rg[1] = ld8h(gh + k0 + 8);
+        rg[2] = ld8h(gl + k0);
+        rg[3] = ld8h(gl + k0 + 8);
+    };
+    auto stage_store = [&](int buf) {
+        *(v8h*)&st[buf][0][sm][16 * sp] = mm_stage_order<DT>(rg[0]);
+        *(v8h*)&st[buf][0][sm][16 * sp + 8] = mm_stage_order<DT>(rg[1]);
+        *(v8h*)&st[buf][1][sm][16 * sp] = mm_stage_order<DT>(rg[2]);
+        *(v8h*)&st[buf][1][sm][16 * sp + 8] = mm_stage_order<DT>(rg[3]);
+    };
+
+    v4f acc[MM_NT][MM_MS];
+#pragma unroll
+    for (int t = 0; t < MM_NT; ++t)
+#pragma unroll
+        for (int ms = 0; ms < MM_MS; ++ms) acc[t][ms] = v4f{0.f, 0.f, 0.f, 0.f};
+    const v4f zero4 = {0.f, 0.f, 0.f, 0.f};
+
+    MmW<DT> wc, wn;
+    if (sb0 < sb1) {
+        mm_load_w<DT>(wc, sg, rbase, sb0, a.nsb, col, kq);
+        stage_load((int64_t)sb0 * 256);
+        stage_store(0);
+    }
+    __syncthreads();
+    int buf = 0;
+    for (int sb = sb0; sb < sb1; ++sb) {
+        // the next step's weights are in flight during this step's MFMAs
+        mm_load_w<DT>(wn, sg, rbase, sb + 1 < sb1 ? sb + 1 : sb, a.nsb, col, kq);
+        v4f tmp[MM_NT][MM_MS];
+        // Q4_K: the scales / mins of the lane's rows in this super-block
+        uint32_t scw[MM_NT][2], mnw[MM_NT][2];
+        if constexpr (DT == FTX_Q4_K) {
+#pragma unroll
+            for (int t = 0; t < MM_NT; ++t) {
+                const uint32_t S0 = wc.hdr[t].y, S1 = wc.hdr[t].z, S2 = wc.hdr[t].w;
+                scw[t][0] = S0 & 0x3F3F3F3Fu;
+                mnw[t][0] = S1 & 0x3F3F3F3Fu;
+                scw[t][1] = (S2 & 0x0F0F0F0Fu) | ((S0 >> 2) & 0x30303030u);
+                mnw[t][1] = ((S2 >> 4) & 0x0F0F0F0Fu) | ((S1 >> 2) & 0x30303030u);
+            }
+        }
+#pragma unroll
+        for (int c = 0; c < 4; ++c) {
+            // the next stage's activations in flight during this stage
+            const bool more = c < 3 || sb + 1 < sb1;
+            if (more) stage_load((int64_t)sb * 256 + (c + 1) * MM_KC);
+#pragma unroll
+            for (int s = 0; s < 2; ++s) {
+                const int j = 2 * c + s;  // 32-element K-step (sub-block / block) of the super-block
+                v8h bw[MM_NT];
+                float bs[MM_NT];
+#pragma unroll
+                for (int t = 0; t < MM_NT; ++t) {
+                    if constexpr (DT == FTX_Q4_K) {
+                        const int scv = (int)((scw[t][j >> 2] >> (8 * (j & 3))) & 0xFF);
+                        const _Float16 sch = (_Float16)(float)scv;
+                        bw[t] = nib8_bytes(wc.qs[t][c], s != 0) * v8h{sch, sch, sch, sch, sch, sch, sch, sch};
+                        bs[t] = 0.f;
+                    } else if constexpr (DT == FTX_Q8_0_PLANAR) {
+                        bw[t] = i8x8(wc.q[t][j]);
+                        bs[t] = scale8(wc.d[t], j);
+                    } else {
+                        bw[t] = nib8(wc.q[t][j], 8.f);
+                        bs[t] = scale8(wc.d[t], j);
+                    }
+                }
+#pragma unroll
+                for (int ms = 0; ms < MM_MS; ++ms) {
+                    const v8h ah = ld8h(&st[buf][0][16 * ms + col][32 * s + 8 * kq]);
+                    const v8h al = ld8h(&st[buf][1][16 * ms + col][32 * s + 8 * kq]);
+#pragma unroll
+                    for (int t = 0; t < MM_NT; ++t) {
+                        if (!live) continue;
+                        if constexpr (DT == FTX_Q4_K) {
+                            const v4f c0 = j == 0 ? zero4 : tmp[t][ms];
+                            tmp[t][ms] = __builtin_amdgcn_mfma_f32_16x16x32_f16(ah, bw[t], c0, 0, 0, 0);
+                            tmp[t][ms] = __builtin_amdgcn_mfma_f32_16x16x32_f16(al, bw[t], tmp[t][ms], 0, 0, 0);
+                        } else {
+                            v4f p = __builtin_amdgcn_mfma_f32_16x16x32_f16(ah, bw[t], zero4, 0, 0, 0);
+                            p = __builtin_amdgcn_mfma_f32_16x16x32_f16(al, bw[t], p, 0, 0, 0);
+#pragma unroll
+                            for (int r = 0; r < 4; ++r) acc[t][ms][r] += bs[t] * p[r];
+                        }
+                    }
+                }
+            }
+            if (more) stage_store(buf ^ 1);
+            __syncthreads();
+            buf ^= 1;
+        }
+        if constexpr (DT == FTX_Q4_K) {
+            // acc += d * tmp - dmin * sum_j m_j X_j; the min term's A operand is
+            // the sub-block sums (K slots 4 kq .. 4 kq + 3 = sub-blocks of this
+            // super-block for kq < 2, zero above), its B operand the mins
+#pragma unroll
+            for (int ms = 0; ms < MM_MS; ++ms) {
+                v4h xh4 = {}, xl4 = {};
+                if (kq < 2) {
+                    const int64_t o = (m0 + 16 * ms + col) * (K / 32) + (int64_t)sb * 8 + 4 * kq;
+                    xh4 = *(const v4h*)(a.sh + o);
+                    xl4 = *(const v4h*)(a.sl + o);
+                }
+#pragma unroll
+                for (int t = 0; t < MM_NT; ++t) {
+                    if (!live) continue;
+                    v4h bm = {};
+                    if (kq < 2) {
+                        const uint32_t mw = mnw[t][kq];
+                        bm = v4h{(_Float16)(float)(mw & 0xFF), (_Float16)(float)((mw >> 8) & 0xFF),
+                                 (_Float16)(float)((mw >> 16) & 0xFF), (_Float16)(float)(mw >> 24)};
+                    }
+                    v4f mt = __builtin_amdgcn_mfma_f32_16x16x16f16(xh4, bm, zero4, 0, 0, 0);
+                    mt = __builtin_amdgcn_mfma_f32_16x16x16f16(xl4, bm, mt, 0, 0, 0);
+                    const float d = hdr_half(wc.hdr[t], false), dmin = hdr_half(wc.hdr[t], true);
+#pragma unroll
+                    for (int r = 0; r < 4; ++r)
+                        acc[t][ms][r] += d * tmp[t][ms][r] - dmin * mt[r];
+                }
+            }
+        }
+        wc = wn;
+    }
+    if (!live) return;
+    // lane (col, kq) holds C[4 kq + r][col] of each tile: token m0 + 16 ms +
+    // 4 kq + r, output column col0 + rbase + 16 t + col
+    const MmOutDev& o = a.out;
+#pragma unroll
+    for (int ms = 0; ms < MM_MS; ++ms)
+#pragma unroll
+        for (int r = 0; r < 4; ++r) {
+            const int64_t m = m0 + 16 * ms + 4 * kq + r;
+            if (m >= a.M) continue;
+            int s = 0;
+            while (s + 1 < o.nseq && m >= o.row0[s + 1]) ++s;
+            float* yrow = o.base[s] + (m - o.row0[s]) * o.ld + (int64_t)ks * o.split_stride;
+#pragma unroll
+            for (int t = 0; t < MM_NT; ++t) {
+                const int64_t n = rbase + 16 * t + col;
+                if (n >= sg.N) continue;
+                float* yp = yrow + sg.col0 + n;
+                *yp = o.accum ? *yp + acc[t][ms][r] : acc[t][ms][r];
+            }
+        }
+}
+
+// ---------------------------------------------------------------- ffn_down
+
+struct MmDownArgs {
+    const uint8_t* qs;   // QS plane of the re-tiled copy
+    const uint8_t* hdr;  // headers [N / 256][n_in] x 16 B
+    const float* h;      // [M][ldh]
+    int64_t ldh;
+    int M;
+    int64_t n_in, N;
+    int slices_per_split;
+    MmOutDev out;
+};
+
+// grid = (N / 256, Mp / 64, splits); block = 256: wave w owns columns
+// 256 bx + 64 w .. + 63 (four 16-column tiles ct); per 32-row slice the
+// workgroup stages, for its 64 tokens, A_d = h d 2^10 and A_m = h dmin 2^10
+// (hi / lo) and the fp16 tables sc[s][i], mn[s][i] of the block's 8
+// sub-blocks; y = (sum_i A_d sc q - sum_i A_m mn) / 2^10 with the min term
+// (one 16-column MFMA tile whose columns are the sub-blocks) done by wave w
+// for tokens 16 w .. 16 w + 15 and handed to the other waves through LDS.
+constexpr int MMD_PITCH = 32 + 8;
+__global__ void __launch_bounds__(64 * MM_WAVES) __attribute__((amdgpu_waves_per_eu(1, 1)))
+k_mm_down(MmDownArgs a) {
+    __shared__ _Float16 ad[2][2][MM_TOK][MMD_PITCH];  // [buf][hi / lo][token][row i]
+    __shared__ _Float16 am[2][2][MM_TOK][MMD_PITCH];
+    __shared__ _Float16 tsc[2][8][MMD_PITCH];          // [buf][sub-block][row i]
+    __shared__ _Float16 tmn[2][8][MMD_PITCH];
+    __shared__ float mins[MM_TOK][9];                  // [token][sub-block]
+    const int tid = threadIdx.x, lane = tid & 63;
+    const int w = __builtin_amdgcn_readfirstlane(tid >> 6);
+    const int col = lane & 15, kq = lane >> 4;
+    const int64_t jb = blockIdx.x;
+    const int64_t m0 = (int64_t)blockIdx.y * MM_TOK;
+    const int ks = blockIdx.z;
+    const int64_t nsl = a.n_in / 32, nc64 = a.N / 64;
+    const int64_t I0 = (int64_t)ks * a.slices_per_split;
+    const int64_t I1 = min(I0 + (int64_t)a.slices_per_split, nsl);
+    const int64_t C = jb * 4 + w;
+
+    // staging: thread t takes token sm = t / 4 and rows 8 sp .. 8 sp + 7 of
+    // the slice (h of tokens past M is zero)
+    const int sm = tid >> 2, sp = tid & 3;
+    const bool tok_ok = m0 + sm < a.M;
+    const float* hrow = a.h + (tok_ok ? m0 + sm : 0) * a.ldh;
+    float hv[8];
+    uint32_t dw[8];      // d | dmin << 16 of rows 8 sp + e
+    v4i hq;              // threads t < 32: the header of row t (scales / mins)
+    auto stage_load = [&](int64_t I) {
+        const int64_t i0 = I * 32 + 8 * sp;
+        const float4 h0 = *(const float4*)(hrow + i0), h1 = *(const float4*)(hrow + i0 + 4);
+        hv[0] = h0.x; hv[1] = h0.y; hv[2] = h0.z; hv[3] = h0.w;
+        hv[4] = h1.x; hv[5] = h1.y; hv[6] = h1.z; hv[7] = h1.w;
+#pragma unroll
+        for (int e = 0; e < 8; ++e) dw[e] = *(const uint32_t*)(a.hdr + (jb * a.n_in + i0 + e) * 16);
+        hq = *(const v4i*)(a.hdr + (jb * a.n_in + I * 32 + (tid & 31)) * 16);
+    };
+    auto stage_store = [&](int buf) {
+#pragma clang fp contract(off)
+        v8h dh, dl, mh, ml;
+#pragma unroll
+        for (int e = 0; e < 8; ++e) {
+            const float hvv = tok_ok ? hv[e] : 0.f;
+            const float pd = hvv * h2f((uint16_t)(dw[e] & 0xFFFF)) * MMD_ASCALE;
+            const float pm = hvv * h2f((uint16_t)(dw[e] >> 16)) * MMD_ASCALE;
+            _Float16 x0, x1;
+            split_hl(pd, x0, x1);
+            dh[e] = x0;
+            dl[e] = x1;
+            split_hl(pm, x0, x1);
+            mh[e] = x0;
+            ml[e] = x1;
+        }
+        *(v8h*)&ad[buf][0][sm][8 * sp] = dh;
+        *(v8h*)&ad[buf][1][sm][8 * sp] = dl;
+        *(v8h*)&am[buf][0][sm][8 * sp] = mh;
+        *(v8h*)&am[buf][1][sm][8 * sp] = ml;
+        if (tid < 32) {
+            const uint32_t S0 = hq.y, S1 = hq.z, S2 = hq.w;
+            const uint32_t sc_lo = S0 & 0x3F3F3F3Fu, mn_lo = S1 & 0x3F3F3F3Fu;
+            const uint32_t sc_hi = (S2 & 0x0F0F0F0Fu) | ((S0 >> 2) & 0x30303030u);
+            const uint32_t mn_hi = ((S2 >> 4) & 0x0F0F0F0Fu) | ((S1 >> 2) & 0x30303030u);
+#pragma unroll
+            for (int s = 0; s < 8; ++s) {
+                const uint32_t scv = ((s < 4 ? sc_lo : sc_hi) >> (8 * (s & 3))) & 0xFF;
+                const uint32_t mnv = ((s < 4 ? mn_lo : mn_hi) >> (8 * (s & 3))) & 0xFF;
+                tsc[buf][s][tid] = (_Float16)(float)scv;
+                tmn[buf][s][tid] = (_Float16)(float)mnv;
+            }
+        }
+    };
+    auto load_w = [&](int64_t I) -> v4i {
+        const int64_t blk = (I * nc64 + C) * 4 + kq;
+        return *(const v4i*)(a.qs + (blk * 16 + col) * 16);
+    };
+
+    v4f acc[4][MM_MS];
+#pragma unroll
+    for (int ct = 0; ct < 4; ++ct)
+#pragma unroll
+        for (int ms = 0; ms < MM_MS; ++ms) acc[ct][ms] = v4f{0.f, 0.f, 0.f, 0.f};
+    v4f accm = {0.f, 0.f, 0.f, 0.f};
+
+    v4i wq = {}, wqn = {};
+    if (I0 < I1) {
+        wq = load_w(I0);
+        stage_load(I0);
+        stage_store(0);
+    }
+    __syncthreads();
+    int buf = 0;
+    for (int64_t I = I0; I < I1; ++I) {
+        const bool more = I + 1 < I1;
+        if (more) {
+            wqn = load_w(I + 1);
+            stage_load(I + 1);
+        }
+        const uint32_t* qw = (const uint32_t*)&wq;
+#pragma unroll
+        for (int ct = 0; ct < 4; ++ct) {
+            const int s = 2 * w + (ct >> 1);  // sub-block of the block holding these columns
+            const v8h q = nib8(qw[ct], 0.f);
+            const v8h scv = ld8h(&tsc[buf][s][8 * kq]);
+            const v8h b = q * scv;
+#pragma unroll
+            for (int ms = 0; ms < MM_MS; ++ms) {
+                const v8h ah = ld8h(&ad[buf][0][16 * ms + col][8 * kq]);
+                const v8h al = ld8h(&ad[buf][1][16 * ms + col][8 * kq]);
+                acc[ct][ms] = __builtin_amdgcn_mfma_f32_16x16x32_f16(ah, b, acc[ct][ms], 0, 0, 0);
+                acc[ct][ms] = __builtin_amdgcn_mfma_f32_16x16x32_f16(al, b, acc[ct][ms], 0, 0, 0);
+            }
+        }
+        {
+            // min term of tokens 16 w .. + 15: B columns = the 8 sub-blocks
+            const v8h bm = col < 8 ? ld8h(&tmn[buf][col & 7][8 * kq]) : v8h{};
+            const v8h mh = ld8h(&am[buf][0][16 * w + col][8 * kq]);
+            const v8h ml = ld8h(&am[buf][1][16 * w + col][8 * kq]);
+            accm = __builtin_amdgcn_mfma_f32_16x16x32_f16(mh, bm, accm, 0, 0, 0);
+            accm = __builtin_amdgcn_mfma_f32_16x16x32_f16(ml, bm, accm, 0, 0, 0);
+        }
+        if (more) stage_store(buf ^ 1);
+        __syncthreads();
+        buf ^= 1;
+        wq = wqn;
+    }
+    // the min terms of every token and sub-block, through LDS
+    if (col < 8) {
+#pragma unroll
+        for (int r = 0; r < 4; ++r) mins[16 * w + 4 * kq + r][col] = accm[r];
+    }
+    __syncthreads();
+    const MmOutDev& o = a.out;
+#pragma unroll
+    for (int ms = 0; ms < MM_MS; ++ms)
+#pragma unroll
+        for (int r = 0; r < 4; ++r) {
+            const int tk = 16 * ms + 4 * kq + r;
+            const int64_t m = m0 + tk;
+            if (m >= a.M) continue;
+            int sq = 0;
+            while (sq + 1 < o.nseq && m >= o.row0[sq + 1]) ++sq;
+            float* yrow = o.base[sq] + (m - o.row0[sq]) * o.ld + (int64_t)ks * o.split_stride;
+#pragma unroll
+            for (int ct = 0; ct < 4; ++ct) {
+                const int s = 2 * w + (ct >> 1);
+                const float v = (acc[ct][ms][r] - mins[tk][s]) * (1.f / MMD_ASCALE);
+                float* yp = yrow + jb * 256 + 64 * w + 16 * ct + col;
+                *yp = o.accum ? *yp + v : v;
+            }
+        }
+}
+
+// ---------------------------------------------------------------- reduce
+// out[m][n] (= or +=) sum_ks part[ks][m][n] in split order; SwiGLU:
+// out[m][n] = silu(g) * u with g, u the sums of columns n and n + N
+// (src/engine.cpp:271-273).  grid = (ceil(N / 256), M).
+struct MmReduceArgs {
+    const float* part;
+    int64_t split_stride, ldp;
+    int S;
+    int64_t N;
+    int swiglu;
+    MmOutDev out;
+};
+
+__global__ void __launch_bounds__(256) k_mm_reduce(MmReduceArgs a) {
+    const int64_t n = (int64_t)blockIdx.x * 256 + threadIdx.x;
+    const int64_t m = blockIdx.y;
+    if (n >= a.N) return;
+    const float* p = a.part + m * a.ldp + n;
+    float g = 0.f, u = 0.f;
+    for (int s = 0; s < a.S; ++s) g += p[(int64_t)s * a.split_stride];
+    if (a.swiglu)
+        for (int s = 0; s < a.S; ++s) u += p[(int64_t)s * a.split_stride + a.N];
+    const MmOutDev& o = a.out;
+    int sq = 0;
+    while (sq + 1 < o.nseq && m >= o.row0[sq + 1]) ++sq;
+    float* yp = o.base[sq] + (m - o.row0[sq]) * o.ld + n;
+    const float v = a.swiglu ? g / (1.f + expf(-g)) * u : g;
+    *yp = o.accum ? *yp + v : v;
+}
+
+}  // namespace
+
+// ---------------------------------------------------------------- host
+
+int64_t mm_pad_tokens(int64_t M) { return (M + MM_TOK - 1) / MM_TOK * MM_TOK; }
+
+size_t mm_act_halves(int64_t Mp, int64_t K) { return (size_t)(Mp * K * 2 + Mp * (K / 32) * 2); }
+
+MmAct mm_act(void* buf, int64_t Mp, int64_t K) {
+    MmAct a;
+    a.xh = (_Float16*)buf;
+    a.xl = a.xh + Mp * K;
+    a.sh = a.xl + Mp * K;
+    a.sl = a.sh + Mp * (K / 32);
+    a.Mp = Mp;
+    a.K = K;
+    return a;
+}
+
+hipError_t launch_mm_prep(hipStream_t st, const float* x, int64_t ldx, const float* normw,
+                          float eps, int64_t M, const MmAct& act) {
+    if (act.K % 256 || M < 1 || M > act.Mp || ldx % 4 || ((uintptr_t)x & 15))
+        return hipErrorInvalidValue;
+    hipLaunchKernelGGL(k_mm_prep, dim3((unsigned)act.Mp), dim3(256), 0, st, x, ldx, normw, eps,
+                       act.K, (int)M, act.xh, act.xl, act.sh, act.sl);
+    return hipGetLastError();
+}
+
+bool mm_supported(int dt, int64_t K) {
+    return (dt == FTX_Q4_K || dt == FTX_Q8_0_PLANAR || dt == FTX_Q4_0_PLANAR) && K % 256 == 0 &&
+           K >= 256;
+}
+
+bool mm_down_supported(int dt, int64_t n_in, int64_t N) {
+    return dt == FTX_Q4_K && n_in % 32 == 0 && N % 256 == 0;
+}
+
+static MmOutDev out_dev(const MmOut& o) {
+    MmOutDev d{};
+    d.nseq = o.nseq;
+    for (int s = 0; s < o.nseq; ++s) {
+        d.base[s] = o.base[s];
+        d.row0[s] = o.row0[s];
+    }
+    d.row0[o.nseq] = o.row0[o.nseq];
+    d.ld = o.ld;
+    d.split_stride = 0;
+    d.accum = o.accum;
+    return d;
+}
+
+// split count for `tiles` workgroups over `steps` contraction steps: none
+// when the tiles fill the device, else about two workgroups per CU, at least
+// two steps per split
+static int mm_splits(int64_t tiles, int64_t steps, int cu_count) {
+    const int64_t cus = cu_count > 0 ? cu_count : 256;
+    if (tiles < 1 || tiles >= cus) return 1;
+    int64_t S = (2 * cus + tiles - 1) / tiles;
+    if (S > steps / 2) S = steps / 2;
+    if (S > 32) S = 32;
+    return S < 1 ? 1 : (int)S;
+}
+
+size_t mm_part_floats(int64_t Mp, int64_t N, int64_t steps, int64_t ntiles, int cu_count) {
+    const int S = mm_splits(ntiles * (Mp / MM_TOK), steps, cu_count);
+    return S > 1 ? (size_t)S * (size_t)Mp * (size_t)N : 0;
+}
+
+hipError_t launch_mm(hipStream_t st, const MmSeg* segs, int nseg, const MmAct& act, int64_t M,
+                     int epi, const MmOut& out, float* part, size_t part_floats, int cu_count) {
+    if (nseg < 1 || nseg > 3 || M < 1 || M > act.Mp || out.nseq < 1 || out.nseq > FTX_MAX_SEQ)
+        return hipErrorInvalidValue;
+    const int dt = segs[0].dt;
+    MmArgs a{};
+    a.nseg = nseg;
+    int64_t units = 0, cols = 0;
+    for (int i = 0; i < nseg; ++i) {
+        if (segs[i].dt != dt || !mm_supported(dt, act.K)) return hipErrorInvalidValue;
+        if (dt == FTX_Q4_K && segs[i].rpt != 16 && segs[i].rpt != 32) return hipErrorInvalidValue;
+        MmSegDev& d = a.seg[i];
+        d.W = segs[i].W;
+        d.N = segs[i].N;
+        d.unit0 = units;
+        d.col0 = cols;
+        d.row_bytes = segs[i].row_bytes;
+        d.rpt = segs[i].rpt;
+        units += (segs[i].N + MM_WROWS - 1) / MM_WROWS;
+        cols += segs[i].N;
+    }
+    a.units = units;
+    a.K = act.K;
+    a.nsb = (int)(act.K / 256);
+    a.xh = act.xh;
+    a.xl = act.xl;
+    a.sh = act.sh;
+    a.sl = act.sl;
+    a.M = (int)M;
+    const int64_t wg = (units + MM_WAVES - 1) / MM_WAVES, mt = act.Mp / MM_TOK;
+    int S = mm_splits(wg * mt, a.nsb, cu_count);
+    // SwiGLU needs the gate and up sums together: always through the reduce
+    const bool via_part = S > 1 || epi == EPI_SWIGLU;
+    if (via_part) {
+        if (!part || (size_t)S * (size_t)act.Mp * (size_t)cols > part_floats) {
+            S = 1;
+            if (!part || (size_t)act.Mp * (size_t)cols > part_floats) return hipErrorInvalidValue;
+        }
+        MmOutDev& o = a.out;
+        o.nseq = 1;
+        o.base[0] = part;
+        o.row0[0] = 0;
+        o.row0[1] = act.Mp;
+        o.ld = cols;
+        o.split_stride = act.Mp * cols;
+        o.accum = 0;
+    } else {
+        a.out = out_dev(out);
+    }
+    a.sb_per_split = (a.nsb + S - 1) / S;
+    S = (a.nsb + a.sb_per_split - 1) / a.sb_per_split;
+    const dim3 grid((unsigned)wg, (unsigned)mt, (unsigned)S);
+    if (dt == FTX_Q4_K)
+        hipLaunchKernelGGL(k_mm<FTX_Q4_K>, grid, dim3(64 * MM_WAVES), 0, st, a);
+    else if (dt == FTX_Q8_0_PLANAR)
+        hipLaunchKernelGGL(k_mm<FTX_Q8_0_PLANAR>, grid, dim3(64 * MM_WAVES), 0, st, a);
+    else
+        hipLaunchKernelGGL(k_mm<FTX_Q4_0_PLANAR>, grid, dim3(64 * MM_WAVES), 0, st, a);
+    hipError_t e = hipGetLastError();
+    if (e != hipSuccess || !via_part) return e;
+    MmReduceArgs r{};
+    r.part = part;
+    r.split_stride = act.Mp * cols;
+    r.ldp = cols;
+    r.S = S;
+    r.swiglu = epi == EPI_SWIGLU;
+    r.N = r.swiglu ? cols / 2 : cols;
+    r.out = out_dev(out);
+    hipLaunchKernelGGL(k_mm_reduce, dim3((unsigned)((r.N + 255) / 256), (unsigned)M), dim3(256), 0,
+                       st, r);
+    return hipGetLastError();
+}
+
+hipError_t launch_mm_down(hipStream_t st, const uint8_t* tiled, int64_t n_in, int64_t N,
+                          const float* h, int64_t ldh, int64_t M, const MmOut& out, float* part,
+                          size_t part_floats, int cu_count) {
+    const int64_t Mp = mm_pad_tokens(M);
+    if (!mm_down_supported(FTX_Q4_K, n_in, N) || M < 1 || out.nseq < 1 || out.nseq > FTX_MAX_SEQ ||
+        ldh % 4 || ((uintptr_t)h & 15))
+        return hipErrorInvalidValue;
+    MmDownArgs a{};
+    a.qs = tiled;
+    a.hdr = tiled + n_in * N / 2;
+    a.h = h;
+    a.ldh = ldh;
+    a.M = (int)M;
+    a.n_in = n_in;
+    a.N = N;
+    const int64_t nsl = n_in / 32, nb = N / 256, mt = Mp / MM_TOK;
+    int S = mm_splits(nb * mt, nsl, cu_count);
+    if (S > 1 && (!part || (size_t)S * (size_t)Mp * (size_t)N > part_floats)) S = 1;
+    a.slices_per_split = (int)((nsl + S - 1) / S);
+    S = (int)((nsl + a.slices_per_split - 1) / a.slices_per_split);
+    if (S > 1) {
+        MmOutDev& o = a.out;
+        o.nseq = 1;
+        o.base[0] = part;
+        o.row0[0] = 0;
+        o.row0[1] = Mp;
+        o.ld = N;
+        o.split_stride = Mp * N;
+        o.accum = 0;
+    } else {
+        a.out = out_dev(out);
+    }
+    hipLaunchKernelGGL(k_mm_down, dim3((unsigned)nb, (unsigned)mt, (unsigned)S), dim3(64 * MM_WAVES),
+                       0, st, a);
+    hipError_t e = hipGetLastError();
+    if (e != hipSuccess || S == 1) return e;
+    MmReduceArgs r{};
+    r.part = part;
+    r.split_stride = Mp * N;
+    r.ldp = N;
+    r.S = S;
+    r.swiglu = 0;
+    r.N = N;
+    r.out = out_dev(out);
+    hipLaunchKernelGGL(k_mm_reduce, dim3((unsigned)((N + 255) / 256), (unsigned)M), dim3(256), 0,
+                       st, r);
+    return hipGetLastError();
+}
+
+size_t mm_down_part_floats(int64_t Mp, int64_t n_in, int64_t N, int cu_count) {
+    const int S = mm_splits((N / 256) * (Mp / MM_TOK), n_in / 32, cu_count);
+    return S > 1 ? (size_t)S * (size_t)Mp * (size_t)N : 0;
+}

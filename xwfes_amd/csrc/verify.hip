@@ -45,6 +45,11 @@ struct ftx_model {
     std::vector<uint8_t*> pln;
     std::vector<int> pln_dt;
     float* downpart = nullptr;
+    // large-M path (more than 8 tokens, or several sequences): activation
+    // operands and split-sum partials of the k_gemm.hip launches
+    _Float16* mm_act = nullptr;
+    float* mm_part = nullptr;
+    size_t mm_part_n = 0;
     // pinned host argument blocks, used in turn; an event recorded after a
     // block's copy to the device guards its reuse, so the host prepares the
     // next step while earlier steps still run
@@ -55,22 +60,24 @@ struct ftx_model {
 };
 
 // Per-step argument block (pinned host copy and device copy share the
-// layout): tokens [M] | depth [M] | ancestor masks [M][aw] | npast (8-byte
-// aligned) | RoPE cos / sin [M][hd / 2][2]
+// layout): tokens [M] | depth [M] | ancestor masks [M][aw] | npast [nseq]
+// (8-byte aligned) | RoPE cos / sin [M][hd / 2][2].  M counts the tokens of
+// every sequence; a mask row holds bits of its own sequence's nodes.
 struct StepArgsLayout {
     size_t depth, anc, np, cs, bytes;
 };
-static StepArgsLayout step_args_layout(int64_t M, int64_t hd) {
-    const int64_t aw = (M + 31) / 32;
+static StepArgsLayout step_args_layout(int64_t M, int64_t hd, int64_t aw, int64_t nseq = 1) {
     StepArgsLayout L;
     L.depth = (size_t)M * 4;
     L.anc = L.depth + (size_t)M * 4;
     L.np = (L.anc + (size_t)(M * aw) * 4 + 7) & ~(size_t)7;
-    L.cs = L.np + 8;
+    L.cs = L.np + 8 * (size_t)nseq;
     L.bytes = L.cs + (size_t)(M * (hd / 2) * 2) * 4;
     return L;
 }
-static size_t step_args_bytes(int64_t Mmax, int64_t hd) { return step_args_layout(Mmax, hd).bytes; }
+static size_t step_args_bytes(int64_t Mmax, int64_t hd) {
+    return step_args_layout(Mmax, hd, (Mmax + 31) / 32, FTX_MAX_SEQ).bytes;
+}
 
 // the MFMA row-dot path applies to every segment of a projection, or none
 static bool mv_all(const ftx_tensor* const* ts, int n, int64_t K, int64_t M) {
@@ -105,6 +112,8 @@ static void model_release(ftx_model* m) {
     for (uint8_t* b : m->pln)
         if (b) (void)hipFree(b);
     if (m->downpart) (void)hipFree(m->downpart);
+    if (m->mm_act) (void)hipFree(m->mm_act);
+    if (m->mm_part) (void)hipFree(m->mm_part);
     for (int i = 0; i < ftx_model::PIN_RING; ++i) {
         if (m->pin[i]) (void)hipHostFree(m->pin[i]);
         if (m->pin_ev[i]) (void)hipEventDestroy(m->pin_ev[i]);
@@ -120,6 +129,309 @@ static bool dalloc(T** p, size_t n) {
         return false;
     }
     return true;
+}
+
+// The verify step for more than 8 tokens or for several sequences: every
+// projection over the tokens of all sequences at once, through the one-pass
+// GEMMs of k_gemm.hip where the weights allow (tiled Q4_K, planar Q8_0 /
+// Q4_0 copies) and the generic kernels otherwise; RoPE, the KV write and
+// attention per sequence against its own cache (Engine::forward,
+// src/engine.cpp:461-596, per sequence).  The caller has checked the
+// arguments.
+static int verify_large(ftx_ctx* ctx, ftx_model* m, const ftx_seq_args* sq, int64_t nseq) {
+    const ftx_model_desc& d = m->d;
+    const int64_t D = d.n_embd, F = d.n_ff, V = d.vocab, hd = d.head_dim;
+    int64_t row0[FTX_MAX_SEQ + 1];
+    int64_t Mt = 0, Mmx = 0;
+    for (int64_t s = 0; s < nseq; ++s) {
+        row0[s] = Mt;
+        Mt += sq[s].M;
+        Mmx = std::max(Mmx, sq[s].M);
+    }
+    row0[nseq] = Mt;
+    const int aw = (int)((Mmx + 31) / 32);
+    const int64_t hd2 = hd / 2;
+    const StepArgsLayout AL = step_args_layout(Mt, hd, aw, nseq);
+    const int slot = m->pin_next;
+    uint8_t* pin = m->pin[slot];
+    FTX_HIP(ctx, hipEventSynchronize(m->pin_ev[slot]));
+    int32_t* toks = (int32_t*)pin;
+    int32_t* depth = (int32_t*)(pin + AL.depth);
+    uint32_t* anc = (uint32_t*)(pin + AL.anc);
+    int64_t* np = (int64_t*)(pin + AL.np);
+    float* cs = (float*)(pin + AL.cs);
+    for (int64_t s = 0; s < nseq; ++s) {
+        const int64_t r0 = row0[s], M = sq[s].M, npast = sq[s].kv->npast;
+        np[s] = npast;
+        for (int64_t i = 0; i < M; ++i) {
+            const int32_t t = sq[s].tokens[i];
+            if (t < 0 || t >= d.vocab) return ftx_fail(ctx, FTX_E_RANGE, "token id out of range");
+            const int32_t p = sq[s].parents ? sq[s].parents[i] : (int32_t)i - 1;
+            if (p < -1 || p >= i) return ftx_fail(ctx, FTX_E_INVALID, "parents[i] must be in [-1, i)");
+            toks[r0 + i] = t;
+            depth[r0 + i] = p < 0 ? 0 : depth[r0 + p] + 1;
+            uint32_t* row = anc + (r0 + i) * aw;
+            for (int w = 0; w < aw; ++w) row[w] = p >= 0 ? anc[(r0 + p) * aw + w] : 0u;
+            row[i / 32] |= 1u << (i % 32);
+            // rope_vec's angles (src/engine.cpp:43-60) at npast + depth
+            for (int64_t q = 0; q < hd2; ++q) {
+                const double f = std::pow(d.rope_theta, -2.0 * (double)q / (double)hd);
+                const double ang = (double)(npast + depth[r0 + i]) * f;
+                cs[((r0 + i) * hd2 + q) * 2] = (float)std::cos(ang);
+                cs[((r0 + i) * hd2 + q) * 2 + 1] = (float)std::sin(ang);
+            }
+        }
+    }
+    hipStream_t st = ctx->stream;
+    int32_t* d_toks = (int32_t*)m->args;
+    int32_t* d_depth = (int32_t*)(m->args + AL.depth);
+    uint32_t* d_anc = (uint32_t*)(m->args + AL.anc);
+    int64_t* d_np = (int64_t*)(m->args + AL.np);
+    float* d_cs = (float*)(m->args + AL.cs);
+    (void)d_cs;
+    FTX_HIP(ctx, hipMemcpyAsync(m->args, pin, AL.bytes, hipMemcpyHostToDevice, st));
+    FTX_HIP(ctx, hipEventRecord(m->pin_ev[slot], st));
+    m->pin_next = (slot + 1) % ftx_model::PIN_RING;
+
+    const float eps = d.rms_eps;
+    const double f4 = 4.0, Md = (double)Mt;
+    auto wbytes = [](const ftx_tensor* t) { return (double)(t->row_bytes * t->nrows); };
+#define TRACED_L(kind, bytes, call)                \
+    do {                                           \
+        const int tk_ = tr_begin(ctx);             \
+        FTX_HIP(ctx, call);                        \
+        tr_end(ctx, tk_, (kind), (double)(bytes)); \
+    } while (0)
+    TRACED_L(TK_EMBED, Md * d.tok_embd->row_bytes + Md * D * f4,
+             launch_embed(st, d.tok_embd->data, d.tok_embd->dtype, d.tok_embd->row_bytes, D,
+                          d_toks, Mt, m->x));
+    // the k_mm operand of tensor index i, if it has one
+    auto mm_seg = [&](size_t i, const ftx_tensor* w, MmSeg& sg) -> bool {
+        if (w->dtype == FTX_Q4_K && m->mvt[i] && mm_supported(FTX_Q4_K, w->ne[0])) {
+            sg = MmSeg{m->mvt[i], FTX_Q4_K, w->nrows, m->mvt_rpt[i], 0};
+            return true;
+        }
+        if (m->pln[i] && mm_supported(m->pln_dt[i], w->ne[0])) {
+            sg = MmSeg{m->pln[i], m->pln_dt[i], w->nrows, 0, w->row_bytes};
+            return true;
+        }
+        return false;
+    };
+    auto out1 = [&](float* y, int64_t ld, int accum) {
+        MmOut o{};
+        o.nseq = 1;
+        o.base[0] = y;
+        o.row0[0] = 0;
+        o.row0[1] = Mt;
+        o.ld = ld;
+        o.accum = accum;
+        return o;
+    };
+    // one projection of rows [r0, r0 + Mr) of xin: [RMSNorm ->] segments ->
+    // out (k_mm) or gs (generic kernels, whose outputs are the segments' y)
+    auto project = [&](int kind, double bytes, const float* xin, int64_t ldx, const float* normw,
+                       const size_t* idx, const ftx_tensor* const* ts, GemvSeg* gs, int nseg,
+                       int64_t K, int epi, const MmOut& out, int64_t Mr) -> int {
+        MmSeg sg[3];
+        bool all = true;
+        for (int i = 0; i < nseg; ++i) all = all && mm_seg(idx[i], ts[i], sg[i]);
+        for (int i = 1; all && i < nseg; ++i) all = sg[i].dt == sg[0].dt;
+        if (all) {
+            const MmAct act = mm_act(m->mm_act, mm_pad_tokens(Mr), K);
+            TRACED_L(TK_XQ_PREP, Mr * K * f4 + 4.0 * mm_pad_tokens(Mr) * K,
+                     launch_mm_prep(st, xin, ldx, normw, eps, Mr, act));
+            TRACED_L(kind, bytes,
+                     launch_mm(st, sg, nseg, act, Mr, epi, out, m->mm_part, m->mm_part_n,
+                               ctx->cu_count));
+            return FTX_OK;
+        }
+        bool pl_all = true;
+        for (int i = 0; i < nseg; ++i) pl_all = pl_all && m->pln[idx[i]] != nullptr;
+        for (int i = 0; pl_all && i < nseg; ++i) {
+            gs[i].W = m->pln[idx[i]];
+            gs[i].dt = m->pln_dt[idx[i]];
+        }
+        const float* src = xin;
+        int64_t lds = ldx;
+        if (normw) {
+            TRACED_L(TK_RMSNORM, 2 * Mr * K * f4, launch_rmsnorm(st, xin, normw, K, Mr, eps, m->xn));
+            src = m->xn;
+            lds = K;
+        }
+        if (epi == EPI_SWIGLU)
+            TRACED_L(kind, bytes,
+                     launch_gemv_swiglu(st, gs[0].W, gs[1].W, gs[0].dt, gs[0].row_bytes, gs[0].N,
+                                        src, lds, K, Mr, gs[0].y, gs[0].ldy, true));
+        else
+            TRACED_L(kind, bytes, launch_gemv(st, gs, nseg, src, lds, K, Mr, epi, true));
+        return FTX_OK;
+    };
+    auto seg = [](const ftx_tensor* t, float* y, int64_t ldy) {
+        return GemvSeg{t->data, t->dtype, t->row_bytes, t->nrows, y, ldy};
+    };
+    _Float16* qh = m->qhl;
+    _Float16* ql = m->qhl + Mt * m->qdim;
+    int rc;
+    for (int64_t l = 0; l < d.n_layer; ++l) {
+        const int64_t lt = l * FTX_LAYER_TENSORS;
+        const ftx_tensor* const* T = m->layers.data() + lt;
+        // q / k / v into qkv [Mt][ldq]
+        {
+            const ftx_tensor* ts[3] = {T[FTX_T_Q], T[FTX_T_K], T[FTX_T_V]};
+            const size_t idx[3] = {(size_t)(lt + FTX_T_Q), (size_t)(lt + FTX_T_K),
+                                   (size_t)(lt + FTX_T_V)};
+            GemvSeg gs[3] = {seg(T[FTX_T_Q], m->qkv, m->ldq),
+                             seg(T[FTX_T_K], m->qkv + m->qdim, m->ldq),
+                             seg(T[FTX_T_V], m->qkv + m->qdim + m->kdim, m->ldq)};
+            rc = project(TK_GEMV_QKV,
+                         wbytes(ts[0]) + wbytes(ts[1]) + wbytes(ts[2]) + Md * D * f4 +
+                             Md * m->ldq * f4,
+                         m->x, D, m->norms + (l * 2) * D, idx, ts, gs, 3, D, EPI_STORE,
+                         out1(m->qkv, m->ldq, 0), Mt);
+            if (rc) return rc;
+        }
+        // RoPE, the KV write and attention, per sequence
+        for (int64_t s = 0; s < nseq; ++s) {
+            ftx_kv* kv = sq[s].kv;
+            const int64_t r0 = row0[s], M = sq[s].M, npast = kv->npast;
+            const size_t kvel = kv->kv_f16 ? 2 : 4;
+            uint8_t* kl = (uint8_t*)kv->k + (size_t)(l * kv->cap_alloc * kv->kdim) * kvel;
+            uint8_t* vl = (uint8_t*)kv->v + (size_t)(l * kv->cap_alloc * kv->kdim) * kvel;
+            const bool mattn = attn_mfma_supported(hd, kv->kv_f16, M, d.n_head, d.n_head_kv);
+            RopeArgs ra{m->qkv + r0 * m->ldq, m->ldq,  d.n_head,   d.n_head_kv, hd,
+                        d_depth + r0,         d_np + s, d.rope_theta, d.rope_neox, kl,
+                        vl,                   kv->kv_f16, kv->cap_alloc};
+            if (mattn) {
+                ra.qh16 = qh + r0 * m->qdim;
+                ra.ql16 = ql + r0 * m->qdim;
+            }
+            TRACED_L(TK_ROPE_KV, 2.0 * M * m->ldq * f4 + 2.0 * M * m->kdim * (double)kvel,
+                     launch_rope_kv(st, ra, M));
+            const double attn_b =
+                2.0 * (double)(npast + M) * m->kdim * (double)kvel + 2.0 * M * m->qdim * f4;
+            if (mattn) {
+                AttnMArgs am{};
+                am.qkv = m->qkv + r0 * m->ldq;
+                am.ldq = m->ldq;
+                am.qh16 = ra.qh16;
+                am.ql16 = ra.ql16;
+                am.kc = (const _Float16*)kl;
+                am.vt = (const _Float16*)vl;
+                am.cap = kv->cap_alloc;
+                am.npast = npast;
+                am.anc = d_anc + r0 * aw;
+                am.anc_words = aw;
+                am.M = (int)M;
+                am.n_head = (int)d.n_head;
+                am.n_kv = (int)d.n_head_kv;
+                am.hd = (int)hd;
+                am.out = m->att + r0 * m->qdim;
+                TRACED_L(TK_ATTENTION, attn_b, launch_attn_mfma(st, am, kv->attn_part, nullptr));
+            } else {
+                AttnArgs aa{m->qkv + r0 * m->ldq, m->ldq, kl, vl, kv->kv_f16, d_np + s,
+                            d_anc + r0 * aw, aw, d.n_head, d.n_head_kv, hd, npast + M,
+                            m->att + r0 * m->qdim, kv->cap_alloc};
+                TRACED_L(TK_ATTENTION, attn_b, launch_attention(st, aa, M));
+            }
+        }
+        // o, added into x
+        {
+            const size_t idx[1] = {(size_t)(lt + FTX_T_O)};
+            GemvSeg gs[1] = {seg(T[FTX_T_O], m->x, D)};
+            rc = project(TK_GEMV_O, wbytes(T[FTX_T_O]) + Md * m->qdim * f4 + 2 * Md * D * f4, m->att,
+                         m->qdim, nullptr, idx, &T[FTX_T_O], gs, 1, m->qdim, EPI_ACCUM,
+                         out1(m->x, D, 1), Mt);
+            if (rc) return rc;
+        }
+        // gate / up with SwiGLU into h
+        {
+            const ftx_tensor* ts[2] = {T[FTX_T_GATE], T[FTX_T_UP]};
+            const size_t idx[2] = {(size_t)(lt + FTX_T_GATE), (size_t)(lt + FTX_T_UP)};
+            GemvSeg gs[2] = {seg(T[FTX_T_GATE], m->h, F), seg(T[FTX_T_UP], nullptr, 0)};
+            rc = project(TK_GEMV_SWIGLU,
+                         wbytes(ts[0]) + wbytes(ts[1]) + Md * D * f4 + Md * F * f4, m->x, D,
+                         m->norms + (l * 2 + 1) * D, idx, ts, gs, 2, D, EPI_SWIGLU,
+                         out1(m->h, F, 0), Mt);
+            if (rc) return rc;
+        }
+        // ffn_down, added into x
+        const ftx_tensor* dn = T[FTX_T_DOWN];
+        const double down_b = wbytes(dn) + Md * F * f4 + 2 * Md * D * f4;
+        if (m->down_tiled[l] && mm_down_supported(dn->dtype, F, D)) {
+            TRACED_L(TK_DOWN, down_b,
+                     launch_mm_down(st, m->down_tiled[l], F, D, m->h, F, Mt, out1(m->x, D, 1),
+                                    m->mm_part, m->mm_part_n, ctx->cu_count));
+        } else if (m->down_tiled[l] && down_mfma_supported(dn->dtype, F, D, 8)) {
+            // the MFMA down kernel on 8-row chunks, every chunk's split
+            // partials added into x by one reduce
+            auto chunks = [&]() -> hipError_t {
+                int S = 0;
+                for (int64_t c0 = 0; c0 < Mt; c0 += 8) {
+                    const int64_t mc = Mt - c0 < 8 ? Mt - c0 : 8;
+                    float* pc = m->downpart + (S ? (c0 / 8) * (int64_t)S * 8 * D : 0);
+                    hipError_t e = launch_down_mfma(st, dn->dtype, m->down_tiled[l], F, D,
+                                                    m->h + c0 * F, F, mc, m->x + c0 * D, D, pc,
+                                                    ctx->cu_count, &S);
+                    if (e != hipSuccess) return e;
+                }
+                return launch_part_reduce(st, m->downpart, S, D, Mt, m->x, D);
+            };
+            TRACED_L(TK_DOWN, down_b, chunks());
+        } else {
+            TRACED_L(TK_DOWN, down_b,
+                     launch_down(st, dn->data, dn->dtype, dn->row_bytes, F, D, m->h, F, Mt, m->x,
+                                 D, m->part));
+        }
+    }
+    // the LM head, each sequence's rows into its own logits
+    if (sq[0].logits) {
+        const ftx_tensor* lm = d.output ? d.output : d.tok_embd;
+        const size_t idx[1] = {(size_t)(d.n_layer * FTX_LAYER_TENSORS)};
+        MmSeg probe;
+        if (mm_seg(idx[0], lm, probe) || nseq == 1) {
+            MmOut o{};
+            o.nseq = (int)nseq;
+            for (int64_t s = 0; s < nseq; ++s) {
+                o.base[s] = sq[s].logits;
+                o.row0[s] = row0[s];
+            }
+            o.row0[nseq] = Mt;
+            o.ld = V;
+            GemvSeg gs[1] = {seg(lm, sq[0].logits, V)};
+            rc = project(TK_HEAD, wbytes(lm) + Md * D * f4 + Md * V * f4, m->x, D,
+                         m->norms + (d.n_layer * 2) * D, idx, &lm, gs, 1, D, EPI_STORE, o, Mt);
+            if (rc) return rc;
+        } else {
+            // the generic head per sequence (its weights are read once each)
+            for (int64_t s = 0; s < nseq; ++s) {
+                const int64_t M = sq[s].M;
+                GemvSeg gs[1] = {seg(lm, sq[s].logits, V)};
+                rc = project(TK_HEAD, wbytes(lm) + M * D * f4 + M * V * f4, m->x + row0[s] * D,
+                             D, m->norms + (d.n_layer * 2) * D, idx, &lm, gs, 1, D, EPI_STORE,
+                             out1(sq[s].logits, V, 0), M);
+                if (rc) return rc;
+            }
+        }
+    }
+#undef TRACED_L
+    for (int64_t s = 0; s < nseq; ++s)
+        if (sq[s].advance) sq[s].kv->npast += sq[s].M;
+    return FTX_OK;
+}
+
+// checks of one sequence's arguments against the model and its cache
+static int check_seq(ftx_ctx* ctx, const ftx_model* m, const ftx_kv* kv, int64_t M,
+                     const int32_t* tokens) {
+    const ftx_model_desc& d = m->d;
+    if (!kv || !tokens) return ftx_fail(ctx, FTX_E_INVALID, "null argument");
+    if (M < 1 || M > m->Mmax) return ftx_fail(ctx, FTX_E_INVALID, "M out of range");
+    if (kv->n_layer != d.n_layer || kv->kdim != m->kdim || kv->n_kv != d.n_head_kv ||
+        kv->hd != d.head_dim || kv->n_head != d.n_head)
+        return ftx_fail(ctx, FTX_E_INVALID, "kv cache does not match the model");
+    if (M > kv->mmax)
+        return ftx_fail(ctx, FTX_E_INVALID, "M above the max_tokens of the kv cache's model");
+    if (kv->npast + M > kv->cap) return ftx_fail(ctx, FTX_E_RANGE, "kv capacity exceeded");
+    return FTX_OK;
 }
 
 extern "C" {
@@ -254,6 +566,24 @@ int ftx_model_create(ftx_ctx* ctx, const ftx_model_desc* d, ftx_model** out) {
         m->pln_dt[i] = pdt;
         if (launch_planar(ctx->stream, w->data, w->dtype, w->nrows, w->ne[0], buf) != hipSuccess)
             ok = false;
+    }
+    // the large-M path (more than 8 tokens, or several sequences):
+    // activation operands for the widest contraction and split-sum partials
+    // for the widest projection (SwiGLU's gate and up sums always pass
+    // through them)
+    if (ok) {
+        const int64_t Mp = mm_pad_tokens(Mmax), Kmax = std::max(D, qdim);
+        const int cu = ctx->cu_count;
+        size_t pf = (size_t)Mp * 2 * (size_t)d->n_ff;
+        auto upd = [&](int64_t N, int64_t K) {
+            pf = std::max(pf, mm_part_floats(Mp, N, K / 256, (N + 255) / 256, cu));
+        };
+        upd(qdim + 2 * kdim, D);
+        upd(D, qdim);
+        upd(2 * d->n_ff, D);
+        pf = std::max(pf, mm_down_part_floats(Mp, d->n_ff, D, cu));
+        ok = dalloc(&m->mm_act, mm_act_halves(Mp, Kmax)) && dalloc(&m->mm_part, pf);
+        m->mm_part_n = pf;
     }
     if (!ok) {
         model_release(m);
@@ -421,23 +751,48 @@ int ftx_kv_commit(ftx_kv* kv, const int32_t* nodes, int64_t n) {
     return FTX_OK;
 }
 
+int ftx_verify_batch(ftx_ctx* ctx, ftx_model* m, const ftx_seq_args* seqs, int64_t nseq) {
+    if (!ctx || !m || !seqs) return ftx_fail(ctx, FTX_E_INVALID, "null argument");
+    if (nseq < 1 || nseq > FTX_MAX_SEQ)
+        return ftx_fail(ctx, FTX_E_INVALID, "nseq out of range (1 .. FTX_MAX_SEQ)");
+    if (nseq == 1) {
+        const ftx_verify_args a{seqs[0].M, seqs[0].tokens, seqs[0].parents, seqs[0].logits,
+                                seqs[0].advance, 0};
+        return ftx_verify_step(ctx, m, seqs[0].kv, &a);
+    }
+    int64_t Mt = 0;
+    for (int64_t s = 0; s < nseq; ++s) {
+        int rc = check_seq(ctx, m, seqs[s].kv, seqs[s].M, seqs[s].tokens);
+        if (rc) return rc;
+        if ((seqs[s].logits != nullptr) != (seqs[0].logits != nullptr))
+            return ftx_fail(ctx, FTX_E_INVALID, "logits must be given for every sequence or none");
+        for (int64_t r = 0; r < s; ++r)
+            if (seqs[r].kv == seqs[s].kv)
+                return ftx_fail(ctx, FTX_E_INVALID, "two sequences share a kv cache");
+        Mt += seqs[s].M;
+    }
+    if (Mt > m->Mmax) return ftx_fail(ctx, FTX_E_INVALID, "tokens of all sequences above max_tokens");
+    return verify_large(ctx, m, seqs, nseq);
+}
+
 int ftx_verify_step(ftx_ctx* ctx, ftx_model* m, ftx_kv* kv, const ftx_verify_args* a) {
     if (!ctx || !m || !kv || !a || !a->tokens)
         return ftx_fail(ctx, FTX_E_INVALID, "null argument");
     const ftx_model_desc& d = m->d;
     const int64_t M = a->M;
-    if (M < 1 || M > m->Mmax) return ftx_fail(ctx, FTX_E_INVALID, "M out of range");
-    if (kv->n_layer != d.n_layer || kv->kdim != m->kdim || kv->n_kv != d.n_head_kv ||
-        kv->hd != d.head_dim || kv->n_head != d.n_head)
-        return ftx_fail(ctx, FTX_E_INVALID, "kv cache does not match the model");
-    if (M > kv->mmax)
-        return ftx_fail(ctx, FTX_E_INVALID, "M above the max_tokens of the kv cache's model");
+    {
+        int rc = check_seq(ctx, m, kv, M, a->tokens);
+        if (rc) return rc;
+    }
+    if (M > 8) {
+        const ftx_seq_args sa{kv, M, a->tokens, a->parents, a->logits, a->advance, 0};
+        return verify_large(ctx, m, &sa, 1);
+    }
     const int64_t npast = kv->npast;
-    if (npast + M > kv->cap) return ftx_fail(ctx, FTX_E_RANGE, "kv capacity exceeded");
     // host-side argument prep: tokens, depth, ancestor masks, npast
     const int aw = (int)((M + 31) / 32);
     const int64_t hd2 = d.head_dim / 2;
-    const StepArgsLayout AL = step_args_layout(M, d.head_dim);
+    const StepArgsLayout AL = step_args_layout(M, d.head_dim, aw);
     const int slot = m->pin_next;
     uint8_t* pin = m->pin[slot];
     FTX_HIP(ctx, hipEventSynchronize(m->pin_ev[slot]));  // this block's last copy is done

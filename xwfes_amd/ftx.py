@@ -61,6 +61,11 @@ class VerifyArgs(C.Structure):
                 ("advance", C.c_int32), ("pad_", C.c_int32)]
 
 
+class SeqArgs(C.Structure):
+    _fields_ = [("kv", _vp), ("M", _i64), ("tokens", _i32p), ("parents", _i32p),
+                ("logits", _vp), ("advance", C.c_int32), ("pad_", C.c_int32)]
+
+
 class AcceptArgs(C.Structure):
     _fields_ = [("base_row", _vp), ("rows", _vp), ("q", _vp), ("M", _i64), ("V", _i64),
                 ("props", _i32p), ("parents", _i32p), ("pd", _fp), ("mode", C.c_int32),
@@ -119,6 +124,7 @@ def load(path=LIB_PATH):
         "ftx_kv_write": (C.c_int, [_vp, _vp, _vp]),
         "ftx_kv_read": (C.c_int, [_vp, _vp, _vp]),
         "ftx_verify_step": (C.c_int, [_vp, _vp, _vp, C.POINTER(VerifyArgs)]),
+        "ftx_verify_batch": (C.c_int, [_vp, _vp, C.POINTER(SeqArgs), _i64]),
         "ftx_accept": (C.c_int, [_vp, C.POINTER(AcceptArgs)]),
         "ftx_argmax_prob": (C.c_int, [_vp, _vp, _i64, _i32p, _fp]),
         "ftx_fill_normal": (C.c_int, [_vp, _vp, C.c_int, _i64, C.c_uint64, C.c_float]),
@@ -362,6 +368,20 @@ class Model:
                        int(advance), 0)
         self.ctx.check(self.ctx.lib.ftx_verify_step(self.ctx.h, self.handle, kv.handle,
                                                     C.byref(a)))
+
+    def verify_batch(self, seqs):
+        """Several sequences in one step: seqs = [(kv, tokens, logits_ptr,
+        parents or None, advance), ...]; each sequence verifies its draft
+        against its own cache."""
+        keep, arr = [], (SeqArgs * len(seqs))()
+        for i, (kv, tokens, logits_ptr, parents, advance) in enumerate(seqs):
+            toks = np.ascontiguousarray(tokens, np.int32)
+            par = None if parents is None else np.ascontiguousarray(parents, np.int32)
+            keep += [toks, par]
+            arr[i] = SeqArgs(kv.handle, toks.size, toks.ctypes.data_as(_i32p),
+                             None if par is None else par.ctypes.data_as(_i32p), logits_ptr,
+                             int(advance), 0)
+        self.ctx.check(self.ctx.lib.ftx_verify_batch(self.ctx.h, self.handle, arr, len(seqs)))
 
     def step(self, kv, token, logits_ptr):
         """Engine::step (src/engine.cpp:650-658): `token` at the committed
