@@ -215,8 +215,9 @@ struct MmOut {
 int64_t mm_pad_tokens(int64_t M);
 size_t mm_act_halves(int64_t Mp, int64_t K);
 MmAct mm_act(void* buf, int64_t Mp, int64_t K);
+// weight_dt: the consumer's operand (Q4_0 takes its octets reordered)
 hipError_t launch_mm_prep(hipStream_t st, const float* x, int64_t ldx, const float* normw,
-                          float eps, int64_t M, const MmAct& act);
+                          float eps, int64_t M, const MmAct& act, int weight_dt);
 bool mm_supported(int dt, int64_t K);
 bool mm_down_supported(int dt, int64_t n_in, int64_t N);
 // split-sum scratch of a launch over N output columns (`ntiles` 256-row

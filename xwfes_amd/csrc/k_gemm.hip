@@ -16,10 +16,10 @@
 // of fp32 accumulation.
 //
 // Row-dot form (y = x W^T, blocks along the contraction; every projection
-// but ffn_down): a workgroup of 4 waves owns 256 weight rows (64 per wave,
-// four 16-column MFMA tiles) and a 64-token tile (four 16-row MFMA tiles);
-// the activation tile is staged in LDS 64 contraction elements at a time
-// (double-buffered, one barrier per stage) and shared by the four waves,
+// but ffn_down): a workgroup of 8 waves owns 256 weight rows (32 per wave,
+// two 16-column MFMA tiles) and a 64-token tile (four 16-row MFMA tiles);
+// the activation tile is staged in LDS 256 contraction elements at a time
+// (double-buffered, one barrier per stage) and shared by the eight waves,
 // which read their weights straight from the tiled (Q4_K) or planar (Q8_0,
 // Q4_0) copies the model keeps.  Split-K across workgroups where the tiles
 // alone do not fill the device; partial sums then go to a buffer that the
@@ -45,11 +45,12 @@ typedef int v2i __attribute__((ext_vector_type(2)));
 
 constexpr int MM_TOK = 64;              // tokens per workgroup tile
 constexpr int MM_MS = MM_TOK / 16;      // 16-token MFMA tiles
-constexpr int MM_WAVES = 4;
-constexpr int MM_WROWS = 64;            // weight rows (output columns) per wave
+// 8 waves of 32 weight rows (two waves per SIMD, so that one wave's
+// unpacking and LDS reads overlap the other's MFMAs; measured 12% faster
+// than 4 waves of 64 rows on the 52-token gate / up shape)
+constexpr int MM_WAVES = 8;  // waves per workgroup (256 weight rows)
+constexpr int MM_WROWS = 256 / MM_WAVES;  // weight rows (output columns) per wave
 constexpr int MM_NT = MM_WROWS / 16;    // 16-column MFMA tiles per wave
-constexpr int MM_KC = 64;               // contraction elements per LDS stage
-constexpr int MM_PITCH = MM_KC + 8;     // halves per staged token row
 
 // the activation operands of ffn_down are formed as (h d) * 2^10 so that
 // their fp16 lo parts stay clear of the subnormal range (undone on the
@@ -69,20 +70,6 @@ __device__ __forceinline__ v8h nib8(uint32_t w, float bias) {
     const v2h b = {(_Float16)(-1024.f - bias), (_Float16)(-1024.f - bias)};
     const v2h h0 = __builtin_bit_cast(v2h, p0) + b, h1 = __builtin_bit_cast(v2h, p1) + b;
     const v2h h2 = __builtin_bit_cast(v2h, p2) + b, h3 = __builtin_bit_cast(v2h, p3) + b;
-    return v8h{h0[0], h0[1], h1[0], h1[1], h2[0], h2[1], h3[0], h3[1]};
-}
-
-// 8 low (hi = false) or high nibbles of 8 bytes, byte order -> fp16 q, exact
-__device__ __forceinline__ v8h nib8_bytes(v2i w, bool high) {
-    const uint32_t a = high ? ((uint32_t)w.x >> 4) & 0x0F0F0F0Fu : (uint32_t)w.x & 0x0F0F0F0Fu;
-    const uint32_t b = high ? ((uint32_t)w.y >> 4) & 0x0F0F0F0Fu : (uint32_t)w.y & 0x0F0F0F0Fu;
-    const uint32_t p0 = __builtin_amdgcn_perm(a, 0x64646464u, 0x00050004u);
-    const uint32_t p1 = __builtin_amdgcn_perm(a, 0x64646464u, 0x00070006u);
-    const uint32_t p2 = __builtin_amdgcn_perm(b, 0x64646464u, 0x00050004u);
-    const uint32_t p3 = __builtin_amdgcn_perm(b, 0x64646464u, 0x00070006u);
-    const v2h o = {(_Float16)(-1024.f), (_Float16)(-1024.f)};
-    const v2h h0 = __builtin_bit_cast(v2h, p0) + o, h1 = __builtin_bit_cast(v2h, p1) + o;
-    const v2h h2 = __builtin_bit_cast(v2h, p2) + o, h3 = __builtin_bit_cast(v2h, p3) + o;
     return v8h{h0[0], h0[1], h1[0], h1[1], h2[0], h2[1], h3[0], h3[1]};
 }
 
@@ -107,37 +94,45 @@ __device__ __forceinline__ void split_hl(float v, _Float16& h, _Float16& l) {
 }
 
 // ---------------------------------------------------------------- prep
-// One workgroup (256 threads) per token row m < Mp; rows m >= M are zeros.
+// The activation operand in MFMA fragment order, so that a workgroup copies
+// it to LDS with one direct global->LDS load per 1 KB and every lane reads
+// its fragment from 16 contiguous bytes: for 16-token tile mt and 32-element
+// K-step ks, fragment (mt, ks) is 64 lanes x 8 halves with lane l holding
+// elements 8 (l / 16) .. + 7 of the step for token 16 mt + l % 16 (Q4_0
+// consumers: each octet stored as its even then its odd elements, the order
+// of that format's nibbles).  Planes: hi [Mp / 16][K / 32][64][8], lo the
+// same; the 32-element sums of the token rows, for the Q4_K min term, as
+// fragments of the 16x16x16 operand: [Mp / 16][K / 256][32 lanes][4] with
+// lane l holding sub-blocks 4 (l / 16) .. + 3 of the super-block for token
+// 16 mt + l % 16 (hi and lo planes).
+__device__ __forceinline__ int64_t frag_at(int64_t m, int64_t k, int64_t K, bool inter) {
+    const int64_t mt = m >> 4, ks = k >> 5;
+    const int lane = (int)(m & 15) + 16 * (int)((k & 31) >> 3);
+    int e = (int)(k & 7);
+    if (inter) e = (e & 1) ? 4 + (e >> 1) : (e >> 1);
+    return ((mt * (K / 32) + ks) * 64 + lane) * 8 + e;
+}
+
+// Workgroup (token row m < Mp, 1024-element slice): rows m >= M are zeros.
 // v = (x * inv) * w with inv = 1 / sqrt(sum x^2 / K + eps) when normw is
-// given (src/engine.cpp:23-41), else v = x; writes v as fp16 hi / lo planes
-// [Mp][K] and the 32-element sums of v as hi / lo planes [Mp][K / 32].
+// given (src/engine.cpp:23-41; every slice's workgroup forms the row's sum
+// itself), else v = x; v is split into fp16 hi + lo.
 __global__ void __launch_bounds__(256) k_mm_prep(const float* __restrict__ x, int64_t ldx,
                                                  const float* __restrict__ normw, float eps,
-                                                 int64_t K, int M, _Float16* __restrict__ xh,
+                                                 int64_t K, int M, int inter,
+                                                 _Float16* __restrict__ xh,
                                                  _Float16* __restrict__ xl,
                                                  _Float16* __restrict__ sh,
                                                  _Float16* __restrict__ sl) {
 #pragma clang fp contract(off)
     __shared__ float red[4];
     const int m = blockIdx.x, t = threadIdx.x;
-    const int64_t nsub = K / 32;
-    _Float16* oh = xh + (int64_t)m * K;
-    _Float16* ol = xl + (int64_t)m * K;
-    if (m >= M) {  // block-uniform
-        const v4h z = {};
-        for (int64_t k = 4 * t; k < K; k += 1024) {
-            *(v4h*)(oh + k) = z;
-            *(v4h*)(ol + k) = z;
-        }
-        for (int64_t j = t; j < nsub; j += 256) {
-            sh[m * nsub + j] = (_Float16)0.f;
-            sl[m * nsub + j] = (_Float16)0.f;
-        }
-        return;
-    }
-    const float* row = x + (int64_t)m * ldx;
+    const int64_t nsb = K / 256;
+    const int64_t k0 = (int64_t)blockIdx.y * 1024, k1 = min(k0 + 1024, K);
+    const bool live = m < M;  // block-uniform
+    const float* row = x + (int64_t)(live ? m : 0) * ldx;
     float inv = 1.f;
-    if (normw) {
+    if (live && normw) {
         float ss = 0.f;
         for (int64_t k = 4 * t; k < K; k += 1024) {
             const float4 v = *(const float4*)(row + k);
@@ -153,36 +148,51 @@ __global__ void __launch_bounds__(256) k_mm_prep(const float* __restrict__ x, in
         ss = (red[0] + red[1]) + (red[2] + red[3]);
         inv = 1.f / sqrtf(ss / (float)K + eps);
     }
-    for (int64_t k = 4 * t; k < K; k += 1024) {
-        const float4 v = *(const float4*)(row + k);
-        float o[4] = {v.x, v.y, v.z, v.w};
-        if (normw) {
-            const float4 w = *(const float4*)(normw + k);
-            o[0] = (o[0] * inv) * w.x;
-            o[1] = (o[1] * inv) * w.y;
-            o[2] = (o[2] * inv) * w.z;
-            o[3] = (o[3] * inv) * w.w;
+    for (int64_t k = k0 + 4 * t; k < k1; k += 1024) {
+        float o[4] = {0.f, 0.f, 0.f, 0.f};
+        if (live) {
+            const float4 v = *(const float4*)(row + k);
+            o[0] = v.x;
+            o[1] = v.y;
+            o[2] = v.z;
+            o[3] = v.w;
+            if (normw) {
+                const float4 w = *(const float4*)(normw + k);
+                o[0] = (o[0] * inv) * w.x;
+                o[1] = (o[1] * inv) * w.y;
+                o[2] = (o[2] * inv) * w.z;
+                o[3] = (o[3] * inv) * w.w;
+            }
         }
-        v4h hv, lv;
+        _Float16 hv[4], lv[4];
 #pragma unroll
-        for (int i = 0; i < 4; ++i) {
-            _Float16 h, l;
-            split_hl(o[i], h, l);
-            hv[i] = h;
-            lv[i] = l;
+        for (int i = 0; i < 4; ++i) split_hl(o[i], hv[i], lv[i]);
+        if (!inter) {
+            const int64_t at = frag_at(m, k, K, false);  // 4 consecutive slots
+            *(v4h*)(xh + at) = v4h{hv[0], hv[1], hv[2], hv[3]};
+            *(v4h*)(xl + at) = v4h{lv[0], lv[1], lv[2], lv[3]};
+        } else {
+#pragma unroll
+            for (int i = 0; i < 4; ++i) {
+                const int64_t at = frag_at(m, k + i, K, true);
+                xh[at] = hv[i];
+                xl[at] = lv[i];
+            }
         }
-        *(v4h*)(oh + k) = hv;
-        *(v4h*)(ol + k) = lv;
         // the 8 threads of a 32-element sub-block
         float s = (o[0] + o[1]) + (o[2] + o[3]);
         s += __shfl_xor(s, 1, 64);
         s += __shfl_xor(s, 2, 64);
         s += __shfl_xor(s, 4, 64);
         if ((t & 7) == 0) {
+            const int64_t j = k / 32, sb = j / 8;
+            const int jj = (int)(j % 8);
+            const int lane = (m & 15) + 16 * (jj >> 2);
+            const int64_t at = (((int64_t)(m >> 4) * nsb + sb) * 32 + lane) * 4 + (jj & 3);
             _Float16 h, l;
             split_hl(s, h, l);
-            sh[m * nsub + k / 32] = h;
-            sl[m * nsub + k / 32] = l;
+            sh[at] = h;
+            sl[at] = l;
         }
     }
 }
@@ -217,7 +227,7 @@ struct MmArgs {
     int64_t K;
     int nsb;            // 256-element steps of the contraction
     int sb_per_split;
-    const _Float16 *xh, *xl, *sh, *sl;
+    const _Float16 *xh, *xl, *sh, *sl;  // fragment-order operands (k_mm_prep)
     int M;
     MmOutDev out;
 };
@@ -228,7 +238,7 @@ __device__ __forceinline__ int mm_seg_of(const MmArgs& a, int64_t u) {
     return si;
 }
 
-// weights of one 256-element step for the wave's four column tiles
+// weights of one 256-element step for the wave's column tiles
 template <int DT>
 struct MmW;
 template <>
@@ -247,68 +257,94 @@ struct MmW<FTX_Q4_0_PLANAR> {
     v4i d[MM_NT];
 };
 
-// Lane (col = l % 16, kq = l / 16) of MFMA column tile t holds B[8 kq + e][col]
-// of each 32-element K-step.
+// The lane's weight addresses at step 0, computed once per wave: lane (col
+// = l % 16, kq = l / 16) of MFMA column tile t holds B[8 kq + e][col] of
+// each 32-element K-step, i.e. elements 8 kq .. 8 kq + 7 of its row.
+struct MmPtr {
+    const uint8_t* q[MM_NT];  // Q4_K: the lane's bytes of chunk 0; planar: of block 0
+    const uint8_t* h[MM_NT];  // Q4_K: its row's header; planar: its row's scales
+    int64_t qstep, hstep;     // bytes per 256-element step
+    int cstride;              // Q4_K: bytes from one 64-element chunk to the next
+};
+
 template <int DT>
-__device__ __forceinline__ void mm_load_w(MmW<DT>& o, const MmSegDev& sg, int64_t rbase, int sb,
-                                          int nsb, int col, int kq) {
+__device__ __forceinline__ void mm_ptrs(MmPtr& p, const MmSegDev& sg, int64_t rbase, int nsb,
+                                        int col, int kq) {
 #pragma unroll
     for (int t = 0; t < MM_NT; ++t) {
         int64_t n = rbase + 16 * t + col;  // the lane's weight row in the segment
         if (n >= sg.N) n = sg.N - 1;
         if constexpr (DT == FTX_Q4_K) {
             const int R = sg.rpt;
-            const int64_t T = n / R;
-            const int r = (int)(n % R), li = r + R * (kq >> 1), half = kq & 1;
-            const uint8_t* blk = sg.W + (T * nsb + sb) * (int64_t)R * 144;
-#pragma unroll
-            for (int c = 0; c < 4; ++c)
-                o.qs[t][c] = *(const v2i*)(blk + c * R * 32 + li * 16 + 8 * half);
-            o.hdr[t] = *(const v4i*)(blk + 4 * R * 32 + r * 16);
-        } else if constexpr (DT == FTX_Q8_0_PLANAR) {
-            const uint8_t* row = sg.W + n * sg.row_bytes;
-            const int64_t nb = sg.row_bytes / 34;
-#pragma unroll
-            for (int b = 0; b < 8; ++b)
-                o.q[t][b] = *(const v2i*)(row + 2 * nb + (int64_t)(8 * sb + b) * 32 + 8 * kq);
-            o.d[t] = *(const v4i*)(row + (int64_t)16 * sb);
+            const int T = (int)n / R, r = (int)n % R, li = r + R * (kq >> 1), half = kq & 1;
+            const uint8_t* tile = sg.W + (int64_t)T * nsb * R * 144;
+            p.q[t] = tile + li * 16 + 8 * half;
+            p.h[t] = tile + 4 * R * 32 + r * 16;
         } else {
             const uint8_t* row = sg.W + n * sg.row_bytes;
-            const int64_t nb = sg.row_bytes / 18;
+            const int64_t nb = sg.row_bytes / (DT == FTX_Q8_0_PLANAR ? 34 : 18);
+            p.q[t] = row + 2 * nb + (DT == FTX_Q8_0_PLANAR ? 8 : 4) * kq;
+            p.h[t] = row;
+        }
+    }
+    if constexpr (DT == FTX_Q4_K) {
+        p.qstep = p.hstep = (int64_t)sg.rpt * 144;
+        p.cstride = sg.rpt * 32;
+    } else {
+        p.qstep = DT == FTX_Q8_0_PLANAR ? 256 : 128;
+        p.hstep = 16;
+        p.cstride = 0;
+    }
+}
+
+template <int DT>
+__device__ __forceinline__ void mm_load(MmW<DT>& o, const MmPtr& p, int sb) {
+    const int64_t qo = sb * p.qstep, ho = sb * p.hstep;
 #pragma unroll
-            for (int b = 0; b < 8; ++b)
-                o.q[t][b] = *(const uint32_t*)(row + 2 * nb + (int64_t)(8 * sb + b) * 16 + 4 * kq);
-            o.d[t] = *(const v4i*)(row + (int64_t)16 * sb);
+    for (int t = 0; t < MM_NT; ++t) {
+        const uint8_t* q = p.q[t] + qo;
+        if constexpr (DT == FTX_Q4_K) {
+#pragma unroll
+            for (int c = 0; c < 4; ++c) o.qs[t][c] = *(const v2i*)(q + c * p.cstride);
+            o.hdr[t] = *(const v4i*)(p.h[t] + ho);
+        } else if constexpr (DT == FTX_Q8_0_PLANAR) {
+#pragma unroll
+            for (int b = 0; b < 8; ++b) o.q[t][b] = *(const v2i*)(q + 32 * b);
+            o.d[t] = *(const v4i*)(p.h[t] + ho);
+        } else {
+#pragma unroll
+            for (int b = 0; b < 8; ++b) o.q[t][b] = *(const uint32_t*)(q + 16 * b);
+            o.d[t] = *(const v4i*)(p.h[t] + ho);
         }
     }
 }
 
-// fp16 of the d (or dmin: hi = true) word of a Q4_K header, of block b of 8 planar scales
-__device__ __forceinline__ float hdr_half(const v4i& h, bool hi) {
-    return h2f((uint16_t)(hi ? ((uint32_t)h.x >> 16) : ((uint32_t)h.x & 0xFFFF)));
-}
 __device__ __forceinline__ float scale8(const v4i& d, int b) {
     const uint32_t w = (uint32_t)d[b >> 1];
     return h2f((uint16_t)((b & 1) ? (w >> 16) : (w & 0xFFFF)));
 }
 
-// Q4_0's nibbles are interleaved (element j = nibble j & 1 of byte j / 2,
-// include/ft/quant.h:45-60): its B slots are [even elements, odd elements]
-// of each octet, so its activation stage stores octets in that order
-template <int DT>
-__device__ __forceinline__ v8h mm_stage_order(v8h v) {
-    if constexpr (DT == FTX_Q4_0_PLANAR)
-        return v8h{v[0], v[2], v[4], v[6], v[1], v[3], v[5], v[7]};
-    return v;
+// four bytes (values < 2048) -> two fp16 pairs, exact
+__device__ __forceinline__ void bytes4_h(uint32_t w, v2h& lo, v2h& hi) {
+    const v2h o = {(_Float16)(-1024.f), (_Float16)(-1024.f)};
+    lo = __builtin_bit_cast(v2h, __builtin_amdgcn_perm(w, 0x64646464u, 0x00050004u)) + o;
+    hi = __builtin_bit_cast(v2h, __builtin_amdgcn_perm(w, 0x64646464u, 0x00070006u)) + o;
 }
 
-// grid = (ceil(units / 4), Mp / 64, splits); block = 256.  Every wave takes
-// part in the activation staging and its barriers; a wave past the last
-// unit computes nothing.
+typedef __attribute__((address_space(3))) void lds_void;
+
+// grid = (ceil(units / 4), Mp / 64, splits); block = 256.  Per 256-element
+// step the workgroup's activation fragments (4 token tiles x 8 K-steps, hi
+// and lo: 64 KB) are copied to one of two LDS buffers by direct loads (16
+// per wave), issued a whole step ahead together with the next step's
+// weights (two register sets used in turn); one wait and one barrier per
+// step.  Every wave takes part in the copies and barriers, and none
+// branches around its MFMAs: a wave past the last unit computes on its
+// clamped rows and stores nothing.
 template <int DT>
-__global__ void __launch_bounds__(64 * MM_WAVES) __attribute__((amdgpu_waves_per_eu(1, 1)))
-k_mm(MmArgs a) {
-    __shared__ _Float16 st[2][2][MM_TOK][MM_PITCH];  // [buf][hi / lo][token][k]
+__global__ void __launch_bounds__(64 * MM_WAVES)
+    __attribute__((amdgpu_waves_per_eu(MM_WAVES / 4, MM_WAVES / 4))) k_mm(MmArgs a) {
+    extern __shared__ __attribute__((aligned(16))) uint8_t mm_lds[];  // [2][64 KB]
     const int tid = threadIdx.x, lane = tid & 63;
     const int w = __builtin_amdgcn_readfirstlane(tid >> 6);
     const int col = lane & 15, kq = lane >> 4;
@@ -317,30 +353,35 @@ k_mm(MmArgs a) {
     const int si = mm_seg_of(a, live ? u : a.units - 1);
     const MmSegDev& sg = a.seg[si];
     const int64_t rbase = ((live ? u : a.units - 1) - sg.unit0) * MM_WROWS;
-    const int64_t m0 = (int64_t)blockIdx.y * MM_TOK;
+    const int64_t mt0 = (int64_t)blockIdx.y * MM_MS;  // first 16-token tile
     const int ks = blockIdx.z;
     const int sb0 = ks * a.sb_per_split;
     const int sb1 = min(sb0 + a.sb_per_split, a.nsb);
-    const int64_t K = a.K;
+    const int64_t nks = a.K / 32;
+    MmPtr wp;
+    mm_ptrs<DT>(wp, sg, rbase, a.nsb, col, kq);
 
-    // activation staging: thread t copies token row m0 + t / 4, elements
-    // 16 (t % 4) .. + 15 of the stage, hi and lo
-    const int sm = tid >> 2, sp = tid & 3;
-    const _Float16* gh = a.xh + (m0 + sm) * K + 16 * sp;
-    const _Float16* gl = a.xl + (m0 + sm) * K + 16 * sp;
-    v8h rg[4];
-    auto stage_load = [&](int64_t k0) {
-        rg[0] = ld8h(gh + k0);
-        rg[1] = ld8h(gh + k0 + 8);
-        rg[2] = ld8h(gl + k0);
-        rg[3] = ld8h(gl + k0 + 8);
+    // the step's 64 fragments: block b = (hl, ms, j) = 32 hl + 8 ms + j ->
+    // LDS offset b KB; wave w copies blocks BPW w .. BPW w + BPW - 1
+    constexpr int BPW = 64 / MM_WAVES;
+    const int b0 = BPW * w, hl0 = b0 >> 5, ms0 = (b0 >> 3) & 3;
+    const _Float16* gsrc = (hl0 ? a.xl : a.xh) + ((mt0 + ms0) * nks * 64 + lane) * 8;
+    auto stage = [&](int sb, int buf) {
+        const _Float16* src = gsrc + (int64_t)sb * 8 * 64 * 8;
+#pragma unroll
+        for (int i = 0; i < BPW; ++i)
+            __builtin_amdgcn_global_load_lds(
+                (const void*)(src + ((i >> 3) * nks + (i & 7)) * 64 * 8),
+                (lds_void*)(mm_lds + buf * 65536 + (b0 + i) * 1024), 16, 0, 0);
     };
-    auto stage_store = [&](int buf) {
-        *(v8h*)&st[buf][0][sm][16 * sp] = mm_stage_order<DT>(rg[0]);
-        *(v8h*)&st[buf][0][sm][16 * sp + 8] = mm_stage_order<DT>(rg[1]);
-        *(v8h*)&st[buf][1][sm][16 * sp] = mm_stage_order<DT>(rg[2]);
-        *(v8h*)&st[buf][1][sm][16 * sp + 8] = mm_stage_order<DT>(rg[3]);
+    auto frag = [&](int buf, int hl, int ms, int j) -> v8h {
+        return *(const v8h*)(mm_lds + buf * 65536 + ((hl * 4 + ms) * 8 + j) * 1024 + lane * 16);
     };
+    // Q4_K min term: this lane's sub-block sums (K slots of the 16x16x16
+    // operand; zero for kq >= 2)
+    // (lanes kq >= 2 read lane - 32's sums and discard them: in bounds)
+    const _Float16* xs0 = a.sh + (mt0 * a.nsb * 32 + (lane & 31)) * 4;
+    const _Float16* xl0 = a.sl + (mt0 * a.nsb * 32 + (lane & 31)) * 4;
 
     v4f acc[MM_NT][MM_MS];
 #pragma unroll
@@ -349,120 +390,159 @@ k_mm(MmArgs a) {
         for (int ms = 0; ms < MM_MS; ++ms) acc[t][ms] = v4f{0.f, 0.f, 0.f, 0.f};
     const v4f zero4 = {0.f, 0.f, 0.f, 0.f};
 
-    MmW<DT> wc, wn;
-    if (sb0 < sb1) {
-        mm_load_w<DT>(wc, sg, rbase, sb0, a.nsb, col, kq);
-        stage_load((int64_t)sb0 * 256);
-        stage_store(0);
-    }
-    __syncthreads();
-    int buf = 0;
-    for (int sb = sb0; sb < sb1; ++sb) {
-        // the next step's weights are in flight during this step's MFMAs
-        mm_load_w<DT>(wn, sg, rbase, sb + 1 < sb1 ? sb + 1 : sb, a.nsb, col, kq);
-        v4f tmp[MM_NT][MM_MS];
-        // Q4_K: the scales / mins of the lane's rows in this super-block
-        uint32_t scw[MM_NT][2], mnw[MM_NT][2];
+    // one 256-element step from LDS buffer `buf` with weights `wc`; the
+    // next step's copies and weights (into `wn`) are issued first
+    auto step = [&](int sb, int buf, const MmW<DT>& wc, MmW<DT>& wn) {
+        __builtin_amdgcn_s_waitcnt(0x0F70);  // this step's fragments and weights
+        __syncthreads();                     // every wave is done with the other buffer
+        if (sb + 1 < sb1) {
+            stage(sb + 1, buf ^ 1);
+            mm_load<DT>(wn, wp, sb + 1);
+        }
+        v4h xsh[MM_MS], xsl[MM_MS];
+        v2h scp[MM_NT][4], scn[MM_NT][4];  // Q4_K: sc and -1024 sc per sub-block, fp16 pairs
+        v4h mnh[MM_NT];                    // Q4_K: the 4 mins of the lane's K slots
         if constexpr (DT == FTX_Q4_K) {
+#pragma unroll
+            for (int ms = 0; ms < MM_MS; ++ms) {
+                const int64_t o = ((int64_t)ms * a.nsb + sb) * 32 * 4;
+                const v4h hh = *(const v4h*)(xs0 + o), ll = *(const v4h*)(xl0 + o);
+                xsh[ms] = kq < 2 ? hh : v4h{};
+                xsl[ms] = kq < 2 ? ll : v4h{};
+            }
 #pragma unroll
             for (int t = 0; t < MM_NT; ++t) {
                 const uint32_t S0 = wc.hdr[t].y, S1 = wc.hdr[t].z, S2 = wc.hdr[t].w;
-                scw[t][0] = S0 & 0x3F3F3F3Fu;
-                mnw[t][0] = S1 & 0x3F3F3F3Fu;
-                scw[t][1] = (S2 & 0x0F0F0F0Fu) | ((S0 >> 2) & 0x30303030u);
-                mnw[t][1] = ((S2 >> 4) & 0x0F0F0F0Fu) | ((S1 >> 2) & 0x30303030u);
+                const uint32_t sc0 = S0 & 0x3F3F3F3Fu;
+                const uint32_t sc1 = (S2 & 0x0F0F0F0Fu) | ((S0 >> 2) & 0x30303030u);
+                const uint32_t mn = (kq & 1) ? ((S2 >> 4) & 0x0F0F0F0Fu) | ((S1 >> 2) & 0x30303030u)
+                                             : S1 & 0x3F3F3F3Fu;
+                v2h a0, a1;
+                bytes4_h(sc0, scp[t][0], scp[t][1]);
+                bytes4_h(sc1, scp[t][2], scp[t][3]);
+                bytes4_h(mn, a0, a1);
+                mnh[t] = v4h{a0[0], a0[1], a1[0], a1[1]};
+#pragma unroll
+                for (int i = 0; i < 4; ++i) scn[t][i] = scp[t][i] * v2h{(_Float16)(-1024.f), (_Float16)(-1024.f)};
             }
         }
+        v4f tmp[MM_NT][MM_MS];
 #pragma unroll
-        for (int c = 0; c < 4; ++c) {
-            // the next stage's activations in flight during this stage
-            const bool more = c < 3 || sb + 1 < sb1;
-            if (more) stage_load((int64_t)sb * 256 + (c + 1) * MM_KC);
-#pragma unroll
-            for (int s = 0; s < 2; ++s) {
-                const int j = 2 * c + s;  // 32-element K-step (sub-block / block) of the super-block
-                v8h bw[MM_NT];
-                float bs[MM_NT];
-#pragma unroll
-                for (int t = 0; t < MM_NT; ++t) {
-                    if constexpr (DT == FTX_Q4_K) {
-                        const int scv = (int)((scw[t][j >> 2] >> (8 * (j & 3))) & 0xFF);
-                        const _Float16 sch = (_Float16)(float)scv;
-                        bw[t] = nib8_bytes(wc.qs[t][c], s != 0) * v8h{sch, sch, sch, sch, sch, sch, sch, sch};
-                        bs[t] = 0.f;
-                    } else if constexpr (DT == FTX_Q8_0_PLANAR) {
-                        bw[t] = i8x8(wc.q[t][j]);
-                        bs[t] = scale8(wc.d[t], j);
-                    } else {
-                        bw[t] = nib8(wc.q[t][j], 8.f);
-                        bs[t] = scale8(wc.d[t], j);
-                    }
-                }
-#pragma unroll
-                for (int ms = 0; ms < MM_MS; ++ms) {
-                    const v8h ah = ld8h(&st[buf][0][16 * ms + col][32 * s + 8 * kq]);
-                    const v8h al = ld8h(&st[buf][1][16 * ms + col][32 * s + 8 * kq]);
-#pragma unroll
-                    for (int t = 0; t < MM_NT; ++t) {
-                        if (!live) continue;
-                        if constexpr (DT == FTX_Q4_K) {
-                            const v4f c0 = j == 0 ? zero4 : tmp[t][ms];
-                            tmp[t][ms] = __builtin_amdgcn_mfma_f32_16x16x32_f16(ah, bw[t], c0, 0, 0, 0);
-                            tmp[t][ms] = __builtin_amdgcn_mfma_f32_16x16x32_f16(al, bw[t], tmp[t][ms], 0, 0, 0);
-                        } else {
-                            v4f p = __builtin_amdgcn_mfma_f32_16x16x32_f16(ah, bw[t], zero4, 0, 0, 0);
-                            p = __builtin_amdgcn_mfma_f32_16x16x32_f16(al, bw[t], p, 0, 0, 0);
-#pragma unroll
-                            for (int r = 0; r < 4; ++r) acc[t][ms][r] += bs[t] * p[r];
-                        }
-                    }
-                }
-            }
-            if (more) stage_store(buf ^ 1);
-            __syncthreads();
-            buf ^= 1;
-        }
-        if constexpr (DT == FTX_Q4_K) {
-            // acc += d * tmp - dmin * sum_j m_j X_j; the min term's A operand is
-            // the sub-block sums (K slots 4 kq .. 4 kq + 3 = sub-blocks of this
-            // super-block for kq < 2, zero above), its B operand the mins
+        for (int j = 0; j < 8; ++j) {  // 32-element K-step (sub-block / block) of the step
+            // every fragment read of the K-step first, then the weight
+            // operands, then the MFMAs
+            v8h ah[MM_MS], al[MM_MS];
 #pragma unroll
             for (int ms = 0; ms < MM_MS; ++ms) {
-                v4h xh4 = {}, xl4 = {};
-                if (kq < 2) {
-                    const int64_t o = (m0 + 16 * ms + col) * (K / 32) + (int64_t)sb * 8 + 4 * kq;
-                    xh4 = *(const v4h*)(a.sh + o);
-                    xl4 = *(const v4h*)(a.sl + o);
-                }
+                ah[ms] = frag(buf, 0, ms, j);
+                al[ms] = frag(buf, 1, ms, j);
+            }
+            v8h bw[MM_NT];
+            float bs[MM_NT];
 #pragma unroll
-                for (int t = 0; t < MM_NT; ++t) {
-                    if (!live) continue;
-                    v4h bm = {};
-                    if (kq < 2) {
-                        const uint32_t mw = mnw[t][kq];
-                        bm = v4h{(_Float16)(float)(mw & 0xFF), (_Float16)(float)((mw >> 8) & 0xFF),
-                                 (_Float16)(float)((mw >> 16) & 0xFF), (_Float16)(float)(mw >> 24)};
-                    }
-                    v4f mt = __builtin_amdgcn_mfma_f32_16x16x16f16(xh4, bm, zero4, 0, 0, 0);
-                    mt = __builtin_amdgcn_mfma_f32_16x16x16f16(xl4, bm, mt, 0, 0, 0);
-                    const float d = hdr_half(wc.hdr[t], false), dmin = hdr_half(wc.hdr[t], true);
+            for (int t = 0; t < MM_NT; ++t) {
+                if constexpr (DT == FTX_Q4_K) {
+                    // (1024 + q) * sc - 1024 sc = sc q, one rounding of an exact
+                    // integer <= 945
+                    const v2i wv = wc.qs[t][j >> 1];
+                    const uint32_t x0 = (j & 1) ? ((uint32_t)wv.x >> 4) & 0x0F0F0F0Fu
+                                                : (uint32_t)wv.x & 0x0F0F0F0Fu;
+                    const uint32_t x1 = (j & 1) ? ((uint32_t)wv.y >> 4) & 0x0F0F0F0Fu
+                                                : (uint32_t)wv.y & 0x0F0F0F0Fu;
+                    const v2h sc = (j & 1) ? v2h{scp[t][j >> 1][1], scp[t][j >> 1][1]}
+                                           : v2h{scp[t][j >> 1][0], scp[t][j >> 1][0]};
+                    const v2h sn = (j & 1) ? v2h{scn[t][j >> 1][1], scn[t][j >> 1][1]}
+                                           : v2h{scn[t][j >> 1][0], scn[t][j >> 1][0]};
+                    v2h q[4];
+                    q[0] = __builtin_bit_cast(v2h, __builtin_amdgcn_perm(x0, 0x64646464u, 0x00050004u));
+                    q[1] = __builtin_bit_cast(v2h, __builtin_amdgcn_perm(x0, 0x64646464u, 0x00070006u));
+                    q[2] = __builtin_bit_cast(v2h, __builtin_amdgcn_perm(x1, 0x64646464u, 0x00050004u));
+                    q[3] = __builtin_bit_cast(v2h, __builtin_amdgcn_perm(x1, 0x64646464u, 0x00070006u));
+#pragma unroll
+                    for (int i = 0; i < 4; ++i) q[i] = __builtin_elementwise_fma(q[i], sc, sn);
+                    bw[t] = v8h{q[0][0], q[0][1], q[1][0], q[1][1], q[2][0], q[2][1], q[3][0], q[3][1]};
+                    bs[t] = 0.f;
+                } else if constexpr (DT == FTX_Q8_0_PLANAR) {
+                    bw[t] = i8x8(wc.q[t][j]);
+                    bs[t] = scale8(wc.d[t], j);
+                } else {
+                    bw[t] = nib8(wc.q[t][j], 8.f);
+                    bs[t] = scale8(wc.d[t], j);
+                }
+            }
+            if constexpr (DT == FTX_Q4_K) {
+                // hi parts of every tile first, then lo: no MFMA waits on the
+                // one before it
+#pragma unroll
+                for (int t = 0; t < MM_NT; ++t)
+#pragma unroll
+                    for (int ms = 0; ms < MM_MS; ++ms)
+                        tmp[t][ms] = __builtin_amdgcn_mfma_f32_16x16x32_f16(
+                            ah[ms], bw[t], j == 0 ? zero4 : tmp[t][ms], 0, 0, 0);
+#pragma unroll
+                for (int t = 0; t < MM_NT; ++t)
+#pragma unroll
+                    for (int ms = 0; ms < MM_MS; ++ms)
+                        tmp[t][ms] =
+                            __builtin_amdgcn_mfma_f32_16x16x32_f16(al[ms], bw[t], tmp[t][ms], 0, 0, 0);
+            } else {
+                v4f p[MM_NT][MM_MS];
+#pragma unroll
+                for (int t = 0; t < MM_NT; ++t)
+#pragma unroll
+                    for (int ms = 0; ms < MM_MS; ++ms)
+                        p[t][ms] = __builtin_amdgcn_mfma_f32_16x16x32_f16(ah[ms], bw[t], zero4, 0, 0, 0);
+#pragma unroll
+                for (int t = 0; t < MM_NT; ++t)
+#pragma unroll
+                    for (int ms = 0; ms < MM_MS; ++ms)
+                        p[t][ms] = __builtin_amdgcn_mfma_f32_16x16x32_f16(al[ms], bw[t], p[t][ms], 0, 0, 0);
+#pragma unroll
+                for (int t = 0; t < MM_NT; ++t)
+#pragma unroll
+                    for (int ms = 0; ms < MM_MS; ++ms)
+#pragma unroll
+                        for (int r = 0; r < 4; ++r) acc[t][ms][r] += bs[t] * p[t][ms][r];
+            }
+        }
+        if constexpr (DT == FTX_Q4_K) {
+            // acc += d * tmp - dmin * sum_j m_j X_j (the min term one 16x16x16
+            // MFMA on the sub-block sums and the mins)
+#pragma unroll
+            for (int t = 0; t < MM_NT; ++t) {
+                const float d = h2f((uint16_t)((uint32_t)wc.hdr[t].x & 0xFFFF));
+                const float dmin = h2f((uint16_t)((uint32_t)wc.hdr[t].x >> 16));
+#pragma unroll
+                for (int ms = 0; ms < MM_MS; ++ms) {
+                    v4f mt = __builtin_amdgcn_mfma_f32_16x16x16f16(xsh[ms], mnh[t], zero4, 0, 0, 0);
+                    mt = __builtin_amdgcn_mfma_f32_16x16x16f16(xsl[ms], mnh[t], mt, 0, 0, 0);
 #pragma unroll
                     for (int r = 0; r < 4; ++r)
                         acc[t][ms][r] += d * tmp[t][ms][r] - dmin * mt[r];
                 }
             }
         }
-        wc = wn;
+    };
+    MmW<DT> wa, wb;
+    if (sb0 < sb1) {
+        stage(sb0, 0);
+        mm_load<DT>(wa, wp, sb0);
+    }
+    // two weight register sets used in turn (no copy between steps)
+    for (int sb = sb0; sb < sb1; sb += 2) {
+        step(sb, 0, wa, wb);
+        if (sb + 1 >= sb1) break;
+        step(sb + 1, 1, wb, wa);
     }
     if (!live) return;
-    // lane (col, kq) holds C[4 kq + r][col] of each tile: token m0 + 16 ms +
-    // 4 kq + r, output column col0 + rbase + 16 t + col
+    // lane (col, kq) holds C[4 kq + r][col] of each tile: token 16 (mt0 + ms)
+    // + 4 kq + r, output column col0 + rbase + 16 t + col
     const MmOutDev& o = a.out;
 #pragma unroll
     for (int ms = 0; ms < MM_MS; ++ms)
 #pragma unroll
         for (int r = 0; r < 4; ++r) {
-            const int64_t m = m0 + 16 * ms + 4 * kq + r;
+            const int64_t m = 16 * (mt0 + ms) + 4 * kq + r;
             if (m >= a.M) continue;
             int s = 0;
             while (s + 1 < o.nseq && m >= o.row0[s + 1]) ++s;
@@ -498,7 +578,8 @@ struct MmDownArgs {
 // (one 16-column MFMA tile whose columns are the sub-blocks) done by wave w
 // for tokens 16 w .. 16 w + 15 and handed to the other waves through LDS.
 constexpr int MMD_PITCH = 32 + 8;
-__global__ void __launch_bounds__(64 * MM_WAVES) __attribute__((amdgpu_waves_per_eu(1, 1)))
+constexpr int MMD_WAVES = 4;
+__global__ void __launch_bounds__(64 * MMD_WAVES) __attribute__((amdgpu_waves_per_eu(1, 1)))
 k_mm_down(MmDownArgs a) {
     __shared__ _Float16 ad[2][2][MM_TOK][MMD_PITCH];  // [buf][hi / lo][token][row i]
     __shared__ _Float16 am[2][2][MM_TOK][MMD_PITCH];
@@ -698,11 +779,13 @@ MmAct mm_act(void* buf, int64_t Mp, int64_t K) {
 }
 
 hipError_t launch_mm_prep(hipStream_t st, const float* x, int64_t ldx, const float* normw,
-                          float eps, int64_t M, const MmAct& act) {
-    if (act.K % 256 || M < 1 || M > act.Mp || ldx % 4 || ((uintptr_t)x & 15))
+                          float eps, int64_t M, const MmAct& act, int weight_dt) {
+    if (act.K % 256 || M < 1 || M > act.Mp || act.Mp % MM_TOK || ldx % 4 || ((uintptr_t)x & 15))
         return hipErrorInvalidValue;
-    hipLaunchKernelGGL(k_mm_prep, dim3((unsigned)act.Mp), dim3(256), 0, st, x, ldx, normw, eps,
-                       act.K, (int)M, act.xh, act.xl, act.sh, act.sl);
+    hipLaunchKernelGGL(k_mm_prep, dim3((unsigned)act.Mp, (unsigned)((act.K + 1023) / 1024)),
+                       dim3(256), 0, st, x, ldx, normw, eps,
+                       act.K, (int)M, weight_dt == FTX_Q4_0_PLANAR ? 1 : 0, act.xh, act.xl,
+                       act.sh, act.sl);
     return hipGetLastError();
 }
 
@@ -730,12 +813,13 @@ static MmOutDev out_dev(const MmOut& o) {
 }
 
 // split count for `tiles` workgroups over `steps` contraction steps: none
-// when the tiles fill the device, else about two workgroups per CU, at least
-// two steps per split
+// when the tiles fill the device, else as many as one workgroup per CU
+// allows (the kernels hold one workgroup per CU), at least two steps per
+// split
 static int mm_splits(int64_t tiles, int64_t steps, int cu_count) {
     const int64_t cus = cu_count > 0 ? cu_count : 256;
     if (tiles < 1 || tiles >= cus) return 1;
-    int64_t S = (2 * cus + tiles - 1) / tiles;
+    int64_t S = cus / tiles;
     if (S > steps / 2) S = steps / 2;
     if (S > 32) S = 32;
     return S < 1 ? 1 : (int)S;
@@ -798,12 +882,20 @@ hipError_t launch_mm(hipStream_t st, const MmSeg* segs, int nseg, const MmAct& a
     a.sb_per_split = (a.nsb + S - 1) / S;
     S = (a.nsb + a.sb_per_split - 1) / a.sb_per_split;
     const dim3 grid((unsigned)wg, (unsigned)mt, (unsigned)S);
-    if (dt == FTX_Q4_K)
-        hipLaunchKernelGGL(k_mm<FTX_Q4_K>, grid, dim3(64 * MM_WAVES), 0, st, a);
-    else if (dt == FTX_Q8_0_PLANAR)
-        hipLaunchKernelGGL(k_mm<FTX_Q8_0_PLANAR>, grid, dim3(64 * MM_WAVES), 0, st, a);
-    else
-        hipLaunchKernelGGL(k_mm<FTX_Q4_0_PLANAR>, grid, dim3(64 * MM_WAVES), 0, st, a);
+    constexpr size_t lds = 2 * 65536;
+    using K_t = void (*)(MmArgs);
+    const K_t kern = dt == FTX_Q4_K          ? k_mm<FTX_Q4_K>
+                     : dt == FTX_Q8_0_PLANAR ? k_mm<FTX_Q8_0_PLANAR>
+                                             : k_mm<FTX_Q4_0_PLANAR>;
+    static bool lds_set[3] = {false, false, false};
+    const int ki = dt == FTX_Q4_K ? 0 : (dt == FTX_Q8_0_PLANAR ? 1 : 2);
+    if (!lds_set[ki]) {
+        hipError_t e = hipFuncSetAttribute((const void*)kern,
+                                           hipFuncAttributeMaxDynamicSharedMemorySize, (int)lds);
+        if (e != hipSuccess) return e;
+        lds_set[ki] = true;
+    }
+    hipLaunchKernelGGL(kern, grid, dim3(64 * MM_WAVES), lds, st, a);
     hipError_t e = hipGetLastError();
     if (e != hipSuccess || !via_part) return e;
     MmReduceArgs r{};
@@ -851,7 +943,7 @@ hipError_t launch_mm_down(hipStream_t st, const uint8_t* tiled, int64_t n_in, in
     } else {
         a.out = out_dev(out);
     }
-    hipLaunchKernelGGL(k_mm_down, dim3((unsigned)nb, (unsigned)mt, (unsigned)S), dim3(64 * MM_WAVES),
+    hipLaunchKernelGGL(k_mm_down, dim3((unsigned)nb, (unsigned)mt, (unsigned)S), dim3(64 * MMD_WAVES),
                        0, st, a);
     hipError_t e = hipGetLastError();
     if (e != hipSuccess || S == 1) return e;

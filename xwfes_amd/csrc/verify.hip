@@ -239,10 +239,37 @@ static int verify_large(ftx_ctx* ctx, ftx_model* m, const ftx_seq_args* sq, int6
         if (all) {
             const MmAct act = mm_act(m->mm_act, mm_pad_tokens(Mr), K);
             TRACED_L(TK_XQ_PREP, Mr * K * f4 + 4.0 * mm_pad_tokens(Mr) * K,
-                     launch_mm_prep(st, xin, ldx, normw, eps, Mr, act));
+                     launch_mm_prep(st, xin, ldx, normw, eps, Mr, act, sg[0].dt));
             TRACED_L(kind, bytes,
                      launch_mm(st, sg, nseg, act, Mr, epi, out, m->mm_part, m->mm_part_n,
                                ctx->cu_count));
+            return FTX_OK;
+        }
+        // tiled K-quants the one-pass kernels do not take (Q6_K): the
+        // row-dot MFMA kernel on 8-row chunks (one activation prep for all)
+        bool tiled_all = mv_all(ts, nseg, K, 8) && (epi != EPI_SWIGLU || mv_swiglu_supported(K));
+        for (int i = 0; tiled_all && i < nseg; ++i) tiled_all = m->mvt[idx[i]] != nullptr;
+        if (tiled_all) {
+            auto chunks = [&]() -> hipError_t {
+                hipError_t e = launch_xq_prep(st, (float*)xin, ldx, normw, nullptr, 0, D, K, Mr, m->xq);
+                if (e != hipSuccess) return e;
+                for (int64_t c0 = 0; c0 < Mr; c0 += 8) {
+                    const int64_t mc = Mr - c0 < 8 ? Mr - c0 : 8;
+                    GemvSeg cs[3];
+                    for (int i = 0; i < nseg; ++i) {
+                        cs[i] = gs[i];
+                        cs[i].W = m->mvt[idx[i]];
+                        cs[i].tiled = 1;
+                        cs[i].rpt = m->mvt_rpt[idx[i]];
+                        if (cs[i].y) cs[i].y += c0 * cs[i].ldy;
+                    }
+                    e = launch_mv(st, cs, nseg, m->xq + (c0 / 8) * (int64_t)xq_chunk_bytes(K), K, mc,
+                                  epi, ctx->cu_count, normw != nullptr, eps, nullptr);
+                    if (e != hipSuccess) return e;
+                }
+                return hipSuccess;
+            };
+            TRACED_L(kind, bytes, chunks());
             return FTX_OK;
         }
         bool pl_all = true;
