@@ -100,6 +100,31 @@ enum {
     ORC_LAYER_TENSORS = 9
 };
 
+/* optional per-layer tensors (data == NULL: absent), in
+ * orc_model.ext[l*ORC_LAYER_EXT + i]:
+ *   attention bias added after the q / k / v projections and per-head
+ *   RMSNorm of q and k (src/engine.cpp:519-542, loaded at 325-332);
+ *   the MoE FFN (src/engine.cpp:179-258, loaded at 348-369): the router
+ *   (n_expert rows of n_embd), its optional bias, the experts' gate / up /
+ *   down planes (n_expert planes of n_ff rows x n_embd cols, down in the
+ *   reference orientation) and an optional shared expert */
+enum {
+    ORC_X_Q_BIAS = 0,
+    ORC_X_K_BIAS = 1,
+    ORC_X_V_BIAS = 2,
+    ORC_X_Q_NORM = 3,
+    ORC_X_K_NORM = 4,
+    ORC_X_GATE_INP = 5,
+    ORC_X_GATE_EXPS = 6,
+    ORC_X_UP_EXPS = 7,
+    ORC_X_DOWN_EXPS = 8,
+    ORC_X_ROUTER_BIAS = 9,
+    ORC_X_GATE_SH = 10,
+    ORC_X_UP_SH = 11,
+    ORC_X_DOWN_SH = 12,
+    ORC_LAYER_EXT = 13
+};
+
 typedef struct {
     int64_t n_layer, n_embd, n_head, n_head_kv, head_dim, n_ff, vocab;
     float rms_eps;
@@ -109,7 +134,24 @@ typedef struct {
     orc_tensor out_norm;
     orc_tensor output; /* data == NULL -> tied to tok_embd */
     const orc_tensor* layers;
+    const orc_tensor* ext;  /* NULL or n_layer * ORC_LAYER_EXT */
+    int64_t n_expert, n_expert_used;  /* a layer with a router runs the MoE FFN */
 } orc_model;
+
+/* one expert's SwiGLU FFN, out[S][K] += ...; h1 / h2 scratch of S*F floats
+ * or NULL (src/cpu_backend.cpp:106-149 over all F neurons) */
+void orc_expert_ffn(const float* x, int64_t S, int64_t K, const uint8_t* gate, const uint8_t* up,
+                    int gu_dt, const uint8_t* down, int down_dt, int64_t F, float* out,
+                    float* h1, float* h2);
+
+/* MoE routing of M router rows [M][E] (src/engine.cpp:197-217): the row
+ * plus the optional bias, softmax_inplace, the top U by value (ties: lower
+ * expert index), weights renormalised by their float sum; experts listed in
+ * first-use order over (token, rank).  out_e / out_w [M*U]: expert and
+ * weight of (token m, rank u); used [E], n_used: the first-use order.
+ * router is modified in place (the probabilities). */
+void orc_moe_route(float* router, int64_t M, int64_t E, int64_t U, const float* bias,
+                   int32_t* out_e, float* out_w, int32_t* used, int32_t* n_used);
 
 /* KV cache element type for orc_forward */
 enum { ORC_KV_F32 = 0, ORC_KV_F16 = 1 };

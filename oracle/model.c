@@ -132,6 +132,167 @@ static float* vec_f32(const orc_tensor* t, int64_t n) {
     return v;
 }
 
+static const orc_tensor* ext_of(const orc_model* md, int64_t l, int i) {
+    if (!md->ext) return NULL;
+    const orc_tensor* t = md->ext + l * ORC_LAYER_EXT + i;
+    return t->data ? t : NULL;
+}
+
+/* src/engine.cpp:197-217 */
+void orc_moe_route(float* router, int64_t M, int64_t E, int64_t U, const float* bias,
+                   int32_t* out_e, float* out_w, int32_t* used, int32_t* n_used) {
+    int32_t* first = (int32_t*)malloc((size_t)E * sizeof(int32_t));
+    for (int64_t e = 0; e < E; ++e) first[e] = 0;
+    *n_used = 0;
+    for (int64_t m = 0; m < M; ++m) {
+        float* r = router + m * E;
+        if (bias)
+            for (int64_t j = 0; j < E; ++j) r[j] += bias[j];
+        orc_softmax_inplace(r, E);
+        /* the U largest in descending order, a tie to the lower index: the
+         * order std::partial_sort gives for distinct values */
+        int32_t* top = out_e + m * U;
+        for (int64_t u = 0; u < U; ++u) {
+            int32_t best = -1;
+            for (int64_t j = 0; j < E; ++j) {
+                int taken = 0;
+                for (int64_t v = 0; v < u; ++v) taken |= top[v] == j;
+                if (taken) continue;
+                if (best < 0 || r[j] > r[best]) best = (int32_t)j;
+            }
+            top[u] = best;
+        }
+        float wsum = 0.f;
+        for (int64_t u = 0; u < U; ++u) wsum += r[top[u]];
+        const float inv = wsum > 0 ? 1.f / wsum : 0.f;
+        for (int64_t u = 0; u < U; ++u) {
+            out_w[m * U + u] = r[top[u]] * inv;
+            if (!first[top[u]]) {
+                first[top[u]] = 1;
+                used[(*n_used)++] = top[u];
+            }
+        }
+    }
+    free(first);
+}
+
+/* one expert's SwiGLU FFN over S rows: out[S][K] += down^T (silu(x gate^T)
+ * * (x up^T)); gate / up are F rows of K, down F rows of K (reference
+ * orientation).  The reference runs it in windows of neurons
+ * (include/ft/chunker.h:32-77, src/cpu_backend.cpp:106-149) whose down rows
+ * add in ascending order, so one pass over all F gives the same sums.
+ * h1 / h2: scratch of S*F floats each (NULL: allocated here). */
+void orc_expert_ffn(const float* x, int64_t S, int64_t K, const uint8_t* gate, const uint8_t* up,
+                    int gu_dt, const uint8_t* down, int down_dt, int64_t F, float* out,
+                    float* h1, float* h2) {
+    float* a = h1 ? h1 : (float*)malloc((size_t)(S * F) * sizeof(float));
+    float* b = h2 ? h2 : (float*)malloc((size_t)(S * F) * sizeof(float));
+    orc_matmul(x, S, K, gate, gu_dt, F, a);
+    orc_matmul(x, S, K, up, gu_dt, F, b);
+    for (int64_t i = 0; i < S * F; ++i) {
+        float g = a[i];
+        g = g / (1.f + expf(-g));
+        a[i] = g * b[i];
+    }
+    orc_down_axpy(a, S, F, down, down_dt, K, out);
+    if (!h1) free(a);
+    if (!h2) free(b);
+}
+
+/* src/engine.cpp:179-258: router, per-expert SwiGLU FFN over the expert's
+ * rows (ExpertStreamer windows add the down rows in ascending order, which a
+ * single pass reproduces, include/ft/chunker.h:32-89 and
+ * src/cpu_backend.cpp:106-149), the weighted sum into tmpo in first-use
+ * order, then the optional shared expert */
+static void moe_ffn(const orc_model* md, int64_t l, const float* xn, int64_t M, float* tmpo) {
+    const int64_t K = md->n_embd, E = md->n_expert;
+    const int64_t U = md->n_expert_used < E ? md->n_expert_used : E;
+    const orc_tensor* gi = ext_of(md, l, ORC_X_GATE_INP);
+    const orc_tensor* ge = ext_of(md, l, ORC_X_GATE_EXPS);
+    const orc_tensor* ue = ext_of(md, l, ORC_X_UP_EXPS);
+    const orc_tensor* de = ext_of(md, l, ORC_X_DOWN_EXPS);
+    const orc_tensor* rb = ext_of(md, l, ORC_X_ROUTER_BIAS);
+    const int64_t F = ge->ne1 / E;  /* rows per expert plane */
+    float* router = (float*)malloc((size_t)(M * E) * sizeof(float));
+    orc_matmul(xn, M, K, gi->data, gi->dtype, E, router);
+    float* bias = rb ? vec_f32(rb, E) : NULL;
+    int32_t* te = (int32_t*)malloc((size_t)(M * U) * sizeof(int32_t));
+    float* tw = (float*)malloc((size_t)(M * U) * sizeof(float));
+    int32_t* used = (int32_t*)malloc((size_t)E * sizeof(int32_t));
+    int32_t n_used = 0;
+    orc_moe_route(router, M, E, U, bias, te, tw, used, &n_used);
+    float* xe = (float*)malloc((size_t)(M * K) * sizeof(float));
+    float* acb = (float*)malloc((size_t)(M * K) * sizeof(float));
+    float* h1 = (float*)malloc((size_t)(M * F) * sizeof(float));
+    float* h2 = (float*)malloc((size_t)(M * F) * sizeof(float));
+    int64_t* rows_m = (int64_t*)malloc((size_t)M * sizeof(int64_t));
+    float* rows_w = (float*)malloc((size_t)M * sizeof(float));
+    const int64_t gstride = orc_row_bytes(ge->dtype, K) * F;
+    const int64_t ustride = orc_row_bytes(ue->dtype, K) * F;
+    const int64_t dstride = orc_row_bytes(de->dtype, K) * F;
+    for (int32_t ui = 0; ui < n_used; ++ui) {
+        const int32_t e = used[ui];
+        int64_t S = 0;
+        for (int64_t m = 0; m < M; ++m)
+            for (int64_t u = 0; u < U; ++u)
+                if (te[m * U + u] == e) {
+                    rows_m[S] = m;
+                    rows_w[S] = tw[m * U + u];
+                    memcpy(xe + S * K, xn + m * K, (size_t)K * sizeof(float));
+                    ++S;
+                }
+        memset(acb, 0, (size_t)(S * K) * sizeof(float));
+        orc_expert_ffn(xe, S, K, ge->data + gstride * e, ue->data + ustride * e, ge->dtype,
+                       de->data + dstride * e, de->dtype, F, acb, h1, h2);
+        for (int64_t si = 0; si < S; ++si) {
+            float* trow = tmpo + rows_m[si] * K;
+            const float* arow = acb + si * K;
+            for (int64_t j = 0; j < K; ++j) trow[j] += rows_w[si] * arow[j];
+        }
+    }
+    const orc_tensor* sg = ext_of(md, l, ORC_X_GATE_SH);
+    const orc_tensor* su = ext_of(md, l, ORC_X_UP_SH);
+    const orc_tensor* sd = ext_of(md, l, ORC_X_DOWN_SH);
+    if (sg && su && sd)
+        orc_expert_ffn(xn, M, K, sg->data, su->data, sg->dtype, sd->data, sd->dtype, sg->ne1,
+                       tmpo, NULL, NULL);
+    free(router); free(bias); free(te); free(tw); free(used); free(xe); free(acb);
+    free(h1); free(h2); free(rows_m); free(rows_w);
+}
+
+/* src/engine.cpp:519-542: bias on q / k / v, then RMSNorm of every head of q
+ * and of k with the norm vector of head_dim */
+static void attn_extras(const orc_model* md, int64_t l, int64_t M, float* q, float* kb, float* vb) {
+    const int64_t hd = md->head_dim, nh = md->n_head, dk = md->n_head_kv * hd;
+    const orc_tensor* bq = ext_of(md, l, ORC_X_Q_BIAS);
+    const orc_tensor* bk = ext_of(md, l, ORC_X_K_BIAS);
+    const orc_tensor* bv = ext_of(md, l, ORC_X_V_BIAS);
+    const orc_tensor* nq = ext_of(md, l, ORC_X_Q_NORM);
+    const orc_tensor* nk = ext_of(md, l, ORC_X_K_NORM);
+    float* buf[3] = {q, kb, vb};
+    const orc_tensor* bias[3] = {bq, bk, bv};
+    const int64_t dim[3] = {nh * hd, dk, dk};
+    for (int b = 0; b < 3; ++b) {
+        if (!bias[b]) continue;
+        float* bv32 = vec_f32(bias[b], dim[b]);
+        for (int64_t m = 0; m < M; ++m)
+            for (int64_t j = 0; j < dim[b]; ++j) buf[b][m * dim[b] + j] += bv32[j];
+        free(bv32);
+    }
+    const orc_tensor* nrm[2] = {nq, nk};
+    const int64_t heads[2] = {nh, md->n_head_kv};
+    for (int b = 0; b < 2; ++b) {
+        if (!nrm[b]) continue;
+        float* w = vec_f32(nrm[b], hd);
+        for (int64_t m = 0; m < M; ++m)
+            for (int64_t h = 0; h < heads[b]; ++h) {
+                float* v = buf[b] + (m * heads[b] + h) * hd;
+                orc_rms_norm(v, v, w, hd, md->rms_eps);
+            }
+        free(w);
+    }
+}
+
 int orc_forward(const orc_model* md, void* kc, void* vc, int kv_dt, int64_t cap,
                 int64_t npast, const int32_t* toks, int64_t M,
                 const int32_t* parents, int layer_limit, float* logits) {
@@ -182,6 +343,7 @@ int orc_forward(const orc_model* md, void* kc, void* vc, int kv_dt, int64_t cap,
         orc_matmul(xn, M, K, T[ORC_T_Q].data, T[ORC_T_Q].dtype, nh * hd, q);
         orc_matmul(xn, M, K, T[ORC_T_K].data, T[ORC_T_K].dtype, dk, kb);
         orc_matmul(xn, M, K, T[ORC_T_V].data, T[ORC_T_V].dtype, dk, vb);
+        attn_extras(md, l, M, q, kb, vb);
         /* src/engine.cpp:544-551, position = npast + depth */
         for (int64_t m = 0; m < M; ++m) {
             for (int64_t h = 0; h < nh; ++h)
@@ -231,16 +393,20 @@ int orc_forward(const orc_model* md, void* kc, void* vc, int kv_dt, int64_t cap,
         float* fn = vec_f32(&T[ORC_T_FFN_NORM], K);
         for (int64_t m = 0; m < M; ++m) orc_rms_norm(xn + m * K, x + m * K, fn, K, md->rms_eps);
         free(fn);
-        /* dense FFN, src/engine.cpp:260-276 */
-        orc_matmul(xn, M, K, T[ORC_T_GATE].data, T[ORC_T_GATE].dtype, F, h1);
-        orc_matmul(xn, M, K, T[ORC_T_UP].data, T[ORC_T_UP].dtype, F, h2);
-        for (int64_t i = 0; i < M * F; ++i) {
-            float g = h1[i];
-            g = g / (1.f + expf(-g));
-            h1[i] = g * h2[i];
-        }
         memset(tmpo, 0, (size_t)(M * K) * sizeof(float));
-        orc_down_axpy(h1, M, F, T[ORC_T_DOWN].data, T[ORC_T_DOWN].dtype, K, tmpo);
+        if (ext_of(md, l, ORC_X_GATE_INP)) {
+            moe_ffn(md, l, xn, M, tmpo);
+        } else {
+            /* dense FFN, src/engine.cpp:260-276 */
+            orc_matmul(xn, M, K, T[ORC_T_GATE].data, T[ORC_T_GATE].dtype, F, h1);
+            orc_matmul(xn, M, K, T[ORC_T_UP].data, T[ORC_T_UP].dtype, F, h2);
+            for (int64_t i = 0; i < M * F; ++i) {
+                float g = h1[i];
+                g = g / (1.f + expf(-g));
+                h1[i] = g * h2[i];
+            }
+            orc_down_axpy(h1, M, F, T[ORC_T_DOWN].data, T[ORC_T_DOWN].dtype, K, tmpo);
+        }
         for (int64_t i = 0; i < M * K; ++i) x[i] += tmpo[i];
     }
     /* final norm and LM head (tied to tok_embd when output is absent),

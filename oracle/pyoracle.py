@@ -26,6 +26,11 @@ BLOCK = {F32: (1, 4), F16: (1, 2), BF16: (1, 2), Q4_0: (32, 18), Q4_1: (32, 20),
 ACCEPT_GREEDY, ACCEPT_RATIO, ACCEPT_RESIDUAL = 0, 1, 2
 KV_F32, KV_F16 = 0, 1
 LAYER_TENSORS = ("attn_norm", "q", "k", "v", "o", "ffn_norm", "gate", "up", "down")
+# optional per-layer roles, in the order of orc_model.ext (ftx_oracle.h):
+# attention bias and per-head q / k norms, the MoE router, the experts'
+# planes (ne1 = n_expert * rows of one plane), router bias, shared expert
+LAYER_EXT = ("q_bias", "k_bias", "v_bias", "q_norm", "k_norm", "gate_inp", "gate_exps",
+             "up_exps", "down_exps", "router_bias", "gate_sh", "up_sh", "down_sh")
 
 _fp = C.POINTER(C.c_float)
 _u8p = C.POINTER(C.c_uint8)
@@ -66,7 +71,9 @@ class _ModelC(C.Structure):
                 ("n_head_kv", C.c_int64), ("head_dim", C.c_int64), ("n_ff", C.c_int64),
                 ("vocab", C.c_int64), ("rms_eps", C.c_float), ("rope_neox", C.c_int32),
                 ("rope_theta", C.c_double), ("tok_embd", _TensorC), ("out_norm", _TensorC),
-                ("output", _TensorC), ("layers", C.POINTER(_TensorC))]
+                ("output", _TensorC), ("layers", C.POINTER(_TensorC)),
+                ("ext", C.POINTER(_TensorC)), ("n_expert", C.c_int64),
+                ("n_expert_used", C.c_int64)]
 
 
 class Oracle:
@@ -90,6 +97,10 @@ class Oracle:
         L.orc_rms_norm.argtypes = [_fp, _fp, _fp, C.c_int64, C.c_float]
         L.orc_rope_vec.argtypes = [_fp, C.c_int64, C.c_int64, C.c_double, C.c_int]
         L.orc_softmax_inplace.argtypes = [_fp, C.c_int64]
+        L.orc_expert_ffn.argtypes = [_fp, C.c_int64, C.c_int64, C.c_void_p, C.c_void_p, C.c_int,
+                                     C.c_void_p, C.c_int, C.c_int64, _fp, _fp, _fp]
+        L.orc_moe_route.argtypes = [_fp, C.c_int64, C.c_int64, C.c_int64, _fp, _i32p, _fp, _i32p,
+                                    _i32p]
         L.orc_forward.argtypes = [C.POINTER(_ModelC), C.c_void_p, C.c_void_p, C.c_int, C.c_int64,
                                   C.c_int64, _i32p, C.c_int64, _i32p, C.c_int, _fp]
         L.orc_rng_next.restype = C.c_uint64
@@ -179,6 +190,29 @@ class Oracle:
         v = np.ascontiguousarray(v, np.float32).copy()
         self.lib.orc_rope_vec(_ptr(v, _fp), v.size, pos, theta, int(neox))
         return v
+
+    def expert_ffn(self, x, gate, up, gu_dt, down, down_dt, F, out=None):
+        """One expert's SwiGLU FFN over the rows of x: out [S][K] + the FFN."""
+        x = np.ascontiguousarray(x, np.float32)
+        S, K = x.shape
+        y = np.zeros((S, K), np.float32) if out is None else np.array(out, np.float32)
+        self.lib.orc_expert_ffn(_ptr(x, _fp), S, K, gate.ctypes.data, up.ctypes.data, gu_dt,
+                                down.ctypes.data, down_dt, F, _ptr(y, _fp), None, None)
+        return y
+
+    def moe_route(self, router, U, bias=None):
+        """Routing of router rows [M][E]: (probabilities [M][E], experts
+        [M][U], weights [M][U], experts in first-use order)."""
+        r = np.ascontiguousarray(router, np.float32).copy()
+        M, E = r.shape
+        te = np.empty((M, U), np.int32)
+        tw = np.empty((M, U), np.float32)
+        used = np.empty(E, np.int32)
+        n = C.c_int32(0)
+        b = None if bias is None else np.ascontiguousarray(bias, np.float32)
+        self.lib.orc_moe_route(_ptr(r, _fp), M, E, U, None if b is None else _ptr(b, _fp),
+                               _ptr(te, _i32p), _ptr(tw, _fp), _ptr(used, _i32p), C.byref(n))
+        return r, te, tw, used[:n.value].copy()
 
     def softmax(self, p):
         p = np.ascontiguousarray(p, np.float32).copy()
@@ -316,15 +350,25 @@ class Oracle:
             keep.append(t["raw"])
             return _TensorC(t["raw"].ctypes.data, t["dtype"], 0, t["ne0"], t["ne1"])
 
-        lay = (_TensorC * (cfg["n_layer"] * 9))()
-        for l in range(cfg["n_layer"]):
+        def opt(name):
+            return tc(name) if name in model else _TensorC(None, 0, 0, 0, 0)
+
+        nl, nt, nx = cfg["n_layer"], len(LAYER_TENSORS), len(LAYER_EXT)
+        lay = (_TensorC * (nl * nt))()
+        ext = (_TensorC * (nl * nx))()
+        has_ext = False
+        for l in range(nl):
             for i, nm in enumerate(LAYER_TENSORS):
-                lay[l * 9 + i] = tc("blk.%d.%s" % (l, nm))
-        out_t = tc("output") if "output" in model else _TensorC(None, 0, 0, 0, 0)
+                lay[l * nt + i] = opt("blk.%d.%s" % (l, nm))
+            for i, nm in enumerate(LAYER_EXT):
+                ext[l * nx + i] = opt("blk.%d.%s" % (l, nm))
+                has_ext |= ("blk.%d.%s" % (l, nm)) in model
         md = _ModelC(cfg["n_layer"], cfg["n_embd"], cfg["n_head"], cfg["n_head_kv"],
                      cfg["head_dim"], cfg["n_ff"], cfg["vocab"], cfg.get("rms_eps", 1e-5),
                      int(cfg.get("rope_neox", 0)), cfg.get("rope_theta", 10000.0),
-                     tc("tok_embd"), tc("out_norm"), out_t, lay)
+                     tc("tok_embd"), tc("out_norm"), opt("output"), lay,
+                     ext if has_ext else None, cfg.get("n_expert", 0),
+                     cfg.get("n_expert_used", 0))
         toks = np.ascontiguousarray(toks, np.int32)
         M = toks.size
         par = None if parents is None else np.ascontiguousarray(parents, np.int32)
@@ -437,6 +481,8 @@ class Ref:
         L.ref_accept_chain_greedy.argtypes = [_fp, _fp, C.c_int64, _i32p, C.c_int64]
         L.ref_accept_chain_sampling.argtypes = [_fp, _fp, _fp, C.c_int64, _i32p, C.c_int64,
                                                 C.c_float, _u64p]
+        L.ref_expert_stream.argtypes = [_fp, C.c_int64, C.c_int64, C.c_void_p, C.c_void_p,
+                                        C.c_void_p, C.c_int, C.c_int64, C.c_int64, _fp]
         L.ref_engine_load.restype = C.c_void_p
         L.ref_engine_load.argtypes = [C.c_char_p, C.c_int, C.c_int64]
         L.ref_engine_free.argtypes = [C.c_void_p]
@@ -509,6 +555,16 @@ class Ref:
                                                C.byref(s))
         return a, s.value
 
+    def expert_stream(self, x, gate, up, down, dtype, F, chunk, out=None):
+        """ExpertStreamer::run of one expert (F rows of K each) in windows of
+        `chunk` neurons; returns out [M][K] + the FFN."""
+        x = np.ascontiguousarray(x, np.float32)
+        M, K = x.shape
+        y = np.zeros((M, K), np.float32) if out is None else np.array(out, np.float32)
+        self.lib.ref_expert_stream(_ptr(x, _fp), M, K, gate.ctypes.data, up.ctypes.data,
+                                   down.ctypes.data, dtype, F, chunk, _ptr(y, _fp))
+        return y
+
     def engine_load(self, path, threads=1, ctx_len=0):
         h = self.lib.ref_engine_load(path.encode(), threads, ctx_len)
         assert h, "reference Engine failed to load " + path
@@ -556,41 +612,66 @@ class Ref:
 # ---------------- synthetic models (test data) ----------------
 
 def model_cfg(n_layer, n_embd, n_head, n_head_kv, head_dim, n_ff, vocab, rope_theta=10000.0,
-              rope_neox=0, rms_eps=1e-5):
+              rope_neox=0, rms_eps=1e-5, n_expert=0, n_expert_used=0):
+    """n_expert > 0 makes every layer a MoE layer of n_expert experts of
+    n_ff rows each, n_expert_used routed per token."""
     return dict(n_layer=n_layer, n_embd=n_embd, n_head=n_head, n_head_kv=n_head_kv,
                 head_dim=head_dim, n_ff=n_ff, vocab=vocab, rope_theta=rope_theta,
-                rope_neox=rope_neox, rms_eps=rms_eps)
+                rope_neox=rope_neox, rms_eps=rms_eps, n_expert=n_expert,
+                n_expert_used=n_expert_used)
 
 
-def tensor_shapes(cfg):
+def tensor_shapes(cfg, extras=()):
     """(name, ne0 cols, ne1 rows) of every tensor; down uses the reference
-    orientation (n_ff rows of n_embd cols)."""
-    d, hd = cfg["n_embd"], cfg["head_dim"]
+    orientation (n_ff rows of n_embd cols).  A MoE config (n_expert > 0)
+    has the router and the experts' planes (ne1 = n_expert * n_ff) instead
+    of the dense FFN; extras adds optional roles of LAYER_EXT (attention
+    bias, q / k norms, router bias, a shared expert of n_ff rows)."""
+    d, hd, F = cfg["n_embd"], cfg["head_dim"], cfg["n_ff"]
     qd, kd = cfg["n_head"] * hd, cfg["n_head_kv"] * hd
+    E = cfg.get("n_expert", 0)
+    ext = {"q_bias": (qd, 1), "k_bias": (kd, 1), "v_bias": (kd, 1), "q_norm": (hd, 1),
+           "k_norm": (hd, 1), "router_bias": (E, 1), "gate_sh": (d, F), "up_sh": (d, F),
+           "down_sh": (d, F)}
     out = [("tok_embd", d, cfg["vocab"]), ("out_norm", d, 1), ("output", d, cfg["vocab"])]
     for l in range(cfg["n_layer"]):
         p = "blk.%d." % l
         out += [(p + "attn_norm", d, 1), (p + "q", d, qd), (p + "k", d, kd), (p + "v", d, kd),
-                (p + "o", qd, d), (p + "ffn_norm", d, 1), (p + "gate", d, cfg["n_ff"]),
-                (p + "up", d, cfg["n_ff"]), (p + "down", d, cfg["n_ff"])]
+                (p + "o", qd, d), (p + "ffn_norm", d, 1)]
+        if E:
+            out += [(p + "gate_inp", d, E), (p + "gate_exps", d, E * F),
+                    (p + "up_exps", d, E * F), (p + "down_exps", d, E * F)]
+        else:
+            out += [(p + "gate", d, F), (p + "up", d, F), (p + "down", d, F)]
+        out += [(p + x, ext[x][0], ext[x][1]) for x in extras]
     return out
 
 
-def make_model(orc, cfg, dtypes, seed=1, std=0.02, tied=False):
+def make_model(orc, cfg, dtypes, seed=1, std=0.02, tied=False, extras=()):
     """Random-init model: weights N(0, std) quantised to dtypes[name-suffix]
-    (keys: 'tok_embd', 'output', 'q', 'k', 'v', 'o', 'gate', 'up', 'down';
-    norms are F32 vectors of 1 + 0.3 N(0, 1), different per layer and role)."""
+    (keys: 'tok_embd', 'output', 'q', 'k', 'v', 'o', 'gate', 'up', 'down',
+    and for MoE 'gate_inp', 'gate_exps', 'up_exps', 'down_exps', and the
+    extras' matrices 'gate_sh', 'up_sh', 'down_sh'); norms (also q_norm /
+    k_norm) are F32 vectors of 1 + 0.3 N(0, 1), different per layer and
+    role; biases are F32 N(0, 0.5) (router bias N(0, 1)).  The router
+    weights are N(0, 1) so the routing differs from token to token."""
     rng = np.random.default_rng(seed)
     model = {"cfg": dict(cfg)}
-    for name, ne0, ne1 in tensor_shapes(cfg):
+    for name, ne0, ne1 in tensor_shapes(cfg, extras):
         if name == "output" and tied:
             continue
         key = name.split(".")[-1]
-        if key in ("attn_norm", "ffn_norm", "out_norm"):
+        if key in ("attn_norm", "ffn_norm", "out_norm", "q_norm", "k_norm"):
             w = (1.0 + 0.3 * rng.standard_normal(ne0)).astype(np.float32)
             model[name] = dict(raw=w.view(np.uint8).copy(), dtype=F32, ne0=ne0, ne1=1)
             continue
+        if key.endswith("bias"):
+            sd = 1.0 if key == "router_bias" else 0.5
+            w = (sd * rng.standard_normal(ne0)).astype(np.float32)
+            model[name] = dict(raw=w.view(np.uint8).copy(), dtype=F32, ne0=ne0, ne1=1)
+            continue
         dt = dtypes[key]
-        w = (rng.standard_normal((ne1, ne0)) * std).astype(np.float32)
+        sd = 1.0 if key == "gate_inp" else std
+        w = (rng.standard_normal((ne1, ne0)) * sd).astype(np.float32)
         model[name] = dict(raw=orc.quantize(w, dt), dtype=dt, ne0=ne0, ne1=ne1)
     return model

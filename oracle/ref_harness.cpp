@@ -9,6 +9,7 @@
 #include "ft/engine.h"
 #include "ft/gguf.h"
 #include "ft/graph.h"
+#include "ft/chunker.h"
 
 #include <algorithm>
 #include <cstdint>
@@ -76,6 +77,18 @@ int ref_accept_chain_sampling(const float* base, const float* rows,
                               const float* pd, int64_t V, const int32_t* props,
                               int64_t k, float temp, uint64_t* rng) {
     return accept_chain_sampling(base, rows, pd, V, props, k, temp, *rng);
+}
+
+// One expert's FFN through ExpertStreamer::run (include/ft/chunker.h:32-77)
+// on a one-thread CpuBackend with `chunk` neurons per window: out[M][K] +=.
+// gate / up / down: F rows of K columns of dtype dt.
+void ref_expert_stream(const float* x, int64_t M, int64_t K, const void* gate, const void* up,
+                       const void* down, int dtype, int64_t F, int64_t chunk, float* out) {
+    CpuBackend cpu(1);
+    StreamerConfig sc;
+    sc.chunk_neurons = chunk;
+    ExpertStreamer st(cpu, sc);
+    st.run(x, M, K, view(gate, dtype, K, F), view(up, dtype, K, F), view(down, dtype, K, F), out);
 }
 
 // Engine: load a GGUF, run steps, copy the logits row out.

@@ -451,6 +451,9 @@ def model_kv(cfg, arch="llama", tokens=None, float_eps=True):
           (a + ".rope.freq_base", T_F32, float(cfg["rope_theta"]))]
     if float_eps:
         kv.append((a + ".attention.layer_norm_rms_epsilon", T_F32, float(cfg["rms_eps"])))
+    if cfg.get("n_expert"):
+        kv.append((a + ".expert_count", T_U32, cfg["n_expert"]))
+        kv.append((a + ".expert_used_count", T_U32, cfg["n_expert_used"]))
     if tokens is None:
         tokens = ["<t%d>" % i for i in range(cfg["vocab"])]
     kv.append(("tokenizer.ggml.model", T_STR, "llama"))
@@ -461,13 +464,24 @@ def model_kv(cfg, arch="llama", tokens=None, float_eps=True):
 # model-dict role -> GGUF tensor name (the llama.cpp names)
 GGUF_NAMES = {"attn_norm": "attn_norm.weight", "q": "attn_q.weight", "k": "attn_k.weight",
               "v": "attn_v.weight", "o": "attn_output.weight", "ffn_norm": "ffn_norm.weight",
-              "gate": "ffn_gate.weight", "up": "ffn_up.weight", "down": "ffn_down.weight"}
+              "gate": "ffn_gate.weight", "up": "ffn_up.weight", "down": "ffn_down.weight",
+              "q_bias": "attn_q.bias", "k_bias": "attn_k.bias", "v_bias": "attn_v.bias",
+              "q_norm": "attn_q_norm.weight", "k_norm": "attn_k_norm.weight",
+              "gate_inp": "ffn_gate_inp.weight", "gate_exps": "ffn_gate_exps.weight",
+              "up_exps": "ffn_up_exps.weight", "down_exps": "ffn_down_exps.weight",
+              "router_bias": "exp_probs_b.bias", "gate_sh": "ffn_gate_shexp.weight",
+              "up_sh": "ffn_up_shexp.weight", "down_sh": "ffn_down_shexp.weight"}
 
 
-def model_tensor_list(model, embd_3d=True):
+def model_tensor_list(model, embd_3d=True, bias_2d=True):
     """GGUF tensor list of a pyoracle-style model dict (name -> {raw,
     dtype, ne0, ne1}).  embd_3d writes the token embedding as [d, 1, V]
-    (the layout the reference's plane lookup reads as rows)."""
+    (the layout the reference's plane lookup reads as rows).  Expert planes
+    are written as [d, rows, n_expert].  bias_2d writes a bias of n values as
+    [1, n]: the reference takes a bias's length from ne[1]
+    (src/engine.cpp:334-339), which reads a one-dimensional [n] bias as a
+    single value."""
+    E = model["cfg"].get("n_expert", 0)
     out = []
     for name, t in model.items():
         if name == "cfg":
@@ -486,6 +500,10 @@ def model_tensor_list(model, embd_3d=True):
             gname = "blk.%s.%s" % (l, GGUF_NAMES[role])
             if role.endswith("norm"):
                 ne = (t["ne0"],)
+            elif role.endswith("bias"):
+                ne = (1, t["ne0"]) if bias_2d else (t["ne0"],)
+            elif role.endswith("_exps"):
+                ne = (t["ne0"], t["ne1"] // E, E)
         out.append((gname, t["dtype"], ne, np.ascontiguousarray(t["raw"]).tobytes()))
     return out
 
