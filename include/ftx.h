@@ -191,6 +191,33 @@ enum {
     FTX_LAYER_TENSORS = 9
 };
 
+/* optional per-layer tensors in ftx_model_desc.layer_ext[l*FTX_LAYER_EXT + i]
+ * (NULL entries: absent).  Attention: bias vectors added after the q / k / v
+ * projections and RMSNorm weights (head_dim) applied to every head of q and
+ * k before RoPE (src/engine.cpp:519-542, loaded at 325-339).  MoE FFN
+ * (src/engine.cpp:179-258, loaded at 348-369): a layer with a router runs
+ * it instead of the dense FFN (its FTX_T_GATE / UP / DOWN are then NULL):
+ * router n_expert rows of n_embd; expert planes ne = {n_embd, n_ff,
+ * n_expert} (down in the reference orientation, n_ff rows of n_embd per
+ * plane); optional router bias (n_expert) and shared expert (gate / up:
+ * rows of n_embd; down: the same rows, reference orientation). */
+enum {
+    FTX_X_Q_BIAS = 0,
+    FTX_X_K_BIAS = 1,
+    FTX_X_V_BIAS = 2,
+    FTX_X_Q_NORM = 3,
+    FTX_X_K_NORM = 4,
+    FTX_X_GATE_INP = 5,
+    FTX_X_GATE_EXPS = 6,
+    FTX_X_UP_EXPS = 7,
+    FTX_X_DOWN_EXPS = 8,
+    FTX_X_ROUTER_BIAS = 9,
+    FTX_X_GATE_SH = 10,
+    FTX_X_UP_SH = 11,
+    FTX_X_DOWN_SH = 12,
+    FTX_LAYER_EXT = 13
+};
+
 typedef struct {
     int64_t n_layer, n_embd, n_head, n_head_kv, head_dim, n_ff, vocab;
     float rms_eps;     /* the reference always ends up at 1e-5 (src/graph.cpp:42-43) */
@@ -201,6 +228,10 @@ typedef struct {
     const ftx_tensor* output;  /* NULL: tied to tok_embd */
     const ftx_tensor* const* layers;  /* n_layer * FTX_LAYER_TENSORS */
     int64_t max_tokens;  /* largest M a verify step will use (<= 256) */
+    const ftx_tensor* const* layer_ext;  /* NULL or n_layer * FTX_LAYER_EXT */
+    /* MoE layers: experts per layer and experts routed per token
+     * (ModelConfig::n_experts / n_expert_used, src/graph.cpp:48-50) */
+    int64_t n_expert, n_expert_used;
 } ftx_model_desc;
 
 int ftx_model_create(ftx_ctx* ctx, const ftx_model_desc* desc, ftx_model** out);

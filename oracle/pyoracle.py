@@ -654,7 +654,9 @@ def make_model(orc, cfg, dtypes, seed=1, std=0.02, tied=False, extras=()):
     extras' matrices 'gate_sh', 'up_sh', 'down_sh'); norms (also q_norm /
     k_norm) are F32 vectors of 1 + 0.3 N(0, 1), different per layer and
     role; biases are F32 N(0, 0.5) (router bias N(0, 1)).  The router
-    weights are N(0, 1) so the routing differs from token to token."""
+    weights are N(0, 4 / n_embd), router logits of a few units, so that the
+    routing differs from token to token and the second expert's weight is
+    not negligible."""
     rng = np.random.default_rng(seed)
     model = {"cfg": dict(cfg)}
     for name, ne0, ne1 in tensor_shapes(cfg, extras):
@@ -671,7 +673,7 @@ def make_model(orc, cfg, dtypes, seed=1, std=0.02, tied=False, extras=()):
             model[name] = dict(raw=w.view(np.uint8).copy(), dtype=F32, ne0=ne0, ne1=1)
             continue
         dt = dtypes[key]
-        sd = 1.0 if key == "gate_inp" else std
+        sd = 2.0 / np.sqrt(ne0) if key == "gate_inp" else std
         w = (rng.standard_normal((ne1, ne0)) * sd).astype(np.float32)
         model[name] = dict(raw=orc.quantize(w, dt), dtype=dt, ne0=ne0, ne1=ne1)
     return model

@@ -26,6 +26,8 @@ enum TraceKind {
     TK_ROW_STATS,
     TK_ACCEPT,
     TK_XQ_PREP,
+    TK_MOE_ROUTE,
+    TK_MOE_COMBINE,
     TK_COUNT
 };
 
@@ -215,9 +217,11 @@ struct MmOut {
 int64_t mm_pad_tokens(int64_t M);
 size_t mm_act_halves(int64_t Mp, int64_t K);
 MmAct mm_act(void* buf, int64_t Mp, int64_t K);
-// weight_dt: the consumer's operand (Q4_0 takes its octets reordered)
+// weight_dt: the consumer's operand (Q4_0 takes its octets reordered);
+// gather: operand row m is x row gather[m] (< 0: zeros), for expert launches
 hipError_t launch_mm_prep(hipStream_t st, const float* x, int64_t ldx, const float* normw,
-                          float eps, int64_t M, const MmAct& act, int weight_dt);
+                          float eps, int64_t M, const MmAct& act, int weight_dt,
+                          const int32_t* gather = nullptr);
 bool mm_supported(int dt, int64_t K);
 bool mm_down_supported(int dt, int64_t n_in, int64_t N);
 // split-sum scratch of a launch over N output columns (`ntiles` 256-row
@@ -230,8 +234,52 @@ hipError_t launch_mm(hipStream_t st, const MmSeg* segs, int nseg, const MmAct& a
 hipError_t launch_mm_down(hipStream_t st, const uint8_t* tiled, int64_t n_in, int64_t N,
                           const float* h, int64_t ldh, int64_t M, const MmOut& out, float* part,
                           size_t part_floats, int cu_count);
+// SwiGLU output of an expert launch as the next GEMM's operand: fp16 hi / lo
+// planes in k_mm_prep's fragment order (contraction K), values times scale
+struct MmFragOut {
+    _Float16 *h, *l;
+    float scale;
+    int64_t K;
+};
+// gate / up of the routed experts (segments gate, up with `plane` bytes per
+// expert plane) over the gathered operand `act` (ntile_max * 64 rows), tile
+// by tile of the routing's table xtab; SwiGLU into fo.
+hipError_t launch_mm_experts(hipStream_t st, const MmSeg* segs, int nseg, const int64_t* plane,
+                             const MmAct& act, const int32_t* xtab, int64_t ntile_max,
+                             const MmFragOut& fo, float* part, size_t part_floats, int cu_count);
 
-// MFMA ffn_down (k_down.hip) over a re-tiled copy of the weights// MFMA ffn_down (k_down.hip) over a re-tiled copy of the weights
+// MoE routing, expert ffn_down and the weighted sum (k_moe.hip)
+struct MoeRoute {
+    int32_t* tab;        // [1 + 2 * ntile_max]: tiles in use, (expert, rows) per tile
+    int32_t* slot_tok;   // [ntile_max * 64]: token of each operand row, -1 for padding
+    int32_t* comb_slot;  // [M][U]: operand rows of token m in first-use order of experts
+    float* comb_w;       // [M][U]: their renormalised weights
+};
+int64_t moe_tiles_max(int64_t M, int64_t E, int64_t U);
+size_t moe_route_bytes(int64_t Mmax, int64_t E, int64_t U);
+MoeRoute moe_route_view(void* buf, int64_t Mmax, int64_t E, int64_t U);
+// router [M][E] (rows of logits, turned into probabilities in place), rbias
+// [E] or null
+hipError_t launch_moe_route(hipStream_t st, float* router, const float* rbias, int64_t M,
+                            int64_t E, int64_t U, const MoeRoute& r);
+bool moe_down_supported(int dt, int64_t F, int64_t K);
+size_t moe_down_tiled_bytes(int dt, int64_t F, int64_t K, int64_t E);
+hipError_t launch_moe_down_tile(hipStream_t st, const uint8_t* src, int dt, int64_t F, int64_t K,
+                                int64_t E, uint8_t* dst);
+int moe_down_splits(int64_t F, int64_t K, int64_t ntile_max, int cu_count);
+// part[S][ntile_max * 64][K] = the experts' down of the operand rows (fp16
+// hi / lo planes of h * 2^10 in fragment order, contraction F), S splits of F
+hipError_t launch_moe_down(hipStream_t st, const uint8_t* tiled, int dt, int64_t F, int64_t K,
+                           const _Float16* ah, const _Float16* al, const int32_t* xtab,
+                           int64_t ntile_max, int S, float* part, size_t part_floats);
+// y[m][:] (+)= sum over token m's experts, in first-use order, of weight *
+// (sum_s part[s][slot][:]) / 2^10; accum = 0 stores (the MoE FFN's tmpo)
+hipError_t launch_moe_combine(hipStream_t st, const float* part, int S, int64_t rows, int64_t K,
+                              const MoeRoute& r, int64_t M, int64_t U, float* y, int accum);
+// y[i] += x[i], n elements
+hipError_t launch_add(hipStream_t st, const float* x, float* y, int64_t n);
+
+// MFMA ffn_down (k_down.hip) over a re-tiled copy of the weights
 bool down_mfma_supported(int dt, int64_t n_in, int64_t N, int64_t M);
 size_t down_tiled_bytes(int dt, int64_t n_in, int64_t N);
 hipError_t launch_down_tile(hipStream_t st, const uint8_t* src, int64_t src_row_bytes, int dt,
@@ -280,6 +328,13 @@ struct RopeArgs {
     // optional: the rotated q also as fp16 hi + lo parts, [m][n_head][hd]
     _Float16* qh16 = nullptr;
     _Float16* ql16 = nullptr;
+    // optional attention extras (src/engine.cpp:519-542), applied before
+    // RoPE: bias [qdim + 2 kdim] added to q | k | v, RMSNorm weights [hd] of
+    // every q head and every k head, with eps
+    const float* bias = nullptr;
+    const float* qnorm = nullptr;
+    const float* knorm = nullptr;
+    float eps = 0.f;
 };
 hipError_t launch_rope_kv(hipStream_t st, const RopeArgs& a, int64_t M);
 struct AttnArgs {

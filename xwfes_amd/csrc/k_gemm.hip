@@ -32,16 +32,10 @@
 // hi/lo activation operands and the 6-bit scales / mins as fp16 tables; the
 // weights (the re-tiled copy of k_down.hip) enter as sc*q.
 #include "ftx_internal.h"
+#include "mm_dev.h"
 #include "quant_dev.h"
 
 namespace {
-
-typedef _Float16 v8h __attribute__((ext_vector_type(8)));
-typedef _Float16 v4h __attribute__((ext_vector_type(4)));
-typedef _Float16 v2h __attribute__((ext_vector_type(2)));
-typedef float v4f __attribute__((ext_vector_type(4)));
-typedef int v4i __attribute__((ext_vector_type(4)));
-typedef int v2i __attribute__((ext_vector_type(2)));
 
 constexpr int MM_TOK = 64;              // tokens per workgroup tile
 constexpr int MM_MS = MM_TOK / 16;      // 16-token MFMA tiles
@@ -56,42 +50,6 @@ constexpr int MM_NT = MM_WROWS / 16;    // 16-column MFMA tiles per wave
 // their fp16 lo parts stay clear of the subnormal range (undone on the
 // outputs)
 constexpr float MMD_ASCALE = 1024.f;
-
-__device__ __forceinline__ v8h ld8h(const _Float16* p) { return *(const v8h*)p; }
-
-// 8 nibbles (slot t: byte t % 4, nibble t / 4) -> fp16 q - bias, exact
-__device__ __forceinline__ v8h nib8(uint32_t w, float bias) {
-    const uint32_t lo = w & 0x0F0F0F0Fu, hi = (w >> 4) & 0x0F0F0F0Fu;
-    // 0x64 in the high byte: fp16 1024 + q
-    const uint32_t p0 = __builtin_amdgcn_perm(lo, 0x64646464u, 0x00050004u);
-    const uint32_t p1 = __builtin_amdgcn_perm(lo, 0x64646464u, 0x00070006u);
-    const uint32_t p2 = __builtin_amdgcn_perm(hi, 0x64646464u, 0x00050004u);
-    const uint32_t p3 = __builtin_amdgcn_perm(hi, 0x64646464u, 0x00070006u);
-    const v2h b = {(_Float16)(-1024.f - bias), (_Float16)(-1024.f - bias)};
-    const v2h h0 = __builtin_bit_cast(v2h, p0) + b, h1 = __builtin_bit_cast(v2h, p1) + b;
-    const v2h h2 = __builtin_bit_cast(v2h, p2) + b, h3 = __builtin_bit_cast(v2h, p3) + b;
-    return v8h{h0[0], h0[1], h1[0], h1[1], h2[0], h2[1], h3[0], h3[1]};
-}
-
-// 8 signed bytes -> fp16 q, exact: (q ^ 0x80) = q + 128 as the low byte of
-// fp16 1024 + q + 128, then - 1152
-__device__ __forceinline__ v8h i8x8(v2i w) {
-    const uint32_t a = (uint32_t)w.x ^ 0x80808080u, b = (uint32_t)w.y ^ 0x80808080u;
-    const uint32_t p0 = __builtin_amdgcn_perm(a, 0x64646464u, 0x00050004u);
-    const uint32_t p1 = __builtin_amdgcn_perm(a, 0x64646464u, 0x00070006u);
-    const uint32_t p2 = __builtin_amdgcn_perm(b, 0x64646464u, 0x00050004u);
-    const uint32_t p3 = __builtin_amdgcn_perm(b, 0x64646464u, 0x00070006u);
-    const v2h o = {(_Float16)(-1152.f), (_Float16)(-1152.f)};
-    const v2h h0 = __builtin_bit_cast(v2h, p0) + o, h1 = __builtin_bit_cast(v2h, p1) + o;
-    const v2h h2 = __builtin_bit_cast(v2h, p2) + o, h3 = __builtin_bit_cast(v2h, p3) + o;
-    return v8h{h0[0], h0[1], h1[0], h1[1], h2[0], h2[1], h3[0], h3[1]};
-}
-
-__device__ __forceinline__ void split_hl(float v, _Float16& h, _Float16& l) {
-#pragma clang fp contract(off)
-    h = (_Float16)v;
-    l = (_Float16)(v - (float)h);
-}
 
 // ---------------------------------------------------------------- prep
 // The activation operand in MFMA fragment order, so that a workgroup copies
@@ -116,10 +74,13 @@ __device__ __forceinline__ int64_t frag_at(int64_t m, int64_t k, int64_t K, bool
 // Workgroup (token row m < Mp, 1024-element slice): rows m >= M are zeros.
 // v = (x * inv) * w with inv = 1 / sqrt(sum x^2 / K + eps) when normw is
 // given (src/engine.cpp:23-41; every slice's workgroup forms the row's sum
-// itself), else v = x; v is split into fp16 hi + lo.
+// itself), else v = x; v is split into fp16 hi + lo.  gather (expert
+// launches): operand row m is row gather[m] of x, a zero row where
+// gather[m] < 0.
 __global__ void __launch_bounds__(256) k_mm_prep(const float* __restrict__ x, int64_t ldx,
                                                  const float* __restrict__ normw, float eps,
                                                  int64_t K, int M, int inter,
+                                                 const int32_t* __restrict__ gather,
                                                  _Float16* __restrict__ xh,
                                                  _Float16* __restrict__ xl,
                                                  _Float16* __restrict__ sh,
@@ -129,8 +90,9 @@ __global__ void __launch_bounds__(256) k_mm_prep(const float* __restrict__ x, in
     const int m = blockIdx.x, t = threadIdx.x;
     const int64_t nsb = K / 256;
     const int64_t k0 = (int64_t)blockIdx.y * 1024, k1 = min(k0 + 1024, K);
-    const bool live = m < M;  // block-uniform
-    const float* row = x + (int64_t)(live ? m : 0) * ldx;
+    const int src = m >= M ? -1 : (gather ? gather[m] : m);
+    const bool live = src >= 0;  // block-uniform
+    const float* row = x + (int64_t)(live ? src : 0) * ldx;
     float inv = 1.f;
     if (live && normw) {
         float ss = 0.f;
@@ -222,6 +184,11 @@ struct MmOutDev {
 
 struct MmArgs {
     MmSegDev seg[3];
+    int64_t plane[3];   // expert launches: bytes from one expert's plane to the next
+    // expert launches (null otherwise): the tile table of the routing,
+    // [0] = tiles in use, then per tile (expert, rows in use); tile t covers
+    // operand rows 64 t .. 64 t + 63
+    const int32_t* xtab;
     int nseg;
     int64_t units;      // 64-row units over all segments
     int64_t K;
@@ -333,15 +300,19 @@ __device__ __forceinline__ void bytes4_h(uint32_t w, v2h& lo, v2h& hi) {
 
 typedef __attribute__((address_space(3))) void lds_void;
 
-// grid = (ceil(units / 4), Mp / 64, splits); block = 256.  Per 256-element
+// grid = (ceil(units / 8), Mp / 64, splits); block = 512.  Per 256-element
 // step the workgroup's activation fragments (4 token tiles x 8 K-steps, hi
-// and lo: 64 KB) are copied to one of two LDS buffers by direct loads (16
+// and lo: 64 KB) are copied to one of two LDS buffers by direct loads (8
 // per wave), issued a whole step ahead together with the next step's
 // weights (two register sets used in turn); one wait and one barrier per
 // step.  Every wave takes part in the copies and barriers, and none
 // branches around its MFMAs: a wave past the last unit computes on its
 // clamped rows and stores nothing.
-template <int DT>
+// XT (expert launches): grid.y walks the routing's tile table; a tile past
+// the tiles in use ends at once (the whole workgroup), the weights are the
+// tile's expert's planes, and 16-token tiles past the tile's rows in use
+// are neither copied nor multiplied (a block-uniform choice).
+template <int DT, bool XT>
 __global__ void __launch_bounds__(64 * MM_WAVES)
     __attribute__((amdgpu_waves_per_eu(MM_WAVES / 4, MM_WAVES / 4))) k_mm(MmArgs a) {
     extern __shared__ __attribute__((aligned(16))) uint8_t mm_lds[];  // [2][64 KB]
@@ -351,9 +322,17 @@ __global__ void __launch_bounds__(64 * MM_WAVES)
     const int64_t u = (int64_t)blockIdx.x * MM_WAVES + w;
     const bool live = u < a.units;  // wave-uniform
     const int si = mm_seg_of(a, live ? u : a.units - 1);
-    const MmSegDev& sg = a.seg[si];
+    MmSegDev sg = a.seg[si];
     const int64_t rbase = ((live ? u : a.units - 1) - sg.unit0) * MM_WROWS;
     const int64_t mt0 = (int64_t)blockIdx.y * MM_MS;  // first 16-token tile
+    int nsub = MM_MS, mend = a.M;  // 16-token tiles in use, rows in use end
+    if constexpr (XT) {
+        if ((int)blockIdx.y >= a.xtab[0]) return;
+        const int ex = a.xtab[1 + 2 * blockIdx.y], nv = a.xtab[2 + 2 * blockIdx.y];
+        sg.W += (int64_t)ex * a.plane[si];
+        nsub = (nv + 15) >> 4;
+        mend = (int)blockIdx.y * MM_TOK + nv;
+    }
     const int ks = blockIdx.z;
     const int sb0 = ks * a.sb_per_split;
     const int sb1 = min(sb0 + a.sb_per_split, a.nsb);
@@ -367,6 +346,7 @@ __global__ void __launch_bounds__(64 * MM_WAVES)
     const int b0 = BPW * w, hl0 = b0 >> 5, ms0 = (b0 >> 3) & 3;
     const _Float16* gsrc = (hl0 ? a.xl : a.xh) + ((mt0 + ms0) * nks * 64 + lane) * 8;
     auto stage = [&](int sb, int buf) {
+        if (XT && ms0 >= nsub) return;  // this wave's blocks belong to an unused token tile
         const _Float16* src = gsrc + (int64_t)sb * 8 * 64 * 8;
 #pragma unroll
         for (int i = 0; i < BPW; ++i)
@@ -405,6 +385,7 @@ __global__ void __launch_bounds__(64 * MM_WAVES)
         if constexpr (DT == FTX_Q4_K) {
 #pragma unroll
             for (int ms = 0; ms < MM_MS; ++ms) {
+                if (XT && ms >= nsub) break;
                 const int64_t o = ((int64_t)ms * a.nsb + sb) * 32 * 4;
                 const v4h hh = *(const v4h*)(xs0 + o), ll = *(const v4h*)(xl0 + o);
                 xsh[ms] = kq < 2 ? hh : v4h{};
@@ -434,6 +415,7 @@ __global__ void __launch_bounds__(64 * MM_WAVES)
             v8h ah[MM_MS], al[MM_MS];
 #pragma unroll
             for (int ms = 0; ms < MM_MS; ++ms) {
+                if (XT && ms >= nsub) break;
                 ah[ms] = frag(buf, 0, ms, j);
                 al[ms] = frag(buf, 1, ms, j);
             }
@@ -476,33 +458,43 @@ __global__ void __launch_bounds__(64 * MM_WAVES)
 #pragma unroll
                 for (int t = 0; t < MM_NT; ++t)
 #pragma unroll
-                    for (int ms = 0; ms < MM_MS; ++ms)
+                    for (int ms = 0; ms < MM_MS; ++ms) {
+                        if (XT && ms >= nsub) break;
                         tmp[t][ms] = __builtin_amdgcn_mfma_f32_16x16x32_f16(
                             ah[ms], bw[t], j == 0 ? zero4 : tmp[t][ms], 0, 0, 0);
+                    }
 #pragma unroll
                 for (int t = 0; t < MM_NT; ++t)
 #pragma unroll
-                    for (int ms = 0; ms < MM_MS; ++ms)
+                    for (int ms = 0; ms < MM_MS; ++ms) {
+                        if (XT && ms >= nsub) break;
                         tmp[t][ms] =
                             __builtin_amdgcn_mfma_f32_16x16x32_f16(al[ms], bw[t], tmp[t][ms], 0, 0, 0);
+                    }
             } else {
                 v4f p[MM_NT][MM_MS];
 #pragma unroll
                 for (int t = 0; t < MM_NT; ++t)
 #pragma unroll
-                    for (int ms = 0; ms < MM_MS; ++ms)
+                    for (int ms = 0; ms < MM_MS; ++ms) {
+                        if (XT && ms >= nsub) break;
                         p[t][ms] = __builtin_amdgcn_mfma_f32_16x16x32_f16(ah[ms], bw[t], zero4, 0, 0, 0);
+                    }
 #pragma unroll
                 for (int t = 0; t < MM_NT; ++t)
 #pragma unroll
-                    for (int ms = 0; ms < MM_MS; ++ms)
+                    for (int ms = 0; ms < MM_MS; ++ms) {
+                        if (XT && ms >= nsub) break;
                         p[t][ms] = __builtin_amdgcn_mfma_f32_16x16x32_f16(al[ms], bw[t], p[t][ms], 0, 0, 0);
+                    }
 #pragma unroll
                 for (int t = 0; t < MM_NT; ++t)
 #pragma unroll
-                    for (int ms = 0; ms < MM_MS; ++ms)
+                    for (int ms = 0; ms < MM_MS; ++ms) {
+                        if (XT && ms >= nsub) break;
 #pragma unroll
                         for (int r = 0; r < 4; ++r) acc[t][ms][r] += bs[t] * p[t][ms][r];
+                    }
             }
         }
         if constexpr (DT == FTX_Q4_K) {
@@ -514,6 +506,7 @@ __global__ void __launch_bounds__(64 * MM_WAVES)
                 const float dmin = h2f((uint16_t)((uint32_t)wc.hdr[t].x >> 16));
 #pragma unroll
                 for (int ms = 0; ms < MM_MS; ++ms) {
+                    if (XT && ms >= nsub) break;
                     v4f mt = __builtin_amdgcn_mfma_f32_16x16x16f16(xsh[ms], mnh[t], zero4, 0, 0, 0);
                     mt = __builtin_amdgcn_mfma_f32_16x16x16f16(xsl[ms], mnh[t], mt, 0, 0, 0);
 #pragma unroll
@@ -543,7 +536,7 @@ __global__ void __launch_bounds__(64 * MM_WAVES)
 #pragma unroll
         for (int r = 0; r < 4; ++r) {
             const int64_t m = 16 * (mt0 + ms) + 4 * kq + r;
-            if (m >= a.M) continue;
+            if (m >= mend) continue;
             int s = 0;
             while (s + 1 < o.nseq && m >= o.row0[s + 1]) ++s;
             float* yrow = o.base[s] + (m - o.row0[s]) * o.ld + (int64_t)ks * o.split_stride;
@@ -733,6 +726,10 @@ k_mm_down(MmDownArgs a) {
 // out[m][n] (= or +=) sum_ks part[ks][m][n] in split order; SwiGLU:
 // out[m][n] = silu(g) * u with g, u the sums of columns n and n + N
 // (src/engine.cpp:271-273).  grid = (ceil(N / 256), M).
+// Expert launches (xtab set): rows outside the tiles in use, and past a
+// tile's rows in use, are zeros.  Fragment output (fh set): the result
+// times fscale goes to the fp16 hi + lo operand planes (k_mm_prep's
+// fragment order, contraction fK) instead of out.
 struct MmReduceArgs {
     const float* part;
     int64_t split_stride, ldp;
@@ -740,22 +737,43 @@ struct MmReduceArgs {
     int64_t N;
     int swiglu;
     MmOutDev out;
+    const int32_t* xtab;
+    _Float16 *fh, *fl;
+    float fscale;
+    int64_t fK;
 };
 
 __global__ void __launch_bounds__(256) k_mm_reduce(MmReduceArgs a) {
     const int64_t n = (int64_t)blockIdx.x * 256 + threadIdx.x;
     const int64_t m = blockIdx.y;
     if (n >= a.N) return;
-    const float* p = a.part + m * a.ldp + n;
-    float g = 0.f, u = 0.f;
-    for (int s = 0; s < a.S; ++s) g += p[(int64_t)s * a.split_stride];
-    if (a.swiglu)
-        for (int s = 0; s < a.S; ++s) u += p[(int64_t)s * a.split_stride + a.N];
+    bool valid = true;
+    if (a.xtab) {
+        const int64_t t = m / MM_TOK;
+        valid = t < a.xtab[0] && m - t * MM_TOK < a.xtab[2 + 2 * t];
+    }
+    float v = 0.f;
+    if (valid) {
+        const float* p = a.part + m * a.ldp + n;
+        float g = 0.f, u = 0.f;
+        for (int s = 0; s < a.S; ++s) g += p[(int64_t)s * a.split_stride];
+        if (a.swiglu)
+            for (int s = 0; s < a.S; ++s) u += p[(int64_t)s * a.split_stride + a.N];
+        v = a.swiglu ? g / (1.f + expf(-g)) * u : g;
+    }
+    if (a.fh) {
+#pragma clang fp contract(off)
+        const int64_t at = frag_at(m, n, a.fK, false);
+        _Float16 h, l;
+        split_hl(v * a.fscale, h, l);
+        a.fh[at] = h;
+        a.fl[at] = l;
+        return;
+    }
     const MmOutDev& o = a.out;
     int sq = 0;
     while (sq + 1 < o.nseq && m >= o.row0[sq + 1]) ++sq;
     float* yp = o.base[sq] + (m - o.row0[sq]) * o.ld + n;
-    const float v = a.swiglu ? g / (1.f + expf(-g)) * u : g;
     *yp = o.accum ? *yp + v : v;
 }
 
@@ -779,13 +797,14 @@ MmAct mm_act(void* buf, int64_t Mp, int64_t K) {
 }
 
 hipError_t launch_mm_prep(hipStream_t st, const float* x, int64_t ldx, const float* normw,
-                          float eps, int64_t M, const MmAct& act, int weight_dt) {
+                          float eps, int64_t M, const MmAct& act, int weight_dt,
+                          const int32_t* gather) {
     if (act.K % 256 || M < 1 || M > act.Mp || act.Mp % MM_TOK || ldx % 4 || ((uintptr_t)x & 15))
         return hipErrorInvalidValue;
     hipLaunchKernelGGL(k_mm_prep, dim3((unsigned)act.Mp, (unsigned)((act.K + 1023) / 1024)),
                        dim3(256), 0, st, x, ldx, normw, eps,
-                       act.K, (int)M, weight_dt == FTX_Q4_0_PLANAR ? 1 : 0, act.xh, act.xl,
-                       act.sh, act.sl);
+                       act.K, (int)M, weight_dt == FTX_Q4_0_PLANAR ? 1 : 0, gather, act.xh,
+                       act.xl, act.sh, act.sl);
     return hipGetLastError();
 }
 
@@ -830,10 +849,18 @@ size_t mm_part_floats(int64_t Mp, int64_t N, int64_t steps, int64_t ntiles, int 
     return S > 1 ? (size_t)S * (size_t)Mp * (size_t)N : 0;
 }
 
-hipError_t launch_mm(hipStream_t st, const MmSeg* segs, int nseg, const MmAct& act, int64_t M,
-                     int epi, const MmOut& out, float* part, size_t part_floats, int cu_count) {
+// both forms: dense (xtab null: rows 0 .. M - 1 of the operand, tiles of
+// 64) and expert (grid.y = ntile_max entries of the tile table; plane:
+// bytes per expert plane of each segment; the outputs are operand rows)
+static hipError_t mm_launch(hipStream_t st, const MmSeg* segs, int nseg, const MmAct& act,
+                            int64_t M, int epi, const MmOut& out, float* part,
+                            size_t part_floats, int cu_count, const int32_t* xtab,
+                            const int64_t* plane, int64_t ntile_max, const MmFragOut* fo) {
     if (nseg < 1 || nseg > 3 || M < 1 || M > act.Mp || out.nseq < 1 || out.nseq > FTX_MAX_SEQ)
         return hipErrorInvalidValue;
+    if (xtab && (ntile_max < 1 || ntile_max * MM_TOK > act.Mp || !plane))
+        return hipErrorInvalidValue;
+    if (fo && (!xtab || epi != EPI_SWIGLU)) return hipErrorInvalidValue;
     const int dt = segs[0].dt;
     MmArgs a{};
     a.nseg = nseg;
@@ -850,7 +877,9 @@ hipError_t launch_mm(hipStream_t st, const MmSeg* segs, int nseg, const MmAct& a
         d.rpt = segs[i].rpt;
         units += (segs[i].N + MM_WROWS - 1) / MM_WROWS;
         cols += segs[i].N;
+        a.plane[i] = plane ? plane[i] : 0;
     }
+    a.xtab = xtab;
     a.units = units;
     a.K = act.K;
     a.nsb = (int)(act.K / 256);
@@ -859,10 +888,11 @@ hipError_t launch_mm(hipStream_t st, const MmSeg* segs, int nseg, const MmAct& a
     a.sh = act.sh;
     a.sl = act.sl;
     a.M = (int)M;
-    const int64_t wg = (units + MM_WAVES - 1) / MM_WAVES, mt = act.Mp / MM_TOK;
+    const int64_t wg = (units + MM_WAVES - 1) / MM_WAVES,
+                  mt = xtab ? ntile_max : act.Mp / MM_TOK;
     int S = mm_splits(wg * mt, a.nsb, cu_count);
     // SwiGLU needs the gate and up sums together: always through the reduce
-    const bool via_part = S > 1 || epi == EPI_SWIGLU;
+    const bool via_part = S > 1 || epi == EPI_SWIGLU || xtab;
     if (via_part) {
         if (!part || (size_t)S * (size_t)act.Mp * (size_t)cols > part_floats) {
             S = 1;
@@ -884,11 +914,14 @@ hipError_t launch_mm(hipStream_t st, const MmSeg* segs, int nseg, const MmAct& a
     const dim3 grid((unsigned)wg, (unsigned)mt, (unsigned)S);
     constexpr size_t lds = 2 * 65536;
     using K_t = void (*)(MmArgs);
-    const K_t kern = dt == FTX_Q4_K          ? k_mm<FTX_Q4_K>
-                     : dt == FTX_Q8_0_PLANAR ? k_mm<FTX_Q8_0_PLANAR>
-                                             : k_mm<FTX_Q4_0_PLANAR>;
-    static bool lds_set[3] = {false, false, false};
-    const int ki = dt == FTX_Q4_K ? 0 : (dt == FTX_Q8_0_PLANAR ? 1 : 2);
+    const K_t kern = xtab ? (dt == FTX_Q4_K          ? k_mm<FTX_Q4_K, true>
+                             : dt == FTX_Q8_0_PLANAR ? k_mm<FTX_Q8_0_PLANAR, true>
+                                                     : k_mm<FTX_Q4_0_PLANAR, true>)
+                          : (dt == FTX_Q4_K          ? k_mm<FTX_Q4_K, false>
+                             : dt == FTX_Q8_0_PLANAR ? k_mm<FTX_Q8_0_PLANAR, false>
+                                                     : k_mm<FTX_Q4_0_PLANAR, false>);
+    static bool lds_set[6] = {false, false, false, false, false, false};
+    const int ki = (dt == FTX_Q4_K ? 0 : (dt == FTX_Q8_0_PLANAR ? 1 : 2)) + (xtab ? 3 : 0);
     if (!lds_set[ki]) {
         hipError_t e = hipFuncSetAttribute((const void*)kern,
                                            hipFuncAttributeMaxDynamicSharedMemorySize, (int)lds);
@@ -906,9 +939,34 @@ hipError_t launch_mm(hipStream_t st, const MmSeg* segs, int nseg, const MmAct& a
     r.swiglu = epi == EPI_SWIGLU;
     r.N = r.swiglu ? cols / 2 : cols;
     r.out = out_dev(out);
-    hipLaunchKernelGGL(k_mm_reduce, dim3((unsigned)((r.N + 255) / 256), (unsigned)M), dim3(256), 0,
-                       st, r);
+    r.xtab = xtab;
+    if (fo) {
+        r.fh = fo->h;
+        r.fl = fo->l;
+        r.fscale = fo->scale;
+        r.fK = fo->K;
+    }
+    const int64_t rows = xtab ? ntile_max * MM_TOK : M;
+    hipLaunchKernelGGL(k_mm_reduce, dim3((unsigned)((r.N + 255) / 256), (unsigned)rows), dim3(256),
+                       0, st, r);
     return hipGetLastError();
+}
+
+hipError_t launch_mm(hipStream_t st, const MmSeg* segs, int nseg, const MmAct& act, int64_t M,
+                     int epi, const MmOut& out, float* part, size_t part_floats, int cu_count) {
+    return mm_launch(st, segs, nseg, act, M, epi, out, part, part_floats, cu_count, nullptr,
+                     nullptr, 0, nullptr);
+}
+
+hipError_t launch_mm_experts(hipStream_t st, const MmSeg* segs, int nseg, const int64_t* plane,
+                             const MmAct& act, const int32_t* xtab, int64_t ntile_max,
+                             const MmFragOut& fo, float* part, size_t part_floats, int cu_count) {
+    if (fo.K != segs[0].N || fo.K % 32) return hipErrorInvalidValue;
+    MmOut o{};
+    o.nseq = 1;
+    o.row0[1] = ntile_max * MM_TOK;
+    return mm_launch(st, segs, nseg, act, ntile_max * MM_TOK, EPI_SWIGLU, o, part, part_floats,
+                     cu_count, xtab, plane, ntile_max, &fo);
 }
 
 hipError_t launch_mm_down(hipStream_t st, const uint8_t* tiled, int64_t n_in, int64_t N,

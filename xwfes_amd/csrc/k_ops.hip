@@ -64,7 +64,9 @@ hipError_t launch_rmsnorm(hipStream_t st, const float* x, const float* w, int64_
 // src/engine.cpp:43-60 (frequencies and angles in double, cos/sin rounded
 // to float; neox pairs (i, i+hd/2), else interleaved (2i, 2i+1)) applied to
 // q and k at position npast + depth[m]; k and v are then written to KV slot
-// npast + m (src/engine.cpp:555-561).
+// npast + m (src/engine.cpp:555-561).  Before RoPE, when given: the bias of
+// q / k / v and the per-head RMSNorm of q and k (src/engine.cpp:519-542;
+// the head's sum of squares as a wave sum).  One wave per (token, head).
 __global__ void k_rope_kv(RopeArgs a) {
 #pragma clang fp contract(off)
     const int64_t m = blockIdx.x;
@@ -75,8 +77,29 @@ __global__ void k_rope_kv(RopeArgs a) {
     const int64_t qdim = a.n_head * a.hd, kdim = a.n_kv * a.hd;
     float* row = a.qkv + m * a.ldq;
     float* v;
-    if (h < a.n_head) v = row + h * a.hd;
-    else v = row + qdim + (h - a.n_head) * a.hd;
+    const bool is_q = h < a.n_head;
+    const int64_t off = is_q ? h * a.hd : qdim + (h - a.n_head) * a.hd;
+    v = row + off;
+    const float* nw = is_q ? a.qnorm : a.knorm;
+    if (a.bias || nw) {
+        float ss = 0.f;
+        for (int64_t t = threadIdx.x; t < a.hd; t += blockDim.x) {
+            float x = v[t];
+            if (a.bias) {
+                x = x + a.bias[off + t];
+                v[t] = x;
+                if (!is_q) row[off + kdim + t] += a.bias[off + kdim + t];  // v of this kv head
+            }
+            ss += x * x;
+        }
+        if (nw) {
+#pragma unroll
+            for (int o = 32; o > 0; o >>= 1) ss += __shfl_xor(ss, o, 64);
+            const float inv = 1.f / sqrtf(ss / (float)a.hd + a.eps);
+            for (int64_t t = threadIdx.x; t < a.hd; t += blockDim.x) v[t] = v[t] * inv * nw[t];
+        }
+        __syncthreads();  // RoPE pairs cross the threads' elements
+    }
     for (int64_t i = threadIdx.x; i < half; i += blockDim.x) {
         const double f = pow(a.theta, -2.0 * (double)i / (double)a.hd);
         const double ang = (double)pos * f;

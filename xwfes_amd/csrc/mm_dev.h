@@ -1,0 +1,54 @@
+// mm_dev.h -- operand helpers shared by the fp16-MFMA kernels (k_gemm.hip,
+// k_moe.hip): vector types, exact integer -> fp16 conversions and the fp16
+// hi + lo split of an fp32 value.
+#pragma once
+
+#include <hip/hip_runtime.h>
+#include <stdint.h>
+
+namespace {
+
+typedef _Float16 v8h __attribute__((ext_vector_type(8)));
+typedef _Float16 v4h __attribute__((ext_vector_type(4)));
+typedef _Float16 v2h __attribute__((ext_vector_type(2)));
+typedef float v4f __attribute__((ext_vector_type(4)));
+typedef int v4i __attribute__((ext_vector_type(4)));
+typedef int v2i __attribute__((ext_vector_type(2)));
+
+__device__ __forceinline__ v8h ld8h(const _Float16* p) { return *(const v8h*)p; }
+
+// 8 nibbles (slot t: byte t % 4, nibble t / 4) -> fp16 q - bias, exact
+__device__ __forceinline__ v8h nib8(uint32_t w, float bias) {
+    const uint32_t lo = w & 0x0F0F0F0Fu, hi = (w >> 4) & 0x0F0F0F0Fu;
+    // 0x64 in the high byte: fp16 1024 + q
+    const uint32_t p0 = __builtin_amdgcn_perm(lo, 0x64646464u, 0x00050004u);
+    const uint32_t p1 = __builtin_amdgcn_perm(lo, 0x64646464u, 0x00070006u);
+    const uint32_t p2 = __builtin_amdgcn_perm(hi, 0x64646464u, 0x00050004u);
+    const uint32_t p3 = __builtin_amdgcn_perm(hi, 0x64646464u, 0x00070006u);
+    const v2h b = {(_Float16)(-1024.f - bias), (_Float16)(-1024.f - bias)};
+    const v2h h0 = __builtin_bit_cast(v2h, p0) + b, h1 = __builtin_bit_cast(v2h, p1) + b;
+    const v2h h2 = __builtin_bit_cast(v2h, p2) + b, h3 = __builtin_bit_cast(v2h, p3) + b;
+    return v8h{h0[0], h0[1], h1[0], h1[1], h2[0], h2[1], h3[0], h3[1]};
+}
+
+// 8 signed bytes -> fp16 q, exact: (q ^ 0x80) = q + 128 as the low byte of
+// fp16 1024 + q + 128, then - 1152
+__device__ __forceinline__ v8h i8x8(v2i w) {
+    const uint32_t a = (uint32_t)w.x ^ 0x80808080u, b = (uint32_t)w.y ^ 0x80808080u;
+    const uint32_t p0 = __builtin_amdgcn_perm(a, 0x64646464u, 0x00050004u);
+    const uint32_t p1 = __builtin_amdgcn_perm(a, 0x64646464u, 0x00070006u);
+    const uint32_t p2 = __builtin_amdgcn_perm(b, 0x64646464u, 0x00050004u);
+    const uint32_t p3 = __builtin_amdgcn_perm(b, 0x64646464u, 0x00070006u);
+    const v2h o = {(_Float16)(-1152.f), (_Float16)(-1152.f)};
+    const v2h h0 = __builtin_bit_cast(v2h, p0) + o, h1 = __builtin_bit_cast(v2h, p1) + o;
+    const v2h h2 = __builtin_bit_cast(v2h, p2) + o, h3 = __builtin_bit_cast(v2h, p3) + o;
+    return v8h{h0[0], h0[1], h1[0], h1[1], h2[0], h2[1], h3[0], h3[1]};
+}
+
+__device__ __forceinline__ void split_hl(float v, _Float16& h, _Float16& l) {
+#pragma clang fp contract(off)
+    h = (_Float16)v;
+    l = (_Float16)(v - (float)h);
+}
+
+}  // namespace

@@ -7,7 +7,8 @@
 
 static const char* kTraceNames[TK_COUNT] = {
     "embed", "rmsnorm", "gemv_qkv", "rope_kv", "attention", "gemv_o",
-    "gemv_swiglu", "down", "head", "row_stats", "accept", "xq_prep"};
+    "gemv_swiglu", "down", "head", "row_stats", "accept", "xq_prep", "moe_route",
+    "moe_combine"};
 
 static void resolve(ftx_ctx* ctx) {
     if (ctx->pending.empty()) {

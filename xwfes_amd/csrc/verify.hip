@@ -50,6 +50,28 @@ struct ftx_model {
     _Float16* mm_act = nullptr;
     float* mm_part = nullptr;
     size_t mm_part_n = 0;
+    // optional per-layer tensors (layer_ext) and what the device keeps of
+    // them: any attention extra or MoE layer sends every step through
+    // verify_large
+    std::vector<const ftx_tensor*> ext;
+    bool has_ext = false;
+    std::vector<float*> attn_bias;  // [qdim + 2 kdim] q | k | v bias per layer, or null
+    std::vector<float*> qnorm, knorm;  // [hd] per layer, or null
+    // MoE layers: planar copies of the gate and up expert planes, the
+    // re-tiled down planes, the router bias as F32; shared buffers for the
+    // router rows, the routing tables, the gathered operand, the down
+    // operand, split partials, and tmpo for shared experts
+    std::vector<uint8_t*> moe_gate, moe_up, moe_down;
+    std::vector<int> moe_gu_dt;
+    std::vector<float*> moe_rbias;
+    float* router = nullptr;
+    void* route = nullptr;
+    _Float16* moe_act = nullptr;
+    _Float16* moe_h = nullptr;
+    float* moe_part = nullptr;
+    size_t moe_part_n = 0;
+    float* tmpo = nullptr;
+    int64_t F_alloc = 0;  // columns of h (the widest of n_ff and the shared experts')
     // pinned host argument blocks, used in turn; an event recorded after a
     // block's copy to the device guards its reuse, so the host prepares the
     // next step while earlier steps still run
@@ -114,6 +136,15 @@ static void model_release(ftx_model* m) {
     if (m->downpart) (void)hipFree(m->downpart);
     if (m->mm_act) (void)hipFree(m->mm_act);
     if (m->mm_part) (void)hipFree(m->mm_part);
+    for (auto* v : {&m->attn_bias, &m->qnorm, &m->knorm, &m->moe_rbias})
+        for (float* b : *v)
+            if (b) (void)hipFree(b);
+    for (auto* v : {&m->moe_gate, &m->moe_up, &m->moe_down})
+        for (uint8_t* b : *v)
+            if (b) (void)hipFree(b);
+    void* mb[] = {m->router, m->route, m->moe_act, m->moe_h, m->moe_part, m->tmpo};
+    for (void* b : mb)
+        if (b) (void)hipFree(b);
     for (int i = 0; i < ftx_model::PIN_RING; ++i) {
         if (m->pin[i]) (void)hipHostFree(m->pin[i]);
         if (m->pin_ev[i]) (void)hipEventDestroy(m->pin_ev[i]);
@@ -298,6 +329,59 @@ static int verify_large(ftx_ctx* ctx, ftx_model* m, const ftx_seq_args* sq, int6
     };
     _Float16* qh = m->qhl;
     _Float16* ql = m->qhl + Mt * m->qdim;
+    // The MoE FFN of layer l (src/engine.cpp:179-258), added into x: ffn_norm
+    // rows, router logits, routing, the routed experts' gate / up (one-pass
+    // GEMM over the gathered rows, SwiGLU into the down operand), their down,
+    // the weighted sum in first-use order; a shared expert's FFN is added to
+    // that sum before the sum goes into x (src/engine.cpp:243-257, 577-579).
+    auto moe_layer = [&](int64_t l, const ftx_tensor* const* X) -> int {
+        const int64_t E = d.n_expert, U = d.n_expert_used;
+        const int64_t T = moe_tiles_max(Mt, E, U), rows = T * 64;
+        const ftx_tensor* gi = X[FTX_X_GATE_INP];
+        const ftx_tensor *ge = X[FTX_X_GATE_EXPS], *de = X[FTX_X_DOWN_EXPS];
+        const MoeRoute rt = moe_route_view(m->route, m->Mmax, E, U);
+        TRACED_L(TK_RMSNORM, 2 * Md * D * f4,
+                 launch_rmsnorm(st, m->x, m->norms + (l * 2 + 1) * D, D, Mt, eps, m->xn));
+        GemvSeg rs[1] = {GemvSeg{gi->data, gi->dtype, gi->row_bytes, E, m->router, E}};
+        TRACED_L(TK_MOE_ROUTE, wbytes(gi) + Md * D * f4 + Md * E * f4,
+                 launch_gemv(st, rs, 1, m->xn, D, D, Mt, EPI_STORE, true));
+        TRACED_L(TK_MOE_ROUTE, 2 * Md * E * f4,
+                 launch_moe_route(st, m->router, m->moe_rbias[l], Mt, E, U, rt));
+        const int gdt = m->moe_gu_dt[l];
+        const MmAct act = mm_act(m->moe_act, rows, D);
+        TRACED_L(TK_XQ_PREP, Md * U * D * f4 + 4.0 * rows * D,
+                 launch_mm_prep(st, m->xn, D, nullptr, eps, rows, act, gdt, rt.slot_tok));
+        // every plane is read at most once; the routed planes are what moves
+        const double plane_gu = (double)(ge->row_bytes * F);
+        const double used = (double)std::min<int64_t>(E, Mt * U);
+        MmSeg gs[2] = {MmSeg{m->moe_gate[l], gdt, F, 0, ge->row_bytes},
+                       MmSeg{m->moe_up[l], gdt, F, 0, ge->row_bytes}};
+        const int64_t plane[2] = {F * ge->row_bytes, F * ge->row_bytes};
+        MmFragOut fo{m->moe_h, m->moe_h + rows * F, 1.f, F};
+        TRACED_L(TK_GEMV_SWIGLU, 2 * used * plane_gu + Md * U * D * 4.0 + Md * U * F * 4.0,
+                 launch_mm_experts(st, gs, 2, plane, act, rt.tab, T, fo, m->moe_part,
+                                   m->moe_part_n, ctx->cu_count));
+        const int S = moe_down_splits(F, D, T, ctx->cu_count);
+        TRACED_L(TK_DOWN, used * (double)(de->row_bytes * F) + Md * U * F * 4.0 + S * Md * U * D * f4,
+                 launch_moe_down(st, m->moe_down[l], de->dtype, F, D, fo.h, fo.l, rt.tab, T, S,
+                                 m->moe_part, m->moe_part_n));
+        const ftx_tensor *sg = X[FTX_X_GATE_SH], *su = X[FTX_X_UP_SH], *sd = X[FTX_X_DOWN_SH];
+        TRACED_L(TK_MOE_COMBINE, S * Md * U * D * f4 + 2 * Md * D * f4,
+                 launch_moe_combine(st, m->moe_part, S, rows, D, rt, Mt, U, sg ? m->tmpo : m->x,
+                                    sg ? 0 : 1));
+        if (sg) {
+            // the shared expert over all rows (generic kernels), into tmpo
+            const int64_t FS = sg->nrows;
+            TRACED_L(TK_GEMV_SWIGLU, wbytes(sg) + wbytes(su) + Md * D * f4 + Md * FS * f4,
+                     launch_gemv_swiglu(st, sg->data, su->data, sg->dtype, sg->row_bytes, FS,
+                                        m->xn, D, D, Mt, m->h, FS, true));
+            TRACED_L(TK_DOWN, wbytes(sd) + Md * FS * f4 + 2 * Md * D * f4,
+                     launch_down(st, sd->data, sd->dtype, sd->row_bytes, FS, D, m->h, FS, Mt,
+                                 m->tmpo, D, m->part));
+            TRACED_L(TK_MOE_COMBINE, 3 * Md * D * f4, launch_add(st, m->tmpo, m->x, Mt * D));
+        }
+        return FTX_OK;
+    };
     int rc;
     for (int64_t l = 0; l < d.n_layer; ++l) {
         const int64_t lt = l * FTX_LAYER_TENSORS;
@@ -328,6 +412,10 @@ static int verify_large(ftx_ctx* ctx, ftx_model* m, const ftx_seq_args* sq, int6
             RopeArgs ra{m->qkv + r0 * m->ldq, m->ldq,  d.n_head,   d.n_head_kv, hd,
                         d_depth + r0,         d_np + s, d.rope_theta, d.rope_neox, kl,
                         vl,                   kv->kv_f16, kv->cap_alloc};
+            ra.bias = m->attn_bias[l];
+            ra.qnorm = m->qnorm[l];
+            ra.knorm = m->knorm[l];
+            ra.eps = eps;
             if (mattn) {
                 ra.qh16 = qh + r0 * m->qdim;
                 ra.ql16 = ql + r0 * m->qdim;
@@ -369,6 +457,12 @@ static int verify_large(ftx_ctx* ctx, ftx_model* m, const ftx_seq_args* sq, int6
                          m->qdim, nullptr, idx, &T[FTX_T_O], gs, 1, m->qdim, EPI_ACCUM,
                          out1(m->x, D, 1), Mt);
             if (rc) return rc;
+        }
+        const ftx_tensor* const* X = m->ext.data() + l * FTX_LAYER_EXT;
+        if (X[FTX_X_GATE_INP]) {
+            rc = moe_layer(l, X);
+            if (rc) return rc;
+            continue;
         }
         // gate / up with SwiGLU into h
         {
@@ -484,15 +578,70 @@ int ftx_model_create(ftx_ctx* ctx, const ftx_model_desc* d, ftx_model** out) {
     if ((rc = need(d->tok_embd, D, d->vocab, "tok_embd"))) return rc;
     if ((rc = need(d->out_norm, D, 1, "out_norm"))) return rc;
     if (d->output && (rc = need(d->output, D, d->vocab, "output"))) return rc;
+    // a vector of n values (stored [n] or [1, n])
+    auto need_vec = [&](const ftx_tensor* t, int64_t n, const char* nm) -> int {
+        if (t->ne[0] * t->nrows != n)
+            return ftx_fail(ctx, FTX_E_INVALID, std::string("bad shape of tensor ") + nm);
+        return FTX_OK;
+    };
+    const int64_t E = d->n_expert, U = d->n_expert_used;
+    bool any_moe = false, any_ext = false;
+    int64_t F_sh = 0;
     for (int64_t l = 0; l < d->n_layer; ++l) {
         const ftx_tensor* const* T = d->layers + l * FTX_LAYER_TENSORS;
+        const ftx_tensor* const* X = d->layer_ext ? d->layer_ext + l * FTX_LAYER_EXT : nullptr;
+        auto x = [&](int i) { return X ? X[i] : nullptr; };
         if ((rc = need(T[FTX_T_ATTN_NORM], D, 1, "attn_norm")) ||
             (rc = need(T[FTX_T_Q], D, qdim, "attn_q")) ||
             (rc = need(T[FTX_T_K], D, kdim, "attn_k")) ||
             (rc = need(T[FTX_T_V], D, kdim, "attn_v")) ||
             (rc = need(T[FTX_T_O], qdim, D, "attn_output")) ||
-            (rc = need(T[FTX_T_FFN_NORM], D, 1, "ffn_norm")) ||
-            (rc = need(T[FTX_T_GATE], D, d->n_ff, "ffn_gate")) ||
+            (rc = need(T[FTX_T_FFN_NORM], D, 1, "ffn_norm")))
+            return rc;
+        const int64_t vn[5] = {qdim, kdim, kdim, d->head_dim, d->head_dim};
+        static const char* const vnm[5] = {"attn_q.bias", "attn_k.bias", "attn_v.bias",
+                                           "attn_q_norm", "attn_k_norm"};
+        for (int i = 0; i < 5; ++i)
+            if (x(i)) {
+                if ((rc = need_vec(x(i), vn[i], vnm[i]))) return rc;
+                any_ext = true;
+            }
+        if (x(FTX_X_GATE_INP)) {
+            // MoE layer (src/engine.cpp:348-369)
+            any_moe = true;
+            if (E < 2 || E > 256 || U < 1 || U > 8 || U > E)
+                return ftx_fail(ctx, FTX_E_UNSUPPORTED,
+                                "MoE: n_expert must be in [2, 256], n_expert_used in [1, min(8, n_expert)]");
+            const ftx_tensor *ge = x(FTX_X_GATE_EXPS), *ue = x(FTX_X_UP_EXPS), *de = x(FTX_X_DOWN_EXPS);
+            if ((rc = need(x(FTX_X_GATE_INP), D, E, "ffn_gate_inp"))) return rc;
+            if (!ge || !ue || !de)
+                return ftx_fail(ctx, FTX_E_INVALID, "incomplete MoE tensors at a layer");
+            for (const ftx_tensor* t : {ge, ue, de})
+                if (t->ne[0] != D || t->ne[1] != d->n_ff || t->ne[2] != E || t->ne[3] != 1)
+                    return ftx_fail(ctx, FTX_E_INVALID, "bad shape of an expert tensor");
+            if (ge->dtype != ue->dtype || planar_dtype(ge->dtype, D) < 0 ||
+                !mm_supported(planar_dtype(ge->dtype, D), D))
+                return ftx_fail(ctx, FTX_E_UNSUPPORTED,
+                                "MoE gate / up experts must share Q4_0 or Q8_0 with n_embd % 256 == 0");
+            if (!moe_down_supported(de->dtype, d->n_ff, D))
+                return ftx_fail(ctx, FTX_E_UNSUPPORTED,
+                                "MoE down experts must be Q4_0 with n_ff % 32 == 0, n_embd % 256 == 0");
+            if (x(FTX_X_ROUTER_BIAS) && (rc = need_vec(x(FTX_X_ROUTER_BIAS), E, "exp_probs_b")))
+                return rc;
+            const ftx_tensor *sg = x(FTX_X_GATE_SH), *su = x(FTX_X_UP_SH), *sd = x(FTX_X_DOWN_SH);
+            if (sg || su || sd) {
+                if (!sg || !su || !sd) return ftx_fail(ctx, FTX_E_INVALID, "incomplete shared expert");
+                const int64_t fs = sg->nrows;
+                if ((rc = need(sg, D, fs, "ffn_gate_shexp")) || (rc = need(su, D, fs, "ffn_up_shexp")) ||
+                    (rc = need(sd, D, fs, "ffn_down_shexp")))
+                    return rc;
+                if (sg->dtype != su->dtype)
+                    return ftx_fail(ctx, FTX_E_UNSUPPORTED, "shared gate and up must share a dtype");
+                F_sh = std::max(F_sh, fs);
+            }
+            continue;
+        }
+        if ((rc = need(T[FTX_T_GATE], D, d->n_ff, "ffn_gate")) ||
             (rc = need(T[FTX_T_UP], D, d->n_ff, "ffn_up")) ||
             (rc = need(T[FTX_T_DOWN], D, d->n_ff, "ffn_down")))
             return rc;
@@ -505,15 +654,21 @@ int ftx_model_create(ftx_ctx* ctx, const ftx_model_desc* d, ftx_model** out) {
     m->d = *d;
     m->layers.assign(d->layers, d->layers + d->n_layer * FTX_LAYER_TENSORS);
     m->d.layers = nullptr;
+    m->ext.assign((size_t)(d->n_layer * FTX_LAYER_EXT), nullptr);
+    if (d->layer_ext) m->ext.assign(d->layer_ext, d->layer_ext + d->n_layer * FTX_LAYER_EXT);
+    m->d.layer_ext = nullptr;
+    m->has_ext = any_moe || any_ext;
+    m->F_alloc = std::max(d->n_ff, F_sh);
     m->qdim = qdim;
     m->kdim = kdim;
     m->ldq = qdim + 2 * kdim;
     m->Mmax = Mmax;
     m->part_floats = down_scratch_floats(Mmax, d->n_ff, D);
+    if (F_sh) m->part_floats = std::max(m->part_floats, down_scratch_floats(Mmax, F_sh, D));
     const size_t nn = (size_t)(d->n_layer * 2 + 1);
     bool ok = dalloc(&m->norms, nn * D) && dalloc(&m->x, Mmax * D) && dalloc(&m->xn, Mmax * D) &&
               dalloc(&m->qkv, Mmax * m->ldq) && dalloc(&m->att, Mmax * qdim) &&
-              dalloc(&m->h, Mmax * d->n_ff) && dalloc(&m->part, m->part_floats) &&
+              dalloc(&m->h, Mmax * m->F_alloc) && dalloc(&m->part, m->part_floats) &&
               dalloc(&m->args, step_args_bytes(Mmax, d->head_dim));
     for (int i = 0; ok && i < ftx_model::PIN_RING; ++i) {
         ok = hipHostMalloc((void**)&m->pin[i], step_args_bytes(Mmax, d->head_dim),
@@ -531,7 +686,7 @@ int ftx_model_create(ftx_ctx* ctx, const ftx_model_desc* d, ftx_model** out) {
     bool any_tiled = false;
     for (int64_t l = 0; ok && l < d->n_layer; ++l) {
         const ftx_tensor* dn = d->layers[l * FTX_LAYER_TENSORS + FTX_T_DOWN];
-        if (!down_mfma_supported(dn->dtype, d->n_ff, D, 1)) continue;
+        if (!dn || !down_mfma_supported(dn->dtype, d->n_ff, D, 1)) continue;
         uint8_t* buf = nullptr;
         if (!dalloc(&buf, down_tiled_bytes(dn->dtype, d->n_ff, D))) {
             ok = false;
@@ -560,7 +715,7 @@ int ftx_model_create(ftx_ctx* ctx, const ftx_model_desc* d, ftx_model** out) {
             t != FTX_T_GATE && t != FTX_T_UP)
             continue;
         const ftx_tensor* w = head ? (d->output ? d->output : d->tok_embd) : d->layers[i];
-        if (!mv_supported(w->dtype, w->ne[0], 1)) continue;
+        if (!w || !mv_supported(w->dtype, w->ne[0], 1)) continue;
         const int rpt = mv_tile_rows(w->nrows, ctx->cu_count);
         uint8_t* buf = nullptr;
         if (!dalloc(&buf, mv_tiled_bytes(w->dtype, w->nrows, w->ne[0], rpt))) {
@@ -582,6 +737,7 @@ int ftx_model_create(ftx_ctx* ctx, const ftx_model_desc* d, ftx_model** out) {
             t != FTX_T_GATE && t != FTX_T_UP)
             continue;
         const ftx_tensor* w = head ? (d->output ? d->output : d->tok_embd) : d->layers[i];
+        if (!w) continue;
         const int pdt = planar_dtype(w->dtype, w->ne[0]);
         if (pdt < 0 || w->row_bytes * 32 != w->ne[0] * (w->dtype == FTX_Q8_0 ? 34 : 18)) continue;
         uint8_t* buf = nullptr;
@@ -611,6 +767,69 @@ int ftx_model_create(ftx_ctx* ctx, const ftx_model_desc* d, ftx_model** out) {
         pf = std::max(pf, mm_down_part_floats(Mp, d->n_ff, D, cu));
         ok = dalloc(&m->mm_act, mm_act_halves(Mp, Kmax)) && dalloc(&m->mm_part, pf);
         m->mm_part_n = pf;
+    }
+    // attention extras as F32 vectors (absent parts of a present bias are zero)
+    m->attn_bias.assign((size_t)d->n_layer, nullptr);
+    m->qnorm.assign((size_t)d->n_layer, nullptr);
+    m->knorm.assign((size_t)d->n_layer, nullptr);
+    auto vec_f32 = [&](const ftx_tensor* t, float* dst) {
+        return launch_dequant(ctx->stream, t->data, t->dtype, t->row_bytes, t->ne[0], t->nrows,
+                              dst) == hipSuccess;
+    };
+    for (int64_t l = 0; ok && l < d->n_layer; ++l) {
+        const ftx_tensor* const* X = m->ext.data() + l * FTX_LAYER_EXT;
+        if (X[FTX_X_Q_BIAS] || X[FTX_X_K_BIAS] || X[FTX_X_V_BIAS]) {
+            ok = dalloc(&m->attn_bias[l], (size_t)m->ldq) &&
+                 hipMemsetAsync(m->attn_bias[l], 0, (size_t)m->ldq * 4, ctx->stream) == hipSuccess;
+            const int64_t at[3] = {0, qdim, qdim + kdim};
+            for (int i = 0; ok && i < 3; ++i)
+                if (X[FTX_X_Q_BIAS + i]) ok = vec_f32(X[FTX_X_Q_BIAS + i], m->attn_bias[l] + at[i]);
+        }
+        if (ok && X[FTX_X_Q_NORM])
+            ok = dalloc(&m->qnorm[l], (size_t)d->head_dim) && vec_f32(X[FTX_X_Q_NORM], m->qnorm[l]);
+        if (ok && X[FTX_X_K_NORM])
+            ok = dalloc(&m->knorm[l], (size_t)d->head_dim) && vec_f32(X[FTX_X_K_NORM], m->knorm[l]);
+    }
+    // MoE: per-layer copies and the shared buffers
+    m->moe_gate.assign((size_t)d->n_layer, nullptr);
+    m->moe_up.assign((size_t)d->n_layer, nullptr);
+    m->moe_down.assign((size_t)d->n_layer, nullptr);
+    m->moe_gu_dt.assign((size_t)d->n_layer, -1);
+    m->moe_rbias.assign((size_t)d->n_layer, nullptr);
+    for (int64_t l = 0; ok && any_moe && l < d->n_layer; ++l) {
+        const ftx_tensor* const* X = m->ext.data() + l * FTX_LAYER_EXT;
+        if (!X[FTX_X_GATE_INP]) continue;
+        const ftx_tensor *ge = X[FTX_X_GATE_EXPS], *ue = X[FTX_X_UP_EXPS], *de = X[FTX_X_DOWN_EXPS];
+        m->moe_gu_dt[l] = planar_dtype(ge->dtype, D);
+        const size_t gub = (size_t)(ge->row_bytes * ge->nrows);
+        ok = dalloc(&m->moe_gate[l], gub) && dalloc(&m->moe_up[l], gub) &&
+             dalloc(&m->moe_down[l], moe_down_tiled_bytes(de->dtype, d->n_ff, D, E));
+        ok = ok &&
+             launch_planar(ctx->stream, ge->data, ge->dtype, ge->nrows, D, m->moe_gate[l]) == hipSuccess &&
+             launch_planar(ctx->stream, ue->data, ue->dtype, ue->nrows, D, m->moe_up[l]) == hipSuccess &&
+             launch_moe_down_tile(ctx->stream, de->data, de->dtype, d->n_ff, D, E, m->moe_down[l]) ==
+                 hipSuccess;
+        if (ok && X[FTX_X_ROUTER_BIAS])
+            ok = dalloc(&m->moe_rbias[l], (size_t)E) && vec_f32(X[FTX_X_ROUTER_BIAS], m->moe_rbias[l]);
+    }
+    if (ok && any_moe) {
+        const int64_t T = moe_tiles_max(Mmax, E, U), rows = T * 64;
+        const int cu = ctx->cu_count;
+        // gate / up partials and the down partials share one buffer, sized
+        // for every step size up to Mmax (the split counts depend on it)
+        size_t pn = 0;
+        for (int64_t mt = 1; mt <= Mmax; ++mt) {
+            const int64_t t = moe_tiles_max(mt, E, U), r = t * 64;
+            const int S = moe_down_splits(d->n_ff, D, t, cu);
+            const size_t gu = mm_part_floats(r, 2 * d->n_ff, D / 256, (2 * d->n_ff + 255) / 256, cu);
+            pn = std::max({pn, gu, (size_t)r * 2 * (size_t)d->n_ff, (size_t)S * r * D});
+        }
+        m->moe_part_n = pn;
+        ok = dalloc(&m->router, (size_t)(Mmax * E)) &&
+             dalloc((uint8_t**)&m->route, moe_route_bytes(Mmax, E, U)) &&
+             dalloc(&m->moe_act, mm_act_halves(rows, D)) &&
+             dalloc(&m->moe_h, (size_t)(2 * rows * d->n_ff)) && dalloc(&m->moe_part, m->moe_part_n) &&
+             (!F_sh || dalloc(&m->tmpo, (size_t)(Mmax * D)));
     }
     if (!ok) {
         model_release(m);
@@ -811,7 +1030,7 @@ int ftx_verify_step(ftx_ctx* ctx, ftx_model* m, ftx_kv* kv, const ftx_verify_arg
         int rc = check_seq(ctx, m, kv, M, a->tokens);
         if (rc) return rc;
     }
-    if (M > 8) {
+    if (M > 8 || m->has_ext) {
         const ftx_seq_args sa{kv, M, a->tokens, a->parents, a->logits, a->advance, 0};
         return verify_large(ctx, m, &sa, 1);
     }

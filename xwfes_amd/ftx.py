@@ -22,6 +22,9 @@ KV_F32, KV_F16 = 0, 1
 SAMPLER_SEED = 0x9E3779B97F4A7C15
 ACCEPT_GREEDY, ACCEPT_RATIO, ACCEPT_RESIDUAL = 0, 1, 2
 LAYER_TENSORS = ("attn_norm", "q", "k", "v", "o", "ffn_norm", "gate", "up", "down")
+# optional per-layer tensors in the order of FTX_X_* (include/ftx.h)
+LAYER_EXT = ("q_bias", "k_bias", "v_bias", "q_norm", "k_norm", "gate_inp", "gate_exps",
+             "up_exps", "down_exps", "router_bias", "gate_sh", "up_sh", "down_sh")
 ERRORS = {-1: "invalid argument", -2: "unsupported", -3: "device error", -4: "out of memory",
           -5: "out of range"}
 
@@ -53,7 +56,8 @@ class ModelDesc(C.Structure):
                 ("head_dim", _i64), ("n_ff", _i64), ("vocab", _i64), ("rms_eps", C.c_float),
                 ("rope_neox", C.c_int32), ("rope_theta", C.c_double), ("tok_embd", _vp),
                 ("out_norm", _vp), ("output", _vp), ("layers", C.POINTER(_vp)),
-                ("max_tokens", _i64)]
+                ("max_tokens", _i64), ("layer_ext", C.POINTER(_vp)), ("n_expert", _i64),
+                ("n_expert_used", _i64)]
 
 
 class VerifyArgs(C.Structure):
@@ -302,19 +306,31 @@ class Context:
 
     # ---- verify path ----
     def model(self, cfg, tensors, max_tokens=64):
-        """cfg: dict of hyper-parameters; tensors: name -> Tensor with names
-        tok_embd, out_norm, output (optional) and blk.<l>.<attn_norm|q|...>."""
+        """cfg: dict of hyper-parameters (n_expert / n_expert_used for MoE);
+        tensors: name -> Tensor with names tok_embd, out_norm, output
+        (optional) and blk.<l>.<role> for the roles of LAYER_TENSORS (the
+        dense FFN ones absent on MoE layers) and of LAYER_EXT (optional)."""
         L = cfg["n_layer"]
-        lay = (_vp * (L * 9))()
+        nt, nx = len(LAYER_TENSORS), len(LAYER_EXT)
+        lay = (_vp * (L * nt))()
+        ext = (_vp * (L * nx))()
+        has_ext = False
         for l in range(L):
             for i, nm in enumerate(LAYER_TENSORS):
-                lay[l * 9 + i] = tensors["blk.%d.%s" % (l, nm)].handle
+                t = tensors.get("blk.%d.%s" % (l, nm))
+                lay[l * nt + i] = t.handle if t is not None else None
+            for i, nm in enumerate(LAYER_EXT):
+                t = tensors.get("blk.%d.%s" % (l, nm))
+                ext[l * nx + i] = t.handle if t is not None else None
+                has_ext |= t is not None
         out_t = tensors.get("output")
         d = ModelDesc(cfg["n_layer"], cfg["n_embd"], cfg["n_head"], cfg["n_head_kv"],
                       cfg["head_dim"], cfg["n_ff"], cfg["vocab"], cfg.get("rms_eps", 1e-5),
                       int(cfg.get("rope_neox", 0)), cfg.get("rope_theta", 10000.0),
                       tensors["tok_embd"].handle, tensors["out_norm"].handle,
-                      out_t.handle if out_t is not None else None, lay, max_tokens)
+                      out_t.handle if out_t is not None else None, lay, max_tokens,
+                      ext if has_ext else None, cfg.get("n_expert", 0),
+                      cfg.get("n_expert_used", 0))
         h = _vp()
         self.check(self.lib.ftx_model_create(self.h, C.byref(d), C.byref(h)))
         return Model(self, h.value, cfg, tensors)
