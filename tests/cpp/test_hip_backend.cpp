@@ -348,7 +348,8 @@ static void test_gguf_verifier(HipBackend& be, const char* path) {
     GgufConfig gc = config_from_gguf(g);
     ModelConfig& c = gc.cfg;
     ModelWeights w = weights_from_gguf(g, c);
-    CHECK(c.n_ff == w.layers[0][6].rows(), "n_ff from the gate rows");
+    CHECK(w.layers[0][6].data ? c.n_ff == w.layers[0][6].rows() : c.n_expert > 1,
+          "n_ff from the gate rows");
     const int64_t cap = 64, npast = 9, M = 5;
     const int64_t kdim = c.n_head_kv * c.head_dim;
     {
@@ -358,17 +359,20 @@ static void test_gguf_verifier(HipBackend& be, const char* path) {
     for (auto& v : vc) v = orc_float_to_half(rnd());
     ver.write_kv(kc.data(), vc.data());
     ver.truncate_to(npast);
+    // the oracle takes every tensor as ne0 columns of all its rows
     auto ot = [](const HostTensor& t) {
         orc_tensor o{};
         o.data = t.data;
         o.dtype = (int32_t)t.dtype;
         o.ne0 = t.ne[0];
-        o.ne1 = t.ne[1];
+        o.ne1 = t.ne[1] * t.ne[2] * t.ne[3];
         return o;
     };
-    std::vector<orc_tensor> ol;
+    std::vector<orc_tensor> ol, ox;
     for (const auto& L : w.layers)
         for (const auto& t : L) ol.push_back(ot(t));
+    for (const auto& X : w.ext)
+        for (const auto& t : X) ox.push_back(ot(t));
     orc_model om{};
     om.n_layer = c.n_layer;
     om.n_embd = c.n_embd;
@@ -384,6 +388,9 @@ static void test_gguf_verifier(HipBackend& be, const char* path) {
     om.out_norm = ot(w.out_norm);
     om.output = ot(w.output);
     om.layers = ol.data();
+    om.ext = ox.empty() ? nullptr : ox.data();
+    om.n_expert = c.n_expert;
+    om.n_expert_used = c.n_expert_used;
     const std::vector<int32_t> toks = {1, (int32_t)c.vocab - 1, 7, 0, 3};
     const float* dev = ver.extend_verify(toks);
     std::vector<float> got((size_t)(M * c.vocab)), want(got.size());

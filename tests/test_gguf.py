@@ -101,8 +101,8 @@ def test_writer_reader_roundtrip(tmp_path, orc):
         for name, t in model.items():
             if name == "cfg":
                 continue
-            info, ne0, rows = roles[name]
-            assert (ne0, rows, info.dtype) == (t["ne0"], t["ne1"], t["dtype"]), name
+            info, ne = roles[name]
+            assert (ne, info.dtype) == ((t["ne0"], t["ne1"]), t["dtype"]), name
             assert np.array_equal(g.data(info.name), np.ascontiguousarray(t["raw"]).view(np.uint8).ravel())
         assert all(t.offset % 32 == 0 for t in g.tensors.values())
 
@@ -196,22 +196,58 @@ def test_malformed_files_rejected(tmp_path, orc, request):
 def test_model_tensors_refuses_what_it_cannot_run(tmp_path, orc):
     m = P.make_model(orc, TINY, TINY_DT, seed=2)
     tl = G.model_tensor_list(m)
-    p = str(tmp_path / "bias.gguf")
-    G.write_gguf(p, G.model_kv(TINY), tl + [("blk.1.attn_q.bias", G.F32, (64,), b"\0" * 256)])
-    with G.GgufFile(p) as g:
-        with pytest.raises(G.GgufError, match="not supported"):
-            G.model_tensors(g, G.config_from_gguf(g))
     p = str(tmp_path / "missing.gguf")
     G.write_gguf(p, G.model_kv(TINY), [t for t in tl if t[0] != "blk.1.ffn_up.weight"])
     with G.GgufFile(p) as g:
         with pytest.raises(G.GgufError, match="missing up tensor at layer 1"):
             G.model_tensors(g, G.config_from_gguf(g))
+    # MoE by its metadata, without expert tensors (src/engine.cpp:353-356)
     p = str(tmp_path / "moe.gguf")
     G.write_gguf(p, G.model_kv(TINY) + [("llama.expert_count", G.T_U32, 8),
                                          ("llama.expert_used_count", G.T_U32, 2)], tl)
     with G.GgufFile(p) as g:
-        with pytest.raises(G.GgufError, match="MoE"):
+        with pytest.raises(G.GgufError, match="incomplete MoE tensors at layer 0"):
             G.model_tensors(g, G.config_from_gguf(g))
+
+
+MOE_DT = dict(TINY_DT, gate_inp=P.F32, gate_exps=P.Q4_0, up_exps=P.Q4_0, down_exps=P.Q4_0,
+              gate_sh=P.Q8_0, up_sh=P.Q8_0, down_sh=P.Q8_0)
+
+
+def test_model_tensors_moe_and_extras(tmp_path, orc):
+    """Router, expert planes (three dims), router bias, shared expert and
+    the attention extras come back by role with their shapes; without the
+    expert keys the expert count comes from the planes and the routed count
+    defaults as Engine::load does (8 of >= 8 experts, else 2)."""
+    cfg = P.model_cfg(2, 64, 4, 2, 16, 32, 50, n_expert=4, n_expert_used=3)
+    ex = ("q_bias", "k_bias", "v_bias", "q_norm", "k_norm", "router_bias", "gate_sh", "up_sh",
+          "down_sh")
+    m = P.make_model(orc, cfg, MOE_DT, seed=3, extras=ex)
+    for keys, want_u in ((True, 3), (False, 2)):
+        kv = G.model_kv(cfg)
+        if not keys:
+            kv = [k for k in kv if "expert" not in k[0]]
+        p = str(tmp_path / ("m%d.gguf" % keys))
+        G.write_gguf(p, kv, G.model_tensor_list(m))
+        with G.GgufFile(p) as g:
+            c = G.config_from_gguf(g)
+            roles = G.model_tensors(g, c)
+        assert (c["n_expert"], c["n_expert_used"], c["moe"]) == (4, want_u, 1)
+        assert "blk.0.gate" not in roles
+        assert roles["blk.1.gate_exps"][1] == (64, 32, 4)
+        assert roles["blk.1.down_exps"][1] == (64, 32, 4)
+        assert roles["blk.0.gate_inp"][1] == (64, 4)
+        assert roles["blk.0.q_bias"][1] == (1, 64)  # the reference's [1, n] layout
+        assert roles["blk.0.k_norm"][1] == (16, 1)
+        assert roles["blk.1.down_sh"][1] == (64, 32)
+    # a dense model keeps the attention extras
+    d = P.make_model(orc, TINY, TINY_DT, seed=4, extras=("q_norm", "k_norm"))
+    p = str(tmp_path / "dense.gguf")
+    G.write_gguf(p, G.model_kv(TINY), G.model_tensor_list(d))
+    with G.GgufFile(p) as g:
+        c = G.config_from_gguf(g)
+        roles = G.model_tensors(g, c)
+    assert c["n_expert"] == 0 and "blk.1.q_norm" in roles and "blk.1.gate" in roles
 
 
 def test_reference_engine_steps_equal_oracle_forward(tmp_path, orc, ref):

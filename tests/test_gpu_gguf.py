@@ -19,21 +19,31 @@ ROOT = os.path.dirname(os.path.dirname(os.path.abspath(__file__)))
 BIN = os.path.join(ROOT, "tests", "cpp", "test_hip_backend")
 LOGIT_TOL = 1e-3
 
+MOE_DT = dict(tok_embd=P.F32, output=P.Q8_0, q=P.Q8_0, k=P.Q8_0, v=P.Q8_0, o=P.Q8_0,
+              gate_inp=P.F32, gate_exps=P.Q4_0, up_exps=P.Q4_0, down_exps=P.Q4_0,
+              gate_sh=P.Q8_0, up_sh=P.Q8_0, down_sh=P.Q8_0)
 MODELS = {
     # reference dtypes, the reference's [d, 1, V] embedding layout
     "tiny": (P.model_cfg(2, 64, 4, 2, 16, 96, 50, rope_theta=10000.0),
              dict(tok_embd=P.F32, output=P.Q4_1, q=P.Q4_0, k=P.Q8_0, v=P.Q4_0, o=P.Q8_0,
-                  gate=P.Q4_0, up=P.Q4_0, down=P.Q8_0), {}),
+                  gate=P.Q4_0, up=P.Q4_0, down=P.Q8_0), {}, ()),
     # K-quants on the MFMA paths (head_dim 128), neox rotation by arch name
     "kquant": (P.model_cfg(2, 1024, 8, 2, 128, 1024, 1000, rope_theta=500000.0, rope_neox=1),
                dict(tok_embd=P.Q4_K, output=P.Q6_K, q=P.Q4_K, k=P.Q4_K, v=P.Q6_K, o=P.Q4_K,
-                    gate=P.Q4_K, up=P.Q4_K, down=P.Q6_K), dict(arch="qwen2")),
+                    gate=P.Q4_K, up=P.Q4_K, down=P.Q6_K), dict(arch="qwen2"), ()),
+    # MoE (8 experts, top-2) with a router bias and a shared expert
+    "moe": (P.model_cfg(2, 256, 4, 2, 64, 256, 300, n_expert=8, n_expert_used=2), MOE_DT, {},
+            ("router_bias", "gate_sh", "up_sh", "down_sh")),
+    # q / k / v bias and per-head q / k norms, neox by arch name
+    "qwen": (P.model_cfg(2, 256, 4, 2, 64, 512, 300, rope_neox=1),
+             dict(MOE_DT, gate=P.Q8_0, up=P.Q8_0, down=P.Q4_0), dict(arch="qwen3"),
+             ("q_bias", "k_bias", "v_bias", "q_norm", "k_norm")),
 }
 
 
 def write(tmp_path, orc, name, seed=4):
-    cfg, dts, kvo = MODELS[name]
-    model = P.make_model(orc, cfg, dts, seed=seed)
+    cfg, dts, kvo, extras = MODELS[name]
+    model = P.make_model(orc, cfg, dts, seed=seed, extras=extras)
     path = str(tmp_path / (name + ".gguf"))
     G.write_gguf(path, G.model_kv(cfg, **kvo), G.model_tensor_list(model))
     return path, model

@@ -291,10 +291,12 @@ def config_from_gguf(g):
     n_ff = _kv_i(g, arch, ["expert_feed_forward_length", "feed_forward_length"], 0)
     if not (n_layer and n_embd and n_head and head_dim and vocab):
         raise GgufError("gguf: incomplete model config for arch " + arch)
+    moe = n_experts > 1 and n_expert_used > 0
     return dict(arch=arch, n_layer=n_layer, n_embd=n_embd, n_head=n_head, n_head_kv=n_head_kv,
                 head_dim=head_dim, n_ff=n_ff, vocab=vocab, ctx_train=ctx_train,
                 rms_eps=np.float32(eps).item(), rope_theta=float(theta), rope_neox=int(neox),
-                moe=int(n_experts > 1 and n_expert_used > 0))
+                moe=int(moe), n_expert=n_experts if moe else 0,
+                n_expert_used=n_expert_used if moe else 0)
 
 
 # tensor names tried per role, first found wins (src/engine.cpp:320-395)
@@ -310,36 +312,66 @@ LAYER_NAMES = {
     "up": ["blk.%d.ffn_up.weight", "blk.%d.mlp.up_proj.weight"],
     "down": ["blk.%d.ffn_down.weight", "blk.%d.mlp.down_proj.weight"],
 }
-# layer tensors the resident model has no place for (the reference applies
-# them when present): a file that holds them is refused, not run without them
-UNSUPPORTED = ["blk.%d.attn_q.bias", "blk.%d.attn_k.bias", "blk.%d.attn_v.bias",
-               "blk.%d.attn_q_norm.weight", "blk.%d.self_attn.q_norm.weight",
-               "blk.%d.attn_k_norm.weight", "blk.%d.self_attn.k_norm.weight",
-               "blk.%d.ffn_gate_inp.weight"]
+# optional layer tensors, by the roles of ftx.LAYER_EXT (src/engine.cpp:325-369)
+EXT_NAMES = {
+    "q_bias": ["blk.%d.attn_q.bias"], "k_bias": ["blk.%d.attn_k.bias"],
+    "v_bias": ["blk.%d.attn_v.bias"],
+    "q_norm": ["blk.%d.attn_q_norm.weight", "blk.%d.self_attn.q_norm.weight"],
+    "k_norm": ["blk.%d.attn_k_norm.weight", "blk.%d.self_attn.k_norm.weight"],
+    "gate_inp": ["blk.%d.ffn_gate_inp.weight"], "gate_exps": ["blk.%d.ffn_gate_exps.weight"],
+    "up_exps": ["blk.%d.ffn_up_exps.weight"], "down_exps": ["blk.%d.ffn_down_exps.weight"],
+    "router_bias": ["blk.%d.exp_probs_b.bias"], "gate_sh": ["blk.%d.ffn_gate_shexp.weight"],
+    "up_sh": ["blk.%d.ffn_up_shexp.weight"], "down_sh": ["blk.%d.ffn_down_shexp.weight"],
+}
+MOE_ROLES = ("gate_inp", "gate_exps", "up_exps", "down_exps", "router_bias", "gate_sh", "up_sh",
+             "down_sh")
+EXPERT_PLANES = ("gate_exps", "up_exps", "down_exps")
 
 
 def model_tensors(g, cfg):
-    """The dense model's tensors by role: name -> (TensorInfo, ne0, rows).
-    Fills cfg["n_ff"] from the gate rows when the metadata has none (as
-    Engine::load does).  A tensor of more than two dims is taken as a matrix
-    of all its planes' rows (the reference's 3-D embedding layout [d, 1, V]
-    is then V rows of d)."""
-    if cfg.get("moe"):
-        raise GgufError("gguf: MoE models go through ftx_expert_chunk, not the resident model")
+    """The model's tensors by role: name -> (TensorInfo, ne), ne the upload
+    shape: ne0 columns of all the tensor's rows (the reference's 3-D
+    embedding layout [d, 1, V] is V rows of d), except expert planes, which
+    keep (ne0, rows, n_expert).  MoE as Engine::load decides it
+    (src/engine.cpp:318-387): from the metadata, or from the first layer
+    with a router and expert planes (every later layer is then MoE); a MoE
+    layer has no dense FFN tensors.  Fills cfg n_ff, n_expert and
+    n_expert_used the way Engine::load does when the metadata has none."""
     out = {}
 
-    def take(role, t):
-        out[role] = (t, t.ne[0], t.rows)
+    def take(role, t, planes=False):
+        out[role] = (t, (t.ne[0], t.ne[1], t.ne[2]) if planes else (t.ne[0], t.rows))
 
+    def first(names, l):
+        return next((g.tensor(n % l) for n in names if g.tensor(n % l)), None)
+
+    moe = bool(cfg.get("moe"))
     for l in range(cfg["n_layer"]):
+        ext = {role: first(names, l) for role, names in EXT_NAMES.items()}
+        if not moe and ext["gate_inp"] is not None and ext["gate_exps"] is not None:
+            moe = True
         for role, names in LAYER_NAMES.items():
-            t = next((g.tensor(n % l) for n in names if g.tensor(n % l)), None)
+            if moe and role in ("gate", "up", "down"):
+                continue
+            t = first(names, l)
             if t is None:
                 raise GgufError("gguf: missing %s tensor at layer %d" % (role, l))
             take("blk.%d.%s" % (l, role), t)
-        for n in UNSUPPORTED:
-            if g.tensor(n % l):
-                raise GgufError("gguf: %s is not supported by the resident model" % (n % l))
+        if moe:
+            if any(ext[r] is None for r in ("gate_inp", "gate_exps", "up_exps", "down_exps")):
+                raise GgufError("gguf: incomplete MoE tensors at layer %d" % l)
+            if not cfg.get("n_expert"):
+                E = ext["gate_exps"].ne[2]
+                cfg["n_expert"], cfg["n_expert_used"] = E, (8 if E >= 8 else 2)
+            if not cfg["n_ff"]:
+                cfg["n_ff"] = ext["gate_exps"].ne[1]
+        for role, t in ext.items():
+            if t is None or (role in MOE_ROLES and not moe):
+                continue
+            take("blk.%d.%s" % (l, role), t, planes=role in EXPERT_PLANES)
+    if not moe:
+        cfg["n_expert"] = cfg["n_expert_used"] = 0
+    cfg["moe"] = int(moe)
     emb = g.tensor("token_embd.weight")
     if emb is None:
         raise GgufError("gguf: missing token_embd.weight")
@@ -350,8 +382,8 @@ def model_tensors(g, cfg):
     take("out_norm", on)
     outw = g.tensor("output.weight")
     take("output", outw if outw is not None else emb)  # tied embeddings
-    if not cfg["n_ff"]:
-        cfg["n_ff"] = out["blk.0.gate"][2]
+    if not cfg["n_ff"] and "blk.0.gate" in out:
+        cfg["n_ff"] = out["blk.0.gate"][1][1]
     return out
 
 
@@ -365,10 +397,10 @@ def load_model(ctx, path, max_tokens=8):
         roles = model_tensors(g, cfg)
         tensors = {}
         try:
-            for role, (t, ne0, rows) in roles.items():
+            for role, (t, ne) in roles.items():
                 if role == "output" and t.name == "token_embd.weight":
                     continue  # tied: the model reads tok_embd
-                tensors[role] = ctx.upload(g.data(t.name), t.dtype, (ne0, rows))
+                tensors[role] = ctx.upload(g.data(t.name), t.dtype, ne)
             model = ctx.model(cfg, tensors, max_tokens=max_tokens)
         except BaseException:
             for t in tensors.values():

@@ -395,9 +395,9 @@ GgufConfig config_from_gguf(const Gguf& g) {
     double theta = g.get_f64(a + ".rope.freq_base", 0);
     if (!theta) theta = g.get_f64("llama.rope.freq_base", 10000.0);
     c.rope_theta = theta;
-    const int64_t ne = kv_i(g, a, {"expert_count"}, 0);
-    const int64_t nu = kv_i(g, a, {"expert_used_count"}, 0);
-    r.moe = ne > 1 && nu > 0;
+    c.n_expert = kv_i(g, a, {"expert_count"}, 0);
+    c.n_expert_used = kv_i(g, a, {"expert_used_count"}, 0);
+    r.moe = c.n_expert > 1 && c.n_expert_used > 0;
     std::string al = a;
     std::transform(al.begin(), al.end(), al.begin(), [](unsigned char ch) { return (char)std::tolower(ch); });
     c.rope_neox = false;
@@ -436,9 +436,11 @@ HostTensor as_matrix(const HostTensor& t) {
 }  // namespace
 
 ModelWeights weights_from_gguf(const Gguf& g, ModelConfig& cfg) {
-    if (config_from_gguf(g).moe)
-        throw std::runtime_error("gguf: MoE models go through run_expert_chunk, not the resident model");
     ModelWeights w;
+    // src/engine.cpp:318-387: MoE from the metadata, or from the first layer
+    // holding a router and expert planes (then every later layer is MoE)
+    bool moe = cfg.n_expert > 1 && cfg.n_expert_used > 0;
+    bool any_ext = false;
     for (int64_t l = 0; l < cfg.n_layer; ++l) {
         const HostTensor* t[9] = {
             first_of(g, l, {"blk.%d.attn_norm.weight", "blk.%d.input_layernorm.weight"}),
@@ -453,22 +455,57 @@ ModelWeights weights_from_gguf(const Gguf& g, ModelConfig& cfg) {
             first_of(g, l, {"blk.%d.ffn_down.weight", "blk.%d.mlp.down_proj.weight"})};
         static const char* roles[9] = {"attn_norm", "q", "k", "v", "o", "ffn_norm", "gate", "up",
                                        "down"};
+        const HostTensor* x[FTX_LAYER_EXT] = {
+            first_of(g, l, {"blk.%d.attn_q.bias"}),
+            first_of(g, l, {"blk.%d.attn_k.bias"}),
+            first_of(g, l, {"blk.%d.attn_v.bias"}),
+            first_of(g, l, {"blk.%d.attn_q_norm.weight", "blk.%d.self_attn.q_norm.weight"}),
+            first_of(g, l, {"blk.%d.attn_k_norm.weight", "blk.%d.self_attn.k_norm.weight"}),
+            first_of(g, l, {"blk.%d.ffn_gate_inp.weight"}),
+            first_of(g, l, {"blk.%d.ffn_gate_exps.weight"}),
+            first_of(g, l, {"blk.%d.ffn_up_exps.weight"}),
+            first_of(g, l, {"blk.%d.ffn_down_exps.weight"}),
+            first_of(g, l, {"blk.%d.exp_probs_b.bias"}),
+            first_of(g, l, {"blk.%d.ffn_gate_shexp.weight"}),
+            first_of(g, l, {"blk.%d.ffn_up_shexp.weight"}),
+            first_of(g, l, {"blk.%d.ffn_down_shexp.weight"})};
+        if (!moe && x[FTX_X_GATE_INP] && x[FTX_X_GATE_EXPS]) moe = true;
         std::vector<HostTensor> L;
         for (int i = 0; i < 9; ++i) {
+            if (i >= 6 && moe) {
+                L.push_back(HostTensor{});  // the dense FFN has no place on a MoE layer
+                continue;
+            }
             if (!t[i])
                 throw std::runtime_error(std::string("gguf: missing ") + roles[i] +
                                          " tensor at layer " + std::to_string(l));
             L.push_back(as_matrix(*t[i]));
         }
-        for (const char* p : {"blk.%d.attn_q.bias", "blk.%d.attn_k.bias", "blk.%d.attn_v.bias",
-                              "blk.%d.attn_q_norm.weight", "blk.%d.self_attn.q_norm.weight",
-                              "blk.%d.attn_k_norm.weight", "blk.%d.self_attn.k_norm.weight",
-                              "blk.%d.ffn_gate_inp.weight"})
-            if (g.tensor(layer_name(p, l)))
-                throw std::runtime_error("gguf: " + layer_name(p, l) +
-                                         " is not supported by the resident model");
+        std::vector<HostTensor> X(FTX_LAYER_EXT);
+        if (moe) {
+            if (!x[FTX_X_GATE_INP] || !x[FTX_X_GATE_EXPS] || !x[FTX_X_UP_EXPS] || !x[FTX_X_DOWN_EXPS])
+                throw std::runtime_error("gguf: incomplete MoE tensors at layer " + std::to_string(l));
+            if (!cfg.n_expert) {
+                cfg.n_expert = x[FTX_X_GATE_EXPS]->ne[2];
+                cfg.n_expert_used = cfg.n_expert >= 8 ? 8 : 2;
+            }
+            if (!cfg.n_ff) cfg.n_ff = x[FTX_X_GATE_EXPS]->rows();
+        }
+        for (int i = 0; i < FTX_LAYER_EXT; ++i) {
+            if (!x[i]) continue;
+            const bool moe_part = i >= FTX_X_GATE_INP;
+            if (moe_part && !moe) continue;  // the reference reads them on MoE layers only
+            // expert planes keep their three dims; the rest are matrices
+            X[i] = (i == FTX_X_GATE_EXPS || i == FTX_X_UP_EXPS || i == FTX_X_DOWN_EXPS)
+                       ? *x[i]
+                       : as_matrix(*x[i]);
+            any_ext = true;
+        }
         w.layers.push_back(std::move(L));
+        w.ext.push_back(std::move(X));
     }
+    if (!moe) cfg.n_expert = cfg.n_expert_used = 0;
+    if (!any_ext) w.ext.clear();
     const HostTensor* e = g.tensor("token_embd.weight");
     if (!e) throw std::runtime_error("gguf: missing token_embd.weight");
     const HostTensor* on = g.tensor("output_norm.weight");
@@ -477,7 +514,7 @@ ModelWeights weights_from_gguf(const Gguf& g, ModelConfig& cfg) {
     w.out_norm = as_matrix(*on);
     const HostTensor* o = g.tensor("output.weight");
     w.output = as_matrix(o ? *o : *e);  // tied embeddings
-    if (!cfg.n_ff) cfg.n_ff = w.layers.empty() ? 0 : w.layers[0][6].rows();
+    if (!cfg.n_ff && !w.layers.empty() && w.layers[0][6].data) cfg.n_ff = w.layers[0][6].rows();
     return w;
 }
 

@@ -59,11 +59,13 @@ struct GgufConfig {
 };
 GgufConfig config_from_gguf(const Gguf& g);
 
-// the dense model's tensors by role, each as a matrix of ne[0] columns (a
-// tensor of more than two dims is taken as all its planes' rows: the
-// reference's [d, 1, V] embedding is V rows of d); fills cfg.n_ff from the
-// gate rows when the metadata has none; throws for a MoE model or for layer
-// tensors the resident model cannot apply (biases, q / k norms)
+// the model's tensors by role, each as a matrix of ne[0] columns (a tensor
+// of more than two dims is taken as all its planes' rows: the reference's
+// [d, 1, V] embedding is V rows of d) except the expert planes, which keep
+// their three dims; the optional per-layer tensors (attention bias, q / k
+// norms, MoE router, experts, router bias, shared expert) in w.ext; fills
+// cfg.n_ff (and, for MoE, n_expert / n_expert_used) as Engine::load does
+// (src/engine.cpp:318-387) when the metadata has none
 ModelWeights weights_from_gguf(const Gguf& g, ModelConfig& cfg);
 
 }  // namespace ftx_host

@@ -120,11 +120,20 @@ HipVerifier::HipVerifier(HipBackend& be, const ModelConfig& cfg, const ModelWeig
     : be_(be), cfg_(cfg), max_tokens_(max_tokens) {
     if ((int64_t)w.layers.size() != cfg.n_layer)
         throw std::runtime_error("HipVerifier: layer count does not match the config");
-    std::vector<const ftx_tensor*> layers;
+    std::vector<const ftx_tensor*> layers, ext;
     for (const auto& L : w.layers) {
         if (L.size() != FTX_LAYER_TENSORS)
             throw std::runtime_error("HipVerifier: a layer needs 9 tensors");
-        for (const auto& t : L) layers.push_back(be_.resident(t));
+        for (const auto& t : L) layers.push_back(t.data ? be_.resident(t) : nullptr);
+    }
+    if (!w.ext.empty()) {
+        if ((int64_t)w.ext.size() != cfg.n_layer)
+            throw std::runtime_error("HipVerifier: ext layer count does not match the config");
+        for (const auto& X : w.ext) {
+            if (X.size() != FTX_LAYER_EXT)
+                throw std::runtime_error("HipVerifier: a layer's ext needs FTX_LAYER_EXT entries");
+            for (const auto& t : X) ext.push_back(t.data ? be_.resident(t) : nullptr);
+        }
     }
     ftx_model_desc d{};
     d.n_layer = cfg.n_layer;
@@ -142,6 +151,9 @@ HipVerifier::HipVerifier(HipBackend& be, const ModelConfig& cfg, const ModelWeig
     d.output = w.output.data ? be_.resident(w.output) : nullptr;
     d.layers = layers.data();
     d.max_tokens = max_tokens;
+    d.layer_ext = ext.empty() ? nullptr : ext.data();
+    d.n_expert = cfg.n_expert;
+    d.n_expert_used = cfg.n_expert_used;
     be_.check(ftx_model_create(be_.ctx(), &d, &model_), "model_create");
     be_.check(ftx_kv_create(be_.ctx(), model_, ctx_cap, kv_f16 ? FTX_KV_F16 : FTX_KV_F32, &kv_),
               "kv_create");

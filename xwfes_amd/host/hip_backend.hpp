@@ -122,13 +122,19 @@ struct ModelConfig {
     float rms_eps = 1e-5f;
     bool rope_neox = false;
     double rope_theta = 10000.0;
+    // MoE layers (ModelConfig::n_experts / n_expert_used, src/graph.cpp:48-50)
+    int64_t n_expert = 0, n_expert_used = 0;
 };
 
 // per-layer tensors in the order attn_norm, q, k, v, o, ffn_norm, gate, up,
-// down (down in the reference orientation: n_ff rows of n_embd columns)
+// down (down in the reference orientation: n_ff rows of n_embd columns; the
+// three FFN tensors have data == nullptr on a MoE layer), and the optional
+// ones in the order of FTX_X_* (data == nullptr: absent; expert planes keep
+// their three dims)
 struct ModelWeights {
     HostTensor tok_embd, out_norm, output;  // output.data == nullptr: tied
     std::vector<std::vector<HostTensor>> layers;
+    std::vector<std::vector<HostTensor>> ext;  // empty, or n_layer x FTX_LAYER_EXT
 };
 
 enum class AcceptMode : int32_t {
