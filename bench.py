@@ -30,6 +30,11 @@ TINY_LLAMA = dict(n_layer=4, n_embd=512, n_head=8, n_head_kv=8, head_dim=64, n_f
                   vocab=32000, rope_theta=10000.0, rope_neox=0, rms_eps=1e-5)
 LLAMA32_1B = dict(n_layer=16, n_embd=2048, n_head=32, n_head_kv=8, head_dim=64, n_ff=8192,
                   vocab=128256, rope_theta=500000.0, rope_neox=0, rms_eps=1e-5)
+MIXTRAL_8X7B = dict(n_layer=32, n_embd=4096, n_head=32, n_head_kv=8, head_dim=128, n_ff=14336,
+                    vocab=32000, rope_theta=1e6, rope_neox=0, rms_eps=1e-5, n_expert=8,
+                    n_expert_used=2)
+LLAMA3_70B = dict(n_layer=80, n_embd=8192, n_head=64, n_head_kv=8, head_dim=128, n_ff=28672,
+                  vocab=128256, rope_theta=500000.0, rope_neox=0, rms_eps=1e-5)
 WORKLOADS = {
     # kind verify: one verify step (M draft tokens at context ctx) plus ratio
     # acceptance; decode: one Engine::step at context ctx; prefill: P prompt
@@ -56,17 +61,35 @@ WORKLOADS = {
     # Q4_K FFN
     "llama3-8b-q8attn-tree52-ctx4096": dict(kind="tree", cfg=LLAMA3_8B, mix="q8_0_attn", ctx=4096,
                                             M=52, branching=(4, 4, 2), temp=0.8),
+    # batch: `seqs` sequences verified in one step (ftx_verify_batch), each
+    # against its own cache at context ctx, then accepted one by one.
+    # Mixtral-8x7B-shaped Q4_0 MoE (8 experts top-2, all resident), 8-token
+    # linear drafts for 4 sequences at context 1024, ratio acceptance at T 0.8
+    "mixtral-8x7b-q4_0-k8x4-ctx1024": dict(kind="batch", cfg=MIXTRAL_8X7B, mix="q4_0_moe",
+                                           ctx=1024, M=8, seqs=4, tree=None, temp=0.8),
+    # Llama-3-70B-shaped Q4_K, a 64-node draft tree (depth <= 6, branching
+    # <= 4) for each of 4 sequences at context 8192, residual acceptance
+    "llama3-70b-q4k-tree64x4-ctx8192": dict(kind="batch", cfg=LLAMA3_70B, mix="q4_k", ctx=8192,
+                                            M=64, seqs=4, tree=(6, 4), temp=0.8),
 }
-DTYPES = {"q4_k_m": "q4_k/q6_k weights, f16 KV, fp32 accumulate",
-          "q4_0": "q4_0 weights (f32 embedding), f16 KV, fp32 accumulate",
-          "q8_0_attn": "q8_0 attention / q4_k FFN / q6_k head weights, f16 KV, fp32 accumulate"}
+# the arithmetic the step's projections compute in (weights enter the
+# MFMAs as their exact quantised integers; block scales on the accumulators)
+DTYPES = {"q4_k_m": "q4_k/q6_k weights x int8x2-limb activations (MFMA i8), int32/fp32 accumulate; "
+                    "f16 KV",
+          "q4_0": "q4_0 weights (f32 embedding) x fp32 activations, fp32 accumulate; f16 KV",
+          "q8_0_attn": "q8_0 / q4_k / q6_k weights x fp16 hi+lo activations (MFMA f16), fp32 "
+                       "accumulate; f16 KV",
+          "q4_0_moe": "q4_0 weights x fp16 hi+lo activations (MFMA f16), fp32 accumulate; f16 KV",
+          "q4_k": "q4_k weights x fp16 hi+lo activations (MFMA f16), fp32 accumulate; f16 KV"}
 
 
 def mix_of(name, cfg):
     from xwfes_amd import synth
     return {"q4_k_m": lambda: synth.q4_k_m_mix(cfg),
             "q4_0": lambda: synth.uniform_mix(synth.Q4_0, embd=synth.F32),
-            "q8_0_attn": lambda: synth.q8_attn_mix(cfg)}[name]()
+            "q8_0_attn": lambda: synth.q8_attn_mix(cfg),
+            "q4_0_moe": lambda: synth.uniform_mix(synth.Q4_0),
+            "q4_k": lambda: synth.uniform_mix(synth.Q4_K)}[name]()
 
 
 def draft_tree(V, branching, seed):
@@ -88,6 +111,59 @@ def draft_tree(V, branching, seed):
                 q.append(dist)
                 nxt.append(len(parents) - 1)
         level = nxt
+    return (np.array(parents, np.int32), np.array(props, np.int32),
+            np.ascontiguousarray(np.stack(q)))
+
+
+def random_tree(V, n, max_depth, max_branch, seed):
+    """An n-node draft tree in breadth-first order: each node of a level
+    below max_depth gets 1 .. max_branch children until n nodes; a node's
+    children share one Dirichlet(1) draft distribution (their q rows) and are
+    drawn from it.  A draw that stays below n nodes is redrawn from the next
+    seed."""
+    for attempt in range(100):
+        t = _random_tree(V, n, max_depth, max_branch, seed + 1000 * attempt)
+        if t is not None:
+            return t
+    raise ValueError("no %d-node tree of depth <= %d" % (n, max_depth))
+
+
+def _random_tree(V, n, max_depth, max_branch, seed):
+    rng = np.random.default_rng(seed)
+    shape = []
+    level, depth, count = [-1], 0, 0
+    while count < n and depth < max_depth:
+        nxt = []
+        for par in level:
+            for _ in range(int(rng.integers(1, max_branch + 1))):
+                if count == n:
+                    break
+                shape.append(par)
+                nxt.append(count)
+                count += 1
+        level, depth = nxt, depth + 1
+    if count < n:
+        return None
+    parents, props, q = [], [], []
+    level, depth = [-1], 0
+    rng = np.random.default_rng(seed + 1)
+    kids = {}
+    for i, par in enumerate(shape):
+        kids.setdefault(par, []).append(i)
+    while len(parents) < n and depth < max_depth:
+        nxt = []
+        for par in level:
+            if par not in kids:
+                continue
+            e = -np.log(rng.random(V))
+            dist = (e / e.sum()).astype(np.float32)
+            cdf = np.cumsum(dist.astype(np.float64))
+            for _ in kids[par]:
+                parents.append(par)
+                props.append(min(int(np.searchsorted(cdf, rng.random() * cdf[-1])), V - 1))
+                q.append(dist)
+                nxt.append(len(parents) - 1)
+        level, depth = nxt, depth + 1
     return (np.array(parents, np.int32), np.array(props, np.int32),
             np.ascontiguousarray(np.stack(q)))
 
@@ -138,11 +214,32 @@ def prefill_bytes(tensors, cfg, P, chunk):
     return total
 
 
-def cpu_baseline(ctx, tensors, cfg, ctx_len, M, props, threads):
+def cpu_model():
+    """The host CPU's model name (/proc/cpuinfo, as lscpu shows it)."""
+    try:
+        with open("/proc/cpuinfo") as f:
+            for line in f:
+                if line.startswith("model name"):
+                    return line.split(":", 1)[1].strip()
+    except OSError:
+        pass
+    return "unknown"
+
+
+def cpu_threads():
+    """Threads for the CPU baseline: the process's CPU share (OMP_NUM_THREADS
+    where the host sets it, else the CPUs this process may run on)."""
+    n = int(os.environ.get("OMP_NUM_THREADS", "0") or 0)
+    return n if n > 0 else len(os.sched_getaffinity(0))
+
+
+def cpu_baseline(ctx, tensors, cfg, ctx_len, M, props, threads, layers=(1, 2)):
     """The oracle's reference loop nest (CpuBackend::matmul, matmul_down_axpy,
     Impl::attn) timed on this host on a bounded sample: 1-layer and 2-layer
     forwards of the same weights (layer 0, tok_embd, output) at the same M and
-    context, extrapolated linearly to all layers."""
+    context, extrapolated linearly to all layers (layers=(1,): the 1-layer
+    forward and L - 1 more layers at the 1-layer model's per-layer share,
+    measured separately by the caller)."""
     sys.path.insert(0, os.path.join(ROOT, "oracle"))
     import pyoracle as P
     orc = P.Oracle()
@@ -158,7 +255,7 @@ def cpu_baseline(ctx, tensors, cfg, ctx_len, M, props, threads):
     kdim = cfg["n_head_kv"] * cfg["head_dim"]
     rng = np.random.default_rng(4)
     times = {}
-    for nl in (1, 2):
+    for nl in layers:
         model = dict(base)
         model["cfg"] = dict(cfg, n_layer=nl)
         for l in range(nl):
@@ -171,12 +268,16 @@ def cpu_baseline(ctx, tensors, cfg, ctx_len, M, props, threads):
         t0 = time.perf_counter()
         orc.forward(model, k, v, ctx_len, props)
         times[nl] = time.perf_counter() - t0
+    return times
+
+
+def cpu_summary(times, cfg, M, ctx_len, threads):
     t_layer = max(times[2] - times[1], 0.0)
     t_step = times[1] + (cfg["n_layer"] - 1) * t_layer
-    return dict(value=M / t_step, unit="verified tokens/s", cores=threads, kind="port",
-                sample="oracle forward of M=%d tokens at ctx %d over 1 and 2 layers of the same "
-                       "weights (%.2f s, %.2f s), extrapolated to %d layers: %.3f s/step"
-                       % (M, ctx_len, times[1], times[2], cfg["n_layer"], t_step))
+    return t_step, t_layer, ("oracle forward of M=%d tokens at ctx %d over 1 and 2 layers of the "
+                             "same weights (%.2f s, %.2f s) on %d threads, extrapolated to %d "
+                             "layers: %.3f s/step" % (M, ctx_len, times[1], times[2], threads,
+                                                      cfg["n_layer"], t_step))
 
 
 def measured_traffic(workload, kernel_class):
@@ -230,8 +331,13 @@ def main():
                                                         synth.weight_bytes(tensors) / 1e9))
     kind = W["kind"]
     P_tok = W.get("P", 0)
-    model = ctx.model(cfg, tensors, max_tokens=max(M, 8))
+    nseq = W.get("seqs", 1)
+    model = ctx.model(cfg, tensors, max_tokens=max(M * nseq, 8))
     kv = model.kv(max(ctx_len, P_tok + W.get("N", 0) + 16) + M + 8)
+    # batch: one cache, logits, base row and draft per sequence
+    bkv, blog, bbase, bdraft = [], [], [], []
+    if kind == "batch":
+        bkv = [kv] + [model.kv(ctx_len + M + 8) for _ in range(nseq - 1)]
     drafter = dtensors = dmodel = dkv = None
     gen_stats = []
     if kind == "generate":
@@ -241,10 +347,11 @@ def main():
         dkv = dmodel.kv(P_tok + W["N"] + 32)
         drafter = spec.DraftModelDrafter(ctx, dmodel, dkv)
         log("draft model built (%.3f GB of weights)" % (synth.weight_bytes(dtensors) / 1e9))
-    kp, vp, _ = kv.pointers()
-    n_kv = cfg["n_layer"] * kv.cap_alloc * cfg["n_head_kv"] * cfg["head_dim"]
-    ctx.fill_normal(kp, n_kv, seed=4, std=1.0, dtype=ftx.F16)
-    ctx.fill_normal(vp, n_kv, seed=5, std=1.0, dtype=ftx.F16)
+    for i, c in enumerate(bkv or [kv]):
+        kp, vp, _ = c.pointers()
+        n_kv = cfg["n_layer"] * c.cap_alloc * cfg["n_head_kv"] * cfg["head_dim"]
+        ctx.fill_normal(kp, n_kv, seed=4 + 2 * i, std=1.0, dtype=ftx.F16)
+        ctx.fill_normal(vp, n_kv, seed=5 + 2 * i, std=1.0, dtype=ftx.F16)
     logits = ctx.buffer(M * V * 4)
     base = ctx.buffer(V * 4)
     if kind in ("verify", "tree"):
@@ -260,6 +367,26 @@ def main():
         qbuf = ctx.buffer(qrows.nbytes)
         qbuf.write(qrows)
         del qrows
+    if kind == "batch":
+        for i in range(nseq):
+            blog.append(ctx.buffer(M * V * 4))
+            bbase.append(ctx.buffer(V * 4))
+            if W["tree"]:
+                par, pr, qrows = random_tree(V, M, W["tree"][0], W["tree"][1], seed=60 + i)
+                qb = ctx.buffer(qrows.nbytes)
+                qb.write(qrows)
+                del qrows
+                bdraft.append(dict(parents=par, props=pr, q=qb, pd=None))
+            else:
+                pr, pdv = draft(V, M, seed=60 + i)
+                bdraft.append(dict(parents=None, props=pr, q=None, pd=pdv))
+        # base rows: the logits of each sequence's last committed token
+        for c in bkv:
+            c.truncate(ctx_len - 1)
+        first = np.random.default_rng(3).integers(V, size=nseq)
+        model.verify_batch([(c, [int(t)], b.ptr, None, True)
+                            for c, t, b in zip(bkv, first, bbase)])
+        ctx.sync()
     prompt = [int(t) for t in np.random.default_rng(8).integers(0, V, P_tok)]
     rng_state = [5, ftx.SAMPLER_SEED]
     accepted = []
@@ -279,6 +406,22 @@ def main():
                            rng=rng_state[0], parents=parents, q_ptr=qbuf.ptr)
             rng_state[0] = r["rng"]
             accepted.append(len(r["accepted"]))
+        elif kind == "batch":
+            for c in bkv:
+                c.truncate(ctx_len)
+            model.verify_batch([(c, dr["props"], lg.ptr, dr["parents"], False)
+                                for c, dr, lg in zip(bkv, bdraft, blog)])
+            for i, (dr, lg, bs) in enumerate(zip(bdraft, blog, bbase)):
+                if dr["q"] is not None:
+                    r = ctx.accept(bs.ptr, lg.ptr, M, V, dr["props"], ftx.ACCEPT_RESIDUAL,
+                                   temp=temp, rng=rng_state[0], parents=dr["parents"],
+                                   q_ptr=dr["q"].ptr)
+                else:
+                    r = ctx.accept(bs.ptr, lg.ptr, M, V, dr["props"], ftx.ACCEPT_RATIO, temp=temp,
+                                   rng=rng_state[0], pd=dr["pd"], sampler_state=rng_state[1])
+                    rng_state[1] = r["sampler_state"]
+                rng_state[0] = r["rng"]
+                accepted.append(len(r["accepted"]))
         elif kind == "decode":
             kv.truncate(ctx_len)
             model.step(kv, int(props[0]), logits.ptr)
@@ -317,19 +460,21 @@ def main():
     traced_ms = sum(e["ms"] for e in tr.values()) / max(args.trace_steps, 1)
     dom_name, dom = max(tr.items(), key=lambda kv_: kv_[1]["ms"])
     per_launch_b = dom["bytes"] / dom["launches"]
-    # the dominant class's launch time: each of its launches replayed
-    # REPLAY times back to back between the two events, so the events' own
-    # overhead (a few microseconds per bracket) is spread over the replays
+    # the dominant class's launch time inside the step (HIP events around
+    # each launch on its stream, in the steps' own order and cache state)
+    per_launch_ms = dom["ms"] / dom["launches"]
+    achieved = per_launch_b / (per_launch_ms * 1e-3) / 1e9
+    # for comparison: the same launches replayed back to back (their weights
+    # then partly cache-resident), which spreads the events' overhead
     ctx.trace_replay(dom_name, REPLAY)
     ctx.trace(True)
     step()
     rep = ctx.trace_read()[dom_name]
     ctx.trace(False)
     ctx.trace_replay(dom_name, 1)
-    per_launch_ms = rep["ms"] / rep["launches"]
-    achieved = per_launch_b / (per_launch_ms * 1e-3) / 1e9
-    log("dominant class %s: %.2f us per launch (events, %d replays), %.2f us in the step trace" % (
-        dom_name, per_launch_ms * 1e3, REPLAY, dom["ms"] / dom["launches"] * 1e3))
+    replay_ms = rep["ms"] / rep["launches"]
+    log("dominant class %s: %.2f us per launch in the step trace, %.2f us replayed x%d" % (
+        dom_name, per_launch_ms * 1e3, replay_ms * 1e3, REPLAY))
     for name, e in sorted(tr.items(), key=lambda kv_: -kv_[1]["ms"]):
         log("  %-12s %5d launches %8.3f ms/step  %7.1f GB/s" % (
             name, e["launches"] // args.trace_steps, e["ms"] / args.trace_steps,
@@ -341,6 +486,12 @@ def main():
     elif kind == "generate":
         tokens = statistics.mean(n for n, _ in gen_stats)
         sb = 0
+    elif kind == "batch":
+        # the weights once, each sequence's KV, embedding rows and logits
+        sb = step_bytes(tensors, cfg, ctx_len, M)
+        sb += (nseq - 1) * (step_bytes(tensors, cfg, ctx_len, M) - synth.weight_bytes(
+            {n: t for n, t in tensors.items() if n != "tok_embd"}))
+        tokens = M * nseq
     else:
         sb = step_bytes(tensors, cfg, ctx_len, M)
         tokens = M
@@ -350,6 +501,11 @@ def main():
               "tree": "tree verify-step tokens/s + HBM GB/s (% of peak), 8B-shape Q8_0 attention "
                       "/ Q4_K FFN, 52-node draft tree, ctx 4096, 1 GPU",
               "decode": "decode tokens/s (Engine::step, M=1, ctx 2048), 8B-shape Q4_K, 1 GPU",
+              "batch": "batched verify-step tokens/s + HBM GB/s (%% of peak), %s, %d sequences x "
+                       "%s, ctx %d, 1 GPU" % (
+                           args.workload.split("-")[0] + "-shape " + W["mix"], nseq,
+                           ("%d-node draft trees" % M) if W.get("tree") else
+                           ("%d-token drafts" % M), ctx_len),
               "prefill": "prefill tokens/s (512-token prompt, chains of 8), 8B-shape Q4_K, "
                          "1 GPU",
               "generate": "generated tokens/s (speculative: %s target, %s draft, %d draft "
@@ -358,7 +514,8 @@ def main():
                               "%d-layer d%d" % (W["draft_cfg"]["n_layer"],
                                                 W["draft_cfg"]["n_embd"]) if "draft_cfg" in W
                               else "", M)}[kind]
-    unit = {"verify": "verified tokens/s", "tree": "verified tokens/s", "decode": "decoded tokens/s",
+    unit = {"verify": "verified tokens/s", "tree": "verified tokens/s",
+            "batch": "verified tokens/s", "decode": "decoded tokens/s",
             "prefill": "prefilled tokens/s", "generate": "generated tokens/s"}[kind]
     out = {
         "metric": metric,
@@ -373,8 +530,11 @@ def main():
                 "Dirichlet(1) draft",
         "config": {"workload": args.workload, "kind": kind, "M": M, "ctx": ctx_len,
                    "prompt": P_tok, "layers": cfg["n_layer"], "d_model": cfg["n_embd"],
-                   "vocab": V, "mix": W["mix"], "accept": {"verify": "ratio", "tree": "residual"}.get(kind),
-                   "temperature": temp, "batch": 1},
+                   "vocab": V, "mix": W["mix"],
+                   "accept": {"verify": "ratio", "tree": "residual",
+                              "batch": "residual" if W.get("tree") else "ratio"}.get(kind),
+                   "temperature": temp, "batch": nseq,
+                   "experts": cfg.get("n_expert", 0), "experts_used": cfg.get("n_expert_used", 0)},
         "step_bytes": sb,
         "hbm_gbs": round(gbs, 1),
         "hbm_frac": round(gbs / HBM_PEAK_GBS, 4),
@@ -391,14 +551,27 @@ def main():
                      "peak": HBM_PEAK_GBS, "unit": "GB/s",
                      "frac": round(achieved / HBM_PEAK_GBS, 4),
                      "bytes_per_launch": per_launch_b, "us_per_launch": round(per_launch_ms * 1e3, 2),
-                     "replays": REPLAY,
+                     "source": "in-step HIP events",
+                     "replay_us_per_launch": round(replay_ms * 1e3, 2), "replays": REPLAY,
                      "traffic": measured_traffic(args.workload, dom_name)},
         "cpu_baseline": None,
     }
     if not args.no_cpu_baseline and kind == "verify":
-        threads = min(16, os.cpu_count() or 1)
+        threads = cpu_threads()
         t0 = time.perf_counter()
-        out["cpu_baseline"] = cpu_baseline(ctx, tensors, cfg, ctx_len, M, props, threads)
+        times = cpu_baseline(ctx, tensors, cfg, ctx_len, M, props, threads)
+        t_step, t_layer, sample = cpu_summary(times, cfg, M, ctx_len, threads)
+        # one thread: the 1-layer forward, the per-layer time scaled by the
+        # multi-thread run's layer / 1-layer ratio (the layer work splits
+        # over threads the same way as the head's)
+        t1 = cpu_baseline(ctx, tensors, cfg, ctx_len, M, props, 1, layers=(1,))[1]
+        t_step1 = t1 * t_step / times[1]
+        out["cpu_baseline"] = dict(
+            value=round(M / t_step, 3), unit="verified tokens/s", cores=threads, kind="port",
+            sample=sample, single_thread_value=round(M / t_step1, 4),
+            single_thread_sample="1-layer forward on 1 thread %.2f s, scaled by the %d-thread "
+                                 "step / 1-layer ratio" % (t1, threads),
+            nproc=os.cpu_count(), cpu_model=cpu_model())
         log("cpu baseline in %.1f s" % (time.perf_counter() - t0))
     print(json.dumps(out), flush=True)
     if drafter is not None:
@@ -408,6 +581,8 @@ def main():
         synth.free(dtensors)
     if qbuf is not None:
         qbuf.free()
+    for b in blog + bbase + [dr["q"] for dr in bdraft if dr["q"] is not None] + bkv[1:]:
+        b.free()
     logits.free()
     base.free()
     kv.free()

@@ -15,22 +15,31 @@ F32, F16, Q4_0, Q8_0, Q4_K, Q6_K = ftx.F32, ftx.F16, ftx.Q4_0, ftx.Q8_0, ftx.Q4_
 
 
 def model_cfg(n_layer, n_embd, n_head, n_head_kv, head_dim, n_ff, vocab, rope_theta=10000.0,
-              rope_neox=0, rms_eps=1e-5):
+              rope_neox=0, rms_eps=1e-5, n_expert=0, n_expert_used=0):
     return dict(n_layer=n_layer, n_embd=n_embd, n_head=n_head, n_head_kv=n_head_kv,
                 head_dim=head_dim, n_ff=n_ff, vocab=vocab, rope_theta=rope_theta,
-                rope_neox=rope_neox, rms_eps=rms_eps)
+                rope_neox=rope_neox, rms_eps=rms_eps, n_expert=n_expert,
+                n_expert_used=n_expert_used)
 
 
 def tensor_shapes(cfg):
-    """(name, ne0 cols, ne1 rows) of every tensor of a dense llama layout."""
-    d, hd = cfg["n_embd"], cfg["head_dim"]
+    """(name, ne) of every tensor of the llama layout: ne = (cols, rows), or
+    (cols, rows, n_expert) for expert planes.  A MoE config (n_expert > 0)
+    has the router (n_expert rows) and the experts' gate / up / down planes
+    in place of the dense FFN."""
+    d, hd, F = cfg["n_embd"], cfg["head_dim"], cfg["n_ff"]
     qd, kd = cfg["n_head"] * hd, cfg["n_head_kv"] * hd
-    out = [("tok_embd", d, cfg["vocab"]), ("out_norm", d, 1), ("output", d, cfg["vocab"])]
+    E = cfg.get("n_expert", 0)
+    out = [("tok_embd", (d, cfg["vocab"])), ("out_norm", (d, 1)), ("output", (d, cfg["vocab"]))]
     for l in range(cfg["n_layer"]):
         p = "blk.%d." % l
-        out += [(p + "attn_norm", d, 1), (p + "q", d, qd), (p + "k", d, kd), (p + "v", d, kd),
-                (p + "o", qd, d), (p + "ffn_norm", d, 1), (p + "gate", d, cfg["n_ff"]),
-                (p + "up", d, cfg["n_ff"]), (p + "down", d, cfg["n_ff"])]
+        out += [(p + "attn_norm", (d, 1)), (p + "q", (d, qd)), (p + "k", (d, kd)),
+                (p + "v", (d, kd)), (p + "o", (qd, d)), (p + "ffn_norm", (d, 1))]
+        if E:
+            out += [(p + "gate_inp", (d, E)), (p + "gate_exps", (d, F, E)),
+                    (p + "up_exps", (d, F, E)), (p + "down_exps", (d, F, E))]
+        else:
+            out += [(p + "gate", (d, F)), (p + "up", (d, F)), (p + "down", (d, F))]
     return out
 
 
@@ -63,32 +72,43 @@ def q8_attn_mix(cfg):
 
 
 def uniform_mix(dt, embd=None):
+    """Every matrix in dt (the MoE router stays F32, as GGUF converters keep
+    ffn_gate_inp), the embedding in `embd` if given."""
     def dtype(name):
         if name == "tok_embd" and embd is not None:
             return embd
+        if name.endswith("gate_inp"):
+            return F32
         return dt
     return dtype
 
 
 def build(ctx, cfg, dtype_of, seed=1, std=0.02, tied=False):
     """Returns {name: ftx.Tensor}.  Norm weights are F32 vectors of
-    1 + 0.1 N(0, 1), one per layer and role."""
+    1 + 0.1 N(0, 1), one per layer and role; the MoE router is F32
+    N(0, 4 / n_embd) (router logits of a few units, so that routing varies
+    from token to token)."""
     shapes = [s for s in tensor_shapes(cfg) if not (tied and s[0] == "output")]
-    big = max(ne0 * ne1 for name, ne0, ne1 in shapes)
+    big = max(int(np.prod(ne)) for name, ne in shapes)
     scratch = ctx.buffer(big * 4)
     tensors = {}
     nrng = np.random.default_rng(seed)
     try:
-        for i, (name, ne0, ne1) in enumerate(shapes):
+        for i, (name, ne) in enumerate(shapes):
             key = name.split(".")[-1]
             if key in ("attn_norm", "ffn_norm", "out_norm"):
-                w = (1.0 + 0.1 * nrng.standard_normal(ne0)).astype(np.float32)
-                tensors[name] = ctx.upload(w.view(np.uint8), F32, (ne0, 1))
+                w = (1.0 + 0.1 * nrng.standard_normal(ne[0])).astype(np.float32)
+                tensors[name] = ctx.upload(w.view(np.uint8), F32, (ne[0], 1))
                 continue
             dt = dtype_of(name)
-            t = ctx.alloc(dt, (ne0, ne1))
-            ctx.fill_normal(scratch.ptr, ne0 * ne1, seed * 1000003 + i, std)
-            ctx.quantize(scratch.ptr, t)
+            t = ctx.alloc(dt, ne)
+            n = int(np.prod(ne))
+            sd = 2.0 / np.sqrt(ne[0]) if key == "gate_inp" else std
+            if dt == F32:
+                ctx.fill_normal(t.ptr, n, seed * 1000003 + i, sd)
+            else:
+                ctx.fill_normal(scratch.ptr, n, seed * 1000003 + i, sd)
+                ctx.quantize(scratch.ptr, t)
             tensors[name] = t
     finally:
         scratch.free()
