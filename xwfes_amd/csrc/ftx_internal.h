@@ -200,7 +200,7 @@ struct MmAct {
 };
 struct MmSeg {
     const uint8_t* W;
-    int dt;             // FTX_Q4_K (tiled), FTX_Q8_0_PLANAR or FTX_Q4_0_PLANAR
+    int dt;             // FTX_Q4_K (tiled), FTX_Q8_0_MMT or FTX_Q4_0_MMT (re-tiled copies)
     int64_t N;          // rows
     int rpt;            // Q4_K tile rows
     int64_t row_bytes;  // planar rows
@@ -223,6 +223,13 @@ hipError_t launch_mm_prep(hipStream_t st, const float* x, int64_t ldx, const flo
                           float eps, int64_t M, const MmAct& act, int weight_dt,
                           const int32_t* gather = nullptr);
 bool mm_supported(int dt, int64_t K);
+// the one-pass GEMM's copy of Q8_0 / Q4_0 weights (per 16-row tile and
+// 256-element step, every lane's bytes contiguous): its internal dtype (or
+// -1), size, and the re-tiling of nplanes planes of `rows` rows each
+int mm_tiled_dtype(int dt, int64_t K);
+size_t mm_tiled_bytes(int mdt, int64_t rows, int64_t K);
+hipError_t launch_mm_tile(hipStream_t st, const uint8_t* src, int dt, int64_t rows,
+                          int64_t nplanes, int64_t K, uint8_t* dst);
 bool mm_down_supported(int dt, int64_t n_in, int64_t N);
 // split-sum scratch of a launch over N output columns (`ntiles` 256-row
 // workgroup columns, `steps` 256-element contraction steps)
@@ -254,14 +261,17 @@ struct MoeRoute {
     int32_t* slot_tok;   // [ntile_max * 64]: token of each operand row, -1 for padding
     int32_t* comb_slot;  // [M][U]: operand rows of token m in first-use order of experts
     float* comb_w;       // [M][U]: their renormalised weights
+    int32_t* te;         // [M][U]: token m's experts, descending probability
+    float* tw;           // [M][U]: their renormalised weights
 };
 int64_t moe_tiles_max(int64_t M, int64_t E, int64_t U);
 size_t moe_route_bytes(int64_t Mmax, int64_t E, int64_t U);
 MoeRoute moe_route_view(void* buf, int64_t Mmax, int64_t E, int64_t U);
-// router [M][E] (rows of logits, turned into probabilities in place), rbias
-// [E] or null
-hipError_t launch_moe_route(hipStream_t st, float* router, const float* rbias, int64_t M,
-                            int64_t E, int64_t U, const MoeRoute& r);
+// the router (E rows of K, any stored dtype) on the ffn_norm rows xn [M][K],
+// plus rbias [E] or null, and the routing tables
+hipError_t launch_moe_route(hipStream_t st, const float* xn, int64_t K, const uint8_t* W, int dt,
+                            int64_t row_bytes, const float* rbias, int64_t M, int64_t E, int64_t U,
+                            const MoeRoute& r);
 bool moe_down_supported(int dt, int64_t F, int64_t K);
 size_t moe_down_tiled_bytes(int dt, int64_t F, int64_t K, int64_t E);
 hipError_t launch_moe_down_tile(hipStream_t st, const uint8_t* src, int dt, int64_t F, int64_t K,

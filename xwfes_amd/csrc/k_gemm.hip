@@ -214,22 +214,29 @@ struct MmW<FTX_Q4_K> {
     v4i hdr[MM_NT];    // d | dmin, 12 scale bytes of the lane's row
 };
 template <>
-struct MmW<FTX_Q8_0_PLANAR> {
-    v2i q[MM_NT][8];   // 8 quant bytes of each 32-block
+struct MmW<FTX_Q8_0_MMT> {
+    v4i q[MM_NT][4];   // 8 quant bytes of each 32-block, two blocks per vector
     v4i d[MM_NT];      // the 8 fp16 block scales
 };
 template <>
-struct MmW<FTX_Q4_0_PLANAR> {
-    uint32_t q[MM_NT][8];  // 4 quant bytes (8 nibbles) of each 32-block
+struct MmW<FTX_Q4_0_MMT> {
+    v4i q[MM_NT][2];   // 4 quant bytes (8 nibbles) of each 32-block, four blocks per vector
     v4i d[MM_NT];
 };
+
+// the re-tiled Q8_0 / Q4_0 copy (k_mm_tile): per 16-row tile and 256-element
+// step, [lane 64][bytes of the lane's 8 blocks] then [row 16][8 fp16 scales]
+__host__ __device__ constexpr int64_t mmt_lane_bytes(int dt) { return dt == FTX_Q8_0_MMT ? 64 : 32; }
+__host__ __device__ constexpr int64_t mmt_step_bytes(int dt) {
+    return 64 * mmt_lane_bytes(dt) + 16 * 16;
+}
 
 // The lane's weight addresses at step 0, computed once per wave: lane (col
 // = l % 16, kq = l / 16) of MFMA column tile t holds B[8 kq + e][col] of
 // each 32-element K-step, i.e. elements 8 kq .. 8 kq + 7 of its row.
 struct MmPtr {
-    const uint8_t* q[MM_NT];  // Q4_K: the lane's bytes of chunk 0; planar: of block 0
-    const uint8_t* h[MM_NT];  // Q4_K: its row's header; planar: its row's scales
+    const uint8_t* q[MM_NT];  // Q4_K: the lane's bytes of chunk 0; Q8_0 / Q4_0: of step 0
+    const uint8_t* h[MM_NT];  // Q4_K: its row's header; Q8_0 / Q4_0: its row's scales
     int64_t qstep, hstep;     // bytes per 256-element step
     int cstride;              // Q4_K: bytes from one 64-element chunk to the next
 };
@@ -248,18 +255,19 @@ __device__ __forceinline__ void mm_ptrs(MmPtr& p, const MmSegDev& sg, int64_t rb
             p.q[t] = tile + li * 16 + 8 * half;
             p.h[t] = tile + 4 * R * 32 + r * 16;
         } else {
-            const uint8_t* row = sg.W + n * sg.row_bytes;
-            const int64_t nb = sg.row_bytes / (DT == FTX_Q8_0_PLANAR ? 34 : 18);
-            p.q[t] = row + 2 * nb + (DT == FTX_Q8_0_PLANAR ? 8 : 4) * kq;
-            p.h[t] = row;
+            // rows past N are the zero padding of the last tile; a column
+            // tile wholly past N (results discarded) reads the last tile
+            const int64_t T = min((rbase + 16 * t) / 16, (sg.N - 1) / 16);
+            const uint8_t* tile = sg.W + T * nsb * mmt_step_bytes(DT);
+            p.q[t] = tile + (col + 16 * kq) * mmt_lane_bytes(DT);
+            p.h[t] = tile + 64 * mmt_lane_bytes(DT) + col * 16;
         }
     }
     if constexpr (DT == FTX_Q4_K) {
         p.qstep = p.hstep = (int64_t)sg.rpt * 144;
         p.cstride = sg.rpt * 32;
     } else {
-        p.qstep = DT == FTX_Q8_0_PLANAR ? 256 : 128;
-        p.hstep = 16;
+        p.qstep = p.hstep = mmt_step_bytes(DT);
         p.cstride = 0;
     }
 }
@@ -274,13 +282,13 @@ __device__ __forceinline__ void mm_load(MmW<DT>& o, const MmPtr& p, int sb) {
 #pragma unroll
             for (int c = 0; c < 4; ++c) o.qs[t][c] = *(const v2i*)(q + c * p.cstride);
             o.hdr[t] = *(const v4i*)(p.h[t] + ho);
-        } else if constexpr (DT == FTX_Q8_0_PLANAR) {
+        } else if constexpr (DT == FTX_Q8_0_MMT) {
 #pragma unroll
-            for (int b = 0; b < 8; ++b) o.q[t][b] = *(const v2i*)(q + 32 * b);
+            for (int v = 0; v < 4; ++v) o.q[t][v] = *(const v4i*)(q + 16 * v);
             o.d[t] = *(const v4i*)(p.h[t] + ho);
         } else {
 #pragma unroll
-            for (int b = 0; b < 8; ++b) o.q[t][b] = *(const uint32_t*)(q + 16 * b);
+            for (int v = 0; v < 2; ++v) o.q[t][v] = *(const v4i*)(q + 16 * v);
             o.d[t] = *(const v4i*)(p.h[t] + ho);
         }
     }
@@ -444,11 +452,12 @@ __global__ void __launch_bounds__(64 * MM_WAVES)
                     for (int i = 0; i < 4; ++i) q[i] = __builtin_elementwise_fma(q[i], sc, sn);
                     bw[t] = v8h{q[0][0], q[0][1], q[1][0], q[1][1], q[2][0], q[2][1], q[3][0], q[3][1]};
                     bs[t] = 0.f;
-                } else if constexpr (DT == FTX_Q8_0_PLANAR) {
-                    bw[t] = i8x8(wc.q[t][j]);
+                } else if constexpr (DT == FTX_Q8_0_MMT) {
+                    const v4i qv = wc.q[t][j >> 1];
+                    bw[t] = i8x8((j & 1) ? v2i{qv[2], qv[3]} : v2i{qv[0], qv[1]});
                     bs[t] = scale8(wc.d[t], j);
                 } else {
-                    bw[t] = nib8(wc.q[t][j], 8.f);
+                    bw[t] = nib8((uint32_t)wc.q[t][j >> 2][j & 3], 8.f);
                     bs[t] = scale8(wc.d[t], j);
                 }
             }
@@ -722,6 +731,42 @@ k_mm_down(MmDownArgs a) {
         }
 }
 
+// ---------------------------------------------------------------- re-tile
+// Q8_0 / Q4_0 rows (planes of `rows` rows, nplanes of them) into the
+// one-pass GEMM's tiles: thread (plane, tile T, step s, lane l) copies the
+// lane's bytes of the step's 8 blocks (row 16 T + l % 16, bytes 8 (l / 16) ..
+// (Q8_0) or 4 (l / 16) .. (Q4_0) of each block's quants), threads past the
+// lanes copy the tile's 16 x 8 scales; rows past `rows` are zeros.
+__global__ void __launch_bounds__(256) k_mm_tile(const uint8_t* __restrict__ src, int dt,
+                                                 int64_t rows, int64_t nplanes, int64_t K,
+                                                 uint8_t* __restrict__ dst) {
+    const int64_t nsb = K / 256, tiles = (rows + 15) / 16;
+    const int bb = dt == FTX_Q8_0_MMT ? 34 : 18;
+    const int lb = (int)mmt_lane_bytes(dt);
+    const int64_t rb = K / 32 * bb;
+    const int64_t id = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
+    if (id >= nplanes * tiles * nsb * 80) return;
+    const int64_t u = id / 80;  // (plane, tile, step)
+    const int w = (int)(id % 80);
+    const int64_t s = u % nsb, T = (u / nsb) % tiles, pl = u / (nsb * tiles);
+    uint8_t* out = dst + u * mmt_step_bytes(dt);
+    const uint8_t* plane = src + pl * rows * rb;
+    if (w < 64) {
+        const int col = w & 15, kq = w >> 4;
+        const int64_t n = 16 * T + col;
+        for (int j = 0; j < 8; ++j)
+            for (int i = 0; i < lb / 8; ++i)
+                out[w * lb + j * (lb / 8) + i] =
+                    n < rows ? plane[n * rb + (8 * s + j) * bb + 2 + kq * (lb / 8) + i] : 0;
+    } else {
+        const int r = w - 64;
+        const int64_t n = 16 * T + r;
+        for (int j = 0; j < 8; ++j)
+            for (int i = 0; i < 2; ++i)
+                out[64 * lb + r * 16 + 2 * j + i] = n < rows ? plane[n * rb + (8 * s + j) * bb + i] : 0;
+    }
+}
+
 // ---------------------------------------------------------------- reduce
 // out[m][n] (= or +=) sum_ks part[ks][m][n] in split order; SwiGLU:
 // out[m][n] = silu(g) * u with g, u the sums of columns n and n + N
@@ -803,14 +848,33 @@ hipError_t launch_mm_prep(hipStream_t st, const float* x, int64_t ldx, const flo
         return hipErrorInvalidValue;
     hipLaunchKernelGGL(k_mm_prep, dim3((unsigned)act.Mp, (unsigned)((act.K + 1023) / 1024)),
                        dim3(256), 0, st, x, ldx, normw, eps,
-                       act.K, (int)M, weight_dt == FTX_Q4_0_PLANAR ? 1 : 0, gather, act.xh,
+                       act.K, (int)M, weight_dt == FTX_Q4_0_MMT ? 1 : 0, gather, act.xh,
                        act.xl, act.sh, act.sl);
     return hipGetLastError();
 }
 
 bool mm_supported(int dt, int64_t K) {
-    return (dt == FTX_Q4_K || dt == FTX_Q8_0_PLANAR || dt == FTX_Q4_0_PLANAR) && K % 256 == 0 &&
+    return (dt == FTX_Q4_K || dt == FTX_Q8_0_MMT || dt == FTX_Q4_0_MMT) && K % 256 == 0 &&
            K >= 256;
+}
+
+int mm_tiled_dtype(int dt, int64_t K) {
+    if (K % 256) return -1;
+    return dt == FTX_Q8_0 ? FTX_Q8_0_MMT : (dt == FTX_Q4_0 ? FTX_Q4_0_MMT : -1);
+}
+
+size_t mm_tiled_bytes(int mdt, int64_t rows, int64_t K) {
+    return (size_t)((rows + 15) / 16) * (size_t)(K / 256) * (size_t)mmt_step_bytes(mdt);
+}
+
+hipError_t launch_mm_tile(hipStream_t st, const uint8_t* src, int dt, int64_t rows,
+                          int64_t nplanes, int64_t K, uint8_t* dst) {
+    const int mdt = mm_tiled_dtype(dt, K);
+    if (mdt < 0 || rows < 1 || nplanes < 1) return hipErrorInvalidValue;
+    const int64_t n = nplanes * ((rows + 15) / 16) * (K / 256) * 80;
+    hipLaunchKernelGGL(k_mm_tile, dim3((unsigned)((n + 255) / 256)), dim3(256), 0, st, src, mdt,
+                       rows, nplanes, K, dst);
+    return hipGetLastError();
 }
 
 bool mm_down_supported(int dt, int64_t n_in, int64_t N) {
@@ -914,14 +978,14 @@ static hipError_t mm_launch(hipStream_t st, const MmSeg* segs, int nseg, const M
     const dim3 grid((unsigned)wg, (unsigned)mt, (unsigned)S);
     constexpr size_t lds = 2 * 65536;
     using K_t = void (*)(MmArgs);
-    const K_t kern = xtab ? (dt == FTX_Q4_K          ? k_mm<FTX_Q4_K, true>
-                             : dt == FTX_Q8_0_PLANAR ? k_mm<FTX_Q8_0_PLANAR, true>
-                                                     : k_mm<FTX_Q4_0_PLANAR, true>)
-                          : (dt == FTX_Q4_K          ? k_mm<FTX_Q4_K, false>
-                             : dt == FTX_Q8_0_PLANAR ? k_mm<FTX_Q8_0_PLANAR, false>
-                                                     : k_mm<FTX_Q4_0_PLANAR, false>);
+    const K_t kern = xtab ? (dt == FTX_Q4_K       ? k_mm<FTX_Q4_K, true>
+                             : dt == FTX_Q8_0_MMT ? k_mm<FTX_Q8_0_MMT, true>
+                                                  : k_mm<FTX_Q4_0_MMT, true>)
+                          : (dt == FTX_Q4_K       ? k_mm<FTX_Q4_K, false>
+                             : dt == FTX_Q8_0_MMT ? k_mm<FTX_Q8_0_MMT, false>
+                                                  : k_mm<FTX_Q4_0_MMT, false>);
     static bool lds_set[6] = {false, false, false, false, false, false};
-    const int ki = (dt == FTX_Q4_K ? 0 : (dt == FTX_Q8_0_PLANAR ? 1 : 2)) + (xtab ? 3 : 0);
+    const int ki = (dt == FTX_Q4_K ? 0 : (dt == FTX_Q8_0_MMT ? 1 : 2)) + (xtab ? 3 : 0);
     if (!lds_set[ki]) {
         hipError_t e = hipFuncSetAttribute((const void*)kern,
                                            hipFuncAttributeMaxDynamicSharedMemorySize, (int)lds);

@@ -48,59 +48,93 @@ constexpr int MOE_MAXU = 8;    // experts per token
 constexpr int MOE_TB = 1152;   // bytes of one re-tiled (pair-block, row-group) tile
 
 // ---------------------------------------------------------------- route
-// One workgroup.  Thread m (strided) takes token m: router row plus bias,
-// softmax_inplace (float max, float exp, double sum, float scale;
-// src/engine.cpp:62-72), the U largest in descending order with ties to the
-// lower index (std::partial_sort's order for distinct values), the weights
-// renormalised by their float sum (src/engine.cpp:201-215).  Then thread e
-// (strided) takes expert e: first use and token count; thread 0 lays out
-// the tiles (experts in index order, ceil(count / 64) tiles each); thread e
-// assigns its tokens' operand rows in token order; thread m orders its
-// experts by first use for the combine.
-__global__ void __launch_bounds__(256) k_moe_route(float* __restrict__ router,
-                                                   const float* __restrict__ rbias, int M, int E,
-                                                   int U, int ntile_max, MoeRoute r) {
+// Router and per-token choice, one workgroup per token m: the router row
+// (router weights dot the ffn_norm row, any stored dtype, wave sums) plus
+// the bias, then one thread: softmax_inplace (float max, float exp, double
+// sum in expert order, float scale; src/engine.cpp:62-72), the U largest in
+// descending order with ties to the lower index (std::partial_sort's order
+// for distinct values), the weights renormalised by their float sum
+// (src/engine.cpp:197-215).  Writes te[m][u] (expert), tw[m][u] (weight).
+__global__ void __launch_bounds__(256) k_moe_gate(const float* __restrict__ xn, int64_t K,
+                                                  const uint8_t* __restrict__ W, int dt,
+                                                  int64_t row_bytes, const float* __restrict__ rbias,
+                                                  int E, int U, int32_t* __restrict__ te,
+                                                  float* __restrict__ tw) {
 #pragma clang fp contract(off)
+    extern __shared__ float xs[];  // [K] then the E logits
+    float* lg = xs + K;
+    const int m = blockIdx.x, t = threadIdx.x, lane = t & 63, w = t >> 6;
+    const float* x = xn + (int64_t)m * K;
+    for (int64_t k = t; k < K; k += 256) xs[k] = x[k];
+    __syncthreads();
+    for (int e = w; e < E; e += 4) {
+        const uint8_t* row = W + (int64_t)e * row_bytes;
+        float acc = 0.f;
+        for (int64_t c = lane; c < K / 8; c += 64) {
+            float v[8];
+            dq8(row, dt, 8 * c, K, v);
+#pragma unroll
+            for (int i = 0; i < 8; ++i) acc += v[i] * xs[8 * c + i];
+        }
+#pragma unroll
+        for (int o = 32; o > 0; o >>= 1) acc += __shfl_xor(acc, o, 64);
+        if (lane == 0) lg[e] = acc;
+    }
+    __syncthreads();
+    if (t != 0) return;
+    if (rbias)
+        for (int j = 0; j < E; ++j) lg[j] = lg[j] + rbias[j];
+    float mx = lg[0];
+    for (int j = 1; j < E; ++j) mx = fmaxf(mx, lg[j]);
+    double sum = 0.0;
+    for (int j = 0; j < E; ++j) {
+        const float e = expf(lg[j] - mx);
+        lg[j] = e;
+        sum += (double)e;
+    }
+    const float inv = (float)(1.0 / sum);
+    for (int j = 0; j < E; ++j) lg[j] = lg[j] * inv;
+    int top[MOE_MAXU];
+    for (int u = 0; u < U; ++u) {
+        int best = -1;
+        float bv = 0.f;
+        for (int j = 0; j < E; ++j) {
+            bool taken = false;
+            for (int v = 0; v < u; ++v) taken |= top[v] == j;
+            if (taken) continue;
+            if (best < 0 || lg[j] > bv) {
+                best = j;
+                bv = lg[j];
+            }
+        }
+        top[u] = best;
+    }
+    float wsum = 0.f;
+    for (int u = 0; u < U; ++u) wsum = wsum + lg[top[u]];
+    const float winv = wsum > 0.f ? 1.f / wsum : 0.f;
+    for (int u = 0; u < U; ++u) {
+        te[m * U + u] = top[u];
+        tw[m * U + u] = lg[top[u]] * winv;
+    }
+}
+
+// Grouping, one workgroup: thread e (strided) takes expert e: first use over
+// (token, rank) and token count; thread 0 lays out the tiles (experts in
+// index order, ceil(count / 64) tiles each); thread e assigns its tokens'
+// operand rows in token order; thread m orders its experts by first use
+// for the combine (src/engine.cpp:210-239).
+__global__ void __launch_bounds__(256) k_moe_route(const int32_t* __restrict__ te_g,
+                                                   const float* __restrict__ tw_g, int M, int E,
+                                                   int U, int ntile_max, MoeRoute r) {
     __shared__ int te[MOE_MAXM * MOE_MAXU];
     __shared__ float tw[MOE_MAXM * MOE_MAXU];
     __shared__ int slot_of[MOE_MAXM * MOE_MAXU];
     __shared__ int firstpos[MOE_MAXE], cnt[MOE_MAXE], tile0[MOE_MAXE], rank[MOE_MAXE];
     const int t = threadIdx.x;
     const int MU = M * U;
-    for (int m = t; m < M; m += blockDim.x) {
-        float* p = router + (int64_t)m * E;
-        if (rbias)
-            for (int j = 0; j < E; ++j) p[j] = p[j] + rbias[j];
-        float mx = p[0];
-        for (int j = 1; j < E; ++j) mx = fmaxf(mx, p[j]);
-        double sum = 0.0;
-        for (int j = 0; j < E; ++j) {
-            const float e = expf(p[j] - mx);
-            p[j] = e;
-            sum += (double)e;
-        }
-        const float inv = (float)(1.0 / sum);
-        for (int j = 0; j < E; ++j) p[j] = p[j] * inv;
-        int* top = te + m * U;
-        for (int u = 0; u < U; ++u) {
-            int best = -1;
-            float bv = 0.f;
-            for (int j = 0; j < E; ++j) {
-                bool taken = false;
-                for (int v = 0; v < u; ++v) taken |= top[v] == j;
-                if (taken) continue;
-                const float pj = p[j];
-                if (best < 0 || pj > bv) {
-                    best = j;
-                    bv = pj;
-                }
-            }
-            top[u] = best;
-        }
-        float wsum = 0.f;
-        for (int u = 0; u < U; ++u) wsum = wsum + p[top[u]];
-        const float winv = wsum > 0.f ? 1.f / wsum : 0.f;
-        for (int u = 0; u < U; ++u) tw[m * U + u] = p[top[u]] * winv;
+    for (int i = t; i < MU; i += blockDim.x) {
+        te[i] = te_g[i];
+        tw[i] = tw_g[i];
     }
     __syncthreads();
     for (int e = t; e < E; e += blockDim.x) {
@@ -201,22 +235,28 @@ struct MoeDownArgs {
     const _Float16 *ah, *al;
     const int32_t* xtab;
     int64_t F, K, rows;   // rows: operand rows (ntile_max * 64)
-    int g_per_split;
+    int g_per_split;      // 32-row groups per split, a multiple of MOE_CG
     float* part;          // [S][rows][K]
 };
 
-struct MoeDownOps {
-    v4i nib;      // this lane's nibble words of the four column tiles
-    v4i s0, s1;   // d of its 8 rows in block 0 and block 1
-    v8h ah[4], al[4];
-};
+constexpr int MOE_CG = 4;  // row groups per staged chunk
+// LDS per chunk buffer: the operand fragments [ms 4][g][hi / lo][1 KB], then
+// the scales of the workgroup's four pair-blocks [P 4][g][2 blocks x 32 rows]
+constexpr int MOE_A_BYTES = 4 * MOE_CG * 2 * 1024;
+constexpr int MOE_S_BYTES = 4 * MOE_CG * 128;
+constexpr int MOE_BUF = MOE_A_BYTES + MOE_S_BYTES;
+
+typedef __attribute__((address_space(3))) void moe_lds_void;
 
 // grid = (K / 256, ntile_max, S); block = 256: wave w owns the pair-block
 // P = 4 bx + w (64 columns, four 16-column MFMA tiles) for the tile's rows
 // in use (16-row MFMA tiles, a block-uniform count) over its split's row
-// groups; the next row group's operands are loaded while the current one's
-// are multiplied.
+// groups, MOE_CG groups at a time.  Per chunk the operand fragments (of the
+// rows in use) and the workgroup's scales go to one of two LDS buffers by
+// direct loads, and each wave's nibbles to one of two register sets, all
+// issued a chunk ahead; one wait and one barrier per chunk.
 __global__ void __launch_bounds__(256) k_moe_down(MoeDownArgs a) {
+    extern __shared__ __attribute__((aligned(16))) uint8_t lds[];  // [2][MOE_BUF]
     const int tid = threadIdx.x, lane = tid & 63;
     const int w = __builtin_amdgcn_readfirstlane(tid >> 6);
     const int col = lane & 15, kq = lane >> 4;
@@ -227,50 +267,91 @@ __global__ void __launch_bounds__(256) k_moe_down(MoeDownArgs a) {
     const int64_t G = a.F / 32;
     const int64_t g0 = (int64_t)blockIdx.z * a.g_per_split;
     const int64_t g1 = min(g0 + (int64_t)a.g_per_split, G);
+    const uint8_t* wb = a.W + ex * a.plane;  // the expert's tiles
     const int64_t P = 4 * (int64_t)blockIdx.x + w;
-    const uint8_t* tb = a.W + ex * a.plane + P * G * MOE_TB;
-    // fragment (mt, g) of the operand at ((mt * G + g) * 64 + lane) * 8
+    const uint8_t* tb = wb + P * G * MOE_TB;  // this wave's pair-block
     const int64_t mt0 = (int64_t)by * 4;
-    auto load = [&](MoeDownOps& o, int64_t g) {
-        const uint8_t* t = tb + g * MOE_TB;
-        o.nib = *(const v4i*)(t + lane * 16);
-        o.s0 = *(const v4i*)(t + 1024 + 16 * kq);
-        o.s1 = *(const v4i*)(t + 1088 + 16 * kq);
+    // a group index for addresses: groups past the split's end (never
+    // multiplied) read the last group of the plane
+    auto gc = [&](int64_t g) { return g < G ? g : G - 1; };
+    auto stage = [&](int64_t c0, int buf, v4i* nib) {
+        uint8_t* L = lds + buf * MOE_BUF;
+        // fragment copies q = w + 4 i over (ms, g, hl), one direct load each
 #pragma unroll
-        for (int ms = 0; ms < 4; ++ms) {
-            if (ms >= nsub) break;
-            const int64_t f = (((mt0 + ms) * G + g) * 64 + lane) * 8;
-            o.ah[ms] = ld8h(a.ah + f);
-            o.al[ms] = ld8h(a.al + f);
+        for (int i = 0; i < 2 * MOE_CG; ++i) {
+            const int q = w + 4 * i;
+            const int ms = q / (2 * MOE_CG), g = (q / 2) % MOE_CG, hl = q & 1;
+            if (ms >= nsub || c0 + g >= g1) continue;
+            const _Float16* src =
+                (hl ? a.al : a.ah) + (((mt0 + ms) * G + c0 + g) * 64 + lane) * 8;
+            __builtin_amdgcn_global_load_lds(
+                (const void*)src, (moe_lds_void*)(L + ((ms * MOE_CG + g) * 2 + hl) * 1024), 16, 0,
+                0);
         }
+        // scales: waves 0 and 1, piece p = 64 w + lane -> pair-block p / 32,
+        // group (p / 8) % 4, 16 bytes at 16 (p % 8) of the tile's scales
+        if (w < 2) {
+            const int p = 64 * w + lane;
+            const int pw = p / (8 * MOE_CG), g = (p / 8) % MOE_CG, piece = p % 8;
+            const uint8_t* src =
+                wb + ((4 * (int64_t)blockIdx.x + pw) * G + gc(c0 + g)) * MOE_TB + 1024 + 16 * piece;
+            __builtin_amdgcn_global_load_lds((const void*)src,
+                                             (moe_lds_void*)(L + MOE_A_BYTES + 1024 * w), 16, 0, 0);
+        }
+#pragma unroll
+        for (int g = 0; g < MOE_CG; ++g) nib[g] = *(const v4i*)(tb + gc(c0 + g) * MOE_TB + lane * 16);
     };
     v4f acc[4][4];
 #pragma unroll
     for (int c = 0; c < 4; ++c)
 #pragma unroll
         for (int ms = 0; ms < 4; ++ms) acc[c][ms] = v4f{0.f, 0.f, 0.f, 0.f};
-    MoeDownOps cur, nxt;
-    if (g0 < g1) load(cur, g0);
-    for (int64_t g = g0; g < g1; ++g) {
-        if (g + 1 < g1) load(nxt, g + 1);
-        const v4i hmask = {(int)0xFFF8FFF8u, (int)0xFFF8FFF8u, (int)0xFFF8FFF8u, (int)0xFFF8FFF8u};
-        const v8h d0 = __builtin_bit_cast(v8h, cur.s0), d1 = __builtin_bit_cast(v8h, cur.s1);
-        const v8h d0h = __builtin_bit_cast(v8h, cur.s0 & hmask), d1h = __builtin_bit_cast(v8h, cur.s1 & hmask);
-        const v8h d0l = d0 - d0h, d1l = d1 - d1h;
+    const v4i hmask = {(int)0xFFF8FFF8u, (int)0xFFF8FFF8u, (int)0xFFF8FFF8u, (int)0xFFF8FFF8u};
+    auto compute = [&](int64_t c0, int buf, const v4i* nib) {
+        const uint8_t* L = lds + buf * MOE_BUF;
 #pragma unroll
-        for (int c = 0; c < 4; ++c) {
-            const v8h q = nib8((uint32_t)cur.nib[c], 8.f);
-            const v8h bh = q * (c < 2 ? d0h : d1h);
-            const v8h bl = q * (c < 2 ? d0l : d1l);
+        for (int g = 0; g < MOE_CG; ++g) {
+            if (c0 + g >= g1) break;
+            const uint8_t* sc = L + MOE_A_BYTES + (w * MOE_CG + g) * 128 + 16 * kq;
+            const v4i s0 = *(const v4i*)sc, s1 = *(const v4i*)(sc + 64);
+            const v8h d0 = __builtin_bit_cast(v8h, s0), d1 = __builtin_bit_cast(v8h, s1);
+            const v8h d0h = __builtin_bit_cast(v8h, s0 & hmask);
+            const v8h d1h = __builtin_bit_cast(v8h, s1 & hmask);
+            const v8h d0l = d0 - d0h, d1l = d1 - d1h;
+            v8h ah[4], al[4];
 #pragma unroll
             for (int ms = 0; ms < 4; ++ms) {
                 if (ms >= nsub) break;
-                acc[c][ms] = __builtin_amdgcn_mfma_f32_16x16x32_f16(cur.ah[ms], bh, acc[c][ms], 0, 0, 0);
-                acc[c][ms] = __builtin_amdgcn_mfma_f32_16x16x32_f16(cur.al[ms], bh, acc[c][ms], 0, 0, 0);
-                acc[c][ms] = __builtin_amdgcn_mfma_f32_16x16x32_f16(cur.ah[ms], bl, acc[c][ms], 0, 0, 0);
+                ah[ms] = *(const v8h*)(L + ((ms * MOE_CG + g) * 2 + 0) * 1024 + lane * 16);
+                al[ms] = *(const v8h*)(L + ((ms * MOE_CG + g) * 2 + 1) * 1024 + lane * 16);
+            }
+#pragma unroll
+            for (int c = 0; c < 4; ++c) {
+                const v8h q = nib8((uint32_t)nib[g][c], 8.f);
+                const v8h bh = q * (c < 2 ? d0h : d1h);
+                const v8h bl = q * (c < 2 ? d0l : d1l);
+#pragma unroll
+                for (int ms = 0; ms < 4; ++ms) {
+                    if (ms >= nsub) break;
+                    acc[c][ms] = __builtin_amdgcn_mfma_f32_16x16x32_f16(ah[ms], bh, acc[c][ms], 0, 0, 0);
+                    acc[c][ms] = __builtin_amdgcn_mfma_f32_16x16x32_f16(al[ms], bh, acc[c][ms], 0, 0, 0);
+                    acc[c][ms] = __builtin_amdgcn_mfma_f32_16x16x32_f16(ah[ms], bl, acc[c][ms], 0, 0, 0);
+                }
             }
         }
-        if (g + 1 < g1) cur = nxt;
+    };
+    v4i na[MOE_CG], nb[MOE_CG];
+    if (g0 < g1) stage(g0, 0, na);
+    for (int64_t c0 = g0; c0 < g1; c0 += 2 * MOE_CG) {
+        __builtin_amdgcn_s_waitcnt(0x0F70);  // this chunk's copies and nibbles
+        __syncthreads();                     // every wave is done with the other buffer
+        if (c0 + MOE_CG < g1) stage(c0 + MOE_CG, 1, nb);
+        compute(c0, 0, na);
+        if (c0 + MOE_CG >= g1) break;
+        __builtin_amdgcn_s_waitcnt(0x0F70);
+        __syncthreads();
+        if (c0 + 2 * MOE_CG < g1) stage(c0 + 2 * MOE_CG, 0, na);
+        compute(c0 + MOE_CG, 1, nb);
     }
     // lane (col, kq) holds C[4 kq + r][col]: operand row 64 by + 16 ms + 4 kq
     // + r, column 64 P + 16 c + col
@@ -330,7 +411,7 @@ static size_t align256(size_t b) { return (b + 255) & ~(size_t)255; }
 size_t moe_route_bytes(int64_t Mmax, int64_t E, int64_t U) {
     const int64_t T = moe_tiles_max(Mmax, E, U);
     return align256((size_t)(1 + 2 * T) * 4) + align256((size_t)(T * MOE_TILE) * 4) +
-           align256((size_t)(Mmax * U) * 4) * 2;
+           align256((size_t)(Mmax * U) * 4) * 4;
 }
 
 MoeRoute moe_route_view(void* buf, int64_t Mmax, int64_t E, int64_t U) {
@@ -344,15 +425,26 @@ MoeRoute moe_route_view(void* buf, int64_t Mmax, int64_t E, int64_t U) {
     r.comb_slot = (int32_t*)p;
     p += align256((size_t)(Mmax * U) * 4);
     r.comb_w = (float*)p;
+    p += align256((size_t)(Mmax * U) * 4);
+    r.te = (int32_t*)p;
+    p += align256((size_t)(Mmax * U) * 4);
+    r.tw = (float*)p;
     return r;
 }
 
-hipError_t launch_moe_route(hipStream_t st, float* router, const float* rbias, int64_t M,
-                            int64_t E, int64_t U, const MoeRoute& r) {
-    if (M < 1 || M > MOE_MAXM || E < 2 || E > MOE_MAXE || U < 1 || U > MOE_MAXU || U > E)
+hipError_t launch_moe_route(hipStream_t st, const float* xn, int64_t K, const uint8_t* W, int dt,
+                            int64_t row_bytes, const float* rbias, int64_t M, int64_t E, int64_t U,
+                            const MoeRoute& r) {
+    if (M < 1 || M > MOE_MAXM || E < 2 || E > MOE_MAXE || U < 1 || U > MOE_MAXU || U > E ||
+        K < 8 || K % 8 || (K + E) * 4 > 65536)
         return hipErrorInvalidValue;
-    hipLaunchKernelGGL(k_moe_route, dim3(1), dim3(256), 0, st, router, rbias, (int)M, (int)E,
-                       (int)U, (int)moe_tiles_max(M, E, U), r);
+    const size_t lds = (size_t)(K + E) * sizeof(float);
+    hipLaunchKernelGGL(k_moe_gate, dim3((unsigned)M), dim3(256), lds, st, xn, K, W, dt, row_bytes,
+                       rbias, (int)E, (int)U, r.te, r.tw);
+    hipError_t e = hipGetLastError();
+    if (e != hipSuccess) return e;
+    hipLaunchKernelGGL(k_moe_route, dim3(1), dim3(256), 0, st, r.te, r.tw, (int)M, (int)E, (int)U,
+                       (int)moe_tiles_max(M, E, U), r);
     return hipGetLastError();
 }
 
@@ -383,7 +475,10 @@ int moe_down_splits(int64_t F, int64_t K, int64_t ntile_max, int cu_count) {
     const int64_t G = F / 32;
     if (S > G / 8) S = G / 8;
     if (S > 32) S = 32;
-    return S < 1 ? 1 : (int)S;
+    if (S < 1) S = 1;
+    // every split a whole number of chunks, and none empty
+    const int64_t per = ((G + S - 1) / S + MOE_CG - 1) / MOE_CG * MOE_CG;
+    return (int)((G + per - 1) / per);
 }
 
 hipError_t launch_moe_down(hipStream_t st, const uint8_t* tiled, int dt, int64_t F, int64_t K,
@@ -402,13 +497,21 @@ hipError_t launch_moe_down(hipStream_t st, const uint8_t* tiled, int dt, int64_t
     a.rows = ntile_max * MOE_TILE;
     a.part = part;
     const int64_t G = F / 32;
-    a.g_per_split = (int)((G + S - 1) / S);
+    a.g_per_split = (int)(((G + S - 1) / S + MOE_CG - 1) / MOE_CG * MOE_CG);
     // the real split count: splits past the last row group would leave
     // their partial rows unwritten
     if ((int64_t)a.g_per_split * (S - 1) >= G) return hipErrorInvalidValue;
     a.plane = (K / 64) * G * MOE_TB;
+    constexpr size_t lds = 2 * MOE_BUF;
+    static bool lds_set = false;
+    if (!lds_set) {
+        hipError_t e = hipFuncSetAttribute((const void*)k_moe_down,
+                                           hipFuncAttributeMaxDynamicSharedMemorySize, (int)lds);
+        if (e != hipSuccess) return e;
+        lds_set = true;
+    }
     hipLaunchKernelGGL(k_moe_down, dim3((unsigned)(K / 256), (unsigned)ntile_max, (unsigned)S),
-                       dim3(256), 0, st, a);
+                       dim3(256), lds, st, a);
     return hipGetLastError();
 }
 

@@ -19,6 +19,10 @@
 // row holds a multiple of 4 blocks.  Never seen outside the library.
 constexpr int FTX_Q8_0_PLANAR = 108;
 constexpr int FTX_Q4_0_PLANAR = 102;
+// Q8_0 / Q4_0 re-tiled for the one-pass GEMM (k_gemm.hip): per 16-row tile
+// and 256-element step, every lane's bytes of the step contiguous
+constexpr int FTX_Q8_0_MMT = 118;
+constexpr int FTX_Q4_0_MMT = 112;
 
 __device__ __forceinline__ float h2f(uint16_t h) {
     return (float)__builtin_bit_cast(_Float16, h);

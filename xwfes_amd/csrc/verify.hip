@@ -44,6 +44,10 @@ struct ftx_model {
     // indexing; null where they do not apply) and their internal dtypes
     std::vector<uint8_t*> pln;
     std::vector<int> pln_dt;
+    // the one-pass GEMM's re-tiled copies of Q8_0 / Q4_0 projections (same
+    // indexing; null where they do not apply) and their internal dtypes
+    std::vector<uint8_t*> mmt;
+    std::vector<int> mmt_dt;
     float* downpart = nullptr;
     // large-M path (more than 8 tokens, or several sequences): activation
     // operands and split-sum partials of the k_gemm.hip launches
@@ -59,12 +63,11 @@ struct ftx_model {
     std::vector<float*> qnorm, knorm;  // [hd] per layer, or null
     // MoE layers: planar copies of the gate and up expert planes, the
     // re-tiled down planes, the router bias as F32; shared buffers for the
-    // router rows, the routing tables, the gathered operand, the down
-    // operand, split partials, and tmpo for shared experts
+    // routing tables, the gathered operand, the down operand, split partials,
+    // and tmpo for shared experts
     std::vector<uint8_t*> moe_gate, moe_up, moe_down;
     std::vector<int> moe_gu_dt;
     std::vector<float*> moe_rbias;
-    float* router = nullptr;
     void* route = nullptr;
     _Float16* moe_act = nullptr;
     _Float16* moe_h = nullptr;
@@ -133,6 +136,8 @@ static void model_release(ftx_model* m) {
         if (b) (void)hipFree(b);
     for (uint8_t* b : m->pln)
         if (b) (void)hipFree(b);
+    for (uint8_t* b : m->mmt)
+        if (b) (void)hipFree(b);
     if (m->downpart) (void)hipFree(m->downpart);
     if (m->mm_act) (void)hipFree(m->mm_act);
     if (m->mm_part) (void)hipFree(m->mm_part);
@@ -142,7 +147,7 @@ static void model_release(ftx_model* m) {
     for (auto* v : {&m->moe_gate, &m->moe_up, &m->moe_down})
         for (uint8_t* b : *v)
             if (b) (void)hipFree(b);
-    void* mb[] = {m->router, m->route, m->moe_act, m->moe_h, m->moe_part, m->tmpo};
+    void* mb[] = {m->route, m->moe_act, m->moe_h, m->moe_part, m->tmpo};
     for (void* b : mb)
         if (b) (void)hipFree(b);
     for (int i = 0; i < ftx_model::PIN_RING; ++i) {
@@ -242,8 +247,8 @@ static int verify_large(ftx_ctx* ctx, ftx_model* m, const ftx_seq_args* sq, int6
             sg = MmSeg{m->mvt[i], FTX_Q4_K, w->nrows, m->mvt_rpt[i], 0};
             return true;
         }
-        if (m->pln[i] && mm_supported(m->pln_dt[i], w->ne[0])) {
-            sg = MmSeg{m->pln[i], m->pln_dt[i], w->nrows, 0, w->row_bytes};
+        if (m->mmt[i] && mm_supported(m->mmt_dt[i], w->ne[0])) {
+            sg = MmSeg{m->mmt[i], m->mmt_dt[i], w->nrows, 0, w->row_bytes};
             return true;
         }
         return false;
@@ -342,11 +347,9 @@ static int verify_large(ftx_ctx* ctx, ftx_model* m, const ftx_seq_args* sq, int6
         const MoeRoute rt = moe_route_view(m->route, m->Mmax, E, U);
         TRACED_L(TK_RMSNORM, 2 * Md * D * f4,
                  launch_rmsnorm(st, m->x, m->norms + (l * 2 + 1) * D, D, Mt, eps, m->xn));
-        GemvSeg rs[1] = {GemvSeg{gi->data, gi->dtype, gi->row_bytes, E, m->router, E}};
-        TRACED_L(TK_MOE_ROUTE, wbytes(gi) + Md * D * f4 + Md * E * f4,
-                 launch_gemv(st, rs, 1, m->xn, D, D, Mt, EPI_STORE, true));
-        TRACED_L(TK_MOE_ROUTE, 2 * Md * E * f4,
-                 launch_moe_route(st, m->router, m->moe_rbias[l], Mt, E, U, rt));
+        TRACED_L(TK_MOE_ROUTE, wbytes(gi) + Md * D * f4 + 4.0 * Md * U * f4,
+                 launch_moe_route(st, m->xn, D, gi->data, gi->dtype, gi->row_bytes,
+                                  m->moe_rbias[l], Mt, E, U, rt));
         const int gdt = m->moe_gu_dt[l];
         const MmAct act = mm_act(m->moe_act, rows, D);
         TRACED_L(TK_XQ_PREP, Md * U * D * f4 + 4.0 * rows * D,
@@ -356,7 +359,8 @@ static int verify_large(ftx_ctx* ctx, ftx_model* m, const ftx_seq_args* sq, int6
         const double used = (double)std::min<int64_t>(E, Mt * U);
         MmSeg gs[2] = {MmSeg{m->moe_gate[l], gdt, F, 0, ge->row_bytes},
                        MmSeg{m->moe_up[l], gdt, F, 0, ge->row_bytes}};
-        const int64_t plane[2] = {F * ge->row_bytes, F * ge->row_bytes};
+        const int64_t pb = (int64_t)mm_tiled_bytes(gdt, F, D);
+        const int64_t plane[2] = {pb, pb};
         MmFragOut fo{m->moe_h, m->moe_h + rows * F, 1.f, F};
         TRACED_L(TK_GEMV_SWIGLU, 2 * used * plane_gu + Md * U * D * 4.0 + Md * U * F * 4.0,
                  launch_mm_experts(st, gs, 2, plane, act, rt.tab, T, fo, m->moe_part,
@@ -609,9 +613,10 @@ int ftx_model_create(ftx_ctx* ctx, const ftx_model_desc* d, ftx_model** out) {
         if (x(FTX_X_GATE_INP)) {
             // MoE layer (src/engine.cpp:348-369)
             any_moe = true;
-            if (E < 2 || E > 256 || U < 1 || U > 8 || U > E)
+            if (E < 2 || E > 256 || U < 1 || U > 8 || U > E || (D + E) * 4 > 65536)
                 return ftx_fail(ctx, FTX_E_UNSUPPORTED,
-                                "MoE: n_expert must be in [2, 256], n_expert_used in [1, min(8, n_expert)]");
+                                "MoE: n_expert must be in [2, 256], n_expert_used in [1, min(8, "
+                                "n_expert)], n_embd + n_expert <= 16384");
             const ftx_tensor *ge = x(FTX_X_GATE_EXPS), *ue = x(FTX_X_UP_EXPS), *de = x(FTX_X_DOWN_EXPS);
             if ((rc = need(x(FTX_X_GATE_INP), D, E, "ffn_gate_inp"))) return rc;
             if (!ge || !ue || !de)
@@ -619,8 +624,8 @@ int ftx_model_create(ftx_ctx* ctx, const ftx_model_desc* d, ftx_model** out) {
             for (const ftx_tensor* t : {ge, ue, de})
                 if (t->ne[0] != D || t->ne[1] != d->n_ff || t->ne[2] != E || t->ne[3] != 1)
                     return ftx_fail(ctx, FTX_E_INVALID, "bad shape of an expert tensor");
-            if (ge->dtype != ue->dtype || planar_dtype(ge->dtype, D) < 0 ||
-                !mm_supported(planar_dtype(ge->dtype, D), D))
+            if (ge->dtype != ue->dtype || mm_tiled_dtype(ge->dtype, D) < 0 ||
+                !mm_supported(mm_tiled_dtype(ge->dtype, D), D))
                 return ftx_fail(ctx, FTX_E_UNSUPPORTED,
                                 "MoE gate / up experts must share Q4_0 or Q8_0 with n_embd % 256 == 0");
             if (!moe_down_supported(de->dtype, d->n_ff, D))
@@ -750,6 +755,28 @@ int ftx_model_create(ftx_ctx* ctx, const ftx_model_desc* d, ftx_model** out) {
         if (launch_planar(ctx->stream, w->data, w->dtype, w->nrows, w->ne[0], buf) != hipSuccess)
             ok = false;
     }
+    m->mmt.assign(nmvt, nullptr);
+    m->mmt_dt.assign(nmvt, -1);
+    for (size_t i = 0; ok && i < nmvt; ++i) {
+        const int t = (int)(i % FTX_LAYER_TENSORS);
+        const bool head = i + 1 == nmvt;
+        if (!head && t != FTX_T_Q && t != FTX_T_K && t != FTX_T_V && t != FTX_T_O &&
+            t != FTX_T_GATE && t != FTX_T_UP)
+            continue;
+        const ftx_tensor* w = head ? (d->output ? d->output : d->tok_embd) : d->layers[i];
+        if (!w) continue;
+        const int mdt = mm_tiled_dtype(w->dtype, w->ne[0]);
+        if (mdt < 0 || !mm_supported(mdt, w->ne[0])) continue;
+        uint8_t* buf = nullptr;
+        if (!dalloc(&buf, mm_tiled_bytes(mdt, w->nrows, w->ne[0]))) {
+            ok = false;
+            break;
+        }
+        m->mmt[i] = buf;
+        m->mmt_dt[i] = mdt;
+        if (launch_mm_tile(ctx->stream, w->data, w->dtype, w->nrows, 1, w->ne[0], buf) != hipSuccess)
+            ok = false;
+    }
     // the large-M path (more than 8 tokens, or several sequences):
     // activation operands for the widest contraction and split-sum partials
     // for the widest projection (SwiGLU's gate and up sums always pass
@@ -800,13 +827,15 @@ int ftx_model_create(ftx_ctx* ctx, const ftx_model_desc* d, ftx_model** out) {
         const ftx_tensor* const* X = m->ext.data() + l * FTX_LAYER_EXT;
         if (!X[FTX_X_GATE_INP]) continue;
         const ftx_tensor *ge = X[FTX_X_GATE_EXPS], *ue = X[FTX_X_UP_EXPS], *de = X[FTX_X_DOWN_EXPS];
-        m->moe_gu_dt[l] = planar_dtype(ge->dtype, D);
-        const size_t gub = (size_t)(ge->row_bytes * ge->nrows);
+        m->moe_gu_dt[l] = mm_tiled_dtype(ge->dtype, D);
+        const size_t gub = E * mm_tiled_bytes(m->moe_gu_dt[l], d->n_ff, D);
         ok = dalloc(&m->moe_gate[l], gub) && dalloc(&m->moe_up[l], gub) &&
              dalloc(&m->moe_down[l], moe_down_tiled_bytes(de->dtype, d->n_ff, D, E));
         ok = ok &&
-             launch_planar(ctx->stream, ge->data, ge->dtype, ge->nrows, D, m->moe_gate[l]) == hipSuccess &&
-             launch_planar(ctx->stream, ue->data, ue->dtype, ue->nrows, D, m->moe_up[l]) == hipSuccess &&
+             launch_mm_tile(ctx->stream, ge->data, ge->dtype, d->n_ff, E, D, m->moe_gate[l]) ==
+                 hipSuccess &&
+             launch_mm_tile(ctx->stream, ue->data, ue->dtype, d->n_ff, E, D, m->moe_up[l]) ==
+                 hipSuccess &&
              launch_moe_down_tile(ctx->stream, de->data, de->dtype, d->n_ff, D, E, m->moe_down[l]) ==
                  hipSuccess;
         if (ok && X[FTX_X_ROUTER_BIAS])
@@ -825,8 +854,7 @@ int ftx_model_create(ftx_ctx* ctx, const ftx_model_desc* d, ftx_model** out) {
             pn = std::max({pn, gu, (size_t)r * 2 * (size_t)d->n_ff, (size_t)S * r * D});
         }
         m->moe_part_n = pn;
-        ok = dalloc(&m->router, (size_t)(Mmax * E)) &&
-             dalloc((uint8_t**)&m->route, moe_route_bytes(Mmax, E, U)) &&
+        ok = dalloc((uint8_t**)&m->route, moe_route_bytes(Mmax, E, U)) &&
              dalloc(&m->moe_act, mm_act_halves(rows, D)) &&
              dalloc(&m->moe_h, (size_t)(2 * rows * d->n_ff)) && dalloc(&m->moe_part, m->moe_part_n) &&
              (!F_sh || dalloc(&m->tmpo, (size_t)(Mmax * D)));
