@@ -249,22 +249,27 @@ struct MmFragOut {
     int64_t K;
 };
 // gate / up of the routed experts (segments gate, up with `plane` bytes per
-// expert plane) over the gathered operand `act` (ntile_max * 64 rows), tile
-// by tile of the routing's table xtab; SwiGLU into fo.
+// expert plane) over the gathered operand `act` (ntile_max * trows rows,
+// trows 16 or 64), tile by tile of the routing's table xtab; SwiGLU into fo.
 hipError_t launch_mm_experts(hipStream_t st, const MmSeg* segs, int nseg, const int64_t* plane,
                              const MmAct& act, const int32_t* xtab, int64_t ntile_max,
-                             const MmFragOut& fo, float* part, size_t part_floats, int cu_count);
+                             int64_t trows, const MmFragOut& fo, float* part, size_t part_floats,
+                             int cu_count);
 
 // MoE routing, expert ffn_down and the weighted sum (k_moe.hip)
 struct MoeRoute {
     int32_t* tab;        // [1 + 2 * ntile_max]: tiles in use, (expert, rows) per tile
-    int32_t* slot_tok;   // [ntile_max * 64]: token of each operand row, -1 for padding
+    int32_t* slot_tok;   // [ntile_max * tile rows]: token of each operand row, -1 for padding
     int32_t* comb_slot;  // [M][U]: operand rows of token m in first-use order of experts
     float* comb_w;       // [M][U]: their renormalised weights
     int32_t* te;         // [M][U]: token m's experts, descending probability
     float* tw;           // [M][U]: their renormalised weights
 };
+// rows per routing tile (16 or 64) and the tile table bound of an M-token
+// step; the largest operand row count of any step up to Mmax tokens
+int64_t moe_tile_rows(int64_t M, int64_t E, int64_t U);
 int64_t moe_tiles_max(int64_t M, int64_t E, int64_t U);
+int64_t moe_rows_max(int64_t Mmax, int64_t E, int64_t U);
 size_t moe_route_bytes(int64_t Mmax, int64_t E, int64_t U);
 MoeRoute moe_route_view(void* buf, int64_t Mmax, int64_t E, int64_t U);
 // the router (E rows of K, any stored dtype) on the ffn_norm rows xn [M][K],
@@ -277,11 +282,12 @@ size_t moe_down_tiled_bytes(int dt, int64_t F, int64_t K, int64_t E);
 hipError_t launch_moe_down_tile(hipStream_t st, const uint8_t* src, int dt, int64_t F, int64_t K,
                                 int64_t E, uint8_t* dst);
 int moe_down_splits(int64_t F, int64_t K, int64_t ntile_max, int cu_count);
-// part[S][ntile_max * 64][K] = the experts' down of the operand rows (fp16
-// hi / lo planes of h * 2^10 in fragment order, contraction F), S splits of F
+// part[S][ntile_max * trows][K] = the experts' down of the operand rows (fp16
+// hi / lo planes of h in fragment order, contraction F), S splits of F
 hipError_t launch_moe_down(hipStream_t st, const uint8_t* tiled, int dt, int64_t F, int64_t K,
                            const _Float16* ah, const _Float16* al, const int32_t* xtab,
-                           int64_t ntile_max, int S, float* part, size_t part_floats);
+                           int64_t ntile_max, int64_t trows, int S, float* part,
+                           size_t part_floats);
 // y[m][:] (+)= sum over token m's experts, in first-use order, of weight *
 // (sum_s part[s][slot][:]) / 2^10; accum = 0 stores (the MoE FFN's tmpo)
 hipError_t launch_moe_combine(hipStream_t st, const float* part, int S, int64_t rows, int64_t K,

@@ -308,6 +308,12 @@ __device__ __forceinline__ void bytes4_h(uint32_t w, v2h& lo, v2h& hi) {
 
 typedef __attribute__((address_space(3))) void lds_void;
 
+// waves per SIMD the register allocation targets: two workgroups per CU for
+// Q4_0 16-row tiles (they fit 128 registers), one otherwise (the larger
+// weight register sets of Q8_0 and Q4_K would spill at 128)
+template <int DT, int MS>
+constexpr int MM_WPE = (MS == 1 && DT == FTX_Q4_0_MMT) ? 4 : 2;
+
 // grid = (ceil(units / 8), Mp / 64, splits); block = 512.  Per 256-element
 // step the workgroup's activation fragments (4 token tiles x 8 K-steps, hi
 // and lo: 64 KB) are copied to one of two LDS buffers by direct loads (8
@@ -319,11 +325,14 @@ typedef __attribute__((address_space(3))) void lds_void;
 // XT (expert launches): grid.y walks the routing's tile table; a tile past
 // the tiles in use ends at once (the whole workgroup), the weights are the
 // tile's expert's planes, and 16-token tiles past the tile's rows in use
-// are neither copied nor multiplied (a block-uniform choice).
-template <int DT, bool XT>
+// are neither copied nor multiplied (a block-uniform choice).  MS: 16-token
+// MFMA tiles per workgroup tile (4 for 64-token tiles; 1 for the 16-row
+// expert tiles of routings with few tokens per expert, whose 32 KB of LDS
+// and smaller register set let several workgroups share a CU).
+template <int DT, bool XT, int MS>
 __global__ void __launch_bounds__(64 * MM_WAVES)
-    __attribute__((amdgpu_waves_per_eu(MM_WAVES / 4, MM_WAVES / 4))) k_mm(MmArgs a) {
-    extern __shared__ __attribute__((aligned(16))) uint8_t mm_lds[];  // [2][64 KB]
+    __attribute__((amdgpu_waves_per_eu(MM_WPE<DT, MS>, MM_WPE<DT, MS>))) k_mm(MmArgs a) {
+    extern __shared__ __attribute__((aligned(16))) uint8_t mm_lds[];  // [2][MS * 16 KB]
     const int tid = threadIdx.x, lane = tid & 63;
     const int w = __builtin_amdgcn_readfirstlane(tid >> 6);
     const int col = lane & 15, kq = lane >> 4;
@@ -332,14 +341,14 @@ __global__ void __launch_bounds__(64 * MM_WAVES)
     const int si = mm_seg_of(a, live ? u : a.units - 1);
     MmSegDev sg = a.seg[si];
     const int64_t rbase = ((live ? u : a.units - 1) - sg.unit0) * MM_WROWS;
-    const int64_t mt0 = (int64_t)blockIdx.y * MM_MS;  // first 16-token tile
-    int nsub = MM_MS, mend = a.M;  // 16-token tiles in use, rows in use end
+    const int64_t mt0 = (int64_t)blockIdx.y * MS;  // first 16-token tile
+    int nsub = MS, mend = a.M;  // 16-token tiles in use, rows in use end
     if constexpr (XT) {
         if ((int)blockIdx.y >= a.xtab[0]) return;
         const int ex = a.xtab[1 + 2 * blockIdx.y], nv = a.xtab[2 + 2 * blockIdx.y];
         sg.W += (int64_t)ex * a.plane[si];
         nsub = (nv + 15) >> 4;
-        mend = (int)blockIdx.y * MM_TOK + nv;
+        mend = (int)blockIdx.y * 16 * MS + nv;
     }
     const int ks = blockIdx.z;
     const int sb0 = ks * a.sb_per_split;
@@ -348,22 +357,24 @@ __global__ void __launch_bounds__(64 * MM_WAVES)
     MmPtr wp;
     mm_ptrs<DT>(wp, sg, rbase, a.nsb, col, kq);
 
-    // the step's 64 fragments: block b = (hl, ms, j) = 32 hl + 8 ms + j ->
-    // LDS offset b KB; wave w copies blocks BPW w .. BPW w + BPW - 1
-    constexpr int BPW = 64 / MM_WAVES;
-    const int b0 = BPW * w, hl0 = b0 >> 5, ms0 = (b0 >> 3) & 3;
+    // the step's 16 MS fragments: block b = (hl, ms, j) = 8 (MS hl + ms) + j
+    // -> LDS offset b KB; wave w copies blocks BPW w .. BPW w + BPW - 1 (one
+    // (hl, ms) per wave: BPW divides 8)
+    constexpr int BPW = 16 * MS / MM_WAVES;
+    constexpr int BUF = MS * 16384;
+    const int b0 = BPW * w, hl0 = b0 / (8 * MS), ms0 = (b0 / 8) % MS, j0 = b0 % 8;
     const _Float16* gsrc = (hl0 ? a.xl : a.xh) + ((mt0 + ms0) * nks * 64 + lane) * 8;
     auto stage = [&](int sb, int buf) {
         if (XT && ms0 >= nsub) return;  // this wave's blocks belong to an unused token tile
-        const _Float16* src = gsrc + (int64_t)sb * 8 * 64 * 8;
+        const _Float16* src = gsrc + ((int64_t)sb * 8 + j0) * 64 * 8;
 #pragma unroll
         for (int i = 0; i < BPW; ++i)
-            __builtin_amdgcn_global_load_lds(
-                (const void*)(src + ((i >> 3) * nks + (i & 7)) * 64 * 8),
-                (lds_void*)(mm_lds + buf * 65536 + (b0 + i) * 1024), 16, 0, 0);
+            __builtin_amdgcn_global_load_lds((const void*)(src + i * 64 * 8),
+                                             (lds_void*)(mm_lds + buf * BUF + (b0 + i) * 1024), 16,
+                                             0, 0);
     };
     auto frag = [&](int buf, int hl, int ms, int j) -> v8h {
-        return *(const v8h*)(mm_lds + buf * 65536 + ((hl * 4 + ms) * 8 + j) * 1024 + lane * 16);
+        return *(const v8h*)(mm_lds + buf * BUF + ((hl * MS + ms) * 8 + j) * 1024 + lane * 16);
     };
     // Q4_K min term: this lane's sub-block sums (K slots of the 16x16x16
     // operand; zero for kq >= 2)
@@ -371,11 +382,11 @@ __global__ void __launch_bounds__(64 * MM_WAVES)
     const _Float16* xs0 = a.sh + (mt0 * a.nsb * 32 + (lane & 31)) * 4;
     const _Float16* xl0 = a.sl + (mt0 * a.nsb * 32 + (lane & 31)) * 4;
 
-    v4f acc[MM_NT][MM_MS];
+    v4f acc[MM_NT][MS];
 #pragma unroll
     for (int t = 0; t < MM_NT; ++t)
 #pragma unroll
-        for (int ms = 0; ms < MM_MS; ++ms) acc[t][ms] = v4f{0.f, 0.f, 0.f, 0.f};
+        for (int ms = 0; ms < MS; ++ms) acc[t][ms] = v4f{0.f, 0.f, 0.f, 0.f};
     const v4f zero4 = {0.f, 0.f, 0.f, 0.f};
 
     // one 256-element step from LDS buffer `buf` with weights `wc`; the
@@ -387,12 +398,12 @@ __global__ void __launch_bounds__(64 * MM_WAVES)
             stage(sb + 1, buf ^ 1);
             mm_load<DT>(wn, wp, sb + 1);
         }
-        v4h xsh[MM_MS], xsl[MM_MS];
+        v4h xsh[MS], xsl[MS];
         v2h scp[MM_NT][4], scn[MM_NT][4];  // Q4_K: sc and -1024 sc per sub-block, fp16 pairs
         v4h mnh[MM_NT];                    // Q4_K: the 4 mins of the lane's K slots
         if constexpr (DT == FTX_Q4_K) {
 #pragma unroll
-            for (int ms = 0; ms < MM_MS; ++ms) {
+            for (int ms = 0; ms < MS; ++ms) {
                 if (XT && ms >= nsub) break;
                 const int64_t o = ((int64_t)ms * a.nsb + sb) * 32 * 4;
                 const v4h hh = *(const v4h*)(xs0 + o), ll = *(const v4h*)(xl0 + o);
@@ -415,14 +426,14 @@ __global__ void __launch_bounds__(64 * MM_WAVES)
                 for (int i = 0; i < 4; ++i) scn[t][i] = scp[t][i] * v2h{(_Float16)(-1024.f), (_Float16)(-1024.f)};
             }
         }
-        v4f tmp[MM_NT][MM_MS];
+        v4f tmp[MM_NT][MS];
 #pragma unroll
         for (int j = 0; j < 8; ++j) {  // 32-element K-step (sub-block / block) of the step
             // every fragment read of the K-step first, then the weight
             // operands, then the MFMAs
-            v8h ah[MM_MS], al[MM_MS];
+            v8h ah[MS], al[MS];
 #pragma unroll
-            for (int ms = 0; ms < MM_MS; ++ms) {
+            for (int ms = 0; ms < MS; ++ms) {
                 if (XT && ms >= nsub) break;
                 ah[ms] = frag(buf, 0, ms, j);
                 al[ms] = frag(buf, 1, ms, j);
@@ -467,7 +478,7 @@ __global__ void __launch_bounds__(64 * MM_WAVES)
 #pragma unroll
                 for (int t = 0; t < MM_NT; ++t)
 #pragma unroll
-                    for (int ms = 0; ms < MM_MS; ++ms) {
+                    for (int ms = 0; ms < MS; ++ms) {
                         if (XT && ms >= nsub) break;
                         tmp[t][ms] = __builtin_amdgcn_mfma_f32_16x16x32_f16(
                             ah[ms], bw[t], j == 0 ? zero4 : tmp[t][ms], 0, 0, 0);
@@ -475,31 +486,31 @@ __global__ void __launch_bounds__(64 * MM_WAVES)
 #pragma unroll
                 for (int t = 0; t < MM_NT; ++t)
 #pragma unroll
-                    for (int ms = 0; ms < MM_MS; ++ms) {
+                    for (int ms = 0; ms < MS; ++ms) {
                         if (XT && ms >= nsub) break;
                         tmp[t][ms] =
                             __builtin_amdgcn_mfma_f32_16x16x32_f16(al[ms], bw[t], tmp[t][ms], 0, 0, 0);
                     }
             } else {
-                v4f p[MM_NT][MM_MS];
+                v4f p[MM_NT][MS];
 #pragma unroll
                 for (int t = 0; t < MM_NT; ++t)
 #pragma unroll
-                    for (int ms = 0; ms < MM_MS; ++ms) {
+                    for (int ms = 0; ms < MS; ++ms) {
                         if (XT && ms >= nsub) break;
                         p[t][ms] = __builtin_amdgcn_mfma_f32_16x16x32_f16(ah[ms], bw[t], zero4, 0, 0, 0);
                     }
 #pragma unroll
                 for (int t = 0; t < MM_NT; ++t)
 #pragma unroll
-                    for (int ms = 0; ms < MM_MS; ++ms) {
+                    for (int ms = 0; ms < MS; ++ms) {
                         if (XT && ms >= nsub) break;
                         p[t][ms] = __builtin_amdgcn_mfma_f32_16x16x32_f16(al[ms], bw[t], p[t][ms], 0, 0, 0);
                     }
 #pragma unroll
                 for (int t = 0; t < MM_NT; ++t)
 #pragma unroll
-                    for (int ms = 0; ms < MM_MS; ++ms) {
+                    for (int ms = 0; ms < MS; ++ms) {
                         if (XT && ms >= nsub) break;
 #pragma unroll
                         for (int r = 0; r < 4; ++r) acc[t][ms][r] += bs[t] * p[t][ms][r];
@@ -514,7 +525,7 @@ __global__ void __launch_bounds__(64 * MM_WAVES)
                 const float d = h2f((uint16_t)((uint32_t)wc.hdr[t].x & 0xFFFF));
                 const float dmin = h2f((uint16_t)((uint32_t)wc.hdr[t].x >> 16));
 #pragma unroll
-                for (int ms = 0; ms < MM_MS; ++ms) {
+                for (int ms = 0; ms < MS; ++ms) {
                     if (XT && ms >= nsub) break;
                     v4f mt = __builtin_amdgcn_mfma_f32_16x16x16f16(xsh[ms], mnh[t], zero4, 0, 0, 0);
                     mt = __builtin_amdgcn_mfma_f32_16x16x16f16(xsl[ms], mnh[t], mt, 0, 0, 0);
@@ -541,7 +552,7 @@ __global__ void __launch_bounds__(64 * MM_WAVES)
     // + 4 kq + r, output column col0 + rbase + 16 t + col
     const MmOutDev& o = a.out;
 #pragma unroll
-    for (int ms = 0; ms < MM_MS; ++ms)
+    for (int ms = 0; ms < MS; ++ms)
 #pragma unroll
         for (int r = 0; r < 4; ++r) {
             const int64_t m = 16 * (mt0 + ms) + 4 * kq + r;
@@ -783,6 +794,7 @@ struct MmReduceArgs {
     int swiglu;
     MmOutDev out;
     const int32_t* xtab;
+    int64_t trows;  // rows per tile of xtab
     _Float16 *fh, *fl;
     float fscale;
     int64_t fK;
@@ -794,8 +806,8 @@ __global__ void __launch_bounds__(256) k_mm_reduce(MmReduceArgs a) {
     if (n >= a.N) return;
     bool valid = true;
     if (a.xtab) {
-        const int64_t t = m / MM_TOK;
-        valid = t < a.xtab[0] && m - t * MM_TOK < a.xtab[2 + 2 * t];
+        const int64_t t = m / a.trows;
+        valid = t < a.xtab[0] && m - t * a.trows < a.xtab[2 + 2 * t];
     }
     float v = 0.f;
     if (valid) {
@@ -919,11 +931,14 @@ size_t mm_part_floats(int64_t Mp, int64_t N, int64_t steps, int64_t ntiles, int 
 static hipError_t mm_launch(hipStream_t st, const MmSeg* segs, int nseg, const MmAct& act,
                             int64_t M, int epi, const MmOut& out, float* part,
                             size_t part_floats, int cu_count, const int32_t* xtab,
-                            const int64_t* plane, int64_t ntile_max, const MmFragOut* fo) {
+                            const int64_t* plane, int64_t ntile_max, int64_t trows,
+                            const MmFragOut* fo) {
     if (nseg < 1 || nseg > 3 || M < 1 || M > act.Mp || out.nseq < 1 || out.nseq > FTX_MAX_SEQ)
         return hipErrorInvalidValue;
-    if (xtab && (ntile_max < 1 || ntile_max * MM_TOK > act.Mp || !plane))
+    if (xtab && (ntile_max < 1 || (trows != 16 && trows != 64) || ntile_max * trows > act.Mp ||
+                 !plane))
         return hipErrorInvalidValue;
+    const int ms = xtab ? (int)(trows / 16) : MM_MS;
     if (fo && (!xtab || epi != EPI_SWIGLU)) return hipErrorInvalidValue;
     const int dt = segs[0].dt;
     MmArgs a{};
@@ -976,16 +991,18 @@ static hipError_t mm_launch(hipStream_t st, const MmSeg* segs, int nseg, const M
     a.sb_per_split = (a.nsb + S - 1) / S;
     S = (a.nsb + a.sb_per_split - 1) / a.sb_per_split;
     const dim3 grid((unsigned)wg, (unsigned)mt, (unsigned)S);
-    constexpr size_t lds = 2 * 65536;
+    const size_t lds = 2 * (size_t)ms * 16384;
     using K_t = void (*)(MmArgs);
-    const K_t kern = xtab ? (dt == FTX_Q4_K       ? k_mm<FTX_Q4_K, true>
-                             : dt == FTX_Q8_0_MMT ? k_mm<FTX_Q8_0_MMT, true>
-                                                  : k_mm<FTX_Q4_0_MMT, true>)
-                          : (dt == FTX_Q4_K       ? k_mm<FTX_Q4_K, false>
-                             : dt == FTX_Q8_0_MMT ? k_mm<FTX_Q8_0_MMT, false>
-                                                  : k_mm<FTX_Q4_0_MMT, false>);
-    static bool lds_set[6] = {false, false, false, false, false, false};
-    const int ki = (dt == FTX_Q4_K ? 0 : (dt == FTX_Q8_0_MMT ? 1 : 2)) + (xtab ? 3 : 0);
+    // [dtype][dense | expert 64-row tiles | expert 16-row tiles]
+    static const K_t kerns[3][3] = {
+        {k_mm<FTX_Q4_K, false, 4>, k_mm<FTX_Q4_K, true, 4>, k_mm<FTX_Q4_K, true, 1>},
+        {k_mm<FTX_Q8_0_MMT, false, 4>, k_mm<FTX_Q8_0_MMT, true, 4>, k_mm<FTX_Q8_0_MMT, true, 1>},
+        {k_mm<FTX_Q4_0_MMT, false, 4>, k_mm<FTX_Q4_0_MMT, true, 4>, k_mm<FTX_Q4_0_MMT, true, 1>}};
+    const int di = dt == FTX_Q4_K ? 0 : (dt == FTX_Q8_0_MMT ? 1 : 2);
+    const int vi = !xtab ? 0 : (ms == 4 ? 1 : 2);
+    const K_t kern = kerns[di][vi];
+    static bool lds_set[9] = {};
+    const int ki = di * 3 + vi;
     if (!lds_set[ki]) {
         hipError_t e = hipFuncSetAttribute((const void*)kern,
                                            hipFuncAttributeMaxDynamicSharedMemorySize, (int)lds);
@@ -1004,13 +1021,14 @@ static hipError_t mm_launch(hipStream_t st, const MmSeg* segs, int nseg, const M
     r.N = r.swiglu ? cols / 2 : cols;
     r.out = out_dev(out);
     r.xtab = xtab;
+    r.trows = trows;
     if (fo) {
         r.fh = fo->h;
         r.fl = fo->l;
         r.fscale = fo->scale;
         r.fK = fo->K;
     }
-    const int64_t rows = xtab ? ntile_max * MM_TOK : M;
+    const int64_t rows = xtab ? ntile_max * trows : M;
     hipLaunchKernelGGL(k_mm_reduce, dim3((unsigned)((r.N + 255) / 256), (unsigned)rows), dim3(256),
                        0, st, r);
     return hipGetLastError();
@@ -1019,18 +1037,19 @@ static hipError_t mm_launch(hipStream_t st, const MmSeg* segs, int nseg, const M
 hipError_t launch_mm(hipStream_t st, const MmSeg* segs, int nseg, const MmAct& act, int64_t M,
                      int epi, const MmOut& out, float* part, size_t part_floats, int cu_count) {
     return mm_launch(st, segs, nseg, act, M, epi, out, part, part_floats, cu_count, nullptr,
-                     nullptr, 0, nullptr);
+                     nullptr, 0, 0, nullptr);
 }
 
 hipError_t launch_mm_experts(hipStream_t st, const MmSeg* segs, int nseg, const int64_t* plane,
                              const MmAct& act, const int32_t* xtab, int64_t ntile_max,
-                             const MmFragOut& fo, float* part, size_t part_floats, int cu_count) {
+                             int64_t trows, const MmFragOut& fo, float* part, size_t part_floats,
+                             int cu_count) {
     if (fo.K != segs[0].N || fo.K % 32) return hipErrorInvalidValue;
     MmOut o{};
     o.nseq = 1;
-    o.row0[1] = ntile_max * MM_TOK;
-    return mm_launch(st, segs, nseg, act, ntile_max * MM_TOK, EPI_SWIGLU, o, part, part_floats,
-                     cu_count, xtab, plane, ntile_max, &fo);
+    o.row0[1] = ntile_max * trows;
+    return mm_launch(st, segs, nseg, act, ntile_max * trows, EPI_SWIGLU, o, part, part_floats,
+                     cu_count, xtab, plane, ntile_max, trows, &fo);
 }
 
 hipError_t launch_mm_down(hipStream_t st, const uint8_t* tiled, int64_t n_in, int64_t N,

@@ -41,7 +41,6 @@
 
 namespace {
 
-constexpr int MOE_TILE = 64;   // operand rows per tile (the k_mm token tile)
 constexpr int MOE_MAXM = 256;  // tokens of one step
 constexpr int MOE_MAXE = 256;  // experts
 constexpr int MOE_MAXU = 8;    // experts per token
@@ -125,7 +124,7 @@ __global__ void __launch_bounds__(256) k_moe_gate(const float* __restrict__ xn, 
 // for the combine (src/engine.cpp:210-239).
 __global__ void __launch_bounds__(256) k_moe_route(const int32_t* __restrict__ te_g,
                                                    const float* __restrict__ tw_g, int M, int E,
-                                                   int U, int ntile_max, MoeRoute r) {
+                                                   int U, int ntile_max, int TR, MoeRoute r) {
     __shared__ int te[MOE_MAXM * MOE_MAXU];
     __shared__ float tw[MOE_MAXM * MOE_MAXU];
     __shared__ int slot_of[MOE_MAXM * MOE_MAXU];
@@ -147,7 +146,7 @@ __global__ void __launch_bounds__(256) k_moe_route(const int32_t* __restrict__ t
         firstpos[e] = fp;
         cnt[e] = c;
     }
-    for (int i = t; i < ntile_max * MOE_TILE; i += blockDim.x) r.slot_tok[i] = -1;
+    for (int i = t; i < ntile_max * TR; i += blockDim.x) r.slot_tok[i] = -1;
     __syncthreads();
     for (int e = t; e < E; e += blockDim.x) {
         int k = 0;
@@ -158,9 +157,9 @@ __global__ void __launch_bounds__(256) k_moe_route(const int32_t* __restrict__ t
         int nt = 0;
         for (int e = 0; e < E; ++e) {
             tile0[e] = nt;
-            for (int k = 0; k < cnt[e] && nt < ntile_max; k += MOE_TILE, ++nt) {
+            for (int k = 0; k < cnt[e] && nt < ntile_max; k += TR, ++nt) {
                 r.tab[1 + 2 * nt] = e;
-                r.tab[2 + 2 * nt] = min(MOE_TILE, cnt[e] - k);
+                r.tab[2 + 2 * nt] = min(TR, cnt[e] - k);
             }
         }
         r.tab[0] = nt;
@@ -168,11 +167,11 @@ __global__ void __launch_bounds__(256) k_moe_route(const int32_t* __restrict__ t
     __syncthreads();
     for (int e = t; e < E; e += blockDim.x) {
         if (!cnt[e]) continue;
-        const int base = MOE_TILE * tile0[e];
+        const int base = TR * tile0[e];
         int k = 0;
         for (int i = 0; i < MU; ++i)
             if (te[i] == e) {
-                const int s = base + k < ntile_max * MOE_TILE ? base + k : 0;
+                const int s = base + k < ntile_max * TR ? base + k : 0;
                 slot_of[i] = s;
                 r.slot_tok[s] = i / U;
                 ++k;
@@ -234,7 +233,8 @@ struct MoeDownArgs {
     int64_t plane;        // bytes per expert
     const _Float16 *ah, *al;
     const int32_t* xtab;
-    int64_t F, K, rows;   // rows: operand rows (ntile_max * 64)
+    int64_t F, K, rows;   // rows: operand rows (ntile_max * trows)
+    int trows;            // rows per tile (16 or 64)
     int g_per_split;      // 32-row groups per split, a multiple of MOE_CG
     float* part;          // [S][rows][K]
 };
@@ -270,7 +270,7 @@ __global__ void __launch_bounds__(256) k_moe_down(MoeDownArgs a) {
     const uint8_t* wb = a.W + ex * a.plane;  // the expert's tiles
     const int64_t P = 4 * (int64_t)blockIdx.x + w;
     const uint8_t* tb = wb + P * G * MOE_TB;  // this wave's pair-block
-    const int64_t mt0 = (int64_t)by * 4;
+    const int64_t mt0 = (int64_t)by * (a.trows / 16);
     // a group index for addresses: groups past the split's end (never
     // multiplied) read the last group of the plane
     auto gc = [&](int64_t g) { return g < G ? g : G - 1; };
@@ -363,7 +363,7 @@ __global__ void __launch_bounds__(256) k_moe_down(MoeDownArgs a) {
         for (int r = 0; r < 4; ++r) {
             const int rr = 16 * ms + 4 * kq + r;
             if (rr >= nv) continue;
-            float* y = base + ((int64_t)by * MOE_TILE + rr) * a.K + 64 * P + col;
+            float* y = base + ((int64_t)by * a.trows + rr) * a.K + 64 * P + col;
 #pragma unroll
             for (int c = 0; c < 4; ++c) y[16 * c] = acc[c][ms][r];
         }
@@ -400,28 +400,53 @@ __global__ void __launch_bounds__(256) k_add(const float* __restrict__ x, float*
 
 }  // namespace
 
+int64_t moe_tile_rows(int64_t M, int64_t E, int64_t U) {
+    // 16-row tiles while the average expert takes at most 16 rows (each
+    // plane is then read about once either way, and the small tiles waste
+    // no MFMA work), 64-row tiles beyond that (fewer re-reads of a plane)
+    return M * U <= 16 * E ? 16 : 64;
+}
+
 int64_t moe_tiles_max(int64_t M, int64_t E, int64_t U) {
-    // sum_e ceil(c_e / 64) <= (M U) / 64 + (experts in use)
-    const int64_t MU = M * U;
-    return (MU + MOE_TILE - 1) / MOE_TILE + std::min(E, MU);
+    // sum_e ceil(c_e / TR) <= (M U) / TR + (experts in use)
+    const int64_t MU = M * U, TR = moe_tile_rows(M, E, U);
+    return (MU + TR - 1) / TR + std::min(E, MU);
 }
 
 static size_t align256(size_t b) { return (b + 255) & ~(size_t)255; }
 
+// the largest tile table and operand row count of any step up to Mmax tokens
+static void moe_max_dims(int64_t Mmax, int64_t E, int64_t U, int64_t* tiles, int64_t* rows) {
+    *tiles = *rows = 0;
+    for (int64_t m = 1; m <= Mmax; ++m) {
+        const int64_t t = moe_tiles_max(m, E, U);
+        *tiles = std::max(*tiles, t);
+        *rows = std::max(*rows, t * moe_tile_rows(m, E, U));
+    }
+}
+
+int64_t moe_rows_max(int64_t Mmax, int64_t E, int64_t U) {
+    int64_t t, r;
+    moe_max_dims(Mmax, E, U, &t, &r);
+    return r;
+}
+
 size_t moe_route_bytes(int64_t Mmax, int64_t E, int64_t U) {
-    const int64_t T = moe_tiles_max(Mmax, E, U);
-    return align256((size_t)(1 + 2 * T) * 4) + align256((size_t)(T * MOE_TILE) * 4) +
+    int64_t T, R;
+    moe_max_dims(Mmax, E, U, &T, &R);
+    return align256((size_t)(1 + 2 * T) * 4) + align256((size_t)R * 4) +
            align256((size_t)(Mmax * U) * 4) * 4;
 }
 
 MoeRoute moe_route_view(void* buf, int64_t Mmax, int64_t E, int64_t U) {
-    const int64_t T = moe_tiles_max(Mmax, E, U);
+    int64_t T, R;
+    moe_max_dims(Mmax, E, U, &T, &R);
     uint8_t* p = (uint8_t*)buf;
     MoeRoute r;
     r.tab = (int32_t*)p;
     p += align256((size_t)(1 + 2 * T) * 4);
     r.slot_tok = (int32_t*)p;
-    p += align256((size_t)(T * MOE_TILE) * 4);
+    p += align256((size_t)R * 4);
     r.comb_slot = (int32_t*)p;
     p += align256((size_t)(Mmax * U) * 4);
     r.comb_w = (float*)p;
@@ -444,7 +469,7 @@ hipError_t launch_moe_route(hipStream_t st, const float* xn, int64_t K, const ui
     hipError_t e = hipGetLastError();
     if (e != hipSuccess) return e;
     hipLaunchKernelGGL(k_moe_route, dim3(1), dim3(256), 0, st, r.te, r.tw, (int)M, (int)E, (int)U,
-                       (int)moe_tiles_max(M, E, U), r);
+                       (int)moe_tiles_max(M, E, U), (int)moe_tile_rows(M, E, U), r);
     return hipGetLastError();
 }
 
@@ -483,9 +508,10 @@ int moe_down_splits(int64_t F, int64_t K, int64_t ntile_max, int cu_count) {
 
 hipError_t launch_moe_down(hipStream_t st, const uint8_t* tiled, int dt, int64_t F, int64_t K,
                            const _Float16* ah, const _Float16* al, const int32_t* xtab,
-                           int64_t ntile_max, int S, float* part, size_t part_floats) {
-    if (!moe_down_supported(dt, F, K) || ntile_max < 1 || S < 1 ||
-        (size_t)S * (size_t)(ntile_max * MOE_TILE) * (size_t)K > part_floats)
+                           int64_t ntile_max, int64_t trows, int S, float* part,
+                           size_t part_floats) {
+    if (!moe_down_supported(dt, F, K) || ntile_max < 1 || S < 1 || (trows != 16 && trows != 64) ||
+        (size_t)S * (size_t)(ntile_max * trows) * (size_t)K > part_floats)
         return hipErrorInvalidValue;
     MoeDownArgs a{};
     a.W = tiled;
@@ -494,7 +520,8 @@ hipError_t launch_moe_down(hipStream_t st, const uint8_t* tiled, int dt, int64_t
     a.xtab = xtab;
     a.F = F;
     a.K = K;
-    a.rows = ntile_max * MOE_TILE;
+    a.rows = ntile_max * trows;
+    a.trows = (int)trows;
     a.part = part;
     const int64_t G = F / 32;
     a.g_per_split = (int)(((G + S - 1) / S + MOE_CG - 1) / MOE_CG * MOE_CG);

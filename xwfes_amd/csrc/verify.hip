@@ -341,7 +341,8 @@ static int verify_large(ftx_ctx* ctx, ftx_model* m, const ftx_seq_args* sq, int6
     // that sum before the sum goes into x (src/engine.cpp:243-257, 577-579).
     auto moe_layer = [&](int64_t l, const ftx_tensor* const* X) -> int {
         const int64_t E = d.n_expert, U = d.n_expert_used;
-        const int64_t T = moe_tiles_max(Mt, E, U), rows = T * 64;
+        const int64_t TR = moe_tile_rows(Mt, E, U), T = moe_tiles_max(Mt, E, U), rows = T * TR;
+        const int64_t Mp = mm_pad_tokens(rows);
         const ftx_tensor* gi = X[FTX_X_GATE_INP];
         const ftx_tensor *ge = X[FTX_X_GATE_EXPS], *de = X[FTX_X_DOWN_EXPS];
         const MoeRoute rt = moe_route_view(m->route, m->Mmax, E, U);
@@ -351,7 +352,7 @@ static int verify_large(ftx_ctx* ctx, ftx_model* m, const ftx_seq_args* sq, int6
                  launch_moe_route(st, m->xn, D, gi->data, gi->dtype, gi->row_bytes,
                                   m->moe_rbias[l], Mt, E, U, rt));
         const int gdt = m->moe_gu_dt[l];
-        const MmAct act = mm_act(m->moe_act, rows, D);
+        const MmAct act = mm_act(m->moe_act, Mp, D);
         TRACED_L(TK_XQ_PREP, Md * U * D * f4 + 4.0 * rows * D,
                  launch_mm_prep(st, m->xn, D, nullptr, eps, rows, act, gdt, rt.slot_tok));
         // every plane is read at most once; the routed planes are what moves
@@ -361,14 +362,14 @@ static int verify_large(ftx_ctx* ctx, ftx_model* m, const ftx_seq_args* sq, int6
                        MmSeg{m->moe_up[l], gdt, F, 0, ge->row_bytes}};
         const int64_t pb = (int64_t)mm_tiled_bytes(gdt, F, D);
         const int64_t plane[2] = {pb, pb};
-        MmFragOut fo{m->moe_h, m->moe_h + rows * F, 1.f, F};
+        MmFragOut fo{m->moe_h, m->moe_h + Mp * F, 1.f, F};
         TRACED_L(TK_GEMV_SWIGLU, 2 * used * plane_gu + Md * U * D * 4.0 + Md * U * F * 4.0,
-                 launch_mm_experts(st, gs, 2, plane, act, rt.tab, T, fo, m->moe_part,
+                 launch_mm_experts(st, gs, 2, plane, act, rt.tab, T, TR, fo, m->moe_part,
                                    m->moe_part_n, ctx->cu_count));
         const int S = moe_down_splits(F, D, T, ctx->cu_count);
         TRACED_L(TK_DOWN, used * (double)(de->row_bytes * F) + Md * U * F * 4.0 + S * Md * U * D * f4,
-                 launch_moe_down(st, m->moe_down[l], de->dtype, F, D, fo.h, fo.l, rt.tab, T, S,
-                                 m->moe_part, m->moe_part_n));
+                 launch_moe_down(st, m->moe_down[l], de->dtype, F, D, fo.h, fo.l, rt.tab, T, TR,
+                                 S, m->moe_part, m->moe_part_n));
         const ftx_tensor *sg = X[FTX_X_GATE_SH], *su = X[FTX_X_UP_SH], *sd = X[FTX_X_DOWN_SH];
         TRACED_L(TK_MOE_COMBINE, S * Md * U * D * f4 + 2 * Md * D * f4,
                  launch_moe_combine(st, m->moe_part, S, rows, D, rt, Mt, U, sg ? m->tmpo : m->x,
@@ -842,16 +843,20 @@ int ftx_model_create(ftx_ctx* ctx, const ftx_model_desc* d, ftx_model** out) {
             ok = dalloc(&m->moe_rbias[l], (size_t)E) && vec_f32(X[FTX_X_ROUTER_BIAS], m->moe_rbias[l]);
     }
     if (ok && any_moe) {
-        const int64_t T = moe_tiles_max(Mmax, E, U), rows = T * 64;
+        const int64_t rows = mm_pad_tokens(moe_rows_max(Mmax, E, U));
         const int cu = ctx->cu_count;
         // gate / up partials and the down partials share one buffer, sized
         // for every step size up to Mmax (the split counts depend on it)
         size_t pn = 0;
         for (int64_t mt = 1; mt <= Mmax; ++mt) {
-            const int64_t t = moe_tiles_max(mt, E, U), r = t * 64;
+            const int64_t t = moe_tiles_max(mt, E, U), r = t * moe_tile_rows(mt, E, U);
             const int S = moe_down_splits(d->n_ff, D, t, cu);
-            const size_t gu = mm_part_floats(r, 2 * d->n_ff, D / 256, (2 * d->n_ff + 255) / 256, cu);
-            pn = std::max({pn, gu, (size_t)r * 2 * (size_t)d->n_ff, (size_t)S * r * D});
+            // (the gate / up launch's splits depend on its tile count; 64
+            // rows per tile bounds its operand rows)
+            const size_t gu =
+                mm_part_floats(t * 64, 2 * d->n_ff, D / 256, (2 * d->n_ff + 255) / 256, cu);
+            pn = std::max({pn, gu, (size_t)mm_pad_tokens(r) * 2 * (size_t)d->n_ff,
+                           (size_t)S * r * D});
         }
         m->moe_part_n = pn;
         ok = dalloc((uint8_t**)&m->route, moe_route_bytes(Mmax, E, U)) &&
