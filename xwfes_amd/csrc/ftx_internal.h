@@ -272,10 +272,11 @@ int64_t moe_tiles_max(int64_t M, int64_t E, int64_t U);
 int64_t moe_rows_max(int64_t Mmax, int64_t E, int64_t U);
 size_t moe_route_bytes(int64_t Mmax, int64_t E, int64_t U);
 MoeRoute moe_route_view(void* buf, int64_t Mmax, int64_t E, int64_t U);
-// the router (E rows of K, any stored dtype) on the ffn_norm rows xn [M][K],
-// plus rbias [E] or null, and the routing tables
-hipError_t launch_moe_route(hipStream_t st, const float* xn, int64_t K, const uint8_t* W, int dt,
-                            int64_t row_bytes, const float* rbias, int64_t M, int64_t E, int64_t U,
+// ffn_norm of the residual rows x [M][K] into xn, the router (E rows of K,
+// any stored dtype) on them plus rbias [E] or null, and the routing tables
+hipError_t launch_moe_route(hipStream_t st, const float* x, const float* normw, float eps,
+                            float* xn, int64_t K, const uint8_t* W, int dt, int64_t row_bytes,
+                            const float* rbias, int64_t M, int64_t E, int64_t U,
                             const MoeRoute& r);
 bool moe_down_supported(int dt, int64_t F, int64_t K);
 size_t moe_down_tiled_bytes(int dt, int64_t F, int64_t K, int64_t E);
@@ -450,6 +451,12 @@ struct AcceptDev {
     float* margin;           // device scalar
 };
 hipError_t launch_accept(hipStream_t st, const AcceptDev& a);
+// the RESIDUAL mode over many workgroups (row statistics included); scratch
+// of accept_residual_scratch_bytes(); accept_residual_error copies the grid
+// barrier's time-out flag to the host int *err (enqueued on st)
+size_t accept_residual_scratch_bytes();
+hipError_t launch_accept_residual(hipStream_t st, const AcceptDev& a, void* scratch);
+int accept_residual_error(const void* scratch, hipStream_t st, int* err);
 // argmax and its T = 1 softmax probability of one row: out = {token, prob
 // bits} (scratch: row_stats_scratch_bytes(1, V))
 hipError_t launch_argmax_prob(hipStream_t st, const float* row, int64_t V, void* scratch,

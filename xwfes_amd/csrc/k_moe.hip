@@ -47,33 +47,63 @@ constexpr int MOE_MAXU = 8;    // experts per token
 constexpr int MOE_TB = 1152;   // bytes of one re-tiled (pair-block, row-group) tile
 
 // ---------------------------------------------------------------- route
-// Router and per-token choice, one workgroup per token m: the router row
-// (router weights dot the ffn_norm row, any stored dtype, wave sums) plus
-// the bias, then one thread: softmax_inplace (float max, float exp, double
+// ffn_norm, router and per-token choice, one workgroup per token m: the
+// RMSNorm of the residual row (src/engine.cpp:23-41; the row's sum of
+// squares as wave sums), written out as the experts' operand row xn[m]; the
+// router row (router weights dot xn[m], any stored dtype, wave sums) plus
+// the bias; then one thread: softmax_inplace (float max, float exp, double
 // sum in expert order, float scale; src/engine.cpp:62-72), the U largest in
 // descending order with ties to the lower index (std::partial_sort's order
 // for distinct values), the weights renormalised by their float sum
 // (src/engine.cpp:197-215).  Writes te[m][u] (expert), tw[m][u] (weight).
-__global__ void __launch_bounds__(256) k_moe_gate(const float* __restrict__ xn, int64_t K,
+__global__ void __launch_bounds__(256) k_moe_gate(const float* __restrict__ x, int64_t K,
+                                                  const float* __restrict__ normw, float eps,
+                                                  float* __restrict__ xn,
                                                   const uint8_t* __restrict__ W, int dt,
                                                   int64_t row_bytes, const float* __restrict__ rbias,
                                                   int E, int U, int32_t* __restrict__ te,
                                                   float* __restrict__ tw) {
 #pragma clang fp contract(off)
     extern __shared__ float xs[];  // [K] then the E logits
+    __shared__ float red[4];
     float* lg = xs + K;
     const int m = blockIdx.x, t = threadIdx.x, lane = t & 63, w = t >> 6;
-    const float* x = xn + (int64_t)m * K;
-    for (int64_t k = t; k < K; k += 256) xs[k] = x[k];
+    const float* xr = x + (int64_t)m * K;
+    float ss = 0.f;
+    for (int64_t k = t; k < K; k += 256) {
+        const float v = xr[k];
+        xs[k] = v;
+        ss += v * v;
+    }
+#pragma unroll
+    for (int o = 32; o > 0; o >>= 1) ss += __shfl_xor(ss, o, 64);
+    if (lane == 0) red[w] = ss;
+    __syncthreads();
+    const float rinv = 1.f / sqrtf((((red[0] + red[1]) + red[2]) + red[3]) / (float)K + eps);
+    float* xo = xn + (int64_t)m * K;
+    for (int64_t k = t; k < K; k += 256) {
+        const float v = xs[k] * rinv * normw[k];
+        xs[k] = v;
+        xo[k] = v;
+    }
     __syncthreads();
     for (int e = w; e < E; e += 4) {
         const uint8_t* row = W + (int64_t)e * row_bytes;
         float acc = 0.f;
-        for (int64_t c = lane; c < K / 8; c += 64) {
-            float v[8];
-            dq8(row, dt, 8 * c, K, v);
+        if (dt == FTX_F32) {
+            const float4* r4 = (const float4*)row;
+            for (int64_t c = lane; c < K / 4; c += 64) {
+                const float4 v = r4[c];
+                acc += v.x * xs[4 * c] + v.y * xs[4 * c + 1] + v.z * xs[4 * c + 2] +
+                       v.w * xs[4 * c + 3];
+            }
+        } else {
+            for (int64_t c = lane; c < K / 8; c += 64) {
+                float v[8];
+                dq8(row, dt, 8 * c, K, v);
 #pragma unroll
-            for (int i = 0; i < 8; ++i) acc += v[i] * xs[8 * c + i];
+                for (int i = 0; i < 8; ++i) acc += v[i] * xs[8 * c + i];
+            }
         }
 #pragma unroll
         for (int o = 32; o > 0; o >>= 1) acc += __shfl_xor(acc, o, 64);
@@ -457,15 +487,17 @@ MoeRoute moe_route_view(void* buf, int64_t Mmax, int64_t E, int64_t U) {
     return r;
 }
 
-hipError_t launch_moe_route(hipStream_t st, const float* xn, int64_t K, const uint8_t* W, int dt,
-                            int64_t row_bytes, const float* rbias, int64_t M, int64_t E, int64_t U,
+hipError_t launch_moe_route(hipStream_t st, const float* x, const float* normw, float eps,
+                            float* xn, int64_t K, const uint8_t* W, int dt, int64_t row_bytes,
+                            const float* rbias, int64_t M, int64_t E, int64_t U,
                             const MoeRoute& r) {
     if (M < 1 || M > MOE_MAXM || E < 2 || E > MOE_MAXE || U < 1 || U > MOE_MAXU || U > E ||
-        K < 8 || K % 8 || (K + E) * 4 > 65536)
+        K < 8 || K % 8 || (K + E) * 4 > 65536 || (dt == FTX_F32 && ((uintptr_t)W & 15)) ||
+        (dt == FTX_F32 && row_bytes % 16))
         return hipErrorInvalidValue;
     const size_t lds = (size_t)(K + E) * sizeof(float);
-    hipLaunchKernelGGL(k_moe_gate, dim3((unsigned)M), dim3(256), lds, st, xn, K, W, dt, row_bytes,
-                       rbias, (int)E, (int)U, r.te, r.tw);
+    hipLaunchKernelGGL(k_moe_gate, dim3((unsigned)M), dim3(256), lds, st, x, K, normw, eps, xn, W,
+                       dt, row_bytes, rbias, (int)E, (int)U, r.te, r.tw);
     hipError_t e = hipGetLastError();
     if (e != hipSuccess) return e;
     hipLaunchKernelGGL(k_moe_route, dim3(1), dim3(256), 0, st, r.te, r.tw, (int)M, (int)E, (int)U,

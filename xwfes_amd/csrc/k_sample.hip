@@ -18,6 +18,7 @@
 namespace {
 
 constexpr int NT = 1024;  // threads of the single-block acceptance kernel
+constexpr int ACC_RES_WG = 64;  // workgroups of the residual acceptance kernel
 constexpr int SCH = 4096; // elements per statistics chunk
 constexpr int SUB = 128;  // elements per exp-sum sub-chunk (SCH / SUB per chunk)
 
@@ -553,6 +554,39 @@ __device__ void target_dist(const float* __restrict__ lg, int64_t V, float temp,
     __syncthreads();
 }
 
+// Row r's statistics from its chunk results, by one wave (lane l): first-max
+// argmax over the chunks, the exp sum over the sub-chunks (lane-strided sums
+// in index order, then a fixed tree).
+__device__ void row_stat_wave(const AcceptDev& a, int64_t r, int l) {
+    const RowChunks& rc = a.rc;
+    float best = -INFINITY;
+    int32_t bi = 0x7FFFFFFF;
+    for (int c = l; c < rc.nch; c += 64) {
+        const float v = rc.cmax[r * rc.nch + c];
+        const int32_t iv = rc.carg[r * rc.nch + c];
+        if (iv != 0x7FFFFFFF && (bi == 0x7FFFFFFF || better(v, iv, best, bi))) {
+            best = v;
+            bi = iv;
+        }
+    }
+#pragma unroll
+    for (int o = 32; o > 0; o >>= 1) {
+        const float ov = __shfl_xor(best, o, 64);
+        const int32_t oi = __shfl_xor(bi, o, 64);
+        if (oi != 0x7FFFFFFF && (bi == 0x7FFFFFFF || better(ov, oi, best, bi))) {
+            best = ov;
+            bi = oi;
+        }
+    }
+    double sum = 0.0;
+    if (a.with_sum) {
+        for (int j = l; j < rc.nsub; j += 64) sum += rc.csub[r * rc.nsub + j];
+#pragma unroll
+        for (int o = 32; o > 0; o >>= 1) sum += __shfl_xor(sum, o, 64);
+    }
+    if (l == 0) a.stats[r] = RowStats{best, bi, sum};
+}
+
 // Decisions.  GREEDY and RESIDUAL finish here; RATIO records the row the
 // bonus is drawn from and its uniform for the two bonus kernels.
 __global__ void __launch_bounds__(NT) k_accept(AcceptDev a) {
@@ -577,35 +611,7 @@ __global__ void __launch_bounds__(NT) k_accept(AcceptDev a) {
     // sums in index order, then a fixed tree)
     {
         const int w = t >> 6, l = t & 63;
-        const RowChunks& rc = a.rc;
-        for (int64_t r = w; r <= a.M; r += NT / 64) {
-            float best = -INFINITY;
-            int32_t bi = 0x7FFFFFFF;
-            for (int c = l; c < rc.nch; c += 64) {
-                const float v = rc.cmax[r * rc.nch + c];
-                const int32_t iv = rc.carg[r * rc.nch + c];
-                if (iv != 0x7FFFFFFF && (bi == 0x7FFFFFFF || better(v, iv, best, bi))) {
-                    best = v;
-                    bi = iv;
-                }
-            }
-#pragma unroll
-            for (int o = 32; o > 0; o >>= 1) {
-                const float ov = __shfl_xor(best, o, 64);
-                const int32_t oi = __shfl_xor(bi, o, 64);
-                if (oi != 0x7FFFFFFF && (bi == 0x7FFFFFFF || better(ov, oi, best, bi))) {
-                    best = ov;
-                    bi = oi;
-                }
-            }
-            double sum = 0.0;
-            if (a.with_sum) {
-                for (int j = l; j < rc.nsub; j += 64) sum += rc.csub[r * rc.nsub + j];
-#pragma unroll
-                for (int o = 32; o > 0; o >>= 1) sum += __shfl_xor(sum, o, 64);
-            }
-            if (l == 0) a.stats[r] = RowStats{best, bi, sum};
-        }
+        for (int64_t r = w; r <= a.M; r += NT / 64) row_stat_wave(a, r, l);
     }
     __syncthreads();
 #define ROW(c) ((c) < 0 ? a.base_row : a.rows + (int64_t)(c) * V)
@@ -737,6 +743,254 @@ __global__ void __launch_bounds__(NT) k_accept(AcceptDev a) {
     }
 }
 
+// ---- RESIDUAL acceptance over many workgroups.  The decisions are made
+// by every workgroup alike (each runs the same sequential walk on the same
+// data, so no decision is broadcast); the vocabulary-wide work -- the
+// residual p <- norm(max(0, p - q)) of a rejected child and its sum -- is
+// split into one contiguous slice per workgroup, followed by a grid barrier
+// after which every workgroup reads the slices' partial sums in slice order.
+// The residual is kept unnormalised (P with its sum T, p = P / T), in two
+// buffers used in turn by successive passes (as are the partial sums), so
+// that a pass never overwrites what a slower workgroup may still read of
+// the previous one; a node's
+// target p = exp((l - mx) / T) / sum is formed on the fly from the row
+// statistics, so a node whose first child is accepted costs no pass at all.
+// The bonus after an all-rejected node is the inverse-CDF pick of the
+// residual (the crossing slice from the partial sums, then the crossing
+// element by a block scan of the slice); after a node without children it is
+// the pick of the target (the crossing 128-element sub-chunk from the
+// statistics' sub-chunk sums, then the element).  The barrier's waits are
+// bounded: a barrier that does not complete in about 50 ms sets the error
+// word and every workgroup returns.
+
+constexpr int RT = 256;  // threads per workgroup of the residual kernel
+
+struct GridBar {
+    unsigned count, gen;
+    int err, pad_;
+};
+
+__device__ bool grid_barrier(GridBar* gb, unsigned G) {
+    __shared__ int ok;
+    __syncthreads();
+    if (threadIdx.x == 0) {
+        ok = 1;
+        const unsigned g = __hip_atomic_load(&gb->gen, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+        __threadfence();
+        const unsigned arrived =
+            __hip_atomic_fetch_add(&gb->count, 1u, __ATOMIC_ACQ_REL, __HIP_MEMORY_SCOPE_AGENT);
+        if (arrived == G - 1) {
+            __hip_atomic_store(&gb->count, 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+            __hip_atomic_fetch_add(&gb->gen, 1u, __ATOMIC_RELEASE, __HIP_MEMORY_SCOPE_AGENT);
+        } else {
+            unsigned n = 0;
+            while (__hip_atomic_load(&gb->gen, __ATOMIC_ACQUIRE, __HIP_MEMORY_SCOPE_AGENT) == g) {
+                if (++n > (1u << 20) ||
+                    __hip_atomic_load(&gb->err, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT)) {
+                    __hip_atomic_store(&gb->err, 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+                    ok = 0;
+                    break;
+                }
+                __builtin_amdgcn_s_sleep(8);
+            }
+        }
+        __threadfence();
+    }
+    __syncthreads();
+    return ok != 0;
+}
+
+__device__ double rblock_sum(double v, double* sd) {
+    const int t = threadIdx.x;
+#pragma unroll
+    for (int o = 32; o > 0; o >>= 1) v += __shfl_xor(v, o, 64);
+    if ((t & 63) == 0) sd[t >> 6] = v;
+    __syncthreads();
+    const double r = ((sd[0] + sd[1]) + sd[2]) + sd[3];
+    __syncthreads();
+    return r;
+}
+
+// Inverse-CDF pick inside [b, e) for `target` (the weights' running sum
+// from b is compared with it): thread t takes a contiguous run, a block scan
+// finds the crossing run, its thread scans it.  w(i) gives the weight of
+// element i.  Returns the crossing index or, when rounding leaves none, the
+// last positive one (-1 if none).
+template <typename Wf>
+__device__ int32_t range_pick(int64_t b, int64_t e, double target, Wf w) {
+    __shared__ double incl[RT];
+    __shared__ int32_t lastpos[RT];
+    __shared__ int32_t pick;
+    const int t = threadIdx.x;
+    const int64_t run = (e - b + RT - 1) / RT;
+    const int64_t rb = min(e, b + t * run), re = min(e, rb + run);
+    double cs = 0.0;
+    int32_t lp = -1;
+    for (int64_t i = rb; i < re; ++i) {
+        const double v = w(i);
+        cs += v;
+        if (v > 0) lp = (int32_t)i;
+    }
+    incl[t] = cs;
+    lastpos[t] = lp;
+    if (t == 0) pick = -1;
+    __syncthreads();
+    for (int o = 1; o < RT; o <<= 1) {
+        const double add = t >= o ? incl[t - o] : 0.0;
+        const int32_t lpo = t >= o ? lastpos[t - o] : -1;
+        __syncthreads();
+        incl[t] += add;
+        if (lastpos[t] < 0) lastpos[t] = lpo;
+        __syncthreads();
+    }
+    const double ex = t ? incl[t - 1] : 0.0;
+    if (incl[t] > target && ex <= target && rb < re) {
+        double c = ex;
+        for (int64_t i = rb; i < re; ++i) {
+            c += w(i);
+            if (c > target) {
+                pick = (int32_t)i;
+                break;
+            }
+        }
+    }
+    __syncthreads();
+    const int32_t r = pick >= 0 ? pick : lastpos[RT - 1];
+    __syncthreads();
+    return r;
+}
+
+__global__ void __launch_bounds__(RT) k_accept_res(AcceptDev a, GridBar* gb, double* part) {
+#pragma clang fp contract(off)
+    __shared__ double sd[RT / 64];
+    const unsigned G = gridDim.x;
+    const int wg = blockIdx.x, t = threadIdx.x;
+    const int64_t V = a.V, M = a.M;
+    // row statistics: one wave per row, rows spread over the workgroups
+    for (int64_t r = (int64_t)wg * (RT / 64) + (t >> 6); r <= M; r += (int64_t)G * (RT / 64))
+        row_stat_wave(a, r, t & 63);
+    if (!grid_barrier(gb, G)) return;
+    const int64_t slice = (V + G - 1) / G;
+    const int64_t s0 = min(V, (int64_t)wg * slice), s1 = min(V, s0 + slice);
+    uint64_t rng = *a.rng;
+    float mg = INFINITY;
+    int32_t cur = -1, nacc = 0;
+    int64_t pass = 0;  // residual passes so far: buffer pass % 2 holds the latest
+    const double* Pc = a.p;  // the latest residual
+    const double* Pp = part;  // its partial sums
+#define ROW(c) ((c) < 0 ? a.base_row : a.rows + (int64_t)(c) * V)
+    for (int64_t step = 0; step <= M; ++step) {
+        const RowStats st = a.stats[cur + 1];
+        const float* lg = ROW(cur);
+        double T = st.sum;
+        bool have_res = false;
+        int32_t next = -2;
+        for (int64_t ch = 0; ch < M; ++ch) {
+            if (a.parents[ch] != cur) continue;
+            const float* qc = a.q + ch * V;
+            const int32_t tok = a.props[ch];
+            const double pv = have_res ? Pc[tok] / T : texp(lg[tok], st.mx, a.temp) / T;
+            const float pt = (float)pv;
+            const float ratio = fminf(1.f, pt / fmaxf(qc[tok], 1e-9f));
+            const float u = splitmix_float(rng);
+            mg = fminf(mg, fabsf(u - ratio));
+            if (u <= ratio) {
+                next = (int32_t)ch;
+                break;
+            }
+            // p <- max(0, p - q_ch) over this workgroup's slice, its sum
+            double* Pn = a.p + (pass & 1) * V;
+            double* partn = part + (pass & 1) * G;
+            double loc = 0.0;
+            for (int64_t i = s0 + t; i < s1; i += RT) {
+                const double b = have_res ? Pc[i] / T : texp(lg[i], st.mx, a.temp) / T;
+                const double r = b - (double)qc[i];
+                const double v = r > 0 ? r : 0.0;
+                Pn[i] = v;
+                loc += v;
+            }
+            loc = rblock_sum(loc, sd);
+            if (t == 0) partn[wg] = loc;
+            ++pass;
+            Pc = Pn;
+            Pp = partn;
+            if (!grid_barrier(gb, G)) return;
+            double tot = 0.0;
+            for (unsigned w = 0; w < G; ++w) tot += Pp[w];
+            if (tot > 0) {
+                T = tot;
+                have_res = true;
+            } else {  // p == q: back to the target (p untouched by the oracle)
+                T = st.sum;
+                have_res = false;
+            }
+        }
+        if (next >= -1) {
+            if (wg == 0 && t == 0) a.out[2 + nacc] = next;
+            ++nacc;
+            cur = next;
+            continue;
+        }
+        // the bonus
+        const float ub = splitmix_float(rng);
+        int32_t bonus = -1;
+        if (have_res) {
+            const double target = (double)ub * T;
+            double cum = 0.0;
+            unsigned ws = G;
+            for (unsigned w = 0; w < G; ++w) {
+                const double nc = cum + Pp[w];
+                if (nc > target) {
+                    ws = w;
+                    break;
+                }
+                cum = nc;
+            }
+            if (ws == G) {  // rounding: the last slice with weight
+                for (unsigned w = G; w-- > 0;)
+                    if (Pp[w] > 0) {
+                        ws = w;
+                        break;
+                    }
+                cum = -1.0;  // take that slice's last positive element
+            }
+            if ((unsigned)wg == ws) {
+                const int64_t b = min(V, (int64_t)ws * slice), e = min(V, b + slice);
+                const double* P = Pc;
+                const int32_t r = range_pick(b, e, cum < 0 ? INFINITY : target - cum,
+                                             [&](int64_t i) { return P[i]; });
+                bonus = r >= 0 ? r : (int32_t)b;
+            }
+        } else if (wg == 0) {
+            // the target: crossing sub-chunk by the sub-chunk sums, then its
+            // elements
+            const RowChunks& rc = a.rc;
+            const double* cs = rc.csub + (int64_t)(cur + 1) * rc.nsub;
+            const double target = (double)ub * st.sum;
+            const int32_t sc = range_pick(0, rc.nsub, target, [&](int64_t j) { return cs[j]; });
+            if (sc >= 0) {
+                double before = 0.0;
+                for (int32_t j = 0; j < sc; ++j) before += cs[j];
+                const int64_t b = (int64_t)sc * SUB, e = min(V, b + SUB);
+                const float mx = st.mx, tp = a.temp;
+                const int32_t r = range_pick(b, e, target - before,
+                                             [&](int64_t i) { return texp(lg[i], mx, tp); });
+                bonus = r >= 0 ? r : (int32_t)b;
+            } else {
+                bonus = st.amax;
+            }
+        }
+        if (bonus >= 0 && t == 0) a.out[1] = bonus;
+        break;
+    }
+#undef ROW
+    if (wg == 0 && t == 0) {
+        a.out[0] = nacc;
+        *a.rng = rng;
+        *a.margin = mg;
+    }
+}
+
 // Sampler::argmax and softmax_prob of that token (src/spec.cpp:89-95, as
 // DraftModelDrafter::draft uses them, 100-119) from one row's chunk
 // statistics at T = 1: the first maximum and 1 / sum_i exp((double)(l_i -
@@ -820,4 +1074,28 @@ hipError_t launch_row_stats(hipStream_t st, const float* base_row, const float* 
 hipError_t launch_accept(hipStream_t st, const AcceptDev& a) {
     hipLaunchKernelGGL(k_accept, dim3(1), dim3(NT), 0, st, a);
     return hipGetLastError();
+}
+
+size_t accept_residual_scratch_bytes() { return 256 + 2 * ACC_RES_WG * sizeof(double); }
+
+// RESIDUAL acceptance over ACC_RES_WG workgroups, launched cooperatively so
+// that all of them are resident for the grid barriers.  scratch: the
+// barrier word (zeroed here) and the slices' partial sums (two sets); a.p
+// holds two residual buffers of V doubles.
+hipError_t launch_accept_residual(hipStream_t st, const AcceptDev& a, void* scratch) {
+    GridBar* gb = (GridBar*)scratch;
+    double* part = (double*)((uint8_t*)scratch + 256);
+    hipError_t e = hipMemsetAsync(gb, 0, sizeof(GridBar), st);
+    if (e != hipSuccess) return e;
+    AcceptDev ac = a;
+    void* args[] = {(void*)&ac, (void*)&gb, (void*)&part};
+    return hipLaunchCooperativeKernel((const void*)k_accept_res, dim3(ACC_RES_WG), dim3(RT), args,
+                                      0, st);
+}
+
+int accept_residual_error(const void* scratch, hipStream_t st, int* err) {
+    return hipMemcpyAsync(err, (const uint8_t*)scratch + offsetof(GridBar, err), sizeof(int),
+                          hipMemcpyDeviceToHost, st) == hipSuccess
+               ? 0
+               : -1;
 }

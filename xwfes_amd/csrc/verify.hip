@@ -346,11 +346,9 @@ static int verify_large(ftx_ctx* ctx, ftx_model* m, const ftx_seq_args* sq, int6
         const ftx_tensor* gi = X[FTX_X_GATE_INP];
         const ftx_tensor *ge = X[FTX_X_GATE_EXPS], *de = X[FTX_X_DOWN_EXPS];
         const MoeRoute rt = moe_route_view(m->route, m->Mmax, E, U);
-        TRACED_L(TK_RMSNORM, 2 * Md * D * f4,
-                 launch_rmsnorm(st, m->x, m->norms + (l * 2 + 1) * D, D, Mt, eps, m->xn));
-        TRACED_L(TK_MOE_ROUTE, wbytes(gi) + Md * D * f4 + 4.0 * Md * U * f4,
-                 launch_moe_route(st, m->xn, D, gi->data, gi->dtype, gi->row_bytes,
-                                  m->moe_rbias[l], Mt, E, U, rt));
+        TRACED_L(TK_MOE_ROUTE, wbytes(gi) + 2 * Md * D * f4 + 4.0 * Md * U * f4,
+                 launch_moe_route(st, m->x, m->norms + (l * 2 + 1) * D, eps, m->xn, D, gi->data,
+                                  gi->dtype, gi->row_bytes, m->moe_rbias[l], Mt, E, U, rt));
         const int gdt = m->moe_gu_dt[l];
         const MmAct act = mm_act(m->moe_act, Mp, D);
         TRACED_L(TK_XQ_PREP, Md * U * D * f4 + 4.0 * rows * D,
@@ -1420,7 +1418,11 @@ int ftx_accept(ftx_ctx* ctx, const ftx_accept_args* a) {
     // its head out), the chunk statistics of the M + 1 rows
     const size_t stats_b = (size_t)(M + 1) * sizeof(RowStats);
     const size_t off_p = (stats_b + 255) & ~(size_t)255;
-    const size_t pb = a->mode == FTX_ACCEPT_RESIDUAL ? (size_t)V * 8 : 0;
+    // residual mode: two residual buffers of V doubles and the kernel's
+    // barrier and partial sums
+    const size_t pb = a->mode == FTX_ACCEPT_RESIDUAL
+                          ? 2 * (size_t)V * 8 + 256 + accept_residual_scratch_bytes()
+                          : 0;
     const size_t off_small = off_p + ((pb + 255) & ~(size_t)255);
     const size_t out_b = ((size_t)(M + 2) * 4 + 7) & ~(size_t)7;
     const size_t head_b = 24 + out_b;  // rng | sampler rng | margin | pad | out
@@ -1481,10 +1483,19 @@ int ftx_accept(ftx_ctx* ctx, const ftx_accept_args* a) {
     ad.out = (int32_t*)(d_small + 24);
     ad.margin = (float*)(d_small + 16);
     tk = tr_begin(ctx);
-    FTX_HIP(ctx, launch_accept(st, ad));
+    int bar_err = 0;
+    void* res_scratch = ws + off_p + ((2 * (size_t)V * 8 + 255) & ~(size_t)255);
+    if (a->mode == FTX_ACCEPT_RESIDUAL)
+        FTX_HIP(ctx, launch_accept_residual(st, ad, res_scratch));
+    else
+        FTX_HIP(ctx, launch_accept(st, ad));
     tr_end(ctx, tk, TK_ACCEPT, (double)V * 4);
     FTX_HIP(ctx, hipMemcpyAsync(pin, d_small, head_b, hipMemcpyDeviceToHost, st));
+    if (a->mode == FTX_ACCEPT_RESIDUAL && accept_residual_error(res_scratch, st, &bar_err))
+        return ftx_fail(ctx, FTX_E_DEVICE, "acceptance: copy of the barrier state failed");
     FTX_HIP(ctx, hipStreamSynchronize(st));
+    if (bar_err)
+        return ftx_fail(ctx, FTX_E_DEVICE, "acceptance: a grid barrier timed out");
     const int32_t na = h_out[0];
     if (na < 0 || na > M) return ftx_fail(ctx, FTX_E_DEVICE, "acceptance returned a bad count");
     *a->n_acc = na;
