@@ -337,8 +337,14 @@ typedef struct {
     int64_t launches;
     double ms;     /* summed device time between HIP events around each launch */
     double bytes;  /* summed algorithmic bytes (weights at stored size, KV, rows) */
+    /* the class's main kernel timed on its own dispatch (events carried by
+     * the launch itself: kernel start to end, no bracket time) */
+    int64_t kernel_launches;
+    double kernel_ms;
 } ftx_trace_entry;
-/* enable != 0 starts recording (and clears earlier records); 0 stops. */
+/* enable != 0 starts recording (and clears earlier records, then records
+ * 32 empty event brackets as the entry "event_pair": the time a bracket adds
+ * by itself); 0 stops. */
 int ftx_trace(ftx_ctx* ctx, int enable);
 /* Waits for the stream, then returns one entry per kernel class seen. */
 int ftx_trace_read(ftx_ctx* ctx, ftx_trace_entry* out, int max, int* n);

@@ -1,6 +1,7 @@
 // ftx_internal.h -- shared declarations of the HIP library behind ftx.h.
 #pragma once
 
+#include <hip/hip_ext.h>
 #include <hip/hip_runtime.h>
 
 #include <cstdint>
@@ -28,6 +29,7 @@ enum TraceKind {
     TK_XQ_PREP,
     TK_MOE_ROUTE,
     TK_MOE_COMBINE,
+    TK_EVENT_PAIR,  // empty event brackets: the brackets' own time
     TK_COUNT
 };
 
@@ -36,7 +38,30 @@ struct TraceRec {
     int ev0, ev1;
     double bytes;
     int launches;
+    bool kernel = false;  // ev0 / ev1 are the start / end of one kernel's dispatch
 };
+
+// The trace's kernel timer: while armed, the first launch that goes through
+// ktimed_launch carries the timer's events on its own dispatch
+// (hipExtLaunchKernelGGL: the kernel's start and end), so the trace can
+// report kernel durations without the event brackets' own time.
+struct KernelTimer {
+    hipEvent_t e0 = nullptr, e1 = nullptr;
+    bool armed = false, fired = false;
+};
+extern thread_local KernelTimer* g_ktimer;
+
+template <typename F, typename... Args>
+inline void ktimed_launch(F kernel, const dim3& grid, const dim3& block, uint32_t shm,
+                          hipStream_t st, Args... args) {
+    KernelTimer* kt = g_ktimer;
+    if (kt && kt->armed && !kt->fired) {
+        kt->fired = true;
+        hipExtLaunchKernelGGL(kernel, grid, block, shm, st, kt->e0, kt->e1, 0, args...);
+    } else {
+        hipLaunchKernelGGL(kernel, grid, block, shm, st, args...);
+    }
+}
 
 struct ftx_ctx {
     int device = 0;
@@ -48,6 +73,10 @@ struct ftx_ctx {
     int64_t tr_launches[TK_COUNT] = {};
     double tr_ms[TK_COUNT] = {};
     double tr_bytes[TK_COUNT] = {};
+    int64_t tr_klaunches[TK_COUNT] = {};  // launches timed on their own dispatch
+    double tr_kms[TK_COUNT] = {};
+    KernelTimer kt;
+    int kt_ev0 = -1, kt_ev1 = -1;
     // ftx_trace_replay: launches of class replay_kind at idempotent call
     // sites are issued replay_n times between their events
     int replay_kind = -1;

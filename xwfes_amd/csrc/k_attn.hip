@@ -404,10 +404,10 @@ hipError_t launch_attn_mfma(hipStream_t st, AttnMArgs a, float* part, int8_t* xq
     const int qtiles = (int)((a.M * (a.n_head / a.n_kv) + 31) / 32);
     const dim3 grid((unsigned)nch, (unsigned)a.n_kv, (unsigned)qtiles);
     if (a.hd == 128)
-        hipLaunchKernelGGL((k_attn_mfma<128, chunk_slots(128), ATTN_WAVES_128>), grid,
+        ktimed_launch(k_attn_mfma<128, chunk_slots(128), ATTN_WAVES_128>, grid,
                            dim3(64 * ATTN_WAVES_128), 0, st, a);
     else if (a.hd == 64)
-        hipLaunchKernelGGL((k_attn_mfma<64, chunk_slots(64), 4>), grid, dim3(64 * 4), 0, st, a);
+        ktimed_launch(k_attn_mfma<64, chunk_slots(64), 4>, grid, dim3(64 * 4), 0, st, a);
     else
         return hipErrorInvalidValue;
     hipError_t e = hipGetLastError();

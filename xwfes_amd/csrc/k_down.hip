@@ -500,9 +500,9 @@ hipError_t launch_down_mfma(hipStream_t st, int dt, const uint8_t* tiled, int64_
     a.part = part;
     const dim3 grid((unsigned)nsb, (unsigned)S);
     if (dt == FTX_Q4_K)
-        hipLaunchKernelGGL(k_down_mfma<FTX_Q4_K>, grid, dim3(64 * DOWN_WAVES), 0, st, a);
+        ktimed_launch(k_down_mfma<FTX_Q4_K>, grid, dim3(64 * DOWN_WAVES), 0, st, a);
     else
-        hipLaunchKernelGGL(k_down_mfma<FTX_Q6_K>, grid, dim3(64 * DOWN_WAVES), 0, st, a);
+        ktimed_launch(k_down_mfma<FTX_Q6_K>, grid, dim3(64 * DOWN_WAVES), 0, st, a);
     hipError_t e = hipGetLastError();
     if (e != hipSuccess) return e;
     if (splits) {

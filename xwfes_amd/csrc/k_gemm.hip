@@ -190,7 +190,8 @@ struct MmArgs {
     // operand rows 64 t .. 64 t + 63
     const int32_t* xtab;
     int nseg;
-    int64_t units;      // 64-row units over all segments
+    int64_t units;      // 32-row units over all segments
+    int ntt;            // token tiles: workgroup b takes token tile b % ntt of unit group b / ntt
     int64_t K;
     int nsb;            // 256-element steps of the contraction
     int sb_per_split;
@@ -336,19 +337,22 @@ __global__ void __launch_bounds__(64 * MM_WAVES)
     const int tid = threadIdx.x, lane = tid & 63;
     const int w = __builtin_amdgcn_readfirstlane(tid >> 6);
     const int col = lane & 15, kq = lane >> 4;
-    const int64_t u = (int64_t)blockIdx.x * MM_WAVES + w;
+    // the token tiles of one weight unit are neighbours in the grid, so they
+    // run together and a unit's weights come from memory about once
+    const int by = (int)(blockIdx.x % (unsigned)a.ntt);
+    const int64_t u = (int64_t)(blockIdx.x / (unsigned)a.ntt) * MM_WAVES + w;
     const bool live = u < a.units;  // wave-uniform
     const int si = mm_seg_of(a, live ? u : a.units - 1);
     MmSegDev sg = a.seg[si];
     const int64_t rbase = ((live ? u : a.units - 1) - sg.unit0) * MM_WROWS;
-    const int64_t mt0 = (int64_t)blockIdx.y * MS;  // first 16-token tile
+    const int64_t mt0 = (int64_t)by * MS;  // first 16-token tile
     int nsub = MS, mend = a.M;  // 16-token tiles in use, rows in use end
     if constexpr (XT) {
-        if ((int)blockIdx.y >= a.xtab[0]) return;
-        const int ex = a.xtab[1 + 2 * blockIdx.y], nv = a.xtab[2 + 2 * blockIdx.y];
+        if (by >= a.xtab[0]) return;
+        const int ex = a.xtab[1 + 2 * by], nv = a.xtab[2 + 2 * by];
         sg.W += (int64_t)ex * a.plane[si];
         nsub = (nv + 15) >> 4;
-        mend = (int)blockIdx.y * 16 * MS + nv;
+        mend = by * 16 * MS + nv;
     }
     const int ks = blockIdx.z;
     const int sb0 = ks * a.sb_per_split;
@@ -580,10 +584,11 @@ struct MmDownArgs {
     int M;
     int64_t n_in, N;
     int slices_per_split;
+    int ntt;             // token tiles (grid x = column blocks x token tiles)
     MmOutDev out;
 };
 
-// grid = (N / 256, Mp / 64, splits); block = 256: wave w owns columns
+// grid = (N / 256 x Mp / 64, 1, splits); block = 256: wave w owns columns
 // 256 bx + 64 w .. + 63 (four 16-column tiles ct); per 32-row slice the
 // workgroup stages, for its 64 tokens, A_d = h d 2^10 and A_m = h dmin 2^10
 // (hi / lo) and the fp16 tables sc[s][i], mn[s][i] of the block's 8
@@ -602,8 +607,10 @@ k_mm_down(MmDownArgs a) {
     const int tid = threadIdx.x, lane = tid & 63;
     const int w = __builtin_amdgcn_readfirstlane(tid >> 6);
     const int col = lane & 15, kq = lane >> 4;
-    const int64_t jb = blockIdx.x;
-    const int64_t m0 = (int64_t)blockIdx.y * MM_TOK;
+    // token tiles of one column block are neighbours in the grid (they share
+    // the block's weights)
+    const int64_t jb = blockIdx.x / (unsigned)a.ntt;
+    const int64_t m0 = (int64_t)(blockIdx.x % (unsigned)a.ntt) * MM_TOK;
     const int ks = blockIdx.z;
     const int64_t nsl = a.n_in / 32, nc64 = a.N / 64;
     const int64_t I0 = (int64_t)ks * a.slices_per_split;
@@ -990,7 +997,8 @@ static hipError_t mm_launch(hipStream_t st, const MmSeg* segs, int nseg, const M
     }
     a.sb_per_split = (a.nsb + S - 1) / S;
     S = (a.nsb + a.sb_per_split - 1) / a.sb_per_split;
-    const dim3 grid((unsigned)wg, (unsigned)mt, (unsigned)S);
+    a.ntt = (int)mt;
+    const dim3 grid((unsigned)(wg * mt), 1, (unsigned)S);
     const size_t lds = 2 * (size_t)ms * 16384;
     using K_t = void (*)(MmArgs);
     // [dtype][dense | expert 64-row tiles | expert 16-row tiles]
@@ -1009,7 +1017,7 @@ static hipError_t mm_launch(hipStream_t st, const MmSeg* segs, int nseg, const M
         if (e != hipSuccess) return e;
         lds_set[ki] = true;
     }
-    hipLaunchKernelGGL(kern, grid, dim3(64 * MM_WAVES), lds, st, a);
+    ktimed_launch(kern, grid, dim3(64 * MM_WAVES), (uint32_t)lds, st, a);
     hipError_t e = hipGetLastError();
     if (e != hipSuccess || !via_part) return e;
     MmReduceArgs r{};
@@ -1084,7 +1092,8 @@ hipError_t launch_mm_down(hipStream_t st, const uint8_t* tiled, int64_t n_in, in
     } else {
         a.out = out_dev(out);
     }
-    hipLaunchKernelGGL(k_mm_down, dim3((unsigned)nb, (unsigned)mt, (unsigned)S), dim3(64 * MMD_WAVES),
+    a.ntt = (int)mt;
+    ktimed_launch(k_mm_down, dim3((unsigned)(nb * mt), 1, (unsigned)S), dim3(64 * MMD_WAVES),
                        0, st, a);
     hipError_t e = hipGetLastError();
     if (e != hipSuccess || S == 1) return e;

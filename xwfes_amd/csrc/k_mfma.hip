@@ -829,9 +829,9 @@ hipError_t launch_mv(hipStream_t st, const GemvSeg* segs, int nseg, const int8_t
               k_mv<FTX_Q6_K, true, false, false>}}};
         static const K_t kmix[2][2] = {{k_mv_mix<false, false>, k_mv_mix<false, true>},
                                        {k_mv_mix<true, false>, k_mv_mix<true, true>}};
-        hipLaunchKernelGGL(mixed ? kmix[tiled][deep]
-                                 : kern[dt == FTX_Q6_K][tiled][pair ? 1 : (deep ? 2 : 0)],
-                           gd, bd, 0, st, a);
+        const K_t kf = mixed ? kmix[tiled][deep]
+                             : kern[dt == FTX_Q6_K][tiled][pair ? 1 : (deep ? 2 : 0)];
+        ktimed_launch(kf, gd, bd, 0, st, a);
         hipError_t e = hipGetLastError();
         if (e != hipSuccess) return e;
     }

@@ -569,8 +569,8 @@ hipError_t launch_moe_down(hipStream_t st, const uint8_t* tiled, int dt, int64_t
         if (e != hipSuccess) return e;
         lds_set = true;
     }
-    hipLaunchKernelGGL(k_moe_down, dim3((unsigned)(K / 256), (unsigned)ntile_max, (unsigned)S),
-                       dim3(256), lds, st, a);
+    ktimed_launch(k_moe_down, dim3((unsigned)(K / 256), (unsigned)ntile_max, (unsigned)S),
+                  dim3(256), (uint32_t)lds, st, a);
     return hipGetLastError();
 }
 

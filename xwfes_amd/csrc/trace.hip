@@ -5,10 +5,12 @@
 
 #include "ftx_internal.h"
 
+thread_local KernelTimer* g_ktimer = nullptr;
+
 static const char* kTraceNames[TK_COUNT] = {
     "embed", "rmsnorm", "gemv_qkv", "rope_kv", "attention", "gemv_o",
     "gemv_swiglu", "down", "head", "row_stats", "accept", "xq_prep", "moe_route",
-    "moe_combine"};
+    "moe_combine", "event_pair"};
 
 static void resolve(ftx_ctx* ctx) {
     if (ctx->pending.empty()) {
@@ -20,6 +22,11 @@ static void resolve(ftx_ctx* ctx) {
         float ms = 0.f;
         if (hipEventElapsedTime(&ms, ctx->events[r.ev0], ctx->events[r.ev1]) != hipSuccess) {
             (void)hipGetLastError();
+            continue;
+        }
+        if (r.kernel) {
+            ctx->tr_klaunches[r.kind] += 1;
+            ctx->tr_kms[r.kind] += ms;
             continue;
         }
         ctx->tr_launches[r.kind] += r.launches;
@@ -51,11 +58,28 @@ int tr_begin(ftx_ctx* ctx) {
         (void)hipGetLastError();
         return -1;
     }
+    // arm the kernel timer for the first kernel of this call
+    const int k0 = take_event(ctx), k1 = take_event(ctx);
+    if (k0 >= 0 && k1 >= 0) {
+        ctx->kt.e0 = ctx->events[k0];
+        ctx->kt.e1 = ctx->events[k1];
+        ctx->kt.armed = true;
+        ctx->kt.fired = false;
+        ctx->kt_ev0 = k0;
+        ctx->kt_ev1 = k1;
+        g_ktimer = &ctx->kt;
+    }
     return e;
 }
 
 void tr_end(ftx_ctx* ctx, int token, int kind, double bytes, int launches) {
     if (token < 0 || !ctx->trace) return;
+    if (ctx->kt.armed) {
+        if (ctx->kt.fired)
+            ctx->pending.push_back(TraceRec{kind, ctx->kt_ev0, ctx->kt_ev1, 0.0, 1, true});
+        ctx->kt.armed = false;
+        g_ktimer = nullptr;
+    }
     const int e = take_event(ctx);
     if (e < 0) return;
     if (hipEventRecord(ctx->events[e], ctx->stream) != hipSuccess) {
@@ -75,12 +99,17 @@ int ftx_trace(ftx_ctx* ctx, int enable) {
     if (!ctx) return FTX_E_INVALID;
     resolve(ctx);
     ctx->trace = enable != 0;
-    if (enable)
+    if (enable) {
         for (int k = 0; k < TK_COUNT; ++k) {
             ctx->tr_launches[k] = 0;
             ctx->tr_ms[k] = 0;
             ctx->tr_bytes[k] = 0;
+            ctx->tr_klaunches[k] = 0;
+            ctx->tr_kms[k] = 0;
         }
+        // the brackets' own time: 32 event pairs with nothing between them
+        for (int i = 0; i < 32; ++i) tr_end(ctx, tr_begin(ctx), TK_EVENT_PAIR, 0.0, 1);
+    }
     return FTX_OK;
 }
 
@@ -108,6 +137,8 @@ int ftx_trace_read(ftx_ctx* ctx, ftx_trace_entry* out, int max, int* n) {
             out[c].launches = ctx->tr_launches[k];
             out[c].ms = ctx->tr_ms[k];
             out[c].bytes = ctx->tr_bytes[k];
+            out[c].kernel_launches = ctx->tr_klaunches[k];
+            out[c].kernel_ms = ctx->tr_kms[k];
         }
         ++c;
     }

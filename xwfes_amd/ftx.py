@@ -81,7 +81,7 @@ class AcceptArgs(C.Structure):
 
 class TraceEntry(C.Structure):
     _fields_ = [("name", C.c_char * 24), ("launches", C.c_int64), ("ms", C.c_double),
-                ("bytes", C.c_double)]
+                ("bytes", C.c_double), ("kernel_launches", C.c_int64), ("kernel_ms", C.c_double)]
 
 
 def header_functions(path=HEADER):
@@ -239,7 +239,9 @@ class Context:
         n = C.c_int(0)
         self.check(self.lib.ftx_trace_read(self.h, buf, 32, C.byref(n)))
         return {buf[i].name.decode(): dict(launches=buf[i].launches, ms=buf[i].ms,
-                                           bytes=buf[i].bytes) for i in range(n.value)}
+                                           bytes=buf[i].bytes,
+                                           kernel_launches=buf[i].kernel_launches,
+                                           kernel_ms=buf[i].kernel_ms) for i in range(n.value)}
 
     def trace_replay(self, kind, times):
         """While tracing, issue each replayable launch of class `kind` `times`
