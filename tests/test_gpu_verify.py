@@ -605,6 +605,23 @@ def test_accept_residual_chain_and_tree(gctx, orc, V):
             (o["accepted"], o["bonus"], o["rng"], o["sampler_state"])
 
 
+def test_accept_residual_wide_tree(gctx, orc):
+    """130-node trees (more than 64 children scanned per node, children of
+    one node spread over several 64-node groups) with draft tokens drawn near
+    the target, so that walks go several levels deep."""
+    rng = np.random.default_rng(77)
+    V, M = 3000, 130
+    for trial in range(6):
+        parents = [-1] + [int(rng.integers(-1, i)) if trial % 2 else int(rng.integers(max(-1, i - 70), i))
+                          for i in range(1, M)]
+        base, rows, props = case(rng, M, V, spread=1.0, hit=0.7)
+        q = rng.dirichlet(np.ones(V) * 0.3, size=M).astype(np.float32)
+        seed = int(rng.integers(1, 2**63))
+        g, o = accept_both(gctx, orc, base, rows, props, ftx.ACCEPT_RESIDUAL, 0.8, seed,
+                           parents=parents, q=q)
+        assert (g["accepted"], g["bonus"], g["rng"]) == (o["accepted"], o["bonus"], o["rng"])
+
+
 def test_accept_empty_draft(gctx, orc):
     """M = 0: only the bonus token is drawn."""
     rng = np.random.default_rng(4)
