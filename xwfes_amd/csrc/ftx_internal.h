@@ -383,6 +383,13 @@ struct RopeArgs {
     float eps = 0.f;
 };
 hipError_t launch_rope_kv(hipStream_t st, const RopeArgs& a, int64_t M);
+// several sequences in one launch: sequence s's rows are M[s] tokens
+struct RopeBatch {
+    RopeArgs s[FTX_MAX_SEQ];
+    int row0[FTX_MAX_SEQ + 1];  // first token row of each sequence
+    int nseq;
+};
+hipError_t launch_rope_kv_batch(hipStream_t st, const RopeArgs* as, const int64_t* M, int nseq);
 struct AttnArgs {
     const float* qkv;   // q rows, ldq stride
     int64_t ldq;
@@ -421,6 +428,18 @@ size_t attn_part_floats(int64_t M, int64_t n_head, int64_t hd, int64_t cap_alloc
 // operand (xq_dev.h layout, K = n_head * hd) instead of a.out
 bool attn_combine_xq_supported(int64_t hd, int64_t n_head);
 hipError_t launch_attn_mfma(hipStream_t st, AttnMArgs a, float* part, int8_t* xq = nullptr);
+// several sequences' attention (and the fp32 combine) in one launch each:
+// as[s] as for launch_attn_mfma with the sequence's own partial buffer
+// parts[s]; every sequence has the same head size and kv head count
+struct AttnMBatch {
+    AttnMArgs s[FTX_MAX_SEQ];
+    int nch[FTX_MAX_SEQ];        // chunks of each sequence's cache
+    int qt0[FTX_MAX_SEQ + 1];    // first 32-row query tile of each sequence
+    int qi0[FTX_MAX_SEQ + 1];    // first (token, head) row of each sequence
+    int nseq;
+};
+hipError_t launch_attn_mfma_batch(hipStream_t st, const AttnMArgs* as, const float* const* parts,
+                                  int nseq);
 // KV commit of an accepted draft path (nodes by value: at most 256)
 struct KvCommitArgs {
     int64_t npast;     // committed slots before the draft

@@ -34,8 +34,11 @@ constexpr int ATTN_WAVES_128 = 8;
 // chunks measured slower for hd 128)
 __host__ __device__ constexpr int chunk_slots(int hd) { return hd; }
 
+// The workgroup (chunk c, kv head kvh, query tile qtile) of one sequence's
+// attention; nch = the sequence's chunk count (its partials' stride).
 template <int HD, int CHK, int NWV>
-__global__ void __launch_bounds__(64 * NWV) k_attn_mfma(AttnMArgs a) {
+__device__ __forceinline__ void attn_mfma_wg(const AttnMArgs& a, int c, int kvh, int qtile,
+                                             int nch) {
     constexpr int NDT = HD / 16;  // 16-dim output tiles
     constexpr int NST = CHK / 16; // 16-slot tiles of the chunk
     // score tiles (slot tile, query tile) per wave: pair p = w PPW + i takes
@@ -56,13 +59,11 @@ __global__ void __launch_bounds__(64 * NWV) k_attn_mfma(AttnMArgs a) {
     const int tid = threadIdx.x, w = tid >> 6, lane = tid & 63, col = lane & 15, g = lane >> 4;
     const int64_t npast = a.npast;
     const int64_t total = npast + a.M;
-    const int c = blockIdx.x;
     const int64_t slot0 = (int64_t)c * CHK;
     if (slot0 >= total) return;
-    const int kvh = blockIdx.y;
     const int gqa = a.n_head / a.n_kv;
     const int qrows = a.M * gqa;
-    const int qbase = blockIdx.z * 32;  // first query row of this tile
+    const int qbase = qtile * 32;  // first query row of this tile
     const int64_t kdim = (int64_t)a.n_kv * HD;
     const int sst = (w * PPW) >> 1;          // this wave's slot tile
     const int64_t ws0 = slot0 + 16 * sst;    // its score slots
@@ -195,7 +196,6 @@ __global__ void __launch_bounds__(64 * NWV) k_attn_mfma(AttnMArgs a) {
     // ---- O[:, 16 dt .. 16 dt + 15] = P . V over the chunk: A = P (query row
     // col, slots 16 st + 4g ..), B = V^T rows; lane then holds O[query row
     // qt * 16 + 4g + r][dim 16 dt + col]
-    const int nch = (int)gridDim.x;
 #pragma unroll
     for (int qi = 0; qi < QPW; ++qi) {
         const int qt = QPW == 2 ? qi : w / NDT;
@@ -232,13 +232,28 @@ __global__ void __launch_bounds__(64 * NWV) k_attn_mfma(AttnMArgs a) {
     }
 }
 
+template <int HD, int CHK, int NWV>
+__global__ void __launch_bounds__(64 * NWV) k_attn_mfma(AttnMArgs a) {
+    attn_mfma_wg<HD, CHK, NWV>(a, blockIdx.x, blockIdx.y, blockIdx.z, gridDim.x);
+}
+
+// several sequences in one launch: grid.z runs over every sequence's query
+// tiles (sequence s owns tiles qt0[s] .. qt0[s + 1] - 1); chunks past a
+// sequence's own end return at once
+template <int HD, int CHK, int NWV>
+__global__ void __launch_bounds__(64 * NWV) k_attn_mfma_batch(AttnMBatch b) {
+    int s = 0;
+    while (s + 1 < b.nseq && (int)blockIdx.z >= b.qt0[s + 1]) ++s;
+    attn_mfma_wg<HD, CHK, NWV>(b.s[s], blockIdx.x, blockIdx.y, (int)blockIdx.z - b.qt0[s],
+                               b.nch[s]);
+}
+
 // out[m][h*hd + d] = sum_c e^(max_c - M) O_c[d] / sum_c e^(max_c - M) sum_c
 // one block per query row; the chunk weights are formed once in LDS so the
 // output loop is a stream of independent loads
-__global__ void __launch_bounds__(128) k_attn_combine(AttnMArgs a, int nch) {
+__device__ __forceinline__ void attn_combine_row(const AttnMArgs& a, int64_t qi, int nch) {
     __shared__ float wsh[1024];  // chunk weights (nch <= 1024)
     __shared__ float red[128];
-    const int64_t qi = blockIdx.x;  // m * n_head + h
     const int d = threadIdx.x;
     const int64_t npast = a.npast;
     const int ch = chunk_slots(a.hd);
@@ -273,6 +288,17 @@ __global__ void __launch_bounds__(128) k_attn_combine(AttnMArgs a, int nch) {
         for (int c = 0; c < nvalid; ++c) num += wsh[c] * a.pout[(qi * nch + c) * a.hd + d];
         a.out[qi * a.hd + d] = num / den;
     }
+}
+
+__global__ void __launch_bounds__(128) k_attn_combine(AttnMArgs a, int nch) {
+    attn_combine_row(a, blockIdx.x, nch);  // query row m * n_head + h
+}
+
+// several sequences: sequence s owns blocks qi0[s] .. qi0[s + 1] - 1
+__global__ void __launch_bounds__(128) k_attn_combine_batch(AttnMBatch b) {
+    int s = 0;
+    while (s + 1 < b.nseq && (int)blockIdx.x >= b.qi0[s + 1]) ++s;
+    attn_combine_row(b.s[s], (int64_t)blockIdx.x - b.qi0[s], b.nch[s]);
 }
 
 // The combine of k_attn_combine fused with the activation prep of the
@@ -423,5 +449,46 @@ hipError_t launch_attn_mfma(hipStream_t st, AttnMArgs a, float* part, int8_t* xq
     } else {
         hipLaunchKernelGGL(k_attn_combine, dim3((unsigned)qi), dim3(128), 0, st, a, nch);
     }
+    return hipGetLastError();
+}
+
+hipError_t launch_attn_mfma_batch(hipStream_t st, const AttnMArgs* as, const float* const* parts,
+                                  int nseq) {
+    if (nseq < 1 || nseq > FTX_MAX_SEQ) return hipErrorInvalidValue;
+    AttnMBatch b{};
+    b.nseq = nseq;
+    int hd = as[0].hd, nkv = as[0].n_kv, maxch = 0, qt = 0, qi = 0;
+    for (int s = 0; s < nseq; ++s) {
+        AttnMArgs a = as[s];
+        const int ch = chunk_slots(a.hd);
+        if (a.hd != hd || a.n_kv != nkv || a.cap % ch) return hipErrorInvalidValue;
+        const int nch = (int)(a.cap / ch);
+        if (nch > 1024) return hipErrorInvalidValue;  // combine weights live in LDS
+        const int64_t q = (int64_t)a.M * a.n_head;
+        float* part = const_cast<float*>(parts[s]);
+        a.pmax = part;
+        a.psum = part + q * nch;
+        a.pout = part + 2 * q * nch;
+        b.s[s] = a;
+        b.nch[s] = nch;
+        b.qt0[s] = qt;
+        b.qi0[s] = qi;
+        qt += (int)((a.M * (a.n_head / a.n_kv) + 31) / 32);
+        qi += (int)q;
+        maxch = nch > maxch ? nch : maxch;
+    }
+    b.qt0[nseq] = qt;
+    b.qi0[nseq] = qi;
+    const dim3 grid((unsigned)maxch, (unsigned)nkv, (unsigned)qt);
+    if (hd == 128)
+        ktimed_launch(k_attn_mfma_batch<128, chunk_slots(128), ATTN_WAVES_128>, grid,
+                      dim3(64 * ATTN_WAVES_128), 0, st, b);
+    else if (hd == 64)
+        ktimed_launch(k_attn_mfma_batch<64, chunk_slots(64), 4>, grid, dim3(64 * 4), 0, st, b);
+    else
+        return hipErrorInvalidValue;
+    hipError_t e = hipGetLastError();
+    if (e != hipSuccess) return e;
+    hipLaunchKernelGGL(k_attn_combine_batch, dim3((unsigned)qi), dim3(128), 0, st, b);
     return hipGetLastError();
 }

@@ -45,6 +45,7 @@ constexpr int MOE_MAXM = 256;  // tokens of one step
 constexpr int MOE_MAXE = 256;  // experts
 constexpr int MOE_MAXU = 8;    // experts per token
 constexpr int MOE_TB = 1152;   // bytes of one re-tiled (pair-block, row-group) tile
+constexpr int MOE_GB = 4;      // 4096-element batches of a router row (n_embd <= 16384)
 
 // ---------------------------------------------------------------- route
 // ffn_norm, router and per-token choice, one workgroup per token m: the
@@ -70,10 +71,26 @@ __global__ void __launch_bounds__(256) k_moe_gate(const float* __restrict__ x, i
     const int m = blockIdx.x, t = threadIdx.x, lane = t & 63, w = t >> 6;
     const float* xr = x + (int64_t)m * K;
     float ss = 0.f;
-    for (int64_t k = t; k < K; k += 256) {
-        const float v = xr[k];
-        xs[k] = v;
-        ss += v * v;
+    // 16 elements per thread with their loads in flight together (element
+    // order per thread as a plain strided loop)
+    // (the norm weights' loads go out with the row's and wait in registers:
+    // K <= 256 * 16 * MOE_GB)
+    float nv[MOE_GB][16];
+#pragma unroll
+    for (int b = 0; b < MOE_GB; ++b) {
+        const int64_t k0 = t + (int64_t)b * 256 * 16;
+        if (k0 >= K) break;  // block-uniform for all but the last batch's tail
+        float v[16];
+#pragma unroll
+        for (int i = 0; i < 16; ++i) v[i] = xr[min(k0 + 256 * i, K - 1)];
+#pragma unroll
+        for (int i = 0; i < 16; ++i) nv[b][i] = normw[min(k0 + 256 * i, K - 1)];
+#pragma unroll
+        for (int i = 0; i < 16; ++i)
+            if (k0 + 256 * i < K) {
+                xs[k0 + 256 * i] = v[i];
+                ss += v[i] * v[i];
+            }
     }
 #pragma unroll
     for (int o = 32; o > 0; o >>= 1) ss += __shfl_xor(ss, o, 64);
@@ -81,70 +98,140 @@ __global__ void __launch_bounds__(256) k_moe_gate(const float* __restrict__ x, i
     __syncthreads();
     const float rinv = 1.f / sqrtf((((red[0] + red[1]) + red[2]) + red[3]) / (float)K + eps);
     float* xo = xn + (int64_t)m * K;
-    for (int64_t k = t; k < K; k += 256) {
-        const float v = xs[k] * rinv * normw[k];
-        xs[k] = v;
-        xo[k] = v;
-    }
-    __syncthreads();
-    for (int e = w; e < E; e += 4) {
-        const uint8_t* row = W + (int64_t)e * row_bytes;
-        float acc = 0.f;
-        if (dt == FTX_F32) {
-            const float4* r4 = (const float4*)row;
-            for (int64_t c = lane; c < K / 4; c += 64) {
-                const float4 v = r4[c];
-                acc += v.x * xs[4 * c] + v.y * xs[4 * c + 1] + v.z * xs[4 * c + 2] +
-                       v.w * xs[4 * c + 3];
+#pragma unroll
+    for (int b = 0; b < MOE_GB; ++b)
+#pragma unroll
+        for (int i = 0; i < 16; ++i) {
+            const int64_t k = t + (int64_t)b * 256 * 16 + 256 * i;
+            if (k < K) {
+                const float v = xs[k] * rinv * nv[b][i];
+                xs[k] = v;
+                xo[k] = v;
             }
-        } else {
+        }
+    __syncthreads();
+    if (dt == FTX_F32) {
+        // groups of 8 router rows: every thread's float4s of the group's
+        // rows (4 per row per 4096 columns) in flight together; per row, the
+        // threads' partial dots summed by wave (shuffles) and then in wave
+        // order
+        __shared__ float rsum[4][8];
+        const float4* x4 = (const float4*)xs;
+        const int64_t n4 = K / 4;
+        for (int e0 = 0; e0 < E; e0 += 8) {
+            float acc[8];
+#pragma unroll
+            for (int r = 0; r < 8; ++r) acc[r] = 0.f;
+            for (int64_t p0 = 0; p0 < n4; p0 += 1024) {
+                float4 v[8][4];
+#pragma unroll
+                for (int r = 0; r < 8; ++r) {
+                    const float4* r4 = (const float4*)(W + (int64_t)min(e0 + r, E - 1) * row_bytes);
+#pragma unroll
+                    for (int i = 0; i < 4; ++i) v[r][i] = r4[min(p0 + t + 256 * i, n4 - 1)];
+                }
+#pragma unroll
+                for (int i = 0; i < 4; ++i) {
+                    const int64_t c = p0 + t + 256 * i;
+                    if (c < n4) {
+                        const float4 xv = x4[c];
+#pragma unroll
+                        for (int r = 0; r < 8; ++r)
+                            acc[r] += v[r][i].x * xv.x + v[r][i].y * xv.y + v[r][i].z * xv.z +
+                                      v[r][i].w * xv.w;
+                    }
+                }
+            }
+#pragma unroll
+            for (int r = 0; r < 8; ++r) {
+#pragma unroll
+                for (int o = 32; o > 0; o >>= 1) acc[r] += __shfl_xor(acc[r], o, 64);
+            }
+            if (lane == 0)
+#pragma unroll
+                for (int r = 0; r < 8; ++r) rsum[w][r] = acc[r];
+            __syncthreads();
+            if (t < 8 && e0 + t < E) lg[e0 + t] = ((rsum[0][t] + rsum[1][t]) + rsum[2][t]) + rsum[3][t];
+            __syncthreads();
+        }
+    } else {
+        for (int e = w; e < E; e += 4) {
+            const uint8_t* row = W + (int64_t)e * row_bytes;
+            float acc = 0.f;
             for (int64_t c = lane; c < K / 8; c += 64) {
                 float v[8];
                 dq8(row, dt, 8 * c, K, v);
 #pragma unroll
                 for (int i = 0; i < 8; ++i) acc += v[i] * xs[8 * c + i];
             }
-        }
 #pragma unroll
-        for (int o = 32; o > 0; o >>= 1) acc += __shfl_xor(acc, o, 64);
-        if (lane == 0) lg[e] = acc;
+            for (int o = 32; o > 0; o >>= 1) acc += __shfl_xor(acc, o, 64);
+            if (lane == 0) lg[e] = acc;
+        }
+        __syncthreads();
     }
-    __syncthreads();
-    if (t != 0) return;
-    if (rbias)
-        for (int j = 0; j < E; ++j) lg[j] = lg[j] + rbias[j];
-    float mx = lg[0];
-    for (int j = 1; j < E; ++j) mx = fmaxf(mx, lg[j]);
+    if (w != 0) return;
+    // softmax and top-U on wave 0: lane l holds experts l, l + 64, l + 128,
+    // l + 192 (E <= 256); the arithmetic and its order as one thread's
+    // loops: float max, float exp, double sum in expert order, float scale
+    float pv[4];
+    float mx = -INFINITY;
+#pragma unroll
+    for (int q = 0; q < 4; ++q) {
+        const int j = lane + 64 * q;
+        pv[q] = j < E ? (rbias ? lg[j] + rbias[j] : lg[j]) : -INFINITY;
+        mx = fmaxf(mx, pv[q]);
+    }
+#pragma unroll
+    for (int o = 32; o > 0; o >>= 1) mx = fmaxf(mx, __shfl_xor(mx, o, 64));
+#pragma unroll
+    for (int q = 0; q < 4; ++q) pv[q] = lane + 64 * q < E ? expf(pv[q] - mx) : 0.f;
     double sum = 0.0;
     for (int j = 0; j < E; ++j) {
-        const float e = expf(lg[j] - mx);
-        lg[j] = e;
-        sum += (double)e;
+        float ej = __shfl(pv[0], j & 63, 64);
+        if (j >= 64) ej = __shfl(j < 128 ? pv[1] : (j < 192 ? pv[2] : pv[3]), j & 63, 64);
+        sum += (double)ej;
     }
     const float inv = (float)(1.0 / sum);
-    for (int j = 0; j < E; ++j) lg[j] = lg[j] * inv;
+#pragma unroll
+    for (int q = 0; q < 4; ++q) pv[q] = pv[q] * inv;
+    // the U largest, ties to the lower index: U wave reductions of (p, j)
+    // over the experts not yet taken (a taken expert's key is -1 < p)
+    float key[4];
+#pragma unroll
+    for (int q = 0; q < 4; ++q) key[q] = lane + 64 * q < E ? pv[q] : -2.f;
     int top[MOE_MAXU];
+    float topw[MOE_MAXU];
     for (int u = 0; u < U; ++u) {
-        int best = -1;
-        float bv = 0.f;
-        for (int j = 0; j < E; ++j) {
-            bool taken = false;
-            for (int v = 0; v < u; ++v) taken |= top[v] == j;
-            if (taken) continue;
-            if (best < 0 || lg[j] > bv) {
-                best = j;
-                bv = lg[j];
+        float bv = key[0];
+        int bj = lane;
+#pragma unroll
+        for (int q = 1; q < 4; ++q)
+            if (key[q] > bv) {
+                bv = key[q];
+                bj = lane + 64 * q;
+            }
+#pragma unroll
+        for (int o = 32; o > 0; o >>= 1) {
+            const float ov = __shfl_xor(bv, o, 64);
+            const int oj = __shfl_xor(bj, o, 64);
+            if (ov > bv || (ov == bv && oj < bj)) {
+                bv = ov;
+                bj = oj;
             }
         }
-        top[u] = best;
+        top[u] = bj;
+        topw[u] = bv;
+        if ((bj & 63) == lane) key[bj >> 6] = -1.f;
     }
     float wsum = 0.f;
-    for (int u = 0; u < U; ++u) wsum = wsum + lg[top[u]];
+    for (int u = 0; u < U; ++u) wsum = wsum + topw[u];
     const float winv = wsum > 0.f ? 1.f / wsum : 0.f;
-    for (int u = 0; u < U; ++u) {
-        te[m * U + u] = top[u];
-        tw[m * U + u] = lg[top[u]] * winv;
-    }
+    if (lane == 0)
+        for (int u = 0; u < U; ++u) {
+            te[m * U + u] = top[u];
+            tw[m * U + u] = topw[u] * winv;
+        }
 }
 
 // Grouping, one workgroup: thread e (strided) takes expert e: first use over
@@ -195,19 +282,21 @@ __global__ void __launch_bounds__(256) k_moe_route(const int32_t* __restrict__ t
         r.tab[0] = nt;
     }
     __syncthreads();
+    // expert e's entries in (token, rank) order take its operand rows in
+    // turn (LDS only; the row table is written below)
     for (int e = t; e < E; e += blockDim.x) {
         if (!cnt[e]) continue;
         const int base = TR * tile0[e];
         int k = 0;
-        for (int i = 0; i < MU; ++i)
-            if (te[i] == e) {
-                const int s = base + k < ntile_max * TR ? base + k : 0;
-                slot_of[i] = s;
-                r.slot_tok[s] = i / U;
-                ++k;
-            }
+#pragma unroll 8
+        for (int i = 0; i < MU; ++i) {
+            const bool hit = te[i] == e;
+            if (hit) slot_of[i] = base + k < ntile_max * TR ? base + k : 0;
+            k += hit;
+        }
     }
     __syncthreads();
+    for (int i = t; i < MU; i += blockDim.x) r.slot_tok[slot_of[i]] = i / U;
     for (int m = t; m < M; m += blockDim.x) {
         int idx[MOE_MAXU];
         for (int u = 0; u < U; ++u) idx[u] = m * U + u;
@@ -492,8 +581,8 @@ hipError_t launch_moe_route(hipStream_t st, const float* x, const float* normw, 
                             const float* rbias, int64_t M, int64_t E, int64_t U,
                             const MoeRoute& r) {
     if (M < 1 || M > MOE_MAXM || E < 2 || E > MOE_MAXE || U < 1 || U > MOE_MAXU || U > E ||
-        K < 8 || K % 8 || (K + E) * 4 > 65536 || (dt == FTX_F32 && ((uintptr_t)W & 15)) ||
-        (dt == FTX_F32 && row_bytes % 16))
+        K < 8 || K % 8 || K > 256 * 16 * MOE_GB || (K + E) * 4 > 65536 ||
+        (dt == FTX_F32 && ((uintptr_t)W & 15)) || (dt == FTX_F32 && row_bytes % 16))
         return hipErrorInvalidValue;
     const size_t lds = (size_t)(K + E) * sizeof(float);
     hipLaunchKernelGGL(k_moe_gate, dim3((unsigned)M), dim3(256), lds, st, x, K, normw, eps, xn, W,

@@ -67,10 +67,9 @@ hipError_t launch_rmsnorm(hipStream_t st, const float* x, const float* w, int64_
 // npast + m (src/engine.cpp:555-561).  Before RoPE, when given: the bias of
 // q / k / v and the per-head RMSNorm of q and k (src/engine.cpp:519-542;
 // the head's sum of squares as a wave sum).  One wave per (token, head).
-__global__ void k_rope_kv(RopeArgs a) {
+__device__ __forceinline__ void rope_kv_row(const RopeArgs& a, int64_t m, int64_t h) {
 #pragma clang fp contract(off)
-    const int64_t m = blockIdx.x;
-    const int64_t h = blockIdx.y;  // 0..n_head-1: q heads; then kv heads
+    // h: 0..n_head-1 q heads, then kv heads
     const int64_t half = a.hd / 2;
     const int64_t npast = *a.npast;
     const int64_t pos = npast + a.depth[m];
@@ -137,6 +136,15 @@ __global__ void k_rope_kv(RopeArgs a) {
     }
 }
 
+__global__ void k_rope_kv(RopeArgs a) { rope_kv_row(a, blockIdx.x, blockIdx.y); }
+
+// several sequences: sequence s owns token rows row0[s] .. row0[s + 1] - 1
+__global__ void k_rope_kv_batch(RopeBatch b) {
+    int s = 0;
+    while (s + 1 < b.nseq && (int)blockIdx.x >= b.row0[s + 1]) ++s;
+    rope_kv_row(b.s[s], (int64_t)blockIdx.x - b.row0[s], blockIdx.y);
+}
+
 // V between the canonical per-layer [slot][n_kv*hd] layout and the device
 // [n_kv][hd][slot] layout; one thread per element.
 __global__ void __launch_bounds__(256) k_v_layout(const uint8_t* __restrict__ src,
@@ -169,6 +177,24 @@ hipError_t launch_rope_kv(hipStream_t st, const RopeArgs& a, int64_t M) {
     if (M == 0) return hipSuccess;
     hipLaunchKernelGGL(k_rope_kv, dim3((unsigned)M, (unsigned)(a.n_head + a.n_kv)), dim3(64), 0,
                        st, a);
+    return hipGetLastError();
+}
+
+hipError_t launch_rope_kv_batch(hipStream_t st, const RopeArgs* as, const int64_t* M, int nseq) {
+    if (nseq < 1 || nseq > FTX_MAX_SEQ) return hipErrorInvalidValue;
+    RopeBatch b{};
+    b.nseq = nseq;
+    int rows = 0;
+    for (int s = 0; s < nseq; ++s) {
+        if (as[s].n_head != as[0].n_head || as[s].n_kv != as[0].n_kv) return hipErrorInvalidValue;
+        b.s[s] = as[s];
+        b.row0[s] = rows;
+        rows += (int)M[s];
+    }
+    b.row0[nseq] = rows;
+    if (rows == 0) return hipSuccess;
+    hipLaunchKernelGGL(k_rope_kv_batch, dim3((unsigned)rows, (unsigned)(as[0].n_head + as[0].n_kv)),
+                       dim3(64), 0, st, b);
     return hipGetLastError();
 }
 

@@ -404,8 +404,60 @@ static int verify_large(ftx_ctx* ctx, ftx_model* m, const ftx_seq_args* sq, int6
                          out1(m->qkv, m->ldq, 0), Mt);
             if (rc) return rc;
         }
-        // RoPE, the KV write and attention, per sequence
-        for (int64_t s = 0; s < nseq; ++s) {
+        // RoPE, the KV write and attention: one launch each over all
+        // sequences when every sequence takes the MFMA attention, else per
+        // sequence
+        bool all_mattn = nseq > 1;
+        for (int64_t s = 0; s < nseq && all_mattn; ++s)
+            all_mattn = attn_mfma_supported(hd, sq[s].kv->kv_f16, sq[s].M, d.n_head, d.n_head_kv);
+        if (all_mattn) {
+            RopeArgs ras[FTX_MAX_SEQ];
+            AttnMArgs ams[FTX_MAX_SEQ];
+            const float* parts[FTX_MAX_SEQ];
+            int64_t Ms[FTX_MAX_SEQ];
+            double rope_b = 0.0, attn_b = 0.0;
+            for (int64_t s = 0; s < nseq; ++s) {
+                ftx_kv* kv = sq[s].kv;
+                const int64_t r0 = row0[s], M = sq[s].M, npast = kv->npast;
+                const size_t kvel = 2;
+                uint8_t* kl = (uint8_t*)kv->k + (size_t)(l * kv->cap_alloc * kv->kdim) * kvel;
+                uint8_t* vl = (uint8_t*)kv->v + (size_t)(l * kv->cap_alloc * kv->kdim) * kvel;
+                RopeArgs ra{m->qkv + r0 * m->ldq, m->ldq,  d.n_head,   d.n_head_kv, hd,
+                            d_depth + r0,         d_np + s, d.rope_theta, d.rope_neox, kl,
+                            vl,                   kv->kv_f16, kv->cap_alloc};
+                ra.bias = m->attn_bias[l];
+                ra.qnorm = m->qnorm[l];
+                ra.knorm = m->knorm[l];
+                ra.eps = eps;
+                ra.qh16 = qh + r0 * m->qdim;
+                ra.ql16 = ql + r0 * m->qdim;
+                ras[s] = ra;
+                Ms[s] = M;
+                AttnMArgs am{};
+                am.qkv = m->qkv + r0 * m->ldq;
+                am.ldq = m->ldq;
+                am.qh16 = ra.qh16;
+                am.ql16 = ra.ql16;
+                am.kc = (const _Float16*)kl;
+                am.vt = (const _Float16*)vl;
+                am.cap = kv->cap_alloc;
+                am.npast = npast;
+                am.anc = d_anc + r0 * aw;
+                am.anc_words = aw;
+                am.M = (int)M;
+                am.n_head = (int)d.n_head;
+                am.n_kv = (int)d.n_head_kv;
+                am.hd = (int)hd;
+                am.out = m->att + r0 * m->qdim;
+                ams[s] = am;
+                parts[s] = kv->attn_part;
+                rope_b += 2.0 * M * m->ldq * f4 + 2.0 * M * m->kdim * (double)kvel;
+                attn_b += 2.0 * (double)(npast + M) * m->kdim * (double)kvel + 2.0 * M * m->qdim * f4;
+            }
+            TRACED_L(TK_ROPE_KV, rope_b, launch_rope_kv_batch(st, ras, Ms, (int)nseq));
+            TRACED_L(TK_ATTENTION, attn_b, launch_attn_mfma_batch(st, ams, parts, (int)nseq));
+        }
+        for (int64_t s = 0; s < nseq && !all_mattn; ++s) {
             ftx_kv* kv = sq[s].kv;
             const int64_t r0 = row0[s], M = sq[s].M, npast = kv->npast;
             const size_t kvel = kv->kv_f16 ? 2 : 4;
