@@ -12,6 +12,10 @@
 //         super-block on the m_j
 //   Q8_0  w = d*q                   B = q, one temporary per 32-block
 //   Q4_0  w = d*(q - 8)             B = q - 8, the same
+//   Q6_K  w = d*sc_s*(q - 32)       sc_s = 16 sh + sl (sh in -8..7, sl in
+//         0..15): B = sl (q - 32) (<= 480) and 16 sh (q - 32) (<= 4096, a
+//         power-of-two multiple of an exact <= 256), both exact in fp16; a
+//         super-block accumulates into a temporary added with the factor d
 // so every product and sum inside an MFMA is exact and the rounding is that
 // of fp32 accumulation.
 //
@@ -224,12 +228,25 @@ struct MmW<FTX_Q4_0_MMT> {
     v4i q[MM_NT][2];   // 4 quant bytes (8 nibbles) of each 32-block, four blocks per vector
     v4i d[MM_NT];
 };
+template <>
+struct MmW<FTX_Q6_K_MMT> {
+    v4i q[MM_NT][3];   // the lane's 32 ql bytes (4 runs of 8) and 16 qh bytes (2 runs of 8)
+    v4i sc[MM_NT];     // its row's 16 int8 sub-block scales
+    uint32_t d[MM_NT]; // its row's fp16 super-block scale
+};
 
 // the re-tiled Q8_0 / Q4_0 copy (k_mm_tile): per 16-row tile and 256-element
-// step, [lane 64][bytes of the lane's 8 blocks] then [row 16][8 fp16 scales]
-__host__ __device__ constexpr int64_t mmt_lane_bytes(int dt) { return dt == FTX_Q8_0_MMT ? 64 : 32; }
+// step, [lane 64][bytes of the lane's 8 blocks] then [row 16][8 fp16 scales].
+// Q6_K: [lane 64][48 bytes] then [row 16][16 int8 scales] then [row 16][fp16
+// d]; lane (col, kq) of row 16 T + col holds ql bytes 64 h + 32 a + 8 kq ..
+// + 7 as run 2 h + a (h, a = 0, 1) and qh bytes 32 h + 8 kq .. + 7 as run 4
+// + h (GGUF super-block byte indices), i.e. elements 8 kq .. 8 kq + 7 of
+// every 32-element step
+__host__ __device__ constexpr int64_t mmt_lane_bytes(int dt) {
+    return dt == FTX_Q8_0_MMT ? 64 : (dt == FTX_Q6_K_MMT ? 48 : 32);
+}
 __host__ __device__ constexpr int64_t mmt_step_bytes(int dt) {
-    return 64 * mmt_lane_bytes(dt) + 16 * 16;
+    return 64 * mmt_lane_bytes(dt) + 16 * 16 + (dt == FTX_Q6_K_MMT ? 32 : 0);
 }
 
 // The lane's weight addresses at step 0, computed once per wave: lane (col
@@ -237,7 +254,8 @@ __host__ __device__ constexpr int64_t mmt_step_bytes(int dt) {
 // each 32-element K-step, i.e. elements 8 kq .. 8 kq + 7 of its row.
 struct MmPtr {
     const uint8_t* q[MM_NT];  // Q4_K: the lane's bytes of chunk 0; Q8_0 / Q4_0: of step 0
-    const uint8_t* h[MM_NT];  // Q4_K: its row's header; Q8_0 / Q4_0: its row's scales
+    const uint8_t* h[MM_NT];  // Q4_K: its row's header; Q8_0 / Q4_0 / Q6_K: its row's scales
+    const uint8_t* dd[MM_NT]; // Q6_K: its row's d
     int64_t qstep, hstep;     // bytes per 256-element step
     int cstride;              // Q4_K: bytes from one 64-element chunk to the next
 };
@@ -262,6 +280,7 @@ __device__ __forceinline__ void mm_ptrs(MmPtr& p, const MmSegDev& sg, int64_t rb
             const uint8_t* tile = sg.W + T * nsb * mmt_step_bytes(DT);
             p.q[t] = tile + (col + 16 * kq) * mmt_lane_bytes(DT);
             p.h[t] = tile + 64 * mmt_lane_bytes(DT) + col * 16;
+            p.dd[t] = tile + 64 * mmt_lane_bytes(DT) + 256 + col * 2;
         }
     }
     if constexpr (DT == FTX_Q4_K) {
@@ -287,6 +306,11 @@ __device__ __forceinline__ void mm_load(MmW<DT>& o, const MmPtr& p, int sb) {
 #pragma unroll
             for (int v = 0; v < 4; ++v) o.q[t][v] = *(const v4i*)(q + 16 * v);
             o.d[t] = *(const v4i*)(p.h[t] + ho);
+        } else if constexpr (DT == FTX_Q6_K_MMT) {
+#pragma unroll
+            for (int v = 0; v < 3; ++v) o.q[t][v] = *(const v4i*)(q + 16 * v);
+            o.sc[t] = *(const v4i*)(p.h[t] + ho);
+            o.d[t] = *(const uint16_t*)(p.dd[t] + ho);
         } else {
 #pragma unroll
             for (int v = 0; v < 2; ++v) o.q[t][v] = *(const v4i*)(q + 16 * v);
@@ -442,7 +466,7 @@ __global__ void __launch_bounds__(64 * MM_WAVES)
                 ah[ms] = frag(buf, 0, ms, j);
                 al[ms] = frag(buf, 1, ms, j);
             }
-            v8h bw[MM_NT];
+            v8h bw[MM_NT], bw2[MM_NT];
             float bs[MM_NT];
 #pragma unroll
             for (int t = 0; t < MM_NT; ++t) {
@@ -471,12 +495,47 @@ __global__ void __launch_bounds__(64 * MM_WAVES)
                     const v4i qv = wc.q[t][j >> 1];
                     bw[t] = i8x8((j & 1) ? v2i{qv[2], qv[3]} : v2i{qv[0], qv[1]});
                     bs[t] = scale8(wc.d[t], j);
+                } else if constexpr (DT == FTX_Q6_K_MMT) {
+                    // elements 32 j + 8 kq .. + 7: half h, 32-group g of it;
+                    // low nibbles from ql run 2 h + (g & 1) (high half of
+                    // the byte for g >= 2), two high bits from qh run h
+                    const int h = j >> 2, g = j & 3, run = 2 * h + (g & 1);
+                    const v4i qv = wc.q[t][run >> 1], hv = wc.q[t][2];
+                    const uint32_t w0 = (uint32_t)qv[2 * (run & 1)], w1 = (uint32_t)qv[2 * (run & 1) + 1];
+                    const uint32_t h0 = (uint32_t)hv[2 * h], h1 = (uint32_t)hv[2 * h + 1];
+                    const uint32_t b0 = ((w0 >> (4 * (g >> 1))) & 0x0F0F0F0Fu) |
+                                        (((h0 >> (2 * g)) & 0x03030303u) << 4);
+                    const uint32_t b1 = ((w1 >> (4 * (g >> 1))) & 0x0F0F0F0Fu) |
+                                        (((h1 >> (2 * g)) & 0x03030303u) << 4);
+                    // the scale of sub-block 2 j + kq / 2, split 16 sh + sl
+                    const int sc = (int)(int8_t)(((uint32_t)wc.sc[t][j >> 1]) >>
+                                                 (8 * (2 * (j & 1) + (kq >> 1))));
+                    const int sl = sc & 15, sh = sc >> 4;
+                    const _Float16 fl = (_Float16)(float)sl, fh = (_Float16)(float)sh;
+                    const _Float16 ol = (_Float16)(float)(-1056 * sl), oh = (_Float16)(float)(-1056 * sh);
+                    const v2h l1 = {fl, fl}, l0 = {ol, ol}, m1 = {fh, fh}, m0 = {oh, oh};
+                    const v2h s16 = {(_Float16)16.f, (_Float16)16.f};
+                    v2h q[4];
+                    q[0] = __builtin_bit_cast(v2h, __builtin_amdgcn_perm(b0, 0x64646464u, 0x00050004u));
+                    q[1] = __builtin_bit_cast(v2h, __builtin_amdgcn_perm(b0, 0x64646464u, 0x00070006u));
+                    q[2] = __builtin_bit_cast(v2h, __builtin_amdgcn_perm(b1, 0x64646464u, 0x00050004u));
+                    q[3] = __builtin_bit_cast(v2h, __builtin_amdgcn_perm(b1, 0x64646464u, 0x00070006u));
+                    v2h r1[4], r2[4];
+#pragma unroll
+                    for (int i = 0; i < 4; ++i) {
+                        // (1024 + q) x - 1056 x = x (q - 32), exact
+                        r1[i] = __builtin_elementwise_fma(q[i], l1, l0);
+                        r2[i] = __builtin_elementwise_fma(q[i], m1, m0) * s16;
+                    }
+                    bw[t] = v8h{r1[0][0], r1[0][1], r1[1][0], r1[1][1], r1[2][0], r1[2][1], r1[3][0], r1[3][1]};
+                    bw2[t] = v8h{r2[0][0], r2[0][1], r2[1][0], r2[1][1], r2[2][0], r2[2][1], r2[3][0], r2[3][1]};
+                    bs[t] = 0.f;
                 } else {
                     bw[t] = nib8((uint32_t)wc.q[t][j >> 2][j & 3], 8.f);
                     bs[t] = scale8(wc.d[t], j);
                 }
             }
-            if constexpr (DT == FTX_Q4_K) {
+            if constexpr (DT == FTX_Q4_K || DT == FTX_Q6_K_MMT) {
                 // hi parts of every tile first, then lo: no MFMA waits on the
                 // one before it
 #pragma unroll
@@ -495,6 +554,20 @@ __global__ void __launch_bounds__(64 * MM_WAVES)
                         tmp[t][ms] =
                             __builtin_amdgcn_mfma_f32_16x16x32_f16(al[ms], bw[t], tmp[t][ms], 0, 0, 0);
                     }
+                if constexpr (DT == FTX_Q6_K_MMT) {
+#pragma unroll
+                    for (int t = 0; t < MM_NT; ++t)
+#pragma unroll
+                        for (int ms = 0; ms < MS; ++ms)
+                            tmp[t][ms] = __builtin_amdgcn_mfma_f32_16x16x32_f16(ah[ms], bw2[t],
+                                                                                tmp[t][ms], 0, 0, 0);
+#pragma unroll
+                    for (int t = 0; t < MM_NT; ++t)
+#pragma unroll
+                        for (int ms = 0; ms < MS; ++ms)
+                            tmp[t][ms] = __builtin_amdgcn_mfma_f32_16x16x32_f16(al[ms], bw2[t],
+                                                                                tmp[t][ms], 0, 0, 0);
+                }
             } else {
                 v4f p[MM_NT][MS];
 #pragma unroll
@@ -519,6 +592,16 @@ __global__ void __launch_bounds__(64 * MM_WAVES)
 #pragma unroll
                         for (int r = 0; r < 4; ++r) acc[t][ms][r] += bs[t] * p[t][ms][r];
                     }
+            }
+        }
+        if constexpr (DT == FTX_Q6_K_MMT) {
+#pragma unroll
+            for (int t = 0; t < MM_NT; ++t) {
+                const float d = h2f((uint16_t)wc.d[t]);
+#pragma unroll
+                for (int ms = 0; ms < MS; ++ms)
+#pragma unroll
+                    for (int r = 0; r < 4; ++r) acc[t][ms][r] += d * tmp[t][ms][r];
             }
         }
         if constexpr (DT == FTX_Q4_K) {
@@ -754,7 +837,9 @@ k_mm_down(MmDownArgs a) {
 // one-pass GEMM's tiles: thread (plane, tile T, step s, lane l) copies the
 // lane's bytes of the step's 8 blocks (row 16 T + l % 16, bytes 8 (l / 16) ..
 // (Q8_0) or 4 (l / 16) .. (Q4_0) of each block's quants), threads past the
-// lanes copy the tile's 16 x 8 scales; rows past `rows` are zeros.
+// lanes copy the tile's 16 x 8 scales; rows past `rows` are zeros.  Q6_K
+// (from the planar device rows): the lane's ql / qh runs, then the rows'
+// scales and d.
 __global__ void __launch_bounds__(256) k_mm_tile(const uint8_t* __restrict__ src, int dt,
                                                  int64_t rows, int64_t nplanes, int64_t K,
                                                  uint8_t* __restrict__ dst) {
@@ -768,6 +853,31 @@ __global__ void __launch_bounds__(256) k_mm_tile(const uint8_t* __restrict__ src
     const int w = (int)(id % 80);
     const int64_t s = u % nsb, T = (u / nsb) % tiles, pl = u / (nsb * tiles);
     uint8_t* out = dst + u * mmt_step_bytes(dt);
+    if (dt == FTX_Q6_K_MMT) {
+        // from the planar Q6_K rows (quant_dev.h): QL, QH, SC and D planes
+        const int64_t prb = q6k_dev_row_bytes(K);
+        const uint8_t* pp = src + pl * rows * prb;
+        if (w < 64) {
+            const int col = w & 15, kq = w >> 4;
+            const int64_t n = 16 * T + col;
+            const uint8_t* row = pp + n * prb;
+            for (int r = 0; r < 4; ++r)
+                for (int i = 0; i < 8; ++i)
+                    out[w * 48 + 8 * r + i] =
+                        n < rows ? row[s * 128 + q6k_ql_dev(32 * r + 8 * kq + i)] : 0;
+            for (int h = 0; h < 2; ++h)
+                for (int i = 0; i < 8; ++i)
+                    out[w * 48 + 32 + 8 * h + i] =
+                        n < rows ? row[nsb * 128 + s * 64 + q6k_qh_dev(32 * h + 8 * kq + i)] : 0;
+        } else {
+            const int r = w - 64;
+            const int64_t n = 16 * T + r;
+            const uint8_t* row = pp + n * prb;
+            for (int i = 0; i < 16; ++i) out[64 * 48 + r * 16 + i] = n < rows ? row[nsb * 192 + s * 16 + i] : 0;
+            for (int i = 0; i < 2; ++i) out[64 * 48 + 256 + r * 2 + i] = n < rows ? row[nsb * 208 + s * 2 + i] : 0;
+        }
+        return;
+    }
     const uint8_t* plane = src + pl * rows * rb;
     if (w < 64) {
         const int col = w & 15, kq = w >> 4;
@@ -873,13 +983,16 @@ hipError_t launch_mm_prep(hipStream_t st, const float* x, int64_t ldx, const flo
 }
 
 bool mm_supported(int dt, int64_t K) {
-    return (dt == FTX_Q4_K || dt == FTX_Q8_0_MMT || dt == FTX_Q4_0_MMT) && K % 256 == 0 &&
-           K >= 256;
+    return (dt == FTX_Q4_K || dt == FTX_Q8_0_MMT || dt == FTX_Q4_0_MMT || dt == FTX_Q6_K_MMT) &&
+           K % 256 == 0 && K >= 256;
 }
 
 int mm_tiled_dtype(int dt, int64_t K) {
     if (K % 256) return -1;
-    return dt == FTX_Q8_0 ? FTX_Q8_0_MMT : (dt == FTX_Q4_0 ? FTX_Q4_0_MMT : -1);
+    return dt == FTX_Q8_0   ? FTX_Q8_0_MMT
+           : dt == FTX_Q4_0 ? FTX_Q4_0_MMT
+           : dt == FTX_Q6_K ? FTX_Q6_K_MMT
+                            : -1;
 }
 
 size_t mm_tiled_bytes(int mdt, int64_t rows, int64_t K) {
@@ -1001,15 +1114,18 @@ static hipError_t mm_launch(hipStream_t st, const MmSeg* segs, int nseg, const M
     const dim3 grid((unsigned)(wg * mt), 1, (unsigned)S);
     const size_t lds = 2 * (size_t)ms * 16384;
     using K_t = void (*)(MmArgs);
-    // [dtype][dense | expert 64-row tiles | expert 16-row tiles]
-    static const K_t kerns[3][3] = {
+    // [dtype][dense | expert 64-row tiles | expert 16-row tiles] (Q6_K:
+    // dense only)
+    static const K_t kerns[4][3] = {
         {k_mm<FTX_Q4_K, false, 4>, k_mm<FTX_Q4_K, true, 4>, k_mm<FTX_Q4_K, true, 1>},
         {k_mm<FTX_Q8_0_MMT, false, 4>, k_mm<FTX_Q8_0_MMT, true, 4>, k_mm<FTX_Q8_0_MMT, true, 1>},
-        {k_mm<FTX_Q4_0_MMT, false, 4>, k_mm<FTX_Q4_0_MMT, true, 4>, k_mm<FTX_Q4_0_MMT, true, 1>}};
-    const int di = dt == FTX_Q4_K ? 0 : (dt == FTX_Q8_0_MMT ? 1 : 2);
+        {k_mm<FTX_Q4_0_MMT, false, 4>, k_mm<FTX_Q4_0_MMT, true, 4>, k_mm<FTX_Q4_0_MMT, true, 1>},
+        {k_mm<FTX_Q6_K_MMT, false, 4>, nullptr, nullptr}};
+    const int di = dt == FTX_Q4_K ? 0 : (dt == FTX_Q8_0_MMT ? 1 : (dt == FTX_Q4_0_MMT ? 2 : 3));
     const int vi = !xtab ? 0 : (ms == 4 ? 1 : 2);
     const K_t kern = kerns[di][vi];
-    static bool lds_set[9] = {};
+    if (!kern) return hipErrorInvalidValue;
+    static bool lds_set[12] = {};
     const int ki = di * 3 + vi;
     if (!lds_set[ki]) {
         hipError_t e = hipFuncSetAttribute((const void*)kern,

@@ -23,6 +23,7 @@ constexpr int FTX_Q4_0_PLANAR = 102;
 // and 256-element step, every lane's bytes of the step contiguous
 constexpr int FTX_Q8_0_MMT = 118;
 constexpr int FTX_Q4_0_MMT = 112;
+constexpr int FTX_Q6_K_MMT = 114;  // from the planar Q6_K rows below
 
 __device__ __forceinline__ float h2f(uint16_t h) {
     return (float)__builtin_bit_cast(_Float16, h);

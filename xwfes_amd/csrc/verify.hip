@@ -675,7 +675,7 @@ int ftx_model_create(ftx_ctx* ctx, const ftx_model_desc* d, ftx_model** out) {
             for (const ftx_tensor* t : {ge, ue, de})
                 if (t->ne[0] != D || t->ne[1] != d->n_ff || t->ne[2] != E || t->ne[3] != 1)
                     return ftx_fail(ctx, FTX_E_INVALID, "bad shape of an expert tensor");
-            if (ge->dtype != ue->dtype || mm_tiled_dtype(ge->dtype, D) < 0 ||
+            if (ge->dtype != ue->dtype || (ge->dtype != FTX_Q4_0 && ge->dtype != FTX_Q8_0) ||
                 !mm_supported(mm_tiled_dtype(ge->dtype, D), D))
                 return ftx_fail(ctx, FTX_E_UNSUPPORTED,
                                 "MoE gate / up experts must share Q4_0 or Q8_0 with n_embd % 256 == 0");
@@ -818,6 +818,7 @@ int ftx_model_create(ftx_ctx* ctx, const ftx_model_desc* d, ftx_model** out) {
         if (!w) continue;
         const int mdt = mm_tiled_dtype(w->dtype, w->ne[0]);
         if (mdt < 0 || !mm_supported(mdt, w->ne[0])) continue;
+        if (mdt == FTX_Q6_K_MMT && m->Mmax <= 8) continue;  // only the large-M path reads it
         uint8_t* buf = nullptr;
         if (!dalloc(&buf, mm_tiled_bytes(mdt, w->nrows, w->ne[0]))) {
             ok = false;
