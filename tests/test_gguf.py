@@ -270,3 +270,56 @@ def test_reference_engine_steps_equal_oracle_forward(tmp_path, orc, ref):
         for i, r in enumerate(rows):
             err = np.abs(r - want[i]).max() / np.abs(want[i]).max()
             assert err <= 1e-6, (seed, i, err)
+
+
+def test_writer_regenerates_reference_test_model(tmp_path):
+    """The package's writer reproduces the reference's own test model byte
+    for byte (src/tests/test_core.cpp:79-213: qwen3moe, L 2, D 16, 4 / 2
+    heads of 4, 4 experts of FFN 32, vocabulary 27, F32 tensors, norms 1,
+    every other weight rnd() * 0.3 from the test's LCG, 32-byte alignment).
+    The reference's build writes that file as build/ft_test_model.gguf:
+    62240 bytes, sha256 4a024de1...7753."""
+    import hashlib
+    L, D, H, KVH, HD, E, FF, V = 2, 16, 4, 2, 4, 4, 32, 27
+    kv = [("general.architecture", G.T_STR, "qwen3moe"),
+          ("qwen3moe.block_count", G.T_U32, L),
+          ("qwen3moe.embedding_length", G.T_U32, D),
+          ("qwen3moe.attention.head_count", G.T_U32, H),
+          ("qwen3moe.attention.head_count_kv", G.T_U32, KVH),
+          ("qwen3moe.attention.key_length", G.T_U32, HD),
+          ("qwen3moe.context_length", G.T_U32, 128),
+          ("qwen3moe.attention.layer_norm_rms_epsilon", G.T_F32, 1e-5),
+          ("qwen3moe.rope.freq_base", G.T_F32, 10000.0),
+          ("tokenizer.ggml.model", G.T_STR, "llama"),
+          ("tokenizer.ggml.tokens", G.T_ARR, (G.T_STR, ["<pad>"] + [chr(c) for c in range(97, 123)])),
+          ("tokenizer.ggml.bos_token_id", G.T_I32, -1),
+          ("tokenizer.ggml.eos_token_id", G.T_I32, -1)]
+    shapes = [("token_embd.weight", (D, V)), ("output_norm.weight", (D,)), ("output.weight", (D, V))]
+    for l in range(L):
+        p = "blk.%d." % l
+        shapes += [(p + "attn_norm.weight", (D,)), (p + "attn_q.weight", (D, H * HD)),
+                   (p + "attn_k.weight", (D, KVH * HD)), (p + "attn_v.weight", (D, KVH * HD)),
+                   (p + "attn_output.weight", (H * HD, D)), (p + "attn_q_norm.weight", (HD,)),
+                   (p + "attn_k_norm.weight", (HD,)), (p + "post_attention_norm.weight", (D,)),
+                   (p + "ffn_gate_inp.weight", (D, E)), (p + "ffn_gate_exps.weight", (D, FF, E)),
+                   (p + "ffn_up_exps.weight", (D, FF, E)), (p + "ffn_down_exps.weight", (D, FF, E))]
+    state = [123456789]
+
+    def rnd():  # g = g * 1664525 + 1013904223 (mod 2^32); uniform in [-1, 1) in float
+        state[0] = (state[0] * 1664525 + 1013904223) & 0xFFFFFFFF
+        return np.float32((state[0] >> 9) & 0x7FFF) / np.float32(32768) * np.float32(2) - np.float32(1)
+
+    tensors = []
+    for name, ne in shapes:
+        n = int(np.prod(ne))
+        if "norm" in name:
+            vals = np.ones(n, np.float32)
+        else:
+            vals = np.array([rnd() * np.float32(0.3) for _ in range(n)], np.float32)
+        tensors.append((name, G.F32, ne, vals.tobytes()))
+    path = str(tmp_path / "ft_test_model.gguf")
+    G.write_gguf(path, kv, tensors)
+    blob = open(path, "rb").read()
+    assert len(blob) == 62240
+    assert hashlib.sha256(blob).hexdigest() == \
+        "4a024de1c8b1e9bc554cefaf211710c9384f3155833fb95518695fb0c8747753"
