@@ -435,8 +435,48 @@ static void test_gguf_verifier(HipBackend& be, const char* path) {
     be.evict(w.output);
 }
 
+// speculative generate through the C++ host path: target and draft models
+// from GGUF files (C++ loader), DraftModelDrafter + generate on the device;
+// prints the emitted tokens and the round statistics for the caller to
+// compare with the oracle's generate.
+// args: target.gguf draft.gguf temp spec_k max_new cap prompt tokens...
+static int run_generate(HipBackend& be, int argc, char** argv) {
+    if (argc < 9) {
+        std::fprintf(stderr, "--generate target draft temp spec_k max_new cap tokens...\n");
+        return 2;
+    }
+    const float temp = (float)std::atof(argv[4]);
+    const int spec_k = std::atoi(argv[5]);
+    const int64_t max_new = std::atoll(argv[6]), cap = std::atoll(argv[7]);
+    std::vector<int32_t> prompt;
+    for (int i = 8; i < argc; ++i) prompt.push_back((int32_t)std::atoi(argv[i]));
+    Gguf gt(argv[2]), gd(argv[3]);
+    GgufConfig ct = config_from_gguf(gt), cd = config_from_gguf(gd);
+    ModelWeights wt = weights_from_gguf(gt, ct.cfg), wd = weights_from_gguf(gd, cd.cfg);
+    std::vector<int32_t> out;
+    GenerateStats st;
+    {
+        HipVerifier target(be, ct.cfg, wt, cap, 8), draft(be, cd.cfg, wd, cap, 8);
+        DraftModelDrafter drafter(draft);
+        out = generate(target, drafter, prompt, max_new, spec_k, temp, 40, 0.95f, 0, &st);
+    }
+    std::printf("generate tokens:");
+    for (int32_t t : out) std::printf(" %d", t);
+    std::printf("\ngenerate stats: %lld %lld %lld\n", (long long)st.rounds, (long long)st.drafted,
+                (long long)st.accepted);
+    for (ModelWeights* w : {&wt, &wd}) {
+        for (const auto& L : w->layers)
+            for (const auto& t : L) be.evict(t);
+        be.evict(w->tok_embd);
+        be.evict(w->out_norm);
+        be.evict(w->output);
+    }
+    return 0;
+}
+
 int main(int argc, char** argv) {
     HipBackend be(0);
+    if (argc > 1 && !std::strcmp(argv[1], "--generate")) return run_generate(be, argc, argv);
     if (argc > 2 && !std::strcmp(argv[1], "--gguf")) {
         for (int i = 2; i < argc; ++i) test_gguf_verifier(be, argv[i]);
         std::printf("test_hip_backend: all %d checks passed\n", g_checks);

@@ -183,8 +183,15 @@ const float* HipVerifier::extend_verify(const std::vector<int32_t>& props,
     return logits_;
 }
 
-const float* HipVerifier::step(int32_t token) {
-    return extend_verify({token}, {}, true);
+const float* HipVerifier::step(int32_t token, float* logits) {
+    if (!logits) return extend_verify({token}, {}, true);
+    ftx_verify_args a{};
+    a.M = 1;
+    a.tokens = &token;
+    a.logits = logits;
+    a.advance = 1;
+    be_.check(ftx_verify_step(be_.ctx(), model_, kv_, &a), "step");
+    return logits;
 }
 
 const float* HipVerifier::prefill(const std::vector<int32_t>& tokens, int64_t chunk) {
@@ -236,7 +243,8 @@ Accepted accept_on_device(HipBackend& be, int64_t V, const float* base_row, cons
     a.q = q;
     a.M = M;
     a.V = V;
-    a.props = props.data();
+    const int32_t none = 0;  // an empty draft still passes a props pointer
+    a.props = props.empty() ? &none : props.data();
     a.parents = parents.empty() ? nullptr : parents.data();
     a.pd = pd.empty() ? nullptr : pd.data();
     a.mode = (int32_t)mode;
@@ -260,6 +268,116 @@ Accepted HipVerifier::accept(const float* base_row, const float* rows,
                              const std::vector<int32_t>& parents, const float* q) {
     return accept_on_device(be_, cfg_.vocab, base_row, rows, props, mode, temp, rng, pd, parents,
                             q, &sampler);
+}
+
+void DraftModelDrafter::sync(const std::vector<int32_t>& history) {
+    const int64_t n = (int64_t)history.size();
+    if (m_.npast() > n) m_.truncate_to(0);
+    const int64_t have = m_.npast();
+    if (have < n) {
+        constexpr int64_t chunk = 8;
+        const std::vector<int32_t> rest(history.begin() + have, history.end());
+        const float* lg = m_.prefill(rest, chunk);
+        row_ = lg + ((int64_t)rest.size() - 1) % chunk * m_.config().vocab;
+    }
+}
+
+void DraftModelDrafter::draft(const std::vector<int32_t>& history, int k,
+                              std::vector<int32_t>& props, std::vector<float>& probs) {
+    sync(history);
+    if (!row_) throw std::runtime_error("DraftModelDrafter: no logits (empty history)");
+    pending_base_ = (int64_t)history.size();
+    props.clear();
+    probs.clear();
+    for (int j = 0; j < k; ++j) {
+        int32_t t = 0;
+        float p = 0.f;
+        m_.backend().check(ftx_argmax_prob(m_.backend().ctx(), row_, m_.config().vocab, &t, &p),
+                           "argmax_prob");
+        props.push_back(t);
+        probs.push_back(p);
+        if (j + 1 < k) row_ = m_.step(t);
+    }
+}
+
+void DraftModelDrafter::on_commit(int64_t accepted) {
+    m_.truncate_to(std::min(pending_base_ + accepted, m_.npast()));
+}
+
+void cut_draft(std::vector<int32_t>& props, std::vector<float>& probs) {
+    size_t cut = props.size();
+    double cum = 1.0;
+    for (size_t i = 0; i < probs.size(); ++i) {
+        const float p = probs[i];
+        if (p >= 0.f && p < 0.02f) {
+            cut = i;
+            break;
+        }
+        cum *= p > 0.f ? (double)p : 1.0;
+        if (cum < (double)0.05f) {
+            cut = i + 1;
+            break;
+        }
+    }
+    props.resize(cut);
+    probs.resize(cut);
+}
+
+std::vector<int32_t> generate(HipVerifier& target, DraftModelDrafter& drafter,
+                              const std::vector<int32_t>& prompt, int64_t max_new, int spec_k,
+                              float temp, int32_t top_k, float top_p, uint64_t seed,
+                              GenerateStats* stats) {
+    HipBackend& be = target.backend();
+    const int64_t V = target.config().vocab;
+    constexpr int64_t chunk = 8;
+    if (spec_k < 1 || spec_k > 8 || spec_k > target.max_tokens() || target.max_tokens() < chunk)
+        throw std::runtime_error("generate: spec_k must be in 1..8 within the target's max_tokens");
+    if (prompt.empty()) throw std::runtime_error("generate: empty prompt");
+    float* base = (float*)be.alloc_staging((size_t)V * sizeof(float));
+    if (!base) throw std::runtime_error("generate: base row allocation failed");
+    std::vector<int32_t> out;
+    try {
+        target.truncate_to(0);
+        const float* lg = target.prefill(prompt, chunk);
+        be.stage(base, lg + ((int64_t)prompt.size() - 1) % chunk * V, (size_t)V * sizeof(float));
+        std::vector<int32_t> history = prompt;
+        uint64_t rsamp = seed ? seed : 88172645463325252ull;  // src/spec.cpp:259
+        target.sampler.state = seed ? seed : 0x9E3779B97F4A7C15ull;
+        // temp <= 0: the ratio test at T = 1 and a top-1 bonus (the argmax)
+        const float acc_temp = temp > 0.f ? temp : 1.f;
+        target.sampler.top_k = temp > 0.f ? top_k : 1;
+        target.sampler.top_p = temp > 0.f ? top_p : 1.f;
+        std::vector<int32_t> props;
+        std::vector<float> probs;
+        while ((int64_t)out.size() < max_new) {
+            drafter.draft(history, spec_k, props, probs);
+            cut_draft(props, probs);
+            const int64_t np_before = target.npast();
+            const float* rows = props.empty() ? nullptr : target.extend_verify(props);
+            const Accepted r = target.accept(base, rows, props, AcceptMode::Ratio, acc_temp, rsamp,
+                                             probs);
+            const int64_t acc = (int64_t)r.nodes.size();
+            target.truncate_to(np_before + acc);
+            if (stats) {
+                ++stats->rounds;
+                stats->drafted += (int64_t)props.size();
+                stats->accepted += acc;
+            }
+            // a round is emitted whole (src/spec.cpp:314-322)
+            for (int64_t i = 0; i < acc; ++i) out.push_back(props[(size_t)i]);
+            out.push_back(r.bonus);
+            history.insert(history.end(), props.begin(), props.begin() + acc);
+            history.push_back(r.bonus);
+            // one target step on the bonus: the next round's base row
+            target.step(r.bonus, base);
+            drafter.on_commit(acc);
+        }
+    } catch (...) {
+        ftx_free_staging(be.ctx(), base);
+        throw;
+    }
+    ftx_free_staging(be.ctx(), base);
+    return out;
 }
 
 }  // namespace ftx_host

@@ -181,7 +181,8 @@ public:
                                const std::vector<int32_t>& parents = {}, bool advance = false);
     // Engine::step (src/engine.cpp:650-658): one token at the committed
     // position; returns its device logits row, the cache one longer
-    const float* step(int32_t token);
+    // logits != nullptr: the row goes there (device [vocab]) instead
+    const float* step(int32_t token, float* logits = nullptr);
     // Engine::prefill (src/engine.cpp:598-648, without the prefix cache): the
     // tokens in advancing chains of at most `chunk`, the LM head only on the
     // last; returns the device logits of that last chain (rows [0, n % chunk
@@ -204,6 +205,8 @@ public:
                     const std::vector<int32_t>& parents = {}, const float* q = nullptr);
 
     const ModelConfig& config() const { return cfg_; }
+    HipBackend& backend() { return be_; }
+    int64_t max_tokens() const { return max_tokens_; }
 
 private:
     HipBackend& be_;
@@ -213,5 +216,50 @@ private:
     float* logits_ = nullptr;
     int64_t max_tokens_ = 0;
 };
+
+// DraftModelDrafter (src/spec.cpp:72-119) over a resident draft model: its
+// cache synced to the committed history by prefill, k greedy draft tokens
+// each with its T = 1 softmax probability (Sampler::argmax + softmax_prob on
+// the device, one draft step per token after the first), the cache cut back
+// to the accepted prefix on commit
+class DraftModelDrafter {
+public:
+    explicit DraftModelDrafter(HipVerifier& model) : m_(model) {}
+    // src/spec.cpp:77-85: reset when ahead of the history, prefill what it
+    // lacks; the logits of the history's last token are then current
+    void sync(const std::vector<int32_t>& history);
+    // src/spec.cpp:97-112
+    void draft(const std::vector<int32_t>& history, int k, std::vector<int32_t>& props,
+               std::vector<float>& probs);
+    // src/spec.cpp:114-117 with Engine::truncate_to's clamp
+    // (src/engine.cpp:423-428)
+    void on_commit(int64_t accepted);
+
+private:
+    HipVerifier& m_;
+    const float* row_ = nullptr;  // device logits of the current last token
+    int64_t pending_base_ = 0;
+};
+
+// generate's draft cut (src/spec.cpp:276-285): stop at the first probability
+// below 0.02f, or after the token that takes the running product below 0.05f
+void cut_draft(std::vector<int32_t>& props, std::vector<float>& probs);
+
+struct GenerateStats {
+    int64_t rounds = 0, drafted = 0, accepted = 0;
+};
+
+// generate's speculative block (src/spec.cpp:245-333) on the device-resident
+// path: prefill the prompt, then rounds of draft -> cut -> verify on the
+// target -> ratio acceptance with the draft probabilities -> bonus from the
+// row after the last accepted token (Sampler::sample with its state carried
+// over in target.sampler; temp <= 0: the argmax) -> truncate -> one target
+// step on the bonus, until at least max_new tokens are out (a round is
+// emitted whole).  The acceptance test takes the target at temp (T = 1 for
+// temp <= 0).  Returns the generated tokens.
+std::vector<int32_t> generate(HipVerifier& target, DraftModelDrafter& drafter,
+                              const std::vector<int32_t>& prompt, int64_t max_new, int spec_k = 8,
+                              float temp = 0.f, int32_t top_k = 40, float top_p = 0.95f,
+                              uint64_t seed = 0, GenerateStats* stats = nullptr);
 
 }  // namespace ftx_host
