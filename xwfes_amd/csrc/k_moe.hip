@@ -354,28 +354,38 @@ struct MoeDownArgs {
     const int32_t* xtab;
     int64_t F, K, rows;   // rows: operand rows (ntile_max * trows)
     int trows;            // rows per tile (16 or 64)
-    int g_per_split;      // 32-row groups per split, a multiple of MOE_CG
+    int g_per_split;      // 32-row groups per split, a multiple of the chunk (MOE_CGS)
     float* part;          // [S][rows][K]
 };
 
-constexpr int MOE_CG = 4;  // row groups per staged chunk
-// LDS per chunk buffer: the operand fragments [ms 4][g][hi / lo][1 KB], then
+constexpr int MOE_CG = 8;  // the most row groups a chunk stages (split sizes are multiples)
+// row groups per staged chunk: 8 for 16-row routing tiles (more bytes in
+// flight per wave; their smaller operand stage leaves the room), 4 for
+// 64-row tiles
+template <int MS>
+constexpr int MOE_CGS = MS == 1 ? 8 : 4;
+// LDS per chunk buffer: the operand fragments [ms MS][g][hi / lo][1 KB], then
 // the scales of the workgroup's four pair-blocks [P 4][g][2 blocks x 32 rows]
-constexpr int MOE_A_BYTES = 4 * MOE_CG * 2 * 1024;
-constexpr int MOE_S_BYTES = 4 * MOE_CG * 128;
-constexpr int MOE_BUF = MOE_A_BYTES + MOE_S_BYTES;
+template <int MS>
+constexpr int MOE_A_BYTES = MS * MOE_CGS<MS> * 2 * 1024;
+template <int MS>
+constexpr int MOE_BUF = MOE_A_BYTES<MS> + 4 * MOE_CGS<MS> * 128;
 
 typedef __attribute__((address_space(3))) void moe_lds_void;
 
 // grid = (K / 256, ntile_max, S); block = 256: wave w owns the pair-block
 // P = 4 bx + w (64 columns, four 16-column MFMA tiles) for the tile's rows
 // in use (16-row MFMA tiles, a block-uniform count) over its split's row
-// groups, MOE_CG groups at a time.  Per chunk the operand fragments (of the
+// groups, CG groups at a time.  Per chunk the operand fragments (of the
 // rows in use) and the workgroup's scales go to one of two LDS buffers by
 // direct loads, and each wave's nibbles to one of two register sets, all
-// issued a chunk ahead; one wait and one barrier per chunk.
+// issued a chunk ahead; one wait and one barrier per chunk.  MS: 16-row
+// MFMA tiles per routing tile (4 for 64-row tiles, 1 for 16-row tiles, whose
+// smaller LDS and register set let more workgroups share a CU).
+template <int MS>
 __global__ void __launch_bounds__(256) k_moe_down(MoeDownArgs a) {
-    extern __shared__ __attribute__((aligned(16))) uint8_t lds[];  // [2][MOE_BUF]
+    constexpr int CG = MOE_CGS<MS>, BUF = MOE_BUF<MS>, ABYTES = MOE_A_BYTES<MS>;
+    extern __shared__ __attribute__((aligned(16))) uint8_t lds[];  // [2][BUF]
     const int tid = threadIdx.x, lane = tid & 63;
     const int w = __builtin_amdgcn_readfirstlane(tid >> 6);
     const int col = lane & 15, kq = lane >> 4;
@@ -394,55 +404,56 @@ __global__ void __launch_bounds__(256) k_moe_down(MoeDownArgs a) {
     // multiplied) read the last group of the plane
     auto gc = [&](int64_t g) { return g < G ? g : G - 1; };
     auto stage = [&](int64_t c0, int buf, v4i* nib) {
-        uint8_t* L = lds + buf * MOE_BUF;
+        uint8_t* L = lds + buf * BUF;
         // fragment copies q = w + 4 i over (ms, g, hl), one direct load each
 #pragma unroll
-        for (int i = 0; i < 2 * MOE_CG; ++i) {
+        for (int i = 0; i < 2 * CG * MS / 4; ++i) {
             const int q = w + 4 * i;
-            const int ms = q / (2 * MOE_CG), g = (q / 2) % MOE_CG, hl = q & 1;
+            const int ms = q / (2 * CG), g = (q / 2) % CG, hl = q & 1;
             if (ms >= nsub || c0 + g >= g1) continue;
             const _Float16* src =
                 (hl ? a.al : a.ah) + (((mt0 + ms) * G + c0 + g) * 64 + lane) * 8;
             __builtin_amdgcn_global_load_lds(
-                (const void*)src, (moe_lds_void*)(L + ((ms * MOE_CG + g) * 2 + hl) * 1024), 16, 0,
+                (const void*)src, (moe_lds_void*)(L + ((ms * CG + g) * 2 + hl) * 1024), 16, 0,
                 0);
         }
-        // scales: waves 0 and 1, piece p = 64 w + lane -> pair-block p / 32,
-        // group (p / 8) % 4, 16 bytes at 16 (p % 8) of the tile's scales
-        if (w < 2) {
+        // scales: waves w < CG / 2, piece p = 64 w + lane -> pair-block
+        // p / (8 CG), group (p / 8) % CG, 16 bytes at 16 (p % 8) of the
+        // tile's scales
+        if (w < CG / 2) {
             const int p = 64 * w + lane;
-            const int pw = p / (8 * MOE_CG), g = (p / 8) % MOE_CG, piece = p % 8;
+            const int pw = p / (8 * CG), g = (p / 8) % CG, piece = p % 8;
             const uint8_t* src =
                 wb + ((4 * (int64_t)blockIdx.x + pw) * G + gc(c0 + g)) * MOE_TB + 1024 + 16 * piece;
             __builtin_amdgcn_global_load_lds((const void*)src,
-                                             (moe_lds_void*)(L + MOE_A_BYTES + 1024 * w), 16, 0, 0);
+                                             (moe_lds_void*)(L + ABYTES + 1024 * w), 16, 0, 0);
         }
 #pragma unroll
-        for (int g = 0; g < MOE_CG; ++g) nib[g] = *(const v4i*)(tb + gc(c0 + g) * MOE_TB + lane * 16);
+        for (int g = 0; g < CG; ++g) nib[g] = *(const v4i*)(tb + gc(c0 + g) * MOE_TB + lane * 16);
     };
-    v4f acc[4][4];
+    v4f acc[4][MS];
 #pragma unroll
     for (int c = 0; c < 4; ++c)
 #pragma unroll
-        for (int ms = 0; ms < 4; ++ms) acc[c][ms] = v4f{0.f, 0.f, 0.f, 0.f};
+        for (int ms = 0; ms < MS; ++ms) acc[c][ms] = v4f{0.f, 0.f, 0.f, 0.f};
     const v4i hmask = {(int)0xFFF8FFF8u, (int)0xFFF8FFF8u, (int)0xFFF8FFF8u, (int)0xFFF8FFF8u};
     auto compute = [&](int64_t c0, int buf, const v4i* nib) {
-        const uint8_t* L = lds + buf * MOE_BUF;
+        const uint8_t* L = lds + buf * BUF;
 #pragma unroll
-        for (int g = 0; g < MOE_CG; ++g) {
+        for (int g = 0; g < CG; ++g) {
             if (c0 + g >= g1) break;
-            const uint8_t* sc = L + MOE_A_BYTES + (w * MOE_CG + g) * 128 + 16 * kq;
+            const uint8_t* sc = L + ABYTES + (w * CG + g) * 128 + 16 * kq;
             const v4i s0 = *(const v4i*)sc, s1 = *(const v4i*)(sc + 64);
             const v8h d0 = __builtin_bit_cast(v8h, s0), d1 = __builtin_bit_cast(v8h, s1);
             const v8h d0h = __builtin_bit_cast(v8h, s0 & hmask);
             const v8h d1h = __builtin_bit_cast(v8h, s1 & hmask);
             const v8h d0l = d0 - d0h, d1l = d1 - d1h;
-            v8h ah[4], al[4];
+            v8h ah[MS], al[MS];
 #pragma unroll
-            for (int ms = 0; ms < 4; ++ms) {
+            for (int ms = 0; ms < MS; ++ms) {
                 if (ms >= nsub) break;
-                ah[ms] = *(const v8h*)(L + ((ms * MOE_CG + g) * 2 + 0) * 1024 + lane * 16);
-                al[ms] = *(const v8h*)(L + ((ms * MOE_CG + g) * 2 + 1) * 1024 + lane * 16);
+                ah[ms] = *(const v8h*)(L + ((ms * CG + g) * 2 + 0) * 1024 + lane * 16);
+                al[ms] = *(const v8h*)(L + ((ms * CG + g) * 2 + 1) * 1024 + lane * 16);
             }
 #pragma unroll
             for (int c = 0; c < 4; ++c) {
@@ -450,7 +461,7 @@ __global__ void __launch_bounds__(256) k_moe_down(MoeDownArgs a) {
                 const v8h bh = q * (c < 2 ? d0h : d1h);
                 const v8h bl = q * (c < 2 ? d0l : d1l);
 #pragma unroll
-                for (int ms = 0; ms < 4; ++ms) {
+                for (int ms = 0; ms < MS; ++ms) {
                     if (ms >= nsub) break;
                     acc[c][ms] = __builtin_amdgcn_mfma_f32_16x16x32_f16(ah[ms], bh, acc[c][ms], 0, 0, 0);
                     acc[c][ms] = __builtin_amdgcn_mfma_f32_16x16x32_f16(al[ms], bh, acc[c][ms], 0, 0, 0);
@@ -459,24 +470,24 @@ __global__ void __launch_bounds__(256) k_moe_down(MoeDownArgs a) {
             }
         }
     };
-    v4i na[MOE_CG], nb[MOE_CG];
+    v4i na[CG], nb[CG];
     if (g0 < g1) stage(g0, 0, na);
-    for (int64_t c0 = g0; c0 < g1; c0 += 2 * MOE_CG) {
+    for (int64_t c0 = g0; c0 < g1; c0 += 2 * CG) {
         __builtin_amdgcn_s_waitcnt(0x0F70);  // this chunk's copies and nibbles
         __syncthreads();                     // every wave is done with the other buffer
-        if (c0 + MOE_CG < g1) stage(c0 + MOE_CG, 1, nb);
+        if (c0 + CG < g1) stage(c0 + CG, 1, nb);
         compute(c0, 0, na);
-        if (c0 + MOE_CG >= g1) break;
+        if (c0 + CG >= g1) break;
         __builtin_amdgcn_s_waitcnt(0x0F70);
         __syncthreads();
-        if (c0 + 2 * MOE_CG < g1) stage(c0 + 2 * MOE_CG, 0, na);
-        compute(c0 + MOE_CG, 1, nb);
+        if (c0 + 2 * CG < g1) stage(c0 + 2 * CG, 0, na);
+        compute(c0 + CG, 1, nb);
     }
     // lane (col, kq) holds C[4 kq + r][col]: operand row 64 by + 16 ms + 4 kq
     // + r, column 64 P + 16 c + col
     float* base = a.part + (int64_t)blockIdx.z * a.rows * a.K;
 #pragma unroll
-    for (int ms = 0; ms < 4; ++ms) {
+    for (int ms = 0; ms < MS; ++ms) {
         if (ms >= nsub) break;
 #pragma unroll
         for (int r = 0; r < 4; ++r) {
@@ -645,21 +656,26 @@ hipError_t launch_moe_down(hipStream_t st, const uint8_t* tiled, int dt, int64_t
     a.trows = (int)trows;
     a.part = part;
     const int64_t G = F / 32;
-    a.g_per_split = (int)(((G + S - 1) / S + MOE_CG - 1) / MOE_CG * MOE_CG);
+    const int cg = trows == 16 ? MOE_CGS<1> : MOE_CGS<4>;
+    a.g_per_split = (int)(((G + S - 1) / S + cg - 1) / cg * cg);
     // the real split count: splits past the last row group would leave
     // their partial rows unwritten
     if ((int64_t)a.g_per_split * (S - 1) >= G) return hipErrorInvalidValue;
     a.plane = (K / 64) * G * MOE_TB;
-    constexpr size_t lds = 2 * MOE_BUF;
-    static bool lds_set = false;
-    if (!lds_set) {
-        hipError_t e = hipFuncSetAttribute((const void*)k_moe_down,
-                                           hipFuncAttributeMaxDynamicSharedMemorySize, (int)lds);
+    const bool small = trows == 16;
+    const size_t lds = 2 * (size_t)(small ? MOE_BUF<1> : MOE_BUF<4>);
+    const void* kern = small ? (const void*)k_moe_down<1> : (const void*)k_moe_down<4>;
+    static bool lds_set[2] = {};
+    if (!lds_set[small]) {
+        hipError_t e = hipFuncSetAttribute(kern, hipFuncAttributeMaxDynamicSharedMemorySize, (int)lds);
         if (e != hipSuccess) return e;
-        lds_set = true;
+        lds_set[small] = true;
     }
-    ktimed_launch(k_moe_down, dim3((unsigned)(K / 256), (unsigned)ntile_max, (unsigned)S),
-                  dim3(256), (uint32_t)lds, st, a);
+    const dim3 grid((unsigned)(K / 256), (unsigned)ntile_max, (unsigned)S);
+    if (small)
+        ktimed_launch(k_moe_down<1>, grid, dim3(256), (uint32_t)lds, st, a);
+    else
+        ktimed_launch(k_moe_down<4>, grid, dim3(256), (uint32_t)lds, st, a);
     return hipGetLastError();
 }
 
