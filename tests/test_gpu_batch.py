@@ -147,6 +147,22 @@ def test_large_chain_q6k_one_pass(gctx, orc, M):
     assert rel_err_rows(got, want) < LOGIT_TOL
 
 
+def test_long_context_tree_chunk_groups(gctx, orc):
+    """A 64-node tree over context 4030 with 64 query heads of 64 on 8 kv
+    heads: the one-chunk attention grid would hold 8320 workgroups, so each
+    workgroup walks two chunks with a running maximum and sum (one partial
+    per pair)."""
+    cfg = P.model_cfg(1, 4096, 64, 8, 64, 1024, 300, rope_theta=500000.0)
+    dts = dict(tok_embd=P.Q8_0, output=P.Q8_0, q=P.Q8_0, k=P.Q8_0, v=P.Q8_0, o=P.Q8_0,
+               gate=P.Q8_0, up=P.Q8_0, down=P.Q8_0)
+    model = P.make_model(orc, cfg, dts, seed=97)
+    rng = np.random.default_rng(98)
+    par = [-1] + [int(rng.integers(max(-1, i - 6), i)) for i in range(1, 64)]
+    seqs = [(rng.integers(0, 300, 64).tolist(), par, 4030, 4030 + 64 + 2)]
+    (got, want, _, _), = run_batch(gctx, orc, model, seqs, 64)
+    assert rel_err_rows(got, want) < LOGIT_TOL
+
+
 def test_batch_errors(gctx, orc):
     model = P.make_model(orc, SMALL, dict(tok_embd=P.F32, output=P.Q8_0, q=P.Q8_0, k=P.Q8_0,
                                           v=P.Q8_0, o=P.Q8_0, gate=P.Q8_0, up=P.Q8_0,

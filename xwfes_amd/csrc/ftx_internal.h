@@ -421,6 +421,7 @@ struct AttnMArgs {
     int M, n_head, n_kv, hd;
     float* out;          // [M][n_head*hd]
     float *pmax, *psum, *pout;  // chunk partials
+    int nc = 1;          // chunks per workgroup (and per partial)
 };
 bool attn_mfma_supported(int64_t hd, int kv_f16, int64_t M, int64_t n_head, int64_t n_kv);
 size_t attn_part_floats(int64_t M, int64_t n_head, int64_t hd, int64_t cap_alloc);

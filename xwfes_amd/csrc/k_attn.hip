@@ -1,6 +1,7 @@
 // k_attn.hip -- tree-masked GQA attention over the fp16 KV cache on MFMA,
 // split over chunks of the context (flash-decoding) and combined in a second
-// pass.
+// pass (one partial per chunk, or per group of chunks on long contexts with
+// many query rows).
 //
 // Semantics of Impl::attn (src/engine.cpp:137-177) with the draft-tree mask:
 // query row m of head h attends to cache slots [0, npast) and to the tree
@@ -232,20 +233,244 @@ __device__ __forceinline__ void attn_mfma_wg(const AttnMArgs& a, int c, int kvh,
     }
 }
 
+// The workgroup (group grp of nc consecutive chunks, kv head kvh, query
+// tile qtile) of one sequence's attention, for long contexts with many
+// query rows: the group's chunks in turn with a running row maximum and sum
+// (flash attention: O <- e^(m_old - m_new) O + P V with P = e^(s - m_new)),
+// one partial per group (ngrp = the sequence's group count, the partials'
+// stride).  The query is staged once; per chunk the same score / P / output
+// steps as attn_mfma_wg, with each chunk's K / V rows and mask words loaded
+// while the previous chunk's P . V runs.
+template <int HD, int CHK, int NWV>
+__device__ __forceinline__ void attn_mfma_wg_mc(const AttnMArgs& a, int grp, int kvh, int qtile,
+                                                int ngrp) {
+    constexpr int NDT = HD / 16, NST = CHK / 16;
+    constexpr int PPW = 2 * NST / NWV;
+    static_assert(PPW == 1 || PPW == 2, "a wave takes one or two score tiles of one slot tile");
+    constexpr int QPW = 2 * NDT / NWV;
+    static_assert(QPW == 1 || QPW == 2, "a wave takes one or two query tiles of one dim tile");
+    constexpr int NDC = HD / 32, QP = HD + 8, PP = CHK + 8;
+    constexpr int QV = (2 * 32 * HD / 8) / (64 * NWV);
+    __shared__ _Float16 qs[2][32][QP];
+    __shared__ _Float16 ps[2][32][PP];
+    __shared__ float smax[NST][32], ssum[NST][32];
+    __shared__ float rmax[32], rsum[32], ralpha[32];  // running max, sum; this chunk's rescale
+    const int tid = threadIdx.x, w = tid >> 6, lane = tid & 63, col = lane & 15, g = lane >> 4;
+    const int64_t npast = a.npast, total = npast + a.M;
+    const int64_t gslot0 = (int64_t)grp * a.nc * CHK;
+    if (gslot0 >= total) return;
+    // chunks of the group holding slots below total (block-uniform)
+    const int nck = (int)min((int64_t)a.nc, (total - gslot0 + CHK - 1) / CHK);
+    const int gqa = a.n_head / a.n_kv, qrows = a.M * gqa, qbase = qtile * 32;
+    const int64_t kdim = (int64_t)a.n_kv * HD;
+    const int sst = (w * PPW) >> 1, dt = w % NDT;
+    // query staging (once)
+    {
+        v8h qv[QV];
+#pragma unroll
+        for (int k = 0; k < QV; ++k) {
+            const int v = tid + 64 * NWV * k;
+            const int part = v / (32 * HD / 8), r = (v / (HD / 8)) % 32, dv = v % (HD / 8);
+            const int rq = min(qbase + r, qrows - 1);
+            const int64_t qo = ((int64_t)(rq / gqa) * a.n_head + kvh * gqa + rq % gqa) * HD + 8 * dv;
+            qv[k] = *(const v8h*)((part ? a.ql16 : a.qh16) + qo);
+        }
+#pragma unroll
+        for (int k = 0; k < QV; ++k) {
+            const int v = tid + 64 * NWV * k;
+            const int part = v / (32 * HD / 8), r = (v / (HD / 8)) % 32, dv = v % (HD / 8);
+            *(v8h*)&qs[part][r][8 * dv] = qv[k];
+        }
+    }
+    if (tid < 32) {
+        rmax[tid] = -INFINITY;
+        rsum[tid] = 0.f;
+    }
+    // a chunk's operands: mask words of the wave's query rows, K rows, V^T rows
+    auto load = [&](int64_t slot0, uint32_t* aw0, uint32_t* aw1, v8h* kf, v4h* vf) {
+        const int64_t ws0 = slot0 + 16 * sst;
+        const int64_t j0 = ws0 + 4 * g - npast;
+        const int wsel = (int)min(max(j0, (int64_t)0) >> 5, (int64_t)a.anc_words - 1);
+        const int wnext = min(wsel + 1, a.anc_words - 1);
+#pragma unroll
+        for (int pi = 0; pi < PPW; ++pi) {
+            const int qt = (w * PPW + pi) & 1;
+            const int rq = min(qbase + qt * 16 + col, qrows - 1);
+            const uint32_t* an = a.anc + (int64_t)(rq / gqa) * a.anc_words;
+            aw0[pi] = an[wsel];
+            aw1[pi] = an[wnext];
+        }
+        const _Float16* krow = a.kc + (ws0 + col) * kdim + (int64_t)kvh * HD + 8 * g;
+#pragma unroll
+        for (int dc = 0; dc < NDC; ++dc) kf[dc] = *(const v8h*)(krow + 32 * dc);
+        const _Float16* vrow = a.vt + ((int64_t)kvh * HD + 16 * dt + col) * a.cap + slot0 + 4 * g;
+#pragma unroll
+        for (int st = 0; st < NST; ++st) vf[st] = *(const v4h*)(vrow + 16 * st);
+    };
+    uint32_t aw0[PPW], aw1[PPW];
+    v8h kf[NDC];
+    v4h vf[NST];
+    load(gslot0, aw0, aw1, kf, vf);
+    v4f oacc[QPW];
+#pragma unroll
+    for (int qi = 0; qi < QPW; ++qi) oacc[qi] = v4f{0.f, 0.f, 0.f, 0.f};
+    const float scale = 1.f / sqrtf((float)HD);
+    for (int ci = 0; ci < nck; ++ci) {
+        const int64_t slot0 = gslot0 + (int64_t)ci * CHK;
+        const int64_t ws0 = slot0 + 16 * sst;
+        const int64_t j0 = ws0 + 4 * g - npast;
+        const int wsel = (int)min(max(j0, (int64_t)0) >> 5, (int64_t)a.anc_words - 1);
+        __syncthreads();  // the query staged / every wave done with the last chunk's LDS
+        v8h qf[PPW][NDC][2];
+#pragma unroll
+        for (int pi = 0; pi < PPW; ++pi) {
+            const int qt = (w * PPW + pi) & 1;
+#pragma unroll
+            for (int dc = 0; dc < NDC; ++dc) {
+                qf[pi][dc][0] = *(const v8h*)&qs[0][qt * 16 + col][32 * dc + 8 * g];
+                qf[pi][dc][1] = *(const v8h*)&qs[1][qt * 16 + col][32 * dc + 8 * g];
+            }
+        }
+        v4f sc[PPW];
+#pragma unroll
+        for (int pi = 0; pi < PPW; ++pi) {
+            v4f acc = {0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+            for (int dc = 0; dc < NDC; ++dc) {
+                acc = __builtin_amdgcn_mfma_f32_16x16x32_f16(kf[dc], qf[pi][dc][0], acc, 0, 0, 0);
+                acc = __builtin_amdgcn_mfma_f32_16x16x32_f16(kf[dc], qf[pi][dc][1], acc, 0, 0, 0);
+            }
+            sc[pi] = acc;
+        }
+#pragma unroll
+        for (int pi = 0; pi < PPW; ++pi) {
+            const int qt = (w * PPW + pi) & 1;
+            const bool qvalid = qbase + qt * 16 + col < qrows;
+            const uint64_t win = aw0[pi] | ((uint64_t)aw1[pi] << 32);
+            float m_ = -INFINITY;
+#pragma unroll
+            for (int r = 0; r < 4; ++r) {
+                const int64_t j = j0 + r;
+                const bool tree_ok = j >= 0 && j < a.M && ((win >> ((j - 32 * wsel) & 63)) & 1u);
+                const bool ok = qvalid && (j < 0 || tree_ok);
+                const float sv = ok ? sc[pi][r] * scale : -INFINITY;
+                sc[pi][r] = sv;
+                m_ = fmaxf(m_, sv);
+            }
+            m_ = fmaxf(m_, __shfl_xor(m_, 16, 64));
+            m_ = fmaxf(m_, __shfl_xor(m_, 32, 64));
+            if (g == 0) smax[sst][qt * 16 + col] = m_;
+        }
+        __syncthreads();
+        // p = e^(s - m_new), m_new = max(running max, this chunk's max)
+#pragma unroll
+        for (int pi = 0; pi < PPW; ++pi) {
+            const int qt = (w * PPW + pi) & 1;
+            const int q = qt * 16 + col;
+            float mx = rmax[q];
+#pragma unroll
+            for (int k = 0; k < NST; ++k) mx = fmaxf(mx, smax[k][q]);
+            float s_ = 0.f;
+            v4h ph, pl;
+#pragma unroll
+            for (int r = 0; r < 4; ++r) {
+                const float e = sc[pi][r] == -INFINITY ? 0.f : expf(sc[pi][r] - mx);
+                s_ += e;
+                const _Float16 h = (_Float16)e;
+                ph[r] = h;
+                pl[r] = (_Float16)(e - (float)h);
+            }
+            s_ += __shfl_xor(s_, 16, 64);
+            s_ += __shfl_xor(s_, 32, 64);
+            if (g == 0) ssum[sst][q] = s_;
+            *(v4h*)&ps[0][q][16 * sst + 4 * g] = ph;
+            *(v4h*)&ps[1][q][16 * sst + 4 * g] = pl;
+        }
+        // this chunk's V rows stay in vc; the next chunk's operands go out
+        // now and land during this chunk's P . V
+        v4h vc[NST];
+#pragma unroll
+        for (int st = 0; st < NST; ++st) vc[st] = vf[st];
+        if (ci + 1 < nck) load(slot0 + CHK, aw0, aw1, kf, vf);
+        __syncthreads();
+        if (tid < 32) {  // running statistics of row tid
+            const float mo = rmax[tid];
+            float mn = mo, ls = 0.f;
+#pragma unroll
+            for (int k = 0; k < NST; ++k) mn = fmaxf(mn, smax[k][tid]);
+#pragma unroll
+            for (int k = 0; k < NST; ++k) ls += ssum[k][tid];
+            const float al = mo == -INFINITY ? 0.f : expf(mo - mn);
+            rsum[tid] = al * rsum[tid] + ls;
+            rmax[tid] = mn;
+            ralpha[tid] = al;
+        }
+        __syncthreads();
+        // O <- alpha O + P . V over the chunk for the wave's dim tile
+#pragma unroll
+        for (int qi = 0; qi < QPW; ++qi) {
+            const int qt = QPW == 2 ? qi : w / NDT;
+            v4h ph[NST], pl[NST];
+#pragma unroll
+            for (int st = 0; st < NST; ++st) {
+                ph[st] = *(const v4h*)&ps[0][qt * 16 + col][16 * st + 4 * g];
+                pl[st] = *(const v4h*)&ps[1][qt * 16 + col][16 * st + 4 * g];
+            }
+            v4f o = oacc[qi];
+#pragma unroll
+            for (int r = 0; r < 4; ++r) o[r] *= ralpha[qt * 16 + 4 * g + r];
+#pragma unroll
+            for (int st = 0; st < NST; ++st) {
+                o = __builtin_amdgcn_mfma_f32_16x16x16f16(ph[st], vc[st], o, 0, 0, 0);
+                o = __builtin_amdgcn_mfma_f32_16x16x16f16(pl[st], vc[st], o, 0, 0, 0);
+            }
+            oacc[qi] = o;
+        }
+    }
+    // the group's partial: O, the running max and sum of each valid row
+#pragma unroll
+    for (int qi = 0; qi < QPW; ++qi) {
+        const int qt = QPW == 2 ? qi : w / NDT;
+#pragma unroll
+        for (int r = 0; r < 4; ++r) {
+            const int rq = qbase + qt * 16 + 4 * g + r;
+            if (rq >= qrows) continue;
+            const int64_t qrow = (int64_t)(rq / gqa) * a.n_head + kvh * gqa + rq % gqa;
+            a.pout[(qrow * ngrp + grp) * HD + 16 * dt + col] = oacc[qi][r];
+        }
+    }
+    if (w == 0 && lane < 32 && qbase + lane < qrows) {
+        const int rq = qbase + lane;
+        const int64_t qi = (int64_t)(rq / gqa) * a.n_head + kvh * gqa + rq % gqa;
+        a.pmax[qi * ngrp + grp] = rmax[lane];
+        a.psum[qi * ngrp + grp] = rsum[lane];
+    }
+}
+
 template <int HD, int CHK, int NWV>
 __global__ void __launch_bounds__(64 * NWV) k_attn_mfma(AttnMArgs a) {
     attn_mfma_wg<HD, CHK, NWV>(a, blockIdx.x, blockIdx.y, blockIdx.z, gridDim.x);
 }
 
+// groups of a.nc chunks per workgroup (grid.x = the group count)
+template <int HD, int CHK, int NWV>
+__global__ void __launch_bounds__(64 * NWV) k_attn_mfma_mc(AttnMArgs a) {
+    attn_mfma_wg_mc<HD, CHK, NWV>(a, blockIdx.x, blockIdx.y, blockIdx.z, gridDim.x);
+}
+
 // several sequences in one launch: grid.z runs over every sequence's query
 // tiles (sequence s owns tiles qt0[s] .. qt0[s + 1] - 1); chunks past a
 // sequence's own end return at once
-template <int HD, int CHK, int NWV>
+template <int HD, int CHK, int NWV, bool MC>
 __global__ void __launch_bounds__(64 * NWV) k_attn_mfma_batch(AttnMBatch b) {
     int s = 0;
     while (s + 1 < b.nseq && (int)blockIdx.z >= b.qt0[s + 1]) ++s;
-    attn_mfma_wg<HD, CHK, NWV>(b.s[s], blockIdx.x, blockIdx.y, (int)blockIdx.z - b.qt0[s],
-                               b.nch[s]);
+    if constexpr (MC)
+        attn_mfma_wg_mc<HD, CHK, NWV>(b.s[s], blockIdx.x, blockIdx.y, (int)blockIdx.z - b.qt0[s],
+                                      b.nch[s]);
+    else
+        attn_mfma_wg<HD, CHK, NWV>(b.s[s], blockIdx.x, blockIdx.y, (int)blockIdx.z - b.qt0[s],
+                                   b.nch[s]);
 }
 
 // out[m][h*hd + d] = sum_c e^(max_c - M) O_c[d] / sum_c e^(max_c - M) sum_c
@@ -256,7 +481,7 @@ __device__ __forceinline__ void attn_combine_row(const AttnMArgs& a, int64_t qi,
     __shared__ float red[128];
     const int d = threadIdx.x;
     const int64_t npast = a.npast;
-    const int ch = chunk_slots(a.hd);
+    const int ch = chunk_slots(a.hd) * a.nc;  // slots per partial
     const int nvalid = (int)((npast + a.M + ch - 1) / ch);
     float M = -INFINITY;
     for (int c = d; c < nvalid; c += 128) M = fmaxf(M, a.pmax[qi * nch + c]);
@@ -416,6 +641,16 @@ size_t attn_part_floats(int64_t M, int64_t n_head, int64_t hd, int64_t cap_alloc
     return (size_t)(M * n_head * nch) * (size_t)(hd + 2);
 }
 
+// chunks per workgroup: 1 (one partial per chunk) until the one-chunk grid
+// holds more than 8192 workgroups (many query rows over a long context),
+// then doubled while the grid keeps at least 4096, at most 16: the partials
+// (and the combine's reads of them) shrink by that factor
+static int attn_chunks_per_wg(int64_t wgs) {
+    int nc = 1;
+    while (nc < 16 && wgs / (2 * nc) >= 4096) nc *= 2;
+    return nc;
+}
+
 hipError_t launch_attn_mfma(hipStream_t st, AttnMArgs a, float* part, int8_t* xq) {
     // whole chunks of the allocation: every slot a chunk reads is allocated
     const int ch = chunk_slots(a.hd);
@@ -423,15 +658,23 @@ hipError_t launch_attn_mfma(hipStream_t st, AttnMArgs a, float* part, int8_t* xq
     const int nch = (int)(a.cap / ch);
     if (nch > 1024) return hipErrorInvalidValue;  // combine weights live in LDS
     const int64_t qi = (int64_t)a.M * a.n_head;
-    a.pmax = part;
-    a.psum = part + qi * nch;
-    a.pout = part + 2 * qi * nch;
-    // one workgroup per (chunk, kv head, tile of 32 query rows)
+    // one workgroup per (chunk or group of chunks, kv head, tile of 32 query rows)
     const int qtiles = (int)((a.M * (a.n_head / a.n_kv) + 31) / 32);
-    const dim3 grid((unsigned)nch, (unsigned)a.n_kv, (unsigned)qtiles);
-    if (a.hd == 128)
+    const int64_t nvalid = (a.npast + a.M + ch - 1) / ch;
+    a.nc = xq ? 1 : attn_chunks_per_wg(nvalid * a.n_kv * qtiles);
+    const int ngrp = (nch + a.nc - 1) / a.nc;  // the partials' stride
+    a.pmax = part;
+    a.psum = part + qi * ngrp;
+    a.pout = part + 2 * qi * ngrp;
+    const dim3 grid((unsigned)ngrp, (unsigned)a.n_kv, (unsigned)qtiles);
+    if (a.hd == 128 && a.nc > 1)
+        ktimed_launch(k_attn_mfma_mc<128, chunk_slots(128), ATTN_WAVES_128>, grid,
+                      dim3(64 * ATTN_WAVES_128), 0, st, a);
+    else if (a.hd == 128)
         ktimed_launch(k_attn_mfma<128, chunk_slots(128), ATTN_WAVES_128>, grid,
                            dim3(64 * ATTN_WAVES_128), 0, st, a);
+    else if (a.hd == 64 && a.nc > 1)
+        ktimed_launch(k_attn_mfma_mc<64, chunk_slots(64), 4>, grid, dim3(64 * 4), 0, st, a);
     else if (a.hd == 64)
         ktimed_launch(k_attn_mfma<64, chunk_slots(64), 4>, grid, dim3(64 * 4), 0, st, a);
     else
@@ -443,11 +686,11 @@ hipError_t launch_attn_mfma(hipStream_t st, AttnMArgs a, float* part, int8_t* xq
         const int64_t K = (int64_t)a.n_head * a.hd;
         const dim3 cg((unsigned)(K / 256), 8);
         if (a.hd == 128)
-            hipLaunchKernelGGL(k_attn_combine_xq<128>, cg, dim3(256), 0, st, a, nch, xq_ptrs(xq, K));
+            hipLaunchKernelGGL(k_attn_combine_xq<128>, cg, dim3(256), 0, st, a, ngrp, xq_ptrs(xq, K));
         else
-            hipLaunchKernelGGL(k_attn_combine_xq<64>, cg, dim3(256), 0, st, a, nch, xq_ptrs(xq, K));
+            hipLaunchKernelGGL(k_attn_combine_xq<64>, cg, dim3(256), 0, st, a, ngrp, xq_ptrs(xq, K));
     } else {
-        hipLaunchKernelGGL(k_attn_combine, dim3((unsigned)qi), dim3(128), 0, st, a, nch);
+        hipLaunchKernelGGL(k_attn_combine, dim3((unsigned)qi), dim3(128), 0, st, a, ngrp);
     }
     return hipGetLastError();
 }
@@ -458,12 +701,20 @@ hipError_t launch_attn_mfma_batch(hipStream_t st, const AttnMArgs* as, const flo
     AttnMBatch b{};
     b.nseq = nseq;
     int hd = as[0].hd, nkv = as[0].n_kv, maxch = 0, qt = 0, qi = 0;
+    int64_t wgs = 0;  // the one-chunk grid's live workgroups
+    for (int s = 0; s < nseq; ++s) {
+        const int ch = chunk_slots(as[s].hd);
+        if (as[s].hd != hd || as[s].n_kv != nkv || as[s].cap % ch) return hipErrorInvalidValue;
+        wgs += (as[s].npast + as[s].M + ch - 1) / ch * nkv *
+               ((as[s].M * (as[s].n_head / nkv) + 31) / 32);
+    }
+    const int nc = attn_chunks_per_wg(wgs);
     for (int s = 0; s < nseq; ++s) {
         AttnMArgs a = as[s];
         const int ch = chunk_slots(a.hd);
-        if (a.hd != hd || a.n_kv != nkv || a.cap % ch) return hipErrorInvalidValue;
-        const int nch = (int)(a.cap / ch);
-        if (nch > 1024) return hipErrorInvalidValue;  // combine weights live in LDS
+        if (a.cap / ch > 1024) return hipErrorInvalidValue;  // combine weights live in LDS
+        a.nc = nc;
+        const int nch = (int)((a.cap / ch + nc - 1) / nc);  // the partials' stride
         const int64_t q = (int64_t)a.M * a.n_head;
         float* part = const_cast<float*>(parts[s]);
         a.pmax = part;
@@ -480,11 +731,16 @@ hipError_t launch_attn_mfma_batch(hipStream_t st, const AttnMArgs* as, const flo
     b.qt0[nseq] = qt;
     b.qi0[nseq] = qi;
     const dim3 grid((unsigned)maxch, (unsigned)nkv, (unsigned)qt);
-    if (hd == 128)
-        ktimed_launch(k_attn_mfma_batch<128, chunk_slots(128), ATTN_WAVES_128>, grid,
+    if (hd == 128 && nc > 1)
+        ktimed_launch(k_attn_mfma_batch<128, chunk_slots(128), ATTN_WAVES_128, true>, grid,
                       dim3(64 * ATTN_WAVES_128), 0, st, b);
+    else if (hd == 128)
+        ktimed_launch(k_attn_mfma_batch<128, chunk_slots(128), ATTN_WAVES_128, false>, grid,
+                      dim3(64 * ATTN_WAVES_128), 0, st, b);
+    else if (hd == 64 && nc > 1)
+        ktimed_launch(k_attn_mfma_batch<64, chunk_slots(64), 4, true>, grid, dim3(64 * 4), 0, st, b);
     else if (hd == 64)
-        ktimed_launch(k_attn_mfma_batch<64, chunk_slots(64), 4>, grid, dim3(64 * 4), 0, st, b);
+        ktimed_launch(k_attn_mfma_batch<64, chunk_slots(64), 4, false>, grid, dim3(64 * 4), 0, st, b);
     else
         return hipErrorInvalidValue;
     hipError_t e = hipGetLastError();
