@@ -641,13 +641,15 @@ size_t attn_part_floats(int64_t M, int64_t n_head, int64_t hd, int64_t cap_alloc
     return (size_t)(M * n_head * nch) * (size_t)(hd + 2);
 }
 
-// chunks per workgroup: 1 (one partial per chunk) until the one-chunk grid
-// holds more than 8192 workgroups (many query rows over a long context),
-// then doubled while the grid keeps at least 4096, at most 16: the partials
-// (and the combine's reads of them) shrink by that factor
+// chunks per workgroup: doubled from 1 while the grid keeps at least 256
+// workgroups, at most 16: the partials (and the combine's reads of them)
+// shrink by that factor.  Measured: the 52-node tree at context 4096 (1848
+// one-chunk workgroups) 1.68 -> 1.54 ms of attention per step at 4 chunks,
+// 2.08 ms at 8; the 70B batch the same at 8 and 16; grids of at most 511
+// workgroups (the 8-token chains, the 4 x 8-token MoE batch) keep one chunk
 static int attn_chunks_per_wg(int64_t wgs) {
     int nc = 1;
-    while (nc < 16 && wgs / (2 * nc) >= 4096) nc *= 2;
+    while (nc < 16 && wgs / (2 * nc) >= 256) nc *= 2;
     return nc;
 }
 
