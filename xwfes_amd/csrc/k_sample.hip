@@ -230,23 +230,6 @@ __device__ __forceinline__ float sampler_next_float(uint64_t& st) {
     return (float)(u >> 8) * (1.f / 16777216.f);
 }
 
-// Lanes l < n of one wave: out[rank] = l for the rank of (p[l], i[l]) in the
-// order p descending, index ascending (by_index: index ascending only).
-__device__ __forceinline__ void wave_rank_sort(const float* p, const int32_t* idx, int n,
-                                               bool by_index, int32_t* out, int l) {
-    if (l < n) {
-        const float pl = p[l];
-        const int32_t il = idx[l];
-        int r = 0;
-#pragma unroll 8
-        for (int j = 0; j < n; ++j) {
-            const bool before = by_index ? idx[j] < il : (p[j] > pl || (p[j] == pl && idx[j] < il));
-            r += before;
-        }
-        out[r] = l;
-    }
-}
-
 // order-preserving unsigned key of a float
 __device__ __forceinline__ uint32_t fkey(float x) {
     const uint32_t u = __float_as_uint(x);
@@ -340,7 +323,7 @@ __device__ int32_t sampler_pick(const float* __restrict__ lg, int64_t V, float m
     __shared__ uint32_t nsel_gt, neq;
     __shared__ int32_t eqi[SMAXEQ];
     __shared__ float kp[SMAXK];
-    __shared__ int32_t ki[SMAXK], ord[SMAXK];
+    __shared__ int32_t ki[SMAXK];
     __shared__ double ssum;
     __shared__ int32_t pick;
     const int t = threadIdx.x, l = t & 63;
@@ -350,7 +333,15 @@ __device__ int32_t sampler_pick(const float* __restrict__ lg, int64_t V, float m
     // the normaliser and the sub-chunk maxima
     if (t < 64) {
         double sv = 0.0;
-        for (int j = t; j < nsub; j += 64) sv += csubf[j];
+        // lane-strided in index order, 16 loads in flight per lane
+        for (int j0 = t; j0 < nsub; j0 += 64 * 16) {
+            double v[16];
+#pragma unroll
+            for (int k = 0; k < 16; ++k) v[k] = csubf[min(j0 + 64 * k, nsub - 1)];
+#pragma unroll
+            for (int k = 0; k < 16; ++k)
+                if (j0 + 64 * k < nsub) sv += v[k];
+        }
 #pragma unroll
         for (int o = 32; o > 0; o >>= 1) sv += __shfl_xor(sv, o, 64);
         if (t == 0) {
@@ -446,40 +437,45 @@ __device__ int32_t sampler_pick(const float* __restrict__ lg, int64_t V, float m
         }
     }
     __syncthreads();
-    // the reference's arithmetic over the K kept values in order p
-    // descending, index ascending (every lane of the one wave reads before
-    // any lane writes: LDS in order within a wave)
-    auto sort_desc = [&]() {
-        if (t < 64) {
-            wave_rank_sort(kp, ki, K, false, ord, l);
-            __builtin_amdgcn_wave_barrier();
-            const float pv = l < K ? kp[ord[l]] : 0.f;
-            const int32_t iv = l < K ? ki[ord[l]] : 0;
+    // the reference's arithmetic over the K kept values, on wave 0 with
+    // value l in lane l: the orders by rank (shuffle comparisons, then one
+    // LDS scatter / gather), the sequential sums as loops of shuffles that
+    // every lane runs alike (the same operations in the same order as one
+    // thread's loop over the sorted array)
+    if (t < 64) {
+        float pv = l < K ? kp[l] : 0.f;
+        int32_t iv = l < K ? ki[l] : INT_MAX;
+        // lane r takes the element of rank r (rank of (p, i): p descending,
+        // index ascending; by_index: index ascending)
+        auto permute = [&](bool by_index) {
+            int r = 0;
+            for (int j = 0; j < K; ++j) {
+                const float pj = __shfl(pv, j, 64);
+                const int32_t ij = __shfl(iv, j, 64);
+                r += by_index ? ij < iv : (pj > pv || (pj == pv && ij < iv));
+            }
             __builtin_amdgcn_wave_barrier();
             if (l < K) {
-                kp[l] = pv;
-                ki[l] = iv;
+                kp[r] = pv;
+                ki[r] = iv;
             }
+            __builtin_amdgcn_wave_barrier();
+            pv = l < K ? kp[l] : 0.f;
+            iv = l < K ? ki[l] : INT_MAX;
+            __builtin_amdgcn_wave_barrier();
+        };
+        permute(false);
+        if (use_k) {
+            float keep = 0.f;
+            for (int i = 0; i < K; ++i) keep += __shfl(pv, i, 64);
+            if (l < K) pv = pv / keep;
         }
-        __syncthreads();
-    };
-    sort_desc();
-    if (t == 0 && use_k) {
-        float keep = 0.f;
-#pragma unroll 8
-        for (int i = 0; i < K; ++i) keep += kp[i];
-#pragma unroll 8
-        for (int i = 0; i < K; ++i) kp[i] = kp[i] / keep;
-    }
-    __syncthreads();
-    if (top_p < 1.f) {
-        sort_desc();  // the filtered values sorted again (division can make new ties)
-        if (t == 0) {
+        if (top_p < 1.f) {
+            permute(false);  // the filtered values sorted again (division can make new ties)
             double cum = 0.0;
             int cut = K + 1;  // not reached among the kept: nothing cut
-#pragma unroll 8
             for (int i = 0; i < K; ++i) {
-                cum += kp[i];
+                cum += __shfl(pv, i, 64);
                 if (cum >= (double)top_p) {
                     cut = i + 1;
                     break;
@@ -487,40 +483,33 @@ __device__ int32_t sampler_pick(const float* __restrict__ lg, int64_t V, float m
             }
             if (cut <= K) {
                 double tail = 0.0;
-#pragma unroll 8
-                for (int i = cut; i < K; ++i) {
-                    tail += kp[i];
-                    kp[i] = 0.f;
-                }
-                if (tail > 0.0)
-#pragma unroll 8
-                    for (int i = 0; i < cut; ++i) kp[i] = (float)(kp[i] / (1.0 - tail));
+                for (int i = cut; i < K; ++i) tail += __shfl(pv, i, 64);
+                if (l >= cut) pv = 0.f;
+                if (tail > 0.0 && l < cut) pv = (float)(pv / (1.0 - tail));
             }
         }
-        __syncthreads();
-    }
-    // the draw: the first index whose running double sum, as float, reaches r
-    if (t < 64) wave_rank_sort(kp, ki, K, true, ord, l);
-    __syncthreads();
-    if (t == 0) {
+        // the draw: the first index whose running double sum, as float,
+        // reaches r
+        permute(true);
         uint64_t st = *state;
         const float r = sampler_next_float(st);
-        *state = st;
         int32_t pk = -1;
         if (r <= 0.f) {
             pk = 0;  // the reference's loop stops at index 0
         } else {
             double c = 0.0;
-#pragma unroll 8
             for (int i = 0; i < K; ++i) {
-                c += kp[ord[i]];
+                c += __shfl(pv, i, 64);
                 if ((float)c >= r) {
-                    pk = ki[ord[i]];
+                    pk = __shfl(iv, i, 64);
                     break;
                 }
             }
         }
-        pick = pk >= 0 ? pk : amax;
+        if (l == 0) {
+            *state = st;
+            pick = pk >= 0 ? pk : amax;
+        }
     }
     __syncthreads();
     const int32_t r = pick;
