@@ -447,21 +447,20 @@ __device__ __forceinline__ void attn_mfma_wg_mc(const AttnMArgs& a, int grp, int
     }
 }
 
-// Many query rows per kv head (draft trees, batches of trees): one
-// workgroup of NW waves takes NW * 16 * QU query rows of one kv
-// head over a group of a.nc blocks of chunk_slots(HD) slots (the partials'
-// unit, as in attn_mfma_wg_mc), so each K / V row is read from
-// memory by ceil(rows / (NW * 16 * QU)) workgroups instead of one per
-// 32 rows.  The group's 64-slot chunks are copied to LDS by direct
+// More than 16 query rows per kv head (chains of several tokens, draft
+// trees, batches of trees): one workgroup of FA_WAVES waves takes 16 query
+// rows per wave of one kv head over a group of a.nc blocks of
+// chunk_slots(HD) slots (the partials' unit, as in attn_mfma_wg_mc), so each
+// K / V row is read by ceil(rows / 128) workgroups instead of one per 32
+// rows.  The group's 64-slot chunks are copied to LDS by direct
 // global->LDS loads one chunk ahead (double buffer, one barrier per chunk),
 // in MFMA fragment order: block (st, dc) of K holds, at lane l's 16 bytes,
 // K[slot pi(st, l % 16)][32 dc + 8 (l / 16) ..], with the slot permutation
 // pi(st, m) = 32 (st / 2) + 8 (m / 4) + 4 (st % 2) + m % 4; block (dt, sp)
 // of V^T holds V^T[16 dt + l % 16][32 sp + 8 (l / 16) ..].  Every operand
 // read is one conflict-free 16-byte LDS load per lane.
-// Wave w owns QU units of 16 query rows and keeps, per unit, the query as
-// the B operand (fp16 hi + lo), the running row maximum and sum, and O^T
-// (dims x rows) in registers:
+// A wave keeps its rows' query as the B operand (fp16 hi + lo), the running
+// row maximum and sum, and O^T (dims x rows) in registers:
 //   S^T = K . Q^T on v_mfma_f32_16x16x32_f16: C lane (col, kq) holds the
 //   scores of row col at slots pi(st, 4 kq + r), r < 4 -- for the two tiles
 //   st = 2 sp, 2 sp + 1 these are slots 32 sp + 8 kq + e, e < 8, which is
@@ -471,8 +470,13 @@ __device__ __forceinline__ void attn_mfma_wg_mc(const AttnMArgs& a, int grp, int
 //   and sum are a lane's own values plus two shuffles.
 // Flash attention per chunk: m_new = max(m, max_chunk s), O <- e^(m - m_new)
 // O + P V, l <- e^(m - m_new) l + sum P, P = e^(s - m_new) split fp16 hi +
-// lo.  One partial (O, m, l) per row and group, in the layout of
-// attn_mfma_wg_mc, combined by k_attn_combine.
+// lo (computed as 2^(s c - m c), c = log2(e) / sqrt(hd)).  One partial
+// (O, m, l) per row and group, in the layout of attn_mfma_wg_mc, combined by
+// k_attn_combine (or k_attn_combine_xq).
+// Measured: 8 waves (two per SIMD) beat 16 (four per SIMD) and 32 rows per
+// wave on the 52-node tree and the 70B batch; the workgroup's MFMAs and
+// softmax arithmetic do not overlap, so its time is their sum.
+constexpr int FA_WAVES = 8;
 constexpr int FA_CHK = 64;  // slots per chunk
 typedef __attribute__((address_space(3))) void lds_void;
 
@@ -481,16 +485,16 @@ __host__ __device__ constexpr size_t fa_lds_bytes() {
     return 2 * (size_t)(HD / 8 + HD / 8) * 1024;  // two buffers of K and V^T blocks
 }
 
-template <int HD, int QU, int NW>
+template <int HD>
 __device__ __forceinline__ void attn_fa_wg(const AttnMArgs& a, int grp, int kvh, int qsplit,
                                            int ngrp) {
     constexpr int NDC = HD / 32;     // 32-dim steps of the score contraction
     constexpr int NDT = HD / 16;     // 16-dim tiles of O^T
     constexpr int KB = 4 * NDC;      // K blocks per chunk: (st, dc)
     constexpr int NB = KB + 2 * NDT; // with the V^T blocks (dt, sp)
-    constexpr int BPW = NB / NW;
-    static_assert(NB % NW == 0 && NDC % BPW == 0 && (BPW == 1 || BPW % 2 == 0),
-                  "a wave copies blocks of one kind, of one slot tile / whole dim tiles");
+    constexpr int BPW = NB / FA_WAVES;
+    static_assert(NB % FA_WAVES == 0 && NDC % BPW == 0 && BPW % 2 == 0,
+                  "a wave copies blocks of one slot tile of K, or whole dim tiles of V^T");
     constexpr int BUF = NB * 1024;
     constexpr int CPB = chunk_slots(HD) / FA_CHK;  // chunks per partial block
     static_assert(CPB * FA_CHK == chunk_slots(HD), "whole chunks per block");
@@ -503,21 +507,21 @@ __device__ __forceinline__ void attn_fa_wg(const AttnMArgs& a, int grp, int kvh,
     if (gslot0 >= total) return;  // block-uniform
     const int nck = (int)min((int64_t)a.nc * CPB, (total - gslot0 + FA_CHK - 1) / FA_CHK);
     const int gqa = a.n_head / a.n_kv, qrows = a.M * gqa;
-    const int rbase = (qsplit * NW + w) * 16 * QU;  // the wave's first query row
-    const bool wlive = rbase < qrows;                      // wave-uniform
+    const int rbase = (qsplit * FA_WAVES + w) * 16;  // the wave's first query row
+    const bool wlive = rbase < qrows;                // wave-uniform
 
     // the wave's blocks b0 + i, b0 = BPW w: K blocks (st, dc0 + i) or V^T
-    // blocks (dt0 + i / 2, sp0 + i % 2).  Block i of a chunk at slot0 comes
-    // from lbase + slot0 * sstride + ioff(i) (K rows: kdim apart; V^T rows:
+    // blocks (dt0 + i / 2, i % 2).  Block i of a chunk at slot0 comes from
+    // lbase + slot0 * sstride + ioff(i) (K rows: kdim apart; V^T rows:
     // contiguous)
     const int b0 = BPW * w;
     const bool kwave = b0 < KB;  // wave-uniform
     const int64_t sstride = kwave ? (int64_t)a.n_kv * HD : 1;
-    const int st0 = b0 / NDC, dc0 = b0 % NDC, dt0 = (b0 - KB) >> 1, sp0 = (b0 - KB) & 1;
+    const int st0 = b0 / NDC, dc0 = b0 % NDC, dt0 = (b0 - KB) >> 1;
     const _Float16* lbase =
         kwave ? a.kc + (32 * (st0 >> 1) + 8 * (col >> 2) + 4 * (st0 & 1) + (col & 3)) * sstride +
                     (int64_t)kvh * HD + 32 * dc0 + 8 * kq
-              : a.vt + ((int64_t)kvh * HD + 16 * dt0 + col) * a.cap + 32 * sp0 + 8 * kq;
+              : a.vt + ((int64_t)kvh * HD + 16 * dt0 + col) * a.cap + 8 * kq;
     auto ioff = [&](int i) -> int64_t { return kwave ? 32 * i : 16 * (i >> 1) * a.cap + 32 * (i & 1); };
     auto stage = [&](int64_t slot0, int buf) {
         uint8_t* dst = fa_lds + buf * BUF + BPW * w * 1024;
@@ -529,175 +533,138 @@ __device__ __forceinline__ void attn_fa_wg(const AttnMArgs& a, int grp, int kvh,
     };
     stage(gslot0, 0);
 
-    // the query rows' B operands (rows past qrows repeat the last valid row:
-    // their results stay in their own O^T columns and are never stored)
-    v8h qf[QU][NDC][2];
-    int node[QU];
-#pragma unroll
-    for (int u = 0; u < QU; ++u) {
-        const int rq = min(rbase + 16 * u + col, qrows - 1);
-        node[u] = rq / gqa;
-        const int64_t qo = ((int64_t)node[u] * a.n_head + kvh * gqa + rq % gqa) * HD + 8 * kq;
+    // the rows' B operands (rows past qrows repeat the last valid row: their
+    // results stay in their own O^T columns and are never stored)
+    v8h qf[NDC][2];
+    const int rq0 = min(rbase + col, qrows - 1), node = rq0 / gqa;
+    {
+        const int64_t qo = ((int64_t)node * a.n_head + kvh * gqa + rq0 % gqa) * HD + 8 * kq;
 #pragma unroll
         for (int dc = 0; dc < NDC; ++dc) {
-            qf[u][dc][0] = wlive ? *(const v8h*)(a.qh16 + qo + 32 * dc) : v8h{};
-            qf[u][dc][1] = wlive ? *(const v8h*)(a.ql16 + qo + 32 * dc) : v8h{};
+            qf[dc][0] = wlive ? *(const v8h*)(a.qh16 + qo + 32 * dc) : v8h{};
+            qf[dc][1] = wlive ? *(const v8h*)(a.ql16 + qo + 32 * dc) : v8h{};
         }
     }
-    // scores enter the softmax in base 2: p = 2^(s c - m c), c = log2(e) / sqrt(hd)
     const float c2 = 1.4426950408889634f / sqrtf((float)HD);
-    float mrun[QU], lrun[QU];  // running maximum of the raw scores, running sum
-    v4f o[QU][NDT];
+    float mrun = -INFINITY, lrun = 0.f;  // running maximum of the raw scores, running sum
+    v4f o[NDT];
 #pragma unroll
-    for (int u = 0; u < QU; ++u) {
-        mrun[u] = -INFINITY;
-        lrun[u] = 0.f;
-#pragma unroll
-        for (int dt = 0; dt < NDT; ++dt) o[u][dt] = v4f{0.f, 0.f, 0.f, 0.f};
-    }
-    // raw scores S^T of one chunk from LDS buffer bufp
-    auto scores = [&](const uint8_t* bufp, v4f (&s)[QU][4]) {
-#pragma unroll
-        for (int st = 0; st < 4; ++st)
-#pragma unroll
-            for (int dc = 0; dc < NDC; ++dc) {
-                const v8h kf = *(const v8h*)(bufp + (st * NDC + dc) * 1024 + lane * 16);
-#pragma unroll
-                for (int u = 0; u < QU; ++u) {
-                    s[u][st] = __builtin_amdgcn_mfma_f32_16x16x32_f16(
-                        kf, qf[u][dc][0], dc == 0 ? v4f{0.f, 0.f, 0.f, 0.f} : s[u][st], 0, 0, 0);
-                    s[u][st] = __builtin_amdgcn_mfma_f32_16x16x32_f16(kf, qf[u][dc][1], s[u][st], 0, 0, 0);
-                }
-            }
-    };
-    // the chunk at slot0 (scores s, V^T in buffer bufp): mask, running
-    // maximum and sum, O rescale, O^T += V^T . P^T; tree: the ancestor words
-    // aw of the lane's two 8-slot runs (j0, wsel) for chunks reaching into
-    // the draft
-    auto softmax_pv = [&](const uint8_t* bufp, v4f (&s)[QU][4], bool tree,
-                          const uint32_t (&aw)[QU][2][2], const int (&j0)[2], const int (&wsel)[2]) {
-        v8h ph[QU][2], pl[QU][2];
-#pragma unroll
-        for (int u = 0; u < QU; ++u) {
-            if (tree) {
-                // slot 8 kq + e of run sp: allowed iff before the draft, or a
-                // draft slot j < M whose ancestor bit is set
-#pragma unroll
-                for (int sp = 0; sp < 2; ++sp) {
-                    const uint64_t win = aw[u][sp][0] | ((uint64_t)aw[u][sp][1] << 32);
-#pragma unroll
-                    for (int e = 0; e < 8; ++e) {
-                        const int j = j0[sp] + e;
-                        const bool ok = (j < 0) | ((j < a.M) & (((win >> ((j - 32 * wsel[sp]) & 63)) & 1u) != 0));
-                        const float v = s[u][2 * sp + (e >> 2)][e & 3];
-                        s[u][2 * sp + (e >> 2)][e & 3] = ok ? v : -INFINITY;
-                    }
-                }
-            }
-            float mx = -INFINITY;
-#pragma unroll
-            for (int st = 0; st < 4; ++st)
-#pragma unroll
-                for (int r = 0; r < 4; ++r) mx = fmaxf(mx, s[u][st][r]);
-            mx = fmaxf(mx, __shfl_xor(mx, 16, 64));
-            mx = fmaxf(mx, __shfl_xor(mx, 32, 64));
-            const float mo = mrun[u], mn = fmaxf(mo, mx);
-            // every score so far masked: p = 0, nothing to rescale
-            const float mc = mn == -INFINITY ? 0.f : mn * c2;
-            const float al = __builtin_amdgcn_exp2f(mo * c2 - mc);  // 0 while mo = -inf
-            float sum = 0.f;
-#pragma unroll
-            for (int sp = 0; sp < 2; ++sp)
-#pragma unroll
-                for (int e = 0; e < 8; ++e) {
-                    const float p =
-                        __builtin_amdgcn_exp2f(__builtin_fmaf(s[u][2 * sp + (e >> 2)][e & 3], c2, -mc));
-                    sum += p;
-                    const _Float16 h = (_Float16)p;
-                    ph[u][sp][e] = h;
-                    pl[u][sp][e] = (_Float16)(p - (float)h);
-                }
-            sum += __shfl_xor(sum, 16, 64);
-            sum += __shfl_xor(sum, 32, 64);
-            lrun[u] = al * lrun[u] + sum;
-            mrun[u] = mn;
-            if (__builtin_amdgcn_ballot_w64(al != 1.f))  // a maximum moved (wave-uniform)
-#pragma unroll
-                for (int dt = 0; dt < NDT; ++dt) o[u][dt] *= al;
-        }
-#pragma unroll
-        for (int dt = 0; dt < NDT; ++dt)
-#pragma unroll
-            for (int sp = 0; sp < 2; ++sp) {
-                const v8h vf = *(const v8h*)(bufp + (KB + 2 * dt + sp) * 1024 + lane * 16);
-#pragma unroll
-                for (int u = 0; u < QU; ++u) {
-                    o[u][dt] = __builtin_amdgcn_mfma_f32_16x16x32_f16(vf, ph[u][sp], o[u][dt], 0, 0, 0);
-                    o[u][dt] = __builtin_amdgcn_mfma_f32_16x16x32_f16(vf, pl[u][sp], o[u][dt], 0, 0, 0);
-                }
-            }
-    };
-    v4f s[QU][4];
+    for (int dt = 0; dt < NDT; ++dt) o[dt] = v4f{0.f, 0.f, 0.f, 0.f};
     for (int c = 0; c < nck; ++c) {
         const int64_t slot0 = gslot0 + (int64_t)c * FA_CHK;
         __builtin_amdgcn_s_waitcnt(0x0F70);  // this wave's copies of chunk c
         __syncthreads();                     // every wave's copies; the other buffer free
         // chunks reaching into the draft (block-uniform): the ancestor words
-        // of the lane's 8-slot runs, loaded before the next chunk's copies
+        // of the lane's two 8-slot runs, loaded before the next chunk's copies
         const bool tree = wlive && slot0 + FA_CHK > npast;
-        uint32_t aw[QU][2][2];
+        uint32_t aw[2][2];
         int j0[2] = {0, 0}, wsel[2] = {0, 0};
         if (tree) {
+            const uint32_t* an = a.anc + node * a.anc_words;
 #pragma unroll
             for (int sp = 0; sp < 2; ++sp) {
                 j0[sp] = (int)(slot0 - npast) + 32 * sp + 8 * kq;
                 wsel[sp] = min(max(j0[sp], 0) >> 5, a.anc_words - 1);
-                const int wn = min(wsel[sp] + 1, a.anc_words - 1);
-#pragma unroll
-                for (int u = 0; u < QU; ++u) {
-                    const uint32_t* an = a.anc + node[u] * a.anc_words;
-                    aw[u][sp][0] = an[wsel[sp]];
-                    aw[u][sp][1] = an[wn];
-                }
+                aw[sp][0] = an[wsel[sp]];
+                aw[sp][1] = an[min(wsel[sp] + 1, a.anc_words - 1)];
             }
         }
         if (c + 1 < nck) stage(slot0 + FA_CHK, (c + 1) & 1);
         if (!wlive) continue;
         const uint8_t* bufp = fa_lds + (c & 1) * BUF;
-        scores(bufp, s);
-        softmax_pv(bufp, s, tree, aw, j0, wsel);
+        // raw scores S^T
+        v4f s[4];
+#pragma unroll
+        for (int st = 0; st < 4; ++st)
+#pragma unroll
+            for (int dc = 0; dc < NDC; ++dc) {
+                const v8h kf = *(const v8h*)(bufp + (st * NDC + dc) * 1024 + lane * 16);
+                s[st] = __builtin_amdgcn_mfma_f32_16x16x32_f16(
+                    kf, qf[dc][0], dc == 0 ? v4f{0.f, 0.f, 0.f, 0.f} : s[st], 0, 0, 0);
+                s[st] = __builtin_amdgcn_mfma_f32_16x16x32_f16(kf, qf[dc][1], s[st], 0, 0, 0);
+            }
+        if (tree) {
+            // slot 8 kq + e of run sp: allowed iff before the draft, or a
+            // draft slot j < M whose ancestor bit is set
+#pragma unroll
+            for (int sp = 0; sp < 2; ++sp) {
+                const uint64_t win = aw[sp][0] | ((uint64_t)aw[sp][1] << 32);
+#pragma unroll
+                for (int e = 0; e < 8; ++e) {
+                    const int j = j0[sp] + e;
+                    const bool ok = (j < 0) | ((j < a.M) & (((win >> ((j - 32 * wsel[sp]) & 63)) & 1u) != 0));
+                    const float v = s[2 * sp + (e >> 2)][e & 3];
+                    s[2 * sp + (e >> 2)][e & 3] = ok ? v : -INFINITY;
+                }
+            }
+        }
+        float mx = -INFINITY;
+#pragma unroll
+        for (int st = 0; st < 4; ++st)
+#pragma unroll
+            for (int r = 0; r < 4; ++r) mx = fmaxf(mx, s[st][r]);
+        mx = fmaxf(mx, __shfl_xor(mx, 16, 64));
+        mx = fmaxf(mx, __shfl_xor(mx, 32, 64));
+        const float mn = fmaxf(mrun, mx);
+        // every score so far masked: p = 0, nothing to rescale
+        const float mc = mn == -INFINITY ? 0.f : mn * c2;
+        const float al = __builtin_amdgcn_exp2f(mrun * c2 - mc);  // 0 while mrun = -inf
+        float sum = 0.f;
+        v8h ph[2], pl[2];
+#pragma unroll
+        for (int sp = 0; sp < 2; ++sp)
+#pragma unroll
+            for (int e = 0; e < 8; ++e) {
+                const float p = __builtin_amdgcn_exp2f(__builtin_fmaf(s[2 * sp + (e >> 2)][e & 3], c2, -mc));
+                sum += p;
+                const _Float16 h = (_Float16)p;
+                ph[sp][e] = h;
+                pl[sp][e] = (_Float16)(p - (float)h);
+            }
+        sum += __shfl_xor(sum, 16, 64);
+        sum += __shfl_xor(sum, 32, 64);
+        lrun = al * lrun + sum;
+        mrun = mn;
+        if (__builtin_amdgcn_ballot_w64(al != 1.f))  // a maximum moved (wave-uniform)
+#pragma unroll
+            for (int dt = 0; dt < NDT; ++dt) o[dt] *= al;
+        // O^T += V^T . P^T
+#pragma unroll
+        for (int dt = 0; dt < NDT; ++dt)
+#pragma unroll
+            for (int sp = 0; sp < 2; ++sp) {
+                const v8h vf = *(const v8h*)(bufp + (KB + 2 * dt + sp) * 1024 + lane * 16);
+                o[dt] = __builtin_amdgcn_mfma_f32_16x16x32_f16(vf, ph[sp], o[dt], 0, 0, 0);
+                o[dt] = __builtin_amdgcn_mfma_f32_16x16x32_f16(vf, pl[sp], o[dt], 0, 0, 0);
+            }
     }
-    if (!wlive) return;
+    const int rq = rbase + col;
+    if (!wlive || rq >= qrows) return;
     // the group's partial (m in natural-log units, as the combine expects):
     // lane (col, kq) of tile dt holds dims 16 dt + 4 kq + r of row col
+    const int64_t qrow = (int64_t)(rq / gqa) * a.n_head + kvh * gqa + rq % gqa;
+    float* po = a.pout + (qrow * ngrp + grp) * HD + 4 * kq;
 #pragma unroll
-    for (int u = 0; u < QU; ++u) {
-        const int rq = rbase + 16 * u + col;
-        if (rq >= qrows) continue;
-        const int64_t qrow = (int64_t)(rq / gqa) * a.n_head + kvh * gqa + rq % gqa;
-        float* po = a.pout + (qrow * ngrp + grp) * HD + 4 * kq;
-#pragma unroll
-        for (int dt = 0; dt < NDT; ++dt) *(v4f*)(po + 16 * dt) = o[u][dt];
-        if (kq == 0) {
-            a.pmax[qrow * ngrp + grp] = mrun[u] == -INFINITY ? -INFINITY : mrun[u] * (c2 * 0.6931471805599453f);
-            a.psum[qrow * ngrp + grp] = lrun[u];
-        }
+    for (int dt = 0; dt < NDT; ++dt) *(v4f*)(po + 16 * dt) = o[dt];
+    if (kq == 0) {
+        a.pmax[qrow * ngrp + grp] = mrun == -INFINITY ? -INFINITY : mrun * (c2 * 0.6931471805599453f);
+        a.psum[qrow * ngrp + grp] = lrun;
     }
 }
 
-template <int HD, int QU, int NW>
-__global__ void __launch_bounds__(64 * NW) k_attn_fa(AttnMArgs a) {
-    attn_fa_wg<HD, QU, NW>(a, blockIdx.x, blockIdx.y, blockIdx.z, gridDim.x);
+template <int HD>
+__global__ void __launch_bounds__(64 * FA_WAVES) k_attn_fa(AttnMArgs a) {
+    attn_fa_wg<HD>(a, blockIdx.x, blockIdx.y, blockIdx.z, gridDim.x);
 }
 
 // several sequences: grid.z runs over every sequence's query splits
 // (sequence s owns splits qt0[s] .. qt0[s + 1] - 1)
-template <int HD, int QU, int NW>
-__global__ void __launch_bounds__(64 * NW) k_attn_fa_batch(AttnMBatch b) {
+template <int HD>
+__global__ void __launch_bounds__(64 * FA_WAVES) k_attn_fa_batch(AttnMBatch b) {
     int s = 0;
     while (s + 1 < b.nseq && (int)blockIdx.z >= b.qt0[s + 1]) ++s;
     const AttnMArgs a = b.s[s];  // loaded once
-    attn_fa_wg<HD, QU, NW>(a, blockIdx.x, blockIdx.y, (int)blockIdx.z - b.qt0[s], b.nch[s]);
+    attn_fa_wg<HD>(a, blockIdx.x, blockIdx.y, (int)blockIdx.z - b.qt0[s], b.nch[s]);
 }
 
 template <int HD, int CHK, int NWV>
@@ -906,20 +873,18 @@ static int attn_chunks_per_wg(int64_t wgs) {
     return nc;
 }
 
-// The many-row kernel (k_attn_fa) takes sequences with more than 64 query
-// rows per kv head, 16 rows per wave: 8 waves up to 128 rows, 16 waves (four
-// per SIMD, one workgroup per CU) above, so a workgroup of 256 rows reads
-// the context where eight 32-row tiles did.
-static bool attn_fa_rows(int64_t qrows) { return qrows > 64; }
-static int attn_fa_waves(int64_t qrows) { return qrows > 128 ? 16 : 8; }
-static int attn_fa_splits(int64_t qrows, int nw) { return (int)((qrows + 16 * nw - 1) / (16 * nw)); }
+// The many-row kernel (k_attn_fa) takes sequences with more than 16 query
+// rows per kv head (measured: the 8-token chain of 32 rows per kv head at
+// context 2048 gains a little, the trees and batches most)
+static bool attn_fa_rows(int64_t qrows) { return qrows > 16; }
+static int attn_fa_splits(int64_t qrows) { return (int)((qrows + 16 * FA_WAVES - 1) / (16 * FA_WAVES)); }
 
 // Blocks of chunk_slots(hd) slots per workgroup for the many-row kernel:
 // sequence s has nblk[s] live blocks and splits[s] row splits; with nc
-// blocks per workgroup the live workgroups run in rounds of 256 (one per
-// CU), a round costing about 3 + (chunks per workgroup) chunk times
-// (measured: ~3 us of start and ~1-2 us per 64-slot chunk); the cheapest nc
-// <= 16, the largest on ties (fewer partials for the combine).
+// blocks per workgroup the live workgroups run in rounds of 256, a round
+// costing about 3 + (chunks per workgroup) chunk times (measured: ~3 us of
+// start and ~1-2 us per 64-slot chunk); the cheapest nc <= 16, the largest
+// on ties (fewer partials for the combine).
 static int attn_fa_blocks_per_wg(const int64_t* nblk, const int* splits, int nseq, int n_kv,
                                  int cpb) {
     int best = 1;
@@ -936,7 +901,7 @@ static int attn_fa_blocks_per_wg(const int64_t* nblk, const int* splits, int nse
     return best;
 }
 
-template <int HD, int NW, typename A>
+template <int HD, typename A>
 static hipError_t launch_fa(void (*kern)(A), const dim3& grid, hipStream_t st, const A& args) {
     static bool lds_set = false;
     if (!lds_set) {
@@ -946,7 +911,7 @@ static hipError_t launch_fa(void (*kern)(A), const dim3& grid, hipStream_t st, c
         if (e != hipSuccess) return e;
         lds_set = true;
     }
-    ktimed_launch(kern, grid, dim3(64 * NW), (uint32_t)fa_lds_bytes<HD>(), st, args);
+    ktimed_launch(kern, grid, dim3(64 * FA_WAVES), (uint32_t)fa_lds_bytes<HD>(), st, args);
     return hipGetLastError();
 }
 
@@ -958,26 +923,31 @@ hipError_t launch_attn_mfma(hipStream_t st, AttnMArgs a, float* part, int8_t* xq
     if (nch > 1024) return hipErrorInvalidValue;  // combine weights live in LDS
     const int64_t qi = (int64_t)a.M * a.n_head;
     const int64_t qrows = (int64_t)a.M * (a.n_head / a.n_kv);
-    if (!xq && attn_fa_rows(qrows)) {
-        const int nw = attn_fa_waves(qrows), qs = attn_fa_splits(qrows, nw);
+    if (attn_fa_rows(qrows)) {
+        const int qs = attn_fa_splits(qrows);
         const int64_t nblk = (a.npast + a.M + ch - 1) / ch;
-        a.nc = attn_fa_blocks_per_wg(&nblk, &qs, 1, a.n_kv, ch / FA_CHK);
+        a.nc = xq ? 1 : attn_fa_blocks_per_wg(&nblk, &qs, 1, a.n_kv, ch / FA_CHK);
         const int ngrp = (nch + a.nc - 1) / a.nc;  // the partials' stride
         a.pmax = part;
         a.psum = part + qi * ngrp;
         a.pout = part + 2 * qi * ngrp;
         const dim3 grid((unsigned)ngrp, (unsigned)a.n_kv, (unsigned)qs);
         hipError_t e;
-        if (a.hd == 128 && nw == 16)
-            e = launch_fa<128, 16>(k_attn_fa<128, 1, 16>, grid, st, a);
-        else if (a.hd == 128)
-            e = launch_fa<128, 8>(k_attn_fa<128, 1, 8>, grid, st, a);
-        else if (nw == 16)
-            e = launch_fa<64, 16>(k_attn_fa<64, 1, 16>, grid, st, a);
+        if (a.hd == 128)
+            e = launch_fa<128>(k_attn_fa<128>, grid, st, a);
         else
-            e = launch_fa<64, 8>(k_attn_fa<64, 1, 8>, grid, st, a);
+            e = launch_fa<64>(k_attn_fa<64>, grid, st, a);
         if (e != hipSuccess) return e;
-        hipLaunchKernelGGL(k_attn_combine, dim3((unsigned)qi), dim3(128), 0, st, a, ngrp);
+        if (xq) {
+            const int64_t K = (int64_t)a.n_head * a.hd;
+            const dim3 cg((unsigned)(K / 256), 8);
+            if (a.hd == 128)
+                hipLaunchKernelGGL(k_attn_combine_xq<128>, cg, dim3(256), 0, st, a, ngrp, xq_ptrs(xq, K));
+            else
+                hipLaunchKernelGGL(k_attn_combine_xq<64>, cg, dim3(256), 0, st, a, ngrp, xq_ptrs(xq, K));
+        } else {
+            hipLaunchKernelGGL(k_attn_combine, dim3((unsigned)qi), dim3(128), 0, st, a, ngrp);
+        }
         return hipGetLastError();
     }
     // one workgroup per (chunk or group of chunks, kv head, tile of 32 query rows)
@@ -1023,16 +993,9 @@ hipError_t launch_attn_mfma_batch(hipStream_t st, const AttnMArgs* as, const flo
     AttnMBatch b{};
     b.nseq = nseq;
     int hd = as[0].hd, nkv = as[0].n_kv, maxch = 0, qt = 0, qi = 0;
-    // the many-row kernel when every sequence has the rows for it (one
-    // rows-per-wave choice for the launch, from the largest sequence)
+    // the many-row kernel when every sequence has the rows for it
     bool fa = true;
-    int64_t maxrows = 0;
-    for (int s = 0; s < nseq; ++s) {
-        const int64_t r = (int64_t)as[s].M * (as[s].n_head / nkv);
-        fa = fa && attn_fa_rows(r);
-        maxrows = r > maxrows ? r : maxrows;
-    }
-    const int nw = attn_fa_waves(maxrows);
+    for (int s = 0; s < nseq; ++s) fa = fa && attn_fa_rows((int64_t)as[s].M * (as[s].n_head / nkv));
     int64_t wgs = 0;  // the one-block grid's live workgroups
     int64_t nblk[FTX_MAX_SEQ];
     int splits[FTX_MAX_SEQ];
@@ -1041,7 +1004,7 @@ hipError_t launch_attn_mfma_batch(hipStream_t st, const AttnMArgs* as, const flo
         if (as[s].hd != hd || as[s].n_kv != nkv || as[s].cap % ch) return hipErrorInvalidValue;
         const int64_t r = (int64_t)as[s].M * (as[s].n_head / nkv);
         nblk[s] = (as[s].npast + as[s].M + ch - 1) / ch;
-        splits[s] = fa ? attn_fa_splits(r, nw) : (int)((r + 31) / 32);
+        splits[s] = fa ? attn_fa_splits(r) : (int)((r + 31) / 32);
         wgs += nblk[s] * nkv * splits[s];
     }
     const int nc = fa ? attn_fa_blocks_per_wg(nblk, splits, nseq, nkv, chunk_slots(hd) / FA_CHK)
@@ -1070,14 +1033,10 @@ hipError_t launch_attn_mfma_batch(hipStream_t st, const AttnMArgs* as, const flo
     const dim3 grid((unsigned)maxch, (unsigned)nkv, (unsigned)qt);
     if (fa) {
         hipError_t e;
-        if (hd == 128 && nw == 16)
-            e = launch_fa<128, 16>(k_attn_fa_batch<128, 1, 16>, grid, st, b);
-        else if (hd == 128)
-            e = launch_fa<128, 8>(k_attn_fa_batch<128, 1, 8>, grid, st, b);
-        else if (hd == 64 && nw == 16)
-            e = launch_fa<64, 16>(k_attn_fa_batch<64, 1, 16>, grid, st, b);
+        if (hd == 128)
+            e = launch_fa<128>(k_attn_fa_batch<128>, grid, st, b);
         else if (hd == 64)
-            e = launch_fa<64, 8>(k_attn_fa_batch<64, 1, 8>, grid, st, b);
+            e = launch_fa<64>(k_attn_fa_batch<64>, grid, st, b);
         else
             return hipErrorInvalidValue;
         if (e != hipSuccess) return e;
