@@ -816,9 +816,9 @@ k_mm_down(MmDownArgs a) {
             const int64_t I = Ib + k;
             if (I >= I1) break;  // block-uniform
             const int buf = k & 1;
+            if (I + 1 < I1) stage_store(ring[(k + 1) % MMD_RING], buf ^ 1);
             compute(ring[k].wq, buf);
             if (I + MMD_RING < I1) issue(ring[k], I + MMD_RING);
-            if (I + 1 < I1) stage_store(ring[(k + 1) % MMD_RING], buf ^ 1);
             __syncthreads();
         }
     }
