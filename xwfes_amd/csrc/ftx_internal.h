@@ -251,6 +251,21 @@ MmAct mm_act(void* buf, int64_t Mp, int64_t K);
 hipError_t launch_mm_prep(hipStream_t st, const float* x, int64_t ldx, const float* normw,
                           float eps, int64_t M, const MmAct& act, int weight_dt,
                           const int32_t* gather = nullptr);
+// Split partials of an accumulating GEMM (out += its result) not yet added
+// into out: part + ks * split_stride + m * ldp + n, S splits, N columns
+// (S = 0: nothing pending)
+struct MmPend {
+    const float* part = nullptr;
+    int64_t split_stride = 0, ldp = 0, N = 0;
+    int S = 0;
+};
+// the partials `fold` added into x (rows < M, written back), then the prep
+// of launch_mm_prep without a gather (fold.S = 0: the plain prep)
+hipError_t launch_mm_prep_fold(hipStream_t st, float* x, int64_t ldx, const float* normw,
+                               float eps, int64_t M, const MmAct& act, int weight_dt,
+                               const MmPend& fold);
+// the partials `fold` added into y rows < M (a reduce launch)
+hipError_t launch_mm_fold(hipStream_t st, const MmPend& fold, int64_t M, float* y, int64_t ldy);
 bool mm_supported(int dt, int64_t K);
 // the one-pass GEMM's copy of Q8_0 / Q4_0 weights (per 16-row tile and
 // 256-element step, every lane's bytes contiguous): its internal dtype (or
@@ -265,11 +280,15 @@ bool mm_down_supported(int dt, int64_t n_in, int64_t N);
 size_t mm_part_floats(int64_t Mp, int64_t N, int64_t steps, int64_t ntiles, int cu_count);
 size_t mm_down_part_floats(int64_t Mp, int64_t n_in, int64_t N, int cu_count);
 // epi: EPI_STORE / EPI_ACCUM (out.accum) or EPI_SWIGLU (segments gate, up)
+// pend (EPI_ACCUM into one output, split over the contraction): the
+// partials are left in `part` for the caller to fold (launch_mm_prep_fold /
+// launch_mm_fold) instead of reduced here
 hipError_t launch_mm(hipStream_t st, const MmSeg* segs, int nseg, const MmAct& act, int64_t M,
-                     int epi, const MmOut& out, float* part, size_t part_floats, int cu_count);
+                     int epi, const MmOut& out, float* part, size_t part_floats, int cu_count,
+                     MmPend* pend = nullptr);
 hipError_t launch_mm_down(hipStream_t st, const uint8_t* tiled, int64_t n_in, int64_t N,
                           const float* h, int64_t ldh, int64_t M, const MmOut& out, float* part,
-                          size_t part_floats, int cu_count);
+                          size_t part_floats, int cu_count, MmPend* pend = nullptr);
 // SwiGLU output of an expert launch as the next GEMM's operand: fp16 hi / lo
 // planes in k_mm_prep's fragment order (contraction K), values times scale
 struct MmFragOut {

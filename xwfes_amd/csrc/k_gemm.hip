@@ -163,6 +163,119 @@ __global__ void __launch_bounds__(256) k_mm_prep(const float* __restrict__ x, in
     }
 }
 
+// The split partials of the previous GEMM added into x, then the prep of
+// k_mm_prep, one workgroup of 1024 threads per operand row m (thread t:
+// elements 4 t + 4096 c, c < K / 4096 rounded up):  x[m] <- x[m] +
+// sum_ks part[ks][m] (the sum in split order first, then added, as
+// k_mm_reduce does), written back (the residual add of
+// src/engine.cpp:274-275 / 516-517), then RMSNorm of the new row (every
+// element already in registers) and the fp16 hi + lo fragments and
+// 32-element sums as k_mm_prep writes them.  Rows m >= M: zero operands, x
+// untouched.
+constexpr int MMF_CH = 4;  // float4 chunks per thread: K <= 16384
+__global__ void __launch_bounds__(1024) k_mm_prep_fold(float* __restrict__ x, int64_t ldx,
+                                                       const float* __restrict__ normw, float eps,
+                                                       int64_t K, int M, int inter,
+                                                       const float* __restrict__ part,
+                                                       int64_t split_stride, int64_t ldp, int S,
+                                                       _Float16* __restrict__ xh,
+                                                       _Float16* __restrict__ xl,
+                                                       _Float16* __restrict__ sh,
+                                                       _Float16* __restrict__ sl) {
+#pragma clang fp contract(off)
+    __shared__ float red[16];
+    const int m = blockIdx.x, t = threadIdx.x;
+    const int64_t nsb = K / 256;
+    const bool live = m < M;  // block-uniform
+    float* row = x + (int64_t)(live ? m : 0) * ldx;
+    float4 v[MMF_CH];
+    float ss = 0.f;
+#pragma unroll
+    for (int c = 0; c < MMF_CH; ++c) {
+        v[c] = float4{0.f, 0.f, 0.f, 0.f};
+        const int64_t k = 4 * t + 4096 * c;
+        if (!live || k >= K) continue;
+        float4 g = {0.f, 0.f, 0.f, 0.f};
+        const float* pp = part + (int64_t)m * ldp + k;
+        for (int s0 = 0; s0 < S; s0 += 8) {
+            float4 pv[8];
+#pragma unroll
+            for (int i = 0; i < 8; ++i)
+                pv[i] = s0 + i < S ? *(const float4*)(pp + (int64_t)(s0 + i) * split_stride)
+                                   : float4{0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+            for (int i = 0; i < 8; ++i) {
+                g.x += pv[i].x;
+                g.y += pv[i].y;
+                g.z += pv[i].z;
+                g.w += pv[i].w;
+            }
+        }
+        const float4 xv = *(const float4*)(row + k);
+        v[c] = float4{xv.x + g.x, xv.y + g.y, xv.z + g.z, xv.w + g.w};
+        *(float4*)(row + k) = v[c];
+        ss += v[c].x * v[c].x;
+        ss += v[c].y * v[c].y;
+        ss += v[c].z * v[c].z;
+        ss += v[c].w * v[c].w;
+    }
+    float inv = 1.f;
+    if (normw) {
+#pragma unroll
+        for (int o = 32; o > 0; o >>= 1) ss += __shfl_xor(ss, o, 64);
+        if ((t & 63) == 0) red[t >> 6] = ss;
+        __syncthreads();
+        if (live) {
+            float tot = 0.f;
+#pragma unroll
+            for (int i = 0; i < 16; ++i) tot += red[i];
+            inv = 1.f / sqrtf(tot / (float)K + eps);
+        }
+    }
+#pragma unroll
+    for (int c = 0; c < MMF_CH; ++c) {
+        const int64_t k = 4 * t + 4096 * c;
+        if (k >= K) continue;  // whole 32-element groups of 8 threads alike (K % 256 == 0)
+        float o[4] = {v[c].x, v[c].y, v[c].z, v[c].w};
+        if (live && normw) {
+            const float4 w = *(const float4*)(normw + k);
+            o[0] = (o[0] * inv) * w.x;
+            o[1] = (o[1] * inv) * w.y;
+            o[2] = (o[2] * inv) * w.z;
+            o[3] = (o[3] * inv) * w.w;
+        }
+        _Float16 hv[4], lv[4];
+#pragma unroll
+        for (int i = 0; i < 4; ++i) split_hl(o[i], hv[i], lv[i]);
+        if (!inter) {
+            const int64_t at = frag_at(m, k, K, false);
+            *(v4h*)(xh + at) = v4h{hv[0], hv[1], hv[2], hv[3]};
+            *(v4h*)(xl + at) = v4h{lv[0], lv[1], lv[2], lv[3]};
+        } else {
+#pragma unroll
+            for (int i = 0; i < 4; ++i) {
+                const int64_t at = frag_at(m, k + i, K, true);
+                xh[at] = hv[i];
+                xl[at] = lv[i];
+            }
+        }
+        float s = (o[0] + o[1]) + (o[2] + o[3]);
+        s += __shfl_xor(s, 1, 64);
+        s += __shfl_xor(s, 2, 64);
+        s += __shfl_xor(s, 4, 64);
+        if ((t & 7) == 0) {
+            const int64_t j = k / 32, sb = j / 8;
+            const int jj = (int)(j % 8);
+            const int lane = (m & 15) + 16 * (jj >> 2);
+            const int64_t at = (((int64_t)(m >> 4) * nsb + sb) * 32 + lane) * 4 + (jj & 3);
+            _Float16 h, l;
+            split_hl(s, h, l);
+            sh[at] = h;
+            sl[at] = l;
+        }
+    }
+}
+
 // ---------------------------------------------------------------- row-dot
 
 struct MmSegDev {
@@ -999,6 +1112,39 @@ hipError_t launch_mm_prep(hipStream_t st, const float* x, int64_t ldx, const flo
     return hipGetLastError();
 }
 
+hipError_t launch_mm_prep_fold(hipStream_t st, float* x, int64_t ldx, const float* normw,
+                               float eps, int64_t M, const MmAct& act, int weight_dt,
+                               const MmPend& fold) {
+    if (fold.S < 1) return launch_mm_prep(st, x, ldx, normw, eps, M, act, weight_dt);
+    if (act.K % 256 || act.K > 4096 * MMF_CH || M < 1 || M > act.Mp || act.Mp % MM_TOK ||
+        ldx % 4 || ((uintptr_t)x & 15) || fold.N != act.K || fold.ldp % 4 || fold.split_stride % 4)
+        return hipErrorInvalidValue;
+    hipLaunchKernelGGL(k_mm_prep_fold, dim3((unsigned)act.Mp), dim3(1024), 0, st, x, ldx, normw,
+                       eps, act.K, (int)M, weight_dt == FTX_Q4_0_MMT ? 1 : 0, fold.part,
+                       fold.split_stride, fold.ldp, fold.S, act.xh, act.xl, act.sh, act.sl);
+    return hipGetLastError();
+}
+
+hipError_t launch_mm_fold(hipStream_t st, const MmPend& fold, int64_t M, float* y, int64_t ldy) {
+    if (fold.S < 1) return hipSuccess;
+    MmReduceArgs r{};
+    r.part = fold.part;
+    r.split_stride = fold.split_stride;
+    r.ldp = fold.ldp;
+    r.S = fold.S;
+    r.swiglu = 0;
+    r.N = fold.N;
+    r.out.nseq = 1;
+    r.out.base[0] = y;
+    r.out.row0[0] = 0;
+    r.out.row0[1] = M;
+    r.out.ld = ldy;
+    r.out.accum = 1;
+    hipLaunchKernelGGL(k_mm_reduce, dim3((unsigned)((fold.N + 255) / 256), (unsigned)M), dim3(256),
+                       0, st, r);
+    return hipGetLastError();
+}
+
 bool mm_supported(int dt, int64_t K) {
     return (dt == FTX_Q4_K || dt == FTX_Q8_0_MMT || dt == FTX_Q4_0_MMT || dt == FTX_Q6_K_MMT) &&
            K % 256 == 0 && K >= 256;
@@ -1069,7 +1215,8 @@ static hipError_t mm_launch(hipStream_t st, const MmSeg* segs, int nseg, const M
                             int64_t M, int epi, const MmOut& out, float* part,
                             size_t part_floats, int cu_count, const int32_t* xtab,
                             const int64_t* plane, int64_t ntile_max, int64_t trows,
-                            const MmFragOut* fo) {
+                            const MmFragOut* fo, MmPend* pend) {
+    if (pend) *pend = MmPend{};
     if (nseg < 1 || nseg > 3 || M < 1 || M > act.Mp || out.nseq < 1 || out.nseq > FTX_MAX_SEQ)
         return hipErrorInvalidValue;
     if (xtab && (ntile_max < 1 || (trows != 16 && trows != 64) || ntile_max * trows > act.Mp ||
@@ -1153,6 +1300,15 @@ static hipError_t mm_launch(hipStream_t st, const MmSeg* segs, int nseg, const M
     ktimed_launch(kern, grid, dim3(64 * MM_WAVES), (uint32_t)lds, st, a);
     hipError_t e = hipGetLastError();
     if (e != hipSuccess || !via_part) return e;
+    if (pend && epi == EPI_ACCUM && !xtab && out.nseq == 1 && !fo) {
+        // left for the next activation prep to add into out
+        pend->part = part;
+        pend->split_stride = act.Mp * cols;
+        pend->ldp = cols;
+        pend->S = S;
+        pend->N = cols;
+        return hipSuccess;
+    }
     MmReduceArgs r{};
     r.part = part;
     r.split_stride = act.Mp * cols;
@@ -1176,9 +1332,10 @@ static hipError_t mm_launch(hipStream_t st, const MmSeg* segs, int nseg, const M
 }
 
 hipError_t launch_mm(hipStream_t st, const MmSeg* segs, int nseg, const MmAct& act, int64_t M,
-                     int epi, const MmOut& out, float* part, size_t part_floats, int cu_count) {
+                     int epi, const MmOut& out, float* part, size_t part_floats, int cu_count,
+                     MmPend* pend) {
     return mm_launch(st, segs, nseg, act, M, epi, out, part, part_floats, cu_count, nullptr,
-                     nullptr, 0, 0, nullptr);
+                     nullptr, 0, 0, nullptr, pend);
 }
 
 hipError_t launch_mm_experts(hipStream_t st, const MmSeg* segs, int nseg, const int64_t* plane,
@@ -1190,12 +1347,13 @@ hipError_t launch_mm_experts(hipStream_t st, const MmSeg* segs, int nseg, const 
     o.nseq = 1;
     o.row0[1] = ntile_max * trows;
     return mm_launch(st, segs, nseg, act, ntile_max * trows, EPI_SWIGLU, o, part, part_floats,
-                     cu_count, xtab, plane, ntile_max, trows, &fo);
+                     cu_count, xtab, plane, ntile_max, trows, &fo, nullptr);
 }
 
 hipError_t launch_mm_down(hipStream_t st, const uint8_t* tiled, int64_t n_in, int64_t N,
                           const float* h, int64_t ldh, int64_t M, const MmOut& out, float* part,
-                          size_t part_floats, int cu_count) {
+                          size_t part_floats, int cu_count, MmPend* pend) {
+    if (pend) *pend = MmPend{};
     const int64_t Mp = mm_pad_tokens(M);
     if (!mm_down_supported(FTX_Q4_K, n_in, N) || M < 1 || out.nseq < 1 || out.nseq > FTX_MAX_SEQ ||
         ldh % 4 || ((uintptr_t)h & 15))
@@ -1230,6 +1388,15 @@ hipError_t launch_mm_down(hipStream_t st, const uint8_t* tiled, int64_t n_in, in
                        0, st, a);
     hipError_t e = hipGetLastError();
     if (e != hipSuccess || S == 1) return e;
+    if (pend && out.accum && out.nseq == 1) {
+        // left for the next activation prep to add into out
+        pend->part = part;
+        pend->split_stride = Mp * N;
+        pend->ldp = N;
+        pend->S = S;
+        pend->N = N;
+        return hipSuccess;
+    }
     MmReduceArgs r{};
     r.part = part;
     r.split_stride = Mp * N;

@@ -263,23 +263,50 @@ static int verify_large(ftx_ctx* ctx, ftx_model* m, const ftx_seq_args* sq, int6
         o.accum = accum;
         return o;
     };
+    // the split partials of the last o / ffn_down GEMM not yet added into x
+    // (they stay in mm_part): the next activation prep over x adds them as it
+    // reads x; any other reader of x first adds them by a reduce launch
+    MmPend xpend{};
+    auto flush_x = [&]() -> int {
+        if (xpend.S > 0)
+            TRACED_L(TK_XQ_PREP, (xpend.S + 2.0) * Md * D * f4, launch_mm_fold(st, xpend, Mt, m->x, D));
+        xpend = MmPend{};
+        return FTX_OK;
+    };
     // one projection of rows [r0, r0 + Mr) of xin: [RMSNorm ->] segments ->
-    // out (k_mm) or gs (generic kernels, whose outputs are the segments' y)
+    // out (k_mm) or gs (generic kernels, whose outputs are the segments' y);
+    // pend: an accumulating k_mm GEMM may leave its partials there
     auto project = [&](int kind, double bytes, const float* xin, int64_t ldx, const float* normw,
                        const size_t* idx, const ftx_tensor* const* ts, GemvSeg* gs, int nseg,
-                       int64_t K, int epi, const MmOut& out, int64_t Mr) -> int {
+                       int64_t K, int epi, const MmOut& out, int64_t Mr,
+                       MmPend* pend = nullptr) -> int {
         MmSeg sg[3];
         bool all = true;
         for (int i = 0; i < nseg; ++i) all = all && mm_seg(idx[i], ts[i], sg[i]);
         for (int i = 1; all && i < nseg; ++i) all = sg[i].dt == sg[0].dt;
         if (all) {
             const MmAct act = mm_act(m->mm_act, mm_pad_tokens(Mr), K);
-            TRACED_L(TK_XQ_PREP, Mr * K * f4 + 4.0 * mm_pad_tokens(Mr) * K,
-                     launch_mm_prep(st, xin, ldx, normw, eps, Mr, act, sg[0].dt));
+            if (xpend.S > 0 && xin == m->x && Mr == Mt && ldx == D) {
+                TRACED_L(TK_XQ_PREP, (xpend.S + 2.0) * Mr * K * f4 + 4.0 * mm_pad_tokens(Mr) * K,
+                         launch_mm_prep_fold(st, m->x, ldx, normw, eps, Mr, act, sg[0].dt, xpend));
+                xpend = MmPend{};
+            } else {
+                if (xin >= m->x && xin < m->x + Mt * D) {
+                    const int fr = flush_x();
+                    if (fr) return fr;
+                }
+                TRACED_L(TK_XQ_PREP, Mr * K * f4 + 4.0 * mm_pad_tokens(Mr) * K,
+                         launch_mm_prep(st, xin, ldx, normw, eps, Mr, act, sg[0].dt));
+            }
             TRACED_L(kind, bytes,
                      launch_mm(st, sg, nseg, act, Mr, epi, out, m->mm_part, m->mm_part_n,
-                               ctx->cu_count));
+                               ctx->cu_count, pend));
             return FTX_OK;
+        }
+        // the other kernels read x as it is
+        if (xin >= m->x && xin < m->x + Mt * D) {
+            const int fr = flush_x();
+            if (fr) return fr;
         }
         // tiled K-quants the one-pass kernels do not take (Q6_K): the
         // row-dot MFMA kernel on 8-row chunks (one activation prep for all)
@@ -504,16 +531,17 @@ static int verify_large(ftx_ctx* ctx, ftx_model* m, const ftx_seq_args* sq, int6
                 TRACED_L(TK_ATTENTION, attn_b, launch_attention(st, aa, M));
             }
         }
-        // o, added into x
+        const ftx_tensor* const* X = m->ext.data() + l * FTX_LAYER_EXT;
+        // o, added into x (a dense FFN's prep adds its partials)
         {
             const size_t idx[1] = {(size_t)(lt + FTX_T_O)};
             GemvSeg gs[1] = {seg(T[FTX_T_O], m->x, D)};
+            if (const int fr = flush_x()) return fr;
             rc = project(TK_GEMV_O, wbytes(T[FTX_T_O]) + Md * m->qdim * f4 + 2 * Md * D * f4, m->att,
                          m->qdim, nullptr, idx, &T[FTX_T_O], gs, 1, m->qdim, EPI_ACCUM,
-                         out1(m->x, D, 1), Mt);
+                         out1(m->x, D, 1), Mt, X[FTX_X_GATE_INP] ? nullptr : &xpend);
             if (rc) return rc;
         }
-        const ftx_tensor* const* X = m->ext.data() + l * FTX_LAYER_EXT;
         if (X[FTX_X_GATE_INP]) {
             rc = moe_layer(l, X);
             if (rc) return rc;
@@ -533,10 +561,12 @@ static int verify_large(ftx_ctx* ctx, ftx_model* m, const ftx_seq_args* sq, int6
         // ffn_down, added into x
         const ftx_tensor* dn = T[FTX_T_DOWN];
         const double down_b = wbytes(dn) + Md * F * f4 + 2 * Md * D * f4;
+        if (const int fr = flush_x()) return fr;
         if (m->down_tiled[l] && mm_down_supported(dn->dtype, F, D)) {
+            // added into x by the next prep
             TRACED_L(TK_DOWN, down_b,
                      launch_mm_down(st, m->down_tiled[l], F, D, m->h, F, Mt, out1(m->x, D, 1),
-                                    m->mm_part, m->mm_part_n, ctx->cu_count));
+                                    m->mm_part, m->mm_part_n, ctx->cu_count, &xpend));
         } else if (m->down_tiled[l] && down_mfma_supported(dn->dtype, F, D, 8)) {
             // the MFMA down kernel on 8-row chunks, every chunk's split
             // partials added into x by one reduce
@@ -559,7 +589,11 @@ static int verify_large(ftx_ctx* ctx, ftx_model* m, const ftx_seq_args* sq, int6
                                  D, m->part));
         }
     }
-    // the LM head, each sequence's rows into its own logits
+    // the LM head, each sequence's rows into its own logits (without one,
+    // x is left complete)
+    if (!sq[0].logits) {
+        if (const int fr = flush_x()) return fr;
+    }
     if (sq[0].logits) {
         const ftx_tensor* lm = d.output ? d.output : d.tok_embd;
         const size_t idx[1] = {(size_t)(d.n_layer * FTX_LAYER_TENSORS)};
@@ -579,6 +613,7 @@ static int verify_large(ftx_ctx* ctx, ftx_model* m, const ftx_seq_args* sq, int6
             if (rc) return rc;
         } else {
             // the generic head per sequence (its weights are read once each)
+            if (const int fr = flush_x()) return fr;
             for (int64_t s = 0; s < nseq; ++s) {
                 const int64_t M = sq[s].M;
                 GemvSeg gs[1] = {seg(lm, sq[s].logits, V)};
