@@ -426,6 +426,15 @@ struct AttnArgs {
 hipError_t launch_attention(hipStream_t st, const AttnArgs& a, int64_t M);
 
 // MFMA attention (k_attn.hip): fp16 KV, hd 64 or 128
+// the one-pass GEMM's activation operand (fp16 hi / lo planes and
+// 32-element sums in fragment order, as k_mm_prep writes them) as the
+// destination of a producer: token row m of the producer is operand row
+// row0 + m; contraction K; inter for Q4_0 weights
+struct MmFragDst {
+    _Float16 *xh = nullptr, *xl = nullptr, *sh = nullptr, *sl = nullptr;
+    int64_t row0 = 0, K = 0;
+    int inter = 0;
+};
 struct AttnMArgs {
     const float* qkv;
     int64_t ldq;
@@ -441,6 +450,7 @@ struct AttnMArgs {
     float* out;          // [M][n_head*hd]
     float *pmax, *psum, *pout;  // chunk partials
     int nc = 1;          // chunks per workgroup (and per partial)
+    MmFragDst frag;      // frag.xh set: the fp32 combine writes this operand instead of out
 };
 bool attn_mfma_supported(int64_t hd, int kv_f16, int64_t M, int64_t n_head, int64_t n_kv);
 size_t attn_part_floats(int64_t M, int64_t n_head, int64_t hd, int64_t cap_alloc);

@@ -20,6 +20,7 @@
 // [dim][slot]) so its B operand is one 8-byte load.  The chunk partial (max,
 // sum, O) goes straight from the MFMA registers to memory.
 #include "ftx_internal.h"
+#include "mm_dev.h"
 #include "xq_dev.h"
 
 namespace {
@@ -727,11 +728,32 @@ __device__ __forceinline__ void attn_combine_row(const AttnMArgs& a, int64_t qi,
         __syncthreads();
     }
     den = red[0];
-    if (d < a.hd) {
+    if (d < a.hd) {  // whole waves (hd = 64 or 128)
         float num = 0.f;
 #pragma unroll 8
         for (int c = 0; c < nvalid; ++c) num += wsh[c] * a.pout[(qi * nch + c) * a.hd + d];
-        a.out[qi * a.hd + d] = num / den;
+        const float v = num / den;
+        if (!a.frag.xh) {
+            a.out[qi * a.hd + d] = v;
+            return;
+        }
+        // the o projection's operand (k_mm_prep without a norm): element k
+        // = h hd + d of operand row row0 + m, and the 32-element sums
+        const int64_t R = a.frag.row0 + qi / a.n_head, k = (qi % a.n_head) * a.hd + d;
+        _Float16 h, l;
+        split_hl(v, h, l);
+        const int64_t at = frag_at(R, k, a.frag.K, a.frag.inter != 0);
+        a.frag.xh[at] = h;
+        a.frag.xl[at] = l;
+        float s = v;
+#pragma unroll
+        for (int o = 1; o < 32; o <<= 1) s += __shfl_xor(s, o, 64);
+        if ((d & 31) == 0) {
+            split_hl(s, h, l);
+            const int64_t sa = frag_sum_at(R, k / 32, a.frag.K);
+            a.frag.sh[sa] = h;
+            a.frag.sl[sa] = l;
+        }
     }
 }
 

@@ -66,14 +66,8 @@ constexpr float MMD_ASCALE = 1024.f;
 // same; the 32-element sums of the token rows, for the Q4_K min term, as
 // fragments of the 16x16x16 operand: [Mp / 16][K / 256][32 lanes][4] with
 // lane l holding sub-blocks 4 (l / 16) .. + 3 of the super-block for token
-// 16 mt + l % 16 (hi and lo planes).
-__device__ __forceinline__ int64_t frag_at(int64_t m, int64_t k, int64_t K, bool inter) {
-    const int64_t mt = m >> 4, ks = k >> 5;
-    const int lane = (int)(m & 15) + 16 * (int)((k & 31) >> 3);
-    int e = (int)(k & 7);
-    if (inter) e = (e & 1) ? 4 + (e >> 1) : (e >> 1);
-    return ((mt * (K / 32) + ks) * 64 + lane) * 8 + e;
-}
+// 16 mt + l % 16 (hi and lo planes).  frag_at and frag_sum_at (mm_dev.h)
+// give the slots.
 
 // Workgroup (token row m < Mp, 1024-element slice): rows m >= M are zeros.
 // v = (x * inv) * w with inv = 1 / sqrt(sum x^2 / K + eps) when normw is

@@ -45,6 +45,26 @@ __device__ __forceinline__ v8h i8x8(v2i w) {
     return v8h{h0[0], h0[1], h1[0], h1[1], h2[0], h2[1], h3[0], h3[1]};
 }
 
+// slot of element (token m, contraction k) in the one-pass GEMM's fragment-
+// order operand planes ([Mp / 16][K / 32][64 lanes][8]; inter: each octet
+// as its even then its odd elements, for Q4_0 weights)
+__device__ __forceinline__ int64_t frag_at(int64_t m, int64_t k, int64_t K, bool inter) {
+    const int64_t mt = m >> 4, ks = k >> 5;
+    const int lane = (int)(m & 15) + 16 * (int)((k & 31) >> 3);
+    int e = (int)(k & 7);
+    if (inter) e = (e & 1) ? 4 + (e >> 1) : (e >> 1);
+    return ((mt * (K / 32) + ks) * 64 + lane) * 8 + e;
+}
+
+// slot of the 32-element sum j of token m (the Q4_K min term's operand,
+// [Mp / 16][K / 256][32 lanes][4])
+__device__ __forceinline__ int64_t frag_sum_at(int64_t m, int64_t j, int64_t K) {
+    const int64_t sb = j / 8;
+    const int jj = (int)(j % 8);
+    const int lane = (int)(m & 15) + 16 * (jj >> 2);
+    return (((m >> 4) * (K / 256) + sb) * 32 + lane) * 4 + (jj & 3);
+}
+
 __device__ __forceinline__ void split_hl(float v, _Float16& h, _Float16& l) {
 #pragma clang fp contract(off)
     h = (_Float16)v;

@@ -279,14 +279,16 @@ static int verify_large(ftx_ctx* ctx, ftx_model* m, const ftx_seq_args* sq, int6
     auto project = [&](int kind, double bytes, const float* xin, int64_t ldx, const float* normw,
                        const size_t* idx, const ftx_tensor* const* ts, GemvSeg* gs, int nseg,
                        int64_t K, int epi, const MmOut& out, int64_t Mr,
-                       MmPend* pend = nullptr) -> int {
+                       MmPend* pend = nullptr, bool act_ready = false) -> int {
         MmSeg sg[3];
         bool all = true;
         for (int i = 0; i < nseg; ++i) all = all && mm_seg(idx[i], ts[i], sg[i]);
         for (int i = 1; all && i < nseg; ++i) all = sg[i].dt == sg[0].dt;
         if (all) {
             const MmAct act = mm_act(m->mm_act, mm_pad_tokens(Mr), K);
-            if (xpend.S > 0 && xin == m->x && Mr == Mt && ldx == D) {
+            if (act_ready) {
+                // the producer wrote the operand
+            } else if (xpend.S > 0 && xin == m->x && Mr == Mt && ldx == D) {
                 TRACED_L(TK_XQ_PREP, (xpend.S + 2.0) * Mr * K * f4 + 4.0 * mm_pad_tokens(Mr) * K,
                          launch_mm_prep_fold(st, m->x, ldx, normw, eps, Mr, act, sg[0].dt, xpend));
                 xpend = MmPend{};
@@ -437,6 +439,21 @@ static int verify_large(ftx_ctx* ctx, ftx_model* m, const ftx_seq_args* sq, int6
         bool all_mattn = nseq > 1;
         for (int64_t s = 0; s < nseq && all_mattn; ++s)
             all_mattn = attn_mfma_supported(hd, sq[s].kv->kv_f16, sq[s].M, d.n_head, d.n_head_kv);
+        // the attention combine writes the o projection's one-pass GEMM
+        // operand when every sequence takes the MFMA attention (its prep is
+        // then skipped)
+        MmFragDst ofd{};
+        {
+            MmSeg oseg;
+            bool of = mm_seg((size_t)(lt + FTX_T_O), T[FTX_T_O], oseg);
+            for (int64_t s = 0; s < nseq && of; ++s)
+                of = attn_mfma_supported(hd, sq[s].kv->kv_f16, sq[s].M, d.n_head, d.n_head_kv);
+            if (of) {
+                const MmAct oact = mm_act(m->mm_act, mm_pad_tokens(Mt), m->qdim);
+                ofd = MmFragDst{oact.xh, oact.xl, oact.sh, oact.sl, 0, m->qdim,
+                                oseg.dt == FTX_Q4_0_MMT ? 1 : 0};
+            }
+        }
         if (all_mattn) {
             RopeArgs ras[FTX_MAX_SEQ];
             AttnMArgs ams[FTX_MAX_SEQ];
@@ -476,6 +493,8 @@ static int verify_large(ftx_ctx* ctx, ftx_model* m, const ftx_seq_args* sq, int6
                 am.n_kv = (int)d.n_head_kv;
                 am.hd = (int)hd;
                 am.out = m->att + r0 * m->qdim;
+                am.frag = ofd;
+                am.frag.row0 = r0;
                 ams[s] = am;
                 parts[s] = kv->attn_part;
                 rope_b += 2.0 * M * m->ldq * f4 + 2.0 * M * m->kdim * (double)kvel;
@@ -523,6 +542,8 @@ static int verify_large(ftx_ctx* ctx, ftx_model* m, const ftx_seq_args* sq, int6
                 am.n_kv = (int)d.n_head_kv;
                 am.hd = (int)hd;
                 am.out = m->att + r0 * m->qdim;
+                am.frag = ofd;
+                am.frag.row0 = r0;
                 TRACED_L(TK_ATTENTION, attn_b, launch_attn_mfma(st, am, kv->attn_part, nullptr));
             } else {
                 AttnArgs aa{m->qkv + r0 * m->ldq, m->ldq, kl, vl, kv->kv_f16, d_np + s,
@@ -539,7 +560,8 @@ static int verify_large(ftx_ctx* ctx, ftx_model* m, const ftx_seq_args* sq, int6
             if (const int fr = flush_x()) return fr;
             rc = project(TK_GEMV_O, wbytes(T[FTX_T_O]) + Md * m->qdim * f4 + 2 * Md * D * f4, m->att,
                          m->qdim, nullptr, idx, &T[FTX_T_O], gs, 1, m->qdim, EPI_ACCUM,
-                         out1(m->x, D, 1), Mt, X[FTX_X_GATE_INP] ? nullptr : &xpend);
+                         out1(m->x, D, 1), Mt, X[FTX_X_GATE_INP] ? nullptr : &xpend,
+                         ofd.xh != nullptr);
             if (rc) return rc;
         }
         if (X[FTX_X_GATE_INP]) {
