@@ -258,6 +258,7 @@ struct MmPend {
     const float* part = nullptr;
     int64_t split_stride = 0, ldp = 0, N = 0;
     int S = 0;
+    int accum = 0;  // out += the sum (else out = the sum)
 };
 // the partials `fold` added into x (rows < M, written back), then the prep
 // of launch_mm_prep without a gather (fold.S = 0: the plain prep)
@@ -280,9 +281,10 @@ bool mm_down_supported(int dt, int64_t n_in, int64_t N);
 size_t mm_part_floats(int64_t Mp, int64_t N, int64_t steps, int64_t ntiles, int cu_count);
 size_t mm_down_part_floats(int64_t Mp, int64_t n_in, int64_t N, int cu_count);
 // epi: EPI_STORE / EPI_ACCUM (out.accum) or EPI_SWIGLU (segments gate, up)
-// pend (EPI_ACCUM into one output, split over the contraction): the
-// partials are left in `part` for the caller to fold (launch_mm_prep_fold /
-// launch_mm_fold) instead of reduced here
+// pend (EPI_STORE / EPI_ACCUM into one output, split over the
+// contraction): the partials are left in `part` for the caller to fold
+// (launch_mm_prep_fold, launch_mm_fold, or RoPE's partial rows) instead of
+// reduced here
 hipError_t launch_mm(hipStream_t st, const MmSeg* segs, int nseg, const MmAct& act, int64_t M,
                      int epi, const MmOut& out, float* part, size_t part_floats, int cu_count,
                      MmPend* pend = nullptr);
@@ -400,6 +402,11 @@ struct RopeArgs {
     const float* qnorm = nullptr;
     const float* knorm = nullptr;
     float eps = 0.f;
+    // optional: the q | k | v row m is first formed from the split partials
+    // of its GEMM, sum_s part[s * split_stride + m * ldp + col] in split order
+    const float* part = nullptr;
+    int64_t split_stride = 0, ldp = 0;
+    int S = 0;
 };
 hipError_t launch_rope_kv(hipStream_t st, const RopeArgs& a, int64_t M);
 // several sequences in one launch: sequence s's rows are M[s] tokens

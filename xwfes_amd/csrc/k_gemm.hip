@@ -1110,7 +1110,7 @@ hipError_t launch_mm_prep_fold(hipStream_t st, float* x, int64_t ldx, const floa
                                float eps, int64_t M, const MmAct& act, int weight_dt,
                                const MmPend& fold) {
     if (fold.S < 1) return launch_mm_prep(st, x, ldx, normw, eps, M, act, weight_dt);
-    if (act.K % 256 || act.K > 4096 * MMF_CH || M < 1 || M > act.Mp || act.Mp % MM_TOK ||
+    if (!fold.accum || act.K % 256 || act.K > 4096 * MMF_CH || M < 1 || M > act.Mp || act.Mp % MM_TOK ||
         ldx % 4 || ((uintptr_t)x & 15) || fold.N != act.K || fold.ldp % 4 || fold.split_stride % 4)
         return hipErrorInvalidValue;
     hipLaunchKernelGGL(k_mm_prep_fold, dim3((unsigned)act.Mp), dim3(1024), 0, st, x, ldx, normw,
@@ -1133,7 +1133,7 @@ hipError_t launch_mm_fold(hipStream_t st, const MmPend& fold, int64_t M, float* 
     r.out.row0[0] = 0;
     r.out.row0[1] = M;
     r.out.ld = ldy;
-    r.out.accum = 1;
+    r.out.accum = fold.accum;
     hipLaunchKernelGGL(k_mm_reduce, dim3((unsigned)((fold.N + 255) / 256), (unsigned)M), dim3(256),
                        0, st, r);
     return hipGetLastError();
@@ -1294,13 +1294,14 @@ static hipError_t mm_launch(hipStream_t st, const MmSeg* segs, int nseg, const M
     ktimed_launch(kern, grid, dim3(64 * MM_WAVES), (uint32_t)lds, st, a);
     hipError_t e = hipGetLastError();
     if (e != hipSuccess || !via_part) return e;
-    if (pend && epi == EPI_ACCUM && !xtab && out.nseq == 1 && !fo) {
-        // left for the next activation prep to add into out
+    if (pend && epi != EPI_SWIGLU && !xtab && out.nseq == 1 && !fo) {
+        // left for the consumer to add into (or store as) out
         pend->part = part;
         pend->split_stride = act.Mp * cols;
         pend->ldp = cols;
         pend->S = S;
         pend->N = cols;
+        pend->accum = out.accum;
         return hipSuccess;
     }
     MmReduceArgs r{};
@@ -1389,6 +1390,7 @@ hipError_t launch_mm_down(hipStream_t st, const uint8_t* tiled, int64_t n_in, in
         pend->ldp = N;
         pend->S = S;
         pend->N = N;
+        pend->accum = 1;
         return hipSuccess;
     }
     MmReduceArgs r{};

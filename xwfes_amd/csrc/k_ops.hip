@@ -80,6 +80,27 @@ __device__ __forceinline__ void rope_kv_row(const RopeArgs& a, int64_t m, int64_
     const int64_t off = is_q ? h * a.hd : qdim + (h - a.n_head) * a.hd;
     v = row + off;
     const float* nw = is_q ? a.qnorm : a.knorm;
+    if (a.part) {
+        // the head's q (or k and v) elements from the GEMM's split partials
+        // (eight splits' loads in flight at a time)
+        const float* p = a.part + m * a.ldp;
+        auto sum = [&](int64_t col) {
+            float g = 0.f;
+            for (int s0 = 0; s0 < a.S; s0 += 8) {
+                float pv[8];
+#pragma unroll
+                for (int i = 0; i < 8; ++i) pv[i] = s0 + i < a.S ? p[(s0 + i) * a.split_stride + col] : 0.f;
+#pragma unroll
+                for (int i = 0; i < 8; ++i) g += pv[i];
+            }
+            return g;
+        };
+        for (int64_t t = threadIdx.x; t < a.hd; t += blockDim.x) {
+            v[t] = sum(off + t);
+            if (!is_q) row[off + kdim + t] = sum(off + kdim + t);
+        }
+        __syncthreads();
+    }
     if (a.bias || nw) {
         float ss = 0.f;
         for (int64_t t = threadIdx.x; t < a.hd; t += blockDim.x) {

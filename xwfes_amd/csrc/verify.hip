@@ -418,7 +418,9 @@ static int verify_large(ftx_ctx* ctx, ftx_model* m, const ftx_seq_args* sq, int6
     for (int64_t l = 0; l < d.n_layer; ++l) {
         const int64_t lt = l * FTX_LAYER_TENSORS;
         const ftx_tensor* const* T = m->layers.data() + lt;
-        // q / k / v into qkv [Mt][ldq]
+        // q / k / v into qkv [Mt][ldq] (its split partials, if any, summed
+        // by RoPE)
+        MmPend qpend{};
         {
             const ftx_tensor* ts[3] = {T[FTX_T_Q], T[FTX_T_K], T[FTX_T_V]};
             const size_t idx[3] = {(size_t)(lt + FTX_T_Q), (size_t)(lt + FTX_T_K),
@@ -430,7 +432,7 @@ static int verify_large(ftx_ctx* ctx, ftx_model* m, const ftx_seq_args* sq, int6
                          wbytes(ts[0]) + wbytes(ts[1]) + wbytes(ts[2]) + Md * D * f4 +
                              Md * m->ldq * f4,
                          m->x, D, m->norms + (l * 2) * D, idx, ts, gs, 3, D, EPI_STORE,
-                         out1(m->qkv, m->ldq, 0), Mt);
+                         out1(m->qkv, m->ldq, 0), Mt, &qpend);
             if (rc) return rc;
         }
         // RoPE, the KV write and attention: one launch each over all
@@ -475,6 +477,12 @@ static int verify_large(ftx_ctx* ctx, ftx_model* m, const ftx_seq_args* sq, int6
                 ra.eps = eps;
                 ra.qh16 = qh + r0 * m->qdim;
                 ra.ql16 = ql + r0 * m->qdim;
+                if (qpend.S > 0) {
+                    ra.part = qpend.part + r0 * qpend.ldp;
+                    ra.split_stride = qpend.split_stride;
+                    ra.ldp = qpend.ldp;
+                    ra.S = qpend.S;
+                }
                 ras[s] = ra;
                 Ms[s] = M;
                 AttnMArgs am{};
@@ -517,6 +525,12 @@ static int verify_large(ftx_ctx* ctx, ftx_model* m, const ftx_seq_args* sq, int6
             ra.qnorm = m->qnorm[l];
             ra.knorm = m->knorm[l];
             ra.eps = eps;
+            if (qpend.S > 0) {
+                ra.part = qpend.part + r0 * qpend.ldp;
+                ra.split_stride = qpend.split_stride;
+                ra.ldp = qpend.ldp;
+                ra.S = qpend.S;
+            }
             if (mattn) {
                 ra.qh16 = qh + r0 * m->qdim;
                 ra.ql16 = ql + r0 * m->qdim;
