@@ -407,6 +407,10 @@ struct RopeArgs {
     const float* part = nullptr;
     int64_t split_stride = 0, ldp = 0;
     int S = 0;
+    // optional: the angles' cos / sin per row and pair, [M][hd / 2][2]
+    // (computed on the host in double as rope_vec does), instead of forming
+    // them on the device
+    const float* cs = nullptr;
 };
 hipError_t launch_rope_kv(hipStream_t st, const RopeArgs& a, int64_t M);
 // several sequences in one launch: sequence s's rows are M[s] tokens

@@ -698,40 +698,53 @@ __global__ void __launch_bounds__(64 * NWV) k_attn_mfma_batch(AttnMBatch b) {
 // one block per query row; the chunk weights are formed once in LDS so the
 // output loop is a stream of independent loads
 __device__ __forceinline__ void attn_combine_row(const AttnMArgs& a, int64_t qi, int nch) {
-    __shared__ float wsh[1024];  // chunk weights (nch <= 1024)
-    __shared__ float red[128];
-    const int d = threadIdx.x;
+    // Every load of the common case is issued at entry, branch-free (indices
+    // clamped): the first CPF partials of this thread's dim and the statistics
+    // of partial `lane`.  Each wave then forms the weights, their maximum and
+    // the denominator itself (shuffles, no workgroup barrier); weights of the
+    // first CPF partials come from their lanes by shuffle, later ones (more
+    // than CPF partials) through the wave's own LDS copy.
+    constexpr int CPF = 8;
+    __shared__ float wsh[2][1024];  // chunk weights (nch <= 1024) per wave
+    const int d = threadIdx.x, wv = d >> 6, lane = d & 63;
     const int64_t npast = a.npast;
     const int ch = chunk_slots(a.hd) * a.nc;  // slots per partial
     const int nvalid = (int)((npast + a.M + ch - 1) / ch);
-    float M = -INFINITY;
-    for (int c = d; c < nvalid; c += 128) M = fmaxf(M, a.pmax[qi * nch + c]);
-    red[d] = M;
-    __syncthreads();
-    for (int o = 64; o > 0; o >>= 1) {
-        if (d < o) red[d] = fmaxf(red[d], red[d + o]);
-        __syncthreads();
-    }
-    M = red[0];
-    __syncthreads();
-    float den = 0.f;
-    for (int c = d; c < nvalid; c += 128) {
-        const float mc = a.pmax[qi * nch + c];
+    const float* pm = a.pmax + qi * nch;
+    const float* pz = a.psum + qi * nch;
+    const float* po = a.pout + qi * nch * a.hd + min(d, a.hd - 1);
+    float pv[CPF];
+#pragma unroll
+    for (int i = 0; i < CPF; ++i) pv[i] = po[(int64_t)min(i, nvalid - 1) * a.hd];
+    const int cl = min(lane, nvalid - 1);
+    const float m0 = pm[cl], z0 = pz[cl];
+    float M = lane < nvalid ? m0 : -INFINITY;
+    for (int c = lane + 64; c < nvalid; c += 64) M = fmaxf(M, pm[c]);
+#pragma unroll
+    for (int o = 32; o > 0; o >>= 1) M = fmaxf(M, __shfl_xor(M, o, 64));
+    const float w0 = lane < nvalid && m0 != -INFINITY ? expf(m0 - M) : 0.f;
+    float den = w0 * z0;
+    for (int c = lane + 64; c < nvalid; c += 64) {
+        const float mc = pm[c];
         const float w = mc == -INFINITY ? 0.f : expf(mc - M);
-        wsh[c] = w;
-        den += w * a.psum[qi * nch + c];
+        wsh[wv][c] = w;
+        den += w * pz[c];
     }
-    red[d] = den;
-    __syncthreads();
-    for (int o = 64; o > 0; o >>= 1) {
-        if (d < o) red[d] += red[d + o];
-        __syncthreads();
+    if (nvalid > CPF) wsh[wv][lane] = w0;  // wave-uniform
+#pragma unroll
+    for (int o = 32; o > 0; o >>= 1) den += __shfl_xor(den, o, 64);
+    // the weights written by the wave's other lanes (LDS in program order
+    // within a wave; the fence keeps the compiler's order too)
+    __builtin_amdgcn_fence(__ATOMIC_ACQ_REL, "wavefront");
+    const float* wl = wsh[wv];
+    float num = 0.f;
+#pragma unroll
+    for (int i = 0; i < CPF; ++i) {
+        const float wi = __shfl(w0, i, 64);
+        if (i < nvalid) num += wi * pv[i];
     }
-    den = red[0];
+    for (int c = CPF; c < nvalid; ++c) num += wl[c] * po[(int64_t)c * a.hd];
     if (d < a.hd) {  // whole waves (hd = 64 or 128)
-        float num = 0.f;
-#pragma unroll 8
-        for (int c = 0; c < nvalid; ++c) num += wsh[c] * a.pout[(qi * nch + c) * a.hd + d];
         const float v = num / den;
         if (!a.frag.xh) {
             a.out[qi * a.hd + d] = v;

@@ -121,9 +121,16 @@ __device__ __forceinline__ void rope_kv_row(const RopeArgs& a, int64_t m, int64_
         __syncthreads();  // RoPE pairs cross the threads' elements
     }
     for (int64_t i = threadIdx.x; i < half; i += blockDim.x) {
-        const double f = pow(a.theta, -2.0 * (double)i / (double)a.hd);
-        const double ang = (double)pos * f;
-        const float c = (float)cos(ang), s = (float)sin(ang);
+        float c, s;
+        if (a.cs) {
+            c = a.cs[(m * half + i) * 2];
+            s = a.cs[(m * half + i) * 2 + 1];
+        } else {
+            const double f = pow(a.theta, -2.0 * (double)i / (double)a.hd);
+            const double ang = (double)pos * f;
+            c = (float)cos(ang);
+            s = (float)sin(ang);
+        }
         const int64_t ia = a.neox ? i : 2 * i, ib = a.neox ? i + half : 2 * i + 1;
         const float x0 = v[ia], x1 = v[ib];
         const float y0 = x0 * c - x1 * s, y1 = x0 * s + x1 * c;

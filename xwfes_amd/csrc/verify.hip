@@ -224,7 +224,6 @@ static int verify_large(ftx_ctx* ctx, ftx_model* m, const ftx_seq_args* sq, int6
     uint32_t* d_anc = (uint32_t*)(m->args + AL.anc);
     int64_t* d_np = (int64_t*)(m->args + AL.np);
     float* d_cs = (float*)(m->args + AL.cs);
-    (void)d_cs;
     FTX_HIP(ctx, hipMemcpyAsync(m->args, pin, AL.bytes, hipMemcpyHostToDevice, st));
     FTX_HIP(ctx, hipEventRecord(m->pin_ev[slot], st));
     m->pin_next = (slot + 1) % ftx_model::PIN_RING;
@@ -483,6 +482,7 @@ static int verify_large(ftx_ctx* ctx, ftx_model* m, const ftx_seq_args* sq, int6
                     ra.ldp = qpend.ldp;
                     ra.S = qpend.S;
                 }
+                ra.cs = d_cs + r0 * hd2 * 2;
                 ras[s] = ra;
                 Ms[s] = M;
                 AttnMArgs am{};
@@ -531,6 +531,7 @@ static int verify_large(ftx_ctx* ctx, ftx_model* m, const ftx_seq_args* sq, int6
                 ra.ldp = qpend.ldp;
                 ra.S = qpend.S;
             }
+            ra.cs = d_cs + r0 * hd2 * 2;
             if (mattn) {
                 ra.qh16 = qh + r0 * m->qdim;
                 ra.ql16 = ql + r0 * m->qdim;
