@@ -1184,21 +1184,32 @@ static MmOutDev out_dev(const MmOut& o) {
     return d;
 }
 
-// split count for `tiles` workgroups over `steps` contraction steps: none
-// when the tiles fill the device, else as many as one workgroup per CU
-// allows (the kernels hold one workgroup per CU), at least two steps per
-// split
-static int mm_splits(int64_t tiles, int64_t steps, int cu_count) {
+// split count for `tiles` workgroups over `steps` contraction steps: the
+// kernels hold one workgroup per CU, so the tiles x S workgroups run in
+// rounds of cu_count, each as long as its ceil(steps / S) steps plus, when
+// split, writing its partials (about pcost steps); the S <= 32 (and at
+// least two steps per split) of the fewest step times, the smallest on ties
+// (a 70B-shaped batch: gate / up 896 tiles -> 2 splits, 7 full rounds
+// instead of 3.5; qkv 160 tiles -> 3 splits)
+constexpr int64_t MM_SPLIT_COST = 2;    // k_mm: 256-element steps
+constexpr int64_t MMD_SPLIT_COST = 14;  // k_mm_down: 32-row slices
+static int mm_splits(int64_t tiles, int64_t steps, int cu_count, int64_t pcost) {
     const int64_t cus = cu_count > 0 ? cu_count : 256;
-    if (tiles < 1 || tiles >= cus) return 1;
-    int64_t S = cus / tiles;
-    if (S > steps / 2) S = steps / 2;
-    if (S > 32) S = 32;
-    return S < 1 ? 1 : (int)S;
+    if (tiles < 1) return 1;
+    int best = 1;
+    int64_t best_cost = -1;
+    for (int64_t S = 1; S <= 32 && (S == 1 || S <= steps / 2); ++S) {
+        const int64_t cost = (tiles * S + cus - 1) / cus * ((steps + S - 1) / S + (S > 1 ? pcost : 0));
+        if (best_cost < 0 || cost < best_cost) {
+            best_cost = cost;
+            best = (int)S;
+        }
+    }
+    return best;
 }
 
 size_t mm_part_floats(int64_t Mp, int64_t N, int64_t steps, int64_t ntiles, int cu_count) {
-    const int S = mm_splits(ntiles * (Mp / MM_TOK), steps, cu_count);
+    const int S = mm_splits(ntiles * (Mp / MM_TOK), steps, cu_count, MM_SPLIT_COST);
     return S > 1 ? (size_t)S * (size_t)Mp * (size_t)N : 0;
 }
 
@@ -1247,7 +1258,7 @@ static hipError_t mm_launch(hipStream_t st, const MmSeg* segs, int nseg, const M
     a.M = (int)M;
     const int64_t wg = (units + MM_WAVES - 1) / MM_WAVES,
                   mt = xtab ? ntile_max : act.Mp / MM_TOK;
-    int S = mm_splits(wg * mt, a.nsb, cu_count);
+    int S = mm_splits(wg * mt, a.nsb, cu_count, MM_SPLIT_COST);
     // SwiGLU needs the gate and up sums together: always through the reduce
     const bool via_part = S > 1 || epi == EPI_SWIGLU || xtab;
     if (via_part) {
@@ -1362,7 +1373,7 @@ hipError_t launch_mm_down(hipStream_t st, const uint8_t* tiled, int64_t n_in, in
     a.n_in = n_in;
     a.N = N;
     const int64_t nsl = n_in / 32, nb = N / 256, mt = Mp / MM_TOK;
-    int S = mm_splits(nb * mt, nsl, cu_count);
+    int S = mm_splits(nb * mt, nsl, cu_count, MMD_SPLIT_COST);
     if (S > 1 && (!part || (size_t)S * (size_t)Mp * (size_t)N > part_floats)) S = 1;
     a.slices_per_split = (int)((nsl + S - 1) / S);
     S = (int)((nsl + a.slices_per_split - 1) / a.slices_per_split);
@@ -1407,6 +1418,6 @@ hipError_t launch_mm_down(hipStream_t st, const uint8_t* tiled, int64_t n_in, in
 }
 
 size_t mm_down_part_floats(int64_t Mp, int64_t n_in, int64_t N, int cu_count) {
-    const int S = mm_splits((N / 256) * (Mp / MM_TOK), n_in / 32, cu_count);
+    const int S = mm_splits((N / 256) * (Mp / MM_TOK), n_in / 32, cu_count, MMD_SPLIT_COST);
     return S > 1 ? (size_t)S * (size_t)Mp * (size_t)N : 0;
 }
