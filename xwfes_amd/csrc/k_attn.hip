@@ -27,6 +27,7 @@ namespace {
 
 typedef _Float16 v8h __attribute__((ext_vector_type(8)));
 typedef _Float16 v4h __attribute__((ext_vector_type(4)));
+typedef _Float16 v2h __attribute__((ext_vector_type(2)));
 typedef float v4f __attribute__((ext_vector_type(4)));
 
 // waves per workgroup for head size 128 (16 waves, one score tile and one
@@ -615,12 +616,25 @@ __device__ __forceinline__ void attn_fa_wg(const AttnMArgs& a, int grp, int kvh,
 #pragma unroll
         for (int sp = 0; sp < 2; ++sp)
 #pragma unroll
-            for (int e = 0; e < 8; ++e) {
-                const float p = __builtin_amdgcn_exp2f(__builtin_fmaf(s[2 * sp + (e >> 2)][e & 3], c2, -mc));
-                sum += p;
-                const _Float16 h = (_Float16)p;
-                ph[sp][e] = h;
-                pl[sp][e] = (_Float16)(p - (float)h);
+            for (int e = 0; e < 8; e += 2) {
+                // a pair: both hi halves in one conversion, then each lo half
+                // = fp16(p - hi) by a mixed-precision fma reading the hi half
+                // in place (p - hi is exact in fp32)
+                const float p0 = __builtin_amdgcn_exp2f(__builtin_fmaf(s[2 * sp + (e >> 2)][e & 3], c2, -mc));
+                const float p1 = __builtin_amdgcn_exp2f(__builtin_fmaf(s[2 * sp + (e >> 2)][(e & 3) + 1], c2, -mc));
+                sum += p0;
+                sum += p1;
+                const v2h hh = {(_Float16)p0, (_Float16)p1};
+                const uint32_t hw = __builtin_bit_cast(uint32_t, hh);
+                // (mixlo writes the low half, mixhi then the high half)
+                uint32_t lw;
+                asm volatile("v_fma_mixlo_f16 %0, -%1, 1.0, %2 op_sel_hi:[1,0,0]" : "=v"(lw) : "v"(hw), "v"(p0));
+                asm volatile("v_fma_mixhi_f16 %0, -%1, 1.0, %2 op_sel:[1,0,0] op_sel_hi:[1,0,0]" : "+v"(lw) : "v"(hw), "v"(p1));
+                const v2h ll = __builtin_bit_cast(v2h, lw);
+                ph[sp][e] = hh[0];
+                ph[sp][e + 1] = hh[1];
+                pl[sp][e] = ll[0];
+                pl[sp][e + 1] = ll[1];
             }
         sum += __shfl_xor(sum, 16, 64);
         sum += __shfl_xor(sum, 32, 64);
