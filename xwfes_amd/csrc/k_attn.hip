@@ -617,20 +617,13 @@ __device__ __forceinline__ void attn_fa_wg(const AttnMArgs& a, int grp, int kvh,
         for (int sp = 0; sp < 2; ++sp)
 #pragma unroll
             for (int e = 0; e < 8; e += 2) {
-                // a pair: both hi halves in one conversion, then each lo half
-                // = fp16(p - hi) by a mixed-precision fma reading the hi half
-                // in place (p - hi is exact in fp32)
+                // a pair: split_hl2 (one conversion, two mixed fmas)
                 const float p0 = __builtin_amdgcn_exp2f(__builtin_fmaf(s[2 * sp + (e >> 2)][e & 3], c2, -mc));
                 const float p1 = __builtin_amdgcn_exp2f(__builtin_fmaf(s[2 * sp + (e >> 2)][(e & 3) + 1], c2, -mc));
                 sum += p0;
                 sum += p1;
-                const v2h hh = {(_Float16)p0, (_Float16)p1};
-                const uint32_t hw = __builtin_bit_cast(uint32_t, hh);
-                // (mixlo writes the low half, mixhi then the high half)
-                uint32_t lw;
-                asm volatile("v_fma_mixlo_f16 %0, -%1, 1.0, %2 op_sel_hi:[1,0,0]" : "=v"(lw) : "v"(hw), "v"(p0));
-                asm volatile("v_fma_mixhi_f16 %0, -%1, 1.0, %2 op_sel:[1,0,0] op_sel_hi:[1,0,0]" : "+v"(lw) : "v"(hw), "v"(p1));
-                const v2h ll = __builtin_bit_cast(v2h, lw);
+                v2h hh, ll;
+                split_hl2(p0, p1, hh, ll);
                 ph[sp][e] = hh[0];
                 ph[sp][e + 1] = hh[1];
                 pl[sp][e] = ll[0];

@@ -841,17 +841,25 @@ k_mm_down(MmDownArgs a) {
 #pragma clang fp contract(off)
         v4h dh, dl, mh, ml;
 #pragma unroll
-        for (int e = 0; e < 4; ++e) {
-            const float hvv = tok_ok ? o.hv[e] : 0.f;
-            const float pd = hvv * h2f((uint16_t)(o.dw[e] & 0xFFFF)) * MMD_ASCALE;
-            const float pm = hvv * h2f((uint16_t)(o.dw[e] >> 16)) * MMD_ASCALE;
-            _Float16 x0, x1;
-            split_hl(pd, x0, x1);
-            dh[e] = x0;
-            dl[e] = x1;
-            split_hl(pm, x0, x1);
-            mh[e] = x0;
-            ml[e] = x1;
+        for (int e = 0; e < 4; e += 2) {
+            float pd[2], pm[2];
+#pragma unroll
+            for (int i = 0; i < 2; ++i) {
+                const float hvv = tok_ok ? o.hv[e + i] : 0.f;
+                pd[i] = hvv * h2f((uint16_t)(o.dw[e + i] & 0xFFFF)) * MMD_ASCALE;
+                pm[i] = hvv * h2f((uint16_t)(o.dw[e + i] >> 16)) * MMD_ASCALE;
+            }
+            v2h h, l;
+            split_hl2(pd[0], pd[1], h, l);
+            dh[e] = h[0];
+            dh[e + 1] = h[1];
+            dl[e] = l[0];
+            dl[e + 1] = l[1];
+            split_hl2(pm[0], pm[1], h, l);
+            mh[e] = h[0];
+            mh[e + 1] = h[1];
+            ml[e] = l[0];
+            ml[e + 1] = l[1];
         }
         *(v4h*)&ad[buf][0][sm][4 * sp] = dh;
         *(v4h*)&ad[buf][1][sm][4 * sp] = dl;

@@ -71,4 +71,17 @@ __device__ __forceinline__ void split_hl(float v, _Float16& h, _Float16& l) {
     l = (_Float16)(v - (float)h);
 }
 
+// split_hl of a pair, packed: both hi halves in one conversion, each lo half
+// fp16(v - hi) by a mixed-precision fma that reads the hi half in place
+// (v - hi is exact in fp32, so the result equals split_hl's)
+__device__ __forceinline__ void split_hl2(float v0, float v1, v2h& h, v2h& l) {
+    h = v2h{(_Float16)v0, (_Float16)v1};
+    const uint32_t hw = __builtin_bit_cast(uint32_t, h);
+    uint32_t lw;  // mixlo writes the low half, mixhi then the high half
+    asm volatile("v_fma_mixlo_f16 %0, -%1, 1.0, %2 op_sel_hi:[1,0,0]" : "=v"(lw) : "v"(hw), "v"(v0));
+    asm volatile("v_fma_mixhi_f16 %0, -%1, 1.0, %2 op_sel:[1,0,0] op_sel_hi:[1,0,0]"
+                 : "+v"(lw) : "v"(hw), "v"(v1));
+    l = __builtin_bit_cast(v2h, lw);
+}
+
 }  // namespace
