@@ -24,6 +24,7 @@
 //             ct the same in bits 0-3
 //         SC  [N/256][n_in] x 16 int8,  D [N/256][n_in] x fp16
 #include "ftx_internal.h"
+#include "mm_dev.h"
 #include "quant_dev.h"
 
 namespace {
@@ -162,7 +163,7 @@ k_down_mfma(DownArgs a) {
         const float hv2[2] = {h2.x * lf, h2.y * lf};
 #pragma unroll
         for (int t = 0; t < NT; ++t) {
-            v2h ph, pl;
+            float p[2];
 #pragma unroll
             for (int k = 0; k < 2; ++k) {
                 uint32_t dw;
@@ -170,11 +171,10 @@ k_down_mfma(DownArgs a) {
                     dw = (uint32_t)si.r[k].x >> (16 * t);  // d | dmin << 16
                 else
                     dw = si.dd >> (16 * k);
-                const float p = hv2[k] * h2f((uint16_t)(dw & 0xFFFF)) * DOWN_ASCALE;
-                const _Float16 hi = (_Float16)p;
-                ph[k] = hi;
-                pl[k] = (_Float16)(p - (float)hi);
+                p[k] = hv2[k] * h2f((uint16_t)(dw & 0xFFFF)) * DOWN_ASCALE;
             }
+            v2h ph, pl;
+            split_hl2(p[0], p[1], ph, pl);
             *(v2h*)&tab[buf][t][b][g8][se][k0] = ph;
             *(v2h*)&tab[buf][t][b][g8][8 + se][k0] = pl;
         }
