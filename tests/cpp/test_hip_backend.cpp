@@ -338,6 +338,83 @@ static void test_verifier(HipBackend& be) {
         }
         be.free_staging(dbase);
     }
+
+    // two sequences in one batched step: the verifier's own cache (a chain,
+    // advancing) and a second sequence with its own history (a tree); each
+    // one's logits equal the oracle forward of that sequence alone
+    {
+        const int64_t np2 = 29;
+        HipSequence seq(ver, cap);
+        std::vector<uint16_t> kb(kc.size()), vb(kc.size());
+        for (auto& v : kb) v = orc_float_to_half(rnd());
+        for (auto& v : vb) v = orc_float_to_half(rnd());
+        seq.write_kv(kb.data(), vb.data());
+        seq.truncate_to(np2);
+        CHECK(seq.npast() == np2 && ver.npast() == npast, "batch histories");
+        const std::vector<int32_t> pa = {7, 250, 31}, pb = {11, 400, 2, 99, 64};
+        const std::vector<int32_t> parb = {-1, 0, 0, 2, 1};
+        float* la = (float*)be.alloc_staging(pa.size() * c.vocab * sizeof(float));
+        float* lb = (float*)be.alloc_staging(pb.size() * c.vocab * sizeof(float));
+        std::vector<HipVerifier::BatchItem> items(2);
+        items[0].props = pa;
+        items[0].logits = la;
+        items[0].advance = true;
+        items[1].seq = &seq;
+        items[1].props = pb;
+        items[1].parents = parb;
+        items[1].logits = lb;
+        ver.verify_batch(items);
+        CHECK(ver.npast() == npast + (int64_t)pa.size(), "an advancing item moves its cache");
+        CHECK(seq.npast() == np2, "a non-advancing item leaves its cache");
+        std::vector<float> ga(pa.size() * c.vocab), wa(ga.size()), gb(pb.size() * c.vocab),
+            wb(gb.size());
+        be.stage(ga.data(), la, ga.size() * sizeof(float));
+        be.stage(gb.data(), lb, gb.size() * sizeof(float));
+        std::vector<uint16_t> k5 = kc, v5 = vc, k6 = kb, v6 = vb;
+        CHECK(orc_forward(&om, k5.data(), v5.data(), ORC_KV_F16, cap, npast, pa.data(),
+                          (int64_t)pa.size(), nullptr, 0, wa.data()) == 0,
+              "oracle forward, sequence 0");
+        CHECK(orc_forward(&om, k6.data(), v6.data(), ORC_KV_F16, cap, np2, pb.data(),
+                          (int64_t)pb.size(), parb.data(), 0, wb.data()) == 0,
+              "oracle forward, sequence 1");
+        CHECK(rel_err(ga.data(), wa.data(), (int64_t)pa.size(), c.vocab) < 1e-3,
+              "batched chain logits");
+        CHECK(rel_err(gb.data(), wb.data(), (int64_t)pb.size(), c.vocab) < 1e-3,
+              "batched tree logits");
+        // the second sequence keeps its tree path 0 -> 2 -> 3; one more
+        // batched step over it alone continues from that path
+        seq.commit({0, 2, 3});
+        CHECK(seq.npast() == np2 + 3, "commit on a sequence");
+        std::vector<HipVerifier::BatchItem> one(1);
+        one[0].seq = &seq;
+        one[0].props = {123};
+        one[0].logits = lb;
+        ver.verify_batch(one);
+        std::vector<float> g1((size_t)c.vocab), w1((size_t)(4 * c.vocab));
+        be.stage(g1.data(), lb, g1.size() * sizeof(float));
+        std::vector<uint16_t> k7 = kb, v7 = vb;
+        const int32_t chain[4] = {pb[0], pb[2], pb[3], 123};
+        CHECK(orc_forward(&om, k7.data(), v7.data(), ORC_KV_F16, cap, np2, chain, 4, nullptr, 0,
+                          w1.data()) == 0,
+              "oracle chain of the sequence's path");
+        CHECK(rel_err(g1.data(), w1.data() + 3 * c.vocab, 1, c.vocab) < 1e-3,
+              "batched logits after a sequence commit");
+        bool threw = false;
+        try {
+            std::vector<HipVerifier::BatchItem> bad(2);
+            bad[0].props = {1};
+            bad[0].logits = la;
+            bad[1].props = {2};  // the verifier's cache twice
+            bad[1].logits = lb;
+            ver.verify_batch(bad);
+        } catch (const std::runtime_error&) {
+            threw = true;
+        }
+        CHECK(threw, "a cache given twice is refused");
+        be.free_staging(la);
+        be.free_staging(lb);
+        ver.truncate_to(npast);
+    }
 }
 
 // a GGUF model through the C++ loader: Gguf -> config_from_gguf ->

@@ -1,8 +1,9 @@
 """The C++ host mirror (HipBackend / HipVerifier, xwfes_amd/host/) on the GPU:
 runs tests/cpp/test_hip_backend, which checks IBackend::matmul,
 run_expert_chunk, the reference's greedy-acceptance known answer, and a
-2-layer chain / tree verify plus greedy / ratio acceptance against the
-oracle (tests/cpp/test_hip_backend.cpp)."""
+2-layer chain / tree verify plus greedy / ratio acceptance, and a
+two-sequence HipVerifier::verify_batch (HipSequence), against the oracle
+(tests/cpp/test_hip_backend.cpp)."""
 import os
 import subprocess
 

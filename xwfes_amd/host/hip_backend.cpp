@@ -226,6 +226,55 @@ int64_t HipVerifier::npast() const {
 void HipVerifier::write_kv(const void* k, const void* v) { be_.check(ftx_kv_write(kv_, k, v), "kv_write"); }
 void HipVerifier::read_kv(void* k, void* v) { be_.check(ftx_kv_read(kv_, k, v), "kv_read"); }
 
+void HipVerifier::verify_batch(const std::vector<BatchItem>& items) {
+    if (items.empty() || items.size() > (size_t)FTX_MAX_SEQ)
+        throw std::runtime_error("HipVerifier: 1-16 sequences per batch");
+    std::vector<ftx_seq_args> a(items.size());
+    for (size_t i = 0; i < items.size(); ++i) {
+        const BatchItem& it = items[i];
+        const int64_t M = (int64_t)it.props.size();
+        if (M < 1) throw std::runtime_error("HipVerifier: empty draft in a batch");
+        if (!it.parents.empty() && (int64_t)it.parents.size() != M)
+            throw std::runtime_error("HipVerifier: parents must match the draft");
+        if (it.seq && &it.seq->be_ != &be_)
+            throw std::runtime_error("HipVerifier: sequence of another backend");
+        a[i] = ftx_seq_args{};
+        a[i].kv = it.seq ? it.seq->kv_ : kv_;
+        a[i].M = M;
+        a[i].tokens = it.props.data();
+        a[i].parents = it.parents.empty() ? nullptr : it.parents.data();
+        a[i].logits = it.logits;
+        a[i].advance = it.advance ? 1 : 0;
+    }
+    // the library checks the token total, distinct caches and the logits rule
+    be_.check(ftx_verify_batch(be_.ctx(), model_, a.data(), (int64_t)a.size()), "verify_batch");
+}
+
+HipSequence::HipSequence(HipVerifier& ver, int64_t ctx_cap, bool kv_f16) : be_(ver.be_) {
+    be_.check(ftx_kv_create(be_.ctx(), ver.model_, ctx_cap, kv_f16 ? FTX_KV_F16 : FTX_KV_F32, &kv_),
+              "kv_create");
+}
+
+HipSequence::~HipSequence() {
+    if (kv_) ftx_kv_free(kv_);
+}
+
+void HipSequence::truncate_to(int64_t npast) { be_.check(ftx_kv_truncate(kv_, npast), "truncate"); }
+
+void HipSequence::commit(const std::vector<int32_t>& nodes) {
+    be_.check(ftx_kv_commit(kv_, nodes.data(), (int64_t)nodes.size()), "commit");
+}
+
+int64_t HipSequence::npast() const {
+    void *k = nullptr, *v = nullptr;
+    int64_t n = 0;
+    be_.check(ftx_kv_pointers(kv_, &k, &v, &n), "kv_pointers");
+    return n;
+}
+
+void HipSequence::write_kv(const void* k, const void* v) { be_.check(ftx_kv_write(kv_, k, v), "kv_write"); }
+void HipSequence::read_kv(void* k, void* v) { be_.check(ftx_kv_read(kv_, k, v), "kv_read"); }
+
 Accepted accept_on_device(HipBackend& be, int64_t V, const float* base_row, const float* rows,
                           const std::vector<int32_t>& props, AcceptMode mode, float temp,
                           uint64_t& rng, const std::vector<float>& pd,

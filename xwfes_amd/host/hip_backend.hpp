@@ -166,6 +166,8 @@ Accepted accept_on_device(HipBackend& be, int64_t V, const float* base_row, cons
                           const std::vector<int32_t>& parents = {}, const float* q = nullptr,
                           BonusSampler* sampler = nullptr);
 
+class HipSequence;
+
 class HipVerifier {
 public:
     HipVerifier(HipBackend& be, const ModelConfig& cfg, const ModelWeights& w, int64_t ctx_cap,
@@ -204,17 +206,55 @@ public:
                     AcceptMode mode, float temp, uint64_t& rng, const std::vector<float>& pd = {},
                     const std::vector<int32_t>& parents = {}, const float* q = nullptr);
 
+    // several sequences of this model in one step (ftx_verify_batch): each
+    // item verifies its draft against its own cache (seq == nullptr: this
+    // verifier's cache), every weight streamed once for all of them; the
+    // logits pointers are all null or all set (device [M][vocab] each)
+    struct BatchItem {
+        HipSequence* seq = nullptr;
+        std::vector<int32_t> props;
+        std::vector<int32_t> parents;  // empty = linear chain
+        float* logits = nullptr;
+        bool advance = false;
+    };
+    void verify_batch(const std::vector<BatchItem>& items);
+
     const ModelConfig& config() const { return cfg_; }
     HipBackend& backend() { return be_; }
     int64_t max_tokens() const { return max_tokens_; }
 
 private:
+    friend class HipSequence;
     HipBackend& be_;
     ModelConfig cfg_;
     ftx_model* model_ = nullptr;
     ftx_kv* kv_ = nullptr;
     float* logits_ = nullptr;
     int64_t max_tokens_ = 0;
+};
+
+// One more sequence over a HipVerifier's model (no counterpart in the
+// reference, whose Engine owns one KvCache, include/ft/kv_cache.h:10-47): a
+// cache of its own with the KvCache operations, verified together with
+// other sequences by HipVerifier::verify_batch.  Must not outlive the
+// verifier.
+class HipSequence {
+public:
+    HipSequence(HipVerifier& ver, int64_t ctx_cap, bool kv_f16 = true);
+    ~HipSequence();
+    HipSequence(const HipSequence&) = delete;
+    HipSequence& operator=(const HipSequence&) = delete;
+
+    void truncate_to(int64_t npast);
+    void commit(const std::vector<int32_t>& nodes);
+    int64_t npast() const;
+    void write_kv(const void* k, const void* v);
+    void read_kv(void* k, void* v);
+
+private:
+    friend class HipVerifier;
+    HipBackend& be_;
+    ftx_kv* kv_ = nullptr;
 };
 
 // DraftModelDrafter (src/spec.cpp:72-119) over a resident draft model: its
