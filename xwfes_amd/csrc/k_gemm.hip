@@ -1083,6 +1083,49 @@ __global__ void __launch_bounds__(256) k_mm_reduce(MmReduceArgs a) {
     *yp = o.accum ? *yp + v : v;
 }
 
+// The same for dense launches (no tile table, no fragment output) with every
+// row, split and output 16-byte aligned: four columns per thread, the same
+// sums in the same order.  grid = (ceil(N / 1024), M).
+__global__ void __launch_bounds__(256) k_mm_reduce4(MmReduceArgs a) {
+    const int64_t n = ((int64_t)blockIdx.x * 256 + threadIdx.x) * 4;
+    const int64_t m = blockIdx.y;
+    if (n >= a.N) return;
+    const float* p = a.part + m * a.ldp + n;
+    float4 g = {0.f, 0.f, 0.f, 0.f}, u = {0.f, 0.f, 0.f, 0.f};
+    for (int s = 0; s < a.S; ++s) {
+        const float4 t = *(const float4*)(p + (int64_t)s * a.split_stride);
+        g.x += t.x;
+        g.y += t.y;
+        g.z += t.z;
+        g.w += t.w;
+    }
+    if (a.swiglu) {
+        for (int s = 0; s < a.S; ++s) {
+            const float4 t = *(const float4*)(p + (int64_t)s * a.split_stride + a.N);
+            u.x += t.x;
+            u.y += t.y;
+            u.z += t.z;
+            u.w += t.w;
+        }
+        g.x = g.x / (1.f + expf(-g.x)) * u.x;
+        g.y = g.y / (1.f + expf(-g.y)) * u.y;
+        g.z = g.z / (1.f + expf(-g.z)) * u.z;
+        g.w = g.w / (1.f + expf(-g.w)) * u.w;
+    }
+    const MmOutDev& o = a.out;
+    int sq = 0;
+    while (sq + 1 < o.nseq && m >= o.row0[sq + 1]) ++sq;
+    float4* yp = (float4*)(o.base[sq] + (m - o.row0[sq]) * o.ld + n);
+    if (o.accum) {
+        const float4 y = *yp;
+        g.x += y.x;
+        g.y += y.y;
+        g.z += y.z;
+        g.w += y.w;
+    }
+    *yp = g;
+}
+
 }  // namespace
 
 // ---------------------------------------------------------------- host
@@ -1127,6 +1170,21 @@ hipError_t launch_mm_prep_fold(hipStream_t st, float* x, int64_t ldx, const floa
     return hipGetLastError();
 }
 
+// k_mm_reduce over `rows` rows, four columns per thread where the operands
+// allow (no tile table or fragment output, 16-byte aligned rows and splits)
+static hipError_t launch_reduce(hipStream_t st, const MmReduceArgs& r, int64_t rows) {
+    bool vec = !r.xtab && !r.fh && r.N % 4 == 0 && r.ldp % 4 == 0 && r.split_stride % 4 == 0 &&
+               ((uintptr_t)r.part & 15) == 0 && r.out.ld % 4 == 0;
+    for (int s = 0; s < r.out.nseq; ++s) vec = vec && ((uintptr_t)r.out.base[s] & 15) == 0;
+    if (vec)
+        hipLaunchKernelGGL(k_mm_reduce4, dim3((unsigned)((r.N + 1023) / 1024), (unsigned)rows),
+                           dim3(256), 0, st, r);
+    else
+        hipLaunchKernelGGL(k_mm_reduce, dim3((unsigned)((r.N + 255) / 256), (unsigned)rows),
+                           dim3(256), 0, st, r);
+    return hipGetLastError();
+}
+
 hipError_t launch_mm_fold(hipStream_t st, const MmPend& fold, int64_t M, float* y, int64_t ldy) {
     if (fold.S < 1) return hipSuccess;
     MmReduceArgs r{};
@@ -1142,9 +1200,7 @@ hipError_t launch_mm_fold(hipStream_t st, const MmPend& fold, int64_t M, float* 
     r.out.row0[1] = M;
     r.out.ld = ldy;
     r.out.accum = fold.accum;
-    hipLaunchKernelGGL(k_mm_reduce, dim3((unsigned)((fold.N + 255) / 256), (unsigned)M), dim3(256),
-                       0, st, r);
-    return hipGetLastError();
+    return launch_reduce(st, r, M);
 }
 
 bool mm_supported(int dt, int64_t K) {
@@ -1339,10 +1395,7 @@ static hipError_t mm_launch(hipStream_t st, const MmSeg* segs, int nseg, const M
         r.fscale = fo->scale;
         r.fK = fo->K;
     }
-    const int64_t rows = xtab ? ntile_max * trows : M;
-    hipLaunchKernelGGL(k_mm_reduce, dim3((unsigned)((r.N + 255) / 256), (unsigned)rows), dim3(256),
-                       0, st, r);
-    return hipGetLastError();
+    return launch_reduce(st, r, xtab ? ntile_max * trows : M);
 }
 
 hipError_t launch_mm(hipStream_t st, const MmSeg* segs, int nseg, const MmAct& act, int64_t M,
@@ -1420,9 +1473,7 @@ hipError_t launch_mm_down(hipStream_t st, const uint8_t* tiled, int64_t n_in, in
     r.swiglu = 0;
     r.N = N;
     r.out = out_dev(out);
-    hipLaunchKernelGGL(k_mm_reduce, dim3((unsigned)((N + 255) / 256), (unsigned)M), dim3(256), 0,
-                       st, r);
-    return hipGetLastError();
+    return launch_reduce(st, r, M);
 }
 
 size_t mm_down_part_floats(int64_t Mp, int64_t n_in, int64_t N, int cu_count) {
