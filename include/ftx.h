@@ -100,6 +100,9 @@ typedef struct {
 } ftx_device_info_t;
 
 /* ---- context ---- */
+/* A context on `device` with its own stream (IBackend construction,
+ * src/engine.cpp:291-300).  Makes `device` the calling thread's current
+ * device, as creating its stream requires. */
 int ftx_create(int device, ftx_ctx** out);
 int ftx_destroy(ftx_ctx* ctx);
 int ftx_device_info(ftx_ctx* ctx, ftx_device_info_t* out);
@@ -150,8 +153,13 @@ int ftx_down_axpy(ftx_ctx* ctx, const float* x, int64_t M, int64_t n_in, const f
  * go to a file-scope device array of the library (16 MiB per GPU, held until
  * the process ends) instead of the context's workspace, so nothing is
  * allocated.  Shapes whose partials exceed that array return FTX_E_RANGE.
- * Every call on one GPU shares that GPU's array: calls that overlap on one
- * GPU (several streams or threads) race. */
+ * The result is stream-ordered: the call returns once its two kernels are
+ * enqueued on the context's stream (ftx_sync, or any later synchronising
+ * call, waits for them), so it may be recorded into a HIP graph.  Every call
+ * on one GPU shares that GPU's array: calls that overlap on one GPU (several
+ * streams or threads) race.  The array's address is looked up per device at
+ * ftx_create; if that lookup fails, only this entry point fails
+ * (FTX_E_DEVICE). */
 int ftx_down_axpy_noalloc(ftx_ctx* ctx, const float* x, int64_t M, int64_t n_in,
                           const ftx_tensor* W, float* y);
 

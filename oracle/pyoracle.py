@@ -221,7 +221,7 @@ class Oracle:
 
     def generate(self, target, draft, prompt, max_new, spec_k=8, temp=0.0, top_k=40, top_p=0.95,
                  seed=0, cap=256, kv_dtype=np.float16, ref_bonus_row=False,
-                 ref_draft_prefill=False):
+                 ref_draft_prefill=False, eos=-1):
         """generate's speculative block (src/spec.cpp:245-333) with a
         DraftModelDrafter (72-119) over two models of this module's form, on
         caches of kv_dtype: draft k greedy tokens with their T = 1
@@ -238,7 +238,14 @@ class Oracle:
         new tokens, as the reference's Engine::prefill does on a non-empty
         engine without a prefix-cache hit (src/engine.cpp:614-621: the loop
         starts at the hit length, 0, not at the history length), again only
-        to compare with it.  Returns (tokens, stats)."""
+        to compare with it.  The ratio test runs at T = 1 whatever temp is
+        (accept_chain_sampling ignores the temperature, spec.cpp:216); temp
+        shapes the bonus draw only.  eos (the tokenizer's
+        tokenizer.ggml.eos_token_id, -1 for none) ends the loop as the
+        reference's does (316-328): an accepted draft token equal to it ends
+        the round after every accepted token is out (no bonus), a bonus equal
+        to it is emitted and stepped, a sampled token of an empty draft is
+        emitted and not stepped.  Returns (tokens, stats)."""
         def state(model):
             c = model["cfg"]
             shape = (c["n_layer"], cap, c["n_head_kv"] * c["head_dim"])
@@ -259,9 +266,9 @@ class Oracle:
         out = []
         rsamp = seed if seed else 88172645463325252
         sstate = seed if seed else SAMPLER_SEED
-        acc_temp = temp if temp > 0 else 1.0
+        acc_temp = 1.0
         bk, bp = (top_k, top_p) if temp > 0 else (1, 1.0)
-        stats = dict(rounds=0, drafted=0, accepted=0)
+        stats = dict(rounds=0, drafted=0, accepted=0, hit_eos=False)
         while len(out) < max_new:
             # DraftModelDrafter::sync + draft
             if D["n"] > len(history):
@@ -308,16 +315,32 @@ class Oracle:
                                                top_k, top_p, sstate)
             rsamp, sstate = r["rng"], r["sampler_state"]
             T["n"] += acc
-            new = props[:acc] + [bonus]
-            out += new
-            history += new
-            base = fwd(T, [bonus])[0]
-            T["n"] += 1
-            D["n"] = min(pending_base + acc, D["n"])
-            D["hist"] = D["hist"][:D["n"]]
             stats["rounds"] += 1
             stats["drafted"] += M
             stats["accepted"] += acc
+
+            def commit():
+                D["n"] = min(pending_base + acc, D["n"])
+                D["hist"] = D["hist"][:D["n"]]
+
+            if M == 0 and bonus == eos:  # an empty draft's sampled token
+                out.append(bonus)
+                stats["hit_eos"] = True
+                break
+            out += props[:acc]  # every accepted token is out, past an eos too
+            history += props[:acc]
+            if eos >= 0 and eos in props[:acc]:
+                commit()
+                stats["hit_eos"] = True
+                break
+            out.append(bonus)
+            history.append(bonus)
+            base = fwd(T, [bonus])[0]
+            T["n"] += 1
+            commit()
+            if bonus == eos:
+                stats["hit_eos"] = True
+                break
         return out, stats
 
     @staticmethod

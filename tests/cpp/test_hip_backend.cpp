@@ -535,12 +535,15 @@ static int run_generate(HipBackend& be, int argc, char** argv) {
     {
         HipVerifier target(be, ct.cfg, wt, cap, 8), draft(be, cd.cfg, wd, cap, 8);
         DraftModelDrafter drafter(draft);
-        out = generate(target, drafter, prompt, max_new, spec_k, temp, 40, 0.95f, 0, &st);
+        // the end-of-sequence id as the reference's tokenizer reads it
+        // (src/tokenizer.cpp:68)
+        const int32_t eos = (int32_t)gt.get_i64("tokenizer.ggml.eos_token_id", -1);
+        out = generate(target, drafter, prompt, max_new, spec_k, temp, 40, 0.95f, 0, &st, eos);
     }
     std::printf("generate tokens:");
     for (int32_t t : out) std::printf(" %d", t);
-    std::printf("\ngenerate stats: %lld %lld %lld\n", (long long)st.rounds, (long long)st.drafted,
-                (long long)st.accepted);
+    std::printf("\ngenerate stats: %lld %lld %lld %d\n", (long long)st.rounds,
+                (long long)st.drafted, (long long)st.accepted, st.hit_eos ? 1 : 0);
     for (ModelWeights* w : {&wt, &wd}) {
         for (const auto& L : w->layers)
             for (const auto& t : L) be.evict(t);

@@ -24,15 +24,18 @@ def test_cpp_host_mirror():
 
 
 @pytest.mark.gpu
-@pytest.mark.parametrize("temp", [0.0, 1.0])
+@pytest.mark.parametrize("eos_at", [None, 6])
+@pytest.mark.parametrize("temp", [0.0, 0.7])
 @pytest.mark.parametrize("same_draft", [True, False])
-def test_cpp_generate_equals_oracle(tmp_path, orc, temp, same_draft):
+def test_cpp_generate_equals_oracle(tmp_path, orc, temp, same_draft, eos_at):
     """Speculative generate through the C++ host path (GGUF files -> C++
     loader -> HipVerifier target and draft -> DraftModelDrafter + generate,
     xwfes_amd/host/hip_backend.cpp) emits the oracle's tokens and statistics
     (pyoracle.Oracle.generate, pinned against the reference's generate in
     tests/test_spec.py), greedy and sampled, draft equal to and different
-    from the target."""
+    from the target; with eos_at, the target file's
+    tokenizer.ggml.eos_token_id is the token the run without one emits at
+    that position, and both loops stop there as the reference's does."""
     import numpy as np
     import pyoracle as P
     from xwfes_amd import gguf as G
@@ -47,21 +50,28 @@ def test_cpp_generate_equals_oracle(tmp_path, orc, temp, same_draft):
 
     target = peaked(31, 30.0)
     draft = target if same_draft else peaked(32, 25.0)
+    prompt = [3, 17, 5, 40, 11, 9, 30, 2, 21]
+    cap, max_new, k = 128, 30, 4
+    eos = -1
+    if eos_at is not None:
+        full, _ = orc.generate(target, draft, prompt, max_new, spec_k=k, temp=temp, cap=cap)
+        eos = full[eos_at]
     paths = []
     for name, m in (("target", target), ("draft", draft)):
         p = str(tmp_path / (name + ".gguf"))
-        G.write_gguf(p, G.model_kv(cfg), G.model_tensor_list(m))
+        G.write_gguf(p, G.model_kv(cfg, eos=eos if eos >= 0 else None), G.model_tensor_list(m))
         paths.append(p)
-    prompt = [3, 17, 5, 40, 11, 9, 30, 2, 21]
-    cap, max_new, k = 128, 30, 4
     r = subprocess.run([BIN, "--generate", paths[0], paths[1], str(temp), str(k), str(max_new),
                         str(cap)] + [str(t) for t in prompt], capture_output=True, text=True,
                        timeout=110)
     assert r.returncode == 0, r.stderr
     lines = {ln.split(":")[0]: ln.split(":")[1].split() for ln in r.stdout.splitlines() if ":" in ln}
     got = [int(t) for t in lines["generate tokens"]]
-    rounds, drafted, accepted = (int(v) for v in lines["generate stats"])
-    want, st = orc.generate(target, draft, prompt, max_new, spec_k=k, temp=temp, cap=cap)
+    rounds, drafted, accepted, hit = (int(v) for v in lines["generate stats"])
+    want, st = orc.generate(target, draft, prompt, max_new, spec_k=k, temp=temp, cap=cap, eos=eos)
     assert got == want
-    assert (rounds, drafted, accepted) == (st["rounds"], st["drafted"], st["accepted"])
+    assert (rounds, drafted, accepted, bool(hit)) == (st["rounds"], st["drafted"],
+                                                       st["accepted"], st["hit_eos"])
     assert drafted > 0 and (accepted > 0 or not same_draft)
+    if eos_at is not None:
+        assert hit and eos in got and len(got) <= eos_at + k + 1

@@ -2,9 +2,10 @@
 generate) against the oracle's restatement (pyoracle.Oracle.generate, itself
 pinned against the reference's generate in tests/test_spec.py): the same
 emitted tokens with up to four draft tokens per round, greedy (temperature 0)
-and sampled (temperature 1, the reference's sampler defaults), with the draft
-equal to the target and a different draft; plus the drafter's per-token pick
-(ftx_argmax_prob) against Sampler::argmax and softmax_prob."""
+and sampled (temperatures 0.7 and 1, the reference's sampler defaults), with
+the draft equal to the target and a different draft, with and without an
+end-of-sequence token; plus the drafter's per-token pick (ftx_argmax_prob)
+against Sampler::argmax and softmax_prob."""
 import numpy as np
 import pytest
 
@@ -32,9 +33,12 @@ def upload(gctx, model):
     return gm
 
 
-@pytest.mark.parametrize("temp", [0.0, 1.0])
+@pytest.mark.parametrize("eos_at", [None, 5])
+@pytest.mark.parametrize("temp", [0.0, 0.7, 1.0])
 @pytest.mark.parametrize("same_draft", [True, False])
-def test_generate_equals_oracle(gctx, orc, temp, same_draft):
+def test_generate_equals_oracle(gctx, orc, temp, same_draft, eos_at):
+    """eos_at: the end-of-sequence id is the token the run without one
+    emits at that position; both loops then stop as the reference's does."""
     target = peaked(orc, 31, 30.0)
     draft = target if same_draft else peaked(orc, 32, 25.0)
     tm = upload(gctx, target)
@@ -43,14 +47,20 @@ def test_generate_equals_oracle(gctx, orc, temp, same_draft):
     tkv, dkv = tm.kv(cap), dm.kv(cap)
     drafter = spec.DraftModelDrafter(gctx, dm, dkv)
     prompt = [3, 17, 5, 40, 11, 9, 30, 2, 21]  # two prefill chains
+    eos = -1
+    if eos_at is not None:
+        full, _ = orc.generate(target, draft, prompt, 30, spec_k=4, temp=temp, cap=cap)
+        eos = full[eos_at]
     try:
-        got, st = spec.generate(gctx, tm, tkv, drafter, prompt, 30, spec_k=4, temp=temp)
+        got, st = spec.generate(gctx, tm, tkv, drafter, prompt, 30, spec_k=4, temp=temp, eos=eos)
     finally:
         drafter.free()
-    want, sto = orc.generate(target, draft, prompt, 30, spec_k=4, temp=temp, cap=cap)
+    want, sto = orc.generate(target, draft, prompt, 30, spec_k=4, temp=temp, cap=cap, eos=eos)
     assert got == want, (st, sto, got, want)
     assert st == sto
     assert st["drafted"] > 0 and (st["accepted"] > 0 or not same_draft)
+    if eos_at is not None:
+        assert st["hit_eos"] and eos in got and len(got) <= eos_at + 5
     tkv.free()
     dkv.free()
     tm.free()

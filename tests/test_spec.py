@@ -4,8 +4,10 @@ loading the same GGUF files (oracle/_ref), on the CPU: identical emitted
 tokens with the draft equal to the target (every draft accepted) and with a
 different draft (rejections: the oracle then takes the bonus from the
 reference's row, rows[min(acc, k - 1)], with ref_bonus_row), at temperature 0
-(argmax bonus) and 1 (where the reference's temperature-free ratio test and
-the oracle's coincide), with the reference's sampler defaults.
+(argmax bonus), 0.7 (the reference's default) and 1 -- the ratio test at T = 1
+in both, the temperature shaping the bonus only -- with the reference's
+sampler defaults, and with an end-of-sequence id in the target file that the
+run reaches (the loops stop alike).
 
 The reference's CPU matmul sums the M rows of a block into the first output
 row (src/cpu_backend.cpp:95-103), so its forwards are right only at M = 1:
@@ -38,27 +40,40 @@ def peaked(orc, seed, gain=30.0):
     return m
 
 
-def write(tmp_path, name, model):
+def write(tmp_path, name, model, eos=None):
     p = str(tmp_path / name)
-    G.write_gguf(p, G.model_kv(CFG), G.model_tensor_list(model))
+    G.write_gguf(p, G.model_kv(CFG, eos=eos), G.model_tensor_list(model))
     return p
 
 
-@pytest.mark.parametrize("temp", [0.0, 1.0])
+@pytest.mark.parametrize("eos_at", [None, 4, 9])
+@pytest.mark.parametrize("temp", [0.0, 0.7, 1.0])
 @pytest.mark.parametrize("same_draft", [True, False])
-def test_oracle_generate_equals_reference(orc, ref, tmp_path, temp, same_draft):
+def test_oracle_generate_equals_reference(orc, ref, tmp_path, temp, same_draft, eos_at):
+    """eos_at: the target file's tokenizer.ggml.eos_token_id is the token
+    the run without one emits at that position (the reference reads it from
+    the file, src/tokenizer.cpp:68); both loops stop as the reference's does
+    (src/spec.cpp:316-328)."""
     target = peaked(orc, 31)
     draft = target if same_draft else peaked(orc, 32, gain=25.0)
-    tp = write(tmp_path, "t.gguf", target)
-    dp = tp if same_draft else write(tmp_path, "d.gguf", draft)
     prompt = [3, 17, 5, 40, 11]
+    kw = dict(spec_k=1, temp=temp, seed=0, cap=2304, kv_dtype=np.float32, ref_bonus_row=True,
+              ref_draft_prefill=True)
+    eos = -1
+    if eos_at is not None:
+        eos = orc.generate(target, draft, prompt, 24, **kw)[0][eos_at]
+    tp = write(tmp_path, "t.gguf", target, eos=eos if eos >= 0 else None)
+    dp = tp if same_draft else write(tmp_path, "d.gguf", draft)
     # seed 0: a non-zero seed makes the reference's Sampler restart from it
     # on every draw (include/ft/sampler.h:31), which the oracle does not copy
     want = ref.generate(tp, dp, prompt, max_new=24, spec_k=1, temp=temp, seed=0, ctx_len=2048,
                         prefill_batch=1)
-    got, st = orc.generate(target, draft, prompt, 24, spec_k=1, temp=temp, seed=0, cap=2304,
-                           kv_dtype=np.float32, ref_bonus_row=True, ref_draft_prefill=True)
+    got, st = orc.generate(target, draft, prompt, 24, eos=eos, **kw)
     assert got == want, (st, got, want)
+    if eos_at is not None:
+        assert st["hit_eos"] and eos in got
+        assert len(got) <= eos_at + 2
+        return
     # drafts were verified; with the draft equal to the target some were
     # accepted (its duplicated context makes others wrong)
     assert st["drafted"] > 0 and st["accepted"] < st["drafted"]

@@ -76,17 +76,20 @@ static std::mutex g_scratch_mu;
 static float* g_scratch_ptr[NOALLOC_MAX_DEVICES] = {};
 
 // the scratch address on `device` (looked up once per device, with the
-// device current); null on failure
+// device current for the lookup and the caller's current device restored
+// after it); null on failure
 static float* noalloc_scratch(int device) {
     if (device < 0 || device >= NOALLOC_MAX_DEVICES) return nullptr;
     std::lock_guard<std::mutex> lk(g_scratch_mu);
     if (!g_scratch_ptr[device]) {
+        int prev = -1;
+        if (hipGetDevice(&prev) != hipSuccess) prev = -1;
         void* ptr = nullptr;
-        if (hipSetDevice(device) != hipSuccess ||
-            hipGetSymbolAddress(&ptr, HIP_SYMBOL(scratch)) != hipSuccess) {
-            (void)hipGetLastError();
-            return nullptr;
-        }
+        const bool ok = hipSetDevice(device) == hipSuccess &&
+                        hipGetSymbolAddress(&ptr, HIP_SYMBOL(scratch)) == hipSuccess;
+        if (!ok) (void)hipGetLastError();
+        if (prev >= 0 && prev != device) (void)hipSetDevice(prev);
+        if (!ok) return nullptr;
         g_scratch_ptr[device] = (float*)ptr;
     }
     return g_scratch_ptr[device];
@@ -128,18 +131,16 @@ int ftx_create(int device, ftx_ctx** out) {
     c->stream = c->own_stream;
     hipDeviceProp_t pr;
     if (hipGetDeviceProperties(&pr, device) == hipSuccess) c->cu_count = pr.multiProcessorCount;
+    // the allocation-free entry point's scratch; a failed lookup fails only
+    // that entry point (it looks again on its first call)
     c->noalloc_scratch = noalloc_scratch(device);
-    if (!c->noalloc_scratch) {
-        (void)hipStreamDestroy(c->own_stream);
-        delete c;
-        return FTX_E_DEVICE;
-    }
     *out = c;
     return FTX_OK;
 }
 
 int ftx_destroy(ftx_ctx* ctx) {
     if (!ctx) return FTX_OK;
+    tr_abort(ctx);  // no armed kernel timer of this thread points into ctx
     (void)hipSetDevice(ctx->device);
     if (ctx->own_stream) (void)hipStreamSynchronize(ctx->own_stream);
     if (ctx->stream && ctx->stream != ctx->own_stream) (void)hipStreamSynchronize(ctx->stream);
@@ -414,9 +415,14 @@ int ftx_down_axpy_noalloc(ftx_ctx* ctx, const float* x, int64_t M, int64_t n_in,
                         "down_axpy_noalloc: the shape needs " + std::to_string(pf) +
                             " floats of scratch, above the limit of " +
                             std::to_string(NOALLOC_SCRATCH_FLOATS));
+    if (!ctx->noalloc_scratch) ctx->noalloc_scratch = noalloc_scratch(ctx->device);
+    if (!ctx->noalloc_scratch)
+        return ftx_fail(ctx, FTX_E_DEVICE, "down_axpy_noalloc: the scratch array's address "
+                                           "could not be looked up on this device");
     FTX_HIP(ctx, launch_down(ctx->stream, W->data, W->dtype, W->row_bytes, n_in, N, x, n_in, M, y,
                              N, ctx->noalloc_scratch));
-    FTX_HIP(ctx, hipStreamSynchronize(ctx->stream));
+    // results are stream-ordered: the call returns once the work is enqueued
+    // (a capturing stream must not be synchronised)
     return FTX_OK;
 }
 

@@ -130,9 +130,30 @@ int ftx_pinned(ftx_ctx* ctx, size_t bytes, void** out);
 bool ftx_is_device_ptr(const void* p);
 
 // trace brackets: tr_begin returns a token (-1 when tracing is off) that
-// tr_end closes after the launch
+// tr_end closes after the launch; tr_begin arms the calling thread's kernel
+// timer with this context's events, which tr_end -- or tr_abort on an error
+// path -- disarms
 int tr_begin(ftx_ctx* ctx);
 void tr_end(ftx_ctx* ctx, int token, int kind, double bytes, int launches = 1);
+void tr_abort(ftx_ctx* ctx);
+// A traced region: the timer is disarmed on every way out of the scope (a
+// launch helper that fails returns through FTX_HIP before end() runs), so no
+// later launch on this thread can reach this context's events.
+struct TraceScope {
+    ftx_ctx* ctx;
+    int tok;
+    bool open = true;
+    explicit TraceScope(ftx_ctx* c) : ctx(c), tok(tr_begin(c)) {}
+    void end(int kind, double bytes, int launches = 1) {
+        open = false;
+        tr_end(ctx, tok, kind, bytes, launches);
+    }
+    ~TraceScope() {
+        if (open) tr_abort(ctx);
+    }
+    TraceScope(const TraceScope&) = delete;
+    TraceScope& operator=(const TraceScope&) = delete;
+};
 // issues of one launch at an idempotent call site (1 unless replayed)
 int tr_repeats(const ftx_ctx* ctx, int kind);
 
@@ -184,9 +205,11 @@ hipError_t launch_down(hipStream_t st, const uint8_t* W, int dt, int64_t row_byt
 size_t xq_bytes(int64_t K);
 // stride of the per-8-row-chunk operands when a prep covers more than 8 rows
 size_t xq_chunk_bytes(int64_t K);
+// layout16: the operand layout of the 16x16x32 row-dot GEMV (launch_rd)
+// instead of launch_mv's
 hipError_t launch_xq_prep(hipStream_t st, float* x, int64_t ldx, const float* normw,
                           const float* part, int S, int64_t ldpart, int64_t K, int64_t M,
-                          int8_t* xq);
+                          int8_t* xq, int layout16 = 0);
 bool mv_supported(int dt, int64_t K, int64_t M);
 // the SwiGLU epilogue needs the whole contraction in one pass
 bool mv_swiglu_supported(int64_t K);
@@ -207,6 +230,8 @@ struct QkvEpi {
     int hd, n_head, n_kv, kv_f16;
 };
 
+
+
 // tiled copies for the row-dot kernel: rows per tile for an N-row tensor,
 // bytes of the copy, and the re-tiling launch (src in the resident row layout)
 int mv_tile_rows(int64_t N, int cu_count);
@@ -216,6 +241,18 @@ hipError_t launch_mv_tile(hipStream_t st, const uint8_t* src, int64_t src_row_by
 hipError_t launch_mv(hipStream_t st, const GemvSeg* segs, int nseg, const int8_t* xq, int64_t K,
                      int64_t M, int epi, int cu_count, int normed, float eps,
                      const QkvEpi* qkv = nullptr);
+// The verify step's row-dot GEMV (k_rowdot.hip): up to 8 rows on
+// v_mfma_i32_16x16x32_i8, weights as the B operand, from the tiled copies
+// above (every segment tiled), the activation operand in the layout16 form;
+// epilogues as launch_mv (EPI_STORE / ACCUM / SWIGLU / QKV)
+bool rd_supported(int dt, int64_t K, int64_t M);
+// whether launch_rd takes a projection of these segments (dtype, rows, tile
+// rows of each): not the SwiGLU pairs, and only launches of one round of
+// resident waves; otherwise launch_mv
+bool rd_take(const int* dts, const int64_t* Ns, const int* rpts, int nseg, int64_t K, int64_t M,
+             int epi, int cu_count);
+hipError_t launch_rd(hipStream_t st, const GemvSeg* segs, int nseg, const int8_t* xq, int64_t K,
+                     int64_t M, int epi, int normed, float eps, const QkvEpi* qkv = nullptr);
 
 hipError_t launch_part_reduce(hipStream_t st, const float* part, int S, int64_t N, int64_t M,
                               float* y, int64_t ldy);
@@ -380,6 +417,34 @@ __host__ __device__ inline int64_t v_index(int64_t slot, int64_t kvh, int64_t di
     return (kvh * hd + dim) * cap + slot;
 }
 
+// The qkv epilogue of one output: RoPE on q / k rows (interleaved pairs:
+// pv = the value of row n ^ 1; (c, s) = cos / sin of this row's angle), the
+// fp16 hi / lo query for attention, the K / transposed-V cache write.
+__device__ __forceinline__ void qkv_store(const QkvEpi& e, int si, int m, int64_t n, float v,
+                                          float pv, float c, float s, float* yp) {
+#pragma clang fp contract(off)
+    const int64_t d = n % e.hd, h = n / e.hd;
+    if (si < 2) {
+        // x0' = x0 c - x1 s, x1' = x0 s + x1 c for the pair (x0, x1) = (2i, 2i + 1)
+        v = (d & 1) ? pv * s + v * c : v * c - pv * s;
+    }
+    *yp = v;
+    const int64_t slot = e.slot0 + m, kdim = (int64_t)e.n_kv * e.hd;
+    if (si == 0) {
+        const int64_t o = ((int64_t)m * e.n_head + h) * e.hd + d;
+        const _Float16 hi = (_Float16)v;
+        e.qh[o] = hi;
+        e.ql[o] = (_Float16)(v - (float)hi);
+    } else if (si == 1) {
+        if (e.kv_f16) ((_Float16*)e.kc)[slot * kdim + n] = (_Float16)v;
+        else ((float*)e.kc)[slot * kdim + n] = v;
+    } else {
+        const int64_t vi = v_index(slot, h, d, e.hd, e.cap);
+        if (e.kv_f16) ((_Float16*)e.vc)[vi] = (_Float16)v;
+        else ((float*)e.vc)[vi] = v;
+    }
+}
+
 struct RopeArgs {
     float* qkv;        // [M][ldq]: q at 0, k at qdim, v at qdim + kdim
     int64_t ldq;
@@ -468,7 +533,9 @@ size_t attn_part_floats(int64_t M, int64_t n_head, int64_t hd, int64_t cap_alloc
 // xq != null: the chunk combine writes the output projection's activation
 // operand (xq_dev.h layout, K = n_head * hd) instead of a.out
 bool attn_combine_xq_supported(int64_t hd, int64_t n_head);
-hipError_t launch_attn_mfma(hipStream_t st, AttnMArgs a, float* part, int8_t* xq = nullptr);
+// xq16: the operand in the layout of the 16x16x32 row-dot GEMV (xq16_emit)
+hipError_t launch_attn_mfma(hipStream_t st, AttnMArgs a, float* part, int8_t* xq = nullptr,
+                            int xq16 = 0);
 // several sequences' attention (and the fp32 combine) in one launch each:
 // as[s] as for launch_attn_mfma with the sequence's own partial buffer
 // parts[s]; every sequence has the same head size and kv head count

@@ -796,7 +796,7 @@ __global__ void __launch_bounds__(128) k_attn_combine_batch(AttnMBatch b) {
 // w, w + 4, ... into per-lane partial numerators (lane l: elements 4l ..
 // 4l+3), which wave 0 sums in wave order and quantises.  Rows m >= M are
 // written as zeros.
-template <int HD>
+template <int HD, bool L16>
 __global__ void __launch_bounds__(256) k_attn_combine_xq(AttnMArgs a, int nch, XqPtrs o) {
     constexpr int HPB = 256 / HD;
     constexpr int CPF = 8;  // chunk partials per thread held in registers
@@ -884,7 +884,12 @@ __global__ void __launch_bounds__(256) k_attn_combine_xq(AttnMArgs a, int nch, X
             v[3] = t.w / den;
         }
     }
-    if (w == 0) xq_emit(v, sb, m, l, o);
+    if (w == 0) {
+        if constexpr (L16)
+            xq16_emit(v, sb, m, l, o);
+        else
+            xq_emit(v, sb, m, l, o);
+    }
 }
 
 }  // namespace
@@ -957,7 +962,7 @@ static hipError_t launch_fa(void (*kern)(A), const dim3& grid, hipStream_t st, c
     return hipGetLastError();
 }
 
-hipError_t launch_attn_mfma(hipStream_t st, AttnMArgs a, float* part, int8_t* xq) {
+hipError_t launch_attn_mfma(hipStream_t st, AttnMArgs a, float* part, int8_t* xq, int xq16) {
     // whole chunks of the allocation: every slot a chunk reads is allocated
     const int ch = chunk_slots(a.hd);
     if (a.cap % ch) return hipErrorInvalidValue;
@@ -983,10 +988,9 @@ hipError_t launch_attn_mfma(hipStream_t st, AttnMArgs a, float* part, int8_t* xq
         if (xq) {
             const int64_t K = (int64_t)a.n_head * a.hd;
             const dim3 cg((unsigned)(K / 256), 8);
-            if (a.hd == 128)
-                hipLaunchKernelGGL(k_attn_combine_xq<128>, cg, dim3(256), 0, st, a, ngrp, xq_ptrs(xq, K));
-            else
-                hipLaunchKernelGGL(k_attn_combine_xq<64>, cg, dim3(256), 0, st, a, ngrp, xq_ptrs(xq, K));
+            const auto kc = a.hd == 128 ? (xq16 ? k_attn_combine_xq<128, true> : k_attn_combine_xq<128, false>)
+                                        : (xq16 ? k_attn_combine_xq<64, true> : k_attn_combine_xq<64, false>);
+            hipLaunchKernelGGL(kc, cg, dim3(256), 0, st, a, ngrp, xq_ptrs(xq, K));
         } else {
             hipLaunchKernelGGL(k_attn_combine, dim3((unsigned)qi), dim3(128), 0, st, a, ngrp);
         }
@@ -1019,10 +1023,9 @@ hipError_t launch_attn_mfma(hipStream_t st, AttnMArgs a, float* part, int8_t* xq
         if (!attn_combine_xq_supported(a.hd, a.n_head)) return hipErrorInvalidValue;
         const int64_t K = (int64_t)a.n_head * a.hd;
         const dim3 cg((unsigned)(K / 256), 8);
-        if (a.hd == 128)
-            hipLaunchKernelGGL(k_attn_combine_xq<128>, cg, dim3(256), 0, st, a, ngrp, xq_ptrs(xq, K));
-        else
-            hipLaunchKernelGGL(k_attn_combine_xq<64>, cg, dim3(256), 0, st, a, ngrp, xq_ptrs(xq, K));
+        const auto kc = a.hd == 128 ? (xq16 ? k_attn_combine_xq<128, true> : k_attn_combine_xq<128, false>)
+                                    : (xq16 ? k_attn_combine_xq<64, true> : k_attn_combine_xq<64, false>);
+        hipLaunchKernelGGL(kc, cg, dim3(256), 0, st, a, ngrp, xq_ptrs(xq, K));
     } else {
         hipLaunchKernelGGL(k_attn_combine, dim3((unsigned)qi), dim3(128), 0, st, a, ngrp);
     }

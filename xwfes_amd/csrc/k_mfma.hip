@@ -66,6 +66,7 @@ __device__ __forceinline__ void reg_fence8(int* v) {
 //    depend on the row's 1 / rms factor, which the consuming GEMV applies
 //    to the block scales from the per-block sums of x^2 stored in ssq[sb][m]
 // and writes the limbs.
+template <bool L16>
 __global__ void __launch_bounds__(256) k_xq_prep(float* __restrict__ x, int64_t ldx,
                                                  const float* __restrict__ normw,
                                                  const float* __restrict__ part, int S,
@@ -145,7 +146,10 @@ __global__ void __launch_bounds__(256) k_xq_prep(float* __restrict__ x, int64_t 
     }
     if (live && part) row[k] = xv;
     if (normw && l == 0) ssq[sb * 8 + m] = ss;
-    xq_emit(v, sb, m, l, XqPtrs{frag, xs32, xs16, scale, ssq});
+    if constexpr (L16)
+        xq16_emit(v, sb, m, l, XqPtrs{frag, xs32, xs16, scale, ssq});
+    else
+        xq_emit(v, sb, m, l, XqPtrs{frag, xs32, xs16, scale, ssq});
 }
 
 // ---------------------------------------------------------------- row-dot
@@ -163,32 +167,6 @@ struct MvSeg {
     int dt;
     int role;       // index of the caller's segment (EPI_QKV: 0 q, 1 k, 2 v)
 };
-
-// (c, s) = cos / sin of this row's rotation angle (q and k segments)
-__device__ __forceinline__ void qkv_store(const QkvEpi& e, int si, int m, int64_t n, float v,
-                                          float pv, float c, float s, float* yp) {
-#pragma clang fp contract(off)
-    const int64_t d = n % e.hd, h = n / e.hd;
-    if (si < 2) {
-        // x0' = x0 c - x1 s, x1' = x0 s + x1 c for the pair (x0, x1) = (2i, 2i + 1)
-        v = (d & 1) ? pv * s + v * c : v * c - pv * s;
-    }
-    *yp = v;
-    const int64_t slot = e.slot0 + m, kdim = (int64_t)e.n_kv * e.hd;
-    if (si == 0) {
-        const int64_t o = ((int64_t)m * e.n_head + h) * e.hd + d;
-        const _Float16 hi = (_Float16)v;
-        e.qh[o] = hi;
-        e.ql[o] = (_Float16)(v - (float)hi);
-    } else if (si == 1) {
-        if (e.kv_f16) ((_Float16*)e.kc)[slot * kdim + n] = (_Float16)v;
-        else ((float*)e.kc)[slot * kdim + n] = v;
-    } else {
-        const int64_t vi = v_index(slot, h, d, e.hd, e.cap);
-        if (e.kv_f16) ((_Float16*)e.vc)[vi] = (_Float16)v;
-        else ((float*)e.vc)[vi] = v;
-    }
-}
 
 struct MvArgs {
     MvSeg seg[3];
@@ -681,16 +659,17 @@ static float* xq_ssq(int8_t* xq, int64_t K) { return xq_ptrs(xq, K).ssq; }
 
 hipError_t launch_xq_prep(hipStream_t st, float* x, int64_t ldx, const float* normw,
                           const float* part, int S, int64_t ldpart, int64_t K, int64_t M,
-                          int8_t* xq) {
+                          int8_t* xq, int layout16) {
     if (K % 512 || K > 16384 || M < 1 || (part && M > 8)) return hipErrorInvalidValue;
     int8_t* frag = xq;
     int8_t* xs32 = xq + K * 16;
     int8_t* xs16 = xs32 + K;
     // one operand per 8-row chunk, xq_chunk_bytes(K) apart
     const int64_t chunks = (M + 7) / 8;
-    hipLaunchKernelGGL(k_xq_prep, dim3((unsigned)(K / 256), (unsigned)(8 * chunks)), dim3(256), 0,
-                       st, x, ldx, normw, part, S, ldpart, K, (int)M, frag, xs32, xs16,
-                       xq_scale(xq, K), xq_ssq(xq, K), (int64_t)xq_chunk_bytes(K));
+    hipLaunchKernelGGL(layout16 ? k_xq_prep<true> : k_xq_prep<false>,
+                       dim3((unsigned)(K / 256), (unsigned)(8 * chunks)), dim3(256), 0, st, x, ldx,
+                       normw, part, S, ldpart, K, (int)M, frag, xs32, xs16, xq_scale(xq, K),
+                       xq_ssq(xq, K), (int64_t)xq_chunk_bytes(K));
     return hipGetLastError();
 }
 

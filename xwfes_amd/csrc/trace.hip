@@ -89,6 +89,12 @@ void tr_end(ftx_ctx* ctx, int token, int kind, double bytes, int launches) {
     ctx->pending.push_back(TraceRec{kind, token, e, bytes, launches});
 }
 
+void tr_abort(ftx_ctx* ctx) {
+    if (!ctx) return;
+    ctx->kt.armed = false;
+    if (g_ktimer == &ctx->kt) g_ktimer = nullptr;
+}
+
 int tr_repeats(const ftx_ctx* ctx, int kind) {
     return ctx->trace && kind == ctx->replay_kind ? ctx->replay_n : 1;
 }
@@ -97,6 +103,7 @@ extern "C" {
 
 int ftx_trace(ftx_ctx* ctx, int enable) {
     if (!ctx) return FTX_E_INVALID;
+    tr_abort(ctx);
     resolve(ctx);
     ctx->trace = enable != 0;
     if (enable) {

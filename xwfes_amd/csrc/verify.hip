@@ -111,6 +111,19 @@ static bool mv_all(const ftx_tensor* const* ts, int n, int64_t K, int64_t M) {
     return true;
 }
 
+// whether the 16x16x32 row-dot kernel (launch_rd) takes a projection whose
+// segments have tiled copies with rpt[i] rows per tile
+static bool rd_use(const ftx_tensor* const* ts, const int* rpt, int n, int64_t K, int64_t M,
+                   int epi, int cu_count) {
+    int dts[3];
+    int64_t Ns[3];
+    for (int i = 0; i < n && i < 3; ++i) {
+        dts[i] = ts[i]->dtype;
+        Ns[i] = ts[i]->nrows;
+    }
+    return n <= 3 && rd_take(dts, Ns, rpt, n, K, M, epi, cu_count);
+}
+
 struct ftx_kv {
     ftx_ctx* ctx = nullptr;
     int64_t n_layer = 0, cap = 0, kdim = 0, n_kv = 0, hd = 0;
@@ -231,11 +244,11 @@ static int verify_large(ftx_ctx* ctx, ftx_model* m, const ftx_seq_args* sq, int6
     const float eps = d.rms_eps;
     const double f4 = 4.0, Md = (double)Mt;
     auto wbytes = [](const ftx_tensor* t) { return (double)(t->row_bytes * t->nrows); };
-#define TRACED_L(kind, bytes, call)                \
-    do {                                           \
-        const int tk_ = tr_begin(ctx);             \
-        FTX_HIP(ctx, call);                        \
-        tr_end(ctx, tk_, (kind), (double)(bytes)); \
+#define TRACED_L(kind, bytes, call)           \
+    do {                                      \
+        TraceScope ts_(ctx);                  \
+        FTX_HIP(ctx, call);                   \
+        ts_.end((kind), (double)(bytes));     \
     } while (0)
     TRACED_L(TK_EMBED, Md * d.tok_embd->row_bytes + Md * D * f4,
              launch_embed(st, d.tok_embd->data, d.tok_embd->dtype, d.tok_embd->row_bytes, D,
@@ -314,8 +327,12 @@ static int verify_large(ftx_ctx* ctx, ftx_model* m, const ftx_seq_args* sq, int6
         bool tiled_all = mv_all(ts, nseg, K, 8) && (epi != EPI_SWIGLU || mv_swiglu_supported(K));
         for (int i = 0; tiled_all && i < nseg; ++i) tiled_all = m->mvt[idx[i]] != nullptr;
         if (tiled_all) {
+            int rpts[3] = {0, 0, 0};
+            for (int i = 0; i < nseg; ++i) rpts[i] = m->mvt_rpt[idx[i]];
+            const bool rd = rd_use(ts, rpts, nseg, K, 8, epi, ctx->cu_count);
             auto chunks = [&]() -> hipError_t {
-                hipError_t e = launch_xq_prep(st, (float*)xin, ldx, normw, nullptr, 0, D, K, Mr, m->xq);
+                hipError_t e = launch_xq_prep(st, (float*)xin, ldx, normw, nullptr, 0, D, K, Mr, m->xq,
+                                              rd);
                 if (e != hipSuccess) return e;
                 for (int64_t c0 = 0; c0 < Mr; c0 += 8) {
                     const int64_t mc = Mr - c0 < 8 ? Mr - c0 : 8;
@@ -327,8 +344,10 @@ static int verify_large(ftx_ctx* ctx, ftx_model* m, const ftx_seq_args* sq, int6
                         cs[i].rpt = m->mvt_rpt[idx[i]];
                         if (cs[i].y) cs[i].y += c0 * cs[i].ldy;
                     }
-                    e = launch_mv(st, cs, nseg, m->xq + (c0 / 8) * (int64_t)xq_chunk_bytes(K), K, mc,
-                                  epi, ctx->cu_count, normw != nullptr, eps, nullptr);
+                    const int8_t* xc = m->xq + (c0 / 8) * (int64_t)xq_chunk_bytes(K);
+                    e = rd ? launch_rd(st, cs, nseg, xc, K, mc, epi, normw != nullptr, eps)
+                           : launch_mv(st, cs, nseg, xc, K, mc, epi, ctx->cu_count, normw != nullptr,
+                                       eps, nullptr);
                     if (e != hipSuccess) return e;
                 }
                 return hipSuccess;
@@ -1242,20 +1261,20 @@ int ftx_verify_step(ftx_ctx* ctx, ftx_model* m, ftx_kv* kv, const ftx_verify_arg
     const float eps = d.rms_eps;
     const double f4 = 4.0, Md = (double)M;
     auto wbytes = [](const ftx_tensor* t) { return (double)(t->row_bytes * t->nrows); };
-#define TRACED(kind, bytes, call)                 \
-    do {                                          \
-        const int tk_ = tr_begin(ctx);            \
-        FTX_HIP(ctx, call);                       \
-        tr_end(ctx, tk_, (kind), (double)(bytes)); \
+#define TRACED(kind, bytes, call)             \
+    do {                                      \
+        TraceScope ts_(ctx);                  \
+        FTX_HIP(ctx, call);                   \
+        ts_.end((kind), (double)(bytes));     \
     } while (0)
     // a launch whose outputs do not depend on its own earlier results
     // (no accumulate into its inputs): replayable by ftx_trace_replay
-#define TRACED_IDEM(kind, bytes, call)                                  \
-    do {                                                                \
-        const int tk_ = tr_begin(ctx);                                  \
-        const int n_ = tr_repeats(ctx, (kind));                         \
-        for (int r_ = 0; r_ < n_; ++r_) FTX_HIP(ctx, call);              \
-        tr_end(ctx, tk_, (kind), (double)(bytes) * n_, n_);             \
+#define TRACED_IDEM(kind, bytes, call)                         \
+    do {                                                       \
+        TraceScope ts_(ctx);                                   \
+        const int n_ = tr_repeats(ctx, (kind));                \
+        for (int r_ = 0; r_ < n_; ++r_) FTX_HIP(ctx, call);     \
+        ts_.end((kind), (double)(bytes) * n_, n_);             \
     } while (0)
     TRACED(TK_EMBED, Md * d.tok_embd->row_bytes + Md * D * f4,
            launch_embed(st, d.tok_embd->data, d.tok_embd->dtype, d.tok_embd->row_bytes, D,
@@ -1282,21 +1301,26 @@ int ftx_verify_step(ftx_ctx* ctx, ftx_model* m, ftx_kv* kv, const ftx_verify_arg
                 segs[i].tiled = 1;
                 segs[i].rpt = m->mvt_rpt[tix0 + tix[i]];
             }
+            // the 16x16x32 row-dot kernel over the tiled copies, else k_mv
+            int rpts[3] = {0, 0, 0};
+            for (int i = 0; all && i < nseg; ++i) rpts[i] = segs[i].rpt;
+            const bool rd = all && rd_use(ts, rpts, nseg, K, M, epi, ctx->cu_count);
             if (!xq_ready && fold)  // adds the split partials into x: not replayable
                 TRACED(TK_XQ_PREP, Md * K * f4 * (2.0 + fold_S) + 19.0 * K,
-                       launch_xq_prep(st, xin, ldx, normw, m->downpart, fold_S, D, K, M, m->xq));
+                       launch_xq_prep(st, xin, ldx, normw, m->downpart, fold_S, D, K, M, m->xq, rd));
             else if (!xq_ready)
                 TRACED_IDEM(TK_XQ_PREP, Md * K * f4 + 19.0 * K,
-                            launch_xq_prep(st, xin, ldx, normw, nullptr, 0, D, K, M, m->xq));
+                            launch_xq_prep(st, xin, ldx, normw, nullptr, 0, D, K, M, m->xq, rd));
             if (fold) fold_S = 0;
+            auto gemv = [&]() -> hipError_t {
+                return rd ? launch_rd(st, segs, nseg, m->xq, K, M, epi, normw != nullptr, eps, qe)
+                          : launch_mv(st, segs, nseg, m->xq, K, M, epi, ctx->cu_count,
+                                      normw != nullptr, eps, qe);
+            };
             if (epi == EPI_ACCUM)
-                TRACED(kind, bytes,
-                       launch_mv(st, segs, nseg, m->xq, K, M, epi, ctx->cu_count,
-                                 normw != nullptr, eps, qe));
+                TRACED(kind, bytes, gemv());
             else
-                TRACED_IDEM(kind, bytes,
-                            launch_mv(st, segs, nseg, m->xq, K, M, epi, ctx->cu_count,
-                                      normw != nullptr, eps, qe));
+                TRACED_IDEM(kind, bytes, gemv());
             return FTX_OK;
         }
         if (fold) {
@@ -1407,6 +1431,11 @@ int ftx_verify_step(ftx_ctx* ctx, ftx_model* m, ftx_kv* kv, const ftx_verify_arg
         // directly when that projection takes the int8-MFMA path
         const bool o_xq = mattn && attn_combine_xq_supported(d.head_dim, d.n_head) &&
                           mv_all(&T[FTX_T_O], 1, m->qdim, M);
+        // the o projection runs launch_rd (its operand in the layout16 form)
+        // when its tiled copy exists and the kernel takes the shape
+        const int o_rpt = m->mvt_rpt[lt + FTX_T_O];
+        const bool o_rd = m->mvt[lt + FTX_T_O] &&
+                          rd_use(&T[FTX_T_O], &o_rpt, 1, m->qdim, M, EPI_ACCUM, ctx->cu_count);
         if (mattn) {
             AttnMArgs am{};
             am.qkv = m->qkv;
@@ -1425,7 +1454,7 @@ int ftx_verify_step(ftx_ctx* ctx, ftx_model* m, ftx_kv* kv, const ftx_verify_arg
             am.hd = (int)d.head_dim;
             am.out = m->att;
             TRACED_IDEM(TK_ATTENTION, attn_b,
-                        launch_attn_mfma(st, am, kv->attn_part, o_xq ? m->xq : nullptr));
+                        launch_attn_mfma(st, am, kv->attn_part, o_xq ? m->xq : nullptr, o_rd));
         } else {
             AttnArgs aa{m->qkv,  m->ldq, kl,       vl,          kv->kv_f16, m->npast,
                         m->anc,  aw,     d.n_head, d.n_head_kv, d.head_dim, npast + M,
@@ -1582,10 +1611,12 @@ int ftx_accept(ftx_ctx* ctx, const ftx_accept_args* a) {
     FTX_HIP(ctx, hipMemcpyAsync(d_small, pin, small_b, hipMemcpyHostToDevice, st));
     RowStats* stats = (RowStats*)ws;
     const RowChunks rch = row_chunks(ws + off_rs, M + 1, V);
-    int tk = tr_begin(ctx);
     const int with_sum = a->mode != FTX_ACCEPT_GREEDY;
-    FTX_HIP(ctx, launch_row_stats(st, a->base_row, a->rows, M + 1, V, a->temp, with_sum, rch));
-    tr_end(ctx, tk, TK_ROW_STATS, (double)(M + 1) * V * 4, with_sum ? 2 : 1);
+    {
+        TraceScope ts(ctx);
+        FTX_HIP(ctx, launch_row_stats(st, a->base_row, a->rows, M + 1, V, a->temp, with_sum, rch));
+        ts.end(TK_ROW_STATS, (double)(M + 1) * V * 4, with_sum ? 2 : 1);
+    }
     AcceptDev ad{};
     ad.base_row = a->base_row;
     ad.rows = a->rows;
@@ -1607,14 +1638,16 @@ int ftx_accept(ftx_ctx* ctx, const ftx_accept_args* a) {
     ad.p = (double*)(ws + off_p);
     ad.out = (int32_t*)(d_small + 24);
     ad.margin = (float*)(d_small + 16);
-    tk = tr_begin(ctx);
     int bar_err = 0;
     void* res_scratch = ws + off_p + ((2 * (size_t)V * 8 + 255) & ~(size_t)255);
-    if (a->mode == FTX_ACCEPT_RESIDUAL)
-        FTX_HIP(ctx, launch_accept_residual(st, ad, res_scratch));
-    else
-        FTX_HIP(ctx, launch_accept(st, ad));
-    tr_end(ctx, tk, TK_ACCEPT, (double)V * 4);
+    {
+        TraceScope ts(ctx);
+        if (a->mode == FTX_ACCEPT_RESIDUAL)
+            FTX_HIP(ctx, launch_accept_residual(st, ad, res_scratch));
+        else
+            FTX_HIP(ctx, launch_accept(st, ad));
+        ts.end(TK_ACCEPT, (double)V * 4);
+    }
     FTX_HIP(ctx, hipMemcpyAsync(pin, d_small, head_b, hipMemcpyDeviceToHost, st));
     if (a->mode == FTX_ACCEPT_RESIDUAL && accept_residual_error(res_scratch, st, &bar_err))
         return ftx_fail(ctx, FTX_E_DEVICE, "acceptance: copy of the barrier state failed");

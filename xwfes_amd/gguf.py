@@ -465,11 +465,12 @@ def write_gguf(path, kv, tensors, alignment=32, version=3):
             pos = o + len(data)
 
 
-def model_kv(cfg, arch="llama", tokens=None, float_eps=True):
+def model_kv(cfg, arch="llama", tokens=None, float_eps=True, eos=None):
     """Metadata for a model of `cfg` (pyoracle.model_cfg keys).  The
     epsilon is written as a float, as GGUF converters write it (the
     reference then keeps its default), or as an integer key when
-    float_eps is False."""
+    float_eps is False; eos: the tokenizer's end-of-sequence id
+    (tokenizer.ggml.eos_token_id), none when None."""
     a = arch
     kv = [("general.architecture", T_STR, a),
           (a + ".block_count", T_U32, cfg["n_layer"]),
@@ -490,6 +491,8 @@ def model_kv(cfg, arch="llama", tokens=None, float_eps=True):
         tokens = ["<t%d>" % i for i in range(cfg["vocab"])]
     kv.append(("tokenizer.ggml.model", T_STR, "llama"))
     kv.append(("tokenizer.ggml.tokens", T_ARR, (T_STR, tokens)))
+    if eos is not None:
+        kv.append(("tokenizer.ggml.eos_token_id", T_U32, int(eos)))
     return kv
 
 

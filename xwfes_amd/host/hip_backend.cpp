@@ -375,7 +375,7 @@ void cut_draft(std::vector<int32_t>& props, std::vector<float>& probs) {
 std::vector<int32_t> generate(HipVerifier& target, DraftModelDrafter& drafter,
                               const std::vector<int32_t>& prompt, int64_t max_new, int spec_k,
                               float temp, int32_t top_k, float top_p, uint64_t seed,
-                              GenerateStats* stats) {
+                              GenerateStats* stats, int32_t eos) {
     HipBackend& be = target.backend();
     const int64_t V = target.config().vocab;
     constexpr int64_t chunk = 8;
@@ -392,8 +392,9 @@ std::vector<int32_t> generate(HipVerifier& target, DraftModelDrafter& drafter,
         std::vector<int32_t> history = prompt;
         uint64_t rsamp = seed ? seed : 88172645463325252ull;  // src/spec.cpp:259
         target.sampler.state = seed ? seed : 0x9E3779B97F4A7C15ull;
-        // temp <= 0: the ratio test at T = 1 and a top-1 bonus (the argmax)
-        const float acc_temp = temp > 0.f ? temp : 1.f;
+        // the ratio test at T = 1 (src/spec.cpp:216); temp <= 0: a top-1
+        // bonus (the argmax)
+        const float acc_temp = 1.f;
         target.sampler.top_k = temp > 0.f ? top_k : 1;
         target.sampler.top_p = temp > 0.f ? top_p : 1.f;
         std::vector<int32_t> props;
@@ -412,14 +413,33 @@ std::vector<int32_t> generate(HipVerifier& target, DraftModelDrafter& drafter,
                 stats->drafted += (int64_t)props.size();
                 stats->accepted += acc;
             }
-            // a round is emitted whole (src/spec.cpp:314-322)
-            for (int64_t i = 0; i < acc; ++i) out.push_back(props[(size_t)i]);
-            out.push_back(r.bonus);
+            if (props.empty() && r.bonus == eos) {  // an empty draft's sampled token
+                out.push_back(r.bonus);
+                if (stats) stats->hit_eos = true;
+                break;
+            }
+            // a round is emitted whole (src/spec.cpp:314-322), every accepted
+            // token even past an eos among them
+            bool eos_acc = false;
+            for (int64_t i = 0; i < acc; ++i) {
+                out.push_back(props[(size_t)i]);
+                eos_acc |= eos >= 0 && props[(size_t)i] == eos;
+            }
             history.insert(history.end(), props.begin(), props.begin() + acc);
+            if (eos_acc) {
+                drafter.on_commit(acc);
+                if (stats) stats->hit_eos = true;
+                break;
+            }
+            out.push_back(r.bonus);
             history.push_back(r.bonus);
             // one target step on the bonus: the next round's base row
             target.step(r.bonus, base);
             drafter.on_commit(acc);
+            if (r.bonus == eos) {
+                if (stats) stats->hit_eos = true;
+                break;
+            }
         }
     } catch (...) {
         ftx_free_staging(be.ctx(), base);

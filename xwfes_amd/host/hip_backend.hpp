@@ -287,6 +287,7 @@ void cut_draft(std::vector<int32_t>& props, std::vector<float>& probs);
 
 struct GenerateStats {
     int64_t rounds = 0, drafted = 0, accepted = 0;
+    bool hit_eos = false;
 };
 
 // generate's speculative block (src/spec.cpp:245-333) on the device-resident
@@ -295,11 +296,17 @@ struct GenerateStats {
 // row after the last accepted token (Sampler::sample with its state carried
 // over in target.sampler; temp <= 0: the argmax) -> truncate -> one target
 // step on the bonus, until at least max_new tokens are out (a round is
-// emitted whole).  The acceptance test takes the target at temp (T = 1 for
-// temp <= 0).  Returns the generated tokens.
+// emitted whole) or the end-of-sequence token eos (the GGUF's
+// tokenizer.ggml.eos_token_id, -1 for none) ends it as the reference's loop
+// does (316-328): an accepted draft token equal to eos ends it once every
+// accepted token is out (no bonus), a bonus equal to eos is emitted and
+// stepped, the sampled token of an empty draft is emitted.  The acceptance
+// test takes the target at T = 1 whatever temp is (accept_chain_sampling,
+// src/spec.cpp:216); temp shapes the bonus.  Returns the generated tokens.
 std::vector<int32_t> generate(HipVerifier& target, DraftModelDrafter& drafter,
                               const std::vector<int32_t>& prompt, int64_t max_new, int spec_k = 8,
                               float temp = 0.f, int32_t top_k = 40, float top_p = 0.95f,
-                              uint64_t seed = 0, GenerateStats* stats = nullptr);
+                              uint64_t seed = 0, GenerateStats* stats = nullptr,
+                              int32_t eos = -1);
 
 }  // namespace ftx_host

@@ -13,9 +13,10 @@ The bonus is drawn from the row after the last accepted token (the reference
 uses rows[min(acc, k - 1)], the next token's row only when every draft token
 is accepted) by the reference's Sampler (temperature, top-k, top-p, its
 state carried over); temp <= 0 takes the argmax, as Sampler::sample does.
-The acceptance test takes the target at temperature temp for temp > 0 (the
-reference uses T = 1 whatever temp is: equal at temp = 1) and at T = 1 for
-temp <= 0.
+The acceptance test takes the target at T = 1 whatever temp is, as
+accept_chain_sampling does (src/spec.cpp:216).  An end-of-sequence token
+(the GGUF's tokenizer.ggml.eos_token_id) ends the loop as the reference's
+does (src/spec.cpp:316-328).
 """
 import numpy as np
 
@@ -98,12 +99,15 @@ def cut_draft(props, probs):
 
 
 def generate(ctx, target, kv, drafter, prompt, max_new, spec_k=8, temp=0.0, top_k=40,
-             top_p=0.95, seed=0):
+             top_p=0.95, seed=0, eos=-1):
     """Speculative generation after `prompt` (the target cache starts
-    empty) until at least max_new tokens are out; a round's accepted tokens
-    and bonus are emitted together, so the last round may go past max_new
-    (as the reference's does).  No end-of-sequence token.  Returns (tokens,
-    stats)."""
+    empty) until at least max_new tokens are out or eos (-1: none) ends it;
+    a round's accepted tokens and bonus are emitted together, so the last
+    round may go past max_new (as the reference's does).  eos: an accepted
+    draft token equal to it ends the loop once every accepted token is out
+    (no bonus), a bonus equal to it is emitted and stepped, the sampled
+    token of an empty draft is emitted (src/spec.cpp:287-295, 316-328).
+    Returns (tokens, stats)."""
     V = target.cfg["vocab"]
     kv.truncate(0)
     if not 1 <= spec_k <= 8:
@@ -118,10 +122,11 @@ def generate(ctx, target, kv, drafter, prompt, max_new, spec_k=8, temp=0.0, top_
     out = []
     rsamp = seed if seed else 88172645463325252  # src/spec.cpp:259
     sstate = seed if seed else ftx.SAMPLER_SEED
-    # temp <= 0: the ratio test at T = 1 and a top-1 bonus (the argmax)
-    acc_temp = temp if temp > 0 else 1.0
+    # the ratio test at T = 1 (src/spec.cpp:216); temp <= 0: a top-1 bonus
+    # (the argmax)
+    acc_temp = 1.0
     bk, bp = (top_k, top_p) if temp > 0 else (1, 1.0)
-    stats = dict(rounds=0, drafted=0, accepted=0)
+    stats = dict(rounds=0, drafted=0, accepted=0, hit_eos=False)
     try:
         while len(out) < max_new:
             props, probs = drafter.draft(history, spec_k)
@@ -135,16 +140,30 @@ def generate(ctx, target, kv, drafter, prompt, max_new, spec_k=8, temp=0.0, top_
                            sampler_state=sstate, top_k=bk, top_p=bp)
             rsamp, sstate = r["rng"], r["sampler_state"]
             acc = len(r["accepted"])
+            bonus = r["bonus"]
             kv.truncate(np_before + acc)
-            new = list(props[:acc]) + [r["bonus"]]
             stats["rounds"] += 1
             stats["drafted"] += M
             stats["accepted"] += acc
-            out += new  # a round is emitted whole (src/spec.cpp:314-322)
-            history += new
+            if M == 0 and bonus == eos:  # an empty draft's sampled token
+                out.append(bonus)
+                stats["hit_eos"] = True
+                break
+            # a round is emitted whole (src/spec.cpp:314-322)
+            out += list(props[:acc])
+            history += list(props[:acc])
+            if eos >= 0 and eos in props[:acc]:
+                drafter.on_commit(acc)
+                stats["hit_eos"] = True
+                break
+            out.append(bonus)
+            history.append(bonus)
             # one target step on the bonus token: the next round's base row
-            target.step(kv, r["bonus"], base.ptr)
+            target.step(kv, bonus, base.ptr)
             drafter.on_commit(acc)
+            if bonus == eos:
+                stats["hit_eos"] = True
+                break
     finally:
         base.free()
         rows.free()
