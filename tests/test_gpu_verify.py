@@ -267,12 +267,14 @@ def tree_parents(branching):
     return parents
 
 
-def test_verify_8b_tree52_q8_attention(gctx, orc):
+@pytest.mark.parametrize("nodes", [52, 32])
+def test_verify_8b_tree52_q8_attention(gctx, orc, nodes):
     """The tree workload's shape: 8B layers (d 4096, 32/8 heads x 128, FFN
     14336) with Q8_0 attention projections and a Q4_K FFN, 2 layers, a
-    52-node draft tree (branching 4, 4, 2) at context 4096, then residual
-    acceptance of the device's logits against the oracle's on the same rows,
-    over the full Llama-3 vocabulary (128256) with a Q6_K head."""
+    52-node draft tree (branching 4, 4, 2) -- and the same tree pruned to
+    its first 32 nodes in breadth-first order -- at context 4096, then
+    residual acceptance of the device's logits against the oracle's on the
+    same rows, over the full Llama-3 vocabulary (128256) with a Q6_K head."""
     orc.set_threads(16)
     V = 128256
     cfg = P.model_cfg(2, 4096, 32, 8, 128, 14336, V, rope_theta=500000.0)
@@ -294,13 +296,13 @@ def test_verify_8b_tree52_q8_attention(gctx, orc):
             model[p + nm] = q(rows, cols, P.Q8_0)
         for nm in ("gate", "up", "down"):
             model[p + nm] = q(14336, 4096, P.Q4_K)
-    parents = tree_parents((4, 4, 2))
-    assert len(parents) == 52
-    toks = rng.integers(0, V, 52).tolist()
+    parents = tree_parents((4, 4, 2))[:nodes]
+    assert len(parents) == nodes and all(p < i for i, p in enumerate(parents))
+    toks = rng.integers(0, V, nodes).tolist()
     got, want, _, _ = run_both(gctx, orc, model, toks, 4096, 4096 + 64, parents=parents)
     assert rel_err_rows(got, want) < LOGIT_TOL
     base = (rng.standard_normal(V) * 2).astype(np.float32)
-    qd = rng.dirichlet(np.ones(V), size=52).astype(np.float32)
+    qd = rng.dirichlet(np.ones(V), size=nodes).astype(np.float32)
     props = np.array(toks, np.int32)
     g, o = accept_both(gctx, orc, base, got, props, ftx.ACCEPT_RESIDUAL, 0.8, 77,
                        parents=parents, q=qd)
