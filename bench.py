@@ -23,6 +23,7 @@ ROOT = os.path.dirname(os.path.abspath(__file__))
 sys.path.insert(0, ROOT)
 
 HBM_PEAK_GBS = 8000.0
+MFMA_PEAK_TFLOPS = 2500.0  # dense fp16 / bf16 MFMA (no sparsity)
 REPLAY = 20  # back-to-back issues of each dominant-class launch when timing it
 LLAMA3_8B = dict(n_layer=32, n_embd=4096, n_head=32, n_head_kv=8, head_dim=128, n_ff=14336,
                 vocab=128256, rope_theta=500000.0, rope_neox=0, rms_eps=1e-5)
@@ -61,6 +62,11 @@ WORKLOADS = {
     # Q4_K FFN
     "llama3-8b-q8attn-tree52-ctx4096": dict(kind="tree", cfg=LLAMA3_8B, mix="q8_0_attn", ctx=4096,
                                             M=52, branching=(4, 4, 2), temp=0.8),
+    # the same tree pruned to its first 32 nodes in breadth-first order (4 +
+    # 16 + the children of the first 6 second-level nodes): the 32-node draft
+    # tree of branching (4, 4, 2)
+    "llama3-8b-q8attn-tree32-ctx4096": dict(kind="tree", cfg=LLAMA3_8B, mix="q8_0_attn", ctx=4096,
+                                            M=32, branching=(4, 4, 2), temp=0.8),
     # batch: `seqs` sequences verified in one step (ftx_verify_batch), each
     # against its own cache at context ctx, then accepted one by one.
     # Mixtral-8x7B-shaped Q4_0 MoE (8 experts top-2, all resident), 8-token
@@ -92,10 +98,11 @@ def mix_of(name, cfg):
             "q4_k": lambda: synth.uniform_mix(synth.Q4_K)}[name]()
 
 
-def draft_tree(V, branching, seed):
+def draft_tree(V, branching, seed, nodes=None):
     """A full draft tree (nodes in breadth-first order, parents[i] < i): each
     node's children are drawn from one Dirichlet(1) distribution over the
-    vocab, which is every child's q row."""
+    vocab, which is every child's q row.  nodes: keep the first `nodes`
+    nodes (a pruned tree: every kept node's parent is kept)."""
     rng = np.random.default_rng(seed)
     parents, props, q = [], [], []
     level = [-1]
@@ -111,8 +118,9 @@ def draft_tree(V, branching, seed):
                 q.append(dist)
                 nxt.append(len(parents) - 1)
         level = nxt
-    return (np.array(parents, np.int32), np.array(props, np.int32),
-            np.ascontiguousarray(np.stack(q)))
+    n = len(parents) if nodes is None else nodes
+    return (np.array(parents[:n], np.int32), np.array(props[:n], np.int32),
+            np.ascontiguousarray(np.stack(q[:n])))
 
 
 def random_tree(V, n, max_depth, max_branch, seed):
@@ -233,51 +241,114 @@ def cpu_threads():
     return n if n > 0 else len(os.sched_getaffinity(0))
 
 
-def cpu_baseline(ctx, tensors, cfg, ctx_len, M, props, threads, layers=(1, 2)):
-    """The oracle's reference loop nest (CpuBackend::matmul, matmul_down_axpy,
-    Impl::attn) timed on this host on a bounded sample: 1-layer and 2-layer
-    forwards of the same weights (layer 0, tok_embd, output) at the same M and
-    context, extrapolated linearly to all layers (layers=(1,): the 1-layer
-    forward and L - 1 more layers at the 1-layer model's per-layer share,
-    measured separately by the caller)."""
+def host_model(ctx, tensors, cfg, n_layer):
+    """Host copies of tok_embd, out_norm, output and layer 0's tensors (any
+    roles, dense or MoE), with every one of n_layer layers taking layer 0's
+    tensors: the oracle's model dict of a bounded sample of the step."""
     sys.path.insert(0, os.path.join(ROOT, "oracle"))
-    import pyoracle as P
-    orc = P.Oracle()
-    orc.set_threads(threads)
 
     def host(t):
         raw = np.empty(t.nbytes, np.uint8)
         ctx.copy(raw.ctypes.data, t.ptr, t.nbytes)
-        return dict(raw=raw, dtype=t.dtype, ne0=t.ne[0], ne1=t.ne[1])
+        return dict(raw=raw, dtype=t.dtype, ne0=t.ne[0], ne1=int(np.prod(t.ne[1:])))
 
-    base = {k: host(tensors[k]) for k in ("tok_embd", "output", "out_norm")}
-    layer0 = {nm: host(tensors["blk.0." + nm]) for nm in P.LAYER_TENSORS}
+    base = {k: host(tensors[k]) for k in ("tok_embd", "output", "out_norm") if k in tensors}
+    layer0 = {n[len("blk.0."):]: host(t) for n, t in tensors.items() if n.startswith("blk.0.")}
+    model = dict(base)
+    model["cfg"] = dict(cfg, n_layer=n_layer)
+    for l in range(n_layer):
+        for nm, t in layer0.items():
+            model["blk.%d.%s" % (l, nm)] = t
+    return model
+
+
+def cpu_baseline(ctx, tensors, cfg, ctx_len, M, props, threads, layers=(1, 2), parents=None):
+    """The oracle's reference loop nest (CpuBackend::matmul, matmul_down_axpy,
+    Impl::attn, moe_ffn) timed on this host on a bounded sample: 1-layer and
+    2-layer forwards of the same weights (layer 0, tok_embd, output) at the
+    same tokens (a tree through its parent array) and context, one
+    sequence; the caller extrapolates to all layers (and sequences)."""
+    sys.path.insert(0, os.path.join(ROOT, "oracle"))
+    import pyoracle as P
+    orc = P.Oracle()
+    orc.set_threads(threads)
     kdim = cfg["n_head_kv"] * cfg["head_dim"]
     rng = np.random.default_rng(4)
     times = {}
     for nl in layers:
-        model = dict(base)
-        model["cfg"] = dict(cfg, n_layer=nl)
-        for l in range(nl):
-            for nm in P.LAYER_TENSORS:
-                model["blk.%d.%s" % (l, nm)] = layer0[nm]
+        model = host_model(ctx, tensors, cfg, nl)
         cap = ctx_len + M
         k = rng.standard_normal((nl, cap, kdim)).astype(np.float16)
         v = rng.standard_normal((nl, cap, kdim)).astype(np.float16)
         orc.forward(model, k, v, ctx_len, props[:1])  # warm caches and threads
         t0 = time.perf_counter()
-        orc.forward(model, k, v, ctx_len, props)
+        orc.forward(model, k, v, ctx_len, props, parents=parents)
         times[nl] = time.perf_counter() - t0
+        del model
     return times
 
 
-def cpu_summary(times, cfg, M, ctx_len, threads):
+def cpu_summary(times, cfg, M, ctx_len, threads, nseq=1):
     t_layer = max(times[2] - times[1], 0.0)
-    t_step = times[1] + (cfg["n_layer"] - 1) * t_layer
+    t_step = (times[1] + (cfg["n_layer"] - 1) * t_layer) * nseq
     return t_step, t_layer, ("oracle forward of M=%d tokens at ctx %d over 1 and 2 layers of the "
                              "same weights (%.2f s, %.2f s) on %d threads, extrapolated to %d "
-                             "layers: %.3f s/step" % (M, ctx_len, times[1], times[2], threads,
-                                                      cfg["n_layer"], t_step))
+                             "layers%s: %.3f s/step" % (
+                                 M, ctx_len, times[1], times[2], threads, cfg["n_layer"],
+                                 (" and x %d sequences (one Engine each, run one after another)"
+                                  % nseq) if nseq > 1 else "", t_step))
+
+
+def cpu_generate_baseline(ctx, tensors, dtensors, cfg, dcfg, prompt, N, M, threads):
+    """The oracle's generate (src/spec.cpp:245-333 with a DraftModelDrafter)
+    over host copies of the same target and draft models, run whole on this
+    host: generated tokens per second."""
+    sys.path.insert(0, os.path.join(ROOT, "oracle"))
+    import pyoracle as P
+    orc = P.Oracle()
+    orc.set_threads(threads)
+
+    def full(ts, c):
+        m = {}
+        for n, t in ts.items():
+            raw = np.empty(t.nbytes, np.uint8)
+            ctx.copy(raw.ctypes.data, t.ptr, t.nbytes)
+            m[n] = dict(raw=raw, dtype=t.dtype, ne0=t.ne[0], ne1=int(np.prod(t.ne[1:])))
+        m["cfg"] = dict(c)
+        return m
+
+    target, draft = full(tensors, cfg), full(dtensors, dcfg)
+    cap = len(prompt) + N + 32
+    t0 = time.perf_counter()
+    out, st = orc.generate(target, draft, prompt, N, spec_k=M, temp=0.0, cap=cap)
+    dt = time.perf_counter() - t0
+    return len(out) / dt, ("oracle generate of %d tokens after a %d-token prompt, %d draft tokens "
+                           "a round, greedy, whole run %.2f s on %d threads (%d rounds)" % (
+                               len(out), len(prompt), M, dt, threads, st["rounds"]))
+
+
+def class_flops(kernel_class, cfg, tokens):
+    """Algorithmic flops of one launch of a GEMM kernel class (one layer's
+    projection, or the LM head) over `tokens` tokens: 2 x tokens x the
+    weight elements it contracts; None for other classes."""
+    d, F, V = cfg["n_embd"], cfg["n_ff"], cfg["vocab"]
+    qd, kd = cfg["n_head"] * cfg["head_dim"], cfg["n_head_kv"] * cfg["head_dim"]
+    w = {"gemv_qkv": (qd + 2 * kd) * d, "gemv_o": d * qd, "gemv_swiglu": 2 * F * d,
+         "down": F * d, "head": V * d}.get(kernel_class)
+    return None if w is None else 2.0 * tokens * w
+
+
+def step_flops(cfg, M, nseq, ctx_len):
+    """Algorithmic flops of a verify step: 2 x tokens x every weight element
+    the step contracts (the projections of every layer and the LM head; the
+    embedding is a lookup) plus attention's 4 x rows x head_dim x slots per
+    head and sequence."""
+    d, F, V, L = cfg["n_embd"], cfg["n_ff"], cfg["vocab"], cfg["n_layer"]
+    qd, kd = cfg["n_head"] * cfg["head_dim"], cfg["n_head_kv"] * cfg["head_dim"]
+    ffn = 3 * F * d * (cfg.get("n_expert_used", 0) or 1)
+    w = L * ((qd + 2 * kd) * d + d * qd + ffn) + V * d
+    attn = 4.0 * M * cfg["n_head"] * cfg["head_dim"] * (ctx_len + M) * L
+    return 2.0 * M * nseq * w + attn * nseq
 
 
 def measured_traffic(workload, kernel_class):
@@ -362,7 +433,7 @@ def main():
     props, pd = draft(V, M, seed=6)
     parents = qbuf = None
     if kind == "tree":
-        parents, props, qrows = draft_tree(V, W["branching"], seed=6)
+        parents, props, qrows = draft_tree(V, W["branching"], seed=6, nodes=M)
         assert len(props) == M
         qbuf = ctx.buffer(qrows.nbytes)
         qbuf.write(qrows)
@@ -511,8 +582,8 @@ def main():
     gbs = sb / (ms_step * 1e-3) / 1e9
     metric = {"verify": "verify-step tokens/s + HBM GB/s (% of peak), 8B-shape Q4_K, K=8 draft, "
                         "1 GPU",
-              "tree": "tree verify-step tokens/s + HBM GB/s (% of peak), 8B-shape Q8_0 attention "
-                      "/ Q4_K FFN, 52-node draft tree, ctx 4096, 1 GPU",
+              "tree": "tree verify-step tokens/s + HBM GB/s (%% of peak), 8B-shape Q8_0 attention "
+                      "/ Q4_K FFN, %d-node draft tree, ctx 4096, 1 GPU" % M,
               "decode": "decode tokens/s (Engine::step, M=1, ctx 2048), 8B-shape Q4_K, 1 GPU",
               "batch": "batched verify-step tokens/s + HBM GB/s (%% of peak), %s, %d sequences x "
                        "%s, ctx %d, 1 GPU" % (
@@ -570,22 +641,54 @@ def main():
                      "traffic": measured_traffic(args.workload, dom_name)},
         "cpu_baseline": None,
     }
-    if not args.no_cpu_baseline and kind == "verify":
+    if kind in ("verify", "tree", "batch"):
+        sf = step_flops(cfg, M, nseq, ctx_len)
+        out["step_tflops"] = round(sf / (ms_step * 1e-3) / 1e12, 2)
+        out["step_mfma_frac"] = round(sf / (ms_step * 1e-3) / 1e12 / MFMA_PEAK_TFLOPS, 4)
+    # the 70B batch of trees is MFMA-bound (256 tokens: ~910 flop per weight
+    # byte against the fp16 ridge of 2.5 PF / 8 TB/s = 312): its roofline is
+    # the dominant GEMM's algorithmic flops per launch over its in-step
+    # launch time against the dense fp16 MFMA peak (the one-pass GEMMs run
+    # v_mfma_f32_16x16x32_f16)
+    cf = class_flops(dom_name, cfg, tokens)
+    if kind == "batch" and W.get("tree") and cf:
+        tf = cf / (per_launch_ms * 1e-3) / 1e12
+        hbm = out["roofline"]
+        out["roofline"] = {"bound": "mfma", "kernel": dom_name, "achieved": round(tf, 1),
+                           "peak": MFMA_PEAK_TFLOPS, "unit": "TFLOP/s",
+                           "frac": round(tf / MFMA_PEAK_TFLOPS, 4), "flops_per_launch": cf,
+                           "us_per_launch": hbm["us_per_launch"], "source": hbm["source"],
+                           "hbm_gbs_of_that_launch": hbm["achieved"],
+                           "bytes_per_launch": per_launch_b, "traffic": hbm["traffic"]}
+    if not args.no_cpu_baseline and kind in ("verify", "tree", "batch"):
         threads = cpu_threads()
         t0 = time.perf_counter()
-        times = cpu_baseline(ctx, tensors, cfg, ctx_len, M, props, threads)
-        t_step, t_layer, sample = cpu_summary(times, cfg, M, ctx_len, threads)
+        par = parents
+        pr = props
+        if kind == "batch":
+            pr, par = bdraft[0]["props"], bdraft[0]["parents"]
+        times = cpu_baseline(ctx, tensors, cfg, ctx_len, M, pr, threads, parents=par)
+        t_step, t_layer, sample = cpu_summary(times, cfg, M, ctx_len, threads, nseq=nseq)
         # one thread: the 1-layer forward, the per-layer time scaled by the
         # multi-thread run's layer / 1-layer ratio (the layer work splits
         # over threads the same way as the head's)
-        t1 = cpu_baseline(ctx, tensors, cfg, ctx_len, M, props, 1, layers=(1,))[1]
+        t1 = cpu_baseline(ctx, tensors, cfg, ctx_len, M, pr, 1, layers=(1,), parents=par)[1]
         t_step1 = t1 * t_step / times[1]
         out["cpu_baseline"] = dict(
-            value=round(M / t_step, 3), unit="verified tokens/s", cores=threads, kind="port",
-            sample=sample, single_thread_value=round(M / t_step1, 4),
+            value=round(tokens / t_step, 3), unit=unit, cores=threads, kind="port",
+            sample=sample, single_thread_value=round(tokens / t_step1, 4),
             single_thread_sample="1-layer forward on 1 thread %.2f s, scaled by the %d-thread "
                                  "step / 1-layer ratio" % (t1, threads),
             nproc=os.cpu_count(), cpu_model=cpu_model())
+        log("cpu baseline in %.1f s" % (time.perf_counter() - t0))
+    elif not args.no_cpu_baseline and kind == "generate" and cfg["n_layer"] * cfg["n_embd"] <= 8192:
+        # the reference's own CPU-runnable case: the whole generate on the host
+        threads = cpu_threads()
+        t0 = time.perf_counter()
+        tps, sample = cpu_generate_baseline(ctx, tensors, dtensors, cfg, W["draft_cfg"], prompt,
+                                            W["N"], M, threads)
+        out["cpu_baseline"] = dict(value=round(tps, 3), unit=unit, cores=threads, kind="port",
+                                   sample=sample, nproc=os.cpu_count(), cpu_model=cpu_model())
         log("cpu baseline in %.1f s" % (time.perf_counter() - t0))
     print(json.dumps(out), flush=True)
     if drafter is not None:
