@@ -778,26 +778,42 @@ struct MmDownArgs {
     MmOutDev out;
 };
 
-// grid = (N / 256 x Mp / 64, 1, splits); block = 512: waves w and w + 4 own
-// columns 256 bx + 64 (w % 4) .. + 63 (four 16-column tiles ct), for tokens
-// 0-31 and 32-63 (two waves per SIMD, so that one wave's staging VALU and
-// LDS waits overlap the other's MFMAs: 7% faster than one wave per SIMD on
-// the tree and 70B shapes); per 32-row slice the workgroup stages, for its
-// 64 tokens, A_d = h d 2^10 and A_m = h dmin 2^10 (hi / lo) and the fp16
-// tables sc[s][i], mn[s][i] of the block's 8 sub-blocks; y = (sum_i A_d sc q
-// - sum_i A_m mn) / 2^10 with the min term (one 16-column MFMA tile whose
-// columns are the sub-blocks) done by wave w < 4 for tokens 16 w .. 16 w + 15
-// and handed to the other waves through LDS.
+// grid = (N / 256 x Mp / 64, 1, splits); block = 512: wave w owns columns
+// 256 bx + 32 w .. + 31 (two 16-column tiles ct, all in sub-block w of the
+// block) for all 64 tokens, so that each weight operand is built once and
+// feeds eight MFMAs; per 32-row slice the workgroup stages, for its 64
+// tokens, A_d = h d 2^10 and A_m = h dmin 2^10 (hi / lo) and the fp16 tables
+// of the block's 8 sub-block scales (also as -1024 sc) and 8 mins, one
+// table entry per thread; y = (sum_i A_d sc q - sum_i A_m mn) / 2^10 with
+// the min term (one 16-column MFMA tile whose columns are the sub-blocks)
+// done by wave w < 4 for tokens 16 w .. 16 w + 15 and handed to the other
+// waves through LDS.
 constexpr int MMD_PITCH = 32 + 8;
-constexpr int MMD_WAVES = 8;  // two per SIMD: waves w and w + 4 share columns, split the tokens
-constexpr int MMD_MS = MM_MS / 2;  // 16-token tiles per wave
+constexpr int MMD_WAVES = 8;  // two per SIMD
 constexpr int MMD_RING = 4;  // slices whose global operands are in flight (even: LDS buffer = slice parity)
+
+// 8 nibbles (slot t: byte t % 4, nibble t / 4) -> fp16 sc_t q_t, exact:
+// (1024 + q) sc + (-1024 sc) in one fused multiply-add per pair
+__device__ __forceinline__ v8h nib8_sc(uint32_t w, const v8h& sc, const v8h& sn) {
+    const uint32_t lo = w & 0x0F0F0F0Fu, hi = (w >> 4) & 0x0F0F0F0Fu;
+    v2h p[4];
+    p[0] = __builtin_bit_cast(v2h, __builtin_amdgcn_perm(lo, 0x64646464u, 0x00050004u));
+    p[1] = __builtin_bit_cast(v2h, __builtin_amdgcn_perm(lo, 0x64646464u, 0x00070006u));
+    p[2] = __builtin_bit_cast(v2h, __builtin_amdgcn_perm(hi, 0x64646464u, 0x00050004u));
+    p[3] = __builtin_bit_cast(v2h, __builtin_amdgcn_perm(hi, 0x64646464u, 0x00070006u));
+#pragma unroll
+    for (int i = 0; i < 4; ++i)
+        p[i] = __builtin_elementwise_fma(p[i], v2h{sc[2 * i], sc[2 * i + 1]},
+                                         v2h{sn[2 * i], sn[2 * i + 1]});
+    return v8h{p[0][0], p[0][1], p[1][0], p[1][1], p[2][0], p[2][1], p[3][0], p[3][1]};
+}
+
 __global__ void __launch_bounds__(64 * MMD_WAVES) __attribute__((amdgpu_waves_per_eu(2, 2)))
 k_mm_down(MmDownArgs a) {
     __shared__ _Float16 ad[2][2][MM_TOK][MMD_PITCH];  // [buf][hi / lo][token][row i]
     __shared__ _Float16 am[2][2][MM_TOK][MMD_PITCH];
-    __shared__ _Float16 tsc[2][8][MMD_PITCH];          // [buf][sub-block][row i]
-    __shared__ _Float16 tmn[2][8][MMD_PITCH];
+    __shared__ _Float16 tsm[2][16][MMD_PITCH];         // [buf][sc of sub-block 0-7, mn 0-7][row i]
+    __shared__ _Float16 tsn[2][16][MMD_PITCH];         // [buf][-1024 sc (rows 8-15 unused)][row i]
     __shared__ float mins[MM_TOK][9];                  // [token][sub-block]
     const int tid = threadIdx.x, lane = tid & 63;
     const int w = __builtin_amdgcn_readfirstlane(tid >> 6);
@@ -810,44 +826,52 @@ k_mm_down(MmDownArgs a) {
     const int64_t nsl = a.n_in / 32, nc64 = a.N / 64;
     const int64_t I0 = (int64_t)ks * a.slices_per_split;
     const int64_t I1 = min(I0 + (int64_t)a.slices_per_split, nsl);
-    const int cw = w & 3, th = w >> 2;  // column group, token half
-    const int64_t C = jb * 4 + cw;
 
-    // staging: thread t takes token sm = t / 4 and rows 8 sp .. 8 sp + 7 of
-    // the slice (h of tokens past M is zero).  A slice's global operands (h,
-    // the rows' d / dmin, the headers, each wave's nibbles) go to one of
-    // MMD_RING register slots MMD_RING slices ahead of its use, so that the
-    // loads of several slices are in flight while one is computed.
+    // staging: thread t takes token sm = t / 8 and rows 4 sp .. 4 sp + 3 of
+    // the slice (h of tokens past M is zero), and table entry (row t / 16,
+    // value t % 16: sub-block scale 0-7, then min 0-7).  A slice's global
+    // operands (h, the rows' d / dmin, the header words, each wave's
+    // nibbles) go to one of MMD_RING register slots MMD_RING slices ahead of
+    // its use, so that the loads of several slices are in flight while one
+    // is computed.  Per slice the bases move by uniform strides; the lanes'
+    // offsets are fixed 32-bit values.
     const int sm = tid >> 3, sp = tid & 7;
+    const int trow = tid >> 4, tv = tid & 15, ts = tv & 7, tmn = tv >> 3;
     const bool tok_ok = m0 + sm < a.M;
-    const float* hrow = a.h + (tok_ok ? m0 + sm : 0) * a.ldh;
+    const float hscale = tok_ok ? MMD_ASCALE : 0.f;
+    const uint32_t h_off = (uint32_t)(((tok_ok ? m0 + sm : 0) * a.ldh + 4 * sp) * 4);
+    const uint32_t d_off = (uint32_t)(4 * sp * 16);
+    const uint32_t t_off = (uint32_t)(trow * 16);
+    const uint32_t q_off = (uint32_t)(((((w >> 1) * 4 + kq) * 16 + col) * 16) + 8 * (w & 1));
+    const uint8_t* hb = (const uint8_t*)a.h;
+    const uint8_t* db = a.hdr + jb * a.n_in * 16;
+    const uint8_t* qb = a.qs + jb * 4 * 4 * 16 * 16;
+    const int64_t q_stride = nc64 * 4 * 16 * 16;
     struct Slot {
-        float hv[4];
+        float4 hv;
         uint32_t dw[4];  // d | dmin << 16 of rows 4 sp + e
-        v4i hq;          // threads t < 32: the header of row t (scales / mins)
-        v4i wq;          // this wave's nibbles of the slice
+        uint32_t ta, tb; // table entry: scale (S0) or min (S1) word, and S2 word
+        v2i wq;          // this wave's nibbles of the slice (two column tiles)
     };
     auto issue = [&](Slot& o, int64_t I) {
-        const int64_t i0 = I * 32 + 4 * sp;
-        const float4 h0 = *(const float4*)(hrow + i0);
-        o.hv[0] = h0.x; o.hv[1] = h0.y; o.hv[2] = h0.z; o.hv[3] = h0.w;
+        o.hv = *(const float4*)(hb + I * 128 + h_off);
+        const uint8_t* dI = db + I * 512;
 #pragma unroll
-        for (int e = 0; e < 4; ++e) o.dw[e] = *(const uint32_t*)(a.hdr + (jb * a.n_in + i0 + e) * 16);
-        o.hq = *(const v4i*)(a.hdr + (jb * a.n_in + I * 32 + (tid & 31)) * 16);
-        const int64_t blk = (I * nc64 + C) * 4 + kq;
-        o.wq = *(const v4i*)(a.qs + (blk * 16 + col) * 16);
+        for (int e = 0; e < 4; ++e) o.dw[e] = *(const uint32_t*)(dI + d_off + e * 16);
+        o.ta = *(const uint32_t*)(dI + t_off + 4 + 4 * tmn);
+        o.tb = *(const uint32_t*)(dI + t_off + 12);
+        o.wq = *(const v2i*)(qb + I * q_stride + q_off);
     };
     auto stage_store = [&](const Slot& o, int buf) {
-#pragma clang fp contract(off)
+        const float hv[4] = {o.hv.x * hscale, o.hv.y * hscale, o.hv.z * hscale, o.hv.w * hscale};
         v4h dh, dl, mh, ml;
 #pragma unroll
         for (int e = 0; e < 4; e += 2) {
             float pd[2], pm[2];
 #pragma unroll
             for (int i = 0; i < 2; ++i) {
-                const float hvv = tok_ok ? o.hv[e + i] : 0.f;
-                pd[i] = hvv * h2f((uint16_t)(o.dw[e + i] & 0xFFFF)) * MMD_ASCALE;
-                pm[i] = hvv * h2f((uint16_t)(o.dw[e + i] >> 16)) * MMD_ASCALE;
+                pd[i] = hv[e + i] * h2f((uint16_t)(o.dw[e + i] & 0xFFFF));
+                pm[i] = hv[e + i] * h2f((uint16_t)(o.dw[e + i] >> 16));
             }
             v2h h, l;
             split_hl2(pd[0], pd[1], h, l);
@@ -865,49 +889,52 @@ k_mm_down(MmDownArgs a) {
         *(v4h*)&ad[buf][1][sm][4 * sp] = dl;
         *(v4h*)&am[buf][0][sm][4 * sp] = mh;
         *(v4h*)&am[buf][1][sm][4 * sp] = ml;
-        if (tid < 32) {
-            const uint32_t S0 = o.hq.y, S1 = o.hq.z, S2 = o.hq.w;
-            const uint32_t sc_lo = S0 & 0x3F3F3F3Fu, mn_lo = S1 & 0x3F3F3F3Fu;
-            const uint32_t sc_hi = (S2 & 0x0F0F0F0Fu) | ((S0 >> 2) & 0x30303030u);
-            const uint32_t mn_hi = ((S2 >> 4) & 0x0F0F0F0Fu) | ((S1 >> 2) & 0x30303030u);
-#pragma unroll
-            for (int s = 0; s < 8; ++s) {
-                const uint32_t scv = ((s < 4 ? sc_lo : sc_hi) >> (8 * (s & 3))) & 0xFF;
-                const uint32_t mnv = ((s < 4 ? mn_lo : mn_hi) >> (8 * (s & 3))) & 0xFF;
-                tsc[buf][s][tid] = (_Float16)(float)scv;
-                tmn[buf][s][tid] = (_Float16)(float)mnv;
-            }
-        }
+        // 6-bit scale (ta = S0) or min (ta = S1) of sub-block ts: byte ts of
+        // the low words for ts < 4, else the low / high nibble of S2's byte
+        // ts - 4 with the top two bits of ta's
+        const int sh = 8 * (ts & 3);
+        const uint32_t a8 = (o.ta >> sh) & 0xFFu, b8 = (o.tb >> sh) & 0xFFu;
+        const uint32_t v = ts < 4 ? (a8 & 63u) : ((tmn ? (b8 >> 4) : (b8 & 15u)) | ((a8 >> 6) << 4));
+        const _Float16 fv = (_Float16)(float)v;
+        tsm[buf][tv][trow] = fv;
+        tsn[buf][tv][trow] = fv * (_Float16)(-1024.f);
     };
 
-    v4f acc[4][MMD_MS];
+    v4f acc[2][MM_MS];
 #pragma unroll
-    for (int ct = 0; ct < 4; ++ct)
+    for (int ct = 0; ct < 2; ++ct)
 #pragma unroll
-        for (int ms = 0; ms < MMD_MS; ++ms) acc[ct][ms] = v4f{0.f, 0.f, 0.f, 0.f};
+        for (int ms = 0; ms < MM_MS; ++ms) acc[ct][ms] = v4f{0.f, 0.f, 0.f, 0.f};
     v4f accm = {0.f, 0.f, 0.f, 0.f};
 
     // one slice from LDS buffer buf with the wave's nibbles wq
-    auto compute = [&](const v4i& wq, int buf) {
-        const uint32_t* qw = (const uint32_t*)&wq;
+    auto compute = [&](const v2i& wq, int buf) {
+        v8h ah[MM_MS], al[MM_MS];
 #pragma unroll
-        for (int ct = 0; ct < 4; ++ct) {
-            const int s = 2 * cw + (ct >> 1);  // sub-block of the block holding these columns
-            const v8h q = nib8(qw[ct], 0.f);
-            const v8h scv = ld8h(&tsc[buf][s][8 * kq]);
-            const v8h b = q * scv;
-#pragma unroll
-            for (int ms = 0; ms < MMD_MS; ++ms) {
-                const int tt = MMD_MS * th + ms;  // 16-token tile
-                const v8h ah = ld8h(&ad[buf][0][16 * tt + col][8 * kq]);
-                const v8h al = ld8h(&ad[buf][1][16 * tt + col][8 * kq]);
-                acc[ct][ms] = __builtin_amdgcn_mfma_f32_16x16x32_f16(ah, b, acc[ct][ms], 0, 0, 0);
-                acc[ct][ms] = __builtin_amdgcn_mfma_f32_16x16x32_f16(al, b, acc[ct][ms], 0, 0, 0);
-            }
+        for (int ms = 0; ms < MM_MS; ++ms) {
+            ah[ms] = ld8h(&ad[buf][0][16 * ms + col][8 * kq]);
+            al[ms] = ld8h(&ad[buf][1][16 * ms + col][8 * kq]);
         }
+        const v8h scv = ld8h(&tsm[buf][w][8 * kq]);
+        const v8h snv = ld8h(&tsn[buf][w][8 * kq]);
+        v8h b[2];
+#pragma unroll
+        for (int ct = 0; ct < 2; ++ct) b[ct] = nib8_sc((uint32_t)wq[ct], scv, snv);
+        // every hi product first, then the lo ones: no MFMA waits on the
+        // one before it
+#pragma unroll
+        for (int ct = 0; ct < 2; ++ct)
+#pragma unroll
+            for (int ms = 0; ms < MM_MS; ++ms)
+                acc[ct][ms] = __builtin_amdgcn_mfma_f32_16x16x32_f16(ah[ms], b[ct], acc[ct][ms], 0, 0, 0);
+#pragma unroll
+        for (int ct = 0; ct < 2; ++ct)
+#pragma unroll
+            for (int ms = 0; ms < MM_MS; ++ms)
+                acc[ct][ms] = __builtin_amdgcn_mfma_f32_16x16x32_f16(al[ms], b[ct], acc[ct][ms], 0, 0, 0);
         // min term of tokens 16 w .. + 15 (waves 0-3): B columns = the 8 sub-blocks
         if (w < 4) {
-            const v8h bm = col < 8 ? ld8h(&tmn[buf][col & 7][8 * kq]) : v8h{};
+            const v8h bm = col < 8 ? ld8h(&tsm[buf][8 + (col & 7)][8 * kq]) : v8h{};
             const v8h mh = ld8h(&am[buf][0][16 * w + col][8 * kq]);
             const v8h ml = ld8h(&am[buf][1][16 * w + col][8 * kq]);
             accm = __builtin_amdgcn_mfma_f32_16x16x32_f16(mh, bm, accm, 0, 0, 0);
@@ -945,20 +972,20 @@ k_mm_down(MmDownArgs a) {
     __syncthreads();
     const MmOutDev& o = a.out;
 #pragma unroll
-    for (int ms = 0; ms < MMD_MS; ++ms)
+    for (int ms = 0; ms < MM_MS; ++ms)
 #pragma unroll
         for (int r = 0; r < 4; ++r) {
-            const int tk = 16 * (MMD_MS * th + ms) + 4 * kq + r;
+            const int tk = 16 * ms + 4 * kq + r;
             const int64_t m = m0 + tk;
             if (m >= a.M) continue;
             int sq = 0;
             while (sq + 1 < o.nseq && m >= o.row0[sq + 1]) ++sq;
             float* yrow = o.base[sq] + (m - o.row0[sq]) * o.ld + (int64_t)ks * o.split_stride;
+            const float mn = mins[tk][w];
 #pragma unroll
-            for (int ct = 0; ct < 4; ++ct) {
-                const int s = 2 * cw + (ct >> 1);
-                const float v = (acc[ct][ms][r] - mins[tk][s]) * (1.f / MMD_ASCALE);
-                float* yp = yrow + jb * 256 + 64 * cw + 16 * ct + col;
+            for (int ct = 0; ct < 2; ++ct) {
+                const float v = (acc[ct][ms][r] - mn) * (1.f / MMD_ASCALE);
+                float* yp = yrow + jb * 256 + 32 * w + 16 * ct + col;
                 *yp = o.accum ? *yp + v : v;
             }
         }
