@@ -356,72 +356,92 @@ __host__ __device__ constexpr int64_t mmt_step_bytes(int dt) {
     return 64 * mmt_lane_bytes(dt) + 16 * 16 + (dt == FTX_Q6_K_MMT ? 32 : 0);
 }
 
-// The lane's weight addresses at step 0, computed once per wave: lane (col
-// = l % 16, kq = l / 16) of MFMA column tile t holds B[8 kq + e][col] of
-// each 32-element K-step, i.e. elements 8 kq .. 8 kq + 7 of its row.
+// raw buffer descriptor over `p` (no range limit): loads then take a lane's
+// 32-bit offset and a uniform offset, with no per-load address arithmetic
+__device__ __forceinline__ __amdgpu_buffer_rsrc_t mm_rsrc(const void* p) {
+    return __builtin_amdgcn_make_buffer_rsrc(const_cast<void*>(p), (short)0, -1, 0x00020000);
+}
+
+// The lane's weight offsets, computed once per wave: per column tile the
+// tile's byte offset in the segment (uniform; a step adds a uniform stride)
+// and the lane's 32-bit offsets in the tile: lane (col = l % 16, kq = l / 16)
+// of MFMA column tile t holds B[8 kq + e][col] of each 32-element K-step,
+// i.e. elements 8 kq .. 8 kq + 7 of its row.
 struct MmPtr {
-    const uint8_t* q[MM_NT];  // Q4_K: the lane's bytes of chunk 0; Q8_0 / Q4_0: of step 0
-    const uint8_t* h[MM_NT];  // Q4_K: its row's header; Q8_0 / Q4_0 / Q6_K: its row's scales
-    const uint8_t* dd[MM_NT]; // Q6_K: its row's d
-    int64_t qstep, hstep;     // bytes per 256-element step
-    int cstride;              // Q4_K: bytes from one 64-element chunk to the next
+    __amdgpu_buffer_rsrc_t rs;   // the segment's weights (expert launches: the expert's plane)
+    uint32_t tile[MM_NT];        // column tile t's weight tile (uniform)
+    uint32_t lq[MM_NT];          // Q4_K: the lane's bytes of chunk 0; others: of the step
+    uint32_t lh[MM_NT];          // Q4_K: its row's header; Q8_0 / Q4_0 / Q6_K: its row's scales
+    uint32_t ld[MM_NT];          // Q6_K: its row's d
+    uint32_t qstep;              // bytes per 256-element step
+    uint32_t cstride;            // Q4_K: bytes from one 64-element chunk to the next
 };
 
+// Rows past N read the last tile's padding rows (the tiled copies hold whole
+// tiles) and a tile wholly past N reads the last tile; their results are
+// discarded.  Segments are below 4 GB.
 template <int DT>
 __device__ __forceinline__ void mm_ptrs(MmPtr& p, const MmSegDev& sg, int64_t rbase, int nsb,
                                         int col, int kq) {
+    p.rs = mm_rsrc(sg.W);
 #pragma unroll
     for (int t = 0; t < MM_NT; ++t) {
-        int64_t n = rbase + 16 * t + col;  // the lane's weight row in the segment
-        if (n >= sg.N) n = sg.N - 1;
         if constexpr (DT == FTX_Q4_K) {
+            // rbase is a multiple of 32: row rbase + 16 t + col is row
+            // (16 t + col) % R of tile (rbase + 16 t) / R
             const int R = sg.rpt;
-            const int T = (int)n / R, r = (int)n % R, li = r + R * (kq >> 1), half = kq & 1;
-            const uint8_t* tile = sg.W + (int64_t)T * nsb * R * 144;
-            p.q[t] = tile + li * 16 + 8 * half;
-            p.h[t] = tile + 4 * R * 32 + r * 16;
+            const int64_t T = min((rbase + 16 * t) / R, (sg.N - 1) / R);
+            const int r = (16 * t + col) % R, li = r + R * (kq >> 1), half = kq & 1;
+            p.tile[t] = (uint32_t)(T * nsb * R * 144);
+            p.lq[t] = (uint32_t)(li * 16 + 8 * half);
+            p.lh[t] = (uint32_t)(4 * R * 32 + r * 16);
+            p.ld[t] = 0;
         } else {
-            // rows past N are the zero padding of the last tile; a column
-            // tile wholly past N (results discarded) reads the last tile
             const int64_t T = min((rbase + 16 * t) / 16, (sg.N - 1) / 16);
-            const uint8_t* tile = sg.W + T * nsb * mmt_step_bytes(DT);
-            p.q[t] = tile + (col + 16 * kq) * mmt_lane_bytes(DT);
-            p.h[t] = tile + 64 * mmt_lane_bytes(DT) + col * 16;
-            p.dd[t] = tile + 64 * mmt_lane_bytes(DT) + 256 + col * 2;
+            p.tile[t] = (uint32_t)(T * nsb * mmt_step_bytes(DT));
+            p.lq[t] = (uint32_t)((col + 16 * kq) * mmt_lane_bytes(DT));
+            p.lh[t] = (uint32_t)(64 * mmt_lane_bytes(DT) + col * 16);
+            p.ld[t] = (uint32_t)(64 * mmt_lane_bytes(DT) + 256 + col * 2);
         }
     }
     if constexpr (DT == FTX_Q4_K) {
-        p.qstep = p.hstep = (int64_t)sg.rpt * 144;
-        p.cstride = sg.rpt * 32;
+        p.qstep = (uint32_t)(sg.rpt * 144);
+        p.cstride = (uint32_t)(sg.rpt * 32);
     } else {
-        p.qstep = p.hstep = mmt_step_bytes(DT);
+        p.qstep = (uint32_t)mmt_step_bytes(DT);
         p.cstride = 0;
     }
 }
 
+__device__ __forceinline__ v2i mm_ld8(const __amdgpu_buffer_rsrc_t& rs, uint32_t v, uint32_t s) {
+    return __builtin_bit_cast(v2i, __builtin_amdgcn_raw_buffer_load_b64(rs, v, s, 0));
+}
+__device__ __forceinline__ v4i mm_ld16(const __amdgpu_buffer_rsrc_t& rs, uint32_t v, uint32_t s) {
+    return __builtin_bit_cast(v4i, __builtin_amdgcn_raw_buffer_load_b128(rs, v, s, 0));
+}
+
 template <int DT>
 __device__ __forceinline__ void mm_load(MmW<DT>& o, const MmPtr& p, int sb) {
-    const int64_t qo = sb * p.qstep, ho = sb * p.hstep;
 #pragma unroll
     for (int t = 0; t < MM_NT; ++t) {
-        const uint8_t* q = p.q[t] + qo;
+        const uint32_t so = p.tile[t] + (uint32_t)sb * p.qstep;  // uniform
         if constexpr (DT == FTX_Q4_K) {
 #pragma unroll
-            for (int c = 0; c < 4; ++c) o.qs[t][c] = *(const v2i*)(q + c * p.cstride);
-            o.hdr[t] = *(const v4i*)(p.h[t] + ho);
+            for (int c = 0; c < 4; ++c) o.qs[t][c] = mm_ld8(p.rs, p.lq[t], so + c * p.cstride);
+            o.hdr[t] = mm_ld16(p.rs, p.lh[t], so);
         } else if constexpr (DT == FTX_Q8_0_MMT) {
 #pragma unroll
-            for (int v = 0; v < 4; ++v) o.q[t][v] = *(const v4i*)(q + 16 * v);
-            o.d[t] = *(const v4i*)(p.h[t] + ho);
+            for (int v = 0; v < 4; ++v) o.q[t][v] = mm_ld16(p.rs, p.lq[t], so + 16 * v);
+            o.d[t] = mm_ld16(p.rs, p.lh[t], so);
         } else if constexpr (DT == FTX_Q6_K_MMT) {
 #pragma unroll
-            for (int v = 0; v < 3; ++v) o.q[t][v] = *(const v4i*)(q + 16 * v);
-            o.sc[t] = *(const v4i*)(p.h[t] + ho);
-            o.d[t] = *(const uint16_t*)(p.dd[t] + ho);
+            for (int v = 0; v < 3; ++v) o.q[t][v] = mm_ld16(p.rs, p.lq[t], so + 16 * v);
+            o.sc[t] = mm_ld16(p.rs, p.lh[t], so);
+            o.d[t] = __builtin_amdgcn_raw_buffer_load_b16(p.rs, p.ld[t], so, 0);
         } else {
 #pragma unroll
-            for (int v = 0; v < 2; ++v) o.q[t][v] = *(const v4i*)(q + 16 * v);
-            o.d[t] = *(const v4i*)(p.h[t] + ho);
+            for (int v = 0; v < 2; ++v) o.q[t][v] = mm_ld16(p.rs, p.lq[t], so + 16 * v);
+            o.d[t] = mm_ld16(p.rs, p.lh[t], so);
         }
     }
 }
@@ -498,24 +518,25 @@ __global__ void __launch_bounds__(64 * MM_WAVES)
     constexpr int BPW = 16 * MS / MM_WAVES;
     constexpr int BUF = MS * 16384;
     const int b0 = BPW * w, hl0 = b0 / (8 * MS), ms0 = (b0 / 8) % MS, j0 = b0 % 8;
-    const _Float16* gsrc = (hl0 ? a.xl : a.xh) + ((mt0 + ms0) * nks * 64 + lane) * 8;
+    const __amdgpu_buffer_rsrc_t xrs = mm_rsrc(hl0 ? a.xl : a.xh);
+    const uint32_t xoff = (uint32_t)((mt0 + ms0) * nks * 64 * 8 * 2);  // bytes, uniform
+    const uint32_t glane = (uint32_t)lane * 16;
     auto stage = [&](int sb, int buf) {
         if (XT && ms0 >= nsub) return;  // this wave's blocks belong to an unused token tile
-        const _Float16* src = gsrc + ((int64_t)sb * 8 + j0) * 64 * 8;
+        const uint32_t so = xoff + (uint32_t)(sb * 8 + j0) * 1024;
 #pragma unroll
         for (int i = 0; i < BPW; ++i)
-            __builtin_amdgcn_global_load_lds((const void*)(src + i * 64 * 8),
-                                             (lds_void*)(mm_lds + buf * BUF + (b0 + i) * 1024), 16,
-                                             0, 0);
+            __builtin_amdgcn_raw_ptr_buffer_load_lds(
+                xrs, (lds_void*)(mm_lds + buf * BUF + (b0 + i) * 1024), 16, glane, so + i * 1024, 0, 0);
     };
     auto frag = [&](int buf, int hl, int ms, int j) -> v8h {
         return *(const v8h*)(mm_lds + buf * BUF + ((hl * MS + ms) * 8 + j) * 1024 + lane * 16);
     };
     // Q4_K min term: this lane's sub-block sums (K slots of the 16x16x16
-    // operand; zero for kq >= 2)
-    // (lanes kq >= 2 read lane - 32's sums and discard them: in bounds)
-    const _Float16* xs0 = a.sh + (mt0 * a.nsb * 32 + (lane & 31)) * 4;
-    const _Float16* xl0 = a.sl + (mt0 * a.nsb * 32 + (lane & 31)) * 4;
+    // operand); lanes kq >= 2 read lane - 32's sums, which meet zero mins
+    const __amdgpu_buffer_rsrc_t srs = mm_rsrc(a.sh), lrs = mm_rsrc(a.sl);
+    const uint32_t soff = (uint32_t)(mt0 * a.nsb * 32 * 4 * 2);  // bytes, uniform
+    const uint32_t xlane = (uint32_t)(lane & 31) * 8;
 
     v4f acc[MM_NT][MS];
 #pragma unroll
@@ -529,29 +550,46 @@ __global__ void __launch_bounds__(64 * MM_WAVES)
     auto step = [&](int sb, int buf, const MmW<DT>& wc, MmW<DT>& wn) {
         __builtin_amdgcn_s_waitcnt(0x0F70);  // this step's fragments and weights
         __syncthreads();                     // every wave is done with the other buffer
-        if (sb + 1 < sb1) {
-            stage(sb + 1, buf ^ 1);
-            mm_load<DT>(wn, wp, sb + 1);
-        }
+        // Q4_K: the step's sub-block sums, loaded before the next step's
+        // copies and weights so that their wait at the min term does not
+        // wait for those
         v4h xsh[MS], xsl[MS];
-        v2h scp[MM_NT][4], scn[MM_NT][4];  // Q4_K: sc and -1024 sc per sub-block, fp16 pairs
-        v4h mnh[MM_NT];                    // Q4_K: the 4 mins of the lane's K slots
         if constexpr (DT == FTX_Q4_K) {
 #pragma unroll
             for (int ms = 0; ms < MS; ++ms) {
                 if (XT && ms >= nsub) break;
-                const int64_t o = ((int64_t)ms * a.nsb + sb) * 32 * 4;
-                const v4h hh = *(const v4h*)(xs0 + o), ll = *(const v4h*)(xl0 + o);
-                xsh[ms] = kq < 2 ? hh : v4h{};
-                xsl[ms] = kq < 2 ? ll : v4h{};
+                const uint32_t o = soff + (uint32_t)((ms * a.nsb + sb) * 32 * 4 * 2);
+                xsh[ms] = __builtin_bit_cast(v4h, mm_ld8(srs, xlane, o));
+                xsl[ms] = __builtin_bit_cast(v4h, mm_ld8(lrs, xlane, o));
             }
+        }
+        // the next step's copies and weights; the last step loads itself
+        // again (unused), so that no branch leaves the waits for the sums
+        // above counting as if these loads were not in flight
+        {
+            const int sbn = min(sb + 1, sb1 - 1);
+            stage(sbn, buf ^ 1);
+            mm_load<DT>(wn, wp, sbn);
+        }
+        // keep every load above ahead of the step's arithmetic (the
+        // scheduler would otherwise sink the weight loads below the MFMAs
+        // to save registers, and their latency would no longer be hidden)
+        __builtin_amdgcn_sched_barrier(0);
+        v2h scp[MM_NT][4], scn[MM_NT][4];  // Q4_K: sc and -1024 sc per sub-block, fp16 pairs
+        v4h mnh[MM_NT];                    // Q4_K: the 4 mins of the lane's K slots
+        if constexpr (DT == FTX_Q4_K) {
 #pragma unroll
             for (int t = 0; t < MM_NT; ++t) {
                 const uint32_t S0 = wc.hdr[t].y, S1 = wc.hdr[t].z, S2 = wc.hdr[t].w;
                 const uint32_t sc0 = S0 & 0x3F3F3F3Fu;
                 const uint32_t sc1 = (S2 & 0x0F0F0F0Fu) | ((S0 >> 2) & 0x30303030u);
-                const uint32_t mn = (kq & 1) ? ((S2 >> 4) & 0x0F0F0F0Fu) | ((S1 >> 2) & 0x30303030u)
-                                             : S1 & 0x3F3F3F3Fu;
+                // the mins of the lane's K slots: sub-blocks 4 kq .. 4 kq + 3
+                // (none for kq >= 2, whose slots are past the 8 sub-blocks)
+                // (blended by masks: a branch here would wait for every load
+                // in flight)
+                const uint32_t odd = 0u - (uint32_t)(kq & 1), low = 0u - (uint32_t)(kq < 2);
+                const uint32_t mhi = ((S2 >> 4) & 0x0F0F0F0Fu) | ((S1 >> 2) & 0x30303030u);
+                const uint32_t mn = ((mhi & odd) | (S1 & 0x3F3F3F3Fu & ~odd)) & low;
                 v2h a0, a1;
                 bytes4_h(sc0, scp[t][0], scp[t][1]);
                 bytes4_h(sc1, scp[t][2], scp[t][3]);
@@ -725,7 +763,7 @@ __global__ void __launch_bounds__(64 * MM_WAVES)
                     mt = __builtin_amdgcn_mfma_f32_16x16x16f16(xsl[ms], mnh[t], mt, 0, 0, 0);
 #pragma unroll
                     for (int r = 0; r < 4; ++r)
-                        acc[t][ms][r] += d * tmp[t][ms][r] - dmin * mt[r];
+                        acc[t][ms][r] = fmaf(-dmin, mt[r], fmaf(d, tmp[t][ms][r], acc[t][ms][r]));
                 }
             }
         }
