@@ -48,18 +48,25 @@ struct DownArgs {
     float* part;         // [S][8][N]
 };
 
-// 8 nibbles (slot t: byte t%4, nibble t/4) -> 8 fp16 values q + bias
-__device__ __forceinline__ v8h nib8_to_h(uint32_t w, float bias) {
+// fp16 pairs 1024 + q (p[i] = slots 2i, 2i + 1) -> x q per slot, exact: one
+// fused multiply-add (1024 + q) x + (-1024 x) per pair
+__device__ __forceinline__ v8h fma8(const v2h* p, const v8h& x, const v8h& nx) {
+    v2h r[4];
+#pragma unroll
+    for (int i = 0; i < 4; ++i)
+        r[i] = __builtin_elementwise_fma(p[i], v2h{x[2 * i], x[2 * i + 1]}, v2h{nx[2 * i], nx[2 * i + 1]});
+    return v8h{r[0][0], r[0][1], r[1][0], r[1][1], r[2][0], r[2][1], r[3][0], r[3][1]};
+}
+
+// 8 nibbles (slot t: byte t%4, nibble t/4) -> 8 fp16 values sc_t q_t, exact
+__device__ __forceinline__ v8h nib8_fma(uint32_t w, const v8h& sc, const v8h& sn) {
     const uint32_t lo = w & 0x0F0F0F0Fu, hi = (w >> 4) & 0x0F0F0F0Fu;
-    // 0x64 in the high byte: fp16 1024 + q, exact
-    const uint32_t p0 = __builtin_amdgcn_perm(lo, 0x64646464u, 0x00050004u);
-    const uint32_t p1 = __builtin_amdgcn_perm(lo, 0x64646464u, 0x00070006u);
-    const uint32_t p2 = __builtin_amdgcn_perm(hi, 0x64646464u, 0x00050004u);
-    const uint32_t p3 = __builtin_amdgcn_perm(hi, 0x64646464u, 0x00070006u);
-    const v2h b = {(_Float16)(-1024.f - bias), (_Float16)(-1024.f - bias)};
-    const v2h h0 = __builtin_bit_cast(v2h, p0) + b, h1 = __builtin_bit_cast(v2h, p1) + b;
-    const v2h h2 = __builtin_bit_cast(v2h, p2) + b, h3 = __builtin_bit_cast(v2h, p3) + b;
-    return v8h{h0[0], h0[1], h1[0], h1[1], h2[0], h2[1], h3[0], h3[1]};
+    v2h p[4];
+    p[0] = __builtin_bit_cast(v2h, __builtin_amdgcn_perm(lo, 0x64646464u, 0x00050004u));
+    p[1] = __builtin_bit_cast(v2h, __builtin_amdgcn_perm(lo, 0x64646464u, 0x00070006u));
+    p[2] = __builtin_bit_cast(v2h, __builtin_amdgcn_perm(hi, 0x64646464u, 0x00050004u));
+    p[3] = __builtin_bit_cast(v2h, __builtin_amdgcn_perm(hi, 0x64646464u, 0x00070006u));
+    return fma8(p, sc, sn);
 }
 
 // One workgroup = one 256-column super-block over a contiguous range of
@@ -125,7 +132,11 @@ __global__ void __launch_bounds__(64 * DOWN_WAVES) __attribute__((amdgpu_waves_p
 k_down_mfma(DownArgs a) {
     constexpr int NS = DownCfg<DT>::NS, NB = DownCfg<DT>::NB, RP = DownCfg<DT>::RP;
     constexpr int NT = DT == FTX_Q4_K ? 2 : 1;  // activation tables: h d (, h dmin)
-    constexpr int NC = DT == FTX_Q4_K ? 2 : 3;  // scale tables: sc, m | sh, sl, sc
+    // scale tables: sc, m, -1024 sc | sh, sl, sc, -1024 sh, -1024 sl (the
+    // negated ones complete (1024 + q) x + (-1024 x) = q x in one fused
+    // multiply-add per pair); TSUB = the sub-block term's B columns
+    constexpr int NC = DT == FTX_Q4_K ? 3 : 5;
+    constexpr int TSUB = DT == FTX_Q4_K ? 1 : 2;
     __shared__ _Float16 tab[2][NT][NB][4][16][8];  // [buf][table][slice][k octet][A row][8]
     __shared__ _Float16 sct[2][NC][NS][RP];        // [buf][table][sub-block][row]
     __shared__ float red[4][16][64];              // slice group 1's outputs
@@ -195,6 +206,7 @@ k_down_mfma(DownArgs a) {
             }
             *(v2h*)&sct[buf][0][se][r0] = sc;
             *(v2h*)&sct[buf][1][se][r0] = mn;
+            *(v2h*)&sct[buf][2][se][r0] = sc * v2h{(_Float16)(-1024.f), (_Float16)(-1024.f)};
         } else {
 #pragma unroll
             for (int h2 = 0; h2 < 2; ++h2) {
@@ -207,9 +219,12 @@ k_down_mfma(DownArgs a) {
                     vl[k] = (_Float16)(float)(sc & 15);
                     vc[k] = (_Float16)(float)sc;
                 }
+                const v2h m1024 = {(_Float16)(-1024.f), (_Float16)(-1024.f)};
                 *(v2h*)&sct[buf][0][sb][r0] = vh;
                 *(v2h*)&sct[buf][1][sb][r0] = vl;
                 *(v2h*)&sct[buf][2][sb][r0] = vc;
+                *(v2h*)&sct[buf][3][sb][r0] = vh * m1024;
+                *(v2h*)&sct[buf][4][sb][r0] = vl * m1024;
             }
         }
     };
@@ -233,9 +248,11 @@ k_down_mfma(DownArgs a) {
 #pragma unroll
         for (int ct = 0; ct < 4; ++ct) {
             if constexpr (DT == FTX_Q4_K) {
-                const v8h q = nib8_to_h(qw[ct], 0.f);
-                const v8h sc = *(const v8h*)&sct[buf][0][2 * cw + (ct >> 1)][r0];
-                acc[ct] = __builtin_amdgcn_mfma_f32_16x16x32_f16(av, q * sc, acc[ct], 0, 0, 0);
+                const int s = 2 * cw + (ct >> 1);
+                const v8h sc = *(const v8h*)&sct[buf][0][s][r0];
+                const v8h sn = *(const v8h*)&sct[buf][2][s][r0];
+                acc[ct] = __builtin_amdgcn_mfma_f32_16x16x32_f16(av, nib8_fma(qw[ct], sc, sn), acc[ct], 0,
+                                                                 0, 0);
             } else {
                 const uint32_t X = ct < 2 ? (uint32_t)wt.h[bb].x : (uint32_t)wt.h[bb].y;
                 const uint32_t hl = (ct & 1) ? (X << 4) & 0x30303030u : X & 0x30303030u;
@@ -244,25 +261,24 @@ k_down_mfma(DownArgs a) {
                 const uint32_t vlo = (L & 0x0F0F0F0Fu) | hl;
                 const uint32_t vhi = ((L >> 4) & 0x0F0F0F0Fu) | hh;
                 // 6-bit q as (lo nibble word, hi nibble word) -> fp16 1024 + q
-                const uint32_t p0 = __builtin_amdgcn_perm(vlo, 0x64646464u, 0x00050004u);
-                const uint32_t p1 = __builtin_amdgcn_perm(vlo, 0x64646464u, 0x00070006u);
-                const uint32_t p2 = __builtin_amdgcn_perm(vhi, 0x64646464u, 0x00050004u);
-                const uint32_t p3 = __builtin_amdgcn_perm(vhi, 0x64646464u, 0x00070006u);
-                const v2h bb = {(_Float16)(-1024.f), (_Float16)(-1024.f)};
-                const v2h h0 = __builtin_bit_cast(v2h, p0) + bb, h1 = __builtin_bit_cast(v2h, p1) + bb;
-                const v2h h2 = __builtin_bit_cast(v2h, p2) + bb, h3 = __builtin_bit_cast(v2h, p3) + bb;
-                const v8h q = v8h{h0[0], h0[1], h1[0], h1[1], h2[0], h2[1], h3[0], h3[1]};
+                v2h p[4];
+                p[0] = __builtin_bit_cast(v2h, __builtin_amdgcn_perm(vlo, 0x64646464u, 0x00050004u));
+                p[1] = __builtin_bit_cast(v2h, __builtin_amdgcn_perm(vlo, 0x64646464u, 0x00070006u));
+                p[2] = __builtin_bit_cast(v2h, __builtin_amdgcn_perm(vhi, 0x64646464u, 0x00050004u));
+                p[3] = __builtin_bit_cast(v2h, __builtin_amdgcn_perm(vhi, 0x64646464u, 0x00070006u));
                 const int s = 4 * cw + ct;
                 const v8h sh = *(const v8h*)&sct[buf][0][s][r0];
                 const v8h sl = *(const v8h*)&sct[buf][1][s][r0];
-                acc[ct] = __builtin_amdgcn_mfma_f32_16x16x32_f16(av16, q * sh, acc[ct], 0, 0, 0);
-                acc[ct] = __builtin_amdgcn_mfma_f32_16x16x32_f16(av, q * sl, acc[ct], 0, 0, 0);
+                const v8h nh = *(const v8h*)&sct[buf][3][s][r0];
+                const v8h nl = *(const v8h*)&sct[buf][4][s][r0];
+                acc[ct] = __builtin_amdgcn_mfma_f32_16x16x32_f16(av16, fma8(p, sh, nh), acc[ct], 0, 0, 0);
+                acc[ct] = __builtin_amdgcn_mfma_f32_16x16x32_f16(av, fma8(p, sl, nl), acc[ct], 0, 0, 0);
             }
         }
         // sub-block term: B column col = sub-block (Q4_K: rows of m, with the
         // h dmin operand; Q6_K: sc, with the h d operand)
         const v8h as = DT == FTX_Q4_K ? *(const v8h*)&tab[buf][NT - 1][b][g][col][0] : av;
-        v8h bsv = *(const v8h*)&sct[buf][NC - 1][col % NS][r0];
+        v8h bsv = *(const v8h*)&sct[buf][TSUB][col % NS][r0];
         if (col >= NS) bsv = v8h{};
         accs = __builtin_amdgcn_mfma_f32_16x16x32_f16(as, bsv, accs, 0, 0, 0);
     };
