@@ -120,10 +120,11 @@ def test_batch_three_sequences(gctx, orc, dts):
         assert np.array_equal(kg[:, :npast], kc[:, :npast])
 
 
-@pytest.mark.parametrize("M", [9, 64, 200])
+@pytest.mark.parametrize("M", [9, 30, 64, 200])
 def test_large_chain_one_pass(gctx, orc, M):
-    """A single sequence of 9, 64 and 200 tokens (one, one and four 64-token
-    tiles) through the one-pass GEMMs, Q4_K projections and down, Q8_0 head."""
+    """A single sequence of 9, 30, 64 and 200 tokens (one 16-, 32- and
+    64-token tile, and four 64-token tiles) through the one-pass GEMMs, Q4_K
+    projections and down, Q8_0 head."""
     dts = dict(tok_embd=P.Q8_0, output=P.Q8_0, q=P.Q4_K, k=P.Q4_K, v=P.Q4_K, o=P.Q4_K,
                gate=P.Q4_K, up=P.Q4_K, down=P.Q4_K)
     cfg = P.model_cfg(1, 1024, 8, 2, 128, 2048, 700, rope_theta=500000.0)
@@ -137,7 +138,7 @@ def test_large_chain_one_pass(gctx, orc, M):
 def test_large_chain_q6k_one_pass(gctx, orc, M):
     """Q6_K projections (q / k / v, o, gate / up with SwiGLU) and a Q6_K head
     through the one-pass GEMM's Q6_K operand (scale split 16 sh + sl), one
-    and three 64-token tiles; ffn_down Q4_K."""
+    32-token tile and three 64-token tiles; ffn_down Q4_K."""
     dts = dict(tok_embd=P.Q8_0, output=P.Q6_K, q=P.Q6_K, k=P.Q6_K, v=P.Q6_K, o=P.Q6_K,
                gate=P.Q6_K, up=P.Q6_K, down=P.Q4_K)
     cfg = P.model_cfg(2, 1024, 8, 2, 128, 2048, 700, rope_theta=500000.0)

@@ -1356,7 +1356,10 @@ static hipError_t mm_launch(hipStream_t st, const MmSeg* segs, int nseg, const M
     if (xtab && (ntile_max < 1 || (trows != 16 && trows != 64) || ntile_max * trows > act.Mp ||
                  !plane))
         return hipErrorInvalidValue;
-    const int ms = xtab ? (int)(trows / 16) : MM_MS;
+    // dense launches of at most 32 tokens take 16- or 32-token tiles: the
+    // MFMAs, fragment reads and accumulator updates of the padding rows of a
+    // 64-token tile are then not spent
+    const int ms = xtab ? (int)(trows / 16) : (M <= 16 ? 1 : (M <= 32 ? 2 : MM_MS));
     if (fo && (!xtab || epi != EPI_SWIGLU)) return hipErrorInvalidValue;
     const int dt = segs[0].dt;
     MmArgs a{};
@@ -1386,7 +1389,7 @@ static hipError_t mm_launch(hipStream_t st, const MmSeg* segs, int nseg, const M
     a.sl = act.sl;
     a.M = (int)M;
     const int64_t wg = (units + MM_WAVES - 1) / MM_WAVES,
-                  mt = xtab ? ntile_max : act.Mp / MM_TOK;
+                  mt = xtab ? ntile_max : (ms == MM_MS ? act.Mp / MM_TOK : 1);
     int S = mm_splits(wg * mt, a.nsb, cu_count, MM_SPLIT_COST);
     // SwiGLU needs the gate and up sums together: always through the reduce
     const bool via_part = S > 1 || epi == EPI_SWIGLU || xtab;
@@ -1412,19 +1415,23 @@ static hipError_t mm_launch(hipStream_t st, const MmSeg* segs, int nseg, const M
     const dim3 grid((unsigned)(wg * mt), 1, (unsigned)S);
     const size_t lds = 2 * (size_t)ms * 16384;
     using K_t = void (*)(MmArgs);
-    // [dtype][dense | expert 64-row tiles | expert 16-row tiles] (Q6_K:
-    // dense only)
-    static const K_t kerns[4][3] = {
-        {k_mm<FTX_Q4_K, false, 4>, k_mm<FTX_Q4_K, true, 4>, k_mm<FTX_Q4_K, true, 1>},
-        {k_mm<FTX_Q8_0_MMT, false, 4>, k_mm<FTX_Q8_0_MMT, true, 4>, k_mm<FTX_Q8_0_MMT, true, 1>},
-        {k_mm<FTX_Q4_0_MMT, false, 4>, k_mm<FTX_Q4_0_MMT, true, 4>, k_mm<FTX_Q4_0_MMT, true, 1>},
-        {k_mm<FTX_Q6_K_MMT, false, 4>, nullptr, nullptr}};
+    // [dtype][dense 64 | expert 64-row tiles | expert 16-row tiles | dense
+    // 32 | dense 16] (Q6_K: dense only)
+    static const K_t kerns[4][5] = {
+        {k_mm<FTX_Q4_K, false, 4>, k_mm<FTX_Q4_K, true, 4>, k_mm<FTX_Q4_K, true, 1>,
+         k_mm<FTX_Q4_K, false, 2>, k_mm<FTX_Q4_K, false, 1>},
+        {k_mm<FTX_Q8_0_MMT, false, 4>, k_mm<FTX_Q8_0_MMT, true, 4>, k_mm<FTX_Q8_0_MMT, true, 1>,
+         k_mm<FTX_Q8_0_MMT, false, 2>, k_mm<FTX_Q8_0_MMT, false, 1>},
+        {k_mm<FTX_Q4_0_MMT, false, 4>, k_mm<FTX_Q4_0_MMT, true, 4>, k_mm<FTX_Q4_0_MMT, true, 1>,
+         k_mm<FTX_Q4_0_MMT, false, 2>, k_mm<FTX_Q4_0_MMT, false, 1>},
+        {k_mm<FTX_Q6_K_MMT, false, 4>, nullptr, nullptr, k_mm<FTX_Q6_K_MMT, false, 2>,
+         k_mm<FTX_Q6_K_MMT, false, 1>}};
     const int di = dt == FTX_Q4_K ? 0 : (dt == FTX_Q8_0_MMT ? 1 : (dt == FTX_Q4_0_MMT ? 2 : 3));
-    const int vi = !xtab ? 0 : (ms == 4 ? 1 : 2);
+    const int vi = xtab ? (ms == 4 ? 1 : 2) : (ms == 4 ? 0 : (ms == 2 ? 3 : 4));
     const K_t kern = kerns[di][vi];
     if (!kern) return hipErrorInvalidValue;
-    static bool lds_set[12] = {};
-    const int ki = di * 3 + vi;
+    static bool lds_set[20] = {};
+    const int ki = di * 5 + vi;
     if (!lds_set[ki]) {
         hipError_t e = hipFuncSetAttribute((const void*)kern,
                                            hipFuncAttributeMaxDynamicSharedMemorySize, (int)lds);
