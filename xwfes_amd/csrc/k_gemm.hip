@@ -846,39 +846,43 @@ __device__ __forceinline__ v8h nib8_sc(uint32_t w, const v8h& sc, const v8h& sn)
     return v8h{p[0][0], p[0][1], p[1][0], p[1][1], p[2][0], p[2][1], p[3][0], p[3][1]};
 }
 
+// MS: 16-token tiles of a workgroup (4: 64 tokens; 2: launches of at most
+// 32 tokens); a thread stages RPT = MS rows of one token
+template <int MS>
 __global__ void __launch_bounds__(64 * MMD_WAVES) __attribute__((amdgpu_waves_per_eu(2, 2)))
 k_mm_down(MmDownArgs a) {
-    __shared__ _Float16 ad[2][2][MM_TOK][MMD_PITCH];  // [buf][hi / lo][token][row i]
-    __shared__ _Float16 am[2][2][MM_TOK][MMD_PITCH];
+    constexpr int TOK = 16 * MS, RPT = MS, TPR = 32 / RPT;  // tokens, rows per thread, threads per token
+    __shared__ _Float16 ad[2][2][TOK][MMD_PITCH];  // [buf][hi / lo][token][row i]
+    __shared__ _Float16 am[2][2][TOK][MMD_PITCH];
     __shared__ _Float16 tsm[2][16][MMD_PITCH];         // [buf][sc of sub-block 0-7, mn 0-7][row i]
     __shared__ _Float16 tsn[2][16][MMD_PITCH];         // [buf][-1024 sc (rows 8-15 unused)][row i]
-    __shared__ float mins[MM_TOK][9];                  // [token][sub-block]
+    __shared__ float mins[TOK][9];                     // [token][sub-block]
     const int tid = threadIdx.x, lane = tid & 63;
     const int w = __builtin_amdgcn_readfirstlane(tid >> 6);
     const int col = lane & 15, kq = lane >> 4;
     // token tiles of one column block are neighbours in the grid (they share
     // the block's weights)
     const int64_t jb = blockIdx.x / (unsigned)a.ntt;
-    const int64_t m0 = (int64_t)(blockIdx.x % (unsigned)a.ntt) * MM_TOK;
+    const int64_t m0 = (int64_t)(blockIdx.x % (unsigned)a.ntt) * TOK;
     const int ks = blockIdx.z;
     const int64_t nsl = a.n_in / 32, nc64 = a.N / 64;
     const int64_t I0 = (int64_t)ks * a.slices_per_split;
     const int64_t I1 = min(I0 + (int64_t)a.slices_per_split, nsl);
 
-    // staging: thread t takes token sm = t / 8 and rows 4 sp .. 4 sp + 3 of
-    // the slice (h of tokens past M is zero), and table entry (row t / 16,
+    // staging: thread t takes token sm = t / TPR and rows RPT sp .. RPT sp +
+    // RPT - 1 of the slice (h of tokens past M is zero), and table entry (row t / 16,
     // value t % 16: sub-block scale 0-7, then min 0-7).  A slice's global
     // operands (h, the rows' d / dmin, the header words, each wave's
     // nibbles) go to one of MMD_RING register slots MMD_RING slices ahead of
     // its use, so that the loads of several slices are in flight while one
     // is computed.  Per slice the bases move by uniform strides; the lanes'
     // offsets are fixed 32-bit values.
-    const int sm = tid >> 3, sp = tid & 7;
+    const int sm = tid / TPR, sp = tid % TPR;
     const int trow = tid >> 4, tv = tid & 15, ts = tv & 7, tmn = tv >> 3;
     const bool tok_ok = m0 + sm < a.M;
     const float hscale = tok_ok ? MMD_ASCALE : 0.f;
-    const uint32_t h_off = (uint32_t)(((tok_ok ? m0 + sm : 0) * a.ldh + 4 * sp) * 4);
-    const uint32_t d_off = (uint32_t)(4 * sp * 16);
+    const uint32_t h_off = (uint32_t)(((tok_ok ? m0 + sm : 0) * a.ldh + RPT * sp) * 4);
+    const uint32_t d_off = (uint32_t)(RPT * sp * 16);
     const uint32_t t_off = (uint32_t)(trow * 16);
     const uint32_t q_off = (uint32_t)(((((w >> 1) * 4 + kq) * 16 + col) * 16) + 8 * (w & 1));
     const uint8_t* hb = (const uint8_t*)a.h;
@@ -886,25 +890,34 @@ k_mm_down(MmDownArgs a) {
     const uint8_t* qb = a.qs + jb * 4 * 4 * 16 * 16;
     const int64_t q_stride = nc64 * 4 * 16 * 16;
     struct Slot {
-        float4 hv;
-        uint32_t dw[4];  // d | dmin << 16 of rows 4 sp + e
+        float hv[RPT];
+        uint32_t dw[RPT];  // d | dmin << 16 of rows RPT sp + e
         uint32_t ta, tb; // table entry: scale (S0) or min (S1) word, and S2 word
         v2i wq;          // this wave's nibbles of the slice (two column tiles)
     };
     auto issue = [&](Slot& o, int64_t I) {
-        o.hv = *(const float4*)(hb + I * 128 + h_off);
+        if constexpr (RPT == 4) {
+            const float4 v = *(const float4*)(hb + I * 128 + h_off);
+            o.hv[0] = v.x; o.hv[1] = v.y; o.hv[2] = v.z; o.hv[3] = v.w;
+        } else {
+            const float2 v = *(const float2*)(hb + I * 128 + h_off);
+            o.hv[0] = v.x; o.hv[1] = v.y;
+        }
         const uint8_t* dI = db + I * 512;
 #pragma unroll
-        for (int e = 0; e < 4; ++e) o.dw[e] = *(const uint32_t*)(dI + d_off + e * 16);
+        for (int e = 0; e < RPT; ++e) o.dw[e] = *(const uint32_t*)(dI + d_off + e * 16);
         o.ta = *(const uint32_t*)(dI + t_off + 4 + 4 * tmn);
         o.tb = *(const uint32_t*)(dI + t_off + 12);
         o.wq = *(const v2i*)(qb + I * q_stride + q_off);
     };
     auto stage_store = [&](const Slot& o, int buf) {
-        const float hv[4] = {o.hv.x * hscale, o.hv.y * hscale, o.hv.z * hscale, o.hv.w * hscale};
-        v4h dh, dl, mh, ml;
+        float hv[RPT];
 #pragma unroll
-        for (int e = 0; e < 4; e += 2) {
+        for (int e = 0; e < RPT; ++e) hv[e] = o.hv[e] * hscale;
+        typedef _Float16 vRh __attribute__((ext_vector_type(RPT)));
+        vRh dh, dl, mh, ml;
+#pragma unroll
+        for (int e = 0; e < RPT; e += 2) {
             float pd[2], pm[2];
 #pragma unroll
             for (int i = 0; i < 2; ++i) {
@@ -923,10 +936,10 @@ k_mm_down(MmDownArgs a) {
             ml[e] = l[0];
             ml[e + 1] = l[1];
         }
-        *(v4h*)&ad[buf][0][sm][4 * sp] = dh;
-        *(v4h*)&ad[buf][1][sm][4 * sp] = dl;
-        *(v4h*)&am[buf][0][sm][4 * sp] = mh;
-        *(v4h*)&am[buf][1][sm][4 * sp] = ml;
+        *(vRh*)&ad[buf][0][sm][RPT * sp] = dh;
+        *(vRh*)&ad[buf][1][sm][RPT * sp] = dl;
+        *(vRh*)&am[buf][0][sm][RPT * sp] = mh;
+        *(vRh*)&am[buf][1][sm][RPT * sp] = ml;
         // 6-bit scale (ta = S0) or min (ta = S1) of sub-block ts: byte ts of
         // the low words for ts < 4, else the low / high nibble of S2's byte
         // ts - 4 with the top two bits of ta's
@@ -938,18 +951,18 @@ k_mm_down(MmDownArgs a) {
         tsn[buf][tv][trow] = fv * (_Float16)(-1024.f);
     };
 
-    v4f acc[2][MM_MS];
+    v4f acc[2][MS];
 #pragma unroll
     for (int ct = 0; ct < 2; ++ct)
 #pragma unroll
-        for (int ms = 0; ms < MM_MS; ++ms) acc[ct][ms] = v4f{0.f, 0.f, 0.f, 0.f};
+        for (int ms = 0; ms < MS; ++ms) acc[ct][ms] = v4f{0.f, 0.f, 0.f, 0.f};
     v4f accm = {0.f, 0.f, 0.f, 0.f};
 
     // one slice from LDS buffer buf with the wave's nibbles wq
     auto compute = [&](const v2i& wq, int buf) {
-        v8h ah[MM_MS], al[MM_MS];
+        v8h ah[MS], al[MS];
 #pragma unroll
-        for (int ms = 0; ms < MM_MS; ++ms) {
+        for (int ms = 0; ms < MS; ++ms) {
             ah[ms] = ld8h(&ad[buf][0][16 * ms + col][8 * kq]);
             al[ms] = ld8h(&ad[buf][1][16 * ms + col][8 * kq]);
         }
@@ -963,15 +976,15 @@ k_mm_down(MmDownArgs a) {
 #pragma unroll
         for (int ct = 0; ct < 2; ++ct)
 #pragma unroll
-            for (int ms = 0; ms < MM_MS; ++ms)
+            for (int ms = 0; ms < MS; ++ms)
                 acc[ct][ms] = __builtin_amdgcn_mfma_f32_16x16x32_f16(ah[ms], b[ct], acc[ct][ms], 0, 0, 0);
 #pragma unroll
         for (int ct = 0; ct < 2; ++ct)
 #pragma unroll
-            for (int ms = 0; ms < MM_MS; ++ms)
+            for (int ms = 0; ms < MS; ++ms)
                 acc[ct][ms] = __builtin_amdgcn_mfma_f32_16x16x32_f16(al[ms], b[ct], acc[ct][ms], 0, 0, 0);
-        // min term of tokens 16 w .. + 15 (waves 0-3): B columns = the 8 sub-blocks
-        if (w < 4) {
+        // min term of tokens 16 w .. + 15 (waves 0 .. MS - 1): B columns = the 8 sub-blocks
+        if (w < MS) {
             const v8h bm = col < 8 ? ld8h(&tsm[buf][8 + (col & 7)][8 * kq]) : v8h{};
             const v8h mh = ld8h(&am[buf][0][16 * w + col][8 * kq]);
             const v8h ml = ld8h(&am[buf][1][16 * w + col][8 * kq]);
@@ -1003,14 +1016,14 @@ k_mm_down(MmDownArgs a) {
         }
     }
     // the min terms of every token and sub-block, through LDS
-    if (w < 4 && col < 8) {
+    if (w < MS && col < 8) {
 #pragma unroll
         for (int r = 0; r < 4; ++r) mins[16 * w + 4 * kq + r][col] = accm[r];
     }
     __syncthreads();
     const MmOutDev& o = a.out;
 #pragma unroll
-    for (int ms = 0; ms < MM_MS; ++ms)
+    for (int ms = 0; ms < MS; ++ms)
 #pragma unroll
         for (int r = 0; r < 4; ++r) {
             const int tk = 16 * ms + 4 * kq + r;
@@ -1505,7 +1518,9 @@ hipError_t launch_mm_down(hipStream_t st, const uint8_t* tiled, int64_t n_in, in
     a.M = (int)M;
     a.n_in = n_in;
     a.N = N;
-    const int64_t nsl = n_in / 32, nb = N / 256, mt = Mp / MM_TOK;
+    // launches of at most 32 tokens take 32-token tiles
+    const int ms = M <= 32 ? 2 : MM_MS;
+    const int64_t nsl = n_in / 32, nb = N / 256, mt = ms == MM_MS ? Mp / MM_TOK : 1;
     int S = mm_splits(nb * mt, nsl, cu_count, MMD_SPLIT_COST);
     if (S > 1 && (!part || (size_t)S * (size_t)Mp * (size_t)N > part_floats)) S = 1;
     a.slices_per_split = (int)((nsl + S - 1) / S);
@@ -1523,8 +1538,12 @@ hipError_t launch_mm_down(hipStream_t st, const uint8_t* tiled, int64_t n_in, in
         a.out = out_dev(out);
     }
     a.ntt = (int)mt;
-    ktimed_launch(k_mm_down, dim3((unsigned)(nb * mt), 1, (unsigned)S), dim3(64 * MMD_WAVES),
-                       0, st, a);
+    if (ms == 2)
+        ktimed_launch(k_mm_down<2>, dim3((unsigned)(nb * mt), 1, (unsigned)S), dim3(64 * MMD_WAVES), 0,
+                      st, a);
+    else
+        ktimed_launch(k_mm_down<MM_MS>, dim3((unsigned)(nb * mt), 1, (unsigned)S),
+                      dim3(64 * MMD_WAVES), 0, st, a);
     hipError_t e = hipGetLastError();
     if (e != hipSuccess || S == 1) return e;
     if (pend && out.accum && out.nseq == 1) {
