@@ -134,11 +134,11 @@ def test_large_chain_one_pass(gctx, orc, M):
     assert rel_err_rows(got, want) < LOGIT_TOL
 
 
-@pytest.mark.parametrize("M", [20, 130])
+@pytest.mark.parametrize("M", [12, 20, 130])
 def test_large_chain_q6k_one_pass(gctx, orc, M):
     """Q6_K projections (q / k / v, o, gate / up with SwiGLU) and a Q6_K head
     through the one-pass GEMM's Q6_K operand (scale split 16 sh + sl), one
-    32-token tile and three 64-token tiles; ffn_down Q4_K."""
+    16- and one 32-token tile, and three 64-token tiles; ffn_down Q4_K."""
     dts = dict(tok_embd=P.Q8_0, output=P.Q6_K, q=P.Q6_K, k=P.Q6_K, v=P.Q6_K, o=P.Q6_K,
                gate=P.Q6_K, up=P.Q6_K, down=P.Q4_K)
     cfg = P.model_cfg(2, 1024, 8, 2, 128, 2048, 700, rope_theta=500000.0)
