@@ -4,7 +4,11 @@ device buffers.  Both run the same kernels in the same order, so the outputs
 are bit-identical; two calls in a row (the second on a smaller input) show
 that the shared scratch array keeps no state a later call depends on.  The
 error paths (host buffers, a shape above the scratch limit) return their
-codes without launching anything."""
+codes without launching anything.  Captured into a HIP graph on a stream of
+the caller's, the call records its kernels only (no allocation, memset or
+synchronisation), and every replay of the graph gives the eager result."""
+import ctypes
+
 import numpy as np
 import pytest
 
@@ -61,3 +65,67 @@ def test_down_axpy_noalloc_errors(gctx):
     assert lib.ftx_down_axpy_noalloc(h, bx.ptr, 2, 32, W.handle, by.ptr) == -1
     for o in (bx, by, W):
         o.free()
+
+
+def _hip():
+    hip = ctypes.CDLL("libamdhip64.so")
+    vp = ctypes.c_void_p
+    for name, args in (("hipStreamCreate", [ctypes.POINTER(vp)]),
+                       ("hipStreamDestroy", [vp]),
+                       ("hipStreamSynchronize", [vp]),
+                       ("hipStreamBeginCapture", [vp, ctypes.c_int]),
+                       ("hipStreamEndCapture", [vp, ctypes.POINTER(vp)]),
+                       ("hipGraphInstantiate", [ctypes.POINTER(vp), vp, vp, vp, ctypes.c_size_t]),
+                       ("hipGraphLaunch", [vp, vp]),
+                       ("hipGraphExecDestroy", [vp]),
+                       ("hipGraphDestroy", [vp])):
+        f = getattr(hip, name)
+        f.restype = ctypes.c_int
+        f.argtypes = args
+    return hip
+
+
+def test_down_axpy_noalloc_graph_capture(gctx, orc):
+    lib, h = gctx.lib, gctx.h
+    hip = _hip()
+    rng = np.random.default_rng(23)
+    M, n_in, N = 8, 2048, 1024
+    w = q_rows(orc, rng, n_in, N, P.Q4_K)
+    W = gctx.upload(w["raw"], P.Q4_K, (N, n_in))
+    x = (rng.standard_normal((M, n_in)) * 0.5).astype(np.float32)
+    y0 = rng.standard_normal((M, N)).astype(np.float32)
+    bx, bw, by = _device(gctx, x), _device(gctx, y0), _device(gctx, y0)
+    assert lib.ftx_down_axpy(h, bx.ptr, M, n_in, W.handle, bw.ptr) == 0
+    want = bw.read(np.float32, M * N).reshape(M, N)
+    # one eager call first: the scratch array's address is looked up then
+    assert lib.ftx_down_axpy_noalloc(h, bx.ptr, M, n_in, W.handle, by.ptr) == 0, gctx.error()
+    gctx.sync()
+    assert np.array_equal(by.read(np.float32, M * N).reshape(M, N), want)
+    st, graph, exe = ctypes.c_void_p(), ctypes.c_void_p(), ctypes.c_void_p()
+    assert hip.hipStreamCreate(ctypes.byref(st)) == 0
+    try:
+        gctx.set_stream(st.value)
+        assert hip.hipStreamBeginCapture(st, 2) == 0  # relaxed mode
+        rc = lib.ftx_down_axpy_noalloc(h, bx.ptr, M, n_in, W.handle, by.ptr)
+        assert hip.hipStreamEndCapture(st, ctypes.byref(graph)) == 0
+        assert rc == 0, gctx.error()
+        assert hip.hipGraphInstantiate(ctypes.byref(exe), graph, None, None, 0) == 0
+        for rep in range(3):
+            # eager work and a synchronisation between the replays
+            by.write(y0)
+            assert lib.ftx_down_axpy(h, bx.ptr, M, n_in, W.handle, bw.ptr) == 0
+            gctx.sync()
+            assert hip.hipGraphLaunch(exe, st) == 0
+            assert hip.hipStreamSynchronize(st) == 0
+            got = by.read(np.float32, M * N).reshape(M, N)
+            assert np.array_equal(got, want), rep
+    finally:
+        gctx.set_stream(None)
+        if exe.value:
+            hip.hipGraphExecDestroy(exe)
+        if graph.value:
+            hip.hipGraphDestroy(graph)
+        hip.hipStreamSynchronize(st)
+        hip.hipStreamDestroy(st)
+    for b in (bx, bw, by, W):
+        b.free()
