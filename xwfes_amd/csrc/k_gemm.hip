@@ -466,21 +466,23 @@ typedef __attribute__((address_space(3))) void lds_void;
 template <int DT, int MS>
 constexpr int MM_WPE = (MS == 1 && DT == FTX_Q4_0_MMT) ? 4 : 2;
 
-// grid = (ceil(units / 8), Mp / 64, splits); block = 512.  Per 256-element
-// step the workgroup's activation fragments (4 token tiles x 8 K-steps, hi
-// and lo: 64 KB) are copied to one of two LDS buffers by direct loads (8
-// per wave), issued a whole step ahead together with the next step's
-// weights (two register sets used in turn); one wait and one barrier per
-// step.  Every wave takes part in the copies and barriers, and none
-// branches around its MFMAs: a wave past the last unit computes on its
-// clamped rows and stores nothing.
-// XT (expert launches): grid.y walks the routing's tile table; a tile past
-// the tiles in use ends at once (the whole workgroup), the weights are the
-// tile's expert's planes, and 16-token tiles past the tile's rows in use
-// are neither copied nor multiplied (a block-uniform choice).  MS: 16-token
-// MFMA tiles per workgroup tile (4 for 64-token tiles; 1 for the 16-row
-// expert tiles of routings with few tokens per expert, whose 32 KB of LDS
-// and smaller register set let several workgroups share a CU).
+// grid = (ceil(units / 8) x token tiles, 1, splits), workgroup b taking
+// token tile b % ntt of unit group b / ntt; block = 512.  Per 256-element
+// step the workgroup's activation fragments (MS 16-token tiles x 8 K-steps,
+// hi and lo: 16 MS KB) are copied to one of two LDS buffers by direct loads,
+// issued a whole step ahead together with the next step's weights (two
+// register sets used in turn); one wait and one barrier per step.  Every
+// wave takes part in the copies and barriers, and none branches around its
+// MFMAs: a wave past the last unit computes on its clamped rows and stores
+// nothing.
+// XT (expert launches): the token tile index walks the routing's tile
+// table; a tile past the tiles in use ends at once (the whole workgroup),
+// the weights are the tile's expert's planes, and 16-token tiles past the
+// tile's rows in use are neither copied nor multiplied (a block-uniform
+// choice).  MS: 16-token MFMA tiles per workgroup tile (4 for 64-token
+// tiles; 2 / 1 for dense launches of at most 32 / 16 tokens; 1 for the
+// 16-row expert tiles of routings with few tokens per expert, whose 32 KB
+// of LDS and smaller register set let several workgroups share a CU).
 template <int DT, bool XT, int MS>
 __global__ void __launch_bounds__(64 * MM_WAVES)
     __attribute__((amdgpu_waves_per_eu(MM_WPE<DT, MS>, MM_WPE<DT, MS>))) k_mm(MmArgs a) {
@@ -816,16 +818,17 @@ struct MmDownArgs {
     MmOutDev out;
 };
 
-// grid = (N / 256 x Mp / 64, 1, splits); block = 512: wave w owns columns
-// 256 bx + 32 w .. + 31 (two 16-column tiles ct, all in sub-block w of the
-// block) for all 64 tokens, so that each weight operand is built once and
-// feeds eight MFMAs; per 32-row slice the workgroup stages, for its 64
+// grid = (N / 256 x token tiles, 1, splits); block = 512: wave w owns
+// columns 256 bx + 32 w .. + 31 (two 16-column tiles ct, all in sub-block w
+// of the block) for all of the workgroup's 16 MS tokens (64, or 32 for
+// launches of at most 32 tokens), so that each weight operand is built once
+// and feeds 4 MS MFMAs; per 32-row slice the workgroup stages, for its
 // tokens, A_d = h d 2^10 and A_m = h dmin 2^10 (hi / lo) and the fp16 tables
-// of the block's 8 sub-block scales (also as -1024 sc) and 8 mins, one
-// table entry per thread; y = (sum_i A_d sc q - sum_i A_m mn) / 2^10 with
-// the min term (one 16-column MFMA tile whose columns are the sub-blocks)
-// done by wave w < 4 for tokens 16 w .. 16 w + 15 and handed to the other
-// waves through LDS.
+// of the block's 8 sub-block scales (also as -1024 sc) and 8 mins, one table
+// entry per thread; y = (sum_i A_d sc q - sum_i A_m mn) / 2^10 with the min
+// term (one 16-column MFMA tile whose columns are the sub-blocks) done by
+// wave w < MS for tokens 16 w .. 16 w + 15 and handed to the other waves
+// through LDS.
 constexpr int MMD_PITCH = 32 + 8;
 constexpr int MMD_WAVES = 8;  // two per SIMD
 constexpr int MMD_RING = 4;  // slices whose global operands are in flight (even: LDS buffer = slice parity)
