@@ -9,6 +9,11 @@ context 2040: the logits within 1e-3 relative of the oracle's forward
 tensors from a pool of four (two per mix), each with its own norm weights,
 so that a layer index error changes the result; the error of the int8 x 2-limb
 activations accumulates over all 32 layers here.
+
+test_tree52_full_depth: the same shape at 32 layers with Q8_0 attention
+projections and a Q4_K FFN, the 52-node draft tree (branching 4, 4, 2) at
+context 4096: every projection on the one-pass GEMMs (fp16 hi + lo
+activations), attention on the many-row tree kernel, all 32 layers' error.
 """
 import numpy as np
 import pytest
@@ -58,15 +63,7 @@ def test_verify_8b_full_depth(gctx, orc):
         model[p + "ffn_norm"] = norm_raw(rng, D)
         for nm, t in src.items():
             model[p + nm] = t
-    # one device tensor per distinct host tensor
-    up = {}
-    tensors = {}
-    for name, t in model.items():
-        if name == "cfg":
-            continue
-        if id(t) not in up:
-            up[id(t)] = gctx.upload(t["raw"], t["dtype"], (t["ne0"], t["ne1"]))
-        tensors[name] = up[id(t)]
+    up, tensors = _upload_dedup(gctx, model)
     npast, M = 2040, 8
     cap = npast + M
     gm = gctx.model(cfg, tensors, max_tokens=M)
@@ -92,6 +89,82 @@ def test_verify_8b_full_depth(gctx, orc):
     want = orc.forward(model, k0, v0, npast, toks)
     err = rel_err_rows(got, want)
     print("32-layer 8B chain at context 2040: max row error %.3g" % err)
+    assert err < LOGIT_TOL
+
+
+def _upload_dedup(gctx, model):
+    """One device tensor per distinct host tensor."""
+    up, tensors = {}, {}
+    for name, t in model.items():
+        if name == "cfg":
+            continue
+        if id(t) not in up:
+            up[id(t)] = gctx.upload(t["raw"], t["dtype"], (t["ne0"], t["ne1"]))
+        tensors[name] = up[id(t)]
+    return up, tensors
+
+
+def _tree_parents(branching):
+    parents, level = [], [-1]
+    for b in branching:
+        nxt = []
+        for par in level:
+            for _ in range(b):
+                parents.append(par)
+                nxt.append(len(parents) - 1)
+        level = nxt
+    return parents
+
+
+def test_tree52_full_depth(gctx, orc):
+    orc.set_threads(16)
+    L, D, F, V = 32, 4096, 14336, 128256
+    cfg = P.model_cfg(L, D, 32, 8, 128, F, V, rope_theta=500000.0)
+    rng = np.random.default_rng(5252)
+
+    def q(rows, cols, dt):
+        return q_rows(orc, rng, rows, cols, dt)
+
+    pool = [dict(q=q(4096, D, P.Q8_0), k=q(1024, D, P.Q8_0), v=q(1024, D, P.Q8_0),
+                 o=q(4096, D, P.Q8_0), gate=q(F, D, P.Q4_K), up=q(F, D, P.Q4_K),
+                 down=q(F, D, P.Q4_K)) for _ in range(4)]
+    model = {"cfg": dict(cfg)}
+    model["tok_embd"] = q(V, D, P.Q4_K)
+    model["output"] = q(V, D, P.Q6_K)
+    model["out_norm"] = norm_raw(rng, D)
+    for l in range(L):
+        p = "blk.%d." % l
+        model[p + "attn_norm"] = norm_raw(rng, D)
+        model[p + "ffn_norm"] = norm_raw(rng, D)
+        for nm, t in pool[(l * 3) % 4].items():
+            model[p + nm] = t
+    up, tensors = _upload_dedup(gctx, model)
+    parents = _tree_parents((4, 4, 2))
+    M = len(parents)
+    npast, cap = 4096, 4096 + 64
+    gm = gctx.model(cfg, tensors, max_tokens=M)
+    kv = gm.kv(cap)
+    krng = np.random.default_rng(6)
+    shape = kv.shape
+    k0 = np.zeros(shape, np.float16)
+    v0 = np.zeros(shape, np.float16)
+    k0[:, :npast] = krng.standard_normal((L, npast, shape[2]))
+    v0[:, :npast] = krng.standard_normal((L, npast, shape[2]))
+    kv.write(k0, v0)
+    kv.truncate(npast)
+    toks = rng.integers(0, V, M).tolist()
+    buf = gctx.buffer(M * V * 4)
+    gm.verify(kv, toks, buf.ptr, parents=parents)
+    gctx.sync()
+    got = buf.read(np.float32, M * V).reshape(M, V)
+    buf.free()
+    kv.free()
+    gm.free()
+    for t in up.values():
+        t.free()
+    want = orc.forward(model, k0, v0, npast, toks, parents=parents)
+    err = rel_err_rows(got, want)
+    print("32-layer 8B 52-node tree at context 4096: max row error %.3g" % err)
     assert err < LOGIT_TOL
 
 
