@@ -14,6 +14,12 @@ test_tree52_full_depth: the same shape at 32 layers with Q8_0 attention
 projections and a Q4_K FFN, the 52-node draft tree (branching 4, 4, 2) at
 context 4096: every projection on the one-pass GEMMs (fp16 hi + lo
 activations), attention on the many-row tree kernel, all 32 layers' error.
+
+test_mixtral_full_depth: the Mixtral 8x7B shape (8 experts of FFN 14336,
+top-2, Q4_0, vocab 32000) at its full 32 layers, four sequences of 8 tokens
+at context 1024 in one batched step: the routing, the expert GEMMs and the
+combine of every layer, against the oracle's forward of each sequence
+(src/engine.cpp:179-258, moe_ffn).
 """
 import numpy as np
 import pytest
@@ -93,13 +99,18 @@ def test_verify_8b_full_depth(gctx, orc):
 
 
 def _upload_dedup(gctx, model):
-    """One device tensor per distinct host tensor."""
+    """One device tensor per distinct host tensor (expert tensors as
+    (cols, rows per expert, experts))."""
+    E = model["cfg"].get("n_expert", 0)
     up, tensors = {}, {}
     for name, t in model.items():
         if name == "cfg":
             continue
         if id(t) not in up:
-            up[id(t)] = gctx.upload(t["raw"], t["dtype"], (t["ne0"], t["ne1"]))
+            ne = (t["ne0"], t["ne1"])
+            if name.endswith("_exps"):
+                ne = (t["ne0"], t["ne1"] // E, E)
+            up[id(t)] = gctx.upload(t["raw"], t["dtype"], ne)
         tensors[name] = up[id(t)]
     return up, tensors
 
@@ -166,6 +177,69 @@ def test_tree52_full_depth(gctx, orc):
     err = rel_err_rows(got, want)
     print("32-layer 8B 52-node tree at context 4096: max row error %.3g" % err)
     assert err < LOGIT_TOL
+
+
+def test_mixtral_full_depth(gctx, orc):
+    orc.set_threads(16)
+    L, D, F, V, E = 32, 4096, 14336, 32000, 8
+    cfg = P.model_cfg(L, D, 32, 8, 128, F, V, rope_theta=1e6, n_expert=E, n_expert_used=2)
+    rng = np.random.default_rng(3232)
+
+    def layer():
+        t = {nm: q_rows(orc, rng, rows, D, P.Q4_0)
+             for nm, rows in (("q", D), ("k", 1024), ("v", 1024), ("o", D))}
+        w = (rng.standard_normal((E, D)) * (2.0 / np.sqrt(D))).astype(np.float32)
+        t["gate_inp"] = dict(raw=w.view(np.uint8).ravel().copy(), dtype=P.F32, ne0=D, ne1=E)
+        for nm in ("gate_exps", "up_exps", "down_exps"):
+            planes = [q_rows(orc, rng, F, D, P.Q4_0, unique=1024)["raw"] for _ in range(E)]
+            t[nm] = dict(raw=np.concatenate(planes), dtype=P.Q4_0, ne0=D, ne1=E * F)
+        return t
+
+    pool = [layer(), layer()]
+    model = {"cfg": dict(cfg)}
+    model["tok_embd"] = q_rows(orc, rng, V, D, P.Q8_0, unique=1024)
+    model["output"] = q_rows(orc, rng, V, D, P.Q4_0, unique=1024)
+    model["out_norm"] = norm_raw(rng, D)
+    for l in range(L):
+        p = "blk.%d." % l
+        model[p + "attn_norm"] = norm_raw(rng, D)
+        model[p + "ffn_norm"] = norm_raw(rng, D)
+        for nm, t in pool[l % 2].items():
+            model[p + nm] = t
+    up, tensors = _upload_dedup(gctx, model)
+    gm = gctx.model(cfg, tensors, max_tokens=32)
+    seqs = [(rng.integers(0, V, 8).tolist(), 1024 - 8 - s, 1024) for s in range(4)]
+    kvs, bufs, ctxs, args = [], [], [], []
+    for i, (toks, npast, cap) in enumerate(seqs):
+        kv = gm.kv(cap)
+        krng = np.random.default_rng(60 + i)
+        shape = kv.shape
+        k0 = np.zeros(shape, np.float16)
+        v0 = np.zeros(shape, np.float16)
+        k0[:, :npast] = krng.standard_normal((L, npast, shape[2]))
+        v0[:, :npast] = krng.standard_normal((L, npast, shape[2]))
+        kv.write(k0, v0)
+        kv.truncate(npast)
+        buf = gctx.buffer(len(toks) * V * 4)
+        kvs.append(kv)
+        bufs.append(buf)
+        ctxs.append((k0, v0))
+        args.append((kv, toks, buf.ptr, None, False))
+    gm.verify_batch(args)
+    gctx.sync()
+    got = [b.read(np.float32, 8 * V).reshape(8, V) for b in bufs]
+    for o in bufs + kvs:
+        o.free()
+    gm.free()
+    for t in up.values():
+        t.free()
+    errs = []
+    for (toks, npast, cap), g, (k0, v0) in zip(seqs, got, ctxs):
+        want = orc.forward(model, k0, v0, npast, toks)
+        errs.append(rel_err_rows(g, want))
+    print("32-layer Mixtral-shaped batch, 4 x 8 tokens at context 1024: max row errors %s"
+          % ", ".join("%.3g" % e for e in errs))
+    assert max(errs) < LOGIT_TOL
 
 
 def test_trace_disarmed_after_failed_launch(orc):
