@@ -490,10 +490,12 @@ __global__ void __launch_bounds__(64 * MM_WAVES)
     const int tid = threadIdx.x, lane = tid & 63;
     const int w = __builtin_amdgcn_readfirstlane(tid >> 6);
     const int col = lane & 15, kq = lane >> 4;
-    // the token tiles of one weight unit are neighbours in the grid, so they
-    // run together and a unit's weights come from memory about once
-    const int by = (int)(blockIdx.x % (unsigned)a.ntt);
-    const int64_t u = (int64_t)(blockIdx.x / (unsigned)a.ntt) * MM_WAVES + w;
+    // the token tiles of one weight unit are logical neighbours on one XCD,
+    // so they run together and a unit's weights come from memory about once
+    const uint32_t lb = xcd_order(blockIdx.x + gridDim.x * blockIdx.z, gridDim.x * gridDim.z);
+    const uint32_t bx = lb % gridDim.x;
+    const int by = (int)(bx % (unsigned)a.ntt);
+    const int64_t u = (int64_t)(bx / (unsigned)a.ntt) * MM_WAVES + w;
     const bool live = u < a.units;  // wave-uniform
     const int si = mm_seg_of(a, live ? u : a.units - 1);
     MmSegDev sg = a.seg[si];
@@ -507,7 +509,7 @@ __global__ void __launch_bounds__(64 * MM_WAVES)
         nsub = (nv + 15) >> 4;
         mend = by * 16 * MS + nv;
     }
-    const int ks = blockIdx.z;
+    const int ks = (int)(lb / gridDim.x);
     const int sb0 = ks * a.sb_per_split;
     const int sb1 = min(sb0 + a.sb_per_split, a.nsb);
     const int64_t nks = a.K / 32;
@@ -863,11 +865,13 @@ k_mm_down(MmDownArgs a) {
     const int tid = threadIdx.x, lane = tid & 63;
     const int w = __builtin_amdgcn_readfirstlane(tid >> 6);
     const int col = lane & 15, kq = lane >> 4;
-    // token tiles of one column block are neighbours in the grid (they share
-    // the block's weights)
-    const int64_t jb = blockIdx.x / (unsigned)a.ntt;
-    const int64_t m0 = (int64_t)(blockIdx.x % (unsigned)a.ntt) * TOK;
-    const int ks = blockIdx.z;
+    // token tiles of one column block are logical neighbours on one XCD
+    // (they share the block's weights)
+    const uint32_t lb = xcd_order(blockIdx.x + gridDim.x * blockIdx.z, gridDim.x * gridDim.z);
+    const uint32_t bx = lb % gridDim.x;
+    const int64_t jb = bx / (unsigned)a.ntt;
+    const int64_t m0 = (int64_t)(bx % (unsigned)a.ntt) * TOK;
+    const int ks = (int)(lb / gridDim.x);
     const int64_t nsl = a.n_in / 32, nc64 = a.N / 64;
     const int64_t I0 = (int64_t)ks * a.slices_per_split;
     const int64_t I1 = min(I0 + (int64_t)a.slices_per_split, nsl);

@@ -45,6 +45,17 @@ __device__ __forceinline__ v8h i8x8(v2i w) {
     return v8h{h0[0], h0[1], h1[0], h1[1], h2[0], h2[1], h3[0], h3[1]};
 }
 
+// The hardware deals a launch's workgroups to the 8 XCDs in turn (linear
+// workgroup id modulo 8), and each XCD has its own L2.  xcd_order maps the
+// linear id to a logical index under which every XCD owns one contiguous run
+// (XCD x: ids x, x + 8, x + 16, .. -> run x, in dispatch order), so that
+// workgroups whose logical indices are neighbours (the token tiles of one
+// weight tile) run on one XCD and share its L2.  A bijection of [0, total).
+__device__ __forceinline__ uint32_t xcd_order(uint32_t lin, uint32_t total) {
+    const uint32_t per = total >> 3, rem = total & 7, x = lin & 7, i = lin >> 3;
+    return (x < rem ? x * (per + 1) : rem * (per + 1) + (x - rem) * per) + i;
+}
+
 // slot of element (token m, contraction k) in the one-pass GEMM's fragment-
 // order operand planes ([Mp / 16][K / 32][64 lanes][8]; inter: each octet
 // as its even then its odd elements, for Q4_0 weights)
