@@ -526,6 +526,7 @@ struct AttnMArgs {
     float* out;          // [M][n_head*hd]
     float *pmax, *psum, *pout;  // chunk partials
     int nc = 1;          // chunks per workgroup (and per partial)
+    int pslots = 0;      // slots per partial (set by the launcher)
     MmFragDst frag;      // frag.xh set: the fp32 combine writes this operand instead of out
 };
 bool attn_mfma_supported(int64_t hd, int kv_f16, int64_t M, int64_t n_head, int64_t n_kv);

@@ -451,8 +451,8 @@ __device__ __forceinline__ void attn_mfma_wg_mc(const AttnMArgs& a, int grp, int
 
 // More than 16 query rows per kv head (chains of several tokens, draft
 // trees, batches of trees): one workgroup of FA_WAVES waves takes 16 query
-// rows per wave of one kv head over a group of a.nc blocks of
-// chunk_slots(HD) slots (the partials' unit, as in attn_mfma_wg_mc), so each
+// rows per wave of one kv head over a group of a.pslots slots (whole
+// 64-slot chunks, at least one chunk_slots(HD) block; one partial each), so each
 // K / V row is read by ceil(rows / 128) workgroups instead of one per 32
 // rows.  The group's 64-slot chunks are copied to LDS by direct
 // global->LDS loads one chunk ahead (double buffer, one barrier per chunk),
@@ -498,16 +498,15 @@ __device__ __forceinline__ void attn_fa_wg(const AttnMArgs& a, int grp, int kvh,
     static_assert(NB % FA_WAVES == 0 && NDC % BPW == 0 && BPW % 2 == 0,
                   "a wave copies blocks of one slot tile of K, or whole dim tiles of V^T");
     constexpr int BUF = NB * 1024;
-    constexpr int CPB = chunk_slots(HD) / FA_CHK;  // chunks per partial block
-    static_assert(CPB * FA_CHK == chunk_slots(HD), "whole chunks per block");
+    static_assert(chunk_slots(HD) % FA_CHK == 0, "whole chunks per block");
     extern __shared__ __attribute__((aligned(16))) uint8_t fa_lds[];
     const int tid = threadIdx.x, lane = tid & 63;
     const int w = __builtin_amdgcn_readfirstlane(tid >> 6);
     const int col = lane & 15, kq = lane >> 4;
     const int64_t npast = a.npast, total = npast + a.M;
-    const int64_t gslot0 = (int64_t)grp * a.nc * chunk_slots(HD);
+    const int64_t gslot0 = (int64_t)grp * a.pslots;
     if (gslot0 >= total) return;  // block-uniform
-    const int nck = (int)min((int64_t)a.nc * CPB, (total - gslot0 + FA_CHK - 1) / FA_CHK);
+    const int nck = (int)min((int64_t)(a.pslots / FA_CHK), (total - gslot0 + FA_CHK - 1) / FA_CHK);
     const int gqa = a.n_head / a.n_kv, qrows = a.M * gqa;
     const int rbase = (qsplit * FA_WAVES + w) * 16;  // the wave's first query row
     const bool wlive = rbase < qrows;                // wave-uniform
@@ -715,7 +714,7 @@ __device__ __forceinline__ void attn_combine_row(const AttnMArgs& a, int64_t qi,
     __shared__ float wsh[2][1024];  // chunk weights (nch <= 1024) per wave
     const int d = threadIdx.x, wv = d >> 6, lane = d & 63;
     const int64_t npast = a.npast;
-    const int ch = chunk_slots(a.hd) * a.nc;  // slots per partial
+    const int ch = a.pslots;  // slots per partial
     const int nvalid = (int)((npast + a.M + ch - 1) / ch);
     const float* pm = a.pmax + qi * nch;
     const float* pz = a.psum + qi * nch;
@@ -805,7 +804,7 @@ __global__ void __launch_bounds__(256) k_attn_combine_xq(AttnMArgs a, int nch, X
     __shared__ float4 red[4][64];
     const int64_t sb = blockIdx.x;
     const int m = blockIdx.y, tid = threadIdx.x, w = tid >> 6, l = tid & 63;
-    constexpr int ch = chunk_slots(HD);
+    const int ch = a.pslots;  // slots per partial
     const int nvalid = (int)((a.npast + a.M + ch - 1) / ch);
     const int hh = (4 * l) / HD, d = (4 * l) % HD;
     float v[4] = {0.f, 0.f, 0.f, 0.f};
@@ -926,23 +925,26 @@ static int attn_chunks_per_wg(int64_t wgs) {
 static bool attn_fa_rows(int64_t qrows) { return qrows > 16; }
 static int attn_fa_splits(int64_t qrows) { return (int)((qrows + 16 * FA_WAVES - 1) / (16 * FA_WAVES)); }
 
-// Blocks of chunk_slots(hd) slots per workgroup for the many-row kernel:
-// sequence s has nblk[s] live blocks and splits[s] row splits; with nc
-// blocks per workgroup the live workgroups run in rounds of 256, a round
-// costing about 3 + (chunks per workgroup) chunk times (measured: ~3 us of
-// start and ~1-2 us per 64-slot chunk); the cheapest nc <= 16, the largest
-// on ties (fewer partials for the combine).
-static int attn_fa_blocks_per_wg(const int64_t* nblk, const int* splits, int nseq, int n_kv,
-                                 int cpb) {
-    int best = 1;
+// 64-slot chunks per workgroup (and per partial) for the many-row kernel:
+// sequence s has nchk[s] live chunks and splits[s] row splits; with g
+// chunks per workgroup the live workgroups run in rounds of 256, a round
+// costing about 3 + g chunk times (measured: ~3 us of start and ~1-2 us per
+// chunk, the chunk's MFMAs and softmax); the cheapest g in [gmin, 32], the
+// largest on ties (fewer partials for the combine).  gmin = the chunks of
+// one chunk_slots(hd) block, so the partials fit the buffer sized per block.
+// Whole chunks rather than whole blocks let the 52-node tree at context
+// 4096 take 224 workgroups of 5 chunks instead of 176 of 6.
+static int attn_fa_chunks_per_wg(const int64_t* nchk, const int* splits, int nseq, int n_kv,
+                                 int gmin) {
+    int best = gmin;
     int64_t best_cost = -1;
-    for (int nc = 1; nc <= 16; ++nc) {
+    for (int g = gmin; g <= 32; ++g) {
         int64_t wgs = 0;
-        for (int s = 0; s < nseq; ++s) wgs += (nblk[s] + nc - 1) / nc * n_kv * splits[s];
-        const int64_t cost = (wgs + 255) / 256 * (3 + (int64_t)nc * cpb);
+        for (int s = 0; s < nseq; ++s) wgs += (nchk[s] + g - 1) / g * n_kv * splits[s];
+        const int64_t cost = (wgs + 255) / 256 * (3 + (int64_t)g);
         if (best_cost < 0 || cost <= best_cost) {
             best_cost = cost;
-            best = nc;
+            best = g;
         }
     }
     return best;
@@ -972,9 +974,12 @@ hipError_t launch_attn_mfma(hipStream_t st, AttnMArgs a, float* part, int8_t* xq
     const int64_t qrows = (int64_t)a.M * (a.n_head / a.n_kv);
     if (attn_fa_rows(qrows)) {
         const int qs = attn_fa_splits(qrows);
-        const int64_t nblk = (a.npast + a.M + ch - 1) / ch;
-        a.nc = xq ? 1 : attn_fa_blocks_per_wg(&nblk, &qs, 1, a.n_kv, ch / FA_CHK);
-        const int ngrp = (nch + a.nc - 1) / a.nc;  // the partials' stride
+        const int64_t nchk = (a.npast + a.M + FA_CHK - 1) / FA_CHK;
+        // the combine that writes the GEMV operand takes one block per
+        // partial (the 8-token chain: 136 workgroups of two chunks)
+        const int g = xq ? ch / FA_CHK : attn_fa_chunks_per_wg(&nchk, &qs, 1, a.n_kv, ch / FA_CHK);
+        a.pslots = g * FA_CHK;
+        const int ngrp = (int)((a.cap + a.pslots - 1) / a.pslots);  // the partials' stride
         a.pmax = part;
         a.psum = part + qi * ngrp;
         a.pout = part + 2 * qi * ngrp;
@@ -1000,6 +1005,7 @@ hipError_t launch_attn_mfma(hipStream_t st, AttnMArgs a, float* part, int8_t* xq
     const int qtiles = (int)((a.M * (a.n_head / a.n_kv) + 31) / 32);
     const int64_t nvalid = (a.npast + a.M + ch - 1) / ch;
     a.nc = xq ? 1 : attn_chunks_per_wg(nvalid * a.n_kv * qtiles);
+    a.pslots = a.nc * ch;
     const int ngrp = (nch + a.nc - 1) / a.nc;  // the partials' stride
     a.pmax = part;
     a.psum = part + qi * ngrp;
@@ -1042,24 +1048,27 @@ hipError_t launch_attn_mfma_batch(hipStream_t st, const AttnMArgs* as, const flo
     bool fa = true;
     for (int s = 0; s < nseq; ++s) fa = fa && attn_fa_rows((int64_t)as[s].M * (as[s].n_head / nkv));
     int64_t wgs = 0;  // the one-block grid's live workgroups
-    int64_t nblk[FTX_MAX_SEQ];
+    int64_t nblk[FTX_MAX_SEQ], nchk[FTX_MAX_SEQ];
     int splits[FTX_MAX_SEQ];
     for (int s = 0; s < nseq; ++s) {
         const int ch = chunk_slots(as[s].hd);
         if (as[s].hd != hd || as[s].n_kv != nkv || as[s].cap % ch) return hipErrorInvalidValue;
         const int64_t r = (int64_t)as[s].M * (as[s].n_head / nkv);
         nblk[s] = (as[s].npast + as[s].M + ch - 1) / ch;
+        nchk[s] = (as[s].npast + as[s].M + FA_CHK - 1) / FA_CHK;
         splits[s] = fa ? attn_fa_splits(r) : (int)((r + 31) / 32);
         wgs += nblk[s] * nkv * splits[s];
     }
-    const int nc = fa ? attn_fa_blocks_per_wg(nblk, splits, nseq, nkv, chunk_slots(hd) / FA_CHK)
-                      : attn_chunks_per_wg(wgs);
+    // many-row: g chunks per partial; otherwise nc blocks
+    const int g = fa ? attn_fa_chunks_per_wg(nchk, splits, nseq, nkv, chunk_slots(hd) / FA_CHK) : 0;
+    const int nc = fa ? 1 : attn_chunks_per_wg(wgs);
     for (int s = 0; s < nseq; ++s) {
         AttnMArgs a = as[s];
         const int ch = chunk_slots(a.hd);
         if (a.cap / ch > 1024) return hipErrorInvalidValue;  // combine weights live in LDS
         a.nc = nc;
-        const int nch = (int)((a.cap / ch + nc - 1) / nc);  // the partials' stride
+        a.pslots = fa ? g * FA_CHK : nc * ch;
+        const int nch = (int)((a.cap + a.pslots - 1) / a.pslots);  // the partials' stride
         const int64_t q = (int64_t)a.M * a.n_head;
         float* part = const_cast<float*>(parts[s]);
         a.pmax = part;
