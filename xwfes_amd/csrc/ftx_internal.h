@@ -351,6 +351,8 @@ struct MoeRoute {
     float* comb_w;       // [M][U]: their renormalised weights
     int32_t* te;         // [M][U]: token m's experts, descending probability
     float* tw;           // [M][U]: their renormalised weights
+    uint32_t* done;      // router workgroups finished in the running launch (0 between
+                         // launches; zero when the buffer is allocated)
 };
 // rows per routing tile (16 or 64) and the tile table bound of an M-token
 // step; the largest operand row count of any step up to Mmax tokens

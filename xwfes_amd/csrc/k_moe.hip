@@ -57,14 +57,18 @@ constexpr int MOE_GB = 4;      // 4096-element batches of a router row (n_embd <
 // descending order with ties to the lower index (std::partial_sort's order
 // for distinct values), the weights renormalised by their float sum
 // (src/engine.cpp:197-215).  Writes te[m][u] (expert), tw[m][u] (weight).
+__device__ void moe_route_wg(const int32_t* __restrict__ te_g, const float* __restrict__ tw_g,
+                             int M, int E, int U, int ntile_max, int TR, const MoeRoute& r);
+
 __global__ void __launch_bounds__(256) k_moe_gate(const float* __restrict__ x, int64_t K,
                                                   const float* __restrict__ normw, float eps,
                                                   float* __restrict__ xn,
                                                   const uint8_t* __restrict__ W, int dt,
                                                   int64_t row_bytes, const float* __restrict__ rbias,
-                                                  int E, int U, int32_t* __restrict__ te,
-                                                  float* __restrict__ tw) {
+                                                  int E, int U, int ntile_max, int TR, MoeRoute r) {
 #pragma clang fp contract(off)
+    int32_t* __restrict__ te = r.te;
+    float* __restrict__ tw = r.tw;
     extern __shared__ float xs[];  // [K] then the E logits
     __shared__ float red[4];
     float* lg = xs + K;
@@ -170,7 +174,7 @@ __global__ void __launch_bounds__(256) k_moe_gate(const float* __restrict__ x, i
         }
         __syncthreads();
     }
-    if (w != 0) return;
+    if (w == 0) {
     // softmax and top-U on wave 0: lane l holds experts l, l + 64, l + 128,
     // l + 192 (E <= 256); the arithmetic and its order as one thread's
     // loops: float max, float exp, double sum in expert order, float scale
@@ -232,16 +236,32 @@ __global__ void __launch_bounds__(256) k_moe_gate(const float* __restrict__ x, i
             te[m * U + u] = top[u];
             tw[m * U + u] = topw[u] * winv;
         }
+    }
+    // The last of the M router workgroups to finish groups the tokens (one
+    // launch fewer per MoE layer than a grouping kernel of its own).  Thread
+    // 0, which stored this token's choice, publishes it with a device-scope
+    // fence before counting the workgroup done; the last one's threads fence
+    // again before reading every token's choice.  The counter is back at 0
+    // when the launch ends.
+    __shared__ int last;
+    if (t == 0) {
+        __threadfence();
+        last = atomicAdd(r.done, 1u) == (unsigned)(gridDim.x - 1);
+    }
+    __syncthreads();
+    if (!last) return;  // block-uniform
+    __threadfence();
+    moe_route_wg(te, tw, (int)gridDim.x, E, U, ntile_max, TR, r);
+    if (t == 0) atomicExch(r.done, 0u);
 }
 
-// Grouping, one workgroup: thread e (strided) takes expert e: first use over
+// Grouping, by the last router workgroup: thread e (strided) takes expert e: first use over
 // (token, rank) and token count; thread 0 lays out the tiles (experts in
 // index order, ceil(count / 64) tiles each); thread e assigns its tokens'
 // operand rows in token order; thread m orders its experts by first use
 // for the combine (src/engine.cpp:210-239).
-__global__ void __launch_bounds__(256) k_moe_route(const int32_t* __restrict__ te_g,
-                                                   const float* __restrict__ tw_g, int M, int E,
-                                                   int U, int ntile_max, int TR, MoeRoute r) {
+__device__ void moe_route_wg(const int32_t* __restrict__ te_g, const float* __restrict__ tw_g,
+                             int M, int E, int U, int ntile_max, int TR, const MoeRoute& r) {
     __shared__ int te[MOE_MAXM * MOE_MAXU];
     __shared__ float tw[MOE_MAXM * MOE_MAXU];
     __shared__ int slot_of[MOE_MAXM * MOE_MAXU];
@@ -565,7 +585,7 @@ size_t moe_route_bytes(int64_t Mmax, int64_t E, int64_t U) {
     int64_t T, R;
     moe_max_dims(Mmax, E, U, &T, &R);
     return align256((size_t)(1 + 2 * T) * 4) + align256((size_t)R * 4) +
-           align256((size_t)(Mmax * U) * 4) * 4;
+           align256((size_t)(Mmax * U) * 4) * 4 + 256;
 }
 
 MoeRoute moe_route_view(void* buf, int64_t Mmax, int64_t E, int64_t U) {
@@ -584,6 +604,8 @@ MoeRoute moe_route_view(void* buf, int64_t Mmax, int64_t E, int64_t U) {
     r.te = (int32_t*)p;
     p += align256((size_t)(Mmax * U) * 4);
     r.tw = (float*)p;
+    p += align256((size_t)(Mmax * U) * 4);
+    r.done = (uint32_t*)p;
     return r;
 }
 
@@ -597,11 +619,8 @@ hipError_t launch_moe_route(hipStream_t st, const float* x, const float* normw, 
         return hipErrorInvalidValue;
     const size_t lds = (size_t)(K + E) * sizeof(float);
     hipLaunchKernelGGL(k_moe_gate, dim3((unsigned)M), dim3(256), lds, st, x, K, normw, eps, xn, W,
-                       dt, row_bytes, rbias, (int)E, (int)U, r.te, r.tw);
-    hipError_t e = hipGetLastError();
-    if (e != hipSuccess) return e;
-    hipLaunchKernelGGL(k_moe_route, dim3(1), dim3(256), 0, st, r.te, r.tw, (int)M, (int)E, (int)U,
-                       (int)moe_tiles_max(M, E, U), (int)moe_tile_rows(M, E, U), r);
+                       dt, row_bytes, rbias, (int)E, (int)U, (int)moe_tiles_max(M, E, U),
+                       (int)moe_tile_rows(M, E, U), r);
     return hipGetLastError();
 }
 

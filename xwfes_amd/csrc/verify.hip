@@ -1005,6 +1005,8 @@ int ftx_model_create(ftx_ctx* ctx, const ftx_model_desc* d, ftx_model** out) {
              dalloc(&m->moe_act, mm_act_halves(rows, D)) &&
              dalloc(&m->moe_h, (size_t)(2 * rows * d->n_ff)) && dalloc(&m->moe_part, m->moe_part_n) &&
              (!F_sh || dalloc(&m->tmpo, (size_t)(Mmax * D)));
+        // the router's finished-workgroup counter starts at zero
+        ok = ok && hipMemset(m->route, 0, moe_route_bytes(Mmax, E, U)) == hipSuccess;
     }
     if (!ok) {
         model_release(m);
