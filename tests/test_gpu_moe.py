@@ -94,11 +94,13 @@ MOE = P.model_cfg(2, 256, 4, 2, 64, 256, 500, n_expert=8, n_expert_used=2)
 
 
 @pytest.mark.parametrize("case", ["q4_0", "q8_0_gate_up", "bias_shared_top3"])
-@pytest.mark.parametrize("M", [1, 7, 40])
+@pytest.mark.parametrize("M", [1, 7, 40, 100, 250])
 def test_moe_chain(gctx, orc, case, M):
-    """One sequence of M tokens (decode, a short chain, a long chain) through
+    """One sequence of M tokens (decode, a short chain, long chains) through
     the MoE layers: Q4_0 experts; Q8_0 gate / up experts; a router bias, a
-    shared expert and top-3 of 8."""
+    shared expert and top-3 of 8.  Above 64 tokens (top-2; 43 for top-3) the
+    routing takes 64-row tiles, and up to 250 router workgroups meet at the
+    grouping."""
     cfg, dts, extras = dict(MOE), dict(DT), ()
     if case == "q8_0_gate_up":
         dts.update(gate_exps=P.Q8_0, up_exps=P.Q8_0)
@@ -108,7 +110,7 @@ def test_moe_chain(gctx, orc, case, M):
     model = P.make_model(orc, cfg, dts, seed=100 + M, extras=extras)
     toks = np.random.default_rng(M).integers(0, 500, M).tolist()
     seqs = [(toks, None, 11, 11 + M + 2)]
-    check(run(gctx, orc, model, seqs, 64), seqs)
+    check(run(gctx, orc, model, seqs, max(64, M)), seqs)
 
 
 def test_moe_three_sequences_and_tree(gctx, orc):
