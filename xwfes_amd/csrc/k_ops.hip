@@ -166,6 +166,157 @@ __device__ __forceinline__ void rope_kv_row(const RopeArgs& a, int64_t m, int64_
 
 __global__ void k_rope_kv(RopeArgs a) { rope_kv_row(a, blockIdx.x, blockIdx.y); }
 
+// The same for head sizes up to 256, one wave per (token, head) and four
+// heads per workgroup: lane l takes the head's rotation pairs l and l + 64,
+// and every value stays in registers from the split partials (or the row)
+// to the row, query and cache writes (the one-wave form above passes each
+// element through memory between its stages).  The arithmetic per element
+// is the one-wave form's: partials in split order, bias, (x * inv) * w, the
+// rotation without contraction; the head's sum of squares is a wave sum.
+constexpr int ROPE_HPW = 4;  // heads per workgroup
+__device__ __forceinline__ void rope_kv_head(const RopeArgs& a, int64_t m, int64_t h, int lane) {
+#pragma clang fp contract(off)
+    const int64_t half = a.hd / 2;
+    const int64_t npast = *a.npast;
+    const int64_t pos = npast + a.depth[m];
+    const int64_t qdim = a.n_head * a.hd, kdim = a.n_kv * a.hd;
+    float* row = a.qkv + m * a.ldq;
+    const bool is_q = h < a.n_head;
+    const int64_t off = is_q ? h * a.hd : qdim + (h - a.n_head) * a.hd;
+    const float* nw = is_q ? a.qnorm : a.knorm;
+    const float* prow = a.part ? a.part + m * a.ldp : nullptr;
+    // pair j of the lane: index i = lane + 64 j, elements ia, ib of the head
+    float x[2][2], v[2][2];
+    int64_t el[2][2];
+    bool ok[2];
+#pragma unroll
+    for (int j = 0; j < 2; ++j) {
+        const int64_t i = lane + 64 * j;
+        ok[j] = i < half;
+        const int64_t ic = ok[j] ? i : 0;
+        el[j][0] = a.neox ? ic : 2 * ic;
+        el[j][1] = a.neox ? ic + half : 2 * ic + 1;
+#pragma unroll
+        for (int e = 0; e < 2; ++e) {
+            x[j][e] = 0.f;
+            v[j][e] = 0.f;
+        }
+    }
+    if (prow) {
+        // eight splits' loads of every element at once (clamped split index,
+        // masked), then each element summed in split order
+        for (int s0 = 0; s0 < a.S; s0 += 8) {
+            float px[8][2][2], pv[8][2][2];
+#pragma unroll
+            for (int q = 0; q < 8; ++q) {
+                const float* ps = prow + min(s0 + q, a.S - 1) * a.split_stride + off;
+#pragma unroll
+                for (int j = 0; j < 2; ++j)
+#pragma unroll
+                    for (int e = 0; e < 2; ++e) {
+                        px[q][j][e] = ps[el[j][e]];
+                        pv[q][j][e] = is_q ? 0.f : ps[kdim + el[j][e]];
+                    }
+            }
+#pragma unroll
+            for (int q = 0; q < 8; ++q)
+#pragma unroll
+                for (int j = 0; j < 2; ++j)
+#pragma unroll
+                    for (int e = 0; e < 2; ++e) {
+                        const bool in = s0 + q < a.S;
+                        x[j][e] += in ? px[q][j][e] : 0.f;
+                        v[j][e] += in ? pv[q][j][e] : 0.f;
+                    }
+        }
+    } else {
+#pragma unroll
+        for (int j = 0; j < 2; ++j)
+#pragma unroll
+            for (int e = 0; e < 2; ++e) {
+                x[j][e] = row[off + el[j][e]];
+                if (!is_q) v[j][e] = row[off + kdim + el[j][e]];
+            }
+    }
+    if (a.bias) {
+#pragma unroll
+        for (int j = 0; j < 2; ++j)
+#pragma unroll
+            for (int e = 0; e < 2; ++e) {
+                x[j][e] = x[j][e] + a.bias[off + el[j][e]];
+                if (!is_q) v[j][e] = v[j][e] + a.bias[off + kdim + el[j][e]];
+            }
+    }
+    if (nw) {
+        float ss = 0.f;
+#pragma unroll
+        for (int j = 0; j < 2; ++j)
+            if (ok[j]) {
+                ss += x[j][0] * x[j][0];
+                ss += x[j][1] * x[j][1];
+            }
+#pragma unroll
+        for (int o = 32; o > 0; o >>= 1) ss += __shfl_xor(ss, o, 64);
+        const float inv = 1.f / sqrtf(ss / (float)a.hd + a.eps);
+#pragma unroll
+        for (int j = 0; j < 2; ++j)
+#pragma unroll
+            for (int e = 0; e < 2; ++e) x[j][e] = x[j][e] * inv * nw[el[j][e]];
+    }
+    const int64_t slot = npast + m;
+    const int64_t kh = h - a.n_head;
+#pragma unroll
+    for (int j = 0; j < 2; ++j) {
+        if (!ok[j]) continue;
+        const int64_t i = lane + 64 * j;
+        float c, sn;
+        if (a.cs) {
+            c = a.cs[(m * half + i) * 2];
+            sn = a.cs[(m * half + i) * 2 + 1];
+        } else {
+            const double f = pow(a.theta, -2.0 * (double)i / (double)a.hd);
+            const double ang = (double)pos * f;
+            c = (float)cos(ang);
+            sn = (float)sin(ang);
+        }
+        const float x0 = x[j][0], x1 = x[j][1];
+        const float y[2] = {x0 * c - x1 * sn, x0 * sn + x1 * c};
+#pragma unroll
+        for (int e = 0; e < 2; ++e) {
+            const int64_t t = el[j][e];
+            row[off + t] = y[e];
+            if (is_q) {
+                if (a.qh16) {
+                    const int64_t o = (m * a.n_head + h) * a.hd + t;
+                    const _Float16 hv = (_Float16)y[e];
+                    a.qh16[o] = hv;
+                    a.ql16[o] = (_Float16)(y[e] - (float)hv);
+                }
+            } else {
+                if (prow || a.bias) row[off + kdim + t] = v[j][e];
+                const int64_t idx = slot * kdim + kh * a.hd + t;
+                const int64_t vidx = v_index(slot, kh, t, a.hd, a.cap);
+                if (a.kv_f16) {
+                    ((_Float16*)a.kc)[idx] = (_Float16)y[e];
+                    ((_Float16*)a.vc)[vidx] = (_Float16)v[j][e];
+                } else {
+                    ((float*)a.kc)[idx] = y[e];
+                    ((float*)a.vc)[vidx] = v[j][e];
+                }
+            }
+        }
+    }
+}
+
+__global__ void __launch_bounds__(64 * ROPE_HPW) k_rope_kv4(RopeBatch b) {
+    int s = 0;
+    while (s + 1 < b.nseq && (int)blockIdx.x >= b.row0[s + 1]) ++s;
+    const int w = threadIdx.x >> 6, lane = threadIdx.x & 63;
+    const int64_t h = (int64_t)blockIdx.y * ROPE_HPW + w;
+    if (h >= b.s[s].n_head + b.s[s].n_kv) return;  // wave-uniform; no barrier below
+    rope_kv_head(b.s[s], (int64_t)blockIdx.x - b.row0[s], h, lane);
+}
+
 // several sequences: sequence s owns token rows row0[s] .. row0[s + 1] - 1
 __global__ void k_rope_kv_batch(RopeBatch b) {
     int s = 0;
@@ -203,6 +354,7 @@ hipError_t launch_v_layout(hipStream_t st, const void* src, void* dst, int64_t n
 
 hipError_t launch_rope_kv(hipStream_t st, const RopeArgs& a, int64_t M) {
     if (M == 0) return hipSuccess;
+    if (a.hd % 2 == 0 && a.hd <= 256) return launch_rope_kv_batch(st, &a, &M, 1);
     hipLaunchKernelGGL(k_rope_kv, dim3((unsigned)M, (unsigned)(a.n_head + a.n_kv)), dim3(64), 0,
                        st, a);
     return hipGetLastError();
@@ -221,8 +373,14 @@ hipError_t launch_rope_kv_batch(hipStream_t st, const RopeArgs* as, const int64_
     }
     b.row0[nseq] = rows;
     if (rows == 0) return hipSuccess;
-    hipLaunchKernelGGL(k_rope_kv_batch, dim3((unsigned)rows, (unsigned)(as[0].n_head + as[0].n_kv)),
-                       dim3(64), 0, st, b);
+    bool regs = true;  // every sequence's head size fits the register form
+    for (int s = 0; s < nseq; ++s) regs = regs && as[s].hd % 2 == 0 && as[s].hd <= 256;
+    const int64_t nh = as[0].n_head + as[0].n_kv;
+    if (regs)
+        hipLaunchKernelGGL(k_rope_kv4, dim3((unsigned)rows, (unsigned)((nh + ROPE_HPW - 1) / ROPE_HPW)),
+                           dim3(64 * ROPE_HPW), 0, st, b);
+    else
+        hipLaunchKernelGGL(k_rope_kv_batch, dim3((unsigned)rows, (unsigned)nh), dim3(64), 0, st, b);
     return hipGetLastError();
 }
 
