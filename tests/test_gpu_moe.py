@@ -124,6 +124,21 @@ def test_moe_three_sequences_and_tree(gctx, orc):
     check(run(gctx, orc, model, seqs, 16), seqs)
 
 
+@pytest.mark.parametrize("E,U,M", [(64, 6, 40), (100, 4, 130), (256, 8, 33)])
+def test_moe_many_experts(gctx, orc, E, U, M):
+    """Routers of 64 to 256 experts at top-4 to top-8: the per-token softmax
+    on one lane per expert (up to 64) and on four experts per lane (above),
+    and the grouping's per-expert prefix sums over several 64-expert rounds
+    with 64-entry chunks of (token, rank) entries (264 to 520 entries)."""
+    cfg = dict(MOE)
+    cfg["n_expert"] = E
+    cfg["n_expert_used"] = U
+    model = P.make_model(orc, cfg, DT, seed=300 + E)
+    toks = np.random.default_rng(E).integers(0, 500, M).tolist()
+    seqs = [(toks, None, 5, 5 + M + 2)]
+    check(run(gctx, orc, model, seqs, max(64, M)), seqs)
+
+
 @pytest.mark.parametrize("extras,neox", [(("q_bias", "k_bias", "v_bias"), 1),
                                          (("q_norm", "k_norm"), 1),
                                          (("q_bias", "k_bias", "v_bias", "q_norm", "k_norm"), 0)])

@@ -52,14 +52,33 @@ constexpr int MOE_GB = 4;      // 4096-element batches of a router row (n_embd <
 // RMSNorm of the residual row (src/engine.cpp:23-41; the row's sum of
 // squares as wave sums), written out as the experts' operand row xn[m]; the
 // router row (router weights dot xn[m], any stored dtype, wave sums) plus
-// the bias; then one thread: softmax_inplace (float max, float exp, double
-// sum in expert order, float scale; src/engine.cpp:62-72), the U largest in
+// the bias; then softmax_inplace (float max, float exp, double sum in
+// expert order, float scale; src/engine.cpp:62-72), the U largest in
 // descending order with ties to the lower index (std::partial_sort's order
 // for distinct values), the weights renormalised by their float sum
 // (src/engine.cpp:197-215).  Writes te[m][u] (expert), tw[m][u] (weight).
+// Every load of the launch's first phase goes out at entry (the bias, the
+// row and its norm weights, then the first eight router rows, which arrive
+// while the row is normalised), and the barriers order LDS only, so no
+// phase waits for the xn stores to complete.
 __device__ void moe_route_wg(const int32_t* __restrict__ te_g, const float* __restrict__ tw_g,
                              int M, int E, int U, int ntile_max, int TR, const MoeRoute& r);
 
+// Workgroup barrier that orders LDS accesses only: each wave waits for its
+// own LDS operations, not (as __syncthreads' release fence does) for every
+// global store it has in flight, which costs a memory round trip.
+__device__ __forceinline__ void lds_barrier() {
+    asm volatile("s_waitcnt lgkmcnt(0)\n\ts_barrier" ::: "memory");
+}
+
+// lane j's value of v (j wave-uniform)
+__device__ __forceinline__ float lane_f(float v, int j) {
+    return __builtin_bit_cast(float, __builtin_amdgcn_readlane(__builtin_bit_cast(int, v), j));
+}
+__device__ __forceinline__ int lane_i(int v, int j) { return __builtin_amdgcn_readlane(v, j); }
+
+// NB = the row's 4096-element batches, ceil(K / 4096) <= MOE_GB
+template <int NB>
 __global__ void __launch_bounds__(256) k_moe_gate(const float* __restrict__ x, int64_t K,
                                                   const float* __restrict__ normw, float eps,
                                                   float* __restrict__ xn,
@@ -74,65 +93,101 @@ __global__ void __launch_bounds__(256) k_moe_gate(const float* __restrict__ x, i
     float* lg = xs + K;
     const int m = blockIdx.x, t = threadIdx.x, lane = t & 63, w = t >> 6;
     const float* xr = x + (int64_t)m * K;
-    float ss = 0.f;
+    // the bias of expert `lane` (read by the softmax of E <= 64 experts;
+    // without a bias the load reads the row, in bounds, and is replaced by
+    // zero)
+    const float* rbp = rbias ? rbias : xr;
+    float rbv = rbp[min(lane, (rbias ? E : (int)min((int64_t)E, K)) - 1)];
+    if (!rbias) rbv = 0.f;
     // 16 elements per thread with their loads in flight together (element
     // order per thread as a plain strided loop)
     // (the norm weights' loads go out with the row's and wait in registers:
-    // K <= 256 * 16 * MOE_GB)
-    float nv[MOE_GB][16];
+    // K <= 256 * 16 * NB)
+    float xv[NB][16], nv[NB][16];
 #pragma unroll
-    for (int b = 0; b < MOE_GB; ++b) {
+    for (int b = 0; b < NB; ++b) {
         const int64_t k0 = t + (int64_t)b * 256 * 16;
         if (k0 >= K) break;  // block-uniform for all but the last batch's tail
-        float v[16];
 #pragma unroll
-        for (int i = 0; i < 16; ++i) v[i] = xr[min(k0 + 256 * i, K - 1)];
+        for (int i = 0; i < 16; ++i) xv[b][i] = xr[min(k0 + 256 * i, K - 1)];
 #pragma unroll
         for (int i = 0; i < 16; ++i) nv[b][i] = normw[min(k0 + 256 * i, K - 1)];
+    }
+    // the first eight router rows' first 1024 float4 columns (the F32
+    // router's first group), behind the row, with the indices clamped to
+    // rows < E and columns < K; another router dtype reads the norm weights
+    // instead (16-byte aligned, K floats) and discards them
+    const bool f32 = dt == FTX_F32;
+    const uint8_t* Wp = f32 ? W : (const uint8_t*)normw;
+    const int64_t rstep = f32 ? row_bytes : 0, n4 = K / 4;
+    float4 rv[8][4];
+#pragma unroll
+    for (int r = 0; r < 8; ++r) {
+        const float4* r4 = (const float4*)(Wp + (int64_t)min(r, E - 1) * rstep);
+#pragma unroll
+        for (int i = 0; i < 4; ++i) rv[r][i] = r4[min((int64_t)t + 256 * i, n4 - 1)];
+    }
+    float ss = 0.f;
+#pragma unroll
+    for (int b = 0; b < NB; ++b) {
+        const int64_t k0 = t + (int64_t)b * 256 * 16;
+        if (k0 >= K) break;
 #pragma unroll
         for (int i = 0; i < 16; ++i)
             if (k0 + 256 * i < K) {
-                xs[k0 + 256 * i] = v[i];
-                ss += v[i] * v[i];
+                xs[k0 + 256 * i] = xv[b][i];
+                ss += xv[b][i] * xv[b][i];
             }
     }
 #pragma unroll
     for (int o = 32; o > 0; o >>= 1) ss += __shfl_xor(ss, o, 64);
     if (lane == 0) red[w] = ss;
-    __syncthreads();
+    lds_barrier();
     const float rinv = 1.f / sqrtf((((red[0] + red[1]) + red[2]) + red[3]) / (float)K + eps);
-    float* xo = xn + (int64_t)m * K;
+    // the normed row stays in xv until the workgroup's last step, where it
+    // is stored as xn[m]: a store in flight would hold up every later wait
+    // for a load (vector-memory counters cover stores too) and the fences
 #pragma unroll
-    for (int b = 0; b < MOE_GB; ++b)
+    for (int b = 0; b < NB; ++b)
 #pragma unroll
         for (int i = 0; i < 16; ++i) {
             const int64_t k = t + (int64_t)b * 256 * 16 + 256 * i;
             if (k < K) {
-                const float v = xs[k] * rinv * nv[b][i];
-                xs[k] = v;
-                xo[k] = v;
+                xv[b][i] = xv[b][i] * rinv * nv[b][i];
+                xs[k] = xv[b][i];
             }
         }
-    __syncthreads();
-    if (dt == FTX_F32) {
+    auto store_xn = [&]() {
+        float* xo = xn + (int64_t)m * K;
+#pragma unroll
+        for (int b = 0; b < NB; ++b)
+#pragma unroll
+            for (int i = 0; i < 16; ++i) {
+                const int64_t k = t + (int64_t)b * 256 * 16 + 256 * i;
+                if (k < K) xo[k] = xv[b][i];
+            }
+    };
+    lds_barrier();
+    if (f32) {
         // groups of 8 router rows: every thread's float4s of the group's
-        // rows (4 per row per 4096 columns) in flight together; per row, the
-        // threads' partial dots summed by wave (shuffles) and then in wave
-        // order
+        // rows (4 per row per 4096 columns) in flight together (the first
+        // group's since entry); per row, the threads' partial dots summed by
+        // wave (shuffles) and then in wave order
         __shared__ float rsum[4][8];
         const float4* x4 = (const float4*)xs;
-        const int64_t n4 = K / 4;
         for (int e0 = 0; e0 < E; e0 += 8) {
             float acc[8];
 #pragma unroll
             for (int r = 0; r < 8; ++r) acc[r] = 0.f;
             for (int64_t p0 = 0; p0 < n4; p0 += 1024) {
-                float4 v[8][4];
+                float4 (&v)[8][4] = rv;
+                if (e0 > 0 || p0 > 0) {
 #pragma unroll
-                for (int r = 0; r < 8; ++r) {
-                    const float4* r4 = (const float4*)(W + (int64_t)min(e0 + r, E - 1) * row_bytes);
+                    for (int r = 0; r < 8; ++r) {
+                        const float4* r4 = (const float4*)(W + (int64_t)min(e0 + r, E - 1) * row_bytes);
 #pragma unroll
-                    for (int i = 0; i < 4; ++i) v[r][i] = r4[min(p0 + t + 256 * i, n4 - 1)];
+                        for (int i = 0; i < 4; ++i) v[r][i] = r4[min(p0 + t + 256 * i, n4 - 1)];
+                    }
                 }
 #pragma unroll
                 for (int i = 0; i < 4; ++i) {
@@ -154,9 +209,9 @@ __global__ void __launch_bounds__(256) k_moe_gate(const float* __restrict__ x, i
             if (lane == 0)
 #pragma unroll
                 for (int r = 0; r < 8; ++r) rsum[w][r] = acc[r];
-            __syncthreads();
+            lds_barrier();
             if (t < 8 && e0 + t < E) lg[e0 + t] = ((rsum[0][t] + rsum[1][t]) + rsum[2][t]) + rsum[3][t];
-            __syncthreads();
+            lds_barrier();
         }
     } else {
         for (int e = w; e < E; e += 4) {
@@ -172,9 +227,37 @@ __global__ void __launch_bounds__(256) k_moe_gate(const float* __restrict__ x, i
             for (int o = 32; o > 0; o >>= 1) acc += __shfl_xor(acc, o, 64);
             if (lane == 0) lg[e] = acc;
         }
-        __syncthreads();
+        lds_barrier();
     }
     if (w == 0) {
+    int top[MOE_MAXU];
+    float topw[MOE_MAXU];
+    if (E <= 64) {
+    // softmax and top-U on wave 0 for up to 64 experts: lane j holds expert
+    // j, and every lane runs one thread's loops over the lanes in expert
+    // order (float max, float exp, double sum, float scale); then each lane
+    // counts the experts ahead of its own in (probability descending, index
+    // ascending) order, and the u-th choice is the lane with u ahead -- the
+    // U passes for the largest not yet taken, ties to the lower index
+    const float pj = lane < E ? (rbias ? lg[lane] + rbv : lg[lane]) : -INFINITY;
+    float mx = -INFINITY;
+    for (int j = 0; j < E; ++j) mx = fmaxf(mx, lane_f(pj, j));
+    const float ej = lane < E ? expf(pj - mx) : 0.f;
+    double sum = 0.0;
+    for (int j = 0; j < E; ++j) sum += (double)lane_f(ej, j);
+    const float pr = ej * (float)(1.0 / sum);
+    int ahead = 0;
+    for (int j = 0; j < E; ++j) {
+        const float v = lane_f(pr, j);
+        ahead += (v > pr) | ((v == pr) & (j < lane));
+    }
+    for (int u = 0; u < U; ++u) {
+        const uint64_t b = __ballot(lane < E && ahead == u);
+        const int j = b ? __builtin_ctzll(b) : 0;
+        top[u] = j;
+        topw[u] = lane_f(pr, j);
+    }
+    } else {
     // softmax and top-U on wave 0: lane l holds experts l, l + 64, l + 128,
     // l + 192 (E <= 256); the arithmetic and its order as one thread's
     // loops: float max, float exp, double sum in expert order, float scale
@@ -204,8 +287,6 @@ __global__ void __launch_bounds__(256) k_moe_gate(const float* __restrict__ x, i
     float key[4];
 #pragma unroll
     for (int q = 0; q < 4; ++q) key[q] = lane + 64 * q < E ? pv[q] : -2.f;
-    int top[MOE_MAXU];
-    float topw[MOE_MAXU];
     for (int u = 0; u < U; ++u) {
         float bv = key[0];
         int bj = lane;
@@ -228,6 +309,7 @@ __global__ void __launch_bounds__(256) k_moe_gate(const float* __restrict__ x, i
         topw[u] = bv;
         if ((bj & 63) == lane) key[bj >> 6] = -1.f;
     }
+    }
     float wsum = 0.f;
     for (int u = 0; u < U; ++u) wsum = wsum + topw[u];
     const float winv = wsum > 0.f ? 1.f / wsum : 0.f;
@@ -242,81 +324,137 @@ __global__ void __launch_bounds__(256) k_moe_gate(const float* __restrict__ x, i
     // 0, which stored this token's choice, publishes it with a device-scope
     // fence before counting the workgroup done; the last one's threads fence
     // again before reading every token's choice.  The counter is back at 0
-    // when the launch ends.
+    // when the launch ends.  (xn[m], which only the next launches read, is
+    // stored after all of this.)
     __shared__ int last;
     if (t == 0) {
         __threadfence();
         last = atomicAdd(r.done, 1u) == (unsigned)(gridDim.x - 1);
     }
-    __syncthreads();
-    if (!last) return;  // block-uniform
+    lds_barrier();
+    if (!last) {  // block-uniform
+        store_xn();
+        return;
+    }
     __threadfence();
     moe_route_wg(te, tw, (int)gridDim.x, E, U, ntile_max, TR, r);
+    store_xn();
     if (t == 0) atomicExch(r.done, 0u);
 }
 
-// Grouping, by the last router workgroup: thread e (strided) takes expert e: first use over
-// (token, rank) and token count; thread 0 lays out the tiles (experts in
-// index order, ceil(count / 64) tiles each); thread e assigns its tokens'
-// operand rows in token order; thread m orders its experts by first use
-// for the combine (src/engine.cpp:210-239).
+// Grouping, by the last router workgroup (src/engine.cpp:210-239).  The
+// entries i = (token, rank) are walked in order by wave 0, 64 at a time:
+// per distinct expert of a 64-entry chunk one ballot gives its entries'
+// places k among the expert's entries so far, its count and its first use.
+// Then wave 0 lays out the tiles (experts in index order, ceil(count / TR)
+// tiles each, at most ntile_max in all), each expert's first entry slot
+// (the prefix sums of counts) and the experts' first-use ranks, and turns
+// every entry's k into its operand row.  After one LDS barrier every thread
+// writes its share of the row table (each row once: the token of the entry
+// that takes it, or -1) and thread m orders token m's experts by first use
+// for the combine.
 __device__ void moe_route_wg(const int32_t* __restrict__ te_g, const float* __restrict__ tw_g,
                              int M, int E, int U, int ntile_max, int TR, const MoeRoute& r) {
     __shared__ int te[MOE_MAXM * MOE_MAXU];
     __shared__ float tw[MOE_MAXM * MOE_MAXU];
-    __shared__ int slot_of[MOE_MAXM * MOE_MAXU];
-    __shared__ int firstpos[MOE_MAXE], cnt[MOE_MAXE], tile0[MOE_MAXE], rank[MOE_MAXE];
-    const int t = threadIdx.x;
+    __shared__ int slot_of[MOE_MAXM * MOE_MAXU];  // k, then the operand row
+    __shared__ int ent[MOE_MAXM * MOE_MAXU];      // entries by expert: ent[off[e] + k]
+    __shared__ int firstpos[MOE_MAXE], cnt[MOE_MAXE], tile0[MOE_MAXE], off[MOE_MAXE],
+        rank[MOE_MAXE];
+    __shared__ int tile_e[MOE_MAXM * MOE_MAXU / 16 + 1 + MOE_MAXE];  // expert of each tile
+    __shared__ int nt_s;
+    const int t = threadIdx.x, lane = t & 63;
     const int MU = M * U;
     for (int i = t; i < MU; i += blockDim.x) {
         te[i] = te_g[i];
         tw[i] = tw_g[i];
     }
-    __syncthreads();
     for (int e = t; e < E; e += blockDim.x) {
-        int fp = INT_MAX, c = 0;
-        for (int i = 0; i < MU; ++i)
-            if (te[i] == e) {
-                if (fp == INT_MAX) fp = i;
-                ++c;
+        cnt[e] = 0;
+        firstpos[e] = INT_MAX;
+    }
+    __syncthreads();
+    if (t < 64) {
+        // (one wave: its LDS accesses are ordered, so no barrier inside)
+        const uint64_t below = (1ull << lane) - 1;
+        for (int c0 = 0; c0 < MU; c0 += 64) {
+            const int i = c0 + lane;
+            const int e = i < MU ? te[i] : -1;
+            uint64_t todo = __ballot(i < MU);
+            int k = 0;
+            while (todo) {
+                const int ld = __builtin_ctzll(todo);
+                const int el = lane_i(e, ld);
+                const uint64_t mk = __ballot(e == el);
+                const int base = cnt[el];
+                if (e == el) k = base + __popcll(mk & below);
+                if (lane == 0) {
+                    if (base == 0) firstpos[el] = c0 + ld;
+                    cnt[el] = base + __popcll(mk);
+                }
+                todo &= ~mk;
             }
-        firstpos[e] = fp;
-        cnt[e] = c;
-    }
-    for (int i = t; i < ntile_max * TR; i += blockDim.x) r.slot_tok[i] = -1;
-    __syncthreads();
-    for (int e = t; e < E; e += blockDim.x) {
-        int k = 0;
-        for (int e2 = 0; e2 < E; ++e2) k += firstpos[e2] < firstpos[e];
-        rank[e] = k;
-    }
-    if (t == 0) {
-        int nt = 0;
-        for (int e = 0; e < E; ++e) {
-            tile0[e] = nt;
-            for (int k = 0; k < cnt[e] && nt < ntile_max; k += TR, ++nt) {
-                r.tab[1 + 2 * nt] = e;
-                r.tab[2 + 2 * nt] = min(TR, cnt[e] - k);
+            if (i < MU) slot_of[i] = k;
+        }
+        // tiles and entry offsets: exclusive prefix sums over the experts
+        // in index order, 64 experts a round
+        int ct = 0, cc = 0;
+        for (int q = 0; q < E; q += 64) {
+            const int e = q + lane;
+            const int c = e < E ? cnt[e] : 0;
+            const int n = (c + TR - 1) / TR;
+            int sn = n, sc = c;
+#pragma unroll
+            for (int o = 1; o < 64; o <<= 1) {
+                const int an = __shfl_up(sn, o, 64), ac = __shfl_up(sc, o, 64);
+                if (lane >= o) {
+                    sn += an;
+                    sc += ac;
+                }
             }
+            if (e < E) {
+                const int t0 = min(ct + sn - n, ntile_max);
+                const int nte = min(n, ntile_max - t0);
+                tile0[e] = t0;
+                off[e] = cc + sc - c;
+                for (int j = 0; j < nte; ++j) {
+                    r.tab[1 + 2 * (t0 + j)] = e;
+                    r.tab[2 + 2 * (t0 + j)] = min(TR, c - j * TR);
+                    tile_e[t0 + j] = e;
+                }
+            }
+            ct += lane_i(sn, 63);
+            cc += lane_i(sc, 63);
         }
-        r.tab[0] = nt;
-    }
-    __syncthreads();
-    // expert e's entries in (token, rank) order take its operand rows in
-    // turn (LDS only; the row table is written below)
-    for (int e = t; e < E; e += blockDim.x) {
-        if (!cnt[e]) continue;
-        const int base = TR * tile0[e];
-        int k = 0;
-#pragma unroll 8
-        for (int i = 0; i < MU; ++i) {
-            const bool hit = te[i] == e;
-            if (hit) slot_of[i] = base + k < ntile_max * TR ? base + k : 0;
-            k += hit;
+        if (lane == 0) {
+            nt_s = min(ct, ntile_max);
+            r.tab[0] = min(ct, ntile_max);
+        }
+        for (int e = lane; e < E; e += 64) {
+            const int fp = firstpos[e];
+            int k = 0;
+            for (int e2 = 0; e2 < E; ++e2) k += firstpos[e2] < fp;
+            rank[e] = k;
+        }
+        for (int i = lane; i < MU; i += 64) {
+            const int e = te[i], k = slot_of[i];
+            const int s = TR * tile0[e] + k;
+            slot_of[i] = s < ntile_max * TR ? s : 0;
+            ent[off[e] + k] = i;
         }
     }
-    __syncthreads();
-    for (int i = t; i < MU; i += blockDim.x) r.slot_tok[slot_of[i]] = i / U;
+    lds_barrier();
+    const int nt = nt_s;
+    for (int row = t; row < ntile_max * TR; row += blockDim.x) {
+        const int tl = row / TR;
+        int tok = -1;
+        if (tl < nt) {
+            const int e = tile_e[tl];
+            const int k = (tl - tile0[e]) * TR + row % TR;
+            if (k < cnt[e]) tok = ent[off[e] + k] / U;
+        }
+        r.slot_tok[row] = tok;
+    }
     for (int m = t; m < M; m += blockDim.x) {
         int idx[MOE_MAXU];
         for (int u = 0; u < U; ++u) idx[u] = m * U + u;
@@ -618,7 +756,9 @@ hipError_t launch_moe_route(hipStream_t st, const float* x, const float* normw, 
         (dt == FTX_F32 && ((uintptr_t)W & 15)) || (dt == FTX_F32 && row_bytes % 16))
         return hipErrorInvalidValue;
     const size_t lds = (size_t)(K + E) * sizeof(float);
-    hipLaunchKernelGGL(k_moe_gate, dim3((unsigned)M), dim3(256), lds, st, x, K, normw, eps, xn, W,
+    const int nb = (int)((K + 4095) / 4096);
+    auto kern = nb == 1 ? k_moe_gate<1> : nb == 2 ? k_moe_gate<2> : nb == 3 ? k_moe_gate<3> : k_moe_gate<4>;
+    hipLaunchKernelGGL(kern, dim3((unsigned)M), dim3(256), lds, st, x, K, normw, eps, xn, W,
                        dt, row_bytes, rbias, (int)E, (int)U, (int)moe_tiles_max(M, E, U),
                        (int)moe_tile_rows(M, E, U), r);
     return hipGetLastError();
