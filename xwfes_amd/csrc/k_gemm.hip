@@ -157,57 +157,87 @@ __global__ void __launch_bounds__(256) k_mm_prep(const float* __restrict__ x, in
     }
 }
 
-// The split partials of the previous GEMM added into x, then the prep of
-// k_mm_prep, one workgroup of 1024 threads per operand row m (thread t:
-// elements 4 t + 4096 c, c < K / 4096 rounded up):  x[m] <- x[m] +
-// sum_ks part[ks][m] (the sum in split order first, then added, as
-// k_mm_reduce does), written back (the residual add of
-// src/engine.cpp:274-275 / 516-517), then RMSNorm of the new row (every
-// element already in registers) and the fp16 hi + lo fragments and
-// 32-element sums as k_mm_prep writes them.  Rows m >= M: zero operands, x
-// untouched.
-constexpr int MMF_CH = 4;  // float4 chunks per thread: K <= 16384
-__global__ void __launch_bounds__(1024) k_mm_prep_fold(float* __restrict__ x, int64_t ldx,
-                                                       const float* __restrict__ normw, float eps,
-                                                       int64_t K, int M, int inter,
-                                                       const float* __restrict__ part,
-                                                       int64_t split_stride, int64_t ldp, int S,
-                                                       _Float16* __restrict__ xh,
-                                                       _Float16* __restrict__ xl,
-                                                       _Float16* __restrict__ sh,
-                                                       _Float16* __restrict__ sl) {
+// The prep of a whole operand row per workgroup of 1024 threads (thread t:
+// elements 4 t + 4096 c, c < CH = K / 4096 rounded up), for K <= 16384.
+// The source row is x row gather[m] (expert launches; a zero operand row
+// where gather[m] < 0) or row m (rows m >= M: zero operands, x untouched).
+// With S > 0 the split partials of the previous GEMM are added into it
+// first: x[m] <- x[m] + sum_ks part[ks][m] (the sum in split order first,
+// then added, as k_mm_reduce does; the residual add of
+// src/engine.cpp:274-275 / 516-517), the new row written back as the
+// workgroup's last step.  Then RMSNorm of the row (every element already
+// in registers) and the fp16 hi + lo fragments and 32-element sums as
+// k_mm_prep writes them.  The norm weights and the row are loaded at entry,
+// ahead of the partials, and the one barrier (the row's sum of squares)
+// has no store in flight to wait for.
+constexpr int MMF_CH = 4;  // 4096-element chunks per row: K <= 16384
+template <int CH>
+__global__ void __launch_bounds__(1024) k_mm_prep_row(float* __restrict__ x, int64_t ldx,
+                                                      const float* __restrict__ normw, float eps,
+                                                      int64_t K, int M, int inter,
+                                                      const int32_t* __restrict__ gather,
+                                                      const float* __restrict__ part,
+                                                      int64_t split_stride, int64_t ldp, int S,
+                                                      _Float16* __restrict__ xh,
+                                                      _Float16* __restrict__ xl,
+                                                      _Float16* __restrict__ sh,
+                                                      _Float16* __restrict__ sl) {
 #pragma clang fp contract(off)
+    // splits loaded together per chunk (the registers of CH x SB float4s)
+    constexpr int SB = CH <= 2 ? 8 : CH == 3 ? 4 : 2;
     __shared__ float red[16];
     const int m = blockIdx.x, t = threadIdx.x;
     const int64_t nsb = K / 256;
-    const bool live = m < M;  // block-uniform
-    float* row = x + (int64_t)(live ? m : 0) * ldx;
-    float4 v[MMF_CH];
+    const int src = m >= M ? -1 : (gather ? gather[m] : m);
+    const bool live = src >= 0;  // block-uniform
+    float* row = x + (int64_t)(live ? src : 0) * ldx;
+    // (without norm weights the row is read in their place: every load is
+    // unconditional, the indices clamped to the row)
+    const float* nwp = normw ? normw : row;
+    float4 w[CH], v[CH];
+#pragma unroll
+    for (int c = 0; c < CH; ++c) {
+        const int64_t k = min((int64_t)(4 * t + 4096 * c), K - 4);
+        w[c] = *(const float4*)(nwp + k);
+        v[c] = *(const float4*)(row + k);
+    }
+    if (S > 0) {
+        float4 g[CH];
+#pragma unroll
+        for (int c = 0; c < CH; ++c) g[c] = float4{0.f, 0.f, 0.f, 0.f};
+        const float* pp = part + (int64_t)(live ? src : 0) * ldp;
+        for (int s0 = 0; s0 < S; s0 += SB) {
+            float4 pv[CH][SB];
+#pragma unroll
+            for (int c = 0; c < CH; ++c) {
+                const int64_t k = min((int64_t)(4 * t + 4096 * c), K - 4);
+#pragma unroll
+                for (int i = 0; i < SB; ++i)
+                    pv[c][i] = s0 + i < S
+                                   ? *(const float4*)(pp + k + (int64_t)(s0 + i) * split_stride)
+                                   : float4{0.f, 0.f, 0.f, 0.f};
+            }
+#pragma unroll
+            for (int c = 0; c < CH; ++c)
+#pragma unroll
+                for (int i = 0; i < SB; ++i) {
+                    g[c].x += pv[c][i].x;
+                    g[c].y += pv[c][i].y;
+                    g[c].z += pv[c][i].z;
+                    g[c].w += pv[c][i].w;
+                }
+        }
+#pragma unroll
+        for (int c = 0; c < CH; ++c)
+            v[c] = float4{v[c].x + g[c].x, v[c].y + g[c].y, v[c].z + g[c].z, v[c].w + g[c].w};
+    }
     float ss = 0.f;
 #pragma unroll
-    for (int c = 0; c < MMF_CH; ++c) {
-        v[c] = float4{0.f, 0.f, 0.f, 0.f};
-        const int64_t k = 4 * t + 4096 * c;
-        if (!live || k >= K) continue;
-        float4 g = {0.f, 0.f, 0.f, 0.f};
-        const float* pp = part + (int64_t)m * ldp + k;
-        for (int s0 = 0; s0 < S; s0 += 8) {
-            float4 pv[8];
-#pragma unroll
-            for (int i = 0; i < 8; ++i)
-                pv[i] = s0 + i < S ? *(const float4*)(pp + (int64_t)(s0 + i) * split_stride)
-                                   : float4{0.f, 0.f, 0.f, 0.f};
-#pragma unroll
-            for (int i = 0; i < 8; ++i) {
-                g.x += pv[i].x;
-                g.y += pv[i].y;
-                g.z += pv[i].z;
-                g.w += pv[i].w;
-            }
+    for (int c = 0; c < CH; ++c) {
+        if (!live || 4 * t + 4096 * c >= K) {
+            v[c] = float4{0.f, 0.f, 0.f, 0.f};
+            continue;
         }
-        const float4 xv = *(const float4*)(row + k);
-        v[c] = float4{xv.x + g.x, xv.y + g.y, xv.z + g.z, xv.w + g.w};
-        *(float4*)(row + k) = v[c];
         ss += v[c].x * v[c].x;
         ss += v[c].y * v[c].y;
         ss += v[c].z * v[c].z;
@@ -227,16 +257,15 @@ __global__ void __launch_bounds__(1024) k_mm_prep_fold(float* __restrict__ x, in
         }
     }
 #pragma unroll
-    for (int c = 0; c < MMF_CH; ++c) {
+    for (int c = 0; c < CH; ++c) {
         const int64_t k = 4 * t + 4096 * c;
         if (k >= K) continue;  // whole 32-element groups of 8 threads alike (K % 256 == 0)
         float o[4] = {v[c].x, v[c].y, v[c].z, v[c].w};
         if (live && normw) {
-            const float4 w = *(const float4*)(normw + k);
-            o[0] = (o[0] * inv) * w.x;
-            o[1] = (o[1] * inv) * w.y;
-            o[2] = (o[2] * inv) * w.z;
-            o[3] = (o[3] * inv) * w.w;
+            o[0] = (o[0] * inv) * w[c].x;
+            o[1] = (o[1] * inv) * w[c].y;
+            o[2] = (o[2] * inv) * w[c].z;
+            o[3] = (o[3] * inv) * w[c].w;
         }
         _Float16 hv[4], lv[4];
 #pragma unroll
@@ -266,6 +295,13 @@ __global__ void __launch_bounds__(1024) k_mm_prep_fold(float* __restrict__ x, in
             split_hl(s, h, l);
             sh[at] = h;
             sl[at] = l;
+        }
+    }
+    if (S > 0 && live) {
+#pragma unroll
+        for (int c = 0; c < CH; ++c) {
+            const int64_t k = 4 * t + 4096 * c;
+            if (k < K) *(float4*)(row + k) = v[c];
         }
     }
 }
@@ -1230,11 +1266,32 @@ MmAct mm_act(void* buf, int64_t Mp, int64_t K) {
     return a;
 }
 
+// k_mm_prep_row for K <= 16384 (S = 0: no partials to add)
+static hipError_t launch_prep_row(hipStream_t st, float* x, int64_t ldx, const float* normw,
+                                  float eps, int64_t M, const MmAct& act, int weight_dt,
+                                  const int32_t* gather, const float* part, int64_t split_stride,
+                                  int64_t ldp, int S) {
+    const int ch = (int)((act.K + 4095) / 4096);
+    auto kern = ch == 1 ? k_mm_prep_row<1>
+              : ch == 2 ? k_mm_prep_row<2>
+              : ch == 3 ? k_mm_prep_row<3>
+                        : k_mm_prep_row<4>;
+    hipLaunchKernelGGL(kern, dim3((unsigned)act.Mp), dim3(1024), 0, st, x, ldx, normw, eps, act.K,
+                       (int)M, weight_dt == FTX_Q4_0_MMT ? 1 : 0, gather, part, split_stride, ldp,
+                       S, act.xh, act.xl, act.sh, act.sl);
+    return hipGetLastError();
+}
+
 hipError_t launch_mm_prep(hipStream_t st, const float* x, int64_t ldx, const float* normw,
                           float eps, int64_t M, const MmAct& act, int weight_dt,
                           const int32_t* gather) {
-    if (act.K % 256 || M < 1 || M > act.Mp || act.Mp % MM_TOK || ldx % 4 || ((uintptr_t)x & 15))
+    if (act.K % 256 || M < 1 || M > act.Mp || act.Mp % MM_TOK || ldx % 4 || ((uintptr_t)x & 15) ||
+        ((uintptr_t)normw & 15))
         return hipErrorInvalidValue;
+    // (the row kernel does not write x when it adds no partials)
+    if (act.K <= 4096 * MMF_CH)
+        return launch_prep_row(st, const_cast<float*>(x), ldx, normw, eps, M, act, weight_dt,
+                               gather, nullptr, 0, 0, 0);
     hipLaunchKernelGGL(k_mm_prep, dim3((unsigned)act.Mp, (unsigned)((act.K + 1023) / 1024)),
                        dim3(256), 0, st, x, ldx, normw, eps,
                        act.K, (int)M, weight_dt == FTX_Q4_0_MMT ? 1 : 0, gather, act.xh,
@@ -1247,12 +1304,11 @@ hipError_t launch_mm_prep_fold(hipStream_t st, float* x, int64_t ldx, const floa
                                const MmPend& fold) {
     if (fold.S < 1) return launch_mm_prep(st, x, ldx, normw, eps, M, act, weight_dt);
     if (!fold.accum || act.K % 256 || act.K > 4096 * MMF_CH || M < 1 || M > act.Mp || act.Mp % MM_TOK ||
-        ldx % 4 || ((uintptr_t)x & 15) || fold.N != act.K || fold.ldp % 4 || fold.split_stride % 4)
+        ldx % 4 || ((uintptr_t)x & 15) || ((uintptr_t)normw & 15) || fold.N != act.K ||
+        fold.ldp % 4 || fold.split_stride % 4 || ((uintptr_t)fold.part & 15))
         return hipErrorInvalidValue;
-    hipLaunchKernelGGL(k_mm_prep_fold, dim3((unsigned)act.Mp), dim3(1024), 0, st, x, ldx, normw,
-                       eps, act.K, (int)M, weight_dt == FTX_Q4_0_MMT ? 1 : 0, fold.part,
-                       fold.split_stride, fold.ldp, fold.S, act.xh, act.xl, act.sh, act.sl);
-    return hipGetLastError();
+    return launch_prep_row(st, x, ldx, normw, eps, M, act, weight_dt, nullptr, fold.part,
+                           fold.split_stride, fold.ldp, fold.S);
 }
 
 // k_mm_reduce over `rows` rows, four columns per thread where the operands
