@@ -661,23 +661,50 @@ __global__ void __launch_bounds__(256) k_moe_down(MoeDownArgs a) {
 // ---------------------------------------------------------------- combine
 // grid = (ceil(K / 256), M); token m, column j: t = sum_k w_k a_k in the
 // token's first-use order with a_k = sum_s part[s][slot_k][j] (fp32, the
-// products rounded before each add as trow[j] += wgt * arow[j]).
+// products rounded before each add as trow[j] += wgt * arow[j]).  The
+// output (when accumulating) and the token's slots and weights are loaded
+// first, then the partials of every expert, eight splits at a time, all in
+// flight together (indices clamped, the surplus masked); UM >= U.
+template <int UM>
 __global__ void __launch_bounds__(256) k_moe_combine(const float* __restrict__ part, int S,
                                                      int64_t rows, int64_t K, MoeRoute r, int U,
                                                      float* __restrict__ y, int accum) {
 #pragma clang fp contract(off)
+    constexpr int QB = 8;  // splits per batch
     const int64_t j = (int64_t)blockIdx.x * 256 + threadIdx.x;
     const int64_t m = blockIdx.y;
     if (j >= K) return;
-    float t = 0.f;
-    for (int k = 0; k < U; ++k) {
-        const int64_t s = r.comb_slot[m * U + k];
-        float acb = 0.f;
-        for (int q = 0; q < S; ++q) acb += part[((int64_t)q * rows + s) * K + j];
-        t = t + r.comb_w[m * U + k] * acb;
-    }
     float* yp = y + m * K + j;
-    *yp = accum ? *yp + t : t;
+    const float y0 = *yp;  // (read whether or not it is used: in bounds)
+    int64_t slot[UM];
+    float wk[UM];
+#pragma unroll
+    for (int k = 0; k < UM; ++k) {
+        const int64_t e = m * U + min(k, U - 1);
+        slot[k] = r.comb_slot[e];
+        wk[k] = r.comb_w[e];
+    }
+    float acb[UM];
+#pragma unroll
+    for (int k = 0; k < UM; ++k) acb[k] = 0.f;
+    for (int q0 = 0; q0 < S; q0 += QB) {
+        float pv[UM][QB];
+#pragma unroll
+        for (int k = 0; k < UM; ++k)
+#pragma unroll
+            for (int i = 0; i < QB; ++i)
+                pv[k][i] = part[((int64_t)min(q0 + i, S - 1) * rows + slot[k]) * K + j];
+#pragma unroll
+        for (int k = 0; k < UM; ++k)
+#pragma unroll
+            for (int i = 0; i < QB; ++i)
+                if (q0 + i < S) acb[k] += pv[k][i];
+    }
+    float t = 0.f;
+#pragma unroll
+    for (int k = 0; k < UM; ++k)
+        if (k < U) t = t + wk[k] * acb[k];
+    *yp = accum ? y0 + t : t;
 }
 
 __global__ void __launch_bounds__(256) k_add(const float* __restrict__ x, float* __restrict__ y,
@@ -840,8 +867,9 @@ hipError_t launch_moe_down(hipStream_t st, const uint8_t* tiled, int dt, int64_t
 
 hipError_t launch_moe_combine(hipStream_t st, const float* part, int S, int64_t rows, int64_t K,
                               const MoeRoute& r, int64_t M, int64_t U, float* y, int accum) {
-    if (M < 1 || K < 1 || S < 1) return hipErrorInvalidValue;
-    hipLaunchKernelGGL(k_moe_combine, dim3((unsigned)((K + 255) / 256), (unsigned)M), dim3(256), 0,
+    if (M < 1 || K < 1 || S < 1 || U < 1 || U > MOE_MAXU) return hipErrorInvalidValue;
+    auto kern = U <= 2 ? k_moe_combine<2> : U <= 4 ? k_moe_combine<4> : k_moe_combine<MOE_MAXU>;
+    hipLaunchKernelGGL(kern, dim3((unsigned)((K + 255) / 256), (unsigned)M), dim3(256), 0,
                        st, part, S, rows, K, r, (int)U, y, accum);
     return hipGetLastError();
 }
