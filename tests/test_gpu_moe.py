@@ -124,16 +124,23 @@ def test_moe_three_sequences_and_tree(gctx, orc):
     check(run(gctx, orc, model, seqs, 16), seqs)
 
 
-@pytest.mark.parametrize("E,U,M", [(64, 6, 40), (100, 4, 130), (256, 8, 33)])
-def test_moe_many_experts(gctx, orc, E, U, M):
+@pytest.mark.parametrize("E,U,M,router", [(64, 6, 40, "f32"), (64, 6, 40, "q8_0_bias"),
+                                          (100, 4, 130, "f32_bias"), (256, 8, 33, "f32")])
+def test_moe_many_experts(gctx, orc, E, U, M, router):
     """Routers of 64 to 256 experts at top-4 to top-8: the per-token softmax
     on one lane per expert (up to 64) and on four experts per lane (above),
     and the grouping's per-expert prefix sums over several 64-expert rounds
-    with 64-entry chunks of (token, rank) entries (264 to 520 entries)."""
+    with 64-entry chunks of (token, rank) entries (264 to 520 entries); a
+    router bias on both softmax forms, and a Q8_0 router (the dequantising
+    router path)."""
     cfg = dict(MOE)
     cfg["n_expert"] = E
     cfg["n_expert_used"] = U
-    model = P.make_model(orc, cfg, DT, seed=300 + E)
+    dts = dict(DT)
+    if router.startswith("q8_0"):
+        dts["gate_inp"] = P.Q8_0
+    extras = ("router_bias",) if router.endswith("bias") else ()
+    model = P.make_model(orc, cfg, dts, seed=300 + E, extras=extras)
     toks = np.random.default_rng(E).integers(0, 500, M).tolist()
     seqs = [(toks, None, 5, 5 + M + 2)]
     check(run(gctx, orc, model, seqs, max(64, M)), seqs)
