@@ -134,6 +134,37 @@ def test_large_chain_one_pass(gctx, orc, M):
     assert rel_err_rows(got, want) < LOGIT_TOL
 
 
+@pytest.mark.parametrize("d,M", [(12288, 9), (16384, 20)])
+def test_wide_rows_one_pass(gctx, orc, d, M):
+    """Model widths of 12288 and 16384 (three and four 4096-element chunks
+    per thread in the one-row operand prep), 2 layers of Q4_K, chains of 9
+    and 20 tokens: the plain prep of the embeddings, the fold of the o
+    projection's split partials into the residual rows before the FFN and
+    of ffn_down's before the second layer."""
+    orc.set_threads(16)
+    V = 300
+    cfg = P.model_cfg(2, d, d // 128, 8, 128, 1024, V, rope_theta=500000.0)
+    rng = np.random.default_rng(d + M)
+    model = {"cfg": dict(cfg)}
+
+    def q(rows, cols):
+        return q_rows(orc, rng, rows, cols, P.Q4_K, unique=1024)
+
+    model["tok_embd"] = q(V, d)
+    model["output"] = q(V, d)
+    model["out_norm"] = norm_raw(rng, d)
+    for l in range(2):
+        p = "blk.%d." % l
+        model[p + "attn_norm"] = norm_raw(rng, d)
+        model[p + "ffn_norm"] = norm_raw(rng, d)
+        for nm, rows, cols in (("q", d, d), ("k", 1024, d), ("v", 1024, d), ("o", d, d),
+                               ("gate", 1024, d), ("up", 1024, d), ("down", 1024, d)):
+            model[p + nm] = q(rows, cols)
+    toks = rng.integers(0, V, M).tolist()
+    (got, want, _, _), = run_batch(gctx, orc, model, [(toks, None, 33, 33 + M + 3)], 64)
+    assert rel_err_rows(got, want) < LOGIT_TOL
+
+
 @pytest.mark.parametrize("M", [12, 20, 130])
 def test_large_chain_q6k_one_pass(gctx, orc, M):
     """Q6_K projections (q / k / v, o, gate / up with SwiGLU) and a Q6_K head
