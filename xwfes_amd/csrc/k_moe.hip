@@ -193,11 +193,11 @@ __global__ void __launch_bounds__(256) k_moe_gate(const float* __restrict__ x, i
                 for (int i = 0; i < 4; ++i) {
                     const int64_t c = p0 + t + 256 * i;
                     if (c < n4) {
-                        const float4 xv = x4[c];
+                        const float4 xc = x4[c];
 #pragma unroll
                         for (int r = 0; r < 8; ++r)
-                            acc[r] += v[r][i].x * xv.x + v[r][i].y * xv.y + v[r][i].z * xv.z +
-                                      v[r][i].w * xv.w;
+                            acc[r] += v[r][i].x * xc.x + v[r][i].y * xc.y + v[r][i].z * xc.z +
+                                      v[r][i].w * xc.w;
                     }
                 }
             }
