@@ -419,6 +419,21 @@ __host__ __device__ inline int64_t v_index(int64_t slot, int64_t kvh, int64_t di
     return (kvh * hd + dim) * cap + slot;
 }
 
+// Lane j's value of v in the wave, j wave-uniform: v_readlane, a register
+// read, where a shuffle (ds_bpermute) makes an LDS round trip -- the loops
+// over the lanes of one wave (softmax sums, sampler ranks, running sums)
+// run at VALU speed.
+__device__ __forceinline__ float lane_f(float v, int j) {
+    return __builtin_bit_cast(float, __builtin_amdgcn_readlane(__builtin_bit_cast(int, v), j));
+}
+__device__ __forceinline__ int lane_i(int v, int j) { return __builtin_amdgcn_readlane(v, j); }
+__device__ __forceinline__ double lane_d(double v, int j) {
+    const uint64_t u = __builtin_bit_cast(uint64_t, v);
+    const uint32_t lo = (uint32_t)__builtin_amdgcn_readlane((int)(uint32_t)u, j);
+    const uint32_t hi = (uint32_t)__builtin_amdgcn_readlane((int)(uint32_t)(u >> 32), j);
+    return __builtin_bit_cast(double, ((uint64_t)hi << 32) | lo);
+}
+
 // The qkv epilogue of one output: RoPE on q / k rows (interleaved pairs:
 // pv = the value of row n ^ 1; (c, s) = cos / sin of this row's angle), the
 // fp16 hi / lo query for attention, the K / transposed-V cache write.

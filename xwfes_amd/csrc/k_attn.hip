@@ -708,8 +708,8 @@ __device__ __forceinline__ void attn_combine_row(const AttnMArgs& a, int64_t qi,
     // clamped): the first CPF partials of this thread's dim and the statistics
     // of partial `lane`.  Each wave then forms the weights, their maximum and
     // the denominator itself (shuffles, no workgroup barrier); weights of the
-    // first CPF partials come from their lanes by shuffle, later ones (more
-    // than CPF partials) through the wave's own LDS copy.
+    // first CPF partials are read from their lanes (v_readlane), later ones
+    // (more than CPF partials) through the wave's own LDS copy.
     constexpr int CPF = 8;
     __shared__ float wsh[2][1024];  // chunk weights (nch <= 1024) per wave
     const int d = threadIdx.x, wv = d >> 6, lane = d & 63;
@@ -746,7 +746,7 @@ __device__ __forceinline__ void attn_combine_row(const AttnMArgs& a, int64_t qi,
     float num = 0.f;
 #pragma unroll
     for (int i = 0; i < CPF; ++i) {
-        const float wi = __shfl(w0, i, 64);
+        const float wi = lane_f(w0, i);
         if (i < nvalid) num += wi * pv[i];
     }
     for (int c = CPF; c < nvalid; ++c) num += wl[c] * po[(int64_t)c * a.hd];

@@ -71,12 +71,6 @@ __device__ __forceinline__ void lds_barrier() {
     asm volatile("s_waitcnt lgkmcnt(0)\n\ts_barrier" ::: "memory");
 }
 
-// lane j's value of v (j wave-uniform)
-__device__ __forceinline__ float lane_f(float v, int j) {
-    return __builtin_bit_cast(float, __builtin_amdgcn_readlane(__builtin_bit_cast(int, v), j));
-}
-__device__ __forceinline__ int lane_i(int v, int j) { return __builtin_amdgcn_readlane(v, j); }
-
 // NB = the row's 4096-element batches, ceil(K / 4096) <= MOE_GB
 template <int NB>
 __global__ void __launch_bounds__(256) k_moe_gate(const float* __restrict__ x, int64_t K,
@@ -275,9 +269,8 @@ __global__ void __launch_bounds__(256) k_moe_gate(const float* __restrict__ x, i
     for (int q = 0; q < 4; ++q) pv[q] = lane + 64 * q < E ? expf(pv[q] - mx) : 0.f;
     double sum = 0.0;
     for (int j = 0; j < E; ++j) {
-        float ej = __shfl(pv[0], j & 63, 64);
-        if (j >= 64) ej = __shfl(j < 128 ? pv[1] : (j < 192 ? pv[2] : pv[3]), j & 63, 64);
-        sum += (double)ej;
+        const float src = j < 64 ? pv[0] : j < 128 ? pv[1] : j < 192 ? pv[2] : pv[3];
+        sum += (double)lane_f(src, j & 63);
     }
     const float inv = (float)(1.0 / sum);
 #pragma unroll

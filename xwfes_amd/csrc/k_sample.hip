@@ -324,6 +324,7 @@ __device__ int32_t sampler_pick(const float* __restrict__ lg, int64_t V, float m
     __shared__ int32_t eqi[SMAXEQ];
     __shared__ float kp[SMAXK];
     __shared__ int32_t ki[SMAXK];
+    __shared__ int32_t kx[SMAXK];
     __shared__ double ssum;
     __shared__ int32_t pick;
     const int t = threadIdx.x, l = t & 63;
@@ -438,44 +439,61 @@ __device__ int32_t sampler_pick(const float* __restrict__ lg, int64_t V, float m
     }
     __syncthreads();
     // the reference's arithmetic over the K kept values, on wave 0 with
-    // value l in lane l: the orders by rank (shuffle comparisons, then one
-    // LDS scatter / gather), the sequential sums as loops of shuffles that
-    // every lane runs alike (the same operations in the same order as one
-    // thread's loop over the sorted array)
+    // value l in lane l: the orders by rank (comparisons with every lane's
+    // value, read by v_readlane, then one LDS scatter / gather), the
+    // sequential sums as loops over the lanes that every lane runs alike
+    // (the same operations in the same order as one thread's loop over the
+    // sorted array)
     if (t < 64) {
         float pv = l < K ? kp[l] : 0.f;
         int32_t iv = l < K ? ki[l] : INT_MAX;
-        // lane r takes the element of rank r (rank of (p, i): p descending,
-        // index ascending; by_index: index ascending)
-        auto permute = [&](bool by_index) {
-            int r = 0;
-            for (int j = 0; j < K; ++j) {
-                const float pj = __shfl(pv, j, 64);
-                const int32_t ij = __shfl(iv, j, 64);
-                r += by_index ? ij < iv : (pj > pv || (pj == pv && ij < iv));
-            }
+        int32_t xr = 0;  // the element's rank by index, carried along
+        // lane r takes the element of rank r of (p, i): p descending, index
+        // ascending (the comparisons combined bitwise: no branch per lane
+        // read); with_index: the ranks by index too
+        auto place = [&](int r) {
             __builtin_amdgcn_wave_barrier();
             if (l < K) {
                 kp[r] = pv;
                 ki[r] = iv;
+                kx[r] = xr;
             }
             __builtin_amdgcn_wave_barrier();
             pv = l < K ? kp[l] : 0.f;
             iv = l < K ? ki[l] : INT_MAX;
+            xr = l < K ? kx[l] : 0;
             __builtin_amdgcn_wave_barrier();
         };
-        permute(false);
+        auto rank = [&](bool with_index) {
+            int r = 0, ri = 0;
+#pragma unroll 4
+            for (int j = 0; j < K; ++j) {
+                const float pj = lane_f(pv, j);
+                const int32_t ij = lane_i(iv, j);
+                r += (int)((pj > pv) | ((pj == pv) & (ij < iv)));
+                ri += (int)(ij < iv);
+            }
+            if (with_index) xr = ri;
+            return r;
+        };
+        place(rank(true));
         if (use_k) {
             float keep = 0.f;
-            for (int i = 0; i < K; ++i) keep += __shfl(pv, i, 64);
+            for (int i = 0; i < K; ++i) keep += lane_f(pv, i);
             if (l < K) pv = pv / keep;
         }
         if (top_p < 1.f) {
-            permute(false);  // the filtered values sorted again (division can make new ties)
+            // the filtered values in (p, i) order again: the division keeps
+            // the order of unequal values but can make neighbours equal,
+            // whose order is then by index -- sorted again only if some
+            // neighbour pair is out of that order
+            const float pn = __shfl_down(pv, 1, 64);
+            const int32_t in = __shfl_down(iv, 1, 64);
+            if (__ballot(l + 1 < K && pn == pv && in < iv)) place(rank(false));
             double cum = 0.0;
             int cut = K + 1;  // not reached among the kept: nothing cut
             for (int i = 0; i < K; ++i) {
-                cum += __shfl(pv, i, 64);
+                cum += lane_f(pv, i);
                 if (cum >= (double)top_p) {
                     cut = i + 1;
                     break;
@@ -483,14 +501,14 @@ __device__ int32_t sampler_pick(const float* __restrict__ lg, int64_t V, float m
             }
             if (cut <= K) {
                 double tail = 0.0;
-                for (int i = cut; i < K; ++i) tail += __shfl(pv, i, 64);
+                for (int i = cut; i < K; ++i) tail += lane_f(pv, i);
                 if (l >= cut) pv = 0.f;
                 if (tail > 0.0 && l < cut) pv = (float)(pv / (1.0 - tail));
             }
         }
         // the draw: the first index whose running double sum, as float,
-        // reaches r
-        permute(true);
+        // reaches r (the elements in index order by their carried ranks)
+        place(xr);
         uint64_t st = *state;
         const float r = sampler_next_float(st);
         int32_t pk = -1;
@@ -499,9 +517,9 @@ __device__ int32_t sampler_pick(const float* __restrict__ lg, int64_t V, float m
         } else {
             double c = 0.0;
             for (int i = 0; i < K; ++i) {
-                c += __shfl(pv, i, 64);
+                c += lane_f(pv, i);
                 if ((float)c >= r) {
-                    pk = __shfl(iv, i, 64);
+                    pk = lane_i(iv, i);
                     break;
                 }
             }
@@ -862,7 +880,7 @@ __device__ bool part_barrier(GridBar* gb, unsigned long long* cur, unsigned long
         if (l == 0) __threadfence();
         double sum = 0.0;
         for (unsigned w = 0; w < G; ++w) {
-            sum += __shfl(v, (int)w, 64);
+            sum += lane_d(v, (int)w);
             if (l == (int)w) {
                 vals[w] = v;
                 incl[w] = sum;
@@ -998,7 +1016,7 @@ __global__ void __launch_bounds__(RT) k_accept_res(AcceptDev a, GridBar* gb,
                 const int64_t ch = c0 + j;
                 kids &= kids - 1;
                 const float* qc = a.q + ch * V;
-                const int32_t tok = __shfl(ptok, j, 64);
+                const int32_t tok = lane_i(ptok, j);
                 const double pv = have_res ? Pc[tok] / T : texp(lg[tok], st.mx, a.temp) / T;
                 const float pt = (float)pv;
                 const float ratio = fminf(1.f, pt / fmaxf(qc[tok], 1e-9f));
