@@ -460,6 +460,7 @@ def main():
         ctx.sync()
     prompt = [int(t) for t in np.random.default_rng(8).integers(0, V, P_tok)]
     rng_state = [5, ftx.SAMPLER_SEED]
+    seq_rng = [[5 + i, ftx.SAMPLER_SEED] for i in range(max(nseq, 1))]
     accepted = []
 
     def step():
@@ -482,16 +483,19 @@ def main():
                 c.truncate(ctx_len)
             model.verify_batch([(c, dr["props"], lg.ptr, dr["parents"], False)
                                 for c, dr, lg in zip(bkv, bdraft, blog)])
+            # every sequence's acceptance (its own streams, as one engine per
+            # sequence has) in one call
+            items = []
             for i, (dr, lg, bs) in enumerate(zip(bdraft, blog, bbase)):
+                it = dict(base_ptr=bs.ptr, rows_ptr=lg.ptr, M=M, V=V, props=dr["props"], temp=temp,
+                          rng=seq_rng[i][0], sampler_state=seq_rng[i][1])
                 if dr["q"] is not None:
-                    r = ctx.accept(bs.ptr, lg.ptr, M, V, dr["props"], ftx.ACCEPT_RESIDUAL,
-                                   temp=temp, rng=rng_state[0], parents=dr["parents"],
-                                   q_ptr=dr["q"].ptr)
+                    it.update(mode=ftx.ACCEPT_RESIDUAL, parents=dr["parents"], q_ptr=dr["q"].ptr)
                 else:
-                    r = ctx.accept(bs.ptr, lg.ptr, M, V, dr["props"], ftx.ACCEPT_RATIO, temp=temp,
-                                   rng=rng_state[0], pd=dr["pd"], sampler_state=rng_state[1])
-                    rng_state[1] = r["sampler_state"]
-                rng_state[0] = r["rng"]
+                    it.update(mode=ftx.ACCEPT_RATIO, pd=dr["pd"])
+                items.append(it)
+            for i, r in enumerate(ctx.accept_batch(items)):
+                seq_rng[i] = [r["rng"], r["sampler_state"]]
                 accepted.append(len(r["accepted"]))
         elif kind == "decode":
             kv.truncate(ctx_len)

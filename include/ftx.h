@@ -329,6 +329,14 @@ typedef struct {
  * the sampler; RESIDUAL: multi-candidate speculative sampling, bonus from the
  * residual distribution with one more uniform of the rng stream). */
 int ftx_accept(ftx_ctx* ctx, const ftx_accept_args* a);
+/* No counterpart in the reference, which runs one Engine per sequence and
+ * so one acceptance per sequence: the acceptances of n (1..FTX_MAX_SEQ)
+ * sequences verified in one step (ftx_verify_batch), each exactly as
+ * ftx_accept would do it with its own arguments and streams, with one host
+ * synchronisation and one copy each way for all of them; the GREEDY and
+ * RATIO ones share one launch.  On an error the outputs of every sequence
+ * are unspecified. */
+int ftx_accept_batch(ftx_ctx* ctx, const ftx_accept_args* args, int n);
 
 /* Greedy draft pick of one device row [V]: the first maximum
  * (Sampler::argmax, include/ft/sampler.h:21-28) and its probability under

@@ -624,6 +624,64 @@ def test_accept_residual_wide_tree(gctx, orc):
         assert (g["accepted"], g["bonus"], g["rng"]) == (o["accepted"], o["bonus"], o["rng"])
 
 
+@pytest.mark.parametrize("V", [1001, 32000])
+def test_accept_batch_matches_single(gctx, orc, V):
+    """ftx_accept_batch over six sequences -- ratio chains of 8 and 3 nodes
+    (their own acceptance and sampler streams), a greedy tree, a residual
+    chain and tree, an empty draft -- returns for each what ftx_accept
+    returns for it alone, and what the oracle's acceptance gives."""
+    rng = np.random.default_rng(V + 9)
+    bufs, items, want = [], [], []
+    for kind, M in (("ratio", 8), ("ratio", 3), ("greedy", 8), ("residual", 8), ("residual", 6),
+                    ("empty", 0)):
+        base, rows, props = case(rng, max(M, 1), V, spread=1.0)
+        rows, props = rows[:M], props[:M]
+        b = gctx.buffer((M + 1) * V * 4)
+        b.write(np.ascontiguousarray(base, np.float32))
+        if M:
+            b.write(np.ascontiguousarray(rows, np.float32), V * 4)
+        it = dict(base_ptr=b.ptr, rows_ptr=b.ptr + V * 4 if M else None, M=M, V=V, props=props,
+                  temp=0.8, rng=int(rng.integers(1, 2**63)),
+                  sampler_state=int(rng.integers(1, 2**63)))
+        o_kw = dict(temp=0.8, seed=it["rng"], sampler_state=it["sampler_state"])
+        if kind == "ratio":
+            it["mode"] = ftx.ACCEPT_RATIO
+            it["pd"] = (rng.random(M) * 0.05).astype(np.float32)
+            o_kw["pd"] = it["pd"]
+        elif kind == "residual":
+            it["mode"] = ftx.ACCEPT_RESIDUAL
+            q = rng.dirichlet(np.ones(V), size=M).astype(np.float32)
+            qb = gctx.buffer(M * V * 4)
+            qb.write(q)
+            bufs.append(qb)
+            it["q_ptr"] = qb.ptr
+            it["parents"] = [-1, -1, 0, 0, 1, 3, 3, 5][:M] if M == 6 else None
+            o_kw.update(q=q, parents=it["parents"])
+        else:
+            it["mode"] = ftx.ACCEPT_GREEDY
+            it["parents"] = [-1, -1, 0, 0, 1, 2, 2, 4] if M == 8 else None
+            o_kw["parents"] = it["parents"]
+        bufs.append(b)
+        items.append(it)
+        if M:
+            want.append(orc.verify_accept(base, rows, props, it["mode"], **o_kw))
+        else:
+            want.append(None)
+    got = gctx.accept_batch(items)
+    for it, g, o in zip(items, got, want):
+        kw = {k: it[k] for k in ("temp", "rng", "parents", "pd", "q_ptr", "sampler_state")
+              if k in it}
+        one = gctx.accept(it["base_ptr"], it["rows_ptr"], it["M"], V, it["props"], it["mode"],
+                          **kw)
+        assert g == one
+        if o is not None:
+            assert (g["accepted"], g["bonus"], g["rng"]) == (o["accepted"], o["bonus"], o["rng"])
+            if it["mode"] == ftx.ACCEPT_RATIO:
+                assert g["sampler_state"] == o["sampler_state"]
+    for b in bufs:
+        b.free()
+
+
 def test_accept_empty_draft(gctx, orc):
     """M = 0: only the bonus token is drawn."""
     rng = np.random.default_rng(4)

@@ -625,6 +625,9 @@ struct AcceptDev {
     float* margin;           // device scalar
 };
 hipError_t launch_accept(hipStream_t st, const AcceptDev& a);
+// n acceptances (GREEDY / RATIO) in one launch, workgroup s taking d_arr[s]
+// (device memory)
+hipError_t launch_accept_multi(hipStream_t st, const AcceptDev* d_arr, int n);
 // the RESIDUAL mode over many workgroups (row statistics included); scratch
 // of accept_residual_scratch_bytes(); accept_residual_error copies the grid
 // barrier's time-out flag to the host int *err (enqueued on st)

@@ -605,9 +605,9 @@ __device__ void row_stat_wave(const AcceptDev& a, int64_t r, int l) {
     if (l == 0) a.stats[r] = RowStats{best, bi, sum};
 }
 
-// Decisions.  GREEDY and RESIDUAL finish here; RATIO records the row the
-// bonus is drawn from and its uniform for the two bonus kernels.
-__global__ void __launch_bounds__(NT) k_accept(AcceptDev a) {
+// Decisions by one workgroup: GREEDY and RESIDUAL (one-block form) finish
+// here; RATIO walks the chain and draws the bonus with the sampler.
+__device__ void accept_wg(const AcceptDev& a) {
 #pragma clang fp contract(off)
     __shared__ double sd[NT];
     __shared__ uint64_t rng;
@@ -759,6 +759,15 @@ __global__ void __launch_bounds__(NT) k_accept(AcceptDev a) {
         if (a.sampler_rng) *a.sampler_rng = srng;
         *a.margin = mg;
     }
+}
+
+__global__ void __launch_bounds__(NT) k_accept(AcceptDev a) { accept_wg(a); }
+
+// several sequences' acceptances at once, workgroup s taking arr[s] (each
+// sequence its own rows, statistics, streams and outputs)
+__global__ void __launch_bounds__(NT) k_accept_multi(const AcceptDev* __restrict__ arr) {
+    const AcceptDev a = arr[blockIdx.x];
+    accept_wg(a);
 }
 
 // ---- RESIDUAL acceptance over many workgroups.  The decisions are made
@@ -1219,6 +1228,12 @@ hipError_t launch_row_stats(hipStream_t st, const float* base_row, const float* 
 
 hipError_t launch_accept(hipStream_t st, const AcceptDev& a) {
     hipLaunchKernelGGL(k_accept, dim3(1), dim3(NT), 0, st, a);
+    return hipGetLastError();
+}
+
+hipError_t launch_accept_multi(hipStream_t st, const AcceptDev* d_arr, int n) {
+    if (n < 1) return hipErrorInvalidValue;
+    hipLaunchKernelGGL(k_accept_multi, dim3((unsigned)n), dim3(NT), 0, st, d_arr);
     return hipGetLastError();
 }
 

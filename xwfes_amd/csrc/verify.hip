@@ -1538,9 +1538,13 @@ int ftx_argmax_prob(ftx_ctx* ctx, const float* row, int64_t V, int32_t* token, f
     return FTX_OK;
 }
 
-int ftx_accept(ftx_ctx* ctx, const ftx_accept_args* a) {
-    if (!ctx || !a || !a->base_row || !a->props || !a->rng || !a->accepted || !a->n_acc ||
-        !a->bonus)
+}  // extern "C"
+
+namespace {
+
+// Checks of one acceptance's arguments (ftx_accept's contract).
+int acc_validate(ftx_ctx* ctx, const ftx_accept_args* a) {
+    if (!a || !a->base_row || !a->props || !a->rng || !a->accepted || !a->n_acc || !a->bonus)
         return ftx_fail(ctx, FTX_E_INVALID, "null argument");
     const int64_t M = a->M, V = a->V;
     if (M < 0 || V < 1 || (M > 0 && !a->rows)) return ftx_fail(ctx, FTX_E_INVALID, "bad M or V");
@@ -1569,66 +1573,66 @@ int ftx_accept(ftx_ctx* ctx, const ftx_accept_args* a) {
         if (a->mode == FTX_ACCEPT_RATIO && p != i - 1)
             return ftx_fail(ctx, FTX_E_INVALID, "ratio mode is chain only");
     }
-    // workspace: stats [M+1], p [V] doubles (residual mode), the small block
-    // (rng, margin, out ints | props, parents, pd: one copy in, one copy of
-    // its head out), the chunk statistics of the M + 1 rows
-    const size_t stats_b = (size_t)(M + 1) * sizeof(RowStats);
-    const size_t off_p = (stats_b + 255) & ~(size_t)255;
-    // residual mode: two residual buffers of V doubles and the kernel's
-    // barrier and partial sums
+    return FTX_OK;
+}
+
+size_t align256(size_t b) { return (b + 255) & ~(size_t)255; }
+
+// Workspace of one acceptance: stats [M+1], p [V] doubles (residual mode:
+// two residual buffers and the kernel's barrier and partial sums), the small
+// block (rng, margin, out ints | props, parents, pd: copied in, its head
+// copied out), the chunk statistics of the M + 1 rows.
+struct AccPlan {
+    size_t off_p, off_small, head_b, small_b, off_rs, bytes;
+};
+
+AccPlan acc_plan(const ftx_accept_args* a) {
+    const int64_t M = a->M, V = a->V;
+    AccPlan P;
+    P.off_p = align256((size_t)(M + 1) * sizeof(RowStats));
     const size_t pb = a->mode == FTX_ACCEPT_RESIDUAL
                           ? 2 * (size_t)V * 8 + 256 + accept_residual_scratch_bytes()
                           : 0;
-    const size_t off_small = off_p + ((pb + 255) & ~(size_t)255);
+    P.off_small = P.off_p + align256(pb);
     const size_t out_b = ((size_t)(M + 2) * 4 + 7) & ~(size_t)7;
-    const size_t head_b = 24 + out_b;  // rng | sampler rng | margin | pad | out
-    const size_t small_b = head_b + (size_t)M * 12 + 64;
-    const size_t off_rs = off_small + ((small_b + 255) & ~(size_t)255);  // row-stat chunks
-    const size_t off_b = off_rs + ((row_stats_scratch_bytes(M + 1, V) + 255) & ~(size_t)255);
-    uint8_t* ws;
-    int rc = ftx_workspace(ctx, off_b + 256, (void**)&ws);
-    if (rc) return rc;
-    uint8_t* pin;
-    rc = ftx_pinned(ctx, small_b, (void**)&pin);
-    if (rc) return rc;
-    hipStream_t st = ctx->stream;
-    FTX_HIP(ctx, hipStreamSynchronize(st));
-    // small host block: rng | sampler rng | margin | pad | out | props | parents | pd
-    uint64_t* h_rng = (uint64_t*)pin;
-    uint64_t* h_srng = (uint64_t*)(pin + 8);
-    float* h_margin = (float*)(pin + 16);
-    int32_t* h_out = (int32_t*)(pin + 24);
-    int32_t* h_props = (int32_t*)(pin + head_b);
+    P.head_b = 24 + out_b;  // rng | sampler rng | margin | pad | out
+    P.small_b = P.head_b + (size_t)M * 12 + 64;
+    P.off_rs = P.off_small + align256(P.small_b);
+    P.bytes = P.off_rs + align256(row_stats_scratch_bytes(M + 1, V)) + 256;
+    return P;
+}
+
+// the small block of a in host memory: rng | sampler rng | margin | pad |
+// out | props | parents | pd
+void acc_fill_small(const ftx_accept_args* a, const AccPlan& P, uint8_t* pin) {
+    const int64_t M = a->M;
+    *(uint64_t*)pin = *a->rng;
+    *(uint64_t*)(pin + 8) = a->sampler_rng ? *a->sampler_rng : 0;
+    *(float*)(pin + 16) = INFINITY;
+    int32_t* h_props = (int32_t*)(pin + P.head_b);
     int32_t* h_par = h_props + M;
     float* h_pd = (float*)(h_par + M);
-    *h_rng = *a->rng;
-    *h_srng = a->sampler_rng ? *a->sampler_rng : 0;
-    *h_margin = INFINITY;
     for (int64_t i = 0; i < M; ++i) {
         h_props[i] = a->props[i];
         h_par[i] = a->parents ? a->parents[i] : (int32_t)i - 1;
         h_pd[i] = a->pd ? a->pd[i] : 0.f;
     }
-    uint8_t* d_small = ws + off_small;
-    FTX_HIP(ctx, hipMemcpyAsync(d_small, pin, small_b, hipMemcpyHostToDevice, st));
-    RowStats* stats = (RowStats*)ws;
-    const RowChunks rch = row_chunks(ws + off_rs, M + 1, V);
-    const int with_sum = a->mode != FTX_ACCEPT_GREEDY;
-    {
-        TraceScope ts(ctx);
-        FTX_HIP(ctx, launch_row_stats(st, a->base_row, a->rows, M + 1, V, a->temp, with_sum, rch));
-        ts.end(TK_ROW_STATS, (double)(M + 1) * V * 4, with_sum ? 2 : 1);
-    }
+}
+
+// the kernels' view of a: ws = its workspace, d_small = its small block on
+// the device
+AcceptDev acc_dev(const ftx_accept_args* a, const AccPlan& P, uint8_t* ws, uint8_t* d_small) {
+    const int64_t M = a->M, V = a->V;
     AcceptDev ad{};
     ad.base_row = a->base_row;
     ad.rows = a->rows;
     ad.q = a->q;
-    ad.rc = rch;
-    ad.with_sum = with_sum;
-    ad.stats = stats;
+    ad.rc = row_chunks(ws + P.off_rs, M + 1, V);
+    ad.with_sum = a->mode != FTX_ACCEPT_GREEDY;
+    ad.stats = (RowStats*)ws;
     ad.M = M;
     ad.V = V;
-    ad.props = (const int32_t*)(d_small + head_b);
+    ad.props = (const int32_t*)(d_small + P.head_b);
     ad.parents = ad.props + M;
     ad.pd = (const float*)(ad.parents + M);
     ad.mode = a->mode;
@@ -1637,33 +1641,147 @@ int ftx_accept(ftx_ctx* ctx, const ftx_accept_args* a) {
     ad.sampler_rng = (uint64_t*)(d_small + 8);
     ad.top_k = a->top_k;
     ad.top_p = a->top_p;
-    ad.p = (double*)(ws + off_p);
+    ad.p = (double*)(ws + P.off_p);
     ad.out = (int32_t*)(d_small + 24);
     ad.margin = (float*)(d_small + 16);
+    return ad;
+}
+
+void* acc_res_scratch(const ftx_accept_args* a, const AccPlan& P, uint8_t* ws) {
+    return ws + P.off_p + align256(2 * (size_t)a->V * 8);
+}
+
+int acc_row_stats(ftx_ctx* ctx, const ftx_accept_args* a, const AcceptDev& ad) {
+    TraceScope ts(ctx);
+    FTX_HIP(ctx, launch_row_stats(ctx->stream, a->base_row, a->rows, a->M + 1, a->V, a->temp,
+                                  ad.with_sum, ad.rc));
+    ts.end(TK_ROW_STATS, (double)(a->M + 1) * a->V * 4, ad.with_sum ? 2 : 1);
+    return FTX_OK;
+}
+
+// the outputs of a from its small block's head, copied back to host memory
+int acc_results(ftx_ctx* ctx, const ftx_accept_args* a, const uint8_t* pin) {
+    const int32_t* h_out = (const int32_t*)(pin + 24);
+    const int32_t na = h_out[0];
+    if (na < 0 || na > a->M) return ftx_fail(ctx, FTX_E_DEVICE, "acceptance returned a bad count");
+    *a->n_acc = na;
+    *a->bonus = h_out[1];
+    for (int32_t i = 0; i < na; ++i) a->accepted[i] = h_out[2 + i];
+    *a->rng = *(const uint64_t*)pin;
+    if (a->sampler_rng) *a->sampler_rng = *(const uint64_t*)(pin + 8);
+    if (a->margin) *a->margin = *(const float*)(pin + 16);
+    return FTX_OK;
+}
+
+}  // namespace
+
+extern "C" {
+
+int ftx_accept(ftx_ctx* ctx, const ftx_accept_args* a) {
+    if (!ctx) return FTX_E_INVALID;
+    int rc = acc_validate(ctx, a);
+    if (rc) return rc;
+    const AccPlan P = acc_plan(a);
+    uint8_t* ws;
+    rc = ftx_workspace(ctx, P.bytes, (void**)&ws);
+    if (rc) return rc;
+    uint8_t* pin;
+    rc = ftx_pinned(ctx, P.small_b, (void**)&pin);
+    if (rc) return rc;
+    hipStream_t st = ctx->stream;
+    FTX_HIP(ctx, hipStreamSynchronize(st));
+    acc_fill_small(a, P, pin);
+    uint8_t* d_small = ws + P.off_small;
+    FTX_HIP(ctx, hipMemcpyAsync(d_small, pin, P.small_b, hipMemcpyHostToDevice, st));
+    const AcceptDev ad = acc_dev(a, P, ws, d_small);
+    rc = acc_row_stats(ctx, a, ad);
+    if (rc) return rc;
     int bar_err = 0;
-    void* res_scratch = ws + off_p + ((2 * (size_t)V * 8 + 255) & ~(size_t)255);
+    void* res_scratch = acc_res_scratch(a, P, ws);
     {
         TraceScope ts(ctx);
         if (a->mode == FTX_ACCEPT_RESIDUAL)
             FTX_HIP(ctx, launch_accept_residual(st, ad, res_scratch));
         else
             FTX_HIP(ctx, launch_accept(st, ad));
-        ts.end(TK_ACCEPT, (double)V * 4);
+        ts.end(TK_ACCEPT, (double)a->V * 4);
     }
-    FTX_HIP(ctx, hipMemcpyAsync(pin, d_small, head_b, hipMemcpyDeviceToHost, st));
+    FTX_HIP(ctx, hipMemcpyAsync(pin, d_small, P.head_b, hipMemcpyDeviceToHost, st));
     if (a->mode == FTX_ACCEPT_RESIDUAL && accept_residual_error(res_scratch, st, &bar_err))
         return ftx_fail(ctx, FTX_E_DEVICE, "acceptance: copy of the barrier state failed");
     FTX_HIP(ctx, hipStreamSynchronize(st));
     if (bar_err)
         return ftx_fail(ctx, FTX_E_DEVICE, "acceptance: a grid barrier timed out");
-    const int32_t na = h_out[0];
-    if (na < 0 || na > M) return ftx_fail(ctx, FTX_E_DEVICE, "acceptance returned a bad count");
-    *a->n_acc = na;
-    *a->bonus = h_out[1];
-    for (int32_t i = 0; i < na; ++i) a->accepted[i] = h_out[2 + i];
-    *a->rng = *h_rng;
-    if (a->sampler_rng) *a->sampler_rng = *h_srng;
-    if (a->margin) *a->margin = *h_margin;
+    return acc_results(ctx, a, pin);
+}
+
+int ftx_accept_batch(ftx_ctx* ctx, const ftx_accept_args* args, int n) {
+    if (!ctx) return FTX_E_INVALID;
+    if (!args || n < 1 || n > FTX_MAX_SEQ)
+        return ftx_fail(ctx, FTX_E_INVALID, "accept_batch: 1..FTX_MAX_SEQ acceptances");
+    AccPlan P[FTX_MAX_SEQ];
+    size_t ws_off[FTX_MAX_SEQ], pin_off[FTX_MAX_SEQ];
+    size_t ws_total = 0, pin_total = 0;
+    int nmulti = 0;
+    for (int i = 0; i < n; ++i) {
+        const int rc = acc_validate(ctx, &args[i]);
+        if (rc) return rc;
+        P[i] = acc_plan(&args[i]);
+        ws_off[i] = ws_total;
+        ws_total += align256(P[i].bytes);
+        pin_off[i] = pin_total;
+        pin_total += align256(P[i].small_b);
+        nmulti += args[i].mode != FTX_ACCEPT_RESIDUAL;
+    }
+    // the small blocks, then the one-launch acceptances' descriptions, in
+    // one pinned block copied to one device region (one copy each way)
+    const size_t adv_off = pin_total;
+    pin_total += align256((size_t)nmulti * sizeof(AcceptDev));
+    uint8_t* ws;
+    int rc = ftx_workspace(ctx, ws_total + pin_total, (void**)&ws);
+    if (rc) return rc;
+    uint8_t* pin;
+    rc = ftx_pinned(ctx, pin_total, (void**)&pin);
+    if (rc) return rc;
+    uint8_t* d_small = ws + ws_total;
+    hipStream_t st = ctx->stream;
+    FTX_HIP(ctx, hipStreamSynchronize(st));
+    AcceptDev ad[FTX_MAX_SEQ];
+    AcceptDev* h_adv = (AcceptDev*)(pin + adv_off);
+    int k = 0;
+    for (int i = 0; i < n; ++i) {
+        acc_fill_small(&args[i], P[i], pin + pin_off[i]);
+        ad[i] = acc_dev(&args[i], P[i], ws + ws_off[i], d_small + pin_off[i]);
+        if (args[i].mode != FTX_ACCEPT_RESIDUAL) h_adv[k++] = ad[i];
+    }
+    FTX_HIP(ctx, hipMemcpyAsync(d_small, pin, pin_total, hipMemcpyHostToDevice, st));
+    for (int i = 0; i < n; ++i) {
+        rc = acc_row_stats(ctx, &args[i], ad[i]);
+        if (rc) return rc;
+    }
+    int bar_err[FTX_MAX_SEQ] = {};
+    for (int i = 0; i < n; ++i) {
+        if (args[i].mode != FTX_ACCEPT_RESIDUAL) continue;
+        TraceScope ts(ctx);
+        FTX_HIP(ctx, launch_accept_residual(st, ad[i], acc_res_scratch(&args[i], P[i], ws + ws_off[i])));
+        ts.end(TK_ACCEPT, (double)args[i].V * 4);
+    }
+    if (nmulti) {
+        TraceScope ts(ctx);
+        FTX_HIP(ctx, launch_accept_multi(st, (const AcceptDev*)(d_small + adv_off), nmulti));
+        ts.end(TK_ACCEPT, (double)args[0].V * 4 * nmulti);
+    }
+    FTX_HIP(ctx, hipMemcpyAsync(pin, d_small, adv_off, hipMemcpyDeviceToHost, st));
+    for (int i = 0; i < n; ++i)
+        if (args[i].mode == FTX_ACCEPT_RESIDUAL &&
+            accept_residual_error(acc_res_scratch(&args[i], P[i], ws + ws_off[i]), st, &bar_err[i]))
+            return ftx_fail(ctx, FTX_E_DEVICE, "acceptance: copy of the barrier state failed");
+    FTX_HIP(ctx, hipStreamSynchronize(st));
+    for (int i = 0; i < n; ++i) {
+        if (bar_err[i]) return ftx_fail(ctx, FTX_E_DEVICE, "acceptance: a grid barrier timed out");
+        rc = acc_results(ctx, &args[i], pin + pin_off[i]);
+        if (rc) return rc;
+    }
     return FTX_OK;
 }
 

@@ -130,6 +130,7 @@ def load(path=LIB_PATH):
         "ftx_verify_step": (C.c_int, [_vp, _vp, _vp, C.POINTER(VerifyArgs)]),
         "ftx_verify_batch": (C.c_int, [_vp, _vp, C.POINTER(SeqArgs), _i64]),
         "ftx_accept": (C.c_int, [_vp, C.POINTER(AcceptArgs)]),
+        "ftx_accept_batch": (C.c_int, [_vp, C.POINTER(AcceptArgs), C.c_int]),
         "ftx_argmax_prob": (C.c_int, [_vp, _vp, _i64, _i32p, _fp]),
         "ftx_fill_normal": (C.c_int, [_vp, _vp, C.c_int, _i64, C.c_uint64, C.c_float]),
         "ftx_trace": (C.c_int, [_vp, C.c_int]),
@@ -363,6 +364,37 @@ class Context:
         self.check(self.lib.ftx_accept(self.h, C.byref(a)))
         return dict(accepted=acc[:na.value].tolist(), bonus=bonus.value, rng=s.value,
                     sampler_state=ss.value, margin=mg.value)
+
+    def accept_batch(self, items):
+        """ftx_accept_batch over several sequences: items are dicts of
+        accept()'s arguments (base_ptr, rows_ptr, M, V, props, mode and the
+        optional ones); returns accept()'s result for each, in order."""
+        keep, outs = [], []
+        args = (AcceptArgs * len(items))()
+        for k, it in enumerate(items):
+            M, V = it["M"], it["V"]
+            props = np.ascontiguousarray(it["props"], np.int32)
+            par = it.get("parents")
+            par = None if par is None else np.ascontiguousarray(par, np.int32)
+            pd = it.get("pd")
+            pdv = None if pd is None else np.ascontiguousarray(pd, np.float32)
+            acc = np.zeros(max(M, 1), np.int32)
+            na, bonus, mg = C.c_int32(0), C.c_int32(0), C.c_float(0)
+            s = C.c_uint64(it.get("rng", 0))
+            ss = C.c_uint64(it.get("sampler_state", SAMPLER_SEED))
+            args[k] = AcceptArgs(it["base_ptr"], it["rows_ptr"], it.get("q_ptr"), M, V,
+                                 props.ctypes.data_as(_i32p),
+                                 None if par is None else par.ctypes.data_as(_i32p),
+                                 None if pdv is None else pdv.ctypes.data_as(_fp), it["mode"],
+                                 it.get("temp", 1.0), C.pointer(s), acc.ctypes.data_as(_i32p),
+                                 C.pointer(na), C.pointer(bonus), C.pointer(mg), C.pointer(ss),
+                                 it.get("top_k", 40), it.get("top_p", 0.95))
+            keep += [props, par, pdv]
+            outs.append((acc, na, bonus, s, ss, mg))
+        self.check(self.lib.ftx_accept_batch(self.h, args, len(items)))
+        return [dict(accepted=acc[:na.value].tolist(), bonus=bonus.value, rng=s.value,
+                     sampler_state=ss.value, margin=mg.value)
+                for acc, na, bonus, s, ss, mg in outs]
 
 
 class Model:
