@@ -1529,7 +1529,6 @@ int ftx_argmax_prob(ftx_ctx* ctx, const float* row, int64_t V, int32_t* token, f
     if (rc) return rc;
     hipStream_t st = ctx->stream;
     int32_t* d_out = (int32_t*)(ws + rs);
-    FTX_HIP(ctx, hipStreamSynchronize(st));  // the pinned buffer is shared
     FTX_HIP(ctx, launch_argmax_prob(st, row, V, ws, d_out));
     FTX_HIP(ctx, hipMemcpyAsync(pin, d_out, 8, hipMemcpyDeviceToHost, st));
     FTX_HIP(ctx, hipStreamSynchronize(st));
@@ -1688,8 +1687,11 @@ int ftx_accept(ftx_ctx* ctx, const ftx_accept_args* a) {
     uint8_t* pin;
     rc = ftx_pinned(ctx, P.small_b, (void**)&pin);
     if (rc) return rc;
+    // (every user of the context's pinned block has waited for its copies
+    // before returning, also on its error paths, so the block is filled
+    // while the stream may still run earlier work: the acceptance's copies
+    // and launches queue behind it without a host round trip)
     hipStream_t st = ctx->stream;
-    FTX_HIP(ctx, hipStreamSynchronize(st));
     acc_fill_small(a, P, pin);
     uint8_t* d_small = ws + P.off_small;
     FTX_HIP(ctx, hipMemcpyAsync(d_small, pin, P.small_b, hipMemcpyHostToDevice, st));
@@ -1707,8 +1709,10 @@ int ftx_accept(ftx_ctx* ctx, const ftx_accept_args* a) {
         ts.end(TK_ACCEPT, (double)a->V * 4);
     }
     FTX_HIP(ctx, hipMemcpyAsync(pin, d_small, P.head_b, hipMemcpyDeviceToHost, st));
-    if (a->mode == FTX_ACCEPT_RESIDUAL && accept_residual_error(res_scratch, st, &bar_err))
+    if (a->mode == FTX_ACCEPT_RESIDUAL && accept_residual_error(res_scratch, st, &bar_err)) {
+        (void)hipStreamSynchronize(st);  // the copy into the pinned block has landed
         return ftx_fail(ctx, FTX_E_DEVICE, "acceptance: copy of the barrier state failed");
+    }
     FTX_HIP(ctx, hipStreamSynchronize(st));
     if (bar_err)
         return ftx_fail(ctx, FTX_E_DEVICE, "acceptance: a grid barrier timed out");
@@ -1744,8 +1748,7 @@ int ftx_accept_batch(ftx_ctx* ctx, const ftx_accept_args* args, int n) {
     rc = ftx_pinned(ctx, pin_total, (void**)&pin);
     if (rc) return rc;
     uint8_t* d_small = ws + ws_total;
-    hipStream_t st = ctx->stream;
-    FTX_HIP(ctx, hipStreamSynchronize(st));
+    hipStream_t st = ctx->stream;  // (filled without waiting: see ftx_accept)
     AcceptDev ad[FTX_MAX_SEQ];
     AcceptDev* h_adv = (AcceptDev*)(pin + adv_off);
     int k = 0;
@@ -1774,8 +1777,10 @@ int ftx_accept_batch(ftx_ctx* ctx, const ftx_accept_args* args, int n) {
     FTX_HIP(ctx, hipMemcpyAsync(pin, d_small, adv_off, hipMemcpyDeviceToHost, st));
     for (int i = 0; i < n; ++i)
         if (args[i].mode == FTX_ACCEPT_RESIDUAL &&
-            accept_residual_error(acc_res_scratch(&args[i], P[i], ws + ws_off[i]), st, &bar_err[i]))
+            accept_residual_error(acc_res_scratch(&args[i], P[i], ws + ws_off[i]), st, &bar_err[i])) {
+            (void)hipStreamSynchronize(st);  // the copy into the pinned block has landed
             return ftx_fail(ctx, FTX_E_DEVICE, "acceptance: copy of the barrier state failed");
+        }
     FTX_HIP(ctx, hipStreamSynchronize(st));
     for (int i = 0; i < n; ++i) {
         if (bar_err[i]) return ftx_fail(ctx, FTX_E_DEVICE, "acceptance: a grid barrier timed out");
