@@ -34,6 +34,9 @@ struct ftx_model {
     _Float16* qhl = nullptr;
     // RoPE cos / sin per (token, pair) of the current step, [M][hd / 2][2]
     float* rcs = nullptr;  // (a view into args)
+    // rope_vec's frequencies f_p = theta^(-2p / hd), p < hd / 2 (formed once;
+    // a step computes only its angles' cos / sin)
+    std::vector<double> rope_f;
     // per-layer re-tiled ffn_down copies for the MFMA down kernel (or null)
     std::vector<uint8_t*> down_tiled;
     // tiled copies for the int8-MFMA row-dot kernel, [layer * LAYER_TENSORS +
@@ -223,11 +226,13 @@ static int verify_large(ftx_ctx* ctx, ftx_model* m, const ftx_seq_args* sq, int6
             for (int w = 0; w < aw; ++w) row[w] = p >= 0 ? anc[(r0 + p) * aw + w] : 0u;
             row[i / 32] |= 1u << (i % 32);
             // rope_vec's angles (src/engine.cpp:43-60) at npast + depth
+            // (sincos: the values of cos and sin, in one call)
             for (int64_t q = 0; q < hd2; ++q) {
-                const double f = std::pow(d.rope_theta, -2.0 * (double)q / (double)hd);
-                const double ang = (double)(npast + depth[r0 + i]) * f;
-                cs[((r0 + i) * hd2 + q) * 2] = (float)std::cos(ang);
-                cs[((r0 + i) * hd2 + q) * 2 + 1] = (float)std::sin(ang);
+                const double ang = (double)(npast + depth[r0 + i]) * m->rope_f[(size_t)q];
+                double sn, cn;
+                sincos(ang, &sn, &cn);
+                cs[((r0 + i) * hd2 + q) * 2] = (float)cn;
+                cs[((r0 + i) * hd2 + q) * 2 + 1] = (float)sn;
             }
         }
     }
@@ -799,6 +804,10 @@ int ftx_model_create(ftx_ctx* ctx, const ftx_model_desc* d, ftx_model** out) {
     if (!m) return ftx_fail(ctx, FTX_E_NOMEM, "host allocation failed");
     m->ctx = ctx;
     m->d = *d;
+    // (the same expression as rope_vec's, src/engine.cpp:43-60)
+    m->rope_f.resize((size_t)(d->head_dim / 2));
+    for (int64_t p = 0; p < d->head_dim / 2; ++p)
+        m->rope_f[(size_t)p] = std::pow(d->rope_theta, -2.0 * (double)p / (double)d->head_dim);
     m->layers.assign(d->layers, d->layers + d->n_layer * FTX_LAYER_TENSORS);
     m->d.layers = nullptr;
     m->ext.assign((size_t)(d->n_layer * FTX_LAYER_EXT), nullptr);
@@ -1240,14 +1249,16 @@ int ftx_verify_step(ftx_ctx* ctx, ftx_model* m, ftx_kv* kv, const ftx_verify_arg
         row[i / 32] |= 1u << (i % 32);
     }
     *np = npast;
-    // rope_vec's angles (src/engine.cpp:43-60): f = theta^(-2i/hd) and the
-    // angle in double, cos / sin rounded to float, at position npast + depth
+    // rope_vec's angles (src/engine.cpp:43-60): f = theta^(-2i/hd) (the
+    // model's table) and the angle in double, cos / sin rounded to float, at
+    // position npast + depth (sincos: the values of cos and sin, in one call)
     for (int64_t i = 0; i < M; ++i)
         for (int64_t p = 0; p < hd2; ++p) {
-            const double f = std::pow(d.rope_theta, -2.0 * (double)p / (double)d.head_dim);
-            const double ang = (double)(npast + depth[i]) * f;
-            cs[(i * hd2 + p) * 2] = (float)std::cos(ang);
-            cs[(i * hd2 + p) * 2 + 1] = (float)std::sin(ang);
+            const double ang = (double)(npast + depth[i]) * m->rope_f[(size_t)p];
+            double sn, cn;
+            sincos(ang, &sn, &cn);
+            cs[(i * hd2 + p) * 2] = (float)cn;
+            cs[(i * hd2 + p) * 2 + 1] = (float)sn;
         }
     hipStream_t st = ctx->stream;
     m->toks = (int32_t*)m->args;
