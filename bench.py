@@ -500,12 +500,16 @@ def main():
         elif kind == "decode":
             kv.truncate(ctx_len)
             model.step(kv, int(props[0]), logits.ptr)
+            # the token's logits are complete when the step returns, as the
+            # caller samples from them before the next step
+            ctx.sync()
         elif kind == "generate":
             out, st = spec.generate(ctx, model, kv, drafter, prompt, W["N"], spec_k=M, temp=temp)
             gen_stats.append((len(out), st))
         else:
             kv.truncate(0)
             model.prefill(kv, prompt, logits.ptr, chunk=M)
+            ctx.sync()
 
     for _ in range(args.warmup):
         step()
