@@ -1,7 +1,7 @@
 /*
  * ftx_oracle.h -- CPU oracle for the speculative-decoding verify path.
  *
- * TEST INFRASTRUCTURE ONLY.  This library is the checker that the HIP path is
+ * TEST INFRASTRUCTURE ONLY.  This library is the oracle that the HIP path is
  * compared against.  Only tests/, __graft_entry__.smoke() and the
  * cpu_baseline leg of bench.py may load it.  Nothing in the product
  * (xwfes_amd/) links or calls it.

@@ -1,5 +1,5 @@
-"""ctypes view of the CPU oracle (liboracle.so) and of the reference checker
-library (_ref/libftref.so).
+"""ctypes view of the CPU oracle (liboracle.so) and of the library built
+from the reference's own sources (_ref/libftref.so).
 
 TEST INFRASTRUCTURE ONLY: imported by tests/, __graft_entry__.smoke() and the
 cpu_baseline leg of bench.py.  The product (xwfes_amd/) never imports it.
@@ -44,7 +44,7 @@ def build():
 
 
 def build_ref(ref_root="/root/reference/ft-igpu-src"):
-    """Compile the reference checker where the reference tree exists."""
+    """Compile the reference's own build where the reference tree exists."""
     if not os.path.isdir(ref_root):
         return False
     subprocess.check_call(["make", "-s", "-C", HERE, "-f", "Makefile.ref",
@@ -482,7 +482,7 @@ class Oracle:
 class Ref:
     """The reference's own functions (compiled from its sources by
     Makefile.ref).  Available only where the reference tree was present when
-    the checker was built."""
+    the library was built."""
 
     def __init__(self, path=REF_PATH):
         L = self.lib = C.CDLL(path)

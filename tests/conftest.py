@@ -23,7 +23,7 @@ def orc():
 def ref():
     import pyoracle
     if not pyoracle.Ref.available():
-        pytest.skip("reference checker library oracle/_ref not built here")
+        pytest.skip("reference build oracle/_ref not present here")
     return pyoracle.Ref()
 
 
